@@ -1,0 +1,164 @@
+// Shared device helpers and host-side error plumbing for libcvsa_hip.so.
+// Target: gfx950 (CDNA4), wave64.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <math.h>
+
+#include "../../include/cvsa_hip.h"
+
+namespace cvsa {
+
+constexpr int kWave = 64;
+constexpr int kHeadDim = 128;   // the only supported head dimension
+constexpr int kPageTokens = 16; // the only supported page (block) size
+constexpr int kMaxPages = 32768;
+
+// ---------------------------------------------------------------- numerics
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// acc + a.lo*b.lo + a.hi*b.hi on packed bf16 pairs (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc,
+                                         false);
+}
+
+// Sum of the 8 products of two 16-byte bf16 vectors, accumulated onto acc.
+__device__ __forceinline__ float dot8_bf16(const uint4 &a, const uint4 &b, float acc) {
+  acc = dot2_bf16(a.x, b.x, acc);
+  acc = dot2_bf16(a.y, b.y, acc);
+  acc = dot2_bf16(a.z, b.z, acc);
+  acc = dot2_bf16(a.w, b.w, acc);
+  return acc;
+}
+
+// exp(x) through the hardware base-2 exponential.
+__device__ __forceinline__ float fast_exp(float x) { return exp2f(x * 1.4426950408889634f); }
+
+// ------------------------------------------------------------- lane moves
+// DPP controls (gfx9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                         0xF, 0xF, true));
+}
+
+// Value of lane (l ^ 16) and of lane (l ^ 32): the two halves of each
+// permlane swap pair hold {v[l], v[l^16]} (resp. {v[l], v[l^32]}).
+__device__ __forceinline__ void xchg16(float v, float &a, float &b) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                            false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void xchg32(float v, float &a, float &b) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                            false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
+// All-reduce over aligned groups of W lanes (W in 1,2,4,8,16); every lane
+// of a group ends with the same bits.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (W >= 2) v += dpp_f<kDppQuadXor1>(v);
+  if constexpr (W >= 4) v += dpp_f<kDppQuadXor2>(v);
+  if constexpr (W >= 8) v += dpp_f<kDppRowHalfMirror>(v);
+  if constexpr (W >= 16) v += dpp_f<kDppRowMirror>(v);
+  return v;
+}
+
+// Max over the whole wave of a value that is uniform inside aligned groups
+// of W lanes (W in 1,2,4,8,16).  Returns a wave-uniform value.
+template <int W>
+__device__ __forceinline__ float wave_max_from_groups(float v) {
+  if constexpr (W < 2) v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+  if constexpr (W < 4) v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+  if constexpr (W < 8) v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+  if constexpr (W < 16) v = fmaxf(v, dpp_f<kDppRowMirror>(v));
+  float a, b;
+  xchg16(v, a, b);
+  v = fmaxf(a, b);
+  xchg32(v, a, b);
+  v = fmaxf(a, b);
+  return v;
+}
+
+template <int W>
+__device__ __forceinline__ float wave_sum_from_groups(float v) {
+  if constexpr (W < 2) v += dpp_f<kDppQuadXor1>(v);
+  if constexpr (W < 4) v += dpp_f<kDppQuadXor2>(v);
+  if constexpr (W < 8) v += dpp_f<kDppRowHalfMirror>(v);
+  if constexpr (W < 16) v += dpp_f<kDppRowMirror>(v);
+  float a, b;
+  xchg16(v, a, b);
+  v = a + b;
+  xchg32(v, a, b);
+  v = a + b;
+  return v;
+}
+
+// Sum over lanes that share (lane mod W): adds the 64/W lanes
+// {l, l+W, l+2W, ...}.  All those lanes end with the same value.
+template <int W>
+__device__ __forceinline__ float sum_across_groups(float v) {
+  if constexpr (W <= 4) v += dpp_f<kDppRowRor4>(v);
+  if constexpr (W <= 8) v += dpp_f<kDppRowRor8>(v);
+  float a, b;
+  xchg16(v, a, b);
+  v = a + b;
+  xchg32(v, a, b);
+  v = a + b;
+  return v;
+}
+
+// Pages of a sequence that hold at least one position below ctx, following
+// the reference's ((ctx - 1) / bs) + 1 with truncating division, so ctx = 0
+// still counts one page (cvsa/backend.py:687, coverage.py:60).
+__device__ __host__ __forceinline__ int n_valid_pages(int ctx, int bs) {
+  return (ctx - 1) / bs + 1;
+}
+
+}  // namespace cvsa
+
+// ------------------------------------------------------------ host helpers
+namespace cvsa_host {
+
+void set_error(const char *fmt, ...);
+int fail(int code, const char *fmt, ...);
+int check_launch(const char *what);
+
+}  // namespace cvsa_host
+
+#define CVSA_REQUIRE(cond, code, ...)                 \
+  do {                                                \
+    if (!(cond)) return cvsa_host::fail(code, __VA_ARGS__); \
+  } while (0)

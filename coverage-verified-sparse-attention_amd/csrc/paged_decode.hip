@@ -1,0 +1,542 @@
+// Paged decode attention over a per-KV-head page list, emitting the
+// un-normalised softmax state (o, m, l) and/or the normalised output.
+//
+// Semantics follow the reference's sparse decode kernels
+// (cvsa/kernels/sparse_decode.py:14-132, :136-234, :423-500): for each
+// q-head, over the first n_sel listed pages of its KV head and the tokens
+// t < min(bs, ctx - page*bs) of each page (:76-80), s = (q . K) * D^-0.5,
+// m = max s, l = sum exp(s - m), o = sum exp(s - m) V (:101-124); the
+// normalised output is o / max(l, 1e-6) (:127, :271).  Split-K partial
+// states are combined with the log-sum-exp rule of _reduce_tiles_kernel
+// (:237-276, :576-606).
+//
+// MI355X mapping.  The reference launches one program per q-head, so each
+// K/V page tile is fetched G times.  Here a workgroup owns one KV head and a
+// contiguous range of its page list; each of its four waves takes every
+// fourth page, loads the page's 16 K rows and 16 V rows once (256 B per row,
+// 16-byte lane loads) and applies them to all G query heads of the group.
+// Lane l holds d-segment (l % LPT) of token slot (l / LPT); the q.K dot is
+// finished with an LPT-lane DPP reduction, the page max with DPP and
+// permlane swaps, and P.V accumulates in registers.  The four waves merge in
+// LDS, every workgroup stores its partial (o, m, l), and the last workgroup
+// of a head (completion counter) merges all partials and writes the
+// outputs, so one launch does the whole decode.
+//
+// Head modes: a listed head walks page_indices[b,h,:n_per_head]; an
+// all-pages head walks pages 0..n_valid-1 (dense decode).  In verified mode
+// accepted heads are listed and rejected heads walk every valid page: the
+// draft pages plus the complement pages in one pass, which equals the LSE
+// merge of the draft and complement partial softmaxes.
+#include "cvsa_common.h"
+#include <hip/hip_fp16.h>
+
+namespace cvsa {
+
+constexpr int kDecThreads = 256;
+constexpr int kDecWaves = kDecThreads / kWave;
+constexpr int kPartStride = kHeadDim + 2;  // o[D], m, l
+constexpr int kTargetWorkgroups = 640;     // ~2.5 workgroups per CU
+constexpr int kMinPagesPerSplit = 8;       // two pages per wave
+
+struct DecodeArgs {
+  const uint16_t *q;
+  int64_t q_sb, q_sh;
+  const uint16_t *k_cache;
+  const uint16_t *v_cache;
+  int64_t num_blocks;
+  const int32_t *block_tables;
+  int64_t bt_sb;
+  const int32_t *ctx_lens;
+  const int32_t *page_idx;  // NULL: every head walks all valid pages
+  int64_t idx_stride;
+  int max_sel;
+  const int32_t *n_pages;
+  const uint8_t *accept;  // non-NULL: verified mode
+  int H_kv, W;
+  float scale;
+  int pps_sel, pps_all, n_splits;
+  float *o_unnorm, *m_out, *l_out;
+  void *out;
+  int out_dtype;
+  float *part;
+  uint32_t *counters;
+  unsigned long long *work;  // optional effective-budget counters
+};
+
+__device__ __forceinline__ void store_out(void *out, int dtype, int64_t i, float y) {
+  if (dtype == CVSA_DTYPE_BF16) {
+    reinterpret_cast<uint16_t *>(out)[i] = (uint16_t)f32_to_bf16_bits(y);
+  } else if (dtype == CVSA_DTYPE_FP16) {
+    reinterpret_cast<__half *>(out)[i] = __float2half_rn(y);
+  } else {
+    reinterpret_cast<float *>(out)[i] = y;
+  }
+}
+
+template <int G, int LPT>
+__global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeArgs a) {
+  constexpr int E = kHeadDim / LPT;      // d-elements per lane
+  constexpr int NV = E / 8;              // 16-byte vectors per lane per row
+  constexpr int TPP = kWave / LPT;       // token slots per pass
+  constexpr int NPASS = kPageTokens / TPP;
+  static_assert(NPASS >= 1 && NV >= 1, "bad lane layout");
+
+  __shared__ float s_o[kDecWaves][G][kHeadDim];
+  __shared__ float s_m[kDecWaves][G];
+  __shared__ float s_l[kDecWaves][G];
+  __shared__ int s_last;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tg = lane / LPT;
+  const int seg = lane % LPT;
+  const int bh = blockIdx.y;
+  const int split = blockIdx.x;
+  const int b = bh / a.H_kv;
+  const int h = bh - b * a.H_kv;
+  const int ctx = a.ctx_lens[b];
+
+  const bool listed = a.page_idx != nullptr && (a.accept == nullptr || a.accept[bh] != 0);
+  int n, pps;
+  if (listed) {
+    n = min(max(a.n_pages[bh], 0), a.max_sel);
+    pps = a.pps_sel;
+  } else {
+    n = max(0, min(n_valid_pages(ctx, kPageTokens), a.W));
+    pps = a.pps_all;
+  }
+  const int r0 = split * pps;
+  const int r1 = min(n, r0 + pps);
+
+  if (r0 < r1) {
+    float m[G], l[G], o[G][E];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = -INFINITY;
+      l[g] = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[g][e] = 0.f;
+    }
+    uint4 qv[G][NV];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        qv[g][v] = *reinterpret_cast<const uint4 *>(
+            a.q + b * a.q_sb + (int64_t)(h * G + g) * a.q_sh + seg * E + v * 8);
+
+    const int64_t row_stride = (int64_t)a.H_kv * kHeadDim;  // between tokens
+    const int32_t *idx_row = listed ? a.page_idx + (int64_t)bh * a.idx_stride : nullptr;
+
+    for (int r = r0 + wave; r < r1; r += kDecWaves) {
+      const int lp = listed ? idx_row[r] : r;
+      int ntok = 0;
+      int64_t base = 0;
+      if (lp >= 0 && lp < a.W) {
+        const int phys = a.block_tables[b * a.bt_sb + lp];
+        if (phys >= 0 && phys < a.num_blocks) {
+          ntok = min(kPageTokens, ctx - lp * kPageTokens);
+          base = ((int64_t)phys * kPageTokens * a.H_kv + h) * kHeadDim + seg * E;
+        }
+      }
+      if (ntok <= 0) continue;  // no valid token: contributes nothing
+
+      uint4 kr[NPASS][NV], vr[NPASS][NV];
+#pragma unroll
+      for (int ps = 0; ps < NPASS; ++ps) {
+        const int64_t off = base + (int64_t)(ps * TPP + tg) * row_stride;
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+          kr[ps][v] = *reinterpret_cast<const uint4 *>(a.k_cache + off + v * 8);
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+          vr[ps][v] = *reinterpret_cast<const uint4 *>(a.v_cache + off + v * 8);
+      }
+
+      float s[NPASS][G];
+#pragma unroll
+      for (int ps = 0; ps < NPASS; ++ps) {
+        const bool valid = ps * TPP + tg < ntok;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float acc = 0.f;
+#pragma unroll
+          for (int v = 0; v < NV; ++v) acc = dot8_bf16(kr[ps][v], qv[g][v], acc);
+          acc = group_sum<LPT>(acc) * a.scale;
+          s[ps][g] = valid ? acc : -INFINITY;
+        }
+      }
+
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float pm = s[0][g];
+#pragma unroll
+        for (int ps = 1; ps < NPASS; ++ps) pm = fmaxf(pm, s[ps][g]);
+        pm = wave_max_from_groups<LPT>(pm);
+        if (pm > m[g]) {  // wave-uniform
+          const float alpha = fast_exp(m[g] - pm);
+          l[g] *= alpha;
+#pragma unroll
+          for (int e = 0; e < E; ++e) o[g][e] *= alpha;
+          m[g] = pm;
+        }
+#pragma unroll
+        for (int ps = 0; ps < NPASS; ++ps) {
+          const float p = fast_exp(s[ps][g] - m[g]);
+          l[g] += p;
+#pragma unroll
+          for (int v = 0; v < NV; ++v) {
+            const uint4 w = vr[ps][v];
+            o[g][v * 8 + 0] += p * bf16_lo(w.x);
+            o[g][v * 8 + 1] += p * bf16_hi(w.x);
+            o[g][v * 8 + 2] += p * bf16_lo(w.y);
+            o[g][v * 8 + 3] += p * bf16_hi(w.y);
+            o[g][v * 8 + 4] += p * bf16_lo(w.z);
+            o[g][v * 8 + 5] += p * bf16_hi(w.z);
+            o[g][v * 8 + 6] += p * bf16_lo(w.w);
+            o[g][v * 8 + 7] += p * bf16_hi(w.w);
+          }
+        }
+      }
+    }
+
+    // Sum the token slots of the wave (lanes that share a d-segment).
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      l[g] = sum_across_groups<LPT>(l[g]);
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[g][e] = sum_across_groups<LPT>(o[g][e]);
+    }
+    if (tg == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < E; ++e) s_o[wave][g][seg * E + e] = o[g][e];
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Merge the four waves and store this workgroup's partial state.
+  if (r0 < r1) {
+    float *my_part = a.part + ((int64_t)bh * a.n_splits + split) * G * kPartStride;
+    for (int i = threadIdx.x; i < G * kHeadDim; i += kDecThreads) {
+      const int g = i / kHeadDim, d = i - g * kHeadDim;
+      float M = s_m[0][g];
+#pragma unroll
+      for (int w = 1; w < kDecWaves; ++w) M = fmaxf(M, s_m[w][g]);
+      float O = 0.f, L = 0.f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < kDecWaves; ++w) {
+          const float mw = s_m[w][g];
+          if (mw != -INFINITY) {
+            const float f = fast_exp(mw - M);
+            O += s_o[w][g][d] * f;
+            L += s_l[w][g] * f;
+          }
+        }
+      }
+      my_part[g * kPartStride + d] = O;
+      if (d == 0) {
+        my_part[g * kPartStride + kHeadDim] = M;
+        my_part[g * kPartStride + kHeadDim + 1] = L;
+      }
+    }
+  }
+
+  // Completion counter: the last workgroup of this head merges all partials.
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = atomicAdd(&a.counters[bh], 1u) == (uint32_t)(a.n_splits - 1);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+
+  const int n_act = (n + pps - 1) / pps;
+  const float *hp = a.part + (int64_t)bh * a.n_splits * G * kPartStride;
+  for (int i = threadIdx.x; i < G * kHeadDim; i += kDecThreads) {
+    const int g = i / kHeadDim, d = i - g * kHeadDim;
+    float M = -INFINITY;
+    for (int sp = 0; sp < n_act; ++sp)
+      M = fmaxf(M, hp[(sp * G + g) * kPartStride + kHeadDim]);
+    float O = 0.f, L = 0.f;
+    if (M != -INFINITY) {
+      for (int sp = 0; sp < n_act; ++sp) {
+        const float *ps = hp + (sp * G + g) * kPartStride;
+        const float ms = ps[kHeadDim];
+        if (ms != -INFINITY) {
+          const float f = fast_exp(ms - M);
+          O += ps[d] * f;
+          L += ps[kHeadDim + 1] * f;
+        }
+      }
+    }
+    const int64_t qrow = (int64_t)bh * G + g;  // == b * H_q + h * G + g
+    if (a.o_unnorm != nullptr) {
+      a.o_unnorm[qrow * kHeadDim + d] = O;
+      if (d == 0) {
+        a.m_out[qrow] = M;
+        a.l_out[qrow] = L;
+      }
+    }
+    if (a.out != nullptr) store_out(a.out, a.out_dtype, qrow * kHeadDim + d, O / fmaxf(L, 1e-6f));
+  }
+  if (threadIdx.x == 0) {
+    a.counters[bh] = 0u;
+    if (a.work != nullptr) {
+      atomicAdd(&a.work[0], (unsigned long long)n);
+      atomicAdd(&a.work[1], (unsigned long long)max(0, n_valid_pages(ctx, kPageTokens)));
+    }
+  }
+}
+
+__global__ void fill_zero_kernel(uint32_t *p, size_t n_words) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words;
+       i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+struct DecodePlan {
+  int pps_sel, pps_all, n_splits;
+};
+
+// Pages per split: spread the heads over ~kTargetWorkgroups workgroups with
+// at least two pages per wave.
+static DecodePlan plan_decode(int B, int H_kv, int max_sel, int W, bool listed,
+                              bool all_pages) {
+  const int heads = B * H_kv;
+  const int wg_per_head = heads >= kTargetWorkgroups ? 1 : kTargetWorkgroups / heads;
+  auto pps_for = [&](int pages) {
+    int pps = (pages + wg_per_head - 1) / wg_per_head;
+    if (pps < kMinPagesPerSplit) pps = kMinPagesPerSplit;
+    return (pps + kDecWaves - 1) / kDecWaves * kDecWaves;
+  };
+  DecodePlan p;
+  p.pps_sel = pps_for(listed ? max_sel : 0);
+  p.pps_all = pps_for(all_pages ? W : 0);
+  const int s1 = listed ? (max_sel + p.pps_sel - 1) / p.pps_sel : 0;
+  const int s2 = all_pages ? (W + p.pps_all - 1) / p.pps_all : 0;
+  p.n_splits = s1 > s2 ? s1 : s2;
+  if (p.n_splits < 1) p.n_splits = 1;
+  return p;
+}
+
+static size_t counters_bytes(int heads) { return ((size_t)heads * 4 + 255) / 256 * 256; }
+
+static size_t workspace_bytes_for(int B, int H_q, int H_kv, int max_sel, int W, bool listed,
+                                  bool all_pages) {
+  const int heads = B * H_kv;
+  const int G = H_q / H_kv;
+  const DecodePlan p = plan_decode(B, H_kv, max_sel, W, listed, all_pages);
+  return counters_bytes(heads) + (size_t)heads * p.n_splits * G * kPartStride * sizeof(float);
+}
+
+// Lanes per token row, chosen so that the o accumulators stay at <= 64
+// VGPRs for every group size.
+template <int G>
+struct LanesPerRow {
+  static constexpr int value = G <= 2 ? 4 : (G <= 4 ? 8 : 16);
+};
+
+static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_kv, int D,
+                         int block_size, int W, bool listed, bool all_pages,
+                         void *workspace, size_t workspace_bytes, hipStream_t st) {
+  CVSA_REQUIRE(a.q && a.k_cache && a.v_cache && a.block_tables && a.ctx_lens,
+               CVSA_ERR_INVALID, "%s: null pointer argument", name);
+  CVSA_REQUIRE(B > 0 && B * (int64_t)H_kv <= 65535 && W > 0 && a.num_blocks > 0,
+               CVSA_ERR_INVALID, "%s: bad sizes B=%d H_kv=%d W=%d", name, B, H_kv, W);
+  CVSA_REQUIRE(H_kv > 0 && H_q > 0 && H_q % H_kv == 0, CVSA_ERR_INVALID,
+               "%s: H_q=%d is not a multiple of H_kv=%d", name, H_q, H_kv);
+  const int G = H_q / H_kv;
+  CVSA_REQUIRE(G >= 1 && G <= 8, CVSA_ERR_UNSUPPORTED,
+               "%s: GQA group size %d not in 1..8", name, G);
+  CVSA_REQUIRE(D == kHeadDim && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
+               "%s: only D=128, block_size=16 are supported (got D=%d, bs=%d)", name, D,
+               block_size);
+  CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
+               kMaxPages);
+  CVSA_REQUIRE(a.bt_sb >= W, CVSA_ERR_INVALID, "%s: block-table row stride %lld < W=%d",
+               name, (long long)a.bt_sb, W);
+  CVSA_REQUIRE(((uintptr_t)a.q & 15) == 0 && a.q_sb % 8 == 0 && a.q_sh % 8 == 0 &&
+                   ((uintptr_t)a.k_cache & 15) == 0 && ((uintptr_t)a.v_cache & 15) == 0,
+               CVSA_ERR_INVALID,
+               "%s: q / caches must be 16-byte aligned with strides that are multiples "
+               "of 8 elements",
+               name);
+  if (listed) {
+    CVSA_REQUIRE(a.page_idx && a.n_pages, CVSA_ERR_INVALID,
+                 "%s: page_indices / n_per_head missing", name);
+    CVSA_REQUIRE(a.max_sel >= 0 && a.max_sel <= kMaxPages && a.idx_stride >= a.max_sel,
+                 CVSA_ERR_INVALID, "%s: bad selection width %d (row stride %lld)", name,
+                 a.max_sel, (long long)a.idx_stride);
+  }
+  const bool want_unnorm = a.o_unnorm || a.m_out || a.l_out;
+  CVSA_REQUIRE(!want_unnorm || (a.o_unnorm && a.m_out && a.l_out), CVSA_ERR_INVALID,
+               "%s: o_unnorm, m_out and l_out must be given together", name);
+  CVSA_REQUIRE(want_unnorm || a.out, CVSA_ERR_INVALID, "%s: no output requested", name);
+  CVSA_REQUIRE(a.out == nullptr || (a.out_dtype >= CVSA_DTYPE_BF16 &&
+                                    a.out_dtype <= CVSA_DTYPE_FP32),
+               CVSA_ERR_INVALID, "%s: bad output dtype %d", name, a.out_dtype);
+
+  const DecodePlan p = plan_decode(B, H_kv, listed ? a.max_sel : 0, W, listed, all_pages);
+  const size_t need = workspace_bytes_for(B, H_q, H_kv, listed ? a.max_sel : 0, W, listed,
+                                          all_pages);
+  CVSA_REQUIRE(workspace != nullptr && workspace_bytes >= need &&
+                   ((uintptr_t)workspace & 255) == 0,
+               CVSA_ERR_WORKSPACE,
+               "%s: workspace of %zu bytes (256-byte aligned) required, got %zu", name,
+               need, workspace_bytes);
+  a.pps_sel = p.pps_sel;
+  a.pps_all = p.pps_all;
+  a.n_splits = p.n_splits;
+  a.W = W;
+  a.H_kv = H_kv;
+  a.scale = (float)pow((double)D, -0.5);
+  a.counters = reinterpret_cast<uint32_t *>(workspace);
+  a.part = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) +
+                                     counters_bytes(B * H_kv));
+  const dim3 grid(p.n_splits, B * H_kv);
+  switch (G) {
+#define CVSA_DEC_CASE(GG)                                                                 \
+  case GG:                                                                                \
+    hipLaunchKernelGGL((paged_decode_kernel<GG, LanesPerRow<GG>::value>), grid,          \
+                       dim3(kDecThreads), 0, st, a);                                      \
+    break;
+    CVSA_DEC_CASE(1)
+    CVSA_DEC_CASE(2)
+    CVSA_DEC_CASE(3)
+    CVSA_DEC_CASE(4)
+    CVSA_DEC_CASE(5)
+    CVSA_DEC_CASE(6)
+    CVSA_DEC_CASE(7)
+    CVSA_DEC_CASE(8)
+#undef CVSA_DEC_CASE
+    default:
+      break;
+  }
+  return cvsa_host::check_launch(name);
+}
+
+static DecodeArgs base_args(const uint16_t *q, int64_t q_sb, int64_t q_sh,
+                            const uint16_t *k_cache, const uint16_t *v_cache,
+                            int64_t num_blocks, const int32_t *block_tables, int64_t bt_sb,
+                            const int32_t *context_lens, float *o_unnorm, float *m_out,
+                            float *l_out, void *out, int32_t out_dtype, int64_t *work) {
+  DecodeArgs a{};
+  a.work = reinterpret_cast<unsigned long long *>(work);
+  a.q = q;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.num_blocks = num_blocks;
+  a.block_tables = block_tables;
+  a.bt_sb = bt_sb;
+  a.ctx_lens = context_lens;
+  a.o_unnorm = o_unnorm;
+  a.m_out = m_out;
+  a.l_out = l_out;
+  a.out = out;
+  a.out_dtype = out_dtype;
+  return a;
+}
+
+}  // namespace cvsa
+
+using namespace cvsa;
+
+extern "C" size_t cvsa_decode_workspace_bytes(int32_t B, int32_t H_q, int32_t H_kv,
+                                              int32_t D, int32_t max_sel_pages, int32_t W,
+                                              int32_t all_pages) {
+  (void)D;
+  if (B <= 0 || H_kv <= 0 || H_q <= 0 || H_q % H_kv != 0 || W <= 0 || max_sel_pages < 0)
+    return 0;
+  const bool listed = max_sel_pages > 0;
+  return workspace_bytes_for(B, H_q, H_kv, max_sel_pages, W, listed, all_pages != 0);
+}
+
+extern "C" int cvsa_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
+  CVSA_REQUIRE(workspace && ((uintptr_t)workspace & 3) == 0 && workspace_bytes % 4 == 0,
+               CVSA_ERR_INVALID, "workspace_init: workspace must be 4-byte aligned and sized");
+  const size_t words = workspace_bytes / 4;
+  if (words == 0) return CVSA_OK;
+  size_t blocks = (words + 255) / 256;
+  if (blocks > 1024) blocks = 1024;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<uint32_t *>(workspace), words);
+  return cvsa_host::check_launch("workspace_init");
+}
+
+extern "C" int cvsa_sparse_decode(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
+                                  const uint16_t *k_cache, const uint16_t *v_cache,
+                                  int64_t num_blocks, const int32_t *block_tables,
+                                  int64_t bt_stride_b, const int32_t *context_lens,
+                                  const int32_t *page_indices, int64_t idx_stride,
+                                  const int32_t *n_per_head, int32_t max_selected,
+                                  int32_t B, int32_t H_q, int32_t H_kv, int32_t D,
+                                  int32_t block_size, int32_t W, float *o_unnorm,
+                                  float *m_out, float *l_out, void *out, int32_t out_dtype,
+                                  int64_t *work, void *workspace, size_t workspace_bytes,
+                                  void *stream) {
+  DecodeArgs a = base_args(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                           block_tables, bt_stride_b, context_lens, o_unnorm, m_out, l_out,
+                           out, out_dtype, work);
+  a.page_idx = page_indices;
+  a.idx_stride = idx_stride;
+  a.max_sel = max_selected;
+  a.n_pages = n_per_head;
+  if (page_indices == nullptr)
+    return cvsa_host::fail(CVSA_ERR_INVALID, "sparse_decode: page_indices is NULL");
+  return launch_decode("sparse_decode", a, B, H_q, H_kv, D, block_size, W, true, false,
+                       workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int cvsa_dense_decode(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
+                                 const uint16_t *k_cache, const uint16_t *v_cache,
+                                 int64_t num_blocks, const int32_t *block_tables,
+                                 int64_t bt_stride_b, const int32_t *context_lens, int32_t B,
+                                 int32_t H_q, int32_t H_kv, int32_t D, int32_t block_size,
+                                 int32_t W, float *o_unnorm, float *m_out, float *l_out,
+                                 void *out, int32_t out_dtype, int64_t *work,
+                                 void *workspace, size_t workspace_bytes, void *stream) {
+  DecodeArgs a = base_args(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                           block_tables, bt_stride_b, context_lens, o_unnorm, m_out, l_out,
+                           out, out_dtype, work);
+  return launch_decode("dense_decode", a, B, H_q, H_kv, D, block_size, W, false, true,
+                       workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int cvsa_verified_decode(const uint16_t *q, int64_t q_stride_b,
+                                    int64_t q_stride_h, const uint16_t *k_cache,
+                                    const uint16_t *v_cache, int64_t num_blocks,
+                                    const int32_t *block_tables, int64_t bt_stride_b,
+                                    const int32_t *context_lens,
+                                    const int32_t *page_indices, int64_t idx_stride,
+                                    const int32_t *n_per_head, int32_t max_selected,
+                                    const uint8_t *accept, int32_t B, int32_t H_q,
+                                    int32_t H_kv, int32_t D, int32_t block_size, int32_t W,
+                                    float *o_unnorm, float *m_out, float *l_out, void *out,
+                                    int32_t out_dtype, int64_t *work, void *workspace,
+                                    size_t workspace_bytes, void *stream) {
+  DecodeArgs a = base_args(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                           block_tables, bt_stride_b, context_lens, o_unnorm, m_out, l_out,
+                           out, out_dtype, work);
+  a.page_idx = page_indices;
+  a.idx_stride = idx_stride;
+  a.max_sel = max_selected;
+  a.n_pages = n_per_head;
+  a.accept = accept;
+  if (page_indices == nullptr || accept == nullptr)
+    return cvsa_host::fail(CVSA_ERR_INVALID,
+                           "verified_decode: page_indices and accept are required");
+  return launch_decode("verified_decode", a, B, H_q, H_kv, D, block_size, W, true, true,
+                       workspace, workspace_bytes, (hipStream_t)stream);
+}

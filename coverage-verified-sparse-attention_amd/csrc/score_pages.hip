@@ -1,0 +1,173 @@
+// Page scoring: page_scores[b,h,p] = max over valid tokens of (q_rep . K) * D^-0.5.
+//
+// Follows triton_score_pages (cvsa/kernels/page_scores.py:77-119, kernel
+// :12-74): q_rep is the bf16-rounded GQA group mean of q (:94-95), the dot is
+// accumulated in fp32 and scaled after the sum (:67), masked tokens are -inf
+// (:68) and pages starting at or beyond the context are -inf (:44-47).
+//
+// MI355X mapping: the reference runs one tiny program per (b, kv-head, page).
+// Here one wave streams a whole page for all KV heads: a page is
+// block_size x H_kv rows of 256 B stored back to back (32 KiB for H_kv = 8),
+// so every 16-byte lane load is part of a fully coalesced 1 KiB wave load.
+// Lane l covers row (l >> 4) of each group of four rows and d-segment
+// (l & 15) * 8; the 16 lanes of a DPP row hold one (token, head) row and
+// reduce its dot product with four fused DPP adds.
+#include "cvsa_common.h"
+
+namespace cvsa {
+
+template <int HKV>
+__global__ __launch_bounds__(256) void score_pages_kernel(
+    const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh,
+    const uint16_t *__restrict__ k_cache, int64_t num_blocks,
+    const int32_t *__restrict__ block_tables, int64_t bt_sb,
+    const int32_t *__restrict__ context_lens, float *__restrict__ scores,
+    int W, int G, float inv_g, float scale, int ppw) {
+  constexpr int NHL = HKV >= 4 ? HKV / 4 : 1;      // heads held per lane
+  constexpr int NLOAD = kPageTokens * HKV / 4;     // 16-byte loads per lane per page
+  constexpr int PAGE_ELEMS = kPageTokens * HKV * kHeadDim;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rsub = lane >> 4;
+  const int seg = lane & 15;
+  const int b = blockIdx.y;
+  const int p_begin = (blockIdx.x * 4 + wave) * ppw;
+  if (p_begin >= W) return;
+  const int ctx = context_lens[b];
+
+  // Head of the j-th row group this lane touches.
+  auto head_of = [&](int j) { return HKV >= 4 ? 4 * j + rsub : rsub % HKV; };
+
+  // q_rep[h][seg*8 .. seg*8+8): fp32 sum over the group, times 1/G, rounded
+  // to bf16 (the bf16 result of q.view(B,H_kv,G,D).mean(2)).
+  uint4 qr[NHL];
+#pragma unroll
+  for (int j = 0; j < NHL; ++j) {
+    const int h = head_of(j);
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+    for (int g = 0; g < G; ++g) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(
+          q + b * q_sb + (int64_t)(h * G + g) * q_sh + seg * 8);
+      acc[0] += bf16_lo(v.x); acc[1] += bf16_hi(v.x);
+      acc[2] += bf16_lo(v.y); acc[3] += bf16_hi(v.y);
+      acc[4] += bf16_lo(v.z); acc[5] += bf16_hi(v.z);
+      acc[6] += bf16_lo(v.w); acc[7] += bf16_hi(v.w);
+    }
+    qr[j].x = pack_bf16x2(acc[0] * inv_g, acc[1] * inv_g);
+    qr[j].y = pack_bf16x2(acc[2] * inv_g, acc[3] * inv_g);
+    qr[j].z = pack_bf16x2(acc[4] * inv_g, acc[5] * inv_g);
+    qr[j].w = pack_bf16x2(acc[6] * inv_g, acc[7] * inv_g);
+  }
+
+  const int p_end = min(W, p_begin + ppw);
+  for (int p = p_begin; p < p_end; ++p) {
+    float *dst = scores + (int64_t)b * HKV * W + p;
+    const int ntok = min(kPageTokens, ctx - p * kPageTokens);
+    const int phys = ntok > 0 ? block_tables[b * bt_sb + p] : -1;
+    if (phys < 0 || phys >= num_blocks) {
+      // Beyond the context (or an out-of-range block id): no valid token.
+      if (seg == 0 && (HKV >= 4 || rsub < HKV)) {
+#pragma unroll
+        for (int j = 0; j < NHL; ++j) dst[(int64_t)head_of(j) * W] = -INFINITY;
+      }
+      continue;
+    }
+    const uint4 *src =
+        reinterpret_cast<const uint4 *>(k_cache + (int64_t)phys * PAGE_ELEMS) + lane;
+    uint4 kv[NLOAD];
+#pragma unroll
+    for (int i = 0; i < NLOAD; ++i) kv[i] = src[i * 64];
+
+    float mx[NHL];
+#pragma unroll
+    for (int j = 0; j < NHL; ++j) mx[j] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NLOAD; ++i) {
+      const int row = i * 4 + rsub;
+      const int t = row / HKV;
+      const int j = HKV >= 4 ? (i % NHL) : 0;
+      const float s = group_sum<16>(dot8_bf16(kv[i], qr[j], 0.f)) * scale;
+      if (t < ntok) mx[j] = fmaxf(mx[j], s);
+    }
+    // With fewer than four heads several row groups share a head.
+    if constexpr (HKV == 1) {
+      float a, c;
+      xchg16(mx[0], a, c); mx[0] = fmaxf(a, c);
+      xchg32(mx[0], a, c); mx[0] = fmaxf(a, c);
+    } else if constexpr (HKV == 2) {
+      float a, c;
+      xchg32(mx[0], a, c); mx[0] = fmaxf(a, c);
+    }
+    if (seg == 0 && (HKV >= 4 || rsub < HKV)) {
+#pragma unroll
+      for (int j = 0; j < NHL; ++j) dst[(int64_t)head_of(j) * W] = mx[j];
+    }
+  }
+}
+
+}  // namespace cvsa
+
+using namespace cvsa;
+
+extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
+                                int64_t q_stride_h, const uint16_t *k_cache,
+                                int64_t num_blocks,
+                                const int32_t *block_tables,
+                                int64_t bt_stride_b,
+                                const int32_t *context_lens, int32_t B,
+                                int32_t H_q, int32_t H_kv, int32_t D,
+                                int32_t block_size, int32_t W,
+                                float *page_scores, void *stream) {
+  CVSA_REQUIRE(q && k_cache && block_tables && context_lens && page_scores,
+               CVSA_ERR_INVALID, "score_pages: null pointer argument");
+  CVSA_REQUIRE(B > 0 && B <= 65535 && W > 0 && num_blocks > 0, CVSA_ERR_INVALID,
+               "score_pages: bad sizes B=%d W=%d num_blocks=%lld", B, W,
+               (long long)num_blocks);
+  CVSA_REQUIRE(H_kv > 0 && H_q > 0 && H_q % H_kv == 0, CVSA_ERR_INVALID,
+               "score_pages: H_q=%d is not a multiple of H_kv=%d", H_q, H_kv);
+  CVSA_REQUIRE(D == kHeadDim && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
+               "score_pages: only D=128, block_size=16 are supported (got D=%d, bs=%d)",
+               D, block_size);
+  CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
+               "score_pages: W=%d exceeds %d pages", W, kMaxPages);
+  CVSA_REQUIRE(bt_stride_b >= W, CVSA_ERR_INVALID,
+               "score_pages: block-table row stride %lld < W=%d",
+               (long long)bt_stride_b, W);
+  CVSA_REQUIRE(((uintptr_t)q & 15) == 0 && q_stride_b % 8 == 0 && q_stride_h % 8 == 0 &&
+                   ((uintptr_t)k_cache & 15) == 0,
+               CVSA_ERR_INVALID,
+               "score_pages: q / k_cache must be 16-byte aligned with strides that are "
+               "multiples of 8 elements");
+  const int G = H_q / H_kv;
+  const float inv_g = 1.0f / (float)G;
+  const float scale = (float)pow((double)D, -0.5);
+
+  // Pages per wave: keep roughly 8192 waves in flight-able work.
+  const int64_t total = (int64_t)B * W;
+  int ppw = (int)((total + 8191) / 8192);
+  ppw = ppw < 1 ? 1 : (ppw > 8 ? 8 : ppw);
+  dim3 grid((W + 4 * ppw - 1) / (4 * ppw), B);
+  hipStream_t st = (hipStream_t)stream;
+  switch (H_kv) {
+#define CVSA_SCORE_CASE(HK)                                                     \
+  case HK:                                                                      \
+    hipLaunchKernelGGL(score_pages_kernel<HK>, grid, dim3(256), 0, st, q,       \
+                       q_stride_b, q_stride_h, k_cache, (int64_t)num_blocks,    \
+                       block_tables, bt_stride_b, context_lens, page_scores, W, \
+                       G, inv_g, scale, ppw);                                   \
+    break;
+    CVSA_SCORE_CASE(1)
+    CVSA_SCORE_CASE(2)
+    CVSA_SCORE_CASE(4)
+    CVSA_SCORE_CASE(8)
+    CVSA_SCORE_CASE(16)
+#undef CVSA_SCORE_CASE
+    default:
+      return cvsa_host::fail(CVSA_ERR_UNSUPPORTED,
+                             "score_pages: H_kv=%d not in {1,2,4,8,16}", H_kv);
+  }
+  return cvsa_host::check_launch("score_pages");
+}

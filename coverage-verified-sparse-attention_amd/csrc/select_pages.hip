@@ -1,0 +1,372 @@
+// Top-k page selection and the coverage gate.
+//
+// Selection replaces the uniform-budget branch of CVSABackend._scoring_step
+// (cvsa/backend.py:737-747): the `budget` largest page scores of each
+// (b, kv-head) row.  torch.topk(sorted=False) leaves the order of its result
+// unspecified; this kernel fixes it: the set is ordered by (score desc,
+// page asc), and written in ascending page order.  Because invalid pages
+// (-inf) are exactly the pages >= n_valid, the first n_per_head =
+// min(budget, n_valid) entries are then always valid pages.
+//
+// The coverage gate follows _coverage_kernel (cvsa/kernels/coverage.py:
+// 159-215): lse_all over every page score with the -1e20 floor and the
+// +1e-30 inside the log (:183-195), lse_sel over the first n_sel selected
+// scores (:198-208), coverage = exp(lse_sel - lse_all) and accept =
+// coverage >= tau compared in fp32 (:211-212).
+//
+// One 1024-thread workgroup per (b, kv-head); thread t owns the R
+// consecutive pages [t*R, t*R + R).  The k-th largest score is found with a
+// 4-pass, 8-bit MSB radix select over order-preserving integer keys, then a
+// block scan places the selected pages in ascending order.
+#include "cvsa_common.h"
+
+namespace cvsa {
+
+constexpr int kSelThreads = 1024;
+constexpr int kSelWaves = kSelThreads / kWave;
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Reductions over the 1024-thread block.  `red` holds kSelWaves floats.
+__device__ __forceinline__ float block_max(float v, float *red) {
+  v = wave_max_from_groups<1>(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) r = fmaxf(r, red[w]);
+  return r;
+}
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+  v = wave_sum_from_groups<1>(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) r += red[w];
+  return r;
+}
+
+// Exclusive prefix sum of one uint32 per thread over the block, plus total.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *wsum,
+                                                         uint32_t &total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  __syncthreads();
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  uint32_t before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const uint32_t s = wsum[w];
+    before += (w < wave) ? s : 0u;
+    tot += s;
+  }
+  total = tot;
+  return before + incl - v;
+}
+
+// lse over a set given its fp32 maximum `mx` and sum of exp(s - M); the
+// reference floors the running max at -1e20 (coverage.py:183, :207).
+__device__ __forceinline__ float lse_from(float mx_floor, float sum) {
+  return mx_floor + logf(sum + 1e-30f);
+}
+
+template <int R>
+__global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
+    const float *__restrict__ scores, int W, int H_kv,
+    const int32_t *__restrict__ context_lens, int block_size, int budget,
+    int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
+    uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wsum[kSelWaves];
+  __shared__ float red[kSelWaves];
+  __shared__ uint32_t s_digit, s_krem;
+
+  const int bh = blockIdx.x;
+  const int b = bh / H_kv;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const float *row = scores + (int64_t)bh * W;
+  const int i0 = t * R;
+
+  float val[R];
+  uint32_t key[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = i0 + r;
+    val[r] = i < W ? row[i] : -INFINITY;
+    key[r] = order_key(val[r]);
+  }
+
+  // ---- radix select of the budget-th largest key
+  uint32_t prefix = 0, pmask = 0, krem = (uint32_t)budget;
+#pragma unroll 1
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    if (t < 256) hist[t] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (i0 + r < W && (key[r] & pmask) == prefix)
+        atomicAdd(&hist[(key[r] >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (t < 64) {
+      // Lane l holds digits 4l..4l+3; count the candidates above each digit.
+      const uint32_t c0 = hist[4 * lane], c1 = hist[4 * lane + 1];
+      const uint32_t c2 = hist[4 * lane + 2], c3 = hist[4 * lane + 3];
+      const uint32_t local = c0 + c1 + c2 + c3;
+      uint32_t suffix = local;  // inclusive sum over lanes >= l
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_down(suffix, off, 64);
+        if (lane + off < 64) suffix += o;
+      }
+      uint32_t above = suffix - local;  // candidates with a higher digit
+      const uint32_t cs[4] = {c3, c2, c1, c0};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (above < krem && above + cs[k] >= krem) {
+          s_digit = (uint32_t)(4 * lane + 3 - k);
+          s_krem = krem - above;
+        }
+        above += cs[k];
+      }
+    }
+    __syncthreads();
+    prefix |= s_digit << shift;
+    pmask |= 0xFFu << shift;
+    krem = s_krem;
+    __syncthreads();
+  }
+  const uint32_t T = prefix;  // key of the budget-th largest score
+
+  // ---- ascending-order compaction; ties at T go to the lowest pages
+  uint32_t gt = 0, eq = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (i0 + r < W) {
+      gt += key[r] > T;
+      eq += key[r] == T;
+    }
+  }
+  uint32_t total;
+  const uint32_t excl = block_exclusive_scan(gt | (eq << 16), wsum, total);
+  const uint32_t gt_before = excl & 0xFFFFu, eq_before = excl >> 16;
+  const int ctx = context_lens[b];
+  const int n_sel = min(budget, n_valid_pages(ctx, block_size));
+  uint32_t eq_seen = eq_before;
+  uint32_t pos = gt_before + min(eq_before, krem);
+  int32_t *out_row = page_indices + (int64_t)bh * budget;
+  bool counted[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    bool sel = false;
+    if (i0 + r < W) {
+      if (key[r] > T) {
+        sel = true;
+      } else if (key[r] == T) {
+        sel = eq_seen < krem;
+        ++eq_seen;
+      }
+    }
+    counted[r] = sel && (int)pos < n_sel;
+    if (sel) {
+      if ((int)pos < budget) out_row[pos] = i0 + r;  // always true for a correct select
+      ++pos;
+    }
+  }
+  if (t == 0) n_per_head[bh] = n_sel;
+
+  if (accept_out == nullptr) return;
+  // ---- coverage of the new selection
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < R; ++r) mx = fmaxf(mx, val[r]);
+  const float m_all = fmaxf(block_max(mx, red), -1e20f);
+  float se = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) se += expf(val[r] - m_all);
+  const float lse_all = lse_from(m_all, block_sum(se, red));
+
+  float ms = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < R; ++r) if (counted[r]) ms = fmaxf(ms, val[r]);
+  // Padding lanes of the reference's power-of-two selection block carry
+  // -1e20 into the max whenever n_sel is below that block (coverage.py:205).
+  float m_sel = block_max(ms, red);
+  int msel_block = 1;
+  while (msel_block < budget) msel_block <<= 1;
+  if (n_sel < msel_block) m_sel = fmaxf(m_sel, -1e20f);
+  float ss = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) if (counted[r]) ss += expf(val[r] - m_sel);
+  const float lse_sel = lse_from(m_sel, block_sum(ss, red));
+  if (t == 0) {
+    const float cov = expf(lse_sel - lse_all);
+    coverage_out[bh] = cov;
+    accept_out[bh] = cov >= tau ? 1 : 0;
+  }
+}
+
+// Coverage of a given selection (triton_check_coverage).
+template <int R>
+__global__ __launch_bounds__(kSelThreads) void check_coverage_kernel(
+    const float *__restrict__ scores, int W, const int32_t *__restrict__ selected,
+    int sel_width, int sel_block, const int32_t *__restrict__ n_per_head,
+    float tau, uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out) {
+  __shared__ float red[kSelWaves];
+  const int bh = blockIdx.x;
+  const int t = threadIdx.x;
+  const float *row = scores + (int64_t)bh * W;
+  const int i0 = t * R;
+
+  float val[R];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    val[r] = (i0 + r < W) ? row[i0 + r] : -INFINITY;
+    mx = fmaxf(mx, val[r]);
+  }
+  const float m_all = fmaxf(block_max(mx, red), -1e20f);
+  float se = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) se += expf(val[r] - m_all);
+  const float lse_all = lse_from(m_all, block_sum(se, red));
+
+  // Selected scores: entries j < n_sel of the row (coverage.py:198-208).
+  // n_sel is clamped to the row width and indices outside [0, W) read as
+  // -inf, so a malformed selection cannot read out of bounds.
+  const int n_sel = max(0, min(n_per_head[bh], sel_width));
+  const int32_t *sel = selected + (int64_t)bh * sel_width;
+  float sv[R];
+  float ms = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int j = i0 + r;
+    float v = -INFINITY;
+    if (j < n_sel) {
+      const int p = sel[j];
+      v = (p >= 0 && p < W) ? row[p] : -INFINITY;
+    }
+    sv[r] = v;
+    if (j < n_sel) ms = fmaxf(ms, v);
+  }
+  float m_sel = block_max(ms, red);
+  if (n_sel < sel_block) m_sel = fmaxf(m_sel, -1e20f);
+  float ss = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (i0 + r < n_sel) ss += expf(sv[r] - m_sel);
+  const float lse_sel = lse_from(m_sel, block_sum(ss, red));
+  if (t == 0) {
+    const float cov = expf(lse_sel - lse_all);
+    coverage_out[bh] = cov;
+    accept_out[bh] = cov >= tau ? 1 : 0;
+  }
+}
+
+static int keys_per_thread(int n) {
+  int r = 1;
+  while (r * kSelThreads < n) r <<= 1;
+  return r;
+}
+
+}  // namespace cvsa
+
+using namespace cvsa;
+
+extern "C" int cvsa_select_topk(const float *page_scores, int32_t B,
+                                int32_t H_kv, int32_t W,
+                                const int32_t *context_lens, int32_t block_size,
+                                int32_t budget, int32_t *page_indices,
+                                int32_t *n_per_head, float tau,
+                                uint8_t *accept_out, float *coverage_out,
+                                void *stream) {
+  CVSA_REQUIRE(page_scores && context_lens && page_indices && n_per_head,
+               CVSA_ERR_INVALID, "select_topk: null pointer argument");
+  CVSA_REQUIRE((accept_out == nullptr) == (coverage_out == nullptr), CVSA_ERR_INVALID,
+               "select_topk: accept_out and coverage_out must both be set or both NULL");
+  CVSA_REQUIRE(B > 0 && H_kv > 0 && W > 0 && block_size > 0, CVSA_ERR_INVALID,
+               "select_topk: bad sizes B=%d H_kv=%d W=%d bs=%d", B, H_kv, W, block_size);
+  CVSA_REQUIRE(budget >= 1 && budget <= W, CVSA_ERR_INVALID,
+               "select_topk: budget=%d must be in [1, W=%d]", budget, W);
+  CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
+               "select_topk: W=%d exceeds %d pages", W, kMaxPages);
+  const int R = keys_per_thread(W);
+  const dim3 grid(B * H_kv);
+  hipStream_t st = (hipStream_t)stream;
+  switch (R) {
+#define CVSA_SEL_CASE(RR)                                                        \
+  case RR:                                                                       \
+    hipLaunchKernelGGL(select_topk_kernel<RR>, grid, dim3(kSelThreads), 0, st,    \
+                       page_scores, W, H_kv, context_lens, block_size, budget,    \
+                       page_indices, n_per_head, tau, accept_out, coverage_out);  \
+    break;
+    CVSA_SEL_CASE(1)
+    CVSA_SEL_CASE(2)
+    CVSA_SEL_CASE(4)
+    CVSA_SEL_CASE(8)
+    CVSA_SEL_CASE(16)
+    CVSA_SEL_CASE(32)
+#undef CVSA_SEL_CASE
+    default:
+      return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "select_topk: W=%d too large", W);
+  }
+  return cvsa_host::check_launch("select_topk");
+}
+
+extern "C" int cvsa_check_coverage(const float *page_scores, int32_t B,
+                                   int32_t H_kv, int32_t W,
+                                   const int32_t *selected, int64_t sel_stride,
+                                   const int32_t *n_per_head, float tau,
+                                   uint8_t *accept_out, float *coverage_out,
+                                   void *stream) {
+  CVSA_REQUIRE(page_scores && selected && n_per_head && accept_out && coverage_out,
+               CVSA_ERR_INVALID, "check_coverage: null pointer argument");
+  CVSA_REQUIRE(B > 0 && H_kv > 0 && W > 0 && sel_stride > 0, CVSA_ERR_INVALID,
+               "check_coverage: bad sizes B=%d H_kv=%d W=%d sel_stride=%lld", B, H_kv,
+               W, (long long)sel_stride);
+  CVSA_REQUIRE(W <= kMaxPages && sel_stride <= kMaxPages, CVSA_ERR_UNSUPPORTED,
+               "check_coverage: W=%d / selection width %lld exceed %d", W,
+               (long long)sel_stride, kMaxPages);
+  // The reference pads the selection to a power of two (coverage.py:234-237).
+  int sel_block = 1;
+  while (sel_block < sel_stride) sel_block <<= 1;
+  const int R = keys_per_thread(W > sel_block ? W : sel_block);
+  const dim3 grid(B * H_kv);
+  hipStream_t st = (hipStream_t)stream;
+  const int width = (int)sel_stride;
+  switch (R) {
+#define CVSA_COV_CASE(RR)                                                       \
+  case RR:                                                                      \
+    hipLaunchKernelGGL(check_coverage_kernel<RR>, grid, dim3(kSelThreads), 0, st, \
+                       page_scores, W, selected, width, sel_block,               \
+                       n_per_head, tau, accept_out, coverage_out);               \
+    break;
+    CVSA_COV_CASE(1)
+    CVSA_COV_CASE(2)
+    CVSA_COV_CASE(4)
+    CVSA_COV_CASE(8)
+    CVSA_COV_CASE(16)
+    CVSA_COV_CASE(32)
+#undef CVSA_COV_CASE
+    default:
+      return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "check_coverage: W=%d too large", W);
+  }
+  return cvsa_host::check_launch("check_coverage");
+}

@@ -1,0 +1,492 @@
+"""Coverage-Verified Sparse Attention (CVSA) backend on MI355X.
+
+Sparse attention as draft, coverage as acceptance criterion, and recovery on
+low-coverage heads.  Drop-in for the reference's cvsa/backend.py
+(CVSABackend :45-881): same constructor keywords and defaults, the same
+backend protocol (``__call__``, ``reset``, ``step_done``, ``get_stats``,
+``enable_timing``), the same scheduling (fixed interval R, lazy check every
+M steps, optional coverage-only steps), the same statistics keys and the
+tracing attributes ``_cached_selection``, ``_last_accept_mask``,
+``_last_expanded_selection`` and ``_dense_layers``.
+
+What runs per layer call (HIP kernels from cvsa.ops):
+  scoring step  score_pages -> select_topk (+ coverage gate) -> verified_decode
+  lazy check    score_pages -> check_coverage -> (sparse decode | scoring step)
+  reuse step    sparse decode over the cached selection
+The reference's draft decode, complement, complement decode and LSE merge
+collapse into verified_decode: accepted heads attend their selected pages,
+rejected heads attend every valid page in one pass, which equals the LSE
+merge of draft and complement.  The effective-budget counters are
+accumulated by the decode kernels on the device, and in lazy mode the
+scoring step needs no host synchronisation; the only host reads left are
+the ones whose result decides which kernels run next (the lazy accept-all
+check, approximate recovery) or that feed host-side counters in the fixed
+interval schedule, as in the reference.
+
+Not implemented here (the constructor raises NotImplementedError): the
+alternative selectors of the reference (adaptive_selection,
+static_budget_table, selector="quest", top_p, light_normalizer).
+"""
+from __future__ import annotations
+
+from typing import Dict, List, Optional, Set, Tuple
+
+import torch
+
+from . import ops
+from .runtime.dense import DenseAttentionBackend
+
+
+class _PendingComplement:
+    """Complement pages of a scoring step, computed only if someone reads
+    ``_last_expanded_selection`` (the reference builds them eagerly)."""
+
+    __slots__ = ("accept", "page_indices", "n_per_head", "context_lens", "block_size")
+
+    def __init__(self, accept, page_indices, n_per_head, context_lens, block_size):
+        self.accept = accept
+        self.page_indices = page_indices
+        self.n_per_head = n_per_head
+        self.context_lens = context_lens
+        self.block_size = block_size
+
+    def resolve(self):
+        if bool(self.accept.all()):
+            return None
+        return ops.compute_complement(self.page_indices, self.n_per_head, self.context_lens,
+                                      self.block_size, self.accept)
+
+
+class CVSABackend:
+    """Draft with sparse attention, verify with coverage, recover rejected heads."""
+
+    def __init__(
+        self,
+        num_kv_heads: int,
+        num_q_heads: int,
+        head_dim: int,
+        block_size: int,
+        num_layers: int = 32,
+        budget_pct: float = 0.10,
+        reuse_interval: int = 16,
+        coverage_threshold: float = 0.90,
+        dense_layers: Optional[List[int]] = None,
+        lazy: bool = False,
+        check_interval: Optional[int] = None,
+        coverage_interval: Optional[int] = None,
+        approx_recovery_pct: Optional[float] = None,
+        adaptive_selection: bool = False,
+        adaptive_floor_ratio: float = 0.5,
+        random_reject_prob: Optional[float] = None,
+        static_budget_table: Optional[Dict[int, List[float]]] = None,
+        selector: str = "exact",
+        top_p: Optional[float] = None,
+        light_normalizer: bool = False,
+    ):
+        self.num_kv_heads = num_kv_heads
+        self.num_q_heads = num_q_heads
+        self.head_dim = head_dim
+        self.block_size = block_size
+        self.num_layers = num_layers
+        self.num_q_per_kv = num_q_heads // num_kv_heads
+        self.budget_pct = budget_pct
+        self.reuse_interval = reuse_interval
+        self.tau = coverage_threshold
+
+        self._dense_layers: Set[int] = set(dense_layers or [])
+        self._dense_backend = None
+        if self._dense_layers:
+            self._dense_backend = DenseAttentionBackend(num_kv_heads, num_q_heads, head_dim,
+                                                        block_size)
+        self.approx_recovery_pct = approx_recovery_pct
+        self.lazy = lazy
+        self.check_interval = check_interval or 1
+        self.coverage_interval = coverage_interval or self.check_interval
+        self.adaptive_selection = adaptive_selection
+        self.adaptive_floor_ratio = adaptive_floor_ratio
+        self.random_reject_prob = random_reject_prob
+        self.static_budget_table = None
+        if static_budget_table is not None:
+            self.static_budget_table = {int(layer): torch.as_tensor(f, dtype=torch.float32)
+                                        for layer, f in static_budget_table.items()}
+        # Validation in the reference's order (backend.py:150-151, 163-166, 176-177).
+        if selector not in ("exact", "quest"):
+            raise ValueError(f"Unknown selector: {selector!r}")
+        self.selector = selector
+        if light_normalizer and selector != "quest":
+            raise ValueError(
+                "light_normalizer=True requires selector='quest' "
+                "(the sketch supplies both selection and normalizer)")
+        self.light_normalizer = light_normalizer
+        if top_p is not None and not (0.0 < top_p < 1.0):
+            raise ValueError(f"top_p must be in (0, 1), got {top_p}")
+        self.top_p = top_p
+        unsupported = [name for name, on in (
+            ("adaptive_selection", adaptive_selection),
+            ("static_budget_table", static_budget_table is not None),
+            ("selector='quest'", selector == "quest"),
+            ("top_p", top_p is not None),
+            ("light_normalizer", light_normalizer)) if on]
+        if unsupported:
+            raise NotImplementedError(
+                "CVSABackend on MI355X implements the exact page scorer with a uniform "
+                f"budget; not available: {', '.join(unsupported)}")
+
+        self._last_accept_mask: Dict[int, Optional[torch.Tensor]] = {}
+        self._expanded_store: Dict[int, object] = {}
+        self._attn_work: Optional[torch.Tensor] = None
+        self._attn_work_max: Optional[torch.Tensor] = None
+        self._work_buf: Optional[torch.Tensor] = None
+
+        self._step = 0
+        self._reuse_state: Dict[int, Tuple[torch.Tensor, torch.Tensor, int]] = {}
+        self._cached_selection: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
+        self._cached_page_scores: Dict[int, torch.Tensor] = {}
+
+        self._accept_counts = 0
+        self._reject_counts = 0
+        self._total_scoring_steps = 0
+        self._total_coverage_checks = 0
+        self._per_head_accept_sum = 0
+        self._per_head_total = 0
+        self._dense_layer_steps = 0
+
+        self._track_timing = False
+        self._kernel_times_ms: Dict[str, float] = {
+            "scoring": 0.0, "coverage": 0.0, "sparse_draft": 0.0,
+            "ar_recovery": 0.0, "lse_merge": 0.0, "complement": 0.0,
+        }
+        self._kernel_counts: Dict[str, int] = {k: 0 for k in self._kernel_times_ms}
+        self._pending_events: list = []
+
+    # ------------------------------------------------------------ tracing
+    @property
+    def _last_expanded_selection(self) -> Dict[int, Optional[Tuple[torch.Tensor, torch.Tensor]]]:
+        """Expanded (approximate recovery) or complement (exact recovery) pages
+        of the last scoring step per layer, present only when a head was
+        rejected (backend.py:815, :842).  Complements are built on first read."""
+        for layer in list(self._expanded_store):
+            v = self._expanded_store[layer]
+            if isinstance(v, _PendingComplement):
+                v = v.resolve()
+                if v is None:
+                    del self._expanded_store[layer]
+                    continue
+                self._expanded_store[layer] = v
+        return dict(self._expanded_store)
+
+    # ------------------------------------------------------------ timing
+    def enable_timing(self, track: bool = True):
+        """Per-kernel event timing on/off (backend.py:225-228)."""
+        self._track_timing = track
+
+    def _time_kernel(self, name: str, fn, *args, **kwargs):
+        if not self._track_timing:
+            return fn(*args, **kwargs)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        result = fn(*args, **kwargs)
+        end.record()
+        self._pending_events.append((name, start, end))
+        return result
+
+    def _flush_timing(self):
+        if not self._track_timing or not self._pending_events:
+            return
+        torch.cuda.synchronize()
+        for name, start, end in self._pending_events:
+            self._kernel_times_ms[name] += start.elapsed_time(end)
+            self._kernel_counts[name] += 1
+        self._pending_events.clear()
+
+    # ------------------------------------------------------------ protocol
+    def reset(self):
+        """backend.py:252-272"""
+        self._step = 0
+        self._reuse_state = {}
+        self._cached_selection = {}
+        self._cached_page_scores = {}
+        self._last_accept_mask = {}
+        self._expanded_store = {}
+        if self._attn_work is not None:
+            self._attn_work.zero_()
+            self._attn_work_max.zero_()
+        self._accept_counts = 0
+        self._reject_counts = 0
+        self._total_scoring_steps = 0
+        self._total_coverage_checks = 0
+        self._per_head_accept_sum = 0
+        self._per_head_total = 0
+        self._dense_layer_steps = 0
+        for k in self._kernel_times_ms:
+            self._kernel_times_ms[k] = 0.0
+            self._kernel_counts[k] = 0
+        self._pending_events.clear()
+
+    @property
+    def is_scoring_step(self):
+        return self._step % self.reuse_interval == 0
+
+    def step_done(self, layer_idx: int, num_layers: int):
+        if layer_idx == num_layers - 1:
+            self._step += 1
+
+    def get_stats(self) -> dict:
+        """Same keys and formulas as backend.py:282-311."""
+        total_checks = max(self._total_coverage_checks, self._total_scoring_steps, 1)
+        stats = {
+            "total_scoring_steps": self._total_scoring_steps,
+            "total_coverage_checks": self._total_coverage_checks,
+            "all_accepted_pct": self._accept_counts / max(total_checks, 1) * 100,
+            "some_rejected_pct": self._reject_counts / max(total_checks, 1) * 100,
+            "per_head_accept_rate": self._per_head_accept_sum / max(self._per_head_total, 1) * 100,
+            "total_decode_steps": self._step,
+            "lazy": self.lazy,
+            "check_interval": self.check_interval if self.lazy else None,
+            "rescore_rate": (self._total_scoring_steps / max(self._total_coverage_checks, 1) * 100
+                             if self.lazy else 100.0),
+        }
+        if self._attn_work is not None:
+            pages_attended = int(self._attn_work.item())
+            pages_max = int(self._attn_work_max.item())
+            if pages_max > 0:
+                stats["effective_budget_pct"] = pages_attended / pages_max * 100
+                stats["total_pages_attended"] = pages_attended
+                stats["total_pages_max"] = pages_max
+        if self._track_timing:
+            self._flush_timing()
+            n_decode = max(self._step, 1)
+            stats["kernel_times_ms_total"] = dict(self._kernel_times_ms)
+            stats["kernel_counts"] = dict(self._kernel_counts)
+            stats["kernel_ms_per_decode_step"] = {
+                k: self._kernel_times_ms[k] / n_decode for k in self._kernel_times_ms}
+        return stats
+
+    def __call__(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
+        """backend.py:313-366"""
+        self._last_accept_mask.pop(layer_idx, None)
+        self._expanded_store.pop(layer_idx, None)
+
+        if layer_idx in self._dense_layers:
+            # Dense attends every valid page on every head (:327-333).
+            self._dense_layer_steps += 1
+            work = self._decode_work(context_lens)
+            out = self._dense_backend(q, k_cache, v_cache, block_tables, context_lens,
+                                      layer_idx, work=work)
+            if work is None:
+                n_valid = ((context_lens.float() - 1) / self.block_size).long() + 1
+                self._record_work(context_lens, n_valid.sum() * self.num_kv_heads)
+            return out
+
+        if self.lazy:
+            is_scoring_step = self._step % self.check_interval == 0
+            is_coverage_step = self._step % self.coverage_interval == 0
+            has_cache = layer_idx in self._reuse_state
+            has_scores = layer_idx in self._cached_page_scores
+            if is_scoring_step:
+                return self._lazy_step(q, k_cache, v_cache, block_tables, context_lens,
+                                       layer_idx)
+            elif is_coverage_step and has_cache and has_scores:
+                return self._coverage_only_step(q, k_cache, v_cache, block_tables,
+                                                context_lens, layer_idx)
+            elif has_cache:
+                return self._reuse_step(q, k_cache, v_cache, block_tables, context_lens,
+                                        layer_idx)
+            else:
+                return self._lazy_step(q, k_cache, v_cache, block_tables, context_lens,
+                                       layer_idx)
+        elif self.is_scoring_step:
+            return self._scoring_step(q, k_cache, v_cache, block_tables, context_lens,
+                                      layer_idx)
+        else:
+            return self._reuse_step(q, k_cache, v_cache, block_tables, context_lens, layer_idx)
+
+    # ------------------------------------------------------------ accounting
+    def _ensure_work(self, device) -> torch.Tensor:
+        if self._work_buf is None:
+            self._work_buf = torch.zeros(2, dtype=torch.long, device=device)
+            self._attn_work = self._work_buf[0]
+            self._attn_work_max = self._work_buf[1]
+        return self._work_buf
+
+    def _work(self, device) -> Optional[torch.Tensor]:
+        """The [attended, max] counter pair when it lives on `device`; the
+        decode kernels add to it directly."""
+        buf = self._ensure_work(device)
+        return buf if buf.device == torch.device(device) else None
+
+    def _record_work(self, context_lens: torch.Tensor, pages_attended: torch.Tensor):
+        """backend.py:368-390: pages_attended is summed over batch x KV heads;
+        the maximum is n_valid x H_kv per sequence."""
+        self._ensure_work(context_lens.device)
+        n_valid = ((context_lens.float() - 1) / self.block_size).long() + 1
+        dense_max = n_valid.sum() * self.num_kv_heads
+        self._attn_work += pages_attended.to(torch.long).to(self._attn_work.device)
+        self._attn_work_max += dense_max.to(torch.long).to(self._attn_work_max.device)
+
+    def _decode_work(self, context_lens):
+        """Counter pair for a kernel launch, or None after recording on the host."""
+        return self._work(context_lens.device)
+
+    # ------------------------------------------------------------ steps
+    def _reuse_decode(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
+        pi_flat, nph_flat, padded = self._reuse_state[layer_idx]
+        work = self._decode_work(context_lens)
+        out = self._time_kernel(
+            "sparse_draft", ops.sparse_decode_reuse, q, k_cache, v_cache, block_tables,
+            context_lens, pi_flat, nph_flat, padded, self.num_kv_heads, self.num_q_per_kv,
+            self.block_size, work=work)
+        if work is None:
+            self._record_work(context_lens, self._cached_selection[layer_idx][1].sum())
+        return out
+
+    def _apply_random_reject(self, accept_mask):
+        if self.random_reject_prob is None:
+            return accept_mask
+        if torch.rand(1, device=accept_mask.device).item() < self.random_reject_prob:
+            return torch.zeros_like(accept_mask)
+        return torch.ones_like(accept_mask)
+
+    def _lazy_step(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
+        """backend.py:392-465"""
+        page_scores = self._time_kernel(
+            "scoring", ops.score_pages, q, k_cache, block_tables, context_lens,
+            self.num_kv_heads, self.num_q_per_kv, self.block_size)
+        self._total_coverage_checks += 1
+        if layer_idx in self._cached_selection:
+            page_indices, n_per_head = self._cached_selection[layer_idx]
+            accept_mask, _coverage = self._time_kernel(
+                "coverage", ops.check_coverage, page_scores, page_indices, n_per_head,
+                self.tau)
+            accept_mask = self._apply_random_reject(accept_mask)
+            n_acc = int(accept_mask.sum().item())  # one host read decides the branch
+            self._per_head_accept_sum += n_acc
+            self._per_head_total += accept_mask.numel()
+            if n_acc == accept_mask.numel():
+                self._accept_counts += 1
+                self._last_accept_mask[layer_idx] = accept_mask
+                return self._reuse_decode(q, k_cache, v_cache, block_tables, context_lens,
+                                          layer_idx)
+        self._reject_counts += 1
+        return self._scoring_step(q, k_cache, v_cache, block_tables, context_lens, layer_idx,
+                                  page_scores=page_scores)
+
+    def _coverage_only_step(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
+        """backend.py:467-520"""
+        page_scores = self._cached_page_scores[layer_idx]
+        page_indices, n_per_head = self._cached_selection[layer_idx]
+        accept_mask, _coverage = self._time_kernel(
+            "coverage", ops.check_coverage, page_scores, page_indices, n_per_head, self.tau)
+        accept_mask = self._apply_random_reject(accept_mask)
+        n_acc = int(accept_mask.sum().item())
+        self._per_head_accept_sum += n_acc
+        self._per_head_total += accept_mask.numel()
+        self._total_coverage_checks += 1
+        if n_acc == accept_mask.numel():
+            self._accept_counts += 1
+            self._last_accept_mask[layer_idx] = accept_mask
+            return self._reuse_decode(q, k_cache, v_cache, block_tables, context_lens,
+                                      layer_idx)
+        self._reject_counts += 1
+        return self._scoring_step(q, k_cache, v_cache, block_tables, context_lens, layer_idx,
+                                  page_scores=None)
+
+    def _scoring_step(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx,
+                      page_scores=None):
+        """backend.py:683-864 (uniform budget; exact or approximate recovery)."""
+        B = q.shape[0]
+        n_pages = block_tables.shape[1]
+        budget = max(3, int(n_pages * self.budget_pct))                           # :690
+
+        if page_scores is None:
+            page_scores = self._time_kernel(
+                "scoring", ops.score_pages, q, k_cache, block_tables, context_lens,
+                self.num_kv_heads, self.num_q_per_kv, self.block_size)
+        self._cached_page_scores[layer_idx] = page_scores                         # :713
+
+        # Top-k selection fused with the coverage gate of the new selection.
+        page_indices, n_per_head, accept_mask, _coverage = self._time_kernel(
+            "coverage", ops.select_topk, page_scores, budget, context_lens, self.block_size,
+            self.tau)
+        accept_mask = self._apply_random_reject(accept_mask)
+        self._last_accept_mask[layer_idx] = accept_mask                           # :771
+
+        if self.approx_recovery_pct is None:
+            # Accepted heads: normalised draft (:775-779); rejected heads:
+            # complement + LSE merge == every valid page (:818-844).
+            work = self._decode_work(context_lens)
+            output = self._time_kernel(
+                "sparse_draft", ops.verified_decode, q, k_cache, v_cache, block_tables,
+                context_lens, page_indices, n_per_head, accept_mask, self.num_kv_heads,
+                self.num_q_per_kv, self.block_size, output_dtype=q.dtype, work=work)
+            if work is None:
+                n_valid = ((context_lens.float() - 1) / self.block_size).long() + 1
+                pages = torch.where(accept_mask, n_per_head.long(),
+                                    n_valid.unsqueeze(1).expand_as(n_per_head)).sum()
+                self._record_work(context_lens, pages)
+            self._expanded_store[layer_idx] = _PendingComplement(
+                accept_mask, page_indices, n_per_head, context_lens, self.block_size)
+            if not self.lazy:
+                n_acc = int(accept_mask.sum().item())
+                if n_acc == accept_mask.numel():
+                    self._accept_counts += 1
+                else:
+                    self._reject_counts += 1
+                self._per_head_accept_sum += n_acc
+                self._per_head_total += accept_mask.numel()
+        else:
+            output = self._approx_recovery(q, k_cache, v_cache, block_tables, context_lens,
+                                           layer_idx, page_scores, page_indices, n_per_head,
+                                           accept_mask, budget, n_pages)
+
+        # Reuse state and cached selection (:852-856).  The selection is
+        # used in place; the kernels need no power-of-two padding.
+        self._reuse_state[layer_idx] = (page_indices.view(B * self.num_kv_heads, -1),
+                                        n_per_head.view(B * self.num_kv_heads),
+                                        ops.next_power_of_2(page_indices.shape[2]))
+        self._cached_selection[layer_idx] = (page_indices, n_per_head)
+        self._total_scoring_steps += 1                                            # :859
+        return output
+
+    def _approx_recovery(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx,
+                         page_scores, page_indices, n_per_head, accept_mask, budget, n_pages):
+        """Approximate recovery branch (backend.py:775-817): rejected heads use
+        an expanded top-k at approx_recovery_pct of the pages."""
+        B = q.shape[0]
+        n_acc = int(accept_mask.sum().item())
+        all_acc = n_acc == accept_mask.numel()
+        draft = self._time_kernel(
+            "sparse_draft", ops.sparse_decode, q, k_cache, v_cache, block_tables, page_indices,
+            n_per_head, context_lens, self.num_kv_heads, self.num_q_per_kv, self.block_size)
+        pages = n_per_head.sum()
+        if all_acc:
+            output = draft
+            if not self.lazy:
+                self._accept_counts += 1
+        else:
+            exp_budget = min(max(budget + 1, int(n_pages * self.approx_recovery_pct)), n_pages)
+            exp_indices, exp_nph = ops.select_topk(page_scores, exp_budget, context_lens,
+                                                   self.block_size)
+            expanded = self._time_kernel(
+                "ar_recovery", ops.sparse_decode, q, k_cache, v_cache, block_tables,
+                exp_indices, exp_nph, context_lens, self.num_kv_heads, self.num_q_per_kv,
+                self.block_size)
+            pages = pages + exp_nph.sum()
+            accept_q = accept_mask.repeat_interleave(self.num_q_per_kv, dim=1)
+            output = torch.where(accept_q.unsqueeze(-1), draft, expanded)
+            self._expanded_store[layer_idx] = (exp_indices, exp_nph)
+            if not self.lazy:
+                self._reject_counts += 1
+        self._record_work(context_lens, pages)
+        if not self.lazy:
+            self._per_head_accept_sum += n_acc
+            self._per_head_total += accept_mask.numel()
+        return output
+
+    def _reuse_step(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
+        """backend.py:866-881, including the step-decrement fallback (:868-872)."""
+        if layer_idx not in self._reuse_state:
+            self._step -= 1
+            return self(q, k_cache, v_cache, block_tables, context_lens, layer_idx)
+        return self._reuse_decode(q, k_cache, v_cache, block_tables, context_lens, layer_idx)

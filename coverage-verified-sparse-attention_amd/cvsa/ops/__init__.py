@@ -1,0 +1,469 @@
+"""HIP operators of the CVSA decode path, with the reference's argument lists.
+
+Each function mirrors one entry of the reference's kernel API (the
+``triton_*`` functions of ``cvsa/kernels``) with the same arguments and
+return tuple, allocates its outputs with the torch caching allocator and
+launches the gfx950 kernels of ``libcvsa_hip.so`` on the current stream.
+All tensors must live on one ROCm GPU; there is no CPU path.
+
+Workspaces of the paged decode kernels are cached per (device, stream) and
+their completion counters are zeroed once when allocated; the kernels leave
+them zeroed.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import CVSAError, check
+
+__all__ = [
+    "CVSAError",
+    "score_pages",
+    "select_topk",
+    "check_coverage",
+    "sparse_decode_unnorm",
+    "sparse_decode",
+    "prepare_reuse_state",
+    "sparse_decode_reuse",
+    "dense_decode",
+    "verified_decode",
+    "compute_complement",
+    "lse_merge",
+    "append_kv",
+    "next_power_of_2",
+]
+
+_DTYPE_CODE = {
+    torch.bfloat16: _lib.DTYPE_BF16,
+    torch.float16: _lib.DTYPE_FP16,
+    torch.float32: _lib.DTYPE_FP32,
+}
+
+
+def next_power_of_2(n: int) -> int:
+    """Round up to a power of two, minimum 1 (sparse_decode.py:279-283)."""
+    if n <= 1:
+        return 1
+    return 1 << (n - 1).bit_length()
+
+
+# ---------------------------------------------------------------- helpers
+
+def _device_of(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(
+                f"CVSA ops run on the GPU only; got a tensor on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise ValueError("no tensor argument")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    return t.contiguous()
+
+
+def _check_cache(k_cache: torch.Tensor, name: str = "k_cache") -> None:
+    if k_cache.dim() != 4:
+        raise ValueError(f"{name} must be [num_blocks, block_size, H_kv, D], got {tuple(k_cache.shape)}")
+    if k_cache.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16, got {k_cache.dtype}")
+    if not k_cache.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _check_q(q: torch.Tensor) -> torch.Tensor:
+    if q.dim() != 3:
+        raise ValueError(f"q must be [B, H_q, D], got {tuple(q.shape)}")
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"q must be bfloat16, got {q.dtype}")
+    if q.stride(2) != 1 or q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    return q
+
+
+def _block_tables(bt: torch.Tensor) -> torch.Tensor:
+    bt = bt if bt.dtype == torch.int32 else bt.to(torch.int32)
+    if bt.dim() != 2 or bt.stride(1) != 1:
+        bt = bt.contiguous()
+    return bt
+
+
+_WORKSPACES: dict = {}
+
+
+def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-(device, stream) decode workspace with zeroed completion counters."""
+    stream = torch.cuda.current_stream(dev)
+    key = (dev.index, stream.cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 1 << 20)
+        size = (size + (1 << 20) - 1) // (1 << 20) * (1 << 20)
+        ws = torch.empty(size, dtype=torch.uint8, device=dev)
+        check(_lib.load().cvsa_workspace_init(ws.data_ptr(), size, stream.cuda_stream),
+              "workspace_init")
+        _WORKSPACES[key] = ws
+    return ws
+
+
+# ---------------------------------------------------------------- scoring
+
+def score_pages(q: torch.Tensor, k_cache: torch.Tensor, block_tables: torch.Tensor,
+                context_lens: torch.Tensor, num_kv_heads: int, num_q_per_kv: int,
+                block_size: int) -> torch.Tensor:
+    """max(q_rep . K) * D^-0.5 per page and KV head -> [B, H_kv, W] fp32.
+
+    Mirrors triton_score_pages (cvsa/kernels/page_scores.py:77-119).
+    """
+    dev = _device_of(q, k_cache, block_tables, context_lens)
+    q = _check_q(q)
+    _check_cache(k_cache)
+    bt = _block_tables(block_tables)
+    ctx = _i32(context_lens)
+    B, H_q, D = q.shape
+    if num_kv_heads * num_q_per_kv != H_q or k_cache.shape[2] != num_kv_heads:
+        raise ValueError("score_pages: head counts do not match q / k_cache")
+    if k_cache.shape[1] != block_size or k_cache.shape[3] != D:
+        raise ValueError("score_pages: k_cache block_size / head_dim mismatch")
+    W = bt.shape[1]
+    out = torch.empty(B, num_kv_heads, W, device=dev, dtype=torch.float32)
+    check(_lib.load().cvsa_score_pages(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), k_cache.shape[0],
+        bt.data_ptr(), bt.stride(0), ctx.data_ptr(), B, H_q, num_kv_heads, D,
+        block_size, W, out.data_ptr(), _stream(dev)), "score_pages")
+    return out
+
+
+def select_topk(page_scores: torch.Tensor, budget: int, context_lens: torch.Tensor,
+                block_size: int, tau: Optional[float] = None):
+    """Top-`budget` pages per (b, kv-head) and n_per_head = min(budget, n_valid).
+
+    Replaces ``torch.topk(page_scores, budget, sorted=False)`` plus the
+    n_per_head computation of CVSABackend._scoring_step
+    (cvsa/backend.py:737-747).  The set is the `budget` largest scores with
+    ties to the lower page index, returned in ascending page order.
+    With ``tau`` the coverage gate of the new selection is fused in and
+    (page_indices, n_per_head, accept_mask, coverage) is returned.
+    """
+    dev = _device_of(page_scores, context_lens)
+    if page_scores.dtype != torch.float32 or page_scores.dim() != 3:
+        raise ValueError("page_scores must be [B, H_kv, W] float32")
+    ps = page_scores.contiguous()
+    ctx = _i32(context_lens)
+    B, H_kv, W = ps.shape
+    if not 1 <= budget <= W:
+        raise ValueError(f"select_topk: budget {budget} must be in [1, {W}]")
+    idx = torch.empty(B, H_kv, budget, device=dev, dtype=torch.int32)
+    nph = torch.empty(B, H_kv, device=dev, dtype=torch.int32)
+    acc = cov = None
+    if tau is not None:
+        acc = torch.empty(B, H_kv, device=dev, dtype=torch.uint8)
+        cov = torch.empty(B, H_kv, device=dev, dtype=torch.float32)
+    check(_lib.load().cvsa_select_topk(
+        ps.data_ptr(), B, H_kv, W, ctx.data_ptr(), block_size, budget, idx.data_ptr(),
+        nph.data_ptr(), float(tau) if tau is not None else 0.0, _ptr(acc), _ptr(cov),
+        _stream(dev)), "select_topk")
+    if tau is None:
+        return idx, nph
+    return idx, nph, acc.view(torch.bool), cov
+
+
+def check_coverage(page_scores: torch.Tensor, selected_indices: torch.Tensor,
+                   n_per_head: torch.Tensor, tau: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """coverage = exp(lse(selected) - lse(all)); accept = coverage >= tau.
+
+    Mirrors triton_check_coverage (cvsa/kernels/coverage.py:218-265).
+    Returns (accept_mask [B, H_kv] bool, coverage [B, H_kv] float32).
+    """
+    dev = _device_of(page_scores, selected_indices, n_per_head)
+    if page_scores.dtype != torch.float32 or page_scores.dim() != 3:
+        raise ValueError("page_scores must be [B, H_kv, W] float32")
+    ps = page_scores.contiguous()
+    B, H_kv, W = ps.shape
+    sel = _i32(selected_indices)
+    if sel.dim() != 3 or sel.shape[:2] != (B, H_kv):
+        raise ValueError("selected_indices must be [B, H_kv, budget]")
+    nph = _i32(n_per_head).reshape(B * H_kv)
+    acc = torch.empty(B, H_kv, device=dev, dtype=torch.uint8)
+    cov = torch.empty(B, H_kv, device=dev, dtype=torch.float32)
+    check(_lib.load().cvsa_check_coverage(
+        ps.data_ptr(), B, H_kv, W, sel.data_ptr(), sel.shape[2], nph.data_ptr(),
+        float(tau), acc.data_ptr(), cov.data_ptr(), _stream(dev)), "check_coverage")
+    return acc.view(torch.bool), cov
+
+
+# ---------------------------------------------------------------- decode
+
+def _decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
+            num_q_per_kv, block_size, pi_flat=None, nph_flat=None, max_sel=0,
+            accept=None, want_state=False, want_out=True, out_dtype=None, work=None):
+    dev = _device_of(q, k_cache, v_cache, block_tables, context_lens, pi_flat, nph_flat,
+                     accept, work)
+    if work is not None and (work.dtype != torch.int64 or work.numel() < 2
+                             or not work.is_contiguous()):
+        raise ValueError(f"{kind}: work must be a contiguous int64 tensor of 2 counters")
+    q = _check_q(q)
+    _check_cache(k_cache)
+    _check_cache(v_cache, "v_cache")
+    if k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache shapes differ")
+    bt = _block_tables(block_tables)
+    ctx = _i32(context_lens)
+    B, H_q, D = q.shape
+    if num_kv_heads * num_q_per_kv != H_q or k_cache.shape[2] != num_kv_heads:
+        raise ValueError(f"{kind}: head counts do not match q / caches")
+    if k_cache.shape[1] != block_size or k_cache.shape[3] != D:
+        raise ValueError(f"{kind}: cache block_size / head_dim mismatch")
+    W = bt.shape[1]
+    L = _lib.load()
+    listed = pi_flat is not None
+    all_pages = kind in ("dense_decode", "verified_decode")
+    need = L.cvsa_decode_workspace_bytes(B, H_q, num_kv_heads, D, max_sel if listed else 0,
+                                         W, 1 if all_pages else 0)
+    if need == 0:
+        raise ValueError(f"{kind}: invalid geometry")
+    ws = _workspace(dev, need)
+    o = m = l = out = None
+    if want_state:
+        o = torch.empty(B, H_q, D, device=dev, dtype=torch.float32)
+        m = torch.empty(B, H_q, device=dev, dtype=torch.float32)
+        l = torch.empty(B, H_q, device=dev, dtype=torch.float32)
+    code = 0
+    if want_out:
+        od = out_dtype or q.dtype
+        if od not in _DTYPE_CODE:
+            raise ValueError(f"unsupported output dtype {od}")
+        out = torch.empty(B, H_q, D, device=dev, dtype=od)
+        code = _DTYPE_CODE[od]
+    common_q = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+                k_cache.shape[0], bt.data_ptr(), bt.stride(0), ctx.data_ptr())
+    tail = (_ptr(o), _ptr(m), _ptr(l), _ptr(out), code, _ptr(work), ws.data_ptr(), ws.numel(),
+            _stream(dev))
+    if kind == "sparse_decode":
+        rc = L.cvsa_sparse_decode(*common_q, pi_flat.data_ptr(), pi_flat.stride(0),
+                                  nph_flat.data_ptr(), max_sel, B, H_q, num_kv_heads, D,
+                                  block_size, W, *tail)
+    elif kind == "dense_decode":
+        rc = L.cvsa_dense_decode(*common_q, B, H_q, num_kv_heads, D, block_size, W, *tail)
+    else:
+        rc = L.cvsa_verified_decode(*common_q, pi_flat.data_ptr(), pi_flat.stride(0),
+                                    nph_flat.data_ptr(), max_sel, accept.data_ptr(), B, H_q,
+                                    num_kv_heads, D, block_size, W, *tail)
+    check(rc, kind)
+    return o, m, l, out
+
+
+def _flat_selection(page_indices: torch.Tensor, n_per_head: torch.Tensor, num_kv_heads: int):
+    if page_indices.dim() != 3:
+        raise ValueError("page_indices must be [B, H_kv, max_selected]")
+    B, H, k = page_indices.shape
+    if H != num_kv_heads:
+        raise ValueError("page_indices head dimension does not match num_kv_heads")
+    pi = _i32(page_indices).reshape(B * H, k)
+    nph = _i32(n_per_head).reshape(B * H)
+    return pi, nph, k
+
+
+def sparse_decode_unnorm(q, k_cache, v_cache, block_tables, page_indices, n_per_head,
+                         context_lens, num_kv_heads, num_q_per_kv, block_size=64):
+    """Un-normalised sparse attention (O_unnorm [B,H_q,D], M [B,H_q], L [B,H_q]).
+
+    Mirrors triton_sparse_decode_unnorm (cvsa/kernels/sparse_decode.py:537-573).
+    A head with n_per_head = 0 gives (0, -inf, 0) where the reference gives
+    NaN (the identity of the LSE merge instead of an undefined value).
+    """
+    pi, nph, k = _flat_selection(page_indices, n_per_head, num_kv_heads)
+    o, m, l, _ = _decode("sparse_decode", q, k_cache, v_cache, block_tables, context_lens,
+                         num_kv_heads, num_q_per_kv, block_size, pi, nph, k,
+                         want_state=True, want_out=False)
+    return o, m, l
+
+
+def sparse_decode(q, k_cache, v_cache, block_tables, page_indices, n_per_head,
+                  context_lens, num_kv_heads, num_q_per_kv, block_size=64):
+    """Normalised sparse attention -> [B, H_q, D] in q.dtype.
+
+    Mirrors triton_sparse_decode (cvsa/kernels/sparse_decode.py:286-350).
+    Unlike the reference's tiled path (:371-383) the result never aliases
+    a cached buffer.
+    """
+    pi, nph, k = _flat_selection(page_indices, n_per_head, num_kv_heads)
+    return _decode("sparse_decode", q, k_cache, v_cache, block_tables, context_lens,
+                   num_kv_heads, num_q_per_kv, block_size, pi, nph, k)[3]
+
+
+def prepare_reuse_state(page_indices, n_per_head, num_kv_heads, B):
+    """(pi_flat, nph_flat, padded_max_selected) for sparse_decode_reuse.
+
+    Same contract as the reference (cvsa/kernels/sparse_decode.py:664-678):
+    indices padded with 0 to a power of two, flattened to [B*H_kv, padded].
+    """
+    actual = page_indices.shape[2]
+    padded = next_power_of_2(actual)
+    pi = page_indices
+    if padded > actual:
+        pi = torch.nn.functional.pad(page_indices, (0, padded - actual), value=0)
+    pi_flat = _i32(pi).reshape(B * num_kv_heads, padded).contiguous()
+    nph_flat = _i32(n_per_head).reshape(B * num_kv_heads).contiguous()
+    return pi_flat, nph_flat, padded
+
+
+def sparse_decode_reuse(q, k_cache, v_cache, block_tables, context_lens, pi_flat, nph_flat,
+                        padded_max_selected, num_kv_heads, num_q_per_kv, block_size,
+                        work: Optional[torch.Tensor] = None):
+    """Normalised sparse attention on a prepared selection -> [B, H_q, D].
+
+    Mirrors triton_sparse_decode_reuse (cvsa/kernels/sparse_decode.py:681-721).
+    ``work`` (int64[2]) accumulates the effective-budget counters.
+    """
+    width = min(int(padded_max_selected), pi_flat.shape[1])
+    return _decode("sparse_decode", q, k_cache, v_cache, block_tables, context_lens,
+                   num_kv_heads, num_q_per_kv, block_size, pi_flat, nph_flat, width,
+                   work=work)[3]
+
+
+def dense_decode(q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
+                 num_q_per_kv, block_size, return_state: bool = False,
+                 work: Optional[torch.Tensor] = None):
+    """Attention over every valid page -> [B, H_q, D] in q.dtype.
+
+    The reference's dense fallback (cvsa/runtime/dense.py:40-68) selects all
+    pages; here no index list is built at all.  With ``return_state`` also
+    returns the un-normalised (o, m, l).
+    """
+    o, m, l, out = _decode("dense_decode", q, k_cache, v_cache, block_tables, context_lens,
+                           num_kv_heads, num_q_per_kv, block_size, want_state=return_state,
+                           work=work)
+    return (out, (o, m, l)) if return_state else out
+
+
+def verified_decode(q, k_cache, v_cache, block_tables, context_lens, page_indices, n_per_head,
+                    accept_mask, num_kv_heads, num_q_per_kv, block_size,
+                    return_state: bool = False, output_dtype=None,
+                    work: Optional[torch.Tensor] = None):
+    """Draft for accepted heads, exact recovery for rejected heads, one launch.
+
+    Equivalent to the exact-recovery branch of CVSABackend._scoring_step
+    (cvsa/backend.py:775-779, :818-844): accepted heads return the
+    normalised draft over their selected pages; rejected heads return the
+    LSE merge of draft and complement, which is attention over every valid
+    page, computed here in a single pass over those pages.
+    """
+    pi, nph, k = _flat_selection(page_indices, n_per_head, num_kv_heads)
+    acc = accept_mask
+    if acc.dtype == torch.bool:
+        acc = acc.view(torch.uint8)
+    acc = acc.to(torch.uint8).contiguous().reshape(-1)
+    o, m, l, out = _decode("verified_decode", q, k_cache, v_cache, block_tables, context_lens,
+                           num_kv_heads, num_q_per_kv, block_size, pi, nph, k, accept=acc,
+                           want_state=return_state, out_dtype=output_dtype, work=work)
+    return (out, (o, m, l)) if return_state else out
+
+
+# ---------------------------------------------------------------- recovery
+
+def compute_complement(page_indices, n_per_head, context_lens, block_size, accept_mask,
+                       width: Optional[int] = None):
+    """Valid pages not selected, ascending, per (b, kv-head); 0 for accepted heads.
+
+    Mirrors triton_compute_complement (cvsa/kernels/coverage.py:99-150):
+    returns (complement [B, H_kv, width] int32,
+    n_complement [B, H_kv] int32).  ``width`` defaults to max_b n_valid(b),
+    which costs one host sync as in the reference (coverage.py:121); pass
+    it (e.g. the block-table width) to avoid the sync.
+    """
+    dev = _device_of(page_indices, n_per_head, context_lens, accept_mask)
+    B, H, k = page_indices.shape
+    pi = _i32(page_indices).reshape(B * H, k)
+    nph = _i32(n_per_head).reshape(B * H)
+    ctx = _i32(context_lens)
+    if width is None:
+        width = int(((ctx.max().item() - 1) // block_size) + 1)
+        width = max(width, 1)
+    acc = None
+    if accept_mask is not None:
+        acc = accept_mask.view(torch.uint8) if accept_mask.dtype == torch.bool else accept_mask
+        acc = acc.to(torch.uint8).contiguous().reshape(-1)
+    comp = torch.empty(B, H, width, device=dev, dtype=torch.int32)
+    ncomp = torch.empty(B, H, device=dev, dtype=torch.int32)
+    check(_lib.load().cvsa_compute_complement(
+        pi.data_ptr(), pi.stride(0), nph.data_ptr(), ctx.data_ptr(), block_size, _ptr(acc),
+        B, H, width, comp.data_ptr(), ncomp.data_ptr(), _stream(dev)), "compute_complement")
+    return comp, ncomp
+
+
+def lse_merge(o_draft, m_draft, l_draft, o_comp, m_comp, l_comp, accept_mask, num_kv_heads,
+              num_q_per_kv, output_dtype=torch.bfloat16):
+    """Per-head merge: accepted -> normalised draft, rejected -> LSE merge.
+
+    Mirrors triton_lse_merge (cvsa/kernels/coverage.py:329-367).
+    """
+    dev = _device_of(o_draft, m_draft, l_draft, o_comp, m_comp, l_comp, accept_mask)
+    B, H_q, D = o_draft.shape
+    if num_kv_heads * num_q_per_kv != H_q:
+        raise ValueError("lse_merge: head counts do not match")
+    f32 = lambda t: t.to(torch.float32).contiguous()
+    od, md, ld, oc, mc, lc = map(f32, (o_draft, m_draft, l_draft, o_comp, m_comp, l_comp))
+    acc = accept_mask.view(torch.uint8) if accept_mask.dtype == torch.bool else accept_mask
+    acc = acc.to(torch.uint8).contiguous()
+    if output_dtype not in _DTYPE_CODE:
+        raise ValueError(f"unsupported output dtype {output_dtype}")
+    out = torch.empty(B, H_q, D, device=dev, dtype=output_dtype)
+    check(_lib.load().cvsa_lse_merge(
+        od.data_ptr(), md.data_ptr(), ld.data_ptr(), oc.data_ptr(), mc.data_ptr(), lc.data_ptr(),
+        acc.data_ptr(), B, H_q, num_kv_heads, D, out.data_ptr(), _DTYPE_CODE[output_dtype],
+        _stream(dev)), "lse_merge")
+    return out
+
+
+# ---------------------------------------------------------------- KV append
+
+def append_kv(k_new, v_new, k_cache, v_cache, block_tables, context_lens, pages_allocated,
+              seq_begin: int, next_free_block: int, block_size: int) -> None:
+    """Append one token per sequence [seq_begin, seq_begin + k_new.shape[0]).
+
+    Device-side form of SequenceKVManager.append_token_kv
+    (cvsa/runtime/kv_cache.py:133-150); see cvsa_append_kv in the C header.
+    block_tables, context_lens and pages_allocated are updated in place and
+    must be contiguous int32.
+    """
+    dev = _device_of(k_new, v_new, k_cache, v_cache, block_tables, context_lens,
+                     pages_allocated)
+    _check_cache(k_cache)
+    _check_cache(v_cache, "v_cache")
+    for name, t in (("block_tables", block_tables), ("context_lens", context_lens),
+                    ("pages_allocated", pages_allocated)):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"append_kv: {name} must be contiguous int32")
+    n = k_new.shape[0]
+    if not 1 <= n <= 1024:
+        raise ValueError(f"append_kv: {n} sequences per call (1..1024 supported)")
+    H_kv, D = k_cache.shape[2], k_cache.shape[3]
+    kn = k_new.to(torch.bfloat16).reshape(n, H_kv * D).contiguous()
+    vn = v_new.to(torch.bfloat16).reshape(n, H_kv * D).contiguous()
+    check(_lib.load().cvsa_append_kv(
+        kn.data_ptr(), vn.data_ptr(), kn.stride(0), k_cache.data_ptr(), v_cache.data_ptr(),
+        k_cache.shape[0], block_tables.data_ptr(), block_tables.stride(0),
+        block_tables.shape[1], context_lens.data_ptr(), pages_allocated.data_ptr(), seq_begin,
+        n, next_free_block, H_kv, D, block_size, _stream(dev)), "append_kv")

@@ -1,0 +1,234 @@
+/*
+ * cvsa_hip.h - C ABI of libcvsa_hip.so, the MI355X (gfx950) implementation of
+ * the CVSA decode-step attention path.
+ *
+ * Conventions shared by every entry point:
+ *  - Pointers are device pointers unless stated otherwise.  bf16 tensors are
+ *    passed as uint16_t (raw bfloat16 bits).
+ *  - The paged cache layout is the reference's: k_cache / v_cache are
+ *    [num_blocks, block_size, H_kv, D] bf16, fully contiguous
+ *    (cvsa/runtime/kv_cache.py:40-47).  block_tables are [B, >=W] int32 with
+ *    unit stride along pages; context_lens are [B] int32.
+ *  - `stream` is a hipStream_t (NULL = default stream).  Kernels are only
+ *    enqueued; no entry point synchronises the host.
+ *  - The library allocates nothing.  Outputs and workspaces belong to the
+ *    caller.
+ *  - Return value: CVSA_OK (0), or a negative CVSA_ERR_* code with nothing
+ *    enqueued.  cvsa_last_error() then returns a thread-local message.
+ *  - Supported geometry: D = 128, block_size = 16, G = H_q / H_kv in 1..8,
+ *    H_kv in {1, 2, 4, 8, 16} (page scoring), W <= 32768 pages.  Anything else
+ *    returns CVSA_ERR_UNSUPPORTED.
+ *  - Entry points are re-entrant.  Calls that share a decode workspace must
+ *    be ordered on one stream.
+ */
+#ifndef CVSA_HIP_H
+#define CVSA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CVSA_ABI_VERSION 1
+
+enum {
+  CVSA_OK = 0,
+  CVSA_ERR_INVALID = -1,     /* bad pointer, shape, stride or alignment */
+  CVSA_ERR_UNSUPPORTED = -2, /* geometry outside the supported set */
+  CVSA_ERR_LAUNCH = -3,      /* the HIP runtime refused the launch */
+  CVSA_ERR_WORKSPACE = -4    /* workspace missing or too small */
+};
+
+enum { CVSA_DTYPE_BF16 = 0, CVSA_DTYPE_FP16 = 1, CVSA_DTYPE_FP32 = 2 };
+
+/* Thread-local description of the last failure on this thread. */
+const char *cvsa_last_error(void);
+int cvsa_abi_version(void);
+
+/*
+ * Page scoring.  Replaces triton_score_pages
+ * (cvsa/kernels/page_scores.py:77-119, kernel :12-74).
+ *   q_rep[b,h] = bf16(sum_g q[b, h*G+g] * (1/G))          (fp32 sum, RNE)
+ *   page_scores[b,h,p] = max_{t < tokens(p)} fp32(q_rep . K[bt[b,p], t, h]) * D^-0.5
+ *   page_scores[b,h,p] = -inf when p*block_size >= context_lens[b].
+ * q: [B, H_q, D] bf16 with element strides (q_stride_b, q_stride_h, 1).
+ * page_scores: [B, H_kv, W] fp32, contiguous.
+ */
+int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
+                     const uint16_t *k_cache, int64_t num_blocks,
+                     const int32_t *block_tables, int64_t bt_stride_b,
+                     const int32_t *context_lens, int32_t B, int32_t H_q,
+                     int32_t H_kv, int32_t D, int32_t block_size, int32_t W,
+                     float *page_scores, void *stream);
+
+/*
+ * Top-k page selection.  Replaces the uniform-budget branch of
+ * CVSABackend._scoring_step (cvsa/backend.py:737-747: torch.topk(sorted=False)
+ * then n_per_head = min(budget, n_valid)).
+ *   page_indices[b,h,:budget] = the `budget` largest scores of row (b,h),
+ *     ties broken by lower page index, written in ascending page order.
+ *   n_per_head[b,h] = min(budget, n_valid(b)), n_valid = (ctx-1)/bs + 1.
+ * When accept_out and coverage_out are non-NULL the coverage gate of the new
+ * selection is fused in, with the semantics of cvsa_check_coverage
+ * (cvsa/backend.py:757-761).
+ */
+int cvsa_select_topk(const float *page_scores, int32_t B, int32_t H_kv,
+                     int32_t W, const int32_t *context_lens,
+                     int32_t block_size, int32_t budget, int32_t *page_indices,
+                     int32_t *n_per_head, float tau, uint8_t *accept_out,
+                     float *coverage_out, void *stream);
+
+/*
+ * Coverage gate.  Replaces triton_check_coverage
+ * (cvsa/kernels/coverage.py:218-265, kernel :159-215).
+ *   lse_all = M + log(sum exp(s - M) + 1e-30), M = max(max_p s, -1e20)
+ *   lse_sel = same over the first n_per_head[b,h] selected pages
+ *   coverage = exp(lse_sel - lse_all);  accept = coverage >= tau  (fp32)
+ * selected: rows of `sel_stride` int32 per (b,h).
+ */
+int cvsa_check_coverage(const float *page_scores, int32_t B, int32_t H_kv,
+                        int32_t W, const int32_t *selected, int64_t sel_stride,
+                        const int32_t *n_per_head, float tau,
+                        uint8_t *accept_out, float *coverage_out, void *stream);
+
+/*
+ * Workspace of the paged decode entry points, in bytes, for a call whose
+ * heads visit at most `max_sel_pages` listed pages and, when `all_pages` is
+ * non-zero, up to W pages (dense heads).  The first 4*B*H_kv bytes are
+ * completion counters: they must be zero before the first call (see
+ * cvsa_workspace_init) and every call leaves them zero.
+ */
+size_t cvsa_decode_workspace_bytes(int32_t B, int32_t H_q, int32_t H_kv,
+                                   int32_t D, int32_t max_sel_pages,
+                                   int32_t W, int32_t all_pages);
+
+/* Zero a workspace on `stream` with a fill kernel. */
+int cvsa_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Sparse paged decode over a per-KV-head page list.  Replaces
+ * triton_sparse_decode_unnorm (cvsa/kernels/sparse_decode.py:537-573) when
+ * the (o_unnorm, m_out, l_out) outputs are given, and triton_sparse_decode /
+ * triton_sparse_decode_reuse (:286-350, :681-721) when `out` is given.
+ * Either or both output forms may be requested.
+ *   For q-head j of batch b (KV head h = j / G), over the first
+ *   n_per_head[b*H_kv+h] entries of page_indices row (b,h) and the tokens
+ *   t < min(bs, ctx - page*bs) of each:
+ *     s = (q . K) * D^-0.5,  m = max s,  l = sum exp(s - m),
+ *     o_unnorm = sum exp(s - m) * V,   out = o_unnorm / max(l, 1e-6).
+ *   A head with no pages yields m = -inf, l = 0, o = 0 (out = 0).
+ * page_indices: rows of idx_stride int32 per (b,h); max_selected bounds
+ * n_per_head.  o_unnorm [B,H_q,D] fp32; m_out, l_out [B,H_q] fp32;
+ * out [B,H_q,D] of out_dtype.
+ * work (optional, int64[2]): the effective-budget counters of
+ * CVSABackend._record_work (cvsa/backend.py:368-390); each head adds the
+ * pages it attended to work[0] and n_valid(b) to work[1].
+ */
+int cvsa_sparse_decode(const uint16_t *q, int64_t q_stride_b,
+                       int64_t q_stride_h, const uint16_t *k_cache,
+                       const uint16_t *v_cache, int64_t num_blocks,
+                       const int32_t *block_tables, int64_t bt_stride_b,
+                       const int32_t *context_lens,
+                       const int32_t *page_indices, int64_t idx_stride,
+                       const int32_t *n_per_head, int32_t max_selected,
+                       int32_t B, int32_t H_q, int32_t H_kv, int32_t D,
+                       int32_t block_size, int32_t W, float *o_unnorm,
+                       float *m_out, float *l_out, void *out,
+                       int32_t out_dtype, int64_t *work, void *workspace,
+                       size_t workspace_bytes, void *stream);
+
+/*
+ * Dense paged decode over every valid page.  Replaces
+ * DenseAttentionBackend._triton_dense (cvsa/runtime/dense.py:40-68), i.e.
+ * the sparse kernel with all pages selected.  Outputs as cvsa_sparse_decode.
+ */
+int cvsa_dense_decode(const uint16_t *q, int64_t q_stride_b,
+                      int64_t q_stride_h, const uint16_t *k_cache,
+                      const uint16_t *v_cache, int64_t num_blocks,
+                      const int32_t *block_tables, int64_t bt_stride_b,
+                      const int32_t *context_lens, int32_t B, int32_t H_q,
+                      int32_t H_kv, int32_t D, int32_t block_size, int32_t W,
+                      float *o_unnorm, float *m_out, float *l_out, void *out,
+                      int32_t out_dtype, int64_t *work, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
+/*
+ * Verified decode: the draft/recovery branch of a scoring step in one pass.
+ * Replaces cvsa/backend.py:775-779 (accept-all: o_d / l_d) and the exact
+ * recovery branch :818-844 (triton_compute_complement, complement decode,
+ * triton_lse_merge).  Heads with accept[b*H_kv+h] != 0 attend their selected
+ * pages (the draft); rejected heads attend draft + complement = every valid
+ * page in one pass, which is the LSE merge of the two partial softmaxes.
+ * Outputs as cvsa_sparse_decode.
+ */
+int cvsa_verified_decode(const uint16_t *q, int64_t q_stride_b,
+                         int64_t q_stride_h, const uint16_t *k_cache,
+                         const uint16_t *v_cache, int64_t num_blocks,
+                         const int32_t *block_tables, int64_t bt_stride_b,
+                         const int32_t *context_lens,
+                         const int32_t *page_indices, int64_t idx_stride,
+                         const int32_t *n_per_head, int32_t max_selected,
+                         const uint8_t *accept, int32_t B, int32_t H_q,
+                         int32_t H_kv, int32_t D, int32_t block_size,
+                         int32_t W, float *o_unnorm, float *m_out,
+                         float *l_out, void *out, int32_t out_dtype,
+                         int64_t *work, void *workspace,
+                         size_t workspace_bytes, void *stream);
+
+/*
+ * Complement page lists.  Replaces triton_compute_complement
+ * (cvsa/kernels/coverage.py:99-150, kernel :30-96).
+ *   comp_indices[b,h,:] = ascending valid pages p < n_valid(b) that are not
+ *   among the first n_per_head[b,h] selected pages, zero-filled to `width`;
+ *   n_comp[b,h] = their count, 0 for heads with accept[b,h] != 0.
+ * accept may be NULL (no head accepted).  width must be >= max_b n_valid(b).
+ */
+int cvsa_compute_complement(const int32_t *page_indices, int64_t idx_stride,
+                            const int32_t *n_per_head,
+                            const int32_t *context_lens, int32_t block_size,
+                            const uint8_t *accept, int32_t B, int32_t H_kv,
+                            int32_t width, int32_t *comp_indices,
+                            int32_t *n_comp, void *stream);
+
+/*
+ * Selective LSE merge.  Replaces triton_lse_merge
+ * (cvsa/kernels/coverage.py:329-367, kernel :273-326)
+ * and selective_lse_merge (cvsa/lse_merge.py:11-54).
+ *   accepted kv head: out = o_d / max(l_d, 1e-6)
+ *   rejected: m = max(m_d, m_c), a = exp(m_d - m), c = exp(m_c - m),
+ *             out = (o_d a + o_c c) / max(l_d a + l_c c, 1e-6)
+ * o_*: [B,H_q,D] fp32; m_*, l_*: [B,H_q] fp32; accept [B,H_kv] uint8.
+ */
+int cvsa_lse_merge(const float *o_d, const float *m_d, const float *l_d,
+                   const float *o_c, const float *m_c, const float *l_c,
+                   const uint8_t *accept, int32_t B, int32_t H_q, int32_t H_kv,
+                   int32_t D, void *out, int32_t out_dtype, void *stream);
+
+/*
+ * Batched token append.  Replaces SequenceKVManager.append_token_kv
+ * (cvsa/runtime/kv_cache.py:133-150) for sequences
+ * [seq_begin, seq_begin + n_seqs) in one launch, without host syncs:
+ *   page = ctx / bs, off = ctx % bs;
+ *   if off == 0 and page >= pages_allocated[b]: the r-th such sequence (in
+ *     increasing b) gets block next_free_block + r, block_tables[b,page] is
+ *     set to it and pages_allocated[b] += 1;
+ *   K/V[block_tables[b,page], off] = k_new/v_new row;  context_lens[b] += 1.
+ * k_new/v_new: n_seqs rows of [H_kv, D] bf16, new_stride_b elements apart.
+ * The caller tracks how many blocks were taken (the host mirror of
+ * context_lens / pages_allocated) and must ensure they exist.
+ */
+int cvsa_append_kv(const uint16_t *k_new, const uint16_t *v_new,
+                   int64_t new_stride_b, uint16_t *k_cache, uint16_t *v_cache,
+                   int64_t num_blocks, int32_t *block_tables,
+                   int64_t bt_stride_b, int32_t W, int32_t *context_lens,
+                   int32_t *pages_allocated, int32_t seq_begin, int32_t n_seqs,
+                   int32_t next_free_block, int32_t H_kv, int32_t D,
+                   int32_t block_size, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CVSA_HIP_H */

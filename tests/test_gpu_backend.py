@@ -1,0 +1,177 @@
+"""Multi-step decode parity of the GPU CVSABackend against the oracle state machine.
+
+Both backends run the same decode loop (query jittered per step, one token
+appended per sequence per step through the paged-KV runtime) on identical
+inputs.  Checked per call: output max-abs, the accept mask (exact outside the
+|coverage - tau| margin), the cached page selection (exact outside the
+k-th/(k+1)-th score-gap margin), the append state; at the end get_stats()
+must be identical.
+"""
+import pytest
+import torch
+
+from oracle import cvsa_oracle as ref
+from oracle.backend_oracle import OracleCVSABackend
+from cvsa.backend import CVSABackend
+from cvsa.runtime.kv_cache import PagedKVCache, SequenceKVManager
+from cvsa.synthetic import make_paged_inputs, jitter_query
+
+pytestmark = pytest.mark.gpu
+
+OUT_ATOL = 2e-2
+GAP_MARGIN = 1e-5
+COV_MARGIN = 1e-5
+
+
+class _Runtime:
+    """A GPU cache + manager and a CPU oracle copy of the same state."""
+
+    def __init__(self, inp, dev, extra_tokens):
+        B = inp.q.shape[0]
+        nb = inp.k_cache.shape[0]
+        H, D = inp.k_cache.shape[2], inp.k_cache.shape[3]
+        W = inp.block_tables.shape[1]
+        self.cache = PagedKVCache(nb, 16, H, D, device=str(dev))
+        self.cache.k_cache.copy_(inp.k_cache)
+        self.cache.v_cache.copy_(inp.v_cache)
+        self.cache._next_free = inp.used_blocks
+        self.mgr = SequenceKVManager(self.cache, B, W * 16)
+        self.mgr.block_tables.copy_(inp.block_tables)
+        self.mgr.context_lens.copy_(inp.context_lens)
+        pages = [-(-int(c) // 16) for c in inp.context_lens.tolist()]
+        self.mgr._pages_allocated = list(pages)
+        self.mgr.sync_host_state()
+        self.K = inp.k_cache.clone()
+        self.V = inp.v_cache.clone()
+        self.bt = inp.block_tables.clone()
+        self.ctx = inp.context_lens.clone()
+        self.alloc = torch.tensor(pages, dtype=torch.int32)
+        self.nf = inp.used_blocks
+
+    def append(self, k, v, dev):
+        self.mgr.append_tokens_kv(k.to(dev), v.to(dev))
+        for b in range(k.shape[0]):
+            self.nf = ref.append_token_kv(self.K, self.V, self.bt, self.ctx, self.alloc, self.nf,
+                                          b, k[b], v[b], 16)
+
+
+def _margins(ps, budget, cov, tau):
+    """Heads where selection / acceptance is numerically undecidable."""
+    srt = torch.sort(ps, dim=-1, descending=True).values
+    if budget < ps.shape[-1]:
+        gap = (srt[..., budget - 1] - srt[..., budget]).abs()
+        bad_sel = gap <= GAP_MARGIN * srt[..., budget - 1].abs().clamp(min=1.0)
+    else:
+        bad_sel = torch.zeros(ps.shape[:2], dtype=torch.bool)
+    bad_acc = (cov - tau).abs() <= COV_MARGIN
+    return bad_sel, bad_acc
+
+
+def _run(dev, cfg, kw, steps, seed, extra=32):
+    inp = make_paged_inputs(**cfg, seed=seed, max_pages=None, spare_blocks=extra)
+    B, H_q, D = inp.q.shape
+    H = inp.num_kv_heads
+    W = inp.block_tables.shape[1]
+    # leave room in the block table for the appended tokens
+    W2 = W + (steps + 15) // 16 + 1
+    bt = torch.zeros(B, W2, dtype=torch.int32)
+    bt[:, :W] = inp.block_tables
+    inp.block_tables = bt
+    rt = _Runtime(inp, dev, extra)
+    gpu_b = CVSABackend(num_kv_heads=H, num_q_heads=H_q, head_dim=D, block_size=16, **kw)
+    ora_b = OracleCVSABackend(num_kv_heads=H, num_q_heads=H_q, head_dim=D, block_size=16, **kw)
+    g = torch.Generator().manual_seed(seed + 1)
+    excluded = 0
+    for step in range(steps):
+        q = jitter_query(inp.q, 0.3, seed + 100 + step)
+        out = gpu_b(q.to(dev), rt.cache.k_cache, rt.cache.v_cache, rt.mgr.block_tables,
+                    rt.mgr.context_lens, 0).cpu()
+        n_tr = len(ora_b.trace)
+        want = ora_b(q, rt.K, rt.V, rt.bt, rt.ctx, 0)
+        tr = ora_b.trace[n_tr:]
+        err = (out.float() - want.float()).abs().max().item()
+        scoring = [t for t in tr if t["kind"].startswith("score")]
+        if scoring:
+            t = scoring[-1]
+            budget = t["page_indices"].shape[-1]
+            bad_sel, bad_acc = _margins(t["page_scores"], budget, t["coverage"], kw.get(
+                "coverage_threshold", 0.9))
+            excluded += int(bad_sel.sum() + bad_acc.sum())
+            pi, nph = gpu_b._cached_selection[0]
+            ok = ~bad_sel
+            assert torch.equal(pi.cpu()[ok], t["page_indices"][ok]), step
+            assert torch.equal(nph.cpu(), t["n_per_head"])
+            acc = gpu_b._last_accept_mask[0].cpu()
+            ok = ~bad_acc
+            assert torch.equal(acc[ok], t["accept"][ok]), step
+        assert err < OUT_ATOL, (step, err, [t["kind"] for t in tr])
+        gpu_b.step_done(0, 1)
+        ora_b.step_done(0, 1)
+        kn = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+        vn = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+        rt.append(kn, vn, dev)
+    assert excluded == 0
+    sg, so = gpu_b.get_stats(), ora_b.get_stats()
+    assert sg == so, (sg, so)
+    return sg, ora_b.trace
+
+
+CFG1 = dict(batch=1, num_q_heads=32, num_kv_heads=8, head_dim=128, context_len=8192,
+            hot_heads=[0, 2, 4, 6], n_hot=8, hot_shift=12.0)
+
+
+def test_lazy_schedule_cfg1(gpu):
+    """cfg1 shapes, lazy M=5, budget 1/4, tau 0.9, exact recovery."""
+    stats, trace = _run(gpu, CFG1, dict(budget_pct=0.25, coverage_threshold=0.9, lazy=True,
+                                        check_interval=5), steps=12, seed=1000)
+    kinds = {t["kind"] for t in trace}
+    assert "reuse" in kinds and any(k.startswith("score") for k in kinds)
+
+
+def test_fixed_interval_schedule_ragged_batch(gpu):
+    cfg = dict(batch=3, num_q_heads=32, num_kv_heads=8, head_dim=128,
+               context_len=[3000, 1500, 4100], hot_heads=[1, 3], n_hot=6, hot_shift=10.0)
+    _run(gpu, cfg, dict(budget_pct=0.25, coverage_threshold=0.8, lazy=False,
+                        reuse_interval=3), steps=7, seed=2000)
+
+
+def test_lazy_gqa7_every_step_check(gpu):
+    cfg = dict(batch=2, num_q_heads=28, num_kv_heads=4, head_dim=128, context_len=2048,
+               n_hot_range=(0, 16), hot_shift=11.0)
+    _run(gpu, cfg, dict(budget_pct=0.25, coverage_threshold=0.9, lazy=True), steps=6,
+         seed=3000)
+
+
+def test_approx_recovery_and_dense_layer(gpu):
+    cfg = dict(batch=2, num_q_heads=32, num_kv_heads=8, head_dim=128, context_len=2048,
+               hot_heads=[0, 1, 2, 3], n_hot=4, hot_shift=9.0)
+    _run(gpu, cfg, dict(budget_pct=0.10, coverage_threshold=0.9, lazy=True, check_interval=2,
+                        approx_recovery_pct=0.3), steps=5, seed=4000)
+    _run(gpu, cfg, dict(budget_pct=0.10, dense_layers=[0], lazy=True, check_interval=2),
+         steps=3, seed=4001)
+
+
+def test_coverage_interval_variant(gpu):
+    cfg = dict(batch=1, num_q_heads=32, num_kv_heads=8, head_dim=128, context_len=4096,
+               hot_heads=[0, 2, 4, 6], n_hot=8, hot_shift=12.0)
+    _run(gpu, cfg, dict(budget_pct=0.25, coverage_threshold=0.9, lazy=True, check_interval=4,
+                        coverage_interval=1), steps=9, seed=5000)
+
+
+def test_tracing_attributes(gpu):
+    """_last_expanded_selection holds complement pages only when a head rejected."""
+    inp = make_paged_inputs(1, 32, 8, 128, 2048, seed=6000, hot_heads=[0, 2, 4, 6], n_hot=8,
+                            hot_shift=12.0)
+    q, K, V, bt, cl = (t.to(gpu) for t in (inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
+                                            inp.context_lens))
+    b = CVSABackend(8, 32, 128, 16, budget_pct=0.25, coverage_threshold=0.9)
+    b(q, K, V, bt, cl, 3)
+    acc = b._last_accept_mask[3].cpu()
+    exp = b._last_expanded_selection.get(3)
+    if bool(acc.all()):
+        assert exp is None
+    else:
+        comp, n = exp
+        pi, nph = b._cached_selection[3]
+        wc, wn = ref.compute_complement(pi.cpu(), nph.cpu(), inp.context_lens, 16, acc)
+        assert torch.equal(n.cpu(), wn) and torch.equal(comp.cpu(), wc)

@@ -1,0 +1,268 @@
+"""GPU parity of every HIP op (through the C ABI) against the CPU oracle.
+
+Tolerances: page scores 1e-4 relative, coverage 1e-5,
+normalised bf16 outputs max-abs 2e-2 (observed ~1e-2 or below), LSE
+(m + ln l) 1e-3 relative.  Integer work (selection, complement, block
+tables, append) is compared bit-exact.  Selection and accept masks are
+exact on the same page scores; when compared through independently
+computed scores, heads whose k-th / (k+1)-th score gap or |coverage - tau|
+is below a margin are excluded and counted (the seeds keep that count 0).
+"""
+import pytest
+import torch
+
+from oracle import cvsa_oracle as ref
+from cvsa import ops
+from cvsa.synthetic import make_paged_inputs
+
+pytestmark = pytest.mark.gpu
+
+SCORE_RTOL = 1e-4
+OUT_ATOL = 2e-2
+LSE_RTOL = 1e-3
+COV_ATOL = 1e-5
+
+
+def _inputs(seed, B=1, H_q=32, H_kv=8, ctx=2048, W=None, **kw):
+    return make_paged_inputs(B, H_q, H_kv, 128, ctx, seed=seed, max_pages=W, **kw)
+
+
+def _dev(inp, d):
+    return (inp.q.to(d), inp.k_cache.to(d), inp.v_cache.to(d), inp.block_tables.to(d),
+            inp.context_lens.to(d))
+
+
+GEOMS = [  # (B, H_q, H_kv, ctx)
+    (1, 32, 8, 8192),                 # cfg1 shapes
+    (3, 32, 8, [300, 1024, 17]),      # ragged batch, partial last pages
+    (2, 28, 4, [2048, 1000]),         # Qwen GQA 7
+    (2, 64, 8, 1500),                 # GQA 8
+    (2, 8, 8, 999),                   # G = 1
+    (2, 4, 2, 777),                   # G = 2, H_kv = 2
+    (1, 4, 1, 640),                   # H_kv = 1
+    (1, 32, 16, 512),                 # H_kv = 16
+    (2, 12, 4, 321),                  # G = 3
+]
+
+
+@pytest.mark.parametrize("geom", GEOMS)
+def test_score_pages(gpu, geom):
+    B, H_q, H_kv, ctx = geom
+    inp = _inputs(100, B, H_q, H_kv, ctx)
+    q, K, V, bt, cl = _dev(inp, gpu)
+    got = ops.score_pages(q, K, bt, cl, H_kv, H_q // H_kv, 16).cpu()
+    want = ref.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens, H_kv,
+                           H_q // H_kv, 16)
+    assert torch.equal(torch.isinf(got), torch.isinf(want))
+    fin = torch.isfinite(want)
+    err = ((got[fin] - want[fin]).abs() / want[fin].abs().clamp(min=1.0)).max().item()
+    assert err < SCORE_RTOL, err
+
+
+def test_score_pages_block_table_wider_than_context(gpu):
+    inp = _inputs(101, 2, 32, 8, [100, 5000], W=400)
+    q, K, V, bt, cl = _dev(inp, gpu)
+    got = ops.score_pages(q, K, bt, cl, 8, 4, 16).cpu()
+    want = ref.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens, 8, 4, 16)
+    assert torch.equal(torch.isinf(got), torch.isinf(want))
+    fin = torch.isfinite(want)
+    assert (got[fin] - want[fin]).abs().max().item() < 1e-4
+
+
+@pytest.mark.parametrize("W,budget", [(512, 128), (8192, 1024), (37, 3), (1000, 1000),
+                                      (5000, 1), (32768, 4096)])
+def test_select_topk_bit_exact(gpu, W, budget):
+    g = torch.Generator().manual_seed(W + budget)
+    B, H = 2, 4
+    ps = torch.randn(B, H, W, generator=g)
+    ps[0, 1] = (ps[0, 1] * 2).round() / 2          # heavy ties
+    ctx = torch.tensor([W * 16, max(1, (W // 3) * 16 - 5)], dtype=torch.int32)
+    nv = ref.n_valid_pages(ctx, 16)
+    ps[1, :, int(nv[1]):] = float("-inf")
+    idx, nph, acc, cov = ops.select_topk(ps.to(gpu), budget, ctx.to(gpu), 16, tau=0.9)
+    widx, wnph = ref.select_topk(ps, budget, ctx, 16)
+    assert torch.equal(idx.cpu(), widx)
+    assert torch.equal(nph.cpu(), wnph)
+    wacc, wcov = ref.check_coverage(ps, widx, wnph, 0.9)
+    assert (cov.cpu() - wcov).abs().max().item() < COV_ATOL
+    margin = (wcov - 0.9).abs() > 1e-5
+    assert torch.equal(acc.cpu()[margin], wacc[margin])
+
+
+@pytest.mark.parametrize("k,W", [(128, 512), (1000, 2048), (5, 9)])
+def test_check_coverage(gpu, k, W):
+    g = torch.Generator().manual_seed(k * 7 + W)
+    B, H = 3, 8
+    ps = torch.randn(B, H, W, generator=g) * 2
+    sel = torch.stack([torch.stack([torch.randperm(W, generator=g)[:k] for _ in range(H)])
+                       for _ in range(B)]).to(torch.int32)
+    nph = torch.randint(0, k + 1, (B, H), generator=g).to(torch.int32)
+    for tau in (0.0, 0.5, 0.9):
+        acc, cov = ops.check_coverage(ps.to(gpu), sel.to(gpu), nph.to(gpu), tau)
+        wacc, wcov = ref.check_coverage(ps, sel, nph, tau)
+        assert (cov.cpu() - wcov).abs().max().item() < COV_ATOL
+        margin = (wcov - tau).abs() > 1e-5
+        assert torch.equal(acc.cpu()[margin], wacc[margin])
+
+
+def _check_state(o, m, l, wo, wm, wl):
+    fin = torch.isfinite(wm)
+    assert torch.equal(torch.isfinite(m), fin)
+    if fin.any():
+        lse = m[fin] + torch.log(l[fin])
+        wlse = wm[fin] + torch.log(wl[fin])
+        assert ((lse - wlse).abs() / wlse.abs().clamp(min=1.0)).max().item() < LSE_RTOL
+        on = o / l.clamp(min=1e-30).unsqueeze(-1)
+        won = wo / wl.clamp(min=1e-30).unsqueeze(-1)
+        assert (on[fin] - won[fin]).abs().max().item() < 1e-3
+    assert float(l[~fin].abs().max()) == 0.0 if (~fin).any() else True
+
+
+@pytest.mark.parametrize("geom", GEOMS)
+def test_sparse_decode_unnorm_and_norm(gpu, geom):
+    B, H_q, H_kv, ctx = geom
+    G = H_q // H_kv
+    inp = _inputs(200, B, H_q, H_kv, ctx)
+    q, K, V, bt, cl = _dev(inp, gpu)
+    ps = ref.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens, H_kv, G, 16)
+    W = inp.block_tables.shape[1]
+    budget = max(3, W // 4)
+    idx, nph = ref.select_topk(ps, min(budget, W), inp.context_lens, 16)
+    o, m, l = ops.sparse_decode_unnorm(q, K, V, bt, idx.to(gpu), nph.to(gpu), cl, H_kv, G, 16)
+    wo, wm, wl = ref.sparse_decode_unnorm(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
+                                          idx, nph, inp.context_lens, H_kv, G, 16)
+    _check_state(o.cpu(), m.cpu(), l.cpu(), wo, wm, wl)
+    out = ops.sparse_decode(q, K, V, bt, idx.to(gpu), nph.to(gpu), cl, H_kv, G, 16)
+    wout = ref.normalise(wo, wl, torch.bfloat16)
+    assert out.dtype == torch.bfloat16
+    assert (out.cpu().float() - wout.float()).abs().max().item() < OUT_ATOL
+
+
+def test_sparse_decode_edge_cases(gpu):
+    """Empty selections, out-of-range ids, pages past the context, duplicates."""
+    inp = _inputs(201, 2, 32, 8, [700, 40], W=64)
+    q, K, V, bt, cl = _dev(inp, gpu)
+    idx = torch.zeros(2, 8, 6, dtype=torch.int32)
+    idx[:, :, :] = torch.tensor([0, 3, 63, 2, 2, -5], dtype=torch.int32)
+    nph = torch.tensor([[0, 1, 2, 3, 4, 5, 6, 6], [6, 5, 4, 3, 2, 1, 0, 6]], dtype=torch.int32)
+    o, m, l = ops.sparse_decode_unnorm(q, K, V, bt, idx.to(gpu), nph.to(gpu), cl, 8, 4, 16)
+    wo, wm, wl = ref.sparse_decode_unnorm(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
+                                          idx, nph, inp.context_lens, 8, 4, 16)
+    _check_state(o.cpu(), m.cpu(), l.cpu(), wo, wm, wl)
+    out = ops.sparse_decode(q, K, V, bt, idx.to(gpu), nph.to(gpu), cl, 8, 4, 16).cpu()
+    empty = ~torch.isfinite(wm)
+    assert float(out.float()[empty].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("geom", GEOMS[:6])
+def test_dense_decode(gpu, geom):
+    B, H_q, H_kv, ctx = geom
+    G = H_q // H_kv
+    inp = _inputs(300, B, H_q, H_kv, ctx)
+    q, K, V, bt, cl = _dev(inp, gpu)
+    out, (o, m, l) = ops.dense_decode(q, K, V, bt, cl, H_kv, G, 16, return_state=True)
+    wout, (wo, wm, wl) = ref.dense_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
+                                          inp.context_lens, H_kv, G, 16, return_state=True)
+    _check_state(o.cpu(), m.cpu(), l.cpu(), wo, wm, wl)
+    assert (out.cpu().float() - wout.float()).abs().max().item() < OUT_ATOL
+
+
+@pytest.mark.parametrize("geom", GEOMS[:5])
+def test_verified_decode_matches_reference_recovery(gpu, geom):
+    """Fused verified decode vs the reference's draft + complement + merge."""
+    B, H_q, H_kv, ctx = geom
+    G = H_q // H_kv
+    inp = _inputs(400, B, H_q, H_kv, ctx)
+    q, K, V, bt, cl = _dev(inp, gpu)
+    ps = ref.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens, H_kv, G, 16)
+    W = inp.block_tables.shape[1]
+    idx, nph = ref.select_topk(ps, max(3, W // 8), inp.context_lens, 16)
+    g = torch.Generator().manual_seed(1)
+    accept = torch.rand(B, H_kv, generator=g) > 0.5
+    out = ops.verified_decode(q, K, V, bt, cl, idx.to(gpu), nph.to(gpu), accept.to(gpu), H_kv,
+                              G, 16)
+    want = ref.verified_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
+                               inp.context_lens, idx, nph, accept, H_kv, G, 16)
+    assert (out.cpu().float() - want.float()).abs().max().item() < OUT_ATOL
+
+
+def test_compute_complement_exact(gpu):
+    g = torch.Generator().manual_seed(9)
+    B, H, k = 3, 8, 20
+    ctx = torch.tensor([16 * 64, 16 * 10 + 3, 16 * 64 - 1], dtype=torch.int32)
+    idx = torch.randint(-2, 70, (B, H, k), generator=g).to(torch.int32)
+    nph = torch.randint(0, k + 1, (B, H), generator=g).to(torch.int32)
+    acc = torch.rand(B, H, generator=g) > 0.6
+    comp, n = ops.compute_complement(idx.to(gpu), nph.to(gpu), ctx.to(gpu), 16, acc.to(gpu))
+    wcomp, wn = ref.compute_complement(idx, nph, ctx, 16, acc)
+    assert torch.equal(n.cpu(), wn) and torch.equal(comp.cpu(), wcomp)
+    from cvsa.complement import compute_complement_pages
+    c2, n2 = compute_complement_pages(idx.to(gpu), nph.to(gpu), ctx.to(gpu), 16, acc.to(gpu))
+    wc2, wn2 = ref.compute_complement_pages(idx, nph, ctx, 16, acc)
+    assert torch.equal(n2.cpu(), wn2) and torch.equal(c2.cpu(), wc2)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_lse_merge(gpu, out_dtype):
+    g = torch.Generator().manual_seed(4)
+    B, H_kv, G, D = 3, 8, 4, 128
+    od, oc = torch.randn(B, H_kv * G, D, generator=g), torch.randn(B, H_kv * G, D, generator=g)
+    md, mc = torch.randn(B, H_kv * G, generator=g), torch.randn(B, H_kv * G, generator=g)
+    ld, lc = torch.rand(B, H_kv * G, generator=g) + .1, torch.rand(B, H_kv * G, generator=g) + .1
+    mc[0, :4] = float("-inf")
+    lc[0, :4] = 0.0
+    acc = torch.rand(B, H_kv, generator=g) > 0.5
+    args = [t.to(gpu) for t in (od, md, ld, oc, mc, lc, acc)]
+    got = ops.lse_merge(*args, H_kv, G, out_dtype).cpu()
+    want = ref.lse_merge(od, md, ld, oc, mc, lc, acc, G, out_dtype)
+    tol = 1e-5 if out_dtype == torch.float32 else 1e-2
+    assert (got.float() - want.float()).abs().max().item() < tol
+    from cvsa.lse_merge import selective_lse_merge
+    got2 = selective_lse_merge(*args, G, out_dtype).cpu()
+    assert torch.equal(got2, got)
+
+
+def test_append_kv_matches_reference_loop(gpu):
+    from cvsa.runtime.kv_cache import PagedKVCache, SequenceKVManager
+    B, H, D = 5, 8, 128
+    cache = PagedKVCache(64, 16, H, D, device=str(gpu))
+    mgr = SequenceKVManager(cache, B, 16 * 8)
+    g = torch.Generator().manual_seed(2)
+    lens = [15, 16, 0, 33, 47]
+    for b, n in enumerate(lens):
+        if n:
+            kv = torch.randn(n, H, D, generator=g).to(torch.bfloat16)
+            mgr.prefill_kv(b, kv.to(gpu), (-kv).to(gpu))
+    # CPU oracle copy of the state
+    K = cache.k_cache.cpu().clone()
+    V = cache.v_cache.cpu().clone()
+    bt = mgr.block_tables.cpu().clone()
+    ctx = mgr.context_lens.cpu().clone()
+    alloc = torch.tensor(mgr._pages_allocated, dtype=torch.int32)
+    nf = cache._next_free
+    for step in range(20):
+        kn = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+        vn = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+        if step % 3 == 0:
+            mgr.append_token_kv(1, kn[1].to(gpu), vn[1].to(gpu))
+            nf = ref.append_token_kv(K, V, bt, ctx, alloc, nf, 1, kn[1], vn[1], 16)
+        else:
+            mgr.append_tokens_kv(kn.to(gpu), vn.to(gpu))
+            for b in range(B):
+                nf = ref.append_token_kv(K, V, bt, ctx, alloc, nf, b, kn[b], vn[b], 16)
+    assert cache._next_free == nf
+    assert torch.equal(mgr.block_tables.cpu(), bt)
+    assert torch.equal(mgr.context_lens.cpu(), ctx)
+    assert mgr._ctx_host == ctx.tolist()
+    assert torch.equal(cache.k_cache.cpu(), K) and torch.equal(cache.v_cache.cpu(), V)
+
+
+def test_ops_reject_bad_input(gpu):
+    inp = _inputs(500, 1, 32, 8, 256)
+    q, K, V, bt, cl = _dev(inp, gpu)
+    with pytest.raises(ValueError):
+        ops.score_pages(q.cpu(), K, bt, cl, 8, 4, 16)
+    with pytest.raises(NotImplementedError):
+        ops.score_pages(q[:, :, :64].contiguous(), K[..., :64].contiguous(), bt, cl, 8, 4, 16)
+    with pytest.raises(ValueError):
+        ops.select_topk(torch.zeros(1, 8, 16, device=gpu), 17, cl, 16)
