@@ -29,13 +29,14 @@
 // merge of the draft and complement partial softmaxes.
 #include "cvsa_common.h"
 #include <hip/hip_fp16.h>
+#include <stdlib.h>
 
 namespace cvsa {
 
 constexpr int kDecThreads = 256;
 constexpr int kDecWaves = kDecThreads / kWave;
 constexpr int kPartStride = kHeadDim + 2;  // o[D], m, l
-constexpr int kTargetWorkgroups = 640;     // ~2.5 workgroups per CU
+constexpr int kMaxSplits = kWave;          // partials per head (one per lane in the merge)
 constexpr int kMinPagesPerSplit = 8;       // two pages per wave
 
 struct DecodeArgs {
@@ -73,6 +74,21 @@ __device__ __forceinline__ void store_out(void *out, int dtype, int64_t i, float
   }
 }
 
+// Weighted sum of NS split partials for one output element; loads are
+// unconditional (clamped to the last active split, whose weight beyond
+// n_act is zero) so that all NS loads are in flight together.
+template <int NS>
+__device__ __forceinline__ float combine_splits(const float *hp, const float *w, int n_act,
+                                                int stride, int d) {
+  float v[NS];
+#pragma unroll
+  for (int sp = 0; sp < NS; ++sp) v[sp] = hp[(int64_t)min(sp, n_act - 1) * stride + d];
+  float acc = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < NS; ++sp) acc += w[sp] * v[sp];
+  return acc;
+}
+
 template <int G, int LPT>
 __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeArgs a) {
   constexpr int E = kHeadDim / LPT;      // d-elements per lane
@@ -84,6 +100,8 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
   __shared__ float s_o[kDecWaves][G][kHeadDim];
   __shared__ float s_m[kDecWaves][G];
   __shared__ float s_l[kDecWaves][G];
+  __shared__ float s_w[G][kMaxSplits];
+  __shared__ float s_M[G], s_L[G];
   __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
@@ -125,34 +143,17 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
         qv[g][v] = *reinterpret_cast<const uint4 *>(
             a.q + b * a.q_sb + (int64_t)(h * G + g) * a.q_sh + seg * E + v * 8);
 
-    const int64_t row_stride = (int64_t)a.H_kv * kHeadDim;  // between tokens
+    const int64_t row_stride = (int64_t)a.H_kv * kHeadDim;          // between tokens
+    const int64_t page_elems = (int64_t)kPageTokens * row_stride;   // between blocks
+    const int64_t lane_off = (int64_t)h * kHeadDim + seg * E + (int64_t)tg * row_stride;
     const int32_t *idx_row = listed ? a.page_idx + (int64_t)bh * a.idx_stride : nullptr;
 
-    for (int r = r0 + wave; r < r1; r += kDecWaves) {
-      const int lp = listed ? idx_row[r] : r;
-      int ntok = 0;
-      int64_t base = 0;
-      if (lp >= 0 && lp < a.W) {
-        const int phys = a.block_tables[b * a.bt_sb + lp];
-        if (phys >= 0 && phys < a.num_blocks) {
-          ntok = min(kPageTokens, ctx - lp * kPageTokens);
-          base = ((int64_t)phys * kPageTokens * a.H_kv + h) * kHeadDim + seg * E;
-        }
-      }
-      if (ntok <= 0) continue;  // no valid token: contributes nothing
-
-      uint4 kr[NPASS][NV], vr[NPASS][NV];
-#pragma unroll
-      for (int ps = 0; ps < NPASS; ++ps) {
-        const int64_t off = base + (int64_t)(ps * TPP + tg) * row_stride;
-#pragma unroll
-        for (int v = 0; v < NV; ++v)
-          kr[ps][v] = *reinterpret_cast<const uint4 *>(a.k_cache + off + v * 8);
-#pragma unroll
-        for (int v = 0; v < NV; ++v)
-          vr[ps][v] = *reinterpret_cast<const uint4 *>(a.v_cache + off + v * 8);
-      }
-
+    // This wave's pages are r0 + wave + 4j.  Lane j of the wave looks up
+    // page j's block id and valid-token count up front; the page loop then
+    // reads them with readlane and keeps the next page's K/V loads in flight
+    // while the current page is being consumed.
+    const int npw = (r1 - r0 - wave + kDecWaves - 1) / kDecWaves;
+    auto consume = [&](const uint4 (&kr)[NPASS][NV], const uint4 (&vr)[NPASS][NV], int ntok) {
       float s[NPASS][G];
 #pragma unroll
       for (int ps = 0; ps < NPASS; ++ps) {
@@ -166,7 +167,6 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
           s[ps][g] = valid ? acc : -INFINITY;
         }
       }
-
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float pm = s[0][g];
@@ -197,6 +197,48 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
             o[g][v * 8 + 7] += p * bf16_hi(w.w);
           }
         }
+      }
+    };
+
+    for (int c0 = 0; c0 < npw; c0 += kWave) {
+      const int cn = min(kWave, npw - c0);
+      int my_phys = 0, my_ntok = 0;
+      if (lane < cn) {
+        const int r = r0 + wave + kDecWaves * (c0 + lane);
+        const int lp = listed ? idx_row[r] : r;
+        if (lp >= 0 && lp < a.W) {
+          const int phys = a.block_tables[b * a.bt_sb + lp];
+          if (phys >= 0 && phys < a.num_blocks) {
+            my_phys = phys;
+            my_ntok = min(kPageTokens, ctx - lp * kPageTokens);
+          }
+        }
+      }
+      auto fetch = [&](int j, uint4 (&kr)[NPASS][NV], uint4 (&vr)[NPASS][NV]) {
+        const int ntok = __builtin_amdgcn_readlane(my_ntok, j);
+        if (ntok > 0) {
+          const int phys = __builtin_amdgcn_readlane(my_phys, j);
+          const int64_t base = (int64_t)phys * page_elems + lane_off;
+#pragma unroll
+          for (int ps = 0; ps < NPASS; ++ps) {
+            const int64_t off = base + (int64_t)(ps * TPP) * row_stride;
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+              kr[ps][v] = *reinterpret_cast<const uint4 *>(a.k_cache + off + v * 8);
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+              vr[ps][v] = *reinterpret_cast<const uint4 *>(a.v_cache + off + v * 8);
+          }
+        }
+        return ntok;
+      };
+      uint4 kA[NPASS][NV], vA[NPASS][NV], kB[NPASS][NV], vB[NPASS][NV];
+      int ntA = fetch(0, kA, vA);
+      for (int j = 0; j < cn; j += 2) {
+        const int ntB = (j + 1 < cn) ? fetch(j + 1, kB, vB) : 0;
+        if (ntA > 0) consume(kA, vA, ntA);
+        ntA = (j + 2 < cn) ? fetch(j + 2, kA, vA) : 0;
+        if (ntB > 0) consume(kB, vB, ntB);
       }
     }
 
@@ -260,25 +302,41 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
   if (!s_last) return;
   __threadfence();
 
-  const int n_act = (n + pps - 1) / pps;
+  const int n_act = (n + pps - 1) / pps;  // splits that stored a partial, <= kMaxSplits
   const float *hp = a.part + (int64_t)bh * a.n_splits * G * kPartStride;
+  // Split weights exp(m_s - M) and the merged l, one wave per group member.
+  for (int g = wave; g < G; g += kDecWaves) {
+    float mv = -INFINITY, lv = 0.f;
+    if (lane < n_act) {
+      mv = hp[(lane * G + g) * kPartStride + kHeadDim];
+      lv = hp[(lane * G + g) * kPartStride + kHeadDim + 1];
+    }
+    const float M = wave_max_from_groups<1>(mv);
+    const float w = (mv == -INFINITY) ? 0.f : fast_exp(mv - M);
+    const float L = wave_sum_from_groups<1>(w * lv);
+    s_w[g][lane] = w;
+    if (lane == 0) {
+      s_M[g] = M;
+      s_L[g] = L;
+    }
+  }
+  __syncthreads();
   for (int i = threadIdx.x; i < G * kHeadDim; i += kDecThreads) {
     const int g = i / kHeadDim, d = i - g * kHeadDim;
-    float M = -INFINITY;
-    for (int sp = 0; sp < n_act; ++sp)
-      M = fmaxf(M, hp[(sp * G + g) * kPartStride + kHeadDim]);
-    float O = 0.f, L = 0.f;
-    if (M != -INFINITY) {
-      for (int sp = 0; sp < n_act; ++sp) {
-        const float *ps = hp + (sp * G + g) * kPartStride;
-        const float ms = ps[kHeadDim];
-        if (ms != -INFINITY) {
-          const float f = fast_exp(ms - M);
-          O += ps[d] * f;
-          L += ps[kHeadDim + 1] * f;
-        }
-      }
+    float O = 0.f;
+    if (n_act > 0) {
+      const float *base = hp + g * kPartStride;
+      const int stride = G * kPartStride;
+      if (n_act <= 8)
+        O = combine_splits<8>(base, s_w[g], n_act, stride, d);
+      else if (n_act <= 16)
+        O = combine_splits<16>(base, s_w[g], n_act, stride, d);
+      else if (n_act <= 32)
+        O = combine_splits<32>(base, s_w[g], n_act, stride, d);
+      else
+        O = combine_splits<64>(base, s_w[g], n_act, stride, d);
     }
+    const float M = s_M[g], L = s_L[g];
     const int64_t qrow = (int64_t)bh * G + g;  // == b * H_q + h * G + g
     if (a.o_unnorm != nullptr) {
       a.o_unnorm[qrow * kHeadDim + d] = O;
@@ -308,16 +366,29 @@ struct DecodePlan {
   int pps_sel, pps_all, n_splits;
 };
 
-// Pages per split: spread the heads over ~kTargetWorkgroups workgroups with
-// at least two pages per wave.
+static int target_workgroups() {
+  static const int v = [] {
+    const char *e = getenv("CVSA_DECODE_TARGET_WGS");  // tuning knob
+    const int x = e ? atoi(e) : 0;
+    return x > 0 ? x : 512;
+  }();
+  return v;
+}
+
+// Pages per split: spread the heads over ~target_workgroups() workgroups,
+// at least two pages per wave and at most kMaxSplits splits per head.
 static DecodePlan plan_decode(int B, int H_kv, int max_sel, int W, bool listed,
                               bool all_pages) {
   const int heads = B * H_kv;
-  const int wg_per_head = heads >= kTargetWorkgroups ? 1 : kTargetWorkgroups / heads;
+  const int target = target_workgroups();
+  int wg_per_head = heads >= target ? 1 : target / heads;
+  if (wg_per_head > kMaxSplits) wg_per_head = kMaxSplits;
   auto pps_for = [&](int pages) {
     int pps = (pages + wg_per_head - 1) / wg_per_head;
     if (pps < kMinPagesPerSplit) pps = kMinPagesPerSplit;
-    return (pps + kDecWaves - 1) / kDecWaves * kDecWaves;
+    pps = (pps + kDecWaves - 1) / kDecWaves * kDecWaves;
+    while ((pages + pps - 1) / pps > kMaxSplits) pps += kDecWaves;
+    return pps;
   };
   DecodePlan p;
   p.pps_sel = pps_for(listed ? max_sel : 0);
