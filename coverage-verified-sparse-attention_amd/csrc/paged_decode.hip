@@ -33,11 +33,9 @@
 
 namespace cvsa {
 
-constexpr int kDecThreads = 256;
-constexpr int kDecWaves = kDecThreads / kWave;
 constexpr int kPartStride = kHeadDim + 2;  // o[D], m, l
-constexpr int kMaxSplits = kWave;          // partials per head (one per lane in the merge)
-constexpr int kMinPagesPerSplit = 8;       // two pages per wave
+constexpr int kMaxSplits = 32;             // partials per head
+constexpr int kMinPagesPerSplit = 8;       // at least one page per wave
 
 struct DecodeArgs {
   const uint16_t *q;
@@ -60,7 +58,6 @@ struct DecodeArgs {
   void *out;
   int out_dtype;
   float *part;
-  uint32_t *counters;
   unsigned long long *work;  // optional effective-budget counters
 };
 
@@ -74,35 +71,101 @@ __device__ __forceinline__ void store_out(void *out, int dtype, int64_t i, float
   }
 }
 
-// Weighted sum of NS split partials for one output element; loads are
-// unconditional (clamped to the last active split, whose weight beyond
-// n_act is zero) so that all NS loads are in flight together.
-template <int NS>
-__device__ __forceinline__ float combine_splits(const float *hp, const float *w, int n_act,
-                                                int stride, int d) {
-  float v[NS];
-#pragma unroll
-  for (int sp = 0; sp < NS; ++sp) v[sp] = hp[(int64_t)min(sp, n_act - 1) * stride + d];
-  float acc = 0.f;
-#pragma unroll
-  for (int sp = 0; sp < NS; ++sp) acc += w[sp] * v[sp];
-  return acc;
+
+__device__ __forceinline__ void write_outputs(const DecodeArgs &a, int64_t qrow, int d, float O,
+                                              float M, float L) {
+  if (a.o_unnorm != nullptr) {
+    a.o_unnorm[qrow * kHeadDim + d] = O;
+    if (d == 0) {
+      a.m_out[qrow] = M;
+      a.l_out[qrow] = L;
+    }
+  }
+  if (a.out != nullptr) store_out(a.out, a.out_dtype, qrow * kHeadDim + d, O / fmaxf(L, 1e-6f));
 }
 
-template <int G, int LPT>
-__global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeArgs a) {
+// Effective-budget counters: pages attended by this head and n_valid(b).
+__device__ __forceinline__ void add_work(const DecodeArgs &a, int n, int ctx) {
+  atomicAdd(&a.work[0], (unsigned long long)n);
+  atomicAdd(&a.work[1], (unsigned long long)max(0, n_valid_pages(ctx, kPageTokens)));
+}
+
+
+// Page walk of one head.  MODE is a template parameter so that verified mode
+// loads accept[bh] and n_per_head[bh] unconditionally and picks (n, pages
+// per split) with selects: an earlier form that branched on null pointers
+// was miscompiled (a live scalar register was reused across the branch).
+enum { kModeAll = 0, kModeListed = 1, kModeVerified = 2 };
+
+template <int MODE>
+struct HeadWalk {
+  bool listed;
+  int n, pps;
+  __device__ __forceinline__ HeadWalk(const DecodeArgs &a, int bh, int ctx) {
+    const int n_all = max(0, min(n_valid_pages(ctx, kPageTokens), a.W));
+    if constexpr (MODE == kModeAll) {
+      listed = false;
+      n = n_all;
+      pps = a.pps_all;
+    } else {
+      const int n_list = min(max(__builtin_amdgcn_readfirstlane(a.n_pages[bh]), 0), a.max_sel);
+      if constexpr (MODE == kModeListed) {
+        listed = true;
+        n = n_list;
+        pps = a.pps_sel;
+      } else {
+        listed = __builtin_amdgcn_readfirstlane((int)a.accept[bh]) != 0;
+        n = listed ? n_list : n_all;
+        pps = listed ? a.pps_sel : a.pps_all;
+      }
+    }
+  }
+};
+
+// Merged (o, m, l) of one output element over NS split partials.  All loads
+// are issued together (indices clamped to the last active split; splits at
+// or beyond n_act get weight zero), so the merge costs one memory round trip.
+template <int NS>
+__device__ __forceinline__ void merge_splits(const float *hp, int n_act, int stride, int d,
+                                             float &O, float &M, float &L) {
+  float mv[NS], lv[NS], ov[NS];
+#pragma unroll
+  for (int sp = 0; sp < NS; ++sp) {
+    const float *ps = hp + (int64_t)min(sp, n_act - 1) * stride;
+    mv[sp] = ps[kHeadDim];
+    lv[sp] = ps[kHeadDim + 1];
+    ov[sp] = ps[d];
+  }
+  M = -INFINITY;
+#pragma unroll
+  for (int sp = 0; sp < NS; ++sp)
+    if (sp < n_act) M = fmaxf(M, mv[sp]);
+  O = 0.f;
+  L = 0.f;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int sp = 0; sp < NS; ++sp) {
+      const float w = (sp < n_act && mv[sp] != -INFINITY) ? fast_exp(mv[sp] - M) : 0.f;
+      O += w * ov[sp];
+      L += w * lv[sp];
+    }
+  }
+}
+
+// NW waves per workgroup, PD pages of K/V in flight per wave.
+template <int G, int LPT, int NW, int PD, int MODE>
+__global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeArgs a) {
+  constexpr int NT = NW * kWave;         // threads per workgroup
   constexpr int E = kHeadDim / LPT;      // d-elements per lane
   constexpr int NV = E / 8;              // 16-byte vectors per lane per row
+  constexpr int VSTRIDE = LPT * 8;       // elements between a lane's vectors
   constexpr int TPP = kWave / LPT;       // token slots per pass
   constexpr int NPASS = kPageTokens / TPP;
   static_assert(NPASS >= 1 && NV >= 1, "bad lane layout");
 
-  __shared__ float s_o[kDecWaves][G][kHeadDim];
-  __shared__ float s_m[kDecWaves][G];
-  __shared__ float s_l[kDecWaves][G];
-  __shared__ float s_w[G][kMaxSplits];
-  __shared__ float s_M[G], s_L[G];
-  __shared__ int s_last;
+  __shared__ float s_o[NW][G][kHeadDim];
+  __shared__ float s_m[NW][G];
+  __shared__ float s_l[NW][G];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -112,17 +175,11 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
   const int split = blockIdx.x;
   const int b = bh / a.H_kv;
   const int h = bh - b * a.H_kv;
-  const int ctx = a.ctx_lens[b];
+  const int ctx = __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
 
-  const bool listed = a.page_idx != nullptr && (a.accept == nullptr || a.accept[bh] != 0);
-  int n, pps;
-  if (listed) {
-    n = min(max(a.n_pages[bh], 0), a.max_sel);
-    pps = a.pps_sel;
-  } else {
-    n = max(0, min(n_valid_pages(ctx, kPageTokens), a.W));
-    pps = a.pps_all;
-  }
+  const HeadWalk<MODE> hw(a, bh, ctx);
+  const bool listed = hw.listed;
+  const int n = hw.n, pps = hw.pps;
   const int r0 = split * pps;
   const int r1 = min(n, r0 + pps);
 
@@ -135,24 +192,21 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
 #pragma unroll
       for (int e = 0; e < E; ++e) o[g][e] = 0.f;
     }
+    // Lane vector v covers elements v*VSTRIDE + seg*8 .. +8, so each load
+    // instruction reads whole 128-byte lines of every row it touches.
     uint4 qv[G][NV];
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int v = 0; v < NV; ++v)
         qv[g][v] = *reinterpret_cast<const uint4 *>(
-            a.q + b * a.q_sb + (int64_t)(h * G + g) * a.q_sh + seg * E + v * 8);
+            a.q + b * a.q_sb + (int64_t)(h * G + g) * a.q_sh + v * VSTRIDE + seg * 8);
 
     const int64_t row_stride = (int64_t)a.H_kv * kHeadDim;          // between tokens
     const int64_t page_elems = (int64_t)kPageTokens * row_stride;   // between blocks
-    const int64_t lane_off = (int64_t)h * kHeadDim + seg * E + (int64_t)tg * row_stride;
+    const int64_t lane_off = (int64_t)h * kHeadDim + seg * 8 + (int64_t)tg * row_stride;
     const int32_t *idx_row = listed ? a.page_idx + (int64_t)bh * a.idx_stride : nullptr;
 
-    // This wave's pages are r0 + wave + 4j.  Lane j of the wave looks up
-    // page j's block id and valid-token count up front; the page loop then
-    // reads them with readlane and keeps the next page's K/V loads in flight
-    // while the current page is being consumed.
-    const int npw = (r1 - r0 - wave + kDecWaves - 1) / kDecWaves;
     auto consume = [&](const uint4 (&kr)[NPASS][NV], const uint4 (&vr)[NPASS][NV], int ntok) {
       float s[NPASS][G];
 #pragma unroll
@@ -182,7 +236,7 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
         }
 #pragma unroll
         for (int ps = 0; ps < NPASS; ++ps) {
-          const float p = fast_exp(s[ps][g] - m[g]);
+          const float p = s[ps][g] == -INFINITY ? 0.f : fast_exp(s[ps][g] - m[g]);
           l[g] += p;
 #pragma unroll
           for (int v = 0; v < NV; ++v) {
@@ -200,11 +254,15 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
       }
     };
 
+    // This wave's pages are r0 + wave + NW*j.  Lane j looks up page j's block
+    // id and valid-token count up front; the page loop reads them with
+    // readlane and keeps PD pages of K/V loads in flight.
+    const int npw = (r1 - r0 - wave + NW - 1) / NW;
     for (int c0 = 0; c0 < npw; c0 += kWave) {
       const int cn = min(kWave, npw - c0);
       int my_phys = 0, my_ntok = 0;
       if (lane < cn) {
-        const int r = r0 + wave + kDecWaves * (c0 + lane);
+        const int r = r0 + wave + NW * (c0 + lane);
         const int lp = listed ? idx_row[r] : r;
         if (lp >= 0 && lp < a.W) {
           const int phys = a.block_tables[b * a.bt_sb + lp];
@@ -214,31 +272,36 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
           }
         }
       }
+      // Loads are unconditional so that no branch separates a prefetch from
+      // the page being consumed: a page without valid tokens reads block 0
+      // (in bounds) and is masked out by consume(); prefetches past the end
+      // re-read the wave's last page (already cached) and are never consumed.
       auto fetch = [&](int j, uint4 (&kr)[NPASS][NV], uint4 (&vr)[NPASS][NV]) {
-        const int ntok = __builtin_amdgcn_readlane(my_ntok, j);
-        if (ntok > 0) {
-          const int phys = __builtin_amdgcn_readlane(my_phys, j);
-          const int64_t base = (int64_t)phys * page_elems + lane_off;
+        const int phys = __builtin_amdgcn_readlane(my_phys, j);
+        const int64_t base = (int64_t)phys * page_elems + lane_off;
 #pragma unroll
-          for (int ps = 0; ps < NPASS; ++ps) {
-            const int64_t off = base + (int64_t)(ps * TPP) * row_stride;
+        for (int ps = 0; ps < NPASS; ++ps) {
+          const int64_t off = base + (int64_t)(ps * TPP) * row_stride;
 #pragma unroll
-            for (int v = 0; v < NV; ++v)
-              kr[ps][v] = *reinterpret_cast<const uint4 *>(a.k_cache + off + v * 8);
+          for (int v = 0; v < NV; ++v)
+            kr[ps][v] = *reinterpret_cast<const uint4 *>(a.k_cache + off + v * VSTRIDE);
 #pragma unroll
-            for (int v = 0; v < NV; ++v)
-              vr[ps][v] = *reinterpret_cast<const uint4 *>(a.v_cache + off + v * 8);
-          }
+          for (int v = 0; v < NV; ++v)
+            vr[ps][v] = *reinterpret_cast<const uint4 *>(a.v_cache + off + v * VSTRIDE);
         }
-        return ntok;
+        return __builtin_amdgcn_readlane(my_ntok, j);
       };
-      uint4 kA[NPASS][NV], vA[NPASS][NV], kB[NPASS][NV], vB[NPASS][NV];
-      int ntA = fetch(0, kA, vA);
-      for (int j = 0; j < cn; j += 2) {
-        const int ntB = (j + 1 < cn) ? fetch(j + 1, kB, vB) : 0;
-        if (ntA > 0) consume(kA, vA, ntA);
-        ntA = (j + 2 < cn) ? fetch(j + 2, kA, vA) : 0;
-        if (ntB > 0) consume(kB, vB, ntB);
+      uint4 kb[PD][NPASS][NV], vb[PD][NPASS][NV];
+      int nt[PD];
+#pragma unroll
+      for (int p = 0; p < PD - 1; ++p) nt[p] = fetch(min(p, cn - 1), kb[p], vb[p]);
+      for (int j = 0; j < cn; j += PD) {
+#pragma unroll
+        for (int u = 0; u < PD; ++u) {
+          const int slot = (u + PD - 1) % PD;  // slot of page j+u+PD-1
+          nt[slot] = fetch(min(j + u + PD - 1, cn - 1), kb[slot], vb[slot]);
+          if (j + u < cn) consume(kb[u], vb[u], nt[u]);
+        }
       }
     }
 
@@ -253,7 +316,9 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < E; ++e) s_o[wave][g][seg * E + e] = o[g][e];
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s_o[wave][g][v * VSTRIDE + seg * 8 + e] = o[g][v * 8 + e];
     }
     if (lane == 0) {
 #pragma unroll
@@ -265,95 +330,74 @@ __global__ __launch_bounds__(kDecThreads) void paged_decode_kernel(const DecodeA
   }
   __syncthreads();
 
-  // Merge the four waves and store this workgroup's partial state.
-  if (r0 < r1) {
+  // Merge the waves.  With one split per launch the workgroup owns the whole
+  // head and writes the outputs; otherwise it stores its partial state for
+  // the merge kernel.
+  if (r0 < r1 || a.n_splits == 1) {
     float *my_part = a.part + ((int64_t)bh * a.n_splits + split) * G * kPartStride;
-    for (int i = threadIdx.x; i < G * kHeadDim; i += kDecThreads) {
+    for (int i = threadIdx.x; i < G * kHeadDim; i += NT) {
       const int g = i / kHeadDim, d = i - g * kHeadDim;
-      float M = s_m[0][g];
+      float M = -INFINITY, O = 0.f, L = 0.f;
+      if (r0 < r1) {
+        M = s_m[0][g];
 #pragma unroll
-      for (int w = 1; w < kDecWaves; ++w) M = fmaxf(M, s_m[w][g]);
-      float O = 0.f, L = 0.f;
-      if (M != -INFINITY) {
+        for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w][g]);
+        if (M != -INFINITY) {
 #pragma unroll
-        for (int w = 0; w < kDecWaves; ++w) {
-          const float mw = s_m[w][g];
-          if (mw != -INFINITY) {
-            const float f = fast_exp(mw - M);
-            O += s_o[w][g][d] * f;
-            L += s_l[w][g] * f;
+          for (int w = 0; w < NW; ++w) {
+            const float mw = s_m[w][g];
+            if (mw != -INFINITY) {
+              const float f = fast_exp(mw - M);
+              O += s_o[w][g][d] * f;
+              L += s_l[w][g] * f;
+            }
           }
         }
       }
-      my_part[g * kPartStride + d] = O;
-      if (d == 0) {
-        my_part[g * kPartStride + kHeadDim] = M;
-        my_part[g * kPartStride + kHeadDim + 1] = L;
+      if (a.n_splits == 1) {
+        write_outputs(a, (int64_t)bh * G + g, d, O, M, L);
+      } else {
+        my_part[g * kPartStride + d] = O;
+        if (d == 0) {
+          my_part[g * kPartStride + kHeadDim] = M;
+          my_part[g * kPartStride + kHeadDim + 1] = L;
+        }
       }
     }
   }
+  if (a.n_splits == 1 && threadIdx.x == 0 && a.work != nullptr) add_work(a, n, ctx);
+}
 
-  // Completion counter: the last workgroup of this head merges all partials.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0)
-    s_last = atomicAdd(&a.counters[bh], 1u) == (uint32_t)(a.n_splits - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
+// Merge of the split partials: one thread per (q-head, d) element.  Runs as a
+// second launch, so the partial stores of the first are visible without any
+// cache maintenance inside either kernel.
+template <int G, int MODE>
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArgs a) {
+  const int bh = blockIdx.y;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= G * kHeadDim) return;
+  const int g = i / kHeadDim, d = i - g * kHeadDim;
+  const int b = bh / a.H_kv;
+  const int ctx = __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
+  const HeadWalk<MODE> hw(a, bh, ctx);
+  const bool listed = hw.listed;
+  const int n = hw.n, pps = hw.pps;
   const int n_act = (n + pps - 1) / pps;  // splits that stored a partial, <= kMaxSplits
-  const float *hp = a.part + (int64_t)bh * a.n_splits * G * kPartStride;
-  // Split weights exp(m_s - M) and the merged l, one wave per group member.
-  for (int g = wave; g < G; g += kDecWaves) {
-    float mv = -INFINITY, lv = 0.f;
-    if (lane < n_act) {
-      mv = hp[(lane * G + g) * kPartStride + kHeadDim];
-      lv = hp[(lane * G + g) * kPartStride + kHeadDim + 1];
-    }
-    const float M = wave_max_from_groups<1>(mv);
-    const float w = (mv == -INFINITY) ? 0.f : fast_exp(mv - M);
-    const float L = wave_sum_from_groups<1>(w * lv);
-    s_w[g][lane] = w;
-    if (lane == 0) {
-      s_M[g] = M;
-      s_L[g] = L;
-    }
+  float O = 0.f, M = -INFINITY, L = 0.f;
+  if (n_act > 0) {
+    const float *base = a.part + (int64_t)bh * a.n_splits * G * kPartStride + g * kPartStride;
+    const int stride = G * kPartStride;
+    if (n_act <= 4)
+      merge_splits<4>(base, n_act, stride, d, O, M, L);
+    else if (n_act <= 8)
+      merge_splits<8>(base, n_act, stride, d, O, M, L);
+    else if (n_act <= 16)
+      merge_splits<16>(base, n_act, stride, d, O, M, L);
+    else
+      merge_splits<kMaxSplits>(base, n_act, stride, d, O, M, L);
   }
-  __syncthreads();
-  for (int i = threadIdx.x; i < G * kHeadDim; i += kDecThreads) {
-    const int g = i / kHeadDim, d = i - g * kHeadDim;
-    float O = 0.f;
-    if (n_act > 0) {
-      const float *base = hp + g * kPartStride;
-      const int stride = G * kPartStride;
-      if (n_act <= 8)
-        O = combine_splits<8>(base, s_w[g], n_act, stride, d);
-      else if (n_act <= 16)
-        O = combine_splits<16>(base, s_w[g], n_act, stride, d);
-      else if (n_act <= 32)
-        O = combine_splits<32>(base, s_w[g], n_act, stride, d);
-      else
-        O = combine_splits<64>(base, s_w[g], n_act, stride, d);
-    }
-    const float M = s_M[g], L = s_L[g];
-    const int64_t qrow = (int64_t)bh * G + g;  // == b * H_q + h * G + g
-    if (a.o_unnorm != nullptr) {
-      a.o_unnorm[qrow * kHeadDim + d] = O;
-      if (d == 0) {
-        a.m_out[qrow] = M;
-        a.l_out[qrow] = L;
-      }
-    }
-    if (a.out != nullptr) store_out(a.out, a.out_dtype, qrow * kHeadDim + d, O / fmaxf(L, 1e-6f));
-  }
-  if (threadIdx.x == 0) {
-    a.counters[bh] = 0u;
-    if (a.work != nullptr) {
-      atomicAdd(&a.work[0], (unsigned long long)n);
-      atomicAdd(&a.work[1], (unsigned long long)max(0, n_valid_pages(ctx, kPageTokens)));
-    }
-  }
+  write_outputs(a, (int64_t)bh * G + g, d, O, M, L);
+  if (i == 0 && a.work != nullptr) add_work(a, n, ctx);
 }
 
 __global__ void fill_zero_kernel(uint32_t *p, size_t n_words) {
@@ -366,14 +410,18 @@ struct DecodePlan {
   int pps_sel, pps_all, n_splits;
 };
 
+static int env_int(const char *name, int dflt) {
+  const char *e = getenv(name);
+  const int x = e ? atoi(e) : 0;
+  return x > 0 ? x : dflt;
+}
+
+// Workgroups per launch (tuning knob CVSA_DECODE_TARGET_WGS, read once).
 static int target_workgroups() {
-  static const int v = [] {
-    const char *e = getenv("CVSA_DECODE_TARGET_WGS");  // tuning knob
-    const int x = e ? atoi(e) : 0;
-    return x > 0 ? x : 512;
-  }();
+  static const int v = env_int("CVSA_DECODE_TARGET_WGS", 256);
   return v;
 }
+constexpr int kWavesPerWg = 4;
 
 // Pages per split: spread the heads over ~target_workgroups() workgroups,
 // at least two pages per wave and at most kMaxSplits splits per head.
@@ -386,8 +434,8 @@ static DecodePlan plan_decode(int B, int H_kv, int max_sel, int W, bool listed,
   auto pps_for = [&](int pages) {
     int pps = (pages + wg_per_head - 1) / wg_per_head;
     if (pps < kMinPagesPerSplit) pps = kMinPagesPerSplit;
-    pps = (pps + kDecWaves - 1) / kDecWaves * kDecWaves;
-    while ((pages + pps - 1) / pps > kMaxSplits) pps += kDecWaves;
+    pps = (pps + kWavesPerWg - 1) / kWavesPerWg * kWavesPerWg;
+    while ((pages + pps - 1) / pps > kMaxSplits) pps += kWavesPerWg;
     return pps;
   };
   DecodePlan p;
@@ -400,14 +448,14 @@ static DecodePlan plan_decode(int B, int H_kv, int max_sel, int W, bool listed,
   return p;
 }
 
-static size_t counters_bytes(int heads) { return ((size_t)heads * 4 + 255) / 256 * 256; }
-
+// Split partials [B*H_kv][n_splits][G][D + 2] fp32; none with a single split.
 static size_t workspace_bytes_for(int B, int H_q, int H_kv, int max_sel, int W, bool listed,
                                   bool all_pages) {
   const int heads = B * H_kv;
   const int G = H_q / H_kv;
   const DecodePlan p = plan_decode(B, H_kv, max_sel, W, listed, all_pages);
-  return counters_bytes(heads) + (size_t)heads * p.n_splits * G * kPartStride * sizeof(float);
+  if (p.n_splits == 1) return 0;
+  return (size_t)heads * p.n_splits * G * kPartStride * sizeof(float);
 }
 
 // Lanes per token row, chosen so that the o accumulators stay at <= 64
@@ -460,27 +508,36 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
   const DecodePlan p = plan_decode(B, H_kv, listed ? a.max_sel : 0, W, listed, all_pages);
   const size_t need = workspace_bytes_for(B, H_q, H_kv, listed ? a.max_sel : 0, W, listed,
                                           all_pages);
-  CVSA_REQUIRE(workspace != nullptr && workspace_bytes >= need &&
-                   ((uintptr_t)workspace & 255) == 0,
+  CVSA_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need &&
+                                ((uintptr_t)workspace & 255) == 0),
                CVSA_ERR_WORKSPACE,
                "%s: workspace of %zu bytes (256-byte aligned) required, got %zu", name,
                need, workspace_bytes);
   a.pps_sel = p.pps_sel;
   a.pps_all = p.pps_all;
   a.n_splits = p.n_splits;
+
   a.W = W;
   a.H_kv = H_kv;
   a.scale = (float)pow((double)D, -0.5);
-  a.counters = reinterpret_cast<uint32_t *>(workspace);
-  a.part = reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) +
-                                     counters_bytes(B * H_kv));
+  a.part = reinterpret_cast<float *>(workspace);
   const dim3 grid(p.n_splits, B * H_kv);
-  switch (G) {
-#define CVSA_DEC_CASE(GG)                                                                 \
-  case GG:                                                                                \
-    hipLaunchKernelGGL((paged_decode_kernel<GG, LanesPerRow<GG>::value>), grid,          \
-                       dim3(kDecThreads), 0, st, a);                                      \
+  const dim3 mgrid((G * kHeadDim + 255) / 256, B * H_kv);
+  const int mode = !listed ? kModeAll : (all_pages ? kModeVerified : kModeListed);
+#define CVSA_DEC_LAUNCH(GG, MM)                                                              \
+  do {                                                                                       \
+    hipLaunchKernelGGL((paged_decode_kernel<GG, LanesPerRow<GG>::value, 4, 2, MM>), grid,    \
+                       dim3(4 * kWave), 0, st, a);                                           \
+    if (p.n_splits > 1)                                                                      \
+      hipLaunchKernelGGL((paged_decode_merge_kernel<GG, MM>), mgrid, dim3(256), 0, st, a);   \
+  } while (0)
+#define CVSA_DEC_CASE(GG)                                                                    \
+  case GG:                                                                                   \
+    if (mode == kModeAll) CVSA_DEC_LAUNCH(GG, kModeAll);                                     \
+    else if (mode == kModeListed) CVSA_DEC_LAUNCH(GG, kModeListed);                          \
+    else CVSA_DEC_LAUNCH(GG, kModeVerified);                                                 \
     break;
+  switch (G) {
     CVSA_DEC_CASE(1)
     CVSA_DEC_CASE(2)
     CVSA_DEC_CASE(3)
@@ -489,10 +546,11 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
     CVSA_DEC_CASE(6)
     CVSA_DEC_CASE(7)
     CVSA_DEC_CASE(8)
-#undef CVSA_DEC_CASE
     default:
       break;
   }
+#undef CVSA_DEC_CASE
+#undef CVSA_DEC_LAUNCH
   return cvsa_host::check_launch(name);
 }
 

@@ -6,9 +6,8 @@ return tuple, allocates its outputs with the torch caching allocator and
 launches the gfx950 kernels of ``libcvsa_hip.so`` on the current stream.
 All tensors must live on one ROCm GPU; there is no CPU path.
 
-Workspaces of the paged decode kernels are cached per (device, stream) and
-their completion counters are zeroed once when allocated; the kernels leave
-them zeroed.
+Workspaces of the paged decode kernels (split-K partial states) are cached
+per (device, stream) and grown on demand; they need no initialisation.
 """
 from __future__ import annotations
 
@@ -112,17 +111,16 @@ def _block_tables(bt: torch.Tensor) -> torch.Tensor:
 _WORKSPACES: dict = {}
 
 
-def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-(device, stream) decode workspace with zeroed completion counters."""
+def _workspace(dev: torch.device, nbytes: int) -> Optional[torch.Tensor]:
+    """Per-(device, stream) decode workspace of at least nbytes (None for 0)."""
+    if nbytes == 0:
+        return None
     stream = torch.cuda.current_stream(dev)
     key = (dev.index, stream.cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        size = max(nbytes, 1 << 20)
-        size = (size + (1 << 20) - 1) // (1 << 20) * (1 << 20)
+        size = (nbytes + (1 << 20) - 1) // (1 << 20) * (1 << 20)
         ws = torch.empty(size, dtype=torch.uint8, device=dev)
-        check(_lib.load().cvsa_workspace_init(ws.data_ptr(), size, stream.cuda_stream),
-              "workspace_init")
         _WORKSPACES[key] = ws
     return ws
 
@@ -241,8 +239,6 @@ def _decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, num_kv_h
     all_pages = kind in ("dense_decode", "verified_decode")
     need = L.cvsa_decode_workspace_bytes(B, H_q, num_kv_heads, D, max_sel if listed else 0,
                                          W, 1 if all_pages else 0)
-    if need == 0:
-        raise ValueError(f"{kind}: invalid geometry")
     ws = _workspace(dev, need)
     o = m = l = out = None
     if want_state:
@@ -258,8 +254,8 @@ def _decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, num_kv_h
         code = _DTYPE_CODE[od]
     common_q = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
                 k_cache.shape[0], bt.data_ptr(), bt.stride(0), ctx.data_ptr())
-    tail = (_ptr(o), _ptr(m), _ptr(l), _ptr(out), code, _ptr(work), ws.data_ptr(), ws.numel(),
-            _stream(dev))
+    tail = (_ptr(o), _ptr(m), _ptr(l), _ptr(out), code, _ptr(work), _ptr(ws),
+            0 if ws is None else ws.numel(), _stream(dev))
     if kind == "sparse_decode":
         rc = L.cvsa_sparse_decode(*common_q, pi_flat.data_ptr(), pi_flat.stride(0),
                                   nph_flat.data_ptr(), max_sel, B, H_q, num_kv_heads, D,

@@ -96,15 +96,15 @@ int cvsa_check_coverage(const float *page_scores, int32_t B, int32_t H_kv,
 /*
  * Workspace of the paged decode entry points, in bytes, for a call whose
  * heads visit at most `max_sel_pages` listed pages and, when `all_pages` is
- * non-zero, up to W pages (dense heads).  The first 4*B*H_kv bytes are
- * completion counters: they must be zero before the first call (see
- * cvsa_workspace_init) and every call leaves them zero.
+ * non-zero, up to W pages (dense heads).  It holds the split-K partial
+ * softmax states between the split and merge launches; it needs no
+ * initialisation and may be 0 bytes (then NULL is accepted).
  */
 size_t cvsa_decode_workspace_bytes(int32_t B, int32_t H_q, int32_t H_kv,
                                    int32_t D, int32_t max_sel_pages,
                                    int32_t W, int32_t all_pages);
 
-/* Zero a workspace on `stream` with a fill kernel. */
+/* Zero a workspace on `stream` with a fill kernel (optional). */
 int cvsa_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 
 /*

@@ -266,3 +266,23 @@ def test_ops_reject_bad_input(gpu):
         ops.score_pages(q[:, :, :64].contiguous(), K[..., :64].contiguous(), bt, cl, 8, 4, 16)
     with pytest.raises(ValueError):
         ops.select_topk(torch.zeros(1, 8, 16, device=gpu), 17, cl, 16)
+
+
+@pytest.mark.parametrize("extra", [2, 16])
+def test_verified_decode_block_table_wider_than_context(gpu, extra):
+    """Rejected heads walk n_valid pages with their own split size even when
+    the block table is wider than the context (regression: a miscompiled
+    branch once gave rejected heads the listed heads' split size)."""
+    inp = _inputs(410, 1, 32, 8, 8192, W=512 + extra)
+    q, K, V, bt, cl = _dev(inp, gpu)
+    ps = ref.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens, 8, 4, 16)
+    idx, nph = ref.select_topk(ps, 64, inp.context_lens, 16)
+    accept = torch.tensor([[False, False, True, False, True, False, True, False]])
+    out = ops.verified_decode(q, K, V, bt, cl, idx.to(gpu), nph.to(gpu), accept.to(gpu), 8, 4,
+                              16).cpu()
+    want = ref.verified_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
+                               inp.context_lens, idx, nph, accept, 8, 4, 16)
+    assert (out.float() - want.float()).abs().max().item() < OUT_ATOL
+    dense = ops.dense_decode(q, K, V, bt, cl, 8, 4, 16).cpu()
+    rej = ~accept.repeat_interleave(4, dim=1)[0]
+    assert torch.equal(out[0][rej], dense[0][rej])
