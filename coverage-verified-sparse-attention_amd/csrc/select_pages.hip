@@ -90,11 +90,14 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     const float *__restrict__ scores, int W, int H_kv,
     const int32_t *__restrict__ context_lens, int block_size, int budget,
     int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
-    uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out) {
+    uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
+    const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
+    long long *__restrict__ stats) {
   __shared__ uint32_t hist[256];
   __shared__ uint32_t wsum[kSelWaves];
   __shared__ float red[kSelWaves];
   __shared__ uint32_t s_digit, s_krem;
+  __shared__ int s_nok;
 
   const int bh = blockIdx.x;
   const int b = bh / H_kv;
@@ -103,6 +106,38 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   const float *row = scores + (int64_t)bh * W;
   const int i0 = t * R;
 
+  // Lazy coverage check decided on the device (CVSABackend._lazy_step,
+  // cvsa/backend.py:420-465): when every head of the layer kept its
+  // coverage on the cached selection, that selection stays and all heads
+  // are accepted; otherwise a fresh selection replaces it in place.
+  // Counters: stats[0] accept-all checks, [1] rejections, [2] scoring
+  // steps, [3] heads that passed the check.
+  if (check_accept != nullptr) {
+    if (t == 0) s_nok = 0;
+    __syncthreads();
+    int ok = 1, cnt = 0;
+    for (int i = t; i < n_heads; i += kSelThreads) {
+      const int v = check_accept[i] != 0;
+      ok &= v;
+      cnt += v;
+    }
+    if (cnt) atomicAdd(&s_nok, cnt);
+    const int all_ok = __syncthreads_and(ok);
+    if (stats != nullptr && bh == 0 && t == 0) {
+      stats[0] += all_ok ? 1 : 0;
+      stats[1] += all_ok ? 0 : 1;
+      stats[2] += all_ok ? 0 : 1;
+      stats[3] += s_nok;
+    }
+    if (all_ok) {
+      if (t == 0) accept_out[bh] = 1;
+      return;
+    }
+  } else if (stats != nullptr && bh == 0 && t == 0) {
+    stats[1] += 1;  // a scoring step without a cached selection
+    stats[2] += 1;
+  }
+
   float val[R];
   uint32_t key[R];
 #pragma unroll
@@ -110,6 +145,11 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     const int i = i0 + r;
     val[r] = i < W ? row[i] : -INFINITY;
     key[r] = order_key(val[r]);
+  }
+  if (scores_cache != nullptr) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (i0 + r < W) scores_cache[(int64_t)bh * W + i0 + r] = val[r];
   }
 
   // ---- radix select of the budget-th largest key
@@ -286,36 +326,35 @@ static int keys_per_thread(int n) {
   return r;
 }
 
-}  // namespace cvsa
 
-using namespace cvsa;
-
-extern "C" int cvsa_select_topk(const float *page_scores, int32_t B,
-                                int32_t H_kv, int32_t W,
-                                const int32_t *context_lens, int32_t block_size,
-                                int32_t budget, int32_t *page_indices,
-                                int32_t *n_per_head, float tau,
-                                uint8_t *accept_out, float *coverage_out,
-                                void *stream) {
-  CVSA_REQUIRE(page_scores && context_lens && page_indices && n_per_head,
-               CVSA_ERR_INVALID, "select_topk: null pointer argument");
+static int launch_select(const char *name, const float *page_scores, int32_t B, int32_t H_kv,
+                         int32_t W, const int32_t *context_lens, int32_t block_size,
+                         int32_t budget, int32_t *page_indices, int32_t *n_per_head, float tau,
+                         uint8_t *accept_out, float *coverage_out, const uint8_t *check_accept,
+                         float *scores_cache, int64_t *stats, void *stream) {
+  CVSA_REQUIRE(page_scores && context_lens && page_indices && n_per_head, CVSA_ERR_INVALID,
+               "%s: null pointer argument", name);
   CVSA_REQUIRE((accept_out == nullptr) == (coverage_out == nullptr), CVSA_ERR_INVALID,
-               "select_topk: accept_out and coverage_out must both be set or both NULL");
+               "%s: accept_out and coverage_out must both be set or both NULL", name);
+  CVSA_REQUIRE(check_accept == nullptr || accept_out != nullptr, CVSA_ERR_INVALID,
+               "%s: a device-side check needs accept_out", name);
   CVSA_REQUIRE(B > 0 && H_kv > 0 && W > 0 && block_size > 0, CVSA_ERR_INVALID,
-               "select_topk: bad sizes B=%d H_kv=%d W=%d bs=%d", B, H_kv, W, block_size);
+               "%s: bad sizes B=%d H_kv=%d W=%d bs=%d", name, B, H_kv, W, block_size);
   CVSA_REQUIRE(budget >= 1 && budget <= W, CVSA_ERR_INVALID,
-               "select_topk: budget=%d must be in [1, W=%d]", budget, W);
-  CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
-               "select_topk: W=%d exceeds %d pages", W, kMaxPages);
+               "%s: budget=%d must be in [1, W=%d]", name, budget, W);
+  CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
+               kMaxPages);
   const int R = keys_per_thread(W);
   const dim3 grid(B * H_kv);
   hipStream_t st = (hipStream_t)stream;
+  long long *st64 = reinterpret_cast<long long *>(stats);
   switch (R) {
-#define CVSA_SEL_CASE(RR)                                                        \
-  case RR:                                                                       \
-    hipLaunchKernelGGL(select_topk_kernel<RR>, grid, dim3(kSelThreads), 0, st,    \
-                       page_scores, W, H_kv, context_lens, block_size, budget,    \
-                       page_indices, n_per_head, tau, accept_out, coverage_out);  \
+#define CVSA_SEL_CASE(RR)                                                                \
+  case RR:                                                                               \
+    hipLaunchKernelGGL(select_topk_kernel<RR>, grid, dim3(kSelThreads), 0, st, page_scores, \
+                       W, H_kv, context_lens, block_size, budget, page_indices, n_per_head, \
+                       tau, accept_out, coverage_out, check_accept, B * H_kv, scores_cache,  \
+                       st64);                                                            \
     break;
     CVSA_SEL_CASE(1)
     CVSA_SEL_CASE(2)
@@ -325,9 +364,36 @@ extern "C" int cvsa_select_topk(const float *page_scores, int32_t B,
     CVSA_SEL_CASE(32)
 #undef CVSA_SEL_CASE
     default:
-      return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "select_topk: W=%d too large", W);
+      return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "%s: W=%d too large", name, W);
   }
-  return cvsa_host::check_launch("select_topk");
+  return cvsa_host::check_launch(name);
+}
+
+}  // namespace cvsa
+
+using namespace cvsa;
+
+extern "C" int cvsa_select_topk(const float *page_scores, int32_t B, int32_t H_kv, int32_t W,
+                                const int32_t *context_lens, int32_t block_size,
+                                int32_t budget, int32_t *page_indices, int32_t *n_per_head,
+                                float tau, uint8_t *accept_out, float *coverage_out,
+                                void *stream) {
+  return launch_select("select_topk", page_scores, B, H_kv, W, context_lens, block_size,
+                       budget, page_indices, n_per_head, tau, accept_out, coverage_out,
+                       nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int cvsa_select_or_keep(const float *page_scores, const uint8_t *check_accept,
+                                   int32_t B, int32_t H_kv, int32_t W,
+                                   const int32_t *context_lens, int32_t block_size,
+                                   int32_t budget, int32_t *page_indices, int32_t *n_per_head,
+                                   float tau, uint8_t *accept_out, float *coverage_out,
+                                   float *scores_cache, int64_t *stats, void *stream) {
+  CVSA_REQUIRE(accept_out && coverage_out, CVSA_ERR_INVALID,
+               "select_or_keep: accept_out and coverage_out are required");
+  return launch_select("select_or_keep", page_scores, B, H_kv, W, context_lens, block_size,
+                       budget, page_indices, n_per_head, tau, accept_out, coverage_out,
+                       check_accept, scores_cache, stats, stream);
 }
 
 extern "C" int cvsa_check_coverage(const float *page_scores, int32_t B,

@@ -11,17 +11,18 @@ tracing attributes ``_cached_selection``, ``_last_accept_mask``,
 
 What runs per layer call (HIP kernels from cvsa.ops):
   scoring step  score_pages -> select_topk (+ coverage gate) -> verified_decode
-  lazy check    score_pages -> check_coverage -> (sparse decode | scoring step)
+  lazy check    score_pages -> check_coverage -> select_or_keep -> verified_decode
   reuse step    sparse decode over the cached selection
 The reference's draft decode, complement, complement decode and LSE merge
 collapse into verified_decode: accepted heads attend their selected pages,
 rejected heads attend every valid page in one pass, which equals the LSE
-merge of draft and complement.  The effective-budget counters are
-accumulated by the decode kernels on the device, and in lazy mode the
-scoring step needs no host synchronisation; the only host reads left are
-the ones whose result decides which kernels run next (the lazy accept-all
-check, approximate recovery) or that feed host-side counters in the fixed
-interval schedule, as in the reference.
+merge of draft and complement.  The lazy accept-all decision is taken on
+the device (select_or_keep keeps the cached selection or refreshes it in
+place), and the statistics counters and effective-budget counters are
+accumulated there too, so a lazy decode step never waits for the host.
+Host reads remain where the reference's result needs one: approximate
+recovery, the random-rejection counterfactual, coverage-only steps and the
+counters of the fixed-interval schedule.
 
 Not implemented here (the constructor raises NotImplementedError): the
 alternative selectors of the reference (adaptive_selection,
@@ -57,8 +58,33 @@ class _PendingComplement:
                                       self.block_size, self.accept)
 
 
+def _device_counter(slot: int, host_name: str):
+    """A statistics counter kept partly on the host and partly in slot `slot`
+    of the device counter block (accumulated by the lazy decision kernel).
+    Reading it synchronises; assigning it (as evaluation harnesses do to
+    reset the counters) sets the host part and clears the device part."""
+
+    def fget(self):
+        value = getattr(self, host_name)
+        if self._dev_stats is not None:
+            value += int(self._dev_stats[slot].item())
+        return value
+
+    def fset(self, value):
+        setattr(self, host_name, value)
+        if self._dev_stats is not None:
+            self._dev_stats[slot].zero_()
+
+    return property(fget, fset)
+
+
 class CVSABackend:
     """Draft with sparse attention, verify with coverage, recover rejected heads."""
+
+    _accept_counts = _device_counter(0, "_h_accept_counts")
+    _reject_counts = _device_counter(1, "_h_reject_counts")
+    _total_scoring_steps = _device_counter(2, "_h_total_scoring_steps")
+    _per_head_accept_sum = _device_counter(3, "_h_per_head_accept_sum")
 
     def __init__(
         self,
@@ -137,6 +163,7 @@ class CVSABackend:
         self._attn_work: Optional[torch.Tensor] = None
         self._attn_work_max: Optional[torch.Tensor] = None
         self._work_buf: Optional[torch.Tensor] = None
+        self._dev_stats: Optional[torch.Tensor] = None
 
         self._step = 0
         self._reuse_state: Dict[int, Tuple[torch.Tensor, torch.Tensor, int]] = {}
@@ -234,17 +261,18 @@ class CVSABackend:
 
     def get_stats(self) -> dict:
         """Same keys and formulas as backend.py:282-311."""
-        total_checks = max(self._total_coverage_checks, self._total_scoring_steps, 1)
+        accepts, rejects, scoring, head_accepts = self._counters()
+        total_checks = max(self._total_coverage_checks, scoring, 1)
         stats = {
-            "total_scoring_steps": self._total_scoring_steps,
+            "total_scoring_steps": scoring,
             "total_coverage_checks": self._total_coverage_checks,
-            "all_accepted_pct": self._accept_counts / max(total_checks, 1) * 100,
-            "some_rejected_pct": self._reject_counts / max(total_checks, 1) * 100,
-            "per_head_accept_rate": self._per_head_accept_sum / max(self._per_head_total, 1) * 100,
+            "all_accepted_pct": accepts / max(total_checks, 1) * 100,
+            "some_rejected_pct": rejects / max(total_checks, 1) * 100,
+            "per_head_accept_rate": head_accepts / max(self._per_head_total, 1) * 100,
             "total_decode_steps": self._step,
             "lazy": self.lazy,
             "check_interval": self.check_interval if self.lazy else None,
-            "rescore_rate": (self._total_scoring_steps / max(self._total_coverage_checks, 1) * 100
+            "rescore_rate": (scoring / max(self._total_coverage_checks, 1) * 100
                              if self.lazy else 100.0),
         }
         if self._attn_work is not None:
@@ -325,6 +353,19 @@ class CVSABackend:
         self._attn_work += pages_attended.to(torch.long).to(self._attn_work.device)
         self._attn_work_max += dense_max.to(torch.long).to(self._attn_work_max.device)
 
+    def _counters(self) -> Tuple[int, int, int, int]:
+        """(accept-all checks, rejections, scoring steps, heads accepted)."""
+        host = [self._h_accept_counts, self._h_reject_counts, self._h_total_scoring_steps,
+                self._h_per_head_accept_sum]
+        if self._dev_stats is not None:
+            host = [h + d for h, d in zip(host, self._dev_stats.tolist())]
+        return tuple(host)
+
+    def _ensure_dev_stats(self, device) -> Optional[torch.Tensor]:
+        if self._dev_stats is None:
+            self._dev_stats = torch.zeros(4, dtype=torch.long, device=device)
+        return self._dev_stats if self._dev_stats.device == torch.device(device) else None
+
     def _decode_work(self, context_lens):
         """Counter pair for a kernel launch, or None after recording on the host."""
         return self._work(context_lens.device)
@@ -356,21 +397,70 @@ class CVSABackend:
         self._total_coverage_checks += 1
         if layer_idx in self._cached_selection:
             page_indices, n_per_head = self._cached_selection[layer_idx]
-            accept_mask, _coverage = self._time_kernel(
+            accept_mask, coverage = self._time_kernel(
                 "coverage", ops.check_coverage, page_scores, page_indices, n_per_head,
                 self.tau)
+            if self._device_decision_ok(layer_idx, page_scores, context_lens):
+                return self._lazy_device_step(q, k_cache, v_cache, block_tables,
+                                              context_lens, layer_idx, page_scores,
+                                              accept_mask, coverage)
             accept_mask = self._apply_random_reject(accept_mask)
             n_acc = int(accept_mask.sum().item())  # one host read decides the branch
-            self._per_head_accept_sum += n_acc
+            self._h_per_head_accept_sum += n_acc
             self._per_head_total += accept_mask.numel()
             if n_acc == accept_mask.numel():
-                self._accept_counts += 1
+                self._h_accept_counts += 1
                 self._last_accept_mask[layer_idx] = accept_mask
                 return self._reuse_decode(q, k_cache, v_cache, block_tables, context_lens,
                                           layer_idx)
-        self._reject_counts += 1
+        self._h_reject_counts += 1
         return self._scoring_step(q, k_cache, v_cache, block_tables, context_lens, layer_idx,
                                   page_scores=page_scores)
+
+    def _device_decision_ok(self, layer_idx, page_scores, context_lens) -> bool:
+        """Whether the lazy accept-all decision can stay on the device: exact
+        recovery, no counterfactual rejections, the cached selection and
+        scores match this call's shape, counters live on this device."""
+        if self.random_reject_prob is not None or self.approx_recovery_pct is not None:
+            return False
+        page_indices, n_per_head = self._cached_selection[layer_idx]
+        B, H_kv, W = page_scores.shape
+        budget = max(3, int(W * self.budget_pct))
+        if (tuple(page_indices.shape) != (B, H_kv, budget) or not page_indices.is_contiguous()
+                or tuple(n_per_head.shape) != (B, H_kv) or not n_per_head.is_contiguous()):
+            return False
+        cached = self._cached_page_scores.get(layer_idx)
+        if cached is not None and (cached.shape != page_scores.shape
+                                   or not cached.is_contiguous()):
+            return False
+        dev = page_scores.device
+        return self._work(dev) is not None and self._ensure_dev_stats(dev) is not None
+
+    def _lazy_device_step(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx,
+                          page_scores, check_accept, coverage):
+        """_lazy_step with the accept-all branch (backend.py:440-465) taken on
+        the device: select_or_keep keeps the cached selection when every head
+        passed, or refreshes it in place (the scoring step's top-k and
+        coverage gate, :737-771); verified_decode then attends the selection
+        on accepted heads and every valid page on rejected heads.  The
+        counters of both branches accumulate on the device."""
+        page_indices, n_per_head = self._cached_selection[layer_idx]
+        budget = page_indices.shape[2]
+        self._per_head_total += check_accept.numel()
+        accept_mask = self._time_kernel(
+            "coverage", ops.select_or_keep, page_scores, check_accept, budget, context_lens,
+            self.block_size, self.tau, page_indices, n_per_head, coverage,
+            self._cached_page_scores.get(layer_idx), self._dev_stats)
+        self._last_accept_mask[layer_idx] = accept_mask
+        output = self._time_kernel(
+            "sparse_draft", ops.verified_decode, q, k_cache, v_cache, block_tables,
+            context_lens, page_indices, n_per_head, accept_mask, self.num_kv_heads,
+            self.num_q_per_kv, self.block_size, output_dtype=q.dtype,
+            work=self._work(context_lens.device))
+        # Present only when a head was rejected, as after a scoring step.
+        self._expanded_store[layer_idx] = _PendingComplement(
+            accept_mask, page_indices, n_per_head, context_lens, self.block_size)
+        return output
 
     def _coverage_only_step(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
         """backend.py:467-520"""
@@ -380,15 +470,15 @@ class CVSABackend:
             "coverage", ops.check_coverage, page_scores, page_indices, n_per_head, self.tau)
         accept_mask = self._apply_random_reject(accept_mask)
         n_acc = int(accept_mask.sum().item())
-        self._per_head_accept_sum += n_acc
+        self._h_per_head_accept_sum += n_acc
         self._per_head_total += accept_mask.numel()
         self._total_coverage_checks += 1
         if n_acc == accept_mask.numel():
-            self._accept_counts += 1
+            self._h_accept_counts += 1
             self._last_accept_mask[layer_idx] = accept_mask
             return self._reuse_decode(q, k_cache, v_cache, block_tables, context_lens,
                                       layer_idx)
-        self._reject_counts += 1
+        self._h_reject_counts += 1
         return self._scoring_step(q, k_cache, v_cache, block_tables, context_lens, layer_idx,
                                   page_scores=None)
 
@@ -430,10 +520,10 @@ class CVSABackend:
             if not self.lazy:
                 n_acc = int(accept_mask.sum().item())
                 if n_acc == accept_mask.numel():
-                    self._accept_counts += 1
+                    self._h_accept_counts += 1
                 else:
-                    self._reject_counts += 1
-                self._per_head_accept_sum += n_acc
+                    self._h_reject_counts += 1
+                self._h_per_head_accept_sum += n_acc
                 self._per_head_total += accept_mask.numel()
         else:
             output = self._approx_recovery(q, k_cache, v_cache, block_tables, context_lens,
@@ -446,7 +536,7 @@ class CVSABackend:
                                         n_per_head.view(B * self.num_kv_heads),
                                         ops.next_power_of_2(page_indices.shape[2]))
         self._cached_selection[layer_idx] = (page_indices, n_per_head)
-        self._total_scoring_steps += 1                                            # :859
+        self._h_total_scoring_steps += 1                                          # :859
         return output
 
     def _approx_recovery(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx,
@@ -463,7 +553,7 @@ class CVSABackend:
         if all_acc:
             output = draft
             if not self.lazy:
-                self._accept_counts += 1
+                self._h_accept_counts += 1
         else:
             exp_budget = min(max(budget + 1, int(n_pages * self.approx_recovery_pct)), n_pages)
             exp_indices, exp_nph = ops.select_topk(page_scores, exp_budget, context_lens,
@@ -477,10 +567,10 @@ class CVSABackend:
             output = torch.where(accept_q.unsqueeze(-1), draft, expanded)
             self._expanded_store[layer_idx] = (exp_indices, exp_nph)
             if not self.lazy:
-                self._reject_counts += 1
+                self._h_reject_counts += 1
         self._record_work(context_lens, pages)
         if not self.lazy:
-            self._per_head_accept_sum += n_acc
+            self._h_per_head_accept_sum += n_acc
             self._per_head_total += accept_mask.numel()
         return output
 

@@ -81,6 +81,30 @@ int cvsa_select_topk(const float *page_scores, int32_t B, int32_t H_kv,
                      float *coverage_out, void *stream);
 
 /*
+ * The lazy coverage decision taken on the device.  Replaces the branch of
+ * CVSABackend._lazy_step (cvsa/backend.py:420-465) that reads the accept
+ * mask of the cached selection on the host and then either reuses that
+ * selection or runs a scoring step (backend.py:737-771).
+ *   check_accept[B*H_kv]: coverage gate of the cached selection (the
+ *     accept_out of cvsa_check_coverage); must not alias accept_out.
+ *   all heads passed -> page_indices / n_per_head / coverage_out untouched,
+ *     accept_out[:] = 1.
+ *   otherwise        -> as cvsa_select_topk with the fused gate, writing
+ *     the new selection over page_indices / n_per_head in place, and
+ *     scores_cache (optional, [B,H_kv,W]) receives a copy of page_scores.
+ *   stats (optional, int64[4], accumulated): [0] += all passed,
+ *     [1] += some head failed, [2] += scoring steps run (same as [1]),
+ *     [3] += number of heads that passed.
+ */
+int cvsa_select_or_keep(const float *page_scores, const uint8_t *check_accept,
+                        int32_t B, int32_t H_kv, int32_t W,
+                        const int32_t *context_lens, int32_t block_size,
+                        int32_t budget, int32_t *page_indices,
+                        int32_t *n_per_head, float tau, uint8_t *accept_out,
+                        float *coverage_out, float *scores_cache,
+                        int64_t *stats, void *stream);
+
+/*
  * Coverage gate.  Replaces triton_check_coverage
  * (cvsa/kernels/coverage.py:218-265, kernel :159-215).
  *   lse_all = M + log(sum exp(s - M) + 1e-30), M = max(max_p s, -1e20)

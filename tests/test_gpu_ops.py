@@ -89,6 +89,44 @@ def test_select_topk_bit_exact(gpu, W, budget):
     assert torch.equal(acc.cpu()[margin], wacc[margin])
 
 
+@pytest.mark.parametrize("W,budget", [(2048, 512), (8192, 1024), (100, 3)])
+def test_select_or_keep(gpu, W, budget):
+    """Keep the cached selection when every head passed, else refresh it in
+    place exactly as select_topk; counters as the lazy schedule counts them."""
+    g = torch.Generator().manual_seed(W * 3 + budget)
+    B, H = 2, 8
+    ctx = torch.tensor([W * 16 - 3, max(1, (W // 2) * 16)], dtype=torch.int32)
+    old_ps = torch.randn(B, H, W, generator=g)
+    new_ps = torch.randn(B, H, W, generator=g)
+    nv = ref.n_valid_pages(ctx, 16)
+    new_ps[1, :, int(nv[1]):] = float("-inf")
+    sel0, nph0 = ref.select_topk(old_ps, budget, ctx, 16)
+    stats = torch.zeros(4, dtype=torch.int64, device=gpu)
+    d_sel, d_nph = sel0.to(gpu), nph0.to(gpu)
+    d_cache = old_ps.to(gpu)
+    cov = torch.full((B, H), -7.0, device=gpu)
+    # 1) every head passed: nothing changes, all heads accepted
+    check = torch.ones(B, H, dtype=torch.bool, device=gpu)
+    acc = ops.select_or_keep(new_ps.to(gpu), check, budget, ctx.to(gpu), 16, 0.9, d_sel, d_nph,
+                             cov, d_cache, stats)
+    assert bool(acc.all())
+    assert torch.equal(d_sel.cpu(), sel0) and torch.equal(d_nph.cpu(), nph0)
+    assert torch.equal(d_cache.cpu(), old_ps) and bool((cov == -7.0).all())
+    assert stats.tolist() == [1, 0, 0, B * H]
+    # 2) one head failed: fresh top-k + gate for every head, scores cached
+    check[1, 3] = False
+    acc = ops.select_or_keep(new_ps.to(gpu), check, budget, ctx.to(gpu), 16, 0.9, d_sel, d_nph,
+                             cov, d_cache, stats)
+    widx, wnph = ref.select_topk(new_ps, budget, ctx, 16)
+    assert torch.equal(d_sel.cpu(), widx) and torch.equal(d_nph.cpu(), wnph)
+    assert torch.equal(d_cache.cpu(), new_ps)
+    wacc, wcov = ref.check_coverage(new_ps, widx, wnph, 0.9)
+    assert (cov.cpu() - wcov).abs().max().item() < COV_ATOL
+    margin = (wcov - 0.9).abs() > 1e-5
+    assert torch.equal(acc.cpu()[margin], wacc[margin])
+    assert stats.tolist() == [1, 1, 1, 2 * B * H - 1]
+
+
 @pytest.mark.parametrize("k,W", [(128, 512), (1000, 2048), (5, 9)])
 def test_check_coverage(gpu, k, W):
     g = torch.Generator().manual_seed(k * 7 + W)
