@@ -18,9 +18,14 @@
 // Lane l holds d-segment (l % LPT) of token slot (l / LPT); the q.K dot is
 // finished with an LPT-lane DPP reduction, the page max with DPP and
 // permlane swaps, and P.V accumulates in registers.  The four waves merge in
-// LDS, every workgroup stores its partial (o, m, l), and the last workgroup
-// of a head (completion counter) merges all partials and writes the
-// outputs, so one launch does the whole decode.
+// LDS.  When a head's pages span several workgroups (splits), each stores its
+// partial (o, m, l) and bumps the head's completion counter; the last one to
+// arrive merges the partials and writes the outputs, so one launch does the
+// whole decode.  Partials move through agent-coherent accesses (relaxed
+// agent-scope atomic stores and loads, which bypass the per-XCD L2s) and the
+// counter increment is issued only after the stores have completed, so no
+// L2 writeback or invalidate is needed inside the kernel.  The last
+// workgroup resets the counter to zero for the next launch.
 //
 // Head modes: a listed head walks page_indices[b,h,:n_per_head]; an
 // all-pages head walks pages 0..n_valid-1 (dense decode).  In verified mode
@@ -58,6 +63,7 @@ struct DecodeArgs {
   void *out;
   int out_dtype;
   float *part;
+  unsigned *counters;        // per head, zero between launches
   unsigned long long *work;  // optional effective-budget counters
 };
 
@@ -122,34 +128,64 @@ struct HeadWalk {
   }
 };
 
-// Merged (o, m, l) of one output element over NS split partials.  All loads
-// are issued together (indices clamped to the last active split; splits at
-// or beyond n_act get weight zero), so the merge costs one memory round trip.
-template <int NS>
-__device__ __forceinline__ void merge_splits(const float *hp, int n_act, int stride, int d,
-                                             float &O, float &M, float &L) {
-  float mv[NS], lv[NS], ov[NS];
+__device__ __forceinline__ float coherent_load(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void coherent_store(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge of a head's n_act split partials by its last workgroup.  Every load
+// is issued up front (o values of this thread's elements into registers,
+// (m, l) pairs into LDS; indices clamped to the last active split), so the
+// merge costs a single memory round trip.  Each wave then works on one
+// q-head g at a time (its 64 elements share g): lane sp holds split sp's
+// weight exp(m_sp - M), the wave reduces M and L with lane moves, and the
+// weighted sum over splits reads the weights back with readlane.
+template <int G, int NT, int NS>
+__device__ __forceinline__ void merge_partials(const DecodeArgs &a, const float *head_part,
+                                               int n_act, int bh, int n, int ctx,
+                                               float (*s_pm)[kMaxSplits],
+                                               float (*s_pl)[kMaxSplits]) {
+  static_assert(NS <= kWave && (NT % kHeadDim) == 0, "merge layout");
+  constexpr int EPT = (G * kHeadDim + NT - 1) / NT;
+  constexpr int stride = G * kPartStride;  // between splits
+  const int lane = threadIdx.x & 63;
+  float ov[EPT][NS];
 #pragma unroll
-  for (int sp = 0; sp < NS; ++sp) {
-    const float *ps = hp + (int64_t)min(sp, n_act - 1) * stride;
-    mv[sp] = ps[kHeadDim];
-    lv[sp] = ps[kHeadDim + 1];
-    ov[sp] = ps[d];
+  for (int k = 0; k < EPT; ++k) {
+    const int i = min((int)threadIdx.x + k * NT, G * kHeadDim - 1);
+    const float *pe = head_part + (i / kHeadDim) * kPartStride + (i % kHeadDim);
+#pragma unroll
+    for (int sp = 0; sp < NS; ++sp) ov[k][sp] = coherent_load(pe + min(sp, n_act - 1) * stride);
   }
-  M = -INFINITY;
-#pragma unroll
-  for (int sp = 0; sp < NS; ++sp)
-    if (sp < n_act) M = fmaxf(M, mv[sp]);
-  O = 0.f;
-  L = 0.f;
-  if (M != -INFINITY) {
-#pragma unroll
-    for (int sp = 0; sp < NS; ++sp) {
-      const float w = (sp < n_act && mv[sp] != -INFINITY) ? fast_exp(mv[sp] - M) : 0.f;
-      O += w * ov[sp];
-      L += w * lv[sp];
-    }
+  for (int t = threadIdx.x; t < G * n_act; t += NT) {
+    const int g = t / n_act, sp = t - g * n_act;
+    const float *pg = head_part + (int64_t)sp * stride + g * kPartStride;
+    s_pm[g][sp] = coherent_load(pg + kHeadDim);
+    s_pl[g][sp] = coherent_load(pg + kHeadDim + 1);
   }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int i0 = (int)(threadIdx.x & ~63) + k * NT;  // first element of this wave
+    if (i0 >= G * kHeadDim) break;                     // wave-uniform
+    const int g = i0 / kHeadDim;
+    const float mv = lane < n_act ? s_pm[g][lane] : -INFINITY;
+    const float lv = lane < n_act ? s_pl[g][lane] : 0.f;
+    const float M = wave_max_from_groups<1>(mv);
+    const float w = (M == -INFINITY || mv == -INFINITY) ? 0.f : fast_exp(mv - M);
+    const float L = wave_sum_from_groups<1>(w * lv);
+    float O = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < NS; ++sp)
+      O += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), sp)) *
+           ov[k][sp];
+    const int i = i0 + lane;
+    write_outputs(a, (int64_t)bh * G + g, i % kHeadDim, O, M, L);
+  }
+  if (threadIdx.x == 0 && a.work != nullptr) add_work(a, n, ctx);
 }
 
 // NW waves per workgroup, PD pages of K/V in flight per wave.
@@ -166,6 +202,8 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeAr
   __shared__ float s_o[NW][G][kHeadDim];
   __shared__ float s_m[NW][G];
   __shared__ float s_l[NW][G];
+  __shared__ int s_last;
+  __shared__ float s_pm[G][kMaxSplits], s_pl[G][kMaxSplits];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -176,6 +214,17 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeAr
   const int b = bh / a.H_kv;
   const int h = bh - b * a.H_kv;
   const int ctx = __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
+  // The first page-list entries of a listed head are requested together with
+  // the head's scalar state (their position only needs the split's start,
+  // split * pps_sel), which takes one memory round trip off the page-table
+  // lookups.  Lanes past the head's pages are never consumed.
+  int spec_lp = 0;
+  if constexpr (MODE != kModeAll) {
+    if (a.max_sel > 0) {
+      const int rs = min(split * a.pps_sel + wave + NW * lane, a.max_sel - 1);
+      spec_lp = a.page_idx[(int64_t)bh * a.idx_stride + rs];
+    }
+  }
 
   const HeadWalk<MODE> hw(a, bh, ctx);
   const bool listed = hw.listed;
@@ -263,7 +312,7 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeAr
       int my_phys = 0, my_ntok = 0;
       if (lane < cn) {
         const int r = r0 + wave + NW * (c0 + lane);
-        const int lp = listed ? idx_row[r] : r;
+        const int lp = listed ? (c0 == 0 ? spec_lp : idx_row[r]) : r;
         if (lp >= 0 && lp < a.W) {
           const int phys = a.block_tables[b * a.bt_sb + lp];
           if (phys >= 0 && phys < a.num_blocks) {
@@ -293,14 +342,15 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeAr
       };
       uint4 kb[PD][NPASS][NV], vb[PD][NPASS][NV];
       int nt[PD];
-#pragma unroll
-      for (int p = 0; p < PD - 1; ++p) nt[p] = fetch(min(p, cn - 1), kb[p], vb[p]);
-      for (int j = 0; j < cn; j += PD) {
+      // No separate prologue: the first trip fetches pages 0..PD-1 and
+      // consumes only page 0, so every fetch of a slot uses the same
+      // registers and the wait counts see PD-1 pages outstanding.
+      for (int j = 1 - PD; j < cn; j += PD) {
 #pragma unroll
         for (int u = 0; u < PD; ++u) {
           const int slot = (u + PD - 1) % PD;  // slot of page j+u+PD-1
           nt[slot] = fetch(min(j + u + PD - 1, cn - 1), kb[slot], vb[slot]);
-          if (j + u < cn) consume(kb[u], vb[u], nt[u]);
+          if (j + u >= 0 && j + u < cn) consume(kb[u], vb[u], nt[u]);
         }
       }
     }
@@ -330,74 +380,78 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeAr
   }
   __syncthreads();
 
-  // Merge the waves.  With one split per launch the workgroup owns the whole
-  // head and writes the outputs; otherwise it stores its partial state for
-  // the merge kernel.
-  if (r0 < r1 || a.n_splits == 1) {
-    float *my_part = a.part + ((int64_t)bh * a.n_splits + split) * G * kPartStride;
-    for (int i = threadIdx.x; i < G * kHeadDim; i += NT) {
-      const int g = i / kHeadDim, d = i - g * kHeadDim;
-      float M = -INFINITY, O = 0.f, L = 0.f;
-      if (r0 < r1) {
-        M = s_m[0][g];
+  // Merge the waves: wave-partial (o, m, l) -> workgroup (O, M, L) for
+  // element i = g * D + d.
+  auto wg_state = [&](int i, float &O, float &M, float &L) {
+    const int g = i / kHeadDim, d = i - g * kHeadDim;
+    M = -INFINITY;
+    O = 0.f;
+    L = 0.f;
+    if (r0 < r1) {
+      M = s_m[0][g];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w][g]);
-        if (M != -INFINITY) {
+      for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w][g]);
+      if (M != -INFINITY) {
 #pragma unroll
-          for (int w = 0; w < NW; ++w) {
-            const float mw = s_m[w][g];
-            if (mw != -INFINITY) {
-              const float f = fast_exp(mw - M);
-              O += s_o[w][g][d] * f;
-              L += s_l[w][g] * f;
-            }
+        for (int w = 0; w < NW; ++w) {
+          const float mw = s_m[w][g];
+          if (mw != -INFINITY) {
+            const float f = fast_exp(mw - M);
+            O += s_o[w][g][d] * f;
+            L += s_l[w][g] * f;
           }
         }
       }
-      if (a.n_splits == 1) {
-        write_outputs(a, (int64_t)bh * G + g, d, O, M, L);
-      } else {
-        my_part[g * kPartStride + d] = O;
-        if (d == 0) {
-          my_part[g * kPartStride + kHeadDim] = M;
-          my_part[g * kPartStride + kHeadDim + 1] = L;
-        }
+    }
+  };
+
+  const int n_act = (n + pps - 1) / pps;  // splits holding pages of this head
+  if (n_act <= 1) {
+    // Split 0 owns the whole head (or the head is empty): write the outputs.
+    if (split == 0) {
+      for (int i = threadIdx.x; i < G * kHeadDim; i += NT) {
+        float O, M, L;
+        wg_state(i, O, M, L);
+        write_outputs(a, (int64_t)bh * G + i / kHeadDim, i % kHeadDim, O, M, L);
       }
+      if (threadIdx.x == 0 && a.work != nullptr) add_work(a, n, ctx);
+    }
+    return;
+  }
+  if (r0 >= r1) return;  // no pages for this split (uniform)
+
+  float *head_part = a.part + (int64_t)bh * a.n_splits * G * kPartStride;
+  float *my_part = head_part + (int64_t)split * G * kPartStride;
+  for (int i = threadIdx.x; i < G * kHeadDim; i += NT) {
+    const int g = i / kHeadDim, d = i - g * kHeadDim;
+    float O, M, L;
+    wg_state(i, O, M, L);
+    coherent_store(my_part + g * kPartStride + d, O);
+    if (d == 0) {
+      coherent_store(my_part + g * kPartStride + kHeadDim, M);
+      coherent_store(my_part + g * kPartStride + kHeadDim + 1, L);
     }
   }
-  if (a.n_splits == 1 && threadIdx.x == 0 && a.work != nullptr) add_work(a, n, ctx);
-}
-
-// Merge of the split partials: one thread per (q-head, d) element.  Runs as a
-// second launch, so the partial stores of the first are visible without any
-// cache maintenance inside either kernel.
-template <int G, int MODE>
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const DecodeArgs a) {
-  const int bh = blockIdx.y;
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= G * kHeadDim) return;
-  const int g = i / kHeadDim, d = i - g * kHeadDim;
-  const int b = bh / a.H_kv;
-  const int ctx = __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
-  const HeadWalk<MODE> hw(a, bh, ctx);
-  const bool listed = hw.listed;
-  const int n = hw.n, pps = hw.pps;
-  const int n_act = (n + pps - 1) / pps;  // splits that stored a partial, <= kMaxSplits
-  float O = 0.f, M = -INFINITY, L = 0.f;
-  if (n_act > 0) {
-    const float *base = a.part + (int64_t)bh * a.n_splits * G * kPartStride + g * kPartStride;
-    const int stride = G * kPartStride;
-    if (n_act <= 4)
-      merge_splits<4>(base, n_act, stride, d, O, M, L);
-    else if (n_act <= 8)
-      merge_splits<8>(base, n_act, stride, d, O, M, L);
-    else if (n_act <= 16)
-      merge_splits<16>(base, n_act, stride, d, O, M, L);
-    else
-      merge_splits<kMaxSplits>(base, n_act, stride, d, O, M, L);
+  // Every wave's partial stores have completed before the counter moves.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(&a.counters[bh], 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (unsigned)(n_act - 1);
   }
-  write_outputs(a, (int64_t)bh * G + g, d, O, M, L);
-  if (i == 0 && a.work != nullptr) add_work(a, n, ctx);
+  __syncthreads();
+  if (!s_last) return;
+
+  // Last split of the head: merge all partials and write the outputs.
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&a.counters[bh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (n_act <= 8)
+    merge_partials<G, NT, 8>(a, head_part, n_act, bh, n, ctx, s_pm, s_pl);
+  else if (n_act <= 16)
+    merge_partials<G, NT, 16>(a, head_part, n_act, bh, n, ctx, s_pm, s_pl);
+  else
+    merge_partials<G, NT, kMaxSplits>(a, head_part, n_act, bh, n, ctx, s_pm, s_pl);
 }
 
 __global__ void fill_zero_kernel(uint32_t *p, size_t n_words) {
@@ -448,14 +502,18 @@ static DecodePlan plan_decode(int B, int H_kv, int max_sel, int W, bool listed,
   return p;
 }
 
-// Split partials [B*H_kv][n_splits][G][D + 2] fp32; none with a single split.
+// Workspace: per-head completion counters (uint32, padded to 256 bytes),
+// then split partials [B*H_kv][n_splits][G][D + 2] fp32; none with a single
+// split.
+static size_t counter_bytes(int heads) { return ((size_t)heads * 4 + 255) / 256 * 256; }
+
 static size_t workspace_bytes_for(int B, int H_q, int H_kv, int max_sel, int W, bool listed,
                                   bool all_pages) {
   const int heads = B * H_kv;
   const int G = H_q / H_kv;
   const DecodePlan p = plan_decode(B, H_kv, max_sel, W, listed, all_pages);
   if (p.n_splits == 1) return 0;
-  return (size_t)heads * p.n_splits * G * kPartStride * sizeof(float);
+  return counter_bytes(heads) + (size_t)heads * p.n_splits * G * kPartStride * sizeof(float);
 }
 
 // Lanes per token row, chosen so that the o accumulators stay at <= 64
@@ -520,16 +578,16 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
   a.W = W;
   a.H_kv = H_kv;
   a.scale = (float)pow((double)D, -0.5);
-  a.part = reinterpret_cast<float *>(workspace);
+  a.counters = reinterpret_cast<unsigned *>(workspace);
+  a.part = need == 0 ? nullptr
+                     : reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) +
+                                                 counter_bytes(B * H_kv));
   const dim3 grid(p.n_splits, B * H_kv);
-  const dim3 mgrid((G * kHeadDim + 255) / 256, B * H_kv);
   const int mode = !listed ? kModeAll : (all_pages ? kModeVerified : kModeListed);
 #define CVSA_DEC_LAUNCH(GG, MM)                                                              \
   do {                                                                                       \
     hipLaunchKernelGGL((paged_decode_kernel<GG, LanesPerRow<GG>::value, 4, 2, MM>), grid,    \
                        dim3(4 * kWave), 0, st, a);                                           \
-    if (p.n_splits > 1)                                                                      \
-      hipLaunchKernelGGL((paged_decode_merge_kernel<GG, MM>), mgrid, dim3(256), 0, st, a);   \
   } while (0)
 #define CVSA_DEC_CASE(GG)                                                                    \
   case GG:                                                                                   \

@@ -119,8 +119,12 @@ def _workspace(dev: torch.device, nbytes: int) -> Optional[torch.Tensor]:
     key = (dev.index, stream.cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        # Zeroed once: the decode kernels keep their completion counters at
+        # zero between calls.
         size = (nbytes + (1 << 20) - 1) // (1 << 20) * (1 << 20)
         ws = torch.empty(size, dtype=torch.uint8, device=dev)
+        check(_lib.load().cvsa_workspace_init(ws.data_ptr(), size, stream.cuda_stream),
+              "workspace_init")
         _WORKSPACES[key] = ws
     return ws
 

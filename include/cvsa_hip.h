@@ -120,15 +120,17 @@ int cvsa_check_coverage(const float *page_scores, int32_t B, int32_t H_kv,
 /*
  * Workspace of the paged decode entry points, in bytes, for a call whose
  * heads visit at most `max_sel_pages` listed pages and, when `all_pages` is
- * non-zero, up to W pages (dense heads).  It holds the split-K partial
- * softmax states between the split and merge launches; it needs no
- * initialisation and may be 0 bytes (then NULL is accepted).
+ * non-zero, up to W pages (dense heads).  It holds per-head completion
+ * counters and the split-K partial softmax states.  A workspace must be
+ * zeroed once (cvsa_workspace_init) before its first use; every decode call
+ * leaves its counters at zero again.  May be 0 bytes (then NULL is
+ * accepted).
  */
 size_t cvsa_decode_workspace_bytes(int32_t B, int32_t H_q, int32_t H_kv,
                                    int32_t D, int32_t max_sel_pages,
                                    int32_t W, int32_t all_pages);
 
-/* Zero a workspace on `stream` with a fill kernel (optional). */
+/* Zero a workspace on `stream` with a fill kernel (once, before first use). */
 int cvsa_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 
 /*
