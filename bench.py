@@ -62,7 +62,9 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=M,
                     help="decode steps of the CPU oracle sample (one lazy cycle)")
-    ap.add_argument("--kernel-samples", type=int, default=8)
+    ap.add_argument("--kernel-samples", type=int, default=16)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="also run an elementwise copy of this many MiB (counter calibration)")
     return ap.parse_args()
 
 
@@ -108,19 +110,36 @@ def gpu_sleep(ms):
 
 
 def time_kernel(fn, samples):
-    """Average duration of one launch of fn (HIP events on the current stream;
-    a spin kernel before each sample keeps launch latency out)."""
+    """Average duration of one launch of fn(i), sample i (HIP events on the
+    current stream, which the ops launch on; a spin kernel before each sample
+    keeps host launch latency out)."""
     import torch
     durs = []
-    for _ in range(samples):
+    for i in range(samples):
         gpu_sleep(2.0)
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        fn()
+        fn(i)
         e.record()
         e.synchronize()
         durs.append(s.elapsed_time(e) * 1e3)  # us
     return statistics.mean(durs), durs
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_decode_listed_cfg3_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the listed-page decode kernel, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None if absent)."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1].strip()))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(layer0, n_steps):
@@ -249,24 +268,54 @@ def main():
 
     # ---- per-kernel timing (dominant kernel roofline) and dense baseline
     log("kernel timing")
-    inp = layers[0]
-    q = queries[0][0]
-    K, V, bt, cl = inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens
-    score_us, _ = time_kernel(lambda: ops.score_pages(q, K, bt, cl, H_KV, H_Q // H_KV, BS),
-                              args.kernel_samples)
-    ps = ops.score_pages(q, K, bt, cl, H_KV, H_Q // H_KV, BS)
-    sel_us, _ = time_kernel(lambda: ops.select_topk(ps, n_sel, cl, BS, TAU), args.kernel_samples)
-    pi, nph, acc, cov = ops.select_topk(ps, n_sel, cl, BS, TAU)
-    pif, nphf, pad = ops.prepare_reuse_state(pi, nph, H_KV, B)
-    reuse_us, _ = time_kernel(lambda: ops.sparse_decode_reuse(q, K, V, bt, cl, pif, nphf, pad,
-                                                              H_KV, H_Q // H_KV, BS),
-                              args.kernel_samples)
-    dense_us, _ = time_kernel(lambda: ops.dense_decode(q, K, V, bt, cl, H_KV, H_Q // H_KV, BS),
-                              args.kernel_samples)
-    rej = torch.zeros_like(acc)
-    recover_us, _ = time_kernel(lambda: ops.verified_decode(q, K, V, bt, cl, pi, nph, rej, H_KV,
-                                                            H_Q // H_KV, BS),
-                                args.kernel_samples)
+    # Every sample uses the next layer, so no sample finds its pages cached.
+    G = H_Q // H_KV
+    prep = []
+    for l, inp in enumerate(layers):
+        q = queries[0][l]
+        ps = ops.score_pages(q, inp.k_cache, inp.block_tables, inp.context_lens, H_KV, G, BS)
+        pi, nph, acc, cov = ops.select_topk(ps, n_sel, inp.context_lens, BS, TAU)
+        pif, nphf, pad = ops.prepare_reuse_state(pi, nph, H_KV, B)
+        prep.append((inp, q, ps, pi, nph, torch.zeros_like(acc), pif, nphf, pad))
+
+    def lay(i):
+        return prep[i % L]
+
+    def run_score(i):
+        inp, q = lay(i)[:2]
+        ops.score_pages(q, inp.k_cache, inp.block_tables, inp.context_lens, H_KV, G, BS)
+
+    def run_select(i):
+        inp, q, ps = lay(i)[:3]
+        ops.select_topk(ps, n_sel, inp.context_lens, BS, TAU)
+
+    def run_reuse(i):
+        inp, q, ps, pi, nph, rej, pif, nphf, pad = lay(i)
+        ops.sparse_decode_reuse(q, inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens,
+                                pif, nphf, pad, H_KV, G, BS)
+
+    def run_dense(i):
+        inp, q = lay(i)[:2]
+        ops.dense_decode(q, inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens, H_KV,
+                         G, BS)
+
+    def run_recover(i):
+        inp, q, ps, pi, nph, rej = lay(i)[:6]
+        ops.verified_decode(q, inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens, pi,
+                            nph, rej, H_KV, G, BS)
+
+    n_smp = args.kernel_samples
+    score_us, _ = time_kernel(run_score, n_smp)
+    sel_us, _ = time_kernel(run_select, n_smp)
+    reuse_us, reuse_durs = time_kernel(run_reuse, n_smp)
+    dense_us, _ = time_kernel(run_dense, n_smp)
+    recover_us, _ = time_kernel(run_recover, n_smp)
+    if args.copy_probe_mib:
+        src = torch.ones(args.copy_probe_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
     score_bytes = B * CTX * H_KV * D * 2 + B * H_Q * D * 2 + 4 * W + B * H_KV * W * 4
     reuse_bytes = n_sel * B * H_KV * (2 * BS * D * 2 + 8) + 2 * B * H_Q * D * 2
     dense_bytes = n_valid * B * H_KV * (2 * BS * D * 2 + 8) + 2 * B * H_Q * D * 2
@@ -283,6 +332,7 @@ def main():
     dom_name = "score_pages" if score_us >= M * reuse_us else "sparse_decode(reuse)"
     dom = kernels[dom_name]
 
+    traffic = measured_traffic()
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU oracle baseline")
@@ -326,7 +376,9 @@ def main():
         "kernels": {k: {kk: round(vv, 2) for kk, vv in v.items()} for k, v in kernels.items()},
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(dom["GBps"], 2),
                      "peak": PEAK_HBM_BPS / 1e9, "unit": "GB/s",
-                     "frac": round(dom["GBps"] * 1e9 / PEAK_HBM_BPS, 4), "traffic": None},
+                     "frac": round(dom["GBps"] * 1e9 / PEAK_HBM_BPS, 4),
+                     "traffic": traffic if dom_name == "sparse_decode(reuse)" else None,
+                     "algorithmic_bytes": dom["bytes"], "launch_us": round(dom["us"], 3)},
         "cpu_baseline": cpu,
         "wall_s": round(wall, 4),
         "host_us_per_layer_call": round(host / (args.steps * L) * 1e6, 2),

@@ -1,0 +1,52 @@
+"""The HIP path against the reference implementation's recorded multi-step
+behaviour (golden traces written by tests/golden/make_backend_trace.py):
+outputs, accept masks, selected / complement / expanded page sets, schedule
+counters, statistics and the paged-KV append state."""
+import pytest
+import torch
+
+from golden_trace_check import SCENARIOS, replay
+from cvsa.backend import CVSABackend
+from cvsa.runtime.kv_cache import PagedKVCache, SequenceKVManager
+
+pytestmark = pytest.mark.gpu
+
+
+def _runtime(dev):
+    def make(case):
+        nb, _, H, D = case.k_cache.shape
+        W = case.block_tables.shape[1]
+        B = case.block_tables.shape[0]
+        cache = PagedKVCache(nb, 16, H, D, device=str(dev))
+        cache.k_cache.copy_(case.k_cache)
+        cache.v_cache.copy_(case.v_cache)
+        cache._next_free = case.next_free
+        mgr = SequenceKVManager(cache, B, W * 16)
+        mgr.block_tables.copy_(case.block_tables)
+        mgr.context_lens.copy_(case.context_lens)
+        mgr._pages_allocated = list(case.pages_allocated)
+        mgr.sync_host_state()
+
+        def call_args(q):
+            return q.to(dev), cache.k_cache, cache.v_cache, mgr.block_tables, mgr.context_lens
+
+        def append(b, k, v):
+            mgr.append_token_kv(b, k.to(dev), v.to(dev))
+
+        def state():
+            return mgr.block_tables.cpu().numpy(), mgr.context_lens.cpu().numpy()
+
+        return call_args, append, state
+    return make
+
+
+def _counters(b):
+    return dict(scoring=b._total_scoring_steps, checks=b._total_coverage_checks,
+                accepts=b._accept_counts, rejects=b._reject_counts)
+
+
+@pytest.mark.parametrize("name", sorted(SCENARIOS))
+def test_hip_backend_matches_reference_trace(gpu, name):
+    replay(name, lambda inp, kw: CVSABackend(inp["num_kv_heads"], inp["num_q_heads"],
+                                             inp["head_dim"], 16, **kw),
+           _runtime(gpu), _counters)
