@@ -63,18 +63,21 @@ def parse_args():
     ap.add_argument("--cpu-steps", type=int, default=M,
                     help="decode steps of the CPU oracle sample (one lazy cycle)")
     ap.add_argument("--kernel-samples", type=int, default=16)
+    ap.add_argument("--hot-shift", type=float, default=HOT_SHIFT,
+                    help="hot-page key shift in std units of q_rep.k (default: calibrated)")
+    ap.add_argument("--sink-shift", type=float, default=SINK_SHIFT)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run an elementwise copy of this many MiB (counter calibration)")
     return ap.parse_args()
 
 
-def build_layers(dev, n_layers):
+def build_layers(dev, n_layers, hot_shift, sink_shift):
     from cvsa.synthetic import make_paged_inputs
     layers = []
     for l in range(n_layers):
         inp = make_paged_inputs(B, H_Q, H_KV, D, CTX, seed=1003 + l, device=dev,
-                                hot_heads=list(range(H_KV)), n_hot=N_HOT, hot_shift=HOT_SHIFT,
-                                sink_pages=SINK_PAGES, sink_shift=SINK_SHIFT)
+                                hot_heads=list(range(H_KV)), n_hot=N_HOT, hot_shift=hot_shift,
+                                sink_pages=SINK_PAGES, sink_shift=sink_shift)
         layers.append(inp)
     return layers
 
@@ -110,20 +113,21 @@ def gpu_sleep(ms):
 
 
 def time_kernel(fn, samples):
-    """Average duration of one launch of fn(i), sample i (HIP events on the
-    current stream, which the ops launch on; a spin kernel before each sample
-    keeps host launch latency out)."""
+    """Average duration of one launch of fn(i): `samples` launches back to back
+    (sample i uses layer i mod L, so none finds its pages cached) between two
+    HIP events on the current stream, which the ops launch on.  A spin kernel
+    first lets the host queue the launches ahead of the GPU, so the figure is
+    device time per launch, comparable with rocprofv3's kernel durations."""
     import torch
-    durs = []
+    torch.cuda.synchronize()
+    gpu_sleep(5.0)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
     for i in range(samples):
-        gpu_sleep(2.0)
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
         fn(i)
-        e.record()
-        e.synchronize()
-        durs.append(s.elapsed_time(e) * 1e3)  # us
-    return statistics.mean(durs), durs
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) * 1e3 / samples, None
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_decode_listed_cfg3_traffic.md")
@@ -188,7 +192,7 @@ def main():
     dev = torch.device("cuda:0")
     L = args.layers
     log(f"building {L} layers of {CTX}-token paged KV")
-    layers = build_layers(dev, L)
+    layers = build_layers(dev, L, args.hot_shift, args.sink_shift)
     W = layers[0].block_tables.shape[1]
     n_sel = max(3, int(W * BUDGET_PCT))
     n_valid = -(-CTX // BS)
@@ -361,6 +365,7 @@ def main():
         "config": {"workload": "cfg3: Llama-3.1-8B attention 32q/8kv/d128, B=1, ctx 131072, "
                                "page 16, budget 1/8, lazy M=5, tau 0.9, exact recovery",
                    "layers_rotated": L, "global_batch": B, "seq_len": CTX,
+                   "hot_shift_sigma": args.hot_shift, "sink_shift_sigma": args.sink_shift,
                    "parallelism": "none (1 GPU)"},
         "step_us": {"mean": round(mean_us, 2), "median": round(med_us, 2),
                     **{k: round(statistics.mean(v), 2) for k, v in by_kind.items()}},
