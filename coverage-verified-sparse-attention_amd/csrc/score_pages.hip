@@ -6,16 +6,114 @@
 // (:68) and pages starting at or beyond the context are -inf (:44-47).
 //
 // MI355X mapping: the reference runs one tiny program per (b, kv-head, page).
-// Here one wave streams a whole page for all KV heads: a page is
-// block_size x H_kv rows of 256 B stored back to back (32 KiB for H_kv = 8),
-// so every 16-byte lane load is part of a fully coalesced 1 KiB wave load.
-// Lane l covers row (l >> 4) of each group of four rows and d-segment
-// (l & 15) * 8; the 16 lanes of a DPP row hold one (token, head) row and
-// reduce its dot product with four fused DPP adds.
+// Here a wave streams whole 1 KiB runs of a page: a page is block_size x H_kv
+// rows of 256 B stored back to back (32 KiB for H_kv = 8), so every 16-byte
+// lane load is part of a fully coalesced 1 KiB wave load, and the 16 lanes of
+// a DPP row hold one (token, head) row and reduce its dot product with four
+// fused DPP adds.
 #include "cvsa_common.h"
 
 namespace cvsa {
 
+// q_rep[h][seg*8 .. seg*8+8): fp32 sum over the group, times 1/G, rounded
+// to bf16 (the bf16 result of q.view(B,H_kv,G,D).mean(2)).
+__device__ __forceinline__ uint4 group_mean_q(const uint16_t *__restrict__ q, int64_t q_sb,
+                                              int64_t q_sh, int b, int h, int G, int seg,
+                                              float inv_g) {
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int g = 0; g < G; ++g) {
+    const uint4 v = *reinterpret_cast<const uint4 *>(q + b * q_sb + (int64_t)(h * G + g) * q_sh +
+                                                     seg * 8);
+    acc[0] += bf16_lo(v.x); acc[1] += bf16_hi(v.x);
+    acc[2] += bf16_lo(v.y); acc[3] += bf16_hi(v.y);
+    acc[4] += bf16_lo(v.z); acc[5] += bf16_hi(v.z);
+    acc[6] += bf16_lo(v.w); acc[7] += bf16_hi(v.w);
+  }
+  uint4 r;
+  r.x = pack_bf16x2(acc[0] * inv_g, acc[1] * inv_g);
+  r.y = pack_bf16x2(acc[2] * inv_g, acc[3] * inv_g);
+  r.z = pack_bf16x2(acc[4] * inv_g, acc[5] * inv_g);
+  r.w = pack_bf16x2(acc[6] * inv_g, acc[7] * inv_g);
+  return r;
+}
+
+// H_kv >= 4: a wave owns four KV heads ("quad" hq) of PPW pages.  For each
+// token of a page, the quad's four 256-byte rows are contiguous (1 KiB), so
+// one 16-byte load per lane reads them whole: lane l holds head 4*hq + (l >> 4),
+// d-segment (l & 15) * 8.  The 16 lanes of a DPP row finish the dot product
+// with four fused DPP adds, and each lane keeps the running max of its head.
+// The wave's block-table entries are fetched once (lane j: page j) and the
+// next page's keys are requested before the current page is reduced.
+template <int HKV, int PPW>
+__global__ __launch_bounds__(256) void score_pages_quad_kernel(
+    const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh,
+    const uint16_t *__restrict__ k_cache, int64_t num_blocks,
+    const int32_t *__restrict__ block_tables, int64_t bt_sb,
+    const int32_t *__restrict__ context_lens, float *__restrict__ scores, int W, int G,
+    float inv_g, float scale) {
+  static_assert(HKV >= 4 && HKV % 4 == 0, "quad layout");
+  constexpr int NQ = HKV / 4;  // quads per page
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hq = gw % NQ;
+  const int p_begin = (gw / NQ) * PPW;
+  const int b = blockIdx.y;
+  if (p_begin >= W) return;
+  const int h = 4 * hq + (lane >> 4);
+  const int seg = lane & 15;
+  const int ctx = __builtin_amdgcn_readfirstlane(context_lens[b]);
+  const int n = min(PPW, W - p_begin);
+
+  // Page j of this wave: block id in lane j (-1 when the page holds no
+  // valid token or the id is outside the pool).
+  int my_phys = -1;
+  if (lane < n) {
+    const int p = p_begin + lane;
+    if (p * kPageTokens < ctx) {
+      const int id = block_tables[b * bt_sb + p];
+      if (id >= 0 && id < num_blocks) my_phys = id;
+    }
+  }
+  const uint4 qr = group_mean_q(q, q_sb, q_sh, b, h, G, seg, inv_g);
+  const int64_t lane_off = (int64_t)hq * 4 * kHeadDim + lane * 8;
+  const int64_t row_stride = (int64_t)HKV * kHeadDim;
+  const int64_t page_elems = kPageTokens * row_stride;
+
+  // Unconditional loads (block 0 for pages without valid tokens) keep the
+  // prefetch free of branches.
+  auto fetch = [&](int j, uint4 (&kv)[kPageTokens]) {
+    const int phys = max(__builtin_amdgcn_readlane(my_phys, j), 0);
+    const uint4 *src = reinterpret_cast<const uint4 *>(k_cache + (int64_t)phys * page_elems +
+                                                       lane_off);
+#pragma unroll
+    for (int t = 0; t < kPageTokens; ++t) kv[t] = src[t * (row_stride / 8)];
+  };
+  auto consume = [&](int j, const uint4 (&kv)[kPageTokens]) {
+    const int p = p_begin + j;
+    const int ntok = __builtin_amdgcn_readlane(my_phys, j) < 0
+                         ? 0
+                         : min(kPageTokens, ctx - p * kPageTokens);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < kPageTokens; ++t) {
+      const float s = group_sum<16>(dot8_bf16(kv[t], qr, 0.f)) * scale;
+      if (t < ntok) mx = fmaxf(mx, s);
+    }
+    if (seg == 0) scores[((int64_t)b * HKV + h) * W + p] = mx;
+  };
+  uint4 buf[2][kPageTokens];
+  fetch(0, buf[0]);
+#pragma unroll
+  for (int j = 0; j < PPW; ++j) {
+    if (j + 1 < PPW) fetch(min(j + 1, n - 1), buf[(j + 1) & 1]);
+    if (j < n) consume(j, buf[j & 1]);
+  }
+}
+
+// H_kv < 4: one wave streams a whole page; lane l covers row (l >> 4) of
+// each group of four (token, head) rows and d-segment (l & 15) * 8.
 template <int HKV>
 __global__ __launch_bounds__(256) void score_pages_kernel(
     const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh,
@@ -23,7 +121,7 @@ __global__ __launch_bounds__(256) void score_pages_kernel(
     const int32_t *__restrict__ block_tables, int64_t bt_sb,
     const int32_t *__restrict__ context_lens, float *__restrict__ scores,
     int W, int G, float inv_g, float scale, int ppw) {
-  constexpr int NHL = HKV >= 4 ? HKV / 4 : 1;      // heads held per lane
+  static_assert(HKV < 4, "small-head layout");
   constexpr int NLOAD = kPageTokens * HKV / 4;     // 16-byte loads per lane per page
   constexpr int PAGE_ELEMS = kPageTokens * HKV * kHeadDim;
 
@@ -35,32 +133,8 @@ __global__ __launch_bounds__(256) void score_pages_kernel(
   const int p_begin = (blockIdx.x * 4 + wave) * ppw;
   if (p_begin >= W) return;
   const int ctx = context_lens[b];
-
-  // Head of the j-th row group this lane touches.
-  auto head_of = [&](int j) { return HKV >= 4 ? 4 * j + rsub : rsub % HKV; };
-
-  // q_rep[h][seg*8 .. seg*8+8): fp32 sum over the group, times 1/G, rounded
-  // to bf16 (the bf16 result of q.view(B,H_kv,G,D).mean(2)).
-  uint4 qr[NHL];
-#pragma unroll
-  for (int j = 0; j < NHL; ++j) {
-    const int h = head_of(j);
-    float acc[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-    for (int g = 0; g < G; ++g) {
-      const uint4 v = *reinterpret_cast<const uint4 *>(
-          q + b * q_sb + (int64_t)(h * G + g) * q_sh + seg * 8);
-      acc[0] += bf16_lo(v.x); acc[1] += bf16_hi(v.x);
-      acc[2] += bf16_lo(v.y); acc[3] += bf16_hi(v.y);
-      acc[4] += bf16_lo(v.z); acc[5] += bf16_hi(v.z);
-      acc[6] += bf16_lo(v.w); acc[7] += bf16_hi(v.w);
-    }
-    qr[j].x = pack_bf16x2(acc[0] * inv_g, acc[1] * inv_g);
-    qr[j].y = pack_bf16x2(acc[2] * inv_g, acc[3] * inv_g);
-    qr[j].z = pack_bf16x2(acc[4] * inv_g, acc[5] * inv_g);
-    qr[j].w = pack_bf16x2(acc[6] * inv_g, acc[7] * inv_g);
-  }
+  const int h = rsub % HKV;
+  const uint4 qr = group_mean_q(q, q_sb, q_sh, b, h, G, seg, inv_g);
 
   const int p_end = min(W, p_begin + ppw);
   for (int p = p_begin; p < p_end; ++p) {
@@ -69,10 +143,7 @@ __global__ __launch_bounds__(256) void score_pages_kernel(
     const int phys = ntok > 0 ? block_tables[b * bt_sb + p] : -1;
     if (phys < 0 || phys >= num_blocks) {
       // Beyond the context (or an out-of-range block id): no valid token.
-      if (seg == 0 && (HKV >= 4 || rsub < HKV)) {
-#pragma unroll
-        for (int j = 0; j < NHL; ++j) dst[(int64_t)head_of(j) * W] = -INFINITY;
-      }
+      if (seg == 0 && rsub < HKV) dst[(int64_t)h * W] = -INFINITY;
       continue;
     }
     const uint4 *src =
@@ -80,31 +151,22 @@ __global__ __launch_bounds__(256) void score_pages_kernel(
     uint4 kv[NLOAD];
 #pragma unroll
     for (int i = 0; i < NLOAD; ++i) kv[i] = src[i * 64];
-
-    float mx[NHL];
-#pragma unroll
-    for (int j = 0; j < NHL; ++j) mx[j] = -INFINITY;
+    float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < NLOAD; ++i) {
-      const int row = i * 4 + rsub;
-      const int t = row / HKV;
-      const int j = HKV >= 4 ? (i % NHL) : 0;
-      const float s = group_sum<16>(dot8_bf16(kv[i], qr[j], 0.f)) * scale;
-      if (t < ntok) mx[j] = fmaxf(mx[j], s);
+      const int t = (i * 4 + rsub) / HKV;
+      const float s = group_sum<16>(dot8_bf16(kv[i], qr, 0.f)) * scale;
+      if (t < ntok) mx = fmaxf(mx, s);
     }
-    // With fewer than four heads several row groups share a head.
+    // Several row groups share a head: combine them.
+    float a, c;
     if constexpr (HKV == 1) {
-      float a, c;
-      xchg16(mx[0], a, c); mx[0] = fmaxf(a, c);
-      xchg32(mx[0], a, c); mx[0] = fmaxf(a, c);
-    } else if constexpr (HKV == 2) {
-      float a, c;
-      xchg32(mx[0], a, c); mx[0] = fmaxf(a, c);
+      xchg16(mx, a, c); mx = fmaxf(a, c);
+      xchg32(mx, a, c); mx = fmaxf(a, c);
+    } else {
+      xchg32(mx, a, c); mx = fmaxf(a, c);
     }
-    if (seg == 0 && (HKV >= 4 || rsub < HKV)) {
-#pragma unroll
-      for (int j = 0; j < NHL; ++j) dst[(int64_t)head_of(j) * W] = mx[j];
-    }
+    if (seg == 0 && rsub < HKV) dst[(int64_t)h * W] = mx;
   }
 }
 
@@ -145,12 +207,34 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
   const float inv_g = 1.0f / (float)G;
   const float scale = (float)pow((double)D, -0.5);
 
-  // Pages per wave: keep roughly 8192 waves in flight-able work.
+  hipStream_t st = (hipStream_t)stream;
+  if (H_kv >= 4) {
+    // Quad layout: waves = pages / PPW x H_kv / 4.  Enough pages per wave to
+    // amortise the setup (q_rep, block-table fetch) while keeping >= ~8 waves
+    // per CU.
+    const int64_t quad_pages = (int64_t)B * W * (H_kv / 4);
+    const int ppw = quad_pages >= 8192 ? 2 : 1;
+    const int64_t waves = ((W + ppw - 1) / ppw) * (int64_t)(H_kv / 4);
+    dim3 grid((unsigned)((waves + 3) / 4), B);
+#define CVSA_QUAD_CASE(HK, PP)                                                          \
+  if (H_kv == HK && ppw == PP) {                                                        \
+    hipLaunchKernelGGL((score_pages_quad_kernel<HK, PP>), grid, dim3(256), 0, st, q,    \
+                       q_stride_b, q_stride_h, k_cache, (int64_t)num_blocks,            \
+                       block_tables, bt_stride_b, context_lens, page_scores, W, G,      \
+                       inv_g, scale);                                                   \
+    return cvsa_host::check_launch("score_pages");                                      \
+  }
+    CVSA_QUAD_CASE(4, 1) CVSA_QUAD_CASE(4, 2)
+    CVSA_QUAD_CASE(8, 1) CVSA_QUAD_CASE(8, 2)
+    CVSA_QUAD_CASE(16, 1) CVSA_QUAD_CASE(16, 2)
+#undef CVSA_QUAD_CASE
+    return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d not in {1,2,4,8,16}",
+                           H_kv);
+  }
   const int64_t total = (int64_t)B * W;
   int ppw = (int)((total + 8191) / 8192);
   ppw = ppw < 1 ? 1 : (ppw > 8 ? 8 : ppw);
   dim3 grid((W + 4 * ppw - 1) / (4 * ppw), B);
-  hipStream_t st = (hipStream_t)stream;
   switch (H_kv) {
 #define CVSA_SCORE_CASE(HK)                                                     \
   case HK:                                                                      \
@@ -161,9 +245,6 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
     break;
     CVSA_SCORE_CASE(1)
     CVSA_SCORE_CASE(2)
-    CVSA_SCORE_CASE(4)
-    CVSA_SCORE_CASE(8)
-    CVSA_SCORE_CASE(16)
 #undef CVSA_SCORE_CASE
     default:
       return cvsa_host::fail(CVSA_ERR_UNSUPPORTED,

@@ -264,57 +264,110 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
 }
 
 // Coverage of a given selection (triton_check_coverage).
+// Max (first) and sum (second) of two values over the block; `red` holds
+// 2 x kSelWaves floats and is not reused by the other.
+__device__ __forceinline__ void block_max2(float &a, float &b, float (*red)[2]) {
+  a = wave_max_from_groups<1>(a);
+  b = wave_max_from_groups<1>(b);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    red[wave][0] = a;
+    red[wave][1] = b;
+  }
+  __syncthreads();
+  a = red[0][0];
+  b = red[0][1];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) {
+    a = fmaxf(a, red[w][0]);
+    b = fmaxf(b, red[w][1]);
+  }
+}
+
+__device__ __forceinline__ void block_sum2(float &a, float &b, float (*red)[2]) {
+  a = wave_sum_from_groups<1>(a);
+  b = wave_sum_from_groups<1>(b);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    red[wave][0] = a;
+    red[wave][1] = b;
+  }
+  __syncthreads();
+  a = red[0][0];
+  b = red[0][1];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) {
+    a += red[w][0];
+    b += red[w][1];
+  }
+}
+
+// Coverage gate of a given selection, one workgroup per (b, kv-head).  All
+// global loads are issued at once (the row strided by the block so each
+// load instruction is coalesced, the selection list, n_per_head); for rows
+// of up to 8192 pages the row is staged in LDS and the selected scores are
+// gathered from there.  The two maxima and the two sums each take one block
+// reduction.
 template <int R>
 __global__ __launch_bounds__(kSelThreads) void check_coverage_kernel(
     const float *__restrict__ scores, int W, const int32_t *__restrict__ selected,
     int sel_width, int sel_block, const int32_t *__restrict__ n_per_head,
     float tau, uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out) {
-  __shared__ float red[kSelWaves];
+  constexpr bool kStage = R <= 8;
+  __shared__ float s_row[kStage ? R * kSelThreads : 1];
+  __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2];
   const int bh = blockIdx.x;
   const int t = threadIdx.x;
   const float *row = scores + (int64_t)bh * W;
-  const int i0 = t * R;
+  const int32_t *sel = selected + (int64_t)bh * sel_width;
 
-  float val[R];
-  float mx = -INFINITY;
+  const int n_raw = n_per_head[bh];
+  float v[R];
+  int pidx[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    val[r] = (i0 + r < W) ? row[i0 + r] : -INFINITY;
-    mx = fmaxf(mx, val[r]);
+    const int i = t + r * kSelThreads;
+    v[r] = i < W ? row[i] : -INFINITY;
+    pidx[r] = i < sel_width ? sel[i] : -1;
   }
-  const float m_all = fmaxf(block_max(mx, red), -1e20f);
-  float se = 0.f;
-#pragma unroll
-  for (int r = 0; r < R; ++r) se += expf(val[r] - m_all);
-  const float lse_all = lse_from(m_all, block_sum(se, red));
-
   // Selected scores: entries j < n_sel of the row (coverage.py:198-208).
   // n_sel is clamped to the row width and indices outside [0, W) read as
   // -inf, so a malformed selection cannot read out of bounds.
-  const int n_sel = max(0, min(n_per_head[bh], sel_width));
-  const int32_t *sel = selected + (int64_t)bh * sel_width;
+  const int n_sel = max(0, min(n_raw, sel_width));
   float sv[R];
-  float ms = -INFINITY;
+  if constexpr (kStage) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = t + r * kSelThreads;
+      if (i < W) s_row[i] = v[r];
+    }
+    __syncthreads();
+  }
+  float mx_all = -INFINITY, mx_sel = -INFINITY;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int j = i0 + r;
-    float v = -INFINITY;
-    if (j < n_sel) {
-      const int p = sel[j];
-      v = (p >= 0 && p < W) ? row[p] : -INFINITY;
-    }
-    sv[r] = v;
-    if (j < n_sel) ms = fmaxf(ms, v);
+    const int j = t + r * kSelThreads;
+    const int p = pidx[r];
+    float x = -INFINITY;
+    if (j < n_sel && p >= 0 && p < W) x = kStage ? s_row[p] : row[p];
+    sv[r] = x;
+    mx_all = fmaxf(mx_all, v[r]);
+    mx_sel = fmaxf(mx_sel, x);
   }
-  float m_sel = block_max(ms, red);
-  if (n_sel < sel_block) m_sel = fmaxf(m_sel, -1e20f);
-  float ss = 0.f;
+  block_max2(mx_all, mx_sel, red_max);
+  // lse_all floors its running max at -1e20 (coverage.py:180); lse_sel has
+  // -1e20 padding lanes whenever n_sel is short of the power-of-two block.
+  const float m_all = fmaxf(mx_all, -1e20f);
+  const float m_sel = n_sel < sel_block ? fmaxf(mx_sel, -1e20f) : mx_sel;
+  float se_all = 0.f, se_sel = 0.f;
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-    if (i0 + r < n_sel) ss += expf(sv[r] - m_sel);
-  const float lse_sel = lse_from(m_sel, block_sum(ss, red));
+  for (int r = 0; r < R; ++r) {
+    se_all += expf(v[r] - m_all);
+    if (t + r * kSelThreads < n_sel) se_sel += expf(sv[r] - m_sel);
+  }
+  block_sum2(se_all, se_sel, red_sum);
   if (t == 0) {
-    const float cov = expf(lse_sel - lse_all);
+    const float cov = expf(lse_from(m_sel, se_sel) - lse_from(m_all, se_all));
     coverage_out[bh] = cov;
     accept_out[bh] = cov >= tau ? 1 : 0;
   }
