@@ -24,35 +24,12 @@ namespace cvsa {
 
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / kWave;
+constexpr int kHistCopies = 16;
+constexpr int kHistStride = 257;
 
 __device__ __forceinline__ uint32_t order_key(float f) {
   const uint32_t u = __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Reductions over the 1024-thread block.  `red` holds kSelWaves floats.
-__device__ __forceinline__ float block_max(float v, float *red) {
-  v = wave_max_from_groups<1>(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  float r = red[0];
-#pragma unroll
-  for (int w = 1; w < kSelWaves; ++w) r = fmaxf(r, red[w]);
-  return r;
-}
-
-__device__ __forceinline__ float block_sum(float v, float *red) {
-  v = wave_sum_from_groups<1>(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  float r = red[0];
-#pragma unroll
-  for (int w = 1; w < kSelWaves; ++w) r += red[w];
-  return r;
 }
 
 // Exclusive prefix sum of one uint32 per thread over the block, plus total.
@@ -85,6 +62,44 @@ __device__ __forceinline__ float lse_from(float mx_floor, float sum) {
   return mx_floor + logf(sum + 1e-30f);
 }
 
+// Max (first) and sum (second) of two values over the block; `red` holds
+// 2 x kSelWaves floats and is not reused by the other.
+__device__ __forceinline__ void block_max2(float &a, float &b, float (*red)[2]) {
+  a = wave_max_from_groups<1>(a);
+  b = wave_max_from_groups<1>(b);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    red[wave][0] = a;
+    red[wave][1] = b;
+  }
+  __syncthreads();
+  a = red[0][0];
+  b = red[0][1];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) {
+    a = fmaxf(a, red[w][0]);
+    b = fmaxf(b, red[w][1]);
+  }
+}
+
+__device__ __forceinline__ void block_sum2(float &a, float &b, float (*red)[2]) {
+  a = wave_sum_from_groups<1>(a);
+  b = wave_sum_from_groups<1>(b);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    red[wave][0] = a;
+    red[wave][1] = b;
+  }
+  __syncthreads();
+  a = red[0][0];
+  b = red[0][1];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) {
+    a += red[w][0];
+    b += red[w][1];
+  }
+}
+
 template <int R>
 __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     const float *__restrict__ scores, int W, int H_kv,
@@ -94,8 +109,9 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
     long long *__restrict__ stats) {
   __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist_c[kHistCopies * kHistStride];
   __shared__ uint32_t wsum[kSelWaves];
-  __shared__ float red[kSelWaves];
+  __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2];
   __shared__ uint32_t s_digit, s_krem;
   __shared__ int s_nok;
 
@@ -140,12 +156,22 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
 
   float val[R];
   uint32_t key[R];
+  if (R >= 4 && (W & 3) == 0 && i0 + R <= W) {
+    // Whole 16-byte groups (row starts are 16-byte aligned when W % 4 == 0).
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int i = i0 + r;
-    val[r] = i < W ? row[i] : -INFINITY;
-    key[r] = order_key(val[r]);
+    for (int r = 0; r < R; r += 4) {
+      const float4 v4 = *reinterpret_cast<const float4 *>(row + i0 + r);
+      val[r] = v4.x;
+      val[r + 1 < R ? r + 1 : r] = v4.y;
+      val[r + 2 < R ? r + 2 : r] = v4.z;
+      val[r + 3 < R ? r + 3 : r] = v4.w;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) val[r] = i0 + r < W ? row[i0 + r] : -INFINITY;
   }
+#pragma unroll
+  for (int r = 0; r < R; ++r) key[r] = order_key(val[r]);
   if (scores_cache != nullptr) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -157,12 +183,24 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
 #pragma unroll 1
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
-    if (t < 256) hist[t] = 0;
+    for (int i = t; i < kHistCopies * kHistStride; i += kSelThreads) hist_c[i] = 0;
     __syncthreads();
+    // Scores cluster in a few leading digits, so lanes of one instruction
+    // often hit the same bin: each lane adds into copy (lane % kHistCopies)
+    // of the histogram (rows padded by one word so that the copies of a bin
+    // sit in different LDS banks), and the copies are summed afterwards.
+    uint32_t *my_hist = hist_c + (lane % kHistCopies) * kHistStride;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (i0 + r < W && (key[r] & pmask) == prefix)
-        atomicAdd(&hist[(key[r] >> shift) & 255u], 1u);
+        atomicAdd(&my_hist[(key[r] >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (t < 256) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int k = 0; k < kHistCopies; ++k) c += hist_c[k * kHistStride + t];
+      hist[t] = c;
     }
     __syncthreads();
     if (t < 64) {
@@ -234,71 +272,30 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
 
   if (accept_out == nullptr) return;
   // ---- coverage of the new selection
-  float mx = -INFINITY;
+  float mx = -INFINITY, ms = -INFINITY;
 #pragma unroll
-  for (int r = 0; r < R; ++r) mx = fmaxf(mx, val[r]);
-  const float m_all = fmaxf(block_max(mx, red), -1e20f);
-  float se = 0.f;
-#pragma unroll
-  for (int r = 0; r < R; ++r) se += expf(val[r] - m_all);
-  const float lse_all = lse_from(m_all, block_sum(se, red));
-
-  float ms = -INFINITY;
-#pragma unroll
-  for (int r = 0; r < R; ++r) if (counted[r]) ms = fmaxf(ms, val[r]);
+  for (int r = 0; r < R; ++r) {
+    mx = fmaxf(mx, val[r]);
+    if (counted[r]) ms = fmaxf(ms, val[r]);
+  }
+  block_max2(mx, ms, red_max);
+  const float m_all = fmaxf(mx, -1e20f);
   // Padding lanes of the reference's power-of-two selection block carry
   // -1e20 into the max whenever n_sel is below that block (coverage.py:205).
-  float m_sel = block_max(ms, red);
   int msel_block = 1;
   while (msel_block < budget) msel_block <<= 1;
-  if (n_sel < msel_block) m_sel = fmaxf(m_sel, -1e20f);
-  float ss = 0.f;
+  const float m_sel = n_sel < msel_block ? fmaxf(ms, -1e20f) : ms;
+  float se = 0.f, ss = 0.f;
 #pragma unroll
-  for (int r = 0; r < R; ++r) if (counted[r]) ss += expf(val[r] - m_sel);
-  const float lse_sel = lse_from(m_sel, block_sum(ss, red));
+  for (int r = 0; r < R; ++r) {
+    se += expf(val[r] - m_all);
+    if (counted[r]) ss += expf(val[r] - m_sel);
+  }
+  block_sum2(se, ss, red_sum);
   if (t == 0) {
-    const float cov = expf(lse_sel - lse_all);
+    const float cov = expf(lse_from(m_sel, ss) - lse_from(m_all, se));
     coverage_out[bh] = cov;
     accept_out[bh] = cov >= tau ? 1 : 0;
-  }
-}
-
-// Coverage of a given selection (triton_check_coverage).
-// Max (first) and sum (second) of two values over the block; `red` holds
-// 2 x kSelWaves floats and is not reused by the other.
-__device__ __forceinline__ void block_max2(float &a, float &b, float (*red)[2]) {
-  a = wave_max_from_groups<1>(a);
-  b = wave_max_from_groups<1>(b);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) {
-    red[wave][0] = a;
-    red[wave][1] = b;
-  }
-  __syncthreads();
-  a = red[0][0];
-  b = red[0][1];
-#pragma unroll
-  for (int w = 1; w < kSelWaves; ++w) {
-    a = fmaxf(a, red[w][0]);
-    b = fmaxf(b, red[w][1]);
-  }
-}
-
-__device__ __forceinline__ void block_sum2(float &a, float &b, float (*red)[2]) {
-  a = wave_sum_from_groups<1>(a);
-  b = wave_sum_from_groups<1>(b);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) {
-    red[wave][0] = a;
-    red[wave][1] = b;
-  }
-  __syncthreads();
-  a = red[0][0];
-  b = red[0][1];
-#pragma unroll
-  for (int w = 1; w < kSelWaves; ++w) {
-    a += red[w][0];
-    b += red[w][1];
   }
 }
 
