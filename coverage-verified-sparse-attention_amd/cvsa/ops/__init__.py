@@ -69,7 +69,7 @@ def _device_of(*tensors: torch.Tensor) -> torch.device:
 
 
 def _stream(dev: torch.device) -> int:
-    return torch.cuda.current_stream(dev).cuda_stream
+    return torch._C._cuda_getCurrentRawStream(dev.index)
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -115,16 +115,15 @@ def _workspace(dev: torch.device, nbytes: int) -> Optional[torch.Tensor]:
     """Per-(device, stream) decode workspace of at least nbytes (None for 0)."""
     if nbytes == 0:
         return None
-    stream = torch.cuda.current_stream(dev)
-    key = (dev.index, stream.cuda_stream)
+    stream = _stream(dev)
+    key = (dev.index, stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         # Zeroed once: the decode kernels keep their completion counters at
         # zero between calls.
         size = (nbytes + (1 << 20) - 1) // (1 << 20) * (1 << 20)
         ws = torch.empty(size, dtype=torch.uint8, device=dev)
-        check(_lib.load().cvsa_workspace_init(ws.data_ptr(), size, stream.cuda_stream),
-              "workspace_init")
+        check(_lib.load().cvsa_workspace_init(ws.data_ptr(), size, stream), "workspace_init")
         _WORKSPACES[key] = ws
     return ws
 
@@ -261,9 +260,50 @@ def check_coverage(page_scores: torch.Tensor, selected_indices: torch.Tensor,
 
 # ---------------------------------------------------------------- decode
 
-def _decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
-            num_q_per_kv, block_size, pi_flat=None, nph_flat=None, max_sel=0,
-            accept=None, want_state=False, want_out=True, out_dtype=None, work=None):
+class DecodeCall:
+    """A validated decode launch whose buffers stay fixed between calls.
+
+    Built by :func:`prepare_decode`; ``run(q)`` launches it for a new query
+    of the same shape and strides, allocating only the outputs.  ``matches``
+    tells whether the call can be reused for a given set of buffers (same
+    tensor objects, same stream); callers that hold a DecodeCall across
+    steps check it before every use.
+    """
+
+    __slots__ = ("fn", "args", "kind", "dev", "stream", "q_meta", "out_shape", "out_dtype",
+                 "want_state", "refs", "reusable", "_out_i", "_state_i")
+
+    def matches(self, q, k_cache, v_cache, block_tables, context_lens, work) -> bool:
+        r = self.refs
+        return (self.reusable and r[0] is k_cache and r[1] is v_cache and r[2] is block_tables
+                and r[3] is context_lens and r[4] is work
+                and torch._C._cuda_getCurrentRawStream(self.dev.index) == self.stream
+                and q.device == self.dev and q.dtype == torch.bfloat16
+                and (q.shape, q.stride()) == self.q_meta and q.data_ptr() % 16 == 0)
+
+    def run(self, q):
+        args = self.args
+        args[0] = q.data_ptr()
+        o = m = l = out = None
+        if self.want_state:
+            B, H_q, D = self.out_shape
+            o = torch.empty(B, H_q, D, device=self.dev, dtype=torch.float32)
+            m = torch.empty(B, H_q, device=self.dev, dtype=torch.float32)
+            l = torch.empty(B, H_q, device=self.dev, dtype=torch.float32)
+            i = self._state_i
+            args[i], args[i + 1], args[i + 2] = o.data_ptr(), m.data_ptr(), l.data_ptr()
+        if self.out_dtype is not None:
+            out = torch.empty(self.out_shape, device=self.dev, dtype=self.out_dtype)
+            args[self._out_i] = out.data_ptr()
+        check(self.fn(*args), self.kind)
+        return o, m, l, out
+
+
+def prepare_decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
+                   num_q_per_kv, block_size, pi_flat=None, nph_flat=None, max_sel=0,
+                   accept=None, want_state=False, want_out=True, out_dtype=None,
+                   work=None) -> DecodeCall:
+    """Validate a decode launch and build its argument list (see DecodeCall)."""
     dev = _device_of(q, k_cache, v_cache, block_tables, context_lens, pi_flat, nph_flat,
                      accept, work)
     if work is not None and (work.dtype != torch.int64 or work.numel() < 2
@@ -288,34 +328,57 @@ def _decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, num_kv_h
     need = L.cvsa_decode_workspace_bytes(B, H_q, num_kv_heads, D, max_sel if listed else 0,
                                          W, 1 if all_pages else 0)
     ws = _workspace(dev, need)
-    o = m = l = out = None
-    if want_state:
-        o = torch.empty(B, H_q, D, device=dev, dtype=torch.float32)
-        m = torch.empty(B, H_q, device=dev, dtype=torch.float32)
-        l = torch.empty(B, H_q, device=dev, dtype=torch.float32)
+    od = None
     code = 0
     if want_out:
         od = out_dtype or q.dtype
         if od not in _DTYPE_CODE:
             raise ValueError(f"unsupported output dtype {od}")
-        out = torch.empty(B, H_q, D, device=dev, dtype=od)
         code = _DTYPE_CODE[od]
-    common_q = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
-                k_cache.shape[0], bt.data_ptr(), bt.stride(0), ctx.data_ptr())
-    tail = (_ptr(o), _ptr(m), _ptr(l), _ptr(out), code, _ptr(work), _ptr(ws),
-            0 if ws is None else ws.numel(), _stream(dev))
+    stream = torch._C._cuda_getCurrentRawStream(dev.index)
+    head = [q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+            k_cache.shape[0], bt.data_ptr(), bt.stride(0), ctx.data_ptr()]
     if kind == "sparse_decode":
-        rc = L.cvsa_sparse_decode(*common_q, pi_flat.data_ptr(), pi_flat.stride(0),
-                                  nph_flat.data_ptr(), max_sel, B, H_q, num_kv_heads, D,
-                                  block_size, W, *tail)
+        fn = L.cvsa_sparse_decode
+        mid = [pi_flat.data_ptr(), pi_flat.stride(0), nph_flat.data_ptr(), max_sel]
     elif kind == "dense_decode":
-        rc = L.cvsa_dense_decode(*common_q, B, H_q, num_kv_heads, D, block_size, W, *tail)
+        fn = L.cvsa_dense_decode
+        mid = []
     else:
-        rc = L.cvsa_verified_decode(*common_q, pi_flat.data_ptr(), pi_flat.stride(0),
-                                    nph_flat.data_ptr(), max_sel, accept.data_ptr(), B, H_q,
-                                    num_kv_heads, D, block_size, W, *tail)
-    check(rc, kind)
-    return o, m, l, out
+        fn = L.cvsa_verified_decode
+        mid = [pi_flat.data_ptr(), pi_flat.stride(0), nph_flat.data_ptr(), max_sel,
+               accept.data_ptr()]
+    sizes = [B, H_q, num_kv_heads, D, block_size, W]
+    tail = [None, None, None, None, code, _ptr(work), _ptr(ws),
+            0 if ws is None else ws.numel(), stream]
+    c = DecodeCall()
+    c.fn = fn
+    c.args = head + mid + sizes + tail
+    c._state_i = len(head) + len(mid) + len(sizes)
+    c._out_i = c._state_i + 3
+    c.kind = kind
+    c.dev = dev
+    c.stream = stream
+    c.q_meta = (q.shape, q.stride())
+    c.out_shape = (B, H_q, D)
+    c.out_dtype = od
+    c.want_state = want_state
+    # The tensors the launch reads; the converted ones (if any) are kept
+    # alive here but make the call non-reusable, since their content is a
+    # snapshot of the caller's tensors.
+    c.refs = (k_cache, v_cache, block_tables, context_lens, work, bt, ctx, pi_flat, nph_flat,
+              accept, ws)
+    c.reusable = bt is block_tables and ctx is context_lens
+    return c
+
+
+def _decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
+            num_q_per_kv, block_size, pi_flat=None, nph_flat=None, max_sel=0,
+            accept=None, want_state=False, want_out=True, out_dtype=None, work=None):
+    c = prepare_decode(kind, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
+                       num_q_per_kv, block_size, pi_flat, nph_flat, max_sel, accept, want_state,
+                       want_out, out_dtype, work)
+    return c.run(_check_q(q))
 
 
 def _flat_selection(page_indices: torch.Tensor, n_per_head: torch.Tensor, num_kv_heads: int):
@@ -381,10 +444,19 @@ def sparse_decode_reuse(q, k_cache, v_cache, block_tables, context_lens, pi_flat
     Mirrors triton_sparse_decode_reuse (cvsa/kernels/sparse_decode.py:681-721).
     ``work`` (int64[2]) accumulates the effective-budget counters.
     """
+    return prepare_sparse_decode_reuse(q, k_cache, v_cache, block_tables, context_lens,
+                                       pi_flat, nph_flat, padded_max_selected, num_kv_heads,
+                                       num_q_per_kv, block_size, work).run(_check_q(q))[3]
+
+
+def prepare_sparse_decode_reuse(q, k_cache, v_cache, block_tables, context_lens, pi_flat,
+                                nph_flat, padded_max_selected, num_kv_heads, num_q_per_kv,
+                                block_size, work: Optional[torch.Tensor] = None) -> DecodeCall:
+    """The launch of sparse_decode_reuse as a reusable DecodeCall."""
     width = min(int(padded_max_selected), pi_flat.shape[1])
-    return _decode("sparse_decode", q, k_cache, v_cache, block_tables, context_lens,
-                   num_kv_heads, num_q_per_kv, block_size, pi_flat, nph_flat, width,
-                   work=work)[3]
+    return prepare_decode("sparse_decode", q, k_cache, v_cache, block_tables, context_lens,
+                          num_kv_heads, num_q_per_kv, block_size, pi_flat, nph_flat, width,
+                          work=work)
 
 
 def dense_decode(q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
