@@ -218,12 +218,20 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeAr
   // the head's scalar state (their position only needs the split's start,
   // split * pps_sel), which takes one memory round trip off the page-table
   // lookups.  Lanes past the head's pages are never consumed.
-  int spec_lp = 0;
+  // The block-table entries of those pages are requested as soon as the
+  // entries arrive (clamped into the table; lanes past the head's pages
+  // are discarded later), so the table lookup does not wait for the head's
+  // page count either.
+  int spec_lp = 0, spec_phys = 0;
   if constexpr (MODE != kModeAll) {
     if (a.max_sel > 0) {
       const int rs = min(split * a.pps_sel + wave + NW * lane, a.max_sel - 1);
       spec_lp = a.page_idx[(int64_t)bh * a.idx_stride + rs];
+      spec_phys = a.block_tables[b * a.bt_sb + min(max(spec_lp, 0), a.W - 1)];
     }
+  } else {
+    spec_lp = min(split * a.pps_all + wave + NW * lane, a.W - 1);
+    spec_phys = a.block_tables[b * a.bt_sb + spec_lp];
   }
 
   const HeadWalk<MODE> hw(a, bh, ctx);
@@ -312,9 +320,12 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeAr
       int my_phys = 0, my_ntok = 0;
       if (lane < cn) {
         const int r = r0 + wave + NW * (c0 + lane);
-        const int lp = listed ? (c0 == 0 ? spec_lp : idx_row[r]) : r;
+        // Chunk 0 of a listed head (or of an all-pages launch) uses the
+        // entries requested up front; the spec index equals r there.
+        const bool spec = c0 == 0 && (MODE == kModeAll || listed);
+        const int lp = spec ? spec_lp : (listed ? idx_row[r] : r);
         if (lp >= 0 && lp < a.W) {
-          const int phys = a.block_tables[b * a.bt_sb + lp];
+          const int phys = spec ? spec_phys : a.block_tables[b * a.bt_sb + lp];
           if (phys >= 0 && phys < a.num_blocks) {
             my_phys = phys;
             my_ntok = min(kPageTokens, ctx - lp * kPageTokens);
