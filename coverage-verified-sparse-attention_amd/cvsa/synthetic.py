@@ -46,13 +46,16 @@ def make_paged_inputs(batch: int, num_q_heads: int, num_kv_heads: int, head_dim:
                       device="cpu", max_pages: Optional[int] = None, spare_blocks: int = 16,
                       hot_heads: Optional[Sequence[int]] = None, n_hot: int = 8,
                       n_hot_range: Optional[Sequence[int]] = None, hot_shift: float = 3.0,
-                      sink_pages: int = 0, sink_shift: float = 0.0) -> PagedInputs:
+                      sink_pages: int = 0, sink_shift: float = 0.0,
+                      random_hot_heads: int = 0) -> PagedInputs:
     """Build one layer's decode inputs.
 
     context_len: int, or a per-sequence list.
     hot_heads:   KV heads that get hot pages (default: every other head);
                  ignored when ``n_hot_range`` is given.
     n_hot_range: (lo, hi): every (b, h) draws its hot-page count from U{lo..hi}.
+    random_hot_heads: if > 0, each sequence draws this many hot heads at
+                 random (instead of ``hot_heads``).
     """
     device = torch.device(device)
     g = _generator(device, seed)
@@ -87,6 +90,8 @@ def make_paged_inputs(batch: int, num_q_heads: int, num_kv_heads: int, head_dim:
     for b in range(B):
         nv = pages[b]
         cand = max(0, nv - sink_pages)
+        if random_hot_heads:
+            hot_heads = torch.randperm(H, generator=g, device=device)[:random_hot_heads].tolist()
         if sink_pages and sink_shift:
             phys = bt[b, :min(sink_pages, nv)].long()
             K[phys] += sink_shift * qhat[b].view(1, 1, H, D)
