@@ -107,7 +107,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
     uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
     const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
-    long long *__restrict__ stats) {
+    long long *__restrict__ stats, int count_gate) {
   __shared__ uint32_t hist[256];
   __shared__ uint32_t hist_c[kHistCopies * kHistStride];
   __shared__ uint32_t wsum[kSelWaves];
@@ -149,8 +149,8 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
       if (t == 0) accept_out[bh] = 1;
       return;
     }
-  } else if (stats != nullptr && bh == 0 && t == 0) {
-    stats[1] += 1;  // a scoring step without a cached selection
+  } else if (stats != nullptr && !count_gate && bh == 0 && t == 0) {
+    stats[1] += 1;  // a lazy scoring step without a cached selection
     stats[2] += 1;
   }
 
@@ -294,8 +294,31 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   block_sum2(se, ss, red_sum);
   if (t == 0) {
     const float cov = expf(lse_from(m_sel, ss) - lse_from(m_all, se));
+    const int acc = cov >= tau ? 1 : 0;
     coverage_out[bh] = cov;
-    accept_out[bh] = cov >= tau ? 1 : 0;
+    accept_out[bh] = (uint8_t)acc;
+    if (stats != nullptr && count_gate) {
+      // Fixed-interval scoring step (backend.py:859-863): tally this head,
+      // then the last head of the call books the step as all-accepted or
+      // not.  stats[4] (rejected heads of this call) and stats[5] (heads
+      // done) are scratch that the last head clears again.
+      __hip_atomic_fetch_add(&stats[3], (long long)acc, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(&stats[4], (long long)(1 - acc), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      const long long done = __hip_atomic_fetch_add(&stats[5], 1LL, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+      if (done == (long long)n_heads - 1) {
+        const long long rej = __hip_atomic_fetch_add(&stats[4], 0LL, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        stats[0] += rej == 0 ? 1 : 0;
+        stats[1] += rej != 0 ? 1 : 0;
+        stats[2] += 1;
+        __hip_atomic_store(&stats[4], 0LL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&stats[5], 0LL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
 }
 
@@ -381,13 +404,16 @@ static int launch_select(const char *name, const float *page_scores, int32_t B, 
                          int32_t W, const int32_t *context_lens, int32_t block_size,
                          int32_t budget, int32_t *page_indices, int32_t *n_per_head, float tau,
                          uint8_t *accept_out, float *coverage_out, const uint8_t *check_accept,
-                         float *scores_cache, int64_t *stats, void *stream) {
+                         float *scores_cache, int64_t *stats, int count_gate,
+                         void *stream) {
   CVSA_REQUIRE(page_scores && context_lens && page_indices && n_per_head, CVSA_ERR_INVALID,
                "%s: null pointer argument", name);
   CVSA_REQUIRE((accept_out == nullptr) == (coverage_out == nullptr), CVSA_ERR_INVALID,
                "%s: accept_out and coverage_out must both be set or both NULL", name);
   CVSA_REQUIRE(check_accept == nullptr || accept_out != nullptr, CVSA_ERR_INVALID,
                "%s: a device-side check needs accept_out", name);
+  CVSA_REQUIRE(!count_gate || (check_accept == nullptr && accept_out != nullptr),
+               CVSA_ERR_INVALID, "%s: count_gate needs a fresh selection with its gate", name);
   CVSA_REQUIRE(B > 0 && H_kv > 0 && W > 0 && block_size > 0, CVSA_ERR_INVALID,
                "%s: bad sizes B=%d H_kv=%d W=%d bs=%d", name, B, H_kv, W, block_size);
   CVSA_REQUIRE(budget >= 1 && budget <= W, CVSA_ERR_INVALID,
@@ -404,7 +430,7 @@ static int launch_select(const char *name, const float *page_scores, int32_t B, 
     hipLaunchKernelGGL(select_topk_kernel<RR>, grid, dim3(kSelThreads), 0, st, page_scores, \
                        W, H_kv, context_lens, block_size, budget, page_indices, n_per_head, \
                        tau, accept_out, coverage_out, check_accept, B * H_kv, scores_cache,  \
-                       st64);                                                            \
+                       st64, count_gate);                                                \
     break;
     CVSA_SEL_CASE(1)
     CVSA_SEL_CASE(2)
@@ -430,7 +456,7 @@ extern "C" int cvsa_select_topk(const float *page_scores, int32_t B, int32_t H_k
                                 void *stream) {
   return launch_select("select_topk", page_scores, B, H_kv, W, context_lens, block_size,
                        budget, page_indices, n_per_head, tau, accept_out, coverage_out,
-                       nullptr, nullptr, nullptr, stream);
+                       nullptr, nullptr, nullptr, 0, stream);
 }
 
 extern "C" int cvsa_select_or_keep(const float *page_scores, const uint8_t *check_accept,
@@ -438,12 +464,13 @@ extern "C" int cvsa_select_or_keep(const float *page_scores, const uint8_t *chec
                                    const int32_t *context_lens, int32_t block_size,
                                    int32_t budget, int32_t *page_indices, int32_t *n_per_head,
                                    float tau, uint8_t *accept_out, float *coverage_out,
-                                   float *scores_cache, int64_t *stats, void *stream) {
+                                   float *scores_cache, int64_t *stats, int32_t count_gate,
+                                   void *stream) {
   CVSA_REQUIRE(accept_out && coverage_out, CVSA_ERR_INVALID,
                "select_or_keep: accept_out and coverage_out are required");
   return launch_select("select_or_keep", page_scores, B, H_kv, W, context_lens, block_size,
                        budget, page_indices, n_per_head, tau, accept_out, coverage_out,
-                       check_accept, scores_cache, stats, stream);
+                       check_accept, scores_cache, stats, count_gate, stream);
 }
 
 extern "C" int cvsa_check_coverage(const float *page_scores, int32_t B,

@@ -360,12 +360,12 @@ class CVSABackend:
         host = [self._h_accept_counts, self._h_reject_counts, self._h_total_scoring_steps,
                 self._h_per_head_accept_sum]
         if self._dev_stats is not None:
-            host = [h + d for h, d in zip(host, self._dev_stats.tolist())]
+            host = [h + d for h, d in zip(host, self._dev_stats[:4].tolist())]
         return tuple(host)
 
     def _ensure_dev_stats(self, device) -> Optional[torch.Tensor]:
         if self._dev_stats is None:
-            self._dev_stats = torch.zeros(4, dtype=torch.long, device=device)
+            self._dev_stats = torch.zeros(6, dtype=torch.long, device=device)
         return self._dev_stats if self._dev_stats.device == torch.device(device) else None
 
     def _decode_work(self, context_lens):
@@ -504,9 +504,26 @@ class CVSABackend:
         self._cached_page_scores[layer_idx] = page_scores                         # :713
 
         # Top-k selection fused with the coverage gate of the new selection.
-        page_indices, n_per_head, accept_mask, _coverage = self._time_kernel(
-            "coverage", ops.select_topk, page_scores, budget, context_lens, self.block_size,
-            self.tau)
+        # In the fixed-interval schedule the gate's counters (:859-863) are
+        # booked on the device, so the step needs no host read.
+        dev = page_scores.device
+        device_book = (not self.lazy and self.random_reject_prob is None
+                       and self.approx_recovery_pct is None
+                       and self._ensure_dev_stats(dev) is not None)
+        if device_book:
+            H = self.num_kv_heads
+            page_indices = torch.empty(B, H, budget, dtype=torch.int32, device=dev)
+            n_per_head = torch.empty(B, H, dtype=torch.int32, device=dev)
+            coverage = torch.empty(B, H, dtype=torch.float32, device=dev)
+            accept_mask = self._time_kernel(
+                "coverage", ops.select_or_keep, page_scores, None, budget, context_lens,
+                self.block_size, self.tau, page_indices, n_per_head, coverage, None,
+                self._dev_stats, count_gate=True)
+            self._per_head_total += B * H
+        else:
+            page_indices, n_per_head, accept_mask, _coverage = self._time_kernel(
+                "coverage", ops.select_topk, page_scores, budget, context_lens,
+                self.block_size, self.tau)
         accept_mask = self._apply_random_reject(accept_mask)
         self._last_accept_mask[layer_idx] = accept_mask                           # :771
 
@@ -525,7 +542,7 @@ class CVSABackend:
                 self._record_work(context_lens, pages)
             self._expanded_store[layer_idx] = _PendingComplement(
                 accept_mask, page_indices, n_per_head, context_lens, self.block_size)
-            if not self.lazy:
+            if not self.lazy and not device_book:
                 n_acc = int(accept_mask.sum().item())
                 if n_acc == accept_mask.numel():
                     self._h_accept_counts += 1
@@ -545,7 +562,8 @@ class CVSABackend:
                                         ops.next_power_of_2(page_indices.shape[2]))
         self._reuse_plans.pop(layer_idx, None)
         self._cached_selection[layer_idx] = (page_indices, n_per_head)
-        self._h_total_scoring_steps += 1                                          # :859
+        if not device_book:
+            self._h_total_scoring_steps += 1                                      # :859
         return output
 
     def _approx_recovery(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx,

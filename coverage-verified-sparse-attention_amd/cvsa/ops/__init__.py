@@ -190,20 +190,25 @@ def select_topk(page_scores: torch.Tensor, budget: int, context_lens: torch.Tens
     return idx, nph, acc.view(torch.bool), cov
 
 
-def select_or_keep(page_scores: torch.Tensor, check_accept: torch.Tensor, budget: int,
-                   context_lens: torch.Tensor, block_size: int, tau: float,
+def select_or_keep(page_scores: torch.Tensor, check_accept: Optional[torch.Tensor],
+                   budget: int, context_lens: torch.Tensor, block_size: int, tau: float,
                    page_indices: torch.Tensor, n_per_head: torch.Tensor,
                    coverage: torch.Tensor, scores_cache: Optional[torch.Tensor] = None,
-                   stats: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """The lazy coverage decision of CVSABackend._lazy_step taken on the device
-    (cvsa/backend.py:420-465): when every head of ``check_accept`` (the
-    coverage gate of the cached selection) passed, the cached selection in
-    ``page_indices`` / ``n_per_head`` stays and every head is accepted;
-    otherwise the top-``budget`` selection of ``page_scores`` replaces it in
-    place, ``coverage`` receives its coverage and ``scores_cache`` a copy of
-    ``page_scores``.  ``stats`` (int64[4]) accumulates accept-all checks,
-    rejections, scoring steps and heads that passed.  Returns the accept
-    mask [B, H_kv] bool of the heads for this step.
+                   stats: Optional[torch.Tensor] = None,
+                   count_gate: bool = False) -> torch.Tensor:
+    """The selection decisions of CVSABackend taken on the device.
+
+    With ``check_accept`` (the coverage gate of the cached selection) this is
+    the lazy check of _lazy_step (cvsa/backend.py:420-465): when every head
+    passed, the cached selection in ``page_indices`` / ``n_per_head`` stays
+    and every head is accepted; otherwise the top-``budget`` selection of
+    ``page_scores`` replaces it in place, ``coverage`` receives its coverage
+    and ``scores_cache`` a copy of ``page_scores``.  Without it, a fresh
+    selection is written.  ``stats`` (int64[6], slots 4-5 scratch)
+    accumulates accept-all checks, rejections, scoring steps and heads that
+    passed; with ``count_gate`` a fresh selection is booked as a
+    fixed-interval scoring step by its own gate (backend.py:859-863).
+    Returns the accept mask [B, H_kv] bool of the heads for this step.
     """
     dev = _device_of(page_scores, check_accept, page_indices, n_per_head, coverage)
     if page_scores.dtype != torch.float32 or page_scores.dim() != 3:
@@ -212,25 +217,30 @@ def select_or_keep(page_scores: torch.Tensor, check_accept: torch.Tensor, budget
     B, H_kv, W = ps.shape
     if not 1 <= budget <= W:
         raise ValueError(f"select_or_keep: budget {budget} must be in [1, {W}]")
-    for name, t, shape, dt in (("page_indices", page_indices, (B, H_kv, budget), torch.int32),
-                               ("n_per_head", n_per_head, (B, H_kv), torch.int32),
-                               ("coverage", coverage, (B, H_kv), torch.float32),
-                               ("check_accept", check_accept, (B, H_kv), torch.bool)):
+    checks = [("page_indices", page_indices, (B, H_kv, budget), torch.int32),
+              ("n_per_head", n_per_head, (B, H_kv), torch.int32),
+              ("coverage", coverage, (B, H_kv), torch.float32)]
+    if check_accept is not None:
+        checks.append(("check_accept", check_accept, (B, H_kv), torch.bool))
+    for name, t, shape, dt in checks:
         if tuple(t.shape) != shape or t.dtype != dt or not t.is_contiguous():
             raise ValueError(f"select_or_keep: {name} must be a contiguous {dt} {shape}")
     if scores_cache is not None and (scores_cache.shape != ps.shape or not
                                      scores_cache.is_contiguous() or
                                      scores_cache.dtype != torch.float32):
         raise ValueError("select_or_keep: scores_cache must be a contiguous float32 [B, H_kv, W]")
-    if stats is not None and (stats.dtype != torch.int64 or stats.numel() < 4 or
+    if stats is not None and (stats.dtype != torch.int64 or stats.numel() < 6 or
                               not stats.is_contiguous()):
-        raise ValueError("select_or_keep: stats must be a contiguous int64 tensor of >= 4")
+        raise ValueError("select_or_keep: stats must be a contiguous int64 tensor of >= 6")
+    if count_gate and (check_accept is not None or stats is None):
+        raise ValueError("select_or_keep: count_gate books a fresh selection into stats")
     ctx = _i32(context_lens)
     acc = torch.empty(B, H_kv, device=dev, dtype=torch.uint8)
     check(_lib.load().cvsa_select_or_keep(
-        ps.data_ptr(), check_accept.data_ptr(), B, H_kv, W, ctx.data_ptr(), block_size, budget,
+        ps.data_ptr(), _ptr(check_accept), B, H_kv, W, ctx.data_ptr(), block_size, budget,
         page_indices.data_ptr(), n_per_head.data_ptr(), float(tau), acc.data_ptr(),
-        coverage.data_ptr(), _ptr(scores_cache), _ptr(stats), _stream(dev)), "select_or_keep")
+        coverage.data_ptr(), _ptr(scores_cache), _ptr(stats), 1 if count_gate else 0,
+        _stream(dev)), "select_or_keep")
     return acc.view(torch.bool)
 
 

@@ -38,7 +38,7 @@ SIGNATURES = {
     "cvsa_select_topk": (ctypes.c_int, [
         _p, _i32, _i32, _i32, _p, _i32, _i32, _p, _p, _f32, _p, _p, _p]),
     "cvsa_select_or_keep": (ctypes.c_int, [
-        _p, _p, _i32, _i32, _i32, _p, _i32, _i32, _p, _p, _f32, _p, _p, _p, _p, _p]),
+        _p, _p, _i32, _i32, _i32, _p, _i32, _i32, _p, _p, _f32, _p, _p, _p, _p, _i32, _p]),
     "cvsa_check_coverage": (ctypes.c_int, [
         _p, _i32, _i32, _i32, _p, _i64, _p, _f32, _p, _p, _p]),
     "cvsa_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),

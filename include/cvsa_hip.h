@@ -92,9 +92,16 @@ int cvsa_select_topk(const float *page_scores, int32_t B, int32_t H_kv,
  *   otherwise        -> as cvsa_select_topk with the fused gate, writing
  *     the new selection over page_indices / n_per_head in place, and
  *     scores_cache (optional, [B,H_kv,W]) receives a copy of page_scores.
- *   stats (optional, int64[4], accumulated): [0] += all passed,
- *     [1] += some head failed, [2] += scoring steps run (same as [1]),
- *     [3] += number of heads that passed.
+ *   stats (optional, int64[6], accumulated; [4], [5] are scratch that must
+ *     start at zero and are left at zero): [0] += all passed, [1] += some
+ *     head failed, [2] += scoring steps run (same as [1]), [3] += number
+ *     of heads that passed.
+ *   check_accept == NULL: a fresh selection (no cached one).  With
+ *     count_gate == 0 the stats book a lazy scoring step without a cached
+ *     selection ([1] += 1, [2] += 1); with count_gate != 0 they book a
+ *     fixed-interval scoring step by the new selection's gate
+ *     (backend.py:859-863: [2] += 1, [3] += heads accepted, [0] or [1] += 1
+ *     by whether every head accepted).
  */
 int cvsa_select_or_keep(const float *page_scores, const uint8_t *check_accept,
                         int32_t B, int32_t H_kv, int32_t W,
@@ -102,7 +109,7 @@ int cvsa_select_or_keep(const float *page_scores, const uint8_t *check_accept,
                         int32_t budget, int32_t *page_indices,
                         int32_t *n_per_head, float tau, uint8_t *accept_out,
                         float *coverage_out, float *scores_cache,
-                        int64_t *stats, void *stream);
+                        int64_t *stats, int32_t count_gate, void *stream);
 
 /*
  * Coverage gate.  Replaces triton_check_coverage

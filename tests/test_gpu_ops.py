@@ -101,7 +101,7 @@ def test_select_or_keep(gpu, W, budget):
     nv = ref.n_valid_pages(ctx, 16)
     new_ps[1, :, int(nv[1]):] = float("-inf")
     sel0, nph0 = ref.select_topk(old_ps, budget, ctx, 16)
-    stats = torch.zeros(4, dtype=torch.int64, device=gpu)
+    stats = torch.zeros(6, dtype=torch.int64, device=gpu)
     d_sel, d_nph = sel0.to(gpu), nph0.to(gpu)
     d_cache = old_ps.to(gpu)
     cov = torch.full((B, H), -7.0, device=gpu)
@@ -112,7 +112,7 @@ def test_select_or_keep(gpu, W, budget):
     assert bool(acc.all())
     assert torch.equal(d_sel.cpu(), sel0) and torch.equal(d_nph.cpu(), nph0)
     assert torch.equal(d_cache.cpu(), old_ps) and bool((cov == -7.0).all())
-    assert stats.tolist() == [1, 0, 0, B * H]
+    assert stats.tolist() == [1, 0, 0, B * H, 0, 0]
     # 2) one head failed: fresh top-k + gate for every head, scores cached
     check[1, 3] = False
     acc = ops.select_or_keep(new_ps.to(gpu), check, budget, ctx.to(gpu), 16, 0.9, d_sel, d_nph,
@@ -124,7 +124,17 @@ def test_select_or_keep(gpu, W, budget):
     assert (cov.cpu() - wcov).abs().max().item() < COV_ATOL
     margin = (wcov - 0.9).abs() > 1e-5
     assert torch.equal(acc.cpu()[margin], wacc[margin])
-    assert stats.tolist() == [1, 1, 1, 2 * B * H - 1]
+    assert stats.tolist() == [1, 1, 1, 2 * B * H - 1, 0, 0]
+    # 3) a fresh selection booked by its own gate (fixed-interval schedule)
+    sel3 = torch.empty_like(d_sel)
+    nph3 = torch.empty_like(d_nph)
+    cov3 = torch.empty_like(cov)
+    acc3 = ops.select_or_keep(new_ps.to(gpu), None, budget, ctx.to(gpu), 16, 0.9, sel3, nph3,
+                              cov3, None, stats, count_gate=True)
+    assert torch.equal(sel3.cpu(), widx) and torch.equal(acc3, acc)
+    n_acc = int(acc3.sum())
+    all_acc = int(n_acc == B * H)
+    assert stats.tolist() == [1 + all_acc, 2 - all_acc, 2, 2 * B * H - 1 + n_acc, 0, 0]
 
 
 @pytest.mark.parametrize("k,W", [(128, 512), (1000, 2048), (5, 9)])
