@@ -188,27 +188,319 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const float 
   if (threadIdx.x == 0 && a.work != nullptr) add_work(a, n, ctx);
 }
 
+// ---------------------------------------------------------------- engines
+// A page engine owns one wave's softmax state for the G query heads of a KV
+// head and applies pages to it.  Page = the K and V rows of one page held in
+// registers (fetched PD pages ahead); consume() applies one page; finish()
+// leaves the wave's (o, m, l) in LDS.
+
+// VALU engine: lane l holds d-segment (l % LPT) of token slot (l / LPT);
+// q.K uses packed bf16 dot products with an LPT-lane DPP reduction, P.V is
+// fp32 FMA.  Lane vector v covers elements v*LPT*8 + seg*8 .. +8, so each
+// load instruction reads whole 128-byte lines of every row it touches.
+template <int G, int LPT>
+struct ValuEngine {
+  static constexpr int E = kHeadDim / LPT;      // d-elements per lane
+  static constexpr int NV = E / 8;              // 16-byte vectors per lane per row
+  static constexpr int VSTRIDE = LPT * 8;       // elements between a lane's vectors
+  static constexpr int TPP = kWave / LPT;       // token slots per pass
+  static constexpr int NPASS = kPageTokens / TPP;
+  static_assert(NPASS >= 1 && NV >= 1, "bad lane layout");
+  struct Page {
+    uint4 k[NPASS][NV], v[NPASS][NV];
+  };
+  struct Lds {};
+
+  float m[G], l[G], o[G][E];
+  uint4 qv[G][NV];
+  int tg, seg;
+  int64_t lane_off, row_stride;
+  float scale;
+
+  __device__ __forceinline__ void init(const DecodeArgs &a, int b, int h, int lane, Lds &) {
+    tg = lane / LPT;
+    seg = lane % LPT;
+    scale = a.scale;
+    row_stride = (int64_t)a.H_kv * kHeadDim;
+    lane_off = (int64_t)h * kHeadDim + seg * 8 + (int64_t)tg * row_stride;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = -INFINITY;
+      l[g] = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[g][e] = 0.f;
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        qv[g][v] = *reinterpret_cast<const uint4 *>(
+            a.q + b * a.q_sb + (int64_t)(h * G + g) * a.q_sh + v * VSTRIDE + seg * 8);
+    }
+  }
+
+  __device__ __forceinline__ void fetch(const uint16_t *kp, const uint16_t *vp, Page &pg) const {
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int64_t off = lane_off + (int64_t)(ps * TPP) * row_stride;
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        pg.k[ps][v] = *reinterpret_cast<const uint4 *>(kp + off + v * VSTRIDE);
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        pg.v[ps][v] = *reinterpret_cast<const uint4 *>(vp + off + v * VSTRIDE);
+    }
+  }
+
+  __device__ __forceinline__ void consume(Page &pg, int ntok, Lds &) {
+    float s[NPASS][G];
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const bool valid = ps * TPP + tg < ntok;
+      // Tokens past the context contribute nothing, whatever their V rows
+      // hold (the reference masks those loads); zeroed in place.
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        if (!valid) pg.v[ps][v] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float acc = 0.f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) acc = dot8_bf16(pg.k[ps][v], qv[g][v], acc);
+        acc = group_sum<LPT>(acc) * scale;
+        s[ps][g] = valid ? acc : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float pm = s[0][g];
+#pragma unroll
+      for (int ps = 1; ps < NPASS; ++ps) pm = fmaxf(pm, s[ps][g]);
+      pm = wave_max_from_groups<LPT>(pm);
+      if (pm > m[g]) {  // wave-uniform
+        const float alpha = fast_exp(m[g] - pm);
+        l[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[g][e] *= alpha;
+        m[g] = pm;
+      }
+#pragma unroll
+      for (int ps = 0; ps < NPASS; ++ps) {
+        const bool valid = s[ps][g] != -INFINITY;
+        const float p = valid ? fast_exp(s[ps][g] - m[g]) : 0.f;
+        l[g] += p;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          const uint4 w = pg.v[ps][v];
+          o[g][v * 8 + 0] += p * bf16_lo(w.x);
+          o[g][v * 8 + 1] += p * bf16_hi(w.x);
+          o[g][v * 8 + 2] += p * bf16_lo(w.y);
+          o[g][v * 8 + 3] += p * bf16_hi(w.y);
+          o[g][v * 8 + 4] += p * bf16_lo(w.z);
+          o[g][v * 8 + 5] += p * bf16_hi(w.z);
+          o[g][v * 8 + 6] += p * bf16_lo(w.w);
+          o[g][v * 8 + 7] += p * bf16_hi(w.w);
+        }
+      }
+    }
+  }
+
+  template <int NW>
+  __device__ __forceinline__ void finish(int wave, int lane, float (*s_o)[G][kHeadDim],
+                                         float (*s_m)[G], float (*s_l)[G]) {
+    // Sum the token slots of the wave (lanes that share a d-segment).
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      l[g] = sum_across_groups<LPT>(l[g]);
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[g][e] = sum_across_groups<LPT>(o[g][e]);
+    }
+    if (tg == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s_o[wave][g][v * VSTRIDE + seg * 8 + e] = o[g][v * 8 + e];
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = l[g];
+      }
+    }
+  }
+};
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+// MFMA engine: the G query heads (padded to 16) of a KV head against a page
+// of 16 tokens are two small dense tiles for the matrix cores.
+//   S = K Q^T: v_mfma_f32_16x16x32_bf16, four d-chunks of 32.  A operand =
+//     K rows (lane l: token l%16, d 32kk + 8(l/16) .. +8, one 16-byte load),
+//     B operand = Q^T (loaded once), result lane l: head l%16, tokens
+//     4(l/16) .. +4.
+//   O += P V: v_mfma_f32_16x16x16_bf16, eight 16-column blocks of d.  The S
+//     result layout is exactly the A operand layout of P (head l%16, tokens
+//     4(l/16) .. +4), so P needs no data movement; it is split into a bf16
+//     high part and a bf16 remainder (two MFMAs) to keep ~16 mantissa bits.
+//     The B operand wants 4 tokens of one d column per lane: the V page goes
+//     through a wave-private LDS tile (rows padded to 272 bytes so the four
+//     lane groups read disjoint banks).  Result lane l: heads 4(l/16) .. +4,
+//     d column 16 blk + l%16.
+// Softmax state: m and the running l of head l%16 live in the four lanes of
+// that head; a rescale of O rows goes through LDS (16 factors per wave).
+template <int G>
+struct MfmaEngine {
+  static_assert(G <= 16, "GQA group larger than the MFMA tile");
+  static constexpr int kVRow = kHeadDim + 8;  // LDS row of the V tile, in bf16
+  struct Page {
+    uint4 k[4], v[4];
+  };
+  struct Lds {
+    uint16_t v[kPageTokens * kVRow];
+    float alpha[16];
+  };
+
+  float4_t o[8];
+  bf16x8_t qb[4];
+  float m_g, l_g;
+  int lane;
+  int64_t koff, voff, row_stride;
+  float scale;
+
+  __device__ __forceinline__ void init(const DecodeArgs &a, int b, int h, int lane_, Lds &) {
+    lane = lane_;
+    scale = a.scale;
+    row_stride = (int64_t)a.H_kv * kHeadDim;
+    const int c16 = lane & 15, grp = lane >> 4;
+    koff = (int64_t)h * kHeadDim + c16 * row_stride + 8 * grp;
+    voff = (int64_t)h * kHeadDim + grp * row_stride + 8 * c16;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      uint4 w = make_uint4(0u, 0u, 0u, 0u);
+      if (c16 < G)
+        w = *reinterpret_cast<const uint4 *>(a.q + b * a.q_sb + (int64_t)(h * G + c16) * a.q_sh +
+                                             32 * kk + 8 * grp);
+      qb[kk] = __builtin_bit_cast(bf16x8_t, w);
+    }
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) o[blk] = float4_t{0.f, 0.f, 0.f, 0.f};
+    m_g = -INFINITY;
+    l_g = 0.f;
+  }
+
+  __device__ __forceinline__ void fetch(const uint16_t *kp, const uint16_t *vp, Page &pg) const {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      pg.k[kk] = *reinterpret_cast<const uint4 *>(kp + koff + 32 * kk);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      pg.v[i] = *reinterpret_cast<const uint4 *>(vp + voff + 4 * i * row_stride);
+  }
+
+  __device__ __forceinline__ void consume(Page &pg, int ntok, Lds &lds) {
+    const int c16 = lane & 15, grp = lane >> 4;
+    const int t0 = 4 * grp;
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pg.k[kk]),
+                                                    qb[kk], acc, 0, 0, 0);
+    float sv[4];
+    float pm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sv[j] = t0 + j < ntok ? acc[j] * scale : -INFINITY;
+      pm = fmaxf(pm, sv[j]);
+    }
+    float x, y;
+    xchg16(pm, x, y);
+    pm = fmaxf(x, y);
+    xchg32(pm, x, y);
+    pm = fmaxf(x, y);  // page max of head c16, in all four of its lanes
+    const float m_new = fmaxf(m_g, pm);
+    if (__ballot(m_new > m_g) != 0) {  // some head of the wave rescales
+      const float alpha = m_new > m_g ? (m_g == -INFINITY ? 0.f : fast_exp(m_g - m_new)) : 1.f;
+      l_g *= alpha;
+      m_g = m_new;
+      if (lane < 16) lds.alpha[lane] = alpha;
+      const float4 ar = *reinterpret_cast<const float4 *>(&lds.alpha[t0]);  // rows 4grp .. +4
+#pragma unroll
+      for (int blk = 0; blk < 8; ++blk) {
+        o[blk][0] *= ar.x;
+        o[blk][1] *= ar.y;
+        o[blk][2] *= ar.z;
+        o[blk][3] *= ar.w;
+      }
+    }
+    // P (head c16, tokens t0 .. t0+3) as bf16 high part + bf16 remainder.
+    short4_t ph, pl;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = sv[j] == -INFINITY ? 0.f : fast_exp(sv[j] - m_g);
+      l_g += p;
+      const uint32_t hi = f32_to_bf16_bits(p);
+      const float rem = p - __uint_as_float(hi << 16);
+      ph[j] = (short)hi;
+      pl[j] = (short)f32_to_bf16_bits(rem);
+    }
+    // V page -> LDS tile (rows past the context are stored as zeros: the
+    // reference never reads them).
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 4 * i + grp;
+      const uint4 w = t < ntok ? pg.v[i] : make_uint4(0u, 0u, 0u, 0u);
+      *reinterpret_cast<uint4 *>(&lds.v[t * kVRow + 8 * c16]) = w;
+    }
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk) {
+      short4_t vb;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vb[j] = (short)lds.v[(t0 + j) * kVRow + 16 * blk + c16];
+      o[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, vb, o[blk], 0, 0, 0);
+      o[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, vb, o[blk], 0, 0, 0);
+    }
+  }
+
+  template <int NW>
+  __device__ __forceinline__ void finish(int wave, int lane_, float (*s_o)[G][kHeadDim],
+                                         float (*s_m)[G], float (*s_l)[G]) {
+    const int c16 = lane & 15, grp = lane >> 4;
+    float x, y;
+    xchg16(l_g, x, y);
+    l_g = x + y;
+    xchg32(l_g, x, y);
+    l_g = x + y;  // head c16's l over all 16 token rows
+    if (lane < G) {
+      s_m[wave][lane] = m_g;
+      s_l[wave][lane] = l_g;
+    }
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int g = 4 * grp + j;
+        if (g < G) s_o[wave][g][16 * blk + c16] = o[blk][j];
+      }
+  }
+};
+
 // NW waves per workgroup, PD pages of K/V in flight per wave.
-template <int G, int LPT, int NW, int PD, int MODE>
+template <int G, class Engine, int NW, int PD, int MODE>
 __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeArgs a) {
   constexpr int NT = NW * kWave;         // threads per workgroup
-  constexpr int E = kHeadDim / LPT;      // d-elements per lane
-  constexpr int NV = E / 8;              // 16-byte vectors per lane per row
-  constexpr int VSTRIDE = LPT * 8;       // elements between a lane's vectors
-  constexpr int TPP = kWave / LPT;       // token slots per pass
-  constexpr int NPASS = kPageTokens / TPP;
-  static_assert(NPASS >= 1 && NV >= 1, "bad lane layout");
+  using Page = typename Engine::Page;
 
   __shared__ float s_o[NW][G][kHeadDim];
   __shared__ float s_m[NW][G];
   __shared__ float s_l[NW][G];
   __shared__ int s_last;
   __shared__ float s_pm[G][kMaxSplits], s_pl[G][kMaxSplits];
+  __shared__ __attribute__((aligned(16))) typename Engine::Lds s_eng[NW];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tg = lane / LPT;
-  const int seg = lane % LPT;
   const int bh = blockIdx.y;
   const int split = blockIdx.x;
   const int b = bh / a.H_kv;
@@ -241,75 +533,10 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeAr
   const int r1 = min(n, r0 + pps);
 
   if (r0 < r1) {
-    float m[G], l[G], o[G][E];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      m[g] = -INFINITY;
-      l[g] = 0.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) o[g][e] = 0.f;
-    }
-    // Lane vector v covers elements v*VSTRIDE + seg*8 .. +8, so each load
-    // instruction reads whole 128-byte lines of every row it touches.
-    uint4 qv[G][NV];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int v = 0; v < NV; ++v)
-        qv[g][v] = *reinterpret_cast<const uint4 *>(
-            a.q + b * a.q_sb + (int64_t)(h * G + g) * a.q_sh + v * VSTRIDE + seg * 8);
-
-    const int64_t row_stride = (int64_t)a.H_kv * kHeadDim;          // between tokens
-    const int64_t page_elems = (int64_t)kPageTokens * row_stride;   // between blocks
-    const int64_t lane_off = (int64_t)h * kHeadDim + seg * 8 + (int64_t)tg * row_stride;
+    Engine eng;
+    eng.init(a, b, h, lane, s_eng[wave]);
+    const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * kHeadDim;  // between blocks
     const int32_t *idx_row = listed ? a.page_idx + (int64_t)bh * a.idx_stride : nullptr;
-
-    auto consume = [&](const uint4 (&kr)[NPASS][NV], const uint4 (&vr)[NPASS][NV], int ntok) {
-      float s[NPASS][G];
-#pragma unroll
-      for (int ps = 0; ps < NPASS; ++ps) {
-        const bool valid = ps * TPP + tg < ntok;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float acc = 0.f;
-#pragma unroll
-          for (int v = 0; v < NV; ++v) acc = dot8_bf16(kr[ps][v], qv[g][v], acc);
-          acc = group_sum<LPT>(acc) * a.scale;
-          s[ps][g] = valid ? acc : -INFINITY;
-        }
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float pm = s[0][g];
-#pragma unroll
-        for (int ps = 1; ps < NPASS; ++ps) pm = fmaxf(pm, s[ps][g]);
-        pm = wave_max_from_groups<LPT>(pm);
-        if (pm > m[g]) {  // wave-uniform
-          const float alpha = fast_exp(m[g] - pm);
-          l[g] *= alpha;
-#pragma unroll
-          for (int e = 0; e < E; ++e) o[g][e] *= alpha;
-          m[g] = pm;
-        }
-#pragma unroll
-        for (int ps = 0; ps < NPASS; ++ps) {
-          const float p = s[ps][g] == -INFINITY ? 0.f : fast_exp(s[ps][g] - m[g]);
-          l[g] += p;
-#pragma unroll
-          for (int v = 0; v < NV; ++v) {
-            const uint4 w = vr[ps][v];
-            o[g][v * 8 + 0] += p * bf16_lo(w.x);
-            o[g][v * 8 + 1] += p * bf16_hi(w.x);
-            o[g][v * 8 + 2] += p * bf16_lo(w.y);
-            o[g][v * 8 + 3] += p * bf16_hi(w.y);
-            o[g][v * 8 + 4] += p * bf16_lo(w.z);
-            o[g][v * 8 + 5] += p * bf16_hi(w.z);
-            o[g][v * 8 + 6] += p * bf16_lo(w.w);
-            o[g][v * 8 + 7] += p * bf16_hi(w.w);
-          }
-        }
-      }
-    };
 
     // This wave's pages are r0 + wave + NW*j.  Lane j looks up page j's block
     // id and valid-token count up front; the page loop reads them with
@@ -336,22 +563,12 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeAr
       // the page being consumed: a page without valid tokens reads block 0
       // (in bounds) and is masked out by consume(); prefetches past the end
       // re-read the wave's last page (already cached) and are never consumed.
-      auto fetch = [&](int j, uint4 (&kr)[NPASS][NV], uint4 (&vr)[NPASS][NV]) {
-        const int phys = __builtin_amdgcn_readlane(my_phys, j);
-        const int64_t base = (int64_t)phys * page_elems + lane_off;
-#pragma unroll
-        for (int ps = 0; ps < NPASS; ++ps) {
-          const int64_t off = base + (int64_t)(ps * TPP) * row_stride;
-#pragma unroll
-          for (int v = 0; v < NV; ++v)
-            kr[ps][v] = *reinterpret_cast<const uint4 *>(a.k_cache + off + v * VSTRIDE);
-#pragma unroll
-          for (int v = 0; v < NV; ++v)
-            vr[ps][v] = *reinterpret_cast<const uint4 *>(a.v_cache + off + v * VSTRIDE);
-        }
+      auto fetch = [&](int j, Page &pg) {
+        const int64_t base = (int64_t)__builtin_amdgcn_readlane(my_phys, j) * page_elems;
+        eng.fetch(a.k_cache + base, a.v_cache + base, pg);
         return __builtin_amdgcn_readlane(my_ntok, j);
       };
-      uint4 kb[PD][NPASS][NV], vb[PD][NPASS][NV];
+      Page pb[PD];
       int nt[PD];
       // No separate prologue: the first trip fetches pages 0..PD-1 and
       // consumes only page 0, so every fetch of a slot uses the same
@@ -360,34 +577,12 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeAr
 #pragma unroll
         for (int u = 0; u < PD; ++u) {
           const int slot = (u + PD - 1) % PD;  // slot of page j+u+PD-1
-          nt[slot] = fetch(min(j + u + PD - 1, cn - 1), kb[slot], vb[slot]);
-          if (j + u >= 0 && j + u < cn) consume(kb[u], vb[u], nt[u]);
+          nt[slot] = fetch(min(j + u + PD - 1, cn - 1), pb[slot]);
+          if (j + u >= 0 && j + u < cn) eng.consume(pb[u], nt[u], s_eng[wave]);
         }
       }
     }
-
-    // Sum the token slots of the wave (lanes that share a d-segment).
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      l[g] = sum_across_groups<LPT>(l[g]);
-#pragma unroll
-      for (int e = 0; e < E; ++e) o[g][e] = sum_across_groups<LPT>(o[g][e]);
-    }
-    if (tg == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int v = 0; v < NV; ++v)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) s_o[wave][g][v * VSTRIDE + seg * 8 + e] = o[g][v * 8 + e];
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        s_m[wave][g] = m[g];
-        s_l[wave][g] = l[g];
-      }
-    }
+    eng.template finish<NW>(wave, lane, s_o, s_m, s_l);
   }
   __syncthreads();
 
@@ -479,6 +674,13 @@ static int env_int(const char *name, int dflt) {
   const char *e = getenv(name);
   const int x = e ? atoi(e) : 0;
   return x > 0 ? x : dflt;
+}
+
+// Page engine: 1 = matrix cores (MfmaEngine), 0 = VALU (ValuEngine);
+// CVSA_DECODE_ENGINE overrides the default (read once).
+static int decode_engine() {
+  static const int v = getenv("CVSA_DECODE_ENGINE") ? atoi(getenv("CVSA_DECODE_ENGINE")) : 1;
+  return v;
 }
 
 // Workgroups per launch (tuning knob CVSA_DECODE_TARGET_WGS, read once).
@@ -595,10 +797,16 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
                                                  counter_bytes(B * H_kv));
   const dim3 grid(p.n_splits, B * H_kv);
   const int mode = !listed ? kModeAll : (all_pages ? kModeVerified : kModeListed);
+  const bool use_mfma = decode_engine() == 1;
 #define CVSA_DEC_LAUNCH(GG, MM)                                                              \
   do {                                                                                       \
-    hipLaunchKernelGGL((paged_decode_kernel<GG, LanesPerRow<GG>::value, 4, 2, MM>), grid,    \
-                       dim3(4 * kWave), 0, st, a);                                           \
+    if (use_mfma)                                                                            \
+      hipLaunchKernelGGL((paged_decode_kernel<GG, MfmaEngine<GG>, 4, 2, MM>), grid,          \
+                         dim3(4 * kWave), 0, st, a);                                         \
+    else                                                                                     \
+      hipLaunchKernelGGL(                                                                    \
+          (paged_decode_kernel<GG, ValuEngine<GG, LanesPerRow<GG>::value>, 4, 2, MM>), grid,  \
+          dim3(4 * kWave), 0, st, a);                                                        \
   } while (0)
 #define CVSA_DEC_CASE(GG)                                                                    \
   case GG:                                                                                   \
