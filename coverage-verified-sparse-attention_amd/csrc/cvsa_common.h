@@ -42,6 +42,14 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
                                          false);
 }
 
+// 16-byte load of data read once per launch (K/V pages): the nontemporal hint
+// keeps it from displacing reusable lines in the caches.
+__device__ __forceinline__ uint4 stream_load16(const uint16_t *p) {
+  typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
+  const v4u_t v = __builtin_nontemporal_load(reinterpret_cast<const v4u_t *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Sum of the 8 products of two 16-byte bf16 vectors, accumulated onto acc.
 __device__ __forceinline__ float dot8_bf16(const uint4 &a, const uint4 &b, float acc) {
   acc = dot2_bf16(a.x, b.x, acc);

@@ -40,7 +40,7 @@ namespace cvsa {
 
 constexpr int kPartStride = kHeadDim + 2;  // o[D], m, l
 constexpr int kMaxSplits = 32;             // partials per head
-constexpr int kMinPagesPerSplit = 8;       // at least one page per wave
+constexpr int kMinPagesPerWave = 2;        // pages per wave of a split, at least
 
 struct DecodeArgs {
   const uint16_t *q;
@@ -242,10 +242,10 @@ struct ValuEngine {
       const int64_t off = lane_off + (int64_t)(ps * TPP) * row_stride;
 #pragma unroll
       for (int v = 0; v < NV; ++v)
-        pg.k[ps][v] = *reinterpret_cast<const uint4 *>(kp + off + v * VSTRIDE);
+        pg.k[ps][v] = stream_load16(kp + off + v * VSTRIDE);
 #pragma unroll
       for (int v = 0; v < NV; ++v)
-        pg.v[ps][v] = *reinterpret_cast<const uint4 *>(vp + off + v * VSTRIDE);
+        pg.v[ps][v] = stream_load16(vp + off + v * VSTRIDE);
     }
   }
 
@@ -393,10 +393,10 @@ struct MfmaEngine {
   __device__ __forceinline__ void fetch(const uint16_t *kp, const uint16_t *vp, Page &pg) const {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      pg.k[kk] = *reinterpret_cast<const uint4 *>(kp + koff + 32 * kk);
+      pg.k[kk] = stream_load16(kp + koff + 32 * kk);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      pg.v[i] = *reinterpret_cast<const uint4 *>(vp + voff + 4 * i * row_stride);
+      pg.v[i] = stream_load16(vp + voff + 4 * i * row_stride);
   }
 
   __device__ __forceinline__ void consume(Page &pg, int ntok, Lds &lds) {
@@ -696,13 +696,15 @@ static DecodePlan plan_decode(int B, int H_kv, int max_sel, int W, bool listed,
                               bool all_pages) {
   const int heads = B * H_kv;
   const int target = target_workgroups();
+  const int waves = kWavesPerWg;
+  const int min_pps = kMinPagesPerWave * waves;
   int wg_per_head = heads >= target ? 1 : target / heads;
   if (wg_per_head > kMaxSplits) wg_per_head = kMaxSplits;
   auto pps_for = [&](int pages) {
     int pps = (pages + wg_per_head - 1) / wg_per_head;
-    if (pps < kMinPagesPerSplit) pps = kMinPagesPerSplit;
-    pps = (pps + kWavesPerWg - 1) / kWavesPerWg * kWavesPerWg;
-    while ((pages + pps - 1) / pps > kMaxSplits) pps += kWavesPerWg;
+    if (pps < min_pps) pps = min_pps;
+    pps = (pps + waves - 1) / waves * waves;
+    while ((pages + pps - 1) / pps > kMaxSplits) pps += waves;
     return pps;
   };
   DecodePlan p;
@@ -801,12 +803,12 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
 #define CVSA_DEC_LAUNCH(GG, MM)                                                              \
   do {                                                                                       \
     if (use_mfma)                                                                            \
-      hipLaunchKernelGGL((paged_decode_kernel<GG, MfmaEngine<GG>, 4, 2, MM>), grid,          \
-                         dim3(4 * kWave), 0, st, a);                                         \
+      hipLaunchKernelGGL((paged_decode_kernel<GG, MfmaEngine<GG>, kWavesPerWg, 2, MM>),      \
+                         grid, dim3(kWavesPerWg * kWave), 0, st, a);                         \
     else                                                                                     \
-      hipLaunchKernelGGL(                                                                    \
-          (paged_decode_kernel<GG, ValuEngine<GG, LanesPerRow<GG>::value>, 4, 2, MM>), grid,  \
-          dim3(4 * kWave), 0, st, a);                                                        \
+      hipLaunchKernelGGL((paged_decode_kernel<GG, ValuEngine<GG, LanesPerRow<GG>::value>,    \
+                                              kWavesPerWg, 2, MM>),                          \
+                         grid, dim3(kWavesPerWg * kWave), 0, st, a);                         \
   } while (0)
 #define CVSA_DEC_CASE(GG)                                                                    \
   case GG:                                                                                   \

@@ -85,10 +85,9 @@ __global__ __launch_bounds__(256) void score_pages_quad_kernel(
   // prefetch free of branches.
   auto fetch = [&](int j, uint4 (&kv)[kPageTokens]) {
     const int phys = max(__builtin_amdgcn_readlane(my_phys, j), 0);
-    const uint4 *src = reinterpret_cast<const uint4 *>(k_cache + (int64_t)phys * page_elems +
-                                                       lane_off);
+    const uint16_t *src = k_cache + (int64_t)phys * page_elems + lane_off;
 #pragma unroll
-    for (int t = 0; t < kPageTokens; ++t) kv[t] = src[t * (row_stride / 8)];
+    for (int t = 0; t < kPageTokens; ++t) kv[t] = stream_load16(src + t * row_stride);
   };
   auto consume = [&](int j, const uint4 (&kv)[kPageTokens]) {
     const int p = p_begin + j;
@@ -146,11 +145,10 @@ __global__ __launch_bounds__(256) void score_pages_kernel(
       if (seg == 0 && rsub < HKV) dst[(int64_t)h * W] = -INFINITY;
       continue;
     }
-    const uint4 *src =
-        reinterpret_cast<const uint4 *>(k_cache + (int64_t)phys * PAGE_ELEMS) + lane;
+    const uint16_t *src = k_cache + (int64_t)phys * PAGE_ELEMS + lane * 8;
     uint4 kv[NLOAD];
 #pragma unroll
-    for (int i = 0; i < NLOAD; ++i) kv[i] = src[i * 64];
+    for (int i = 0; i < NLOAD; ++i) kv[i] = stream_load16(src + i * 64 * 8);
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < NLOAD; ++i) {
