@@ -59,6 +59,15 @@ __device__ __forceinline__ float dot8_bf16(const uint4 &a, const uint4 &b, float
   return acc;
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// waits for every outstanding global load of the wave; with this one, loads
+// issued before the barrier stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // exp(x) through the hardware base-2 exponential.
 __device__ __forceinline__ float fast_exp(float x) { return exp2f(x * 1.4426950408889634f); }
 

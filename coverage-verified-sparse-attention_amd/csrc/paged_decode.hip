@@ -38,9 +38,12 @@
 
 namespace cvsa {
 
-constexpr int kPartStride = kHeadDim + 2;  // o[D], m, l
-constexpr int kMaxSplits = 32;             // partials per head
+// Split partials are rows of kPartStride floats: o[D], m, l and two pad
+// words, so every row starts on a 16-byte boundary.
+constexpr int kPartStride = kHeadDim + 4;
+constexpr int kMaxSplits = 256;            // partials per head (and workgroups per launch)
 constexpr int kMinPagesPerWave = 2;        // pages per wave of a split, at least
+constexpr int kChunksPerRow = kHeadDim / 4;  // float4 chunks of one q-head's o
 
 struct DecodeArgs {
   const uint16_t *q;
@@ -57,12 +60,14 @@ struct DecodeArgs {
   const int32_t *n_pages;
   const uint8_t *accept;  // non-NULL: verified mode
   int H_kv, W;
+  int heads;  // B * H_kv
+  int pps, n_splits;  // listed kernel: pages per split, splits per head
   float scale;
-  int pps_sel, pps_all, n_splits;
   float *o_unnorm, *m_out, *l_out;
   void *out;
   int out_dtype;
-  float *part;
+  float *part;               // split partials (see PartBuf)
+  uint32_t part_bytes;
   unsigned *counters;        // per head, zero between launches
   unsigned long long *work;  // optional effective-budget counters
 };
@@ -97,95 +102,188 @@ __device__ __forceinline__ void add_work(const DecodeArgs &a, int n, int ctx) {
 }
 
 
-// Page walk of one head.  MODE is a template parameter so that verified mode
-// loads accept[bh] and n_per_head[bh] unconditionally and picks (n, pages
-// per split) with selects: an earlier form that branched on null pointers
-// was miscompiled (a live scalar register was reused across the branch).
+// Pages walked by head bh: its listed pages (page_indices[bh, :n_per_head]),
+// or every valid page (dense heads, rejected heads of a verified launch).
+// MODE is a template parameter and verified mode loads accept[bh] and
+// n_per_head[bh] unconditionally and picks with selects: an earlier form
+// that branched on null pointers was miscompiled (a live scalar register was
+// reused across the branch).
 enum { kModeAll = 0, kModeListed = 1, kModeVerified = 2 };
 
 template <int MODE>
-struct HeadWalk {
-  bool listed;
-  int n, pps;
-  __device__ __forceinline__ HeadWalk(const DecodeArgs &a, int bh, int ctx) {
-    const int n_all = max(0, min(n_valid_pages(ctx, kPageTokens), a.W));
-    if constexpr (MODE == kModeAll) {
-      listed = false;
-      n = n_all;
-      pps = a.pps_all;
-    } else {
-      const int n_list = min(max(__builtin_amdgcn_readfirstlane(a.n_pages[bh]), 0), a.max_sel);
-      if constexpr (MODE == kModeListed) {
-        listed = true;
-        n = n_list;
-        pps = a.pps_sel;
-      } else {
-        listed = __builtin_amdgcn_readfirstlane((int)a.accept[bh]) != 0;
-        n = listed ? n_list : n_all;
-        pps = listed ? a.pps_sel : a.pps_all;
-      }
-    }
+__device__ __forceinline__ int head_pages(const DecodeArgs &a, int bh, bool &listed) {
+  int n_all = 0, n_list = 0;
+  if constexpr (MODE != kModeListed)
+    n_all = max(0, min(n_valid_pages(a.ctx_lens[bh / a.H_kv], kPageTokens), a.W));
+  if constexpr (MODE != kModeAll) n_list = min(max(a.n_pages[bh], 0), a.max_sel);
+  if constexpr (MODE == kModeAll) {
+    listed = false;
+    return n_all;
+  } else if constexpr (MODE == kModeListed) {
+    listed = true;
+    return n_list;
+  } else {
+    listed = a.accept[bh] != 0;
+    return listed ? n_list : n_all;
+  }
+}
+
+// Stream-K partition.  The heads' page walks are concatenated (head-major)
+// into one list of T pages and cut into n_wg equal ranges; workgroup w owns
+// pages [start(w), start(w + 1)), start(w) = floor(w * T / n_wg).  n_wg is the
+// launch size, reduced so that a workgroup gets at least kMinPagesPerWg
+// pages.  T < 2^31 and n_wg <= kMaxSplits, so every quantity is computed in
+// 32 bits (64-bit division is a long instruction sequence on the GPU).
+constexpr int kMaxHeads = 4096;  // B * H_kv of one launch
+constexpr int kMinPagesPerWg = kMinPagesPerWave * 4;
+
+struct Partition {
+  int T, n, q, r;  // pages, workgroups, T / n, T % n
+  __device__ __forceinline__ Partition(int T_, int grid) : T(T_) {
+    n = max(1, min(grid, (T + kMinPagesPerWg - 1) / kMinPagesPerWg));
+    q = T / n;
+    r = T - q * n;
+  }
+  // floor(w * T / n) = w * q + floor(w * r / n), with w * r < n^2 < 2^31.
+  __device__ __forceinline__ int start(int w) const { return w * q + (w * r) / n; }
+  // The workgroup whose range holds page p (the largest w with start(w) <= p):
+  // a float estimate of (p + 1) * n / T, off by at most one, then corrected.
+  __device__ __forceinline__ int owner(int p) const {
+    int w = min(n - 1, (int)((float)(p + 1) * (float)n / (float)T));
+    if (start(w) > p) --w;
+    else if (w + 1 < n && start(w + 1) <= p) ++w;
+    return w;
   }
 };
 
-__device__ __forceinline__ float coherent_load(const float *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ void coherent_store(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Merge of a head's n_act split partials by its last workgroup.  Every load
-// is issued up front (o values of this thread's elements into registers,
-// (m, l) pairs into LDS; indices clamped to the last active split), so the
-// merge costs a single memory round trip.  Each wave then works on one
-// q-head g at a time (its 64 elements share g): lane sp holds split sp's
-// weight exp(m_sp - M), the wave reduces M and L with lane moves, and the
-// weighted sum over splits reads the weights back with readlane.
-template <int G, int NT, int NS>
-__device__ __forceinline__ void merge_partials(const DecodeArgs &a, const float *head_part,
-                                               int n_act, int bh, int n, int ctx,
-                                               float (*s_pm)[kMaxSplits],
-                                               float (*s_pl)[kMaxSplits]) {
-  static_assert(NS <= kWave && (NT % kHeadDim) == 0, "merge layout");
-  constexpr int EPT = (G * kHeadDim + NT - 1) / NT;
-  constexpr int stride = G * kPartStride;  // between splits
-  const int lane = threadIdx.x & 63;
-  float ov[EPT][NS];
-#pragma unroll
-  for (int k = 0; k < EPT; ++k) {
-    const int i = min((int)threadIdx.x + k * NT, G * kHeadDim - 1);
-    const float *pe = head_part + (i / kHeadDim) * kPartStride + (i % kHeadDim);
-#pragma unroll
-    for (int sp = 0; sp < NS; ++sp) ov[k][sp] = coherent_load(pe + min(sp, n_act - 1) * stride);
+// The split partials of one launch, accessed through a raw buffer resource
+// with the agent-scope cache policy (sc1) at 16 (or 8) bytes per access:
+// stores reach the device coherence point before the split's completion
+// counter moves, and loads never return a line that another XCD's L2 still
+// holds.  Offsets are in floats; accesses past the range read 0 / are
+// dropped by the buffer bounds check.
+struct PartBuf {
+  static constexpr int kCpolAgent = 16;         // sc1
+  static constexpr int kRsrcWord3 = 0x00020000;  // 32-bit data format, raw
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ PartBuf(float *base, uint32_t bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, kRsrcWord3)) {}
+  __device__ __forceinline__ void store4(uint32_t off, f32x4 v) const {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)(off * 4), 0,
+                                           kCpolAgent);
   }
-  for (int t = threadIdx.x; t < G * n_act; t += NT) {
-    const int g = t / n_act, sp = t - g * n_act;
-    const float *pg = head_part + (int64_t)sp * stride + g * kPartStride;
-    s_pm[g][sp] = coherent_load(pg + kHeadDim);
-    s_pl[g][sp] = coherent_load(pg + kHeadDim + 1);
+  __device__ __forceinline__ void store2(uint32_t off, f32x2 v) const {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, (int)(off * 4), 0,
+                                          kCpolAgent);
+  }
+  __device__ __forceinline__ f32x4 load4(uint32_t off) const {
+    return __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off * 4), 0, kCpolAgent));
+  }
+  __device__ __forceinline__ f32x2 load2(uint32_t off) const {
+    return __builtin_bit_cast(
+        f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)(off * 4), 0, kCpolAgent));
+  }
+};
+
+// Outputs for q-row qrow, elements d0 .. d0+3 (one float4 chunk).
+__device__ __forceinline__ void write_outputs4(const DecodeArgs &a, int64_t qrow, int d0,
+                                               f32x4 O, float M, float L) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) write_outputs(a, qrow, d0 + e, O[e], M, L);
+}
+
+// LDS of the merge: (m, l) of every (split, g), rewritten in place as
+// (weight, l); the head's totals; per-thread sums of the split lanes.
+template <int G, int NT>
+struct MergeLds {
+  f32x2 ml[kMaxSplits * G];
+  float M[G], L[G];
+  f32x4 acc[NT];
+};
+
+// Merge of a head's n_act split partials by the last of its workgroups.
+// Thread t owns float4 chunk c = t % NC of the head's G x D outputs and the
+// splits j, j + J, ... (j = t / NC); their o chunks are loaded in batches of
+// KB, the next batch in flight while the current one is summed.  The (m, l)
+// pairs go to LDS first; one wave per q-head turns them into the weights
+// exp(m_sp - M) and the totals (M, L).
+template <int G, int NT>
+__device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBuf &pb,
+                                               uint32_t head_off, int n_act, int bh, int n,
+                                               int ctx, MergeLds<G, NT> &s) {
+  constexpr int NC = G * kChunksPerRow;
+  constexpr int J = NT / NC > 0 ? NT / NC : 1;
+  constexpr int NW = NT / kWave;
+  constexpr int KB = 8;
+  static_assert(NC <= NT, "merge layout: one thread per output chunk");
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int c = t % NC;
+  const int j = t / NC;
+  const bool active = t < NC * J;
+  const int g = c / kChunksPerRow;
+  const int d0 = 4 * (c % kChunksPerRow);
+
+  for (int e = t; e < n_act * G; e += NT) s.ml[e] = pb.load2(head_off + e * kPartStride + kHeadDim);
+  const int per_lane = active ? (n_act - j + J - 1) / J : 0;  // splits of this thread
+  auto load_batch = [&](int b0, f32x4 (&v)[KB]) {
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      const int sp = min(j + (b0 + k) * J, n_act - 1);
+      v[k] = pb.load4(head_off + (sp * G + g) * kPartStride + d0);
+    }
+  };
+  f32x4 cur[KB];
+  load_batch(0, cur);
+  __syncthreads();
+  for (int gg = wave; gg < G; gg += NW) {  // wave-uniform
+    float mx = -INFINITY;
+    for (int sp = lane; sp < n_act; sp += kWave) mx = fmaxf(mx, s.ml[sp * G + gg].x);
+    mx = wave_max_from_groups<1>(mx);
+    float ls = 0.f;
+    for (int sp = lane; sp < n_act; sp += kWave) {
+      const f32x2 v = s.ml[sp * G + gg];
+      const float w = (mx == -INFINITY || v.x == -INFINITY) ? 0.f : fast_exp(v.x - mx);
+      ls += w * v.y;
+      s.ml[sp * G + gg].x = w;
+    }
+    ls = wave_sum_from_groups<1>(ls);
+    if (lane == 0) {
+      s.M[gg] = mx;
+      s.L[gg] = ls;
+    }
   }
   __syncthreads();
+  f32x4 O = {0.f, 0.f, 0.f, 0.f};
+  for (int b0 = 0; b0 < per_lane; b0 += KB) {
+    f32x4 nxt[KB];
+    load_batch(b0 + KB, nxt);
 #pragma unroll
-  for (int k = 0; k < EPT; ++k) {
-    const int i0 = (int)(threadIdx.x & ~63) + k * NT;  // first element of this wave
-    if (i0 >= G * kHeadDim) break;                     // wave-uniform
-    const int g = i0 / kHeadDim;
-    const float mv = lane < n_act ? s_pm[g][lane] : -INFINITY;
-    const float lv = lane < n_act ? s_pl[g][lane] : 0.f;
-    const float M = wave_max_from_groups<1>(mv);
-    const float w = (M == -INFINITY || mv == -INFINITY) ? 0.f : fast_exp(mv - M);
-    const float L = wave_sum_from_groups<1>(w * lv);
-    float O = 0.f;
+    for (int k = 0; k < KB; ++k) {
+      const int sp = min(j + (b0 + k) * J, n_act - 1);
+      const float w = b0 + k < per_lane ? s.ml[sp * G + g].x : 0.f;
+      O += w * cur[k];
+    }
 #pragma unroll
-    for (int sp = 0; sp < NS; ++sp)
-      O += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), sp)) *
-           ov[k][sp];
-    const int i = i0 + lane;
-    write_outputs(a, (int64_t)bh * G + g, i % kHeadDim, O, M, L);
+    for (int k = 0; k < KB; ++k) cur[k] = nxt[k];
   }
-  if (threadIdx.x == 0 && a.work != nullptr) add_work(a, n, ctx);
+  if constexpr (J > 1) {
+    s.acc[t] = O;
+    __syncthreads();
+    if (active && j == 0) {
+#pragma unroll
+      for (int jj = 1; jj < J; ++jj) O += s.acc[t + jj * NC];
+    }
+  }
+  if (active && j == 0) write_outputs4(a, (int64_t)bh * G + g, d0, O, s.M[g], s.L[g]);
+  if (t == 0 && a.work != nullptr) add_work(a, n, ctx);
 }
 
 // ---------------------------------------------------------------- engines
@@ -376,14 +474,13 @@ struct MfmaEngine {
     const int c16 = lane & 15, grp = lane >> 4;
     koff = (int64_t)h * kHeadDim + c16 * row_stride + 8 * grp;
     voff = (int64_t)h * kHeadDim + grp * row_stride + 8 * c16;
+    // Rows past the group repeat head G-1: MFMA output rows are independent
+    // and those rows are never written out.  No select on the loaded value,
+    // so nothing waits for q before the first page is consumed.
+    const uint16_t *qrow = a.q + b * a.q_sb + (int64_t)(h * G + min(c16, G - 1)) * a.q_sh;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      uint4 w = make_uint4(0u, 0u, 0u, 0u);
-      if (c16 < G)
-        w = *reinterpret_cast<const uint4 *>(a.q + b * a.q_sb + (int64_t)(h * G + c16) * a.q_sh +
-                                             32 * kk + 8 * grp);
-      qb[kk] = __builtin_bit_cast(bf16x8_t, w);
-    }
+    for (int kk = 0; kk < 4; ++kk)
+      qb[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(qrow + 32 * kk + 8 * grp));
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) o[blk] = float4_t{0.f, 0.f, 0.f, 0.f};
     m_g = -INFINITY;
@@ -486,18 +583,100 @@ struct MfmaEngine {
   }
 };
 
-// NW waves per workgroup, PD pages of K/V in flight per wave.
-template <int G, class Engine, int NW, int PD, int MODE>
-__global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeArgs a) {
-  constexpr int NT = NW * kWave;         // threads per workgroup
-  using Page = typename Engine::Page;
+template <class L, int NW>
+__device__ __forceinline__ L &s_eng_of(L (&eng)[NW], int wave) { return eng[wave]; }
 
-  __shared__ float s_o[NW][G][kHeadDim];
+// End of one workgroup's walk over pages of head h (the waves' states are in
+// s_o / s_m / s_l, behind a barrier).  If the workgroup is the head's only
+// contributor (n_act == 1) it writes the outputs.  Otherwise it stores its
+// partial (o, m, l) in partial row my_row, bumps the head's counter, and the
+// last of the n_act contributors merges rows first_row .. first_row+n_act-1.
+template <int G, int NW>
+__device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const PartBuf &pb, int h,
+                                                 int n, int ctx, int n_act, uint32_t my_row,
+                                                 uint32_t first_row,
+                                                 const float (&s_o)[NW][G][kHeadDim],
+                                                 const float (&s_m)[NW][G],
+                                                 const float (&s_l)[NW][G], int &s_last,
+                                                 MergeLds<G, NW * kWave> &s_merge) {
+  constexpr int NT = NW * kWave;
+  // Workgroup state of float4 chunk c (q-head g = c / 32, elements d0 .. d0+3):
+  // the waves' (o, m, l) rescaled to the workgroup maximum.
+  auto wg_state4 = [&](int c, f32x4 &O, float &M, float &L) {
+    const int g = c / kChunksPerRow, d0 = 4 * (c % kChunksPerRow);
+    M = s_m[0][g];
+#pragma unroll
+    for (int wv = 1; wv < NW; ++wv) M = fmaxf(M, s_m[wv][g]);
+    O = f32x4{0.f, 0.f, 0.f, 0.f};
+    L = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int wv = 0; wv < NW; ++wv) {
+        const float mw = s_m[wv][g];
+        if (mw != -INFINITY) {
+          const float f = fast_exp(mw - M);
+          O += f * *reinterpret_cast<const f32x4 *>(&s_o[wv][g][d0]);
+          L += s_l[wv][g] * f;
+        }
+      }
+    }
+  };
+  if (n_act <= 1) {
+    for (int c = threadIdx.x; c < G * kChunksPerRow; c += NT) {
+      f32x4 O;
+      float M, L;
+      wg_state4(c, O, M, L);
+      write_outputs4(a, (int64_t)h * G + c / kChunksPerRow, 4 * (c % kChunksPerRow), O, M, L);
+    }
+    if (threadIdx.x == 0 && a.work != nullptr) add_work(a, n, ctx);
+    return;
+  }
+  const uint32_t my_off = my_row * (uint32_t)(G * kPartStride);
+  for (int c = threadIdx.x; c < G * kChunksPerRow; c += NT) {
+    f32x4 O;
+    float M, L;
+    wg_state4(c, O, M, L);
+    const int g = c / kChunksPerRow, d0 = 4 * (c % kChunksPerRow);
+    pb.store4(my_off + g * kPartStride + d0, O);
+    if (d0 == 0) pb.store2(my_off + g * kPartStride + kHeadDim, f32x2{M, L});
+  }
+  // Every wave's partial stores have completed before the counter moves.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(&a.counters[h], 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (unsigned)(n_act - 1);
+  }
+  __syncthreads();
+  if (s_last) {
+    // Last contributor of the head: merge its partials, write the outputs.
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&a.counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    merge_partials<G, NT>(a, pb, first_row * (uint32_t)(G * kPartStride), n_act, h, n, ctx,
+                          s_merge);
+  }
+}
+
+// Listed pages of every head (the sparse decode of reuse steps): a static
+// grid of (split, head) workgroups, split s of head h walking listed pages
+// [s * pps, (s + 1) * pps) of h; splits past a head's pages only take part
+// when the head is empty (split 0 writes its outputs).  No scan, so the first
+// page-list and block-table entries are requested at entry.  Partial row of
+// (split, head) = head * n_splits + split.
+template <int G, class Engine, int NW, int PD>
+__global__ __launch_bounds__(NW * kWave) void listed_decode_kernel(const DecodeArgs a) {
+  constexpr int NT = NW * kWave;
+  using Page = typename Engine::Page;
+  union TailLds {
+    typename Engine::Lds eng[NW];
+    MergeLds<G, NT> merge;
+  };
+  __shared__ __attribute__((aligned(16))) float s_o[NW][G][kHeadDim];
   __shared__ float s_m[NW][G];
   __shared__ float s_l[NW][G];
   __shared__ int s_last;
-  __shared__ float s_pm[G][kMaxSplits], s_pl[G][kMaxSplits];
-  __shared__ __attribute__((aligned(16))) typename Engine::Lds s_eng[NW];
+  __shared__ __attribute__((aligned(16))) TailLds s_tail;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -506,158 +685,321 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(const DecodeAr
   const int b = bh / a.H_kv;
   const int h = bh - b * a.H_kv;
   const int ctx = __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
-  // The first page-list entries of a listed head are requested together with
-  // the head's scalar state (their position only needs the split's start,
-  // split * pps_sel), which takes one memory round trip off the page-table
-  // lookups.  Lanes past the head's pages are never consumed.
-  // The block-table entries of those pages are requested as soon as the
-  // entries arrive (clamped into the table; lanes past the head's pages
-  // are discarded later), so the table lookup does not wait for the head's
-  // page count either.
-  int spec_lp = 0, spec_phys = 0;
-  if constexpr (MODE != kModeAll) {
-    if (a.max_sel > 0) {
-      const int rs = min(split * a.pps_sel + wave + NW * lane, a.max_sel - 1);
-      spec_lp = a.page_idx[(int64_t)bh * a.idx_stride + rs];
-      spec_phys = a.block_tables[b * a.bt_sb + min(max(spec_lp, 0), a.W - 1)];
-    }
-  } else {
-    spec_lp = min(split * a.pps_all + wave + NW * lane, a.W - 1);
-    spec_phys = a.block_tables[b * a.bt_sb + spec_lp];
-  }
-
-  const HeadWalk<MODE> hw(a, bh, ctx);
-  const bool listed = hw.listed;
-  const int n = hw.n, pps = hw.pps;
+  const int pps = a.pps;
   const int r0 = split * pps;
+  const int32_t *idx_row = a.page_idx + (int64_t)bh * a.idx_stride;
+  // The first page-list entries of the split (their position only needs
+  // r0) and then their block-table entries are requested together with the
+  // head's page count: lanes past the head's pages are discarded later.
+  int spec_lp = 0, spec_phys = 0;
+  if (a.max_sel > 0) {
+    spec_lp = idx_row[min(r0 + wave + NW * lane, a.max_sel - 1)];
+    spec_phys = a.block_tables[b * a.bt_sb + min(max(spec_lp, 0), a.W - 1)];
+  }
+  const int n = min(max(__builtin_amdgcn_readfirstlane(a.n_pages[bh]), 0), a.max_sel);
   const int r1 = min(n, r0 + pps);
+  const int n_act = (n + pps - 1) / pps;  // splits holding pages of this head
+  if (r0 >= r1 && !(split == 0 && n_act == 0)) return;  // uniform
 
-  if (r0 < r1) {
-    Engine eng;
-    eng.init(a, b, h, lane, s_eng[wave]);
-    const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * kHeadDim;  // between blocks
-    const int32_t *idx_row = listed ? a.page_idx + (int64_t)bh * a.idx_stride : nullptr;
-
-    // This wave's pages are r0 + wave + NW*j.  Lane j looks up page j's block
-    // id and valid-token count up front; the page loop reads them with
-    // readlane and keeps PD pages of K/V loads in flight.
-    const int npw = (r1 - r0 - wave + NW - 1) / NW;
-    for (int c0 = 0; c0 < npw; c0 += kWave) {
-      const int cn = min(kWave, npw - c0);
-      int my_phys = 0, my_ntok = 0;
-      if (lane < cn) {
-        const int r = r0 + wave + NW * (c0 + lane);
-        // Chunk 0 of a listed head (or of an all-pages launch) uses the
-        // entries requested up front; the spec index equals r there.
-        const bool spec = c0 == 0 && (MODE == kModeAll || listed);
-        const int lp = spec ? spec_lp : (listed ? idx_row[r] : r);
-        if (lp >= 0 && lp < a.W) {
-          const int phys = spec ? spec_phys : a.block_tables[b * a.bt_sb + lp];
-          if (phys >= 0 && phys < a.num_blocks) {
-            my_phys = phys;
-            my_ntok = min(kPageTokens, ctx - lp * kPageTokens);
-          }
-        }
-      }
-      // Loads are unconditional so that no branch separates a prefetch from
-      // the page being consumed: a page without valid tokens reads block 0
-      // (in bounds) and is masked out by consume(); prefetches past the end
-      // re-read the wave's last page (already cached) and are never consumed.
-      auto fetch = [&](int j, Page &pg) {
-        const int64_t base = (int64_t)__builtin_amdgcn_readlane(my_phys, j) * page_elems;
-        eng.fetch(a.k_cache + base, a.v_cache + base, pg);
-        return __builtin_amdgcn_readlane(my_ntok, j);
-      };
-      Page pb[PD];
-      int nt[PD];
-      // No separate prologue: the first trip fetches pages 0..PD-1 and
-      // consumes only page 0, so every fetch of a slot uses the same
-      // registers and the wait counts see PD-1 pages outstanding.
-      for (int j = 1 - PD; j < cn; j += PD) {
-#pragma unroll
-        for (int u = 0; u < PD; ++u) {
-          const int slot = (u + PD - 1) % PD;  // slot of page j+u+PD-1
-          nt[slot] = fetch(min(j + u + PD - 1, cn - 1), pb[slot]);
-          if (j + u >= 0 && j + u < cn) eng.consume(pb[u], nt[u], s_eng[wave]);
+  Engine eng;
+  eng.init(a, b, h, lane, s_eng_of(s_tail.eng, wave));
+  const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * kHeadDim;  // between blocks
+  const int npw = max(0, (r1 - r0 - wave + NW - 1) / NW);
+  for (int c0 = 0; c0 < npw; c0 += kWave) {
+    const int cn = min(kWave, npw - c0);
+    int my_phys = 0, my_ntok = 0;
+    if (lane < cn) {
+      const int lp = c0 == 0 ? spec_lp : idx_row[r0 + wave + NW * (c0 + lane)];
+      if (lp >= 0 && lp < a.W) {
+        const int phys = c0 == 0 ? spec_phys : a.block_tables[b * a.bt_sb + lp];
+        if (phys >= 0 && phys < a.num_blocks) {
+          my_phys = phys;
+          my_ntok = min(kPageTokens, ctx - lp * kPageTokens);
         }
       }
     }
-    eng.template finish<NW>(wave, lane, s_o, s_m, s_l);
+    // Loads are unconditional so that no branch separates a prefetch from
+    // the page being consumed: a page without valid tokens reads block 0 (in
+    // bounds) and is masked out by consume(); prefetches past the end re-read
+    // the wave's last page (already cached) and are never consumed.
+    auto fetch = [&](int j, Page &pg) {
+      const int64_t base = (int64_t)__builtin_amdgcn_readlane(my_phys, j) * page_elems;
+      eng.fetch(a.k_cache + base, a.v_cache + base, pg);
+      return __builtin_amdgcn_readlane(my_ntok, j);
+    };
+    Page pbuf[PD];
+    int nt[PD];
+    // The first trip fetches pages 0..PD-1 and consumes page 0; every fetch
+    // of a slot uses the same registers and the wait counts see PD-1 pages
+    // outstanding.
+    for (int j = 1 - PD; j < cn; j += PD) {
+#pragma unroll
+      for (int u = 0; u < PD; ++u) {
+        const int slot = (u + PD - 1) % PD;  // slot of page j+u+PD-1
+        nt[slot] = fetch(min(j + u + PD - 1, cn - 1), pbuf[slot]);
+        if (j + u >= 0 && j + u < cn) eng.consume(pbuf[u], nt[u], s_eng_of(s_tail.eng, wave));
+      }
+    }
   }
+  eng.template finish<NW>(wave, lane, s_o, s_m, s_l);
   __syncthreads();
+  const PartBuf pb(a.part, a.part_bytes);
+  segment_epilogue<G, NW>(a, pb, bh, n, ctx, n_act, (uint32_t)(bh * a.n_splits + split),
+                          (uint32_t)(bh * a.n_splits), s_o, s_m, s_l, s_last, s_tail.merge);
+}
 
-  // Merge the waves: wave-partial (o, m, l) -> workgroup (O, M, L) for
-  // element i = g * D + d.
-  auto wg_state = [&](int i, float &O, float &M, float &L) {
-    const int g = i / kHeadDim, d = i - g * kHeadDim;
-    M = -INFINITY;
-    O = 0.f;
-    L = 0.f;
-    if (r0 < r1) {
-      M = s_m[0][g];
+// NW waves per workgroup, PD pages of K/V in flight per wave.
+//
+// Every workgroup first computes the pages each head walks and their prefix
+// (the same partition in every workgroup), then walks the segments of its
+// range: (head h, pages s0..s1 of h's walk).  A segment that is a whole head
+// writes the outputs; otherwise it stores a partial (o, m, l) in row w + h of
+// the partial buffer (unique: a later workgroup never starts at an earlier
+// head, so (w, h) -> w + h is one-to-one, and head h's partials are the
+// consecutive rows owner(first page) + h .. owner(last page) + h), bumps the
+// head's counter, and the last contributor merges.  Heads that walk no pages
+// are written by workgroup h mod n_wg.
+template <int G, class Engine, int NW, int PD, int MODE>
+__global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const DecodeArgs a) {
+  constexpr int NT = NW * kWave;         // threads per workgroup
+  static_assert(NW == 4, "kMinPagesPerWg assumes four waves");
+  using Page = typename Engine::Page;
+
+  // The engines' LDS is dead once a page loop ends; the merge reuses it.
+  union TailLds {
+    typename Engine::Lds eng[NW];
+    MergeLds<G, NT> merge;
+  };
+  __shared__ __attribute__((aligned(16))) float s_o[NW][G][kHeadDim];
+  __shared__ float s_m[NW][G];
+  __shared__ float s_l[NW][G];
+  __shared__ int s_last;
+  __shared__ int s_wsum[NW];
+  __shared__ int s_start[kMaxHeads + 1];  // exclusive prefix of pages per head
+  __shared__ uint8_t s_listed[kMaxHeads];
+  __shared__ __attribute__((aligned(16))) TailLds s_tail;
+  auto &s_eng = s_tail.eng;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = blockIdx.x;
+  const int heads = a.heads;
+  const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * kHeadDim;  // between blocks
+
+  // Speculative page lookups for the common case in which every head walks
+  // max_sel listed pages: the range start is then known without the scan.
+  // The first page-list entries, the head's context length and q and the
+  // head counts of the scan are requested at entry, the pages' block-table
+  // entries as soon as the page-list entries arrive, and the first PD pages
+  // of K/V before the scan: two memory round trips fewer before the first
+  // K/V load.  Used only if the scan confirms the case.  The loads are
+  // issued without branches (indices clamped; a WG without a speculated
+  // range reads harmless in-bounds entries and discards them), so the
+  // compiler never has to drain them at a join.
+  Engine eng;
+  const int T_spec = heads * a.max_sel;
+  const Partition spec_part(T_spec, gridDim.x);
+  int spec_lp = 0, spec_phys = 0, h_spec = -1, r_spec = 0, ctx_spec = 0, g1_spec = 0;
+  int b_spec = 0, h_c = 0;  // clamped speculated head and its sequence
+  if constexpr (MODE != kModeAll) {
+    const int ms = max(a.max_sel, 1);
+    const int wc = min(w, spec_part.n - 1);
+    const int g0 = spec_part.start(wc);
+    g1_spec = spec_part.start(wc + 1);
+    const int hs = min(g0 / ms, heads - 1);
+    r_spec = g0 - hs * ms;
+    h_c = hs;
+    b_spec = hs / a.H_kv;
+    const int rs = max(0, min(r_spec + wave + NW * lane, a.max_sel - 1));
+    const int32_t *src =
+        a.max_sel > 0 ? a.page_idx + (int64_t)hs * a.idx_stride + rs : a.block_tables;
+    spec_lp = *src;
+    ctx_spec = __builtin_amdgcn_readfirstlane(a.ctx_lens[b_spec]);
+    eng.init(a, b_spec, hs - b_spec * a.H_kv, lane, s_eng[wave]);
+    if (a.max_sel > 0 && w < spec_part.n) h_spec = hs;
+  }
+
+  // Pages per head, one head per thread and pass of NT heads (loads issued
+  // without a branch, index clamped), scanned into their exclusive prefix
+  // in s_start.
+  auto wave_incl_scan = [&](int c) {
+    int incl = c;
 #pragma unroll
-      for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w][g]);
-      if (M != -INFINITY) {
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int v = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += v;
+    }
+    return incl;
+  };
+  bool l_first = false;
+  int c_first = head_pages<MODE>(a, min((int)threadIdx.x, heads - 1), l_first);
+  if constexpr (MODE != kModeAll)
+    spec_phys = a.block_tables[b_spec * a.bt_sb + min(max(spec_lp, 0), a.W - 1)];
+  if ((int)threadIdx.x >= heads) c_first = 0;
+  const int incl_first = wave_incl_scan(c_first);
+  if (lane == kWave - 1) s_wsum[wave] = incl_first;
+
+  // One wave's walk over its pages s0 + wave + NW*j of a segment, in chunks
+  // of up to 64 pages: lane j of a chunk looks up page j's block id and
+  // valid-token count; the loop reads them with readlane and keeps PD pages
+  // of K/V loads in flight (slot (u + PD - 1) % PD holds page u after the
+  // prologue).  Loads are unconditional so that no branch separates a
+  // prefetch from the page being consumed: a page without valid tokens reads
+  // block 0 (in bounds) and is masked out by consume(); prefetches past the
+  // end re-read the wave's last page (already cached) and are never consumed.
+  Page pbuf[PD];
+  int nt[PD];                 // logical page of each slot (kNoPage: none)
+  int my_phys = 0, my_lp = 0;
+  int cur_ctx = 0;            // context length of the segment being walked
+  constexpr int kNoPage = 1 << 26;  // ctx - kNoPage * 16 < 0: no valid token
+  auto lookup = [&](int s0, int c0, int cn, bool listed, const int32_t *idx_row, int b,
+                    bool spec) {
+    const int r = s0 + wave + NW * (c0 + lane);
+    int lp = r, phys = 0;
+    if (spec) {  // the speculative entries of the chunk (lp of page r), consumed by every lane
+      lp = spec_lp;
+      phys = spec_phys;
+    } else if (lane < cn) {
+      if (listed) lp = idx_row[r];
+      phys = a.block_tables[b * a.bt_sb + min(max(lp, 0), a.W - 1)];
+    }
+    const bool ok = lane < cn && lp >= 0 && lp < a.W && phys >= 0 && phys < a.num_blocks;
+    my_phys = ok ? phys : 0;
+    my_lp = ok ? lp : kNoPage;
+  };
+  // Page j of the chunk into pg; returns its logical page (the valid-token
+  // count needs the context length only when the page is consumed).
+  auto fetch = [&](int j, Page &pg) {
+    const int64_t base = (int64_t)__builtin_amdgcn_readlane(my_phys, j) * page_elems;
+    eng.fetch(a.k_cache + base, a.v_cache + base, pg);
+    return __builtin_amdgcn_readlane(my_lp, j);
+  };
+  auto ntok = [&](int lp) { return min(kPageTokens, max(0, cur_ctx - lp * kPageTokens)); };
+  auto prologue = [&](int cn) {
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-          const float mw = s_m[w][g];
-          if (mw != -INFINITY) {
-            const float f = fast_exp(mw - M);
-            O += s_o[w][g][d] * f;
-            L += s_l[w][g] * f;
-          }
-        }
+    for (int u = 0; u < PD; ++u)
+      nt[(u + PD - 1) % PD] = fetch(max(0, min(u, cn - 1)), pbuf[(u + PD - 1) % PD]);
+  };
+  auto steady = [&](int cn) {
+    eng.consume(pbuf[PD - 1], ntok(nt[PD - 1]), s_eng[wave]);  // page 0
+    for (int j = 1; j < cn; j += PD) {
+#pragma unroll
+      for (int u = 0; u < PD; ++u) {
+        const int slot = (u + PD - 1) % PD;  // slot of page j+u+PD-1
+        nt[slot] = fetch(min(j + u + PD - 1, cn - 1), pbuf[slot]);
+        if (j + u < cn) eng.consume(pbuf[u], ntok(nt[u]), s_eng[wave]);
       }
     }
   };
 
-  const int n_act = (n + pps - 1) / pps;  // splits holding pages of this head
-  if (n_act <= 1) {
-    // Split 0 owns the whole head (or the head is empty): write the outputs.
-    if (split == 0) {
-      for (int i = threadIdx.x; i < G * kHeadDim; i += NT) {
-        float O, M, L;
-        wg_state(i, O, M, L);
-        write_outputs(a, (int64_t)bh * G + i / kHeadDim, i % kHeadDim, O, M, L);
+  // First PD pages of the speculated segment (a WG without one fetches block
+  // 0 and never consumes it).
+  if constexpr (MODE != kModeAll) {
+    const int s1 = min(g1_spec, (h_c + 1) * a.max_sel) - h_c * a.max_sel;
+    const int npw = h_spec >= 0 ? max(0, (s1 - r_spec - wave + NW - 1) / NW) : 0;
+    lookup(r_spec, 0, min(kWave, npw), true, nullptr, b_spec, true);
+    prologue(min(kWave, npw));
+  }
+  // Pass 0 (peeled: a loop header here makes the compiler wait for the
+  // speculative loads), then the passes of launches with more than NT heads.
+  auto finish_pass = [&](int hh, int c, int incl, bool lst, int &carry) {
+    lds_barrier();
+    int excl = incl - c, total = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      if (i < wave) excl += s_wsum[i];
+      total += s_wsum[i];
+    }
+    if (hh < heads) {
+      s_start[hh] = carry + excl;
+      s_listed[hh] = lst;
+    }
+    carry += total;
+    lds_barrier();  // s_wsum is rewritten by the next pass
+  };
+  int carry = 0;
+  finish_pass(threadIdx.x, c_first, incl_first, l_first, carry);
+  if (heads > NT) {  // uniform
+    for (int base = NT; base < heads; base += NT) {
+      const int hh = base + threadIdx.x;
+      bool lst = false;
+      int c = head_pages<MODE>(a, min(hh, heads - 1), lst);
+      if (hh >= heads) c = 0;
+      const int incl = wave_incl_scan(c);
+      if (lane == kWave - 1) s_wsum[wave] = incl;
+      finish_pass(hh, c, incl, lst, carry);
+    }
+  }
+  int T = carry;
+  if (threadIdx.x == 0) s_start[heads] = T;
+  lds_barrier();
+  T = __builtin_amdgcn_readfirstlane(T);
+
+  const bool spec_ok = T == T_spec && h_spec >= 0;  // every head walks max_sel pages
+  const Partition part = spec_ok ? spec_part : Partition(max(T, 1), gridDim.x);
+  const int n_wg = T > 0 ? part.n : (int)gridDim.x;
+  if (w >= n_wg) return;  // uniform
+
+  // Heads without pages: (o, m, l) = (0, -inf, 0), zero output.
+  for (int hh = w; hh < heads; hh += n_wg) {
+    if (s_start[hh + 1] != s_start[hh]) continue;  // uniform
+    const int64_t row0 = (int64_t)hh * G;
+    for (int i = threadIdx.x; i < G * kHeadDim; i += NT)
+      write_outputs(a, row0 + i / kHeadDim, i % kHeadDim, 0.f, -INFINITY, 0.f);
+    if (threadIdx.x == 0 && a.work != nullptr) add_work(a, 0, a.ctx_lens[hh / a.H_kv]);
+  }
+  if (T == 0) return;
+
+  const int g0 = part.start(w);
+  const int g1 = part.start(w + 1);
+  // First head of the range: the last head that starts at or before g0 (it
+  // holds page g0, so it is not empty).
+  int lo = h_spec;
+  if (!spec_ok) {
+    lo = 0;
+    int hi = heads - 1;
+    while (lo < hi) {  // uniform binary search
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_start[mid] <= g0) lo = mid;
+      else hi = mid - 1;
+    }
+  }
+  const PartBuf pb(a.part, a.part_bytes);
+
+  for (int h = lo; h < heads; ++h) {
+    const int P = __builtin_amdgcn_readfirstlane(s_start[h]);
+    if (P >= g1) break;  // uniform
+    const int n = __builtin_amdgcn_readfirstlane(s_start[h + 1]) - P;
+    if (n == 0) continue;
+    const int s0 = max(g0, P) - P, s1 = min(g1, P + n) - P;
+    const int b = h / a.H_kv;
+    const int hk = h - b * a.H_kv;
+    const bool listed = s_listed[h] != 0;
+    const bool on_spec = h == h_spec;  // eng, ctx_spec already belong to this head
+    const int ctx = on_spec ? ctx_spec : __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
+    const int32_t *idx_row = a.page_idx + (int64_t)h * a.idx_stride;
+    const bool use_spec = spec_ok && on_spec && s0 == r_spec && listed;
+
+    if (!on_spec || h != lo) eng.init(a, b, hk, lane, s_eng[wave]);
+    cur_ctx = ctx;
+    const int npw = max(0, (s1 - s0 - wave + NW - 1) / NW);
+    for (int c0 = 0; c0 < npw; c0 += kWave) {
+      const int cn = min(kWave, npw - c0);
+      if (!(use_spec && c0 == 0)) {  // the speculated chunk is already in flight
+        lookup(s0, c0, cn, listed, idx_row, b, false);
+        prologue(cn);
       }
-      if (threadIdx.x == 0 && a.work != nullptr) add_work(a, n, ctx);
+      steady(cn);
     }
-    return;
-  }
-  if (r0 >= r1) return;  // no pages for this split (uniform)
+    eng.template finish<NW>(wave, lane, s_o, s_m, s_l);
+    __syncthreads();
 
-  float *head_part = a.part + (int64_t)bh * a.n_splits * G * kPartStride;
-  float *my_part = head_part + (int64_t)split * G * kPartStride;
-  for (int i = threadIdx.x; i < G * kHeadDim; i += NT) {
-    const int g = i / kHeadDim, d = i - g * kHeadDim;
-    float O, M, L;
-    wg_state(i, O, M, L);
-    coherent_store(my_part + g * kPartStride + d, O);
-    if (d == 0) {
-      coherent_store(my_part + g * kPartStride + kHeadDim, M);
-      coherent_store(my_part + g * kPartStride + kHeadDim + 1, L);
-    }
+    const int first = part.owner(P);
+    segment_epilogue<G, NW>(a, pb, h, n, ctx, part.owner(P + n - 1) - first + 1,
+                            (uint32_t)(w + h), (uint32_t)(first + h), s_o, s_m, s_l, s_last,
+                            s_tail.merge);
+    __syncthreads();  // LDS is reused by the next segment
   }
-  // Every wave's partial stores have completed before the counter moves.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(&a.counters[bh], 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (unsigned)(n_act - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-
-  // Last split of the head: merge all partials and write the outputs.
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&a.counters[bh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (n_act <= 8)
-    merge_partials<G, NT, 8>(a, head_part, n_act, bh, n, ctx, s_pm, s_pl);
-  else if (n_act <= 16)
-    merge_partials<G, NT, 16>(a, head_part, n_act, bh, n, ctx, s_pm, s_pl);
-  else
-    merge_partials<G, NT, kMaxSplits>(a, head_part, n_act, bh, n, ctx, s_pm, s_pl);
 }
 
 __global__ void fill_zero_kernel(uint32_t *p, size_t n_words) {
@@ -665,10 +1007,6 @@ __global__ void fill_zero_kernel(uint32_t *p, size_t n_words) {
        i += (size_t)gridDim.x * blockDim.x)
     p[i] = 0u;
 }
-
-struct DecodePlan {
-  int pps_sel, pps_all, n_splits;
-};
 
 static int env_int(const char *name, int dflt) {
   const char *e = getenv(name);
@@ -683,52 +1021,74 @@ static int decode_engine() {
   return v;
 }
 
-// Workgroups per launch (tuning knob CVSA_DECODE_TARGET_WGS, read once).
+// Workgroups per launch, at most kMaxSplits (a head's partials are merged
+// in one workgroup's LDS); tuning knob CVSA_DECODE_TARGET_WGS, read once.
 static int target_workgroups() {
-  static const int v = env_int("CVSA_DECODE_TARGET_WGS", 256);
+  static const int v = env_int("CVSA_DECODE_TARGET_WGS", 256) < kMaxSplits
+                           ? env_int("CVSA_DECODE_TARGET_WGS", 256)
+                           : kMaxSplits;
   return v;
 }
 constexpr int kWavesPerWg = 4;
 
-// Pages per split: spread the heads over ~target_workgroups() workgroups,
-// at least two pages per wave and at most kMaxSplits splits per head.
-static DecodePlan plan_decode(int B, int H_kv, int max_sel, int W, bool listed,
-                              bool all_pages) {
-  const int heads = B * H_kv;
+// Launch plan.  Listed launches (every head walks its page list) use the
+// static split grid of listed_decode_kernel: ~target_workgroups()
+// workgroups spread over the heads, at least kMinPagesPerWg pages per split,
+// at most kMaxSplits splits per head.  Verified and dense launches use the
+// stream-K grid of streamk_decode_kernel: target_workgroups(), fewer when
+// even the largest possible page list (every head walking all W pages) would
+// give a workgroup less than kMinPagesPerWg pages; the kernel narrows it to
+// the pages actually walked.
+struct DecodeLaunch {
+  bool streamk;
+  int grid_x, grid_y;
+  int pps, n_splits;    // listed grid
+  size_t partial_rows;  // rows of G x kPartStride fp32 (0: no workspace)
+};
+
+static DecodeLaunch plan_launch(int B, int H_kv, int max_sel, int W, bool listed,
+                                bool all_pages) {
+  const int64_t heads = (int64_t)B * H_kv;
   const int target = target_workgroups();
-  const int waves = kWavesPerWg;
-  const int min_pps = kMinPagesPerWave * waves;
-  int wg_per_head = heads >= target ? 1 : target / heads;
-  if (wg_per_head > kMaxSplits) wg_per_head = kMaxSplits;
-  auto pps_for = [&](int pages) {
-    int pps = (pages + wg_per_head - 1) / wg_per_head;
-    if (pps < min_pps) pps = min_pps;
-    pps = (pps + waves - 1) / waves * waves;
-    while ((pages + pps - 1) / pps > kMaxSplits) pps += waves;
-    return pps;
-  };
-  DecodePlan p;
-  p.pps_sel = pps_for(listed ? max_sel : 0);
-  p.pps_all = pps_for(all_pages ? W : 0);
-  const int s1 = listed ? (max_sel + p.pps_sel - 1) / p.pps_sel : 0;
-  const int s2 = all_pages ? (W + p.pps_all - 1) / p.pps_all : 0;
-  p.n_splits = s1 > s2 ? s1 : s2;
-  if (p.n_splits < 1) p.n_splits = 1;
+  DecodeLaunch p{};
+  if (listed && !all_pages) {
+    int wg_per_head = heads >= target ? 1 : (int)(target / heads);
+    if (wg_per_head > kMaxSplits) wg_per_head = kMaxSplits;
+    int pps = (max_sel + wg_per_head - 1) / wg_per_head;
+    if (pps < kMinPagesPerWg) pps = kMinPagesPerWg;
+    pps = (pps + kWavesPerWg - 1) / kWavesPerWg * kWavesPerWg;
+    while ((max_sel + pps - 1) / pps > kMaxSplits) pps += kWavesPerWg;
+    p.streamk = false;
+    p.pps = pps;
+    p.n_splits = max_sel > pps ? (max_sel + pps - 1) / pps : 1;
+    p.grid_x = p.n_splits;
+    p.grid_y = (int)heads;
+    p.partial_rows = p.n_splits > 1 ? (size_t)heads * p.n_splits : 0;
+    return p;
+  }
+  int64_t per_head = listed ? max_sel : 0;
+  if (W > per_head) per_head = W;
+  int64_t g = (heads * per_head + kMinPagesPerWg - 1) / kMinPagesPerWg;
+  if (g > target) g = target;
+  if (g < 1) g = 1;
+  p.streamk = true;
+  p.grid_x = (int)g;
+  p.grid_y = 1;
+  p.partial_rows = g > 1 ? (size_t)g + heads : 0;  // row w + h: workgroup w's partial of head h
   return p;
 }
 
 // Workspace: per-head completion counters (uint32, padded to 256 bytes),
-// then split partials [B*H_kv][n_splits][G][D + 2] fp32; none with a single
-// split.
+// then the partial rows.
 static size_t counter_bytes(int heads) { return ((size_t)heads * 4 + 255) / 256 * 256; }
 
 static size_t workspace_bytes_for(int B, int H_q, int H_kv, int max_sel, int W, bool listed,
                                   bool all_pages) {
   const int heads = B * H_kv;
   const int G = H_q / H_kv;
-  const DecodePlan p = plan_decode(B, H_kv, max_sel, W, listed, all_pages);
-  if (p.n_splits == 1) return 0;
-  return counter_bytes(heads) + (size_t)heads * p.n_splits * G * kPartStride * sizeof(float);
+  const DecodeLaunch p = plan_launch(B, H_kv, max_sel, W, listed, all_pages);
+  if (p.partial_rows == 0) return 0;
+  return counter_bytes(heads) + p.partial_rows * G * kPartStride * sizeof(float);
 }
 
 // Lanes per token row, chosen so that the o accumulators stay at <= 64
@@ -778,7 +1138,10 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
                                     a.out_dtype <= CVSA_DTYPE_FP32),
                CVSA_ERR_INVALID, "%s: bad output dtype %d", name, a.out_dtype);
 
-  const DecodePlan p = plan_decode(B, H_kv, listed ? a.max_sel : 0, W, listed, all_pages);
+  const DecodeLaunch p = plan_launch(B, H_kv, listed ? a.max_sel : 0, W, listed, all_pages);
+  CVSA_REQUIRE(!p.streamk || (int64_t)B * H_kv <= kMaxHeads, CVSA_ERR_UNSUPPORTED,
+               "%s: B * H_kv = %lld exceeds %d heads per launch", name,
+               (long long)B * H_kv, kMaxHeads);
   const size_t need = workspace_bytes_for(B, H_q, H_kv, listed ? a.max_sel : 0, W, listed,
                                           all_pages);
   CVSA_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need &&
@@ -786,36 +1149,41 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
                CVSA_ERR_WORKSPACE,
                "%s: workspace of %zu bytes (256-byte aligned) required, got %zu", name,
                need, workspace_bytes);
-  a.pps_sel = p.pps_sel;
-  a.pps_all = p.pps_all;
-  a.n_splits = p.n_splits;
-
   a.W = W;
   a.H_kv = H_kv;
+  a.heads = B * H_kv;
+  a.pps = p.pps;
+  a.n_splits = p.n_splits;
   a.scale = (float)pow((double)D, -0.5);
   a.counters = reinterpret_cast<unsigned *>(workspace);
   a.part = need == 0 ? nullptr
                      : reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) +
                                                  counter_bytes(B * H_kv));
-  const dim3 grid(p.n_splits, B * H_kv);
-  const int mode = !listed ? kModeAll : (all_pages ? kModeVerified : kModeListed);
+  const size_t pbytes = need == 0 ? 0 : need - counter_bytes(B * H_kv);
+  CVSA_REQUIRE(pbytes < ((size_t)1 << 31), CVSA_ERR_UNSUPPORTED,
+               "%s: %zu bytes of split partials exceed the 2 GiB buffer range", name, pbytes);
+  a.part_bytes = (uint32_t)pbytes;
   const bool use_mfma = decode_engine() == 1;
-#define CVSA_DEC_LAUNCH(GG, MM)                                                              \
+  const dim3 grid(p.grid_x, p.grid_y), block(kWavesPerWg * kWave);
+#define CVSA_DEC_LAUNCH(GG, ENG)                                                             \
   do {                                                                                       \
-    if (use_mfma)                                                                            \
-      hipLaunchKernelGGL((paged_decode_kernel<GG, MfmaEngine<GG>, kWavesPerWg, 2, MM>),      \
-                         grid, dim3(kWavesPerWg * kWave), 0, st, a);                         \
+    if (!p.streamk)                                                                          \
+      hipLaunchKernelGGL((listed_decode_kernel<GG, ENG, kWavesPerWg, 2>), grid, block, 0, st, \
+                         a);                                                                 \
+    else if (listed)                                                                         \
+      hipLaunchKernelGGL((streamk_decode_kernel<GG, ENG, kWavesPerWg, 2, kModeVerified>),    \
+                         grid, block, 0, st, a);                                             \
     else                                                                                     \
-      hipLaunchKernelGGL((paged_decode_kernel<GG, ValuEngine<GG, LanesPerRow<GG>::value>,    \
-                                              kWavesPerWg, 2, MM>),                          \
-                         grid, dim3(kWavesPerWg * kWave), 0, st, a);                         \
+      hipLaunchKernelGGL((streamk_decode_kernel<GG, ENG, kWavesPerWg, 2, kModeAll>), grid,   \
+                         block, 0, st, a);                                                   \
   } while (0)
 #define CVSA_DEC_CASE(GG)                                                                    \
-  case GG:                                                                                   \
-    if (mode == kModeAll) CVSA_DEC_LAUNCH(GG, kModeAll);                                     \
-    else if (mode == kModeListed) CVSA_DEC_LAUNCH(GG, kModeListed);                          \
-    else CVSA_DEC_LAUNCH(GG, kModeVerified);                                                 \
-    break;
+  case GG: {                                                                                 \
+    using EngM = MfmaEngine<GG>;                                                             \
+    using EngV = ValuEngine<GG, LanesPerRow<GG>::value>;                                     \
+    if (use_mfma) CVSA_DEC_LAUNCH(GG, EngM);                                                 \
+    else CVSA_DEC_LAUNCH(GG, EngV);                                                          \
+  } break;
   switch (G) {
     CVSA_DEC_CASE(1)
     CVSA_DEC_CASE(2)

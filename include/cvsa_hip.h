@@ -16,8 +16,9 @@
  *  - Return value: CVSA_OK (0), or a negative CVSA_ERR_* code with nothing
  *    enqueued.  cvsa_last_error() then returns a thread-local message.
  *  - Supported geometry: D = 128, block_size = 16, G = H_q / H_kv in 1..8,
- *    H_kv in {1, 2, 4, 8, 16} (page scoring), W <= 32768 pages.  Anything else
- *    returns CVSA_ERR_UNSUPPORTED.
+ *    H_kv in {1, 2, 4, 8, 16} (page scoring), W <= 32768 pages, and
+ *    B * H_kv <= 4096 for dense and verified decode.  Anything else returns
+ *    CVSA_ERR_UNSUPPORTED.
  *  - Entry points are re-entrant.  Calls that share a decode workspace must
  *    be ordered on one stream.
  */
