@@ -207,11 +207,13 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
 
   hipStream_t st = (hipStream_t)stream;
   if (H_kv >= 4) {
-    // Quad layout: waves = pages / PPW x H_kv / 4.  Enough pages per wave to
-    // amortise the setup (q_rep, block-table fetch) while keeping >= ~8 waves
-    // per CU.
+    // Quad layout: waves = pages / PPW x H_kv / 4.  As many pages per wave
+    // (up to 8) as keep >= ~2048 waves (8 per CU) in the launch: the setup
+    // (q_rep, block-table fetch) is amortised over more pages, and the
+    // last-wave tail stays short.
     const int64_t quad_pages = (int64_t)B * W * (H_kv / 4);
-    const int ppw = quad_pages >= 8192 ? 2 : 1;
+    int ppw = 1;
+    while (ppw < 8 && quad_pages / (2 * ppw) >= 2048) ppw *= 2;
     const int64_t waves = ((W + ppw - 1) / ppw) * (int64_t)(H_kv / 4);
     dim3 grid((unsigned)((waves + 3) / 4), B);
 #define CVSA_QUAD_CASE(HK, PP)                                                          \
@@ -222,9 +224,9 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
                        inv_g, scale);                                                   \
     return cvsa_host::check_launch("score_pages");                                      \
   }
-    CVSA_QUAD_CASE(4, 1) CVSA_QUAD_CASE(4, 2)
-    CVSA_QUAD_CASE(8, 1) CVSA_QUAD_CASE(8, 2)
-    CVSA_QUAD_CASE(16, 1) CVSA_QUAD_CASE(16, 2)
+    CVSA_QUAD_CASE(4, 1) CVSA_QUAD_CASE(4, 2) CVSA_QUAD_CASE(4, 4) CVSA_QUAD_CASE(4, 8)
+    CVSA_QUAD_CASE(8, 1) CVSA_QUAD_CASE(8, 2) CVSA_QUAD_CASE(8, 4) CVSA_QUAD_CASE(8, 8)
+    CVSA_QUAD_CASE(16, 1) CVSA_QUAD_CASE(16, 2) CVSA_QUAD_CASE(16, 4) CVSA_QUAD_CASE(16, 8)
 #undef CVSA_QUAD_CASE
     return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d not in {1,2,4,8,16}",
                            H_kv);

@@ -59,6 +59,21 @@ def test_score_pages(gpu, geom):
     assert err < SCORE_RTOL, err
 
 
+@pytest.mark.parametrize("B,H_q,H_kv,ctx", [(1, 32, 8, 65536 - 7), (1, 32, 8, 131072),
+                                          (2, 28, 4, 32768 + 3)])
+def test_score_pages_long_context(gpu, B, H_q, H_kv, ctx):
+    """Launches with several pages per wave (2 and 8) against the oracle
+    (inputs drawn on the GPU, copied to the host for the oracle)."""
+    inp = make_paged_inputs(B, H_q, H_kv, 128, ctx, seed=110, device=gpu)
+    q, K, bt, cl = inp.q, inp.k_cache, inp.block_tables, inp.context_lens
+    got = ops.score_pages(q, K, bt, cl, H_kv, H_q // H_kv, 16).cpu()
+    want = ref.score_pages(q.cpu(), K.cpu(), bt.cpu(), cl.cpu(), H_kv, H_q // H_kv, 16)
+    assert torch.equal(torch.isinf(got), torch.isinf(want))
+    fin = torch.isfinite(want)
+    err = ((got[fin] - want[fin]).abs() / want[fin].abs().clamp(min=1.0)).max().item()
+    assert err < SCORE_RTOL, err
+
+
 def test_score_pages_block_table_wider_than_context(gpu):
     inp = _inputs(101, 2, 32, 8, [100, 5000], W=400)
     q, K, V, bt, cl = _dev(inp, gpu)
