@@ -487,10 +487,14 @@ struct MfmaEngine {
     l_g = 0.f;
   }
 
+  // K loads are plain: one instruction reads 64 bytes of each of 16 rows, so
+  // every 128-byte line is requested by two instructions, and with the
+  // nontemporal hint the line could leave the cache in between (measured:
+  // more HBM fetches, slower).  V loads read whole rows and keep the hint.
   __device__ __forceinline__ void fetch(const uint16_t *kp, const uint16_t *vp, Page &pg) const {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      pg.k[kk] = stream_load16(kp + koff + 32 * kk);
+      pg.k[kk] = *reinterpret_cast<const uint4 *>(kp + koff + 32 * kk);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       pg.v[i] = stream_load16(vp + voff + 4 * i * row_stride);
