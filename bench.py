@@ -209,7 +209,7 @@ def time_kernel(fn, samples):
     return s.elapsed_time(e) * 1e3 / samples
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_decode_listed_cfg3_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "listed_decode_cfg3_traffic.md")
 
 
 def measured_traffic():
