@@ -143,6 +143,60 @@ __device__ __forceinline__ float wave_sum_from_groups(float v) {
   return v;
 }
 
+// ------------------------------------------------ integer wave reductions
+// DPP and permlane moves instead of __shfl_* (an LDS permute per step).
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+
+__device__ __forceinline__ uint32_t xchg_max16_32(uint32_t v) {
+  auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(r[0], r[1]);
+  r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(r[0], r[1]);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u<kDppQuadXor1>(v));
+  v = max(v, dpp_u<kDppQuadXor2>(v));
+  v = max(v, dpp_u<kDppRowHalfMirror>(v));
+  v = max(v, dpp_u<kDppRowMirror>(v));
+  return xchg_max16_32(v);
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  v += dpp_u<kDppQuadXor1>(v);
+  v += dpp_u<kDppQuadXor2>(v);
+  v += dpp_u<kDppRowHalfMirror>(v);
+  v += dpp_u<kDppRowMirror>(v);
+  auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = r[0] + r[1];
+  r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return r[0] + r[1];
+}
+
+// Inclusive prefix sum over the wave: row_shr steps inside each row of 16
+// lanes (lanes shifted in from outside the row read 0), then the totals of
+// the lower rows, read from lanes 15, 31 and 47.
+constexpr int kDppRowShr1 = 0x111;
+constexpr int kDppRowShr2 = 0x112;
+constexpr int kDppRowShr4 = 0x114;
+constexpr int kDppRowShr8 = 0x118;
+
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  v += dpp_u<kDppRowShr1>(v);
+  v += dpp_u<kDppRowShr2>(v);
+  v += dpp_u<kDppRowShr4>(v);
+  v += dpp_u<kDppRowShr8>(v);
+  const uint32_t t0 = __builtin_amdgcn_readlane(v, 15);
+  const uint32_t t1 = __builtin_amdgcn_readlane(v, 31);
+  const uint32_t t2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = (threadIdx.x & 63) >> 4;
+  return v + (row >= 1 ? t0 : 0u) + (row >= 2 ? t1 : 0u) + (row >= 3 ? t2 : 0u);
+}
+
 // Sum over lanes that share (lane mod W): adds the 64/W lanes
 // {l, l+W, l+2W, ...}.  All those lanes end with the same value.
 template <int W>

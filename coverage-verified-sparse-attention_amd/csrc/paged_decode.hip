@@ -826,15 +826,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   // Pages per head, one head per thread and pass of NT heads (loads issued
   // without a branch, index clamped), scanned into their exclusive prefix
   // in s_start.
-  auto wave_incl_scan = [&](int c) {
-    int incl = c;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const int v = __shfl_up(incl, d, kWave);
-      if (lane >= d) incl += v;
-    }
-    return incl;
-  };
+  auto wave_incl_scan = [&](int c) { return (int)wave_incl_scan_u32((uint32_t)c); };
   bool l_first = false;
   int c_first = head_pages<MODE>(a, min((int)threadIdx.x, heads - 1), l_first);
   if constexpr (MODE != kModeAll)

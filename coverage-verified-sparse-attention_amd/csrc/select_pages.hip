@@ -15,9 +15,20 @@
 // coverage >= tau compared in fp32 (:211-212).
 //
 // One 1024-thread workgroup per (b, kv-head); thread t owns the R
-// consecutive pages [t*R, t*R + R).  The k-th largest score is found with a
-// 4-pass, 8-bit MSB radix select over order-preserving integer keys, then a
-// block scan places the selected pages in ascending order.
+// consecutive pages [t*R, t*R + R).  The k-th largest score is found in two
+// steps: a 4096-bucket histogram over the row's finite value range [min, max]
+// (the bucket of a value is a non-decreasing function of it, so the k-th
+// largest lies in the bucket where the count from the top reaches k), then
+// one wave ranks the few scores of that bucket against each other.  Rows
+// where that bucket holds more than 64 scores (heavy ties, extreme
+// outliers) or that hold +inf / NaN fall back to a 4-pass, 8-bit MSB radix
+// select over order-preserving integer keys.  A block scan then places the
+// selected pages in ascending order.
+//
+// A workgroup per row makes these kernels a chain of short dependent steps
+// on one CU, so latency is what counts: every barrier in this file orders
+// LDS only (lds_barrier), which keeps global loads in flight across it and
+// never waits for earlier global stores, and all loads are issued first.
 #include "cvsa_common.h"
 
 namespace cvsa {
@@ -26,25 +37,67 @@ constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / kWave;
 constexpr int kHistCopies = 16;
 constexpr int kHistStride = 257;
+constexpr int kBuckets = 4096;                          // value buckets of the first step
+constexpr int kBucketsPerThread = kBuckets / kSelThreads;
+constexpr int kRankCands = kWave;                       // scores one wave ranks directly
 
+// Unsigned key in the order of the float, with -0 and +0 one key (they
+// compare equal, so the lower page wins between them).
 __device__ __forceinline__ uint32_t order_key(float f) {
-  const uint32_t u = __float_as_uint(f);
+  uint32_t u = __float_as_uint(f);
+  u = u == 0x80000000u ? 0u : u;
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Bucket of a finite score in [vmin, vmin + kBuckets / inv]: a composition of
+// correctly rounded, monotone operations, so it never decreases as v grows,
+// and every evaluation gives the same bits (no fast-math in this library).
+__device__ __forceinline__ int value_bucket(float v, float vmin, float inv) {
+  return (int)fminf((v - vmin) * inv, (float)(kBuckets - 1));
+}
+
+// Block-wide max of two keys and sum of one counter, one barrier.  `red`
+// holds 3 x kSelWaves words and is not reused by another reduction.
+__device__ __forceinline__ void block_range(uint32_t &kmax, uint32_t &kneg, uint32_t &cnt,
+                                            uint32_t (*red)[3]) {
+  kmax = wave_max_u32(kmax);
+  kneg = wave_max_u32(kneg);
+  cnt = wave_sum_u32(cnt);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    red[wave][0] = kmax;
+    red[wave][1] = kneg;
+    red[wave][2] = cnt;
+  }
+  lds_barrier();
+  kmax = red[0][0];
+  kneg = red[0][1];
+  cnt = red[0][2];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) {
+    kmax = max(kmax, red[w][0]);
+    kneg = max(kneg, red[w][1]);
+    cnt += red[w][2];
+  }
+}
+
+// Counter update whose result is not waited for (a no-return atomic).
+__device__ __forceinline__ void stat_add(long long *p, long long v) {
+  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Exclusive prefix sum of one uint32 per thread over the block, plus total.
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *wsum,
                                                          uint32_t &total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t incl = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t o = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += o;
-  }
-  __syncthreads();
+  const uint32_t incl = wave_incl_scan_u32(v);
+  lds_barrier();
   if (lane == 63) wsum[wave] = incl;
-  __syncthreads();
+  lds_barrier();
   uint32_t before = 0, tot = 0;
 #pragma unroll
   for (int w = 0; w < kSelWaves; ++w) {
@@ -72,7 +125,7 @@ __device__ __forceinline__ void block_max2(float &a, float &b, float (*red)[2]) 
     red[wave][0] = a;
     red[wave][1] = b;
   }
-  __syncthreads();
+  lds_barrier();
   a = red[0][0];
   b = red[0][1];
 #pragma unroll
@@ -90,7 +143,7 @@ __device__ __forceinline__ void block_sum2(float &a, float &b, float (*red)[2]) 
     red[wave][0] = a;
     red[wave][1] = b;
   }
-  __syncthreads();
+  lds_barrier();
   a = red[0][0];
   b = red[0][1];
 #pragma unroll
@@ -100,109 +153,39 @@ __device__ __forceinline__ void block_sum2(float &a, float &b, float (*red)[2]) 
   }
 }
 
-template <int R>
-__global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
-    const float *__restrict__ scores, int W, int H_kv,
-    const int32_t *__restrict__ context_lens, int block_size, int budget,
-    int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
-    uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
-    const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
-    long long *__restrict__ stats, int count_gate) {
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t hist_c[kHistCopies * kHistStride];
-  __shared__ uint32_t wsum[kSelWaves];
-  __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2];
-  __shared__ uint32_t s_digit, s_krem;
-  __shared__ int s_nok;
-
-  const int bh = blockIdx.x;
-  const int b = bh / H_kv;
-  const int t = threadIdx.x;
-  const int lane = t & 63;
-  const float *row = scores + (int64_t)bh * W;
-  const int i0 = t * R;
-
-  // Lazy coverage check decided on the device (CVSABackend._lazy_step,
-  // cvsa/backend.py:420-465): when every head of the layer kept its
-  // coverage on the cached selection, that selection stays and all heads
-  // are accepted; otherwise a fresh selection replaces it in place.
-  // Counters: stats[0] accept-all checks, [1] rejections, [2] scoring
-  // steps, [3] heads that passed the check.
-  if (check_accept != nullptr) {
-    if (t == 0) s_nok = 0;
-    __syncthreads();
-    int ok = 1, cnt = 0;
-    for (int i = t; i < n_heads; i += kSelThreads) {
-      const int v = check_accept[i] != 0;
-      ok &= v;
-      cnt += v;
-    }
-    if (cnt) atomicAdd(&s_nok, cnt);
-    const int all_ok = __syncthreads_and(ok);
-    if (stats != nullptr && bh == 0 && t == 0) {
-      stats[0] += all_ok ? 1 : 0;
-      stats[1] += all_ok ? 0 : 1;
-      stats[2] += all_ok ? 0 : 1;
-      stats[3] += s_nok;
-    }
-    if (all_ok) {
-      if (t == 0) accept_out[bh] = 1;
-      return;
-    }
-  } else if (stats != nullptr && !count_gate && bh == 0 && t == 0) {
-    stats[1] += 1;  // a lazy scoring step without a cached selection
-    stats[2] += 1;
-  }
-
-  float val[R];
-  uint32_t key[R];
-  if (R >= 4 && (W & 3) == 0 && i0 + R <= W) {
-    // Whole 16-byte groups (row starts are 16-byte aligned when W % 4 == 0).
-#pragma unroll
-    for (int r = 0; r < R; r += 4) {
-      const float4 v4 = *reinterpret_cast<const float4 *>(row + i0 + r);
-      val[r] = v4.x;
-      val[r + 1 < R ? r + 1 : r] = v4.y;
-      val[r + 2 < R ? r + 2 : r] = v4.z;
-      val[r + 3 < R ? r + 3 : r] = v4.w;
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < R; ++r) val[r] = i0 + r < W ? row[i0 + r] : -INFINITY;
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) key[r] = order_key(val[r]);
-  if (scores_cache != nullptr) {
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (i0 + r < W) scores_cache[(int64_t)bh * W + i0 + r] = val[r];
-  }
-
-  // ---- radix select of the budget-th largest key
-  uint32_t prefix = 0, pmask = 0, krem = (uint32_t)budget;
+// 4-pass, 8-bit MSB radix select of the k-th largest key among the keys
+// with alive(r) set: returns that key T and k - #(alive keys > T), the
+// number of keys equal to T that the selection takes.  Every lane adds
+// into copy (lane % kHistCopies) of the histogram, rows padded by one word so
+// that the copies of a bin sit in different LDS banks: scores cluster in a
+// few leading digits, so lanes of one instruction often hit the same bin.
+template <int R, typename Alive>
+__device__ __forceinline__ void radix_select(const float (&val)[R], Alive alive, uint32_t k,
+                                             uint32_t *hist, uint32_t *hist_c,
+                                             uint32_t *s_digit, uint32_t *s_krem,
+                                             uint32_t &T, uint32_t &krem) {
+  const int t = threadIdx.x, lane = t & 63;
+  uint32_t prefix = 0, pmask = 0;
+  krem = k;
 #pragma unroll 1
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
     for (int i = t; i < kHistCopies * kHistStride; i += kSelThreads) hist_c[i] = 0;
-    __syncthreads();
-    // Scores cluster in a few leading digits, so lanes of one instruction
-    // often hit the same bin: each lane adds into copy (lane % kHistCopies)
-    // of the histogram (rows padded by one word so that the copies of a bin
-    // sit in different LDS banks), and the copies are summed afterwards.
+    lds_barrier();
     uint32_t *my_hist = hist_c + (lane % kHistCopies) * kHistStride;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      if (i0 + r < W && (key[r] & pmask) == prefix)
-        atomicAdd(&my_hist[(key[r] >> shift) & 255u], 1u);
+      const uint32_t key = order_key(val[r]);
+      if (alive(r) && (key & pmask) == prefix) atomicAdd(&my_hist[(key >> shift) & 255u], 1u);
     }
-    __syncthreads();
+    lds_barrier();
     if (t < 256) {
       uint32_t c = 0;
 #pragma unroll
-      for (int k = 0; k < kHistCopies; ++k) c += hist_c[k * kHistStride + t];
+      for (int j = 0; j < kHistCopies; ++j) c += hist_c[j * kHistStride + t];
       hist[t] = c;
     }
-    __syncthreads();
+    lds_barrier();
     if (t < 64) {
       // Lane l holds digits 4l..4l+3; count the candidates above each digit.
       const uint32_t c0 = hist[4 * lane], c1 = hist[4 * lane + 1];
@@ -217,35 +200,256 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
       uint32_t above = suffix - local;  // candidates with a higher digit
       const uint32_t cs[4] = {c3, c2, c1, c0};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if (above < krem && above + cs[k] >= krem) {
-          s_digit = (uint32_t)(4 * lane + 3 - k);
-          s_krem = krem - above;
+      for (int j = 0; j < 4; ++j) {
+        if (above < krem && above + cs[j] >= krem) {
+          *s_digit = (uint32_t)(4 * lane + 3 - j);
+          *s_krem = krem - above;
         }
-        above += cs[k];
+        above += cs[j];
       }
     }
-    __syncthreads();
-    prefix |= s_digit << shift;
+    lds_barrier();
+    prefix |= *s_digit << shift;
     pmask |= 0xFFu << shift;
-    krem = s_krem;
-    __syncthreads();
+    krem = *s_krem;
+    lds_barrier();
   }
-  const uint32_t T = prefix;  // key of the budget-th largest score
+  T = prefix;
+}
+
+template <int R>
+__global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
+    const float *__restrict__ scores, int W, int H_kv,
+    const int32_t *__restrict__ context_lens, int block_size, int budget,
+    int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
+    uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
+    const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
+    long long *__restrict__ stats, int count_gate) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist_c[kHistCopies * kHistStride];
+  __shared__ uint32_t hist_b[kBuckets];
+  __shared__ uint32_t s_cand[kRankCands];
+  __shared__ uint32_t wsum[kSelWaves];
+  __shared__ uint32_t red_rng[kSelWaves][3];
+  __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2];
+  __shared__ uint32_t s_digit, s_krem, s_T, s_bucket, s_kb, s_nb, s_ncand;
+  __shared__ int s_nok, s_nbad;
+
+  const int bh = blockIdx.x;
+  const int b = bh / H_kv;
+  const int t = threadIdx.x;
+  const float *row = scores + (int64_t)bh * W;
+  const int i0 = t * R;
+  // 16-byte loads when W % 4 == 0 (row starts are then 16-byte aligned and
+  // each group of 4 lies wholly inside or outside the row).  The choice is
+  // uniform and the loads are unconditional (clamped into the row, values
+  // past it replaced by -inf): per-lane branches around loads would make the
+  // compiler wait for all of them at the first later use of any.
+  const bool vec = R >= 4 && (W & 3) == 0;
+
+  // Every global load is issued up front, the lazy check's flags first so
+  // that the keep path waits for nothing else.  The flags come through a
+  // buffer resource whose size is 0 without a check (reads return 0) and
+  // n_heads bytes with one, so there is no branch around the load.  All
+  // barriers below order LDS only: loads stay in flight across them and
+  // stores issued before them are not waited for.
+  const __amdgpu_buffer_rsrc_t chk_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(check_accept), (short)0, check_accept ? n_heads : 0, 0x00020000);
+  const uint32_t chk0 = __builtin_amdgcn_raw_buffer_load_b8(chk_rsrc, t, 0, 0);
+  const int ctx = context_lens[b];
+  float val[R];
+  if (vec) {
+#pragma unroll
+    for (int r = 0; r < R; r += 4) {
+      const float4 v4 = *reinterpret_cast<const float4 *>(row + min(i0 + r, W - 4));
+      val[r] = v4.x;
+      val[r + 1 < R ? r + 1 : r] = v4.y;
+      val[r + 2 < R ? r + 2 : r] = v4.z;
+      val[r + 3 < R ? r + 3 : r] = v4.w;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) val[r] = row[min(i0 + r, W - 1)];
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) val[r] = i0 + r < W ? val[r] : -INFINITY;
+
+  // Lazy coverage check decided on the device (CVSABackend._lazy_step,
+  // cvsa/backend.py:420-465): when every head of the layer kept its
+  // coverage on the cached selection, that selection stays and all heads
+  // are accepted; otherwise a fresh selection replaces it in place.
+  // Counters: stats[0] accept-all checks, [1] rejections, [2] scoring
+  // steps, [3] heads that passed the check.
+  if (check_accept != nullptr) {
+    if (t == 0) {
+      s_nok = 0;
+      s_nbad = 0;
+    }
+    lds_barrier();
+    int cnt = 0, bad = 0;
+    if (t < n_heads) {
+      cnt = chk0 != 0;
+      bad = chk0 == 0;
+    }
+    for (int i = t + kSelThreads; i < n_heads; i += kSelThreads) {
+      const int v = check_accept[i] != 0;
+      cnt += v;
+      bad |= !v;
+    }
+    if (cnt) atomicAdd(&s_nok, cnt);
+    if (bad) s_nbad = 1;
+    lds_barrier();
+    const bool all_ok = s_nbad == 0;
+    if (stats != nullptr && bh == 0 && t == 0) {
+      stat_add(&stats[0], all_ok ? 1 : 0);
+      stat_add(&stats[1], all_ok ? 0 : 1);
+      stat_add(&stats[2], all_ok ? 0 : 1);
+      stat_add(&stats[3], s_nok);
+    }
+    if (all_ok) {
+      if (t == 0) accept_out[bh] = 1;
+      return;
+    }
+  } else if (stats != nullptr && !count_gate && bh == 0 && t == 0) {
+    stat_add(&stats[1], 1);  // a lazy scoring step without a cached selection
+    stat_add(&stats[2], 1);
+  }
+
+  if (scores_cache != nullptr) {
+    float *dst = scores_cache + (int64_t)bh * W + i0;
+    if (vec) {
+#pragma unroll
+      for (int r = 0; r < R; r += 4)
+        if (i0 + r < W)
+          *reinterpret_cast<float4 *>(dst + r) = make_float4(
+              val[r], val[r + 1 < R ? r + 1 : r], val[r + 2 < R ? r + 2 : r],
+              val[r + 3 < R ? r + 3 : r]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (i0 + r < W) dst[r] = val[r];
+    }
+  }
+
+  // ---- the budget-th largest key T and krem = budget - #(keys > T)
+  // Range of the finite scores (as keys) and their count; +inf / NaN
+  // entries are counted in the high half of `cnt`.  -inf (pages past the
+  // context) lies below every finite score.
+  for (int i = t; i < kBuckets; i += kSelThreads) hist_b[i] = 0;
+  if (t == 0) s_ncand = 0;
+  uint32_t kmax = 0, kneg = 0, cnt = 0;
+  const auto finite = [&](int r) { return i0 + r < W && fabsf(val[r]) <= 3.402823466e38f; };
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (finite(r)) {
+      const uint32_t key = order_key(val[r]);
+      kmax = max(kmax, key);
+      kneg = max(kneg, ~key);
+      cnt += 1;
+    } else if (i0 + r < W && val[r] != -INFINITY) {
+      cnt += 1u << 16;
+    }
+  }
+  block_range(kmax, kneg, cnt, red_rng);
+  const uint32_t kmin = ~kneg, n_fin = cnt & 0xFFFFu, n_odd = cnt >> 16;
+  // plan 0: T and krem found; 1: radix select over the row; 2: radix
+  // select of the k_radix-th largest inside bucket bstar.
+  uint32_t T = 0, krem = 0, k_radix = (uint32_t)budget;
+  int plan = 1, bstar = -1;
+  float vmin = 0.f, inv = 0.f;
+  const auto bucket = [&](int r) { return finite(r) ? value_bucket(val[r], vmin, inv) : -1; };
+  if (n_odd == 0 && (uint32_t)budget > n_fin) {
+    // Every finite page, then the lowest -inf pages.
+    T = order_key(-INFINITY);
+    krem = (uint32_t)budget - n_fin;
+    plan = 0;
+  } else if (n_odd == 0 && kmin == kmax) {
+    T = kmax;
+    krem = (uint32_t)budget;
+    plan = 0;
+  } else if (n_odd == 0) {
+    vmin = key_value(kmin);
+    inv = (float)kBuckets / (key_value(kmax) - vmin);
+    // Otherwise max - min overflows.
+    if (inv > 0.f && inv <= 3.402823466e38f) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int bk = bucket(r);
+        if (bk >= 0) atomicAdd(&hist_b[bk], 1u);
+      }
+      lds_barrier();
+      // Thread t holds buckets kBuckets-1-(4t+j), j = 0..3: the exclusive
+      // scan over threads counts the scores in higher buckets.
+      uint32_t c[kBucketsPerThread], local = 0;
+#pragma unroll
+      for (int j = 0; j < kBucketsPerThread; ++j) {
+        c[j] = hist_b[kBuckets - 1 - (kBucketsPerThread * t + j)];
+        local += c[j];
+      }
+      uint32_t total_b;
+      uint32_t above = block_exclusive_scan(local, wsum, total_b);
+#pragma unroll
+      for (int j = 0; j < kBucketsPerThread; ++j) {
+        if (above < (uint32_t)budget && above + c[j] >= (uint32_t)budget) {
+          s_bucket = (uint32_t)(kBuckets - 1 - (kBucketsPerThread * t + j));
+          s_kb = (uint32_t)budget - above;
+          s_nb = c[j];
+        }
+        above += c[j];
+      }
+      lds_barrier();
+      bstar = (int)s_bucket;
+      const uint32_t kb = s_kb, nb = s_nb;
+      // The buckets are recomputed below rather than kept live across the
+      // scan (same operands, same bits).
+      asm volatile("" : "+v"(vmin), "+v"(inv));
+      if (nb <= (uint32_t)kRankCands) {
+        // Rank the bucket's scores: T is the key with gt < kb <= gt + eq.
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (bucket(r) == bstar) s_cand[atomicAdd(&s_ncand, 1u)] = order_key(val[r]);
+        lds_barrier();
+        if (t < kWave) {
+          const uint32_t mine = t < (int)nb ? s_cand[t] : 0u;
+          uint32_t gt = 0, eq = 0;
+          for (uint32_t j = 0; j < nb; ++j) {
+            const uint32_t o = s_cand[j];
+            gt += o > mine;
+            eq += o == mine;
+          }
+          if (t < (int)nb && gt < kb && kb <= gt + eq) {
+            s_T = mine;
+            s_krem = kb - gt;
+          }
+        }
+        lds_barrier();
+        T = s_T;
+        krem = s_krem;
+        plan = 0;
+      } else {
+        plan = 2;
+        k_radix = kb;
+      }
+    }
+  }
+  if (plan != 0) {
+    const auto alive = [&](int r) { return i0 + r < W && (plan == 1 || bucket(r) == bstar); };
+    radix_select<R>(val, alive, k_radix, hist, hist_c, &s_digit, &s_krem, T, krem);
+  }
 
   // ---- ascending-order compaction; ties at T go to the lowest pages
   uint32_t gt = 0, eq = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if (i0 + r < W) {
-      gt += key[r] > T;
-      eq += key[r] == T;
+      const uint32_t key = order_key(val[r]);
+      gt += key > T;
+      eq += key == T;
     }
   }
   uint32_t total;
   const uint32_t excl = block_exclusive_scan(gt | (eq << 16), wsum, total);
   const uint32_t gt_before = excl & 0xFFFFu, eq_before = excl >> 16;
-  const int ctx = context_lens[b];
   const int n_sel = min(budget, n_valid_pages(ctx, block_size));
   uint32_t eq_seen = eq_before;
   uint32_t pos = gt_before + min(eq_before, krem);
@@ -254,10 +458,11 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     bool sel = false;
+    const uint32_t key = order_key(val[r]);
     if (i0 + r < W) {
-      if (key[r] > T) {
+      if (key > T) {
         sel = true;
-      } else if (key[r] == T) {
+      } else if (key == T) {
         sel = eq_seen < krem;
         ++eq_seen;
       }
@@ -288,8 +493,8 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   float se = 0.f, ss = 0.f;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    se += expf(val[r] - m_all);
-    if (counted[r]) ss += expf(val[r] - m_sel);
+    se += fast_exp(val[r] - m_all);
+    if (counted[r]) ss += fast_exp(val[r] - m_sel);
   }
   block_sum2(se, ss, red_sum);
   if (t == 0) {
@@ -361,7 +566,7 @@ __global__ __launch_bounds__(kSelThreads) void check_coverage_kernel(
       const int i = t + r * kSelThreads;
       if (i < W) s_row[i] = v[r];
     }
-    __syncthreads();
+    lds_barrier();
   }
   float mx_all = -INFINITY, mx_sel = -INFINITY;
 #pragma unroll
@@ -382,8 +587,8 @@ __global__ __launch_bounds__(kSelThreads) void check_coverage_kernel(
   float se_all = 0.f, se_sel = 0.f;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    se_all += expf(v[r] - m_all);
-    if (t + r * kSelThreads < n_sel) se_sel += expf(sv[r] - m_sel);
+    se_all += fast_exp(v[r] - m_all);
+    if (t + r * kSelThreads < n_sel) se_sel += fast_exp(sv[r] - m_sel);
   }
   block_sum2(se_all, se_sel, red_sum);
   if (t == 0) {

@@ -104,6 +104,45 @@ def test_select_topk_bit_exact(gpu, W, budget):
     assert torch.equal(acc.cpu()[margin], wacc[margin])
 
 
+@pytest.mark.parametrize("W,budget", [(8192, 1024), (20000, 2500)])
+def test_select_topk_special_rows(gpu, W, budget):
+    """One row per path of the selection: all scores equal, +0/-0 mixed
+    (equal scores), one huge outlier (the k-th bucket overflows the rank
+    step), a value range whose width overflows fp32, +inf and NaN entries,
+    near-ties packed into one bucket, and fewer finite scores than the
+    budget."""
+    g = torch.Generator().manual_seed(W)
+    rows = []
+    rows.append(torch.full((W,), 1.25))
+    z = torch.zeros(W)
+    z[torch.randperm(W, generator=g)[: W // 2]] = -0.0
+    rows.append(z)
+    r = torch.randn(W, generator=g)
+    r[7] = 1e30
+    rows.append(r)
+    r = torch.randn(W, generator=g)
+    r[3], r[W - 2] = 3.0e38, -3.0e38
+    rows.append(r)
+    r = torch.randn(W, generator=g)
+    r[torch.randperm(W, generator=g)[:40]] = float("inf")
+    r[11] = float("nan")
+    rows.append(r)
+    rows.append(1.0 + torch.randint(0, 50, (W,), generator=g).float() * 2.0 ** -20)
+    r = torch.randn(W, generator=g)
+    r[torch.randperm(W, generator=g)[: W - budget // 2]] = float("-inf")
+    rows.append(r)
+    ps = torch.stack(rows).view(1, len(rows), W)
+    ctx = torch.tensor([W * 16], dtype=torch.int32)
+    idx, nph, acc, cov = ops.select_topk(ps.to(gpu), budget, ctx.to(gpu), 16, tau=0.9)
+    widx, wnph = ref.select_topk(ps, budget, ctx, 16)
+    for h in range(len(rows)):
+        assert torch.equal(idx.cpu()[0, h], widx[0, h]), h
+    assert torch.equal(nph.cpu(), wnph)
+    finite_rows = [0, 1, 2, 5]
+    wacc, wcov = ref.check_coverage(ps, widx, wnph, 0.9)
+    assert (cov.cpu()[0, finite_rows] - wcov[0, finite_rows]).abs().max().item() < COV_ATOL
+
+
 @pytest.mark.parametrize("W,budget", [(2048, 512), (8192, 1024), (100, 3)])
 def test_select_or_keep(gpu, W, budget):
     """Keep the cached selection when every head passed, else refresh it in
