@@ -1,0 +1,158 @@
+// Step plans: a layer's reuse, lazy-check and fixed-interval scoring steps,
+// each enqueued by one host call.  The plan copies the caller's descriptor
+// after checking everything the chained entry points check, then replays the
+// chain (cvsa_score_pages, cvsa_check_coverage, cvsa_select_or_keep,
+// cvsa_verified_decode / cvsa_sparse_decode) with the stored arguments.
+// This is host code only: the kernels are the entry points' own.
+#include <hip/hip_runtime.h>
+#include <new>
+#include <stdint.h>
+
+#include "../../include/cvsa_hip.h"
+
+namespace cvsa_host {
+int fail(int code, const char *fmt, ...);
+}
+
+#define STEP_REQUIRE(cond, code, ...)                   \
+  do {                                                  \
+    if (!(cond)) return cvsa_host::fail(code, __VA_ARGS__); \
+  } while (0)
+
+struct cvsa_step_plan {
+  cvsa_step_desc d;
+};
+
+namespace {
+
+constexpr int kHeadDim = 128;
+constexpr int kPageTokens = 16;
+constexpr int kMaxPages = 32768;
+constexpr int64_t kMaxDecodeHeads = 4096;
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+size_t workspace_need(const cvsa_step_desc &d) {
+  const size_t listed =
+      cvsa_decode_workspace_bytes(d.B, d.H_q, d.H_kv, d.D, d.budget, d.W, 0);
+  const size_t verified =
+      cvsa_decode_workspace_bytes(d.B, d.H_q, d.H_kv, d.D, d.budget, d.W, 1);
+  return listed > verified ? listed : verified;
+}
+
+// The union of the checks of the entry points a plan chains.
+int check_desc(const cvsa_step_desc &d) {
+  STEP_REQUIRE(d.B > 0 && d.H_kv > 0 && d.H_q > 0 && d.H_q % d.H_kv == 0, CVSA_ERR_INVALID,
+               "step_plan: bad head counts B=%d H_q=%d H_kv=%d", d.B, d.H_q, d.H_kv);
+  const int G = d.H_q / d.H_kv;
+  STEP_REQUIRE(G <= 8, CVSA_ERR_UNSUPPORTED, "step_plan: GQA group size %d not in 1..8", G);
+  STEP_REQUIRE(d.H_kv == 1 || d.H_kv == 2 || d.H_kv == 4 || d.H_kv == 8 || d.H_kv == 16,
+               CVSA_ERR_UNSUPPORTED, "step_plan: H_kv=%d not in {1,2,4,8,16}", d.H_kv);
+  STEP_REQUIRE((int64_t)d.B * d.H_kv <= kMaxDecodeHeads, CVSA_ERR_UNSUPPORTED,
+               "step_plan: B * H_kv = %lld exceeds %lld heads", (long long)d.B * d.H_kv,
+               (long long)kMaxDecodeHeads);
+  STEP_REQUIRE(d.D == kHeadDim && d.block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
+               "step_plan: only D=128, block_size=16 are supported (got D=%d, bs=%d)", d.D,
+               d.block_size);
+  STEP_REQUIRE(d.W > 0 && d.W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
+               "step_plan: W=%d not in 1..%d", d.W, kMaxPages);
+  STEP_REQUIRE(d.budget >= 1 && d.budget <= d.W, CVSA_ERR_INVALID,
+               "step_plan: budget=%d must be in [1, W=%d]", d.budget, d.W);
+  STEP_REQUIRE(d.num_blocks > 0 && d.bt_stride_b >= d.W, CVSA_ERR_INVALID,
+               "step_plan: num_blocks=%lld, block-table row stride %lld < W=%d",
+               (long long)d.num_blocks, (long long)d.bt_stride_b, d.W);
+  STEP_REQUIRE(d.q_stride_b % 8 == 0 && d.q_stride_h % 8 == 0, CVSA_ERR_INVALID,
+               "step_plan: q strides must be multiples of 8 elements");
+  STEP_REQUIRE(d.k_cache && d.v_cache && d.block_tables && d.context_lens && d.page_indices &&
+                   d.n_per_head && d.page_scores && d.check_accept && d.accept && d.coverage,
+               CVSA_ERR_INVALID, "step_plan: null buffer in the descriptor");
+  STEP_REQUIRE(aligned16(d.k_cache) && aligned16(d.v_cache), CVSA_ERR_INVALID,
+               "step_plan: k_cache / v_cache must be 16-byte aligned");
+  STEP_REQUIRE(d.out_dtype >= CVSA_DTYPE_BF16 && d.out_dtype <= CVSA_DTYPE_FP32,
+               CVSA_ERR_INVALID, "step_plan: bad output dtype %d", d.out_dtype);
+  const size_t need = workspace_need(d);
+  STEP_REQUIRE(need < ((size_t)1 << 31), CVSA_ERR_UNSUPPORTED,
+               "step_plan: a decode workspace of %zu bytes exceeds the 2 GiB buffer range",
+               need);
+  STEP_REQUIRE(need == 0 || (d.workspace != nullptr && d.workspace_bytes >= need &&
+                                ((uintptr_t)d.workspace & 255) == 0),
+               CVSA_ERR_WORKSPACE,
+               "step_plan: workspace of %zu bytes (256-byte aligned) required, got %zu", need,
+               d.workspace_bytes);
+  return CVSA_OK;
+}
+
+int score(const cvsa_step_desc &d, const uint16_t *q, void *stream) {
+  return cvsa_score_pages(q, d.q_stride_b, d.q_stride_h, d.k_cache, d.num_blocks,
+                          d.block_tables, d.bt_stride_b, d.context_lens, d.B, d.H_q, d.H_kv,
+                          d.D, d.block_size, d.W, d.page_scores, stream);
+}
+
+int verified(const cvsa_step_desc &d, const uint16_t *q, void *out, void *stream) {
+  return cvsa_verified_decode(q, d.q_stride_b, d.q_stride_h, d.k_cache, d.v_cache,
+                              d.num_blocks, d.block_tables, d.bt_stride_b, d.context_lens,
+                              d.page_indices, d.budget, d.n_per_head, d.budget, d.accept, d.B,
+                              d.H_q, d.H_kv, d.D, d.block_size, d.W, nullptr, nullptr, nullptr,
+                              out, d.out_dtype, d.work, d.workspace, d.workspace_bytes,
+                              stream);
+}
+
+}  // namespace
+
+extern "C" size_t cvsa_step_workspace_bytes(const cvsa_step_desc *desc) {
+  if (desc == nullptr) return 0;
+  return workspace_need(*desc);
+}
+
+extern "C" int cvsa_step_plan_create(const cvsa_step_desc *desc, cvsa_step_plan **plan) {
+  STEP_REQUIRE(desc && plan, CVSA_ERR_INVALID, "step_plan_create: null argument");
+  *plan = nullptr;
+  const int rc = check_desc(*desc);
+  if (rc != CVSA_OK) return rc;
+  cvsa_step_plan *p = new (std::nothrow) cvsa_step_plan;
+  STEP_REQUIRE(p != nullptr, CVSA_ERR_INVALID, "step_plan_create: out of host memory");
+  p->d = *desc;
+  *plan = p;
+  return CVSA_OK;
+}
+
+extern "C" void cvsa_step_plan_destroy(cvsa_step_plan *plan) { delete plan; }
+
+extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint16_t *q,
+                                  void *out, void *stream) {
+  STEP_REQUIRE(plan && q && out, CVSA_ERR_INVALID, "step_plan_run: null argument");
+  STEP_REQUIRE(aligned16(q), CVSA_ERR_INVALID, "step_plan_run: q must be 16-byte aligned");
+  STEP_REQUIRE(kind == CVSA_STEP_REUSE || kind == CVSA_STEP_LAZY_CHECK ||
+                   kind == CVSA_STEP_SCORE,
+               CVSA_ERR_INVALID, "step_plan_run: unknown step kind %d", kind);
+  const cvsa_step_desc &d = plan->d;
+  int rc;
+  switch (kind) {
+    case CVSA_STEP_REUSE:
+      return cvsa_sparse_decode(q, d.q_stride_b, d.q_stride_h, d.k_cache, d.v_cache,
+                                d.num_blocks, d.block_tables, d.bt_stride_b, d.context_lens,
+                                d.page_indices, d.budget, d.n_per_head, d.budget, d.B, d.H_q,
+                                d.H_kv, d.D, d.block_size, d.W, nullptr, nullptr, nullptr, out,
+                                d.out_dtype, d.work, d.workspace, d.workspace_bytes, stream);
+    case CVSA_STEP_LAZY_CHECK:
+      if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
+      if ((rc = cvsa_check_coverage(d.page_scores, d.B, d.H_kv, d.W, d.page_indices, d.budget,
+                                    d.n_per_head, d.tau, d.check_accept, d.coverage,
+                                    stream)) != CVSA_OK)
+        return rc;
+      if ((rc = cvsa_select_or_keep(d.page_scores, d.check_accept, d.B, d.H_kv, d.W,
+                                    d.context_lens, d.block_size, d.budget, d.page_indices,
+                                    d.n_per_head, d.tau, d.accept, d.coverage, d.scores_cache,
+                                    d.stats, 0, stream)) != CVSA_OK)
+        return rc;
+      return verified(d, q, out, stream);
+    default:  // CVSA_STEP_SCORE
+      if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
+      if ((rc = cvsa_select_or_keep(d.page_scores, nullptr, d.B, d.H_kv, d.W, d.context_lens,
+                                    d.block_size, d.budget, d.page_indices, d.n_per_head,
+                                    d.tau, d.accept, d.coverage, nullptr, d.stats, 1,
+                                    stream)) != CVSA_OK)
+        return rc;
+      return verified(d, q, out, stream);
+  }
+}

@@ -13,6 +13,9 @@ What runs per layer call (HIP kernels from cvsa.ops):
   scoring step  score_pages -> select_topk (+ coverage gate) -> verified_decode
   lazy check    score_pages -> check_coverage -> select_or_keep -> verified_decode
   reuse step    sparse decode over the cached selection
+Once a layer has a selection, these sequences run from a native step plan
+(ops.StepPlan): one host call per step instead of one validated call per
+kernel, while the caches, tables, counters and stream stay the same.
 The reference's draft decode, complement, complement decode and LSE merge
 collapse into verified_decode: accepted heads attend their selected pages,
 rejected heads attend every valid page in one pass, which equals the LSE
@@ -168,6 +171,7 @@ class CVSABackend:
         self._step = 0
         self._reuse_state: Dict[int, Tuple[torch.Tensor, torch.Tensor, int]] = {}
         self._reuse_plans: Dict[int, ops.DecodeCall] = {}
+        self._step_plans: Dict[int, ops.StepPlan] = {}
         self._cached_selection: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
         self._cached_page_scores: Dict[int, torch.Tensor] = {}
 
@@ -234,6 +238,7 @@ class CVSABackend:
         self._step = 0
         self._reuse_state = {}
         self._reuse_plans = {}
+        self._step_plans = {}
         self._cached_selection = {}
         self._cached_page_scores = {}
         self._last_accept_mask = {}
@@ -375,6 +380,9 @@ class CVSABackend:
     # ------------------------------------------------------------ steps
     def _reuse_decode(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
         work = self._decode_work(context_lens)
+        plan = self._matching_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens)
+        if plan is not None:
+            return plan.run(ops._lib.STEP_REUSE, q)
         # The launch of a layer's reuse decode is validated once and replayed
         # while the caches, tables, selection and stream stay the same.
         plan = self._reuse_plans.get(layer_idx)
@@ -399,6 +407,13 @@ class CVSABackend:
 
     def _lazy_step(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
         """backend.py:392-465"""
+        if layer_idx in self._cached_selection:
+            plan = self._lazy_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens)
+            if plan is not None:
+                output = plan.run(ops._lib.STEP_LAZY_CHECK, q)
+                self._total_coverage_checks += 1
+                self._book_plan_gate(plan, layer_idx, context_lens)
+                return output
         page_scores = self._time_kernel(
             "scoring", ops.score_pages, q, k_cache, block_tables, context_lens,
             self.num_kv_heads, self.num_q_per_kv, self.block_size)
@@ -424,6 +439,62 @@ class CVSABackend:
         self._h_reject_counts += 1
         return self._scoring_step(q, k_cache, v_cache, block_tables, context_lens, layer_idx,
                                   page_scores=page_scores)
+
+    # ------------------------------------------------------------ step plans
+    def _matching_plan(self, layer_idx, q, k_cache, v_cache, block_tables, context_lens):
+        """The layer's step plan if it fits this call and still holds the
+        layer's selection and cached scores (the lazy check's scores cache,
+        or the plan's own scores after a fixed-interval scoring step)."""
+        plan = self._step_plans.get(layer_idx)
+        if plan is None or self._track_timing:
+            return None
+        sel = self._cached_selection.get(layer_idx)
+        cached = self._cached_page_scores.get(layer_idx)
+        if (sel is None or sel[0] is not plan.page_indices
+                or not (cached is plan.scores_cache or cached is plan.page_scores)
+                or not plan.matches(q, k_cache, v_cache, block_tables, context_lens,
+                                    self._work(q.device), self._dev_stats)):
+            return None
+        return plan
+
+    def _new_plan(self, layer_idx, q, k_cache, v_cache, block_tables, context_lens,
+                  page_indices=None, n_per_head=None, scores_cache=None):
+        """Build the layer's step plan, or None where a step needs the
+        per-kernel path (timing, host-side decisions, unsupported buffers)."""
+        if (self._track_timing or self.random_reject_prob is not None
+                or self.approx_recovery_pct is not None):
+            return None
+        dev = q.device
+        work = self._work(dev)
+        stats = self._ensure_dev_stats(dev)
+        if work is None or stats is None:
+            return None
+        budget = max(3, int(block_tables.shape[1] * self.budget_pct))
+        try:
+            plan = ops.StepPlan(q, k_cache, v_cache, block_tables, context_lens,
+                                self.num_kv_heads, self.num_q_per_kv, self.block_size, budget,
+                                self.tau, page_indices, n_per_head, scores_cache, stats, work)
+        except (ValueError, NotImplementedError):
+            return None
+        self._step_plans[layer_idx] = plan
+        return plan
+
+    def _lazy_plan(self, layer_idx, q, k_cache, v_cache, block_tables, context_lens):
+        plan = self._matching_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens)
+        if plan is not None:
+            return plan
+        page_indices, n_per_head = self._cached_selection[layer_idx]
+        return self._new_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens,
+                              page_indices, n_per_head,
+                              self._cached_page_scores.get(layer_idx))
+
+    def _book_plan_gate(self, plan, layer_idx, context_lens):
+        """Host-side bookkeeping of a plan's check or scoring step."""
+        accept_mask = plan.accept.view(torch.bool)
+        self._per_head_total += accept_mask.numel()
+        self._last_accept_mask[layer_idx] = accept_mask
+        self._expanded_store[layer_idx] = _PendingComplement(
+            accept_mask, plan.page_indices, plan.n_per_head, context_lens, self.block_size)
 
     def _device_decision_ok(self, layer_idx, page_scores, context_lens) -> bool:
         """Whether the lazy accept-all decision can stay on the device: exact
@@ -496,6 +567,25 @@ class CVSABackend:
         B = q.shape[0]
         n_pages = block_tables.shape[1]
         budget = max(3, int(n_pages * self.budget_pct))                           # :690
+
+        if page_scores is None and not self.lazy:
+            # Fixed-interval scoring step from the layer's step plan: the
+            # selection and scores live in the plan's buffers.
+            plan = self._matching_plan(layer_idx, q, k_cache, v_cache, block_tables,
+                                       context_lens)
+            if plan is None:
+                plan = self._new_plan(layer_idx, q, k_cache, v_cache, block_tables,
+                                      context_lens)
+            if plan is not None:
+                output = plan.run(ops._lib.STEP_SCORE, q)
+                self._book_plan_gate(plan, layer_idx, context_lens)
+                self._cached_page_scores[layer_idx] = plan.page_scores
+                self._reuse_state[layer_idx] = (plan.page_indices.view(B * self.num_kv_heads, -1),
+                                                plan.n_per_head.view(B * self.num_kv_heads),
+                                                ops.next_power_of_2(budget))
+                self._reuse_plans.pop(layer_idx, None)
+                self._cached_selection[layer_idx] = (plan.page_indices, plan.n_per_head)
+                return output
 
         if page_scores is None:
             page_scores = self._time_kernel(

@@ -11,6 +11,8 @@ per (device, stream) and grown on demand; they need no initialisation.
 """
 from __future__ import annotations
 
+import ctypes
+import weakref
 from typing import Optional, Tuple
 
 import torch
@@ -33,6 +35,7 @@ __all__ = [
     "lse_merge",
     "append_kv",
     "next_power_of_2",
+    "StepPlan",
 ]
 
 _DTYPE_CODE = {
@@ -389,6 +392,119 @@ def _decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, num_kv_h
                        num_q_per_kv, block_size, pi_flat, nph_flat, max_sel, accept, want_state,
                        want_out, out_dtype, work)
     return c.run(_check_q(q))
+
+
+class StepPlan:
+    """One layer's decode steps, each enqueued by one native call.
+
+    Wraps cvsa_step_plan_* (include/cvsa_hip.h): ``run(kind, q)`` enqueues a
+    reuse step (sparse decode of the layer's selection), a lazy check (fresh
+    scores, coverage of the kept selection, keep it or reselect in place,
+    decode with exact recovery) or a fixed-interval scoring step (reselect,
+    gate booked in ``stats``, decode) for a new query and returns the
+    [B, H_q, D] output in q's dtype.  The sequences are those of
+    CVSABackend._reuse_step, _lazy_step and _scoring_step
+    (cvsa/backend.py:866-881, :392-465, :683-864).
+
+    The plan keeps the layer's selection (``page_indices`` [B, H_kv, budget],
+    ``n_per_head`` [B, H_kv], updated in place), the step's ``page_scores``
+    [B, H_kv, W] and gate buffers ``check_accept`` / ``accept`` /
+    ``coverage`` [B, H_kv]; every check or scoring step rewrites the latter.
+    ``matches`` tells whether a call's buffers, query layout and stream are
+    the ones the plan was built for.
+    """
+
+    __slots__ = ("dev", "stream", "q_meta", "out_shape", "out_dtype", "refs", "page_indices",
+                 "n_per_head", "page_scores", "scores_cache", "check_accept", "accept",
+                 "coverage", "budget", "_h", "_run", "_fin", "__weakref__")
+
+    def __init__(self, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
+                 num_q_per_kv, block_size, budget, tau, page_indices=None, n_per_head=None,
+                 scores_cache=None, stats=None, work=None):
+        dev = _device_of(q, k_cache, v_cache, block_tables, context_lens, page_indices,
+                         n_per_head, scores_cache, stats, work)
+        q = _check_q(q)
+        _check_cache(k_cache)
+        _check_cache(v_cache, "v_cache")
+        if k_cache.shape != v_cache.shape:
+            raise ValueError("k_cache and v_cache shapes differ")
+        if (block_tables.dtype != torch.int32 or block_tables.dim() != 2
+                or block_tables.stride(1) != 1 or context_lens.dtype != torch.int32
+                or not context_lens.is_contiguous()):
+            raise ValueError("step plan: block_tables must be int32 [B, W] with unit page "
+                             "stride and context_lens contiguous int32")
+        B, H_q, D = q.shape
+        H = num_kv_heads
+        if H * num_q_per_kv != H_q or k_cache.shape[2] != H:
+            raise ValueError("step plan: head counts do not match q / caches")
+        if k_cache.shape[1] != block_size or k_cache.shape[3] != D:
+            raise ValueError("step plan: cache block_size / head_dim mismatch")
+        W = block_tables.shape[1]
+        if page_indices is None:
+            page_indices = torch.empty(B, H, budget, dtype=torch.int32, device=dev)
+            n_per_head = torch.empty(B, H, dtype=torch.int32, device=dev)
+        for name, t, shape, dt in (("page_indices", page_indices, (B, H, budget), torch.int32),
+                                   ("n_per_head", n_per_head, (B, H), torch.int32)):
+            if tuple(t.shape) != shape or t.dtype != dt or not t.is_contiguous():
+                raise ValueError(f"step plan: {name} must be a contiguous {dt} {shape}")
+        if scores_cache is not None and (tuple(scores_cache.shape) != (B, H, W)
+                                         or scores_cache.dtype != torch.float32
+                                         or not scores_cache.is_contiguous()):
+            raise ValueError("step plan: scores_cache must be a contiguous float32 [B, H_kv, W]")
+        for name, t, n in (("stats", stats, 6), ("work", work, 2)):
+            if t is not None and (t.dtype != torch.int64 or t.numel() < n
+                                  or not t.is_contiguous()):
+                raise ValueError(f"step plan: {name} must be a contiguous int64[>= {n}]")
+        if q.dtype not in _DTYPE_CODE:
+            raise ValueError(f"unsupported output dtype {q.dtype}")
+        self.page_scores = torch.empty(B, H, W, dtype=torch.float32, device=dev)
+        self.check_accept = torch.empty(B, H, dtype=torch.uint8, device=dev)
+        self.accept = torch.empty(B, H, dtype=torch.uint8, device=dev)
+        self.coverage = torch.empty(B, H, dtype=torch.float32, device=dev)
+        d = _lib.StepDesc(
+            B=B, H_q=H_q, H_kv=H, D=D, block_size=block_size, W=W, budget=budget,
+            tau=float(tau), out_dtype=_DTYPE_CODE[q.dtype], q_stride_b=q.stride(0),
+            q_stride_h=q.stride(1), k_cache=k_cache.data_ptr(), v_cache=v_cache.data_ptr(),
+            num_blocks=k_cache.shape[0], block_tables=block_tables.data_ptr(),
+            bt_stride_b=block_tables.stride(0), context_lens=context_lens.data_ptr(),
+            page_indices=page_indices.data_ptr(), n_per_head=n_per_head.data_ptr(),
+            page_scores=self.page_scores.data_ptr(), scores_cache=_ptr(scores_cache),
+            check_accept=self.check_accept.data_ptr(), accept=self.accept.data_ptr(),
+            coverage=self.coverage.data_ptr(), stats=_ptr(stats), work=_ptr(work))
+        L = _lib.load()
+        ws = _workspace(dev, L.cvsa_step_workspace_bytes(ctypes.byref(d)))
+        d.workspace = _ptr(ws)
+        d.workspace_bytes = 0 if ws is None else ws.numel()
+        h = ctypes.c_void_p()
+        check(L.cvsa_step_plan_create(ctypes.byref(d), ctypes.byref(h)), "step_plan_create")
+        self._h = h.value
+        self._run = L.cvsa_step_plan_run
+        self._fin = weakref.finalize(self, L.cvsa_step_plan_destroy, h.value)
+        self.dev = dev
+        self.stream = _stream(dev)
+        self.q_meta = (q.shape, q.stride())
+        self.out_shape = (B, H_q, D)
+        self.out_dtype = q.dtype
+        self.page_indices = page_indices
+        self.n_per_head = n_per_head
+        self.scores_cache = scores_cache
+        self.budget = budget
+        # Every buffer the plan's launches touch stays alive with the plan.
+        self.refs = (k_cache, v_cache, block_tables, context_lens, work, stats, ws)
+
+    def matches(self, q, k_cache, v_cache, block_tables, context_lens, work, stats) -> bool:
+        r = self.refs
+        return (r[0] is k_cache and r[1] is v_cache and r[2] is block_tables
+                and r[3] is context_lens and r[4] is work and r[5] is stats
+                and torch._C._cuda_getCurrentRawStream(self.dev.index) == self.stream
+                and q.device == self.dev and q.dtype == self.out_dtype
+                and (q.shape, q.stride()) == self.q_meta and q.data_ptr() % 16 == 0)
+
+    def run(self, kind: int, q: torch.Tensor) -> torch.Tensor:
+        out = torch.empty(self.out_shape, device=self.dev, dtype=self.out_dtype)
+        check(self._run(self._h, kind, q.data_ptr(), out.data_ptr(), self.stream),
+              "step_plan_run")
+        return out
 
 
 def _flat_selection(page_indices: torch.Tensor, n_per_head: torch.Tensor, num_kv_heads: int):

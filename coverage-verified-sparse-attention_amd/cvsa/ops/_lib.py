@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parents[1] / "libcvsa_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 CVSA_OK = 0
 CVSA_ERR_INVALID = -1
@@ -27,6 +27,25 @@ _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 _sz = ctypes.c_size_t
+
+STEP_REUSE = 0
+STEP_LAZY_CHECK = 1
+STEP_SCORE = 2
+
+
+class StepDesc(ctypes.Structure):
+    """cvsa_step_desc (include/cvsa_hip.h), field for field."""
+    _fields_ = [
+        ("B", _i32), ("H_q", _i32), ("H_kv", _i32), ("D", _i32), ("block_size", _i32),
+        ("W", _i32), ("budget", _i32), ("tau", _f32), ("out_dtype", _i32),
+        ("q_stride_b", _i64), ("q_stride_h", _i64),
+        ("k_cache", _p), ("v_cache", _p), ("num_blocks", _i64),
+        ("block_tables", _p), ("bt_stride_b", _i64), ("context_lens", _p),
+        ("page_indices", _p), ("n_per_head", _p), ("page_scores", _p), ("scores_cache", _p),
+        ("check_accept", _p), ("accept", _p), ("coverage", _p), ("stats", _p), ("work", _p),
+        ("workspace", _p), ("workspace_bytes", _sz),
+    ]
+
 
 # name -> (restype, argtypes); mirrors include/cvsa_hip.h
 SIGNATURES = {
@@ -64,6 +83,10 @@ SIGNATURES = {
     "cvsa_append_kv": (ctypes.c_int, [
         _p, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p, _p,
         _i32, _i32, _i32, _i32, _i32, _i32, _p]),
+    "cvsa_step_workspace_bytes": (_sz, [ctypes.POINTER(StepDesc)]),
+    "cvsa_step_plan_create": (ctypes.c_int, [ctypes.POINTER(StepDesc), ctypes.POINTER(_p)]),
+    "cvsa_step_plan_run": (ctypes.c_int, [_p, _i32, _p, _p, _p]),
+    "cvsa_step_plan_destroy": (None, [_p]),
 }
 
 _LIB = None

@@ -11,8 +11,8 @@
  *    unit stride along pages; context_lens are [B] int32.
  *  - `stream` is a hipStream_t (NULL = default stream).  Kernels are only
  *    enqueued; no entry point synchronises the host.
- *  - The library allocates nothing.  Outputs and workspaces belong to the
- *    caller.
+ *  - The library allocates no device memory.  Outputs and workspaces belong
+ *    to the caller; a step plan (below) is a small host object.
  *  - Return value: CVSA_OK (0), or a negative CVSA_ERR_* code with nothing
  *    enqueued.  cvsa_last_error() then returns a thread-local message.
  *  - Supported geometry: D = 128, block_size = 16, G = H_q / H_kv in 1..8,
@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 1
+#define CVSA_ABI_VERSION 2
 
 enum {
   CVSA_OK = 0,
@@ -260,6 +260,65 @@ int cvsa_append_kv(const uint16_t *k_new, const uint16_t *v_new,
                    int32_t *pages_allocated, int32_t seq_begin, int32_t n_seqs,
                    int32_t next_free_block, int32_t H_kv, int32_t D,
                    int32_t block_size, void *stream);
+
+/*
+ * Step plans: one layer's decode steps, each enqueued by a single call.
+ * The native form of the per-layer step sequences of CVSABackend
+ * (cvsa/backend.py): the reuse step (_reuse_step, :866-881: sparse decode of
+ * the kept selection), the lazy check (_lazy_step, :392-465: fresh scores,
+ * coverage of the kept selection, keep it or reselect, decode with exact
+ * recovery) and the fixed-interval scoring step (_scoring_step, :683-864,
+ * counters booked by the new selection's gate).  The reference issues these
+ * as separate Python-level kernel calls; a plan validates the layer's
+ * buffers once so that a step costs one host call.
+ *
+ * The descriptor names the caller's device buffers; they must stay valid
+ * while the plan is used.  The plan itself is host memory allocated by
+ * cvsa_step_plan_create and released by cvsa_step_plan_destroy (no device
+ * memory).  cvsa_step_plan_create checks everything the step's entry points
+ * would check, so cvsa_step_plan_run fails only on a bad query pointer,
+ * kind or output (nothing enqueued) or a refused launch (CVSA_ERR_LAUNCH;
+ * the launches before it stay enqueued).
+ */
+typedef struct cvsa_step_desc {
+  int32_t B, H_q, H_kv, D, block_size, W;
+  int32_t budget;              /* selection width: pages per (b, kv-head) row */
+  float tau;                   /* coverage threshold */
+  int32_t out_dtype;           /* CVSA_DTYPE_* of the step output */
+  int64_t q_stride_b, q_stride_h;
+  const uint16_t *k_cache, *v_cache;
+  int64_t num_blocks;
+  const int32_t *block_tables;
+  int64_t bt_stride_b;
+  const int32_t *context_lens;
+  int32_t *page_indices;       /* [B, H_kv, budget]: the layer's selection, updated in place */
+  int32_t *n_per_head;         /* [B * H_kv] */
+  float *page_scores;          /* [B, H_kv, W]: the step's page scores */
+  float *scores_cache;         /* [B, H_kv, W] or NULL: scores of the last reselection */
+  uint8_t *check_accept;       /* [B * H_kv]: gate of the kept selection (lazy check) */
+  uint8_t *accept;             /* [B * H_kv]: heads accepted by the step */
+  float *coverage;             /* [B * H_kv] */
+  int64_t *stats;              /* int64[6] counters of cvsa_select_or_keep, or NULL */
+  int64_t *work;               /* int64[2] effective-budget counters, or NULL */
+  void *workspace;             /* decode workspace, zeroed once (cvsa_workspace_init) */
+  size_t workspace_bytes;      /* >= cvsa_step_workspace_bytes(desc) */
+} cvsa_step_desc;
+
+enum {
+  CVSA_STEP_REUSE = 0,      /* sparse decode of the kept selection */
+  CVSA_STEP_LAZY_CHECK = 1, /* score, check, keep or reselect, verified decode */
+  CVSA_STEP_SCORE = 2       /* score, reselect (gate booked in stats), verified decode */
+};
+
+typedef struct cvsa_step_plan cvsa_step_plan;
+
+/* Workspace a plan needs: the larger of its listed and verified decodes. */
+size_t cvsa_step_workspace_bytes(const cvsa_step_desc *desc);
+int cvsa_step_plan_create(const cvsa_step_desc *desc, cvsa_step_plan **plan);
+/* q: [B, H_q, D] bf16 with the descriptor's strides; out: [B, H_q, D]. */
+int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint16_t *q, void *out,
+                       void *stream);
+void cvsa_step_plan_destroy(cvsa_step_plan *plan);
 
 #ifdef __cplusplus
 }

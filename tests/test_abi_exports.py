@@ -55,3 +55,50 @@ def test_errors_are_reported_without_gpu_work():
     assert b"select_topk" in lib.cvsa_last_error()
     rc = lib.cvsa_decode_workspace_bytes(1, 32, 8, 128, 64, 8192, 1)
     assert rc > 0
+
+
+def _step_desc(**over):
+    """A well-formed step descriptor over fake (never dereferenced) pointers."""
+    fake = iter(range(1 << 20, 1 << 30, 1 << 16))
+    d = dict(B=1, H_q=32, H_kv=8, D=128, block_size=16, W=512, budget=128, tau=0.9,
+             out_dtype=_lib.DTYPE_BF16, q_stride_b=32 * 128, q_stride_h=128, num_blocks=600,
+             bt_stride_b=512)
+    for name in ("k_cache", "v_cache", "block_tables", "context_lens", "page_indices",
+                 "n_per_head", "page_scores", "check_accept", "accept", "coverage"):
+        d[name] = next(fake)
+    d.update(over)
+    desc = _lib.StepDesc(**{k: v for k, v in d.items() if k != "workspace_bytes"})
+    need = _lib.load().cvsa_step_workspace_bytes(ctypes.byref(desc))
+    desc.workspace = next(fake) * 256 if need else None
+    desc.workspace_bytes = d.get("workspace_bytes", need)
+    return desc
+
+
+def test_step_plan_validates_on_the_host():
+    lib = _lib_or_skip()
+    h = ctypes.c_void_p()
+    desc = _step_desc()
+    assert lib.cvsa_step_workspace_bytes(ctypes.byref(desc)) == max(
+        lib.cvsa_decode_workspace_bytes(1, 32, 8, 128, 128, 512, 0),
+        lib.cvsa_decode_workspace_bytes(1, 32, 8, 128, 128, 512, 1))
+    assert lib.cvsa_step_plan_create(ctypes.byref(desc), ctypes.byref(h)) == _lib.CVSA_OK
+    assert h.value
+    # run-time argument errors are reported before anything is enqueued
+    assert lib.cvsa_step_plan_run(h, 1, None, 1 << 20, None) == _lib.CVSA_ERR_INVALID
+    assert lib.cvsa_step_plan_run(h, 7, 1 << 20, 1 << 20, None) == _lib.CVSA_ERR_INVALID
+    assert b"kind" in lib.cvsa_last_error()
+    assert lib.cvsa_step_plan_run(h, 0, (1 << 20) + 2, 1 << 20, None) == _lib.CVSA_ERR_INVALID
+    lib.cvsa_step_plan_destroy(h)
+    cases = [(dict(budget=513), _lib.CVSA_ERR_INVALID, b"budget"),
+             (dict(H_kv=3, H_q=12), _lib.CVSA_ERR_UNSUPPORTED, b"H_kv"),
+             (dict(D=64), _lib.CVSA_ERR_UNSUPPORTED, b"D=128"),
+             (dict(bt_stride_b=100), _lib.CVSA_ERR_INVALID, b"stride"),
+             (dict(coverage=None), _lib.CVSA_ERR_INVALID, b"null"),
+             (dict(out_dtype=5), _lib.CVSA_ERR_INVALID, b"dtype"),
+             (dict(workspace_bytes=1024), _lib.CVSA_ERR_WORKSPACE, b"workspace")]
+    for over, code, word in cases:
+        h = ctypes.c_void_p()
+        rc = lib.cvsa_step_plan_create(ctypes.byref(_step_desc(**over)), ctypes.byref(h))
+        assert rc == code, over
+        assert word in lib.cvsa_last_error(), (over, lib.cvsa_last_error())
+        assert not h.value

@@ -1,0 +1,134 @@
+"""Step plans (cvsa_step_plan_*): each step kind equals the same kernels
+called one by one, bit for bit, and the backend gives identical outputs and
+statistics with plans and on its per-kernel path (timing enabled)."""
+import pytest
+import torch
+
+from cvsa import ops
+from cvsa.ops import _lib
+from cvsa.backend import CVSABackend
+from cvsa.synthetic import make_paged_inputs, jitter_query
+from test_gpu_backend import _Runtime
+
+pytestmark = pytest.mark.gpu
+
+H, G = 8, 4
+
+
+def _inputs(dev, seed=11):
+    inp = make_paged_inputs(batch=2, num_q_heads=H * G, num_kv_heads=H, head_dim=128,
+                            context_len=[5000, 2300], hot_heads=[0, 3, 5], n_hot=6,
+                            hot_shift=10.0, seed=seed, device=dev)
+    W = inp.block_tables.shape[1]
+    return inp, W, max(3, int(W * 0.25))
+
+
+@pytest.mark.parametrize("tau", [0.0, 0.995])
+def test_plan_kinds_equal_separate_kernels(gpu, tau):
+    inp, W, budget = _inputs(gpu)
+    ctx, bt = inp.context_lens, inp.block_tables
+    ps0 = ops.score_pages(jitter_query(inp.q, 0.5, 3), inp.k_cache, bt, ctx, H, G, 16)
+    sel0, nph0 = ops.select_topk(ps0, budget, ctx, 16)
+    stats_p = torch.zeros(6, dtype=torch.int64, device=gpu)
+    stats_r = torch.zeros(6, dtype=torch.int64, device=gpu)
+    work_p = torch.zeros(2, dtype=torch.int64, device=gpu)
+    work_r = torch.zeros(2, dtype=torch.int64, device=gpu)
+    cache_p, cache_r = ps0.clone(), ps0.clone()
+    plan = ops.StepPlan(inp.q, inp.k_cache, inp.v_cache, bt, ctx, H, G, 16, budget, tau,
+                        sel0.clone(), nph0.clone(), cache_p, stats_p, work_p)
+    sel_r, nph_r = sel0.clone(), nph0.clone()
+
+    # reuse step
+    got = plan.run(_lib.STEP_REUSE, inp.q)
+    want = ops.sparse_decode_reuse(inp.q, inp.k_cache, inp.v_cache, bt, ctx,
+                                   sel_r.view(2 * H, -1), nph_r.view(2 * H),
+                                   ops.next_power_of_2(budget), H, G, 16, work=work_r)
+    assert torch.equal(got, want)
+
+    # lazy check: keep (tau 0: every head passes) or reselect (tau 0.995)
+    q1 = jitter_query(inp.q, 0.5, 4)
+    got = plan.run(_lib.STEP_LAZY_CHECK, q1)
+    ps = ops.score_pages(q1, inp.k_cache, bt, ctx, H, G, 16)
+    chk, cov = ops.check_coverage(ps, sel_r, nph_r, tau)
+    acc = ops.select_or_keep(ps, chk, budget, ctx, 16, tau, sel_r, nph_r, cov, cache_r, stats_r)
+    want = ops.verified_decode(q1, inp.k_cache, inp.v_cache, bt, ctx, sel_r, nph_r, acc, H, G,
+                               16, output_dtype=q1.dtype, work=work_r)
+    assert torch.equal(got, want)
+    assert torch.equal(plan.page_scores, ps)
+    assert torch.equal(plan.check_accept.view(torch.bool), chk)
+    assert torch.equal(plan.accept.view(torch.bool), acc)
+    assert torch.equal(plan.coverage, cov)
+    assert torch.equal(plan.page_indices, sel_r) and torch.equal(plan.n_per_head, nph_r)
+    assert torch.equal(cache_p, cache_r)
+    assert torch.equal(stats_p, stats_r) and torch.equal(work_p, work_r)
+    assert bool(chk.all()) == (tau == 0.0)
+
+    # fixed-interval scoring step (gate booked in the counters)
+    q2 = jitter_query(inp.q, 0.5, 5)
+    got = plan.run(_lib.STEP_SCORE, q2)
+    ps = ops.score_pages(q2, inp.k_cache, bt, ctx, H, G, 16)
+    acc = ops.select_or_keep(ps, None, budget, ctx, 16, tau, sel_r, nph_r, cov, None, stats_r,
+                             count_gate=True)
+    want = ops.verified_decode(q2, inp.k_cache, inp.v_cache, bt, ctx, sel_r, nph_r, acc, H, G,
+                               16, output_dtype=q2.dtype, work=work_r)
+    assert torch.equal(got, want)
+    assert torch.equal(plan.accept.view(torch.bool), acc)
+    assert torch.equal(plan.page_indices, sel_r) and torch.equal(plan.n_per_head, nph_r)
+    assert torch.equal(stats_p, stats_r) and torch.equal(work_p, work_r)
+
+
+def test_plan_rejects_buffers_it_cannot_use(gpu):
+    inp, W, budget = _inputs(gpu)
+    args = (inp.q, inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens, H, G, 16)
+    with pytest.raises(ValueError):
+        ops.StepPlan(*args, budget, 0.9, torch.zeros(2, H, budget + 1, dtype=torch.int32,
+                                                     device=gpu),
+                     torch.zeros(2, H, dtype=torch.int32, device=gpu))
+    with pytest.raises(ValueError):  # int64 block tables would need a converted copy
+        ops.StepPlan(inp.q, inp.k_cache, inp.v_cache, inp.block_tables.long(), inp.context_lens,
+                     H, G, 16, budget, 0.9)
+    with pytest.raises(ValueError):  # budget outside [1, W]
+        ops.StepPlan(*args, W + 1, 0.9)
+
+
+@pytest.mark.parametrize("kw", [
+    dict(lazy=True, check_interval=5),
+    dict(lazy=True, check_interval=2),
+    dict(lazy=False, reuse_interval=1),
+    dict(lazy=False, reuse_interval=3),
+])
+def test_backend_plans_equal_kernel_path(gpu, kw):
+    """Same decode loop (appends included) through step plans and through
+    the per-kernel path: identical outputs and counters."""
+    inp, W, budget = _inputs(gpu, seed=21)
+    steps = 10
+    bt = torch.zeros(2, W + 2, dtype=torch.int32)
+    bt[:, :W] = inp.block_tables.cpu()
+    inp.block_tables = bt
+    for name in ("q", "k_cache", "v_cache", "context_lens"):
+        setattr(inp, name, getattr(inp, name).cpu())
+    rt_a, rt_b = _Runtime(inp, gpu, 16), _Runtime(inp, gpu, 16)
+    mk = dict(num_kv_heads=H, num_q_heads=H * G, head_dim=128, block_size=16,
+              budget_pct=0.25, coverage_threshold=0.9, **kw)
+    plan_b, kern_b = CVSABackend(**mk), CVSABackend(**mk)
+    kern_b.enable_timing(True)
+    g = torch.Generator().manual_seed(5)
+    for step in range(steps):
+        q = jitter_query(inp.q, 0.3, 700 + step).to(gpu)
+        a = plan_b(q, rt_a.cache.k_cache, rt_a.cache.v_cache, rt_a.mgr.block_tables,
+                   rt_a.mgr.context_lens, 0)
+        b = kern_b(q, rt_b.cache.k_cache, rt_b.cache.v_cache, rt_b.mgr.block_tables,
+                   rt_b.mgr.context_lens, 0)
+        assert torch.equal(a, b), step
+        ma, mb = plan_b._last_accept_mask.get(0), kern_b._last_accept_mask.get(0)
+        assert (ma is None) == (mb is None) and (ma is None or torch.equal(ma, mb)), step
+        plan_b.step_done(0, 1)
+        kern_b.step_done(0, 1)
+        kn = torch.randn(2, H, 128, generator=g).to(torch.bfloat16).to(gpu)
+        vn = torch.randn(2, H, 128, generator=g).to(torch.bfloat16).to(gpu)
+        rt_a.mgr.append_tokens_kv(kn, vn)
+        rt_b.mgr.append_tokens_kv(kn, vn)
+    assert 0 in plan_b._step_plans and not kern_b._step_plans
+    sa, sb = plan_b.get_stats(), kern_b.get_stats()
+    for k in sa:
+        assert sa[k] == sb[k], (k, sa[k], sb[k])
