@@ -191,11 +191,37 @@ struct PartBuf {
   }
 };
 
-// Outputs for q-row qrow, elements d0 .. d0+3 (one float4 chunk).
+// Outputs for q-row qrow, elements d0 .. d0+3 (one float4 chunk, d0 % 4 == 0):
+// one 16-byte store of o_unnorm and one 8- or 16-byte store of out.  The
+// outputs are the last stores of a launch, which cannot end before they
+// complete, so they are written as few, wide stores.
 __device__ __forceinline__ void write_outputs4(const DecodeArgs &a, int64_t qrow, int d0,
                                                f32x4 O, float M, float L) {
+  const int64_t i = qrow * kHeadDim + d0;
+  if (a.o_unnorm != nullptr) {
+    *reinterpret_cast<f32x4 *>(a.o_unnorm + i) = O;
+    if (d0 == 0) {
+      a.m_out[qrow] = M;
+      a.l_out[qrow] = L;
+    }
+  }
+  if (a.out == nullptr) return;
+  if (a.out_dtype == CVSA_DTYPE_FP32) {
+    f32x4 y;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) write_outputs(a, qrow, d0 + e, O[e], M, L);
+    for (int e = 0; e < 4; ++e) y[e] = O[e] / fmaxf(L, 1e-6f);
+    *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(a.out) + i) = y;
+    return;
+  }
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float y = O[e] / fmaxf(L, 1e-6f);
+    w[e] = a.out_dtype == CVSA_DTYPE_BF16 ? f32_to_bf16_bits(y)
+                                          : (uint32_t)__half_as_ushort(__float2half_rn(y));
+  }
+  *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(a.out) + i) =
+      make_uint2(w[0] | (w[1] << 16), w[2] | (w[3] << 16));
 }
 
 // LDS of the merge: (m, l) of every (split, g), rewritten in place as
@@ -1130,6 +1156,8 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
   CVSA_REQUIRE(!want_unnorm || (a.o_unnorm && a.m_out && a.l_out), CVSA_ERR_INVALID,
                "%s: o_unnorm, m_out and l_out must be given together", name);
   CVSA_REQUIRE(want_unnorm || a.out, CVSA_ERR_INVALID, "%s: no output requested", name);
+  CVSA_REQUIRE(((uintptr_t)a.out & 15) == 0 && ((uintptr_t)a.o_unnorm & 15) == 0,
+               CVSA_ERR_INVALID, "%s: out / o_unnorm must be 16-byte aligned", name);
   CVSA_REQUIRE(a.out == nullptr || (a.out_dtype >= CVSA_DTYPE_BF16 &&
                                     a.out_dtype <= CVSA_DTYPE_FP32),
                CVSA_ERR_INVALID, "%s: bad output dtype %d", name, a.out_dtype);

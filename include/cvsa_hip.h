@@ -155,7 +155,7 @@ int cvsa_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
  *   A head with no pages yields m = -inf, l = 0, o = 0 (out = 0).
  * page_indices: rows of idx_stride int32 per (b,h); max_selected bounds
  * n_per_head.  o_unnorm [B,H_q,D] fp32; m_out, l_out [B,H_q] fp32;
- * out [B,H_q,D] of out_dtype.
+ * out [B,H_q,D] of out_dtype; out and o_unnorm contiguous, 16-byte aligned.
  * work (optional, int64[2]): the effective-budget counters of
  * CVSABackend._record_work (cvsa/backend.py:368-390); each head adds the
  * pages it attended to work[0] and n_valid(b) to work[1].
