@@ -28,7 +28,8 @@
 // A workgroup per row makes these kernels a chain of short dependent steps
 // on one CU, so latency is what counts: every barrier in this file orders
 // LDS only (lds_barrier), which keeps global loads in flight across it and
-// never waits for earlier global stores, and all loads are issued first.
+// never waits for earlier global stores, and loads are issued as early as
+// the step that needs them allows.
 #include "cvsa_common.h"
 
 namespace cvsa {
@@ -247,39 +248,18 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   // compiler wait for all of them at the first later use of any.
   const bool vec = R >= 4 && (W & 3) == 0;
 
-  // Every global load is issued up front, the lazy check's flags first so
-  // that the keep path waits for nothing else.  The flags come through a
-  // buffer resource whose size is 0 without a check (reads return 0) and
-  // n_heads bytes with one, so there is no branch around the load.  All
-  // barriers below order LDS only: loads stay in flight across them and
-  // stores issued before them are not waited for.
-  const __amdgpu_buffer_rsrc_t chk_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t *>(check_accept), (short)0, check_accept ? n_heads : 0, 0x00020000);
-  const uint32_t chk0 = __builtin_amdgcn_raw_buffer_load_b8(chk_rsrc, t, 0, 0);
-  const int ctx = context_lens[b];
-  float val[R];
-  if (vec) {
-#pragma unroll
-    for (int r = 0; r < R; r += 4) {
-      const float4 v4 = *reinterpret_cast<const float4 *>(row + min(i0 + r, W - 4));
-      val[r] = v4.x;
-      val[r + 1 < R ? r + 1 : r] = v4.y;
-      val[r + 2 < R ? r + 2 : r] = v4.z;
-      val[r + 3 < R ? r + 3 : r] = v4.w;
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < R; ++r) val[r] = row[min(i0 + r, W - 1)];
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) val[r] = i0 + r < W ? val[r] : -INFINITY;
-
   // Lazy coverage check decided on the device (CVSABackend._lazy_step,
   // cvsa/backend.py:420-465): when every head of the layer kept its
   // coverage on the cached selection, that selection stays and all heads
   // are accepted; otherwise a fresh selection replaces it in place.
   // Counters: stats[0] accept-all checks, [1] rejections, [2] scoring
-  // steps, [3] heads that passed the check.
+  // steps, [3] heads that passed the check.  The scores are requested only
+  // once a reselection is certain: a wave cannot retire before its loads
+  // return, so loads issued ahead would hold up the (common) keep path.
+  // All barriers below order LDS only: loads stay in flight across them and
+  // stores issued before them are not waited for.  (Scalar loads count
+  // with LDS operations, so even a context-length load here would hold up
+  // the check's barriers.)
   if (check_accept != nullptr) {
     if (t == 0) {
       s_nok = 0;
@@ -287,11 +267,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     }
     lds_barrier();
     int cnt = 0, bad = 0;
-    if (t < n_heads) {
-      cnt = chk0 != 0;
-      bad = chk0 == 0;
-    }
-    for (int i = t + kSelThreads; i < n_heads; i += kSelThreads) {
+    for (int i = t; i < n_heads; i += kSelThreads) {
       const int v = check_accept[i] != 0;
       cnt += v;
       bad |= !v;
@@ -314,6 +290,24 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     stat_add(&stats[1], 1);  // a lazy scoring step without a cached selection
     stat_add(&stats[2], 1);
   }
+
+  const int ctx = context_lens[b];
+  float val[R];
+  if (vec) {
+#pragma unroll
+    for (int r = 0; r < R; r += 4) {
+      const float4 v4 = *reinterpret_cast<const float4 *>(row + min(i0 + r, W - 4));
+      val[r] = v4.x;
+      val[r + 1 < R ? r + 1 : r] = v4.y;
+      val[r + 2 < R ? r + 2 : r] = v4.z;
+      val[r + 3 < R ? r + 3 : r] = v4.w;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) val[r] = row[min(i0 + r, W - 1)];
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) val[r] = i0 + r < W ? val[r] : -INFINITY;
 
   if (scores_cache != nullptr) {
     float *dst = scores_cache + (int64_t)bh * W + i0;
