@@ -97,7 +97,15 @@ def parse_args():
     ap.add_argument("--sink-shift", type=float, default=None)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run an elementwise copy of this many MiB (counter calibration)")
-    return ap.parse_args()
+    ap.add_argument("--selector", choices=("exact", "quest"), default="exact",
+                    help="page ranking: the exact max q.k scan, or Quest min/max page metadata")
+    ap.add_argument("--light-normalizer", action="store_true",
+                    help="with --selector quest: Quest scores also drive the coverage gate "
+                         "(no full-key scan on any step)")
+    args = ap.parse_args()
+    if args.light_normalizer and args.selector != "quest":
+        ap.error("--light-normalizer requires --selector quest")
+    return args
 
 
 class Layer:
@@ -167,9 +175,16 @@ def step_bytes(kind, accept, cfg, W, budget):
     page_kv = BS * D * 2            # one page of one head, K or V
     q_bytes = out_bytes = B * Hq * D * 2
     scores = B * H * W * 4
+    meta = B * H * n_valid * 2 * D * 2  # Quest kmin + kmax of every valid page
+    quest, ln = cfg.get("selector") == "quest", cfg.get("light_normalizer", False)
     total = 0
     if kind in ("score", "check", "rescore"):
-        total += B * ctx * H * D * 2 + q_bytes + 4 * B * W + scores     # K scan, q, table, write
+        scan = meta if ln else B * ctx * H * D * 2                      # Quest metadata or K
+        total += scan + q_bytes + 4 * B * W + scores                   # scan, q, table, write
+        if quest and not ln:
+            total += meta + q_bytes + 4 * B * W + scores               # ranking scores too
+        if quest and cfg["append"]:
+            total += B * H * (page_kv + 2 * D * 2)                     # metadata refresh
     if kind in ("check", "rescore"):
         total += scores + 4 * n_sel * B * H                           # coverage of cached sel
     if kind in ("score", "rescore"):
@@ -237,7 +252,8 @@ def cpu_baseline(cfg, layer0, n_steps, tau):
     args = [t.cpu() for t in (inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens)]
     b = OracleCVSABackend(cfg["H_kv"], cfg["H_q"], D, BS, budget_pct=cfg["budget"],
                           coverage_threshold=tau, lazy=cfg["lazy"], check_interval=cfg["M"],
-                          reuse_interval=cfg["M"], acc_dtype=torch.float32)
+                          reuse_interval=cfg["M"], selector=cfg["selector"],
+                          light_normalizer=cfg["light_normalizer"], acc_dtype=torch.float32)
     times = []
     for s in range(n_steps):
         q = jitter_query(q0, Q_JITTER, 50_000 + s)
@@ -276,7 +292,8 @@ def run_schedule(cfg, layers, tau, args, dev):
                    for _ in range(L)] for _ in range(total_steps)]
     backend = CVSABackend(H_kv, H_q, D, BS, num_layers=L, budget_pct=cfg["budget"],
                           coverage_threshold=tau, lazy=cfg["lazy"], check_interval=cfg["M"],
-                          reuse_interval=cfg["M"])
+                          reuse_interval=cfg["M"], selector=cfg["selector"],
+                          light_normalizer=cfg["light_normalizer"])
     kinds = []        # (step, layer, kind, accept tensor or None)
 
     def run_step(s, record):
@@ -318,10 +335,13 @@ def run_schedule(cfg, layers, tau, args, dev):
            for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    host_each = []
     for i in range(args.steps):
+        th = time.perf_counter()
         evs[i][0].record()
         run_step(args.warmup + i, False)
         evs[i][1].record()
+        host_each.append((time.perf_counter() - th) * 1e6 / len(layers))
     host = time.perf_counter() - t0
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -354,6 +374,7 @@ def run_schedule(cfg, layers, tau, args, dev):
         achieved=total_bytes / (sum(step_us) * L * 1e-6) / 1e9, by_kind=by_kind,
         stats=stats_pass2, same=stats_pass2 == stats_pass1, host=host, wall=wall,
         recovery=(1 - accepted_heads / total_heads) if total_heads else None, W=W,
+        host_each=host_each,
         budget=budget, queries=queries)
 
 
@@ -367,7 +388,11 @@ def main():
     from cvsa import ops
     from cvsa.ops import _lib
 
-    cfg = CONFIGS[args.config]
+    cfg = dict(CONFIGS[args.config], selector=args.selector,
+               light_normalizer=args.light_normalizer)
+    if args.selector == "quest":
+        cfg["desc"] += (", Quest selector + light normalizer" if args.light_normalizer
+                        else ", Quest selector (exact gate)")
     hot_shift = cfg["hot_shift"] if args.hot_shift is None else args.hot_shift
     sink_shift = cfg["sink_shift"] if args.sink_shift is None else args.sink_shift
     _lib.load()
@@ -423,6 +448,17 @@ def main():
         k, v, bt, cl, q, ps, pi, nph, rej = lay(i)[:9]
         ops.verified_decode(q, k, v, bt, cl, pi, nph, rej, H_kv, G, BS)
 
+    metas = []
+    if args.selector == "quest":
+        for l in range(L):
+            k, v, bt, cl, q = lay(l)[:5]
+            metas.append(ops.QuestPageMeta(k))
+            metas[-1].scores(q, bt, cl, H_kv, G, BS)   # first build
+
+    def run_quest(i):
+        k, v, bt, cl, q = lay(i)[:5]
+        ops.quest_scores(q, metas[i % L].meta, bt, cl, H_kv, G, BS)
+
     n_smp = args.kernel_samples
     score_us = time_kernel(run_score, n_smp)
     sel_us = time_kernel(run_select, n_smp)
@@ -441,6 +477,9 @@ def main():
     dense_bytes = n_valid * B * H_kv * (2 * BS * D * 2 + 8) + 2 * B * H_q * D * 2
     kernels = {
         "score_pages": {"us": score_us, "bytes": score_bytes},
+        **({"quest_scores": {"us": time_kernel(run_quest, n_smp),
+                             "bytes": n_valid * B * H_kv * 2 * D * 2 + B * H_q * D * 2
+                             + 4 * B * W + B * H_kv * W * 4}} if metas else {}),
         "select_topk+coverage": {"us": sel_us, "bytes": 2 * B * H_kv * W * 4},
         "sparse_decode(reuse)": {"us": reuse_us, "bytes": reuse_bytes},
         "dense_decode": {"us": dense_us, "bytes": dense_bytes},
@@ -485,6 +524,8 @@ def main():
                    "sink_shift_sigma": sink_shift, "parallelism": "none (1 GPU)"},
         "step_us": {"mean": round(mean_us, 2), "median": round(med_us, 2),
                     **{k: round(statistics.mean(v), 2) for k, v in res["by_kind"].items()}},
+        "step_us_each": [round(x, 1) for x in res["step_us"]],
+        "host_us_each": [round(x, 1) for x in res["host_each"]],
         "tokens_per_s": round(B * 1e6 / mean_us, 1),
         "roofline_frac_step": round(res["achieved"] * 1e9 / PEAK_HBM_BPS, 4),
         "head_recovery_rate": res["recovery"],

@@ -15,30 +15,6 @@
 
 namespace cvsa {
 
-// q_rep[h][seg*8 .. seg*8+8): fp32 sum over the group, times 1/G, rounded
-// to bf16 (the bf16 result of q.view(B,H_kv,G,D).mean(2)).
-__device__ __forceinline__ uint4 group_mean_q(const uint16_t *__restrict__ q, int64_t q_sb,
-                                              int64_t q_sh, int b, int h, int G, int seg,
-                                              float inv_g) {
-  float acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  for (int g = 0; g < G; ++g) {
-    const uint4 v = *reinterpret_cast<const uint4 *>(q + b * q_sb + (int64_t)(h * G + g) * q_sh +
-                                                     seg * 8);
-    acc[0] += bf16_lo(v.x); acc[1] += bf16_hi(v.x);
-    acc[2] += bf16_lo(v.y); acc[3] += bf16_hi(v.y);
-    acc[4] += bf16_lo(v.z); acc[5] += bf16_hi(v.z);
-    acc[6] += bf16_lo(v.w); acc[7] += bf16_hi(v.w);
-  }
-  uint4 r;
-  r.x = pack_bf16x2(acc[0] * inv_g, acc[1] * inv_g);
-  r.y = pack_bf16x2(acc[2] * inv_g, acc[3] * inv_g);
-  r.z = pack_bf16x2(acc[4] * inv_g, acc[5] * inv_g);
-  r.w = pack_bf16x2(acc[6] * inv_g, acc[7] * inv_g);
-  return r;
-}
-
 // H_kv >= 4: a wave owns four KV heads ("quad" hq) of PPW pages.  For each
 // token of a page, the quad's four 256-byte rows are contiguous (1 KiB), so
 // one 16-byte load per lane reads them whole: lane l holds head 4*hq + (l >> 4),

@@ -218,9 +218,12 @@ __device__ __forceinline__ void radix_select(const float (&val)[R], Alive alive,
   T = prefix;
 }
 
-template <int R>
+// SEP: the selection ranks sel_scores while the coverage gate (and
+// scores_cache) use scores (CVSABackend._scoring_step, backend.py:723-727:
+// the Quest selector proposes, the exact scan verifies).
+template <int R, bool SEP>
 __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
-    const float *__restrict__ scores, int W, int H_kv,
+    const float *__restrict__ scores, const float *__restrict__ sel_scores, int W, int H_kv,
     const int32_t *__restrict__ context_lens, int block_size, int budget,
     int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
     uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
@@ -239,7 +242,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   const int bh = blockIdx.x;
   const int b = bh / H_kv;
   const int t = threadIdx.x;
-  const float *row = scores + (int64_t)bh * W;
+  const float *row = (SEP ? sel_scores : scores) + (int64_t)bh * W;
   const int i0 = t * R;
   // 16-byte loads when W % 4 == 0 (row starts are then 16-byte aligned and
   // each group of 4 lies wholly inside or outside the row).  The choice is
@@ -292,22 +295,31 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   }
 
   const int ctx = context_lens[b];
-  float val[R];
-  if (vec) {
+  auto load_row = [&](const float *src, float (&dst)[R]) {
+    if (vec) {
 #pragma unroll
-    for (int r = 0; r < R; r += 4) {
-      const float4 v4 = *reinterpret_cast<const float4 *>(row + min(i0 + r, W - 4));
-      val[r] = v4.x;
-      val[r + 1 < R ? r + 1 : r] = v4.y;
-      val[r + 2 < R ? r + 2 : r] = v4.z;
-      val[r + 3 < R ? r + 3 : r] = v4.w;
+      for (int r = 0; r < R; r += 4) {
+        const float4 v4 = *reinterpret_cast<const float4 *>(src + min(i0 + r, W - 4));
+        dst[r] = v4.x;
+        dst[r + 1 < R ? r + 1 : r] = v4.y;
+        dst[r + 2 < R ? r + 2 : r] = v4.z;
+        dst[r + 3 < R ? r + 3 : r] = v4.w;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r) dst[r] = src[min(i0 + r, W - 1)];
     }
-  } else {
 #pragma unroll
-    for (int r = 0; r < R; ++r) val[r] = row[min(i0 + r, W - 1)];
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) val[r] = i0 + r < W ? val[r] : -INFINITY;
+    for (int r = 0; r < R; ++r) dst[r] = i0 + r < W ? dst[r] : -INFINITY;
+  };
+  float val[R];  // scores the selection ranks
+  load_row(row, val);
+  float gv[SEP ? R : 1];  // scores of the coverage gate when they differ
+  if constexpr (SEP) load_row(scores + (int64_t)bh * W, gv);
+  auto gate = [&](int r) -> float {
+    if constexpr (SEP) return gv[r];
+    else return val[r];
+  };
 
   if (scores_cache != nullptr) {
     float *dst = scores_cache + (int64_t)bh * W + i0;
@@ -316,12 +328,12 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
       for (int r = 0; r < R; r += 4)
         if (i0 + r < W)
           *reinterpret_cast<float4 *>(dst + r) = make_float4(
-              val[r], val[r + 1 < R ? r + 1 : r], val[r + 2 < R ? r + 2 : r],
-              val[r + 3 < R ? r + 3 : r]);
+              gate(r), gate(r + 1 < R ? r + 1 : r), gate(r + 2 < R ? r + 2 : r),
+              gate(r + 3 < R ? r + 3 : r));
     } else {
 #pragma unroll
       for (int r = 0; r < R; ++r)
-        if (i0 + r < W) dst[r] = val[r];
+        if (i0 + r < W) dst[r] = gate(r);
     }
   }
 
@@ -474,8 +486,8 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   float mx = -INFINITY, ms = -INFINITY;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    mx = fmaxf(mx, val[r]);
-    if (counted[r]) ms = fmaxf(ms, val[r]);
+    mx = fmaxf(mx, gate(r));
+    if (counted[r]) ms = fmaxf(ms, gate(r));
   }
   block_max2(mx, ms, red_max);
   const float m_all = fmaxf(mx, -1e20f);
@@ -487,8 +499,8 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   float se = 0.f, ss = 0.f;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    se += fast_exp(val[r] - m_all);
-    if (counted[r]) ss += fast_exp(val[r] - m_sel);
+    se += fast_exp(gate(r) - m_all);
+    if (counted[r]) ss += fast_exp(gate(r) - m_sel);
   }
   block_sum2(se, ss, red_sum);
   if (t == 0) {
@@ -599,7 +611,8 @@ static int keys_per_thread(int n) {
 }
 
 
-static int launch_select(const char *name, const float *page_scores, int32_t B, int32_t H_kv,
+static int launch_select(const char *name, const float *page_scores, const float *sel_scores,
+                         int32_t B, int32_t H_kv,
                          int32_t W, const int32_t *context_lens, int32_t block_size,
                          int32_t budget, int32_t *page_indices, int32_t *n_per_head, float tau,
                          uint8_t *accept_out, float *coverage_out, const uint8_t *check_accept,
@@ -624,12 +637,15 @@ static int launch_select(const char *name, const float *page_scores, int32_t B, 
   hipStream_t st = (hipStream_t)stream;
   long long *st64 = reinterpret_cast<long long *>(stats);
   switch (R) {
-#define CVSA_SEL_CASE(RR)                                                                \
-  case RR:                                                                               \
-    hipLaunchKernelGGL(select_topk_kernel<RR>, grid, dim3(kSelThreads), 0, st, page_scores, \
-                       W, H_kv, context_lens, block_size, budget, page_indices, n_per_head, \
-                       tau, accept_out, coverage_out, check_accept, B * H_kv, scores_cache,  \
-                       st64, count_gate);                                                \
+#define CVSA_SEL_LAUNCH(RR, SEP)                                                          \
+  hipLaunchKernelGGL((select_topk_kernel<RR, SEP>), grid, dim3(kSelThreads), 0, st,         \
+                     page_scores, sel_scores, W, H_kv, context_lens, block_size, budget,    \
+                     page_indices, n_per_head, tau, accept_out, coverage_out, check_accept, \
+                     B * H_kv, scores_cache, st64, count_gate)
+#define CVSA_SEL_CASE(RR)                                       \
+  case RR:                                                      \
+    if (sel_scores != nullptr) CVSA_SEL_LAUNCH(RR, true);       \
+    else CVSA_SEL_LAUNCH(RR, false);                            \
     break;
     CVSA_SEL_CASE(1)
     CVSA_SEL_CASE(2)
@@ -638,6 +654,7 @@ static int launch_select(const char *name, const float *page_scores, int32_t B, 
     CVSA_SEL_CASE(16)
     CVSA_SEL_CASE(32)
 #undef CVSA_SEL_CASE
+#undef CVSA_SEL_LAUNCH
     default:
       return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "%s: W=%d too large", name, W);
   }
@@ -653,12 +670,13 @@ extern "C" int cvsa_select_topk(const float *page_scores, int32_t B, int32_t H_k
                                 int32_t budget, int32_t *page_indices, int32_t *n_per_head,
                                 float tau, uint8_t *accept_out, float *coverage_out,
                                 void *stream) {
-  return launch_select("select_topk", page_scores, B, H_kv, W, context_lens, block_size,
-                       budget, page_indices, n_per_head, tau, accept_out, coverage_out,
-                       nullptr, nullptr, nullptr, 0, stream);
+  return launch_select("select_topk", page_scores, nullptr, B, H_kv, W, context_lens,
+                       block_size, budget, page_indices, n_per_head, tau, accept_out,
+                       coverage_out, nullptr, nullptr, nullptr, 0, stream);
 }
 
-extern "C" int cvsa_select_or_keep(const float *page_scores, const uint8_t *check_accept,
+extern "C" int cvsa_select_or_keep(const float *page_scores, const float *sel_scores,
+                                   const uint8_t *check_accept,
                                    int32_t B, int32_t H_kv, int32_t W,
                                    const int32_t *context_lens, int32_t block_size,
                                    int32_t budget, int32_t *page_indices, int32_t *n_per_head,
@@ -667,9 +685,9 @@ extern "C" int cvsa_select_or_keep(const float *page_scores, const uint8_t *chec
                                    void *stream) {
   CVSA_REQUIRE(accept_out && coverage_out, CVSA_ERR_INVALID,
                "select_or_keep: accept_out and coverage_out are required");
-  return launch_select("select_or_keep", page_scores, B, H_kv, W, context_lens, block_size,
-                       budget, page_indices, n_per_head, tau, accept_out, coverage_out,
-                       check_accept, scores_cache, stats, count_gate, stream);
+  return launch_select("select_or_keep", page_scores, sel_scores, B, H_kv, W, context_lens,
+                       block_size, budget, page_indices, n_per_head, tau, accept_out,
+                       coverage_out, check_accept, scores_cache, stats, count_gate, stream);
 }
 
 extern "C" int cvsa_check_coverage(const float *page_scores, int32_t B,

@@ -123,7 +123,7 @@ extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint
   STEP_REQUIRE(plan && q && out, CVSA_ERR_INVALID, "step_plan_run: null argument");
   STEP_REQUIRE(aligned16(q), CVSA_ERR_INVALID, "step_plan_run: q must be 16-byte aligned");
   STEP_REQUIRE(kind == CVSA_STEP_REUSE || kind == CVSA_STEP_LAZY_CHECK ||
-                   kind == CVSA_STEP_SCORE,
+                   kind == CVSA_STEP_SCORE || kind == CVSA_STEP_FRESH,
                CVSA_ERR_INVALID, "step_plan_run: unknown step kind %d", kind);
   const cvsa_step_desc &d = plan->d;
   int rc;
@@ -140,7 +140,15 @@ extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint
                                     d.n_per_head, d.tau, d.check_accept, d.coverage,
                                     stream)) != CVSA_OK)
         return rc;
-      if ((rc = cvsa_select_or_keep(d.page_scores, d.check_accept, d.B, d.H_kv, d.W,
+      if ((rc = cvsa_select_or_keep(d.page_scores, nullptr, d.check_accept, d.B, d.H_kv, d.W,
+                                    d.context_lens, d.block_size, d.budget, d.page_indices,
+                                    d.n_per_head, d.tau, d.accept, d.coverage, d.scores_cache,
+                                    d.stats, 0, stream)) != CVSA_OK)
+        return rc;
+      return verified(d, q, out, stream);
+    case CVSA_STEP_FRESH:
+      if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
+      if ((rc = cvsa_select_or_keep(d.page_scores, nullptr, nullptr, d.B, d.H_kv, d.W,
                                     d.context_lens, d.block_size, d.budget, d.page_indices,
                                     d.n_per_head, d.tau, d.accept, d.coverage, d.scores_cache,
                                     d.stats, 0, stream)) != CVSA_OK)
@@ -148,7 +156,8 @@ extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint
       return verified(d, q, out, stream);
     default:  // CVSA_STEP_SCORE
       if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
-      if ((rc = cvsa_select_or_keep(d.page_scores, nullptr, d.B, d.H_kv, d.W, d.context_lens,
+      if ((rc = cvsa_select_or_keep(d.page_scores, nullptr, nullptr, d.B, d.H_kv, d.W,
+                                    d.context_lens,
                                     d.block_size, d.budget, d.page_indices, d.n_per_head,
                                     d.tau, d.accept, d.coverage, nullptr, d.stats, 1,
                                     stream)) != CVSA_OK)

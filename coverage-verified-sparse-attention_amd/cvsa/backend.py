@@ -27,13 +27,21 @@ Host reads remain where the reference's result needs one: approximate
 recovery, the random-rejection counterfactual, coverage-only steps and the
 counters of the fixed-interval schedule.
 
+The Quest selector (selector="quest", cvsa/backend.py:572-620) ranks pages
+by per-page key min/max metadata that is refreshed for the pages that
+gained tokens since the previous call (ops.QuestPageMeta) rather than
+gathered from the whole cache; with light_normalizer its scores also drive
+the coverage gate, so no step reads all keys.
+
 Not implemented here (the constructor raises NotImplementedError): the
-alternative selectors of the reference (adaptive_selection,
-static_budget_table, selector="quest", top_p, light_normalizer).
+reference's other selectors (adaptive_selection, static_budget_table,
+top_p).
 """
 from __future__ import annotations
 
 from typing import Dict, List, Optional, Set, Tuple
+
+import weakref
 
 import torch
 
@@ -153,13 +161,14 @@ class CVSABackend:
         unsupported = [name for name, on in (
             ("adaptive_selection", adaptive_selection),
             ("static_budget_table", static_budget_table is not None),
-            ("selector='quest'", selector == "quest"),
-            ("top_p", top_p is not None),
-            ("light_normalizer", light_normalizer)) if on]
+            ("top_p", top_p is not None)) if on]
         if unsupported:
             raise NotImplementedError(
-                "CVSABackend on MI355X implements the exact page scorer with a uniform "
-                f"budget; not available: {', '.join(unsupported)}")
+                "CVSABackend on MI355X implements the exact and Quest page scorers with a "
+                f"uniform budget; not available: {', '.join(unsupported)}")
+        # Quest metadata per key cache (keyed by id, with a weak reference to
+        # tell a reused id from the cache it was built for).
+        self._quest_meta: Dict[int, Tuple[weakref.ref, ops.QuestPageMeta]] = {}
 
         self._last_accept_mask: Dict[int, Optional[torch.Tensor]] = {}
         self._expanded_store: Dict[int, object] = {}
@@ -238,7 +247,10 @@ class CVSABackend:
         self._step = 0
         self._reuse_state = {}
         self._reuse_plans = {}
-        self._step_plans = {}
+        # Step plans that own their selection stay: the next first selection
+        # of their layer is made in their buffers again.
+        self._step_plans = {k: p for k, p in self._step_plans.items() if p.owns_selection}
+        self._quest_meta = {}
         self._cached_selection = {}
         self._cached_page_scores = {}
         self._last_accept_mask = {}
@@ -414,9 +426,18 @@ class CVSABackend:
                 self._total_coverage_checks += 1
                 self._book_plan_gate(plan, layer_idx, context_lens)
                 return output
-        page_scores = self._time_kernel(
-            "scoring", ops.score_pages, q, k_cache, block_tables, context_lens,
-            self.num_kv_heads, self.num_q_per_kv, self.block_size)
+        else:
+            # The layer's first selection (a lazy scoring step without a
+            # cached selection, :427-465), made in the plan's own buffers.
+            plan = self._fresh_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens,
+                                    own_scores_cache=True)
+            if plan is not None:
+                output = plan.run(ops._lib.STEP_FRESH, q)
+                self._total_coverage_checks += 1
+                self._adopt_plan_selection(plan, layer_idx, context_lens, plan.scores_cache)
+                return output
+        page_scores = self._time_kernel("scoring", self._gate_scores, q, k_cache, block_tables,
+                                        context_lens)
         self._total_coverage_checks += 1
         if layer_idx in self._cached_selection:
             page_indices, n_per_head = self._cached_selection[layer_idx]
@@ -440,6 +461,35 @@ class CVSABackend:
         return self._scoring_step(q, k_cache, v_cache, block_tables, context_lens, layer_idx,
                                   page_scores=page_scores)
 
+    # ------------------------------------------------------------ scorers
+    def _quest_page_scores(self, q, k_cache, block_tables, context_lens):
+        """backend.py:572-620: Quest ranking scores [B, H_kv, W] fp32, from
+        page metadata of this key cache that is refreshed for the pages that
+        gained tokens since the previous call."""
+        entry = self._quest_meta.get(id(k_cache))
+        if entry is None or entry[0]() is not k_cache:
+            entry = (weakref.ref(k_cache), ops.QuestPageMeta(k_cache))
+            self._quest_meta[id(k_cache)] = entry
+        return entry[1].scores(q, block_tables, context_lens, self.num_kv_heads,
+                               self.num_q_per_kv, self.block_size)
+
+    def _gate_scores(self, q, k_cache, block_tables, context_lens):
+        """Scores of the coverage gate (and the cache): the Quest sketch with
+        light_normalizer, else the exact scan (backend.py:407-418, :697-709)."""
+        if self.light_normalizer:
+            return self._quest_page_scores(q, k_cache, block_tables, context_lens)
+        return ops.score_pages(q, k_cache, block_tables, context_lens, self.num_kv_heads,
+                               self.num_q_per_kv, self.block_size)
+
+    def _sel_scores(self, q, k_cache, block_tables, context_lens):
+        """Scores the selection ranks when they differ from the gate's
+        (selector="quest" without light_normalizer, backend.py:723-727), else
+        None."""
+        if self.selector != "quest" or self.light_normalizer:
+            return None
+        return self._time_kernel("scoring", self._quest_page_scores, q, k_cache, block_tables,
+                                 context_lens)
+
     # ------------------------------------------------------------ step plans
     def _matching_plan(self, layer_idx, q, k_cache, v_cache, block_tables, context_lens):
         """The layer's step plan if it fits this call and still holds the
@@ -458,11 +508,13 @@ class CVSABackend:
         return plan
 
     def _new_plan(self, layer_idx, q, k_cache, v_cache, block_tables, context_lens,
-                  page_indices=None, n_per_head=None, scores_cache=None):
+                  page_indices=None, n_per_head=None, scores_cache=None,
+                  own_scores_cache=False):
         """Build the layer's step plan, or None where a step needs the
         per-kernel path (timing, host-side decisions, unsupported buffers)."""
         if (self._track_timing or self.random_reject_prob is not None
-                or self.approx_recovery_pct is not None):
+                or self.approx_recovery_pct is not None or self.selector != "exact"
+                or self.light_normalizer):
             return None
         dev = q.device
         work = self._work(dev)
@@ -473,11 +525,43 @@ class CVSABackend:
         try:
             plan = ops.StepPlan(q, k_cache, v_cache, block_tables, context_lens,
                                 self.num_kv_heads, self.num_q_per_kv, self.block_size, budget,
-                                self.tau, page_indices, n_per_head, scores_cache, stats, work)
+                                self.tau, page_indices, n_per_head, scores_cache, stats, work,
+                                own_scores_cache=own_scores_cache)
         except (ValueError, NotImplementedError):
             return None
         self._step_plans[layer_idx] = plan
         return plan
+
+    def _fresh_plan(self, layer_idx, q, k_cache, v_cache, block_tables, context_lens,
+                    own_scores_cache=False):
+        """The layer's plan for a step that makes a new selection in the
+        plan's own buffers: the existing one if it owns its selection and fits
+        this call, else a new one (None where the per-kernel path is needed)."""
+        plan = self._step_plans.get(layer_idx)
+        if (plan is not None and not self._track_timing and plan.owns_selection
+                and (plan.scores_cache is not None) == own_scores_cache
+                and plan.matches(q, k_cache, v_cache, block_tables, context_lens,
+                                 self._work(q.device), self._dev_stats)):
+            return plan
+        if self._track_timing:
+            return None
+        return self._new_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens,
+                              own_scores_cache=own_scores_cache)
+
+    def _adopt_plan_selection(self, plan, layer_idx, context_lens, cached_scores):
+        """Bookkeeping after a plan made a new selection: it becomes the
+        layer's cached selection (and reuse state), with its gate outputs."""
+        B = plan.page_indices.shape[0]
+        accept_mask = plan.accept.view(torch.bool)
+        self._last_accept_mask[layer_idx] = accept_mask
+        self._expanded_store[layer_idx] = _PendingComplement(
+            accept_mask, plan.page_indices, plan.n_per_head, context_lens, self.block_size)
+        self._cached_page_scores[layer_idx] = cached_scores
+        self._reuse_state[layer_idx] = (plan.page_indices.view(B * self.num_kv_heads, -1),
+                                        plan.n_per_head.view(B * self.num_kv_heads),
+                                        ops.next_power_of_2(plan.budget))
+        self._reuse_plans.pop(layer_idx, None)
+        self._cached_selection[layer_idx] = (plan.page_indices, plan.n_per_head)
 
     def _lazy_plan(self, layer_idx, q, k_cache, v_cache, block_tables, context_lens):
         plan = self._matching_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens)
@@ -526,10 +610,11 @@ class CVSABackend:
         page_indices, n_per_head = self._cached_selection[layer_idx]
         budget = page_indices.shape[2]
         self._per_head_total += check_accept.numel()
+        sel_scores = self._sel_scores(q, k_cache, block_tables, context_lens)
         accept_mask = self._time_kernel(
             "coverage", ops.select_or_keep, page_scores, check_accept, budget, context_lens,
             self.block_size, self.tau, page_indices, n_per_head, coverage,
-            self._cached_page_scores.get(layer_idx), self._dev_stats)
+            self._cached_page_scores.get(layer_idx), self._dev_stats, sel_scores=sel_scores)
         self._last_accept_mask[layer_idx] = accept_mask
         output = self._time_kernel(
             "sparse_draft", ops.verified_decode, q, k_cache, v_cache, block_tables,
@@ -571,27 +656,18 @@ class CVSABackend:
         if page_scores is None and not self.lazy:
             # Fixed-interval scoring step from the layer's step plan: the
             # selection and scores live in the plan's buffers.
-            plan = self._matching_plan(layer_idx, q, k_cache, v_cache, block_tables,
-                                       context_lens)
-            if plan is None:
-                plan = self._new_plan(layer_idx, q, k_cache, v_cache, block_tables,
-                                      context_lens)
+            plan = self._fresh_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens)
             if plan is not None:
                 output = plan.run(ops._lib.STEP_SCORE, q)
-                self._book_plan_gate(plan, layer_idx, context_lens)
-                self._cached_page_scores[layer_idx] = plan.page_scores
-                self._reuse_state[layer_idx] = (plan.page_indices.view(B * self.num_kv_heads, -1),
-                                                plan.n_per_head.view(B * self.num_kv_heads),
-                                                ops.next_power_of_2(budget))
-                self._reuse_plans.pop(layer_idx, None)
-                self._cached_selection[layer_idx] = (plan.page_indices, plan.n_per_head)
+                self._per_head_total += plan.accept.numel()
+                self._adopt_plan_selection(plan, layer_idx, context_lens, plan.page_scores)
                 return output
 
         if page_scores is None:
-            page_scores = self._time_kernel(
-                "scoring", ops.score_pages, q, k_cache, block_tables, context_lens,
-                self.num_kv_heads, self.num_q_per_kv, self.block_size)
+            page_scores = self._time_kernel("scoring", self._gate_scores, q, k_cache,
+                                            block_tables, context_lens)
         self._cached_page_scores[layer_idx] = page_scores                         # :713
+        sel_scores = self._sel_scores(q, k_cache, block_tables, context_lens)      # :723-727
 
         # Top-k selection fused with the coverage gate of the new selection.
         # In the fixed-interval schedule the gate's counters (:859-863) are
@@ -608,12 +684,20 @@ class CVSABackend:
             accept_mask = self._time_kernel(
                 "coverage", ops.select_or_keep, page_scores, None, budget, context_lens,
                 self.block_size, self.tau, page_indices, n_per_head, coverage, None,
-                self._dev_stats, count_gate=True)
+                self._dev_stats, count_gate=True, sel_scores=sel_scores)
             self._per_head_total += B * H
-        else:
+        elif sel_scores is None:
             page_indices, n_per_head, accept_mask, _coverage = self._time_kernel(
                 "coverage", ops.select_topk, page_scores, budget, context_lens,
                 self.block_size, self.tau)
+        else:
+            # The selector proposes, the gate scores verify (:723-761).
+            page_indices, n_per_head = self._time_kernel(
+                "coverage", ops.select_topk, sel_scores, budget, context_lens,
+                self.block_size)
+            accept_mask, _coverage = self._time_kernel(
+                "coverage", ops.check_coverage, page_scores, page_indices, n_per_head,
+                self.tau)
         accept_mask = self._apply_random_reject(accept_mask)
         self._last_accept_mask[layer_idx] = accept_mask                           # :771
 
@@ -642,7 +726,9 @@ class CVSABackend:
                 self._per_head_total += accept_mask.numel()
         else:
             output = self._approx_recovery(q, k_cache, v_cache, block_tables, context_lens,
-                                           layer_idx, page_scores, page_indices, n_per_head,
+                                           layer_idx,
+                                           page_scores if sel_scores is None else sel_scores,
+                                           page_indices, n_per_head,
                                            accept_mask, budget, n_pages)
 
         # Reuse state and cached selection (:852-856).  The selection is
@@ -659,7 +745,8 @@ class CVSABackend:
     def _approx_recovery(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx,
                          page_scores, page_indices, n_per_head, accept_mask, budget, n_pages):
         """Approximate recovery branch (backend.py:775-817): rejected heads use
-        an expanded top-k at approx_recovery_pct of the pages."""
+        an expanded top-k at approx_recovery_pct of the pages, ranked by the
+        selection scores (``page_scores`` here)."""
         B = q.shape[0]
         n_acc = int(accept_mask.sum().item())
         all_acc = n_acc == accept_mask.numel()

@@ -36,6 +36,9 @@ __all__ = [
     "append_kv",
     "next_power_of_2",
     "StepPlan",
+    "quest_meta_update",
+    "quest_scores",
+    "QuestPageMeta",
 ]
 
 _DTYPE_CODE = {
@@ -198,7 +201,8 @@ def select_or_keep(page_scores: torch.Tensor, check_accept: Optional[torch.Tenso
                    page_indices: torch.Tensor, n_per_head: torch.Tensor,
                    coverage: torch.Tensor, scores_cache: Optional[torch.Tensor] = None,
                    stats: Optional[torch.Tensor] = None,
-                   count_gate: bool = False) -> torch.Tensor:
+                   count_gate: bool = False, *,
+                   sel_scores: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The selection decisions of CVSABackend taken on the device.
 
     With ``check_accept`` (the coverage gate of the cached selection) this is
@@ -211,6 +215,9 @@ def select_or_keep(page_scores: torch.Tensor, check_accept: Optional[torch.Tenso
     accumulates accept-all checks, rejections, scoring steps and heads that
     passed; with ``count_gate`` a fresh selection is booked as a
     fixed-interval scoring step by its own gate (backend.py:859-863).
+    With ``sel_scores`` a new selection ranks those scores while
+    ``page_scores`` drive its gate and the cache (the Quest selector with the
+    exact gate, backend.py:723-727).
     Returns the accept mask [B, H_kv] bool of the heads for this step.
     """
     dev = _device_of(page_scores, check_accept, page_indices, n_per_head, coverage)
@@ -237,10 +244,16 @@ def select_or_keep(page_scores: torch.Tensor, check_accept: Optional[torch.Tenso
         raise ValueError("select_or_keep: stats must be a contiguous int64 tensor of >= 6")
     if count_gate and (check_accept is not None or stats is None):
         raise ValueError("select_or_keep: count_gate books a fresh selection into stats")
+    if sel_scores is not None:
+        if (sel_scores.shape != ps.shape or sel_scores.dtype != torch.float32
+                or sel_scores.device != dev):
+            raise ValueError("select_or_keep: sel_scores must be float32 like page_scores")
+        sel_scores = sel_scores.contiguous()
     ctx = _i32(context_lens)
     acc = torch.empty(B, H_kv, device=dev, dtype=torch.uint8)
     check(_lib.load().cvsa_select_or_keep(
-        ps.data_ptr(), _ptr(check_accept), B, H_kv, W, ctx.data_ptr(), block_size, budget,
+        ps.data_ptr(), _ptr(sel_scores), _ptr(check_accept), B, H_kv, W, ctx.data_ptr(),
+        block_size, budget,
         page_indices.data_ptr(), n_per_head.data_ptr(), float(tau), acc.data_ptr(),
         coverage.data_ptr(), _ptr(scores_cache), _ptr(stats), 1 if count_gate else 0,
         _stream(dev)), "select_or_keep")
@@ -269,6 +282,89 @@ def check_coverage(page_scores: torch.Tensor, selected_indices: torch.Tensor,
         ps.data_ptr(), B, H_kv, W, sel.data_ptr(), sel.shape[2], nph.data_ptr(),
         float(tau), acc.data_ptr(), cov.data_ptr(), _stream(dev)), "check_coverage")
     return acc.view(torch.bool), cov
+
+
+# ---------------------------------------------------------------- Quest
+
+def quest_meta_update(k_cache: torch.Tensor, block_tables: torch.Tensor,
+                      context_lens: torch.Tensor, seen_lens: torch.Tensor, meta: torch.Tensor,
+                      seen_out: Optional[torch.Tensor] = None, all_pages: bool = False) -> None:
+    """Refresh the Quest page metadata (per block and KV head: key min and
+    max over the page's valid tokens) for the pages holding positions
+    [seen_lens, context_lens); see cvsa_quest_meta_update.  ``meta`` is
+    [num_blocks, H_kv, 2, D] bf16; ``seen_out`` receives context_lens."""
+    dev = _device_of(k_cache, block_tables, context_lens, seen_lens, meta, seen_out)
+    _check_cache(k_cache)
+    nb, bs, H, D = k_cache.shape
+    if meta.shape != (nb, H, 2, D) or meta.dtype != torch.bfloat16 or not meta.is_contiguous():
+        raise ValueError(f"meta must be a contiguous bfloat16 [{nb}, {H}, 2, {D}]")
+    bt = _block_tables(block_tables)
+    ctx = _i32(context_lens)
+    B, W = bt.shape
+    for name, t in (("seen_lens", seen_lens), ("seen_out", seen_out)):
+        if t is not None and (t.dtype != torch.int32 or t.shape != (B,) or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous int32 [{B}]")
+    check(_lib.load().cvsa_quest_meta_update(
+        k_cache.data_ptr(), nb, bt.data_ptr(), bt.stride(0), ctx.data_ptr(), seen_lens.data_ptr(),
+        _ptr(seen_out), B, H, D, bs, W, 1 if all_pages else 0, meta.data_ptr(), _stream(dev)),
+        "quest_meta_update")
+
+
+def quest_scores(q: torch.Tensor, meta: torch.Tensor, block_tables: torch.Tensor,
+                 context_lens: torch.Tensor, num_kv_heads: int, num_q_per_kv: int,
+                 block_size: int) -> torch.Tensor:
+    """Quest page scores [B, H_kv, W] fp32 from the page metadata: the
+    ranking of CVSABackend._quest_page_scores (cvsa/backend.py:572-620)."""
+    dev = _device_of(q, meta, block_tables, context_lens)
+    q = _check_q(q)
+    B, H_q, D = q.shape
+    if num_kv_heads * num_q_per_kv != H_q:
+        raise ValueError("quest_scores: head counts do not match q")
+    if meta.dim() != 4 or meta.shape[1:] != (num_kv_heads, 2, D) or meta.dtype != torch.bfloat16:
+        raise ValueError(f"meta must be bfloat16 [num_blocks, {num_kv_heads}, 2, {D}]")
+    bt = _block_tables(block_tables)
+    ctx = _i32(context_lens)
+    W = bt.shape[1]
+    out = torch.empty(B, num_kv_heads, W, device=dev, dtype=torch.float32)
+    check(_lib.load().cvsa_quest_scores(
+        q.data_ptr(), q.stride(0), q.stride(1), meta.data_ptr(), meta.shape[0], bt.data_ptr(),
+        bt.stride(0), ctx.data_ptr(), B, H_q, num_kv_heads, D, block_size, W, out.data_ptr(),
+        _stream(dev)), "quest_scores")
+    return out
+
+
+class QuestPageMeta:
+    """The Quest metadata of one paged key cache, kept current across calls.
+
+    ``scores(...)`` first refreshes the pages that gained tokens since the
+    previous call (all pages the first time, or when the batch changes),
+    then scores every page from the metadata.  The seen-lengths live on the
+    device in two buffers used in turn, so no call waits for the host.
+    Valid while keys are only appended through the cache's own page table
+    (a rewritten page needs ``invalidate()``).
+    """
+
+    def __init__(self, k_cache: torch.Tensor):
+        _check_cache(k_cache)
+        nb, _, H, D = k_cache.shape
+        self.k_cache = k_cache
+        self.meta = torch.empty(nb, H, 2, D, device=k_cache.device, dtype=torch.bfloat16)
+        self._seen = None
+
+    def invalidate(self) -> None:
+        self._seen = None
+
+    def scores(self, q, block_tables, context_lens, num_kv_heads, num_q_per_kv, block_size):
+        B = block_tables.shape[0]
+        first = self._seen is None or self._seen[0].shape[0] != B
+        if first:
+            self._seen = [torch.zeros(B, dtype=torch.int32, device=self.meta.device)
+                          for _ in range(2)]
+        quest_meta_update(self.k_cache, block_tables, context_lens, self._seen[0], self.meta,
+                          self._seen[1], all_pages=first)
+        self._seen.reverse()
+        return quest_scores(q, self.meta, block_tables, context_lens, num_kv_heads,
+                            num_q_per_kv, block_size)
 
 
 # ---------------------------------------------------------------- decode
@@ -407,20 +503,24 @@ class StepPlan:
     (cvsa/backend.py:866-881, :392-465, :683-864).
 
     The plan keeps the layer's selection (``page_indices`` [B, H_kv, budget],
-    ``n_per_head`` [B, H_kv], updated in place), the step's ``page_scores``
-    [B, H_kv, W] and gate buffers ``check_accept`` / ``accept`` /
-    ``coverage`` [B, H_kv]; every check or scoring step rewrites the latter.
+    ``n_per_head`` [B, H_kv], updated in place; allocated by the plan when
+    not given, ``owns_selection``), the step's ``page_scores`` [B, H_kv, W],
+    an optional ``scores_cache`` (the scores of the last reselection, given
+    or allocated with ``own_scores_cache``) and gate buffers ``check_accept``
+    / ``accept`` / ``coverage`` [B, H_kv]; every check or scoring step
+    rewrites the latter.  Kind STEP_FRESH makes a lazy layer's first
+    selection in the plan's buffers.
     ``matches`` tells whether a call's buffers, query layout and stream are
     the ones the plan was built for.
     """
 
     __slots__ = ("dev", "stream", "q_meta", "out_shape", "out_dtype", "refs", "page_indices",
                  "n_per_head", "page_scores", "scores_cache", "check_accept", "accept",
-                 "coverage", "budget", "_h", "_run", "_fin", "__weakref__")
+                 "coverage", "budget", "owns_selection", "_h", "_run", "_fin", "__weakref__")
 
     def __init__(self, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
                  num_q_per_kv, block_size, budget, tau, page_indices=None, n_per_head=None,
-                 scores_cache=None, stats=None, work=None):
+                 scores_cache=None, stats=None, work=None, own_scores_cache=False):
         dev = _device_of(q, k_cache, v_cache, block_tables, context_lens, page_indices,
                          n_per_head, scores_cache, stats, work)
         q = _check_q(q)
@@ -440,9 +540,12 @@ class StepPlan:
         if k_cache.shape[1] != block_size or k_cache.shape[3] != D:
             raise ValueError("step plan: cache block_size / head_dim mismatch")
         W = block_tables.shape[1]
+        self.owns_selection = page_indices is None
         if page_indices is None:
             page_indices = torch.empty(B, H, budget, dtype=torch.int32, device=dev)
             n_per_head = torch.empty(B, H, dtype=torch.int32, device=dev)
+        if own_scores_cache:
+            scores_cache = torch.empty(B, H, W, dtype=torch.float32, device=dev)
         for name, t, shape, dt in (("page_indices", page_indices, (B, H, budget), torch.int32),
                                    ("n_per_head", n_per_head, (B, H), torch.int32)):
             if tuple(t.shape) != shape or t.dtype != dt or not t.is_contiguous():

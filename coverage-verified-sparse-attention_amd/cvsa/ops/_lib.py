@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parents[1] / "libcvsa_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 CVSA_OK = 0
 CVSA_ERR_INVALID = -1
@@ -31,6 +31,7 @@ _sz = ctypes.c_size_t
 STEP_REUSE = 0
 STEP_LAZY_CHECK = 1
 STEP_SCORE = 2
+STEP_FRESH = 3
 
 
 class StepDesc(ctypes.Structure):
@@ -57,7 +58,7 @@ SIGNATURES = {
     "cvsa_select_topk": (ctypes.c_int, [
         _p, _i32, _i32, _i32, _p, _i32, _i32, _p, _p, _f32, _p, _p, _p]),
     "cvsa_select_or_keep": (ctypes.c_int, [
-        _p, _p, _i32, _i32, _i32, _p, _i32, _i32, _p, _p, _f32, _p, _p, _p, _p, _i32, _p]),
+        _p, _p, _p, _i32, _i32, _i32, _p, _i32, _i32, _p, _p, _f32, _p, _p, _p, _p, _i32, _p]),
     "cvsa_check_coverage": (ctypes.c_int, [
         _p, _i32, _i32, _i32, _p, _i64, _p, _f32, _p, _p, _p]),
     "cvsa_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
@@ -83,6 +84,10 @@ SIGNATURES = {
     "cvsa_append_kv": (ctypes.c_int, [
         _p, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p, _p,
         _i32, _i32, _i32, _i32, _i32, _i32, _p]),
+    "cvsa_quest_meta_update": (ctypes.c_int, [
+        _p, _i64, _p, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p]),
+    "cvsa_quest_scores": (ctypes.c_int, [
+        _p, _i64, _i64, _p, _i64, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p]),
     "cvsa_step_workspace_bytes": (_sz, [ctypes.POINTER(StepDesc)]),
     "cvsa_step_plan_create": (ctypes.c_int, [ctypes.POINTER(StepDesc), ctypes.POINTER(_p)]),
     "cvsa_step_plan_run": (ctypes.c_int, [_p, _i32, _p, _p, _p]),

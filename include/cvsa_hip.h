@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 2
+#define CVSA_ABI_VERSION 3
 
 enum {
   CVSA_OK = 0,
@@ -103,8 +103,12 @@ int cvsa_select_topk(const float *page_scores, int32_t B, int32_t H_kv,
  *     fixed-interval scoring step by the new selection's gate
  *     (backend.py:859-863: [2] += 1, [3] += heads accepted, [0] or [1] += 1
  *     by whether every head accepted).
+ *   sel_scores (optional, [B,H_kv,W]): scores the new selection ranks while
+ *     page_scores drive its coverage gate and scores_cache (the Quest
+ *     selector with the exact gate, backend.py:723-727); NULL = page_scores.
  */
-int cvsa_select_or_keep(const float *page_scores, const uint8_t *check_accept,
+int cvsa_select_or_keep(const float *page_scores, const float *sel_scores,
+                        const uint8_t *check_accept,
                         int32_t B, int32_t H_kv, int32_t W,
                         const int32_t *context_lens, int32_t block_size,
                         int32_t budget, int32_t *page_indices,
@@ -262,6 +266,45 @@ int cvsa_append_kv(const uint16_t *k_new, const uint16_t *v_new,
                    int32_t block_size, void *stream);
 
 /*
+ * Quest page metadata.  CVSABackend._quest_page_scores
+ * (cvsa/backend.py:572-620) needs, per page and KV head, the extremes of the
+ * keys over the page's valid tokens (:593-603); the reference recomputes
+ * them from the cache on every call, its Quest baseline keeps them per page
+ * (eval/baselines.py:77-140).  This entry point keeps them up to date:
+ *   meta: [num_blocks, H_kv, 2, D] bf16; meta[blk][h][0] = kmin,
+ *     meta[blk][h][1] = kmax over the valid tokens of the page stored in blk.
+ *   seen_lens [B] int32: context lengths at the previous update (0 before
+ *     the first).  The pages holding positions [seen, ctx) are recomputed
+ *     from k_cache (every page up to ctx when ctx < seen); seen_out [B]
+ *     (a different buffer, may be NULL) receives context_lens.
+ *   all_pages != 0 spreads a first build over the whole grid; otherwise one
+ *     workgroup per (b, kv-head) walks the pages that gained tokens.
+ * The metadata describes the keys present at the update: appending tokens
+ * (or rewriting a page) requires another update before cvsa_quest_scores.
+ */
+int cvsa_quest_meta_update(const uint16_t *k_cache, int64_t num_blocks,
+                           const int32_t *block_tables, int64_t bt_stride_b,
+                           const int32_t *context_lens, const int32_t *seen_lens,
+                           int32_t *seen_out, int32_t B, int32_t H_kv, int32_t D,
+                           int32_t block_size, int32_t W, int32_t all_pages,
+                           uint16_t *meta, void *stream);
+
+/*
+ * Quest page scores from the metadata.  Replaces
+ * CVSABackend._quest_page_scores (cvsa/backend.py:572-620):
+ *   page_scores[b,h,p] = sum_d max(q_rep_d * kmin_d, q_rep_d * kmax_d) * D^-0.5
+ *   (q_rep as in cvsa_score_pages; fp32 products and sum), -inf when
+ *   p*block_size >= context_lens[b] or the block id lies outside the pool.
+ * meta: as cvsa_quest_meta_update left it, 16-byte aligned.
+ */
+int cvsa_quest_scores(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
+                      const uint16_t *meta, int64_t num_blocks,
+                      const int32_t *block_tables, int64_t bt_stride_b,
+                      const int32_t *context_lens, int32_t B, int32_t H_q,
+                      int32_t H_kv, int32_t D, int32_t block_size, int32_t W,
+                      float *page_scores, void *stream);
+
+/*
  * Step plans: one layer's decode steps, each enqueued by a single call.
  * The native form of the per-layer step sequences of CVSABackend
  * (cvsa/backend.py): the reuse step (_reuse_step, :866-881: sparse decode of
@@ -307,7 +350,9 @@ typedef struct cvsa_step_desc {
 enum {
   CVSA_STEP_REUSE = 0,      /* sparse decode of the kept selection */
   CVSA_STEP_LAZY_CHECK = 1, /* score, check, keep or reselect, verified decode */
-  CVSA_STEP_SCORE = 2       /* score, reselect (gate booked in stats), verified decode */
+  CVSA_STEP_SCORE = 2,      /* score, reselect (gate booked in stats), verified decode */
+  CVSA_STEP_FRESH = 3       /* score, first selection of a lazy layer (booked as a lazy
+                               scoring step), verified decode */
 };
 
 typedef struct cvsa_step_plan cvsa_step_plan;

@@ -2,7 +2,9 @@
 
 Follows cvsa/backend.py of DJ-Melvin/coverage-verified-sparse-attention
 (line numbers below) for the configurations this build covers: the exact
-page scorer with a uniform budget, exact recovery (complement + LSE merge)
+page scorer or the Quest min/max scorer (selector="quest", for selection
+only or, with light_normalizer, for the coverage gate too) with a uniform
+budget, exact recovery (complement + LSE merge)
 or approximate recovery (``approx_recovery_pct``), dense layers, the fixed
 interval (``reuse_interval``) and lazy (``check_interval`` /
 ``coverage_interval``) schedules, and the statistics of get_stats().
@@ -24,7 +26,7 @@ class OracleCVSABackend:
                  budget_pct=0.10, reuse_interval=16, coverage_threshold=0.90,
                  dense_layers: Optional[List[int]] = None, lazy=False,
                  check_interval=None, coverage_interval=None, approx_recovery_pct=None,
-                 acc_dtype=torch.float64):
+                 selector="exact", light_normalizer=False, acc_dtype=torch.float64):
         # :80-115
         self.num_kv_heads = num_kv_heads
         self.num_q_heads = num_q_heads
@@ -40,6 +42,8 @@ class OracleCVSABackend:
         self.lazy = lazy
         self.check_interval = check_interval or 1
         self.coverage_interval = coverage_interval or self.check_interval
+        self.selector = selector
+        self.light_normalizer = light_normalizer
         self.acc_dtype = acc_dtype
         self.reset()
 
@@ -139,10 +143,16 @@ class OracleCVSABackend:
                                  self.num_kv_heads, self.num_q_per_kv, self.block_size,
                                  self.acc_dtype)
 
+    def _gate_scores(self, q, k_cache, block_tables, context_lens):
+        """Scores of the coverage gate: the Quest sketch with
+        light_normalizer, else the exact scan (:407-418, :697-709)."""
+        fn = ref.quest_page_scores if self.light_normalizer else ref.score_pages
+        return fn(q, k_cache, block_tables, context_lens, self.num_kv_heads, self.num_q_per_kv,
+                  self.block_size, self.acc_dtype)
+
     def _lazy_step(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
         """:392-465"""
-        page_scores = ref.score_pages(q, k_cache, block_tables, context_lens, self.num_kv_heads,
-                                      self.num_q_per_kv, self.block_size, self.acc_dtype)
+        page_scores = self._gate_scores(q, k_cache, block_tables, context_lens)
         self._total_coverage_checks += 1
         if layer_idx in self._cached_selection:
             idx, nph = self._cached_selection[layer_idx]
@@ -187,11 +197,14 @@ class OracleCVSABackend:
         nv = ref.n_valid_pages(context_lens, self.block_size)
         budget = max(3, int(n_pages * self.budget_pct))                          # :690
         if page_scores is None:
-            page_scores = ref.score_pages(q, k_cache, block_tables, context_lens,
-                                          self.num_kv_heads, self.num_q_per_kv,
-                                          self.block_size, self.acc_dtype)
+            page_scores = self._gate_scores(q, k_cache, block_tables, context_lens)
         self._cached_page_scores[layer_idx] = page_scores                        # :713
-        idx, nph = ref.select_topk(page_scores, budget, context_lens, self.block_size)
+        sel_scores = page_scores                                                 # :723-727
+        if self.selector == "quest" and not self.light_normalizer:
+            sel_scores = ref.quest_page_scores(q, k_cache, block_tables, context_lens,
+                                               self.num_kv_heads, self.num_q_per_kv,
+                                               self.block_size, self.acc_dtype)
+        idx, nph = ref.select_topk(sel_scores, budget, context_lens, self.block_size)
         o_d, m_d, l_d = ref.sparse_decode_unnorm(q, k_cache, v_cache, block_tables, idx, nph,
                                                  context_lens, self.num_kv_heads,
                                                  self.num_q_per_kv, self.block_size,
@@ -207,7 +220,7 @@ class OracleCVSABackend:
         elif self.approx_recovery_pct is not None:                               # :780-817
             exp_budget = max(budget + 1, int(n_pages * self.approx_recovery_pct))
             exp_budget = min(exp_budget, n_pages)
-            exp_idx, _ = ref.select_topk(page_scores, exp_budget, context_lens, self.block_size)
+            exp_idx, _ = ref.select_topk(sel_scores, exp_budget, context_lens, self.block_size)
             exp_nph = torch.clamp(nv, max=exp_budget).to(torch.int32).unsqueeze(1).expand(
                 B, self.num_kv_heads).contiguous()
             o_e, m_e, l_e = ref.sparse_decode_unnorm(q, k_cache, v_cache, block_tables, exp_idx,
@@ -247,7 +260,8 @@ class OracleCVSABackend:
             self._per_head_total += accept.numel()
         self.trace.append({"layer": layer_idx, "kind": kind, "accept": accept.clone(),
                            "coverage": cov.clone(), "page_indices": idx.clone(),
-                           "n_per_head": nph.clone(), "page_scores": page_scores})
+                           "n_per_head": nph.clone(), "page_scores": page_scores,
+                           "sel_scores": sel_scores})
         return out
 
     def _reuse_step(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):

@@ -93,6 +93,52 @@ def score_pages(q, k_cache, block_tables, context_lens, num_kv_heads, num_q_per_
     return out
 
 
+def page_key_minmax(k_cache, block_tables, context_lens, block_size):
+    """Per (b, page, kv-head) min and max of the keys over the page's valid
+    tokens (positions < ctx), the metadata of CVSABackend._quest_page_scores
+    (cvsa/backend.py:593-603) and of the Quest baseline
+    (eval/baselines.py:77-117).  Returns (kmin, kmax) [B, W, H_kv, D] fp32,
+    +inf / -inf where a page has no valid token."""
+    B, W = block_tables.shape
+    nb, bs, H, D = k_cache.shape
+    kmin = torch.full((B, W, H, D), float("inf"), dtype=torch.float32)
+    kmax = torch.full((B, W, H, D), float("-inf"), dtype=torch.float32)
+    for b in range(B):
+        ctx = int(context_lens[b])
+        for p in range(W):
+            n = min(block_size, ctx - p * block_size)
+            phys = int(block_tables[b, p])
+            if n <= 0 or not 0 <= phys < nb:
+                continue
+            keys = k_cache[phys, :n].to(torch.float32)            # [n, H, D]
+            kmin[b, p] = keys.amin(dim=0)
+            kmax[b, p] = keys.amax(dim=0)
+    return kmin, kmax
+
+
+def quest_page_scores(q, k_cache, block_tables, context_lens, num_kv_heads, num_q_per_kv,
+                      block_size, acc_dtype=torch.float64) -> torch.Tensor:
+    """CVSABackend._quest_page_scores (cvsa/backend.py:572-620).
+
+    score[b,h,p] = sum_d max(q_rep_d * kmin_d, q_rep_d * kmax_d) * D^-0.5 over
+    the page's valid tokens (the Quest upper bound of the page's max dot
+    product), q_rep the bf16 group mean (:606-607), -inf for pages without a
+    valid token (:616-618).  Block ids outside the pool give -inf (the
+    reference would index its cache with them)."""
+    B, H_q, D = q.shape
+    W = block_tables.shape[1]
+    q_rep = group_mean_bf16(q, num_kv_heads, num_q_per_kv).to(acc_dtype)   # [B, H, D]
+    kmin, kmax = page_key_minmax(k_cache, block_tables, context_lens, block_size)
+    qb = q_rep.unsqueeze(1)                                                # [B, 1, H, D]
+    with torch.no_grad():
+        lo = qb * kmin.to(acc_dtype).nan_to_num(posinf=0.0)
+        hi = qb * kmax.to(acc_dtype).nan_to_num(neginf=0.0)
+        upper = torch.maximum(lo, hi).sum(dim=-1) * fp32_scale(D)          # [B, W, H]
+    out = upper.to(torch.float32).transpose(1, 2).contiguous()             # [B, H, W]
+    valid = torch.isfinite(kmax[..., 0]).transpose(1, 2)                   # [B, H, W]
+    return out.masked_fill(~valid, float("-inf"))
+
+
 # ---------------------------------------------------------------- selection
 
 def select_topk(page_scores: torch.Tensor, budget: int, context_lens: torch.Tensor,

@@ -125,7 +125,8 @@ def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, max_margin_frac=
         if scoring:
             t = scoring[-1]
             budget = t["page_indices"].shape[-1]
-            bad_sel, bad_acc = _margins(t["page_scores"], budget, t["coverage"], kw.get(
+            ranked = t.get("sel_scores", t["page_scores"])   # what the selection ranks
+            bad_sel, bad_acc = _margins(ranked, budget, t["coverage"], kw.get(
                 "coverage_threshold", 0.9))
             margin_sel += int(bad_sel.sum())
             margin_acc += int(bad_acc.sum())
@@ -133,7 +134,7 @@ def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, max_margin_frac=
             pi, nph = gpu_b._cached_selection[0]
             ok = ~bad_sel
             assert torch.equal(pi.cpu()[ok], t["page_indices"][ok]), step
-            _check_near_tie_selection(pi.cpu(), nph.cpu(), t["page_scores"], budget, bad_sel)
+            _check_near_tie_selection(pi.cpu(), nph.cpu(), ranked, budget, bad_sel)
             assert torch.equal(nph.cpu(), t["n_per_head"])
             acc = gpu_b._last_accept_mask[0].cpu()
             ok = ~bad_acc

@@ -77,6 +77,43 @@ def test_plan_kinds_equal_separate_kernels(gpu, tau):
     assert torch.equal(stats_p, stats_r) and torch.equal(work_p, work_r)
 
 
+@pytest.mark.parametrize("tau", [0.0, 0.995])
+def test_fresh_kind_equals_separate_kernels(gpu, tau):
+    """A plan that owns its selection and scores cache: the first selection
+    of a lazy layer (score, fresh select booked as a scoring step, verified
+    decode), twice in a row in the same buffers."""
+    inp, W, budget = _inputs(gpu)
+    ctx, bt = inp.context_lens, inp.block_tables
+    stats_p = torch.zeros(6, dtype=torch.int64, device=gpu)
+    stats_r = torch.zeros(6, dtype=torch.int64, device=gpu)
+    work_p = torch.zeros(2, dtype=torch.int64, device=gpu)
+    work_r = torch.zeros(2, dtype=torch.int64, device=gpu)
+    plan = ops.StepPlan(inp.q, inp.k_cache, inp.v_cache, bt, ctx, H, G, 16, budget, tau,
+                        stats=stats_p, work=work_p, own_scores_cache=True)
+    assert plan.owns_selection and plan.scores_cache is not None
+    for seed in (6, 7):
+        q1 = jitter_query(inp.q, 0.5, seed)
+        got = plan.run(_lib.STEP_FRESH, q1)
+        ps = ops.score_pages(q1, inp.k_cache, bt, ctx, H, G, 16)
+        sel_r = torch.empty(2, H, budget, dtype=torch.int32, device=gpu)
+        nph_r = torch.empty(2, H, dtype=torch.int32, device=gpu)
+        cov = torch.empty(2, H, dtype=torch.float32, device=gpu)
+        cache_r = torch.empty_like(ps)
+        acc = ops.select_or_keep(ps, None, budget, ctx, 16, tau, sel_r, nph_r, cov, cache_r,
+                                 stats_r)
+        want = ops.verified_decode(q1, inp.k_cache, inp.v_cache, bt, ctx, sel_r, nph_r, acc,
+                                   H, G, 16, output_dtype=q1.dtype, work=work_r)
+        assert torch.equal(got, want), seed
+        assert torch.equal(plan.page_scores, ps)
+        assert torch.equal(plan.scores_cache, cache_r)
+        assert torch.equal(plan.accept.view(torch.bool), acc)
+        assert torch.equal(plan.coverage, cov)
+        assert torch.equal(plan.page_indices, sel_r) and torch.equal(plan.n_per_head, nph_r)
+        assert torch.equal(stats_p, stats_r) and torch.equal(work_p, work_r)
+    # each call booked as one rejection and one scoring step
+    assert stats_p[1].item() == 2 and stats_p[2].item() == 2
+
+
 def test_plan_rejects_buffers_it_cannot_use(gpu):
     inp, W, budget = _inputs(gpu)
     args = (inp.q, inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens, H, G, 16)
@@ -114,6 +151,11 @@ def test_backend_plans_equal_kernel_path(gpu, kw):
     kern_b.enable_timing(True)
     g = torch.Generator().manual_seed(5)
     for step in range(steps):
+        if step == 6:
+            # plans that own their selection outlive a reset
+            kept = plan_b._step_plans.get(0)
+            plan_b.reset()
+            kern_b.reset()
         q = jitter_query(inp.q, 0.3, 700 + step).to(gpu)
         a = plan_b(q, rt_a.cache.k_cache, rt_a.cache.v_cache, rt_a.mgr.block_tables,
                    rt_a.mgr.context_lens, 0)
@@ -129,6 +171,7 @@ def test_backend_plans_equal_kernel_path(gpu, kw):
         rt_a.mgr.append_tokens_kv(kn, vn)
         rt_b.mgr.append_tokens_kv(kn, vn)
     assert 0 in plan_b._step_plans and not kern_b._step_plans
+    assert kept is not None and plan_b._step_plans[0] is kept
     sa, sb = plan_b.get_stats(), kern_b.get_stats()
     for k in sa:
         assert sa[k] == sb[k], (k, sa[k], sb[k])
