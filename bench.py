@@ -175,16 +175,17 @@ def step_bytes(kind, accept, cfg, W, budget):
     page_kv = BS * D * 2            # one page of one head, K or V
     q_bytes = out_bytes = B * Hq * D * 2
     scores = B * H * W * 4
-    meta = B * H * n_valid * 2 * D * 2  # Quest kmin + kmax of every valid page
+    meta = B * H * n_valid * (2 * D * 2 + 4)  # Quest kmin + kmax + token count per valid page
     quest, ln = cfg.get("selector") == "quest", cfg.get("light_normalizer", False)
     total = 0
     if kind in ("score", "check", "rescore"):
         scan = meta if ln else B * ctx * H * D * 2                      # Quest metadata or K
         total += scan + q_bytes + 4 * B * W + scores                   # scan, q, table, write
-        if quest and not ln:
+        ranks = quest and not ln and kind != "check"   # a kept selection needs no ranking
+        if ranks:
             total += meta + q_bytes + 4 * B * W + scores               # ranking scores too
-        if quest and cfg["append"]:
-            total += B * H * (page_kv + 2 * D * 2)                     # metadata refresh
+        if (ln or ranks) and cfg["append"]:
+            total += B * H * (page_kv + 2 * D * 2 + 4)                 # metadata refresh
     if kind in ("check", "rescore"):
         total += scores + 4 * n_sel * B * H                           # coverage of cached sel
     if kind in ("score", "rescore"):
@@ -457,7 +458,7 @@ def main():
 
     def run_quest(i):
         k, v, bt, cl, q = lay(i)[:5]
-        ops.quest_scores(q, metas[i % L].meta, bt, cl, H_kv, G, BS)
+        metas[i % L].scores(q, bt, cl, H_kv, G, BS)
 
     n_smp = args.kernel_samples
     score_us = time_kernel(run_score, n_smp)
@@ -478,7 +479,7 @@ def main():
     kernels = {
         "score_pages": {"us": score_us, "bytes": score_bytes},
         **({"quest_scores": {"us": time_kernel(run_quest, n_smp),
-                             "bytes": n_valid * B * H_kv * 2 * D * 2 + B * H_q * D * 2
+                             "bytes": n_valid * B * H_kv * (2 * D * 2 + 4) + B * H_q * D * 2
                              + 4 * B * W + B * H_kv * W * 4}} if metas else {}),
         "select_topk+coverage": {"us": sel_us, "bytes": 2 * B * H_kv * W * 4},
         "sparse_decode(reuse)": {"us": reuse_us, "bytes": reuse_bytes},

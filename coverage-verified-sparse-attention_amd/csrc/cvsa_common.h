@@ -67,14 +67,28 @@ __device__ __forceinline__ uint4 group_mean_q(const uint16_t *__restrict__ q, in
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  for (int g = 0; g < G; ++g) {
-    const uint4 v = *reinterpret_cast<const uint4 *>(q + b * q_sb + (int64_t)(h * G + g) * q_sh +
-                                                     seg * 8);
-    acc[0] += bf16_lo(v.x); acc[1] += bf16_hi(v.x);
-    acc[2] += bf16_lo(v.y); acc[3] += bf16_hi(v.y);
-    acc[4] += bf16_lo(v.z); acc[5] += bf16_hi(v.z);
-    acc[6] += bf16_lo(v.w); acc[7] += bf16_hi(v.w);
-  }
+  // Four rows per batch are loaded before any is summed (one load latency
+  // per batch); the sum still runs over g in order.  The first batch is
+  // outside the loop, so loads the caller issued earlier are not waited for
+  // at a loop entry.
+  const uint16_t *base = q + b * q_sb + (int64_t)h * G * q_sh + seg * 8;
+  auto batch = [&](int g0) {
+    uint4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      v[j] = *reinterpret_cast<const uint4 *>(base + (int64_t)min(g0 + j, G - 1) * q_sh);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (g0 + j < G) {
+        acc[0] += bf16_lo(v[j].x); acc[1] += bf16_hi(v[j].x);
+        acc[2] += bf16_lo(v[j].y); acc[3] += bf16_hi(v[j].y);
+        acc[4] += bf16_lo(v[j].z); acc[5] += bf16_hi(v[j].z);
+        acc[6] += bf16_lo(v[j].w); acc[7] += bf16_hi(v[j].w);
+      }
+    }
+  };
+  batch(0);
+  for (int g0 = 4; g0 < G; g0 += 4) batch(g0);
   uint4 r;
   r.x = pack_bf16x2(acc[0] * inv_g, acc[1] * inv_g);
   r.y = pack_bf16x2(acc[2] * inv_g, acc[3] * inv_g);

@@ -7,76 +7,78 @@
 // token score -inf.  The reference gathers every page's keys on every call.
 // Here the extremes are kept as page metadata (as the reference's Quest
 // baseline does, eval/baselines.py:77-140) and refreshed only for the pages
-// that gained tokens, so a scoring pass reads 512 B per page and head
-// instead of the 4 KiB of keys.
+// whose valid-token count changed, so a scoring pass reads 512 B per page
+// and head instead of the 4 KiB of keys.
 //
 // Metadata layout: meta[block][h][0][d] = kmin, meta[block][h][1][d] = kmax,
-// bf16 (exact: they are key values), indexed by physical block.
+// bf16 (exact: they are key values), indexed by physical block;
+// meta_ntok[block][h] int32 = the number of leading tokens of the block the
+// extremes cover (0: none).  A page is recomputed when its valid-token count
+// under the current context differs from meta_ntok, by the wave that scores
+// it, which also writes the new count.
 #include "cvsa_common.h"
 
 namespace cvsa {
 
-constexpr int kQuestPagesPerWave = 4;  // a wave scores 4 pages per step: 16 lanes each
-
-// One wave per (page, kv-head): lane l owns dimensions 2l, 2l+1 of the
-// page's valid token rows (each load instruction reads one whole 256-byte
-// row), and writes their min and max.
-__global__ __launch_bounds__(256) void quest_meta_kernel(
-    const uint16_t *__restrict__ k_cache, int64_t num_blocks,
-    const int32_t *__restrict__ block_tables, int64_t bt_sb,
-    const int32_t *__restrict__ context_lens, const int32_t *__restrict__ seen_lens,
-    int32_t *__restrict__ seen_out, int H_kv, int W, uint16_t *__restrict__ meta) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int bh = blockIdx.y;
-  const int b = bh / H_kv;
-  const int h = bh - b * H_kv;
-  const int ctx = __builtin_amdgcn_readfirstlane(context_lens[b]);
-  const int seen = __builtin_amdgcn_readfirstlane(seen_lens[b]);
-  if (seen_out != nullptr && h == 0 && blockIdx.x == 0 && threadIdx.x == 0) seen_out[b] = ctx;
-  if (ctx <= 0 || ctx == seen) return;
-  // Pages holding positions [seen, ctx); all pages when the context shrank.
-  const int p_lo = ctx > seen ? seen / kPageTokens : 0;
-  const int p_hi = min((ctx - 1) / kPageTokens, W - 1);
-  const int stride = gridDim.x * 4;
-  const int64_t row_stride = (int64_t)H_kv * kHeadDim;                 // between tokens
-  const int64_t page_elems = (int64_t)kPageTokens * row_stride;       // between blocks
-  for (int p = p_lo + blockIdx.x * 4 + wave; p <= p_hi; p += stride) {
-    const int phys = __builtin_amdgcn_readfirstlane(block_tables[b * bt_sb + p]);
-    if (phys < 0 || phys >= num_blocks) continue;  // uniform
-    const int ntok = min(kPageTokens, ctx - p * kPageTokens);
-    const uint32_t *src = reinterpret_cast<const uint32_t *>(
-        k_cache + (int64_t)phys * page_elems + (int64_t)h * kHeadDim) + lane;
-    uint32_t w[kPageTokens];
+// Extremes of 8 dimensions (one 16-byte segment) of a page's valid token
+// rows, packed as bf16 like the metadata; rows past the last valid one
+// repeat it.
+__device__ __forceinline__ void segment_minmax(const uint16_t *__restrict__ rows,
+                                               int64_t row_stride, int ntok, uint4 &mn,
+                                               uint4 &mx) {
+  uint4 r[kPageTokens];
 #pragma unroll
-    for (int t = 0; t < kPageTokens; ++t)
-      w[t] = src[(int64_t)min(t, ntok - 1) * (row_stride / 2)];
-    float lo0 = bf16_lo(w[0]), hi0 = lo0, lo1 = bf16_hi(w[0]), hi1 = lo1;
+  for (int t = 0; t < kPageTokens; ++t)
+    r[t] = *reinterpret_cast<const uint4 *>(rows + (int64_t)min(t, ntok - 1) * row_stride);
+  float lo[8], hi[8];
+  const uint32_t w0[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
 #pragma unroll
-    for (int t = 1; t < kPageTokens; ++t) {
-      const float x0 = bf16_lo(w[t]), x1 = bf16_hi(w[t]);
-      lo0 = fminf(lo0, x0);
-      hi0 = fmaxf(hi0, x0);
-      lo1 = fminf(lo1, x1);
-      hi1 = fmaxf(hi1, x1);
-    }
-    // The extremes are key values, so their top 16 bits are the bf16 bits.
-    uint32_t *dst = reinterpret_cast<uint32_t *>(meta + ((int64_t)phys * H_kv + h) * 2 * kHeadDim);
-    dst[lane] = (__float_as_uint(lo0) >> 16) | (__float_as_uint(lo1) & 0xffff0000u);
-    dst[kHeadDim / 2 + lane] = (__float_as_uint(hi0) >> 16) | (__float_as_uint(hi1) & 0xffff0000u);
+  for (int i = 0; i < 4; ++i) {
+    lo[2 * i] = hi[2 * i] = bf16_lo(w0[i]);
+    lo[2 * i + 1] = hi[2 * i + 1] = bf16_hi(w0[i]);
   }
+#pragma unroll
+  for (int t = 1; t < kPageTokens; ++t) {
+    const uint32_t w[4] = {r[t].x, r[t].y, r[t].z, r[t].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo[2 * i] = fminf(lo[2 * i], bf16_lo(w[i]));
+      hi[2 * i] = fmaxf(hi[2 * i], bf16_lo(w[i]));
+      lo[2 * i + 1] = fminf(lo[2 * i + 1], bf16_hi(w[i]));
+      hi[2 * i + 1] = fmaxf(hi[2 * i + 1], bf16_hi(w[i]));
+    }
+  }
+  // The extremes are key values, so their top 16 bits are the bf16 bits.
+  auto pack = [](float a, float b) {
+    return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xffff0000u);
+  };
+  mn = make_uint4(pack(lo[0], lo[1]), pack(lo[2], lo[3]), pack(lo[4], lo[5]), pack(lo[6], lo[7]));
+  mx = make_uint4(pack(hi[0], hi[1]), pack(hi[2], hi[3]), pack(hi[4], hi[5]), pack(hi[6], hi[7]));
 }
 
-// One wave per (b, kv-head, run of pages): lanes 16j .. 16j+15 take page j
-// of each group of four, lane seg = l % 16 holds dimensions 8seg .. 8seg+7
-// (16 bytes of kmin and 16 of kmax, read whole by the 16 lanes) and q_rep's
-// matching segment; the 16-lane sum is formed with DPP.
+// One wave per (b, kv-head, run of ppw pages, a multiple of 16): lanes
+// 16j .. 16j+15 take page j of each group of four; lane seg = l % 16 holds
+// dimensions 8seg .. 8seg+7 (16 bytes of kmin and 16 of kmax, read whole by
+// the 16 lanes) and q_rep's matching segment; the 16-lane sum is formed with
+// DPP.  Sixteen pages are in flight per wave: their block-table entries are
+// read first, then their metadata, so each run of 16 pays two load
+// latencies.
+//
+// REFRESH: pages whose valid-token count differs from meta_ntok are
+// recomputed from k_cache, written back (extremes and count) and scored
+// from the new values.  SCORE: write the scores (else only refresh).
+// check_accept (optional, n_heads flags): when every flag is set the
+// launch does nothing; a lazy check that kept its selection needs no
+// ranking scores.
+template <bool REFRESH, bool SCORE>
 __global__ __launch_bounds__(256) void quest_scores_kernel(
-    const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh,
-    const uint16_t *__restrict__ meta, int64_t num_blocks,
+    const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh, uint16_t *__restrict__ meta,
+    int32_t *__restrict__ meta_ntok, int64_t num_blocks,
     const int32_t *__restrict__ block_tables, int64_t bt_sb,
-    const int32_t *__restrict__ context_lens, int H_kv, int G, float inv_g, float scale,
-    int W, int ppw, float *__restrict__ scores) {
+    const int32_t *__restrict__ context_lens, const uint16_t *__restrict__ k_cache,
+    const uint8_t *__restrict__ check_accept, int n_heads, int H_kv, int G, float inv_g,
+    float scale, int W, int ppw, float *__restrict__ scores) {
+  constexpr int kIter = 4;  // groups of four pages per run of sixteen
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int bh = blockIdx.y;
@@ -86,34 +88,87 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
   if (p0 >= W) return;
   const int seg = lane & 15;
   const int sub = lane >> 4;
-  const int ctx = __builtin_amdgcn_readfirstlane(context_lens[b]);
-  const uint4 qv = group_mean_q(q, q_sb, q_sh, b, h, G, seg, inv_g);
-  float qf[8];
-  qf[0] = bf16_lo(qv.x); qf[1] = bf16_hi(qv.x);
-  qf[2] = bf16_lo(qv.y); qf[3] = bf16_hi(qv.y);
-  qf[4] = bf16_lo(qv.z); qf[5] = bf16_hi(qv.z);
-  qf[6] = bf16_lo(qv.w); qf[7] = bf16_hi(qv.w);
-  float *out = scores + (int64_t)bh * W;
   const int p_end = min(W, p0 + ppw);
-  for (int pb = p0; pb < p_end; pb += kQuestPagesPerWave) {
-    const int p = pb + sub;
-    const bool in_row = p < p_end;
-    const int pc = in_row ? p : p_end - 1;
-    const int phys = block_tables[b * bt_sb + pc];
-    const bool valid = in_row && pc * kPageTokens < ctx && phys >= 0 && phys < num_blocks;
-    const uint16_t *m = meta + ((int64_t)(valid ? phys : 0) * H_kv + h) * 2 * kHeadDim + 8 * seg;
-    const uint4 mn = *reinterpret_cast<const uint4 *>(m);
-    const uint4 mx = *reinterpret_cast<const uint4 *>(m + kHeadDim);
-    const uint32_t lo[4] = {mn.x, mn.y, mn.z, mn.w};
-    const uint32_t hi[4] = {mx.x, mx.y, mx.z, mx.w};
-    float acc = 0.f;
+  // Block-table entries of the next run of 16 pages: the first run's are
+  // requested before the check flags and the query rows, so their
+  // latencies overlap.
+  int phys[kIter];
+  auto load_phys = [&](int pb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc += fmaxf(qf[2 * i] * bf16_lo(lo[i]), qf[2 * i] * bf16_lo(hi[i]));
-      acc += fmaxf(qf[2 * i + 1] * bf16_hi(lo[i]), qf[2 * i + 1] * bf16_hi(hi[i]));
+    for (int i = 0; i < kIter; ++i)
+      phys[i] = block_tables[b * bt_sb + min(pb + 4 * i + sub, p_end - 1)];
+  };
+  load_phys(p0);
+  if (check_accept != nullptr) {
+    int bad = 0;
+    for (int i = lane; i < n_heads; i += 64) bad |= check_accept[i] == 0;
+    if (__ballot(bad) == 0) return;
+  }
+  const int ctx = __builtin_amdgcn_readfirstlane(context_lens[b]);
+  float qf[8];
+  if (SCORE) {
+    const uint4 qv = group_mean_q(q, q_sb, q_sh, b, h, G, seg, inv_g);
+    qf[0] = bf16_lo(qv.x); qf[1] = bf16_hi(qv.x);
+    qf[2] = bf16_lo(qv.y); qf[3] = bf16_hi(qv.y);
+    qf[4] = bf16_lo(qv.z); qf[5] = bf16_hi(qv.z);
+    qf[6] = bf16_lo(qv.w); qf[7] = bf16_hi(qv.w);
+  }
+  const int64_t row_stride = (int64_t)H_kv * kHeadDim;  // between tokens of a block
+  for (int pb = p0; pb < p_end; pb += kIter * 4) {
+    bool valid[kIter];
+#pragma unroll
+    for (int i = 0; i < kIter; ++i) {
+      const int p = pb + 4 * i + sub;
+      valid[i] = p < p_end && p * kPageTokens < ctx && phys[i] >= 0 && phys[i] < num_blocks;
     }
-    acc = group_sum<16>(acc) * scale;
-    if (seg == 0 && in_row) out[p] = valid ? acc : -INFINITY;
+    uint4 mn[kIter], mx[kIter];
+    int have[kIter];
+#pragma unroll
+    for (int i = 0; i < kIter; ++i) {
+      const int64_t slot = (int64_t)(valid[i] ? phys[i] : 0) * H_kv + h;
+      if (SCORE) {
+        const uint16_t *m = meta + slot * 2 * kHeadDim + 8 * seg;
+        mn[i] = *reinterpret_cast<const uint4 *>(m);
+        mx[i] = *reinterpret_cast<const uint4 *>(m + kHeadDim);
+      }
+      if (REFRESH) have[i] = meta_ntok[slot];
+    }
+    const int cur[kIter] = {phys[0], phys[1], phys[2], phys[3]};
+    if (pb + kIter * 4 < p_end) load_phys(pb + kIter * 4);
+    if (REFRESH) {
+#pragma unroll
+      for (int i = 0; i < kIter; ++i) {
+        const int p = pb + 4 * i + sub;
+        const int ntok = min(kPageTokens, ctx - p * kPageTokens);
+        if (valid[i] && have[i] != ntok) {
+          const int64_t slot = (int64_t)cur[i] * H_kv + h;
+          segment_minmax(k_cache + (int64_t)cur[i] * kPageTokens * row_stride +
+                             (int64_t)h * kHeadDim + 8 * seg,
+                         row_stride, ntok, mn[i], mx[i]);
+          uint16_t *m = meta + slot * 2 * kHeadDim + 8 * seg;
+          *reinterpret_cast<uint4 *>(m) = mn[i];
+          *reinterpret_cast<uint4 *>(m + kHeadDim) = mx[i];
+          if (seg == 0) meta_ntok[slot] = ntok;
+        }
+      }
+    }
+    if (SCORE) {
+      float *out = scores + (int64_t)bh * W;
+#pragma unroll
+      for (int i = 0; i < kIter; ++i) {
+        const int p = pb + 4 * i + sub;
+        const uint32_t lo[4] = {mn[i].x, mn[i].y, mn[i].z, mn[i].w};
+        const uint32_t hi[4] = {mx[i].x, mx[i].y, mx[i].z, mx[i].w};
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc += fmaxf(qf[2 * e] * bf16_lo(lo[e]), qf[2 * e] * bf16_lo(hi[e]));
+          acc += fmaxf(qf[2 * e + 1] * bf16_hi(lo[e]), qf[2 * e + 1] * bf16_hi(hi[e]));
+        }
+        acc = group_sum<16>(acc) * scale;
+        if (seg == 0 && p < p_end) out[p] = valid[i] ? acc : -INFINITY;
+      }
+    }
   }
 }
 
@@ -121,34 +176,64 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
 
 using namespace cvsa;
 
+namespace {
+
+// Pages per wave: 16, or up to 64 while >= 4096 waves remain in the launch.
+dim3 quest_grid(int B, int H_kv, int W, int &ppw) {
+  const int64_t rows = (int64_t)B * H_kv;
+  ppw = 16;
+  while (ppw < 64 && rows * W / (2 * ppw) >= 4096) ppw *= 2;
+  const int waves = (W + ppw - 1) / ppw;
+  return dim3((waves + 3) / 4, B * H_kv);
+}
+
+int check_quest_sizes(const char *name, int32_t B, int32_t H_kv, int32_t D, int32_t block_size,
+                      int32_t W, int64_t num_blocks, int64_t bt_stride_b, const void *meta) {
+  CVSA_REQUIRE(B > 0 && H_kv > 0 && (int64_t)B * H_kv <= 65535 && W > 0 && num_blocks > 0,
+               CVSA_ERR_INVALID, "%s: bad sizes B=%d H_kv=%d W=%d", name, B, H_kv, W);
+  CVSA_REQUIRE(D == kHeadDim && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
+               "%s: only D=128, block_size=16 are supported (got D=%d, bs=%d)", name, D,
+               block_size);
+  CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
+               kMaxPages);
+  CVSA_REQUIRE(bt_stride_b >= W, CVSA_ERR_INVALID, "%s: block-table row stride %lld < W=%d",
+               name, (long long)bt_stride_b, W);
+  CVSA_REQUIRE(((uintptr_t)meta & 15) == 0, CVSA_ERR_INVALID, "%s: meta must be 16-byte aligned",
+               name);
+  return CVSA_OK;
+}
+
+int check_quest_q(const char *name, const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
+                  int32_t H_q, int32_t H_kv) {
+  CVSA_REQUIRE(H_q > 0 && H_q % H_kv == 0, CVSA_ERR_INVALID,
+               "%s: H_q=%d is not a multiple of H_kv=%d", name, H_q, H_kv);
+  CVSA_REQUIRE(((uintptr_t)q & 15) == 0 && q_stride_b % 8 == 0 && q_stride_h % 8 == 0,
+               CVSA_ERR_INVALID,
+               "%s: q must be 16-byte aligned with strides that are multiples of 8 elements",
+               name);
+  return CVSA_OK;
+}
+
+}  // namespace
+
 extern "C" int cvsa_quest_meta_update(const uint16_t *k_cache, int64_t num_blocks,
                                       const int32_t *block_tables, int64_t bt_stride_b,
-                                      const int32_t *context_lens, const int32_t *seen_lens,
-                                      int32_t *seen_out, int32_t B, int32_t H_kv, int32_t D,
-                                      int32_t block_size, int32_t W, int32_t all_pages,
-                                      uint16_t *meta, void *stream) {
-  CVSA_REQUIRE(k_cache && block_tables && context_lens && seen_lens && meta, CVSA_ERR_INVALID,
-               "quest_meta_update: null pointer argument");
-  CVSA_REQUIRE((const void *)seen_out != (const void *)seen_lens, CVSA_ERR_INVALID,
-               "quest_meta_update: seen_out must not alias seen_lens");
-  CVSA_REQUIRE(B > 0 && B <= 65535 && H_kv > 0 && (int64_t)B * H_kv <= 65535 && W > 0 &&
-                   num_blocks > 0,
-               CVSA_ERR_INVALID, "quest_meta_update: bad sizes B=%d H_kv=%d W=%d", B, H_kv, W);
-  CVSA_REQUIRE(D == kHeadDim && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
-               "quest_meta_update: only D=128, block_size=16 are supported (got D=%d, bs=%d)",
-               D, block_size);
-  CVSA_REQUIRE(bt_stride_b >= W, CVSA_ERR_INVALID,
-               "quest_meta_update: block-table row stride %lld < W=%d", (long long)bt_stride_b,
-               W);
-  CVSA_REQUIRE(((uintptr_t)k_cache & 3) == 0 && ((uintptr_t)meta & 15) == 0, CVSA_ERR_INVALID,
-               "quest_meta_update: k_cache must be 4-byte and meta 16-byte aligned");
-  // all_pages: a workgroup (4 waves) per 4 pages of every row, for a first
-  // build; otherwise one workgroup per (b, kv-head) walks its new pages.
-  const int chunks = all_pages ? (W + 3) / 4 : 1;
-  hipLaunchKernelGGL(quest_meta_kernel, dim3(chunks, B * H_kv), dim3(256), 0,
-                     (hipStream_t)stream, k_cache, num_blocks, block_tables, bt_stride_b,
-                     context_lens, seen_lens, seen_out, H_kv, W, meta);
-  return cvsa_host::check_launch("quest_meta_update");
+                                      const int32_t *context_lens, int32_t B, int32_t H_kv,
+                                      int32_t D, int32_t block_size, int32_t W, uint16_t *meta,
+                                      int32_t *meta_ntok, void *stream) {
+  static const char *name = "quest_meta_update";
+  CVSA_REQUIRE(k_cache && block_tables && context_lens && meta && meta_ntok, CVSA_ERR_INVALID,
+               "%s: null pointer argument", name);
+  int rc = check_quest_sizes(name, B, H_kv, D, block_size, W, num_blocks, bt_stride_b, meta);
+  if (rc != CVSA_OK) return rc;
+  CVSA_REQUIRE(((uintptr_t)k_cache & 15) == 0, CVSA_ERR_INVALID,
+               "%s: k_cache must be 16-byte aligned", name);
+  int ppw;
+  const dim3 grid = quest_grid(B, H_kv, W, ppw);
+  hipLaunchKernelGGL((quest_scores_kernel<true, false>), grid, dim3(256), 0, (hipStream_t)stream,
+                     nullptr, 0, 0, meta, meta_ntok, num_blocks, block_tables, bt_stride_b,
+                     context_lens, k_cache, nullptr, 0, H_kv, 1, 1.0f, 1.0f, W, ppw, nullptr);
+  return cvsa_host::check_launch(name);
 }
 
 extern "C" int cvsa_quest_scores(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
@@ -157,33 +242,45 @@ extern "C" int cvsa_quest_scores(const uint16_t *q, int64_t q_stride_b, int64_t 
                                  const int32_t *context_lens, int32_t B, int32_t H_q,
                                  int32_t H_kv, int32_t D, int32_t block_size, int32_t W,
                                  float *page_scores, void *stream) {
+  static const char *name = "quest_scores";
   CVSA_REQUIRE(q && meta && block_tables && context_lens && page_scores, CVSA_ERR_INVALID,
-               "quest_scores: null pointer argument");
-  CVSA_REQUIRE(B > 0 && H_kv > 0 && (int64_t)B * H_kv <= 65535 && W > 0 && num_blocks > 0,
-               CVSA_ERR_INVALID, "quest_scores: bad sizes B=%d H_kv=%d W=%d", B, H_kv, W);
-  CVSA_REQUIRE(H_q > 0 && H_q % H_kv == 0, CVSA_ERR_INVALID,
-               "quest_scores: H_q=%d is not a multiple of H_kv=%d", H_q, H_kv);
-  CVSA_REQUIRE(D == kHeadDim && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
-               "quest_scores: only D=128, block_size=16 are supported (got D=%d, bs=%d)", D,
-               block_size);
-  CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "quest_scores: W=%d exceeds %d pages", W,
-               kMaxPages);
-  CVSA_REQUIRE(bt_stride_b >= W, CVSA_ERR_INVALID,
-               "quest_scores: block-table row stride %lld < W=%d", (long long)bt_stride_b, W);
-  CVSA_REQUIRE(((uintptr_t)q & 15) == 0 && q_stride_b % 8 == 0 && q_stride_h % 8 == 0 &&
-                   ((uintptr_t)meta & 15) == 0,
-               CVSA_ERR_INVALID,
-               "quest_scores: q / meta must be 16-byte aligned with q strides that are "
-               "multiples of 8 elements");
+               "%s: null pointer argument", name);
+  int rc = check_quest_sizes(name, B, H_kv, D, block_size, W, num_blocks, bt_stride_b, meta);
+  if (rc == CVSA_OK) rc = check_quest_q(name, q, q_stride_b, q_stride_h, H_q, H_kv);
+  if (rc != CVSA_OK) return rc;
   const int G = H_q / H_kv;
-  // Pages per wave: as many (up to 64) as keep >= ~2048 waves in the launch.
-  const int64_t rows = (int64_t)B * H_kv;
-  int ppw = kQuestPagesPerWave;
-  while (ppw < 64 && rows * W / (2 * ppw) >= 2048) ppw *= 2;
-  const int waves = (W + ppw - 1) / ppw;
-  hipLaunchKernelGGL(quest_scores_kernel, dim3((waves + 3) / 4, B * H_kv), dim3(256), 0,
-                     (hipStream_t)stream, q, q_stride_b, q_stride_h, meta, num_blocks,
-                     block_tables, bt_stride_b, context_lens, H_kv, G, 1.0f / (float)G,
-                     (float)pow((double)D, -0.5), W, ppw, page_scores);
-  return cvsa_host::check_launch("quest_scores");
+  int ppw;
+  const dim3 grid = quest_grid(B, H_kv, W, ppw);
+  // Without refresh the kernel only reads the metadata.
+  hipLaunchKernelGGL((quest_scores_kernel<false, true>), grid, dim3(256), 0, (hipStream_t)stream,
+                     q, q_stride_b, q_stride_h, const_cast<uint16_t *>(meta), nullptr, num_blocks,
+                     block_tables, bt_stride_b, context_lens, nullptr, nullptr, 0, H_kv, G,
+                     1.0f / (float)G, (float)pow((double)D, -0.5), W, ppw, page_scores);
+  return cvsa_host::check_launch(name);
+}
+
+extern "C" int cvsa_quest_refresh_scores(const uint16_t *q, int64_t q_stride_b,
+                                         int64_t q_stride_h, const uint16_t *k_cache,
+                                         int64_t num_blocks, const int32_t *block_tables,
+                                         int64_t bt_stride_b, const int32_t *context_lens,
+                                         const uint8_t *check_accept, int32_t B, int32_t H_q,
+                                         int32_t H_kv, int32_t D, int32_t block_size, int32_t W,
+                                         uint16_t *meta, int32_t *meta_ntok, float *page_scores,
+                                         void *stream) {
+  static const char *name = "quest_refresh_scores";
+  CVSA_REQUIRE(q && k_cache && meta && meta_ntok && block_tables && context_lens && page_scores,
+               CVSA_ERR_INVALID, "%s: null pointer argument", name);
+  int rc = check_quest_sizes(name, B, H_kv, D, block_size, W, num_blocks, bt_stride_b, meta);
+  if (rc == CVSA_OK) rc = check_quest_q(name, q, q_stride_b, q_stride_h, H_q, H_kv);
+  if (rc != CVSA_OK) return rc;
+  CVSA_REQUIRE(((uintptr_t)k_cache & 15) == 0, CVSA_ERR_INVALID,
+               "%s: k_cache must be 16-byte aligned", name);
+  const int G = H_q / H_kv;
+  int ppw;
+  const dim3 grid = quest_grid(B, H_kv, W, ppw);
+  hipLaunchKernelGGL((quest_scores_kernel<true, true>), grid, dim3(256), 0, (hipStream_t)stream,
+                     q, q_stride_b, q_stride_h, meta, meta_ntok, num_blocks, block_tables,
+                     bt_stride_b, context_lens, k_cache, check_accept, B * H_kv, H_kv, G,
+                     1.0f / (float)G, (float)pow((double)D, -0.5), W, ppw, page_scores);
+  return cvsa_host::check_launch(name);
 }

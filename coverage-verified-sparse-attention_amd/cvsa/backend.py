@@ -28,10 +28,12 @@ recovery, the random-rejection counterfactual, coverage-only steps and the
 counters of the fixed-interval schedule.
 
 The Quest selector (selector="quest", cvsa/backend.py:572-620) ranks pages
-by per-page key min/max metadata that is refreshed for the pages that
-gained tokens since the previous call (ops.QuestPageMeta) rather than
-gathered from the whole cache; with light_normalizer its scores also drive
-the coverage gate, so no step reads all keys.
+by per-page key min/max metadata that is recomputed only for the pages
+whose valid-token count changed (ops.QuestPageMeta) rather than gathered
+from the whole cache; with light_normalizer its scores also drive the
+coverage gate, so no step reads all keys.  A lazy check on the device asks
+for the ranking scores with its flags: they are computed only when some
+head failed.
 
 Not implemented here (the constructor raises NotImplementedError): the
 reference's other selectors (adaptive_selection, static_budget_table,
@@ -462,16 +464,17 @@ class CVSABackend:
                                   page_scores=page_scores)
 
     # ------------------------------------------------------------ scorers
-    def _quest_page_scores(self, q, k_cache, block_tables, context_lens):
+    def _quest_page_scores(self, q, k_cache, block_tables, context_lens, check_accept=None):
         """backend.py:572-620: Quest ranking scores [B, H_kv, W] fp32, from
-        page metadata of this key cache that is refreshed for the pages that
-        gained tokens since the previous call."""
+        page metadata of this key cache that is recomputed for the pages
+        whose valid-token count changed.  With a lazy check's flags, nothing
+        is computed when every head passed (the scores are then unused)."""
         entry = self._quest_meta.get(id(k_cache))
         if entry is None or entry[0]() is not k_cache:
             entry = (weakref.ref(k_cache), ops.QuestPageMeta(k_cache))
             self._quest_meta[id(k_cache)] = entry
         return entry[1].scores(q, block_tables, context_lens, self.num_kv_heads,
-                               self.num_q_per_kv, self.block_size)
+                               self.num_q_per_kv, self.block_size, check_accept)
 
     def _gate_scores(self, q, k_cache, block_tables, context_lens):
         """Scores of the coverage gate (and the cache): the Quest sketch with
@@ -481,14 +484,14 @@ class CVSABackend:
         return ops.score_pages(q, k_cache, block_tables, context_lens, self.num_kv_heads,
                                self.num_q_per_kv, self.block_size)
 
-    def _sel_scores(self, q, k_cache, block_tables, context_lens):
+    def _sel_scores(self, q, k_cache, block_tables, context_lens, check_accept=None):
         """Scores the selection ranks when they differ from the gate's
         (selector="quest" without light_normalizer, backend.py:723-727), else
         None."""
         if self.selector != "quest" or self.light_normalizer:
             return None
         return self._time_kernel("scoring", self._quest_page_scores, q, k_cache, block_tables,
-                                 context_lens)
+                                 context_lens, check_accept)
 
     # ------------------------------------------------------------ step plans
     def _matching_plan(self, layer_idx, q, k_cache, v_cache, block_tables, context_lens):
@@ -610,7 +613,7 @@ class CVSABackend:
         page_indices, n_per_head = self._cached_selection[layer_idx]
         budget = page_indices.shape[2]
         self._per_head_total += check_accept.numel()
-        sel_scores = self._sel_scores(q, k_cache, block_tables, context_lens)
+        sel_scores = self._sel_scores(q, k_cache, block_tables, context_lens, check_accept)
         accept_mask = self._time_kernel(
             "coverage", ops.select_or_keep, page_scores, check_accept, budget, context_lens,
             self.block_size, self.tau, page_indices, n_per_head, coverage,

@@ -38,6 +38,7 @@ __all__ = [
     "StepPlan",
     "quest_meta_update",
     "quest_scores",
+    "quest_refresh_scores",
     "QuestPageMeta",
 ]
 
@@ -286,28 +287,33 @@ def check_coverage(page_scores: torch.Tensor, selected_indices: torch.Tensor,
 
 # ---------------------------------------------------------------- Quest
 
-def quest_meta_update(k_cache: torch.Tensor, block_tables: torch.Tensor,
-                      context_lens: torch.Tensor, seen_lens: torch.Tensor, meta: torch.Tensor,
-                      seen_out: Optional[torch.Tensor] = None, all_pages: bool = False) -> None:
-    """Refresh the Quest page metadata (per block and KV head: key min and
-    max over the page's valid tokens) for the pages holding positions
-    [seen_lens, context_lens); see cvsa_quest_meta_update.  ``meta`` is
-    [num_blocks, H_kv, 2, D] bf16; ``seen_out`` receives context_lens."""
-    dev = _device_of(k_cache, block_tables, context_lens, seen_lens, meta, seen_out)
-    _check_cache(k_cache)
-    nb, bs, H, D = k_cache.shape
+def _check_quest_state(meta, meta_ntok, k_cache):
+    nb, _, H, D = k_cache.shape
     if meta.shape != (nb, H, 2, D) or meta.dtype != torch.bfloat16 or not meta.is_contiguous():
         raise ValueError(f"meta must be a contiguous bfloat16 [{nb}, {H}, 2, {D}]")
+    if (meta_ntok.shape != (nb, H) or meta_ntok.dtype != torch.int32
+            or not meta_ntok.is_contiguous()):
+        raise ValueError(f"meta_ntok must be a contiguous int32 [{nb}, {H}]")
+
+
+def quest_meta_update(k_cache: torch.Tensor, block_tables: torch.Tensor,
+                      context_lens: torch.Tensor, meta: torch.Tensor,
+                      meta_ntok: torch.Tensor) -> None:
+    """Refresh the Quest page metadata (per block and KV head: key min and
+    max over the page's valid tokens) of every page whose valid-token count
+    differs from ``meta_ntok``; see cvsa_quest_meta_update.  ``meta`` is
+    [num_blocks, H_kv, 2, D] bf16, ``meta_ntok`` [num_blocks, H_kv] int32
+    (zero before the first update)."""
+    dev = _device_of(k_cache, block_tables, context_lens, meta, meta_ntok)
+    _check_cache(k_cache)
+    _check_quest_state(meta, meta_ntok, k_cache)
+    nb, bs, H, D = k_cache.shape
     bt = _block_tables(block_tables)
     ctx = _i32(context_lens)
     B, W = bt.shape
-    for name, t in (("seen_lens", seen_lens), ("seen_out", seen_out)):
-        if t is not None and (t.dtype != torch.int32 or t.shape != (B,) or not t.is_contiguous()):
-            raise ValueError(f"{name} must be a contiguous int32 [{B}]")
     check(_lib.load().cvsa_quest_meta_update(
-        k_cache.data_ptr(), nb, bt.data_ptr(), bt.stride(0), ctx.data_ptr(), seen_lens.data_ptr(),
-        _ptr(seen_out), B, H, D, bs, W, 1 if all_pages else 0, meta.data_ptr(), _stream(dev)),
-        "quest_meta_update")
+        k_cache.data_ptr(), nb, bt.data_ptr(), bt.stride(0), ctx.data_ptr(), B, H, D, bs, W,
+        meta.data_ptr(), meta_ntok.data_ptr(), _stream(dev)), "quest_meta_update")
 
 
 def quest_scores(q: torch.Tensor, meta: torch.Tensor, block_tables: torch.Tensor,
@@ -320,8 +326,7 @@ def quest_scores(q: torch.Tensor, meta: torch.Tensor, block_tables: torch.Tensor
     B, H_q, D = q.shape
     if num_kv_heads * num_q_per_kv != H_q:
         raise ValueError("quest_scores: head counts do not match q")
-    if meta.dim() != 4 or meta.shape[1:] != (num_kv_heads, 2, D) or meta.dtype != torch.bfloat16:
-        raise ValueError(f"meta must be bfloat16 [num_blocks, {num_kv_heads}, 2, {D}]")
+    _check_meta(meta, num_kv_heads, D)
     bt = _block_tables(block_tables)
     ctx = _i32(context_lens)
     W = bt.shape[1]
@@ -333,15 +338,57 @@ def quest_scores(q: torch.Tensor, meta: torch.Tensor, block_tables: torch.Tensor
     return out
 
 
+def _check_meta(meta, num_kv_heads, D):
+    if (meta.dim() != 4 or meta.shape[1:] != (num_kv_heads, 2, D)
+            or meta.dtype != torch.bfloat16 or not meta.is_contiguous()):
+        raise ValueError(f"meta must be a contiguous bfloat16 [num_blocks, {num_kv_heads}, 2, {D}]")
+
+
+def quest_refresh_scores(q: torch.Tensor, k_cache: torch.Tensor, block_tables: torch.Tensor,
+                         context_lens: torch.Tensor, meta: torch.Tensor, meta_ntok: torch.Tensor,
+                         num_kv_heads: int, num_q_per_kv: int, block_size: int,
+                         check_accept: Optional[torch.Tensor] = None,
+                         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """quest_meta_update followed by quest_scores, in one launch
+    (cvsa_quest_refresh_scores).  With ``check_accept`` (a lazy check's
+    [B, H_kv] flags) nothing is computed when every head passed: ``out``
+    then keeps its previous contents."""
+    dev = _device_of(q, k_cache, meta, meta_ntok, block_tables, context_lens, check_accept, out)
+    q = _check_q(q)
+    _check_cache(k_cache)
+    _check_quest_state(meta, meta_ntok, k_cache)
+    nb, bs, H, D = k_cache.shape
+    B, H_q, _ = q.shape
+    if num_kv_heads * num_q_per_kv != H_q or H != num_kv_heads:
+        raise ValueError("quest_refresh_scores: head counts do not match q / k_cache")
+    bt = _block_tables(block_tables)
+    ctx = _i32(context_lens)
+    W = bt.shape[1]
+    if check_accept is not None and (check_accept.shape != (B, num_kv_heads)
+                                     or check_accept.dtype != torch.bool
+                                     or not check_accept.is_contiguous()):
+        raise ValueError(f"check_accept must be a contiguous bool [{B}, {num_kv_heads}]")
+    if out is None:
+        out = torch.empty(B, num_kv_heads, W, device=dev, dtype=torch.float32)
+    elif out.shape != (B, num_kv_heads, W) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous float32 [{B}, {num_kv_heads}, {W}]")
+    check(_lib.load().cvsa_quest_refresh_scores(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), nb, bt.data_ptr(),
+        bt.stride(0), ctx.data_ptr(), _ptr(check_accept), B, H_q, num_kv_heads, D, block_size, W,
+        meta.data_ptr(), meta_ntok.data_ptr(), out.data_ptr(), _stream(dev)),
+        "quest_refresh_scores")
+    return out
+
+
 class QuestPageMeta:
     """The Quest metadata of one paged key cache, kept current across calls.
 
-    ``scores(...)`` first refreshes the pages that gained tokens since the
-    previous call (all pages the first time, or when the batch changes),
-    then scores every page from the metadata.  The seen-lengths live on the
-    device in two buffers used in turn, so no call waits for the host.
-    Valid while keys are only appended through the cache's own page table
-    (a rewritten page needs ``invalidate()``).
+    ``meta`` [num_blocks, H_kv, 2, D] bf16 holds each block's key extremes
+    and ``ntok`` [num_blocks, H_kv] int32 the number of tokens they cover.
+    ``scores(...)`` recomputes the pages whose valid-token count changed
+    and scores every page, in one launch.  Valid while keys are only
+    appended; ``invalidate()`` forgets every block (needed when blocks are
+    rewritten, e.g. reused for another sequence).
     """
 
     def __init__(self, k_cache: torch.Tensor):
@@ -349,22 +396,16 @@ class QuestPageMeta:
         nb, _, H, D = k_cache.shape
         self.k_cache = k_cache
         self.meta = torch.empty(nb, H, 2, D, device=k_cache.device, dtype=torch.bfloat16)
-        self._seen = None
+        self.ntok = torch.zeros(nb, H, device=k_cache.device, dtype=torch.int32)
 
     def invalidate(self) -> None:
-        self._seen = None
+        self.ntok.zero_()
 
-    def scores(self, q, block_tables, context_lens, num_kv_heads, num_q_per_kv, block_size):
-        B = block_tables.shape[0]
-        first = self._seen is None or self._seen[0].shape[0] != B
-        if first:
-            self._seen = [torch.zeros(B, dtype=torch.int32, device=self.meta.device)
-                          for _ in range(2)]
-        quest_meta_update(self.k_cache, block_tables, context_lens, self._seen[0], self.meta,
-                          self._seen[1], all_pages=first)
-        self._seen.reverse()
-        return quest_scores(q, self.meta, block_tables, context_lens, num_kv_heads,
-                            num_q_per_kv, block_size)
+    def scores(self, q, block_tables, context_lens, num_kv_heads, num_q_per_kv, block_size,
+               check_accept=None, out=None):
+        return quest_refresh_scores(q, self.k_cache, block_tables, context_lens, self.meta,
+                                    self.ntok, num_kv_heads, num_q_per_kv, block_size,
+                                    check_accept, out)
 
 
 # ---------------------------------------------------------------- decode

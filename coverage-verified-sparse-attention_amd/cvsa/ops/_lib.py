@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parents[1] / "libcvsa_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 CVSA_OK = 0
 CVSA_ERR_INVALID = -1
@@ -85,9 +85,12 @@ SIGNATURES = {
         _p, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p, _p,
         _i32, _i32, _i32, _i32, _i32, _i32, _p]),
     "cvsa_quest_meta_update": (ctypes.c_int, [
-        _p, _i64, _p, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p]),
+        _p, _i64, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]),
     "cvsa_quest_scores": (ctypes.c_int, [
         _p, _i64, _i64, _p, _i64, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p]),
+    "cvsa_quest_refresh_scores": (ctypes.c_int, [
+        _p, _i64, _i64, _p, _i64, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
+        _p, _p, _p, _p]),
     "cvsa_step_workspace_bytes": (_sz, [ctypes.POINTER(StepDesc)]),
     "cvsa_step_plan_create": (ctypes.c_int, [ctypes.POINTER(StepDesc), ctypes.POINTER(_p)]),
     "cvsa_step_plan_run": (ctypes.c_int, [_p, _i32, _p, _p, _p]),

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 3
+#define CVSA_ABI_VERSION 4
 
 enum {
   CVSA_OK = 0,
@@ -270,24 +270,22 @@ int cvsa_append_kv(const uint16_t *k_new, const uint16_t *v_new,
  * (cvsa/backend.py:572-620) needs, per page and KV head, the extremes of the
  * keys over the page's valid tokens (:593-603); the reference recomputes
  * them from the cache on every call, its Quest baseline keeps them per page
- * (eval/baselines.py:77-140).  This entry point keeps them up to date:
+ * (eval/baselines.py:77-140).  This entry point brings them up to date:
  *   meta: [num_blocks, H_kv, 2, D] bf16; meta[blk][h][0] = kmin,
- *     meta[blk][h][1] = kmax over the valid tokens of the page stored in blk.
- *   seen_lens [B] int32: context lengths at the previous update (0 before
- *     the first).  The pages holding positions [seen, ctx) are recomputed
- *     from k_cache (every page up to ctx when ctx < seen); seen_out [B]
- *     (a different buffer, may be NULL) receives context_lens.
- *   all_pages != 0 spreads a first build over the whole grid; otherwise one
- *     workgroup per (b, kv-head) walks the pages that gained tokens.
- * The metadata describes the keys present at the update: appending tokens
- * (or rewriting a page) requires another update before cvsa_quest_scores.
+ *     meta[blk][h][1] = kmax over the first meta_ntok[blk][h] tokens of blk.
+ *   meta_ntok: [num_blocks, H_kv] int32, zero before the first update.
+ * Every page of every row whose valid-token count under context_lens
+ * differs from meta_ntok is recomputed from k_cache (and its count
+ * written).  Keys are assumed to change only by appends: a block whose
+ * tokens are rewritten (reused for another sequence) needs its meta_ntok
+ * entries cleared first.  A block listed by two rows must hold the same
+ * number of valid tokens in both.  k_cache and meta 16-byte aligned.
  */
 int cvsa_quest_meta_update(const uint16_t *k_cache, int64_t num_blocks,
                            const int32_t *block_tables, int64_t bt_stride_b,
-                           const int32_t *context_lens, const int32_t *seen_lens,
-                           int32_t *seen_out, int32_t B, int32_t H_kv, int32_t D,
-                           int32_t block_size, int32_t W, int32_t all_pages,
-                           uint16_t *meta, void *stream);
+                           const int32_t *context_lens, int32_t B, int32_t H_kv, int32_t D,
+                           int32_t block_size, int32_t W, uint16_t *meta, int32_t *meta_ntok,
+                           void *stream);
 
 /*
  * Quest page scores from the metadata.  Replaces
@@ -303,6 +301,24 @@ int cvsa_quest_scores(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
                       const int32_t *context_lens, int32_t B, int32_t H_q,
                       int32_t H_kv, int32_t D, int32_t block_size, int32_t W,
                       float *page_scores, void *stream);
+
+/*
+ * The Quest scores of CVSABackend._quest_page_scores (cvsa/backend.py:
+ * 572-620) with the metadata refresh of cvsa_quest_meta_update in the same
+ * launch: each page whose count is stale is recomputed, written back and
+ * scored from the new values; the others are scored from meta.  Equal, bit
+ * for bit, to cvsa_quest_meta_update followed by cvsa_quest_scores.
+ * check_accept (may be NULL): B*H_kv flags of a lazy coverage check; when
+ * every flag is set the call does nothing (the kept selection needs no
+ * ranking scores, and the stale pages wait for the next scoring call).
+ */
+int cvsa_quest_refresh_scores(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
+                              const uint16_t *k_cache, int64_t num_blocks,
+                              const int32_t *block_tables, int64_t bt_stride_b,
+                              const int32_t *context_lens, const uint8_t *check_accept,
+                              int32_t B, int32_t H_q, int32_t H_kv, int32_t D,
+                              int32_t block_size, int32_t W, uint16_t *meta, int32_t *meta_ntok,
+                              float *page_scores, void *stream);
 
 /*
  * Step plans: one layer's decode steps, each enqueued by a single call.

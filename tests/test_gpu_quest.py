@@ -1,5 +1,5 @@
-"""Quest page metadata and scores (cvsa_quest_meta_update, cvsa_quest_scores)
-against the oracle's restatement of CVSABackend._quest_page_scores
+"""Quest page metadata and scores (cvsa_quest_meta_update, cvsa_quest_scores,
+cvsa_quest_refresh_scores) against the oracle's restatement of CVSABackend._quest_page_scores
 (cvsa/backend.py:572-620), the selection with separate ranking and gate
 scores, and the backend's selector="quest" / light_normalizer schedules
 against the oracle backend."""
@@ -53,11 +53,18 @@ def test_quest_meta_follows_appends(gpu):
     mgr._pages_allocated = [-(-int(c) // 16) for c in inp.context_lens.tolist()]
     mgr.sync_host_state()
     qm = ops.QuestPageMeta(cache.k_cache)
+    # the same updates through the two separate entry points
+    meta2 = torch.empty_like(qm.meta)
+    ntok2 = torch.zeros_like(qm.ntok)
     g = torch.Generator().manual_seed(3)
 
     def check():
         q = jitter_query(inp.q, 0.5, int(mgr.context_lens.sum())).to(gpu)
         got = qm.scores(q, mgr.block_tables, mgr.context_lens, H, 4, 16).cpu()
+        ops.quest_meta_update(cache.k_cache, mgr.block_tables, mgr.context_lens, meta2, ntok2)
+        sep = ops.quest_scores(q, meta2, mgr.block_tables, mgr.context_lens, H, 4, 16).cpu()
+        assert torch.equal(got, sep)
+        assert torch.equal(ntok2, qm.ntok)
         K, bt, cl = cache.k_cache.cpu(), mgr.block_tables.cpu(), mgr.context_lens.cpu()
         _close(got, ref.quest_page_scores(q.cpu(), K, bt, cl, H, 4, 16))
         kmin, kmax = ref.page_key_minmax(K, bt, cl, 16)
@@ -67,6 +74,9 @@ def test_quest_meta_follows_appends(gpu):
                 blk = int(bt[b, p])
                 assert torch.equal(meta[blk, :, 0], kmin[b, p]), (b, p)
                 assert torch.equal(meta[blk, :, 1], kmax[b, p]), (b, p)
+                assert torch.equal(meta2[blk].cpu(), qm.meta[blk].cpu()), (b, p)
+                n = min(16, int(cl[b]) - 16 * p)
+                assert bool((qm.ntok[blk] == n).all()), (b, p)
 
     check()
     for n in (1, 3, 17, 1, 16):
@@ -77,6 +87,27 @@ def test_quest_meta_follows_appends(gpu):
     # shrink: every page up to the new length is rebuilt
     mgr.context_lens.copy_(torch.tensor([100, 20], dtype=torch.int32))
     check()
+
+
+def test_quest_refresh_skips_when_every_head_passed(gpu):
+    """With a lazy check's flags: nothing is written when every head passed
+    (scores and metadata stay as they were); one failing head computes all."""
+    B, H_q, H = 2, 32, 8
+    inp = make_paged_inputs(B, H_q, H, 128, [3000, 1501], seed=12, device=gpu)
+    qm = ops.QuestPageMeta(inp.k_cache)
+    args = (inp.q, inp.block_tables, inp.context_lens, H, H_q // H, 16)
+    W = inp.block_tables.shape[1]
+    out = torch.full((B, H, W), 7.0, device=gpu)
+    flags = torch.ones(B, H, dtype=torch.bool, device=gpu)
+    qm.scores(*args, check_accept=flags, out=out)
+    assert bool((out == 7.0).all()) and not bool(qm.ntok.any())
+    flags[1, 3] = False
+    got = qm.scores(*args, check_accept=flags, out=out)
+    assert got is out
+    want = ref.quest_page_scores(inp.q.cpu(), inp.k_cache.cpu(), inp.block_tables.cpu(),
+                                 inp.context_lens.cpu(), H, H_q // H, 16)
+    _close(out.cpu(), want)
+    assert torch.equal(qm.scores(*args).cpu(), out.cpu())
 
 
 def test_select_or_keep_with_separate_ranking_scores(gpu):
