@@ -1,8 +1,9 @@
 // Step plans: a layer's reuse, lazy-check and fixed-interval scoring steps,
 // each enqueued by one host call.  The plan copies the caller's descriptor
 // after checking everything the chained entry points check, then replays the
-// chain (cvsa_score_pages, cvsa_check_coverage, cvsa_select_or_keep,
-// cvsa_verified_decode / cvsa_sparse_decode) with the stored arguments.
+// chain (cvsa_score_pages or cvsa_quest_refresh_scores, cvsa_check_coverage,
+// cvsa_select_or_keep, cvsa_verified_decode / cvsa_sparse_decode) with the
+// stored arguments.
 // This is host code only: the kernels are the entry points' own.
 #include <hip/hip_runtime.h>
 #include <new>
@@ -70,6 +71,17 @@ int check_desc(const cvsa_step_desc &d) {
                "step_plan: k_cache / v_cache must be 16-byte aligned");
   STEP_REQUIRE(d.out_dtype >= CVSA_DTYPE_BF16 && d.out_dtype <= CVSA_DTYPE_FP32,
                CVSA_ERR_INVALID, "step_plan: bad output dtype %d", d.out_dtype);
+  STEP_REQUIRE(d.selector >= CVSA_SELECT_EXACT && d.selector <= CVSA_SELECT_QUEST_LN,
+               CVSA_ERR_INVALID, "step_plan: unknown selector %d", d.selector);
+  if (d.selector != CVSA_SELECT_EXACT) {
+    STEP_REQUIRE(d.quest_meta && d.quest_ntok && aligned16(d.quest_meta), CVSA_ERR_INVALID,
+                 "step_plan: the Quest selectors need quest_meta (16-byte aligned) and "
+                 "quest_ntok");
+    STEP_REQUIRE((int64_t)d.B * d.H_kv <= 65535, CVSA_ERR_UNSUPPORTED,
+                 "step_plan: B * H_kv exceeds 65535 rows for the Quest scorer");
+  }
+  STEP_REQUIRE(d.selector != CVSA_SELECT_QUEST || d.sel_scores != nullptr, CVSA_ERR_INVALID,
+               "step_plan: CVSA_SELECT_QUEST needs a sel_scores buffer");
   const size_t need = workspace_need(d);
   STEP_REQUIRE(need < ((size_t)1 << 31), CVSA_ERR_UNSUPPORTED,
                "step_plan: a decode workspace of %zu bytes exceeds the 2 GiB buffer range",
@@ -82,10 +94,28 @@ int check_desc(const cvsa_step_desc &d) {
   return CVSA_OK;
 }
 
+int quest(const cvsa_step_desc &d, const uint16_t *q, const uint8_t *check, float *scores,
+          void *stream) {
+  return cvsa_quest_refresh_scores(q, d.q_stride_b, d.q_stride_h, d.k_cache, d.num_blocks,
+                                   d.block_tables, d.bt_stride_b, d.context_lens, check, d.B,
+                                   d.H_q, d.H_kv, d.D, d.block_size, d.W, d.quest_meta,
+                                   d.quest_ntok, scores, stream);
+}
+
+// The gate's page scores (page_scores): the exact scan, or the Quest
+// scores under light_normalizer.
 int score(const cvsa_step_desc &d, const uint16_t *q, void *stream) {
+  if (d.selector == CVSA_SELECT_QUEST_LN) return quest(d, q, nullptr, d.page_scores, stream);
   return cvsa_score_pages(q, d.q_stride_b, d.q_stride_h, d.k_cache, d.num_blocks,
                           d.block_tables, d.bt_stride_b, d.context_lens, d.B, d.H_q, d.H_kv,
                           d.D, d.block_size, d.W, d.page_scores, stream);
+}
+
+// Separate ranking scores (CVSA_SELECT_QUEST) into sel_scores; with a
+// lazy check's flags they are computed only if a head failed.
+int rank(const cvsa_step_desc &d, const uint16_t *q, const uint8_t *check, void *stream) {
+  if (d.selector != CVSA_SELECT_QUEST) return CVSA_OK;
+  return quest(d, q, check, d.sel_scores, stream);
 }
 
 int verified(const cvsa_step_desc &d, const uint16_t *q, void *out, void *stream) {
@@ -126,6 +156,7 @@ extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint
                    kind == CVSA_STEP_SCORE || kind == CVSA_STEP_FRESH,
                CVSA_ERR_INVALID, "step_plan_run: unknown step kind %d", kind);
   const cvsa_step_desc &d = plan->d;
+  const float *sel = d.selector == CVSA_SELECT_QUEST ? d.sel_scores : nullptr;
   int rc;
   switch (kind) {
     case CVSA_STEP_REUSE:
@@ -140,7 +171,8 @@ extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint
                                     d.n_per_head, d.tau, d.check_accept, d.coverage,
                                     stream)) != CVSA_OK)
         return rc;
-      if ((rc = cvsa_select_or_keep(d.page_scores, nullptr, d.check_accept, d.B, d.H_kv, d.W,
+      if ((rc = rank(d, q, d.check_accept, stream)) != CVSA_OK) return rc;
+      if ((rc = cvsa_select_or_keep(d.page_scores, sel, d.check_accept, d.B, d.H_kv, d.W,
                                     d.context_lens, d.block_size, d.budget, d.page_indices,
                                     d.n_per_head, d.tau, d.accept, d.coverage, d.scores_cache,
                                     d.stats, 0, stream)) != CVSA_OK)
@@ -148,7 +180,8 @@ extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint
       return verified(d, q, out, stream);
     case CVSA_STEP_FRESH:
       if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
-      if ((rc = cvsa_select_or_keep(d.page_scores, nullptr, nullptr, d.B, d.H_kv, d.W,
+      if ((rc = rank(d, q, nullptr, stream)) != CVSA_OK) return rc;
+      if ((rc = cvsa_select_or_keep(d.page_scores, sel, nullptr, d.B, d.H_kv, d.W,
                                     d.context_lens, d.block_size, d.budget, d.page_indices,
                                     d.n_per_head, d.tau, d.accept, d.coverage, d.scores_cache,
                                     d.stats, 0, stream)) != CVSA_OK)
@@ -156,7 +189,8 @@ extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint
       return verified(d, q, out, stream);
     default:  // CVSA_STEP_SCORE
       if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
-      if ((rc = cvsa_select_or_keep(d.page_scores, nullptr, nullptr, d.B, d.H_kv, d.W,
+      if ((rc = rank(d, q, nullptr, stream)) != CVSA_OK) return rc;
+      if ((rc = cvsa_select_or_keep(d.page_scores, sel, nullptr, d.B, d.H_kv, d.W,
                                     d.context_lens,
                                     d.block_size, d.budget, d.page_indices, d.n_per_head,
                                     d.tau, d.accept, d.coverage, nullptr, d.stats, 1,

@@ -13,9 +13,10 @@ What runs per layer call (HIP kernels from cvsa.ops):
   scoring step  score_pages -> select_topk (+ coverage gate) -> verified_decode
   lazy check    score_pages -> check_coverage -> select_or_keep -> verified_decode
   reuse step    sparse decode over the cached selection
-Once a layer has a selection, these sequences run from a native step plan
-(ops.StepPlan): one host call per step instead of one validated call per
-kernel, while the caches, tables, counters and stream stay the same.
+These sequences run from a native step plan (ops.StepPlan), the first
+selection of a layer included: one host call per step instead of one
+validated call per kernel, while the caches, tables, counters and stream
+stay the same.
 The reference's draft decode, complement, complement decode and LSE merge
 collapse into verified_decode: accepted heads attend their selected pages,
 rejected heads attend every valid page in one pass, which equals the LSE
@@ -252,7 +253,13 @@ class CVSABackend:
         # Step plans that own their selection stay: the next first selection
         # of their layer is made in their buffers again.
         self._step_plans = {k: p for k, p in self._step_plans.items() if p.owns_selection}
-        self._quest_meta = {}
+        # Quest metadata objects (and the plans that use them) stay, but
+        # forget every block: a new sequence may rewrite the cache.
+        for ref, meta in list(self._quest_meta.values()):
+            if ref() is None:
+                continue
+            meta.invalidate()
+        self._quest_meta = {k: e for k, e in self._quest_meta.items() if e[0]() is not None}
         self._cached_selection = {}
         self._cached_page_scores = {}
         self._last_accept_mask = {}
@@ -469,12 +476,24 @@ class CVSABackend:
         page metadata of this key cache that is recomputed for the pages
         whose valid-token count changed.  With a lazy check's flags, nothing
         is computed when every head passed (the scores are then unused)."""
+        return self._quest_state(k_cache).scores(q, block_tables, context_lens,
+                                                 self.num_kv_heads, self.num_q_per_kv,
+                                                 self.block_size, check_accept)
+
+    def _quest_state(self, k_cache):
+        """The Quest metadata of this key cache (created on first use)."""
         entry = self._quest_meta.get(id(k_cache))
         if entry is None or entry[0]() is not k_cache:
             entry = (weakref.ref(k_cache), ops.QuestPageMeta(k_cache))
             self._quest_meta[id(k_cache)] = entry
-        return entry[1].scores(q, block_tables, context_lens, self.num_kv_heads,
-                               self.num_q_per_kv, self.block_size, check_accept)
+        return entry[1]
+
+    def _plan_selector(self, k_cache):
+        """The step-plan scorer code and Quest metadata of this backend."""
+        if self.selector != "quest":
+            return ops._lib.SELECT_EXACT, None
+        code = ops._lib.SELECT_QUEST_LN if self.light_normalizer else ops._lib.SELECT_QUEST
+        return code, self._quest_state(k_cache)
 
     def _gate_scores(self, q, k_cache, block_tables, context_lens):
         """Scores of the coverage gate (and the cache): the Quest sketch with
@@ -506,7 +525,8 @@ class CVSABackend:
         if (sel is None or sel[0] is not plan.page_indices
                 or not (cached is plan.scores_cache or cached is plan.page_scores)
                 or not plan.matches(q, k_cache, v_cache, block_tables, context_lens,
-                                    self._work(q.device), self._dev_stats)):
+                                    self._work(q.device), self._dev_stats,
+                                    self._plan_selector(k_cache)[1])):
             return None
         return plan
 
@@ -516,8 +536,7 @@ class CVSABackend:
         """Build the layer's step plan, or None where a step needs the
         per-kernel path (timing, host-side decisions, unsupported buffers)."""
         if (self._track_timing or self.random_reject_prob is not None
-                or self.approx_recovery_pct is not None or self.selector != "exact"
-                or self.light_normalizer):
+                or self.approx_recovery_pct is not None):
             return None
         dev = q.device
         work = self._work(dev)
@@ -525,11 +544,13 @@ class CVSABackend:
         if work is None or stats is None:
             return None
         budget = max(3, int(block_tables.shape[1] * self.budget_pct))
+        selector, quest = self._plan_selector(k_cache)
         try:
             plan = ops.StepPlan(q, k_cache, v_cache, block_tables, context_lens,
                                 self.num_kv_heads, self.num_q_per_kv, self.block_size, budget,
                                 self.tau, page_indices, n_per_head, scores_cache, stats, work,
-                                own_scores_cache=own_scores_cache)
+                                own_scores_cache=own_scores_cache, selector=selector,
+                                quest=quest)
         except (ValueError, NotImplementedError):
             return None
         self._step_plans[layer_idx] = plan
@@ -544,7 +565,8 @@ class CVSABackend:
         if (plan is not None and not self._track_timing and plan.owns_selection
                 and (plan.scores_cache is not None) == own_scores_cache
                 and plan.matches(q, k_cache, v_cache, block_tables, context_lens,
-                                 self._work(q.device), self._dev_stats)):
+                                 self._work(q.device), self._dev_stats,
+                                 self._plan_selector(k_cache)[1])):
             return plan
         if self._track_timing:
             return None

@@ -551,19 +551,32 @@ class StepPlan:
     / ``accept`` / ``coverage`` [B, H_kv]; every check or scoring step
     rewrites the latter.  Kind STEP_FRESH makes a lazy layer's first
     selection in the plan's buffers.
+    ``selector`` (_lib.SELECT_*) picks the page scorer: exact scores rank
+    and gate; SELECT_QUEST ranks by the Quest scores of ``quest`` (a
+    QuestPageMeta of k_cache) into ``sel_scores`` while exact scores gate;
+    SELECT_QUEST_LN ranks and gates by the Quest scores.
     ``matches`` tells whether a call's buffers, query layout and stream are
     the ones the plan was built for.
     """
 
     __slots__ = ("dev", "stream", "q_meta", "out_shape", "out_dtype", "refs", "page_indices",
                  "n_per_head", "page_scores", "scores_cache", "check_accept", "accept",
-                 "coverage", "budget", "owns_selection", "_h", "_run", "_fin", "__weakref__")
+                 "coverage", "budget", "owns_selection", "selector", "sel_scores", "_h", "_run",
+                 "_fin", "__weakref__")
 
     def __init__(self, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
                  num_q_per_kv, block_size, budget, tau, page_indices=None, n_per_head=None,
-                 scores_cache=None, stats=None, work=None, own_scores_cache=False):
+                 scores_cache=None, stats=None, work=None, own_scores_cache=False,
+                 selector=_lib.SELECT_EXACT, quest=None):
         dev = _device_of(q, k_cache, v_cache, block_tables, context_lens, page_indices,
                          n_per_head, scores_cache, stats, work)
+        if selector not in (_lib.SELECT_EXACT, _lib.SELECT_QUEST, _lib.SELECT_QUEST_LN):
+            raise ValueError(f"step plan: unknown selector {selector}")
+        if (selector != _lib.SELECT_EXACT) != (quest is not None):
+            raise ValueError("step plan: the Quest selectors need quest metadata, the exact "
+                             "one none")
+        if quest is not None and (quest.k_cache is not k_cache or quest.meta.device != dev):
+            raise ValueError("step plan: quest metadata belongs to another key cache")
         q = _check_q(q)
         _check_cache(k_cache)
         _check_cache(v_cache, "v_cache")
@@ -605,6 +618,9 @@ class StepPlan:
         self.check_accept = torch.empty(B, H, dtype=torch.uint8, device=dev)
         self.accept = torch.empty(B, H, dtype=torch.uint8, device=dev)
         self.coverage = torch.empty(B, H, dtype=torch.float32, device=dev)
+        self.selector = selector
+        self.sel_scores = (torch.empty(B, H, W, dtype=torch.float32, device=dev)
+                           if selector == _lib.SELECT_QUEST else None)
         d = _lib.StepDesc(
             B=B, H_q=H_q, H_kv=H, D=D, block_size=block_size, W=W, budget=budget,
             tau=float(tau), out_dtype=_DTYPE_CODE[q.dtype], q_stride_b=q.stride(0),
@@ -614,7 +630,10 @@ class StepPlan:
             page_indices=page_indices.data_ptr(), n_per_head=n_per_head.data_ptr(),
             page_scores=self.page_scores.data_ptr(), scores_cache=_ptr(scores_cache),
             check_accept=self.check_accept.data_ptr(), accept=self.accept.data_ptr(),
-            coverage=self.coverage.data_ptr(), stats=_ptr(stats), work=_ptr(work))
+            coverage=self.coverage.data_ptr(), stats=_ptr(stats), work=_ptr(work),
+            selector=selector, quest_meta=None if quest is None else quest.meta.data_ptr(),
+            quest_ntok=None if quest is None else quest.ntok.data_ptr(),
+            sel_scores=_ptr(self.sel_scores))
         L = _lib.load()
         ws = _workspace(dev, L.cvsa_step_workspace_bytes(ctypes.byref(d)))
         d.workspace = _ptr(ws)
@@ -634,12 +653,13 @@ class StepPlan:
         self.scores_cache = scores_cache
         self.budget = budget
         # Every buffer the plan's launches touch stays alive with the plan.
-        self.refs = (k_cache, v_cache, block_tables, context_lens, work, stats, ws)
+        self.refs = (k_cache, v_cache, block_tables, context_lens, work, stats, ws, quest)
 
-    def matches(self, q, k_cache, v_cache, block_tables, context_lens, work, stats) -> bool:
+    def matches(self, q, k_cache, v_cache, block_tables, context_lens, work, stats,
+                quest=None) -> bool:
         r = self.refs
         return (r[0] is k_cache and r[1] is v_cache and r[2] is block_tables
-                and r[3] is context_lens and r[4] is work and r[5] is stats
+                and r[3] is context_lens and r[4] is work and r[5] is stats and r[7] is quest
                 and torch._C._cuda_getCurrentRawStream(self.dev.index) == self.stream
                 and q.device == self.dev and q.dtype == self.out_dtype
                 and (q.shape, q.stride()) == self.q_meta and q.data_ptr() % 16 == 0)

@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parents[1] / "libcvsa_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 CVSA_OK = 0
 CVSA_ERR_INVALID = -1
@@ -33,6 +33,10 @@ STEP_LAZY_CHECK = 1
 STEP_SCORE = 2
 STEP_FRESH = 3
 
+SELECT_EXACT = 0
+SELECT_QUEST = 1
+SELECT_QUEST_LN = 2
+
 
 class StepDesc(ctypes.Structure):
     """cvsa_step_desc (include/cvsa_hip.h), field for field."""
@@ -45,6 +49,7 @@ class StepDesc(ctypes.Structure):
         ("page_indices", _p), ("n_per_head", _p), ("page_scores", _p), ("scores_cache", _p),
         ("check_accept", _p), ("accept", _p), ("coverage", _p), ("stats", _p), ("work", _p),
         ("workspace", _p), ("workspace_bytes", _sz),
+        ("selector", _i32), ("quest_meta", _p), ("quest_ntok", _p), ("sel_scores", _p),
     ]
 
 

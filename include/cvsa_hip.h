@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 4
+#define CVSA_ABI_VERSION 5
 
 enum {
   CVSA_OK = 0,
@@ -327,7 +327,8 @@ int cvsa_quest_refresh_scores(const uint16_t *q, int64_t q_stride_b, int64_t q_s
  * the kept selection), the lazy check (_lazy_step, :392-465: fresh scores,
  * coverage of the kept selection, keep it or reselect, decode with exact
  * recovery) and the fixed-interval scoring step (_scoring_step, :683-864,
- * counters booked by the new selection's gate).  The reference issues these
+ * counters booked by the new selection's gate), with the exact or the
+ * Quest page scorer (selector).  The reference issues these
  * as separate Python-level kernel calls; a plan validates the layer's
  * buffers once so that a step costs one host call.
  *
@@ -361,7 +362,20 @@ typedef struct cvsa_step_desc {
   int64_t *work;               /* int64[2] effective-budget counters, or NULL */
   void *workspace;             /* decode workspace, zeroed once (cvsa_workspace_init) */
   size_t workspace_bytes;      /* >= cvsa_step_workspace_bytes(desc) */
+  int32_t selector;            /* CVSA_SELECT_*: which scores rank and which gate */
+  uint16_t *quest_meta;        /* Quest selectors: metadata of k_cache, as for */
+  int32_t *quest_ntok;         /*   cvsa_quest_refresh_scores (else NULL) */
+  float *sel_scores;           /* CVSA_SELECT_QUEST: [B, H_kv, W] ranking scores (else NULL) */
 } cvsa_step_desc;
+
+/* Page scorers of a plan (CVSABackend selector / light_normalizer,
+ * cvsa/backend.py:150-177, :697-727). */
+enum {
+  CVSA_SELECT_EXACT = 0,     /* exact page scores rank and gate (cvsa_score_pages) */
+  CVSA_SELECT_QUEST = 1,     /* Quest scores rank (into sel_scores), exact scores gate; a
+                                lazy check computes the Quest scores only if a head failed */
+  CVSA_SELECT_QUEST_LN = 2   /* Quest scores rank and gate (light_normalizer) */
+};
 
 enum {
   CVSA_STEP_REUSE = 0,      /* sparse decode of the kept selection */

@@ -95,7 +95,11 @@ def test_step_plan_validates_on_the_host():
              (dict(bt_stride_b=100), _lib.CVSA_ERR_INVALID, b"stride"),
              (dict(coverage=None), _lib.CVSA_ERR_INVALID, b"null"),
              (dict(out_dtype=5), _lib.CVSA_ERR_INVALID, b"dtype"),
-             (dict(workspace_bytes=1024), _lib.CVSA_ERR_WORKSPACE, b"workspace")]
+             (dict(workspace_bytes=1024), _lib.CVSA_ERR_WORKSPACE, b"workspace"),
+             (dict(selector=3), _lib.CVSA_ERR_INVALID, b"selector"),
+             (dict(selector=_lib.SELECT_QUEST_LN), _lib.CVSA_ERR_INVALID, b"quest_meta"),
+             (dict(selector=_lib.SELECT_QUEST, quest_meta=1 << 24, quest_ntok=1 << 25),
+              _lib.CVSA_ERR_INVALID, b"sel_scores")]
     for over, code, word in cases:
         h = ctypes.c_void_p()
         rc = lib.cvsa_step_plan_create(ctypes.byref(_step_desc(**over)), ctypes.byref(h))

@@ -114,6 +114,86 @@ def test_fresh_kind_equals_separate_kernels(gpu, tau):
     assert stats_p[1].item() == 2 and stats_p[2].item() == 2
 
 
+@pytest.mark.parametrize("selector", [_lib.SELECT_QUEST, _lib.SELECT_QUEST_LN])
+@pytest.mark.parametrize("tau", [0.0, 0.995])
+def test_plan_quest_kinds_equal_separate_kernels(gpu, selector, tau):
+    """Quest-ranked plans (exact gate, or the light normalizer's Quest gate):
+    first selection, lazy check and fixed-interval step equal the separate
+    kernels, metadata included."""
+    inp, W, budget = _inputs(gpu)
+    ctx, bt = inp.context_lens, inp.block_tables
+    ln = selector == _lib.SELECT_QUEST_LN
+    qm_p, qm_r = ops.QuestPageMeta(inp.k_cache), ops.QuestPageMeta(inp.k_cache)
+    stats_p = torch.zeros(6, dtype=torch.int64, device=gpu)
+    stats_r = torch.zeros(6, dtype=torch.int64, device=gpu)
+    work_p = torch.zeros(2, dtype=torch.int64, device=gpu)
+    work_r = torch.zeros(2, dtype=torch.int64, device=gpu)
+    plan = ops.StepPlan(inp.q, inp.k_cache, inp.v_cache, bt, ctx, H, G, 16, budget, tau,
+                        stats=stats_p, work=work_p, own_scores_cache=True, selector=selector,
+                        quest=qm_p)
+    assert (plan.sel_scores is None) == ln
+
+    def gate(q):
+        return qm_r.scores(q, bt, ctx, H, G, 16) if ln else ops.score_pages(q, inp.k_cache, bt,
+                                                                            ctx, H, G, 16)
+
+    sel_r = torch.empty(2, H, budget, dtype=torch.int32, device=gpu)
+    nph_r = torch.empty(2, H, dtype=torch.int32, device=gpu)
+    cov_r = torch.empty(2, H, dtype=torch.float32, device=gpu)
+    cache_r = torch.empty(2, H, W, dtype=torch.float32, device=gpu)
+    rank_r = None if ln else torch.empty(2, H, W, dtype=torch.float32, device=gpu)
+
+    def rank(q, check=None):
+        return None if ln else qm_r.scores(q, bt, ctx, H, G, 16, check, rank_r)
+
+    def compare(got, want, ps, acc):
+        assert torch.equal(got, want)
+        assert torch.equal(plan.page_scores, ps)
+        assert torch.equal(plan.accept.view(torch.bool), acc)
+        assert torch.equal(plan.page_indices, sel_r) and torch.equal(plan.n_per_head, nph_r)
+        assert torch.equal(stats_p, stats_r) and torch.equal(work_p, work_r)
+        used = qm_r.ntok > 0   # blocks no row lists hold no metadata
+        assert torch.equal(qm_p.ntok, qm_r.ntok)
+        assert torch.equal(qm_p.meta[used], qm_r.meta[used])
+        if not ln:
+            assert torch.equal(plan.sel_scores, rank_r)
+
+    # first selection of a lazy layer
+    q1 = jitter_query(inp.q, 0.5, 6)
+    got = plan.run(_lib.STEP_FRESH, q1)
+    ps = gate(q1)
+    acc = ops.select_or_keep(ps, None, budget, ctx, 16, tau, sel_r, nph_r, cov_r, cache_r,
+                             stats_r, sel_scores=rank(q1))
+    want = ops.verified_decode(q1, inp.k_cache, inp.v_cache, bt, ctx, sel_r, nph_r, acc, H, G,
+                               16, output_dtype=q1.dtype, work=work_r)
+    compare(got, want, ps, acc)
+    assert torch.equal(plan.scores_cache, cache_r)
+
+    # lazy check (the ranking scores are computed only if a head failed)
+    q2 = jitter_query(inp.q, 0.5, 7)
+    got = plan.run(_lib.STEP_LAZY_CHECK, q2)
+    ps = gate(q2)
+    chk, cov = ops.check_coverage(ps, sel_r, nph_r, tau)
+    acc = ops.select_or_keep(ps, chk, budget, ctx, 16, tau, sel_r, nph_r, cov, cache_r,
+                             stats_r, sel_scores=rank(q2, chk))
+    want = ops.verified_decode(q2, inp.k_cache, inp.v_cache, bt, ctx, sel_r, nph_r, acc, H, G,
+                               16, output_dtype=q2.dtype, work=work_r)
+    compare(got, want, ps, acc)
+    assert torch.equal(plan.check_accept.view(torch.bool), chk)
+    assert torch.equal(plan.scores_cache, cache_r)
+    assert bool(chk.all()) == (tau == 0.0)
+
+    # fixed-interval scoring step
+    q3 = jitter_query(inp.q, 0.5, 8)
+    got = plan.run(_lib.STEP_SCORE, q3)
+    ps = gate(q3)
+    acc = ops.select_or_keep(ps, None, budget, ctx, 16, tau, sel_r, nph_r, cov, None, stats_r,
+                             count_gate=True, sel_scores=rank(q3))
+    want = ops.verified_decode(q3, inp.k_cache, inp.v_cache, bt, ctx, sel_r, nph_r, acc, H, G,
+                               16, output_dtype=q3.dtype, work=work_r)
+    compare(got, want, ps, acc)
+
+
 def test_plan_rejects_buffers_it_cannot_use(gpu):
     inp, W, budget = _inputs(gpu)
     args = (inp.q, inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens, H, G, 16)
@@ -126,6 +206,11 @@ def test_plan_rejects_buffers_it_cannot_use(gpu):
                      H, G, 16, budget, 0.9)
     with pytest.raises(ValueError):  # budget outside [1, W]
         ops.StepPlan(*args, W + 1, 0.9)
+    with pytest.raises(ValueError):  # a Quest selector without metadata
+        ops.StepPlan(*args, budget, 0.9, selector=_lib.SELECT_QUEST)
+    with pytest.raises(ValueError):  # metadata of another cache
+        ops.StepPlan(*args, budget, 0.9, selector=_lib.SELECT_QUEST_LN,
+                     quest=ops.QuestPageMeta(inp.k_cache.clone()))
 
 
 @pytest.mark.parametrize("kw", [
@@ -133,6 +218,10 @@ def test_plan_rejects_buffers_it_cannot_use(gpu):
     dict(lazy=True, check_interval=2),
     dict(lazy=False, reuse_interval=1),
     dict(lazy=False, reuse_interval=3),
+    dict(lazy=True, check_interval=2, selector="quest"),
+    dict(lazy=True, check_interval=3, selector="quest", light_normalizer=True),
+    dict(lazy=False, reuse_interval=2, selector="quest"),
+    dict(lazy=False, reuse_interval=1, selector="quest", light_normalizer=True),
 ])
 def test_backend_plans_equal_kernel_path(gpu, kw):
     """Same decode loop (appends included) through step plans and through
