@@ -110,6 +110,30 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *w
   return before + incl - v;
 }
 
+// Exclusive prefix sum of one uint64 per thread over the block, plus total.
+__device__ __forceinline__ unsigned long long block_exclusive_scan_u64(
+    unsigned long long v, unsigned long long *wsum64, unsigned long long &total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  unsigned long long incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const unsigned long long o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  lds_barrier();
+  if (lane == 63) wsum64[wave] = incl;
+  lds_barrier();
+  unsigned long long before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const unsigned long long x = wsum64[w];
+    before += (w < wave) ? x : 0ull;
+    tot += x;
+  }
+  total = tot;
+  return before + incl - v;
+}
+
 // lse over a set given its fp32 maximum `mx` and sum of exp(s - M); the
 // reference floors the running max at -1e20 (coverage.py:183, :207).
 __device__ __forceinline__ float lse_from(float mx_floor, float sum) {
@@ -218,13 +242,22 @@ __device__ __forceinline__ void radix_select(const float (&val)[R], Alive alive,
   T = prefix;
 }
 
+// Row budgets (MODE): kUniform, the same `budget` for every row;
+// kTopP, the smallest prefix of the row's pages by score whose softmax mass
+// reaches top_p (CVSABackend._topp_select, backend.py:652-681), at least 3;
+// kTable, head_budgets[h] (_static_select, :622-650).  `width` is the row
+// stride of page_indices: k is clamped to it.
+enum { kUniform = 0, kTopP = 1, kTable = 2 };
+static_assert(kHistCopies * kHistStride >= kBuckets, "hist_c holds a second-level histogram");
+
 // SEP: the selection ranks sel_scores while the coverage gate (and
 // scores_cache) use scores (CVSABackend._scoring_step, backend.py:723-727:
 // the Quest selector proposes, the exact scan verifies).
-template <int R, bool SEP>
+template <int R, bool SEP, int MODE>
 __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     const float *__restrict__ scores, const float *__restrict__ sel_scores, int W, int H_kv,
-    const int32_t *__restrict__ context_lens, int block_size, int budget,
+    const int32_t *__restrict__ context_lens, int block_size, int budget, int width,
+    float top_p, const int32_t *__restrict__ head_budgets,
     int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
     uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
     const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
@@ -238,6 +271,13 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2];
   __shared__ uint32_t s_digit, s_krem, s_T, s_bucket, s_kb, s_nb, s_ncand;
   __shared__ int s_nok, s_nbad;
+  // Top-p only: softmax mass per value bucket (64-bit fixed point, so the
+  // sums do not depend on the order of the atomic adds).
+  __shared__ unsigned long long mass_b[MODE == kTopP ? kBuckets : 1];
+  __shared__ unsigned long long s_candm[MODE == kTopP ? kRankCands : 1];
+  __shared__ uint32_t s_candi[MODE == kTopP ? kRankCands : 1];
+  __shared__ unsigned long long wsum64[MODE == kTopP ? kSelWaves : 1];
+  __shared__ unsigned long long s_mass;
 
   const int bh = blockIdx.x;
   const int b = bh / H_kv;
@@ -358,30 +398,215 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   }
   block_range(kmax, kneg, cnt, red_rng);
   const uint32_t kmin = ~kneg, n_fin = cnt & 0xFFFFu, n_odd = cnt >> 16;
-  // plan 0: T and krem found; 1: radix select over the row; 2: radix
-  // select of the k_radix-th largest inside bucket bstar.
-  uint32_t T = 0, krem = 0, k_radix = (uint32_t)budget;
-  int plan = 1, bstar = -1;
   float vmin = 0.f, inv = 0.f;
   const auto bucket = [&](int r) { return finite(r) ? value_bucket(val[r], vmin, inv) : -1; };
-  if (n_odd == 0 && (uint32_t)budget > n_fin) {
+
+  // Top-p budget: 1 + the number of pages, in descending score order, whose
+  // inclusive cumulative softmax mass is below top_p, clamped to [3, W]
+  // (backend.py:672-678).  exp(s - max) is summed as 40-bit fixed point.
+  // The page where the mass crosses top_p * total is found by the same value
+  // buckets as the top-k (mass per bucket, scanned from the top), then among
+  // that bucket's scores: ranked exactly when they are at most 64, else
+  // through a second 4096-bucket level inside the bucket, whose crossing
+  // bucket is then walked in page order (its scores differ by at most
+  // 2^-24 of the row's range, or are equal).
+  const auto find_cross = [&](const uint32_t *cnts, const unsigned long long *ms,
+                              unsigned long long base, unsigned long long target)
+                              __attribute__((always_inline)) {
+    uint32_t c[kBucketsPerThread], lc = 0;
+    unsigned long long m[kBucketsPerThread], lm = 0;
+#pragma unroll
+    for (int j = 0; j < kBucketsPerThread; ++j) {
+      const int idx = kBuckets - 1 - (kBucketsPerThread * t + j);
+      c[j] = cnts[idx];
+      m[j] = ms[idx];
+      lc += c[j];
+      lm += m[j];
+    }
+    if (t == 0) s_bucket = 0xFFFFFFFFu;
+    uint32_t ctot;
+    unsigned long long mtot;
+    uint32_t cab = block_exclusive_scan(lc, wsum, ctot);
+    unsigned long long mab = base + block_exclusive_scan_u64(lm, wsum64, mtot);
+#pragma unroll
+    for (int j = 0; j < kBucketsPerThread; ++j) {
+      if (mab < target && mab + m[j] >= target) {
+        s_bucket = (uint32_t)(kBuckets - 1 - (kBucketsPerThread * t + j));
+        s_kb = cab;
+        s_nb = c[j];
+        s_mass = mab;
+      }
+      cab += c[j];
+      mab += m[j];
+    }
+    lds_barrier();
+  };
+  const auto topp_budget = [&](bool &hist_ready) __attribute__((always_inline)) -> int {
+    // A row holding +inf / NaN, or no finite score, has a NaN softmax in
+    // the reference: no prefix counts as below top_p, need = 1.
+    if (n_odd != 0 || n_fin == 0) return min(3, W);
+    const float M = key_value(kmax);
+    const auto mass = [&](int r) __attribute__((always_inline)) -> unsigned long long {
+      return finite(r) ? (unsigned long long)(expf(val[r] - M) * 1099511627776.0f) : 0ull;
+    };
+    unsigned long long part = 0, total = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) part += mass(r);
+    (void)block_exclusive_scan_u64(part, wsum64, total);
+    const unsigned long long target =
+        (unsigned long long)ceil((double)top_p * (double)total);
+    uint32_t before = 0;          // pages ranked above the range still to walk
+    unsigned long long base = 0;  // their mass
+    int lvl = 0, b1 = -1, b2 = -1;
+    float vmin2 = 0.f, inv2 = 0.f;
+    const float lo = key_value(kmin);
+    const float inv1 = (float)kBuckets / (M - lo);
+    if (kmin != kmax && inv1 > 0.f && inv1 <= 3.402823466e38f) {
+      vmin = lo;  // the buckets of the top-k below
+      inv = inv1;
+      for (int i = t; i < kBuckets; i += kSelThreads) mass_b[i] = 0ull;
+      lds_barrier();
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int bk = bucket(r);
+        if (bk >= 0) {
+          atomicAdd(&hist_b[bk], 1u);
+          atomicAdd(&mass_b[bk], mass(r));
+        }
+      }
+      lds_barrier();
+      hist_ready = true;
+      find_cross(hist_b, mass_b, 0ull, target);
+      if (s_bucket == 0xFFFFFFFFu) return min(max((int)n_fin, 3), W);  // not reached
+      b1 = (int)s_bucket;
+      before = s_kb;
+      base = s_mass;
+      const uint32_t nb = s_nb;
+      lvl = 1;
+      if (nb <= (uint32_t)kRankCands) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (bucket(r) == b1) {
+            const uint32_t slot = atomicAdd(&s_ncand, 1u);
+            s_cand[slot] = order_key(val[r]);
+            s_candm[slot] = mass(r);
+            s_candi[slot] = (uint32_t)(i0 + r);
+          }
+        }
+        lds_barrier();
+        if (t < kWave) {
+          uint32_t lt = 0;
+          if (t < (int)nb) {
+            const uint32_t key = s_cand[t], idx = s_candi[t];
+            unsigned long long prefix = 0;
+            for (uint32_t j = 0; j < nb; ++j) {
+              const uint32_t kj = s_cand[j];
+              prefix += (kj > key || (kj == key && s_candi[j] < idx)) ? s_candm[j] : 0ull;
+            }
+            lt = base + prefix + s_candm[t] < target ? 1u : 0u;
+          }
+          lt = wave_sum_u32(lt);
+          if (t == 0) {
+            s_kb = lt;
+            s_ncand = 0;  // the top-k gathers its own candidates
+          }
+        }
+        lds_barrier();
+        return min(max((int)(before + s_kb + 1), 3), W);
+      }
+      // Second level: the key range of bucket b1's scores.
+      uint32_t kx = 0, kn = 0, cn = 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (bucket(r) == b1) {
+          const uint32_t key = order_key(val[r]);
+          kx = max(kx, key);
+          kn = max(kn, ~key);
+        }
+      }
+      block_range(kx, kn, cn, red_rng);
+      if (kx != ~kn) {
+        vmin2 = key_value(~kn);
+        inv2 = (float)kBuckets / (key_value(kx) - vmin2);
+        if (inv2 > 0.f && inv2 <= 3.402823466e38f) {
+          for (int i = t; i < kBuckets; i += kSelThreads) {
+            hist_c[i] = 0u;
+            mass_b[i] = 0ull;
+          }
+          lds_barrier();
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            if (bucket(r) == b1) {
+              const int bk = value_bucket(val[r], vmin2, inv2);
+              atomicAdd(&hist_c[bk], 1u);
+              atomicAdd(&mass_b[bk], mass(r));
+            }
+          }
+          lds_barrier();
+          find_cross(hist_c, mass_b, base, target);
+          if (s_bucket != 0xFFFFFFFFu) {
+            b2 = (int)s_bucket;
+            before += s_kb;
+            base = s_mass;
+            lvl = 2;
+          }
+        }
+      }
+    }
+    // The remaining range in page order.
+    const auto in_range = [&](int r) __attribute__((always_inline)) {
+      if (!finite(r)) return false;
+      if (lvl == 0) return true;
+      if (bucket(r) != b1) return false;
+      return lvl == 1 || value_bucket(val[r], vmin2, inv2) == b2;
+    };
+    unsigned long long mine = 0, tot = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (in_range(r)) mine += mass(r);
+    unsigned long long run = base + block_exclusive_scan_u64(mine, wsum64, tot);
+    uint32_t lt = 0, lt_total = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (in_range(r)) {
+        run += mass(r);
+        lt += run < target ? 1u : 0u;
+      }
+    }
+    (void)block_exclusive_scan(lt, wsum, lt_total);
+    return min(max((int)(before + lt_total + 1), 3), W);
+  };
+
+  // The row's budget k.
+  int k = budget;
+  bool hist_ready = false;  // hist_b already holds the bucket counts
+  if constexpr (MODE == kTable) k = min(max(head_budgets[bh % H_kv], 1), W);
+  if constexpr (MODE == kTopP) k = topp_budget(hist_ready);
+  k = min(k, width);  // a row holds at most `width` pages: the best ones
+  // plan 0: T and krem found; 1: radix select over the row; 2: radix
+  // select of the k_radix-th largest inside bucket bstar.
+  uint32_t T = 0, krem = 0, k_radix = (uint32_t)k;
+  int plan = 1, bstar = -1;
+  if (n_odd == 0 && (uint32_t)k > n_fin) {
     // Every finite page, then the lowest -inf pages.
     T = order_key(-INFINITY);
-    krem = (uint32_t)budget - n_fin;
+    krem = (uint32_t)k - n_fin;
     plan = 0;
   } else if (n_odd == 0 && kmin == kmax) {
     T = kmax;
-    krem = (uint32_t)budget;
+    krem = (uint32_t)k;
     plan = 0;
   } else if (n_odd == 0) {
     vmin = key_value(kmin);
     inv = (float)kBuckets / (key_value(kmax) - vmin);
     // Otherwise max - min overflows.
     if (inv > 0.f && inv <= 3.402823466e38f) {
+      if (!hist_ready) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int bk = bucket(r);
-        if (bk >= 0) atomicAdd(&hist_b[bk], 1u);
+        for (int r = 0; r < R; ++r) {
+          const int bk = bucket(r);
+          if (bk >= 0) atomicAdd(&hist_b[bk], 1u);
+        }
       }
       lds_barrier();
       // Thread t holds buckets kBuckets-1-(4t+j), j = 0..3: the exclusive
@@ -396,9 +621,9 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
       uint32_t above = block_exclusive_scan(local, wsum, total_b);
 #pragma unroll
       for (int j = 0; j < kBucketsPerThread; ++j) {
-        if (above < (uint32_t)budget && above + c[j] >= (uint32_t)budget) {
+        if (above < (uint32_t)k && above + c[j] >= (uint32_t)k) {
           s_bucket = (uint32_t)(kBuckets - 1 - (kBucketsPerThread * t + j));
-          s_kb = (uint32_t)budget - above;
+          s_kb = (uint32_t)k - above;
           s_nb = c[j];
         }
         above += c[j];
@@ -456,10 +681,11 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   uint32_t total;
   const uint32_t excl = block_exclusive_scan(gt | (eq << 16), wsum, total);
   const uint32_t gt_before = excl & 0xFFFFu, eq_before = excl >> 16;
-  const int n_sel = min(budget, n_valid_pages(ctx, block_size));
+  const int n_write = k;
+  const int n_sel = min(k, n_valid_pages(ctx, block_size));
   uint32_t eq_seen = eq_before;
   uint32_t pos = gt_before + min(eq_before, krem);
-  int32_t *out_row = page_indices + (int64_t)bh * budget;
+  int32_t *out_row = page_indices + (int64_t)bh * width;
   bool counted[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -475,7 +701,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     }
     counted[r] = sel && (int)pos < n_sel;
     if (sel) {
-      if ((int)pos < budget) out_row[pos] = i0 + r;  // always true for a correct select
+      if ((int)pos < n_write) out_row[pos] = i0 + r;  // pos < k for a correct select
       ++pos;
     }
   }
@@ -494,7 +720,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   // Padding lanes of the reference's power-of-two selection block carry
   // -1e20 into the max whenever n_sel is below that block (coverage.py:205).
   int msel_block = 1;
-  while (msel_block < budget) msel_block <<= 1;
+  while (msel_block < width) msel_block <<= 1;
   const float m_sel = n_sel < msel_block ? fmaxf(ms, -1e20f) : ms;
   float se = 0.f, ss = 0.f;
 #pragma unroll
@@ -617,7 +843,8 @@ static int launch_select(const char *name, const float *page_scores, const float
                          int32_t budget, int32_t *page_indices, int32_t *n_per_head, float tau,
                          uint8_t *accept_out, float *coverage_out, const uint8_t *check_accept,
                          float *scores_cache, int64_t *stats, int count_gate,
-                         void *stream) {
+                         void *stream, int mode = kUniform, float top_p = 0.f,
+                         const int32_t *head_budgets = nullptr) {
   CVSA_REQUIRE(page_scores && context_lens && page_indices && n_per_head, CVSA_ERR_INVALID,
                "%s: null pointer argument", name);
   CVSA_REQUIRE((accept_out == nullptr) == (coverage_out == nullptr), CVSA_ERR_INVALID,
@@ -636,16 +863,25 @@ static int launch_select(const char *name, const float *page_scores, const float
   const dim3 grid(B * H_kv);
   hipStream_t st = (hipStream_t)stream;
   long long *st64 = reinterpret_cast<long long *>(stats);
+  // In the variable-budget modes `budget` is the row stride of page_indices.
+  const int width = budget;
   switch (R) {
-#define CVSA_SEL_LAUNCH(RR, SEP)                                                          \
-  hipLaunchKernelGGL((select_topk_kernel<RR, SEP>), grid, dim3(kSelThreads), 0, st,         \
+#define CVSA_SEL_LAUNCH(RR, SEP, MODE)                                                      \
+  hipLaunchKernelGGL((select_topk_kernel<RR, SEP, MODE>), grid, dim3(kSelThreads), 0, st,   \
                      page_scores, sel_scores, W, H_kv, context_lens, block_size, budget,    \
-                     page_indices, n_per_head, tau, accept_out, coverage_out, check_accept, \
-                     B * H_kv, scores_cache, st64, count_gate)
+                     width, top_p, head_budgets, page_indices, n_per_head, tau, accept_out, \
+                     coverage_out, check_accept, B * H_kv, scores_cache, st64, count_gate)
+#define CVSA_SEL_MODES(RR, SEP)                                    \
+  if (mode == kTopP) CVSA_SEL_LAUNCH(RR, SEP, kTopP);              \
+  else if (mode == kTable) CVSA_SEL_LAUNCH(RR, SEP, kTable);       \
+  else CVSA_SEL_LAUNCH(RR, SEP, kUniform);
 #define CVSA_SEL_CASE(RR)                                       \
   case RR:                                                      \
-    if (sel_scores != nullptr) CVSA_SEL_LAUNCH(RR, true);       \
-    else CVSA_SEL_LAUNCH(RR, false);                            \
+    if (sel_scores != nullptr) {                                \
+      CVSA_SEL_MODES(RR, true)                                  \
+    } else {                                                    \
+      CVSA_SEL_MODES(RR, false)                                 \
+    }                                                           \
     break;
     CVSA_SEL_CASE(1)
     CVSA_SEL_CASE(2)
@@ -654,6 +890,7 @@ static int launch_select(const char *name, const float *page_scores, const float
     CVSA_SEL_CASE(16)
     CVSA_SEL_CASE(32)
 #undef CVSA_SEL_CASE
+#undef CVSA_SEL_MODES
 #undef CVSA_SEL_LAUNCH
     default:
       return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "%s: W=%d too large", name, W);
@@ -688,6 +925,22 @@ extern "C" int cvsa_select_or_keep(const float *page_scores, const float *sel_sc
   return launch_select("select_or_keep", page_scores, sel_scores, B, H_kv, W, context_lens,
                        block_size, budget, page_indices, n_per_head, tau, accept_out,
                        coverage_out, check_accept, scores_cache, stats, count_gate, stream);
+}
+
+extern "C" int cvsa_select_budgeted(const float *page_scores, const float *sel_scores,
+                                    int32_t B, int32_t H_kv, int32_t W,
+                                    const int32_t *context_lens, int32_t block_size,
+                                    float top_p, const int32_t *head_budgets, int32_t width,
+                                    int32_t *page_indices, int32_t *n_per_head, float tau,
+                                    uint8_t *accept_out, float *coverage_out, void *stream) {
+  CVSA_REQUIRE((top_p > 0.f) != (head_budgets != nullptr), CVSA_ERR_INVALID,
+               "select_budgeted: give exactly one of top_p and head_budgets");
+  CVSA_REQUIRE(head_budgets != nullptr || top_p < 1.f, CVSA_ERR_INVALID,
+               "select_budgeted: top_p=%g must be in (0, 1)", (double)top_p);
+  return launch_select("select_budgeted", page_scores, sel_scores, B, H_kv, W, context_lens,
+                       block_size, width, page_indices, n_per_head, tau, accept_out,
+                       coverage_out, nullptr, nullptr, nullptr, 0, stream,
+                       top_p > 0.f ? kTopP : kTable, top_p, head_budgets);
 }
 
 extern "C" int cvsa_check_coverage(const float *page_scores, int32_t B,

@@ -36,9 +36,13 @@ coverage gate, so no step reads all keys.  A lazy check on the device asks
 for the ranking scores with its flags: they are computed only when some
 head failed.
 
-Not implemented here (the constructor raises NotImplementedError): the
-reference's other selectors (adaptive_selection, static_budget_table,
-top_p).
+Per-head budgets: ``top_p`` (the smallest page set per head whose softmax
+mass over the ranking scores reaches top_p, backend.py:652-681) and
+``static_budget_table`` (offline per-head fractions, :622-650) select through
+ops.select_budgeted with the new selection's gate fused; like the reference
+they read the largest budget on the host (top-p) and take the per-kernel
+path.  Not implemented here (the constructor raises NotImplementedError):
+adaptive_selection.
 """
 from __future__ import annotations
 
@@ -161,14 +165,12 @@ class CVSABackend:
         if top_p is not None and not (0.0 < top_p < 1.0):
             raise ValueError(f"top_p must be in (0, 1), got {top_p}")
         self.top_p = top_p
-        unsupported = [name for name, on in (
-            ("adaptive_selection", adaptive_selection),
-            ("static_budget_table", static_budget_table is not None),
-            ("top_p", top_p is not None)) if on]
-        if unsupported:
+        if adaptive_selection:
             raise NotImplementedError(
-                "CVSABackend on MI355X implements the exact and Quest page scorers with a "
-                f"uniform budget; not available: {', '.join(unsupported)}")
+                "CVSABackend on MI355X implements the uniform, top-p and static-table "
+                "budgets; not available: adaptive_selection")
+        # Per-head budgets of the static table on the device, per (layer, W).
+        self._head_budgets: Dict[Tuple[int, int, torch.device], Tuple[torch.Tensor, int]] = {}
         # Quest metadata per key cache (keyed by id, with a weak reference to
         # tell a reused id from the cache it was built for).
         self._quest_meta: Dict[int, Tuple[weakref.ref, ops.QuestPageMeta]] = {}
@@ -536,7 +538,8 @@ class CVSABackend:
         """Build the layer's step plan, or None where a step needs the
         per-kernel path (timing, host-side decisions, unsupported buffers)."""
         if (self._track_timing or self.random_reject_prob is not None
-                or self.approx_recovery_pct is not None):
+                or self.approx_recovery_pct is not None or self.top_p is not None
+                or self.static_budget_table is not None):
             return None
         dev = q.device
         work = self._work(dev)
@@ -609,7 +612,8 @@ class CVSABackend:
         """Whether the lazy accept-all decision can stay on the device: exact
         recovery, no counterfactual rejections, the cached selection and
         scores match this call's shape, counters live on this device."""
-        if self.random_reject_prob is not None or self.approx_recovery_pct is not None:
+        if (self.random_reject_prob is not None or self.approx_recovery_pct is not None
+                or self.top_p is not None or self.static_budget_table is not None):
             return False
         page_indices, n_per_head = self._cached_selection[layer_idx]
         B, H_kv, W = page_scores.shape
@@ -698,10 +702,17 @@ class CVSABackend:
         # In the fixed-interval schedule the gate's counters (:859-863) are
         # booked on the device, so the step needs no host read.
         dev = page_scores.device
-        device_book = (not self.lazy and self.random_reject_prob is None
+        budgeted = self.top_p is not None or self.static_budget_table is not None
+        device_book = (not budgeted and not self.lazy and self.random_reject_prob is None
                        and self.approx_recovery_pct is None
                        and self._ensure_dev_stats(dev) is not None)
-        if device_book:
+        if budgeted:
+            # Per-head budgets (:727-732), gate fused; budget becomes the
+            # largest one, as in the reference.
+            page_indices, n_per_head, accept_mask, budget = self._time_kernel(
+                "coverage", self._budgeted_select, page_scores, sel_scores, layer_idx,
+                context_lens)
+        elif device_book:
             H = self.num_kv_heads
             page_indices = torch.empty(B, H, budget, dtype=torch.int32, device=dev)
             n_per_head = torch.empty(B, H, dtype=torch.int32, device=dev)
@@ -766,6 +777,30 @@ class CVSABackend:
         if not device_book:
             self._h_total_scoring_steps += 1                                      # :859
         return output
+
+    def _budgeted_select(self, page_scores, sel_scores, layer_idx, context_lens):
+        """_topp_select / _static_select (backend.py:622-681) with the coverage
+        gate of the new selection: (page_indices [B, H_kv, max_budget],
+        n_per_head, accept_mask, max_budget)."""
+        W = page_scores.shape[2]
+        if self.top_p is not None:
+            idx, nph, acc, _cov = ops.select_budgeted(
+                page_scores, context_lens, self.block_size, top_p=self.top_p, tau=self.tau,
+                sel_scores=sel_scores)
+            max_budget = int(nph.max().item())   # :679, a host read as in the reference
+            return idx[:, :, :max_budget].contiguous(), nph, acc, max_budget
+        key = (layer_idx, W, page_scores.device)
+        entry = self._head_budgets.get(key)
+        if entry is None:
+            fracs = self.static_budget_table[layer_idx]
+            per_head = torch.clamp((fracs * W).round().long(), min=3, max=W)      # :638
+            entry = (per_head.to(torch.int32).to(page_scores.device), int(per_head.max()))
+            self._head_budgets[key] = entry
+        budgets, max_budget = entry
+        idx, nph, acc, _cov = ops.select_budgeted(
+            page_scores, context_lens, self.block_size, head_budgets=budgets, width=max_budget,
+            tau=self.tau, sel_scores=sel_scores)
+        return idx, nph, acc, max_budget
 
     def _approx_recovery(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx,
                          page_scores, page_indices, n_per_head, accept_mask, budget, n_pages):

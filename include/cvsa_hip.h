@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 5
+#define CVSA_ABI_VERSION 6
 
 enum {
   CVSA_OK = 0,
@@ -115,6 +115,36 @@ int cvsa_select_or_keep(const float *page_scores, const float *sel_scores,
                         int32_t *n_per_head, float tau, uint8_t *accept_out,
                         float *coverage_out, float *scores_cache,
                         int64_t *stats, int32_t count_gate, void *stream);
+
+/*
+ * Selection with a budget per (b, kv-head) row.  Replaces the top-p branch
+ * of CVSABackend._scoring_step (_topp_select, cvsa/backend.py:652-681) and
+ * the static-table branch (_static_select, :622-650).
+ *   top_p in (0, 1), head_budgets NULL: with p = softmax(sel row),
+ *     need = 1 + #{k : sum of the k largest p < top_p}, k_row =
+ *     clamp(need, 3, W).  The masses exp(s - max) are summed exactly as
+ *     40-bit fixed point, in descending score order; the reference's fp32
+ *     cumsum can put need one page off where the cumulative mass lies
+ *     within rounding of top_p.  A row with +inf / NaN or no finite score
+ *     (NaN softmax in the reference) gets need = 1.
+ *   head_budgets [H_kv] int32 (top_p = 0): k_row = head_budgets[h]
+ *     (clamped to [1, W]; the reference's clamp(round(frac*P), 3, P) is
+ *     applied by the caller).
+ *   k_row is then clamped to `width`, the row stride of page_indices: the
+ *     row's first k_row entries receive the pages of its k_row largest
+ *     ranking scores (ties to the lower page) in ascending page order;
+ *     entries past k_row are left unwritten.  width = W never clamps.
+ *   n_per_head[b,h] = min(k_row, n_valid(b)).
+ *   sel_scores (optional): the ranking scores (the Quest selector); NULL =
+ *     page_scores.  accept_out / coverage_out (optional): the coverage
+ *     gate of the new selection on page_scores, as cvsa_select_topk.
+ */
+int cvsa_select_budgeted(const float *page_scores, const float *sel_scores,
+                         int32_t B, int32_t H_kv, int32_t W,
+                         const int32_t *context_lens, int32_t block_size,
+                         float top_p, const int32_t *head_budgets, int32_t width,
+                         int32_t *page_indices, int32_t *n_per_head, float tau,
+                         uint8_t *accept_out, float *coverage_out, void *stream);
 
 /*
  * Coverage gate.  Replaces triton_check_coverage

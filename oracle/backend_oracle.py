@@ -4,7 +4,8 @@ Follows cvsa/backend.py of DJ-Melvin/coverage-verified-sparse-attention
 (line numbers below) for the configurations this build covers: the exact
 page scorer or the Quest min/max scorer (selector="quest", for selection
 only or, with light_normalizer, for the coverage gate too) with a uniform
-budget, exact recovery (complement + LSE merge)
+budget, top-p budgets (``top_p``) or a static per-head budget table
+(``static_budget_table``), exact recovery (complement + LSE merge)
 or approximate recovery (``approx_recovery_pct``), dense layers, the fixed
 interval (``reuse_interval``) and lazy (``check_interval`` /
 ``coverage_interval``) schedules, and the statistics of get_stats().
@@ -26,7 +27,8 @@ class OracleCVSABackend:
                  budget_pct=0.10, reuse_interval=16, coverage_threshold=0.90,
                  dense_layers: Optional[List[int]] = None, lazy=False,
                  check_interval=None, coverage_interval=None, approx_recovery_pct=None,
-                 selector="exact", light_normalizer=False, acc_dtype=torch.float64):
+                 selector="exact", light_normalizer=False, top_p=None,
+                 static_budget_table=None, acc_dtype=torch.float64):
         # :80-115
         self.num_kv_heads = num_kv_heads
         self.num_q_heads = num_q_heads
@@ -44,6 +46,10 @@ class OracleCVSABackend:
         self.coverage_interval = coverage_interval or self.check_interval
         self.selector = selector
         self.light_normalizer = light_normalizer
+        self.top_p = top_p
+        self.static_budget_table = None if static_budget_table is None else {
+            int(layer): torch.as_tensor(f, dtype=torch.float32)
+            for layer, f in static_budget_table.items()}
         self.acc_dtype = acc_dtype
         self.reset()
 
@@ -204,7 +210,15 @@ class OracleCVSABackend:
             sel_scores = ref.quest_page_scores(q, k_cache, block_tables, context_lens,
                                                self.num_kv_heads, self.num_q_per_kv,
                                                self.block_size, self.acc_dtype)
-        idx, nph = ref.select_topk(sel_scores, budget, context_lens, self.block_size)
+        if self.top_p is not None:                                               # :727-729
+            idx, nph = ref.topp_select(sel_scores, self.top_p, context_lens, self.block_size)
+            budget = idx.shape[-1]
+        elif self.static_budget_table is not None:                               # :730-732
+            idx, nph = ref.static_select(sel_scores, self.static_budget_table[layer_idx],
+                                         context_lens, self.block_size)
+            budget = idx.shape[-1]
+        else:
+            idx, nph = ref.select_topk(sel_scores, budget, context_lens, self.block_size)
         o_d, m_d, l_d = ref.sparse_decode_unnorm(q, k_cache, v_cache, block_tables, idx, nph,
                                                  context_lens, self.num_kv_heads,
                                                  self.num_q_per_kv, self.block_size,

@@ -155,6 +155,72 @@ def select_topk(page_scores: torch.Tensor, budget: int, context_lens: torch.Tens
     return idx, nph
 
 
+def topp_need(sel_scores: torch.Tensor, top_p: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The top-p budget of CVSABackend._topp_select (cvsa/backend.py:664-678)
+    in fp64: p = softmax(row), sorted descending (ties to the lower page),
+    need = 1 + #{k : cumsum_k < top_p}, clamped to [3, P].  top_p is compared
+    as fp32, as torch compares a float32 tensor with a Python float.  Returns
+    (need [B, H] int64, the descending order [B, H, P]).  A row whose
+    softmax is NaN (+inf / NaN scores, or no finite one) gets need = 3."""
+    B, H, P = sel_scores.shape
+    s = sel_scores.to(torch.float64)
+    order = torch.sort(s, dim=-1, descending=True, stable=True).indices
+    with torch.no_grad():
+        probs = torch.softmax(s, dim=-1)
+    cum = torch.cumsum(probs.gather(-1, order), dim=-1)
+    p32 = float(torch.tensor(top_p, dtype=torch.float32))
+    need = (cum < p32).sum(dim=-1) + 1
+    return need.clamp(min=3, max=P), order
+
+
+def topp_select(sel_scores, top_p, context_lens, block_size):
+    """CVSABackend._topp_select (cvsa/backend.py:652-681): the pages of each
+    row's top-p set (see topp_need) in ascending page order, rows of
+    max_budget = max n_per_head entries whose first n_per_head are the
+    valid pages of the set; n_per_head = min(need, n_valid)."""
+    B, H, P = sel_scores.shape
+    need, order = topp_need(sel_scores, top_p)
+    nv = n_valid_pages(context_lens, block_size).view(B, 1)
+    nph = torch.minimum(need, nv.expand(B, H)).to(torch.int32)
+    return _prefix_sets(order, need, nph)
+
+
+def static_select(sel_scores, fractions, context_lens, block_size):
+    """CVSABackend._static_select (cvsa/backend.py:622-650): per-head budgets
+    clamp(round(frac * P), 3, P) from an offline table, n_per_head =
+    min(budget_h, n_valid); the top budget_h pages of each row in ascending
+    page order (ties to the lower page), rows of max budget entries."""
+    B, H, P = sel_scores.shape
+    per_head = static_budgets(fractions, P)
+    order = torch.sort(sel_scores.to(torch.float64), dim=-1, descending=True,
+                       stable=True).indices
+    k = per_head.view(1, H).expand(B, H)
+    nv = n_valid_pages(context_lens, block_size).view(B, 1)
+    nph = torch.minimum(k, nv.expand(B, H)).to(torch.int32)
+    return _prefix_sets(order, k, nph)
+
+
+def static_budgets(fractions, P: int) -> torch.Tensor:
+    """Per-head page budgets of a static table row (backend.py:638):
+    clamp(round(frac * P), 3, P), round half to even as torch.round."""
+    f = torch.as_tensor(fractions, dtype=torch.float32)
+    return torch.clamp(torch.round(f * P).long(), min=3, max=P)
+
+
+def _prefix_sets(order, k_row, nph):
+    """Rows of the k_row first pages of `order`, sorted ascending, truncated
+    to max(nph) entries (the valid ones come first: invalid pages score -inf
+    and have the highest indices)."""
+    B, H, P = order.shape
+    width = max(int(nph.max()), 1)
+    out = torch.zeros(B, H, width, dtype=torch.int32)
+    for b in range(B):
+        for h in range(H):
+            sel = torch.sort(order[b, h, :int(k_row[b, h])]).values[:width]
+            out[b, h, :sel.numel()] = sel.to(torch.int32)
+    return out, nph
+
+
 def check_coverage(page_scores, selected_indices, n_per_head, tau,
                    acc_dtype=torch.float64) -> Tuple[torch.Tensor, torch.Tensor]:
     """triton_check_coverage (cvsa/kernels/coverage.py:218-265, kernel

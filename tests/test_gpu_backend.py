@@ -84,6 +84,42 @@ def _check_near_tie_selection(pi, nph, ps, budget, bad_sel):
         assert float(rest.max()) <= kth + tol, (b, h)
 
 
+def _check_budgeted_selection(pi, nph, t, kw, tau):
+    """Per-head budgets (top_p / static_budget_table): each row's first
+    n_per_head pages equal the oracle's, except rows whose budget or k-th
+    page is numerically undecidable (top-p boundary within 1e-4 of top_p:
+    the GPU ranks its fp32 page scores, the oracle fp64 ones; or the score
+    gap after the k-th page within the margin), which are counted and not
+    compared.  Returns (undecidable rows, accept-margin mask)."""
+    ranked = t.get("sel_scores", t["page_scores"])
+    wi, wn = t["page_indices"], t["n_per_head"]
+    B, H, W = ranked.shape
+    srt = torch.sort(ranked, dim=-1, descending=True).values
+    loose = torch.zeros(B, H, dtype=torch.bool)
+    if kw.get("top_p") is not None:
+        need, order = ref.topp_need(ranked, kw["top_p"])
+        cum = torch.cumsum(torch.softmax(ranked.double(), -1).gather(-1, order), -1)
+        p32 = float(torch.tensor(kw["top_p"], dtype=torch.float32))
+        for b in range(B):
+            for h in range(H):
+                k = int(need[b, h])
+                near = abs(float(cum[b, h, k - 1]) - p32) < 1e-4
+                near |= k >= 2 and abs(float(cum[b, h, k - 2]) - p32) < 1e-4
+                loose[b, h] = bool(near)
+    for b in range(B):
+        for h in range(H):
+            n = int(wn[b, h])
+            if n < W:
+                gap = float(srt[b, h, n - 1] - srt[b, h, n])
+                if abs(gap) <= GAP_MARGIN * max(abs(float(srt[b, h, n - 1])), 1.0):
+                    loose[b, h] = True
+            if loose[b, h]:
+                continue
+            assert int(nph[b, h]) == n, (b, h)
+            assert pi[b, h, :n].tolist() == wi[b, h, :n].tolist(), (b, h)
+    return loose, (t["coverage"] - tau).abs() <= COV_MARGIN
+
+
 def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, max_margin_frac=0.0):
     """Run both backends for ``steps`` calls and compare them.
 
@@ -122,7 +158,19 @@ def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, max_margin_frac=
         tr = ora_b.trace[n_tr:]
         err = (out.float() - want.float()).abs().max().item()
         scoring = [t for t in tr if t["kind"].startswith("score")]
-        if scoring:
+        budgeted = kw.get("top_p") is not None or kw.get("static_budget_table") is not None
+        if scoring and budgeted:
+            t = scoring[-1]
+            pi, nph = gpu_b._cached_selection[0]
+            bad_sel, bad_acc = _check_budgeted_selection(
+                pi.cpu(), nph.cpu(), t, kw, kw.get("coverage_threshold", 0.9))
+            margin_sel += int(bad_sel.sum())
+            margin_acc += int(bad_acc.sum())
+            checks += bad_sel.numel()
+            acc = gpu_b._last_accept_mask[0].cpu()
+            ok = ~(bad_acc | bad_sel)
+            assert torch.equal(acc[ok], t["accept"][ok]), step
+        elif scoring:
             t = scoring[-1]
             budget = t["page_indices"].shape[-1]
             ranked = t.get("sel_scores", t["page_scores"])   # what the selection ranks
@@ -147,7 +195,7 @@ def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, max_margin_frac=
         rt.append(kn, vn, dev)
     assert margin_acc <= max_margin_frac * checks, (margin_sel, margin_acc, checks)
     sg, so = gpu_b.get_stats(), ora_b.get_stats()
-    if margin_acc == 0:
+    if margin_acc == 0 and not (budgeted and margin_sel):
         assert sg == so, (sg, so)
     return sg, ora_b.trace
 
