@@ -245,8 +245,9 @@ __device__ __forceinline__ void radix_select(const float (&val)[R], Alive alive,
 // Row budgets (MODE): kUniform, the same `budget` for every row;
 // kTopP, the smallest prefix of the row's pages by score whose softmax mass
 // reaches top_p (CVSABackend._topp_select, backend.py:652-681), at least 3;
-// kTable, head_budgets[h] (_static_select, :622-650).  `width` is the row
-// stride of page_indices: k is clamped to it.
+// kTable, row_budgets[b * H_kv + h] (_static_select, :622-650, and the
+// budgets of _adaptive_select, :522-570).  `width` is the row stride of
+// page_indices: k is clamped to it.
 enum { kUniform = 0, kTopP = 1, kTable = 2 };
 static_assert(kHistCopies * kHistStride >= kBuckets, "hist_c holds a second-level histogram");
 
@@ -257,7 +258,7 @@ template <int R, bool SEP, int MODE>
 __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     const float *__restrict__ scores, const float *__restrict__ sel_scores, int W, int H_kv,
     const int32_t *__restrict__ context_lens, int block_size, int budget, int width,
-    float top_p, const int32_t *__restrict__ head_budgets,
+    float top_p, const int32_t *__restrict__ row_budgets,
     int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
     uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
     const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
@@ -580,7 +581,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   // The row's budget k.
   int k = budget;
   bool hist_ready = false;  // hist_b already holds the bucket counts
-  if constexpr (MODE == kTable) k = min(max(head_budgets[bh % H_kv], 1), W);
+  if constexpr (MODE == kTable) k = min(max(row_budgets[bh], 1), W);
   if constexpr (MODE == kTopP) k = topp_budget(hist_ready);
   k = min(k, width);  // a row holds at most `width` pages: the best ones
   // plan 0: T and krem found; 1: radix select over the row; 2: radix
@@ -759,6 +760,110 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   }
 }
 
+// Budgets of CVSABackend._adaptive_select (cvsa/backend.py:522-570): the
+// kv-heads of sequence b compete for K = H_kv * base slots.  raw[h] counts
+// head h's scores among the K largest of all H_kv * W scores of b (ties at
+// the K-th value go to the lower heads; the reference's torch.topk leaves
+// them unspecified), then budget = round(fp32(raw) * keep + floor_cap)
+// (round half to even, keep = 1 - floor_ratio and floor_cap = base *
+// floor_ratio as fp32, :550-552), clamped to [1, n_valid] (:554-557).
+// One workgroup per sequence: an 8-bit MSB radix select of the K-th largest
+// key over the row's scores (four passes over them), then per-head counts.
+constexpr int kMaxAdaptiveHeads = 64;
+
+__global__ __launch_bounds__(kSelThreads) void adaptive_budget_kernel(
+    const float *__restrict__ scores, int H_kv, int W,
+    const int32_t *__restrict__ context_lens, int block_size, int base, float keep,
+    float floor_cap, int32_t *__restrict__ budgets) {
+  __shared__ uint32_t hist_c[kHistCopies * kHistStride];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t s_digit, s_krem;
+  __shared__ uint32_t s_gt[kMaxAdaptiveHeads], s_eq[kMaxAdaptiveHeads];
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63;
+  const float *row = scores + (int64_t)b * H_kv * W;
+  const int N = H_kv * W;
+  uint32_t prefix = 0, pmask = 0, krem = (uint32_t)min(H_kv * base, N);
+#pragma unroll 1
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int i = t; i < kHistCopies * kHistStride; i += kSelThreads) hist_c[i] = 0;
+    lds_barrier();
+    uint32_t *my_hist = hist_c + (lane % kHistCopies) * kHistStride;
+    for (int i = t; i < N; i += kSelThreads) {
+      const uint32_t key = order_key(row[i]);
+      if ((key & pmask) == prefix) atomicAdd(&my_hist[(key >> shift) & 255u], 1u);
+    }
+    lds_barrier();
+    if (t < 256) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int j = 0; j < kHistCopies; ++j) c += hist_c[j * kHistStride + t];
+      hist[t] = c;
+    }
+    lds_barrier();
+    if (t < 64) {
+      // Lane l holds digits 4l..4l+3; count the keys above each digit.
+      const uint32_t c0 = hist[4 * lane], c1 = hist[4 * lane + 1];
+      const uint32_t c2 = hist[4 * lane + 2], c3 = hist[4 * lane + 3];
+      const uint32_t local = c0 + c1 + c2 + c3;
+      uint32_t suffix = local;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_down(suffix, off, 64);
+        if (lane + off < 64) suffix += o;
+      }
+      uint32_t above = suffix - local;
+      const uint32_t cs[4] = {c3, c2, c1, c0};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (above < krem && above + cs[j] >= krem) {
+          s_digit = (uint32_t)(4 * lane + 3 - j);
+          s_krem = krem - above;
+        }
+        above += cs[j];
+      }
+    }
+    lds_barrier();
+    prefix |= s_digit << shift;
+    pmask |= 0xFFu << shift;
+    krem = s_krem;
+    lds_barrier();
+  }
+  const uint32_t T = prefix;
+  if (t < H_kv) {
+    s_gt[t] = 0;
+    s_eq[t] = 0;
+  }
+  lds_barrier();
+  for (int h = 0; h < H_kv; ++h) {
+    uint32_t gt = 0, eq = 0;
+    for (int p = t; p < W; p += kSelThreads) {
+      const uint32_t key = order_key(row[(int64_t)h * W + p]);
+      gt += key > T;
+      eq += key == T;
+    }
+    gt = wave_sum_u32(gt);
+    eq = wave_sum_u32(eq);
+    if (lane == 0 && (gt | eq) != 0) {
+      atomicAdd(&s_gt[h], gt);
+      atomicAdd(&s_eq[h], eq);
+    }
+  }
+  lds_barrier();
+  if (t == 0) {
+    const int nv = n_valid_pages(context_lens[b], block_size);
+    uint32_t ties = krem;  // keys equal to T among the K largest
+    for (int h = 0; h < H_kv; ++h) {
+      const uint32_t take = min(ties, s_eq[h]);
+      ties -= take;
+      const float raw = (float)(s_gt[h] + take);
+      const float mixed = __fadd_rn(__fmul_rn(raw, keep), floor_cap);
+      const int fb = (int)rintf(mixed);
+      budgets[b * H_kv + h] = min(max(fb, 1), nv);
+    }
+  }
+}
+
 // Coverage gate of a given selection, one workgroup per (b, kv-head).  All
 // global loads are issued at once (the row strided by the block so each
 // load instruction is coalesced, the selection list, n_per_head); for rows
@@ -844,7 +949,7 @@ static int launch_select(const char *name, const float *page_scores, const float
                          uint8_t *accept_out, float *coverage_out, const uint8_t *check_accept,
                          float *scores_cache, int64_t *stats, int count_gate,
                          void *stream, int mode = kUniform, float top_p = 0.f,
-                         const int32_t *head_budgets = nullptr) {
+                         const int32_t *row_budgets = nullptr) {
   CVSA_REQUIRE(page_scores && context_lens && page_indices && n_per_head, CVSA_ERR_INVALID,
                "%s: null pointer argument", name);
   CVSA_REQUIRE((accept_out == nullptr) == (coverage_out == nullptr), CVSA_ERR_INVALID,
@@ -869,7 +974,7 @@ static int launch_select(const char *name, const float *page_scores, const float
 #define CVSA_SEL_LAUNCH(RR, SEP, MODE)                                                      \
   hipLaunchKernelGGL((select_topk_kernel<RR, SEP, MODE>), grid, dim3(kSelThreads), 0, st,   \
                      page_scores, sel_scores, W, H_kv, context_lens, block_size, budget,    \
-                     width, top_p, head_budgets, page_indices, n_per_head, tau, accept_out, \
+                     width, top_p, row_budgets, page_indices, n_per_head, tau, accept_out,  \
                      coverage_out, check_accept, B * H_kv, scores_cache, st64, count_gate)
 #define CVSA_SEL_MODES(RR, SEP)                                    \
   if (mode == kTopP) CVSA_SEL_LAUNCH(RR, SEP, kTopP);              \
@@ -930,17 +1035,40 @@ extern "C" int cvsa_select_or_keep(const float *page_scores, const float *sel_sc
 extern "C" int cvsa_select_budgeted(const float *page_scores, const float *sel_scores,
                                     int32_t B, int32_t H_kv, int32_t W,
                                     const int32_t *context_lens, int32_t block_size,
-                                    float top_p, const int32_t *head_budgets, int32_t width,
+                                    float top_p, const int32_t *row_budgets, int32_t width,
                                     int32_t *page_indices, int32_t *n_per_head, float tau,
                                     uint8_t *accept_out, float *coverage_out, void *stream) {
-  CVSA_REQUIRE((top_p > 0.f) != (head_budgets != nullptr), CVSA_ERR_INVALID,
-               "select_budgeted: give exactly one of top_p and head_budgets");
-  CVSA_REQUIRE(head_budgets != nullptr || top_p < 1.f, CVSA_ERR_INVALID,
+  CVSA_REQUIRE((top_p > 0.f) != (row_budgets != nullptr), CVSA_ERR_INVALID,
+               "select_budgeted: give exactly one of top_p and row_budgets");
+  CVSA_REQUIRE(row_budgets != nullptr || top_p < 1.f, CVSA_ERR_INVALID,
                "select_budgeted: top_p=%g must be in (0, 1)", (double)top_p);
   return launch_select("select_budgeted", page_scores, sel_scores, B, H_kv, W, context_lens,
                        block_size, width, page_indices, n_per_head, tau, accept_out,
                        coverage_out, nullptr, nullptr, nullptr, 0, stream,
-                       top_p > 0.f ? kTopP : kTable, top_p, head_budgets);
+                       top_p > 0.f ? kTopP : kTable, top_p, row_budgets);
+}
+
+extern "C" int cvsa_adaptive_budgets(const float *page_scores, int32_t B, int32_t H_kv,
+                                     int32_t W, const int32_t *context_lens,
+                                     int32_t block_size, int32_t base_budget,
+                                     double floor_ratio, int32_t *budgets, void *stream) {
+  CVSA_REQUIRE(page_scores && context_lens && budgets, CVSA_ERR_INVALID,
+               "adaptive_budgets: null pointer argument");
+  CVSA_REQUIRE(B > 0 && H_kv > 0 && W > 0 && block_size > 0 && base_budget > 0,
+               CVSA_ERR_INVALID, "adaptive_budgets: bad sizes B=%d H_kv=%d W=%d base=%d", B,
+               H_kv, W, base_budget);
+  CVSA_REQUIRE(H_kv <= kMaxAdaptiveHeads && (int64_t)H_kv * W <= (int64_t)1 << 24,
+               CVSA_ERR_UNSUPPORTED,
+               "adaptive_budgets: H_kv=%d (max %d) or H_kv*W=%lld (max 2^24) too large", H_kv,
+               kMaxAdaptiveHeads, (long long)H_kv * W);
+  // The reference forms these in Python (double) and torch applies them to
+  // an fp32 tensor.
+  const float keep = (float)(1.0 - floor_ratio);
+  const float floor_cap = (float)((double)base_budget * floor_ratio);
+  hipLaunchKernelGGL(adaptive_budget_kernel, dim3(B), dim3(kSelThreads), 0,
+                     (hipStream_t)stream, page_scores, H_kv, W, context_lens, block_size,
+                     base_budget, keep, floor_cap, budgets);
+  return cvsa_host::check_launch("adaptive_budgets");
 }
 
 extern "C" int cvsa_check_coverage(const float *page_scores, int32_t B,

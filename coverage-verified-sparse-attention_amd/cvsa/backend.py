@@ -37,12 +37,12 @@ for the ranking scores with its flags: they are computed only when some
 head failed.
 
 Per-head budgets: ``top_p`` (the smallest page set per head whose softmax
-mass over the ranking scores reaches top_p, backend.py:652-681) and
-``static_budget_table`` (offline per-head fractions, :622-650) select through
-ops.select_budgeted with the new selection's gate fused; like the reference
-they read the largest budget on the host (top-p) and take the per-kernel
-path.  Not implemented here (the constructor raises NotImplementedError):
-adaptive_selection.
+mass over the ranking scores reaches top_p, backend.py:652-681),
+``static_budget_table`` (offline per-head fractions, :622-650) and
+``adaptive_selection`` (heads compete for H_kv * budget slots, :522-570)
+select through ops.select_budgeted with the new selection's gate fused;
+like the reference they read the largest budget on the host (top-p,
+adaptive) and take the per-kernel path.
 """
 from __future__ import annotations
 
@@ -165,12 +165,8 @@ class CVSABackend:
         if top_p is not None and not (0.0 < top_p < 1.0):
             raise ValueError(f"top_p must be in (0, 1), got {top_p}")
         self.top_p = top_p
-        if adaptive_selection:
-            raise NotImplementedError(
-                "CVSABackend on MI355X implements the uniform, top-p and static-table "
-                "budgets; not available: adaptive_selection")
-        # Per-head budgets of the static table on the device, per (layer, W).
-        self._head_budgets: Dict[Tuple[int, int, torch.device], Tuple[torch.Tensor, int]] = {}
+        # Row budgets of the static table on the device, per (layer, B, W).
+        self._table_budgets: Dict[tuple, Tuple[torch.Tensor, int]] = {}
         # Quest metadata per key cache (keyed by id, with a weak reference to
         # tell a reused id from the cache it was built for).
         self._quest_meta: Dict[int, Tuple[weakref.ref, ops.QuestPageMeta]] = {}
@@ -539,7 +535,7 @@ class CVSABackend:
         per-kernel path (timing, host-side decisions, unsupported buffers)."""
         if (self._track_timing or self.random_reject_prob is not None
                 or self.approx_recovery_pct is not None or self.top_p is not None
-                or self.static_budget_table is not None):
+                or self.static_budget_table is not None or self.adaptive_selection):
             return None
         dev = q.device
         work = self._work(dev)
@@ -613,7 +609,8 @@ class CVSABackend:
         recovery, no counterfactual rejections, the cached selection and
         scores match this call's shape, counters live on this device."""
         if (self.random_reject_prob is not None or self.approx_recovery_pct is not None
-                or self.top_p is not None or self.static_budget_table is not None):
+                or self.top_p is not None or self.static_budget_table is not None
+                or self.adaptive_selection):
             return False
         page_indices, n_per_head = self._cached_selection[layer_idx]
         B, H_kv, W = page_scores.shape
@@ -702,7 +699,8 @@ class CVSABackend:
         # In the fixed-interval schedule the gate's counters (:859-863) are
         # booked on the device, so the step needs no host read.
         dev = page_scores.device
-        budgeted = self.top_p is not None or self.static_budget_table is not None
+        budgeted = (self.top_p is not None or self.static_budget_table is not None
+                    or self.adaptive_selection)
         device_book = (not budgeted and not self.lazy and self.random_reject_prob is None
                        and self.approx_recovery_pct is None
                        and self._ensure_dev_stats(dev) is not None)
@@ -711,7 +709,7 @@ class CVSABackend:
             # largest one, as in the reference.
             page_indices, n_per_head, accept_mask, budget = self._time_kernel(
                 "coverage", self._budgeted_select, page_scores, sel_scores, layer_idx,
-                context_lens)
+                context_lens, budget)
         elif device_book:
             H = self.num_kv_heads
             page_indices = torch.empty(B, H, budget, dtype=torch.int32, device=dev)
@@ -778,27 +776,39 @@ class CVSABackend:
             self._h_total_scoring_steps += 1                                      # :859
         return output
 
-    def _budgeted_select(self, page_scores, sel_scores, layer_idx, context_lens):
-        """_topp_select / _static_select (backend.py:622-681) with the coverage
-        gate of the new selection: (page_indices [B, H_kv, max_budget],
-        n_per_head, accept_mask, max_budget)."""
+    def _budgeted_select(self, page_scores, sel_scores, layer_idx, context_lens, base_budget):
+        """_topp_select / _static_select / _adaptive_select (backend.py:
+        522-681, in the reference's order of precedence, :727-736) with the
+        coverage gate of the new selection: (page_indices [B, H_kv,
+        max_budget], n_per_head, accept_mask, max_budget)."""
         W = page_scores.shape[2]
+        if self.top_p is None and self.static_budget_table is None:
+            ranked = page_scores if sel_scores is None else sel_scores
+            budgets = ops.adaptive_budgets(ranked, base_budget, context_lens, self.block_size,
+                                           self.adaptive_floor_ratio)
+            max_budget = int(budgets.max().item())   # :559, a host read as in the reference
+            idx, nph, acc, _cov = ops.select_budgeted(
+                page_scores, context_lens, self.block_size, row_budgets=budgets,
+                width=max_budget, tau=self.tau, sel_scores=sel_scores)
+            return idx, nph, acc, max_budget
         if self.top_p is not None:
             idx, nph, acc, _cov = ops.select_budgeted(
                 page_scores, context_lens, self.block_size, top_p=self.top_p, tau=self.tau,
                 sel_scores=sel_scores)
             max_budget = int(nph.max().item())   # :679, a host read as in the reference
             return idx[:, :, :max_budget].contiguous(), nph, acc, max_budget
-        key = (layer_idx, W, page_scores.device)
-        entry = self._head_budgets.get(key)
+        B = page_scores.shape[0]
+        key = (layer_idx, B, W, page_scores.device)
+        entry = self._table_budgets.get(key)
         if entry is None:
             fracs = self.static_budget_table[layer_idx]
             per_head = torch.clamp((fracs * W).round().long(), min=3, max=W)      # :638
-            entry = (per_head.to(torch.int32).to(page_scores.device), int(per_head.max()))
-            self._head_budgets[key] = entry
+            rows = per_head.to(torch.int32).view(1, -1).expand(B, -1).contiguous()
+            entry = (rows.to(page_scores.device), int(per_head.max()))
+            self._table_budgets[key] = entry
         budgets, max_budget = entry
         idx, nph, acc, _cov = ops.select_budgeted(
-            page_scores, context_lens, self.block_size, head_budgets=budgets, width=max_budget,
+            page_scores, context_lens, self.block_size, row_budgets=budgets, width=max_budget,
             tau=self.tau, sel_scores=sel_scores)
         return idx, nph, acc, max_budget
 

@@ -25,6 +25,7 @@ __all__ = [
     "score_pages",
     "select_topk",
     "select_budgeted",
+    "adaptive_budgets",
     "check_coverage",
     "sparse_decode_unnorm",
     "sparse_decode",
@@ -199,15 +200,16 @@ def select_topk(page_scores: torch.Tensor, budget: int, context_lens: torch.Tens
 
 
 def select_budgeted(page_scores: torch.Tensor, context_lens: torch.Tensor, block_size: int, *,
-                    top_p: Optional[float] = None, head_budgets: Optional[torch.Tensor] = None,
+                    top_p: Optional[float] = None, row_budgets: Optional[torch.Tensor] = None,
                     width: Optional[int] = None, tau: Optional[float] = None,
                     sel_scores: Optional[torch.Tensor] = None):
     """Selection with a budget per (b, kv-head) row (cvsa_select_budgeted).
 
     ``top_p``: each row takes the smallest prefix of its pages by score whose
     softmax mass reaches top_p, at least 3 (CVSABackend._topp_select,
-    cvsa/backend.py:652-681).  ``head_budgets`` ([H_kv] int32 on the device):
-    row (b, h) takes head_budgets[h] pages (_static_select, :622-650).  The
+    cvsa/backend.py:652-681).  ``row_budgets`` ([B, H_kv] int32 on the
+    device): row (b, h) takes row_budgets[b, h] pages (_static_select,
+    :622-650, or the budgets of adaptive_budgets).  The
     pages are ranked by ``sel_scores`` when given, else by ``page_scores``.
     Returns ``page_indices`` [B, H_kv, width] (default width W; each row's
     first n_per_head entries are its selected valid pages, in ascending page
@@ -215,19 +217,19 @@ def select_budgeted(page_scores: torch.Tensor, context_lens: torch.Tensor, block
     ``n_per_head``; with ``tau`` also the accept mask and coverage of the
     selection's gate on ``page_scores``.
     """
-    dev = _device_of(page_scores, context_lens, head_budgets, sel_scores)
+    dev = _device_of(page_scores, context_lens, row_budgets, sel_scores)
     if page_scores.dtype != torch.float32 or page_scores.dim() != 3:
         raise ValueError("page_scores must be [B, H_kv, W] float32")
     ps = page_scores.contiguous()
     B, H_kv, W = ps.shape
-    if (top_p is None) == (head_budgets is None):
-        raise ValueError("select_budgeted: give exactly one of top_p and head_budgets")
+    if (top_p is None) == (row_budgets is None):
+        raise ValueError("select_budgeted: give exactly one of top_p and row_budgets")
     if top_p is not None and not 0.0 < top_p < 1.0:
         raise ValueError(f"select_budgeted: top_p must be in (0, 1), got {top_p}")
-    if head_budgets is not None and (head_budgets.dtype != torch.int32
-                                     or head_budgets.shape != (H_kv,)
-                                     or not head_budgets.is_contiguous()):
-        raise ValueError(f"select_budgeted: head_budgets must be a contiguous int32 [{H_kv}]")
+    if row_budgets is not None and (row_budgets.dtype != torch.int32
+                                    or row_budgets.shape != (B, H_kv)
+                                    or not row_budgets.is_contiguous()):
+        raise ValueError(f"select_budgeted: row_budgets must be a contiguous int32 [{B}, {H_kv}]")
     if sel_scores is not None:
         if sel_scores.shape != ps.shape or sel_scores.dtype != torch.float32:
             raise ValueError("select_budgeted: sel_scores must match page_scores")
@@ -244,12 +246,34 @@ def select_budgeted(page_scores: torch.Tensor, context_lens: torch.Tensor, block
         cov = torch.empty(B, H_kv, device=dev, dtype=torch.float32)
     check(_lib.load().cvsa_select_budgeted(
         ps.data_ptr(), _ptr(sel_scores), B, H_kv, W, ctx.data_ptr(), block_size,
-        float(top_p) if top_p is not None else 0.0, _ptr(head_budgets), width, idx.data_ptr(),
+        float(top_p) if top_p is not None else 0.0, _ptr(row_budgets), width, idx.data_ptr(),
         nph.data_ptr(), float(tau) if tau is not None else 0.0, _ptr(acc), _ptr(cov),
         _stream(dev)), "select_budgeted")
     if tau is None:
         return idx, nph
     return idx, nph, acc.view(torch.bool), cov
+
+
+def adaptive_budgets(sel_scores: torch.Tensor, base_budget: int, context_lens: torch.Tensor,
+                     block_size: int, floor_ratio: float) -> torch.Tensor:
+    """Per-head budgets [B, H_kv] int32 of CVSABackend._adaptive_select
+    (cvsa/backend.py:522-570), computed on the device
+    (cvsa_adaptive_budgets): the heads of a sequence compete for
+    H_kv * base_budget of their largest scores, blended toward base_budget by
+    floor_ratio and clamped to [1, n_valid]."""
+    dev = _device_of(sel_scores, context_lens)
+    if sel_scores.dtype != torch.float32 or sel_scores.dim() != 3:
+        raise ValueError("sel_scores must be [B, H_kv, W] float32")
+    ss = sel_scores.contiguous()
+    B, H_kv, W = ss.shape
+    if base_budget < 1:
+        raise ValueError("adaptive_budgets: base_budget must be >= 1")
+    ctx = _i32(context_lens)
+    out = torch.empty(B, H_kv, device=dev, dtype=torch.int32)
+    check(_lib.load().cvsa_adaptive_budgets(
+        ss.data_ptr(), B, H_kv, W, ctx.data_ptr(), block_size, int(base_budget),
+        float(floor_ratio), out.data_ptr(), _stream(dev)), "adaptive_budgets")
+    return out
 
 
 def select_or_keep(page_scores: torch.Tensor, check_accept: Optional[torch.Tensor],

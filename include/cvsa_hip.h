@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 6
+#define CVSA_ABI_VERSION 7
 
 enum {
   CVSA_OK = 0,
@@ -118,17 +118,19 @@ int cvsa_select_or_keep(const float *page_scores, const float *sel_scores,
 
 /*
  * Selection with a budget per (b, kv-head) row.  Replaces the top-p branch
- * of CVSABackend._scoring_step (_topp_select, cvsa/backend.py:652-681) and
- * the static-table branch (_static_select, :622-650).
- *   top_p in (0, 1), head_budgets NULL: with p = softmax(sel row),
+ * of CVSABackend._scoring_step (_topp_select, cvsa/backend.py:652-681), the
+ * static-table branch (_static_select, :622-650) and the selection of the
+ * adaptive branch (_adaptive_select, :522-570, budgets from
+ * cvsa_adaptive_budgets).
+ *   top_p in (0, 1), row_budgets NULL: with p = softmax(sel row),
  *     need = 1 + #{k : sum of the k largest p < top_p}, k_row =
  *     clamp(need, 3, W).  The masses exp(s - max) are summed exactly as
  *     40-bit fixed point, in descending score order; the reference's fp32
  *     cumsum can put need one page off where the cumulative mass lies
  *     within rounding of top_p.  A row with +inf / NaN or no finite score
  *     (NaN softmax in the reference) gets need = 1.
- *   head_budgets [H_kv] int32 (top_p = 0): k_row = head_budgets[h]
- *     (clamped to [1, W]; the reference's clamp(round(frac*P), 3, P) is
+ *   row_budgets [B*H_kv] int32 (top_p = 0): k_row = row_budgets[b*H_kv+h]
+ *     (clamped to [1, W]; the static table's clamp(round(frac*P), 3, P) is
  *     applied by the caller).
  *   k_row is then clamped to `width`, the row stride of page_indices: the
  *     row's first k_row entries receive the pages of its k_row largest
@@ -142,9 +144,25 @@ int cvsa_select_or_keep(const float *page_scores, const float *sel_scores,
 int cvsa_select_budgeted(const float *page_scores, const float *sel_scores,
                          int32_t B, int32_t H_kv, int32_t W,
                          const int32_t *context_lens, int32_t block_size,
-                         float top_p, const int32_t *head_budgets, int32_t width,
+                         float top_p, const int32_t *row_budgets, int32_t width,
                          int32_t *page_indices, int32_t *n_per_head, float tau,
                          uint8_t *accept_out, float *coverage_out, void *stream);
+
+/*
+ * Per-head budgets of CVSABackend._adaptive_select (cvsa/backend.py:
+ * 522-570): the kv-heads of each sequence compete for H_kv * base_budget
+ * slots among all their page scores; raw[b,h] = head h's share of the
+ * H_kv * base_budget largest scores of sequence b (ties at the last value
+ * to the lower heads; the reference's torch.topk leaves them unspecified);
+ * budgets[b*H_kv+h] = clamp(round(fp32(raw) * fp32(1 - floor_ratio) +
+ * fp32(base_budget * floor_ratio)), 1, n_valid(b)), round half to even.
+ * The selection itself is cvsa_select_budgeted with these row budgets.
+ * H_kv <= 64.
+ */
+int cvsa_adaptive_budgets(const float *page_scores, int32_t B, int32_t H_kv, int32_t W,
+                          const int32_t *context_lens, int32_t block_size,
+                          int32_t base_budget, double floor_ratio, int32_t *budgets,
+                          void *stream);
 
 /*
  * Coverage gate.  Replaces triton_check_coverage

@@ -4,8 +4,9 @@ Follows cvsa/backend.py of DJ-Melvin/coverage-verified-sparse-attention
 (line numbers below) for the configurations this build covers: the exact
 page scorer or the Quest min/max scorer (selector="quest", for selection
 only or, with light_normalizer, for the coverage gate too) with a uniform
-budget, top-p budgets (``top_p``) or a static per-head budget table
-(``static_budget_table``), exact recovery (complement + LSE merge)
+budget, top-p budgets (``top_p``), a static per-head budget table
+(``static_budget_table``) or adaptive budgets (``adaptive_selection``),
+exact recovery (complement + LSE merge)
 or approximate recovery (``approx_recovery_pct``), dense layers, the fixed
 interval (``reuse_interval``) and lazy (``check_interval`` /
 ``coverage_interval``) schedules, and the statistics of get_stats().
@@ -28,7 +29,8 @@ class OracleCVSABackend:
                  dense_layers: Optional[List[int]] = None, lazy=False,
                  check_interval=None, coverage_interval=None, approx_recovery_pct=None,
                  selector="exact", light_normalizer=False, top_p=None,
-                 static_budget_table=None, acc_dtype=torch.float64):
+                 static_budget_table=None, adaptive_selection=False, adaptive_floor_ratio=0.5,
+                 acc_dtype=torch.float64):
         # :80-115
         self.num_kv_heads = num_kv_heads
         self.num_q_heads = num_q_heads
@@ -50,6 +52,8 @@ class OracleCVSABackend:
         self.static_budget_table = None if static_budget_table is None else {
             int(layer): torch.as_tensor(f, dtype=torch.float32)
             for layer, f in static_budget_table.items()}
+        self.adaptive_selection = adaptive_selection
+        self.adaptive_floor_ratio = adaptive_floor_ratio
         self.acc_dtype = acc_dtype
         self.reset()
 
@@ -216,6 +220,10 @@ class OracleCVSABackend:
         elif self.static_budget_table is not None:                               # :730-732
             idx, nph = ref.static_select(sel_scores, self.static_budget_table[layer_idx],
                                          context_lens, self.block_size)
+            budget = idx.shape[-1]
+        elif self.adaptive_selection:                                            # :733-735
+            idx, nph = ref.adaptive_select(sel_scores, budget, context_lens, self.block_size,
+                                           self.adaptive_floor_ratio)
             budget = idx.shape[-1]
         else:
             idx, nph = ref.select_topk(sel_scores, budget, context_lens, self.block_size)

@@ -207,6 +207,41 @@ def static_budgets(fractions, P: int) -> torch.Tensor:
     return torch.clamp(torch.round(f * P).long(), min=3, max=P)
 
 
+def adaptive_budgets(sel_scores, base_budget, context_lens, block_size, floor_ratio):
+    """The budgets of CVSABackend._adaptive_select (cvsa/backend.py:522-559):
+    raw[b,h] = head h's share of the H * base_budget largest scores of
+    sequence b, ties at the last value to the lower heads (torch.topk leaves
+    them unspecified); budget = round(fp32(raw) * fp32(1 - floor_ratio) +
+    fp32(base * floor_ratio)) with round half to even, clamped to
+    [1, n_valid]."""
+    B, H, P = sel_scores.shape
+    K = min(H * base_budget, H * P)
+    keep = torch.tensor(1.0 - floor_ratio, dtype=torch.float32)
+    cap = torch.tensor(base_budget * floor_ratio, dtype=torch.float32)
+    nv = n_valid_pages(context_lens, block_size)
+    out = torch.empty(B, H, dtype=torch.int32)
+    for b in range(B):
+        vals = sel_scores[b].to(torch.float64).reshape(-1)          # head-major
+        heads = torch.arange(H).repeat_interleave(P)
+        # order by (value desc, head asc): a stable sort of the head-major row
+        order = torch.sort(vals, descending=True, stable=True).indices[:K]
+        raw = torch.bincount(heads[order], minlength=H).to(torch.float32)
+        mixed = raw * keep + cap          # two fp32 roundings, as torch
+        fb = torch.round(mixed).to(torch.int32)
+        out[b] = torch.clamp(fb, min=1).clamp(max=int(nv[b]))
+    return out
+
+
+def adaptive_select(sel_scores, base_budget, context_lens, block_size, floor_ratio):
+    """CVSABackend._adaptive_select (cvsa/backend.py:522-570): the pages of
+    each row's top budget[b,h] scores in ascending page order (ties to the
+    lower page), rows of max budget entries; n_per_head = budget."""
+    budgets = adaptive_budgets(sel_scores, base_budget, context_lens, block_size, floor_ratio)
+    order = torch.sort(sel_scores.to(torch.float64), dim=-1, descending=True,
+                       stable=True).indices
+    return _prefix_sets(order, budgets, budgets)
+
+
 def _prefix_sets(order, k_row, nph):
     """Rows of the k_row first pages of `order`, sorted ascending, truncated
     to max(nph) entries (the valid ones come first: invalid pages score -inf

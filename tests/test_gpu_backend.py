@@ -85,7 +85,8 @@ def _check_near_tie_selection(pi, nph, ps, budget, bad_sel):
 
 
 def _check_budgeted_selection(pi, nph, t, kw, tau):
-    """Per-head budgets (top_p / static_budget_table): each row's first
+    """Per-head budgets (top_p / static_budget_table / adaptive_selection):
+    each row's first
     n_per_head pages equal the oracle's, except rows whose budget or k-th
     page is numerically undecidable (top-p boundary within 1e-4 of top_p:
     the GPU ranks its fp32 page scores, the oracle fp64 ones; or the score
@@ -158,7 +159,8 @@ def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, max_margin_frac=
         tr = ora_b.trace[n_tr:]
         err = (out.float() - want.float()).abs().max().item()
         scoring = [t for t in tr if t["kind"].startswith("score")]
-        budgeted = kw.get("top_p") is not None or kw.get("static_budget_table") is not None
+        budgeted = (kw.get("top_p") is not None or kw.get("static_budget_table") is not None
+                    or kw.get("adaptive_selection", False))
         if scoring and budgeted:
             t = scoring[-1]
             pi, nph = gpu_b._cached_selection[0]

@@ -1,7 +1,8 @@
-"""Per-head budget selection (cvsa_select_budgeted) against the oracle's
-restatements of CVSABackend._topp_select and _static_select
-(cvsa/backend.py:622-681), and the backend's top-p / static-table schedules
-against the oracle backend.
+"""Per-head budget selection (cvsa_select_budgeted, cvsa_adaptive_budgets)
+against the oracle's restatements of CVSABackend._topp_select,
+_static_select and _adaptive_select (cvsa/backend.py:522-681), and the
+backend's top-p / static-table / adaptive schedules against the oracle
+backend.
 
 Top-p budgets depend on where the cumulative softmax mass crosses top_p.
 The kernel sums the masses as 40-bit fixed point (cumulative error below
@@ -142,8 +143,9 @@ def test_static_table_matches_oracle(gpu, W):
     per_head = ref.static_budgets(fr, W)
     width = int(per_head.max())
     idx, nph, acc, cov = ops.select_budgeted(
-        s.to(gpu), ctx.to(gpu), 16, head_budgets=per_head.to(torch.int32).to(gpu), width=width,
-        tau=0.9)
+        s.to(gpu), ctx.to(gpu), 16,
+        row_budgets=per_head.to(torch.int32).view(1, H).expand(B, H).contiguous().to(gpu),
+        width=width, tau=0.9)
     widx, wnph = ref.static_select(s, fr, ctx, 16)
     assert torch.equal(nph.cpu(), wnph)
     for b in range(B):
@@ -152,6 +154,32 @@ def test_static_table_matches_oracle(gpu, W):
             assert idx[b, h, :n].cpu().tolist() == widx[b, h, :n].tolist(), (b, h)
     wacc, wcov = ref.check_coverage(s, widx, wnph, 0.9)
     assert (cov.cpu() - wcov).abs().max().item() < 1e-5
+
+
+@pytest.mark.parametrize("H,W,base,floor", [(4, 64, 10, 0.0), (8, 3000, 300, 0.5),
+                                            (8, 2048, 200, 0.25), (2, 500, 499, 0.0)])
+def test_adaptive_budgets_match_oracle(gpu, H, W, base, floor):
+    """Budgets exact (ties at the threshold to the lower head on both sides;
+    rounded scores make many ties), then the selection by those budgets."""
+    B = 3
+    valid = [W, W // 2, 5]
+    g = torch.Generator().manual_seed(W + H)
+    s = (torch.randn(B, H, W, generator=g) * 3).round()
+    for b, v in enumerate(valid):
+        s[b, :, v:] = float("-inf")
+    ctx = _ctx_for(W, valid)
+    got = ops.adaptive_budgets(s.to(gpu), base, ctx.to(gpu), 16, floor)
+    want = ref.adaptive_budgets(s, base, ctx, 16, floor)
+    assert torch.equal(got.cpu(), want)
+    width = int(want.max())
+    idx, nph, acc, cov = ops.select_budgeted(s.to(gpu), ctx.to(gpu), 16, row_budgets=got,
+                                             width=width, tau=0.9)
+    widx, wnph = ref.adaptive_select(s, base, ctx, 16, floor)
+    assert torch.equal(nph.cpu(), wnph)
+    for b in range(B):
+        for h in range(H):
+            n = int(wnph[b, h])
+            assert idx[b, h, :n].cpu().tolist() == widx[b, h, :n].tolist(), (b, h)
 
 
 def test_select_budgeted_rejects_bad_arguments(gpu):
@@ -164,8 +192,8 @@ def test_select_budgeted_rejects_bad_arguments(gpu):
     with pytest.raises(ValueError):
         ops.select_budgeted(s, ctx, 16, top_p=0.5, width=11)
     with pytest.raises(ValueError):
-        ops.select_budgeted(s, ctx, 16, head_budgets=torch.ones(3, dtype=torch.int32,
-                                                                 device=gpu))
+        ops.select_budgeted(s, ctx, 16, row_budgets=torch.ones(1, 3, dtype=torch.int32,
+                                                                device=gpu))
 
 
 CFG = dict(batch=2, num_q_heads=32, num_kv_heads=8, head_dim=128, context_len=[5000, 2600],
@@ -184,6 +212,9 @@ CFG = dict(batch=2, num_q_heads=32, num_kv_heads=8, head_dim=128, context_len=[5
          coverage_threshold=0.9, lazy=True, check_interval=3),
     dict(static_budget_table={0: [0.2] * 4 + [0.1] * 4}, coverage_threshold=0.9, lazy=False,
          reuse_interval=2),
+    dict(adaptive_selection=True, coverage_threshold=0.9, lazy=True, check_interval=3),
+    dict(adaptive_selection=True, adaptive_floor_ratio=0.2, coverage_threshold=0.8,
+         lazy=False, reuse_interval=2, selector="quest"),
 ])
 def test_backend_budgeted_schedules(gpu, kw):
     kw = dict(budget_pct=0.2, **kw)

@@ -1,9 +1,11 @@
 """Pins of the oracle's per-head budget selections: ref.topp_need /
-ref.topp_select (restating CVSABackend._topp_select, cvsa/backend.py:652-681)
-and ref.static_select (_static_select, :622-650).  The reference's tests do
+ref.topp_select (restating CVSABackend._topp_select, cvsa/backend.py:652-681),
+ref.static_select (_static_select, :622-650) and ref.adaptive_budgets /
+ref.adaptive_select (_adaptive_select, :522-570).  The reference's tests do
 not cover these selectors, so they are pinned by closed forms (uniform and
-geometric page masses), the strict "< top_p" boundary, the clamps, the NaN
-rows, and a scalar brute force on small rows."""
+geometric page masses, a dominating head, floor ratios 0 and 1), the strict
+"< top_p" boundary, the clamps and rounding, the NaN rows, and scalar brute
+forces on small rows."""
 import math
 
 import torch
@@ -116,3 +118,65 @@ def test_static_select_budgets_and_sets():
             assert int(nph[b, h]) == n
             want = sorted(sorted(range(P), key=lambda i: (-float(s[b, h, i]), i))[:n])
             assert idx[b, h, :n].tolist() == want
+
+
+def _adaptive_brute(s, base, floor, nv):
+    """Scalar restatement: count heads among the H*base largest (value desc,
+    head asc), blend in fp32, round half to even, clamp."""
+    H, P = len(s), len(s[0])
+    cells = sorted(((-s[h][p], h) for h in range(H) for p in range(P)))
+    raw = [0] * H
+    for _, h in cells[:min(H * base, H * P)]:
+        raw[h] += 1
+    keep = torch.tensor(1.0 - floor, dtype=torch.float32)
+    cap = torch.tensor(base * floor, dtype=torch.float32)
+    out = []
+    for r in raw:
+        m = float(torch.tensor(float(r), dtype=torch.float32) * keep + cap)
+        out.append(min(max(int(round(m)), 1), nv))   # Python round is half to even
+    return out
+
+
+def test_adaptive_floor_ratio_limits():
+    g = torch.Generator().manual_seed(11)
+    s = torch.randn(2, 4, 50, generator=g)
+    ctx = torch.tensor([50 * 16, 20 * 16], dtype=torch.int32)
+    # floor 1: every head gets the base budget (clamped to n_valid)
+    assert ref.adaptive_budgets(s, 12, ctx, 16, 1.0).tolist() == [[12] * 4, [12] * 4]
+    assert ref.adaptive_budgets(s, 30, ctx, 16, 1.0).tolist() == [[30] * 4, [20] * 4]
+    # floor 0: the raw shares, which add up to H * base
+    b0 = ref.adaptive_budgets(s, 12, torch.tensor([800, 800], dtype=torch.int32), 16, 0.0)
+    assert b0.sum(dim=1).tolist() == [48, 48]
+
+
+def test_adaptive_dominating_head_and_rounding():
+    # head 0 above everything: it takes min(P, H * base) slots, the rest
+    # compete for what is left
+    s = torch.zeros(1, 3, 10)
+    s[0, 0] = 10.0 + torch.arange(10, dtype=torch.float32)
+    s[0, 1] = torch.arange(10, dtype=torch.float32) * 0.1
+    s[0, 2] = torch.arange(10, dtype=torch.float32) * 0.1 + 0.05
+    ctx = torch.tensor([160], dtype=torch.int32)
+    assert ref.adaptive_budgets(s, 4, ctx, 16, 0.0).tolist() == [[10, 1, 1]]
+    # raw (10, 1, 1) at floor 0.5, base 3: 10*0.5+1.5 = 6.5 -> 6; 1*0.5+1.5 = 2
+    assert ref.adaptive_budgets(s, 3, ctx, 16, 0.5).tolist() == [[6, 2, 2]]
+
+
+def test_adaptive_brute_force_and_ties():
+    g = torch.Generator().manual_seed(13)
+    for trial in range(12):
+        H = int(torch.randint(1, 6, (1,), generator=g))
+        P = int(torch.randint(3, 25, (1,), generator=g))
+        base = int(torch.randint(1, P + 1, (1,), generator=g))
+        floor = [0.0, 0.25, 0.5, 0.9][trial % 4]
+        s = torch.randn(1, H, P, generator=g).round()     # many exact ties
+        nv = int(torch.randint(1, P + 1, (1,), generator=g))
+        s[0, :, nv:] = float("-inf")
+        ctx = torch.tensor([nv * 16], dtype=torch.int32)
+        got = ref.adaptive_budgets(s, base, ctx, 16, floor)[0].tolist()
+        assert got == _adaptive_brute(s[0].tolist(), base, floor, nv), trial
+        idx, nph = ref.adaptive_select(s, base, ctx, 16, floor)
+        for h in range(H):
+            n = int(nph[0, h])
+            want = sorted(sorted(range(P), key=lambda p: (-float(s[0, h, p]), p))[:n])
+            assert idx[0, h, :n].tolist() == want
