@@ -99,6 +99,9 @@ def parse_args():
                     help="also run an elementwise copy of this many MiB (counter calibration)")
     ap.add_argument("--selector", choices=("exact", "quest"), default="exact",
                     help="page ranking: the exact max q.k scan, or Quest min/max page metadata")
+    ap.add_argument("--budget-samples", action="store_true",
+                    help="also time the per-head budget selections (top-p 0.9, adaptive "
+                         "budgets + selection, static table) on the workload's page scores")
     ap.add_argument("--light-normalizer", action="store_true",
                     help="with --selector quest: Quest scores also drive the coverage gate "
                          "(no full-key scan on any step)")
@@ -460,6 +463,22 @@ def main():
         k, v, bt, cl, q = lay(i)[:5]
         metas[i % L].scores(q, bt, cl, H_kv, G, BS)
 
+    def run_topp(i):
+        k, v, bt, cl, q, ps = lay(i)[:6]
+        ops.select_budgeted(ps, cl, BS, top_p=0.9, tau=tau0)
+
+    def run_adaptive(i):
+        k, v, bt, cl, q, ps = lay(i)[:6]
+        rb = ops.adaptive_budgets(ps, budget, cl, BS, 0.5)
+        ops.select_budgeted(ps, cl, BS, row_budgets=rb, width=W, tau=tau0)
+
+    table = torch.full((B, H_kv), budget, dtype=torch.int32, device=dev)
+    table[:, ::2] = budget // 2
+
+    def run_table(i):
+        k, v, bt, cl, q, ps = lay(i)[:6]
+        ops.select_budgeted(ps, cl, BS, row_budgets=table, width=budget, tau=tau0)
+
     n_smp = args.kernel_samples
     score_us = time_kernel(run_score, n_smp)
     sel_us = time_kernel(run_select, n_smp)
@@ -486,6 +505,14 @@ def main():
         "dense_decode": {"us": dense_us, "bytes": dense_bytes},
         "verified_decode(all rejected)": {"us": recover_us, "bytes": dense_bytes},
     }
+    if args.budget_samples:
+        sel_bytes = 2 * B * H_kv * W * 4
+        kernels["select_budgeted(top_p=0.9)"] = {"us": time_kernel(run_topp, n_smp),
+                                                 "bytes": sel_bytes}
+        kernels["adaptive_budgets+select"] = {"us": time_kernel(run_adaptive, n_smp),
+                                              "bytes": 5 * B * H_kv * W * 4}
+        kernels["select_budgeted(table)"] = {"us": time_kernel(run_table, n_smp),
+                                             "bytes": sel_bytes}
     for v in kernels.values():
         v["GBps"] = v["bytes"] / (v["us"] * 1e-6) / 1e9
     # dominant kernel over an M-step cycle: one scoring pass vs M decode passes

@@ -769,7 +769,10 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
 // floor_ratio as fp32, :550-552), clamped to [1, n_valid] (:554-557).
 // One workgroup per sequence: an 8-bit MSB radix select of the K-th largest
 // key over the row's scores (four passes over them), then per-head counts.
+// Each thread requests eight scores before it updates the histogram with
+// any of them.
 constexpr int kMaxAdaptiveHeads = 64;
+constexpr int kAdaptiveBatch = 8;
 
 __global__ __launch_bounds__(kSelThreads) void adaptive_budget_kernel(
     const float *__restrict__ scores, int H_kv, int W,
@@ -789,9 +792,16 @@ __global__ __launch_bounds__(kSelThreads) void adaptive_budget_kernel(
     for (int i = t; i < kHistCopies * kHistStride; i += kSelThreads) hist_c[i] = 0;
     lds_barrier();
     uint32_t *my_hist = hist_c + (lane % kHistCopies) * kHistStride;
-    for (int i = t; i < N; i += kSelThreads) {
-      const uint32_t key = order_key(row[i]);
-      if ((key & pmask) == prefix) atomicAdd(&my_hist[(key >> shift) & 255u], 1u);
+    for (int i0 = t; i0 < N; i0 += kAdaptiveBatch * kSelThreads) {
+      float v[kAdaptiveBatch];
+#pragma unroll
+      for (int j = 0; j < kAdaptiveBatch; ++j) v[j] = row[min(i0 + j * kSelThreads, N - 1)];
+#pragma unroll
+      for (int j = 0; j < kAdaptiveBatch; ++j) {
+        const uint32_t key = order_key(v[j]);
+        if (i0 + j * kSelThreads < N && (key & pmask) == prefix)
+          atomicAdd(&my_hist[(key >> shift) & 255u], 1u);
+      }
     }
     lds_barrier();
     if (t < 256) {
@@ -837,10 +847,18 @@ __global__ __launch_bounds__(kSelThreads) void adaptive_budget_kernel(
   lds_barrier();
   for (int h = 0; h < H_kv; ++h) {
     uint32_t gt = 0, eq = 0;
-    for (int p = t; p < W; p += kSelThreads) {
-      const uint32_t key = order_key(row[(int64_t)h * W + p]);
-      gt += key > T;
-      eq += key == T;
+    const float *hrow = row + (int64_t)h * W;
+    for (int p0 = t; p0 < W; p0 += kAdaptiveBatch * kSelThreads) {
+      float v[kAdaptiveBatch];
+#pragma unroll
+      for (int j = 0; j < kAdaptiveBatch; ++j) v[j] = hrow[min(p0 + j * kSelThreads, W - 1)];
+#pragma unroll
+      for (int j = 0; j < kAdaptiveBatch; ++j) {
+        const uint32_t key = order_key(v[j]);
+        const bool in = p0 + j * kSelThreads < W;
+        gt += in && key > T;
+        eq += in && key == T;
+      }
     }
     gt = wave_sum_u32(gt);
     eq = wave_sum_u32(eq);
