@@ -356,6 +356,34 @@ class CVSABackend:
         else:
             return self._reuse_step(q, k_cache, v_cache, block_tables, context_lens, layer_idx)
 
+    # ------------------------------------------------------------ graph replay
+    def reuse_plan_for(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
+        """The step plan this call would run as a reuse step at the current
+        step, or None when the call would score, check, or take another
+        path.  A reuse step through a plan is device work only (its counters
+        accumulate on the device), so a caller may capture it in a graph and
+        replay it for later reuse steps while this keeps returning the same
+        plan, calling ``note_replayed_reuse`` and ``step_done`` per replayed
+        call."""
+        if layer_idx in self._dense_layers or layer_idx not in self._reuse_state:
+            return None
+        if self.lazy:
+            if self._step % self.check_interval == 0:
+                return None
+            if (self._step % self.coverage_interval == 0
+                    and layer_idx in self._cached_page_scores):
+                return None
+        elif self.is_scoring_step:
+            return None
+        return self._matching_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens)
+
+    def note_replayed_reuse(self, layer_idx: int) -> None:
+        """Host bookkeeping of a reuse call that was replayed from a graph
+        instead of made (backend.py:313-321: the call clears the layer's
+        accept mask and expanded selection)."""
+        self._last_accept_mask.pop(layer_idx, None)
+        self._expanded_store.pop(layer_idx, None)
+
     # ------------------------------------------------------------ accounting
     def _ensure_work(self, device) -> torch.Tensor:
         if self._work_buf is None:

@@ -1,0 +1,206 @@
+"""Multi-layer decode driver with the reference harnesses' per-layer protocol.
+
+The reference decode loops (eval/latency_benchmark.py:361-562,
+eval/longbench_harness.py:323-391) run, for every generated token and every
+layer: project q/k/v, append the token's K/V to the layer's paged cache
+(SequenceKVManager.append_token_kv), call the attention backend on the
+layer's cache, then ``step_done(layer, num_layers)``; a step's latency is
+taken end to end with a synchronisation before it.  This driver runs the
+same protocol over synthetic per-step q/k/v (no model weights: the layer's
+output is not fed to the next layer, whose projections are synthetic too),
+so it measures the attention path as the harness drives it: the batched
+append, the backend's schedule and its host cost per layer call.
+
+With ``graphs=True`` a step whose every layer call is a reuse step through a
+step plan (``CVSABackend.reuse_plan_for``) is captured once as a HIP graph
+and replayed for later such steps while every layer still maps to the same
+plan: one launch for the attention of all layers instead of one validated
+host call per layer.  The appends stay eager (their block ids come from the
+host allocator).  Replays repeat the calls' host bookkeeping
+(``note_replayed_reuse``, ``step_done``), so schedule, counters and tracing
+state match an eager run; outputs are bit-identical to it.
+"""
+from __future__ import annotations
+
+import statistics
+from typing import List, Optional
+
+import torch
+
+from ..synthetic import jitter_query, make_paged_inputs
+from .kv_cache import PagedKVCache, SequenceKVManager
+
+
+class SyntheticDecodeLayers:
+    """Per-layer paged caches prefilled with synthetic K/V (independent seeds
+    per layer, hot pages as in the benchmark inputs) and a generator of the
+    per-step q / k / v of every layer."""
+
+    def __init__(self, num_layers: int, batch: int, num_q_heads: int, num_kv_heads: int,
+                 head_dim: int, context_len, max_new_tokens: int, block_size: int = 16,
+                 seed: int = 0, device="cuda", **hot):
+        self.num_layers = num_layers
+        self.batch = batch
+        self.num_q_heads = num_q_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.block_size = block_size
+        self.seed = seed
+        self.device = torch.device(device)
+        ctxs = [int(context_len)] * batch if isinstance(context_len, int) else list(context_len)
+        extra_pages = -(-max_new_tokens // block_size) + 1
+        self.caches: List[PagedKVCache] = []
+        self.managers: List[SequenceKVManager] = []
+        self.base_q: List[torch.Tensor] = []
+        for layer in range(num_layers):
+            inp = make_paged_inputs(batch, num_q_heads, num_kv_heads, head_dim, ctxs,
+                                    block_size=block_size, seed=seed + 7919 * layer,
+                                    device=self.device, spare_blocks=batch * extra_pages,
+                                    **hot)
+            nb = inp.k_cache.shape[0]
+            cache = PagedKVCache(nb, block_size, num_kv_heads, head_dim, device=str(self.device))
+            cache.k_cache.copy_(inp.k_cache)
+            cache.v_cache.copy_(inp.v_cache)
+            mgr = SequenceKVManager(cache, batch, max(ctxs) + max_new_tokens + block_size)
+            mgr.adopt(inp.block_tables, inp.context_lens, inp.used_blocks)
+            self.caches.append(cache)
+            self.managers.append(mgr)
+            self.base_q.append(inp.q)
+            del inp
+
+    def step_inputs(self, step: int):
+        """q [L, B, H_q, D] and the new token's k, v [L, B, H_kv, D] of a step
+        (bf16, deterministic in (seed, step))."""
+        L, B = self.num_layers, self.batch
+        q = torch.stack([jitter_query(self.base_q[l], 0.3, self.seed + 1000 * step + l)
+                         for l in range(L)])
+        g = torch.Generator(device=self.device).manual_seed(self.seed * 31 + step)
+        kv = torch.randn(2, L, B, self.num_kv_heads, self.head_dim, generator=g,
+                         device=self.device).to(torch.bfloat16)
+        return q, kv[0], kv[1]
+
+
+class DecodeDriver:
+    """Runs decode steps of ``layers`` through ``backend`` with the
+    reference per-layer protocol; see the module docstring."""
+
+    def __init__(self, backend, layers: SyntheticDecodeLayers, graphs: bool = False,
+                 stream: Optional[torch.cuda.Stream] = None):
+        self.backend = backend
+        self.layers = layers
+        self.graphs = graphs
+        # Graph capture needs a stream other than the legacy default one, and
+        # the step plans are bound to the stream they were made on: every
+        # step of the driver runs on this one.
+        self.stream = stream if stream is not None else torch.cuda.Stream(layers.device)
+        L, B = layers.num_layers, layers.batch
+        self.q_static = torch.empty(L, B, layers.num_q_heads, layers.head_dim,
+                                    dtype=torch.bfloat16, device=layers.device)
+        self._graph = None
+        self._graph_plans = None
+        self._graph_outs = None
+        self.replays = 0
+        self.captures = 0
+
+    # ------------------------------------------------------------ one step
+    def _append(self, k, v):
+        for l, mgr in enumerate(self.layers.managers):
+            mgr.append_tokens_kv(k[l], v[l])
+
+    def _eager(self, q) -> List[torch.Tensor]:
+        outs = []
+        L = self.layers.num_layers
+        for l in range(L):
+            cache, mgr = self.layers.caches[l], self.layers.managers[l]
+            outs.append(self.backend(q[l], cache.k_cache, cache.v_cache, mgr.block_tables,
+                                     mgr.context_lens, l))
+            self.backend.step_done(l, L)
+        return outs
+
+    def _plans_now(self):
+        """Every layer's reuse plan at the current step (None if any layer
+        would not run a plan-driven reuse step)."""
+        plans = []
+        for l in range(self.layers.num_layers):
+            cache, mgr = self.layers.caches[l], self.layers.managers[l]
+            p = self.backend.reuse_plan_for(self.q_static[l], cache.k_cache, cache.v_cache,
+                                            mgr.block_tables, mgr.context_lens, l)
+            if p is None:
+                return None
+            plans.append(p)
+        return plans
+
+    def step(self, q, k, v) -> List[torch.Tensor]:
+        """One decode step: q [L, B, H_q, D], k / v [L, B, H_kv, D], made on
+        the caller's current stream.  Returns the per-layer outputs, ready on
+        that stream; in graph mode they may be the graph's output buffers,
+        valid until the next step."""
+        caller = torch.cuda.current_stream(self.layers.device)
+        self.stream.wait_stream(caller)
+        outs = self._step(q, k, v)
+        caller.wait_stream(self.stream)
+        return outs
+
+    def _step(self, q, k, v) -> List[torch.Tensor]:
+        with torch.cuda.stream(self.stream):
+            self._append(k, v)
+            if not self.graphs:
+                return self._eager(q)
+            self.q_static.copy_(q)
+            plans = self._plans_now()
+            if plans is None:
+                return self._eager(self.q_static)
+            if self._graph is None or any(a is not b for a, b in zip(plans, self._graph_plans)):
+                # Capture this step's calls (their host bookkeeping runs now,
+                # their kernels only when the graph is replayed).
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=self.stream):
+                    outs = self._eager(self.q_static)
+                self._graph, self._graph_plans, self._graph_outs = graph, plans, outs
+                self.captures += 1
+                self._graph.replay()
+                return outs
+            self._graph.replay()
+            self.replays += 1
+            L = self.layers.num_layers
+            for l in range(L):
+                self.backend.note_replayed_reuse(l)
+                self.backend.step_done(l, L)
+            return self._graph_outs
+
+    # ------------------------------------------------------------ timing
+    def run(self, steps: int, warmup: int = 5, first_step: int = 0):
+        """The reference's timed decode (latency_benchmark.py:478-520):
+        warmup steps, a counter reset, then per-step end-to-end latency with
+        a synchronisation before each step.  Inputs of every step are made
+        before its timing starts."""
+        times = []
+        for i in range(warmup + steps):
+            s = first_step + i
+            q, k, v = self.layers.step_inputs(s)
+            torch.cuda.synchronize()
+            if i == warmup and hasattr(self.backend, "_accept_counts"):
+                self.backend._accept_counts = 0
+                self.backend._reject_counts = 0
+                self.backend._total_scoring_steps = 0
+                self.backend._per_head_accept_sum = 0
+                self.backend._per_head_total = 0
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record(self.stream)
+            self.step(q, k, v)
+            end.record(self.stream)
+            torch.cuda.synchronize()
+            if i >= warmup:
+                times.append(start.elapsed_time(end))
+        ms = sorted(times)
+        B = self.layers.batch
+        return {
+            "steps": steps, "warmup": warmup,
+            "mean_ms": statistics.mean(times), "median_ms": statistics.median(times),
+            "p95_ms": ms[min(len(ms) - 1, int(0.95 * len(ms)))],
+            "p99_ms": ms[min(len(ms) - 1, int(0.99 * len(ms)))],
+            "tokens_per_sec": B * 1000.0 / statistics.mean(times),
+            "per_step_ms": times,
+            "graph_replays": self.replays, "graph_captures": self.captures,
+        }

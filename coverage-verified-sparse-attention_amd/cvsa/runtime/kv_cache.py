@@ -102,6 +102,23 @@ class SequenceKVManager:
         self._pages_allocated_dev = torch.zeros(batch_size, dtype=torch.int32, device=dev)
         self._ctx_host = [0] * batch_size
 
+    def adopt(self, block_tables: torch.Tensor, context_lens: torch.Tensor,
+              next_free_block: int) -> None:
+        """Take over a prepared layout: page tables [B, <= max_pages] and
+        context lengths [B] whose pages are already written to the cache,
+        with blocks [0, next_free_block) in use."""
+        B, W = block_tables.shape
+        if B != self.batch_size or W > self.max_pages:
+            raise ValueError(f"block tables {tuple(block_tables.shape)} do not fit "
+                             f"[{self.batch_size}, {self.max_pages}]")
+        self.block_tables.zero_()
+        self.block_tables[:, :W].copy_(block_tables)
+        self.context_lens.copy_(context_lens)
+        bs = self.block_size
+        self._pages_allocated = [-(-int(c) // bs) for c in context_lens.tolist()]
+        self.cache._next_free = int(next_free_block)
+        self.sync_host_state()
+
     def sync_host_state(self):
         """Re-read context lengths and allocation counts from the device."""
         self._ctx_host = [int(x) for x in self.context_lens.tolist()]
