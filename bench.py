@@ -99,6 +99,10 @@ def parse_args():
                     help="also run an elementwise copy of this many MiB (counter calibration)")
     ap.add_argument("--selector", choices=("exact", "quest"), default="exact",
                     help="page ranking: the exact max q.k scan, or Quest min/max page metadata")
+    ap.add_argument("--e2e-layers", type=int, default=0,
+                    help="also run the decode driver (append + backend + step_done per layer, "
+                         "the reference harness protocol) over this many layers, eager and "
+                         "with graph-replayed reuse steps")
     ap.add_argument("--budget-samples", action="store_true",
                     help="also time the per-head budget selections (top-p 0.9, adaptive "
                          "budgets + selection, static table) on the workload's page scores")
@@ -200,6 +204,38 @@ def step_bytes(kind, accept, cfg, W, budget):
     if cfg["append"]:
         total += B * H * D * 2 * 2 * 2                                 # token K/V read + write
     return total
+
+
+def run_e2e(name, cfg, n_layers, args, dev, hot_shift, sink_shift):
+    """Whole decode steps through the decode driver (the reference
+    harness's per-layer protocol with appends), eager and with graph replay
+    of the reuse steps; inputs of each step made before its timing."""
+    import torch
+    from cvsa.backend import CVSABackend
+    from cvsa.runtime.decode_driver import DecodeDriver, SyntheticDecodeLayers
+    out = {"layers": n_layers, "protocol": "per layer: append_tokens_kv, backend call, "
+           "step_done; synchronised end-to-end step timing (latency_benchmark.py:478-520)"}
+    for graphs in (False, True):
+        layers = SyntheticDecodeLayers(
+            n_layers, cfg["B"], cfg["H_q"], cfg["H_kv"], D, cfg["ctx"],
+            max_new_tokens=args.warmup + args.steps + 1, seed=2000 + int(name[3]), device=dev,
+            hot_shift=hot_shift, sink_pages=cfg["sink_pages"], sink_shift=sink_shift,
+            **cfg["gen"])
+        sched = (dict(lazy=True, check_interval=cfg["M"]) if cfg["lazy"]
+                 else dict(lazy=False, reuse_interval=cfg["M"]))
+        backend = CVSABackend(num_kv_heads=cfg["H_kv"], num_q_heads=cfg["H_q"], head_dim=D,
+                              block_size=BS, num_layers=n_layers, budget_pct=cfg["budget"],
+                              coverage_threshold=0.9, selector=cfg["selector"],
+                              light_normalizer=cfg["light_normalizer"], **sched)
+        res = DecodeDriver(backend, layers, graphs=graphs).run(args.steps, args.warmup)
+        key = "graphs" if graphs else "eager"
+        out[key] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()
+                    if k != "per_step_ms"}
+        out[key]["per_step_ms"] = [round(x, 3) for x in res["per_step_ms"]]
+        out[key]["us_per_layer_call"] = round(res["mean_ms"] * 1e3 / n_layers, 2)
+        del layers, backend
+        torch.cuda.empty_cache()
+    return out
 
 
 def gpu_sleep(ms):
@@ -583,6 +619,10 @@ def main():
             for t, r in per_tau.items()}
     if args.config == "cfg5":
         result["stack_us_per_step"] = round(mean_us * L, 1)
+    if args.e2e_layers > 0:
+        log(f"decode driver over {args.e2e_layers} layers")
+        result["e2e"] = run_e2e(args.config, cfg, args.e2e_layers, args, dev, hot_shift,
+                                sink_shift)
     print(json.dumps(result), flush=True)
 
 

@@ -23,6 +23,7 @@ state match an eager run; outputs are bit-identical to it.
 from __future__ import annotations
 
 import statistics
+import time
 from typing import List, Optional
 
 import torch
@@ -174,7 +175,7 @@ class DecodeDriver:
         warmup steps, a counter reset, then per-step end-to-end latency with
         a synchronisation before each step.  Inputs of every step are made
         before its timing starts."""
-        times = []
+        times, host = [], []
         for i in range(warmup + steps):
             s = first_step + i
             q, k, v = self.layers.step_inputs(s)
@@ -188,11 +189,14 @@ class DecodeDriver:
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
             start.record(self.stream)
+            t0 = time.perf_counter()
             self.step(q, k, v)
+            t1 = time.perf_counter()
             end.record(self.stream)
             torch.cuda.synchronize()
             if i >= warmup:
                 times.append(start.elapsed_time(end))
+                host.append((t1 - t0) * 1e3)
         ms = sorted(times)
         B = self.layers.batch
         return {
@@ -202,5 +206,6 @@ class DecodeDriver:
             "p99_ms": ms[min(len(ms) - 1, int(0.99 * len(ms)))],
             "tokens_per_sec": B * 1000.0 / statistics.mean(times),
             "per_step_ms": times,
+            "host_ms_mean": statistics.mean(host),   # time to issue a step
             "graph_replays": self.replays, "graph_captures": self.captures,
         }
