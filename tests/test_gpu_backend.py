@@ -288,3 +288,41 @@ def test_baseline_configuration_full_size(gpu, name):
                         max_margin_frac=0.02)
     kinds = [t["kind"] for t in trace]
     assert "reuse" in kinds and kinds[0].startswith("score"), kinds
+
+
+def test_timing_buckets(gpu):
+    """enable_timing: get_stats adds the reference's per-kernel buckets
+    (backend.py:217-223, :300-310) with the same keys; the scoring, coverage
+    and draft buckets are filled, complement and LSE merge stay at zero (they
+    are folded into the verified decode), and the counters leave the
+    schedule statistics unchanged."""
+    inp = make_paged_inputs(1, 32, 8, 128, 3000, seed=6100, hot_heads=[0, 2, 4, 6], n_hot=8,
+                            hot_shift=12.0)
+    q, K, V, bt, cl = (t.to(gpu) for t in (inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
+                                            inp.context_lens))
+    timed = CVSABackend(8, 32, 128, 16, num_layers=2, budget_pct=0.25, lazy=True,
+                        check_interval=3)
+    plain = CVSABackend(8, 32, 128, 16, num_layers=2, budget_pct=0.25, lazy=True,
+                        check_interval=3)
+    timed.enable_timing(True)
+    for step in range(7):
+        qs = jitter_query(q, 0.3, 40 + step)
+        for layer in range(2):
+            a = timed(qs, K, V, bt, cl, layer)
+            b = plain(qs, K, V, bt, cl, layer)
+            assert torch.equal(a, b)
+            timed.step_done(layer, 2)
+            plain.step_done(layer, 2)
+    st, sp = timed.get_stats(), plain.get_stats()
+    keys = {"scoring", "coverage", "sparse_draft", "ar_recovery", "lse_merge", "complement"}
+    assert set(st["kernel_times_ms_total"]) == keys
+    assert set(st["kernel_counts"]) == keys and set(st["kernel_ms_per_decode_step"]) == keys
+    for k in ("scoring", "coverage", "sparse_draft"):
+        assert st["kernel_counts"][k] > 0 and st["kernel_times_ms_total"][k] > 0, k
+    assert st["kernel_counts"]["complement"] == 0 and st["kernel_counts"]["lse_merge"] == 0
+    n = st["total_decode_steps"]
+    assert n == 7
+    for k in keys:
+        assert st["kernel_ms_per_decode_step"][k] == pytest.approx(
+            st["kernel_times_ms_total"][k] / n)
+    assert {k: v for k, v in st.items() if not k.startswith("kernel_")} == sp
