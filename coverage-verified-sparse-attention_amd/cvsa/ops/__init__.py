@@ -36,6 +36,7 @@ __all__ = [
     "compute_complement",
     "lse_merge",
     "append_kv",
+    "AppendCall",
     "next_power_of_2",
     "StepPlan",
     "quest_meta_update",
@@ -952,3 +953,62 @@ def append_kv(k_new, v_new, k_cache, v_cache, block_tables, context_lens, pages_
         k_cache.shape[0], block_tables.data_ptr(), block_tables.stride(0),
         block_tables.shape[1], context_lens.data_ptr(), pages_allocated.data_ptr(), seq_begin,
         n, next_free_block, H_kv, D, block_size, _stream(dev)), "append_kv")
+
+
+class AppendCall:
+    """A validated cvsa_append_kv launch over fixed cache and table buffers.
+
+    Built once per set of buffers (and stream); ``run(k, v, seq_begin,
+    next_free_block)`` appends one token per sequence with only the per-call
+    arguments set, for the host cost of a decode loop that appends every
+    layer of every step.  ``k`` / ``v`` must be contiguous bfloat16
+    [n, H_kv, D] on the cache's device.
+    """
+
+    __slots__ = ("fn", "args", "dev", "stream", "refs", "H_kv", "D", "batch")
+
+    def __init__(self, k_cache, v_cache, block_tables, context_lens, pages_allocated,
+                 block_size: int):
+        dev = _device_of(k_cache, v_cache, block_tables, context_lens, pages_allocated)
+        _check_cache(k_cache)
+        _check_cache(v_cache, "v_cache")
+        if k_cache.shape != v_cache.shape:
+            raise ValueError("append_kv: k_cache and v_cache shapes differ")
+        for name, t in (("block_tables", block_tables), ("context_lens", context_lens),
+                        ("pages_allocated", pages_allocated)):
+            if t.dtype != torch.int32 or not t.is_contiguous():
+                raise ValueError(f"append_kv: {name} must be contiguous int32")
+        self.H_kv, self.D = k_cache.shape[2], k_cache.shape[3]
+        self.batch = block_tables.shape[0]
+        self.fn = _lib.load().cvsa_append_kv
+        self.args = [0, 0, self.H_kv * self.D, k_cache.data_ptr(), v_cache.data_ptr(),
+                     k_cache.shape[0], block_tables.data_ptr(), block_tables.stride(0),
+                     block_tables.shape[1], context_lens.data_ptr(), pages_allocated.data_ptr(),
+                     0, 0, 0, self.H_kv, self.D, block_size, _stream(dev)]
+        self.dev = dev
+        self.stream = self.args[-1]
+        self.refs = (k_cache, v_cache, block_tables, context_lens, pages_allocated)
+
+    def matches(self, k_cache, v_cache, block_tables, context_lens, pages_allocated) -> bool:
+        r = self.refs
+        return (r[0] is k_cache and r[1] is v_cache and r[2] is block_tables
+                and r[3] is context_lens and r[4] is pages_allocated
+                and torch._C._cuda_getCurrentRawStream(self.dev.index) == self.stream)
+
+    def run(self, k_new, v_new, seq_begin: int, next_free_block: int) -> None:
+        n = k_new.shape[0]
+        shape = (n, self.H_kv, self.D)
+        if (k_new.dtype != torch.bfloat16 or v_new.dtype != torch.bfloat16
+                or k_new.shape != shape or v_new.shape != shape
+                or not (k_new.is_contiguous() and v_new.is_contiguous())
+                or k_new.device != self.dev or v_new.device != self.dev
+                or not (0 <= seq_begin and seq_begin + n <= self.batch)):
+            raise ValueError(f"append_kv: k / v must be contiguous bfloat16 {shape} on "
+                             f"{self.dev} for sequences inside the batch of {self.batch}")
+        args = self.args
+        args[0] = k_new.data_ptr()
+        args[1] = v_new.data_ptr()
+        args[11] = seq_begin
+        args[12] = n
+        args[13] = next_free_block
+        check(self.fn(*args), "append_kv")

@@ -16,7 +16,8 @@ step plan (``CVSABackend.reuse_plan_for``) is captured once as a HIP graph
 and replayed for later such steps while every layer still maps to the same
 plan: one launch for the attention of all layers instead of one validated
 host call per layer.  The appends stay eager (their block ids come from the
-host allocator).  Replays repeat the calls' host bookkeeping
+host allocator) and run before the replay: each layer's cache is its own,
+so only a layer's own append has to precede its call.  Replays repeat the calls' host bookkeeping
 (``note_replayed_reuse``, ``step_done``), so schedule, counters and tracing
 state match an eager run; outputs are bit-identical to it.
 """
@@ -108,11 +109,15 @@ class DecodeDriver:
         for l, mgr in enumerate(self.layers.managers):
             mgr.append_tokens_kv(k[l], v[l])
 
-    def _eager(self, q) -> List[torch.Tensor]:
+    def _eager(self, q, k=None, v=None) -> List[torch.Tensor]:
+        """Per layer: the append of the new token (when k / v are given), the
+        backend call, step_done -- the reference's order."""
         outs = []
         L = self.layers.num_layers
         for l in range(L):
             cache, mgr = self.layers.caches[l], self.layers.managers[l]
+            if k is not None:
+                mgr.append_tokens_kv(k[l], v[l])
             outs.append(self.backend(q[l], cache.k_cache, cache.v_cache, mgr.block_tables,
                                      mgr.context_lens, l))
             self.backend.step_done(l, L)
@@ -144,9 +149,11 @@ class DecodeDriver:
 
     def _step(self, q, k, v) -> List[torch.Tensor]:
         with torch.cuda.stream(self.stream):
-            self._append(k, v)
             if not self.graphs:
-                return self._eager(q)
+                return self._eager(q, k, v)
+            # Graph mode: the appends go first (each layer's cache is its
+            # own, so only the layer's own append must precede its call).
+            self._append(k, v)
             self.q_static.copy_(q)
             plans = self._plans_now()
             if plans is None:

@@ -101,6 +101,7 @@ class SequenceKVManager:
         # host mirror of context_lens.
         self._pages_allocated_dev = torch.zeros(batch_size, dtype=torch.int32, device=dev)
         self._ctx_host = [0] * batch_size
+        self._append_call = None
 
     def adopt(self, block_tables: torch.Tensor, context_lens: torch.Tensor,
               next_free_block: int) -> None:
@@ -182,8 +183,17 @@ class SequenceKVManager:
     def _append(self, seq_begin: int, k: torch.Tensor, v: torch.Tensor):
         n = k.shape[0]
         seqs = range(seq_begin, seq_begin + n)
-        first = self.cache._reserve(self._plan_append(seqs))
-        ops.append_kv(k, v, self.cache.k_cache, self.cache.v_cache, self.block_tables,
-                      self.context_lens, self._pages_allocated_dev, seq_begin, first,
-                      self.block_size)
+        need = self._plan_append(seqs)
+        buffers = (self.cache.k_cache, self.cache.v_cache, self.block_tables, self.context_lens,
+                   self._pages_allocated_dev)
+        if (k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16 and k.is_contiguous()
+                and v.is_contiguous() and k.device == buffers[0].device):
+            # The launch over this manager's buffers is validated once.
+            call = self._append_call
+            if call is None or not call.matches(*buffers):
+                call = self._append_call = ops.AppendCall(*buffers, self.block_size)
+            call.run(k, v, seq_begin, self.cache._reserve(need))
+        else:
+            ops.append_kv(k, v, *buffers, seq_begin, self.cache._reserve(need),
+                          self.block_size)
         self._commit_append(seqs)
