@@ -702,7 +702,8 @@ class CVSABackend:
 
     def _scoring_step(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx,
                       page_scores=None):
-        """backend.py:683-864 (uniform budget; exact or approximate recovery)."""
+        """backend.py:683-864 (uniform, top-p, static-table or adaptive budgets;
+        exact or approximate recovery)."""
         B = q.shape[0]
         n_pages = block_tables.shape[1]
         budget = max(3, int(n_pages * self.budget_pct))                           # :690
