@@ -90,7 +90,8 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=None, help="layer caches rotated per step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=None,
-                    help="decode steps of the CPU oracle sample (default: one M-step cycle)")
+                    help="decode steps of the CPU oracle sample (default: whole schedule "
+                         "cycles until about 12 s of CPU work)")
     ap.add_argument("--kernel-samples", type=int, default=16)
     ap.add_argument("--hot-shift", type=float, default=None,
                     help="hot-page key shift in std units of q_rep.k (default: per config)")
@@ -280,9 +281,14 @@ def measured_traffic():
     return None
 
 
+CPU_SAMPLE_S = 12.0   # CPU work the default baseline sample aims for
+
+
 def cpu_baseline(cfg, layer0, n_steps, tau):
-    """The CPU oracle (fp32, all host cores) on layer 0's cache, n_steps decode
-    steps from a fresh backend (the first is a scoring step)."""
+    """The CPU oracle (fp32, all host cores) on layer 0's cache: decode steps
+    from a fresh backend (the first is a scoring step), n_steps of them, or
+    (n_steps None) whole schedule cycles of M steps until CPU_SAMPLE_S
+    seconds of step time have accumulated."""
     import torch
     from oracle.backend_oracle import OracleCVSABackend
     from cvsa.synthetic import jitter_query
@@ -295,12 +301,19 @@ def cpu_baseline(cfg, layer0, n_steps, tau):
                           reuse_interval=cfg["M"], selector=cfg["selector"],
                           light_normalizer=cfg["light_normalizer"], acc_dtype=torch.float32)
     times = []
-    for s in range(n_steps):
+    s = 0
+    while True:
         q = jitter_query(q0, Q_JITTER, 50_000 + s)
         t0 = time.perf_counter()
         b(q, *args, 0)
         times.append(time.perf_counter() - t0)
         b.step_done(0, 1)
+        s += 1
+        if n_steps is not None:
+            if s >= n_steps:
+                break
+        elif s % cfg["M"] == 0 and sum(times) >= CPU_SAMPLE_S:
+            break
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -559,15 +572,16 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        n_cpu = args.cpu_steps or M
-        log(f"CPU oracle baseline ({n_cpu} steps)")
-        times, threads, model = cpu_baseline(cfg, layers[0], n_cpu, tau0)
+        log("CPU oracle baseline")
+        times, threads, model = cpu_baseline(cfg, layers[0], args.cpu_steps, tau0)
+        n_cpu = len(times)
         cpu = {"value": statistics.mean(times) * 1e6,
                "unit": f"us per decode step (mean of {n_cpu} steps)",
                "cores": threads, "kind": "port",
-               "sample": f"{n_cpu} decode steps (first a scoring step) of layer 0 at full "
-                         f"{args.config} size, fp32 oracle, torch CPU, {model}",
-               "step_s": times}
+               "sample": f"{n_cpu} decode steps ({n_cpu // M} schedule cycles of {M}, the "
+                         f"first a scoring step; {sum(times):.1f} s of CPU work) of layer 0 "
+                         f"at full {args.config} size, fp32 oracle, torch CPU, {model}",
+               "step_s": [round(t, 4) for t in times]}
 
     mean_us, med_us = res["mean_us"], res["med_us"]
     result = {
