@@ -290,6 +290,24 @@ def test_baseline_configuration_full_size(gpu, name):
     assert "reuse" in kinds and kinds[0].startswith("score"), kinds
 
 
+@pytest.mark.parametrize("kw", [
+    dict(selector="quest"),
+    dict(selector="quest", light_normalizer=True),
+    dict(top_p=0.9, coverage_threshold=0.95),
+    dict(adaptive_selection=True),
+])
+def test_selectors_at_cfg3_full_size(gpu, kw):
+    """The Quest, light-normalizer, top-p and adaptive schedules at cfg3's
+    full size (128K context, 8192 pages) against the oracle backend."""
+    cfg, budget, seed = FULL_SIZE["cfg3"]
+    kw = dict(dict(budget_pct=budget, coverage_threshold=0.9, lazy=True, check_interval=5),
+              **kw)
+    stats, trace = _run(gpu, cfg, kw, steps=6, seed=seed + 11, gen_on_gpu=True,
+                        max_margin_frac=0.02)
+    kinds = [t["kind"] for t in trace]
+    assert "reuse" in kinds and kinds[0].startswith("score"), kinds
+
+
 def test_timing_buckets(gpu):
     """enable_timing: get_stats adds the reference's per-kernel buckets
     (backend.py:217-223, :300-310) with the same keys; the scoring, coverage
