@@ -15,7 +15,26 @@ C header):
   * empty page list: (o, m, l) = (0, -inf, 0) and a zero normalised output
     (the reference produces NaN, cvsa/kernels/sparse_decode.py:107,263);
   * listed pages outside [0, W) or mapping to a block outside the pool, and
-    pages without a valid token, contribute nothing.
+    pages without a valid token, contribute nothing;
+  * top-p, static-table and adaptive selections: ties to the lower page (and,
+    for the adaptive head competition, to the lower head), where torch's
+    sort / topk leave them open (cvsa/backend.py:537-541, :567, :647, :672).
+
+How each function is pinned (tests/test_oracle_*.py unless noted):
+  * score_pages, check_coverage, select_topk, sparse_decode(_unnorm),
+    dense_decode, compute_complement, lse_merge, append_token_kv: the
+    reference backend's golden traces (tests/golden/), the reference tests'
+    known answers, closed forms and brute force (test_oracle_known_answers,
+    test_oracle_closed_form, test_golden_backend_trace);
+  * page_key_minmax, quest_page_scores: the Quest bound's mathematics
+    (upper bound of the exact page max, equality on one-token pages, brute
+    force, masked slots, q . kmax for a non-negative query), test_oracle_quest;
+  * topp_need, topp_select, static_budgets, static_select, adaptive_budgets,
+    adaptive_select: closed forms (uniform and geometric masses, the strict
+    boundary, clamps, half-even rounding, floor ratios 0 and 1, a dominating
+    head) and scalar brute force, test_oracle_selectors.
+Parity unpinned: the tie order at top-p / adaptive boundaries (implementation
+defined in the reference) and the dense baseline's FlashInfer arithmetic.
 """
 from __future__ import annotations
 
