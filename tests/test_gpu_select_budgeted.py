@@ -157,10 +157,13 @@ def test_static_table_matches_oracle(gpu, W):
 
 
 @pytest.mark.parametrize("H,W,base,floor", [(4, 64, 10, 0.0), (8, 3000, 300, 0.5),
-                                            (8, 2048, 200, 0.25), (2, 500, 499, 0.0)])
+                                            (8, 2048, 200, 0.25), (2, 500, 499, 0.0),
+                                            (8, 8192, 1024, 0.5), (16, 5000, 100, 0.5)])
 def test_adaptive_budgets_match_oracle(gpu, H, W, base, floor):
     """Budgets exact (ties at the threshold to the lower head on both sides;
-    rounded scores make many ties), then the selection by those budgets."""
+    rounded scores make many ties), then the selection by those budgets.
+    The shapes take the register-resident kernels (H * W up to 64K scores)
+    and the streaming one (16 x 5000)."""
     B = 3
     valid = [W, W // 2, 5]
     g = torch.Generator().manual_seed(W + H)
