@@ -433,3 +433,40 @@ def test_decode_many_splits(gpu, ctx, budget):
         assert (dense[0, rows].float() - dwant).abs().max().item() < OUT_ATOL, h
         dlse = dm[0, rows] + torch.log(dl[0, rows])
         assert ((dlse - dwant_lse).abs() / dwant_lse.abs().clamp(min=1.0)).max().item() < LSE_RTOL
+
+
+def test_append_prepared_and_converting_paths_agree(gpu):
+    """SequenceKVManager appends bf16 rows through a prepared launch
+    (ops.AppendCall) and other dtypes through ops.append_kv: the same
+    tokens give the same caches, tables and lengths either way, across page
+    boundaries; the prepared call rejects rows that do not fit it."""
+    from cvsa.runtime.kv_cache import PagedKVCache, SequenceKVManager
+    B, H, D = 3, 8, 128
+    caches, mgrs = [], []
+    for _ in range(2):
+        c = PagedKVCache(32, 16, H, D, device=str(gpu))
+        m = SequenceKVManager(c, B, 16 * 6)
+        caches.append(c)
+        mgrs.append(m)
+    g = torch.Generator().manual_seed(8)
+    for step in range(40):
+        k = torch.randn(B, H, D, generator=g).to(gpu)
+        v = torch.randn(B, H, D, generator=g).to(gpu)
+        mgrs[0].append_tokens_kv(k.to(torch.bfloat16), v.to(torch.bfloat16))   # prepared
+        mgrs[1].append_tokens_kv(k, v)                                         # converting
+        if step % 7 == 3:   # a single sequence through the prepared call
+            kb = torch.randn(H, D, generator=g).to(torch.bfloat16).to(gpu)
+            mgrs[0].append_token_kv(1, kb, kb)
+            mgrs[1].append_token_kv(1, kb.float(), kb.float())
+    assert mgrs[0]._append_call is not None and mgrs[1]._append_call is None
+    for a, b in ((caches[0].k_cache, caches[1].k_cache), (caches[0].v_cache, caches[1].v_cache),
+                 (mgrs[0].block_tables, mgrs[1].block_tables),
+                 (mgrs[0].context_lens, mgrs[1].context_lens)):
+        assert torch.equal(a, b)
+    call = mgrs[0]._append_call
+    bad = torch.zeros(B, H, D - 1, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        call.run(bad, bad, 0, caches[0]._next_free)
+    ok = torch.zeros(2, H, D, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):   # rows past the batch
+        call.run(ok, ok, 2, caches[0]._next_free)
