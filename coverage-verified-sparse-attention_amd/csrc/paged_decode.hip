@@ -1100,17 +1100,22 @@ static DecodeLaunch plan_launch(int B, int H_kv, int max_sel, int W, bool listed
   return p;
 }
 
-// Workspace: per-head completion counters (uint32, padded to 256 bytes),
-// then the partial rows.
-static size_t counter_bytes(int heads) { return ((size_t)heads * 4 + 255) / 256 * 256; }
+// Workspace: a fixed area of kMaxHeads completion counters (uint32), then
+// the partial rows.  The counter area has the same size and place for every
+// launch, so launches of different B * H_kv that share a workspace never
+// read one another's partial rows as counters: counter h of every launch is
+// word h, and every launch leaves the words it used at zero.  Launches with
+// split partials have at most kMaxHeads heads (stream-K: checked at launch;
+// listed: more than one split per head only below kMaxSplits heads).
+constexpr size_t kCounterAreaBytes = (size_t)kMaxHeads * sizeof(unsigned);
+static_assert(kCounterAreaBytes % 256 == 0, "partial rows start 256-byte aligned");
 
 static size_t workspace_bytes_for(int B, int H_q, int H_kv, int max_sel, int W, bool listed,
                                   bool all_pages) {
-  const int heads = B * H_kv;
   const int G = H_q / H_kv;
   const DecodeLaunch p = plan_launch(B, H_kv, max_sel, W, listed, all_pages);
   if (p.partial_rows == 0) return 0;
-  return counter_bytes(heads) + p.partial_rows * G * kPartStride * sizeof(float);
+  return kCounterAreaBytes + p.partial_rows * G * kPartStride * sizeof(float);
 }
 
 // Lanes per token row, chosen so that the o accumulators stay at <= 64
@@ -1163,8 +1168,8 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
                CVSA_ERR_INVALID, "%s: bad output dtype %d", name, a.out_dtype);
 
   const DecodeLaunch p = plan_launch(B, H_kv, listed ? a.max_sel : 0, W, listed, all_pages);
-  CVSA_REQUIRE(!p.streamk || (int64_t)B * H_kv <= kMaxHeads, CVSA_ERR_UNSUPPORTED,
-               "%s: B * H_kv = %lld exceeds %d heads per launch", name,
+  CVSA_REQUIRE((!p.streamk && p.partial_rows == 0) || (int64_t)B * H_kv <= kMaxHeads,
+               CVSA_ERR_UNSUPPORTED, "%s: B * H_kv = %lld exceeds %d heads per launch", name,
                (long long)B * H_kv, kMaxHeads);
   const size_t need = workspace_bytes_for(B, H_q, H_kv, listed ? a.max_sel : 0, W, listed,
                                           all_pages);
@@ -1182,8 +1187,8 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
   a.counters = reinterpret_cast<unsigned *>(workspace);
   a.part = need == 0 ? nullptr
                      : reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) +
-                                                 counter_bytes(B * H_kv));
-  const size_t pbytes = need == 0 ? 0 : need - counter_bytes(B * H_kv);
+                                                 kCounterAreaBytes);
+  const size_t pbytes = need == 0 ? 0 : need - kCounterAreaBytes;
   CVSA_REQUIRE(pbytes < ((size_t)1 << 31), CVSA_ERR_UNSUPPORTED,
                "%s: %zu bytes of split partials exceed the 2 GiB buffer range", name, pbytes);
   a.part_bytes = (uint32_t)pbytes;

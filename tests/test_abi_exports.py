@@ -57,6 +57,26 @@ def test_errors_are_reported_without_gpu_work():
     assert rc > 0
 
 
+def test_decode_workspace_layout_is_fixed():
+    """Every decode workspace starts with the same 16 KiB counter area
+    (4096 heads x 4 bytes) followed by whole partial rows of G x 132 fp32, so
+    launches of any B * H_kv can share one workspace: the counters of one
+    launch never overlap the partial rows of another."""
+    lib = _lib_or_skip()
+    seen = 0
+    for B in (1, 2, 3, 16, 32, 64):
+        for H_kv, G in ((8, 4), (4, 7), (8, 8), (1, 1)):
+            for max_sel, W, all_pages in ((1024, 8192, 0), (128, 512, 1), (64, 2048, 0),
+                                          (0, 512, 1)):
+                n = lib.cvsa_decode_workspace_bytes(B, H_kv * G, H_kv, 128, max_sel, W,
+                                                    all_pages)
+                if n == 0:
+                    continue
+                seen += 1
+                assert n > 16384 and (n - 16384) % (G * 132 * 4) == 0, (B, H_kv, G, n)
+    assert seen > 20
+
+
 def _step_desc(**over):
     """A well-formed step descriptor over fake (never dereferenced) pointers."""
     fake = iter(range(1 << 20, 1 << 30, 1 << 16))

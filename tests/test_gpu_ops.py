@@ -435,6 +435,52 @@ def test_decode_many_splits(gpu, ctx, budget):
         assert ((dlse - dwant_lse).abs() / dwant_lse.abs().clamp(min=1.0)).max().item() < LSE_RTOL
 
 
+def test_workspace_shared_across_head_counts(gpu):
+    """Decode launches of different B * H_kv share one workspace on one
+    stream: a split listed decode at B=1, H_kv=8, W=8192 (256 partial rows)
+    followed by a verified decode at B=16, H_kv=8, 8K context (128 heads,
+    stream-K), and then the listed decode again.  Regression: the counter
+    area was sized per launch, so the second launch read the first one's
+    partial rows as the counters of heads 64..127, skipped their merges and
+    left their outputs unwritten.  Both launches are compared with the
+    oracle."""
+    ops._WORKSPACES.clear()       # the first launch below sizes the workspace
+    H, G = 8, 4
+    big = make_paged_inputs(1, 32, H, 128, 131072, seed=430, device=gpu, hot_heads=[1, 5],
+                            n_hot=16, hot_shift=8.0)
+    ps = ops.score_pages(big.q, big.k_cache, big.block_tables, big.context_lens, H, G, 16)
+    idx, nph = ops.select_topk(ps, 1024, big.context_lens, 16)
+    small = _inputs(431, 16, 32, H, 8192)
+    sq, sK, sV, sbt, scl = _dev(small, gpu)
+    sps = ref.score_pages(small.q, small.k_cache, small.block_tables, small.context_lens, H, G,
+                          16)
+    sidx, snph = ref.select_topk(sps, 128, small.context_lens, 16)
+    g = torch.Generator().manual_seed(432)
+    sacc = torch.rand(16, H, generator=g) > 0.3
+    swant = ref.verified_decode(small.q, small.k_cache, small.v_cache, small.block_tables,
+                                small.context_lens, sidx, snph, sacc, H, G, 16)
+    bq, bK, bV, bbt, bcl = (t.cpu() for t in (big.q, big.k_cache, big.v_cache,
+                                              big.block_tables, big.context_lens))
+    bwant = ref.sparse_decode(bq, bK, bV, bbt, idx.cpu(), nph.cpu(), bcl, H, G, 16)
+
+    def listed():
+        return ops.sparse_decode(big.q, big.k_cache, big.v_cache, big.block_tables, idx, nph,
+                                 big.context_lens, H, G, 16).cpu()
+
+    def verified():
+        return ops.verified_decode(sq, sK, sV, sbt, scl, sidx.to(gpu), snph.to(gpu),
+                                   sacc.to(gpu), H, G, 16).cpu()
+
+    first = listed()
+    ws = ops._WORKSPACES[(gpu.index, ops._stream(gpu))]
+    second = verified()
+    assert ops._WORKSPACES[(gpu.index, ops._stream(gpu))] is ws   # the same workspace
+    third = listed()
+    for got, want in ((first, bwant), (second, swant), (third, bwant)):
+        assert (got.float() - want.float()).abs().max().item() < OUT_ATOL
+    assert torch.equal(first, third)
+
+
 def test_append_prepared_and_converting_paths_agree(gpu):
     """SequenceKVManager appends bf16 rows through a prepared launch
     (ops.AppendCall) and other dtypes through ops.append_kv: the same
