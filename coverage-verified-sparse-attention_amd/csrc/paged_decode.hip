@@ -36,6 +36,8 @@
 #include <hip/hip_fp16.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 namespace cvsa {
 
 // Split partials are rows of kPartStride floats: o[D], m, l and two pad
@@ -1125,9 +1127,11 @@ struct LanesPerRow {
   static constexpr int value = G <= 2 ? 4 : (G <= 4 ? 8 : 16);
 };
 
-static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_kv, int D,
-                         int block_size, int W, bool listed, bool all_pages,
-                         void *workspace, size_t workspace_bytes, hipStream_t st) {
+// Argument checks of a decode launch (everything but the workspace) and its
+// launch plan; fills the launch-shape fields of `a`.  Returns a status.
+static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int H_kv, int D,
+                           int block_size, int W, bool listed, bool all_pages,
+                           DecodeLaunch &p, size_t &need) {
   CVSA_REQUIRE(a.q && a.k_cache && a.v_cache && a.block_tables && a.ctx_lens,
                CVSA_ERR_INVALID, "%s: null pointer argument", name);
   CVSA_REQUIRE(B > 0 && B * (int64_t)H_kv <= 65535 && W > 0 && a.num_blocks > 0,
@@ -1167,31 +1171,32 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
                                     a.out_dtype <= CVSA_DTYPE_FP32),
                CVSA_ERR_INVALID, "%s: bad output dtype %d", name, a.out_dtype);
 
-  const DecodeLaunch p = plan_launch(B, H_kv, listed ? a.max_sel : 0, W, listed, all_pages);
+  p = plan_launch(B, H_kv, listed ? a.max_sel : 0, W, listed, all_pages);
   CVSA_REQUIRE((!p.streamk && p.partial_rows == 0) || (int64_t)B * H_kv <= kMaxHeads,
                CVSA_ERR_UNSUPPORTED, "%s: B * H_kv = %lld exceeds %d heads per launch", name,
                (long long)B * H_kv, kMaxHeads);
-  const size_t need = workspace_bytes_for(B, H_q, H_kv, listed ? a.max_sel : 0, W, listed,
-                                          all_pages);
-  CVSA_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need &&
-                                ((uintptr_t)workspace & 255) == 0),
-               CVSA_ERR_WORKSPACE,
-               "%s: workspace of %zu bytes (256-byte aligned) required, got %zu", name,
-               need, workspace_bytes);
+  need = workspace_bytes_for(B, H_q, H_kv, listed ? a.max_sel : 0, W, listed, all_pages);
+  CVSA_REQUIRE(need == 0 || need - kCounterAreaBytes < ((size_t)1 << 31),
+               CVSA_ERR_UNSUPPORTED,
+               "%s: %zu bytes of split partials exceed the 2 GiB buffer range", name,
+               need - kCounterAreaBytes);
   a.W = W;
   a.H_kv = H_kv;
   a.heads = B * H_kv;
   a.pps = p.pps;
   a.n_splits = p.n_splits;
   a.scale = (float)pow((double)D, -0.5);
+  return CVSA_OK;
+}
+
+// Enqueue a validated launch with its workspace (need bytes, 0 = none).
+static int enqueue_decode(const char *name, DecodeArgs a, int G, bool listed,
+                          const DecodeLaunch &p, void *workspace, size_t need, hipStream_t st) {
   a.counters = reinterpret_cast<unsigned *>(workspace);
   a.part = need == 0 ? nullptr
                      : reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) +
                                                  kCounterAreaBytes);
-  const size_t pbytes = need == 0 ? 0 : need - kCounterAreaBytes;
-  CVSA_REQUIRE(pbytes < ((size_t)1 << 31), CVSA_ERR_UNSUPPORTED,
-               "%s: %zu bytes of split partials exceed the 2 GiB buffer range", name, pbytes);
-  a.part_bytes = (uint32_t)pbytes;
+  a.part_bytes = need == 0 ? 0u : (uint32_t)(need - kCounterAreaBytes);
   const bool use_mfma = decode_engine() == 1;
   const dim3 grid(p.grid_x, p.grid_y), block(kWavesPerWg * kWave);
 #define CVSA_DEC_LAUNCH(GG, ENG)                                                             \
@@ -1228,6 +1233,22 @@ static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_k
 #undef CVSA_DEC_CASE
 #undef CVSA_DEC_LAUNCH
   return cvsa_host::check_launch(name);
+}
+
+static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_kv, int D,
+                         int block_size, int W, bool listed, bool all_pages,
+                         void *workspace, size_t workspace_bytes, hipStream_t st) {
+  DecodeLaunch p{};
+  size_t need = 0;
+  const int rc = validate_decode(name, a, B, H_q, H_kv, D, block_size, W, listed, all_pages, p,
+                                 need);
+  if (rc != CVSA_OK) return rc;
+  CVSA_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need &&
+                                ((uintptr_t)workspace & 255) == 0),
+               CVSA_ERR_WORKSPACE,
+               "%s: workspace of %zu bytes (256-byte aligned) required, got %zu", name,
+               need, workspace_bytes);
+  return enqueue_decode(name, a, H_q / H_kv, listed, p, workspace, need, st);
 }
 
 static DecodeArgs base_args(const uint16_t *q, int64_t q_sb, int64_t q_sh,
@@ -1302,6 +1323,97 @@ extern "C" int cvsa_sparse_decode(const uint16_t *q, int64_t q_stride_b, int64_t
     return cvsa_host::fail(CVSA_ERR_INVALID, "sparse_decode: page_indices is NULL");
   return launch_decode("sparse_decode", a, B, H_q, H_kv, D, block_size, W, true, false,
                        workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+// ------------------------------------------------ allocation-free variant
+// cvsa_sparse_decode_noalloc keeps the decode workspace in this file-scope
+// device array instead of a caller-owned buffer.  Each GPU the library runs
+// on holds its own copy until the process ends.  A listed launch needs at
+// most kCounterAreaBytes + kMaxSplits partial rows of 8 x 132 fp32 (1.1 MB:
+// plan_launch splits heads only when there are fewer than kMaxSplits of them,
+// into at most kMaxSplits / heads splits each), so every call
+// cvsa_sparse_decode accepts fits; a larger need is refused all the same.
+constexpr size_t kScratchBytes = (size_t)2 << 20;
+static_assert(kScratchBytes >= kCounterAreaBytes + (size_t)kMaxSplits * 8 * kPartStride *
+                                                       sizeof(float),
+              "scratch holds every listed launch");
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch`, per device
+
+// The device address of `scratch` on the stream's device, looked up once per
+// device (with that device current).  The first lookup also zeroes the
+// counter area on `st`, ahead of the call's own launch; every launch leaves
+// the counters it used at zero again.  The partial rows need no clearing:
+// each launch writes a row before any workgroup reads it.
+static int scratch_for(hipStream_t st, void **out) {
+  int dev = 0;
+  hipError_t e = st != nullptr ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+  CVSA_REQUIRE(e == hipSuccess, CVSA_ERR_INVALID,
+               "sparse_decode_noalloc: cannot tell the stream's device: %s",
+               hipGetErrorString(e));
+  CVSA_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, CVSA_ERR_UNSUPPORTED,
+               "sparse_decode_noalloc: device %d beyond the %d supported", dev,
+               kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = 0;
+    bool switched = false;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) {
+      e = hipSetDevice(dev);
+      switched = e == hipSuccess;
+    }
+    void *ptr = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(fill_zero_kernel, dim3(16), dim3(256), 0, st,
+                         reinterpret_cast<uint32_t *>(ptr), kCounterAreaBytes / 4);
+      e = hipGetLastError();
+    }
+    if (switched) (void)hipSetDevice(cur);
+    CVSA_REQUIRE(e == hipSuccess && ptr != nullptr, CVSA_ERR_LAUNCH,
+                 "sparse_decode_noalloc: scratch set-up on device %d failed: %s", dev,
+                 hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return CVSA_OK;
+}
+
+extern "C" int cvsa_sparse_decode_noalloc(
+    const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t *k_cache,
+    const uint16_t *v_cache, int64_t num_blocks, const int32_t *block_tables,
+    int64_t bt_stride_b, const int32_t *context_lens, const int32_t *page_indices,
+    int64_t idx_stride, const int32_t *n_per_head, int32_t max_selected, int32_t B,
+    int32_t H_q, int32_t H_kv, int32_t D, int32_t block_size, int32_t W, float *o_unnorm,
+    float *m_out, float *l_out, void *out, int32_t out_dtype, int64_t *work, void *stream) {
+  const char *name = "sparse_decode_noalloc";
+  DecodeArgs a = base_args(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                           block_tables, bt_stride_b, context_lens, o_unnorm, m_out, l_out,
+                           out, out_dtype, work);
+  a.page_idx = page_indices;
+  a.idx_stride = idx_stride;
+  a.max_sel = max_selected;
+  a.n_pages = n_per_head;
+  if (page_indices == nullptr)
+    return cvsa_host::fail(CVSA_ERR_INVALID, "%s: page_indices is NULL", name);
+  DecodeLaunch p{};
+  size_t need = 0;
+  const int rc = validate_decode(name, a, B, H_q, H_kv, D, block_size, W, true, false, p, need);
+  if (rc != CVSA_OK) return rc;
+  CVSA_REQUIRE(need <= kScratchBytes, CVSA_ERR_WORKSPACE,
+               "%s: the launch needs %zu bytes of scratch, more than the %zu-byte static "
+               "scratch; use cvsa_sparse_decode with a workspace",
+               name, need, kScratchBytes);
+  void *ws = nullptr;
+  if (need > 0) {
+    const int src = scratch_for((hipStream_t)stream, &ws);
+    if (src != CVSA_OK) return src;
+  }
+  return enqueue_decode(name, a, H_q / H_kv, true, p, ws, need, (hipStream_t)stream);
 }
 
 extern "C" int cvsa_dense_decode(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,

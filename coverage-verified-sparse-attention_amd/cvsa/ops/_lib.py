@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parents[1] / "libcvsa_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 CVSA_OK = 0
 CVSA_ERR_INVALID = -1
@@ -77,6 +77,11 @@ SIGNATURES = {
         _p, _i64, _p, _i32,
         _i32, _i32, _i32, _i32, _i32, _i32,
         _p, _p, _p, _p, _i32, _p, _p, _sz, _p]),
+    "cvsa_sparse_decode_noalloc": (ctypes.c_int, [
+        _p, _i64, _i64, _p, _p, _i64, _p, _i64, _p,
+        _p, _i64, _p, _i32,
+        _i32, _i32, _i32, _i32, _i32, _i32,
+        _p, _p, _p, _p, _i32, _p, _p]),
     "cvsa_dense_decode": (ctypes.c_int, [
         _p, _i64, _i64, _p, _p, _i64, _p, _i64, _p,
         _i32, _i32, _i32, _i32, _i32, _i32,

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 7
+#define CVSA_ABI_VERSION 8
 
 enum {
   CVSA_OK = 0,
@@ -224,6 +224,34 @@ int cvsa_sparse_decode(const uint16_t *q, int64_t q_stride_b,
                        float *m_out, float *l_out, void *out,
                        int32_t out_dtype, int64_t *work, void *workspace,
                        size_t workspace_bytes, void *stream);
+
+/*
+ * cvsa_sparse_decode without a workspace argument: allocates nothing and
+ * needs no caller-owned scratch.  No counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The split-K
+ * counters and partials live in a static 2 MiB device array of the library
+ * (one per GPU, held until the process ends; every listed launch needs at
+ * most 1.1 MB of it, a larger need returns CVSA_ERR_WORKSPACE).  Its first
+ * call on a device looks the array up and zeroes its counters on `stream`.
+ * All calls on one GPU share the array: calls that overlap in time on one
+ * GPU (other streams, other threads) race and must be ordered by the
+ * caller.  Arguments, outputs and errors as cvsa_sparse_decode.
+ */
+int cvsa_sparse_decode_noalloc(const uint16_t *q, int64_t q_stride_b,
+                               int64_t q_stride_h, const uint16_t *k_cache,
+                               const uint16_t *v_cache, int64_t num_blocks,
+                               const int32_t *block_tables,
+                               int64_t bt_stride_b,
+                               const int32_t *context_lens,
+                               const int32_t *page_indices,
+                               int64_t idx_stride,
+                               const int32_t *n_per_head,
+                               int32_t max_selected, int32_t B, int32_t H_q,
+                               int32_t H_kv, int32_t D, int32_t block_size,
+                               int32_t W, float *o_unnorm, float *m_out,
+                               float *l_out, void *out, int32_t out_dtype,
+                               int64_t *work, void *stream);
 
 /*
  * Dense paged decode over every valid page.  Replaces
