@@ -172,6 +172,11 @@ class CVSABackend:
         self._quest_meta: Dict[int, Tuple[weakref.ref, ops.QuestPageMeta]] = {}
 
         self._last_accept_mask: Dict[int, Optional[torch.Tensor]] = {}
+        # (gate scores, per-head accept) of the coverage check of a layer's
+        # cached selection in its last call, when that call ran one (lazy
+        # check or coverage-only step); views of live buffers, read them
+        # before the layer's next call.
+        self._last_check: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
         self._expanded_store: Dict[int, object] = {}
         self._attn_work: Optional[torch.Tensor] = None
         self._attn_work_max: Optional[torch.Tensor] = None
@@ -261,6 +266,7 @@ class CVSABackend:
         self._cached_selection = {}
         self._cached_page_scores = {}
         self._last_accept_mask = {}
+        self._last_check = {}
         self._expanded_store = {}
         if self._attn_work is not None:
             self._attn_work.zero_()
@@ -320,6 +326,7 @@ class CVSABackend:
     def __call__(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
         """backend.py:313-366"""
         self._last_accept_mask.pop(layer_idx, None)
+        self._last_check.pop(layer_idx, None)
         self._expanded_store.pop(layer_idx, None)
 
         if layer_idx in self._dense_layers:
@@ -382,6 +389,7 @@ class CVSABackend:
         instead of made (backend.py:313-321: the call clears the layer's
         accept mask and expanded selection)."""
         self._last_accept_mask.pop(layer_idx, None)
+        self._last_check.pop(layer_idx, None)
         self._expanded_store.pop(layer_idx, None)
 
     # ------------------------------------------------------------ accounting
@@ -458,6 +466,8 @@ class CVSABackend:
             plan = self._lazy_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens)
             if plan is not None:
                 output = plan.run(ops._lib.STEP_LAZY_CHECK, q)
+                self._last_check[layer_idx] = (plan.page_scores,
+                                               plan.check_accept.view(torch.bool))
                 self._total_coverage_checks += 1
                 self._book_plan_gate(plan, layer_idx, context_lens)
                 return output
@@ -479,6 +489,7 @@ class CVSABackend:
             accept_mask, coverage = self._time_kernel(
                 "coverage", ops.check_coverage, page_scores, page_indices, n_per_head,
                 self.tau)
+            self._last_check[layer_idx] = (page_scores, accept_mask)
             if self._device_decision_ok(layer_idx, page_scores, context_lens):
                 return self._lazy_device_step(q, k_cache, v_cache, block_tables,
                                               context_lens, layer_idx, page_scores,
@@ -686,6 +697,7 @@ class CVSABackend:
         page_indices, n_per_head = self._cached_selection[layer_idx]
         accept_mask, _coverage = self._time_kernel(
             "coverage", ops.check_coverage, page_scores, page_indices, n_per_head, self.tau)
+        self._last_check[layer_idx] = (page_scores, accept_mask)
         accept_mask = self._apply_random_reject(accept_mask)
         n_acc = int(accept_mask.sum().item())
         self._h_per_head_accept_sum += n_acc

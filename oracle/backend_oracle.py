@@ -55,6 +55,17 @@ class OracleCVSABackend:
         self.adaptive_selection = adaptive_selection
         self.adaptive_floor_ratio = adaptive_floor_ratio
         self.acc_dtype = acc_dtype
+        # Optional test hooks (None: the reference behaviour).  A parity test
+        # that runs this oracle beside another implementation uses them to
+        # compare every selection and gate where it is made, and to adopt the
+        # other side's answer on heads whose fp64 and fp32 answers may
+        # legitimately differ (near ties), so both sides keep one state.
+        #   on_select(layer, ranked, idx, nph) -> (idx, nph)
+        #   on_gate(layer, where, gate_scores, idx, nph, accept, cov) -> accept
+        #     where: "check" (lazy check of the cached selection),
+        #     "coverage_only", or "new" (gate of a new selection).
+        self.on_select = None
+        self.on_gate = None
         self.reset()
 
     def reset(self):
@@ -167,6 +178,8 @@ class OracleCVSABackend:
         if layer_idx in self._cached_selection:
             idx, nph = self._cached_selection[layer_idx]
             accept, cov = ref.check_coverage(page_scores, idx, nph, self.tau, self.acc_dtype)
+            if self.on_gate is not None:
+                accept = self.on_gate(layer_idx, "check", page_scores, idx, nph, accept, cov)
             self._per_head_accept_sum += int(accept.sum())
             self._per_head_total += accept.numel()
             if bool(accept.all()):
@@ -185,6 +198,8 @@ class OracleCVSABackend:
         page_scores = self._cached_page_scores[layer_idx]
         idx, nph = self._cached_selection[layer_idx]
         accept, cov = ref.check_coverage(page_scores, idx, nph, self.tau, self.acc_dtype)
+        if self.on_gate is not None:
+            accept = self.on_gate(layer_idx, "coverage_only", page_scores, idx, nph, accept, cov)
         self._per_head_accept_sum += int(accept.sum())
         self._per_head_total += accept.numel()
         self._total_coverage_checks += 1
@@ -227,11 +242,15 @@ class OracleCVSABackend:
             budget = idx.shape[-1]
         else:
             idx, nph = ref.select_topk(sel_scores, budget, context_lens, self.block_size)
+        if self.on_select is not None:
+            idx, nph = self.on_select(layer_idx, sel_scores, idx, nph)
         o_d, m_d, l_d = ref.sparse_decode_unnorm(q, k_cache, v_cache, block_tables, idx, nph,
                                                  context_lens, self.num_kv_heads,
                                                  self.num_q_per_kv, self.block_size,
                                                  self.acc_dtype)
         accept, cov = ref.check_coverage(page_scores, idx, nph, self.tau, self.acc_dtype)
+        if self.on_gate is not None:
+            accept = self.on_gate(layer_idx, "new", page_scores, idx, nph, accept, cov)
         self._last_accept_mask[layer_idx] = accept
         recovery_pages = None
         if bool(accept.all()):                                                   # :775-779

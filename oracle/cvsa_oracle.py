@@ -21,6 +21,9 @@ C header):
     sort / topk leave them open (cvsa/backend.py:537-541, :567, :647, :672).
 
 How each function is pinned (tests/test_oracle_*.py unless noted):
+  * prepare_reuse_state, sparse_decode_reuse: closed form (padding with page
+    0 to a power of two) and invariance (a padded state decodes exactly as
+    the unpadded selection), test_oracle_closed_form;
   * score_pages, check_coverage, select_topk, sparse_decode(_unnorm),
     dense_decode, compute_complement, lse_merge, append_token_kv: the
     reference backend's golden traces (tests/golden/), the reference tests'
@@ -377,6 +380,31 @@ def sparse_decode(q, k_cache, v_cache, block_tables, page_indices, n_per_head, c
                                    n_per_head, context_lens, num_kv_heads, num_q_per_kv,
                                    block_size, acc_dtype)
     return normalise(o, l, q.dtype)
+
+
+def prepare_reuse_state(page_indices, n_per_head, num_kv_heads, B):
+    """cvsa/kernels/sparse_decode.py:664-678: the selection padded with page 0
+    to the next power of two of its width and flattened to [B * H_kv, padded],
+    n_per_head to [B * H_kv]; returns (pi_flat, nph_flat, padded)."""
+    k = page_indices.shape[2]
+    padded = next_power_of_2(k)
+    pi = torch.zeros(B, num_kv_heads, padded, dtype=torch.int32)
+    pi[:, :, :k] = page_indices.to(torch.int32)
+    return (pi.reshape(B * num_kv_heads, padded), n_per_head.to(torch.int32).reshape(-1),
+            padded)
+
+
+def sparse_decode_reuse(q, k_cache, v_cache, block_tables, context_lens, pi_flat, nph_flat,
+                        padded_max_selected, num_kv_heads, num_q_per_kv, block_size,
+                        acc_dtype=torch.float64):
+    """triton_sparse_decode_reuse (cvsa/kernels/sparse_decode.py:681-721): the
+    normalised sparse decode of a prepared state; each row's first
+    n_per_head entries are its pages (the padding is never read)."""
+    B = q.shape[0]
+    idx = pi_flat[:, :padded_max_selected].reshape(B, num_kv_heads, padded_max_selected)
+    nph = nph_flat.reshape(B, num_kv_heads)
+    return sparse_decode(q, k_cache, v_cache, block_tables, idx, nph, context_lens,
+                         num_kv_heads, num_q_per_kv, block_size, acc_dtype)
 
 
 def all_pages_selection(context_lens, block_tables, num_kv_heads, block_size):

@@ -1,11 +1,21 @@
-"""The multi-layer decode driver (cvsa.runtime.decode_driver): graph-replayed
-reuse steps are bit-identical to the eager per-layer protocol, step after
-step with appends and scoring steps in between (each replay is checked
-against the eager run), and leave the same schedule, statistics and tracing
-state."""
+"""The multi-layer decode driver (cvsa.runtime.decode_driver).
+
+* Against the oracle: the driver's per-layer protocol (append, backend call,
+  step_done for every layer of a step; eager and with graph-replayed reuse
+  steps) over several layers and steps gives the oracle backend's outputs,
+  selections, accept masks, complement pages and statistics, the oracle
+  running the same protocol on CPU copies of every layer's cache with the
+  reference's append rule.
+* Graph-replayed reuse steps are bit-identical to the eager per-layer
+  protocol, step after step with appends and scoring steps in between (each
+  replay is checked against the eager run), and leave the same schedule,
+  statistics and tracing state.
+"""
 import pytest
 import torch
 
+from oracle import cvsa_oracle as ref
+from oracle.backend_oracle import OracleCVSABackend
 from cvsa.backend import CVSABackend
 from cvsa.runtime.decode_driver import DecodeDriver, SyntheticDecodeLayers
 
@@ -14,6 +24,86 @@ pytestmark = pytest.mark.gpu
 SHAPE = dict(num_layers=4, batch=2, num_q_heads=32, num_kv_heads=8, head_dim=128,
              context_len=[3000, 1700], max_new_tokens=24, seed=5, hot_heads=[0, 3, 6],
              n_hot=6, hot_shift=10.0)
+
+
+class _OracleLayers:
+    """CPU copies of every layer's cache, table, lengths and allocator."""
+
+    def __init__(self, layers):
+        self.K = [c.k_cache.cpu() for c in layers.caches]
+        self.V = [c.v_cache.cpu() for c in layers.caches]
+        self.bt = [m.block_tables.cpu() for m in layers.managers]
+        self.ctx = [m.context_lens.cpu() for m in layers.managers]
+        self.alloc = [torch.tensor(m._pages_allocated, dtype=torch.int32)
+                      for m in layers.managers]
+        self.nf = [c._next_free for c in layers.caches]
+
+    def append(self, l, k, v):
+        for b in range(k.shape[0]):
+            self.nf[l] = ref.append_token_kv(self.K[l], self.V[l], self.bt[l], self.ctx[l],
+                                             self.alloc[l], self.nf[l], b, k[b], v[b], 16)
+
+
+ORACLE_SHAPE = dict(num_layers=3, batch=2, num_q_heads=32, num_kv_heads=8, head_dim=128,
+                    context_len=[2600, 1900], max_new_tokens=16, seed=11,
+                    hot_heads=[0, 2, 5, 7], n_hot=6, hot_shift=9.0)
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+@pytest.mark.parametrize("kw", [dict(lazy=True, check_interval=3),
+                                dict(lazy=False, reuse_interval=2)])
+def test_driver_matches_oracle_backend(gpu, graphs, kw):
+    """3 layers x 12 steps with one token appended per sequence per layer and
+    step: every layer's output, cached selection, accept mask and complement
+    pages after every step, and the final statistics, against the oracle
+    backend driven through the same protocol."""
+    L = ORACLE_SHAPE["num_layers"]
+    layers = SyntheticDecodeLayers(device=gpu, **ORACLE_SHAPE)
+    cfg = dict(num_kv_heads=8, num_q_heads=32, head_dim=128, block_size=16, num_layers=L,
+               budget_pct=0.2, coverage_threshold=0.9, **kw)
+    backend = CVSABackend(**cfg)
+    oracle = OracleCVSABackend(**cfg)
+    state = _OracleLayers(layers)
+    driver = DecodeDriver(backend, layers, graphs=graphs)
+    kinds = set()
+    for step in range(12):
+        q, k, v = layers.step_inputs(step)
+        outs = [o.float().cpu() for o in driver.step(q, k, v)]
+        qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+        for l in range(L):
+            state.append(l, kc[l], vc[l])
+            n_tr = len(oracle.trace)
+            want = oracle(qc[l], state.K[l], state.V[l], state.bt[l], state.ctx[l], l)
+            oracle.step_done(l, L)
+            kinds.update(t["kind"] for t in oracle.trace[n_tr:])
+            err = (outs[l] - want.float()).abs().max().item()
+            assert err < 2e-2, (step, l, err)
+            gs, os_ = backend._cached_selection[l], oracle._cached_selection[l]
+            assert torch.equal(gs[1].cpu(), os_[1]), (step, l)
+            for b in range(2):
+                for h in range(8):
+                    n = int(os_[1][b, h])
+                    assert torch.equal(gs[0][b, h, :n].cpu(), os_[0][b, h, :n]), (step, l, b, h)
+            ga, oa = backend._last_accept_mask.get(l), oracle._last_accept_mask.get(l)
+            assert (ga is None) == (oa is None), (step, l)
+            if ga is not None:
+                assert torch.equal(ga.cpu(), oa), (step, l)
+            ge = backend._last_expanded_selection.get(l)
+            oe = oracle._last_expanded_selection.get(l)
+            assert (ge is None) == (oe is None), (step, l)
+            if ge is not None:
+                assert torch.equal(ge[1].cpu(), oe[1]), (step, l)
+                for b in range(2):
+                    for h in range(8):
+                        n = int(oe[1][b, h])
+                        assert torch.equal(ge[0][b, h, :n].cpu(), oe[0][b, h, :n])
+        for l in range(L):
+            assert torch.equal(layers.managers[l].context_lens.cpu(), state.ctx[l])
+            assert torch.equal(layers.managers[l].block_tables.cpu(), state.bt[l])
+    assert backend.get_stats() == oracle.get_stats()
+    assert {"reuse"} < kinds and any(k.startswith("score") for k in kinds), kinds
+    if graphs:
+        assert driver.replays >= 1, driver.replays
 
 
 def _pair(gpu, kw):

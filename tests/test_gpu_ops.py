@@ -435,6 +435,44 @@ def test_decode_many_splits(gpu, ctx, budget):
         assert ((dlse - dwant_lse).abs() / dwant_lse.abs().clamp(min=1.0)).max().item() < LSE_RTOL
 
 
+def test_prepare_reuse_state_then_reuse_decode(gpu):
+    """prepare_reuse_state (sparse_decode.py:664-678) pads a width-100
+    selection to 128 with page 0; sparse_decode_reuse (:681-721) on that
+    state attends only each row's first n_per_head pages.  Some heads have
+    n_per_head below the budget (one is empty); both steps are compared with
+    the oracle (the state exactly, the output to the bf16 tolerance)."""
+    B, H, G = 2, 8, 4
+    inp = _inputs(440, B, 32, H, [4000, 2500], W=256)
+    q, K, V, bt, cl = _dev(inp, gpu)
+    ps = ref.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens, H, G, 16)
+    idx, nph = ref.select_topk(ps, 100, inp.context_lens, 16)
+    nph[0, 3] = 37
+    nph[1, 5] = 0
+    nph[1, 6] = 99
+    pi, n, padded = ops.prepare_reuse_state(idx.to(gpu), nph.to(gpu), H, B)
+    wpi, wn, wpadded = ref.prepare_reuse_state(idx, nph, H, B)
+    assert padded == wpadded == 128
+    assert torch.equal(pi.cpu(), wpi) and torch.equal(n.cpu(), wn)
+    out = ops.sparse_decode_reuse(q, K, V, bt, cl, pi, n, padded, H, G, 16).cpu()
+    want = ref.sparse_decode_reuse(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
+                                   inp.context_lens, wpi, wn, wpadded, H, G, 16)
+    assert out.dtype == torch.bfloat16
+    assert (out.float() - want.float()).abs().max().item() < OUT_ATOL
+    assert float(out[1, 5 * G:6 * G].float().abs().max()) == 0.0   # empty head
+
+
+def test_group_mean_matches_torch_gpu_mean(gpu):
+    """The reference forms q_rep with torch's mean on the GPU
+    (page_scores.py:94-95); the oracle's bf16(fp32 sum x fp32(1/G)) equals it
+    bit for bit for every group size, G = 7 included (torch's CPU mean
+    divides instead, and differs there)."""
+    g = torch.Generator().manual_seed(441)
+    for G in range(1, 9):
+        q = torch.randn(16, 8 * G, 128, generator=g).to(torch.bfloat16)
+        got = q.to(gpu).view(16, 8, G, 128).mean(dim=2).cpu()
+        assert torch.equal(ref.group_mean_bf16(q, 8, G), got), G
+
+
 def test_workspace_shared_across_head_counts(gpu):
     """Decode launches of different B * H_kv share one workspace on one
     stream: a split listed decode at B=1, H_kv=8, W=8192 (256 partial rows)

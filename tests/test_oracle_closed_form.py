@@ -65,6 +65,43 @@ def test_group_mean_matches_torch_mean_for_power_of_two_groups():
         assert torch.equal(a, b), G
 
 
+def test_prepare_reuse_state_pads_to_a_power_of_two_with_page_zero():
+    """sparse_decode.py:664-678: width 100 pads to 128 with page 0; a width
+    that is already a power of two is kept; rows flatten head-major."""
+    g = torch.Generator().manual_seed(11)
+    for k, want in ((100, 128), (128, 128), (3, 4), (1, 1)):
+        idx = torch.randint(1, 50, (2, 3, k), generator=g).to(torch.int32)
+        nph = torch.randint(0, k + 1, (2, 3), generator=g).to(torch.int32)
+        pi, n, padded = ref.prepare_reuse_state(idx, nph, 3, 2)
+        assert padded == want and pi.shape == (6, want) and pi.dtype == torch.int32
+        for b in range(2):
+            for h in range(3):
+                assert pi[b * 3 + h, :k].tolist() == idx[b, h].tolist()
+                assert pi[b * 3 + h, k:].tolist() == [0] * (want - k)
+                assert int(n[b * 3 + h]) == int(nph[b, h])
+
+
+def test_reuse_decode_of_padded_state_equals_unpadded_decode():
+    """The padding is never read: decoding a prepared state gives exactly the
+    decode of the unpadded selection, on rows with n_per_head below the
+    width, an empty row and a full row."""
+    inp = _tiny(seed=12, ctx=(90, 60), W=6)
+    idx = torch.tensor([[[5, 0, 2], [1, 3, 4]], [[2, 1, 0], [3, 0, 1]]], dtype=torch.int32)
+    nph = torch.tensor([[1, 3], [0, 2]], dtype=torch.int32)
+    want = ref.sparse_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_tables, idx, nph,
+                             inp.context_lens, 2, 4, 16)
+    pi, n, padded = ref.prepare_reuse_state(idx, nph, 2, 2)
+    assert padded == 4
+    got = ref.sparse_decode_reuse(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
+                                  inp.context_lens, pi, n, padded, 2, 4, 16)
+    assert torch.equal(got, want)
+    # a padded page would change the result if it were read
+    n_all = torch.full((4,), 4, dtype=torch.int32)
+    other = ref.sparse_decode_reuse(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
+                                    inp.context_lens, pi, n_all, padded, 2, 4, 16)
+    assert not torch.equal(other, want)
+
+
 def test_select_topk_brute_force_with_ties_and_invalid_pages():
     g = torch.Generator().manual_seed(5)
     B, H, W, bs = 3, 2, 40, 16
