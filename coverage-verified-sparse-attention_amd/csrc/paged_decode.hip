@@ -14,18 +14,24 @@
 // K/V page tile is fetched G times.  Here a workgroup owns one KV head and a
 // contiguous range of its page list; each of its four waves takes every
 // fourth page, loads the page's 16 K rows and 16 V rows once (256 B per row,
-// 16-byte lane loads) and applies them to all G query heads of the group.
-// Lane l holds d-segment (l % LPT) of token slot (l / LPT); the q.K dot is
-// finished with an LPT-lane DPP reduction, the page max with DPP and
-// permlane swaps, and P.V accumulates in registers.  The four waves merge in
-// LDS.  When a head's pages span several workgroups (splits), each stores its
-// partial (o, m, l) and bumps the head's completion counter; the last one to
-// arrive merges the partials and writes the outputs, so one launch does the
-// whole decode.  Partials move through agent-coherent accesses (relaxed
-// agent-scope atomic stores and loads, which bypass the per-XCD L2s) and the
-// counter increment is issued only after the stores have completed, so no
-// L2 writeback or invalidate is needed inside the kernel.  The last
-// workgroup resets the counter to zero for the next launch.
+// 16-byte lane loads) and applies them to all G query heads of the group as
+// two small matrix-core tiles (S = K Q^T, O += P V; see MfmaEngine).  The
+// four waves merge in LDS.  When a head's pages span several workgroups
+// (splits), each stores its partial (o, m, l) and bumps the head's
+// completion counter; the last one to arrive merges the partials and writes
+// the outputs, so one launch does the whole decode.  The last workgroup
+// resets the counter to zero for the next launch.
+//
+// Ordering of the split hand-off.  Partials are written and read through a
+// raw buffer resource with the sc1 cache policy: on gfx950 such stores are
+// written through the issuing XCD's L2 to the device coherence point and
+// such loads miss in the reading XCD's L2, so no L2 writeback or invalidate
+// (an agent-scope release / acquire fence) is needed.  A workgroup waits
+// for its partial stores to complete (s_waitcnt vmcnt(0) and a barrier)
+// before its relaxed agent-scope atomic increment of the head's counter; the
+// last arriver issues its partial loads only after that atomic has
+// returned.  This rests on the gfx950 cache policy described, not on the
+// HIP memory model's release / acquire pairing.
 //
 // Head modes: a listed head walks page_indices[b,h,:n_per_head]; an
 // all-pages head walks pages 0..n_valid-1 (dense decode).  In verified mode
@@ -34,7 +40,6 @@
 // merge of the draft and complement partial softmaxes.
 #include "cvsa_common.h"
 #include <hip/hip_fp16.h>
-#include <stdlib.h>
 
 #include <mutex>
 
@@ -319,142 +324,6 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBu
 // head and applies pages to it.  Page = the K and V rows of one page held in
 // registers (fetched PD pages ahead); consume() applies one page; finish()
 // leaves the wave's (o, m, l) in LDS.
-
-// VALU engine: lane l holds d-segment (l % LPT) of token slot (l / LPT);
-// q.K uses packed bf16 dot products with an LPT-lane DPP reduction, P.V is
-// fp32 FMA.  Lane vector v covers elements v*LPT*8 + seg*8 .. +8, so each
-// load instruction reads whole 128-byte lines of every row it touches.
-template <int G, int LPT>
-struct ValuEngine {
-  static constexpr int E = kHeadDim / LPT;      // d-elements per lane
-  static constexpr int NV = E / 8;              // 16-byte vectors per lane per row
-  static constexpr int VSTRIDE = LPT * 8;       // elements between a lane's vectors
-  static constexpr int TPP = kWave / LPT;       // token slots per pass
-  static constexpr int NPASS = kPageTokens / TPP;
-  static_assert(NPASS >= 1 && NV >= 1, "bad lane layout");
-  struct Page {
-    uint4 k[NPASS][NV], v[NPASS][NV];
-  };
-  struct Lds {};
-
-  float m[G], l[G], o[G][E];
-  uint4 qv[G][NV];
-  int tg, seg;
-  int64_t lane_off, row_stride;
-  float scale;
-
-  __device__ __forceinline__ void init(const DecodeArgs &a, int b, int h, int lane, Lds &) {
-    tg = lane / LPT;
-    seg = lane % LPT;
-    scale = a.scale;
-    row_stride = (int64_t)a.H_kv * kHeadDim;
-    lane_off = (int64_t)h * kHeadDim + seg * 8 + (int64_t)tg * row_stride;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      m[g] = -INFINITY;
-      l[g] = 0.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) o[g][e] = 0.f;
-#pragma unroll
-      for (int v = 0; v < NV; ++v)
-        qv[g][v] = *reinterpret_cast<const uint4 *>(
-            a.q + b * a.q_sb + (int64_t)(h * G + g) * a.q_sh + v * VSTRIDE + seg * 8);
-    }
-  }
-
-  __device__ __forceinline__ void fetch(const uint16_t *kp, const uint16_t *vp, Page &pg) const {
-#pragma unroll
-    for (int ps = 0; ps < NPASS; ++ps) {
-      const int64_t off = lane_off + (int64_t)(ps * TPP) * row_stride;
-#pragma unroll
-      for (int v = 0; v < NV; ++v)
-        pg.k[ps][v] = stream_load16(kp + off + v * VSTRIDE);
-#pragma unroll
-      for (int v = 0; v < NV; ++v)
-        pg.v[ps][v] = stream_load16(vp + off + v * VSTRIDE);
-    }
-  }
-
-  __device__ __forceinline__ void consume(Page &pg, int ntok, Lds &) {
-    float s[NPASS][G];
-#pragma unroll
-    for (int ps = 0; ps < NPASS; ++ps) {
-      const bool valid = ps * TPP + tg < ntok;
-      // Tokens past the context contribute nothing, whatever their V rows
-      // hold (the reference masks those loads); zeroed in place.
-#pragma unroll
-      for (int v = 0; v < NV; ++v)
-        if (!valid) pg.v[ps][v] = make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float acc = 0.f;
-#pragma unroll
-        for (int v = 0; v < NV; ++v) acc = dot8_bf16(pg.k[ps][v], qv[g][v], acc);
-        acc = group_sum<LPT>(acc) * scale;
-        s[ps][g] = valid ? acc : -INFINITY;
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float pm = s[0][g];
-#pragma unroll
-      for (int ps = 1; ps < NPASS; ++ps) pm = fmaxf(pm, s[ps][g]);
-      pm = wave_max_from_groups<LPT>(pm);
-      if (pm > m[g]) {  // wave-uniform
-        const float alpha = fast_exp(m[g] - pm);
-        l[g] *= alpha;
-#pragma unroll
-        for (int e = 0; e < E; ++e) o[g][e] *= alpha;
-        m[g] = pm;
-      }
-#pragma unroll
-      for (int ps = 0; ps < NPASS; ++ps) {
-        const bool valid = s[ps][g] != -INFINITY;
-        const float p = valid ? fast_exp(s[ps][g] - m[g]) : 0.f;
-        l[g] += p;
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-          const uint4 w = pg.v[ps][v];
-          o[g][v * 8 + 0] += p * bf16_lo(w.x);
-          o[g][v * 8 + 1] += p * bf16_hi(w.x);
-          o[g][v * 8 + 2] += p * bf16_lo(w.y);
-          o[g][v * 8 + 3] += p * bf16_hi(w.y);
-          o[g][v * 8 + 4] += p * bf16_lo(w.z);
-          o[g][v * 8 + 5] += p * bf16_hi(w.z);
-          o[g][v * 8 + 6] += p * bf16_lo(w.w);
-          o[g][v * 8 + 7] += p * bf16_hi(w.w);
-        }
-      }
-    }
-  }
-
-  template <int NW>
-  __device__ __forceinline__ void finish(int wave, int lane, float (*s_o)[G][kHeadDim],
-                                         float (*s_m)[G], float (*s_l)[G]) {
-    // Sum the token slots of the wave (lanes that share a d-segment).
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      l[g] = sum_across_groups<LPT>(l[g]);
-#pragma unroll
-      for (int e = 0; e < E; ++e) o[g][e] = sum_across_groups<LPT>(o[g][e]);
-    }
-    if (tg == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int v = 0; v < NV; ++v)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) s_o[wave][g][v * VSTRIDE + seg * 8 + e] = o[g][v * 8 + e];
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        s_m[wave][g] = m[g];
-        s_l[wave][g] = l[g];
-      }
-    }
-  }
-};
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -1032,27 +901,10 @@ __global__ void fill_zero_kernel(uint32_t *p, size_t n_words) {
     p[i] = 0u;
 }
 
-static int env_int(const char *name, int dflt) {
-  const char *e = getenv(name);
-  const int x = e ? atoi(e) : 0;
-  return x > 0 ? x : dflt;
-}
-
-// Page engine: 1 = matrix cores (MfmaEngine), 0 = VALU (ValuEngine);
-// CVSA_DECODE_ENGINE overrides the default (read once).
-static int decode_engine() {
-  static const int v = getenv("CVSA_DECODE_ENGINE") ? atoi(getenv("CVSA_DECODE_ENGINE")) : 1;
-  return v;
-}
-
 // Workgroups per launch, at most kMaxSplits (a head's partials are merged
-// in one workgroup's LDS); tuning knob CVSA_DECODE_TARGET_WGS, read once.
-static int target_workgroups() {
-  static const int v = env_int("CVSA_DECODE_TARGET_WGS", 256) < kMaxSplits
-                           ? env_int("CVSA_DECODE_TARGET_WGS", 256)
-                           : kMaxSplits;
-  return v;
-}
+// in one workgroup's LDS): one per CU of the 256-CU part.
+constexpr int kTargetWorkgroups = 256;
+static_assert(kTargetWorkgroups <= kMaxSplits, "one merge per head fits the merge LDS");
 constexpr int kWavesPerWg = 4;
 
 // Launch plan.  Listed launches (every head walks its page list) use the
@@ -1073,7 +925,7 @@ struct DecodeLaunch {
 static DecodeLaunch plan_launch(int B, int H_kv, int max_sel, int W, bool listed,
                                 bool all_pages) {
   const int64_t heads = (int64_t)B * H_kv;
-  const int target = target_workgroups();
+  const int target = kTargetWorkgroups;
   DecodeLaunch p{};
   if (listed && !all_pages) {
     int wg_per_head = heads >= target ? 1 : (int)(target / heads);
@@ -1119,13 +971,6 @@ static size_t workspace_bytes_for(int B, int H_q, int H_kv, int max_sel, int W, 
   if (p.partial_rows == 0) return 0;
   return kCounterAreaBytes + p.partial_rows * G * kPartStride * sizeof(float);
 }
-
-// Lanes per token row, chosen so that the o accumulators stay at <= 64
-// VGPRs for every group size.
-template <int G>
-struct LanesPerRow {
-  static constexpr int value = G <= 2 ? 4 : (G <= 4 ? 8 : 16);
-};
 
 // Argument checks of a decode launch (everything but the workspace) and its
 // launch plan; fills the launch-shape fields of `a`.  Returns a status.
@@ -1197,7 +1042,6 @@ static int enqueue_decode(const char *name, DecodeArgs a, int G, bool listed,
                      : reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) +
                                                  kCounterAreaBytes);
   a.part_bytes = need == 0 ? 0u : (uint32_t)(need - kCounterAreaBytes);
-  const bool use_mfma = decode_engine() == 1;
   const dim3 grid(p.grid_x, p.grid_y), block(kWavesPerWg * kWave);
 #define CVSA_DEC_LAUNCH(GG, ENG)                                                             \
   do {                                                                                       \
@@ -1212,12 +1056,9 @@ static int enqueue_decode(const char *name, DecodeArgs a, int G, bool listed,
                          block, 0, st, a);                                                   \
   } while (0)
 #define CVSA_DEC_CASE(GG)                                                                    \
-  case GG: {                                                                                 \
-    using EngM = MfmaEngine<GG>;                                                             \
-    using EngV = ValuEngine<GG, LanesPerRow<GG>::value>;                                     \
-    if (use_mfma) CVSA_DEC_LAUNCH(GG, EngM);                                                 \
-    else CVSA_DEC_LAUNCH(GG, EngV);                                                          \
-  } break;
+  case GG:                                                                                   \
+    CVSA_DEC_LAUNCH(GG, MfmaEngine<GG>);                                                     \
+    break;
   switch (G) {
     CVSA_DEC_CASE(1)
     CVSA_DEC_CASE(2)

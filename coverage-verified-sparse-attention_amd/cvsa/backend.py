@@ -177,6 +177,9 @@ class CVSABackend:
         # check or coverage-only step); views of live buffers, read them
         # before the layer's next call.
         self._last_check: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
+        # Ranking scores of a layer's new selection in its last call, when
+        # they differ from the gate's (the Quest selector with the exact gate).
+        self._last_rank_scores: Dict[int, torch.Tensor] = {}
         self._expanded_store: Dict[int, object] = {}
         self._attn_work: Optional[torch.Tensor] = None
         self._attn_work_max: Optional[torch.Tensor] = None
@@ -267,6 +270,7 @@ class CVSABackend:
         self._cached_page_scores = {}
         self._last_accept_mask = {}
         self._last_check = {}
+        self._last_rank_scores = {}
         self._expanded_store = {}
         if self._attn_work is not None:
             self._attn_work.zero_()
@@ -327,6 +331,7 @@ class CVSABackend:
         """backend.py:313-366"""
         self._last_accept_mask.pop(layer_idx, None)
         self._last_check.pop(layer_idx, None)
+        self._last_rank_scores.pop(layer_idx, None)
         self._expanded_store.pop(layer_idx, None)
 
         if layer_idx in self._dense_layers:
@@ -390,6 +395,7 @@ class CVSABackend:
         accept mask and expanded selection)."""
         self._last_accept_mask.pop(layer_idx, None)
         self._last_check.pop(layer_idx, None)
+        self._last_rank_scores.pop(layer_idx, None)
         self._expanded_store.pop(layer_idx, None)
 
     # ------------------------------------------------------------ accounting
@@ -625,6 +631,8 @@ class CVSABackend:
                                         ops.next_power_of_2(plan.budget))
         self._reuse_plans.pop(layer_idx, None)
         self._cached_selection[layer_idx] = (plan.page_indices, plan.n_per_head)
+        if plan.sel_scores is not None:
+            self._last_rank_scores[layer_idx] = plan.sel_scores
 
     def _lazy_plan(self, layer_idx, q, k_cache, v_cache, block_tables, context_lens):
         plan = self._matching_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens)
@@ -637,6 +645,8 @@ class CVSABackend:
 
     def _book_plan_gate(self, plan, layer_idx, context_lens):
         """Host-side bookkeeping of a plan's check or scoring step."""
+        if plan.sel_scores is not None:
+            self._last_rank_scores[layer_idx] = plan.sel_scores
         accept_mask = plan.accept.view(torch.bool)
         self._per_head_total += accept_mask.numel()
         self._last_accept_mask[layer_idx] = accept_mask
@@ -676,6 +686,8 @@ class CVSABackend:
         budget = page_indices.shape[2]
         self._per_head_total += check_accept.numel()
         sel_scores = self._sel_scores(q, k_cache, block_tables, context_lens, check_accept)
+        if sel_scores is not None:
+            self._last_rank_scores[layer_idx] = sel_scores
         accept_mask = self._time_kernel(
             "coverage", ops.select_or_keep, page_scores, check_accept, budget, context_lens,
             self.block_size, self.tau, page_indices, n_per_head, coverage,
@@ -735,6 +747,8 @@ class CVSABackend:
                                             block_tables, context_lens)
         self._cached_page_scores[layer_idx] = page_scores                         # :713
         sel_scores = self._sel_scores(q, k_cache, block_tables, context_lens)      # :723-727
+        if sel_scores is not None:
+            self._last_rank_scores[layer_idx] = sel_scores
 
         # Top-k selection fused with the coverage gate of the new selection.
         # In the fixed-interval schedule the gate's counters (:859-863) are

@@ -91,6 +91,22 @@ SCENARIOS = {
                     context_lens=[640], steps=7, hot_heads=[0, 1], n_hot=4, shift=9.0),
         backend=dict(budget_pct=0.25, coverage_threshold=0.77, lazy=True, check_interval=3,
                      coverage_interval=1)),
+    # cfg1 of BASELINE: 8B attention shapes, one sequence of 8192 tokens (512
+    # pages), budget 1/4, tau 0.9, exact recovery; a scoring step then a reuse
+    # step.  "cfg1": the literal recipe (+3 sigma hot pages on heads 0, 2, 4,
+    # 6: every head's coverage falls below tau and is recovered); "cfg1_mixed":
+    # +12 sigma, so the hot heads pass and the others are recovered.
+    "cfg1": dict(
+        inputs=dict(seed=1001, batch=1, num_q_heads=32, num_kv_heads=8, head_dim=128,
+                    context_lens=[8192], steps=2, hot_heads=[0, 2, 4, 6], n_hot=8, shift=3.0),
+        backend=dict(budget_pct=0.25, coverage_threshold=0.9, lazy=False, reuse_interval=2),
+        record_state=True),
+    "cfg1_mixed": dict(
+        inputs=dict(seed=1011, batch=1, num_q_heads=32, num_kv_heads=8, head_dim=128,
+                    context_lens=[8192], steps=2, hot_heads=[0, 2, 4, 6], n_hot=8,
+                    shift=12.0),
+        backend=dict(budget_pct=0.25, coverage_threshold=0.9, lazy=False, reuse_interval=2),
+        record_state=True),
     "approx_lazy": dict(
         inputs=dict(seed=1104, batch=1, num_q_heads=8, num_kv_heads=2, head_dim=128,
                     context_lens=[512], steps=5, hot_heads=[0, 1], n_hot=3, shift=8.0),

@@ -11,6 +11,11 @@ reference SequenceKVManager) and records, per call: the output bits, the
 accept mask, the cached selection (as sorted sets: torch.topk(sorted=False)
 leaves the order open), the expanded/complement selection, and the schedule
 counters; at the end get_stats(), the block tables and context lengths.
+Scenarios with ``record_state`` also keep, per scoring step, the coverage the
+reference's coverage kernel returned and the log-sum-exp of the merged
+result per query head (from the draft's and the complement's (m, l), as the
+reference's LSE merge combines them), captured by wrapping the kernel
+functions the reference backend calls.
 Outputs: backend_trace_<scenario>.npz (arrays) and backend_trace.json
 (stats, counters, input digests).  Nothing from the reference is stored
 except these numbers.
@@ -31,7 +36,8 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 from golden_inputs import SCENARIOS, input_digest, make_case  # noqa: E402
-from cvsa.backend import CVSABackend  # noqa: E402  (the reference package)
+import cvsa.backend as reference_backend  # noqa: E402  (the reference package)
+from cvsa.backend import CVSABackend  # noqa: E402
 from cvsa.runtime.kv_cache import PagedKVCache, SequenceKVManager  # noqa: E402
 
 
@@ -44,6 +50,51 @@ def sorted_rows(t, n):
             k = int(n[b, h])
             out[b, h, :k] = torch.sort(t[b, h, :k]).values
     return out.to(torch.int32).numpy()
+
+
+class _Capture:
+    """Wraps the reference backend's kernel entry points to keep what one
+    call computed: the coverage and the (m, l) of the draft and complement
+    sparse decodes."""
+
+    def __init__(self, module):
+        self.module = module
+        self.calls = {}
+        self.saved = {}
+        for name in ("triton_check_coverage", "triton_sparse_decode_unnorm"):
+            fn = getattr(module, name)
+            self.saved[name] = fn
+            setattr(module, name, self._wrap(name, fn))
+
+    def _wrap(self, name, fn):
+        def inner(*args, **kwargs):
+            out = fn(*args, **kwargs)
+            self.calls.setdefault(name, []).append(out)
+            return out
+        return inner
+
+    def take(self):
+        calls, self.calls = self.calls, {}
+        return calls
+
+    def restore(self):
+        for name, fn in self.saved.items():
+            setattr(self.module, name, fn)
+
+
+def merged_lse(decodes, accept, G):
+    """LSE per q-head: the draft's m + ln l on accepted heads, the
+    log-add of the draft's and the complement's on rejected ones."""
+    _, m_d, l_d = decodes[0]
+    lse = m_d + torch.log(l_d)
+    if len(decodes) > 1:
+        _, m_c, l_c = decodes[1]
+        lse_c = m_c + torch.log(l_c)
+        lse_c = torch.where(torch.isnan(lse_c), torch.full_like(lse_c, -float("inf")), lse_c)
+        both = torch.logaddexp(lse, lse_c)
+        rej = ~accept.repeat_interleave(G, dim=1)
+        lse = torch.where(rej, both, lse)
+    return lse.to(torch.float32).numpy()
 
 
 def run(name, sc):
@@ -61,11 +112,19 @@ def run(name, sc):
     mgr.context_lens.copy_(case.context_lens)
     mgr._pages_allocated = list(case.pages_allocated)
     backend = CVSABackend(H_kv, H_q, D, 16, **sc["backend"])
+    capture = _Capture(reference_backend) if sc.get("record_state") else None
     arrays, counters = {}, []
     for s in range(inp["steps"]):
         out = backend(case.q[s], cache.k_cache, cache.v_cache, mgr.block_tables,
                       mgr.context_lens, 0)
         arrays[f"out_{s}"] = out.contiguous().view(torch.int16).numpy()
+        if capture is not None:
+            calls = capture.take()
+            if "triton_check_coverage" in calls:
+                acc, cov = calls["triton_check_coverage"][-1]
+                arrays[f"cov_{s}"] = cov.to(torch.float32).numpy()
+                arrays[f"lse_{s}"] = merged_lse(calls["triton_sparse_decode_unnorm"], acc,
+                                                H_q // H_kv)
         acc = backend._last_accept_mask.get(0)
         if acc is not None:
             arrays[f"accept_{s}"] = acc.to(torch.uint8).numpy()
@@ -85,6 +144,8 @@ def run(name, sc):
         backend.step_done(0, 1)
         for b in range(B):
             mgr.append_token_kv(b, case.k_new[s][b], case.v_new[s][b])
+    if capture is not None:
+        capture.restore()
     arrays["block_tables"] = mgr.block_tables.numpy()
     arrays["context_lens"] = mgr.context_lens.numpy()
     np.savez_compressed(os.path.join(HERE, f"backend_trace_{name}.npz"), **arrays)
@@ -93,11 +154,18 @@ def run(name, sc):
 
 
 def main():
+    """Regenerates every scenario, or only those named on the command line
+    (the others keep their recorded entries)."""
+    path = os.path.join(HERE, "backend_trace.json")
     meta = {}
-    for name, sc in SCENARIOS.items():
-        meta[name] = run(name, sc)
+    if os.path.exists(path):
+        with open(path) as f:
+            meta = json.load(f)
+    names = sys.argv[1:] or list(SCENARIOS)
+    for name in names:
+        meta[name] = run(name, SCENARIOS[name])
         print(name, meta[name]["stats"], flush=True)
-    with open(os.path.join(HERE, "backend_trace.json"), "w") as f:
+    with open(path, "w") as f:
         json.dump(meta, f, indent=1, sort_keys=True)
 
 

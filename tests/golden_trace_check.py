@@ -35,9 +35,15 @@ def _sorted_sets(idx, n):
     return out.to(torch.int32).numpy()
 
 
-def replay(name, make_backend, make_runtime, counters_of):
+COV_ATOL = 1e-3      # coverage (BASELINE north-star tolerance)
+LSE_RTOL = 1e-3      # log-sum-exp of the merged result, relative
+
+
+def replay(name, make_backend, make_runtime, counters_of, state_of=None):
     """make_backend(kwargs) -> backend; make_runtime(case) -> (call_args_fn,
-    append_fn, state_fn); counters_of(backend) -> dict like the recorded one."""
+    append_fn, state_fn); counters_of(backend) -> dict like the recorded one.
+    state_of(backend, call_args) -> (coverage [B, H_kv], lse [B, H_q]) of the
+    backend's last scoring step, for scenarios that recorded them."""
     sc = SCENARIOS[name]
     meta, arr = load(name)
     case = make_case(**sc["inputs"])
@@ -66,6 +72,13 @@ def replay(name, make_backend, make_runtime, counters_of):
             assert np.array_equal(en.cpu().to(torch.int32).numpy(), arr[f"expn_{s}"]), (name, s)
             assert np.array_equal(_sorted_sets(ei, en), arr[f"exp_{s}"]), (name, s, "expanded")
         assert counters_of(backend) == meta["counters"][s], (name, s, "counters")
+        if state_of is not None and f"cov_{s}" in arr:
+            cov, lse = state_of(backend, call_args(case.q[s]))
+            want_cov = torch.from_numpy(arr[f"cov_{s}"])
+            want_lse = torch.from_numpy(arr[f"lse_{s}"])
+            assert (cov.cpu().float() - want_cov).abs().max().item() < COV_ATOL, (name, s)
+            rel = ((lse.cpu().float() - want_lse).abs() / want_lse.abs().clamp(min=1.0))
+            assert rel.max().item() < LSE_RTOL, (name, s, "lse")
         backend.step_done(0, 1)
         for b in range(inp["batch"]):
             append(b, case.k_new[s][b], case.v_new[s][b])

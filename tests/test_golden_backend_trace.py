@@ -36,6 +36,22 @@ def _counters(b):
                 accepts=b._accept_counts, rejects=b._reject_counts)
 
 
+def _oracle_state(b, args):
+    """Coverage of the last selection on its gate scores, and the merged
+    result's LSE per q-head: the draft's on accepted heads, attention over
+    every valid page (draft + complement) on rejected heads."""
+    q, K, V, bt, ctx = args
+    idx, nph = b._cached_selection[0]
+    _, cov = ref.check_coverage(b._cached_page_scores[0], idx, nph, b.tau)
+    acc = b._last_accept_mask[0]
+    H, G = b.num_kv_heads, b.num_q_per_kv
+    _, md, ld = ref.sparse_decode_unnorm(q, K, V, bt, idx, nph, ctx, H, G, 16)
+    _, (_, ma, la) = ref.dense_decode(q, K, V, bt, ctx, H, G, 16, return_state=True)
+    rej = ~acc.repeat_interleave(G, dim=1)
+    lse = torch.where(rej, ma + torch.log(la), md + torch.log(ld))
+    return cov, lse
+
+
 @pytest.mark.parametrize("name", sorted(SCENARIOS))
 def test_oracle_matches_reference_trace(name):
-    replay(name, _oracle_backend, _oracle_runtime, _counters)
+    replay(name, _oracle_backend, _oracle_runtime, _counters, _oracle_state)

@@ -132,10 +132,8 @@ class _Lockstep:
             pi, nph = b._cached_selection[layer]
             g["idx"], g["nph"] = _cpu(pi), _cpu(nph)
             g["gate"] = _cpu(b._cached_page_scores[layer])
-            ranked = g["gate"]
-            if self.kw.get("selector") == "quest" and not self.kw.get("light_normalizer"):
-                ranked = _cpu(b._step_plans[layer].sel_scores)
-            g["ranked"] = ranked
+            rank = b._last_rank_scores.get(layer)
+            g["ranked"] = g["gate"] if rank is None else _cpu(rank)
         self.g = g
 
     # ------------------------------------------------------------ helpers

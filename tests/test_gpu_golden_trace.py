@@ -1,7 +1,9 @@
 """The HIP path against the reference implementation's recorded multi-step
 behaviour (golden traces written by tests/golden/make_backend_trace.py):
 outputs, accept masks, selected / complement / expanded page sets, schedule
-counters, statistics and the paged-KV append state."""
+counters, statistics and the paged-KV append state; for the two cfg1-shaped
+traces (8B attention, one 8192-token sequence) also the coverage and the
+merged result's log-sum-exp of the scoring step."""
 import pytest
 import torch
 
@@ -45,8 +47,22 @@ def _counters(b):
                 accepts=b._accept_counts, rejects=b._reject_counts)
 
 
+def _hip_state(b, args):
+    """Coverage of the last selection on its gate scores and the merged
+    result's LSE per q-head, through the HIP ops (the verified decode's
+    (m, l): draft pages on accepted heads, every valid page on rejected)."""
+    from cvsa import ops
+    q, K, V, bt, ctx = args
+    idx, nph = b._cached_selection[0]
+    _, cov = ops.check_coverage(b._cached_page_scores[0], idx, nph, b.tau)
+    acc = b._last_accept_mask[0]
+    _, (_, m, l) = ops.verified_decode(q, K, V, bt, ctx, idx, nph, acc, b.num_kv_heads,
+                                       b.num_q_per_kv, 16, return_state=True)
+    return cov, m + torch.log(l)
+
+
 @pytest.mark.parametrize("name", sorted(SCENARIOS))
 def test_hip_backend_matches_reference_trace(gpu, name):
     replay(name, lambda inp, kw: CVSABackend(inp["num_kv_heads"], inp["num_q_heads"],
                                              inp["head_dim"], 16, **kw),
-           _runtime(gpu), _counters)
+           _runtime(gpu), _counters, _hip_state)

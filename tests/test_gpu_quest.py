@@ -147,5 +147,5 @@ CFG = dict(batch=2, num_q_heads=32, num_kv_heads=8, head_dim=128, context_len=[6
 ])
 def test_backend_quest_schedules(gpu, kw):
     kw = dict(budget_pct=0.25, coverage_threshold=0.9, **kw)
-    stats, trace = _run(gpu, CFG, kw, steps=8, seed=4242)
+    stats, trace, _ = _run(gpu, CFG, kw, steps=8, seed=4242)
     assert any(t["kind"].startswith("score") for t in trace)

@@ -221,5 +221,5 @@ CFG = dict(batch=2, num_q_heads=32, num_kv_heads=8, head_dim=128, context_len=[5
 ])
 def test_backend_budgeted_schedules(gpu, kw):
     kw = dict(budget_pct=0.2, **kw)
-    stats, trace = _run(gpu, CFG, kw, steps=7, seed=777)
+    stats, trace, _ = _run(gpu, CFG, kw, steps=7, seed=777)
     assert any(t["kind"].startswith("score") for t in trace)
