@@ -1,0 +1,40 @@
+// Entry points internal to libcvsa_hip.so (not exported): a step plan's
+// lazy check with its speculative decode (page scoring fused with the decode
+// of the cached selection, the select-or-keep that records its decision,
+// and the verified decode that skips what the speculation wrote).
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+namespace cvsa_internal {
+
+// H_kv for which score_and_speculate has a fused launch (4, 8, 16).
+bool score_spec_fusable(int32_t H_kv);
+
+int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
+                        const uint16_t *k_cache, const uint16_t *v_cache, int64_t num_blocks,
+                        const int32_t *block_tables, int64_t bt_stride_b,
+                        const int32_t *context_lens, const int32_t *page_indices,
+                        int64_t idx_stride, const int32_t *n_per_head, int32_t max_selected,
+                        int32_t B, int32_t H_q, int32_t H_kv, int32_t D, int32_t block_size,
+                        int32_t W, float *page_scores, void *out, int32_t out_dtype,
+                        int32_t *spec_state, void *workspace, size_t workspace_bytes,
+                        void *stream);
+
+int verified_decode_after_speculation(
+    const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t *k_cache,
+    const uint16_t *v_cache, int64_t num_blocks, const int32_t *block_tables,
+    int64_t bt_stride_b, const int32_t *context_lens, const int32_t *page_indices,
+    int64_t idx_stride, const int32_t *n_per_head, int32_t max_selected, const uint8_t *accept,
+    int32_t B, int32_t H_q, int32_t H_kv, int32_t D, int32_t block_size, int32_t W, void *out,
+    int32_t out_dtype, int64_t *work, int32_t *spec_state, void *workspace,
+    size_t workspace_bytes, void *stream);
+
+int select_or_keep_flag(const float *page_scores, const float *sel_scores,
+                        const uint8_t *check_accept, int32_t B, int32_t H_kv, int32_t W,
+                        const int32_t *context_lens, int32_t block_size, int32_t budget,
+                        int32_t *page_indices, int32_t *n_per_head, float tau,
+                        uint8_t *accept_out, float *coverage_out, float *scores_cache,
+                        int64_t *stats, int32_t *keep_flag, void *stream);
+
+}  // namespace cvsa_internal

@@ -39,6 +39,8 @@
 // draft pages plus the complement pages in one pass, which equals the LSE
 // merge of the draft and complement partial softmaxes.
 #include "cvsa_common.h"
+#include "internal.h"
+#include "score_body.h"
 #include <hip/hip_fp16.h>
 
 #include <mutex>
@@ -68,7 +70,8 @@ struct DecodeArgs {
   const uint8_t *accept;  // non-NULL: verified mode
   int H_kv, W;
   int heads;  // B * H_kv
-  int pps, n_splits;  // listed kernel: pages per split, splits per head
+  int pps, n_splits;  // listed partition: pages per split, splits per head
+  int sk_grid;        // stream-K partition: workgroups (<= kMaxSplits)
   float scale;
   float *o_unnorm, *m_out, *l_out;
   void *out;
@@ -77,6 +80,10 @@ struct DecodeArgs {
   uint32_t part_bytes;
   unsigned *counters;        // per head, zero between launches
   unsigned long long *work;  // optional effective-budget counters
+  // A lazy check's speculative decode of its kept selection (or NULL):
+  // [0] != 0 predicts that the check keeps its selection, [1] records
+  // whether the speculative listed decode ran (and wrote the outputs).
+  int32_t *spec_state;
 };
 
 __device__ __forceinline__ void store_out(void *out, int dtype, int64_t i, float y) {
@@ -559,51 +566,63 @@ __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const Part
   }
 }
 
-// Listed pages of every head (the sparse decode of reuse steps): a static
-// grid of (split, head) workgroups, split s of head h walking listed pages
-// [s * pps, (s + 1) * pps) of h; splits past a head's pages only take part
-// when the head is empty (split 0 writes its outputs).  No scan, so the first
-// page-list and block-table entries are requested at entry.  Partial row of
+// LDS of a workgroup's page walk and epilogue: the waves' (o, m, l), the
+// last-arriver flag, and the engines' LDS, which is dead once a walk ends and
+// is reused by the merge.
+template <int G, class Engine, int NW>
+struct WalkLds {
+  union Tail {
+    typename Engine::Lds eng[NW];
+    MergeLds<G, NW * kWave> merge;
+  };
+  float o[NW][G][kHeadDim] __attribute__((aligned(16)));
+  float m[NW][G];
+  float l[NW][G];
+  int last;
+  Tail tail __attribute__((aligned(16)));
+};
+
+// The first page-list entries of split `split` of head bh (lane j of wave
+// w: entry r0 + w + NW j) and their block-table entries, requested as early
+// as possible: their position only needs r0 = split * pps.  Lanes past the
+// head's pages are discarded by the walk.
+template <int NW>
+__device__ __forceinline__ void listed_first_pages(const DecodeArgs &a, int split, int bh,
+                                                   int wave, int lane, int &lp, int &phys) {
+  lp = 0;
+  phys = 0;
+  if (a.max_sel > 0) {
+    const int b = bh / a.H_kv;
+    lp = a.page_idx[(int64_t)bh * a.idx_stride + min(split * a.pps + wave + NW * lane,
+                                                     a.max_sel - 1)];
+    phys = a.block_tables[b * a.bt_sb + min(max(lp, 0), a.W - 1)];
+  }
+}
+
+// Listed pages of a head (the sparse decode of reuse steps, and verified
+// launches whose heads are all accepted): split s of head bh walks listed
+// pages [s * pps, (s + 1) * pps) of bh; splits past a head's pages only take
+// part when the head is empty (split 0 writes its outputs).  Partial row of
 // (split, head) = head * n_splits + split.
 template <int G, class Engine, int NW, int PD>
-__global__ __launch_bounds__(NW * kWave) void listed_decode_kernel(const DecodeArgs a) {
-  constexpr int NT = NW * kWave;
+__device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int bh, int spec_lp,
+                                            int spec_phys, WalkLds<G, Engine, NW> &L) {
   using Page = typename Engine::Page;
-  union TailLds {
-    typename Engine::Lds eng[NW];
-    MergeLds<G, NT> merge;
-  };
-  __shared__ __attribute__((aligned(16))) float s_o[NW][G][kHeadDim];
-  __shared__ float s_m[NW][G];
-  __shared__ float s_l[NW][G];
-  __shared__ int s_last;
-  __shared__ __attribute__((aligned(16))) TailLds s_tail;
-
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int bh = blockIdx.y;
-  const int split = blockIdx.x;
   const int b = bh / a.H_kv;
   const int h = bh - b * a.H_kv;
   const int ctx = __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
   const int pps = a.pps;
   const int r0 = split * pps;
   const int32_t *idx_row = a.page_idx + (int64_t)bh * a.idx_stride;
-  // The first page-list entries of the split (their position only needs
-  // r0) and then their block-table entries are requested together with the
-  // head's page count: lanes past the head's pages are discarded later.
-  int spec_lp = 0, spec_phys = 0;
-  if (a.max_sel > 0) {
-    spec_lp = idx_row[min(r0 + wave + NW * lane, a.max_sel - 1)];
-    spec_phys = a.block_tables[b * a.bt_sb + min(max(spec_lp, 0), a.W - 1)];
-  }
   const int n = min(max(__builtin_amdgcn_readfirstlane(a.n_pages[bh]), 0), a.max_sel);
   const int r1 = min(n, r0 + pps);
   const int n_act = (n + pps - 1) / pps;  // splits holding pages of this head
   if (r0 >= r1 && !(split == 0 && n_act == 0)) return;  // uniform
 
   Engine eng;
-  eng.init(a, b, h, lane, s_eng_of(s_tail.eng, wave));
+  eng.init(a, b, h, lane, s_eng_of(L.tail.eng, wave));
   const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * kHeadDim;  // between blocks
   const int npw = max(0, (r1 - r0 - wave + NW - 1) / NW);
   for (int c0 = 0; c0 < npw; c0 += kWave) {
@@ -638,15 +657,87 @@ __global__ __launch_bounds__(NW * kWave) void listed_decode_kernel(const DecodeA
       for (int u = 0; u < PD; ++u) {
         const int slot = (u + PD - 1) % PD;  // slot of page j+u+PD-1
         nt[slot] = fetch(min(j + u + PD - 1, cn - 1), pbuf[slot]);
-        if (j + u >= 0 && j + u < cn) eng.consume(pbuf[u], nt[u], s_eng_of(s_tail.eng, wave));
+        if (j + u >= 0 && j + u < cn) eng.consume(pbuf[u], nt[u], s_eng_of(L.tail.eng, wave));
       }
     }
   }
-  eng.template finish<NW>(wave, lane, s_o, s_m, s_l);
+  eng.template finish<NW>(wave, lane, L.o, L.m, L.l);
   __syncthreads();
   const PartBuf pb(a.part, a.part_bytes);
   segment_epilogue<G, NW>(a, pb, bh, n, ctx, n_act, (uint32_t)(bh * a.n_splits + split),
-                          (uint32_t)(bh * a.n_splits), s_o, s_m, s_l, s_last, s_tail.merge);
+                          (uint32_t)(bh * a.n_splits), L.o, L.m, L.l, L.last, L.tail.merge);
+}
+
+// The listed decode: a static grid of (split, head) workgroups.
+template <int G, class Engine, int NW, int PD>
+__global__ __launch_bounds__(NW * kWave) void listed_decode_kernel(const DecodeArgs a) {
+  __shared__ WalkLds<G, Engine, NW> L;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int lp, phys;
+  listed_first_pages<NW>(a, blockIdx.x, blockIdx.y, wave, lane, lp, phys);
+  listed_walk<G, Engine, NW, PD>(a, blockIdx.x, blockIdx.y, lp, phys, L);
+}
+
+// Pages per scoring wave of the fused launch below.
+constexpr int kSpecScorePPW = 8;
+
+// A lazy check's page scoring and the speculative listed decode of its
+// cached selection in one launch.  Workgroups [0, n_splits * heads) are the
+// listed decode's (split, head) workgroups, w -> (w % n_splits, w /
+// n_splits), bit for bit listed_decode_kernel; they run only if
+// spec_state[0] predicts that the check keeps its selection, and workgroup 0
+// records in spec_state[1] whether they ran.  The other workgroups score
+// pages as score_pages_quad_kernel does (score_body.h; kSpecScorePPW pages
+// per wave, workgroup x of sequence b at index n_dec + b * score_gx + x).
+// The parts share no memory: the decode reads the cached selection, which
+// only the check's select-or-keep, launched after this kernel, rewrites.
+// One launch lets the decode's dependent metadata loads and split hand-off
+// overlap the scoring stream without a second stream and its events.
+template <int G, class Engine, int NW, int PD>
+__global__ __launch_bounds__(NW * kWave) void score_spec_kernel(const DecodeArgs a,
+                                                                const ScoreArgs s,
+                                                                int score_gx) {
+  static_assert(NW == 4, "the scoring part runs four waves per workgroup");
+  __shared__ WalkLds<G, Engine, NW> L;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n_dec = a.n_splits * a.heads;
+  const int w = blockIdx.x;
+  if (w >= n_dec) {  // uniform
+    const int sw = w - n_dec;
+    score_quad_wave<kSpecScorePPW>(s, a.H_kv, (sw % score_gx) * NW + wave, sw / score_gx);
+    return;
+  }
+  const int split = w % a.n_splits;
+  const int bh = w / a.n_splits;
+  int lp, phys;
+  listed_first_pages<NW>(a, split, bh, wave, lane, lp, phys);
+  const int go = __builtin_amdgcn_readfirstlane(a.spec_state[0]);
+  if (w == 0 && threadIdx.x == 0) a.spec_state[1] = go;
+  if (go == 0) return;  // uniform
+  listed_walk<G, Engine, NW, PD>(a, split, bh, lp, phys, L);
+}
+
+// Effective-budget counters of a verified launch whose heads were all
+// accepted and whose outputs a speculative listed decode already wrote:
+// what the listed walks would have added, summed by one workgroup.
+template <int NT>
+__device__ __forceinline__ void add_listed_work(const DecodeArgs &a, unsigned long long *red) {
+  unsigned long long n = 0, nv = 0;
+  for (int bh = threadIdx.x; bh < a.heads; bh += NT) {
+    n += (unsigned long long)min(max(a.n_pages[bh], 0), a.max_sel);
+    nv += (unsigned long long)max(0, n_valid_pages(a.ctx_lens[bh / a.H_kv], kPageTokens));
+  }
+  if (threadIdx.x == 0) red[0] = red[1] = 0ull;
+  __syncthreads();
+  if (n) atomicAdd(&red[0], n);
+  if (nv) atomicAdd(&red[1], nv);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    atomicAdd(&a.work[0], red[0]);
+    atomicAdd(&a.work[1], red[1]);
+  }
 }
 
 // NW waves per workgroup, PD pages of K/V in flight per wave.
@@ -666,19 +757,16 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   static_assert(NW == 4, "kMinPagesPerWg assumes four waves");
   using Page = typename Engine::Page;
 
-  // The engines' LDS is dead once a page loop ends; the merge reuses it.
-  union TailLds {
-    typename Engine::Lds eng[NW];
-    MergeLds<G, NT> merge;
-  };
-  __shared__ __attribute__((aligned(16))) float s_o[NW][G][kHeadDim];
-  __shared__ float s_m[NW][G];
-  __shared__ float s_l[NW][G];
-  __shared__ int s_last;
+  __shared__ WalkLds<G, Engine, NW> L;
   __shared__ int s_wsum[NW];
   __shared__ int s_start[kMaxHeads + 1];  // exclusive prefix of pages per head
   __shared__ uint8_t s_listed[kMaxHeads];
-  __shared__ __attribute__((aligned(16))) TailLds s_tail;
+  __shared__ unsigned long long s_work[2];
+  auto &s_o = L.o;
+  auto &s_m = L.m;
+  auto &s_l = L.l;
+  auto &s_last = L.last;
+  auto &s_tail = L.tail;
   auto &s_eng = s_tail.eng;
 
   const int lane = threadIdx.x & 63;
@@ -686,6 +774,38 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   const int w = blockIdx.x;
   const int heads = a.heads;
   const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * kHeadDim;  // between blocks
+
+  // Verified launches whose heads are all accepted (a lazy check that keeps
+  // its selection, or a scoring step whose gate passes everywhere) run the
+  // listed decode's static partition: workgroup w takes split w % n_splits
+  // of head w / n_splits, exactly as listed_decode_kernel, so the outputs
+  // are bit for bit those of the listed decode.  Its first page lookups are
+  // requested together with the accept flags.  When the check kept its
+  // selection (spec_state[0], written by the check's select-or-keep) and a
+  // speculative listed decode of that selection already wrote the outputs
+  // (spec_state[1]), only the effective-budget counters are booked.  Every
+  // head accepted does not imply a kept selection: a rejected head is
+  // reselected and accepted when the new selection passes its gate.
+  if constexpr (MODE == kModeVerified) {
+    const int n_listed = a.n_splits * heads;
+    const int split = w % max(a.n_splits, 1);
+    const int bh = min(w / max(a.n_splits, 1), heads - 1);
+    int lp, phys;
+    listed_first_pages<NW>(a, split, bh, wave, lane, lp, phys);
+    int spec_done = 0;
+    if (a.spec_state != nullptr)
+      spec_done = __builtin_amdgcn_readfirstlane(a.spec_state[0] & a.spec_state[1]);
+    int rejected = 0;
+    for (int i = threadIdx.x; i < heads; i += NT) rejected |= a.accept[i] == 0;
+    if (__syncthreads_or(rejected) == 0) {  // uniform
+      if (spec_done != 0) {
+        if (w == 0 && a.work != nullptr) add_listed_work<NT>(a, s_work);
+        return;
+      }
+      if (w < n_listed) listed_walk<G, Engine, NW, PD>(a, split, bh, lp, phys, L);
+      return;
+    }
+  }
 
   // Speculative page lookups for the common case in which every head walks
   // max_sel listed pages: the range start is then known without the scan.
@@ -699,7 +819,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   // compiler never has to drain them at a join.
   Engine eng;
   const int T_spec = heads * a.max_sel;
-  const Partition spec_part(T_spec, gridDim.x);
+  const Partition spec_part(T_spec, a.sk_grid);
   int spec_lp = 0, spec_phys = 0, h_spec = -1, r_spec = 0, ctx_spec = 0, g1_spec = 0;
   int b_spec = 0, h_c = 0;  // clamped speculated head and its sequence
   if constexpr (MODE != kModeAll) {
@@ -829,8 +949,8 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   T = __builtin_amdgcn_readfirstlane(T);
 
   const bool spec_ok = T == T_spec && h_spec >= 0;  // every head walks max_sel pages
-  const Partition part = spec_ok ? spec_part : Partition(max(T, 1), gridDim.x);
-  const int n_wg = T > 0 ? part.n : (int)gridDim.x;
+  const Partition part = spec_ok ? spec_part : Partition(max(T, 1), a.sk_grid);
+  const int n_wg = T > 0 ? part.n : a.sk_grid;
   if (w >= n_wg) return;  // uniform
 
   // Heads without pages: (o, m, l) = (0, -inf, 0), zero output.
@@ -918,7 +1038,8 @@ constexpr int kWavesPerWg = 4;
 struct DecodeLaunch {
   bool streamk;
   int grid_x, grid_y;
-  int pps, n_splits;    // listed grid
+  int pps, n_splits;    // listed partition
+  int sk_grid;          // stream-K partition (<= kMaxSplits workgroups)
   size_t partial_rows;  // rows of G x kPartStride fp32 (0: no workspace)
 };
 
@@ -948,9 +1069,20 @@ static DecodeLaunch plan_launch(int B, int H_kv, int max_sel, int W, bool listed
   if (g > target) g = target;
   if (g < 1) g = 1;
   p.streamk = true;
+  p.sk_grid = (int)g;
   p.grid_x = (int)g;
   p.grid_y = 1;
   p.partial_rows = g > 1 ? (size_t)g + heads : 0;  // row w + h: workgroup w's partial of head h
+  if (listed) {
+    // Verified launches also carry the listed partition, which they run
+    // when every head is accepted: at least one workgroup per (split, head).
+    const DecodeLaunch lp = plan_launch(B, H_kv, max_sel, W, true, false);
+    p.pps = lp.pps;
+    p.n_splits = lp.n_splits;
+    const int64_t n_listed = (int64_t)lp.grid_x * lp.grid_y;
+    if (n_listed > p.grid_x) p.grid_x = (int)n_listed;
+    if (lp.partial_rows > p.partial_rows) p.partial_rows = lp.partial_rows;
+  }
   return p;
 }
 
@@ -1030,18 +1162,23 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   a.heads = B * H_kv;
   a.pps = p.pps;
   a.n_splits = p.n_splits;
+  a.sk_grid = p.sk_grid;
   a.scale = (float)pow((double)D, -0.5);
   return CVSA_OK;
 }
 
 // Enqueue a validated launch with its workspace (need bytes, 0 = none).
-static int enqueue_decode(const char *name, DecodeArgs a, int G, bool listed,
-                          const DecodeLaunch &p, void *workspace, size_t need, hipStream_t st) {
+static void bind_workspace(DecodeArgs &a, void *workspace, size_t need) {
   a.counters = reinterpret_cast<unsigned *>(workspace);
   a.part = need == 0 ? nullptr
                      : reinterpret_cast<float *>(reinterpret_cast<char *>(workspace) +
                                                  kCounterAreaBytes);
   a.part_bytes = need == 0 ? 0u : (uint32_t)(need - kCounterAreaBytes);
+}
+
+static int enqueue_decode(const char *name, DecodeArgs a, int G, bool listed,
+                          const DecodeLaunch &p, void *workspace, size_t need, hipStream_t st) {
+  bind_workspace(a, workspace, need);
   const dim3 grid(p.grid_x, p.grid_y), block(kWavesPerWg * kWave);
 #define CVSA_DEC_LAUNCH(GG, ENG)                                                             \
   do {                                                                                       \
@@ -1076,19 +1213,24 @@ static int enqueue_decode(const char *name, DecodeArgs a, int G, bool listed,
   return cvsa_host::check_launch(name);
 }
 
-static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_kv, int D,
-                         int block_size, int W, bool listed, bool all_pages,
-                         void *workspace, size_t workspace_bytes, hipStream_t st) {
-  DecodeLaunch p{};
-  size_t need = 0;
-  const int rc = validate_decode(name, a, B, H_q, H_kv, D, block_size, W, listed, all_pages, p,
-                                 need);
-  if (rc != CVSA_OK) return rc;
+static int check_workspace(const char *name, void *workspace, size_t workspace_bytes,
+                           size_t need) {
   CVSA_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need &&
                                 ((uintptr_t)workspace & 255) == 0),
                CVSA_ERR_WORKSPACE,
                "%s: workspace of %zu bytes (256-byte aligned) required, got %zu", name,
                need, workspace_bytes);
+  return CVSA_OK;
+}
+
+static int launch_decode(const char *name, DecodeArgs a, int B, int H_q, int H_kv, int D,
+                         int block_size, int W, bool listed, bool all_pages,
+                         void *workspace, size_t workspace_bytes, hipStream_t st) {
+  DecodeLaunch p{};
+  size_t need = 0;
+  int rc = validate_decode(name, a, B, H_q, H_kv, D, block_size, W, listed, all_pages, p, need);
+  if (rc != CVSA_OK) return rc;
+  if ((rc = check_workspace(name, workspace, workspace_bytes, need)) != CVSA_OK) return rc;
   return enqueue_decode(name, a, H_q / H_kv, listed, p, workspace, need, st);
 }
 
@@ -1256,6 +1398,101 @@ extern "C" int cvsa_sparse_decode_noalloc(
   }
   return enqueue_decode(name, a, H_q / H_kv, true, p, ws, need, (hipStream_t)stream);
 }
+
+namespace cvsa_internal {
+
+bool score_spec_fusable(int32_t H_kv) { return H_kv >= 4 && H_kv % 4 == 0 && H_kv <= 16; }
+
+// A lazy check's page scoring (cvsa_score_pages into page_scores) fused
+// with the speculative decode of its cached selection (cvsa_sparse_decode
+// into out, run only if spec_state[0] predicts that the check keeps the
+// selection; spec_state[1] records whether it ran).  Effective-budget
+// counters are left to the verified decode.  H_kv must be 4, 8 or 16.
+int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
+                        const uint16_t *k_cache, const uint16_t *v_cache, int64_t num_blocks,
+                        const int32_t *block_tables, int64_t bt_stride_b,
+                        const int32_t *context_lens, const int32_t *page_indices,
+                        int64_t idx_stride, const int32_t *n_per_head, int32_t max_selected,
+                        int32_t B, int32_t H_q, int32_t H_kv, int32_t D, int32_t block_size,
+                        int32_t W, float *page_scores, void *out, int32_t out_dtype,
+                        int32_t *spec_state, void *workspace, size_t workspace_bytes,
+                        void *stream) {
+  const char *name = "score_pages + speculative decode";
+  DecodeArgs a = base_args(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                           block_tables, bt_stride_b, context_lens, nullptr, nullptr, nullptr,
+                           out, out_dtype, nullptr);
+  a.page_idx = page_indices;
+  a.idx_stride = idx_stride;
+  a.max_sel = max_selected;
+  a.n_pages = n_per_head;
+  a.spec_state = spec_state;
+  CVSA_REQUIRE(page_indices && spec_state && page_scores, CVSA_ERR_INVALID,
+               "%s: page_indices, spec_state and page_scores are required", name);
+  CVSA_REQUIRE(score_spec_fusable(H_kv), CVSA_ERR_UNSUPPORTED, "%s: H_kv=%d not in {4,8,16}",
+               name, H_kv);
+  DecodeLaunch p{};
+  size_t need = 0;
+  int rc = validate_decode(name, a, B, H_q, H_kv, D, block_size, W, true, false, p, need);
+  if (rc != CVSA_OK) return rc;
+  if ((rc = check_workspace(name, workspace, workspace_bytes, need)) != CVSA_OK) return rc;
+  bind_workspace(a, workspace, need);
+  const int G = H_q / H_kv;
+  const ScoreArgs sa{q, q_stride_b, q_stride_h, k_cache, num_blocks, block_tables,
+                     bt_stride_b, context_lens, page_scores, W, G, 1.0f / (float)G, a.scale};
+  const int64_t waves = (int64_t)((W + kSpecScorePPW - 1) / kSpecScorePPW) * (H_kv / 4);
+  const int score_gx = (int)((waves + kWavesPerWg - 1) / kWavesPerWg);
+  const int64_t grid = (int64_t)p.grid_x * p.grid_y + (int64_t)score_gx * B;
+  hipStream_t st = (hipStream_t)stream;
+#define CVSA_SPEC_CASE(GG)                                                                   \
+  case GG:                                                                                   \
+    hipLaunchKernelGGL((score_spec_kernel<GG, MfmaEngine<GG>, kWavesPerWg, 2>),             \
+                       dim3((unsigned)grid), dim3(kWavesPerWg * kWave), 0, st, a, sa,        \
+                       score_gx);                                                            \
+    break;
+  switch (G) {
+    CVSA_SPEC_CASE(1)
+    CVSA_SPEC_CASE(2)
+    CVSA_SPEC_CASE(3)
+    CVSA_SPEC_CASE(4)
+    CVSA_SPEC_CASE(5)
+    CVSA_SPEC_CASE(6)
+    CVSA_SPEC_CASE(7)
+    CVSA_SPEC_CASE(8)
+    default:
+      break;
+  }
+#undef CVSA_SPEC_CASE
+  return cvsa_host::check_launch(name);
+}
+
+// cvsa_verified_decode after score_and_speculate and the check's
+// select-or-keep: when the check kept its selection (spec_state[0]) and the
+// speculative decode wrote the outputs (spec_state[1]), the launch only
+// books the effective-budget counters.
+int verified_decode_after_speculation(
+    const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t *k_cache,
+    const uint16_t *v_cache, int64_t num_blocks, const int32_t *block_tables,
+    int64_t bt_stride_b, const int32_t *context_lens, const int32_t *page_indices,
+    int64_t idx_stride, const int32_t *n_per_head, int32_t max_selected, const uint8_t *accept,
+    int32_t B, int32_t H_q, int32_t H_kv, int32_t D, int32_t block_size, int32_t W, void *out,
+    int32_t out_dtype, int64_t *work, int32_t *spec_state, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  DecodeArgs a = base_args(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                           block_tables, bt_stride_b, context_lens, nullptr, nullptr, nullptr,
+                           out, out_dtype, work);
+  a.page_idx = page_indices;
+  a.idx_stride = idx_stride;
+  a.max_sel = max_selected;
+  a.n_pages = n_per_head;
+  a.accept = accept;
+  a.spec_state = spec_state;
+  CVSA_REQUIRE(page_indices && accept && spec_state, CVSA_ERR_INVALID,
+               "verified decode: page_indices, accept and spec_state are required");
+  return launch_decode("verified_decode", a, B, H_q, H_kv, D, block_size, W, true, true,
+                       workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+}  // namespace cvsa_internal
 
 extern "C" int cvsa_dense_decode(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
                                  const uint16_t *k_cache, const uint16_t *v_cache,

@@ -1,0 +1,97 @@
+// Page scoring of one wave in the quad layout (H_kv a multiple of 4), shared
+// by the scoring kernel and the lazy check's fused scoring + speculative
+// decode launch.
+//
+// page_scores[b,h,p] = max over valid tokens of (q_rep . K) * D^-0.5, as
+// triton_score_pages (cvsa/kernels/page_scores.py:77-119, kernel :12-74):
+// q_rep is the bf16-rounded GQA group mean of q (:94-95), the dot is
+// accumulated in fp32 and scaled after the sum (:67), masked tokens are -inf
+// (:68) and pages starting at or beyond the context are -inf (:44-47).
+// A page's score does not depend on which wave computes it, so launches with
+// different pages per wave write the same bits.
+#pragma once
+#include "cvsa_common.h"
+
+namespace cvsa {
+
+struct ScoreArgs {
+  const uint16_t *q;
+  int64_t q_sb, q_sh;
+  const uint16_t *k_cache;
+  int64_t num_blocks;
+  const int32_t *block_tables;
+  int64_t bt_sb;
+  const int32_t *context_lens;
+  float *scores;
+  int W, G;
+  float inv_g, scale;
+};
+
+// Wave gw of sequence b owns KV-head quad hq = gw % (hkv / 4) of pages
+// [(gw / (hkv / 4)) * PPW, +PPW).  For each token of a page, the quad's four
+// 256-byte rows are contiguous (1 KiB), so one 16-byte load per lane reads
+// them whole: lane l holds head 4*hq + (l >> 4), d-segment (l & 15) * 8.  The
+// 16 lanes of a DPP row finish the dot product with four fused DPP adds, and
+// each lane keeps the running max of its head.  The wave's block-table
+// entries are fetched once (lane j: page j) and the next page's keys are
+// requested before the current page is reduced.  hkv is a compile-time
+// constant where the caller's is.
+template <int PPW>
+__device__ __forceinline__ void score_quad_wave(const ScoreArgs &s, int hkv, int gw, int b) {
+  const int nq = hkv / 4;  // quads per page
+  const int lane = threadIdx.x & 63;
+  const int hq = gw % nq;
+  const int p_begin = (gw / nq) * PPW;
+  const int W = s.W;
+  if (p_begin >= W) return;
+  const int h = 4 * hq + (lane >> 4);
+  const int seg = lane & 15;
+  const int ctx = __builtin_amdgcn_readfirstlane(s.context_lens[b]);
+  const int n = min(PPW, W - p_begin);
+
+  // Page j of this wave: block id in lane j (-1 when the page holds no
+  // valid token or the id is outside the pool).
+  int my_phys = -1;
+  if (lane < n) {
+    const int p = p_begin + lane;
+    if (p * kPageTokens < ctx) {
+      const int id = s.block_tables[b * s.bt_sb + p];
+      if (id >= 0 && id < s.num_blocks) my_phys = id;
+    }
+  }
+  const uint4 qr = group_mean_q(s.q, s.q_sb, s.q_sh, b, h, s.G, seg, s.inv_g);
+  const int64_t lane_off = (int64_t)hq * 4 * kHeadDim + lane * 8;
+  const int64_t row_stride = (int64_t)hkv * kHeadDim;
+  const int64_t page_elems = kPageTokens * row_stride;
+
+  // Unconditional loads (block 0 for pages without valid tokens) keep the
+  // prefetch free of branches.
+  auto fetch = [&](int j, uint4 (&kv)[kPageTokens]) {
+    const int phys = max(__builtin_amdgcn_readlane(my_phys, j), 0);
+    const uint16_t *src = s.k_cache + (int64_t)phys * page_elems + lane_off;
+#pragma unroll
+    for (int t = 0; t < kPageTokens; ++t) kv[t] = stream_load16(src + t * row_stride);
+  };
+  auto consume = [&](int j, const uint4 (&kv)[kPageTokens]) {
+    const int p = p_begin + j;
+    const int ntok = __builtin_amdgcn_readlane(my_phys, j) < 0
+                         ? 0
+                         : min(kPageTokens, ctx - p * kPageTokens);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < kPageTokens; ++t) {
+      const float sc = group_sum<16>(dot8_bf16(kv[t], qr, 0.f)) * s.scale;
+      if (t < ntok) mx = fmaxf(mx, sc);
+    }
+    if (seg == 0) s.scores[((int64_t)b * hkv + h) * W + p] = mx;
+  };
+  uint4 buf[2][kPageTokens];
+  fetch(0, buf[0]);
+#pragma unroll
+  for (int j = 0; j < PPW; ++j) {
+    if (j + 1 < PPW) fetch(min(j + 1, n - 1), buf[(j + 1) & 1]);
+    if (j < n) consume(j, buf[j & 1]);
+  }
+}
+
+}  // namespace cvsa

@@ -12,79 +12,16 @@
 // a DPP row hold one (token, head) row and reduce its dot product with four
 // fused DPP adds.
 #include "cvsa_common.h"
+#include "score_body.h"
 
 namespace cvsa {
 
-// H_kv >= 4: a wave owns four KV heads ("quad" hq) of PPW pages.  For each
-// token of a page, the quad's four 256-byte rows are contiguous (1 KiB), so
-// one 16-byte load per lane reads them whole: lane l holds head 4*hq + (l >> 4),
-// d-segment (l & 15) * 8.  The 16 lanes of a DPP row finish the dot product
-// with four fused DPP adds, and each lane keeps the running max of its head.
-// The wave's block-table entries are fetched once (lane j: page j) and the
-// next page's keys are requested before the current page is reduced.
+// H_kv >= 4: a wave owns four KV heads ("quad") of PPW pages (score_body.h).
 template <int HKV, int PPW>
-__global__ __launch_bounds__(256) void score_pages_quad_kernel(
-    const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh,
-    const uint16_t *__restrict__ k_cache, int64_t num_blocks,
-    const int32_t *__restrict__ block_tables, int64_t bt_sb,
-    const int32_t *__restrict__ context_lens, float *__restrict__ scores, int W, int G,
-    float inv_g, float scale) {
+__global__ __launch_bounds__(256) void score_pages_quad_kernel(const ScoreArgs s) {
   static_assert(HKV >= 4 && HKV % 4 == 0, "quad layout");
-  constexpr int NQ = HKV / 4;  // quads per page
-  const int lane = threadIdx.x & 63;
-  const int gw = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int hq = gw % NQ;
-  const int p_begin = (gw / NQ) * PPW;
-  const int b = blockIdx.y;
-  if (p_begin >= W) return;
-  const int h = 4 * hq + (lane >> 4);
-  const int seg = lane & 15;
-  const int ctx = __builtin_amdgcn_readfirstlane(context_lens[b]);
-  const int n = min(PPW, W - p_begin);
-
-  // Page j of this wave: block id in lane j (-1 when the page holds no
-  // valid token or the id is outside the pool).
-  int my_phys = -1;
-  if (lane < n) {
-    const int p = p_begin + lane;
-    if (p * kPageTokens < ctx) {
-      const int id = block_tables[b * bt_sb + p];
-      if (id >= 0 && id < num_blocks) my_phys = id;
-    }
-  }
-  const uint4 qr = group_mean_q(q, q_sb, q_sh, b, h, G, seg, inv_g);
-  const int64_t lane_off = (int64_t)hq * 4 * kHeadDim + lane * 8;
-  const int64_t row_stride = (int64_t)HKV * kHeadDim;
-  const int64_t page_elems = kPageTokens * row_stride;
-
-  // Unconditional loads (block 0 for pages without valid tokens) keep the
-  // prefetch free of branches.
-  auto fetch = [&](int j, uint4 (&kv)[kPageTokens]) {
-    const int phys = max(__builtin_amdgcn_readlane(my_phys, j), 0);
-    const uint16_t *src = k_cache + (int64_t)phys * page_elems + lane_off;
-#pragma unroll
-    for (int t = 0; t < kPageTokens; ++t) kv[t] = stream_load16(src + t * row_stride);
-  };
-  auto consume = [&](int j, const uint4 (&kv)[kPageTokens]) {
-    const int p = p_begin + j;
-    const int ntok = __builtin_amdgcn_readlane(my_phys, j) < 0
-                         ? 0
-                         : min(kPageTokens, ctx - p * kPageTokens);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < kPageTokens; ++t) {
-      const float s = group_sum<16>(dot8_bf16(kv[t], qr, 0.f)) * scale;
-      if (t < ntok) mx = fmaxf(mx, s);
-    }
-    if (seg == 0) scores[((int64_t)b * HKV + h) * W + p] = mx;
-  };
-  uint4 buf[2][kPageTokens];
-  fetch(0, buf[0]);
-#pragma unroll
-  for (int j = 0; j < PPW; ++j) {
-    if (j + 1 < PPW) fetch(min(j + 1, n - 1), buf[(j + 1) & 1]);
-    if (j < n) consume(j, buf[j & 1]);
-  }
+  score_quad_wave<PPW>(s, HKV, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+                       blockIdx.y);
 }
 
 // H_kv < 4: one wave streams a whole page; lane l covers row (l >> 4) of
@@ -192,12 +129,11 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
     while (ppw < 8 && quad_pages / (2 * ppw) >= 2048) ppw *= 2;
     const int64_t waves = ((W + ppw - 1) / ppw) * (int64_t)(H_kv / 4);
     dim3 grid((unsigned)((waves + 3) / 4), B);
+    const ScoreArgs sa{q, q_stride_b, q_stride_h, k_cache, (int64_t)num_blocks, block_tables,
+                       bt_stride_b, context_lens, page_scores, W, G, inv_g, scale};
 #define CVSA_QUAD_CASE(HK, PP)                                                          \
   if (H_kv == HK && ppw == PP) {                                                        \
-    hipLaunchKernelGGL((score_pages_quad_kernel<HK, PP>), grid, dim3(256), 0, st, q,    \
-                       q_stride_b, q_stride_h, k_cache, (int64_t)num_blocks,            \
-                       block_tables, bt_stride_b, context_lens, page_scores, W, G,      \
-                       inv_g, scale);                                                   \
+    hipLaunchKernelGGL((score_pages_quad_kernel<HK, PP>), grid, dim3(256), 0, st, sa);  \
     return cvsa_host::check_launch("score_pages");                                      \
   }
     CVSA_QUAD_CASE(4, 1) CVSA_QUAD_CASE(4, 2) CVSA_QUAD_CASE(4, 4) CVSA_QUAD_CASE(4, 8)

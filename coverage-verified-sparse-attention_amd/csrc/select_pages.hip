@@ -31,6 +31,7 @@
 // never waits for earlier global stores, and loads are issued as early as
 // the step that needs them allows.
 #include "cvsa_common.h"
+#include "internal.h"
 
 namespace cvsa {
 
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
     uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
     const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
-    long long *__restrict__ stats, int count_gate) {
+    long long *__restrict__ stats, int count_gate, int32_t *__restrict__ keep_flag) {
   __shared__ uint32_t hist[256];
   __shared__ uint32_t hist_c[kHistCopies * kHistStride];
   __shared__ uint32_t hist_b[kBuckets];
@@ -326,6 +327,9 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
       stat_add(&stats[2], all_ok ? 0 : 1);
       stat_add(&stats[3], s_nok);
     }
+    // The decision, for the next check's speculative decode (a step plan's
+    // prediction that the check keeps its selection).
+    if (keep_flag != nullptr && bh == 0 && t == 0) *keep_flag = all_ok ? 1 : 0;
     if (all_ok) {
       if (t == 0) accept_out[bh] = 1;
       return;
@@ -967,7 +971,7 @@ static int launch_select(const char *name, const float *page_scores, const float
                          uint8_t *accept_out, float *coverage_out, const uint8_t *check_accept,
                          float *scores_cache, int64_t *stats, int count_gate,
                          void *stream, int mode = kUniform, float top_p = 0.f,
-                         const int32_t *row_budgets = nullptr) {
+                         const int32_t *row_budgets = nullptr, int32_t *keep_flag = nullptr) {
   CVSA_REQUIRE(page_scores && context_lens && page_indices && n_per_head, CVSA_ERR_INVALID,
                "%s: null pointer argument", name);
   CVSA_REQUIRE((accept_out == nullptr) == (coverage_out == nullptr), CVSA_ERR_INVALID,
@@ -993,7 +997,8 @@ static int launch_select(const char *name, const float *page_scores, const float
   hipLaunchKernelGGL((select_topk_kernel<RR, SEP, MODE>), grid, dim3(kSelThreads), 0, st,   \
                      page_scores, sel_scores, W, H_kv, context_lens, block_size, budget,    \
                      width, top_p, row_budgets, page_indices, n_per_head, tau, accept_out,  \
-                     coverage_out, check_accept, B * H_kv, scores_cache, st64, count_gate)
+                     coverage_out, check_accept, B * H_kv, scores_cache, st64, count_gate,    \
+                     keep_flag)
 #define CVSA_SEL_MODES(RR, SEP)                                    \
   if (mode == kTopP) CVSA_SEL_LAUNCH(RR, SEP, kTopP);              \
   else if (mode == kTable) CVSA_SEL_LAUNCH(RR, SEP, kTable);       \
@@ -1049,6 +1054,27 @@ extern "C" int cvsa_select_or_keep(const float *page_scores, const float *sel_sc
                        block_size, budget, page_indices, n_per_head, tau, accept_out,
                        coverage_out, check_accept, scores_cache, stats, count_gate, stream);
 }
+
+namespace cvsa_internal {
+
+// cvsa_select_or_keep that also writes its keep decision to *keep_flag (1:
+// every head passed the check and the selection stayed, 0: reselected) --
+// the prediction a step plan's next lazy check speculates on.
+int select_or_keep_flag(const float *page_scores, const float *sel_scores,
+                        const uint8_t *check_accept, int32_t B, int32_t H_kv, int32_t W,
+                        const int32_t *context_lens, int32_t block_size, int32_t budget,
+                        int32_t *page_indices, int32_t *n_per_head, float tau,
+                        uint8_t *accept_out, float *coverage_out, float *scores_cache,
+                        int64_t *stats, int32_t *keep_flag, void *stream) {
+  CVSA_REQUIRE(accept_out && coverage_out && check_accept, CVSA_ERR_INVALID,
+               "select_or_keep: accept_out, coverage_out and check_accept are required");
+  return launch_select("select_or_keep", page_scores, sel_scores, B, H_kv, W, context_lens,
+                       block_size, budget, page_indices, n_per_head, tau, accept_out,
+                       coverage_out, check_accept, scores_cache, stats, 0, stream, kUniform,
+                       0.f, nullptr, keep_flag);
+}
+
+}  // namespace cvsa_internal
 
 extern "C" int cvsa_select_budgeted(const float *page_scores, const float *sel_scores,
                                     int32_t B, int32_t H_kv, int32_t W,

@@ -10,6 +10,7 @@
 #include <stdint.h>
 
 #include "../../include/cvsa_hip.h"
+#include "internal.h"
 
 namespace cvsa_host {
 int fail(int code, const char *fmt, ...);
@@ -146,7 +147,52 @@ extern "C" int cvsa_step_plan_create(const cvsa_step_desc *desc, cvsa_step_plan 
   return CVSA_OK;
 }
 
-extern "C" void cvsa_step_plan_destroy(cvsa_step_plan *plan) { delete plan; }
+extern "C" void cvsa_step_plan_destroy(cvsa_step_plan *plan) {
+  if (plan == nullptr) return;
+  delete plan;
+}
+
+namespace {
+
+// Whether a lazy check of this plan speculates: spec_state given, gate
+// scores from the exact scan, and a fused scoring + decode launch for H_kv.
+bool speculates(const cvsa_step_desc &d) {
+  return d.spec_state != nullptr && d.selector != CVSA_SELECT_QUEST_LN &&
+         cvsa_internal::score_spec_fusable(d.H_kv);
+}
+
+// The lazy check with the speculative decode: one launch scores the pages
+// and decodes the cached selection (if spec_state[0] predicts a keep), then
+// the check, the select-or-keep that records its decision in spec_state[0],
+// and the verified decode, which only books counters when the selection was
+// kept and the speculative decode ran.
+int speculative_check(const cvsa_step_desc &d, const uint16_t *q, void *out, void *stream) {
+  int rc;
+  if ((rc = cvsa_internal::score_and_speculate(
+           q, d.q_stride_b, d.q_stride_h, d.k_cache, d.v_cache, d.num_blocks, d.block_tables,
+           d.bt_stride_b, d.context_lens, d.page_indices, d.budget, d.n_per_head, d.budget, d.B,
+           d.H_q, d.H_kv, d.D, d.block_size, d.W, d.page_scores, out, d.out_dtype,
+           d.spec_state, d.workspace, d.workspace_bytes, stream)) != CVSA_OK)
+    return rc;
+  if ((rc = cvsa_check_coverage(d.page_scores, d.B, d.H_kv, d.W, d.page_indices, d.budget,
+                                d.n_per_head, d.tau, d.check_accept, d.coverage, stream)) !=
+      CVSA_OK)
+    return rc;
+  if ((rc = rank(d, q, d.check_accept, stream)) != CVSA_OK) return rc;
+  const float *sel = d.selector == CVSA_SELECT_QUEST ? d.sel_scores : nullptr;
+  if ((rc = cvsa_internal::select_or_keep_flag(
+           d.page_scores, sel, d.check_accept, d.B, d.H_kv, d.W, d.context_lens, d.block_size,
+           d.budget, d.page_indices, d.n_per_head, d.tau, d.accept, d.coverage, d.scores_cache,
+           d.stats, d.spec_state, stream)) != CVSA_OK)
+    return rc;
+  return cvsa_internal::verified_decode_after_speculation(
+      q, d.q_stride_b, d.q_stride_h, d.k_cache, d.v_cache, d.num_blocks, d.block_tables,
+      d.bt_stride_b, d.context_lens, d.page_indices, d.budget, d.n_per_head, d.budget, d.accept,
+      d.B, d.H_q, d.H_kv, d.D, d.block_size, d.W, out, d.out_dtype, d.work, d.spec_state,
+      d.workspace, d.workspace_bytes, stream);
+}
+
+}  // namespace
 
 extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint16_t *q,
                                   void *out, void *stream) {
@@ -166,6 +212,7 @@ extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint
                                 d.H_kv, d.D, d.block_size, d.W, nullptr, nullptr, nullptr, out,
                                 d.out_dtype, d.work, d.workspace, d.workspace_bytes, stream);
     case CVSA_STEP_LAZY_CHECK:
+      if (speculates(d)) return speculative_check(d, q, out, stream);
       if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
       if ((rc = cvsa_check_coverage(d.page_scores, d.B, d.H_kv, d.W, d.page_indices, d.budget,
                                     d.n_per_head, d.tau, d.check_accept, d.coverage,

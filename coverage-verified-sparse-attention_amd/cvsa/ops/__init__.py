@@ -637,17 +637,22 @@ class StepPlan:
     SELECT_QUEST_LN ranks and gates by the Quest scores.
     ``matches`` tells whether a call's buffers, query layout and stream are
     the ones the plan was built for.
+    With ``speculate`` (default) a lazy check decodes the cached selection
+    in the same launch as the page scoring, and the verified decode skips
+    its work when the check kept that selection (see
+    cvsa_step_desc.spec_state; exact gate scores and H_kv in 4, 8, 16 only);
+    results are bit-identical either way.
     """
 
     __slots__ = ("dev", "stream", "q_meta", "out_shape", "out_dtype", "refs", "page_indices",
                  "n_per_head", "page_scores", "scores_cache", "check_accept", "accept",
-                 "coverage", "budget", "owns_selection", "selector", "sel_scores", "_h", "_run",
-                 "_fin", "__weakref__")
+                 "coverage", "budget", "owns_selection", "selector", "sel_scores", "spec_state",
+                 "_h", "_run", "_fin", "__weakref__")
 
     def __init__(self, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
                  num_q_per_kv, block_size, budget, tau, page_indices=None, n_per_head=None,
                  scores_cache=None, stats=None, work=None, own_scores_cache=False,
-                 selector=_lib.SELECT_EXACT, quest=None):
+                 selector=_lib.SELECT_EXACT, quest=None, speculate=True):
         dev = _device_of(q, k_cache, v_cache, block_tables, context_lens, page_indices,
                          n_per_head, scores_cache, stats, work)
         if selector not in (_lib.SELECT_EXACT, _lib.SELECT_QUEST, _lib.SELECT_QUEST_LN):
@@ -701,6 +706,10 @@ class StepPlan:
         self.selector = selector
         self.sel_scores = (torch.empty(B, H, W, dtype=torch.float32, device=dev)
                            if selector == _lib.SELECT_QUEST else None)
+        # [0]: the previous check kept its selection (predicted for the first
+        # check), [1]: the speculative decode ran.
+        self.spec_state = (torch.tensor([1, 0], dtype=torch.int32, device=dev)
+                           if speculate else None)
         d = _lib.StepDesc(
             B=B, H_q=H_q, H_kv=H, D=D, block_size=block_size, W=W, budget=budget,
             tau=float(tau), out_dtype=_DTYPE_CODE[q.dtype], q_stride_b=q.stride(0),
@@ -713,7 +722,7 @@ class StepPlan:
             coverage=self.coverage.data_ptr(), stats=_ptr(stats), work=_ptr(work),
             selector=selector, quest_meta=None if quest is None else quest.meta.data_ptr(),
             quest_ntok=None if quest is None else quest.ntok.data_ptr(),
-            sel_scores=_ptr(self.sel_scores))
+            sel_scores=_ptr(self.sel_scores), spec_state=_ptr(self.spec_state))
         L = _lib.load()
         ws = _workspace(dev, L.cvsa_step_workspace_bytes(ctypes.byref(d)))
         d.workspace = _ptr(ws)

@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parents[1] / "libcvsa_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 CVSA_OK = 0
 CVSA_ERR_INVALID = -1
@@ -50,6 +50,7 @@ class StepDesc(ctypes.Structure):
         ("check_accept", _p), ("accept", _p), ("coverage", _p), ("stats", _p), ("work", _p),
         ("workspace", _p), ("workspace_bytes", _sz),
         ("selector", _i32), ("quest_meta", _p), ("quest_ntok", _p), ("sel_scores", _p),
+        ("spec_state", _p),
     ]
 
 

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 8
+#define CVSA_ABI_VERSION 9
 
 enum {
   CVSA_OK = 0,
@@ -442,6 +442,8 @@ typedef struct cvsa_step_desc {
   uint16_t *quest_meta;        /* Quest selectors: metadata of k_cache, as for */
   int32_t *quest_ntok;         /*   cvsa_quest_refresh_scores (else NULL) */
   float *sel_scores;           /* CVSA_SELECT_QUEST: [B, H_kv, W] ranking scores (else NULL) */
+  int32_t *spec_state;         /* int32[2] or NULL: speculative lazy checks (below); [0] is
+                                  initialised to 1, [1] to 0 */
 } cvsa_step_desc;
 
 /* Page scorers of a plan (CVSABackend selector / light_normalizer,
@@ -453,6 +455,20 @@ enum {
   CVSA_SELECT_QUEST_LN = 2   /* Quest scores rank and gate (light_normalizer) */
 };
 
+/*
+ * Speculative lazy checks (spec_state non-NULL).  A lazy check that keeps
+ * its selection outputs the sparse decode of that selection, which does not
+ * depend on the step's new page scores.  The plan then decodes the cached
+ * selection in the same launch as the page scoring (the decode's latency
+ * hides under the scoring stream), and the verified decode only books the
+ * effective-budget counters when the check kept the selection.  Whether to
+ * speculate is predicted from the previous check of the same plan
+ * (spec_state[0], written by the selection kernel); a wrong prediction costs
+ * time, never results: the outputs, selections, masks and counters equal
+ * those of the sequential chain bit for bit.  Plans whose gate scores are
+ * Quest scores (CVSA_SELECT_QUEST_LN) or whose H_kv is 1 or 2 run the
+ * sequential chain and leave spec_state unchanged.
+ */
 enum {
   CVSA_STEP_REUSE = 0,      /* sparse decode of the kept selection */
   CVSA_STEP_LAZY_CHECK = 1, /* score, check, keep or reselect, verified decode */

@@ -15,10 +15,10 @@ pytestmark = pytest.mark.gpu
 H, G = 8, 4
 
 
-def _inputs(dev, seed=11):
-    inp = make_paged_inputs(batch=2, num_q_heads=H * G, num_kv_heads=H, head_dim=128,
-                            context_len=[5000, 2300], hot_heads=[0, 3, 5], n_hot=6,
-                            hot_shift=10.0, seed=seed, device=dev)
+def _inputs(dev, seed=11, h=H, g=G):
+    inp = make_paged_inputs(batch=2, num_q_heads=h * g, num_kv_heads=h, head_dim=128,
+                            context_len=[5000, 2300], hot_heads=[x for x in (0, 3, 5) if x < h],
+                            n_hot=6, hot_shift=10.0, seed=seed, device=dev)
     W = inp.block_tables.shape[1]
     return inp, W, max(3, int(W * 0.25))
 
@@ -75,6 +75,86 @@ def test_plan_kinds_equal_separate_kernels(gpu, tau):
     assert torch.equal(plan.accept.view(torch.bool), acc)
     assert torch.equal(plan.page_indices, sel_r) and torch.equal(plan.n_per_head, nph_r)
     assert torch.equal(stats_p, stats_r) and torch.equal(work_p, work_r)
+
+
+def _worst_pages(ps, budget, nph):
+    """The `budget` lowest-scoring valid pages of every row (ascending page
+    order): a selection whose coverage any top-k selection exceeds."""
+    key = torch.where(torch.isfinite(ps), ps, torch.full_like(ps, float("inf")))
+    worst = torch.sort(torch.argsort(key, dim=2)[:, :, :budget], dim=2).values.to(torch.int32)
+    cols = torch.arange(budget, device=ps.device).view(1, 1, -1)
+    return torch.where(cols < nph.unsqueeze(2), worst, torch.zeros_like(worst))
+
+
+@pytest.mark.parametrize("case", ["keep", "reselect", "reselect_passes"])
+@pytest.mark.parametrize("predict_keep", [1, 0])
+@pytest.mark.parametrize("shape", [(8, 4), (4, 7), (16, 2), (2, 4)])
+def test_speculative_check_every_prediction(gpu, case, predict_keep, shape):
+    """A lazy check whose speculative decode is predicted right or wrong
+    equals the separate kernels and a plan without speculation bit for bit:
+    output, selection, gate, counters.  "keep": tau 0, the check keeps its
+    selection; "reselect": tau 0.995, it reselects and the new gate rejects;
+    "reselect_passes": the cached selection is every row's worst page and
+    tau lies between its coverage and the fresh selection's, so the check
+    rejects every head and the new gate accepts every head.  spec_state
+    records whether the speculative decode ran and, afterwards, the check's
+    own decision.  Shapes (H_kv, G): the fused launch for H_kv 8, 4 and 16;
+    H_kv 2 runs the sequential chain and leaves spec_state as it was."""
+    H, G = shape
+    inp, W, budget = _inputs(gpu, h=H, g=G)
+    ctx, bt = inp.context_lens, inp.block_tables
+    ps0 = ops.score_pages(jitter_query(inp.q, 0.5, 3), inp.k_cache, bt, ctx, H, G, 16)
+    sel0, nph0 = ops.select_topk(ps0, budget, ctx, 16)
+    q1 = jitter_query(inp.q, 0.5, 4)
+    tau = {"keep": 0.0, "reselect": 0.995}.get(case)
+    if case == "reselect_passes":
+        ps1 = ops.score_pages(q1, inp.k_cache, bt, ctx, H, G, 16)
+        nph0 = torch.ones_like(nph0)
+        sel0 = _worst_pages(ps1, budget, nph0)
+        cov_old = ops.check_coverage(ps1, sel0, nph0, 0.5)[1]
+        cov_new = ops.check_coverage(ps1, *ops.select_topk(ps1, budget, ctx, 16), 0.5)[1]
+        assert float(cov_old.max()) < float(cov_new.min())
+        tau = 0.5 * (float(cov_old.max()) + float(cov_new.min()))
+    plans, bufs = [], []
+    for speculate in (True, False):
+        b = dict(stats=torch.zeros(6, dtype=torch.int64, device=gpu),
+                 work=torch.zeros(2, dtype=torch.int64, device=gpu), cache=ps0.clone())
+        plans.append(ops.StepPlan(inp.q, inp.k_cache, inp.v_cache, bt, ctx, H, G, 16, budget,
+                                  tau, sel0.clone(), nph0.clone(), b["cache"], b["stats"],
+                                  b["work"], speculate=speculate))
+        bufs.append(b)
+    assert plans[1].spec_state is None
+    plans[0].spec_state[0] = predict_keep
+    got = plans[0].run(_lib.STEP_LAZY_CHECK, q1)
+    plain = plans[1].run(_lib.STEP_LAZY_CHECK, q1)
+    stats_r = torch.zeros(6, dtype=torch.int64, device=gpu)
+    work_r = torch.zeros(2, dtype=torch.int64, device=gpu)
+    sel_r, nph_r, cache_r = sel0.clone(), nph0.clone(), ps0.clone()
+    ps = ops.score_pages(q1, inp.k_cache, bt, ctx, H, G, 16)
+    chk, cov = ops.check_coverage(ps, sel_r, nph_r, tau)
+    acc = ops.select_or_keep(ps, chk, budget, ctx, 16, tau, sel_r, nph_r, cov, cache_r, stats_r)
+    want = ops.verified_decode(q1, inp.k_cache, inp.v_cache, bt, ctx, sel_r, nph_r, acc, H, G,
+                               16, output_dtype=q1.dtype, work=work_r)
+    for plan, b, out in ((plans[0], bufs[0], got), (plans[1], bufs[1], plain)):
+        assert torch.equal(out, want)
+        assert torch.equal(plan.accept.view(torch.bool), acc)
+        assert torch.equal(plan.page_indices, sel_r) and torch.equal(plan.n_per_head, nph_r)
+        assert torch.equal(b["cache"], cache_r)
+        assert torch.equal(b["stats"], stats_r) and torch.equal(b["work"], work_r)
+    keep = bool(chk.all())
+    assert keep == (case == "keep")
+    assert bool(acc.all()) == (case != "reselect")
+    assert case != "reselect_passes" or not bool(chk.any())
+    fused = H in (4, 8, 16)
+    assert plans[0].spec_state.tolist() == ([int(keep), predict_keep] if fused
+                                            else [predict_keep, 0])
+    # the next check speculates on this one's decision: a reuse step between
+    # them reads the (possibly reselected) selection and still matches
+    got = plans[0].run(_lib.STEP_REUSE, q1)
+    want = ops.sparse_decode_reuse(q1, inp.k_cache, inp.v_cache, bt, ctx,
+                                   sel_r.view(2 * H, -1), nph_r.view(2 * H),
+                                   ops.next_power_of_2(budget), H, G, 16)
+    assert torch.equal(got, want)
 
 
 @pytest.mark.parametrize("tau", [0.0, 0.995])
