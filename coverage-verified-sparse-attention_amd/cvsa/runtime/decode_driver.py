@@ -11,13 +11,17 @@ output is not fed to the next layer, whose projections are synthetic too),
 so it measures the attention path as the harness drives it: the batched
 append, the backend's schedule and its host cost per layer call.
 
-With ``graphs=True`` a step whose every layer call is a reuse step through a
-step plan (``CVSABackend.reuse_plan_for``) is captured once as a HIP graph
-and replayed for later such steps while every layer still maps to the same
-plan: one launch for the attention of all layers instead of one validated
-host call per layer.  The appends stay eager (their block ids come from the
-host allocator) and run before the replay: each layer's cache is its own,
-so only a layer's own append has to precede its call.  Replays repeat the calls' host bookkeeping
+With ``graphs=True`` the layers run in chunks of ``graph_chunk``
+consecutive layers: a chunk whose every layer call is a reuse step through
+a step plan (``CVSABackend.reuse_plan_for``) is captured once as a HIP graph
+and replayed for later such steps while each of its layers still maps to
+the same plan: one launch per chunk instead of one validated host call per
+layer.  The appends stay eager (their block ids come from the host
+allocator); each layer's cache is its own, so only a layer's own append has
+to precede its call: a chunk's appends are issued, then its replay, and the
+host prepares the next chunk while the GPU runs this one (one graph for
+every layer would leave the GPU idle while the host issues every append and
+checks every plan first).  Replays repeat the calls' host bookkeeping
 (``note_replayed_reuse``, ``step_done``), so schedule, counters and tracing
 state match an eager run; outputs are bit-identical to it.
 """
@@ -87,10 +91,11 @@ class DecodeDriver:
     reference per-layer protocol; see the module docstring."""
 
     def __init__(self, backend, layers: SyntheticDecodeLayers, graphs: bool = False,
-                 stream: Optional[torch.cuda.Stream] = None):
+                 stream: Optional[torch.cuda.Stream] = None, graph_chunk: int = 8):
         self.backend = backend
         self.layers = layers
         self.graphs = graphs
+        self.graph_chunk = max(1, int(graph_chunk))
         # Graph capture needs a stream other than the legacy default one, and
         # the step plans are bound to the stream they were made on: every
         # step of the driver runs on this one.
@@ -98,23 +103,25 @@ class DecodeDriver:
         L, B = layers.num_layers, layers.batch
         self.q_static = torch.empty(L, B, layers.num_q_heads, layers.head_dim,
                                     dtype=torch.bfloat16, device=layers.device)
-        self._graph = None
-        self._graph_plans = None
-        self._graph_outs = None
+        self._graphs = {}   # chunk index -> (graph, plans, output buffers)
         self.replays = 0
         self.captures = 0
 
     # ------------------------------------------------------------ one step
-    def _append(self, k, v):
-        for l, mgr in enumerate(self.layers.managers):
-            mgr.append_tokens_kv(k[l], v[l])
+    def _append(self, k, v, layers):
+        for l in layers:
+            self.layers.managers[l].append_tokens_kv(k[l], v[l])
 
-    def _eager(self, q, k=None, v=None) -> List[torch.Tensor]:
+    def _chunks(self):
+        L, c = self.layers.num_layers, self.graph_chunk
+        return [range(i, min(L, i + c)) for i in range(0, L, c)]
+
+    def _eager(self, q, k=None, v=None, layers=None) -> List[torch.Tensor]:
         """Per layer: the append of the new token (when k / v are given), the
         backend call, step_done -- the reference's order."""
         outs = []
         L = self.layers.num_layers
-        for l in range(L):
+        for l in (range(L) if layers is None else layers):
             cache, mgr = self.layers.caches[l], self.layers.managers[l]
             if k is not None:
                 mgr.append_tokens_kv(k[l], v[l])
@@ -123,11 +130,11 @@ class DecodeDriver:
             self.backend.step_done(l, L)
         return outs
 
-    def _plans_now(self):
-        """Every layer's reuse plan at the current step (None if any layer
-        would not run a plan-driven reuse step)."""
+    def _plans_now(self, layers):
+        """The reuse plan of every layer in ``layers`` at the current step
+        (None if one of them would not run a plan-driven reuse step)."""
         plans = []
-        for l in range(self.layers.num_layers):
+        for l in layers:
             cache, mgr = self.layers.caches[l], self.layers.managers[l]
             p = self.backend.reuse_plan_for(self.q_static[l], cache.k_cache, cache.v_cache,
                                             mgr.block_tables, mgr.context_lens, l)
@@ -151,30 +158,37 @@ class DecodeDriver:
         with torch.cuda.stream(self.stream):
             if not self.graphs:
                 return self._eager(q, k, v)
-            # Graph mode: the appends go first (each layer's cache is its
-            # own, so only the layer's own append must precede its call).
-            self._append(k, v)
+            # Graph mode, chunk by chunk: the chunk's appends, then its
+            # calls -- replayed when every layer of the chunk maps to the
+            # plans its graph was captured with, else captured (host
+            # bookkeeping now, kernels at the replay) or, when a layer takes
+            # another path, made eagerly.
             self.q_static.copy_(q)
-            plans = self._plans_now()
-            if plans is None:
-                return self._eager(self.q_static)
-            if self._graph is None or any(a is not b for a, b in zip(plans, self._graph_plans)):
-                # Capture this step's calls (their host bookkeeping runs now,
-                # their kernels only when the graph is replayed).
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph, stream=self.stream):
-                    outs = self._eager(self.q_static)
-                self._graph, self._graph_plans, self._graph_outs = graph, plans, outs
-                self.captures += 1
-                self._graph.replay()
-                return outs
-            self._graph.replay()
-            self.replays += 1
             L = self.layers.num_layers
-            for l in range(L):
-                self.backend.note_replayed_reuse(l)
-                self.backend.step_done(l, L)
-            return self._graph_outs
+            outs = []
+            for ci, chunk in enumerate(self._chunks()):
+                self._append(k, v, chunk)
+                plans = self._plans_now(chunk)
+                if plans is None:
+                    outs += self._eager(self.q_static, layers=chunk)
+                    continue
+                cached = self._graphs.get(ci)
+                if cached is None or any(a is not b for a, b in zip(plans, cached[1])):
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph, stream=self.stream):
+                        chunk_outs = self._eager(self.q_static, layers=chunk)
+                    graph.replay()
+                    self._graphs[ci] = (graph, plans, chunk_outs)
+                    self.captures += 1
+                    outs += chunk_outs
+                    continue
+                cached[0].replay()
+                self.replays += 1
+                for l in chunk:
+                    self.backend.note_replayed_reuse(l)
+                    self.backend.step_done(l, L)
+                outs += cached[2]
+            return outs
 
     # ------------------------------------------------------------ timing
     def run(self, steps: int, warmup: int = 5, first_step: int = 0):

@@ -113,7 +113,9 @@ def _pair(gpu, kw):
         backend = CVSABackend(num_kv_heads=8, num_q_heads=32, head_dim=128, block_size=16,
                               num_layers=SHAPE["num_layers"], budget_pct=0.2,
                               coverage_threshold=0.9, **kw)
-        runs.append((layers, backend, DecodeDriver(backend, layers, graphs=graphs)))
+        # chunks of 2 layers: several graphs per step, appends between them
+        runs.append((layers, backend, DecodeDriver(backend, layers, graphs=graphs,
+                                                   graph_chunk=2)))
     return runs
 
 
