@@ -587,16 +587,23 @@ struct WalkLds {
 // as possible: their position only needs r0 = split * pps.  Lanes past the
 // head's pages are discarded by the walk.
 template <int NW>
+__device__ __forceinline__ int listed_first_entry(const DecodeArgs &a, int split, int bh,
+                                                  int wave, int lane) {
+  if (a.max_sel <= 0) return 0;
+  return a.page_idx[(int64_t)bh * a.idx_stride +
+                    min(split * a.pps + wave + NW * lane, a.max_sel - 1)];
+}
+
+__device__ __forceinline__ int listed_first_block(const DecodeArgs &a, int bh, int lp) {
+  if (a.max_sel <= 0) return 0;
+  return a.block_tables[(bh / a.H_kv) * a.bt_sb + min(max(lp, 0), a.W - 1)];
+}
+
+template <int NW>
 __device__ __forceinline__ void listed_first_pages(const DecodeArgs &a, int split, int bh,
                                                    int wave, int lane, int &lp, int &phys) {
-  lp = 0;
-  phys = 0;
-  if (a.max_sel > 0) {
-    const int b = bh / a.H_kv;
-    lp = a.page_idx[(int64_t)bh * a.idx_stride + min(split * a.pps + wave + NW * lane,
-                                                     a.max_sel - 1)];
-    phys = a.block_tables[b * a.bt_sb + min(max(lp, 0), a.W - 1)];
-  }
+  lp = listed_first_entry<NW>(a, split, bh, wave, lane);
+  phys = listed_first_block(a, bh, lp);
 }
 
 // Listed pages of a head (the sparse decode of reuse steps, and verified
@@ -779,19 +786,20 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   // its selection, or a scoring step whose gate passes everywhere) run the
   // listed decode's static partition: workgroup w takes split w % n_splits
   // of head w / n_splits, exactly as listed_decode_kernel, so the outputs
-  // are bit for bit those of the listed decode.  Its first page lookups are
-  // requested together with the accept flags.  When the check kept its
-  // selection (spec_state[0], written by the check's select-or-keep) and a
-  // speculative listed decode of that selection already wrote the outputs
-  // (spec_state[1]), only the effective-budget counters are booked.  Every
-  // head accepted does not imply a kept selection: a rejected head is
-  // reselected and accepted when the new selection passes its gate.
+  // are bit for bit those of the listed decode.  Its first page-list
+  // entries are requested together with the accept flags and spec_state,
+  // their block-table entries once the launch is known to walk.  When the
+  // check kept its selection (spec_state[0], written by the check's
+  // select-or-keep) and a speculative listed decode of that selection
+  // already wrote the outputs (spec_state[1]), only the effective-budget
+  // counters are booked.  Every head accepted does not imply a kept
+  // selection: a rejected head is reselected and accepted when the new
+  // selection passes its gate.
   if constexpr (MODE == kModeVerified) {
     const int n_listed = a.n_splits * heads;
     const int split = w % max(a.n_splits, 1);
     const int bh = min(w / max(a.n_splits, 1), heads - 1);
-    int lp, phys;
-    listed_first_pages<NW>(a, split, bh, wave, lane, lp, phys);
+    const int lp = listed_first_entry<NW>(a, split, bh, wave, lane);
     int spec_done = 0;
     if (a.spec_state != nullptr)
       spec_done = __builtin_amdgcn_readfirstlane(a.spec_state[0] & a.spec_state[1]);
@@ -802,7 +810,8 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
         if (w == 0 && a.work != nullptr) add_listed_work<NT>(a, s_work);
         return;
       }
-      if (w < n_listed) listed_walk<G, Engine, NW, PD>(a, split, bh, lp, phys, L);
+      if (w < n_listed)
+        listed_walk<G, Engine, NW, PD>(a, split, bh, lp, listed_first_block(a, bh, lp), L);
       return;
     }
   }
