@@ -766,6 +766,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
 
   __shared__ WalkLds<G, Engine, NW> L;
   __shared__ int s_wsum[NW];
+  __shared__ int s_odd[NW];               // a head of the wave's pass walks != max_sel pages
   __shared__ int s_start[kMaxHeads + 1];  // exclusive prefix of pages per head
   __shared__ uint8_t s_listed[kMaxHeads];
   __shared__ unsigned long long s_work[2];
@@ -860,6 +861,8 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   if ((int)threadIdx.x >= heads) c_first = 0;
   const int incl_first = wave_incl_scan(c_first);
   if (lane == kWave - 1) s_wsum[wave] = incl_first;
+  const bool odd_first = __ballot((int)threadIdx.x < heads && c_first != a.max_sel) != 0;
+  if (lane == 0) s_odd[wave] = odd_first ? 1 : 0;
 
   // One wave's walk over its pages s0 + wave + NW*j of a segment, in chunks
   // of up to 64 pages: lane j of a chunk looks up page j's block id and
@@ -924,6 +927,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   }
   // Pass 0 (peeled: a loop header here makes the compiler wait for the
   // speculative loads), then the passes of launches with more than NT heads.
+  int uneven = 0;  // some head walks a number of pages other than max_sel
   auto finish_pass = [&](int hh, int c, int incl, bool lst, int &carry) {
     lds_barrier();
     int excl = incl - c, total = 0;
@@ -931,6 +935,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     for (int i = 0; i < NW; ++i) {
       if (i < wave) excl += s_wsum[i];
       total += s_wsum[i];
+      uneven |= s_odd[i];
     }
     if (hh < heads) {
       s_start[hh] = carry + excl;
@@ -949,6 +954,8 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
       if (hh >= heads) c = 0;
       const int incl = wave_incl_scan(c);
       if (lane == kWave - 1) s_wsum[wave] = incl;
+      const bool odd = __ballot(hh < heads && c != a.max_sel) != 0;
+      if (lane == 0) s_odd[wave] = odd ? 1 : 0;
       finish_pass(hh, c, incl, lst, carry);
     }
   }
@@ -957,7 +964,9 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   lds_barrier();
   T = __builtin_amdgcn_readfirstlane(T);
 
-  const bool spec_ok = T == T_spec && h_spec >= 0;  // every head walks max_sel pages
+  // Every head walks max_sel pages (a matching total is not enough: one
+  // head's extra pages can make up for another's missing ones).
+  const bool spec_ok = uneven == 0 && T == T_spec && h_spec >= 0;
   const Partition part = spec_ok ? spec_part : Partition(max(T, 1), a.sk_grid);
   const int n_wg = T > 0 ? part.n : a.sk_grid;
   if (w >= n_wg) return;  // uniform

@@ -435,6 +435,37 @@ def test_decode_many_splits(gpu, ctx, budget):
         assert ((dlse - dwant_lse).abs() / dwant_lse.abs().clamp(min=1.0)).max().item() < LSE_RTOL
 
 
+@pytest.mark.parametrize("rejected", [0, 3, 7])
+def test_verified_decode_uneven_walks_with_the_uniform_total(gpu, rejected):
+    """A verified launch whose heads walk max_sel pages in total on average
+    but not each: one rejected head walks all 1024 valid pages, the seven
+    accepted heads walk none, and 8 x max_sel = 1024 as well.  Regression:
+    the stream-K kernel took a matching total for "every head walks max_sel
+    pages", started workgroups at the wrong head and skipped pages of the
+    rejected head (which pages depended on the head's index).  Every head is
+    compared with torch attention over its pages."""
+    H, G, ctx, budget = 8, 4, 16 * 1024, 128
+    inp = make_paged_inputs(1, 32, H, 128, ctx, seed=431, device=gpu, hot_heads=[rejected],
+                            n_hot=8, hot_shift=6.0)
+    q, K, V, bt, cl = inp.q, inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens
+    idx = torch.zeros(1, H, budget, dtype=torch.int32, device=gpu)
+    nph = torch.zeros(1, H, dtype=torch.int32, device=gpu)
+    accept = torch.ones(1, H, dtype=torch.bool, device=gpu)
+    accept[0, rejected] = False
+    out, (o, m, l) = ops.verified_decode(q, K, V, bt, cl, idx, nph, accept, H, G, 16,
+                                         return_state=True, output_dtype=torch.float32)
+    every = torch.arange(1024, device=gpu)
+    for h in range(H):
+        rows = slice(h * G, (h + 1) * G)
+        if h != rejected:
+            assert bool((out[0, rows] == 0).all()) and bool((l[0, rows] == 0).all()), h
+            continue
+        want, want_lse = _torch_attention(q, K, V, bt, cl, every, h, G)
+        assert (out[0, rows] - want).abs().max().item() < 1e-3, h
+        lse = m[0, rows] + torch.log(l[0, rows])
+        assert ((lse - want_lse).abs() / want_lse.abs().clamp(min=1.0)).max().item() < LSE_RTOL
+
+
 def test_prepare_reuse_state_then_reuse_decode(gpu):
     """prepare_reuse_state (sparse_decode.py:664-678) pads a width-100
     selection to 128 with page 0; sparse_decode_reuse (:681-721) on that
