@@ -743,7 +743,13 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
       // Fixed-interval scoring step (backend.py:859-863): tally this head,
       // then the last head of the call books the step as all-accepted or
       // not.  stats[4] (rejected heads of this call) and stats[5] (heads
-      // done) are scratch that the last head clears again.
+      // done) are scratch that the last head clears again.  Ordering: every
+      // atomic here is performed at the device's coherence point (agent
+      // scope, no cached copy), and the s_waitcnt below makes this head's
+      // stats[4] add complete before its stats[5] add is issued, so the
+      // head that sees done == n_heads - 1 reads every head's stats[4]
+      // add.  This rests on that gfx950 behaviour of atomics, not on a
+      // release / acquire pairing of the HIP memory model.
       __hip_atomic_fetch_add(&stats[3], (long long)acc, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_fetch_add(&stats[4], (long long)(1 - acc), __ATOMIC_RELAXED,
