@@ -344,3 +344,70 @@ def test_backend_plans_equal_kernel_path(gpu, kw):
     sa, sb = plan_b.get_stats(), kern_b.get_stats()
     for k in sa:
         assert sa[k] == sb[k], (k, sa[k], sb[k])
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_shapes_plan_equals_separate_kernels(gpu, seed):
+    """Random B, H_kv, G, ragged contexts, budget and tau: a plan (with and
+    without speculation) runs a first selection, two lazy checks, a reuse
+    step and a fixed-interval scoring step; every output, selection, gate and
+    counter equals the same kernels called one by one, bit for bit."""
+    g = torch.Generator().manual_seed(100 + seed)
+    rnd = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))  # noqa: E731
+    H = [1, 2, 4, 8, 16][rnd(0, 4)]
+    G = rnd(1, 8)
+    B = rnd(1, 3)
+    ctx = [rnd(40, 6000) for _ in range(B)]
+    inp = make_paged_inputs(B, H * G, H, 128, ctx, seed=seed, device=gpu,
+                            max_pages=max((c - 1) // 16 + 1 for c in ctx) + rnd(0, 3),
+                            hot_heads=list(range(0, H, 2)), n_hot=4, hot_shift=8.0)
+    W = inp.block_tables.shape[1]
+    budget = max(3, int(W * [0.125, 0.25, 0.5][rnd(0, 2)]))
+    tau = [0.0, 0.5, 0.9, 0.995][rnd(0, 3)]
+    ctx_t, bt = inp.context_lens, inp.block_tables
+    runs = []
+    for speculate in (True, False):
+        stats = torch.zeros(6, dtype=torch.int64, device=gpu)
+        work = torch.zeros(2, dtype=torch.int64, device=gpu)
+        plan = ops.StepPlan(inp.q, inp.k_cache, inp.v_cache, bt, ctx_t, H, G, 16, budget, tau,
+                            stats=stats, work=work, own_scores_cache=True, speculate=speculate)
+        outs = []
+        for step, kind in enumerate((_lib.STEP_FRESH, _lib.STEP_LAZY_CHECK, _lib.STEP_LAZY_CHECK,
+                                     _lib.STEP_REUSE, _lib.STEP_SCORE)):
+            q = jitter_query(inp.q, 0.4, 300 + 10 * seed + step)
+            outs.append(plan.run(kind, q).clone())
+        runs.append((plan, stats, work, outs))
+    # the separate kernels
+    stats = torch.zeros(6, dtype=torch.int64, device=gpu)
+    work = torch.zeros(2, dtype=torch.int64, device=gpu)
+    sel = torch.empty(B, H, budget, dtype=torch.int32, device=gpu)
+    nph = torch.empty(B, H, dtype=torch.int32, device=gpu)
+    cov = torch.empty(B, H, dtype=torch.float32, device=gpu)
+    cache = torch.empty(B, H, W, dtype=torch.float32, device=gpu)
+    want = []
+    for step, kind in enumerate(("fresh", "check", "check", "reuse", "score")):
+        q = jitter_query(inp.q, 0.4, 300 + 10 * seed + step)
+        if kind == "reuse":
+            want.append(ops.sparse_decode_reuse(q, inp.k_cache, inp.v_cache, bt, ctx_t,
+                                                sel.view(B * H, -1), nph.view(B * H),
+                                                ops.next_power_of_2(budget), H, G, 16,
+                                                work=work))
+            continue
+        ps = ops.score_pages(q, inp.k_cache, bt, ctx_t, H, G, 16)
+        if kind == "fresh":
+            acc = ops.select_or_keep(ps, None, budget, ctx_t, 16, tau, sel, nph, cov, cache,
+                                     stats)
+        elif kind == "check":
+            chk, cov = ops.check_coverage(ps, sel, nph, tau)
+            acc = ops.select_or_keep(ps, chk, budget, ctx_t, 16, tau, sel, nph, cov, cache,
+                                     stats)
+        else:
+            acc = ops.select_or_keep(ps, None, budget, ctx_t, 16, tau, sel, nph, cov, None,
+                                     stats, count_gate=True)
+        want.append(ops.verified_decode(q, inp.k_cache, inp.v_cache, bt, ctx_t, sel, nph, acc,
+                                        H, G, 16, output_dtype=q.dtype, work=work))
+    for plan, p_stats, p_work, outs in runs:
+        for step, (got, ref_out) in enumerate(zip(outs, want)):
+            assert torch.equal(got, ref_out), (seed, step, plan.spec_state is not None)
+        assert torch.equal(plan.page_indices, sel) and torch.equal(plan.n_per_head, nph)
+        assert torch.equal(p_stats, stats) and torch.equal(p_work, work), seed
