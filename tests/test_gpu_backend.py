@@ -462,3 +462,37 @@ def test_timing_buckets(gpu):
         assert st["kernel_ms_per_decode_step"][k] == pytest.approx(
             st["kernel_times_ms_total"][k] / n)
     assert {k: v for k, v in st.items() if not k.startswith("kernel_")} == sp
+
+
+def _random_schedule(seed):
+    """A random shape and schedule: B, H_kv, G, ragged contexts, budget, tau,
+    lazy (M, coverage interval) or fixed interval, approximate recovery or a
+    dense layer now and then."""
+    g = torch.Generator().manual_seed(5000 + seed)
+    rnd = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))  # noqa: E731
+    H = [1, 2, 4, 8][rnd(0, 3)]
+    G = rnd(1, 8)
+    B = rnd(1, 3)
+    cfg = dict(batch=B, num_q_heads=H * G, num_kv_heads=H, head_dim=128,
+               context_len=[rnd(200, 5000) for _ in range(B)],
+               hot_heads=list(range(0, H, 2)), n_hot=rnd(2, 8), hot_shift=float(rnd(6, 12)))
+    kw = dict(budget_pct=[0.125, 0.25, 0.5][rnd(0, 2)],
+              coverage_threshold=[0.5, 0.8, 0.9, 0.95][rnd(0, 3)])
+    if rnd(0, 1):
+        kw.update(lazy=True, check_interval=rnd(2, 5))
+        if rnd(0, 2) == 0:
+            kw["coverage_interval"] = 1
+    else:
+        kw.update(lazy=False, reuse_interval=rnd(1, 4))
+    if rnd(0, 3) == 0:
+        kw["approx_recovery_pct"] = 0.25
+    return cfg, kw
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_schedules_against_oracle(gpu, seed):
+    """Eight random shapes and schedules, ten steps with appends, in lockstep
+    with the oracle backend: selections, masks, outputs and statistics."""
+    cfg, kw = _random_schedule(seed)
+    stats, trace, lock = _run(gpu, cfg, kw, steps=10, seed=600 + seed)
+    print(f"seed {seed} {cfg} {kw}: {lock.summary()}")
