@@ -318,6 +318,15 @@ def cpu_baseline(cfg, layer0, n_steps, tau):
                 break
         elif s % cfg["M"] == 0 and sum(times) >= CPU_SAMPLE_S:
             break
+    # The dense baseline on the CPU: one warmup, then five repetitions.
+    from oracle import cvsa_oracle as ref
+    G = cfg["H_q"] // cfg["H_kv"]
+    dense_s = []
+    for rep in range(6):
+        t0 = time.perf_counter()
+        ref.dense_decode(q0, *args, cfg["H_kv"], G, BS, acc_dtype=torch.float32)
+        if rep:
+            dense_s.append(time.perf_counter() - t0)
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -327,7 +336,7 @@ def cpu_baseline(cfg, layer0, n_steps, tau):
                     break
     except OSError:
         pass
-    return times, torch.get_num_threads(), model
+    return times, torch.get_num_threads(), model, dense_s
 
 
 def run_schedule(cfg, layers, tau, args, dev):
@@ -586,14 +595,20 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU oracle baseline")
-        times, threads, model = cpu_baseline(cfg, layers[0], args.cpu_steps, tau0)
+        times, threads, model, dense_s = cpu_baseline(cfg, layers[0], args.cpu_steps, tau0)
         n_cpu = len(times)
+        first = [t for i, t in enumerate(times) if i % M == 0]    # scoring / check steps
+        rest = [t for i, t in enumerate(times) if i % M != 0]     # reuse steps
         cpu = {"value": statistics.mean(times) * 1e6,
                "unit": f"us per decode step (mean of {n_cpu} steps)",
-               "cores": threads, "kind": "port",
+               "cores": threads, "cpu_count": os.cpu_count(), "kind": "port",
                "sample": f"{n_cpu} decode steps ({n_cpu // M} schedule cycles of {M}, the "
                          f"first a scoring step; {sum(times):.1f} s of CPU work) of layer 0 "
                          f"at full {args.config} size, fp32 oracle, torch CPU, {model}",
+               "median_us_by_step": {
+                   "scoring_or_check": round(statistics.median(first) * 1e6, 1),
+                   **({"reuse": round(statistics.median(rest) * 1e6, 1)} if rest else {}),
+                   "dense": round(statistics.median(dense_s) * 1e6, 1)},
                "step_s": [round(t, 4) for t in times]}
 
     mean_us, med_us = res["mean_us"], res["med_us"]
