@@ -12,8 +12,13 @@
 namespace cvsa {
 
 constexpr int kWave = 64;
-constexpr int kHeadDim = 128;   // the only supported head dimension
+constexpr int kHeadDim = 128;   // the head dimension of the fused lazy-check launch
 constexpr int kPageTokens = 16; // the only supported page (block) size
+
+// Head dimensions the kernels are compiled for.
+__host__ __device__ constexpr bool head_dim_supported(int D) {
+  return D == 64 || D == 128 || D == 256;
+}
 constexpr int kMaxPages = 32768;
 
 // ---------------------------------------------------------------- numerics
@@ -140,14 +145,19 @@ __device__ __forceinline__ void xchg32(float v, float &a, float &b) {
   b = __uint_as_float(r[1]);
 }
 
-// All-reduce over aligned groups of W lanes (W in 1,2,4,8,16); every lane
-// of a group ends with the same bits.
+// All-reduce over aligned groups of W lanes (W in 1,2,4,8,16,32); every
+// lane of a group ends with the same bits.
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
   if constexpr (W >= 2) v += dpp_f<kDppQuadXor1>(v);
   if constexpr (W >= 4) v += dpp_f<kDppQuadXor2>(v);
   if constexpr (W >= 8) v += dpp_f<kDppRowHalfMirror>(v);
   if constexpr (W >= 16) v += dpp_f<kDppRowMirror>(v);
+  if constexpr (W >= 32) {
+    float a, b;
+    xchg16(v, a, b);
+    v = a + b;
+  }
   return v;
 }
 

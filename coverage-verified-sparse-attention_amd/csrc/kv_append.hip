@@ -20,7 +20,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_kv_kernel(
     int64_t new_sb, uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache,
     int64_t num_blocks, int32_t *__restrict__ block_tables, int64_t bt_sb, int W,
     int32_t *__restrict__ context_lens, int32_t *__restrict__ pages_allocated,
-    int seq_begin, int n_seqs, int next_free, int H_kv, int block_size) {
+    int seq_begin, int n_seqs, int next_free, int H_kv, int D, int block_size) {
   __shared__ int s_blk[kAppendThreads];
   __shared__ int s_off[kAppendThreads];
   __shared__ uint32_t wsum[kAppendThreads / kWave];
@@ -66,14 +66,14 @@ __global__ __launch_bounds__(kAppendThreads) void append_kv_kernel(
   __syncthreads();
 
   // Copy the K and V rows: [H_kv, D] bf16 per sequence, as 16-byte vectors.
-  const int vec_per_row = H_kv * kHeadDim / 8;
+  const int vec_per_row = H_kv * D / 8;
   const int total = n_seqs * vec_per_row;
   for (int v = i; v < total; v += kAppendThreads) {
     const int s = v / vec_per_row;
     const int w = v - s * vec_per_row;
     const int blk = s_blk[s];
     if (blk < 0) continue;
-    const int64_t dst = ((int64_t)blk * block_size + s_off[s]) * H_kv * kHeadDim + w * 8;
+    const int64_t dst = ((int64_t)blk * block_size + s_off[s]) * H_kv * D + w * 8;
     const int64_t src = s * new_sb + w * 8;
     *reinterpret_cast<uint4 *>(k_cache + dst) = *reinterpret_cast<const uint4 *>(k_new + src);
     *reinterpret_cast<uint4 *>(v_cache + dst) = *reinterpret_cast<const uint4 *>(v_new + src);
@@ -98,8 +98,8 @@ extern "C" int cvsa_append_kv(const uint16_t *k_new, const uint16_t *v_new,
                    W > 0 && num_blocks > 0 && block_size > 0 && bt_stride_b >= W,
                CVSA_ERR_INVALID, "append_kv: bad sizes n_seqs=%d H_kv=%d W=%d", n_seqs,
                H_kv, W);
-  CVSA_REQUIRE(D == kHeadDim, CVSA_ERR_UNSUPPORTED, "append_kv: only D=128 supported (got %d)",
-               D);
+  CVSA_REQUIRE(head_dim_supported(D), CVSA_ERR_UNSUPPORTED,
+               "append_kv: D=%d not in {64, 128, 256}", D);
   CVSA_REQUIRE(((uintptr_t)k_new & 15) == 0 && ((uintptr_t)v_new & 15) == 0 &&
                    new_stride_b % 8 == 0 && ((uintptr_t)k_cache & 15) == 0 &&
                    ((uintptr_t)v_cache & 15) == 0,
@@ -107,6 +107,6 @@ extern "C" int cvsa_append_kv(const uint16_t *k_new, const uint16_t *v_new,
   hipLaunchKernelGGL(append_kv_kernel, dim3(1), dim3(kAppendThreads), 0, (hipStream_t)stream,
                      k_new, v_new, new_stride_b, k_cache, v_cache, num_blocks, block_tables,
                      bt_stride_b, W, context_lens, pages_allocated, seq_begin, n_seqs,
-                     next_free_block, H_kv, block_size);
+                     next_free_block, H_kv, D, block_size);
   return cvsa_host::check_launch("append_kv");
 }

@@ -47,12 +47,12 @@
 
 namespace cvsa {
 
-// Split partials are rows of kPartStride floats: o[D], m, l and two pad
-// words, so every row starts on a 16-byte boundary.
-constexpr int kPartStride = kHeadDim + 4;
+// Split partials of head dimension D are rows of part_stride(D) floats:
+// o[D], m, l and two pad words, so every row starts on a 16-byte boundary.
+// A q-head's o is D / 4 float4 chunks.
+__host__ __device__ constexpr int part_stride(int D) { return D + 4; }
 constexpr int kMaxSplits = 256;            // partials per head (and workgroups per launch)
 constexpr int kMinPagesPerWave = 2;        // pages per wave of a split, at least
-constexpr int kChunksPerRow = kHeadDim / 4;  // float4 chunks of one q-head's o
 
 struct DecodeArgs {
   const uint16_t *q;
@@ -69,6 +69,7 @@ struct DecodeArgs {
   const int32_t *n_pages;
   const uint8_t *accept;  // non-NULL: verified mode
   int H_kv, W;
+  int D;      // head dimension (the launch's engine is compiled for it)
   int heads;  // B * H_kv
   int pps, n_splits;  // listed partition: pages per split, splits per head
   int sk_grid;        // stream-K partition: workgroups (<= kMaxSplits)
@@ -97,16 +98,17 @@ __device__ __forceinline__ void store_out(void *out, int dtype, int64_t i, float
 }
 
 
+template <int D>
 __device__ __forceinline__ void write_outputs(const DecodeArgs &a, int64_t qrow, int d, float O,
                                               float M, float L) {
   if (a.o_unnorm != nullptr) {
-    a.o_unnorm[qrow * kHeadDim + d] = O;
+    a.o_unnorm[qrow * D + d] = O;
     if (d == 0) {
       a.m_out[qrow] = M;
       a.l_out[qrow] = L;
     }
   }
-  if (a.out != nullptr) store_out(a.out, a.out_dtype, qrow * kHeadDim + d, O / fmaxf(L, 1e-6f));
+  if (a.out != nullptr) store_out(a.out, a.out_dtype, qrow * D + d, O / fmaxf(L, 1e-6f));
 }
 
 // Effective-budget counters: pages attended by this head and n_valid(b).
@@ -209,9 +211,10 @@ struct PartBuf {
 // one 16-byte store of o_unnorm and one 8- or 16-byte store of out.  The
 // outputs are the last stores of a launch, which cannot end before they
 // complete, so they are written as few, wide stores.
+template <int D>
 __device__ __forceinline__ void write_outputs4(const DecodeArgs &a, int64_t qrow, int d0,
                                                f32x4 O, float M, float L) {
-  const int64_t i = qrow * kHeadDim + d0;
+  const int64_t i = qrow * D + d0;
   if (a.o_unnorm != nullptr) {
     *reinterpret_cast<f32x4 *>(a.o_unnorm + i) = O;
     if (d0 == 0) {
@@ -250,30 +253,31 @@ struct MergeLds {
 // Merge of a head's n_act split partials by the last of its workgroups.
 // Thread t owns float4 chunk c = t % NC of the head's G x D outputs and the
 // splits j, j + J, ... (j = t / NC); their o chunks are loaded in batches of
-// KB, the next batch in flight while the current one is summed.  The (m, l)
-// pairs go to LDS first; one wave per q-head turns them into the weights
-// exp(m_sp - M) and the totals (M, L).
-template <int G, int NT>
+// KB, the next batch in flight while the current one is summed.  When the
+// outputs hold more chunks than the workgroup has threads (G x D > 4 NT) each
+// thread takes chunks t, t + NT, ... in turn, every split of each.  The
+// (m, l) pairs go to LDS first; one wave per q-head turns them into the
+// weights exp(m_sp - M) and the totals (M, L).
+template <int G, int D, int NT>
 __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBuf &pb,
                                                uint32_t head_off, int n_act, int bh, int n,
                                                int ctx, MergeLds<G, NT> &s) {
+  constexpr int kChunksPerRow = D / 4;
+  constexpr int kPartStride = part_stride(D);
   constexpr int NC = G * kChunksPerRow;
   constexpr int J = NT / NC > 0 ? NT / NC : 1;
+  constexpr int NPASS = (NC + NT - 1) / NT;
   constexpr int NW = NT / kWave;
   constexpr int KB = 8;
-  static_assert(NC <= NT, "merge layout: one thread per output chunk");
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const int c = t % NC;
-  const int j = t / NC;
+  const int j = NPASS == 1 ? t / NC : 0;
   const bool active = t < NC * J;
-  const int g = c / kChunksPerRow;
-  const int d0 = 4 * (c % kChunksPerRow);
 
-  for (int e = t; e < n_act * G; e += NT) s.ml[e] = pb.load2(head_off + e * kPartStride + kHeadDim);
+  for (int e = t; e < n_act * G; e += NT) s.ml[e] = pb.load2(head_off + e * kPartStride + D);
   const int per_lane = active ? (n_act - j + J - 1) / J : 0;  // splits of this thread
-  auto load_batch = [&](int b0, f32x4 (&v)[KB]) {
+  auto load_batch = [&](int g, int d0, int b0, f32x4 (&v)[KB]) {
 #pragma unroll
     for (int k = 0; k < KB; ++k) {
       const int sp = min(j + (b0 + k) * J, n_act - 1);
@@ -281,7 +285,10 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBu
     }
   };
   f32x4 cur[KB];
-  load_batch(0, cur);
+  {
+    const int c = NPASS == 1 ? t % NC : t;  // NPASS > 1: t < NT < NC
+    load_batch(c / kChunksPerRow, 4 * (c % kChunksPerRow), 0, cur);
+  }
   __syncthreads();
   for (int gg = wave; gg < G; gg += NW) {  // wave-uniform
     float mx = -INFINITY;
@@ -301,28 +308,36 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBu
     }
   }
   __syncthreads();
-  f32x4 O = {0.f, 0.f, 0.f, 0.f};
-  for (int b0 = 0; b0 < per_lane; b0 += KB) {
-    f32x4 nxt[KB];
-    load_batch(b0 + KB, nxt);
+#pragma unroll 1
+  for (int pass = 0; pass < NPASS; ++pass) {
+    const int c = NPASS == 1 ? t % NC : min(t + pass * NT, NC - 1);
+    const bool live = NPASS == 1 ? active : t + pass * NT < NC;
+    const int g = c / kChunksPerRow;
+    const int d0 = 4 * (c % kChunksPerRow);
+    if (pass > 0) load_batch(g, d0, 0, cur);
+    f32x4 O = {0.f, 0.f, 0.f, 0.f};
+    for (int b0 = 0; b0 < per_lane; b0 += KB) {
+      f32x4 nxt[KB];
+      load_batch(g, d0, b0 + KB, nxt);
 #pragma unroll
-    for (int k = 0; k < KB; ++k) {
-      const int sp = min(j + (b0 + k) * J, n_act - 1);
-      const float w = b0 + k < per_lane ? s.ml[sp * G + g].x : 0.f;
-      O += w * cur[k];
+      for (int k = 0; k < KB; ++k) {
+        const int sp = min(j + (b0 + k) * J, n_act - 1);
+        const float w = b0 + k < per_lane ? s.ml[sp * G + g].x : 0.f;
+        O += w * cur[k];
+      }
+#pragma unroll
+      for (int k = 0; k < KB; ++k) cur[k] = nxt[k];
     }
+    if constexpr (J > 1) {
+      s.acc[t] = O;
+      __syncthreads();
+      if (active && j == 0) {
 #pragma unroll
-    for (int k = 0; k < KB; ++k) cur[k] = nxt[k];
-  }
-  if constexpr (J > 1) {
-    s.acc[t] = O;
-    __syncthreads();
-    if (active && j == 0) {
-#pragma unroll
-      for (int jj = 1; jj < J; ++jj) O += s.acc[t + jj * NC];
+        for (int jj = 1; jj < J; ++jj) O += s.acc[t + jj * NC];
+      }
     }
+    if (live && j == 0) write_outputs4<D>(a, (int64_t)bh * G + g, d0, O, s.M[g], s.L[g]);
   }
-  if (active && j == 0) write_outputs4(a, (int64_t)bh * G + g, d0, O, s.M[g], s.L[g]);
   if (t == 0 && a.work != nullptr) add_work(a, n, ctx);
 }
 
@@ -352,20 +367,27 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 //     d column 16 blk + l%16.
 // Softmax state: m and the running l of head l%16 live in the four lanes of
 // that head; a rescale of O rows goes through LDS (16 factors per wave).
-template <int G>
+template <int G, int D>
 struct MfmaEngine {
   static_assert(G <= 16, "GQA group larger than the MFMA tile");
-  static constexpr int kVRow = kHeadDim + 8;  // LDS row of the V tile, in bf16
+  static_assert(D == 64 || D == 128 || D == 256, "head dimension");
+  static constexpr int kD = D;
+  static constexpr int NK = D / 32;         // S = K Q^T MFMAs (32 dimensions each)
+  static constexpr int NB = D / 16;         // O column blocks (16 dimensions each)
+  static constexpr int LPR = D / 8;         // lanes per V row (16 bytes each)
+  static constexpr int RPL = kWave / LPR;   // V rows per wave load
+  static constexpr int NV = kPageTokens / RPL;  // V loads per page
+  static constexpr int kVRow = D + 8;       // LDS row of the V tile, in bf16
   struct Page {
-    uint4 k[4], v[4];
+    uint4 k[NK], v[NV];
   };
   struct Lds {
     uint16_t v[kPageTokens * kVRow];
     float alpha[16];
   };
 
-  float4_t o[8];
-  bf16x8_t qb[4];
+  float4_t o[NB];
+  bf16x8_t qb[NK];
   float m_g, l_g;
   int lane;
   int64_t koff, voff, row_stride;
@@ -374,19 +396,19 @@ struct MfmaEngine {
   __device__ __forceinline__ void init(const DecodeArgs &a, int b, int h, int lane_, Lds &) {
     lane = lane_;
     scale = a.scale;
-    row_stride = (int64_t)a.H_kv * kHeadDim;
+    row_stride = (int64_t)a.H_kv * D;
     const int c16 = lane & 15, grp = lane >> 4;
-    koff = (int64_t)h * kHeadDim + c16 * row_stride + 8 * grp;
-    voff = (int64_t)h * kHeadDim + grp * row_stride + 8 * c16;
+    koff = (int64_t)h * D + c16 * row_stride + 8 * grp;
+    voff = (int64_t)h * D + (lane / LPR) * row_stride + 8 * (lane % LPR);
     // Rows past the group repeat head G-1: MFMA output rows are independent
     // and those rows are never written out.  No select on the loaded value,
     // so nothing waits for q before the first page is consumed.
     const uint16_t *qrow = a.q + b * a.q_sb + (int64_t)(h * G + min(c16, G - 1)) * a.q_sh;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
+    for (int kk = 0; kk < NK; ++kk)
       qb[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(qrow + 32 * kk + 8 * grp));
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk) o[blk] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int blk = 0; blk < NB; ++blk) o[blk] = float4_t{0.f, 0.f, 0.f, 0.f};
     m_g = -INFINITY;
     l_g = 0.f;
   }
@@ -397,11 +419,11 @@ struct MfmaEngine {
   // more HBM fetches, slower).  V loads read whole rows and keep the hint.
   __device__ __forceinline__ void fetch(const uint16_t *kp, const uint16_t *vp, Page &pg) const {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
+    for (int kk = 0; kk < NK; ++kk)
       pg.k[kk] = *reinterpret_cast<const uint4 *>(kp + koff + 32 * kk);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      pg.v[i] = stream_load16(vp + voff + 4 * i * row_stride);
+    for (int i = 0; i < NV; ++i)
+      pg.v[i] = stream_load16(vp + voff + RPL * i * row_stride);
   }
 
   __device__ __forceinline__ void consume(Page &pg, int ntok, Lds &lds) {
@@ -409,7 +431,7 @@ struct MfmaEngine {
     const int t0 = 4 * grp;
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
+    for (int kk = 0; kk < NK; ++kk)
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pg.k[kk]),
                                                     qb[kk], acc, 0, 0, 0);
     float sv[4];
@@ -432,7 +454,7 @@ struct MfmaEngine {
       if (lane < 16) lds.alpha[lane] = alpha;
       const float4 ar = *reinterpret_cast<const float4 *>(&lds.alpha[t0]);  // rows 4grp .. +4
 #pragma unroll
-      for (int blk = 0; blk < 8; ++blk) {
+      for (int blk = 0; blk < NB; ++blk) {
         o[blk][0] *= ar.x;
         o[blk][1] *= ar.y;
         o[blk][2] *= ar.z;
@@ -453,13 +475,13 @@ struct MfmaEngine {
     // V page -> LDS tile (rows past the context are stored as zeros: the
     // reference never reads them).
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 4 * i + grp;
+    for (int i = 0; i < NV; ++i) {
+      const int t = RPL * i + lane / LPR;
       const uint4 w = t < ntok ? pg.v[i] : make_uint4(0u, 0u, 0u, 0u);
-      *reinterpret_cast<uint4 *>(&lds.v[t * kVRow + 8 * c16]) = w;
+      *reinterpret_cast<uint4 *>(&lds.v[t * kVRow + 8 * (lane % LPR)]) = w;
     }
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk) {
+    for (int blk = 0; blk < NB; ++blk) {
       short4_t vb;
 #pragma unroll
       for (int j = 0; j < 4; ++j) vb[j] = (short)lds.v[(t0 + j) * kVRow + 16 * blk + c16];
@@ -469,7 +491,7 @@ struct MfmaEngine {
   }
 
   template <int NW>
-  __device__ __forceinline__ void finish(int wave, int lane_, float (*s_o)[G][kHeadDim],
+  __device__ __forceinline__ void finish(int wave, int lane_, float (*s_o)[G][D],
                                          float (*s_m)[G], float (*s_l)[G]) {
     const int c16 = lane & 15, grp = lane >> 4;
     float x, y;
@@ -482,7 +504,7 @@ struct MfmaEngine {
       s_l[wave][lane] = l_g;
     }
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk)
+    for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int g = 4 * grp + j;
@@ -499,16 +521,18 @@ __device__ __forceinline__ L &s_eng_of(L (&eng)[NW], int wave) { return eng[wave
 // contributor (n_act == 1) it writes the outputs.  Otherwise it stores its
 // partial (o, m, l) in partial row my_row, bumps the head's counter, and the
 // last of the n_act contributors merges rows first_row .. first_row+n_act-1.
-template <int G, int NW>
+template <int G, int D, int NW>
 __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const PartBuf &pb, int h,
                                                  int n, int ctx, int n_act, uint32_t my_row,
                                                  uint32_t first_row,
-                                                 const float (&s_o)[NW][G][kHeadDim],
+                                                 const float (&s_o)[NW][G][D],
                                                  const float (&s_m)[NW][G],
                                                  const float (&s_l)[NW][G], int &s_last,
                                                  MergeLds<G, NW * kWave> &s_merge) {
   constexpr int NT = NW * kWave;
-  // Workgroup state of float4 chunk c (q-head g = c / 32, elements d0 .. d0+3):
+  constexpr int kChunksPerRow = D / 4;
+  constexpr int kPartStride = part_stride(D);
+  // Workgroup state of float4 chunk c (q-head g = c / (D/4), elements d0 .. d0+3):
   // the waves' (o, m, l) rescaled to the workgroup maximum.
   auto wg_state4 = [&](int c, f32x4 &O, float &M, float &L) {
     const int g = c / kChunksPerRow, d0 = 4 * (c % kChunksPerRow);
@@ -534,7 +558,8 @@ __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const Part
       f32x4 O;
       float M, L;
       wg_state4(c, O, M, L);
-      write_outputs4(a, (int64_t)h * G + c / kChunksPerRow, 4 * (c % kChunksPerRow), O, M, L);
+      write_outputs4<D>(a, (int64_t)h * G + c / kChunksPerRow, 4 * (c % kChunksPerRow), O, M,
+                        L);
     }
     if (threadIdx.x == 0 && a.work != nullptr) add_work(a, n, ctx);
     return;
@@ -546,7 +571,7 @@ __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const Part
     wg_state4(c, O, M, L);
     const int g = c / kChunksPerRow, d0 = 4 * (c % kChunksPerRow);
     pb.store4(my_off + g * kPartStride + d0, O);
-    if (d0 == 0) pb.store2(my_off + g * kPartStride + kHeadDim, f32x2{M, L});
+    if (d0 == 0) pb.store2(my_off + g * kPartStride + D, f32x2{M, L});
   }
   // Every wave's partial stores have completed before the counter moves.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -561,8 +586,8 @@ __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const Part
     // Last contributor of the head: merge its partials, write the outputs.
     if (threadIdx.x == 0)
       __hip_atomic_store(&a.counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_partials<G, NT>(a, pb, first_row * (uint32_t)(G * kPartStride), n_act, h, n, ctx,
-                          s_merge);
+    merge_partials<G, D, NT>(a, pb, first_row * (uint32_t)(G * kPartStride), n_act, h, n,
+                             ctx, s_merge);
   }
 }
 
@@ -575,7 +600,7 @@ struct WalkLds {
     typename Engine::Lds eng[NW];
     MergeLds<G, NW * kWave> merge;
   };
-  float o[NW][G][kHeadDim] __attribute__((aligned(16)));
+  float o[NW][G][Engine::kD] __attribute__((aligned(16)));
   float m[NW][G];
   float l[NW][G];
   int last;
@@ -630,7 +655,7 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
 
   Engine eng;
   eng.init(a, b, h, lane, s_eng_of(L.tail.eng, wave));
-  const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * kHeadDim;  // between blocks
+  const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * Engine::kD;  // between blocks
   const int npw = max(0, (r1 - r0 - wave + NW - 1) / NW);
   for (int c0 = 0; c0 < npw; c0 += kWave) {
     const int cn = min(kWave, npw - c0);
@@ -671,7 +696,8 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
   eng.template finish<NW>(wave, lane, L.o, L.m, L.l);
   __syncthreads();
   const PartBuf pb(a.part, a.part_bytes);
-  segment_epilogue<G, NW>(a, pb, bh, n, ctx, n_act, (uint32_t)(bh * a.n_splits + split),
+  segment_epilogue<G, Engine::kD, NW>(a, pb, bh, n, ctx, n_act,
+                                      (uint32_t)(bh * a.n_splits + split),
                           (uint32_t)(bh * a.n_splits), L.o, L.m, L.l, L.last, L.tail.merge);
 }
 
@@ -695,7 +721,7 @@ constexpr int kSpecScorePPW = 8;
 // n_splits), bit for bit listed_decode_kernel; they run only if
 // spec_state[0] predicts that the check keeps its selection, and workgroup 0
 // records in spec_state[1] whether they ran.  The other workgroups score
-// pages as score_pages_quad_kernel does (score_body.h; kSpecScorePPW pages
+// pages as score_pages_group_kernel<128, ...> does (score_body.h; kSpecScorePPW pages
 // per wave, workgroup x of sequence b at index n_dec + b * score_gx + x).
 // The parts share no memory: the decode reads the cached selection, which
 // only the check's select-or-keep, launched after this kernel, rewrites.
@@ -718,7 +744,7 @@ void score_spec_kernel(const DecodeArgs a,
   const int w = blockIdx.x;
   if (w >= n_dec) {  // uniform
     const int sw = w - n_dec;
-    score_quad_wave<kSpecScorePPW>(s, a.H_kv, (sw % score_gx) * NW + wave, sw / score_gx);
+    score_group_wave<128, kSpecScorePPW>(s, a.H_kv, (sw % score_gx) * NW + wave, sw / score_gx);
     return;
   }
   const int split = w % a.n_splits;
@@ -786,7 +812,8 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int w = blockIdx.x;
   const int heads = a.heads;
-  const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * kHeadDim;  // between blocks
+  constexpr int D = Engine::kD;
+  const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * D;  // between blocks
 
   // Verified launches whose heads are all accepted (a lazy check that keeps
   // its selection, or a scoring step whose gate passes everywhere) run the
@@ -980,8 +1007,8 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   for (int hh = w; hh < heads; hh += n_wg) {
     if (s_start[hh + 1] != s_start[hh]) continue;  // uniform
     const int64_t row0 = (int64_t)hh * G;
-    for (int i = threadIdx.x; i < G * kHeadDim; i += NT)
-      write_outputs(a, row0 + i / kHeadDim, i % kHeadDim, 0.f, -INFINITY, 0.f);
+    for (int i = threadIdx.x; i < G * D; i += NT)
+      write_outputs<D>(a, row0 + i / D, i % D, 0.f, -INFINITY, 0.f);
     if (threadIdx.x == 0 && a.work != nullptr) add_work(a, 0, a.ctx_lens[hh / a.H_kv]);
   }
   if (T == 0) return;
@@ -1031,7 +1058,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     __syncthreads();
 
     const int first = part.owner(P);
-    segment_epilogue<G, NW>(a, pb, h, n, ctx, part.owner(P + n - 1) - first + 1,
+    segment_epilogue<G, D, NW>(a, pb, h, n, ctx, part.owner(P + n - 1) - first + 1,
                             (uint32_t)(w + h), (uint32_t)(first + h), s_o, s_m, s_l, s_last,
                             s_tail.merge);
     __syncthreads();  // LDS is reused by the next segment
@@ -1063,7 +1090,7 @@ struct DecodeLaunch {
   int grid_x, grid_y;
   int pps, n_splits;    // listed partition
   int sk_grid;          // stream-K partition (<= kMaxSplits workgroups)
-  size_t partial_rows;  // rows of G x kPartStride fp32 (0: no workspace)
+  size_t partial_rows;  // rows of G x part_stride(D) fp32 (0: no workspace)
 };
 
 static DecodeLaunch plan_launch(int B, int H_kv, int max_sel, int W, bool listed,
@@ -1119,13 +1146,16 @@ static DecodeLaunch plan_launch(int B, int H_kv, int max_sel, int W, bool listed
 constexpr size_t kCounterAreaBytes = (size_t)kMaxHeads * sizeof(unsigned);
 static_assert(kCounterAreaBytes % 256 == 0, "partial rows start 256-byte aligned");
 
-static size_t workspace_bytes_for(int B, int H_q, int H_kv, int max_sel, int W, bool listed,
-                                  bool all_pages) {
+static size_t workspace_bytes_for(int B, int H_q, int H_kv, int D, int max_sel, int W,
+                                  bool listed, bool all_pages) {
   const int G = H_q / H_kv;
   const DecodeLaunch p = plan_launch(B, H_kv, max_sel, W, listed, all_pages);
   if (p.partial_rows == 0) return 0;
-  return kCounterAreaBytes + p.partial_rows * G * kPartStride * sizeof(float);
+  return kCounterAreaBytes + p.partial_rows * G * part_stride(D) * sizeof(float);
 }
+
+// Head dimensions with decode kernels.
+static bool decode_head_dim(int D) { return D == 64 || D == 128 || D == 256; }
 
 // Argument checks of a decode launch (everything but the workspace) and its
 // launch plan; fills the launch-shape fields of `a`.  Returns a status.
@@ -1141,9 +1171,9 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   const int G = H_q / H_kv;
   CVSA_REQUIRE(G >= 1 && G <= 8, CVSA_ERR_UNSUPPORTED,
                "%s: GQA group size %d not in 1..8", name, G);
-  CVSA_REQUIRE(D == kHeadDim && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
-               "%s: only D=128, block_size=16 are supported (got D=%d, bs=%d)", name, D,
-               block_size);
+  CVSA_REQUIRE(decode_head_dim(D) && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
+               "%s: D=%d, block_size=%d not supported (D in {64, 128, 256}, block_size 16)",
+               name, D, block_size);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
                kMaxPages);
   CVSA_REQUIRE(a.bt_sb >= W, CVSA_ERR_INVALID, "%s: block-table row stride %lld < W=%d",
@@ -1175,7 +1205,7 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   CVSA_REQUIRE((!p.streamk && p.partial_rows == 0) || (int64_t)B * H_kv <= kMaxHeads,
                CVSA_ERR_UNSUPPORTED, "%s: B * H_kv = %lld exceeds %d heads per launch", name,
                (long long)B * H_kv, kMaxHeads);
-  need = workspace_bytes_for(B, H_q, H_kv, listed ? a.max_sel : 0, W, listed, all_pages);
+  need = workspace_bytes_for(B, H_q, H_kv, D, listed ? a.max_sel : 0, W, listed, all_pages);
   CVSA_REQUIRE(need == 0 || need - kCounterAreaBytes < ((size_t)1 << 31),
                CVSA_ERR_UNSUPPORTED,
                "%s: %zu bytes of split partials exceed the 2 GiB buffer range", name,
@@ -1186,6 +1216,7 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   a.pps = p.pps;
   a.n_splits = p.n_splits;
   a.sk_grid = p.sk_grid;
+  a.D = D;
   a.scale = (float)pow((double)D, -0.5);
   return CVSA_OK;
 }
@@ -1203,21 +1234,31 @@ static int enqueue_decode(const char *name, DecodeArgs a, int G, bool listed,
                           const DecodeLaunch &p, void *workspace, size_t need, hipStream_t st) {
   bind_workspace(a, workspace, need);
   const dim3 grid(p.grid_x, p.grid_y), block(kWavesPerWg * kWave);
-#define CVSA_DEC_LAUNCH(GG, ENG)                                                             \
+  // Pages of K/V in flight per wave: 2, or 1 at D = 256, whose pages hold
+  // twice the registers.
+#define CVSA_DEC_LAUNCH(GG, DD)                                                              \
   do {                                                                                       \
+    constexpr int PDD = DD > 128 ? 1 : 2;                                                    \
     if (!p.streamk)                                                                          \
-      hipLaunchKernelGGL((listed_decode_kernel<GG, ENG, kWavesPerWg, 2>), grid, block, 0, st, \
-                         a);                                                                 \
-    else if (listed)                                                                         \
-      hipLaunchKernelGGL((streamk_decode_kernel<GG, ENG, kWavesPerWg, 2, kModeVerified>),    \
+      hipLaunchKernelGGL((listed_decode_kernel<GG, MfmaEngine<GG, DD>, kWavesPerWg, PDD>),   \
                          grid, block, 0, st, a);                                             \
+    else if (listed)                                                                         \
+      hipLaunchKernelGGL(                                                                    \
+          (streamk_decode_kernel<GG, MfmaEngine<GG, DD>, kWavesPerWg, PDD, kModeVerified>),  \
+          grid, block, 0, st, a);                                                            \
     else                                                                                     \
-      hipLaunchKernelGGL((streamk_decode_kernel<GG, ENG, kWavesPerWg, 2, kModeAll>), grid,   \
-                         block, 0, st, a);                                                   \
+      hipLaunchKernelGGL(                                                                    \
+          (streamk_decode_kernel<GG, MfmaEngine<GG, DD>, kWavesPerWg, PDD, kModeAll>), grid, \
+          block, 0, st, a);                                                                  \
   } while (0)
 #define CVSA_DEC_CASE(GG)                                                                    \
   case GG:                                                                                   \
-    CVSA_DEC_LAUNCH(GG, MfmaEngine<GG>);                                                     \
+    if (a.D == 64)                                                                           \
+      CVSA_DEC_LAUNCH(GG, 64);                                                               \
+    else if (a.D == 256)                                                                     \
+      CVSA_DEC_LAUNCH(GG, 256);                                                              \
+    else                                                                                     \
+      CVSA_DEC_LAUNCH(GG, 128);                                                              \
     break;
   switch (G) {
     CVSA_DEC_CASE(1)
@@ -1288,11 +1329,11 @@ using namespace cvsa;
 extern "C" size_t cvsa_decode_workspace_bytes(int32_t B, int32_t H_q, int32_t H_kv,
                                               int32_t D, int32_t max_sel_pages, int32_t W,
                                               int32_t all_pages) {
-  (void)D;
-  if (B <= 0 || H_kv <= 0 || H_q <= 0 || H_q % H_kv != 0 || W <= 0 || max_sel_pages < 0)
+  if (B <= 0 || H_kv <= 0 || H_q <= 0 || H_q % H_kv != 0 || W <= 0 || max_sel_pages < 0 ||
+      !decode_head_dim(D))
     return 0;
   const bool listed = max_sel_pages > 0;
-  return workspace_bytes_for(B, H_q, H_kv, max_sel_pages, W, listed, all_pages != 0);
+  return workspace_bytes_for(B, H_q, H_kv, D, max_sel_pages, W, listed, all_pages != 0);
 }
 
 extern "C" int cvsa_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
@@ -1335,12 +1376,13 @@ extern "C" int cvsa_sparse_decode(const uint16_t *q, int64_t q_stride_b, int64_t
 // cvsa_sparse_decode_noalloc keeps the decode workspace in this file-scope
 // device array instead of a caller-owned buffer.  Each GPU the library runs
 // on holds its own copy until the process ends.  A listed launch needs at
-// most kCounterAreaBytes + kMaxSplits partial rows of 8 x 132 fp32 (1.1 MB:
-// plan_launch splits heads only when there are fewer than kMaxSplits of them,
-// into at most kMaxSplits / heads splits each), so every call
-// cvsa_sparse_decode accepts fits; a larger need is refused all the same.
-constexpr size_t kScratchBytes = (size_t)2 << 20;
-static_assert(kScratchBytes >= kCounterAreaBytes + (size_t)kMaxSplits * 8 * kPartStride *
+// most kCounterAreaBytes + kMaxSplits partials of G x (D + 4) fp32, G <= 8,
+// D <= 256 (2.1 MB: plan_launch splits heads only when there are fewer than
+// kMaxSplits of them, into at most kMaxSplits / heads splits each), so every
+// call cvsa_sparse_decode accepts fits; a larger need is refused all the
+// same.
+constexpr size_t kScratchBytes = (size_t)9 << 18;  // 2.25 MiB
+static_assert(kScratchBytes >= kCounterAreaBytes + (size_t)kMaxSplits * 8 * part_stride(256) *
                                                        sizeof(float),
               "scratch holds every listed launch");
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
@@ -1424,7 +1466,9 @@ extern "C" int cvsa_sparse_decode_noalloc(
 
 namespace cvsa_internal {
 
-bool score_spec_fusable(int32_t H_kv) { return H_kv >= 4 && H_kv % 4 == 0 && H_kv <= 16; }
+bool score_spec_fusable(int32_t H_kv, int32_t D) {
+  return D == 128 && H_kv >= 4 && H_kv % 4 == 0 && H_kv <= 16;
+}
 
 // A lazy check's page scoring (cvsa_score_pages into page_scores) fused
 // with the speculative decode of its cached selection (cvsa_sparse_decode
@@ -1451,8 +1495,8 @@ int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_
   a.spec_state = spec_state;
   CVSA_REQUIRE(page_indices && spec_state && page_scores, CVSA_ERR_INVALID,
                "%s: page_indices, spec_state and page_scores are required", name);
-  CVSA_REQUIRE(score_spec_fusable(H_kv), CVSA_ERR_UNSUPPORTED, "%s: H_kv=%d not in {4,8,16}",
-               name, H_kv);
+  CVSA_REQUIRE(score_spec_fusable(H_kv, D), CVSA_ERR_UNSUPPORTED,
+               "%s: H_kv=%d not in {4,8,16} or D=%d not 128", name, H_kv, D);
   DecodeLaunch p{};
   size_t need = 0;
   int rc = validate_decode(name, a, B, H_q, H_kv, D, block_size, W, true, false, p, need);
@@ -1468,7 +1512,7 @@ int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_
   hipStream_t st = (hipStream_t)stream;
 #define CVSA_SPEC_CASE(GG)                                                                   \
   case GG:                                                                                   \
-    hipLaunchKernelGGL((score_spec_kernel<GG, MfmaEngine<GG>, kWavesPerWg, 2>),             \
+    hipLaunchKernelGGL((score_spec_kernel<GG, MfmaEngine<GG, 128>, kWavesPerWg, 2>),        \
                        dim3((unsigned)grid), dim3(kWavesPerWg * kWave), 0, st, a, sa,        \
                        score_gx);                                                            \
     break;

@@ -7,8 +7,8 @@
 // token score -inf.  The reference gathers every page's keys on every call.
 // Here the extremes are kept as page metadata (as the reference's Quest
 // baseline does, eval/baselines.py:77-140) and refreshed only for the pages
-// whose valid-token count changed, so a scoring pass reads 512 B per page
-// and head instead of the 4 KiB of keys.
+// whose valid-token count changed, so a scoring pass reads 4D bytes per page
+// and head (512 B at D = 128) instead of the 32D bytes of keys.
 //
 // Metadata layout: meta[block][h][0][d] = kmin, meta[block][h][1][d] = kmax,
 // bf16 (exact: they are key values), indexed by physical block;
@@ -56,13 +56,14 @@ __device__ __forceinline__ void segment_minmax(const uint16_t *__restrict__ rows
   mx = make_uint4(pack(hi[0], hi[1]), pack(hi[2], hi[3]), pack(hi[4], hi[5]), pack(hi[6], hi[7]));
 }
 
-// One wave per (b, kv-head, run of ppw pages, a multiple of 16): lanes
-// 16j .. 16j+15 take page j of each group of four; lane seg = l % 16 holds
-// dimensions 8seg .. 8seg+7 (16 bytes of kmin and 16 of kmax, read whole by
-// the 16 lanes) and q_rep's matching segment; the 16-lane sum is formed with
-// DPP.  Sixteen pages are in flight per wave: their block-table entries are
-// read first, then their metadata, so each run of 16 pays two load
-// latencies.
+// One wave per (b, kv-head, run of ppw pages, a multiple of 16), LPR = D / 8
+// lanes per page: lanes LPR*j .. LPR*j+LPR-1 take page j of each group of
+// RPL = 64 / LPR pages (8, 4, 2 at D = 64, 128, 256); lane seg = l % LPR
+// holds dimensions 8seg .. 8seg+7 (16 bytes of kmin and 16 of kmax, read
+// whole by the LPR lanes) and q_rep's matching segment; the LPR-lane sum is
+// formed with DPP (and a permlane swap at LPR = 32).  Sixteen pages are in
+// flight per wave: their block-table entries are read first, then their
+// metadata, so each run of 16 pays two load latencies.
 //
 // REFRESH: pages whose valid-token count differs from meta_ntok are
 // recomputed from k_cache, written back (extremes and count) and scored
@@ -70,7 +71,7 @@ __device__ __forceinline__ void segment_minmax(const uint16_t *__restrict__ rows
 // check_accept (optional, n_heads flags): when every flag is set the
 // launch does nothing; a lazy check that kept its selection needs no
 // ranking scores.
-template <bool REFRESH, bool SCORE>
+template <int D, bool REFRESH, bool SCORE>
 __global__ __launch_bounds__(256) void quest_scores_kernel(
     const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh, uint16_t *__restrict__ meta,
     int32_t *__restrict__ meta_ntok, int64_t num_blocks,
@@ -78,7 +79,9 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
     const int32_t *__restrict__ context_lens, const uint16_t *__restrict__ k_cache,
     const uint8_t *__restrict__ check_accept, int n_heads, int H_kv, int G, float inv_g,
     float scale, int W, int ppw, float *__restrict__ scores) {
-  constexpr int kIter = 4;  // groups of four pages per run of sixteen
+  constexpr int LPR = D / 8;
+  constexpr int RPL = kWave / LPR;  // pages per wave load
+  constexpr int kIter = 16 / RPL;   // wave loads per run of sixteen pages
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int bh = blockIdx.y;
@@ -86,8 +89,8 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
   const int h = bh - b * H_kv;
   const int p0 = (blockIdx.x * 4 + wave) * ppw;
   if (p0 >= W) return;
-  const int seg = lane & 15;
-  const int sub = lane >> 4;
+  const int seg = lane % LPR;
+  const int sub = lane / LPR;
   const int p_end = min(W, p0 + ppw);
   // Block-table entries of the next run of 16 pages: the first run's are
   // requested before the check flags and the query rows, so their
@@ -96,7 +99,7 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
   auto load_phys = [&](int pb) {
 #pragma unroll
     for (int i = 0; i < kIter; ++i)
-      phys[i] = block_tables[b * bt_sb + min(pb + 4 * i + sub, p_end - 1)];
+      phys[i] = block_tables[b * bt_sb + min(pb + RPL * i + sub, p_end - 1)];
   };
   load_phys(p0);
   if (check_accept != nullptr) {
@@ -113,12 +116,12 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
     qf[4] = bf16_lo(qv.z); qf[5] = bf16_hi(qv.z);
     qf[6] = bf16_lo(qv.w); qf[7] = bf16_hi(qv.w);
   }
-  const int64_t row_stride = (int64_t)H_kv * kHeadDim;  // between tokens of a block
-  for (int pb = p0; pb < p_end; pb += kIter * 4) {
+  const int64_t row_stride = (int64_t)H_kv * D;  // between tokens of a block
+  for (int pb = p0; pb < p_end; pb += kIter * RPL) {
     bool valid[kIter];
 #pragma unroll
     for (int i = 0; i < kIter; ++i) {
-      const int p = pb + 4 * i + sub;
+      const int p = pb + RPL * i + sub;
       valid[i] = p < p_end && p * kPageTokens < ctx && phys[i] >= 0 && phys[i] < num_blocks;
     }
     uint4 mn[kIter], mx[kIter];
@@ -127,27 +130,29 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
     for (int i = 0; i < kIter; ++i) {
       const int64_t slot = (int64_t)(valid[i] ? phys[i] : 0) * H_kv + h;
       if (SCORE) {
-        const uint16_t *m = meta + slot * 2 * kHeadDim + 8 * seg;
+        const uint16_t *m = meta + slot * 2 * D + 8 * seg;
         mn[i] = *reinterpret_cast<const uint4 *>(m);
-        mx[i] = *reinterpret_cast<const uint4 *>(m + kHeadDim);
+        mx[i] = *reinterpret_cast<const uint4 *>(m + D);
       }
       if (REFRESH) have[i] = meta_ntok[slot];
     }
-    const int cur[kIter] = {phys[0], phys[1], phys[2], phys[3]};
-    if (pb + kIter * 4 < p_end) load_phys(pb + kIter * 4);
+    int cur[kIter];
+#pragma unroll
+    for (int i = 0; i < kIter; ++i) cur[i] = phys[i];
+    if (pb + kIter * RPL < p_end) load_phys(pb + kIter * RPL);
     if (REFRESH) {
 #pragma unroll
       for (int i = 0; i < kIter; ++i) {
-        const int p = pb + 4 * i + sub;
+        const int p = pb + RPL * i + sub;
         const int ntok = min(kPageTokens, ctx - p * kPageTokens);
         if (valid[i] && have[i] != ntok) {
           const int64_t slot = (int64_t)cur[i] * H_kv + h;
           segment_minmax(k_cache + (int64_t)cur[i] * kPageTokens * row_stride +
-                             (int64_t)h * kHeadDim + 8 * seg,
+                             (int64_t)h * D + 8 * seg,
                          row_stride, ntok, mn[i], mx[i]);
-          uint16_t *m = meta + slot * 2 * kHeadDim + 8 * seg;
+          uint16_t *m = meta + slot * 2 * D + 8 * seg;
           *reinterpret_cast<uint4 *>(m) = mn[i];
-          *reinterpret_cast<uint4 *>(m + kHeadDim) = mx[i];
+          *reinterpret_cast<uint4 *>(m + D) = mx[i];
           if (seg == 0) meta_ntok[slot] = ntok;
         }
       }
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
       float *out = scores + (int64_t)bh * W;
 #pragma unroll
       for (int i = 0; i < kIter; ++i) {
-        const int p = pb + 4 * i + sub;
+        const int p = pb + RPL * i + sub;
         const uint32_t lo[4] = {mn[i].x, mn[i].y, mn[i].z, mn[i].w};
         const uint32_t hi[4] = {mx[i].x, mx[i].y, mx[i].z, mx[i].w};
         float acc = 0.f;
@@ -165,7 +170,7 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
           acc += fmaxf(qf[2 * e] * bf16_lo(lo[e]), qf[2 * e] * bf16_lo(hi[e]));
           acc += fmaxf(qf[2 * e + 1] * bf16_hi(lo[e]), qf[2 * e + 1] * bf16_hi(hi[e]));
         }
-        acc = group_sum<16>(acc) * scale;
+        acc = group_sum<LPR>(acc) * scale;
         if (seg == 0 && p < p_end) out[p] = valid[i] ? acc : -INFINITY;
       }
     }
@@ -191,9 +196,8 @@ int check_quest_sizes(const char *name, int32_t B, int32_t H_kv, int32_t D, int3
                       int32_t W, int64_t num_blocks, int64_t bt_stride_b, const void *meta) {
   CVSA_REQUIRE(B > 0 && H_kv > 0 && (int64_t)B * H_kv <= 65535 && W > 0 && num_blocks > 0,
                CVSA_ERR_INVALID, "%s: bad sizes B=%d H_kv=%d W=%d", name, B, H_kv, W);
-  CVSA_REQUIRE(D == kHeadDim && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
-               "%s: only D=128, block_size=16 are supported (got D=%d, bs=%d)", name, D,
-               block_size);
+  CVSA_REQUIRE(head_dim_supported(D) && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
+               "%s: D=%d not in {64, 128, 256} or block_size=%d not 16", name, D, block_size);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
                kMaxPages);
   CVSA_REQUIRE(bt_stride_b >= W, CVSA_ERR_INVALID, "%s: block-table row stride %lld < W=%d",
@@ -230,9 +234,18 @@ extern "C" int cvsa_quest_meta_update(const uint16_t *k_cache, int64_t num_block
                "%s: k_cache must be 16-byte aligned", name);
   int ppw;
   const dim3 grid = quest_grid(B, H_kv, W, ppw);
-  hipLaunchKernelGGL((quest_scores_kernel<true, false>), grid, dim3(256), 0, (hipStream_t)stream,
-                     nullptr, 0, 0, meta, meta_ntok, num_blocks, block_tables, bt_stride_b,
-                     context_lens, k_cache, nullptr, 0, H_kv, 1, 1.0f, 1.0f, W, ppw, nullptr);
+#define CVSA_QUEST_REFRESH(DD)                                                               \
+  hipLaunchKernelGGL((quest_scores_kernel<DD, true, false>), grid, dim3(256), 0,             \
+                     (hipStream_t)stream, nullptr, 0, 0, meta, meta_ntok, num_blocks,        \
+                     block_tables, bt_stride_b, context_lens, k_cache, nullptr, 0, H_kv, 1,  \
+                     1.0f, 1.0f, W, ppw, nullptr)
+  if (D == 64)
+    CVSA_QUEST_REFRESH(64);
+  else if (D == 256)
+    CVSA_QUEST_REFRESH(256);
+  else
+    CVSA_QUEST_REFRESH(128);
+#undef CVSA_QUEST_REFRESH
   return cvsa_host::check_launch(name);
 }
 
@@ -252,10 +265,20 @@ extern "C" int cvsa_quest_scores(const uint16_t *q, int64_t q_stride_b, int64_t 
   int ppw;
   const dim3 grid = quest_grid(B, H_kv, W, ppw);
   // Without refresh the kernel only reads the metadata.
-  hipLaunchKernelGGL((quest_scores_kernel<false, true>), grid, dim3(256), 0, (hipStream_t)stream,
-                     q, q_stride_b, q_stride_h, const_cast<uint16_t *>(meta), nullptr, num_blocks,
-                     block_tables, bt_stride_b, context_lens, nullptr, nullptr, 0, H_kv, G,
-                     1.0f / (float)G, (float)pow((double)D, -0.5), W, ppw, page_scores);
+  const float scale = (float)pow((double)D, -0.5);
+#define CVSA_QUEST_SCORE(DD)                                                                 \
+  hipLaunchKernelGGL((quest_scores_kernel<DD, false, true>), grid, dim3(256), 0,             \
+                     (hipStream_t)stream, q, q_stride_b, q_stride_h,                         \
+                     const_cast<uint16_t *>(meta), nullptr, num_blocks, block_tables,        \
+                     bt_stride_b, context_lens, nullptr, nullptr, 0, H_kv, G,                \
+                     1.0f / (float)G, scale, W, ppw, page_scores)
+  if (D == 64)
+    CVSA_QUEST_SCORE(64);
+  else if (D == 256)
+    CVSA_QUEST_SCORE(256);
+  else
+    CVSA_QUEST_SCORE(128);
+#undef CVSA_QUEST_SCORE
   return cvsa_host::check_launch(name);
 }
 
@@ -278,9 +301,19 @@ extern "C" int cvsa_quest_refresh_scores(const uint16_t *q, int64_t q_stride_b,
   const int G = H_q / H_kv;
   int ppw;
   const dim3 grid = quest_grid(B, H_kv, W, ppw);
-  hipLaunchKernelGGL((quest_scores_kernel<true, true>), grid, dim3(256), 0, (hipStream_t)stream,
-                     q, q_stride_b, q_stride_h, meta, meta_ntok, num_blocks, block_tables,
-                     bt_stride_b, context_lens, k_cache, check_accept, B * H_kv, H_kv, G,
-                     1.0f / (float)G, (float)pow((double)D, -0.5), W, ppw, page_scores);
+  const float scale = (float)pow((double)D, -0.5);
+#define CVSA_QUEST_BOTH(DD)                                                                   \
+  hipLaunchKernelGGL((quest_scores_kernel<DD, true, true>), grid, dim3(256), 0,               \
+                     (hipStream_t)stream, q, q_stride_b, q_stride_h, meta, meta_ntok,         \
+                     num_blocks, block_tables, bt_stride_b, context_lens, k_cache,            \
+                     check_accept, B * H_kv, H_kv, G, 1.0f / (float)G, scale, W, ppw,         \
+                     page_scores)
+  if (D == 64)
+    CVSA_QUEST_BOTH(64);
+  else if (D == 256)
+    CVSA_QUEST_BOTH(256);
+  else
+    CVSA_QUEST_BOTH(128);
+#undef CVSA_QUEST_BOTH
   return cvsa_host::check_launch(name);
 }

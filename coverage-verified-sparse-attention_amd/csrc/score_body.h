@@ -1,6 +1,6 @@
-// Page scoring of one wave in the quad layout (H_kv a multiple of 4), shared
-// by the scoring kernel and the lazy check's fused scoring + speculative
-// decode launch.
+// Page scoring of one wave in the head-group layout (H_kv a multiple of the
+// heads one wave load covers), shared by the scoring kernel and the lazy
+// check's fused scoring + speculative decode launch.
 //
 // page_scores[b,h,p] = max over valid tokens of (q_rep . K) * D^-0.5, as
 // triton_score_pages (cvsa/kernels/page_scores.py:77-119, kernel :12-74):
@@ -27,25 +27,29 @@ struct ScoreArgs {
   float inv_g, scale;
 };
 
-// Wave gw of sequence b owns KV-head quad hq = gw % (hkv / 4) of pages
-// [(gw / (hkv / 4)) * PPW, +PPW).  For each token of a page, the quad's four
-// 256-byte rows are contiguous (1 KiB), so one 16-byte load per lane reads
-// them whole: lane l holds head 4*hq + (l >> 4), d-segment (l & 15) * 8.  The
-// 16 lanes of a DPP row finish the dot product with four fused DPP adds, and
-// each lane keeps the running max of its head.  The wave's block-table
+// Wave gw of sequence b owns head group hg = gw % (hkv / R) of pages
+// [(gw / (hkv / R)) * PPW, +PPW), where LPR = D / 8 lanes hold one 2D-byte
+// key row and R = 64 / LPR rows make one wave load (R = 8, 4, 2 heads at
+// D = 64, 128, 256).  For each token of a page, the group's R rows are
+// contiguous (1 KiB), so one 16-byte load per lane reads them whole: lane l
+// holds head R*hg + l / LPR, d-segment (l % LPR) * 8.  The LPR lanes of a
+// row finish the dot product with DPP adds (and a permlane swap at LPR = 32),
+// and each lane keeps the running max of its head.  The wave's block-table
 // entries are fetched once (lane j: page j) and the next page's keys are
 // requested before the current page is reduced.  hkv is a compile-time
 // constant where the caller's is.
-template <int PPW>
-__device__ __forceinline__ void score_quad_wave(const ScoreArgs &s, int hkv, int gw, int b) {
-  const int nq = hkv / 4;  // quads per page
+template <int D, int PPW>
+__device__ __forceinline__ void score_group_wave(const ScoreArgs &s, int hkv, int gw, int b) {
+  constexpr int LPR = D / 8;
+  constexpr int R = kWave / LPR;
+  const int ng = hkv / R;  // head groups per page
   const int lane = threadIdx.x & 63;
-  const int hq = gw % nq;
-  const int p_begin = (gw / nq) * PPW;
+  const int hg = gw % ng;
+  const int p_begin = (gw / ng) * PPW;
   const int W = s.W;
   if (p_begin >= W) return;
-  const int h = 4 * hq + (lane >> 4);
-  const int seg = lane & 15;
+  const int h = R * hg + lane / LPR;
+  const int seg = lane % LPR;
   const int ctx = __builtin_amdgcn_readfirstlane(s.context_lens[b]);
   const int n = min(PPW, W - p_begin);
 
@@ -60,8 +64,8 @@ __device__ __forceinline__ void score_quad_wave(const ScoreArgs &s, int hkv, int
     }
   }
   const uint4 qr = group_mean_q(s.q, s.q_sb, s.q_sh, b, h, s.G, seg, s.inv_g);
-  const int64_t lane_off = (int64_t)hq * 4 * kHeadDim + lane * 8;
-  const int64_t row_stride = (int64_t)hkv * kHeadDim;
+  const int64_t lane_off = (int64_t)hg * R * D + lane * 8;
+  const int64_t row_stride = (int64_t)hkv * D;
   const int64_t page_elems = kPageTokens * row_stride;
 
   // Unconditional loads (block 0 for pages without valid tokens) keep the
@@ -80,7 +84,7 @@ __device__ __forceinline__ void score_quad_wave(const ScoreArgs &s, int hkv, int
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < kPageTokens; ++t) {
-      const float sc = group_sum<16>(dot8_bf16(kv[t], qr, 0.f)) * s.scale;
+      const float sc = group_sum<LPR>(dot8_bf16(kv[t], qr, 0.f)) * s.scale;
       if (t < ntok) mx = fmaxf(mx, sc);
     }
     if (seg == 0) s.scores[((int64_t)b * hkv + h) * W + p] = mx;

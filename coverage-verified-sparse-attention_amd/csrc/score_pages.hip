@@ -7,40 +7,47 @@
 //
 // MI355X mapping: the reference runs one tiny program per (b, kv-head, page).
 // Here a wave streams whole 1 KiB runs of a page: a page is block_size x H_kv
-// rows of 256 B stored back to back (32 KiB for H_kv = 8), so every 16-byte
-// lane load is part of a fully coalesced 1 KiB wave load, and the 16 lanes of
-// a DPP row hold one (token, head) row and reduce its dot product with four
-// fused DPP adds.
+// rows of 2D bytes stored back to back (32 KiB for H_kv = 8, D = 128), so
+// every 16-byte lane load is part of a fully coalesced 1 KiB wave load, and
+// the D / 8 lanes that hold one (token, head) row reduce its dot product
+// with DPP adds.
 #include "cvsa_common.h"
 #include "score_body.h"
 
 namespace cvsa {
 
-// H_kv >= 4: a wave owns four KV heads ("quad") of PPW pages (score_body.h).
-template <int HKV, int PPW>
-__global__ __launch_bounds__(256) void score_pages_quad_kernel(const ScoreArgs s) {
-  static_assert(HKV >= 4 && HKV % 4 == 0, "quad layout");
-  score_quad_wave<PPW>(s, HKV, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
-                       blockIdx.y);
+// Heads of one 1 KiB wave load at head dimension D: 64 / (D / 8).
+constexpr int rows_per_load(int D) { return kWave / (D / 8); }
+
+// H_kv a multiple of R = rows_per_load(D): a wave owns R KV heads of PPW
+// pages (score_body.h).
+template <int D, int HKV, int PPW>
+__global__ __launch_bounds__(256) void score_pages_group_kernel(const ScoreArgs s) {
+  static_assert(HKV % rows_per_load(D) == 0, "head-group layout");
+  score_group_wave<D, PPW>(s, HKV, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+                           blockIdx.y);
 }
 
-// H_kv < 4: one wave streams a whole page; lane l covers row (l >> 4) of
-// each group of four (token, head) rows and d-segment (l & 15) * 8.
-template <int HKV>
+// H_kv < R: one wave streams a whole page; lane l covers row l / LPR of each
+// group of R (token, head) rows and d-segment (l % LPR) * 8 (LPR = D / 8).
+template <int D, int HKV>
 __global__ __launch_bounds__(256) void score_pages_kernel(
     const uint16_t *__restrict__ q, int64_t q_sb, int64_t q_sh,
     const uint16_t *__restrict__ k_cache, int64_t num_blocks,
     const int32_t *__restrict__ block_tables, int64_t bt_sb,
     const int32_t *__restrict__ context_lens, float *__restrict__ scores,
     int W, int G, float inv_g, float scale, int ppw) {
-  static_assert(HKV < 4, "small-head layout");
-  constexpr int NLOAD = kPageTokens * HKV / 4;     // 16-byte loads per lane per page
-  constexpr int PAGE_ELEMS = kPageTokens * HKV * kHeadDim;
+  constexpr int LPR = D / 8;
+  constexpr int R = rows_per_load(D);
+  static_assert(HKV < R && R % HKV == 0, "small-head layout");
+  constexpr int NLOAD = kPageTokens * HKV / R;     // 16-byte loads per lane per page
+  constexpr int PAGE_ELEMS = kPageTokens * HKV * D;
+  constexpr int S = HKV * LPR;                     // lane distance between rows of one head
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rsub = lane >> 4;
-  const int seg = lane & 15;
+  const int rsub = lane / LPR;
+  const int seg = lane % LPR;
   const int b = blockIdx.y;
   const int p_begin = (blockIdx.x * 4 + wave) * ppw;
   if (p_begin >= W) return;
@@ -65,18 +72,19 @@ __global__ __launch_bounds__(256) void score_pages_kernel(
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < NLOAD; ++i) {
-      const int t = (i * 4 + rsub) / HKV;
-      const float s = group_sum<16>(dot8_bf16(kv[i], qr, 0.f)) * scale;
-      if (t < ntok) mx = fmaxf(mx, s);
+      const int t = (i * R + rsub) / HKV;
+      const float sc = group_sum<LPR>(dot8_bf16(kv[i], qr, 0.f)) * scale;
+      if (t < ntok) mx = fmaxf(mx, sc);
     }
-    // Several row groups share a head: combine them.
+    // Rows of one head sit S lanes apart: combine them.
     float a, c;
-    if constexpr (HKV == 1) {
-      xchg16(mx, a, c); mx = fmaxf(a, c);
-      xchg32(mx, a, c); mx = fmaxf(a, c);
-    } else {
-      xchg32(mx, a, c); mx = fmaxf(a, c);
+    if constexpr (S <= 8) mx = fmaxf(mx, dpp_f<kDppRowRor8>(mx));
+    if constexpr (S <= 16) {
+      xchg16(mx, a, c);
+      mx = fmaxf(a, c);
     }
+    xchg32(mx, a, c);
+    mx = fmaxf(a, c);
     if (seg == 0 && rsub < HKV) dst[(int64_t)h * W] = mx;
   }
 }
@@ -101,9 +109,11 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
                (long long)num_blocks);
   CVSA_REQUIRE(H_kv > 0 && H_q > 0 && H_q % H_kv == 0, CVSA_ERR_INVALID,
                "score_pages: H_q=%d is not a multiple of H_kv=%d", H_q, H_kv);
-  CVSA_REQUIRE(D == kHeadDim && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
-               "score_pages: only D=128, block_size=16 are supported (got D=%d, bs=%d)",
-               D, block_size);
+  CVSA_REQUIRE(head_dim_supported(D) && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
+               "score_pages: D=%d not in {64, 128, 256} or block_size=%d not 16", D,
+               block_size);
+  CVSA_REQUIRE(H_kv == 1 || H_kv == 2 || H_kv == 4 || H_kv == 8 || H_kv == 16,
+               CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d not in {1,2,4,8,16}", H_kv);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
                "score_pages: W=%d exceeds %d pages", W, kMaxPages);
   CVSA_REQUIRE(bt_stride_b >= W, CVSA_ERR_INVALID,
@@ -119,48 +129,51 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
   const float scale = (float)pow((double)D, -0.5);
 
   hipStream_t st = (hipStream_t)stream;
-  if (H_kv >= 4) {
-    // Quad layout: waves = pages / PPW x H_kv / 4.  As many pages per wave
-    // (up to 8) as keep >= ~2048 waves (8 per CU) in the launch: the setup
-    // (q_rep, block-table fetch) is amortised over more pages, and the
+  const int R = kWave / (D / 8);
+  if (H_kv % R == 0) {
+    // Head-group layout: waves = pages / PPW x H_kv / R.  As many pages per
+    // wave (up to 8) as keep >= ~2048 waves (8 per CU) in the launch: the
+    // setup (q_rep, block-table fetch) is amortised over more pages, and the
     // last-wave tail stays short.
-    const int64_t quad_pages = (int64_t)B * W * (H_kv / 4);
+    const int64_t group_pages = (int64_t)B * W * (H_kv / R);
     int ppw = 1;
-    while (ppw < 8 && quad_pages / (2 * ppw) >= 2048) ppw *= 2;
-    const int64_t waves = ((W + ppw - 1) / ppw) * (int64_t)(H_kv / 4);
+    while (ppw < 8 && group_pages / (2 * ppw) >= 2048) ppw *= 2;
+    const int64_t waves = ((W + ppw - 1) / ppw) * (int64_t)(H_kv / R);
     dim3 grid((unsigned)((waves + 3) / 4), B);
     const ScoreArgs sa{q, q_stride_b, q_stride_h, k_cache, (int64_t)num_blocks, block_tables,
                        bt_stride_b, context_lens, page_scores, W, G, inv_g, scale};
-#define CVSA_QUAD_CASE(HK, PP)                                                          \
-  if (H_kv == HK && ppw == PP) {                                                        \
-    hipLaunchKernelGGL((score_pages_quad_kernel<HK, PP>), grid, dim3(256), 0, st, sa);  \
-    return cvsa_host::check_launch("score_pages");                                      \
+#define CVSA_GROUP_CASE(DD, HK, PP)                                                          \
+  if (D == DD && H_kv == HK && ppw == PP) {                                                  \
+    hipLaunchKernelGGL((score_pages_group_kernel<DD, HK, PP>), grid, dim3(256), 0, st, sa);  \
+    return cvsa_host::check_launch("score_pages");                                           \
   }
-    CVSA_QUAD_CASE(4, 1) CVSA_QUAD_CASE(4, 2) CVSA_QUAD_CASE(4, 4) CVSA_QUAD_CASE(4, 8)
-    CVSA_QUAD_CASE(8, 1) CVSA_QUAD_CASE(8, 2) CVSA_QUAD_CASE(8, 4) CVSA_QUAD_CASE(8, 8)
-    CVSA_QUAD_CASE(16, 1) CVSA_QUAD_CASE(16, 2) CVSA_QUAD_CASE(16, 4) CVSA_QUAD_CASE(16, 8)
-#undef CVSA_QUAD_CASE
-    return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d not in {1,2,4,8,16}",
-                           H_kv);
+#define CVSA_GROUP_PPW(DD, HK) \
+  CVSA_GROUP_CASE(DD, HK, 1) CVSA_GROUP_CASE(DD, HK, 2) CVSA_GROUP_CASE(DD, HK, 4) \
+  CVSA_GROUP_CASE(DD, HK, 8)
+    CVSA_GROUP_PPW(64, 8) CVSA_GROUP_PPW(64, 16)
+    CVSA_GROUP_PPW(128, 4) CVSA_GROUP_PPW(128, 8) CVSA_GROUP_PPW(128, 16)
+    CVSA_GROUP_PPW(256, 2) CVSA_GROUP_PPW(256, 4) CVSA_GROUP_PPW(256, 8) CVSA_GROUP_PPW(256, 16)
+#undef CVSA_GROUP_PPW
+#undef CVSA_GROUP_CASE
+    return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d, D=%d has no launch",
+                           H_kv, D);
   }
   const int64_t total = (int64_t)B * W;
   int ppw = (int)((total + 8191) / 8192);
   ppw = ppw < 1 ? 1 : (ppw > 8 ? 8 : ppw);
   dim3 grid((W + 4 * ppw - 1) / (4 * ppw), B);
-  switch (H_kv) {
-#define CVSA_SCORE_CASE(HK)                                                     \
-  case HK:                                                                      \
-    hipLaunchKernelGGL(score_pages_kernel<HK>, grid, dim3(256), 0, st, q,       \
-                       q_stride_b, q_stride_h, k_cache, (int64_t)num_blocks,    \
-                       block_tables, bt_stride_b, context_lens, page_scores, W, \
-                       G, inv_g, scale, ppw);                                   \
-    break;
-    CVSA_SCORE_CASE(1)
-    CVSA_SCORE_CASE(2)
-#undef CVSA_SCORE_CASE
-    default:
-      return cvsa_host::fail(CVSA_ERR_UNSUPPORTED,
-                             "score_pages: H_kv=%d not in {1,2,4,8,16}", H_kv);
+#define CVSA_SCORE_CASE(DD, HK)                                                          \
+  if (D == DD && H_kv == HK) {                                                           \
+    hipLaunchKernelGGL((score_pages_kernel<DD, HK>), grid, dim3(256), 0, st, q,          \
+                       q_stride_b, q_stride_h, k_cache, (int64_t)num_blocks,             \
+                       block_tables, bt_stride_b, context_lens, page_scores, W, G,       \
+                       inv_g, scale, ppw);                                               \
+    return cvsa_host::check_launch("score_pages");                                       \
   }
-  return cvsa_host::check_launch("score_pages");
+  CVSA_SCORE_CASE(64, 1) CVSA_SCORE_CASE(64, 2) CVSA_SCORE_CASE(64, 4)
+  CVSA_SCORE_CASE(128, 1) CVSA_SCORE_CASE(128, 2)
+  CVSA_SCORE_CASE(256, 1)
+#undef CVSA_SCORE_CASE
+  return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d, D=%d has no launch", H_kv,
+                         D);
 }

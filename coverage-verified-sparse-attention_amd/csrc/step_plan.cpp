@@ -27,7 +27,6 @@ struct cvsa_step_plan {
 
 namespace {
 
-constexpr int kHeadDim = 128;
 constexpr int kPageTokens = 16;
 constexpr int kMaxPages = 32768;
 constexpr int64_t kMaxDecodeHeads = 4096;
@@ -53,8 +52,9 @@ int check_desc(const cvsa_step_desc &d) {
   STEP_REQUIRE((int64_t)d.B * d.H_kv <= kMaxDecodeHeads, CVSA_ERR_UNSUPPORTED,
                "step_plan: B * H_kv = %lld exceeds %lld heads", (long long)d.B * d.H_kv,
                (long long)kMaxDecodeHeads);
-  STEP_REQUIRE(d.D == kHeadDim && d.block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
-               "step_plan: only D=128, block_size=16 are supported (got D=%d, bs=%d)", d.D,
+  STEP_REQUIRE((d.D == 64 || d.D == 128 || d.D == 256) && d.block_size == kPageTokens,
+               CVSA_ERR_UNSUPPORTED,
+               "step_plan: D=%d not in {64, 128, 256} or block_size=%d not 16", d.D,
                d.block_size);
   STEP_REQUIRE(d.W > 0 && d.W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
                "step_plan: W=%d not in 1..%d", d.W, kMaxPages);
@@ -158,7 +158,7 @@ namespace {
 // scores from the exact scan, and a fused scoring + decode launch for H_kv.
 bool speculates(const cvsa_step_desc &d) {
   return d.spec_state != nullptr && d.selector != CVSA_SELECT_QUEST_LN &&
-         cvsa_internal::score_spec_fusable(d.H_kv);
+         cvsa_internal::score_spec_fusable(d.H_kv, d.D);
 }
 
 // The lazy check with the speculative decode: one launch scores the pages

@@ -640,7 +640,8 @@ class StepPlan:
     With ``speculate`` (default) a lazy check decodes the cached selection
     in the same launch as the page scoring, and the verified decode skips
     its work when the check kept that selection (see
-    cvsa_step_desc.spec_state; exact gate scores and H_kv in 4, 8, 16 only);
+    cvsa_step_desc.spec_state; exact gate scores, H_kv in 4, 8, 16 and D = 128
+    only);
     results are bit-identical either way.
     """
 

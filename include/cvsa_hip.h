@@ -15,7 +15,8 @@
  *    to the caller; a step plan (below) is a small host object.
  *  - Return value: CVSA_OK (0), or a negative CVSA_ERR_* code with nothing
  *    enqueued.  cvsa_last_error() then returns a thread-local message.
- *  - Supported geometry: D = 128, block_size = 16, G = H_q / H_kv in 1..8,
+ *  - Supported geometry: D in {64, 128, 256}, block_size = 16,
+ *    G = H_q / H_kv in 1..8,
  *    H_kv in {1, 2, 4, 8, 16} (page scoring), W <= 32768 pages, and
  *    B * H_kv <= 4096 for dense and verified decode.  Anything else returns
  *    CVSA_ERR_UNSUPPORTED.
@@ -230,9 +231,10 @@ int cvsa_sparse_decode(const uint16_t *q, int64_t q_stride_b,
  * needs no caller-owned scratch.  No counterpart in the reference; it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  The split-K
- * counters and partials live in a static 2 MiB device array of the library
- * (one per GPU, held until the process ends; every listed launch needs at
- * most 1.1 MB of it, a larger need returns CVSA_ERR_WORKSPACE).  Its first
+ * counters and partials live in a static 2.25 MiB device array of the
+ * library (one per GPU, held until the process ends; every listed launch
+ * needs at most 2.1 MB of it, 1.1 MB at D = 128; a larger need returns
+ * CVSA_ERR_WORKSPACE).  Its first
  * call on a device looks the array up and zeroes its counters on `stream`.
  * All calls on one GPU share the array: calls that overlap in time on one
  * GPU (other streams, other threads) race and must be ordered by the
@@ -466,8 +468,8 @@ enum {
  * (spec_state[0], written by the selection kernel); a wrong prediction costs
  * time, never results: the outputs, selections, masks and counters equal
  * those of the sequential chain bit for bit.  Plans whose gate scores are
- * Quest scores (CVSA_SELECT_QUEST_LN) or whose H_kv is 1 or 2 run the
- * sequential chain and leave spec_state unchanged.
+ * Quest scores (CVSA_SELECT_QUEST_LN), whose H_kv is 1 or 2 or whose D is
+ * not 128 run the sequential chain and leave spec_state unchanged.
  */
 enum {
   CVSA_STEP_REUSE = 0,      /* sparse decode of the kept selection */

@@ -59,22 +59,25 @@ def test_errors_are_reported_without_gpu_work():
 
 def test_decode_workspace_layout_is_fixed():
     """Every decode workspace starts with the same 16 KiB counter area
-    (4096 heads x 4 bytes) followed by whole partial rows of G x 132 fp32, so
-    launches of any B * H_kv can share one workspace: the counters of one
-    launch never overlap the partial rows of another."""
+    (4096 heads x 4 bytes) followed by whole partial rows of G x (D + 4)
+    fp32, so launches of any B * H_kv can share one workspace: the counters
+    of one launch never overlap the partial rows of another.  Head dimensions
+    outside {64, 128, 256} have no workspace (0)."""
     lib = _lib_or_skip()
     seen = 0
-    for B in (1, 2, 3, 16, 32, 64):
-        for H_kv, G in ((8, 4), (4, 7), (8, 8), (1, 1)):
-            for max_sel, W, all_pages in ((1024, 8192, 0), (128, 512, 1), (64, 2048, 0),
-                                          (0, 512, 1)):
-                n = lib.cvsa_decode_workspace_bytes(B, H_kv * G, H_kv, 128, max_sel, W,
-                                                    all_pages)
-                if n == 0:
-                    continue
-                seen += 1
-                assert n > 16384 and (n - 16384) % (G * 132 * 4) == 0, (B, H_kv, G, n)
-    assert seen > 20
+    for D in (64, 128, 256):
+        for B in (1, 2, 3, 16, 32, 64):
+            for H_kv, G in ((8, 4), (4, 7), (8, 8), (1, 1)):
+                for max_sel, W, all_pages in ((1024, 8192, 0), (128, 512, 1), (64, 2048, 0),
+                                              (0, 512, 1)):
+                    n = lib.cvsa_decode_workspace_bytes(B, H_kv * G, H_kv, D, max_sel, W,
+                                                        all_pages)
+                    if n == 0:
+                        continue
+                    seen += 1
+                    assert n > 16384 and (n - 16384) % (G * (D + 4) * 4) == 0, (B, H_kv, G, n)
+    assert seen > 60
+    assert lib.cvsa_decode_workspace_bytes(1, 32, 8, 96, 64, 8192, 1) == 0
 
 
 def _step_desc(**over):
@@ -111,7 +114,8 @@ def test_step_plan_validates_on_the_host():
     lib.cvsa_step_plan_destroy(h)
     cases = [(dict(budget=513), _lib.CVSA_ERR_INVALID, b"budget"),
              (dict(H_kv=3, H_q=12), _lib.CVSA_ERR_UNSUPPORTED, b"H_kv"),
-             (dict(D=64), _lib.CVSA_ERR_UNSUPPORTED, b"D=128"),
+             (dict(D=96), _lib.CVSA_ERR_UNSUPPORTED, b"D=96"),
+             (dict(block_size=32), _lib.CVSA_ERR_UNSUPPORTED, b"block_size"),
              (dict(bt_stride_b=100), _lib.CVSA_ERR_INVALID, b"stride"),
              (dict(coverage=None), _lib.CVSA_ERR_INVALID, b"null"),
              (dict(out_dtype=5), _lib.CVSA_ERR_INVALID, b"dtype"),

@@ -10,6 +10,9 @@ the dense decode are compared per (sequence, KV head) with softmax attention
 over those pages in fp32.  Cases 0..3 make the verified walk total equal to
 B * H_kv * width with uneven per-head walks (the situation of the
 "every head walks max_sel pages" regression), the others are free draws.
+The same draws run at head dimensions 64 and 256 (engines compiled per D,
+split partials of G x (D + 4) floats, merges over several chunk passes when
+G x D / 4 exceeds the workgroup).
 """
 import pytest
 import torch
@@ -21,12 +24,13 @@ pytestmark = pytest.mark.gpu
 
 OUT_ATOL = 2e-3        # fp32 outputs against fp32 attention
 LSE_RTOL = 1e-3
-BS, D = 16, 128
+BS = 16
 
 
 def _attention(q, K, V, bt, b, ctx, h, G, pages):
     """Softmax attention of q-heads h*G..h*G+G-1 of sequence b over logical
     `pages` (fp32, torch); (zeros, -inf) when no token is valid."""
+    D = q.shape[-1]
     rows = q[b, h * G:(h + 1) * G].float()
     if pages.numel() == 0:
         return torch.zeros_like(rows), torch.full((G,), -float("inf"), device=q.device)
@@ -42,7 +46,7 @@ def _attention(q, K, V, bt, b, ctx, h, G, pages):
     return (p @ v) / l[:, None], m + torch.log(l)
 
 
-def _case(seed, dev):
+def _case(seed, dev, D=128):
     g = torch.Generator().manual_seed(seed)
     rnd = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))  # noqa: E731
     H = [1, 2, 4, 8, 16][rnd(0, 4)]
@@ -79,9 +83,8 @@ def _case(seed, dev):
     return inp, W, budget, idx.to(dev), nph.to(dev), accept.to(dev), H, G, B, ctx, n_valid
 
 
-@pytest.mark.parametrize("seed", range(16))
-def test_random_decode_launches(gpu, seed):
-    inp, W, budget, idx, nph, accept, H, G, B, ctx, n_valid = _case(seed, gpu)
+def _check(gpu, seed, D):
+    inp, W, budget, idx, nph, accept, H, G, B, ctx, n_valid = _case(seed, gpu, D)
     q, K, V, bt, cl = inp.q, inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens
     lo, lm, ll = ops.sparse_decode_unnorm(q, K, V, bt, idx, nph, cl, H, G, BS)
     ver, (vo, vm, vl) = ops.verified_decode(q, K, V, bt, cl, idx, nph, accept, H, G, BS,
@@ -104,3 +107,14 @@ def test_random_decode_launches(gpu, seed):
                 assert rel.max().item() < LSE_RTOL, (seed, b, h)
             want_d, _ = _attention(q, K, V, bt, b, ctx[b], h, G, every)
             assert (dense[b, rows].float() - want_d).abs().max().item() < 2e-2, (seed, b, h)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_decode_launches(gpu, seed):
+    _check(gpu, seed, 128)
+
+
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("seed", range(8))
+def test_random_decode_launches_head_dims(gpu, seed, D):
+    _check(gpu, seed, D)

@@ -324,9 +324,10 @@ def test_lse_merge(gpu, out_dtype):
     assert torch.equal(got2, got)
 
 
-def test_append_kv_matches_reference_loop(gpu):
+@pytest.mark.parametrize("D", [128, 64, 256])
+def test_append_kv_matches_reference_loop(gpu, D):
     from cvsa.runtime.kv_cache import PagedKVCache, SequenceKVManager
-    B, H, D = 5, 8, 128
+    B, H = 5, 8
     cache = PagedKVCache(64, 16, H, D, device=str(gpu))
     mgr = SequenceKVManager(cache, B, 16 * 8)
     g = torch.Generator().manual_seed(2)
@@ -365,7 +366,7 @@ def test_ops_reject_bad_input(gpu):
     with pytest.raises(ValueError):
         ops.score_pages(q.cpu(), K, bt, cl, 8, 4, 16)
     with pytest.raises(NotImplementedError):
-        ops.score_pages(q[:, :, :64].contiguous(), K[..., :64].contiguous(), bt, cl, 8, 4, 16)
+        ops.score_pages(q[:, :, :96].contiguous(), K[..., :96].contiguous(), bt, cl, 8, 4, 16)
     with pytest.raises(ValueError):
         ops.select_topk(torch.zeros(1, 8, 16, device=gpu), 17, cl, 16)
 

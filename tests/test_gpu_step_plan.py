@@ -352,13 +352,26 @@ def test_random_shapes_plan_equals_separate_kernels(gpu, seed):
     without speculation) runs a first selection, two lazy checks, a reuse
     step and a fixed-interval scoring step; every output, selection, gate and
     counter equals the same kernels called one by one, bit for bit."""
+    _plan_equals_separate_kernels(gpu, seed, 128)
+
+
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("seed", range(3))
+def test_random_shapes_plan_head_dims(gpu, seed, D):
+    """The same at head dimensions 64 and 256 (no speculation there: the
+    fused lazy-check launch is compiled for D = 128, so the plan runs the
+    plain chain whether or not it was asked to speculate)."""
+    _plan_equals_separate_kernels(gpu, seed, D)
+
+
+def _plan_equals_separate_kernels(gpu, seed, D):
     g = torch.Generator().manual_seed(100 + seed)
     rnd = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))  # noqa: E731
     H = [1, 2, 4, 8, 16][rnd(0, 4)]
     G = rnd(1, 8)
     B = rnd(1, 3)
     ctx = [rnd(40, 6000) for _ in range(B)]
-    inp = make_paged_inputs(B, H * G, H, 128, ctx, seed=seed, device=gpu,
+    inp = make_paged_inputs(B, H * G, H, D, ctx, seed=seed, device=gpu,
                             max_pages=max((c - 1) // 16 + 1 for c in ctx) + rnd(0, 3),
                             hot_heads=list(range(0, H, 2)), n_hot=4, hot_shift=8.0)
     W = inp.block_tables.shape[1]
