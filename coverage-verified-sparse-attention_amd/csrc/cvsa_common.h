@@ -13,11 +13,18 @@ namespace cvsa {
 
 constexpr int kWave = 64;
 constexpr int kHeadDim = 128;   // the head dimension of the fused lazy-check launch
-constexpr int kPageTokens = 16; // the only supported page (block) size
+constexpr int kPageTokens = 16; // tokens of a tile (a page is 1, 2 or 4 tiles)
 
 // Head dimensions the kernels are compiled for.
 __host__ __device__ constexpr bool head_dim_supported(int D) {
   return D == 64 || D == 128 || D == 256;
+}
+
+// The kernels walk pages as 16-token tiles: a page of block_size tokens is
+// 1 << tile_shift(block_size) consecutive tiles of its block.  -1: the block
+// size is not supported.
+__host__ __device__ constexpr int tile_shift(int block_size) {
+  return block_size == 16 ? 0 : block_size == 32 ? 1 : block_size == 64 ? 2 : -1;
 }
 constexpr int kMaxPages = 32768;
 

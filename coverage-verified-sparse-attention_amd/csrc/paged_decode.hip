@@ -34,7 +34,13 @@
 // HIP memory model's release / acquire pairing.
 //
 // Head modes: a listed head walks page_indices[b,h,:n_per_head]; an
-// all-pages head walks pages 0..n_valid-1 (dense decode).  In verified mode
+// all-pages head walks pages 0..n_valid-1 (dense decode).
+//
+// Tiles: the kernels walk 16-token tiles.  A page (block) of block_size =
+// 16 * 2^ts tokens is 2^ts consecutive tiles of its block, so tile sub of
+// logical page lp is logical tile (lp << ts) | sub, stored at physical tile
+// (block << ts) | sub, 16 * H_kv * D elements apart.  Head walks, splits and
+// stream-K ranges count tiles; the effective-budget counters count pages.  In verified mode
 // accepted heads are listed and rejected heads walk every valid page: the
 // draft pages plus the complement pages in one pass, which equals the LSE
 // merge of the draft and complement partial softmaxes.
@@ -70,8 +76,11 @@ struct DecodeArgs {
   const uint8_t *accept;  // non-NULL: verified mode
   int H_kv, W;
   int D;      // head dimension (the launch's engine is compiled for it)
+  int bs;     // block size (tokens per page)
+  int ts;     // tiles per page = 1 << ts
+  int max_sel_t;  // max_sel << ts
   int heads;  // B * H_kv
-  int pps, n_splits;  // listed partition: pages per split, splits per head
+  int pps, n_splits;  // listed partition: tiles per split, splits per head
   int sk_grid;        // stream-K partition: workgroups (<= kMaxSplits)
   float scale;
   float *o_unnorm, *m_out, *l_out;
@@ -111,15 +120,32 @@ __device__ __forceinline__ void write_outputs(const DecodeArgs &a, int64_t qrow,
   if (a.out != nullptr) store_out(a.out, a.out_dtype, qrow * D + d, O / fmaxf(L, 1e-6f));
 }
 
-// Effective-budget counters: pages attended by this head and n_valid(b).
+// Effective-budget counters: pages attended by this head (n tiles) and
+// n_valid(b).
 __device__ __forceinline__ void add_work(const DecodeArgs &a, int n, int ctx) {
-  atomicAdd(&a.work[0], (unsigned long long)n);
-  atomicAdd(&a.work[1], (unsigned long long)max(0, n_valid_pages(ctx, kPageTokens)));
+  atomicAdd(&a.work[0], (unsigned long long)(n >> a.ts));
+  atomicAdd(&a.work[1], (unsigned long long)max(0, n_valid_pages(ctx, a.bs)));
+}
+
+// Logical tile of entry e of a head's listed walk (tile e & (2^ts - 1) of
+// page idx_row[e >> ts]), or -1 when that page is outside [0, W).
+__device__ __forceinline__ int listed_tile(const DecodeArgs &a, const int32_t *idx_row, int e) {
+  const int lp = idx_row[e >> a.ts];
+  return lp >= 0 && lp < a.W ? (lp << a.ts) | (e & ((1 << a.ts) - 1)) : -1;
+}
+
+// Physical tile of logical tile lt of sequence b, or -1 (lt < 0, or a block
+// id outside the pool).  The block-table load is unconditional (clamped).
+__device__ __forceinline__ int tile_block(const DecodeArgs &a, int b, int lt) {
+  const int phys = a.block_tables[b * a.bt_sb + min(max(lt, 0) >> a.ts, a.W - 1)];
+  return lt >= 0 && phys >= 0 && phys < a.num_blocks ? (phys << a.ts) | (lt & ((1 << a.ts) - 1))
+                                                     : -1;
 }
 
 
-// Pages walked by head bh: its listed pages (page_indices[bh, :n_per_head]),
-// or every valid page (dense heads, rejected heads of a verified launch).
+// Tiles walked by head bh: those of its listed pages (page_indices[bh,
+// :n_per_head]), or of every valid page (dense heads, rejected heads of a
+// verified launch).
 // MODE is a template parameter and verified mode loads accept[bh] and
 // n_per_head[bh] unconditionally and picks with selects: an earlier form
 // that branched on null pointers was miscompiled (a live scalar register was
@@ -130,8 +156,8 @@ template <int MODE>
 __device__ __forceinline__ int head_pages(const DecodeArgs &a, int bh, bool &listed) {
   int n_all = 0, n_list = 0;
   if constexpr (MODE != kModeListed)
-    n_all = max(0, min(n_valid_pages(a.ctx_lens[bh / a.H_kv], kPageTokens), a.W));
-  if constexpr (MODE != kModeAll) n_list = min(max(a.n_pages[bh], 0), a.max_sel);
+    n_all = max(0, min(n_valid_pages(a.ctx_lens[bh / a.H_kv], a.bs), a.W)) << a.ts;
+  if constexpr (MODE != kModeAll) n_list = min(max(a.n_pages[bh], 0), a.max_sel) << a.ts;
   if constexpr (MODE == kModeAll) {
     listed = false;
     return n_all;
@@ -615,13 +641,13 @@ template <int NW>
 __device__ __forceinline__ int listed_first_entry(const DecodeArgs &a, int split, int bh,
                                                   int wave, int lane) {
   if (a.max_sel <= 0) return 0;
-  return a.page_idx[(int64_t)bh * a.idx_stride +
-                    min(split * a.pps + wave + NW * lane, a.max_sel - 1)];
+  return listed_tile(a, a.page_idx + (int64_t)bh * a.idx_stride,
+                     min(split * a.pps + wave + NW * lane, a.max_sel_t - 1));
 }
 
-__device__ __forceinline__ int listed_first_block(const DecodeArgs &a, int bh, int lp) {
+__device__ __forceinline__ int listed_first_block(const DecodeArgs &a, int bh, int lt) {
   if (a.max_sel <= 0) return 0;
-  return a.block_tables[(bh / a.H_kv) * a.bt_sb + min(max(lp, 0), a.W - 1)];
+  return tile_block(a, bh / a.H_kv, lt);
 }
 
 template <int NW>
@@ -648,7 +674,7 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
   const int pps = a.pps;
   const int r0 = split * pps;
   const int32_t *idx_row = a.page_idx + (int64_t)bh * a.idx_stride;
-  const int n = min(max(__builtin_amdgcn_readfirstlane(a.n_pages[bh]), 0), a.max_sel);
+  const int n = min(max(__builtin_amdgcn_readfirstlane(a.n_pages[bh]), 0), a.max_sel) << a.ts;
   const int r1 = min(n, r0 + pps);
   const int n_act = (n + pps - 1) / pps;  // splits holding pages of this head
   if (r0 >= r1 && !(split == 0 && n_act == 0)) return;  // uniform
@@ -661,12 +687,12 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
     const int cn = min(kWave, npw - c0);
     int my_phys = 0, my_ntok = 0;
     if (lane < cn) {
-      const int lp = c0 == 0 ? spec_lp : idx_row[r0 + wave + NW * (c0 + lane)];
-      if (lp >= 0 && lp < a.W) {
-        const int phys = c0 == 0 ? spec_phys : a.block_tables[b * a.bt_sb + lp];
-        if (phys >= 0 && phys < a.num_blocks) {
-          my_phys = phys;
-          my_ntok = min(kPageTokens, ctx - lp * kPageTokens);
+      const int lt = c0 == 0 ? spec_lp : listed_tile(a, idx_row, r0 + wave + NW * (c0 + lane));
+      if (lt >= 0) {
+        const int pt = c0 == 0 ? spec_phys : tile_block(a, b, lt);
+        if (pt >= 0) {
+          my_phys = pt;
+          my_ntok = max(0, min(kPageTokens, ctx - lt * kPageTokens));
         }
       }
     }
@@ -712,7 +738,7 @@ __global__ __launch_bounds__(NW * kWave) void listed_decode_kernel(const DecodeA
   listed_walk<G, Engine, NW, PD>(a, blockIdx.x, blockIdx.y, lp, phys, L);
 }
 
-// Pages per scoring wave of the fused launch below.
+// 16-token tiles per scoring wave of the fused launch below.
 constexpr int kSpecScorePPW = 8;
 
 // A lazy check's page scoring and the speculative listed decode of its
@@ -721,8 +747,8 @@ constexpr int kSpecScorePPW = 8;
 // n_splits), bit for bit listed_decode_kernel; they run only if
 // spec_state[0] predicts that the check keeps its selection, and workgroup 0
 // records in spec_state[1] whether they ran.  The other workgroups score
-// pages as score_pages_group_kernel<128, ...> does (score_body.h; kSpecScorePPW pages
-// per wave, workgroup x of sequence b at index n_dec + b * score_gx + x).
+// pages as score_pages_group_kernel<128, ...> does (score_body.h; kSpecScorePPW
+// tiles per wave, workgroup x of sequence b at index n_dec + b * score_gx + x).
 // The parts share no memory: the decode reads the cached selection, which
 // only the check's select-or-keep, launched after this kernel, rewrites.
 // One launch lets the decode's dependent metadata loads and split hand-off
@@ -765,7 +791,7 @@ __device__ __forceinline__ void add_listed_work(const DecodeArgs &a, unsigned lo
   unsigned long long n = 0, nv = 0;
   for (int bh = threadIdx.x; bh < a.heads; bh += NT) {
     n += (unsigned long long)min(max(a.n_pages[bh], 0), a.max_sel);
-    nv += (unsigned long long)max(0, n_valid_pages(a.ctx_lens[bh / a.H_kv], kPageTokens));
+    nv += (unsigned long long)max(0, n_valid_pages(a.ctx_lens[bh / a.H_kv], a.bs));
   }
   if (threadIdx.x == 0) red[0] = red[1] = 0ull;
   __syncthreads();
@@ -860,12 +886,12 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   // range reads harmless in-bounds entries and discards them), so the
   // compiler never has to drain them at a join.
   Engine eng;
-  const int T_spec = heads * a.max_sel;
+  const int T_spec = heads * a.max_sel_t;
   const Partition spec_part(T_spec, a.sk_grid);
   int spec_lp = 0, spec_phys = 0, h_spec = -1, r_spec = 0, ctx_spec = 0, g1_spec = 0;
   int b_spec = 0, h_c = 0;  // clamped speculated head and its sequence
   if constexpr (MODE != kModeAll) {
-    const int ms = max(a.max_sel, 1);
+    const int ms = max(a.max_sel_t, 1);
     const int wc = min(w, spec_part.n - 1);
     const int g0 = spec_part.start(wc);
     g1_spec = spec_part.start(wc + 1);
@@ -873,10 +899,11 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     r_spec = g0 - hs * ms;
     h_c = hs;
     b_spec = hs / a.H_kv;
-    const int rs = max(0, min(r_spec + wave + NW * lane, a.max_sel - 1));
+    const int rs = max(0, min(r_spec + wave + NW * lane, a.max_sel_t - 1));
     const int32_t *src =
-        a.max_sel > 0 ? a.page_idx + (int64_t)hs * a.idx_stride + rs : a.block_tables;
-    spec_lp = *src;
+        a.max_sel > 0 ? a.page_idx + (int64_t)hs * a.idx_stride + (rs >> a.ts) : a.block_tables;
+    const int lp0 = *src;
+    spec_lp = lp0 >= 0 && lp0 < a.W ? (lp0 << a.ts) | (rs & ((1 << a.ts) - 1)) : -1;
     ctx_spec = __builtin_amdgcn_readfirstlane(a.ctx_lens[b_spec]);
     eng.init(a, b_spec, hs - b_spec * a.H_kv, lane, s_eng[wave]);
     if (a.max_sel > 0 && w < spec_part.n) h_spec = hs;
@@ -889,11 +916,11 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   bool l_first = false;
   int c_first = head_pages<MODE>(a, min((int)threadIdx.x, heads - 1), l_first);
   if constexpr (MODE != kModeAll)
-    spec_phys = a.block_tables[b_spec * a.bt_sb + min(max(spec_lp, 0), a.W - 1)];
+    spec_phys = tile_block(a, b_spec, spec_lp);
   if ((int)threadIdx.x >= heads) c_first = 0;
   const int incl_first = wave_incl_scan(c_first);
   if (lane == kWave - 1) s_wsum[wave] = incl_first;
-  const bool odd_first = __ballot((int)threadIdx.x < heads && c_first != a.max_sel) != 0;
+  const bool odd_first = __ballot((int)threadIdx.x < heads && c_first != a.max_sel_t) != 0;
   if (lane == 0) s_odd[wave] = odd_first ? 1 : 0;
 
   // One wave's walk over its pages s0 + wave + NW*j of a segment, in chunks
@@ -913,14 +940,14 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
                     bool spec) {
     const int r = s0 + wave + NW * (c0 + lane);
     int lp = r, phys = 0;
-    if (spec) {  // the speculative entries of the chunk (lp of page r), consumed by every lane
+    if (spec) {  // the speculative entries of the chunk (tile of entry r), consumed by every lane
       lp = spec_lp;
       phys = spec_phys;
     } else if (lane < cn) {
-      if (listed) lp = idx_row[r];
-      phys = a.block_tables[b * a.bt_sb + min(max(lp, 0), a.W - 1)];
+      if (listed) lp = listed_tile(a, idx_row, r);
+      phys = tile_block(a, b, lp);
     }
-    const bool ok = lane < cn && lp >= 0 && lp < a.W && phys >= 0 && phys < a.num_blocks;
+    const bool ok = lane < cn && lp >= 0 && phys >= 0;
     my_phys = ok ? phys : 0;
     my_lp = ok ? lp : kNoPage;
   };
@@ -952,7 +979,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   // First PD pages of the speculated segment (a WG without one fetches block
   // 0 and never consumes it).
   if constexpr (MODE != kModeAll) {
-    const int s1 = min(g1_spec, (h_c + 1) * a.max_sel) - h_c * a.max_sel;
+    const int s1 = min(g1_spec, (h_c + 1) * a.max_sel_t) - h_c * a.max_sel_t;
     const int npw = h_spec >= 0 ? max(0, (s1 - r_spec - wave + NW - 1) / NW) : 0;
     lookup(r_spec, 0, min(kWave, npw), true, nullptr, b_spec, true);
     prologue(min(kWave, npw));
@@ -986,7 +1013,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
       if (hh >= heads) c = 0;
       const int incl = wave_incl_scan(c);
       if (lane == kWave - 1) s_wsum[wave] = incl;
-      const bool odd = __ballot(hh < heads && c != a.max_sel) != 0;
+      const bool odd = __ballot(hh < heads && c != a.max_sel_t) != 0;
       if (lane == 0) s_odd[wave] = odd ? 1 : 0;
       finish_pass(hh, c, incl, lst, carry);
     }
@@ -1171,9 +1198,13 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   const int G = H_q / H_kv;
   CVSA_REQUIRE(G >= 1 && G <= 8, CVSA_ERR_UNSUPPORTED,
                "%s: GQA group size %d not in 1..8", name, G);
-  CVSA_REQUIRE(decode_head_dim(D) && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
-               "%s: D=%d, block_size=%d not supported (D in {64, 128, 256}, block_size 16)",
+  const int ts = tile_shift(block_size);
+  CVSA_REQUIRE(decode_head_dim(D) && ts >= 0, CVSA_ERR_UNSUPPORTED,
+               "%s: D=%d, block_size=%d not supported (D in {64, 128, 256}, block_size in "
+               "{16, 32, 64})",
                name, D, block_size);
+  CVSA_REQUIRE(a.num_blocks <= (INT32_MAX >> ts), CVSA_ERR_UNSUPPORTED,
+               "%s: %lld blocks exceed the tile index range", name, (long long)a.num_blocks);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
                kMaxPages);
   CVSA_REQUIRE(a.bt_sb >= W, CVSA_ERR_INVALID, "%s: block-table row stride %lld < W=%d",
@@ -1213,10 +1244,13 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   a.W = W;
   a.H_kv = H_kv;
   a.heads = B * H_kv;
-  a.pps = p.pps;
+  a.pps = p.pps << ts;
   a.n_splits = p.n_splits;
   a.sk_grid = p.sk_grid;
   a.D = D;
+  a.bs = block_size;
+  a.ts = ts;
+  a.max_sel_t = listed ? a.max_sel << ts : 0;
   a.scale = (float)pow((double)D, -0.5);
   return CVSA_OK;
 }
@@ -1505,8 +1539,11 @@ int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_
   bind_workspace(a, workspace, need);
   const int G = H_q / H_kv;
   const ScoreArgs sa{q, q_stride_b, q_stride_h, k_cache, num_blocks, block_tables,
-                     bt_stride_b, context_lens, page_scores, W, G, 1.0f / (float)G, a.scale};
-  const int64_t waves = (int64_t)((W + kSpecScorePPW - 1) / kSpecScorePPW) * (H_kv / 4);
+                     bt_stride_b, context_lens, page_scores, W, G, 1.0f / (float)G, a.scale,
+                     block_size, a.ts};
+  static_assert(kSpecScorePPW % 4 == 0, "a scoring wave holds whole pages of up to 4 tiles");
+  const int64_t waves =
+      (int64_t)(((W << a.ts) + kSpecScorePPW - 1) / kSpecScorePPW) * (H_kv / 4);
   const int score_gx = (int)((waves + kWavesPerWg - 1) / kWavesPerWg);
   const int64_t grid = (int64_t)p.grid_x * p.grid_y + (int64_t)score_gx * B;
   hipStream_t st = (hipStream_t)stream;

@@ -20,32 +20,33 @@
 
 namespace cvsa {
 
-// Extremes of 8 dimensions (one 16-byte segment) of a page's valid token
-// rows, packed as bf16 like the metadata; rows past the last valid one
-// repeat it.
+// Extremes of 8 dimensions (one 16-byte segment) of a page's ntok >= 1
+// valid token rows, packed as bf16 like the metadata.  Rows are read 16 at a
+// time (rows past the last valid one repeat it).
 __device__ __forceinline__ void segment_minmax(const uint16_t *__restrict__ rows,
                                                int64_t row_stride, int ntok, uint4 &mn,
                                                uint4 &mx) {
-  uint4 r[kPageTokens];
-#pragma unroll
-  for (int t = 0; t < kPageTokens; ++t)
-    r[t] = *reinterpret_cast<const uint4 *>(rows + (int64_t)min(t, ntok - 1) * row_stride);
   float lo[8], hi[8];
-  const uint32_t w0[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    lo[2 * i] = hi[2 * i] = bf16_lo(w0[i]);
-    lo[2 * i + 1] = hi[2 * i + 1] = bf16_hi(w0[i]);
+  for (int e = 0; e < 8; ++e) {
+    lo[e] = INFINITY;
+    hi[e] = -INFINITY;
   }
+  for (int t0 = 0; t0 < ntok; t0 += kPageTokens) {
+    uint4 r[kPageTokens];
 #pragma unroll
-  for (int t = 1; t < kPageTokens; ++t) {
-    const uint32_t w[4] = {r[t].x, r[t].y, r[t].z, r[t].w};
+    for (int t = 0; t < kPageTokens; ++t)
+      r[t] = *reinterpret_cast<const uint4 *>(rows + (int64_t)min(t0 + t, ntok - 1) * row_stride);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lo[2 * i] = fminf(lo[2 * i], bf16_lo(w[i]));
-      hi[2 * i] = fmaxf(hi[2 * i], bf16_lo(w[i]));
-      lo[2 * i + 1] = fminf(lo[2 * i + 1], bf16_hi(w[i]));
-      hi[2 * i + 1] = fmaxf(hi[2 * i + 1], bf16_hi(w[i]));
+    for (int t = 0; t < kPageTokens; ++t) {
+      const uint32_t w[4] = {r[t].x, r[t].y, r[t].z, r[t].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lo[2 * i] = fminf(lo[2 * i], bf16_lo(w[i]));
+        hi[2 * i] = fmaxf(hi[2 * i], bf16_lo(w[i]));
+        lo[2 * i + 1] = fminf(lo[2 * i + 1], bf16_hi(w[i]));
+        hi[2 * i + 1] = fmaxf(hi[2 * i + 1], bf16_hi(w[i]));
+      }
     }
   }
   // The extremes are key values, so their top 16 bits are the bf16 bits.
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
     const int32_t *__restrict__ block_tables, int64_t bt_sb,
     const int32_t *__restrict__ context_lens, const uint16_t *__restrict__ k_cache,
     const uint8_t *__restrict__ check_accept, int n_heads, int H_kv, int G, float inv_g,
-    float scale, int W, int ppw, float *__restrict__ scores) {
+    float scale, int W, int ppw, int bs, float *__restrict__ scores) {
   constexpr int LPR = D / 8;
   constexpr int RPL = kWave / LPR;  // pages per wave load
   constexpr int kIter = 16 / RPL;   // wave loads per run of sixteen pages
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
 #pragma unroll
     for (int i = 0; i < kIter; ++i) {
       const int p = pb + RPL * i + sub;
-      valid[i] = p < p_end && p * kPageTokens < ctx && phys[i] >= 0 && phys[i] < num_blocks;
+      valid[i] = p < p_end && p * bs < ctx && phys[i] >= 0 && phys[i] < num_blocks;
     }
     uint4 mn[kIter], mx[kIter];
     int have[kIter];
@@ -144,10 +145,10 @@ __global__ __launch_bounds__(256) void quest_scores_kernel(
 #pragma unroll
       for (int i = 0; i < kIter; ++i) {
         const int p = pb + RPL * i + sub;
-        const int ntok = min(kPageTokens, ctx - p * kPageTokens);
+        const int ntok = min(bs, ctx - p * bs);
         if (valid[i] && have[i] != ntok) {
           const int64_t slot = (int64_t)cur[i] * H_kv + h;
-          segment_minmax(k_cache + (int64_t)cur[i] * kPageTokens * row_stride +
+          segment_minmax(k_cache + (int64_t)cur[i] * bs * row_stride +
                              (int64_t)h * D + 8 * seg,
                          row_stride, ntok, mn[i], mx[i]);
           uint16_t *m = meta + slot * 2 * D + 8 * seg;
@@ -196,8 +197,9 @@ int check_quest_sizes(const char *name, int32_t B, int32_t H_kv, int32_t D, int3
                       int32_t W, int64_t num_blocks, int64_t bt_stride_b, const void *meta) {
   CVSA_REQUIRE(B > 0 && H_kv > 0 && (int64_t)B * H_kv <= 65535 && W > 0 && num_blocks > 0,
                CVSA_ERR_INVALID, "%s: bad sizes B=%d H_kv=%d W=%d", name, B, H_kv, W);
-  CVSA_REQUIRE(head_dim_supported(D) && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
-               "%s: D=%d not in {64, 128, 256} or block_size=%d not 16", name, D, block_size);
+  CVSA_REQUIRE(head_dim_supported(D) && tile_shift(block_size) >= 0, CVSA_ERR_UNSUPPORTED,
+               "%s: D=%d not in {64, 128, 256} or block_size=%d not in {16, 32, 64}", name, D,
+               block_size);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
                kMaxPages);
   CVSA_REQUIRE(bt_stride_b >= W, CVSA_ERR_INVALID, "%s: block-table row stride %lld < W=%d",
@@ -238,7 +240,7 @@ extern "C" int cvsa_quest_meta_update(const uint16_t *k_cache, int64_t num_block
   hipLaunchKernelGGL((quest_scores_kernel<DD, true, false>), grid, dim3(256), 0,             \
                      (hipStream_t)stream, nullptr, 0, 0, meta, meta_ntok, num_blocks,        \
                      block_tables, bt_stride_b, context_lens, k_cache, nullptr, 0, H_kv, 1,  \
-                     1.0f, 1.0f, W, ppw, nullptr)
+                     1.0f, 1.0f, W, ppw, block_size, nullptr)
   if (D == 64)
     CVSA_QUEST_REFRESH(64);
   else if (D == 256)
@@ -271,7 +273,7 @@ extern "C" int cvsa_quest_scores(const uint16_t *q, int64_t q_stride_b, int64_t 
                      (hipStream_t)stream, q, q_stride_b, q_stride_h,                         \
                      const_cast<uint16_t *>(meta), nullptr, num_blocks, block_tables,        \
                      bt_stride_b, context_lens, nullptr, nullptr, 0, H_kv, G,                \
-                     1.0f / (float)G, scale, W, ppw, page_scores)
+                     1.0f / (float)G, scale, W, ppw, block_size, page_scores)
   if (D == 64)
     CVSA_QUEST_SCORE(64);
   else if (D == 256)
@@ -307,7 +309,7 @@ extern "C" int cvsa_quest_refresh_scores(const uint16_t *q, int64_t q_stride_b,
                      (hipStream_t)stream, q, q_stride_b, q_stride_h, meta, meta_ntok,         \
                      num_blocks, block_tables, bt_stride_b, context_lens, k_cache,            \
                      check_accept, B * H_kv, H_kv, G, 1.0f / (float)G, scale, W, ppw,         \
-                     page_scores)
+                     block_size, page_scores)
   if (D == 64)
     CVSA_QUEST_BOTH(64);
   else if (D == 256)

@@ -25,19 +25,21 @@ struct ScoreArgs {
   float *scores;
   int W, G;
   float inv_g, scale;
+  int bs, ts;  // block size, tiles per page = 1 << ts
 };
 
-// Wave gw of sequence b owns head group hg = gw % (hkv / R) of pages
-// [(gw / (hkv / R)) * PPW, +PPW), where LPR = D / 8 lanes hold one 2D-byte
+// Wave gw of sequence b owns head group hg = gw % (hkv / R) of 16-token
+// tiles [(gw / (hkv / R)) * PPW, +PPW) (whole pages: PPW is a multiple of
+// the tiles per page), where LPR = D / 8 lanes hold one 2D-byte
 // key row and R = 64 / LPR rows make one wave load (R = 8, 4, 2 heads at
 // D = 64, 128, 256).  For each token of a page, the group's R rows are
 // contiguous (1 KiB), so one 16-byte load per lane reads them whole: lane l
 // holds head R*hg + l / LPR, d-segment (l % LPR) * 8.  The LPR lanes of a
 // row finish the dot product with DPP adds (and a permlane swap at LPR = 32),
-// and each lane keeps the running max of its head.  The wave's block-table
-// entries are fetched once (lane j: page j) and the next page's keys are
-// requested before the current page is reduced.  hkv is a compile-time
-// constant where the caller's is.
+// and each lane keeps the running max of its head over the tiles of a page.
+// The wave's block-table entries are fetched once (lane j: tile j) and the
+// next tile's keys are requested before the current tile is reduced.  hkv
+// is a compile-time constant where the caller's is.
 template <int D, int PPW>
 __device__ __forceinline__ void score_group_wave(const ScoreArgs &s, int hkv, int gw, int b) {
   constexpr int LPR = D / 8;
@@ -45,22 +47,24 @@ __device__ __forceinline__ void score_group_wave(const ScoreArgs &s, int hkv, in
   const int ng = hkv / R;  // head groups per page
   const int lane = threadIdx.x & 63;
   const int hg = gw % ng;
-  const int p_begin = (gw / ng) * PPW;
+  const int t_begin = (gw / ng) * PPW;
   const int W = s.W;
-  if (p_begin >= W) return;
+  const int tm = (1 << s.ts) - 1;
+  if (t_begin >= (W << s.ts)) return;
   const int h = R * hg + lane / LPR;
   const int seg = lane % LPR;
   const int ctx = __builtin_amdgcn_readfirstlane(s.context_lens[b]);
-  const int n = min(PPW, W - p_begin);
+  const int n = min(PPW, (W << s.ts) - t_begin);
 
-  // Page j of this wave: block id in lane j (-1 when the page holds no
-  // valid token or the id is outside the pool).
+  // Tile j of this wave: physical tile in lane j (-1 when its page holds no
+  // valid token or the page's block id is outside the pool).
   int my_phys = -1;
   if (lane < n) {
-    const int p = p_begin + lane;
-    if (p * kPageTokens < ctx) {
+    const int lt = t_begin + lane;
+    const int p = lt >> s.ts;
+    if (p * s.bs < ctx) {
       const int id = s.block_tables[b * s.bt_sb + p];
-      if (id >= 0 && id < s.num_blocks) my_phys = id;
+      if (id >= 0 && id < s.num_blocks) my_phys = (id << s.ts) | (lt & tm);
     }
   }
   const uint4 qr = group_mean_q(s.q, s.q_sb, s.q_sh, b, h, s.G, seg, s.inv_g);
@@ -76,18 +80,20 @@ __device__ __forceinline__ void score_group_wave(const ScoreArgs &s, int hkv, in
 #pragma unroll
     for (int t = 0; t < kPageTokens; ++t) kv[t] = stream_load16(src + t * row_stride);
   };
+  float pm = -INFINITY;  // running max over the tiles of the current page
   auto consume = [&](int j, const uint4 (&kv)[kPageTokens]) {
-    const int p = p_begin + j;
+    const int lt = t_begin + j;
     const int ntok = __builtin_amdgcn_readlane(my_phys, j) < 0
                          ? 0
-                         : min(kPageTokens, ctx - p * kPageTokens);
-    float mx = -INFINITY;
+                         : min(kPageTokens, ctx - lt * kPageTokens);
+    float mx = (j & tm) == 0 ? -INFINITY : pm;
 #pragma unroll
     for (int t = 0; t < kPageTokens; ++t) {
       const float sc = group_sum<LPR>(dot8_bf16(kv[t], qr, 0.f)) * s.scale;
       if (t < ntok) mx = fmaxf(mx, sc);
     }
-    if (seg == 0) s.scores[((int64_t)b * hkv + h) * W + p] = mx;
+    pm = mx;
+    if (seg == 0 && (j & tm) == tm) s.scores[((int64_t)b * hkv + h) * W + (lt >> s.ts)] = mx;
   };
   uint4 buf[2][kPageTokens];
   fetch(0, buf[0]);

@@ -36,12 +36,12 @@ __global__ __launch_bounds__(256) void score_pages_kernel(
     const uint16_t *__restrict__ k_cache, int64_t num_blocks,
     const int32_t *__restrict__ block_tables, int64_t bt_sb,
     const int32_t *__restrict__ context_lens, float *__restrict__ scores,
-    int W, int G, float inv_g, float scale, int ppw) {
+    int W, int G, float inv_g, float scale, int ppw, int bs, int ts) {
   constexpr int LPR = D / 8;
   constexpr int R = rows_per_load(D);
   static_assert(HKV < R && R % HKV == 0, "small-head layout");
-  constexpr int NLOAD = kPageTokens * HKV / R;     // 16-byte loads per lane per page
-  constexpr int PAGE_ELEMS = kPageTokens * HKV * D;
+  constexpr int NLOAD = kPageTokens * HKV / R;     // 16-byte loads per lane per tile
+  constexpr int TILE_ELEMS = kPageTokens * HKV * D;
   constexpr int S = HKV * LPR;                     // lane distance between rows of one head
 
   const int lane = threadIdx.x & 63;
@@ -58,23 +58,27 @@ __global__ __launch_bounds__(256) void score_pages_kernel(
   const int p_end = min(W, p_begin + ppw);
   for (int p = p_begin; p < p_end; ++p) {
     float *dst = scores + (int64_t)b * HKV * W + p;
-    const int ntok = min(kPageTokens, ctx - p * kPageTokens);
+    const int ntok = min(bs, ctx - p * bs);
     const int phys = ntok > 0 ? block_tables[b * bt_sb + p] : -1;
     if (phys < 0 || phys >= num_blocks) {
       // Beyond the context (or an out-of-range block id): no valid token.
       if (seg == 0 && rsub < HKV) dst[(int64_t)h * W] = -INFINITY;
       continue;
     }
-    const uint16_t *src = k_cache + (int64_t)phys * PAGE_ELEMS + lane * 8;
-    uint4 kv[NLOAD];
-#pragma unroll
-    for (int i = 0; i < NLOAD; ++i) kv[i] = stream_load16(src + i * 64 * 8);
     float mx = -INFINITY;
+    for (int sub = 0; sub < (1 << ts); ++sub) {  // the page's 16-token tiles
+      const uint16_t *src =
+          k_cache + ((int64_t)phys << ts | sub) * TILE_ELEMS + lane * 8;
+      uint4 kv[NLOAD];
 #pragma unroll
-    for (int i = 0; i < NLOAD; ++i) {
-      const int t = (i * R + rsub) / HKV;
-      const float sc = group_sum<LPR>(dot8_bf16(kv[i], qr, 0.f)) * scale;
-      if (t < ntok) mx = fmaxf(mx, sc);
+      for (int i = 0; i < NLOAD; ++i) kv[i] = stream_load16(src + i * 64 * 8);
+      const int tn = ntok - sub * kPageTokens;  // valid tokens of the tile (<= 0: none)
+#pragma unroll
+      for (int i = 0; i < NLOAD; ++i) {
+        const int t = (i * R + rsub) / HKV;
+        const float sc = group_sum<LPR>(dot8_bf16(kv[i], qr, 0.f)) * scale;
+        if (t < tn) mx = fmaxf(mx, sc);
+      }
     }
     // Rows of one head sit S lanes apart: combine them.
     float a, c;
@@ -109,9 +113,12 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
                (long long)num_blocks);
   CVSA_REQUIRE(H_kv > 0 && H_q > 0 && H_q % H_kv == 0, CVSA_ERR_INVALID,
                "score_pages: H_q=%d is not a multiple of H_kv=%d", H_q, H_kv);
-  CVSA_REQUIRE(head_dim_supported(D) && block_size == kPageTokens, CVSA_ERR_UNSUPPORTED,
-               "score_pages: D=%d not in {64, 128, 256} or block_size=%d not 16", D,
-               block_size);
+  const int ts = tile_shift(block_size);
+  CVSA_REQUIRE(head_dim_supported(D) && ts >= 0, CVSA_ERR_UNSUPPORTED,
+               "score_pages: D=%d not in {64, 128, 256} or block_size=%d not in {16, 32, 64}",
+               D, block_size);
+  CVSA_REQUIRE(num_blocks <= (INT32_MAX >> ts), CVSA_ERR_UNSUPPORTED,
+               "score_pages: %lld blocks exceed the tile index range", (long long)num_blocks);
   CVSA_REQUIRE(H_kv == 1 || H_kv == 2 || H_kv == 4 || H_kv == 8 || H_kv == 16,
                CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d not in {1,2,4,8,16}", H_kv);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
@@ -131,17 +138,19 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
   hipStream_t st = (hipStream_t)stream;
   const int R = kWave / (D / 8);
   if (H_kv % R == 0) {
-    // Head-group layout: waves = pages / PPW x H_kv / R.  As many pages per
-    // wave (up to 8) as keep >= ~2048 waves (8 per CU) in the launch: the
-    // setup (q_rep, block-table fetch) is amortised over more pages, and the
-    // last-wave tail stays short.
-    const int64_t group_pages = (int64_t)B * W * (H_kv / R);
-    int ppw = 1;
-    while (ppw < 8 && group_pages / (2 * ppw) >= 2048) ppw *= 2;
-    const int64_t waves = ((W + ppw - 1) / ppw) * (int64_t)(H_kv / R);
+    // Head-group layout: waves = tiles / PPW x H_kv / R.  As many 16-token
+    // tiles per wave (up to 8, at least one page) as keep >= ~2048 waves
+    // (8 per CU) in the launch: the setup (q_rep, block-table fetch) is
+    // amortised over more tiles, and the last-wave tail stays short.
+    const int Wt = W << ts;
+    const int64_t group_tiles = (int64_t)B * Wt * (H_kv / R);
+    int ppw = 1 << ts;
+    while (ppw < 8 && group_tiles / (2 * ppw) >= 2048) ppw *= 2;
+    const int64_t waves = ((Wt + ppw - 1) / ppw) * (int64_t)(H_kv / R);
     dim3 grid((unsigned)((waves + 3) / 4), B);
     const ScoreArgs sa{q, q_stride_b, q_stride_h, k_cache, (int64_t)num_blocks, block_tables,
-                       bt_stride_b, context_lens, page_scores, W, G, inv_g, scale};
+                       bt_stride_b, context_lens, page_scores, W, G, inv_g, scale,
+                       block_size, ts};
 #define CVSA_GROUP_CASE(DD, HK, PP)                                                          \
   if (D == DD && H_kv == HK && ppw == PP) {                                                  \
     hipLaunchKernelGGL((score_pages_group_kernel<DD, HK, PP>), grid, dim3(256), 0, st, sa);  \
@@ -167,7 +176,7 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
     hipLaunchKernelGGL((score_pages_kernel<DD, HK>), grid, dim3(256), 0, st, q,          \
                        q_stride_b, q_stride_h, k_cache, (int64_t)num_blocks,             \
                        block_tables, bt_stride_b, context_lens, page_scores, W, G,       \
-                       inv_g, scale, ppw);                                               \
+                       inv_g, scale, ppw, block_size, ts);                               \
     return cvsa_host::check_launch("score_pages");                                       \
   }
   CVSA_SCORE_CASE(64, 1) CVSA_SCORE_CASE(64, 2) CVSA_SCORE_CASE(64, 4)

@@ -48,16 +48,17 @@ class _Runtime:
     def __init__(self, inp, dev, extra_tokens):
         B = inp.q.shape[0]
         nb = inp.k_cache.shape[0]
-        H, D = inp.k_cache.shape[2], inp.k_cache.shape[3]
+        bs, H, D = inp.k_cache.shape[1], inp.k_cache.shape[2], inp.k_cache.shape[3]
         W = inp.block_tables.shape[1]
-        self.cache = PagedKVCache(nb, 16, H, D, device=str(dev))
+        self.bs = bs
+        self.cache = PagedKVCache(nb, bs, H, D, device=str(dev))
         self.cache.k_cache.copy_(inp.k_cache)
         self.cache.v_cache.copy_(inp.v_cache)
         self.cache._next_free = inp.used_blocks
-        self.mgr = SequenceKVManager(self.cache, B, W * 16)
+        self.mgr = SequenceKVManager(self.cache, B, W * bs)
         self.mgr.block_tables.copy_(inp.block_tables)
         self.mgr.context_lens.copy_(inp.context_lens)
-        pages = [-(-int(c) // 16) for c in inp.context_lens.tolist()]
+        pages = [-(-int(c) // bs) for c in inp.context_lens.tolist()]
         self.mgr._pages_allocated = list(pages)
         self.mgr.sync_host_state()
         self.K = inp.k_cache.clone()
@@ -71,7 +72,7 @@ class _Runtime:
         self.mgr.append_tokens_kv(k.to(dev), v.to(dev))
         for b in range(k.shape[0]):
             self.nf = ref.append_token_kv(self.K, self.V, self.bt, self.ctx, self.alloc, self.nf,
-                                          b, k[b], v[b], 16)
+                                          b, k[b], v[b], self.bs)
 
 
 def _cpu(t):
@@ -106,6 +107,7 @@ class _Lockstep:
         self.gpu_b = gpu_b
         self.kw = kw
         self.tau = float(kw.get("coverage_threshold", 0.9))
+        self.bs = gpu_b.block_size
         self.ctx = ctx_cpu                   # the oracle runtime's context lengths (live)
         self.own_margin = 0                  # fp32-vs-fp64 on the GPU's own scores
         self.margin_sel = 0                  # fp64 selection decided within the score error
@@ -140,16 +142,16 @@ class _Lockstep:
     def _select(self, scores, layer):
         kw = self.kw
         if kw.get("top_p") is not None:
-            return ref.topp_select(scores, kw["top_p"], self.ctx, 16)
+            return ref.topp_select(scores, kw["top_p"], self.ctx, self.bs)
         if kw.get("static_budget_table") is not None:
             return ref.static_select(scores, torch.as_tensor(kw["static_budget_table"][layer]),
-                                     self.ctx, 16)
+                                     self.ctx, self.bs)
         W = scores.shape[-1]
         budget = max(3, int(W * kw.get("budget_pct", 0.10)))
         if kw.get("adaptive_selection"):
-            return ref.adaptive_select(scores, budget, self.ctx, 16,
+            return ref.adaptive_select(scores, budget, self.ctx, self.bs,
                                        kw.get("adaptive_floor_ratio", 0.5))
-        return ref.select_topk(scores, budget, self.ctx, 16)
+        return ref.select_topk(scores, budget, self.ctx, self.bs)
 
     @staticmethod
     def _score_error(gpu, ora, what):
@@ -253,15 +255,16 @@ def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, expect_margin=0)
         inp = make_paged_inputs(**cfg, seed=seed, max_pages=None, spare_blocks=extra)
     B, H_q, D = inp.q.shape
     H = inp.num_kv_heads
+    bs = inp.k_cache.shape[1]
     W = inp.block_tables.shape[1]
     # leave room in the block table for the appended tokens
-    W2 = W + (steps + 15) // 16 + 1
+    W2 = W + (steps + bs - 1) // bs + 1
     bt = torch.zeros(B, W2, dtype=torch.int32)
     bt[:, :W] = inp.block_tables
     inp.block_tables = bt
     rt = _Runtime(inp, dev, extra)
-    gpu_b = CVSABackend(num_kv_heads=H, num_q_heads=H_q, head_dim=D, block_size=16, **kw)
-    ora_b = OracleCVSABackend(num_kv_heads=H, num_q_heads=H_q, head_dim=D, block_size=16, **kw)
+    gpu_b = CVSABackend(num_kv_heads=H, num_q_heads=H_q, head_dim=D, block_size=bs, **kw)
+    ora_b = OracleCVSABackend(num_kv_heads=H, num_q_heads=H_q, head_dim=D, block_size=bs, **kw)
     lock = _Lockstep(gpu_b, ora_b, kw, rt.ctx)
     g = torch.Generator().manual_seed(seed + 1)
     for step in range(steps):

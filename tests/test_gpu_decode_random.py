@@ -12,7 +12,8 @@ B * H_kv * width with uneven per-head walks (the situation of the
 "every head walks max_sel pages" regression), the others are free draws.
 The same draws run at head dimensions 64 and 256 (engines compiled per D,
 split partials of G x (D + 4) floats, merges over several chunk passes when
-G x D / 4 exceeds the workgroup).
+G x D / 4 exceeds the workgroup) and at block sizes 32 and 64 (pages walked
+as 2 or 4 tiles of 16 tokens).
 """
 import pytest
 import torch
@@ -24,13 +25,11 @@ pytestmark = pytest.mark.gpu
 
 OUT_ATOL = 2e-3        # fp32 outputs against fp32 attention
 LSE_RTOL = 1e-3
-BS = 16
-
-
 def _attention(q, K, V, bt, b, ctx, h, G, pages):
     """Softmax attention of q-heads h*G..h*G+G-1 of sequence b over logical
     `pages` (fp32, torch); (zeros, -inf) when no token is valid."""
     D = q.shape[-1]
+    BS = K.shape[1]
     rows = q[b, h * G:(h + 1) * G].float()
     if pages.numel() == 0:
         return torch.zeros_like(rows), torch.full((G,), -float("inf"), device=q.device)
@@ -46,7 +45,7 @@ def _attention(q, K, V, bt, b, ctx, h, G, pages):
     return (p @ v) / l[:, None], m + torch.log(l)
 
 
-def _case(seed, dev, D=128):
+def _case(seed, dev, D=128, BS=16):
     g = torch.Generator().manual_seed(seed)
     rnd = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))  # noqa: E731
     H = [1, 2, 4, 8, 16][rnd(0, 4)]
@@ -57,11 +56,12 @@ def _case(seed, dev, D=128):
         B, H = 1, [4, 8][seed % 2]
     ctx = [rnd(1, 9000) for _ in range(B)]
     if uneven:
-        ctx = [16 * H * 64]                       # n_valid = 64 * H pages
+        ctx = [BS * H * 64]                       # n_valid = 64 * H pages
     n_valid = [(c - 1) // BS + 1 for c in ctx]
     W = max(n_valid) + rnd(0, 6)
     budget = 64 if uneven else rnd(1, W)
-    inp = make_paged_inputs(B, H * G, H, D, ctx, seed=seed, device=dev, max_pages=W,
+    inp = make_paged_inputs(B, H * G, H, D, ctx, block_size=BS, seed=seed, device=dev,
+                            max_pages=W,
                             hot_heads=list(range(0, H, 2)), n_hot=4, hot_shift=4.0)
     idx = torch.randint(-3, W + 3, (B, H, budget), generator=g).to(torch.int32)
     nph = torch.zeros(B, H, dtype=torch.int32)
@@ -83,8 +83,8 @@ def _case(seed, dev, D=128):
     return inp, W, budget, idx.to(dev), nph.to(dev), accept.to(dev), H, G, B, ctx, n_valid
 
 
-def _check(gpu, seed, D):
-    inp, W, budget, idx, nph, accept, H, G, B, ctx, n_valid = _case(seed, gpu, D)
+def _check(gpu, seed, D, BS=16):
+    inp, W, budget, idx, nph, accept, H, G, B, ctx, n_valid = _case(seed, gpu, D, BS)
     q, K, V, bt, cl = inp.q, inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens
     lo, lm, ll = ops.sparse_decode_unnorm(q, K, V, bt, idx, nph, cl, H, G, BS)
     ver, (vo, vm, vl) = ops.verified_decode(q, K, V, bt, cl, idx, nph, accept, H, G, BS,
@@ -118,3 +118,9 @@ def test_random_decode_launches(gpu, seed):
 @pytest.mark.parametrize("seed", range(8))
 def test_random_decode_launches_head_dims(gpu, seed, D):
     _check(gpu, seed, D)
+
+
+@pytest.mark.parametrize("BS", [32, 64])
+@pytest.mark.parametrize("seed", range(8))
+def test_random_decode_launches_block_sizes(gpu, seed, BS):
+    _check(gpu, seed, [128, 64, 256][seed % 3], BS)

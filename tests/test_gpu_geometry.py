@@ -1,0 +1,104 @@
+"""Head dimensions 64 and 256 and block sizes 32 and 64 through the entry
+points that take them, against the oracle: page scoring in both of its
+layouts (a wave load holds 64 / (D/8) key rows, so the head-group layout
+needs H_kv a multiple of 8, 4, 2 at D = 64, 128, 256 and smaller H_kv take
+the whole-page layout) and with several tiles per wave, Quest metadata and
+scores, and the backend's schedules in lockstep with the oracle backend.
+Decode launches and step plans at these geometries run with the random
+draws of test_gpu_decode_random.py and test_gpu_step_plan.py, the KV append
+in test_gpu_ops.py.
+"""
+import pytest
+import torch
+
+from oracle import cvsa_oracle as ref
+from cvsa import ops
+from cvsa.synthetic import make_paged_inputs
+from test_gpu_backend import _random_schedule, _run
+
+pytestmark = pytest.mark.gpu
+
+SCORE_RTOL = 1e-4      # page scores, relative (as at D = 128)
+QUEST_RTOL = 1e-5
+
+GEOMS = [  # (B, H_q, H_kv, ctx)
+    (2, 32, 8, [3000, 517]),
+    (1, 28, 4, 2048),
+    (3, 12, 4, [17, 300, 1024]),
+    (2, 4, 2, 777),
+    (1, 4, 1, 640),
+    (1, 32, 16, 512),
+]
+
+
+def _close(got, want, rtol):
+    fin = torch.isfinite(want)
+    assert torch.equal(torch.isfinite(got), fin)
+    assert torch.equal(got[~fin], want[~fin])
+    err = ((got[fin] - want[fin]).abs() / want[fin].abs().clamp(min=1.0)).max().item()
+    assert err < rtol, err
+
+
+GEOMETRIES = [(64, 16), (256, 16), (128, 32), (128, 64), (64, 32), (256, 64)]  # (D, bs)
+
+
+@pytest.mark.parametrize("D,bs", GEOMETRIES)
+@pytest.mark.parametrize("geom", GEOMS)
+def test_score_pages_geometry(gpu, geom, D, bs):
+    B, H_q, H_kv, ctx = geom
+    inp = make_paged_inputs(B, H_q, H_kv, D, ctx, block_size=bs, seed=200 + H_kv, device=gpu,
+                            hot_heads=[0], n_hot=4, hot_shift=4.0)
+    got = ops.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens, H_kv,
+                          H_q // H_kv, bs).cpu()
+    want = ref.score_pages(inp.q.cpu(), inp.k_cache.cpu(), inp.block_tables.cpu(),
+                           inp.context_lens.cpu(), H_kv, H_q // H_kv, bs)
+    _close(got, want, SCORE_RTOL)
+
+
+@pytest.mark.parametrize("D,bs,H_kv,ctx", [(64, 16, 16, 131072), (256, 16, 16, 65536),
+                                           (256, 16, 2, 65539), (64, 16, 2, 40000),
+                                           (128, 32, 8, 131072), (128, 64, 8, 65536 - 5),
+                                           (256, 64, 4, 65536)])
+def test_score_pages_geometry_long_context(gpu, D, bs, H_kv, ctx):
+    """Launches with 2 to 8 tiles per wave (and the whole-page layout over
+    many pages) against the oracle."""
+    inp = make_paged_inputs(1, 4 * H_kv, H_kv, D, ctx, block_size=bs, seed=210, device=gpu)
+    got = ops.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens, H_kv, 4,
+                          bs).cpu()
+    want = ref.score_pages(inp.q.cpu(), inp.k_cache.cpu(), inp.block_tables.cpu(),
+                           inp.context_lens.cpu(), H_kv, 4, bs)
+    _close(got, want, SCORE_RTOL)
+
+
+@pytest.mark.parametrize("D,bs", GEOMETRIES)
+@pytest.mark.parametrize("B,H_q,H,ctx", [(2, 32, 8, [3000, 1501]), (1, 28, 4, [8191]),
+                                         (3, 16, 2, [17, 530, 16]), (1, 8, 1, [5000])])
+def test_quest_geometry(gpu, B, H_q, H, ctx, D, bs):
+    """Quest scores of a first build and the page extremes it stores."""
+    inp = make_paged_inputs(B, H_q, H, D, ctx, block_size=bs, seed=B * 100 + H, device=gpu,
+                            hot_heads=[0], n_hot=4, hot_shift=6.0)
+    qm = ops.QuestPageMeta(inp.k_cache)
+    got = qm.scores(inp.q, inp.block_tables, inp.context_lens, H, H_q // H, bs)
+    K, bt, cl = inp.k_cache.cpu(), inp.block_tables.cpu(), inp.context_lens.cpu()
+    _close(got.cpu(), ref.quest_page_scores(inp.q.cpu(), K, bt, cl, H, H_q // H, bs),
+           QUEST_RTOL)
+    kmin, kmax = ref.page_key_minmax(K, bt, cl, bs)
+    meta = qm.meta.cpu().float()
+    for b in range(B):
+        for p in range(-(-int(cl[b]) // bs)):
+            blk = int(bt[b, p])
+            assert torch.equal(meta[blk, :, 0], kmin[b, p]), (b, p)
+            assert torch.equal(meta[blk, :, 1], kmax[b, p]), (b, p)
+
+
+@pytest.mark.parametrize("D,bs", GEOMETRIES)
+@pytest.mark.parametrize("seed", [0, 3, 5])
+def test_random_schedules_geometry(gpu, seed, D, bs):
+    """Random shapes and schedules of the backend at other head dimensions
+    and block sizes, ten steps with appends (crossing pages), in lockstep
+    with the oracle backend."""
+    cfg, kw = _random_schedule(seed)
+    cfg["head_dim"] = D
+    cfg["block_size"] = bs
+    stats, trace, lock = _run(gpu, cfg, kw, steps=10, seed=700 + seed)
+    print(f"seed {seed} D {D} bs {bs} {cfg} {kw}: {lock.summary()}")

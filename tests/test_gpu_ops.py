@@ -324,12 +324,12 @@ def test_lse_merge(gpu, out_dtype):
     assert torch.equal(got2, got)
 
 
-@pytest.mark.parametrize("D", [128, 64, 256])
-def test_append_kv_matches_reference_loop(gpu, D):
+@pytest.mark.parametrize("D,bs", [(128, 16), (64, 16), (256, 16), (128, 32), (64, 64)])
+def test_append_kv_matches_reference_loop(gpu, D, bs):
     from cvsa.runtime.kv_cache import PagedKVCache, SequenceKVManager
     B, H = 5, 8
-    cache = PagedKVCache(64, 16, H, D, device=str(gpu))
-    mgr = SequenceKVManager(cache, B, 16 * 8)
+    cache = PagedKVCache(64, bs, H, D, device=str(gpu))
+    mgr = SequenceKVManager(cache, B, bs * 8)
     g = torch.Generator().manual_seed(2)
     lens = [15, 16, 0, 33, 47]
     for b, n in enumerate(lens):
@@ -348,11 +348,11 @@ def test_append_kv_matches_reference_loop(gpu, D):
         vn = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
         if step % 3 == 0:
             mgr.append_token_kv(1, kn[1].to(gpu), vn[1].to(gpu))
-            nf = ref.append_token_kv(K, V, bt, ctx, alloc, nf, 1, kn[1], vn[1], 16)
+            nf = ref.append_token_kv(K, V, bt, ctx, alloc, nf, 1, kn[1], vn[1], bs)
         else:
             mgr.append_tokens_kv(kn.to(gpu), vn.to(gpu))
             for b in range(B):
-                nf = ref.append_token_kv(K, V, bt, ctx, alloc, nf, b, kn[b], vn[b], 16)
+                nf = ref.append_token_kv(K, V, bt, ctx, alloc, nf, b, kn[b], vn[b], bs)
     assert cache._next_free == nf
     assert torch.equal(mgr.block_tables.cpu(), bt)
     assert torch.equal(mgr.context_lens.cpu(), ctx)

@@ -364,15 +364,22 @@ def test_random_shapes_plan_head_dims(gpu, seed, D):
     _plan_equals_separate_kernels(gpu, seed, D)
 
 
-def _plan_equals_separate_kernels(gpu, seed, D):
+@pytest.mark.parametrize("BS", [32, 64])
+@pytest.mark.parametrize("seed", range(3))
+def test_random_shapes_plan_block_sizes(gpu, seed, BS):
+    """The same at block sizes 32 and 64 (speculation included at D = 128)."""
+    _plan_equals_separate_kernels(gpu, seed, [128, 64, 128][seed], BS)
+
+
+def _plan_equals_separate_kernels(gpu, seed, D, BS=16):
     g = torch.Generator().manual_seed(100 + seed)
     rnd = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))  # noqa: E731
     H = [1, 2, 4, 8, 16][rnd(0, 4)]
     G = rnd(1, 8)
     B = rnd(1, 3)
     ctx = [rnd(40, 6000) for _ in range(B)]
-    inp = make_paged_inputs(B, H * G, H, D, ctx, seed=seed, device=gpu,
-                            max_pages=max((c - 1) // 16 + 1 for c in ctx) + rnd(0, 3),
+    inp = make_paged_inputs(B, H * G, H, D, ctx, block_size=BS, seed=seed, device=gpu,
+                            max_pages=max((c - 1) // BS + 1 for c in ctx) + rnd(0, 3),
                             hot_heads=list(range(0, H, 2)), n_hot=4, hot_shift=8.0)
     W = inp.block_tables.shape[1]
     budget = max(3, int(W * [0.125, 0.25, 0.5][rnd(0, 2)]))
@@ -382,7 +389,7 @@ def _plan_equals_separate_kernels(gpu, seed, D):
     for speculate in (True, False):
         stats = torch.zeros(6, dtype=torch.int64, device=gpu)
         work = torch.zeros(2, dtype=torch.int64, device=gpu)
-        plan = ops.StepPlan(inp.q, inp.k_cache, inp.v_cache, bt, ctx_t, H, G, 16, budget, tau,
+        plan = ops.StepPlan(inp.q, inp.k_cache, inp.v_cache, bt, ctx_t, H, G, BS, budget, tau,
                             stats=stats, work=work, own_scores_cache=True, speculate=speculate)
         outs = []
         for step, kind in enumerate((_lib.STEP_FRESH, _lib.STEP_LAZY_CHECK, _lib.STEP_LAZY_CHECK,
@@ -403,22 +410,22 @@ def _plan_equals_separate_kernels(gpu, seed, D):
         if kind == "reuse":
             want.append(ops.sparse_decode_reuse(q, inp.k_cache, inp.v_cache, bt, ctx_t,
                                                 sel.view(B * H, -1), nph.view(B * H),
-                                                ops.next_power_of_2(budget), H, G, 16,
+                                                ops.next_power_of_2(budget), H, G, BS,
                                                 work=work))
             continue
-        ps = ops.score_pages(q, inp.k_cache, bt, ctx_t, H, G, 16)
+        ps = ops.score_pages(q, inp.k_cache, bt, ctx_t, H, G, BS)
         if kind == "fresh":
-            acc = ops.select_or_keep(ps, None, budget, ctx_t, 16, tau, sel, nph, cov, cache,
+            acc = ops.select_or_keep(ps, None, budget, ctx_t, BS, tau, sel, nph, cov, cache,
                                      stats)
         elif kind == "check":
             chk, cov = ops.check_coverage(ps, sel, nph, tau)
-            acc = ops.select_or_keep(ps, chk, budget, ctx_t, 16, tau, sel, nph, cov, cache,
+            acc = ops.select_or_keep(ps, chk, budget, ctx_t, BS, tau, sel, nph, cov, cache,
                                      stats)
         else:
-            acc = ops.select_or_keep(ps, None, budget, ctx_t, 16, tau, sel, nph, cov, None,
+            acc = ops.select_or_keep(ps, None, budget, ctx_t, BS, tau, sel, nph, cov, None,
                                      stats, count_gate=True)
         want.append(ops.verified_decode(q, inp.k_cache, inp.v_cache, bt, ctx_t, sel, nph, acc,
-                                        H, G, 16, output_dtype=q.dtype, work=work))
+                                        H, G, BS, output_dtype=q.dtype, work=work))
     for plan, p_stats, p_work, outs in runs:
         for step, (got, ref_out) in enumerate(zip(outs, want)):
             assert torch.equal(got, ref_out), (seed, step, plan.spec_state is not None)
