@@ -1,1096 +1,31 @@
-// Paged decode attention over a per-KV-head page list, emitting the
-// un-normalised softmax state (o, m, l) and/or the normalised output.
-//
-// Semantics follow the reference's sparse decode kernels
-// (cvsa/kernels/sparse_decode.py:14-132, :136-234, :423-500): for each
-// q-head, over the first n_sel listed pages of its KV head and the tokens
-// t < min(bs, ctx - page*bs) of each page (:76-80), s = (q . K) * D^-0.5,
-// m = max s, l = sum exp(s - m), o = sum exp(s - m) V (:101-124); the
-// normalised output is o / max(l, 1e-6) (:127, :271).  Split-K partial
-// states are combined with the log-sum-exp rule of _reduce_tiles_kernel
-// (:237-276, :576-606).
-//
-// MI355X mapping.  The reference launches one program per q-head, so each
-// K/V page tile is fetched G times.  Here a workgroup owns one KV head and a
-// contiguous range of its page list; each of its four waves takes every
-// fourth page, loads the page's 16 K rows and 16 V rows once (256 B per row,
-// 16-byte lane loads) and applies them to all G query heads of the group as
-// two small matrix-core tiles (S = K Q^T, O += P V; see MfmaEngine).  The
-// four waves merge in LDS.  When a head's pages span several workgroups
-// (splits), each stores its partial (o, m, l) and bumps the head's
-// completion counter; the last one to arrive merges the partials and writes
-// the outputs, so one launch does the whole decode.  The last workgroup
-// resets the counter to zero for the next launch.
-//
-// Ordering of the split hand-off.  Partials are written and read through a
-// raw buffer resource with the sc1 cache policy: on gfx950 such stores are
-// written through the issuing XCD's L2 to the device coherence point and
-// such loads miss in the reading XCD's L2, so no L2 writeback or invalidate
-// (an agent-scope release / acquire fence) is needed.  A workgroup waits
-// for its partial stores to complete (s_waitcnt vmcnt(0) and a barrier)
-// before its relaxed agent-scope atomic increment of the head's counter; the
-// last arriver issues its partial loads only after that atomic has
-// returned.  This rests on the gfx950 cache policy described, not on the
-// HIP memory model's release / acquire pairing.
-//
-// Head modes: a listed head walks page_indices[b,h,:n_per_head]; an
-// all-pages head walks pages 0..n_valid-1 (dense decode).
-//
-// Tiles: the kernels walk 16-token tiles.  A page (block) of block_size =
-// 16 * 2^ts tokens is 2^ts consecutive tiles of its block, so tile sub of
-// logical page lp is logical tile (lp << ts) | sub, stored at physical tile
-// (block << ts) | sub, 16 * H_kv * D elements apart.  Head walks, splits and
-// stream-K ranges count tiles; the effective-budget counters count pages.  In verified mode
-// accepted heads are listed and rejected heads walk every valid page: the
-// draft pages plus the complement pages in one pass, which equals the LSE
-// merge of the draft and complement partial softmaxes.
-#include "cvsa_common.h"
+// Host side of the paged decode: launch planning, argument checks,
+// workspaces and the C-ABI entry points (cvsa_sparse_decode,
+// cvsa_sparse_decode_noalloc, cvsa_verified_decode, cvsa_dense_decode and
+// their workspace helpers).  The kernels and their semantics are in
+// decode_kernels.h; decode_g*.hip instantiate them per GQA group size.
+#include "decode_kernels.h"
 #include "internal.h"
-#include "score_body.h"
-#include <hip/hip_fp16.h>
 
 #include <mutex>
 
 namespace cvsa {
 
-// Split partials of head dimension D are rows of part_stride(D) floats:
-// o[D], m, l and two pad words, so every row starts on a 16-byte boundary.
-// A q-head's o is D / 4 float4 chunks.
-__host__ __device__ constexpr int part_stride(int D) { return D + 4; }
-constexpr int kMaxSplits = 256;            // partials per head (and workgroups per launch)
-constexpr int kMinPagesPerWave = 2;        // pages per wave of a split, at least
-
-struct DecodeArgs {
-  const uint16_t *q;
-  int64_t q_sb, q_sh;
-  const uint16_t *k_cache;
-  const uint16_t *v_cache;
-  int64_t num_blocks;
-  const int32_t *block_tables;
-  int64_t bt_sb;
-  const int32_t *ctx_lens;
-  const int32_t *page_idx;  // NULL: every head walks all valid pages
-  int64_t idx_stride;
-  int max_sel;
-  const int32_t *n_pages;
-  const uint8_t *accept;  // non-NULL: verified mode
-  int H_kv, W;
-  int D;      // head dimension (the launch's engine is compiled for it)
-  int bs;     // block size (tokens per page)
-  int ts;     // tiles per page = 1 << ts
-  int max_sel_t;  // max_sel << ts
-  int heads;  // B * H_kv
-  int pps, n_splits;  // listed partition: tiles per split, splits per head
-  int sk_grid;        // stream-K partition: workgroups (<= kMaxSplits)
-  float scale;
-  float *o_unnorm, *m_out, *l_out;
-  void *out;
-  int out_dtype;
-  float *part;               // split partials (see PartBuf)
-  uint32_t part_bytes;
-  unsigned *counters;        // per head, zero between launches
-  unsigned long long *work;  // optional effective-budget counters
-  // A lazy check's speculative decode of its kept selection (or NULL):
-  // [0] != 0 predicts that the check keeps its selection, [1] records
-  // whether the speculative listed decode ran (and wrote the outputs).
-  int32_t *spec_state;
-};
-
-__device__ __forceinline__ void store_out(void *out, int dtype, int64_t i, float y) {
-  if (dtype == CVSA_DTYPE_BF16) {
-    reinterpret_cast<uint16_t *>(out)[i] = (uint16_t)f32_to_bf16_bits(y);
-  } else if (dtype == CVSA_DTYPE_FP16) {
-    reinterpret_cast<__half *>(out)[i] = __float2half_rn(y);
-  } else {
-    reinterpret_cast<float *>(out)[i] = y;
-  }
-}
-
-
-template <int D>
-__device__ __forceinline__ void write_outputs(const DecodeArgs &a, int64_t qrow, int d, float O,
-                                              float M, float L) {
-  if (a.o_unnorm != nullptr) {
-    a.o_unnorm[qrow * D + d] = O;
-    if (d == 0) {
-      a.m_out[qrow] = M;
-      a.l_out[qrow] = L;
-    }
-  }
-  if (a.out != nullptr) store_out(a.out, a.out_dtype, qrow * D + d, O / fmaxf(L, 1e-6f));
-}
-
-// Effective-budget counters: pages attended by this head (n tiles) and
-// n_valid(b).
-__device__ __forceinline__ void add_work(const DecodeArgs &a, int n, int ctx) {
-  atomicAdd(&a.work[0], (unsigned long long)(n >> a.ts));
-  atomicAdd(&a.work[1], (unsigned long long)max(0, n_valid_pages(ctx, a.bs)));
-}
-
-// Logical tile of entry e of a head's listed walk (tile e & (2^ts - 1) of
-// page idx_row[e >> ts]), or -1 when that page is outside [0, W).
-__device__ __forceinline__ int listed_tile(const DecodeArgs &a, const int32_t *idx_row, int e) {
-  const int lp = idx_row[e >> a.ts];
-  return lp >= 0 && lp < a.W ? (lp << a.ts) | (e & ((1 << a.ts) - 1)) : -1;
-}
-
-// Physical tile of logical tile lt of sequence b, or -1 (lt < 0, or a block
-// id outside the pool).  The block-table load is unconditional (clamped).
-__device__ __forceinline__ int tile_block(const DecodeArgs &a, int b, int lt) {
-  const int phys = a.block_tables[b * a.bt_sb + min(max(lt, 0) >> a.ts, a.W - 1)];
-  return lt >= 0 && phys >= 0 && phys < a.num_blocks ? (phys << a.ts) | (lt & ((1 << a.ts) - 1))
-                                                     : -1;
-}
-
-
-// Tiles walked by head bh: those of its listed pages (page_indices[bh,
-// :n_per_head]), or of every valid page (dense heads, rejected heads of a
-// verified launch).
-// MODE is a template parameter and verified mode loads accept[bh] and
-// n_per_head[bh] unconditionally and picks with selects: an earlier form
-// that branched on null pointers was miscompiled (a live scalar register was
-// reused across the branch).
-enum { kModeAll = 0, kModeListed = 1, kModeVerified = 2 };
-
-template <int MODE>
-__device__ __forceinline__ int head_pages(const DecodeArgs &a, int bh, bool &listed) {
-  int n_all = 0, n_list = 0;
-  if constexpr (MODE != kModeListed)
-    n_all = max(0, min(n_valid_pages(a.ctx_lens[bh / a.H_kv], a.bs), a.W)) << a.ts;
-  if constexpr (MODE != kModeAll) n_list = min(max(a.n_pages[bh], 0), a.max_sel) << a.ts;
-  if constexpr (MODE == kModeAll) {
-    listed = false;
-    return n_all;
-  } else if constexpr (MODE == kModeListed) {
-    listed = true;
-    return n_list;
-  } else {
-    listed = a.accept[bh] != 0;
-    return listed ? n_list : n_all;
-  }
-}
-
-// Stream-K partition.  The heads' page walks are concatenated (head-major)
-// into one list of T pages and cut into n_wg equal ranges; workgroup w owns
-// pages [start(w), start(w + 1)), start(w) = floor(w * T / n_wg).  n_wg is the
-// launch size, reduced so that a workgroup gets at least kMinPagesPerWg
-// pages.  T < 2^31 and n_wg <= kMaxSplits, so every quantity is computed in
-// 32 bits (64-bit division is a long instruction sequence on the GPU).
-constexpr int kMaxHeads = 4096;  // B * H_kv of one launch
-constexpr int kMinPagesPerWg = kMinPagesPerWave * 4;
-
-struct Partition {
-  int T, n, q, r;  // pages, workgroups, T / n, T % n
-  __device__ __forceinline__ Partition(int T_, int grid) : T(T_) {
-    n = max(1, min(grid, (T + kMinPagesPerWg - 1) / kMinPagesPerWg));
-    q = T / n;
-    r = T - q * n;
-  }
-  // floor(w * T / n) = w * q + floor(w * r / n), with w * r < n^2 < 2^31.
-  __device__ __forceinline__ int start(int w) const { return w * q + (w * r) / n; }
-  // The workgroup whose range holds page p (the largest w with start(w) <= p):
-  // a float estimate of (p + 1) * n / T, off by at most one, then corrected.
-  __device__ __forceinline__ int owner(int p) const {
-    int w = min(n - 1, (int)((float)(p + 1) * (float)n / (float)T));
-    if (start(w) > p) --w;
-    else if (w + 1 < n && start(w + 1) <= p) ++w;
-    return w;
-  }
-};
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-
-// The split partials of one launch, accessed through a raw buffer resource
-// with the agent-scope cache policy (sc1) at 16 (or 8) bytes per access:
-// stores reach the device coherence point before the split's completion
-// counter moves, and loads never return a line that another XCD's L2 still
-// holds.  Offsets are in floats; accesses past the range read 0 / are
-// dropped by the buffer bounds check.
-struct PartBuf {
-  static constexpr int kCpolAgent = 16;         // sc1
-  static constexpr int kRsrcWord3 = 0x00020000;  // 32-bit data format, raw
-  __amdgpu_buffer_rsrc_t r;
-  __device__ __forceinline__ PartBuf(float *base, uint32_t bytes)
-      : r(__builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, kRsrcWord3)) {}
-  __device__ __forceinline__ void store4(uint32_t off, f32x4 v) const {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)(off * 4), 0,
-                                           kCpolAgent);
-  }
-  __device__ __forceinline__ void store2(uint32_t off, f32x2 v) const {
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, (int)(off * 4), 0,
-                                          kCpolAgent);
-  }
-  __device__ __forceinline__ f32x4 load4(uint32_t off) const {
-    return __builtin_bit_cast(
-        f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off * 4), 0, kCpolAgent));
-  }
-  __device__ __forceinline__ f32x2 load2(uint32_t off) const {
-    return __builtin_bit_cast(
-        f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)(off * 4), 0, kCpolAgent));
-  }
-};
-
-// Outputs for q-row qrow, elements d0 .. d0+3 (one float4 chunk, d0 % 4 == 0):
-// one 16-byte store of o_unnorm and one 8- or 16-byte store of out.  The
-// outputs are the last stores of a launch, which cannot end before they
-// complete, so they are written as few, wide stores.
-template <int D>
-__device__ __forceinline__ void write_outputs4(const DecodeArgs &a, int64_t qrow, int d0,
-                                               f32x4 O, float M, float L) {
-  const int64_t i = qrow * D + d0;
-  if (a.o_unnorm != nullptr) {
-    *reinterpret_cast<f32x4 *>(a.o_unnorm + i) = O;
-    if (d0 == 0) {
-      a.m_out[qrow] = M;
-      a.l_out[qrow] = L;
-    }
-  }
-  if (a.out == nullptr) return;
-  if (a.out_dtype == CVSA_DTYPE_FP32) {
-    f32x4 y;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) y[e] = O[e] / fmaxf(L, 1e-6f);
-    *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(a.out) + i) = y;
-    return;
-  }
-  uint32_t w[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float y = O[e] / fmaxf(L, 1e-6f);
-    w[e] = a.out_dtype == CVSA_DTYPE_BF16 ? f32_to_bf16_bits(y)
-                                          : (uint32_t)__half_as_ushort(__float2half_rn(y));
-  }
-  *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(a.out) + i) =
-      make_uint2(w[0] | (w[1] << 16), w[2] | (w[3] << 16));
-}
-
-// LDS of the merge: (m, l) of every (split, g), rewritten in place as
-// (weight, l); the head's totals; per-thread sums of the split lanes.
-template <int G, int NT>
-struct MergeLds {
-  f32x2 ml[kMaxSplits * G];
-  float M[G], L[G];
-  f32x4 acc[NT];
-};
-
-// Merge of a head's n_act split partials by the last of its workgroups.
-// Thread t owns float4 chunk c = t % NC of the head's G x D outputs and the
-// splits j, j + J, ... (j = t / NC); their o chunks are loaded in batches of
-// KB, the next batch in flight while the current one is summed.  When the
-// outputs hold more chunks than the workgroup has threads (G x D > 4 NT) each
-// thread takes chunks t, t + NT, ... in turn, every split of each.  The
-// (m, l) pairs go to LDS first; one wave per q-head turns them into the
-// weights exp(m_sp - M) and the totals (M, L).
-template <int G, int D, int NT>
-__device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBuf &pb,
-                                               uint32_t head_off, int n_act, int bh, int n,
-                                               int ctx, MergeLds<G, NT> &s) {
-  constexpr int kChunksPerRow = D / 4;
-  constexpr int kPartStride = part_stride(D);
-  constexpr int NC = G * kChunksPerRow;
-  constexpr int J = NT / NC > 0 ? NT / NC : 1;
-  constexpr int NPASS = (NC + NT - 1) / NT;
-  constexpr int NW = NT / kWave;
-  constexpr int KB = 8;
-  const int t = threadIdx.x;
-  const int lane = t & 63;
-  const int wave = t >> 6;
-  const int j = NPASS == 1 ? t / NC : 0;
-  const bool active = t < NC * J;
-
-  for (int e = t; e < n_act * G; e += NT) s.ml[e] = pb.load2(head_off + e * kPartStride + D);
-  const int per_lane = active ? (n_act - j + J - 1) / J : 0;  // splits of this thread
-  auto load_batch = [&](int g, int d0, int b0, f32x4 (&v)[KB]) {
-#pragma unroll
-    for (int k = 0; k < KB; ++k) {
-      const int sp = min(j + (b0 + k) * J, n_act - 1);
-      v[k] = pb.load4(head_off + (sp * G + g) * kPartStride + d0);
-    }
-  };
-  f32x4 cur[KB];
-  {
-    const int c = NPASS == 1 ? t % NC : t;  // NPASS > 1: t < NT < NC
-    load_batch(c / kChunksPerRow, 4 * (c % kChunksPerRow), 0, cur);
-  }
-  __syncthreads();
-  for (int gg = wave; gg < G; gg += NW) {  // wave-uniform
-    float mx = -INFINITY;
-    for (int sp = lane; sp < n_act; sp += kWave) mx = fmaxf(mx, s.ml[sp * G + gg].x);
-    mx = wave_max_from_groups<1>(mx);
-    float ls = 0.f;
-    for (int sp = lane; sp < n_act; sp += kWave) {
-      const f32x2 v = s.ml[sp * G + gg];
-      const float w = (mx == -INFINITY || v.x == -INFINITY) ? 0.f : fast_exp(v.x - mx);
-      ls += w * v.y;
-      s.ml[sp * G + gg].x = w;
-    }
-    ls = wave_sum_from_groups<1>(ls);
-    if (lane == 0) {
-      s.M[gg] = mx;
-      s.L[gg] = ls;
-    }
-  }
-  __syncthreads();
-#pragma unroll 1
-  for (int pass = 0; pass < NPASS; ++pass) {
-    const int c = NPASS == 1 ? t % NC : min(t + pass * NT, NC - 1);
-    const bool live = NPASS == 1 ? active : t + pass * NT < NC;
-    const int g = c / kChunksPerRow;
-    const int d0 = 4 * (c % kChunksPerRow);
-    if (pass > 0) load_batch(g, d0, 0, cur);
-    f32x4 O = {0.f, 0.f, 0.f, 0.f};
-    for (int b0 = 0; b0 < per_lane; b0 += KB) {
-      f32x4 nxt[KB];
-      load_batch(g, d0, b0 + KB, nxt);
-#pragma unroll
-      for (int k = 0; k < KB; ++k) {
-        const int sp = min(j + (b0 + k) * J, n_act - 1);
-        const float w = b0 + k < per_lane ? s.ml[sp * G + g].x : 0.f;
-        O += w * cur[k];
-      }
-#pragma unroll
-      for (int k = 0; k < KB; ++k) cur[k] = nxt[k];
-    }
-    if constexpr (J > 1) {
-      s.acc[t] = O;
-      __syncthreads();
-      if (active && j == 0) {
-#pragma unroll
-        for (int jj = 1; jj < J; ++jj) O += s.acc[t + jj * NC];
-      }
-    }
-    if (live && j == 0) write_outputs4<D>(a, (int64_t)bh * G + g, d0, O, s.M[g], s.L[g]);
-  }
-  if (t == 0 && a.work != nullptr) add_work(a, n, ctx);
-}
-
-// ---------------------------------------------------------------- engines
-// A page engine owns one wave's softmax state for the G query heads of a KV
-// head and applies pages to it.  Page = the K and V rows of one page held in
-// registers (fetched PD pages ahead); consume() applies one page; finish()
-// leaves the wave's (o, m, l) in LDS.
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef short short4_t __attribute__((ext_vector_type(4)));
-typedef float float4_t __attribute__((ext_vector_type(4)));
-
-// MFMA engine: the G query heads (padded to 16) of a KV head against a page
-// of 16 tokens are two small dense tiles for the matrix cores.
-//   S = K Q^T: v_mfma_f32_16x16x32_bf16, four d-chunks of 32.  A operand =
-//     K rows (lane l: token l%16, d 32kk + 8(l/16) .. +8, one 16-byte load),
-//     B operand = Q^T (loaded once), result lane l: head l%16, tokens
-//     4(l/16) .. +4.
-//   O += P V: v_mfma_f32_16x16x16_bf16, eight 16-column blocks of d.  The S
-//     result layout is exactly the A operand layout of P (head l%16, tokens
-//     4(l/16) .. +4), so P needs no data movement; it is split into a bf16
-//     high part and a bf16 remainder (two MFMAs) to keep ~16 mantissa bits.
-//     The B operand wants 4 tokens of one d column per lane: the V page goes
-//     through a wave-private LDS tile (rows padded to 272 bytes so the four
-//     lane groups read disjoint banks).  Result lane l: heads 4(l/16) .. +4,
-//     d column 16 blk + l%16.
-// Softmax state: m and the running l of head l%16 live in the four lanes of
-// that head; a rescale of O rows goes through LDS (16 factors per wave).
-template <int G, int D>
-struct MfmaEngine {
-  static_assert(G <= 16, "GQA group larger than the MFMA tile");
-  static_assert(D == 64 || D == 128 || D == 256, "head dimension");
-  static constexpr int kD = D;
-  static constexpr int NK = D / 32;         // S = K Q^T MFMAs (32 dimensions each)
-  static constexpr int NB = D / 16;         // O column blocks (16 dimensions each)
-  static constexpr int LPR = D / 8;         // lanes per V row (16 bytes each)
-  static constexpr int RPL = kWave / LPR;   // V rows per wave load
-  static constexpr int NV = kPageTokens / RPL;  // V loads per page
-  static constexpr int kVRow = D + 8;       // LDS row of the V tile, in bf16
-  struct Page {
-    uint4 k[NK], v[NV];
-  };
-  struct Lds {
-    uint16_t v[kPageTokens * kVRow];
-    float alpha[16];
-  };
-
-  float4_t o[NB];
-  bf16x8_t qb[NK];
-  float m_g, l_g;
-  int lane;
-  int64_t koff, voff, row_stride;
-  float scale;
-
-  __device__ __forceinline__ void init(const DecodeArgs &a, int b, int h, int lane_, Lds &) {
-    lane = lane_;
-    scale = a.scale;
-    row_stride = (int64_t)a.H_kv * D;
-    const int c16 = lane & 15, grp = lane >> 4;
-    koff = (int64_t)h * D + c16 * row_stride + 8 * grp;
-    voff = (int64_t)h * D + (lane / LPR) * row_stride + 8 * (lane % LPR);
-    // Rows past the group repeat head G-1: MFMA output rows are independent
-    // and those rows are never written out.  No select on the loaded value,
-    // so nothing waits for q before the first page is consumed.
-    const uint16_t *qrow = a.q + b * a.q_sb + (int64_t)(h * G + min(c16, G - 1)) * a.q_sh;
-#pragma unroll
-    for (int kk = 0; kk < NK; ++kk)
-      qb[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(qrow + 32 * kk + 8 * grp));
-#pragma unroll
-    for (int blk = 0; blk < NB; ++blk) o[blk] = float4_t{0.f, 0.f, 0.f, 0.f};
-    m_g = -INFINITY;
-    l_g = 0.f;
-  }
-
-  // K loads are plain: one instruction reads 64 bytes of each of 16 rows, so
-  // every 128-byte line is requested by two instructions, and with the
-  // nontemporal hint the line could leave the cache in between (measured:
-  // more HBM fetches, slower).  V loads read whole rows and keep the hint.
-  __device__ __forceinline__ void fetch(const uint16_t *kp, const uint16_t *vp, Page &pg) const {
-#pragma unroll
-    for (int kk = 0; kk < NK; ++kk)
-      pg.k[kk] = *reinterpret_cast<const uint4 *>(kp + koff + 32 * kk);
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-      pg.v[i] = stream_load16(vp + voff + RPL * i * row_stride);
-  }
-
-  __device__ __forceinline__ void consume(Page &pg, int ntok, Lds &lds) {
-    const int c16 = lane & 15, grp = lane >> 4;
-    const int t0 = 4 * grp;
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < NK; ++kk)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, pg.k[kk]),
-                                                    qb[kk], acc, 0, 0, 0);
-    float sv[4];
-    float pm = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      sv[j] = t0 + j < ntok ? acc[j] * scale : -INFINITY;
-      pm = fmaxf(pm, sv[j]);
-    }
-    float x, y;
-    xchg16(pm, x, y);
-    pm = fmaxf(x, y);
-    xchg32(pm, x, y);
-    pm = fmaxf(x, y);  // page max of head c16, in all four of its lanes
-    const float m_new = fmaxf(m_g, pm);
-    if (__ballot(m_new > m_g) != 0) {  // some head of the wave rescales
-      const float alpha = m_new > m_g ? (m_g == -INFINITY ? 0.f : fast_exp(m_g - m_new)) : 1.f;
-      l_g *= alpha;
-      m_g = m_new;
-      if (lane < 16) lds.alpha[lane] = alpha;
-      const float4 ar = *reinterpret_cast<const float4 *>(&lds.alpha[t0]);  // rows 4grp .. +4
-#pragma unroll
-      for (int blk = 0; blk < NB; ++blk) {
-        o[blk][0] *= ar.x;
-        o[blk][1] *= ar.y;
-        o[blk][2] *= ar.z;
-        o[blk][3] *= ar.w;
-      }
-    }
-    // P (head c16, tokens t0 .. t0+3) as bf16 high part + bf16 remainder.
-    short4_t ph, pl;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float p = sv[j] == -INFINITY ? 0.f : fast_exp(sv[j] - m_g);
-      l_g += p;
-      const uint32_t hi = f32_to_bf16_bits(p);
-      const float rem = p - __uint_as_float(hi << 16);
-      ph[j] = (short)hi;
-      pl[j] = (short)f32_to_bf16_bits(rem);
-    }
-    // V page -> LDS tile (rows past the context are stored as zeros: the
-    // reference never reads them).
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int t = RPL * i + lane / LPR;
-      const uint4 w = t < ntok ? pg.v[i] : make_uint4(0u, 0u, 0u, 0u);
-      *reinterpret_cast<uint4 *>(&lds.v[t * kVRow + 8 * (lane % LPR)]) = w;
-    }
-#pragma unroll
-    for (int blk = 0; blk < NB; ++blk) {
-      short4_t vb;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) vb[j] = (short)lds.v[(t0 + j) * kVRow + 16 * blk + c16];
-      o[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, vb, o[blk], 0, 0, 0);
-      o[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, vb, o[blk], 0, 0, 0);
-    }
-  }
-
-  template <int NW>
-  __device__ __forceinline__ void finish(int wave, int lane_, float (*s_o)[G][D],
-                                         float (*s_m)[G], float (*s_l)[G]) {
-    const int c16 = lane & 15, grp = lane >> 4;
-    float x, y;
-    xchg16(l_g, x, y);
-    l_g = x + y;
-    xchg32(l_g, x, y);
-    l_g = x + y;  // head c16's l over all 16 token rows
-    if (lane < G) {
-      s_m[wave][lane] = m_g;
-      s_l[wave][lane] = l_g;
-    }
-#pragma unroll
-    for (int blk = 0; blk < NB; ++blk)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int g = 4 * grp + j;
-        if (g < G) s_o[wave][g][16 * blk + c16] = o[blk][j];
-      }
-  }
-};
-
-template <class L, int NW>
-__device__ __forceinline__ L &s_eng_of(L (&eng)[NW], int wave) { return eng[wave]; }
-
-// End of one workgroup's walk over pages of head h (the waves' states are in
-// s_o / s_m / s_l, behind a barrier).  If the workgroup is the head's only
-// contributor (n_act == 1) it writes the outputs.  Otherwise it stores its
-// partial (o, m, l) in partial row my_row, bumps the head's counter, and the
-// last of the n_act contributors merges rows first_row .. first_row+n_act-1.
-template <int G, int D, int NW>
-__device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const PartBuf &pb, int h,
-                                                 int n, int ctx, int n_act, uint32_t my_row,
-                                                 uint32_t first_row,
-                                                 const float (&s_o)[NW][G][D],
-                                                 const float (&s_m)[NW][G],
-                                                 const float (&s_l)[NW][G], int &s_last,
-                                                 MergeLds<G, NW * kWave> &s_merge) {
-  constexpr int NT = NW * kWave;
-  constexpr int kChunksPerRow = D / 4;
-  constexpr int kPartStride = part_stride(D);
-  // Workgroup state of float4 chunk c (q-head g = c / (D/4), elements d0 .. d0+3):
-  // the waves' (o, m, l) rescaled to the workgroup maximum.
-  auto wg_state4 = [&](int c, f32x4 &O, float &M, float &L) {
-    const int g = c / kChunksPerRow, d0 = 4 * (c % kChunksPerRow);
-    M = s_m[0][g];
-#pragma unroll
-    for (int wv = 1; wv < NW; ++wv) M = fmaxf(M, s_m[wv][g]);
-    O = f32x4{0.f, 0.f, 0.f, 0.f};
-    L = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int wv = 0; wv < NW; ++wv) {
-        const float mw = s_m[wv][g];
-        if (mw != -INFINITY) {
-          const float f = fast_exp(mw - M);
-          O += f * *reinterpret_cast<const f32x4 *>(&s_o[wv][g][d0]);
-          L += s_l[wv][g] * f;
-        }
-      }
-    }
-  };
-  if (n_act <= 1) {
-    for (int c = threadIdx.x; c < G * kChunksPerRow; c += NT) {
-      f32x4 O;
-      float M, L;
-      wg_state4(c, O, M, L);
-      write_outputs4<D>(a, (int64_t)h * G + c / kChunksPerRow, 4 * (c % kChunksPerRow), O, M,
-                        L);
-    }
-    if (threadIdx.x == 0 && a.work != nullptr) add_work(a, n, ctx);
-    return;
-  }
-  const uint32_t my_off = my_row * (uint32_t)(G * kPartStride);
-  for (int c = threadIdx.x; c < G * kChunksPerRow; c += NT) {
-    f32x4 O;
-    float M, L;
-    wg_state4(c, O, M, L);
-    const int g = c / kChunksPerRow, d0 = 4 * (c % kChunksPerRow);
-    pb.store4(my_off + g * kPartStride + d0, O);
-    if (d0 == 0) pb.store2(my_off + g * kPartStride + D, f32x2{M, L});
-  }
-  // Every wave's partial stores have completed before the counter moves.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(&a.counters[h], 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (unsigned)(n_act - 1);
-  }
-  __syncthreads();
-  if (s_last) {
-    // Last contributor of the head: merge its partials, write the outputs.
-    if (threadIdx.x == 0)
-      __hip_atomic_store(&a.counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_partials<G, D, NT>(a, pb, first_row * (uint32_t)(G * kPartStride), n_act, h, n,
-                             ctx, s_merge);
-  }
-}
-
-// LDS of a workgroup's page walk and epilogue: the waves' (o, m, l), the
-// last-arriver flag, and the engines' LDS, which is dead once a walk ends and
-// is reused by the merge.
-template <int G, class Engine, int NW>
-struct WalkLds {
-  union Tail {
-    typename Engine::Lds eng[NW];
-    MergeLds<G, NW * kWave> merge;
-  };
-  float o[NW][G][Engine::kD] __attribute__((aligned(16)));
-  float m[NW][G];
-  float l[NW][G];
-  int last;
-  Tail tail __attribute__((aligned(16)));
-};
-
-// The first page-list entries of split `split` of head bh (lane j of wave
-// w: entry r0 + w + NW j) and their block-table entries, requested as early
-// as possible: their position only needs r0 = split * pps.  Lanes past the
-// head's pages are discarded by the walk.
-template <int NW>
-__device__ __forceinline__ int listed_first_entry(const DecodeArgs &a, int split, int bh,
-                                                  int wave, int lane) {
-  if (a.max_sel <= 0) return 0;
-  return listed_tile(a, a.page_idx + (int64_t)bh * a.idx_stride,
-                     min(split * a.pps + wave + NW * lane, a.max_sel_t - 1));
-}
-
-__device__ __forceinline__ int listed_first_block(const DecodeArgs &a, int bh, int lt) {
-  if (a.max_sel <= 0) return 0;
-  return tile_block(a, bh / a.H_kv, lt);
-}
-
-template <int NW>
-__device__ __forceinline__ void listed_first_pages(const DecodeArgs &a, int split, int bh,
-                                                   int wave, int lane, int &lp, int &phys) {
-  lp = listed_first_entry<NW>(a, split, bh, wave, lane);
-  phys = listed_first_block(a, bh, lp);
-}
-
-// Listed pages of a head (the sparse decode of reuse steps, and verified
-// launches whose heads are all accepted): split s of head bh walks listed
-// pages [s * pps, (s + 1) * pps) of bh; splits past a head's pages only take
-// part when the head is empty (split 0 writes its outputs).  Partial row of
-// (split, head) = head * n_splits + split.
-template <int G, class Engine, int NW, int PD>
-__device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int bh, int spec_lp,
-                                            int spec_phys, WalkLds<G, Engine, NW> &L) {
-  using Page = typename Engine::Page;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int b = bh / a.H_kv;
-  const int h = bh - b * a.H_kv;
-  const int ctx = __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
-  const int pps = a.pps;
-  const int r0 = split * pps;
-  const int32_t *idx_row = a.page_idx + (int64_t)bh * a.idx_stride;
-  const int n = min(max(__builtin_amdgcn_readfirstlane(a.n_pages[bh]), 0), a.max_sel) << a.ts;
-  const int r1 = min(n, r0 + pps);
-  const int n_act = (n + pps - 1) / pps;  // splits holding pages of this head
-  if (r0 >= r1 && !(split == 0 && n_act == 0)) return;  // uniform
-
-  Engine eng;
-  eng.init(a, b, h, lane, s_eng_of(L.tail.eng, wave));
-  const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * Engine::kD;  // between blocks
-  const int npw = max(0, (r1 - r0 - wave + NW - 1) / NW);
-  for (int c0 = 0; c0 < npw; c0 += kWave) {
-    const int cn = min(kWave, npw - c0);
-    int my_phys = 0, my_ntok = 0;
-    if (lane < cn) {
-      const int lt = c0 == 0 ? spec_lp : listed_tile(a, idx_row, r0 + wave + NW * (c0 + lane));
-      if (lt >= 0) {
-        const int pt = c0 == 0 ? spec_phys : tile_block(a, b, lt);
-        if (pt >= 0) {
-          my_phys = pt;
-          my_ntok = max(0, min(kPageTokens, ctx - lt * kPageTokens));
-        }
-      }
-    }
-    // Loads are unconditional so that no branch separates a prefetch from
-    // the page being consumed: a page without valid tokens reads block 0 (in
-    // bounds) and is masked out by consume(); prefetches past the end re-read
-    // the wave's last page (already cached) and are never consumed.
-    auto fetch = [&](int j, Page &pg) {
-      const int64_t base = (int64_t)__builtin_amdgcn_readlane(my_phys, j) * page_elems;
-      eng.fetch(a.k_cache + base, a.v_cache + base, pg);
-      return __builtin_amdgcn_readlane(my_ntok, j);
-    };
-    Page pbuf[PD];
-    int nt[PD];
-    // The first trip fetches pages 0..PD-1 and consumes page 0; every fetch
-    // of a slot uses the same registers and the wait counts see PD-1 pages
-    // outstanding.
-    for (int j = 1 - PD; j < cn; j += PD) {
-#pragma unroll
-      for (int u = 0; u < PD; ++u) {
-        const int slot = (u + PD - 1) % PD;  // slot of page j+u+PD-1
-        nt[slot] = fetch(min(j + u + PD - 1, cn - 1), pbuf[slot]);
-        if (j + u >= 0 && j + u < cn) eng.consume(pbuf[u], nt[u], s_eng_of(L.tail.eng, wave));
-      }
-    }
-  }
-  eng.template finish<NW>(wave, lane, L.o, L.m, L.l);
-  __syncthreads();
-  const PartBuf pb(a.part, a.part_bytes);
-  segment_epilogue<G, Engine::kD, NW>(a, pb, bh, n, ctx, n_act,
-                                      (uint32_t)(bh * a.n_splits + split),
-                          (uint32_t)(bh * a.n_splits), L.o, L.m, L.l, L.last, L.tail.merge);
-}
-
-// The listed decode: a static grid of (split, head) workgroups.
-template <int G, class Engine, int NW, int PD>
-__global__ __launch_bounds__(NW * kWave) void listed_decode_kernel(const DecodeArgs a) {
-  __shared__ WalkLds<G, Engine, NW> L;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  int lp, phys;
-  listed_first_pages<NW>(a, blockIdx.x, blockIdx.y, wave, lane, lp, phys);
-  listed_walk<G, Engine, NW, PD>(a, blockIdx.x, blockIdx.y, lp, phys, L);
-}
-
-// 16-token tiles per scoring wave of the fused launch below.
-constexpr int kSpecScorePPW = 8;
-
-// A lazy check's page scoring and the speculative listed decode of its
-// cached selection in one launch.  Workgroups [0, n_splits * heads) are the
-// listed decode's (split, head) workgroups, w -> (w % n_splits, w /
-// n_splits), bit for bit listed_decode_kernel; they run only if
-// spec_state[0] predicts that the check keeps its selection, and workgroup 0
-// records in spec_state[1] whether they ran.  The other workgroups score
-// pages as score_pages_group_kernel<128, ...> does (score_body.h; kSpecScorePPW
-// tiles per wave, workgroup x of sequence b at index n_dec + b * score_gx + x).
-// The parts share no memory: the decode reads the cached selection, which
-// only the check's select-or-keep, launched after this kernel, rewrites.
-// One launch lets the decode's dependent metadata loads and split hand-off
-// overlap the scoring stream without a second stream and its events.
-// Three waves per SIMD (the register budget that allows, 168 VGPRs, holds
-// the decode without spills): 768 workgroups resident instead of 512, so the
-// decode and scoring workgroups of a cfg3 launch all run at once (check
-// step 68.4 -> 64.5 us at cfg3, 82.2 -> 75.5 us at cfg4).
-template <int G, class Engine, int NW, int PD>
-__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(3)))
-void score_spec_kernel(const DecodeArgs a,
-                                                                const ScoreArgs s,
-                                                                int score_gx) {
-  static_assert(NW == 4, "the scoring part runs four waves per workgroup");
-  __shared__ WalkLds<G, Engine, NW> L;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n_dec = a.n_splits * a.heads;
-  const int w = blockIdx.x;
-  if (w >= n_dec) {  // uniform
-    const int sw = w - n_dec;
-    score_group_wave<128, kSpecScorePPW>(s, a.H_kv, (sw % score_gx) * NW + wave, sw / score_gx);
-    return;
-  }
-  const int split = w % a.n_splits;
-  const int bh = w / a.n_splits;
-  int lp, phys;
-  listed_first_pages<NW>(a, split, bh, wave, lane, lp, phys);
-  const int go = __builtin_amdgcn_readfirstlane(a.spec_state[0]);
-  if (w == 0 && threadIdx.x == 0) a.spec_state[1] = go;
-  if (go == 0) return;  // uniform
-  listed_walk<G, Engine, NW, PD>(a, split, bh, lp, phys, L);
-}
-
-// Effective-budget counters of a verified launch whose heads were all
-// accepted and whose outputs a speculative listed decode already wrote:
-// what the listed walks would have added, summed by one workgroup.
-template <int NT>
-__device__ __forceinline__ void add_listed_work(const DecodeArgs &a, unsigned long long *red) {
-  unsigned long long n = 0, nv = 0;
-  for (int bh = threadIdx.x; bh < a.heads; bh += NT) {
-    n += (unsigned long long)min(max(a.n_pages[bh], 0), a.max_sel);
-    nv += (unsigned long long)max(0, n_valid_pages(a.ctx_lens[bh / a.H_kv], a.bs));
-  }
-  if (threadIdx.x == 0) red[0] = red[1] = 0ull;
-  __syncthreads();
-  if (n) atomicAdd(&red[0], n);
-  if (nv) atomicAdd(&red[1], nv);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    atomicAdd(&a.work[0], red[0]);
-    atomicAdd(&a.work[1], red[1]);
-  }
-}
-
-// NW waves per workgroup, PD pages of K/V in flight per wave.
-//
-// Every workgroup first computes the pages each head walks and their prefix
-// (the same partition in every workgroup), then walks the segments of its
-// range: (head h, pages s0..s1 of h's walk).  A segment that is a whole head
-// writes the outputs; otherwise it stores a partial (o, m, l) in row w + h of
-// the partial buffer (unique: a later workgroup never starts at an earlier
-// head, so (w, h) -> w + h is one-to-one, and head h's partials are the
-// consecutive rows owner(first page) + h .. owner(last page) + h), bumps the
-// head's counter, and the last contributor merges.  Heads that walk no pages
-// are written by workgroup h mod n_wg.
-template <int G, class Engine, int NW, int PD, int MODE>
-__global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const DecodeArgs a) {
-  constexpr int NT = NW * kWave;         // threads per workgroup
-  static_assert(NW == 4, "kMinPagesPerWg assumes four waves");
-  using Page = typename Engine::Page;
-
-  __shared__ WalkLds<G, Engine, NW> L;
-  __shared__ int s_wsum[NW];
-  __shared__ int s_odd[NW];               // a head of the wave's pass walks != max_sel pages
-  __shared__ int s_start[kMaxHeads + 1];  // exclusive prefix of pages per head
-  __shared__ uint8_t s_listed[kMaxHeads];
-  __shared__ unsigned long long s_work[2];
-  auto &s_o = L.o;
-  auto &s_m = L.m;
-  auto &s_l = L.l;
-  auto &s_last = L.last;
-  auto &s_tail = L.tail;
-  auto &s_eng = s_tail.eng;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int w = blockIdx.x;
-  const int heads = a.heads;
-  constexpr int D = Engine::kD;
-  const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * D;  // between blocks
-
-  // Verified launches whose heads are all accepted (a lazy check that keeps
-  // its selection, or a scoring step whose gate passes everywhere) run the
-  // listed decode's static partition: workgroup w takes split w % n_splits
-  // of head w / n_splits, exactly as listed_decode_kernel, so the outputs
-  // are bit for bit those of the listed decode.  Its first page-list
-  // entries are requested together with the accept flags and spec_state,
-  // their block-table entries once the launch is known to walk.  When the
-  // check kept its selection (spec_state[0], written by the check's
-  // select-or-keep) and a speculative listed decode of that selection
-  // already wrote the outputs (spec_state[1]), only the effective-budget
-  // counters are booked.  Every head accepted does not imply a kept
-  // selection: a rejected head is reselected and accepted when the new
-  // selection passes its gate.
-  if constexpr (MODE == kModeVerified) {
-    const int n_listed = a.n_splits * heads;
-    const int split = w % max(a.n_splits, 1);
-    const int bh = min(w / max(a.n_splits, 1), heads - 1);
-    const int lp = listed_first_entry<NW>(a, split, bh, wave, lane);
-    int spec_done = 0;
-    if (a.spec_state != nullptr)
-      spec_done = __builtin_amdgcn_readfirstlane(a.spec_state[0] & a.spec_state[1]);
-    int rejected = 0;
-    for (int i = threadIdx.x; i < heads; i += NT) rejected |= a.accept[i] == 0;
-    if (__syncthreads_or(rejected) == 0) {  // uniform
-      if (spec_done != 0) {
-        if (w == 0 && a.work != nullptr) add_listed_work<NT>(a, s_work);
-        return;
-      }
-      if (w < n_listed)
-        listed_walk<G, Engine, NW, PD>(a, split, bh, lp, listed_first_block(a, bh, lp), L);
-      return;
-    }
-  }
-
-  // Speculative page lookups for the common case in which every head walks
-  // max_sel listed pages: the range start is then known without the scan.
-  // The first page-list entries, the head's context length and q and the
-  // head counts of the scan are requested at entry, the pages' block-table
-  // entries as soon as the page-list entries arrive, and the first PD pages
-  // of K/V before the scan: two memory round trips fewer before the first
-  // K/V load.  Used only if the scan confirms the case.  The loads are
-  // issued without branches (indices clamped; a WG without a speculated
-  // range reads harmless in-bounds entries and discards them), so the
-  // compiler never has to drain them at a join.
-  Engine eng;
-  const int T_spec = heads * a.max_sel_t;
-  const Partition spec_part(T_spec, a.sk_grid);
-  int spec_lp = 0, spec_phys = 0, h_spec = -1, r_spec = 0, ctx_spec = 0, g1_spec = 0;
-  int b_spec = 0, h_c = 0;  // clamped speculated head and its sequence
-  if constexpr (MODE != kModeAll) {
-    const int ms = max(a.max_sel_t, 1);
-    const int wc = min(w, spec_part.n - 1);
-    const int g0 = spec_part.start(wc);
-    g1_spec = spec_part.start(wc + 1);
-    const int hs = min(g0 / ms, heads - 1);
-    r_spec = g0 - hs * ms;
-    h_c = hs;
-    b_spec = hs / a.H_kv;
-    const int rs = max(0, min(r_spec + wave + NW * lane, a.max_sel_t - 1));
-    const int32_t *src =
-        a.max_sel > 0 ? a.page_idx + (int64_t)hs * a.idx_stride + (rs >> a.ts) : a.block_tables;
-    const int lp0 = *src;
-    spec_lp = lp0 >= 0 && lp0 < a.W ? (lp0 << a.ts) | (rs & ((1 << a.ts) - 1)) : -1;
-    ctx_spec = __builtin_amdgcn_readfirstlane(a.ctx_lens[b_spec]);
-    eng.init(a, b_spec, hs - b_spec * a.H_kv, lane, s_eng[wave]);
-    if (a.max_sel > 0 && w < spec_part.n) h_spec = hs;
-  }
-
-  // Pages per head, one head per thread and pass of NT heads (loads issued
-  // without a branch, index clamped), scanned into their exclusive prefix
-  // in s_start.
-  auto wave_incl_scan = [&](int c) { return (int)wave_incl_scan_u32((uint32_t)c); };
-  bool l_first = false;
-  int c_first = head_pages<MODE>(a, min((int)threadIdx.x, heads - 1), l_first);
-  if constexpr (MODE != kModeAll)
-    spec_phys = tile_block(a, b_spec, spec_lp);
-  if ((int)threadIdx.x >= heads) c_first = 0;
-  const int incl_first = wave_incl_scan(c_first);
-  if (lane == kWave - 1) s_wsum[wave] = incl_first;
-  const bool odd_first = __ballot((int)threadIdx.x < heads && c_first != a.max_sel_t) != 0;
-  if (lane == 0) s_odd[wave] = odd_first ? 1 : 0;
-
-  // One wave's walk over its pages s0 + wave + NW*j of a segment, in chunks
-  // of up to 64 pages: lane j of a chunk looks up page j's block id and
-  // valid-token count; the loop reads them with readlane and keeps PD pages
-  // of K/V loads in flight (slot (u + PD - 1) % PD holds page u after the
-  // prologue).  Loads are unconditional so that no branch separates a
-  // prefetch from the page being consumed: a page without valid tokens reads
-  // block 0 (in bounds) and is masked out by consume(); prefetches past the
-  // end re-read the wave's last page (already cached) and are never consumed.
-  Page pbuf[PD];
-  int nt[PD];                 // logical page of each slot (kNoPage: none)
-  int my_phys = 0, my_lp = 0;
-  int cur_ctx = 0;            // context length of the segment being walked
-  constexpr int kNoPage = 1 << 26;  // ctx - kNoPage * 16 < 0: no valid token
-  auto lookup = [&](int s0, int c0, int cn, bool listed, const int32_t *idx_row, int b,
-                    bool spec) {
-    const int r = s0 + wave + NW * (c0 + lane);
-    int lp = r, phys = 0;
-    if (spec) {  // the speculative entries of the chunk (tile of entry r), consumed by every lane
-      lp = spec_lp;
-      phys = spec_phys;
-    } else if (lane < cn) {
-      if (listed) lp = listed_tile(a, idx_row, r);
-      phys = tile_block(a, b, lp);
-    }
-    const bool ok = lane < cn && lp >= 0 && phys >= 0;
-    my_phys = ok ? phys : 0;
-    my_lp = ok ? lp : kNoPage;
-  };
-  // Page j of the chunk into pg; returns its logical page (the valid-token
-  // count needs the context length only when the page is consumed).
-  auto fetch = [&](int j, Page &pg) {
-    const int64_t base = (int64_t)__builtin_amdgcn_readlane(my_phys, j) * page_elems;
-    eng.fetch(a.k_cache + base, a.v_cache + base, pg);
-    return __builtin_amdgcn_readlane(my_lp, j);
-  };
-  auto ntok = [&](int lp) { return min(kPageTokens, max(0, cur_ctx - lp * kPageTokens)); };
-  auto prologue = [&](int cn) {
-#pragma unroll
-    for (int u = 0; u < PD; ++u)
-      nt[(u + PD - 1) % PD] = fetch(max(0, min(u, cn - 1)), pbuf[(u + PD - 1) % PD]);
-  };
-  auto steady = [&](int cn) {
-    eng.consume(pbuf[PD - 1], ntok(nt[PD - 1]), s_eng[wave]);  // page 0
-    for (int j = 1; j < cn; j += PD) {
-#pragma unroll
-      for (int u = 0; u < PD; ++u) {
-        const int slot = (u + PD - 1) % PD;  // slot of page j+u+PD-1
-        nt[slot] = fetch(min(j + u + PD - 1, cn - 1), pbuf[slot]);
-        if (j + u < cn) eng.consume(pbuf[u], ntok(nt[u]), s_eng[wave]);
-      }
-    }
-  };
-
-  // First PD pages of the speculated segment (a WG without one fetches block
-  // 0 and never consumes it).
-  if constexpr (MODE != kModeAll) {
-    const int s1 = min(g1_spec, (h_c + 1) * a.max_sel_t) - h_c * a.max_sel_t;
-    const int npw = h_spec >= 0 ? max(0, (s1 - r_spec - wave + NW - 1) / NW) : 0;
-    lookup(r_spec, 0, min(kWave, npw), true, nullptr, b_spec, true);
-    prologue(min(kWave, npw));
-  }
-  // Pass 0 (peeled: a loop header here makes the compiler wait for the
-  // speculative loads), then the passes of launches with more than NT heads.
-  int uneven = 0;  // some head walks a number of pages other than max_sel
-  auto finish_pass = [&](int hh, int c, int incl, bool lst, int &carry) {
-    lds_barrier();
-    int excl = incl - c, total = 0;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) {
-      if (i < wave) excl += s_wsum[i];
-      total += s_wsum[i];
-      uneven |= s_odd[i];
-    }
-    if (hh < heads) {
-      s_start[hh] = carry + excl;
-      s_listed[hh] = lst;
-    }
-    carry += total;
-    lds_barrier();  // s_wsum is rewritten by the next pass
-  };
-  int carry = 0;
-  finish_pass(threadIdx.x, c_first, incl_first, l_first, carry);
-  if (heads > NT) {  // uniform
-    for (int base = NT; base < heads; base += NT) {
-      const int hh = base + threadIdx.x;
-      bool lst = false;
-      int c = head_pages<MODE>(a, min(hh, heads - 1), lst);
-      if (hh >= heads) c = 0;
-      const int incl = wave_incl_scan(c);
-      if (lane == kWave - 1) s_wsum[wave] = incl;
-      const bool odd = __ballot(hh < heads && c != a.max_sel_t) != 0;
-      if (lane == 0) s_odd[wave] = odd ? 1 : 0;
-      finish_pass(hh, c, incl, lst, carry);
-    }
-  }
-  int T = carry;
-  if (threadIdx.x == 0) s_start[heads] = T;
-  lds_barrier();
-  T = __builtin_amdgcn_readfirstlane(T);
-
-  // Every head walks max_sel pages (a matching total is not enough: one
-  // head's extra pages can make up for another's missing ones).
-  const bool spec_ok = uneven == 0 && T == T_spec && h_spec >= 0;
-  const Partition part = spec_ok ? spec_part : Partition(max(T, 1), a.sk_grid);
-  const int n_wg = T > 0 ? part.n : a.sk_grid;
-  if (w >= n_wg) return;  // uniform
-
-  // Heads without pages: (o, m, l) = (0, -inf, 0), zero output.
-  for (int hh = w; hh < heads; hh += n_wg) {
-    if (s_start[hh + 1] != s_start[hh]) continue;  // uniform
-    const int64_t row0 = (int64_t)hh * G;
-    for (int i = threadIdx.x; i < G * D; i += NT)
-      write_outputs<D>(a, row0 + i / D, i % D, 0.f, -INFINITY, 0.f);
-    if (threadIdx.x == 0 && a.work != nullptr) add_work(a, 0, a.ctx_lens[hh / a.H_kv]);
-  }
-  if (T == 0) return;
-
-  const int g0 = part.start(w);
-  const int g1 = part.start(w + 1);
-  // First head of the range: the last head that starts at or before g0 (it
-  // holds page g0, so it is not empty).
-  int lo = h_spec;
-  if (!spec_ok) {
-    lo = 0;
-    int hi = heads - 1;
-    while (lo < hi) {  // uniform binary search
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_start[mid] <= g0) lo = mid;
-      else hi = mid - 1;
-    }
-  }
-  const PartBuf pb(a.part, a.part_bytes);
-
-  for (int h = lo; h < heads; ++h) {
-    const int P = __builtin_amdgcn_readfirstlane(s_start[h]);
-    if (P >= g1) break;  // uniform
-    const int n = __builtin_amdgcn_readfirstlane(s_start[h + 1]) - P;
-    if (n == 0) continue;
-    const int s0 = max(g0, P) - P, s1 = min(g1, P + n) - P;
-    const int b = h / a.H_kv;
-    const int hk = h - b * a.H_kv;
-    const bool listed = s_listed[h] != 0;
-    const bool on_spec = h == h_spec;  // eng, ctx_spec already belong to this head
-    const int ctx = on_spec ? ctx_spec : __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
-    const int32_t *idx_row = a.page_idx + (int64_t)h * a.idx_stride;
-    const bool use_spec = spec_ok && on_spec && s0 == r_spec && listed;
-
-    if (!on_spec || h != lo) eng.init(a, b, hk, lane, s_eng[wave]);
-    cur_ctx = ctx;
-    const int npw = max(0, (s1 - s0 - wave + NW - 1) / NW);
-    for (int c0 = 0; c0 < npw; c0 += kWave) {
-      const int cn = min(kWave, npw - c0);
-      if (!(use_spec && c0 == 0)) {  // the speculated chunk is already in flight
-        lookup(s0, c0, cn, listed, idx_row, b, false);
-        prologue(cn);
-      }
-      steady(cn);
-    }
-    eng.template finish<NW>(wave, lane, s_o, s_m, s_l);
-    __syncthreads();
-
-    const int first = part.owner(P);
-    segment_epilogue<G, D, NW>(a, pb, h, n, ctx, part.owner(P + n - 1) - first + 1,
-                            (uint32_t)(w + h), (uint32_t)(first + h), s_o, s_m, s_l, s_last,
-                            s_tail.merge);
-    __syncthreads();  // LDS is reused by the next segment
-  }
-}
+CVSA_DECODE_EXTERN(1)
+CVSA_DECODE_EXTERN(2)
+CVSA_DECODE_EXTERN(3)
+CVSA_DECODE_EXTERN(4)
+CVSA_DECODE_EXTERN(5)
+CVSA_DECODE_EXTERN(6)
+CVSA_DECODE_EXTERN(7)
+CVSA_DECODE_EXTERN(8)
+CVSA_DECODE_EXTERN(9)
+CVSA_DECODE_EXTERN(10)
+CVSA_DECODE_EXTERN(11)
+CVSA_DECODE_EXTERN(12)
+CVSA_DECODE_EXTERN(13)
+CVSA_DECODE_EXTERN(14)
+CVSA_DECODE_EXTERN(15)
+CVSA_DECODE_EXTERN(16)
 
 __global__ void fill_zero_kernel(uint32_t *p, size_t n_words) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_words;
@@ -1098,11 +33,6 @@ __global__ void fill_zero_kernel(uint32_t *p, size_t n_words) {
     p[i] = 0u;
 }
 
-// Workgroups per launch, at most kMaxSplits (a head's partials are merged
-// in one workgroup's LDS): one per CU of the 256-CU part.
-constexpr int kTargetWorkgroups = 256;
-static_assert(kTargetWorkgroups <= kMaxSplits, "one merge per head fits the merge LDS");
-constexpr int kWavesPerWg = 4;
 
 // Launch plan.  Listed launches (every head walks its page list) use the
 // static split grid of listed_decode_kernel: ~target_workgroups()
@@ -1196,8 +126,8 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   CVSA_REQUIRE(H_kv > 0 && H_q > 0 && H_q % H_kv == 0, CVSA_ERR_INVALID,
                "%s: H_q=%d is not a multiple of H_kv=%d", name, H_q, H_kv);
   const int G = H_q / H_kv;
-  CVSA_REQUIRE(G >= 1 && G <= 8, CVSA_ERR_UNSUPPORTED,
-               "%s: GQA group size %d not in 1..8", name, G);
+  CVSA_REQUIRE(G >= 1 && G <= kMaxGroup, CVSA_ERR_UNSUPPORTED,
+               "%s: GQA group size %d not in 1..%d", name, G, kMaxGroup);
   const int ts = tile_shift(block_size);
   CVSA_REQUIRE(decode_head_dim(D) && ts >= 0, CVSA_ERR_UNSUPPORTED,
                "%s: D=%d, block_size=%d not supported (D in {64, 128, 256}, block_size in "
@@ -1250,7 +180,6 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   a.D = D;
   a.bs = block_size;
   a.ts = ts;
-  a.max_sel_t = listed ? a.max_sel << ts : 0;
   a.scale = (float)pow((double)D, -0.5);
   return CVSA_OK;
 }
@@ -1268,46 +197,20 @@ static int enqueue_decode(const char *name, DecodeArgs a, int G, bool listed,
                           const DecodeLaunch &p, void *workspace, size_t need, hipStream_t st) {
   bind_workspace(a, workspace, need);
   const dim3 grid(p.grid_x, p.grid_y), block(kWavesPerWg * kWave);
-  // Pages of K/V in flight per wave: 2, or 1 at D = 256, whose pages hold
-  // twice the registers.
-#define CVSA_DEC_LAUNCH(GG, DD)                                                              \
-  do {                                                                                       \
-    constexpr int PDD = DD > 128 ? 1 : 2;                                                    \
-    if (!p.streamk)                                                                          \
-      hipLaunchKernelGGL((listed_decode_kernel<GG, MfmaEngine<GG, DD>, kWavesPerWg, PDD>),   \
-                         grid, block, 0, st, a);                                             \
-    else if (listed)                                                                         \
-      hipLaunchKernelGGL(                                                                    \
-          (streamk_decode_kernel<GG, MfmaEngine<GG, DD>, kWavesPerWg, PDD, kModeVerified>),  \
-          grid, block, 0, st, a);                                                            \
-    else                                                                                     \
-      hipLaunchKernelGGL(                                                                    \
-          (streamk_decode_kernel<GG, MfmaEngine<GG, DD>, kWavesPerWg, PDD, kModeAll>), grid, \
-          block, 0, st, a);                                                                  \
-  } while (0)
-#define CVSA_DEC_CASE(GG)                                                                    \
-  case GG:                                                                                   \
-    if (a.D == 64)                                                                           \
-      CVSA_DEC_LAUNCH(GG, 64);                                                               \
-    else if (a.D == 256)                                                                     \
-      CVSA_DEC_LAUNCH(GG, 256);                                                              \
-    else                                                                                     \
-      CVSA_DEC_LAUNCH(GG, 128);                                                              \
-    break;
+  const int kind = !p.streamk ? kLaunchListed : listed ? kLaunchVerified : kLaunchAll;
   switch (G) {
-    CVSA_DEC_CASE(1)
-    CVSA_DEC_CASE(2)
-    CVSA_DEC_CASE(3)
-    CVSA_DEC_CASE(4)
-    CVSA_DEC_CASE(5)
-    CVSA_DEC_CASE(6)
-    CVSA_DEC_CASE(7)
-    CVSA_DEC_CASE(8)
+#define CVSA_DEC_CASE(GG)                           \
+  case GG:                                          \
+    launch_decode_g<GG>(a, kind, grid, block, st);  \
+    break;
+    CVSA_DEC_CASE(1) CVSA_DEC_CASE(2) CVSA_DEC_CASE(3) CVSA_DEC_CASE(4)
+    CVSA_DEC_CASE(5) CVSA_DEC_CASE(6) CVSA_DEC_CASE(7) CVSA_DEC_CASE(8)
+    CVSA_DEC_CASE(9) CVSA_DEC_CASE(10) CVSA_DEC_CASE(11) CVSA_DEC_CASE(12)
+    CVSA_DEC_CASE(13) CVSA_DEC_CASE(14) CVSA_DEC_CASE(15) CVSA_DEC_CASE(16)
+#undef CVSA_DEC_CASE
     default:
       break;
   }
-#undef CVSA_DEC_CASE
-#undef CVSA_DEC_LAUNCH
   return cvsa_host::check_launch(name);
 }
 
@@ -1410,14 +313,14 @@ extern "C" int cvsa_sparse_decode(const uint16_t *q, int64_t q_stride_b, int64_t
 // cvsa_sparse_decode_noalloc keeps the decode workspace in this file-scope
 // device array instead of a caller-owned buffer.  Each GPU the library runs
 // on holds its own copy until the process ends.  A listed launch needs at
-// most kCounterAreaBytes + kMaxSplits partials of G x (D + 4) fp32, G <= 8,
-// D <= 256 (2.1 MB: plan_launch splits heads only when there are fewer than
+// most kCounterAreaBytes + kMaxSplits partials of G x (D + 4) fp32, G <= 16,
+// D <= 256 (4.3 MB: plan_launch splits heads only when there are fewer than
 // kMaxSplits of them, into at most kMaxSplits / heads splits each), so every
 // call cvsa_sparse_decode accepts fits; a larger need is refused all the
 // same.
-constexpr size_t kScratchBytes = (size_t)9 << 18;  // 2.25 MiB
-static_assert(kScratchBytes >= kCounterAreaBytes + (size_t)kMaxSplits * 8 * part_stride(256) *
-                                                       sizeof(float),
+constexpr size_t kScratchBytes = (size_t)9 << 19;  // 4.5 MiB
+static_assert(kScratchBytes >= kCounterAreaBytes + (size_t)kMaxSplits * kMaxGroup *
+                                                       part_stride(256) * sizeof(float),
               "scratch holds every listed launch");
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
@@ -1547,25 +450,19 @@ int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_
   const int score_gx = (int)((waves + kWavesPerWg - 1) / kWavesPerWg);
   const int64_t grid = (int64_t)p.grid_x * p.grid_y + (int64_t)score_gx * B;
   hipStream_t st = (hipStream_t)stream;
-#define CVSA_SPEC_CASE(GG)                                                                   \
-  case GG:                                                                                   \
-    hipLaunchKernelGGL((score_spec_kernel<GG, MfmaEngine<GG, 128>, kWavesPerWg, 2>),        \
-                       dim3((unsigned)grid), dim3(kWavesPerWg * kWave), 0, st, a, sa,        \
-                       score_gx);                                                            \
-    break;
   switch (G) {
-    CVSA_SPEC_CASE(1)
-    CVSA_SPEC_CASE(2)
-    CVSA_SPEC_CASE(3)
-    CVSA_SPEC_CASE(4)
-    CVSA_SPEC_CASE(5)
-    CVSA_SPEC_CASE(6)
-    CVSA_SPEC_CASE(7)
-    CVSA_SPEC_CASE(8)
+#define CVSA_SPEC_CASE(GG)                                                \
+  case GG:                                                                \
+    launch_spec_g<GG>(a, sa, score_gx, dim3((unsigned)grid), st);          \
+    break;
+    CVSA_SPEC_CASE(1) CVSA_SPEC_CASE(2) CVSA_SPEC_CASE(3) CVSA_SPEC_CASE(4)
+    CVSA_SPEC_CASE(5) CVSA_SPEC_CASE(6) CVSA_SPEC_CASE(7) CVSA_SPEC_CASE(8)
+    CVSA_SPEC_CASE(9) CVSA_SPEC_CASE(10) CVSA_SPEC_CASE(11) CVSA_SPEC_CASE(12)
+    CVSA_SPEC_CASE(13) CVSA_SPEC_CASE(14) CVSA_SPEC_CASE(15) CVSA_SPEC_CASE(16)
+#undef CVSA_SPEC_CASE
     default:
       break;
   }
-#undef CVSA_SPEC_CASE
   return cvsa_host::check_launch(name);
 }
 

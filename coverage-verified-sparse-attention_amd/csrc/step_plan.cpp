@@ -45,7 +45,7 @@ int check_desc(const cvsa_step_desc &d) {
   STEP_REQUIRE(d.B > 0 && d.H_kv > 0 && d.H_q > 0 && d.H_q % d.H_kv == 0, CVSA_ERR_INVALID,
                "step_plan: bad head counts B=%d H_q=%d H_kv=%d", d.B, d.H_q, d.H_kv);
   const int G = d.H_q / d.H_kv;
-  STEP_REQUIRE(G <= 8, CVSA_ERR_UNSUPPORTED, "step_plan: GQA group size %d not in 1..8", G);
+  STEP_REQUIRE(G <= 16, CVSA_ERR_UNSUPPORTED, "step_plan: GQA group size %d not in 1..16", G);
   STEP_REQUIRE(d.H_kv == 1 || d.H_kv == 2 || d.H_kv == 4 || d.H_kv == 8 || d.H_kv == 16,
                CVSA_ERR_UNSUPPORTED, "step_plan: H_kv=%d not in {1,2,4,8,16}", d.H_kv);
   STEP_REQUIRE((int64_t)d.B * d.H_kv <= kMaxDecodeHeads, CVSA_ERR_UNSUPPORTED,

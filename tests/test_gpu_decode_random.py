@@ -1,7 +1,7 @@
 """Seeded random decode launches against fp32 torch attention.
 
 Each case draws a batch of ragged contexts (partial last pages, block tables
-wider than the context), G in 1..8, H_kv in {1, 2, 4, 8, 16}, a selection
+wider than the context), G in 1..8 (and 9..16), H_kv in {1, 2, 4, 8, 16}, a selection
 width (budget) and per-head selections of any length from 0 to the width
 (ascending pages, garbage past n_per_head), and an accept mask.  The listed
 decode (every head walks its selection), the verified decode (accepted heads
@@ -45,11 +45,11 @@ def _attention(q, K, V, bt, b, ctx, h, G, pages):
     return (p @ v) / l[:, None], m + torch.log(l)
 
 
-def _case(seed, dev, D=128, BS=16):
+def _case(seed, dev, D=128, BS=16, G_range=(1, 8)):
     g = torch.Generator().manual_seed(seed)
     rnd = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))  # noqa: E731
     H = [1, 2, 4, 8, 16][rnd(0, 4)]
-    G = rnd(1, 8)
+    G = rnd(*G_range)
     B = rnd(1, 4)
     uneven = seed < 4
     if uneven:   # one sequence, pages enough for every head's walk to coincide
@@ -83,8 +83,8 @@ def _case(seed, dev, D=128, BS=16):
     return inp, W, budget, idx.to(dev), nph.to(dev), accept.to(dev), H, G, B, ctx, n_valid
 
 
-def _check(gpu, seed, D, BS=16):
-    inp, W, budget, idx, nph, accept, H, G, B, ctx, n_valid = _case(seed, gpu, D, BS)
+def _check(gpu, seed, D, BS=16, G_range=(1, 8)):
+    inp, W, budget, idx, nph, accept, H, G, B, ctx, n_valid = _case(seed, gpu, D, BS, G_range)
     q, K, V, bt, cl = inp.q, inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens
     lo, lm, ll = ops.sparse_decode_unnorm(q, K, V, bt, idx, nph, cl, H, G, BS)
     ver, (vo, vm, vl) = ops.verified_decode(q, K, V, bt, cl, idx, nph, accept, H, G, BS,
@@ -124,3 +124,9 @@ def test_random_decode_launches_head_dims(gpu, seed, D):
 @pytest.mark.parametrize("seed", range(8))
 def test_random_decode_launches_block_sizes(gpu, seed, BS):
     _check(gpu, seed, [128, 64, 256][seed % 3], BS)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_decode_launches_wide_groups(gpu, seed):
+    """G = 9..16 query heads per KV head (one MFMA tile of 16 columns)."""
+    _check(gpu, seed, [128, 64, 256, 128][seed % 4], [16, 16, 16, 32][seed % 4], (9, 16))

@@ -1,12 +1,13 @@
-"""Head dimensions 64 and 256 and block sizes 32 and 64 through the entry
-points that take them, against the oracle: page scoring in both of its
-layouts (a wave load holds 64 / (D/8) key rows, so the head-group layout
-needs H_kv a multiple of 8, 4, 2 at D = 64, 128, 256 and smaller H_kv take
-the whole-page layout) and with several tiles per wave, Quest metadata and
-scores, and the backend's schedules in lockstep with the oracle backend.
-Decode launches and step plans at these geometries run with the random
-draws of test_gpu_decode_random.py and test_gpu_step_plan.py, the KV append
-in test_gpu_ops.py.
+"""Head dimensions 64 and 256, block sizes 32 and 64 and GQA groups of 9 to
+16 query heads through the entry points that take them, against the
+oracle: page scoring in both of its layouts (a wave load holds 64 / (D/8)
+key rows, so the head-group layout needs H_kv a multiple of 8, 4, 2 at
+D = 64, 128, 256 and smaller H_kv take the whole-page layout) and with
+several tiles per wave, Quest metadata and scores, and the backend's
+schedules in lockstep with the oracle backend.  Decode launches and step
+plans at these geometries run with the random draws of
+test_gpu_decode_random.py and test_gpu_step_plan.py, the KV append in
+test_gpu_ops.py.
 """
 import pytest
 import torch
@@ -102,3 +103,13 @@ def test_random_schedules_geometry(gpu, seed, D, bs):
     cfg["block_size"] = bs
     stats, trace, lock = _run(gpu, cfg, kw, steps=10, seed=700 + seed)
     print(f"seed {seed} D {D} bs {bs} {cfg} {kw}: {lock.summary()}")
+
+
+@pytest.mark.parametrize("G,H,bs", [(12, 8, 16), (16, 4, 16), (10, 2, 32), (16, 1, 64)])
+def test_random_schedules_wide_groups(gpu, G, H, bs):
+    """Backend schedules with 9..16 query heads per KV head."""
+    cfg, kw = _random_schedule(G + H)
+    cfg.update(num_q_heads=H * G, num_kv_heads=H, block_size=bs,
+               hot_heads=list(range(0, H, 2)))
+    stats, trace, lock = _run(gpu, cfg, kw, steps=10, seed=800 + G)
+    print(f"G {G} H {H} bs {bs} {cfg} {kw}: {lock.summary()}")

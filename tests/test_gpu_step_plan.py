@@ -371,11 +371,17 @@ def test_random_shapes_plan_block_sizes(gpu, seed, BS):
     _plan_equals_separate_kernels(gpu, seed, [128, 64, 128][seed], BS)
 
 
-def _plan_equals_separate_kernels(gpu, seed, D, BS=16):
+@pytest.mark.parametrize("seed", range(4))
+def test_random_shapes_plan_wide_groups(gpu, seed):
+    """The same with 9..16 query heads per KV head."""
+    _plan_equals_separate_kernels(gpu, seed, 128, [16, 32, 16, 64][seed], (9, 16))
+
+
+def _plan_equals_separate_kernels(gpu, seed, D, BS=16, G_range=(1, 8)):
     g = torch.Generator().manual_seed(100 + seed)
     rnd = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))  # noqa: E731
     H = [1, 2, 4, 8, 16][rnd(0, 4)]
-    G = rnd(1, 8)
+    G = rnd(*G_range)
     B = rnd(1, 3)
     ctx = [rnd(40, 6000) for _ in range(B)]
     inp = make_paged_inputs(B, H * G, H, D, ctx, block_size=BS, seed=seed, device=gpu,
