@@ -231,10 +231,10 @@ int cvsa_sparse_decode(const uint16_t *q, int64_t q_stride_b,
  * needs no caller-owned scratch.  No counterpart in the reference; it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  The split-K
- * counters and partials live in a static 2.25 MiB device array of the
+ * counters and partials live in a static 4.5 MiB device array of the
  * library (one per GPU, held until the process ends; every listed launch
- * needs at most 2.1 MB of it, 1.1 MB at D = 128; a larger need returns
- * CVSA_ERR_WORKSPACE).  Its first
+ * needs at most 4.3 MB of it, at G = 16 and D = 256, and 1.1 MB at G = 8,
+ * D = 128; a larger need returns CVSA_ERR_WORKSPACE).  Its first
  * call on a device looks the array up and zeroes its counters on `stream`.
  * All calls on one GPU share the array: calls that overlap in time on one
  * GPU (other streams, other threads) race and must be ordered by the
