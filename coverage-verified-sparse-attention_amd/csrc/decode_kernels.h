@@ -75,7 +75,6 @@ struct DecodeArgs {
   const uint8_t *accept;  // non-NULL: verified mode
   int H_kv, W;
   int D;      // head dimension (the launch's engine is compiled for it)
-  int bs;     // block size (tokens per page)
   int ts;     // tiles per page = 1 << ts
   int heads;  // B * H_kv
   int pps, n_splits;  // listed partition: tiles per split, splits per head
@@ -165,7 +164,7 @@ template <int MODE>
 __device__ __forceinline__ int head_pages(const DecodeArgs &a, int bh, bool &listed, int ts) {
   int n_all = 0, n_list = 0;
   if constexpr (MODE != kModeListed)
-    n_all = max(0, min(n_valid_pages(a.ctx_lens[bh / a.H_kv], a.bs), a.W)) << ts;
+    n_all = max(0, min(valid_pages_ts(a.ctx_lens[bh / a.H_kv], ts), a.W)) << ts;
   if constexpr (MODE != kModeAll) n_list = min(max(a.n_pages[bh], 0), a.max_sel) << ts;
   if constexpr (MODE == kModeAll) {
     listed = false;
@@ -802,11 +801,12 @@ void score_spec_kernel(const DecodeArgs a,
 // accepted and whose outputs a speculative listed decode already wrote:
 // what the listed walks would have added, summed by one workgroup.
 template <int NT>
-__device__ __forceinline__ void add_listed_work(const DecodeArgs &a, unsigned long long *red) {
+__device__ __forceinline__ void add_listed_work(const DecodeArgs &a, unsigned long long *red,
+                                                int ts) {
   unsigned long long n = 0, nv = 0;
   for (int bh = threadIdx.x; bh < a.heads; bh += NT) {
     n += (unsigned long long)min(max(a.n_pages[bh], 0), a.max_sel);
-    nv += (unsigned long long)max(0, n_valid_pages(a.ctx_lens[bh / a.H_kv], a.bs));
+    nv += (unsigned long long)max(0, valid_pages_ts(a.ctx_lens[bh / a.H_kv], ts));
   }
   if (threadIdx.x == 0) red[0] = red[1] = 0ull;
   __syncthreads();
@@ -882,7 +882,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     for (int i = threadIdx.x; i < heads; i += NT) rejected |= a.accept[i] == 0;
     if (__syncthreads_or(rejected) == 0) {  // uniform
       if (spec_done != 0) {
-        if (w == 0 && a.work != nullptr) add_listed_work<NT>(a, s_work);
+        if (w == 0 && a.work != nullptr) add_listed_work<NT>(a, s_work, Engine::tshift(a));
         return;
       }
       if (w < n_listed)

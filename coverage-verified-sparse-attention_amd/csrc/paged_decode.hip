@@ -178,7 +178,6 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   a.n_splits = p.n_splits;
   a.sk_grid = p.sk_grid;
   a.D = D;
-  a.bs = block_size;
   a.ts = ts;
   a.scale = (float)pow((double)D, -0.5);
   return CVSA_OK;
