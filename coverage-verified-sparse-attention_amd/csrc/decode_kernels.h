@@ -76,6 +76,10 @@ struct DecodeArgs {
   int H_kv, W;
   int D;      // head dimension (the launch's engine is compiled for it)
   int ts;     // tiles per page = 1 << ts
+  // Query heads: the launch serves heads q_off .. q_off + G - 1 (G the
+  // kernel's group, at most 16) of each KV head's group of q_group; a larger
+  // group runs as one launch per 16 of its heads.
+  int q_group, q_off;
   int heads;  // B * H_kv
   int pps, n_splits;  // listed partition: tiles per split, splits per head
   int sk_grid;        // stream-K partition: workgroups (<= kMaxSplits)
@@ -370,7 +374,8 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBu
         for (int jj = 1; jj < J; ++jj) O += s.acc[t + jj * NC];
       }
     }
-    if (live && j == 0) write_outputs4<D>(a, (int64_t)bh * G + g, d0, O, s.M[g], s.L[g]);
+    if (live && j == 0)
+      write_outputs4<D>(a, (int64_t)bh * a.q_group + a.q_off + g, d0, O, s.M[g], s.L[g]);
   }
   if (t == 0 && a.work != nullptr) add_work(a, n, nv);
 }
@@ -440,7 +445,8 @@ struct MfmaEngine {
     // Rows past the group repeat head G-1: MFMA output rows are independent
     // and those rows are never written out.  No select on the loaded value,
     // so nothing waits for q before the first page is consumed.
-    const uint16_t *qrow = a.q + b * a.q_sb + (int64_t)(h * G + min(c16, G - 1)) * a.q_sh;
+    const uint16_t *qrow =
+        a.q + b * a.q_sb + (int64_t)(h * a.q_group + a.q_off + min(c16, G - 1)) * a.q_sh;
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk)
       qb[kk] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(qrow + 32 * kk + 8 * grp));
@@ -595,8 +601,8 @@ __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const Part
       f32x4 O;
       float M, L;
       wg_state4(c, O, M, L);
-      write_outputs4<D>(a, (int64_t)h * G + c / kChunksPerRow, 4 * (c % kChunksPerRow), O, M,
-                        L);
+      write_outputs4<D>(a, (int64_t)h * a.q_group + a.q_off + c / kChunksPerRow,
+                        4 * (c % kChunksPerRow), O, M, L);
     }
     if (threadIdx.x == 0 && a.work != nullptr) add_work(a, n, nv);
     return;
@@ -1052,7 +1058,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   // Heads without pages: (o, m, l) = (0, -inf, 0), zero output.
   for (int hh = w; hh < heads; hh += n_wg) {
     if (s_start[hh + 1] != s_start[hh]) continue;  // uniform
-    const int64_t row0 = (int64_t)hh * G;
+    const int64_t row0 = (int64_t)hh * a.q_group + a.q_off;
     for (int i = threadIdx.x; i < G * D; i += NT)
       write_outputs<D>(a, row0 + i / D, i % D, 0.f, -INFINITY, 0.f);
     if (threadIdx.x == 0 && a.work != nullptr)
@@ -1177,6 +1183,7 @@ void launch_spec_g(const DecodeArgs &a, const ScoreArgs &s, int score_gx, dim3 g
 #define CVSA_DECODE_EXTERN(GG) CVSA_DECODE_LAUNCHERS(extern, GG)
 #define CVSA_DECODE_INSTANTIATE(GG) CVSA_DECODE_LAUNCHERS(, GG)
 
-constexpr int kMaxGroup = 16;  // query heads per KV head: one MFMA tile
+constexpr int kMaxGroup = 16;       // query heads of one launch: one MFMA tile
+constexpr int kMaxGroupTotal = 128;  // query heads per KV head (launches of 16)
 
 }  // namespace cvsa

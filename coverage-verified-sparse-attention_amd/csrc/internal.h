@@ -9,8 +9,8 @@
 namespace cvsa_internal {
 
 // Shapes for which score_and_speculate has a fused launch: H_kv 4, 8 or 16
-// at D = 128.
-bool score_spec_fusable(int32_t H_kv, int32_t D);
+// at D = 128, G = H_q / H_kv at most 16.
+bool score_spec_fusable(int32_t H_kv, int32_t D, int32_t G);
 
 int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
                         const uint16_t *k_cache, const uint16_t *v_cache, int64_t num_blocks,

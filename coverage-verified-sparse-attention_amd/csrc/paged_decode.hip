@@ -105,7 +105,9 @@ static_assert(kCounterAreaBytes % 256 == 0, "partial rows start 256-byte aligned
 
 static size_t workspace_bytes_for(int B, int H_q, int H_kv, int D, int max_sel, int W,
                                   bool listed, bool all_pages) {
-  const int G = H_q / H_kv;
+  // One launch serves at most kMaxGroup query heads per KV head; larger
+  // groups run as several launches over the same workspace.
+  const int G = min(H_q / H_kv, kMaxGroup);
   const DecodeLaunch p = plan_launch(B, H_kv, max_sel, W, listed, all_pages);
   if (p.partial_rows == 0) return 0;
   return kCounterAreaBytes + p.partial_rows * G * part_stride(D) * sizeof(float);
@@ -126,8 +128,8 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   CVSA_REQUIRE(H_kv > 0 && H_q > 0 && H_q % H_kv == 0, CVSA_ERR_INVALID,
                "%s: H_q=%d is not a multiple of H_kv=%d", name, H_q, H_kv);
   const int G = H_q / H_kv;
-  CVSA_REQUIRE(G >= 1 && G <= kMaxGroup, CVSA_ERR_UNSUPPORTED,
-               "%s: GQA group size %d not in 1..%d", name, G, kMaxGroup);
+  CVSA_REQUIRE(G >= 1 && G <= kMaxGroupTotal, CVSA_ERR_UNSUPPORTED,
+               "%s: GQA group size %d not in 1..%d", name, G, kMaxGroupTotal);
   const int ts = tile_shift(block_size);
   CVSA_REQUIRE(decode_head_dim(D) && ts >= 0, CVSA_ERR_UNSUPPORTED,
                "%s: D=%d, block_size=%d not supported (D in {64, 128, 256}, block_size in "
@@ -179,6 +181,8 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   a.sk_grid = p.sk_grid;
   a.D = D;
   a.ts = ts;
+  a.q_group = G;
+  a.q_off = 0;
   a.scale = (float)pow((double)D, -0.5);
   return CVSA_OK;
 }
@@ -197,20 +201,31 @@ static int enqueue_decode(const char *name, DecodeArgs a, int G, bool listed,
   bind_workspace(a, workspace, need);
   const dim3 grid(p.grid_x, p.grid_y), block(kWavesPerWg * kWave);
   const int kind = !p.streamk ? kLaunchListed : listed ? kLaunchVerified : kLaunchAll;
-  switch (G) {
-#define CVSA_DEC_CASE(GG)                           \
-  case GG:                                          \
-    launch_decode_g<GG>(a, kind, grid, block, st);  \
+  // Groups of more than kMaxGroup query heads: one launch per kMaxGroup of
+  // them, in order on the stream (each leaves the workspace counters at
+  // zero); the first books the effective-budget counters.
+  unsigned long long *work = a.work;
+  a.q_group = G;
+  for (int off = 0; off < G; off += kMaxGroup) {
+    a.q_off = off;
+    a.work = off == 0 ? work : nullptr;
+    switch (min(kMaxGroup, G - off)) {
+#define CVSA_DEC_CASE(GG)                             \
+  case GG:                                            \
+    launch_decode_g<GG>(a, kind, grid, block, st);    \
     break;
-    CVSA_DEC_CASE(1) CVSA_DEC_CASE(2) CVSA_DEC_CASE(3) CVSA_DEC_CASE(4)
-    CVSA_DEC_CASE(5) CVSA_DEC_CASE(6) CVSA_DEC_CASE(7) CVSA_DEC_CASE(8)
-    CVSA_DEC_CASE(9) CVSA_DEC_CASE(10) CVSA_DEC_CASE(11) CVSA_DEC_CASE(12)
-    CVSA_DEC_CASE(13) CVSA_DEC_CASE(14) CVSA_DEC_CASE(15) CVSA_DEC_CASE(16)
+      CVSA_DEC_CASE(1) CVSA_DEC_CASE(2) CVSA_DEC_CASE(3) CVSA_DEC_CASE(4)
+      CVSA_DEC_CASE(5) CVSA_DEC_CASE(6) CVSA_DEC_CASE(7) CVSA_DEC_CASE(8)
+      CVSA_DEC_CASE(9) CVSA_DEC_CASE(10) CVSA_DEC_CASE(11) CVSA_DEC_CASE(12)
+      CVSA_DEC_CASE(13) CVSA_DEC_CASE(14) CVSA_DEC_CASE(15) CVSA_DEC_CASE(16)
 #undef CVSA_DEC_CASE
-    default:
-      break;
+      default:
+        break;
+    }
+    const int rc = cvsa_host::check_launch(name);
+    if (rc != CVSA_OK) return rc;
   }
-  return cvsa_host::check_launch(name);
+  return CVSA_OK;
 }
 
 static int check_workspace(const char *name, void *workspace, size_t workspace_bytes,
@@ -402,8 +417,8 @@ extern "C" int cvsa_sparse_decode_noalloc(
 
 namespace cvsa_internal {
 
-bool score_spec_fusable(int32_t H_kv, int32_t D) {
-  return D == 128 && H_kv >= 4 && H_kv % 4 == 0 && H_kv <= 16;
+bool score_spec_fusable(int32_t H_kv, int32_t D, int32_t G) {
+  return D == 128 && H_kv >= 4 && H_kv % 4 == 0 && H_kv <= 16 && G >= 1 && G <= kMaxGroup;
 }
 
 // A lazy check's page scoring (cvsa_score_pages into page_scores) fused
@@ -431,8 +446,9 @@ int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_
   a.spec_state = spec_state;
   CVSA_REQUIRE(page_indices && spec_state && page_scores, CVSA_ERR_INVALID,
                "%s: page_indices, spec_state and page_scores are required", name);
-  CVSA_REQUIRE(score_spec_fusable(H_kv, D), CVSA_ERR_UNSUPPORTED,
-               "%s: H_kv=%d not in {4,8,16} or D=%d not 128", name, H_kv, D);
+  CVSA_REQUIRE(H_kv > 0 && H_q % H_kv == 0 && score_spec_fusable(H_kv, D, H_q / H_kv),
+               CVSA_ERR_UNSUPPORTED, "%s: H_kv=%d not in {4,8,16}, D=%d not 128 or G > %d",
+               name, H_kv, D, kMaxGroup);
   DecodeLaunch p{};
   size_t need = 0;
   int rc = validate_decode(name, a, B, H_q, H_kv, D, block_size, W, true, false, p, need);

@@ -45,7 +45,8 @@ int check_desc(const cvsa_step_desc &d) {
   STEP_REQUIRE(d.B > 0 && d.H_kv > 0 && d.H_q > 0 && d.H_q % d.H_kv == 0, CVSA_ERR_INVALID,
                "step_plan: bad head counts B=%d H_q=%d H_kv=%d", d.B, d.H_q, d.H_kv);
   const int G = d.H_q / d.H_kv;
-  STEP_REQUIRE(G <= 16, CVSA_ERR_UNSUPPORTED, "step_plan: GQA group size %d not in 1..16", G);
+  STEP_REQUIRE(G <= 128, CVSA_ERR_UNSUPPORTED, "step_plan: GQA group size %d not in 1..128",
+               G);
   STEP_REQUIRE(d.H_kv == 1 || d.H_kv == 2 || d.H_kv == 4 || d.H_kv == 8 || d.H_kv == 16,
                CVSA_ERR_UNSUPPORTED, "step_plan: H_kv=%d not in {1,2,4,8,16}", d.H_kv);
   STEP_REQUIRE((int64_t)d.B * d.H_kv <= kMaxDecodeHeads, CVSA_ERR_UNSUPPORTED,
@@ -158,7 +159,7 @@ namespace {
 // scores from the exact scan, and a fused scoring + decode launch for H_kv.
 bool speculates(const cvsa_step_desc &d) {
   return d.spec_state != nullptr && d.selector != CVSA_SELECT_QUEST_LN &&
-         cvsa_internal::score_spec_fusable(d.H_kv, d.D);
+         cvsa_internal::score_spec_fusable(d.H_kv, d.D, d.H_q / d.H_kv);
 }
 
 // The lazy check with the speculative decode: one launch scores the pages

@@ -3,7 +3,7 @@
 API of the reference's DenseAttentionBackend (cvsa/runtime/dense.py:16-111).
 The reference tries FlashInfer and falls back to its sparse kernel with all
 pages selected (:40-68); here the HIP paged-decode kernel walks every valid
-page directly (no index list), for every GQA ratio in 1..16.
+page directly (no index list), for every GQA ratio in 1..128.
 """
 from __future__ import annotations
 

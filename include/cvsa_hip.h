@@ -16,7 +16,8 @@
  *  - Return value: CVSA_OK (0), or a negative CVSA_ERR_* code with nothing
  *    enqueued.  cvsa_last_error() then returns a thread-local message.
  *  - Supported geometry: D in {64, 128, 256}, block_size in {16, 32, 64},
- *    G = H_q / H_kv in 1..16,
+ *    G = H_q / H_kv in 1..128 (decode launches serve 16 query heads per KV
+ *    head; larger groups are enqueued as one launch per 16),
  *    H_kv in {1, 2, 4, 8, 16} (page scoring), W <= 32768 pages, and
  *    B * H_kv <= 4096 for dense and verified decode.  Anything else returns
  *    CVSA_ERR_UNSUPPORTED.

@@ -1,7 +1,7 @@
 """Seeded random decode launches against fp32 torch attention.
 
 Each case draws a batch of ragged contexts (partial last pages, block tables
-wider than the context), G in 1..8 (and 9..16), H_kv in {1, 2, 4, 8, 16}, a selection
+wider than the context), G in 1..8 (and 9..48), H_kv in {1, 2, 4, 8, 16}, a selection
 width (budget) and per-head selections of any length from 0 to the width
 (ascending pages, garbage past n_per_head), and an accept mask.  The listed
 decode (every head walks its selection), the verified decode (accepted heads
@@ -130,3 +130,9 @@ def test_random_decode_launches_block_sizes(gpu, seed, BS):
 def test_random_decode_launches_wide_groups(gpu, seed):
     """G = 9..16 query heads per KV head (one MFMA tile of 16 columns)."""
     _check(gpu, seed, [128, 64, 256, 128][seed % 4], [16, 16, 16, 32][seed % 4], (9, 16))
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_decode_launches_large_groups(gpu, seed):
+    """G = 17..48 query heads per KV head: one launch per 16 of them."""
+    _check(gpu, 20 + seed, [128, 64, 256, 128][seed], [16, 16, 16, 32][seed], (17, 48))

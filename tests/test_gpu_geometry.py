@@ -1,5 +1,5 @@
 """Head dimensions 64 and 256, block sizes 32 and 64 and GQA groups of 9 to
-16 query heads through the entry points that take them, against the
+40 query heads through the entry points that take them, against the
 oracle: page scoring in both of its layouts (a wave load holds 64 / (D/8)
 key rows, so the head-group layout needs H_kv a multiple of 8, 4, 2 at
 D = 64, 128, 256 and smaller H_kv take the whole-page layout) and with
@@ -105,9 +105,11 @@ def test_random_schedules_geometry(gpu, seed, D, bs):
     print(f"seed {seed} D {D} bs {bs} {cfg} {kw}: {lock.summary()}")
 
 
-@pytest.mark.parametrize("G,H,bs", [(12, 8, 16), (16, 4, 16), (10, 2, 32), (16, 1, 64)])
+@pytest.mark.parametrize("G,H,bs", [(12, 8, 16), (16, 4, 16), (10, 2, 32), (16, 1, 64),
+                                    (32, 1, 16), (24, 4, 16), (40, 2, 32)])
 def test_random_schedules_wide_groups(gpu, G, H, bs):
-    """Backend schedules with 9..16 query heads per KV head."""
+    """Backend schedules with 9..40 query heads per KV head (above 16: one
+    decode launch per 16 of them)."""
     cfg, kw = _random_schedule(G + H)
     cfg.update(num_q_heads=H * G, num_kv_heads=H, block_size=bs,
                hot_heads=list(range(0, H, 2)))

@@ -377,6 +377,13 @@ def test_random_shapes_plan_wide_groups(gpu, seed):
     _plan_equals_separate_kernels(gpu, seed, 128, [16, 32, 16, 64][seed], (9, 16))
 
 
+@pytest.mark.parametrize("seed", range(3))
+def test_random_shapes_plan_large_groups(gpu, seed):
+    """The same with 17..40 query heads per KV head (no speculation: the
+    decode runs as one launch per 16 query heads)."""
+    _plan_equals_separate_kernels(gpu, 10 + seed, 128, [16, 32, 16][seed], (17, 40))
+
+
 def _plan_equals_separate_kernels(gpu, seed, D, BS=16, G_range=(1, 8)):
     g = torch.Generator().manual_seed(100 + seed)
     rnd = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))  # noqa: E731
