@@ -288,15 +288,23 @@ struct MergeLds {
   f32x4 acc[NT];
 };
 
+// o chunks of one merging thread requested together (KB of merge_partials):
+// 16 in the listed decode, whose merge ends the kernel, so a cfg3-sized head
+// (32 splits) is read in one memory round trip; 8 in the stream-K kernel,
+// whose merge sits inside its segment loop, where 16 would cost it an
+// occupancy step.
+constexpr int kMergeBatchListed = 16;
+constexpr int kMergeBatchStreamK = 8;
+
 // Merge of a head's n_act split partials by the last of its workgroups.
 // Thread t owns float4 chunk c = t % NC of the head's G x D outputs and the
-// splits j, j + J, ... (j = t / NC); their o chunks are loaded in batches of
-// KB, the next batch in flight while the current one is summed.  When the
+// splits j, j + J, ... (j = t / NC); their o chunks are loaded KB at a time,
+// the first KB together with the (m, l) pairs.  When the
 // outputs hold more chunks than the workgroup has threads (G x D > 4 NT) each
 // thread takes chunks t, t + NT, ... in turn, every split of each.  The
 // (m, l) pairs go to LDS first; one wave per q-head turns them into the
 // weights exp(m_sp - M) and the totals (M, L).
-template <int G, int D, int NT>
+template <int G, int D, int NT, int KB>
 __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBuf &pb,
                                                uint32_t head_off, int n_act, int bh, int n,
                                                int nv, MergeLds<G, NT> &s) {
@@ -306,7 +314,6 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBu
   constexpr int J = NT / NC > 0 ? NT / NC : 1;
   constexpr int NPASS = (NC + NT - 1) / NT;
   constexpr int NW = NT / kWave;
-  constexpr int KB = 8;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
@@ -354,17 +361,19 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBu
     const int d0 = 4 * (c % kChunksPerRow);
     if (pass > 0) load_batch(g, d0, 0, cur);
     f32x4 O = {0.f, 0.f, 0.f, 0.f};
-    for (int b0 = 0; b0 < per_lane; b0 += KB) {
-      f32x4 nxt[KB];
-      load_batch(g, d0, b0 + KB, nxt);
+    // A thread's first KB splits were requested with the (m, l) pairs, so a
+    // head of up to KB * J splits costs one memory round trip; more splits
+    // are read KB at a time.
+    for (int b0 = 0;;) {
 #pragma unroll
       for (int k = 0; k < KB; ++k) {
         const int sp = min(j + (b0 + k) * J, n_act - 1);
         const float w = b0 + k < per_lane ? s.ml[sp * G + g].x : 0.f;
         O += w * cur[k];
       }
-#pragma unroll
-      for (int k = 0; k < KB; ++k) cur[k] = nxt[k];
+      b0 += KB;
+      if (b0 >= per_lane) break;
+      load_batch(g, d0, b0, cur);
     }
     if constexpr (J > 1) {
       s.acc[t] = O;
@@ -564,7 +573,7 @@ __device__ __forceinline__ L &s_eng_of(L (&eng)[NW], int wave) { return eng[wave
 // contributor (n_act == 1) it writes the outputs.  Otherwise it stores its
 // partial (o, m, l) in partial row my_row, bumps the head's counter, and the
 // last of the n_act contributors merges rows first_row .. first_row+n_act-1.
-template <int G, int D, int NW>
+template <int G, int D, int NW, int KB>
 __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const PartBuf &pb, int h,
                                                  int n, int nv, int n_act, uint32_t my_row,
                                                  uint32_t first_row,
@@ -629,7 +638,7 @@ __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const Part
     // Last contributor of the head: merge its partials, write the outputs.
     if (threadIdx.x == 0)
       __hip_atomic_store(&a.counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_partials<G, D, NT>(a, pb, first_row * (uint32_t)(G * kPartStride), n_act, h, n,
+    merge_partials<G, D, NT, KB>(a, pb, first_row * (uint32_t)(G * kPartStride), n_act, h, n,
                              nv, s_merge);
   }
 }
@@ -742,9 +751,9 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
   eng.template finish<NW>(wave, lane, L.o, L.m, L.l);
   __syncthreads();
   const PartBuf pb(a.part, a.part_bytes);
-  segment_epilogue<G, Engine::kD, NW>(a, pb, bh, n >> ts, valid_pages_ts(ctx, ts), n_act,
-                                      (uint32_t)(bh * a.n_splits + split),
-                          (uint32_t)(bh * a.n_splits), L.o, L.m, L.l, L.last, L.tail.merge);
+  segment_epilogue<G, Engine::kD, NW, kMergeBatchListed>(
+      a, pb, bh, n >> ts, valid_pages_ts(ctx, ts), n_act, (uint32_t)(bh * a.n_splits + split),
+      (uint32_t)(bh * a.n_splits), L.o, L.m, L.l, L.last, L.tail.merge);
 }
 
 // The listed decode: a static grid of (split, head) workgroups.
@@ -1111,7 +1120,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     __syncthreads();
 
     const int first = part.owner(P);
-    segment_epilogue<G, D, NW>(a, pb, h, n >> ts, valid_pages_ts(ctx, ts),
+    segment_epilogue<G, D, NW, kMergeBatchStreamK>(a, pb, h, n >> ts, valid_pages_ts(ctx, ts),
                                part.owner(P + n - 1) - first + 1, (uint32_t)(w + h),
                                (uint32_t)(first + h), s_o, s_m, s_l, s_last, s_tail.merge);
     __syncthreads();  // LDS is reused by the next segment
