@@ -2,7 +2,8 @@
 
 Brute force on tiny inputs, closed forms (all pages selected = textbook
 softmax attention), invariants (draft + complement = dense, coverage = 1 for
-a full selection) and the rounding rule of the bf16 group mean.  A few tests
+a full selection) and the rounding rule of the bf16 group mean, at head
+dimensions 64, 128, 256 and block sizes 16, 32, 64 where they depend on them.  A few tests
 plant a plausible mistake in a copy of the oracle and show the checks fail.
 """
 import math
@@ -14,8 +15,14 @@ from oracle import cvsa_oracle as ref
 from cvsa.synthetic import make_paged_inputs
 
 
-def _tiny(seed=0, B=2, H_q=8, H_kv=2, ctx=(70, 33), W=6):
-    return make_paged_inputs(B, H_q, H_kv, 128, list(ctx), seed=seed, max_pages=W,
+# (head dimension, block size): the kernels' geometries.  Contexts scale with
+# the block size so that every geometry has full, partial and missing pages.
+GEOMETRIES = [(128, 16), (64, 32), (256, 64)]
+
+
+def _tiny(seed=0, B=2, H_q=8, H_kv=2, ctx=(70, 33), W=6, D=128, bs=16):
+    ctx = [c * bs // 16 for c in ctx]
+    return make_paged_inputs(B, H_q, H_kv, D, ctx, block_size=bs, seed=seed, max_pages=W,
                              hot_heads=[0], n_hot=1, hot_shift=2.0)
 
 
@@ -46,8 +53,9 @@ def _brute_scores(inp):
     return out
 
 
-def test_score_pages_brute_force():
-    inp = _tiny()
+@pytest.mark.parametrize("D,bs", GEOMETRIES)
+def test_score_pages_brute_force(D, bs):
+    inp = _tiny(D=D, bs=bs)
     got = ref.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens,
                           inp.num_kv_heads, inp.num_q_per_kv, inp.block_size)
     want = _brute_scores(inp)
@@ -81,24 +89,25 @@ def test_prepare_reuse_state_pads_to_a_power_of_two_with_page_zero():
                 assert int(n[b * 3 + h]) == int(nph[b, h])
 
 
-def test_reuse_decode_of_padded_state_equals_unpadded_decode():
+@pytest.mark.parametrize("D,bs", GEOMETRIES)
+def test_reuse_decode_of_padded_state_equals_unpadded_decode(D, bs):
     """The padding is never read: decoding a prepared state gives exactly the
     decode of the unpadded selection, on rows with n_per_head below the
     width, an empty row and a full row."""
-    inp = _tiny(seed=12, ctx=(90, 60), W=6)
+    inp = _tiny(seed=12, ctx=(90, 60), W=6, D=D, bs=bs)
     idx = torch.tensor([[[5, 0, 2], [1, 3, 4]], [[2, 1, 0], [3, 0, 1]]], dtype=torch.int32)
     nph = torch.tensor([[1, 3], [0, 2]], dtype=torch.int32)
     want = ref.sparse_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_tables, idx, nph,
-                             inp.context_lens, 2, 4, 16)
+                             inp.context_lens, 2, 4, bs)
     pi, n, padded = ref.prepare_reuse_state(idx, nph, 2, 2)
     assert padded == 4
     got = ref.sparse_decode_reuse(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
-                                  inp.context_lens, pi, n, padded, 2, 4, 16)
+                                  inp.context_lens, pi, n, padded, 2, 4, bs)
     assert torch.equal(got, want)
     # a padded page would change the result if it were read
     n_all = torch.full((4,), 4, dtype=torch.int32)
     other = ref.sparse_decode_reuse(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
-                                    inp.context_lens, pi, n_all, padded, 2, 4, 16)
+                                    inp.context_lens, pi, n_all, padded, 2, 4, bs)
     assert not torch.equal(other, want)
 
 
@@ -125,6 +134,9 @@ def test_select_topk_brute_force_with_ties_and_invalid_pages():
 def test_n_valid_pages_formula():
     ctx = torch.tensor([0, 1, 15, 16, 17, 32, 131072])
     assert ref.n_valid_pages(ctx, 16).tolist() == [1, 1, 1, 1, 2, 2, 8192]
+    assert ref.n_valid_pages(ctx, 32).tolist() == [1, 1, 1, 1, 1, 1, 4096]
+    ctx = torch.tensor([0, 1, 63, 64, 65, 131072])
+    assert ref.n_valid_pages(ctx, 64).tolist() == [1, 1, 1, 1, 2, 2048]
 
 
 def test_coverage_special_cases():
@@ -143,8 +155,9 @@ def test_coverage_special_cases():
     assert float(covz.max()) == 0.0
 
 
-def test_decode_all_pages_equals_textbook_softmax():
-    inp = _tiny(seed=11)
+@pytest.mark.parametrize("D,bs", GEOMETRIES)
+def test_decode_all_pages_equals_textbook_softmax(D, bs):
+    inp = _tiny(seed=11, D=D, bs=bs)
     out, (o, m, l) = ref.dense_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
                                       inp.context_lens, inp.num_kv_heads, inp.num_q_per_kv,
                                       inp.block_size, return_state=True)
@@ -152,7 +165,7 @@ def test_decode_all_pages_equals_textbook_softmax():
     G = inp.num_q_per_kv
     for b in range(B):
         c = int(inp.context_lens[b])
-        pages = -(-c // 16)
+        pages = -(-c // bs)
         phys = inp.block_tables[b, :pages].long()
         for j in range(H_q):
             h = j // G
@@ -165,25 +178,26 @@ def test_decode_all_pages_equals_textbook_softmax():
             assert abs(float(m[b, j]) - float(s.max())) < 1e-5
 
 
-def test_draft_plus_complement_equals_dense():
-    inp = _tiny(seed=13)
+@pytest.mark.parametrize("D,bs", GEOMETRIES)
+def test_draft_plus_complement_equals_dense(D, bs):
+    inp = _tiny(seed=13, D=D, bs=bs)
     ps = ref.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens,
                          inp.num_kv_heads, inp.num_q_per_kv, inp.block_size)
-    idx, nph = ref.select_topk(ps, 2, inp.context_lens, 16)
+    idx, nph = ref.select_topk(ps, 2, inp.context_lens, bs)
     rejected = torch.zeros(idx.shape[0], idx.shape[1], dtype=torch.bool)
     got = ref.verified_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
                               inp.context_lens, idx, nph, rejected, inp.num_kv_heads,
-                              inp.num_q_per_kv, 16, acc_dtype=torch.float64)
+                              inp.num_q_per_kv, bs, acc_dtype=torch.float64)
     dense = ref.dense_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
-                             inp.context_lens, inp.num_kv_heads, inp.num_q_per_kv, 16)
+                             inp.context_lens, inp.num_kv_heads, inp.num_q_per_kv, bs)
     assert (got.float() - dense.float()).abs().max().item() <= 1e-2  # bf16 outputs
     # accepted heads return the normalised draft
     accepted = torch.ones_like(rejected)
     got_a = ref.verified_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
                                 inp.context_lens, idx, nph, accepted, inp.num_kv_heads,
-                                inp.num_q_per_kv, 16)
+                                inp.num_q_per_kv, bs)
     draft = ref.sparse_decode(inp.q, inp.k_cache, inp.v_cache, inp.block_tables, idx, nph,
-                              inp.context_lens, inp.num_kv_heads, inp.num_q_per_kv, 16)
+                              inp.context_lens, inp.num_kv_heads, inp.num_q_per_kv, bs)
     assert torch.equal(got_a, draft)
 
 
@@ -197,20 +211,21 @@ def test_empty_selection_contract():
     assert bool(torch.isinf(m).all()) and bool((m < 0).all())
 
 
-def test_append_token_allocation_rule():
+@pytest.mark.parametrize("bs", [16, 32, 64])
+def test_append_token_allocation_rule(bs):
     """kv_cache.py:133-150: a block is taken only at offset 0 of a new page."""
-    K = torch.zeros(8, 16, 1, 4)
-    V = torch.zeros(8, 16, 1, 4)
+    K = torch.zeros(8, bs, 1, 4)
+    V = torch.zeros(8, bs, 1, 4)
     bt = torch.zeros(1, 4, dtype=torch.int32)
-    ctx = torch.tensor([15], dtype=torch.int32)
+    ctx = torch.tensor([bs - 1], dtype=torch.int32)
     alloc = torch.tensor([1], dtype=torch.int32)
     nf = 5
     for i in range(3):
         nf = ref.append_token_kv(K, V, bt, ctx, alloc, nf, 0, torch.full((1, 4), float(i + 1)),
-                                 torch.full((1, 4), -float(i + 1)), 16)
-    assert ctx.tolist() == [18] and alloc.tolist() == [2] and nf == 6
+                                 torch.full((1, 4), -float(i + 1)), bs)
+    assert ctx.tolist() == [bs + 2] and alloc.tolist() == [2] and nf == 6
     assert bt[0, 1].item() == 5
-    assert K[int(bt[0, 0]), 15, 0, 0].item() == 1.0
+    assert K[int(bt[0, 0]), bs - 1, 0, 0].item() == 1.0
     assert K[5, 0, 0, 0].item() == 2.0 and K[5, 1, 0, 0].item() == 3.0
 
 

@@ -13,21 +13,21 @@ import torch
 from oracle import cvsa_oracle as ref
 
 
-def _inputs(seed, B=2, H=2, G=2, W=6, ctx=(85, 50), nb=20):
+def _inputs(seed, B=2, H=2, G=2, W=6, ctx=(85, 50), nb=20, D=128, bs=16):
     g = torch.Generator().manual_seed(seed)
-    D = 128
     q = torch.randn(B, H * G, D, generator=g).to(torch.bfloat16)
-    k = torch.randn(nb, 16, H, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(nb, bs, H, D, generator=g).to(torch.bfloat16)
     bt = torch.randperm(nb, generator=g)[: B * W].view(B, W).to(torch.int32)
     cl = torch.tensor(ctx, dtype=torch.int32)
     return q, k, bt, cl, H, G
 
 
-def test_quest_bounds_the_exact_page_score():
+@pytest.mark.parametrize("D,bs", [(128, 16), (64, 32), (256, 64)])
+def test_quest_bounds_the_exact_page_score(D, bs):
     for seed in range(4):
-        q, k, bt, cl, H, G = _inputs(seed)
-        quest = ref.quest_page_scores(q, k, bt, cl, H, G, 16)
-        exact = ref.score_pages(q, k, bt, cl, H, G, 16)
+        q, k, bt, cl, H, G = _inputs(seed, ctx=(85 * bs // 16, 50 * bs // 16), D=D, bs=bs)
+        quest = ref.quest_page_scores(q, k, bt, cl, H, G, bs)
+        exact = ref.score_pages(q, k, bt, cl, H, G, bs)
         fin = torch.isfinite(exact)
         assert torch.equal(fin, torch.isfinite(quest))
         assert bool((quest[fin] >= exact[fin] - 1e-5).all())
@@ -43,19 +43,21 @@ def test_quest_equals_exact_on_one_token_pages():
         assert torch.allclose(quest[b, :, p], exact[b, :, p], rtol=0, atol=1e-5)
 
 
-def test_quest_brute_force():
-    q, k, bt, cl, H, G = _inputs(3, B=1, W=3, ctx=(40,))
-    got = ref.quest_page_scores(q, k, bt, cl, H, G, 16)
+@pytest.mark.parametrize("D,bs", [(128, 16), (64, 32), (256, 64)])
+def test_quest_brute_force(D, bs):
+    c = 40 * bs // 16
+    q, k, bt, cl, H, G = _inputs(3, B=1, W=3, ctx=(c,), D=D, bs=bs)
+    got = ref.quest_page_scores(q, k, bt, cl, H, G, bs)
     qf = q.float()
-    scale = 128 ** -0.5
+    scale = D ** -0.5
     for h in range(H):
         qr = [float(torch.tensor(sum(float(qf[0, h * G + j, d]) for j in range(G)) / G)
-                    .to(torch.bfloat16)) for d in range(128)]
+                    .to(torch.bfloat16)) for d in range(D)]
         for p in range(3):
-            n = min(16, 40 - 16 * p)
+            n = min(bs, c - bs * p)
             rows = k[int(bt[0, p]), :n, h].float()
             total = 0.0
-            for d in range(128):
+            for d in range(D):
                 lo = min(float(rows[t, d]) for t in range(n))
                 hi = max(float(rows[t, d]) for t in range(n))
                 total += max(qr[d] * lo, qr[d] * hi)
