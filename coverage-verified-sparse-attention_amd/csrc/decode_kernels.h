@@ -814,12 +814,26 @@ void score_spec_kernel(const DecodeArgs a,
 
 // Effective-budget counters of a verified launch whose heads were all
 // accepted and whose outputs a speculative listed decode already wrote:
-// what the listed walks would have added, summed by one workgroup.
+// what the listed walks would have added, summed by one workgroup.  A
+// thread's first head (bh = threadIdx.x) comes in as n0 / nv0, requested
+// with the launch's first loads (listed_work_first).
+template <int NT>
+__device__ __forceinline__ void listed_work_first(const DecodeArgs &a, int ts,
+                                                  unsigned long long &n0,
+                                                  unsigned long long &nv0) {
+  const int bh = min((int)threadIdx.x, a.heads - 1);
+  const int np = a.n_pages[bh];
+  const int ctx = a.ctx_lens[bh / a.H_kv];
+  const bool live = (int)threadIdx.x < a.heads;
+  n0 = live ? (unsigned long long)min(max(np, 0), a.max_sel) : 0ull;
+  nv0 = live ? (unsigned long long)max(0, valid_pages_ts(ctx, ts)) : 0ull;
+}
+
 template <int NT>
 __device__ __forceinline__ void add_listed_work(const DecodeArgs &a, unsigned long long *red,
-                                                int ts) {
-  unsigned long long n = 0, nv = 0;
-  for (int bh = threadIdx.x; bh < a.heads; bh += NT) {
+                                                int ts, unsigned long long n,
+                                                unsigned long long nv) {
+  for (int bh = threadIdx.x + NT; bh < a.heads; bh += NT) {
     n += (unsigned long long)min(max(a.n_pages[bh], 0), a.max_sel);
     nv += (unsigned long long)max(0, valid_pages_ts(a.ctx_lens[bh / a.H_kv], ts));
   }
@@ -893,11 +907,18 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     int spec_done = 0;
     if (a.spec_state != nullptr)
       spec_done = __builtin_amdgcn_readfirstlane(a.spec_state[0] & a.spec_state[1]);
+    // The counters of a kept speculation are booked by workgroup 0, whose
+    // threads request their first head's page count and context length
+    // here, in the same round trip as the flags.
+    unsigned long long n0 = 0, nv0 = 0;
+    if (a.spec_state != nullptr && w == 0 && a.work != nullptr)
+      listed_work_first<NT>(a, Engine::tshift(a), n0, nv0);
     int rejected = 0;
     for (int i = threadIdx.x; i < heads; i += NT) rejected |= a.accept[i] == 0;
     if (__syncthreads_or(rejected) == 0) {  // uniform
       if (spec_done != 0) {
-        if (w == 0 && a.work != nullptr) add_listed_work<NT>(a, s_work, Engine::tshift(a));
+        if (w == 0 && a.work != nullptr)
+          add_listed_work<NT>(a, s_work, Engine::tshift(a), n0, nv0);
         return;
       }
       if (w < n_listed)
