@@ -97,6 +97,28 @@ struct DecodeArgs {
   int32_t *spec_state;
 };
 
+// A reuse step's token append folded into its listed decode
+// (cvsa_sparse_decode_append): sequence b's new K/V rows go to token
+// slot[b].x % 16 of logical page slot[b].x / 16 (16-token pages), into block
+// slot[b].y when that page is allocated by this append, else the block its
+// table entry names; the context length becomes slot[b].x + 1.  The
+// workgroups that attend that page take the new token's rows from k_new /
+// v_new, so no workgroup reads the cache slot being written.
+constexpr int kMaxAppendSeqs = 256;
+struct AppendArgs {
+  const uint16_t *k_new, *v_new;  // [B, H_kv, D] rows, new_sb elements apart
+  int64_t new_sb;
+  int32_t *block_tables, *ctx_lens, *pages_allocated;  // updated by the append
+  int2 slot[kMaxAppendSeqs];  // (context length before the append, new block or -1)
+};
+
+// The new token of a walk's sequence: its logical page and row, its block
+// when the append allocates it (else -1), and its K/V rows for this KV head.
+struct NewToken {
+  int page = -1, off = 0, new_blk = -1;
+  const uint16_t *k = nullptr, *v = nullptr;
+};
+
 __device__ __forceinline__ void store_out(void *out, int dtype, int64_t i, float y) {
   if (dtype == CVSA_DTYPE_BF16) {
     reinterpret_cast<uint16_t *>(out)[i] = (uint16_t)f32_to_bf16_bits(y);
@@ -478,6 +500,25 @@ struct MfmaEngine {
       pg.v[i] = stream_load16(vp + voff + RPL * i * row_stride);
   }
 
+  // fetch() for a walk whose sequence appends a token in this launch: the
+  // lanes of row `newrow` of the page (-1: none) read the new token's K/V
+  // (k_row / v_row, this KV head's D elements) instead of the cache.
+  __device__ __forceinline__ void fetch_new(const uint16_t *kp, const uint16_t *vp, Page &pg,
+                                            int newrow, const uint16_t *k_row,
+                                            const uint16_t *v_row) const {
+    const int grp = lane >> 4;
+    const uint16_t *kb = (lane & 15) == newrow ? k_row + 8 * grp : kp + koff;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk)
+      pg.k[kk] = *reinterpret_cast<const uint4 *>(kb + 32 * kk);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int t = RPL * i + lane / LPR;
+      pg.v[i] = stream_load16(t == newrow ? v_row + 8 * (lane % LPR)
+                                          : vp + voff + RPL * i * row_stride);
+    }
+  }
+
   __device__ __forceinline__ void consume(Page &pg, int ntok, Lds &lds) {
     const int c16 = lane & 15, grp = lane >> 4;
     const int t0 = 4 * grp;
@@ -689,15 +730,21 @@ __device__ __forceinline__ void listed_first_pages(const DecodeArgs &a, int spli
 // pages [s * pps, (s + 1) * pps) of bh; splits past a head's pages only take
 // part when the head is empty (split 0 writes its outputs).  Partial row of
 // (split, head) = head * n_splits + split.
-template <int G, class Engine, int NW, int PD>
+// With APP, the walk's sequence appends token nt in this launch: the
+// context length is nt's page * 16 + row + 1 (16-token pages), and nt's page
+// reads that row from nt's rows (Engine::fetch_new) and, when the append
+// allocates the page, its block from nt.
+template <int G, class Engine, int NW, int PD, bool APP = false>
 __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int bh, int spec_lp,
-                                            int spec_phys, WalkLds<G, Engine, NW> &L) {
+                                            int spec_phys, WalkLds<G, Engine, NW> &L,
+                                            const NewToken &nt = NewToken()) {
   using Page = typename Engine::Page;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = bh / a.H_kv;
   const int h = bh - b * a.H_kv;
-  const int ctx = __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
+  const int ctx = APP ? nt.page * kPageTokens + nt.off + 1
+                      : __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
   const int pps = a.pps;
   const int r0 = split * pps;
   const int32_t *idx_row = a.page_idx + (int64_t)bh * a.idx_stride;
@@ -713,15 +760,17 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
   const int npw = max(0, (r1 - r0 - wave + NW - 1) / NW);
   for (int c0 = 0; c0 < npw; c0 += kWave) {
     const int cn = min(kWave, npw - c0);
-    int my_phys = 0, my_ntok = 0;
+    int my_phys = 0, my_ntok = 0, my_new = -1;
     if (lane < cn) {
       const int lt =
           c0 == 0 ? spec_lp : listed_tile(a, idx_row, r0 + wave + NW * (c0 + lane), ts);
       if (lt >= 0 && lt < (a.W << ts)) {
-        const int pt = c0 == 0 ? spec_phys : tile_block(a, b, lt, ts);
+        int pt = c0 == 0 ? spec_phys : tile_block(a, b, lt, ts);
+        if (APP && lt == nt.page && nt.new_blk >= 0) pt = nt.new_blk;
         if (pt >= 0 && pt < (a.num_blocks << ts)) {
           my_phys = pt;
           my_ntok = max(0, min(kPageTokens, ctx - lt * kPageTokens));
+          if (APP && lt == nt.page) my_new = nt.off;
         }
       }
     }
@@ -731,7 +780,11 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
     // the wave's last page (already cached) and are never consumed.
     auto fetch = [&](int j, Page &pg) {
       const int64_t base = (int64_t)__builtin_amdgcn_readlane(my_phys, j) * page_elems;
-      eng.fetch(a.k_cache + base, a.v_cache + base, pg);
+      if constexpr (APP)
+        eng.fetch_new(a.k_cache + base, a.v_cache + base, pg,
+                      __builtin_amdgcn_readlane(my_new, j), nt.k, nt.v);
+      else
+        eng.fetch(a.k_cache + base, a.v_cache + base, pg);
       return __builtin_amdgcn_readlane(my_ntok, j);
     };
     Page pbuf[PD];
@@ -765,6 +818,62 @@ __global__ __launch_bounds__(NW * kWave) void listed_decode_kernel(const DecodeA
   int lp, phys;
   listed_first_pages<NW>(a, blockIdx.x, blockIdx.y, wave, lane, Engine::tshift(a), lp, phys);
   listed_walk<G, Engine, NW, PD>(a, blockIdx.x, blockIdx.y, lp, phys, L);
+}
+
+// The listed decode of a reuse step with the step's token append folded in
+// (16-token pages, D = 128): workgroup (split, bh) walks as
+// listed_decode_kernel with its sequence's new token taken from k_new / v_new
+// (NewToken), and split 0 of each head writes that head's new K/V rows to
+// the cache slot, which no workgroup of the launch reads; split 0 of a
+// sequence's first head also moves its context length, page-table entry
+// and allocation count as cvsa_append_kv does.  Later launches see the
+// appended cache.
+template <int G, class Engine, int NW, int PD>
+__global__ __launch_bounds__(NW * kWave) void listed_append_kernel(const DecodeArgs a,
+                                                                   const AppendArgs app) {
+  static_assert(Engine::kD == 128, "the fused append is built for D = 128");
+  __shared__ WalkLds<G, Engine, NW> L;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int split = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / a.H_kv;
+  const int h = bh - b * a.H_kv;
+  const int2 sl = app.slot[b];  // workgroup-uniform
+  NewToken nt;
+  nt.page = sl.x >> 4;
+  nt.off = sl.x & 15;
+  nt.new_blk = sl.y;
+  const int64_t row = (int64_t)b * app.new_sb + (int64_t)h * Engine::kD;
+  nt.k = app.k_new + row;
+  nt.v = app.v_new + row;
+  int lp, phys;
+  listed_first_pages<NW>(a, split, bh, wave, lane, 0, lp, phys);
+  if (lp == nt.page && nt.new_blk >= 0) phys = nt.new_blk;
+  // Split 0's wave 0 appends: lanes 0-15 copy the head's K row, lanes 16-31
+  // its V row, 16 bytes each.  Their loads are requested with the walk's
+  // first ones and the stores wait until the walk is done.
+  const bool writer = split == 0 && wave == 0;  // uniform
+  int blk = -1;
+  uint4 x = make_uint4(0u, 0u, 0u, 0u);
+  if (writer) {
+    blk = nt.new_blk >= 0 ? nt.new_blk : a.block_tables[(int64_t)b * a.bt_sb + nt.page];
+    x = *reinterpret_cast<const uint4 *>((lane >= 16 ? nt.v : nt.k) + 8 * (lane & 15));
+  }
+  listed_walk<G, Engine, NW, PD, true>(a, split, bh, lp, phys, L, nt);
+  if (!writer) return;
+  if (lane < 32 && blk >= 0 && blk < a.num_blocks) {
+    const int64_t dst =
+        (((int64_t)blk * kPageTokens + nt.off) * a.H_kv + h) * Engine::kD + 8 * (lane & 15);
+    *reinterpret_cast<uint4 *>(const_cast<uint16_t *>(lane >= 16 ? a.v_cache : a.k_cache) +
+                               dst) = x;
+  }
+  if (h == 0 && lane == 0) {
+    app.ctx_lens[b] = sl.x + 1;
+    if (nt.new_blk >= 0) {
+      app.block_tables[(int64_t)b * a.bt_sb + nt.page] = nt.new_blk;
+      app.pages_allocated[b] += 1;
+    }
+  }
 }
 
 // 16-token tiles per scoring wave of the fused launch below.
@@ -1194,6 +1303,14 @@ void launch_decode_g(const DecodeArgs &a, int kind, dim3 grid, dim3 block, hipSt
     launch_decode_gd<G, 128>(a, kind, grid, block, st);
 }
 
+// The reuse step's listed decode with the token append (D = 128, 16-token
+// pages).
+template <int G>
+void launch_append_g(const DecodeArgs &a, const AppendArgs &app, dim3 grid, hipStream_t st) {
+  hipLaunchKernelGGL((listed_append_kernel<G, MfmaEngine<G, 128, 0>, kWavesPerWg, 2>), grid,
+                     dim3(kWavesPerWg * kWave), 0, st, a, app);
+}
+
 // The lazy check's fused scoring + speculative decode (D = 128).
 template <int G>
 void launch_spec_g(const DecodeArgs &a, const ScoreArgs &s, int score_gx, dim3 grid,
@@ -1209,7 +1326,9 @@ void launch_spec_g(const DecodeArgs &a, const ScoreArgs &s, int score_gx, dim3 g
 #define CVSA_DECODE_LAUNCHERS(PREFIX, GG)                                                    \
   PREFIX template void launch_decode_g<GG>(const DecodeArgs &, int, dim3, dim3, hipStream_t); \
   PREFIX template void launch_spec_g<GG>(const DecodeArgs &, const ScoreArgs &, int, dim3,   \
-                                         hipStream_t);
+                                         hipStream_t);                                         \
+  PREFIX template void launch_append_g<GG>(const DecodeArgs &, const AppendArgs &, dim3,      \
+                                           hipStream_t);
 #define CVSA_DECODE_EXTERN(GG) CVSA_DECODE_LAUNCHERS(extern, GG)
 #define CVSA_DECODE_INSTANTIATE(GG) CVSA_DECODE_LAUNCHERS(, GG)
 

@@ -27,6 +27,25 @@ __global__ __launch_bounds__(kAppendThreads) void append_kv_kernel(
   const int i = threadIdx.x;
   const int lane = i & 63, wave = i >> 6;
   const int b = seq_begin + i;
+  const int vec_per_row = H_kv * D / 8;
+  const int total = n_seqs * vec_per_row;
+
+  // The new rows do not depend on the slot: up to kPre 16-byte vectors per
+  // thread are requested with the context lengths, so the copy below waits
+  // for no load of its own (a batch of more rows loads them in the loop).
+  constexpr int kPre = 4;
+  const bool pre = total <= kPre * kAppendThreads;  // uniform
+  uint4 pk[kPre], pv[kPre];
+  if (pre) {
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+      const int v = min(i + k * kAppendThreads, total - 1);
+      const int s = v / vec_per_row;
+      const int64_t src = s * new_sb + (v - s * vec_per_row) * 8;
+      pk[k] = *reinterpret_cast<const uint4 *>(k_new + src);
+      pv[k] = *reinterpret_cast<const uint4 *>(v_new + src);
+    }
+  }
 
   int ctx = 0, page = 0, off = 0;
   uint32_t need = 0;
@@ -66,17 +85,31 @@ __global__ __launch_bounds__(kAppendThreads) void append_kv_kernel(
   __syncthreads();
 
   // Copy the K and V rows: [H_kv, D] bf16 per sequence, as 16-byte vectors.
-  const int vec_per_row = H_kv * D / 8;
-  const int total = n_seqs * vec_per_row;
-  for (int v = i; v < total; v += kAppendThreads) {
-    const int s = v / vec_per_row;
-    const int w = v - s * vec_per_row;
+  auto dst_of = [&](int v, int &s) {
+    s = v / vec_per_row;
     const int blk = s_blk[s];
-    if (blk < 0) continue;
-    const int64_t dst = ((int64_t)blk * block_size + s_off[s]) * H_kv * D + w * 8;
-    const int64_t src = s * new_sb + w * 8;
-    *reinterpret_cast<uint4 *>(k_cache + dst) = *reinterpret_cast<const uint4 *>(k_new + src);
-    *reinterpret_cast<uint4 *>(v_cache + dst) = *reinterpret_cast<const uint4 *>(v_new + src);
+    return blk < 0 ? (int64_t)-1
+                   : ((int64_t)blk * block_size + s_off[s]) * H_kv * D + (v - s * vec_per_row) * 8;
+  };
+  if (pre) {
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+      const int v = i + k * kAppendThreads;
+      int s;
+      const int64_t dst = v < total ? dst_of(v, s) : (int64_t)-1;
+      if (dst < 0) continue;
+      *reinterpret_cast<uint4 *>(k_cache + dst) = pk[k];
+      *reinterpret_cast<uint4 *>(v_cache + dst) = pv[k];
+    }
+  } else {
+    for (int v = i; v < total; v += kAppendThreads) {
+      int s;
+      const int64_t dst = dst_of(v, s);
+      if (dst < 0) continue;
+      const int64_t src = s * new_sb + (v - s * vec_per_row) * 8;
+      *reinterpret_cast<uint4 *>(k_cache + dst) = *reinterpret_cast<const uint4 *>(k_new + src);
+      *reinterpret_cast<uint4 *>(v_cache + dst) = *reinterpret_cast<const uint4 *>(v_new + src);
+    }
   }
   if (i < n_seqs) context_lens[b] = ctx + 1;
 }

@@ -323,6 +323,110 @@ extern "C" int cvsa_sparse_decode(const uint16_t *q, int64_t q_stride_b, int64_t
                        workspace, workspace_bytes, (hipStream_t)stream);
 }
 
+// ------------------------------------------------ decode with the token append
+// cvsa_sparse_decode_append: the append of cvsa_append_kv (one token per
+// sequence, slots from the caller's host mirror) and the listed decode of
+// cvsa_sparse_decode over the appended cache.  One launch
+// (listed_append_kernel) for 16-token pages, D = 128, G <= 16 and
+// B <= kMaxAppendSeqs; otherwise the two entry points in order.
+static int check_append_slots(const char *name, const int32_t *slots, int B, int block_size,
+                              int W, int64_t num_blocks, int &next_free) {
+  CVSA_REQUIRE(slots != nullptr, CVSA_ERR_INVALID, "%s: slots is NULL", name);
+  next_free = -1;
+  int rank = 0;
+  for (int b = 0; b < B; ++b) {
+    const int ctx = slots[2 * b], blk = slots[2 * b + 1];
+    CVSA_REQUIRE(ctx >= 0 && ctx / block_size < W, CVSA_ERR_INVALID,
+                 "%s: sequence %d: context %d + 1 exceeds the block table (%d pages)", name, b,
+                 ctx, W);
+    if (blk < 0) {
+      CVSA_REQUIRE(blk == -1, CVSA_ERR_INVALID, "%s: sequence %d: bad new block %d", name, b,
+                   blk);
+      continue;
+    }
+    if (next_free < 0) next_free = blk;
+    CVSA_REQUIRE(ctx % block_size == 0 && blk == next_free + rank && blk < num_blocks,
+                 CVSA_ERR_INVALID,
+                 "%s: sequence %d: new block %d is not the next of the allocator (context %d, "
+                 "%lld blocks)",
+                 name, b, blk, ctx, (long long)num_blocks);
+    ++rank;
+  }
+  if (next_free < 0) next_free = 0;
+  return CVSA_OK;
+}
+
+extern "C" int cvsa_sparse_decode_append(
+    const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h, uint16_t *k_cache,
+    uint16_t *v_cache, int64_t num_blocks, int32_t *block_tables, int64_t bt_stride_b,
+    int32_t *context_lens, const int32_t *page_indices, int64_t idx_stride,
+    const int32_t *n_per_head, int32_t max_selected, int32_t B, int32_t H_q, int32_t H_kv,
+    int32_t D, int32_t block_size, int32_t W, void *out, int32_t out_dtype, int64_t *work,
+    void *workspace, size_t workspace_bytes, const uint16_t *k_new, const uint16_t *v_new,
+    int64_t new_stride_b, int32_t *pages_allocated, const int32_t *slots, void *stream) {
+  const char *name = "sparse_decode_append";
+  CVSA_REQUIRE(k_new && v_new && pages_allocated && page_indices, CVSA_ERR_INVALID,
+               "%s: null pointer argument", name);
+  CVSA_REQUIRE(((uintptr_t)k_new & 15) == 0 && ((uintptr_t)v_new & 15) == 0 &&
+                   new_stride_b % 8 == 0 && new_stride_b >= (int64_t)H_kv * D,
+               CVSA_ERR_INVALID,
+               "%s: new K/V rows must be 16-byte aligned, new_stride_b a multiple of 8 >= "
+               "H_kv * D",
+               name);
+  DecodeArgs a = base_args(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                           block_tables, bt_stride_b, context_lens, nullptr, nullptr, nullptr,
+                           out, out_dtype, work);
+  a.page_idx = page_indices;
+  a.idx_stride = idx_stride;
+  a.max_sel = max_selected;
+  a.n_pages = n_per_head;
+  DecodeLaunch p{};
+  size_t need = 0;
+  int rc = validate_decode(name, a, B, H_q, H_kv, D, block_size, W, true, false, p, need);
+  if (rc != CVSA_OK) return rc;
+  if ((rc = check_workspace(name, workspace, workspace_bytes, need)) != CVSA_OK) return rc;
+  int next_free = 0;
+  if ((rc = check_append_slots(name, slots, B, block_size, W, num_blocks, next_free)) !=
+      CVSA_OK)
+    return rc;
+  const int G = H_q / H_kv;
+  hipStream_t st = (hipStream_t)stream;
+  if (D != 128 || block_size != kPageTokens || G > kMaxGroup || B > kMaxAppendSeqs ||
+      p.streamk) {
+    if ((rc = cvsa_append_kv(k_new, v_new, new_stride_b, k_cache, v_cache, num_blocks,
+                             block_tables, bt_stride_b, W, context_lens, pages_allocated, 0, B,
+                             next_free, H_kv, D, block_size, stream)) != CVSA_OK)
+      return rc;
+    return enqueue_decode(name, a, G, true, p, workspace, need, st);
+  }
+  AppendArgs app{};
+  app.k_new = k_new;
+  app.v_new = v_new;
+  app.new_sb = new_stride_b;
+  app.block_tables = block_tables;
+  app.ctx_lens = context_lens;
+  app.pages_allocated = pages_allocated;
+  for (int b = 0; b < B; ++b) app.slot[b] = make_int2(slots[2 * b], slots[2 * b + 1]);
+  bind_workspace(a, workspace, need);
+  a.q_group = G;
+  a.q_off = 0;
+  const dim3 grid(p.grid_x, p.grid_y);
+  switch (G) {
+#define CVSA_APP_CASE(GG)                     \
+  case GG:                                    \
+    launch_append_g<GG>(a, app, grid, st);    \
+    break;
+    CVSA_APP_CASE(1) CVSA_APP_CASE(2) CVSA_APP_CASE(3) CVSA_APP_CASE(4)
+    CVSA_APP_CASE(5) CVSA_APP_CASE(6) CVSA_APP_CASE(7) CVSA_APP_CASE(8)
+    CVSA_APP_CASE(9) CVSA_APP_CASE(10) CVSA_APP_CASE(11) CVSA_APP_CASE(12)
+    CVSA_APP_CASE(13) CVSA_APP_CASE(14) CVSA_APP_CASE(15) CVSA_APP_CASE(16)
+#undef CVSA_APP_CASE
+    default:
+      break;
+  }
+  return cvsa_host::check_launch(name);
+}
+
 // ------------------------------------------------ allocation-free variant
 // cvsa_sparse_decode_noalloc keeps the decode workspace in this file-scope
 // device array instead of a caller-owned buffer.  Each GPU the library runs

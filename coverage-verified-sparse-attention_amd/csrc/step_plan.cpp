@@ -195,6 +195,25 @@ int speculative_check(const cvsa_step_desc &d, const uint16_t *q, void *out, voi
 
 }  // namespace
 
+extern "C" int cvsa_step_plan_run_append(cvsa_step_plan *plan, const uint16_t *q, void *out,
+                                         const uint16_t *k_new, const uint16_t *v_new,
+                                         int64_t new_stride_b, int32_t *pages_allocated,
+                                         const int32_t *slots, void *stream) {
+  STEP_REQUIRE(plan && q && out, CVSA_ERR_INVALID, "step_plan_run_append: null argument");
+  STEP_REQUIRE(aligned16(q), CVSA_ERR_INVALID,
+               "step_plan_run_append: q must be 16-byte aligned");
+  const cvsa_step_desc &d = plan->d;
+  // The descriptor's caches, page table and context lengths are the
+  // caller's writable buffers; this step appends to them.
+  return cvsa_sparse_decode_append(
+      q, d.q_stride_b, d.q_stride_h, const_cast<uint16_t *>(d.k_cache),
+      const_cast<uint16_t *>(d.v_cache), d.num_blocks, const_cast<int32_t *>(d.block_tables),
+      d.bt_stride_b, const_cast<int32_t *>(d.context_lens), d.page_indices, d.budget,
+      d.n_per_head, d.budget, d.B, d.H_q, d.H_kv, d.D, d.block_size, d.W, out, d.out_dtype,
+      d.work, d.workspace, d.workspace_bytes, k_new, v_new, new_stride_b, pages_allocated,
+      slots, stream);
+}
+
 extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint16_t *q,
                                   void *out, void *stream) {
   STEP_REQUIRE(plan && q && out, CVSA_ERR_INVALID, "step_plan_run: null argument");

@@ -389,6 +389,27 @@ class CVSABackend:
             return None
         return self._matching_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens)
 
+    def call_with_append(self, q, k_new, v_new, manager, layer_idx):
+        """The decode loops' append then call (``manager.append_tokens_kv(k_new,
+        v_new)``, then this backend on the manager's cache, tables and context
+        lengths), with the append folded into the decode launch when the call
+        is a reuse step through a step plan (cvsa_step_plan_run_append);
+        otherwise the two in turn.  Same outputs, cache, tables, context
+        lengths and statistics either way; no counterpart in the reference."""
+        cache = manager.cache
+        args = (cache.k_cache, cache.v_cache, manager.block_tables, manager.context_lens)
+        plan = None
+        if manager.fusable_rows(k_new, v_new):
+            plan = self.reuse_plan_for(q, *args, layer_idx)
+        if plan is None:
+            manager.append_tokens_kv(k_new, v_new)
+            return self(q, *args, layer_idx)
+        slots, commit = manager.fused_append_slots()
+        out = plan.run_reuse_append(q, k_new, v_new, manager._pages_allocated_dev, slots)
+        commit()
+        self.note_replayed_reuse(layer_idx)
+        return out
+
     def note_replayed_reuse(self, layer_idx: int) -> None:
         """Host bookkeeping of a reuse call that was replayed from a graph
         instead of made (backend.py:313-321: the call clears the layer's

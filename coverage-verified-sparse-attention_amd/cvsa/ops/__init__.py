@@ -760,6 +760,20 @@ class StepPlan:
               "step_plan_run")
         return out
 
+    def run_reuse_append(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                         pages_allocated: torch.Tensor, slots) -> torch.Tensor:
+        """A reuse step with the step's token append folded in
+        (cvsa_step_plan_run_append): k_new / v_new [B, H_kv, D] contiguous
+        bf16, pages_allocated the int32 [B] allocation counts on the device,
+        slots the host int32 array of SequenceKVManager.fused_append_slots.
+        Writes the plan's caches, block table and context lengths."""
+        out = torch.empty(self.out_shape, device=self.dev, dtype=self.out_dtype)
+        check(_lib.load().cvsa_step_plan_run_append(
+            self._h, q.data_ptr(), out.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
+            k_new.stride(0), pages_allocated.data_ptr(), slots, self.stream),
+            "step_plan_run_append")
+        return out
+
 
 def _flat_selection(page_indices: torch.Tensor, n_per_head: torch.Tensor, num_kv_heads: int):
     if page_indices.dim() != 3:

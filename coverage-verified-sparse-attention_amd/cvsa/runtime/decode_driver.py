@@ -91,10 +91,15 @@ class DecodeDriver:
     reference per-layer protocol; see the module docstring."""
 
     def __init__(self, backend, layers: SyntheticDecodeLayers, graphs: bool = False,
-                 stream: Optional[torch.cuda.Stream] = None, graph_chunk: int = 8):
+                 stream: Optional[torch.cuda.Stream] = None, graph_chunk: int = 8,
+                 fuse_append: bool = False):
         self.backend = backend
         self.layers = layers
         self.graphs = graphs
+        # Eager steps hand each layer's append to the backend
+        # (CVSABackend.call_with_append), which folds it into the decode
+        # launch of a reuse step.
+        self.fuse_append = bool(fuse_append) and hasattr(backend, "call_with_append")
         self.graph_chunk = max(1, int(graph_chunk))
         # Graph capture needs a stream other than the legacy default one, and
         # the step plans are bound to the stream they were made on: every
@@ -123,6 +128,10 @@ class DecodeDriver:
         L = self.layers.num_layers
         for l in (range(L) if layers is None else layers):
             cache, mgr = self.layers.caches[l], self.layers.managers[l]
+            if k is not None and self.fuse_append:
+                outs.append(self.backend.call_with_append(q[l], k[l], v[l], mgr, l))
+                self.backend.step_done(l, L)
+                continue
             if k is not None:
                 mgr.append_tokens_kv(k[l], v[l])
             outs.append(self.backend(q[l], cache.k_cache, cache.v_cache, mgr.block_tables,

@@ -16,6 +16,8 @@ If ``block_tables`` / ``context_lens`` are edited directly, call
 """
 from __future__ import annotations
 
+import ctypes
+
 from dataclasses import dataclass
 
 import torch
@@ -179,6 +181,47 @@ class SequenceKVManager:
         if k.shape[0] != self.batch_size:
             raise ValueError(f"expected {self.batch_size} rows, got {k.shape[0]}")
         self._append(0, k, v)
+
+    def fusable_rows(self, k: torch.Tensor, v: torch.Tensor) -> bool:
+        """Whether [B, H_kv, D] rows k / v can be appended by a decode launch
+        (cvsa_sparse_decode_append): contiguous bf16 on the cache's device,
+        one row per sequence."""
+        c = self.cache.k_cache
+        return (k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16 and k.is_contiguous()
+                and v.is_contiguous() and k.device == c.device and v.device == c.device
+                and tuple(k.shape) == (self.batch_size, c.shape[2], c.shape[3])
+                and k.shape == v.shape and k.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0)
+
+    def fused_append_slots(self):
+        """The slots of one token appended to every sequence by a decode
+        launch: a ctypes int32 array of (context length before the append,
+        block the append allocates or -1) per sequence, the allocation rule
+        of append_token_kv (kv_cache.py:133-150) applied to the host mirror.
+        Returns (slots, commit); call commit() once the launch is enqueued
+        (it reserves the blocks and advances the mirror)."""
+        seqs = range(self.batch_size)
+        need = self._plan_append(seqs)
+        first = self.cache._next_free
+        if first + need > self.cache._total_blocks:
+            raise AssertionError(f"Out of blocks: need {need}, have "
+                                 f"{self.cache._total_blocks - first}")
+        bs = self.block_size
+        slots = (ctypes.c_int32 * (2 * self.batch_size))()
+        r = 0
+        for s in seqs:
+            ctx = self._ctx_host[s]
+            slots[2 * s] = ctx
+            if ctx % bs == 0 and ctx // bs >= self._pages_allocated[s]:
+                slots[2 * s + 1] = first + r
+                r += 1
+            else:
+                slots[2 * s + 1] = -1
+
+        def commit():
+            self.cache._reserve(need)
+            self._commit_append(seqs)
+
+        return slots, commit
 
     def _append(self, seq_begin: int, k: torch.Tensor, v: torch.Tensor):
         n = k.shape[0]

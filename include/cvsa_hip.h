@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 9
+#define CVSA_ABI_VERSION 10
 
 enum {
   CVSA_OK = 0,
@@ -255,6 +255,43 @@ int cvsa_sparse_decode_noalloc(const uint16_t *q, int64_t q_stride_b,
                                int32_t W, float *o_unnorm, float *m_out,
                                float *l_out, void *out, int32_t out_dtype,
                                int64_t *work, void *stream);
+
+/*
+ * cvsa_sparse_decode with the step's token append folded in: for every
+ * sequence b < B, the append of cvsa_append_kv (one token: rows b of
+ * k_new / v_new, [H_kv, D] bf16, new_stride_b elements apart), then the
+ * listed decode of cvsa_sparse_decode over the appended cache, as one launch
+ * for 16-token pages, D = 128, H_q / H_kv <= 16 and B <= 256 (otherwise the
+ * two entry points in order, with the same results).  No counterpart in the
+ * reference, whose decode loops append (SequenceKVManager.append_token_kv,
+ * cvsa/runtime/kv_cache.py:133-150) and then call the backend: it is for
+ * decode drivers whose reuse steps would otherwise pay a second launch per
+ * layer for the append.  The attention is that of the append followed by
+ * cvsa_sparse_decode, bit for bit.
+ * slots: HOST array of 2 * B int32 from the caller's mirror of the
+ * allocation state: slots[2b] = context_lens[b] before the append,
+ * slots[2b + 1] = the block the append allocates for b (its page
+ * slots[2b] / block_size is new: slots[2b] % block_size == 0 and not yet
+ * allocated; the r-th such sequence in increasing b takes next_free + r), or
+ * -1.  Inconsistent slots return CVSA_ERR_INVALID before anything is
+ * enqueued.  block_tables, context_lens and pages_allocated are updated as
+ * cvsa_append_kv does; the other arguments, outputs and errors are those of
+ * cvsa_sparse_decode (normalised output only).
+ */
+int cvsa_sparse_decode_append(const uint16_t *q, int64_t q_stride_b,
+                              int64_t q_stride_h, uint16_t *k_cache,
+                              uint16_t *v_cache, int64_t num_blocks,
+                              int32_t *block_tables, int64_t bt_stride_b,
+                              int32_t *context_lens,
+                              const int32_t *page_indices, int64_t idx_stride,
+                              const int32_t *n_per_head, int32_t max_selected,
+                              int32_t B, int32_t H_q, int32_t H_kv, int32_t D,
+                              int32_t block_size, int32_t W, void *out,
+                              int32_t out_dtype, int64_t *work, void *workspace,
+                              size_t workspace_bytes, const uint16_t *k_new,
+                              const uint16_t *v_new, int64_t new_stride_b,
+                              int32_t *pages_allocated, const int32_t *slots,
+                              void *stream);
 
 /*
  * Dense paged decode over every valid page.  Replaces
@@ -488,6 +525,15 @@ int cvsa_step_plan_create(const cvsa_step_desc *desc, cvsa_step_plan **plan);
 /* q: [B, H_q, D] bf16 with the descriptor's strides; out: [B, H_q, D]. */
 int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint16_t *q, void *out,
                        void *stream);
+/* A reuse step (CVSA_STEP_REUSE) with the step's token append folded in:
+ * cvsa_sparse_decode_append over the plan's buffers, whose k_cache,
+ * v_cache, block_tables and context_lens it writes (see there for k_new,
+ * v_new, new_stride_b, pages_allocated and slots).  No counterpart in the
+ * reference (its loops append, then call the backend). */
+int cvsa_step_plan_run_append(cvsa_step_plan *plan, const uint16_t *q, void *out,
+                              const uint16_t *k_new, const uint16_t *v_new,
+                              int64_t new_stride_b, int32_t *pages_allocated,
+                              const int32_t *slots, void *stream);
 void cvsa_step_plan_destroy(cvsa_step_plan *plan);
 
 #ifdef __cplusplus

@@ -10,6 +10,12 @@
   protocol, step after step with appends and scoring steps in between (each
   replay is checked against the eager run), and leave the same schedule,
   statistics and tracing state.
+* Appends folded into the reuse steps' decode launches
+  (``DecodeDriver(fuse_append=True)``, cvsa_step_plan_run_append) give the
+  outputs, caches, page tables, context lengths, allocation counts and
+  statistics of the separate append followed by the call, bit for bit, with
+  sequences crossing page boundaries, in the one-launch form (16-token
+  pages, D = 128, G <= 16) and in the two-launch form of other shapes.
 """
 import pytest
 import torch
@@ -49,10 +55,10 @@ ORACLE_SHAPE = dict(num_layers=3, batch=2, num_q_heads=32, num_kv_heads=8, head_
                     hot_heads=[0, 2, 5, 7], n_hot=6, hot_shift=9.0)
 
 
-@pytest.mark.parametrize("graphs", [False, True])
+@pytest.mark.parametrize("mode", ["eager", "graphs", "fused"])
 @pytest.mark.parametrize("kw", [dict(lazy=True, check_interval=3),
                                 dict(lazy=False, reuse_interval=2)])
-def test_driver_matches_oracle_backend(gpu, graphs, kw):
+def test_driver_matches_oracle_backend(gpu, mode, kw):
     """3 layers x 12 steps with one token appended per sequence per layer and
     step: every layer's output, cached selection, accept mask and complement
     pages after every step, and the final statistics, against the oracle
@@ -64,7 +70,8 @@ def test_driver_matches_oracle_backend(gpu, graphs, kw):
     backend = CVSABackend(**cfg)
     oracle = OracleCVSABackend(**cfg)
     state = _OracleLayers(layers)
-    driver = DecodeDriver(backend, layers, graphs=graphs)
+    graphs = mode == "graphs"
+    driver = DecodeDriver(backend, layers, graphs=graphs, fuse_append=mode == "fused")
     kinds = set()
     for step in range(12):
         q, k, v = layers.step_inputs(step)
@@ -152,3 +159,96 @@ def test_driver_run_reports_latency(gpu):
     assert res["steps"] == 8 and len(res["per_step_ms"]) == 8
     assert 0 < res["median_ms"] <= res["p99_ms"]
     assert res["graph_replays"] >= 4
+
+
+def _count_fused(monkeypatch):
+    from cvsa import ops
+    calls = []
+    orig = ops.StepPlan.run_reuse_append
+
+    def counted(self, *a, **k):
+        calls.append(1)
+        return orig(self, *a, **k)
+
+    monkeypatch.setattr(ops.StepPlan, "run_reuse_append", counted)
+    return calls
+
+
+@pytest.mark.parametrize("shape", [
+    # one launch: 16-token pages, D = 128, G = 4; sequences cross pages at
+    # steps 8, 12 and 0 / 16
+    dict(num_q_heads=32, num_kv_heads=8, head_dim=128, block_size=16,
+         context_len=[3000, 1700, 1792]),
+    # two launches inside the entry point: D = 64; 32-token pages; G = 20
+    dict(num_q_heads=16, num_kv_heads=4, head_dim=64, block_size=16,
+         context_len=[2040, 1000]),
+    dict(num_q_heads=32, num_kv_heads=8, head_dim=128, block_size=32,
+         context_len=[2016, 990]),
+    dict(num_q_heads=40, num_kv_heads=2, head_dim=128, block_size=16,
+         context_len=[1600, 2047]),
+], ids=["one_launch", "d64", "bs32", "g20"])
+def test_fused_append_equals_separate(gpu, monkeypatch, shape):
+    calls = _count_fused(monkeypatch)
+    L, steps = 3, 20
+    runs = []
+    for fuse in (False, True):
+        layers = SyntheticDecodeLayers(num_layers=L, batch=len(shape["context_len"]),
+                                       max_new_tokens=steps, seed=21, device=gpu,
+                                       hot_heads=[0, 1], n_hot=6, hot_shift=9.0, **shape)
+        backend = CVSABackend(num_kv_heads=shape["num_kv_heads"],
+                              num_q_heads=shape["num_q_heads"], head_dim=shape["head_dim"],
+                              block_size=shape["block_size"], num_layers=L, budget_pct=0.25,
+                              coverage_threshold=0.9, lazy=True, check_interval=4)
+        runs.append((layers, backend, DecodeDriver(backend, layers, fuse_append=fuse)))
+    (la, ba, da), (lb, bb, db) = runs
+    for step in range(steps):
+        q, k, v = la.step_inputs(step)
+        n0 = len(calls)
+        out_a = [o.clone() for o in da.step(q, k, v)]
+        assert len(calls) == n0, "the separate run took the fused path"
+        out_b = [o.clone() for o in db.step(q, k, v)]
+        for layer, (a, b) in enumerate(zip(out_a, out_b)):
+            assert torch.equal(a, b), (step, layer)
+    torch.cuda.synchronize()
+    for l in range(L):
+        ca, cb = la.caches[l], lb.caches[l]
+        ma, mb = la.managers[l], lb.managers[l]
+        assert torch.equal(ca.k_cache, cb.k_cache) and torch.equal(ca.v_cache, cb.v_cache), l
+        assert torch.equal(ma.block_tables, mb.block_tables), l
+        assert torch.equal(ma.context_lens, mb.context_lens), l
+        assert torch.equal(ma._pages_allocated_dev, mb._pages_allocated_dev), l
+        assert ma._pages_allocated == mb._pages_allocated and ma._ctx_host == mb._ctx_host, l
+        assert ca._next_free == cb._next_free, l
+        assert ma._ctx_host == [int(x) for x in mb.context_lens.tolist()], l
+        assert ma._pages_allocated == [int(x) for x in mb._pages_allocated_dev.tolist()], l
+    assert ba.get_stats() == bb.get_stats()
+    # every reuse call of the fused run (3 of every 4 steps per layer) was fused
+    assert len(calls) == L * (steps - steps // 4), len(calls)
+
+
+def test_fused_append_rejects_inconsistent_slots(gpu):
+    """A slot table that does not follow the allocator is refused before any
+    launch: the cache, tables and lengths stay as they were."""
+    import ctypes
+    from cvsa import ops
+    layers = SyntheticDecodeLayers(num_layers=1, batch=2, num_q_heads=32, num_kv_heads=8,
+                                   head_dim=128, context_len=[1601, 1700], max_new_tokens=4,
+                                   seed=3, device=gpu)
+    backend = CVSABackend(num_kv_heads=8, num_q_heads=32, head_dim=128, block_size=16,
+                          num_layers=1, budget_pct=0.25, lazy=True, check_interval=4)
+    mgr, cache = layers.managers[0], layers.caches[0]
+    q, k, v = layers.step_inputs(0)
+    backend(q[0], cache.k_cache, cache.v_cache, mgr.block_tables, mgr.context_lens, 0)
+    backend.step_done(0, 1)
+    plan = backend.reuse_plan_for(q[0], cache.k_cache, cache.v_cache, mgr.block_tables,
+                                  mgr.context_lens, 0)
+    assert plan is not None
+    before = (mgr.context_lens.clone(), mgr.block_tables.clone(), cache.k_cache[:4].clone())
+    slots, _ = mgr.fused_append_slots()
+    bad = (ctypes.c_int32 * 4)(*slots)
+    bad[1] = 7  # sequence 0 is mid-page (1601 % 16 == 1): it takes no new block
+    with pytest.raises(ValueError):
+        plan.run_reuse_append(q[0], k[0], v[0], mgr._pages_allocated_dev, bad)
+    torch.cuda.synchronize()
+    assert torch.equal(mgr.context_lens, before[0]) and torch.equal(mgr.block_tables, before[1])
+    assert torch.equal(cache.k_cache[:4], before[2])
