@@ -814,6 +814,59 @@ def sparse_decode(q, k_cache, v_cache, block_tables, page_indices, n_per_head,
                    num_kv_heads, num_q_per_kv, block_size, pi, nph, k)[3]
 
 
+def sparse_decode_append(q, k_cache, v_cache, block_tables, context_lens, page_indices,
+                         n_per_head, k_new, v_new, pages_allocated, slots, num_kv_heads,
+                         num_q_per_kv, block_size, work: Optional[torch.Tensor] = None):
+    """append_kv of one token per sequence, then sparse_decode over the
+    appended cache, in one launch where the shapes allow
+    (cvsa_sparse_decode_append; no reference counterpart).
+
+    ``slots``: a host sequence of 2 * B int32, (context length before the
+    append, block the append allocates or -1) per sequence, as
+    SequenceKVManager.fused_append_slots builds them.  block_tables,
+    context_lens and pages_allocated (contiguous int32) and the caches are
+    updated in place.  Returns the normalised output [B, H_q, D] in q.dtype.
+    """
+    pi, nph, k = _flat_selection(page_indices, n_per_head, num_kv_heads)
+    dev = _device_of(q, k_cache, v_cache, block_tables, context_lens, pi, nph, k_new, v_new,
+                     pages_allocated, work)
+    q = _check_q(q)
+    _check_cache(k_cache)
+    _check_cache(v_cache, "v_cache")
+    for name, t in (("block_tables", block_tables), ("context_lens", context_lens),
+                    ("pages_allocated", pages_allocated)):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"sparse_decode_append: {name} must be contiguous int32")
+    B, H_q, D = q.shape
+    if k_cache.shape[1] != block_size or k_cache.shape[3] != D:
+        raise ValueError("sparse_decode_append: cache block_size / head_dim mismatch")
+    shape = (B, num_kv_heads, D)
+    if (k_new.dtype != torch.bfloat16 or v_new.dtype != torch.bfloat16
+            or tuple(k_new.shape) != shape or tuple(v_new.shape) != shape
+            or not (k_new.is_contiguous() and v_new.is_contiguous())):
+        raise ValueError(f"sparse_decode_append: k_new / v_new must be contiguous bfloat16 "
+                         f"{shape}")
+    if len(slots) != 2 * B:
+        raise ValueError(f"sparse_decode_append: {2 * B} slot entries expected")
+    slot_arr = slots if isinstance(slots, ctypes.Array) else (ctypes.c_int32 * (2 * B))(*slots)
+    W = block_tables.shape[1]
+    L = _lib.load()
+    need = L.cvsa_decode_workspace_bytes(B, H_q, num_kv_heads, D, k, W, 0)
+    ws = _workspace(dev, need)
+    out = torch.empty(B, H_q, D, device=dev, dtype=q.dtype)
+    if q.dtype not in _DTYPE_CODE:
+        raise ValueError(f"unsupported output dtype {q.dtype}")
+    check(L.cvsa_sparse_decode_append(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+        k_cache.shape[0], block_tables.data_ptr(), block_tables.stride(0),
+        context_lens.data_ptr(), pi.data_ptr(), pi.stride(0), nph.data_ptr(), k, B, H_q,
+        num_kv_heads, D, block_size, W, out.data_ptr(), _DTYPE_CODE[q.dtype], _ptr(work),
+        _ptr(ws), 0 if ws is None else ws.numel(), k_new.data_ptr(), v_new.data_ptr(),
+        k_new.stride(0), pages_allocated.data_ptr(), slot_arr, _stream(dev)),
+        "sparse_decode_append")
+    return out
+
+
 def prepare_reuse_state(page_indices, n_per_head, num_kv_heads, B):
     """(pi_flat, nph_flat, padded_max_selected) for sparse_decode_reuse.
 

@@ -14,6 +14,9 @@ The same draws run at head dimensions 64 and 256 (engines compiled per D,
 split partials of G x (D + 4) floats, merges over several chunk passes when
 G x D / 4 exceeds the workgroup) and at block sizes 32 and 64 (pages walked
 as 2 or 4 tiles of 16 tokens).
+The decode with the token append folded in (cvsa_sparse_decode_append) is
+drawn the same way, with sequences at page offsets 0, mid-page and last
+slot, and compared with the append followed by the decode, bit for bit.
 """
 import pytest
 import torch
@@ -136,3 +139,92 @@ def test_random_decode_launches_wide_groups(gpu, seed):
 def test_random_decode_launches_large_groups(gpu, seed):
     """G = 17..48 query heads per KV head: one launch per 16 of them."""
     _check(gpu, 20 + seed, [128, 64, 256, 128][seed], [16, 16, 16, 32][seed], (17, 48))
+
+
+def _append_case(seed, dev, D, BS, G):
+    """A batch whose sequences sit at random page offsets (0, mid, last),
+    the next free blocks after the used ones, and selections that hold the
+    new token's page on about half of the heads (its page before the append
+    when the token is mid-page, the page the append allocates otherwise)."""
+    g = torch.Generator().manual_seed(1000 + seed)
+    rnd = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))  # noqa: E731
+    H = [1, 2, 4, 8][rnd(0, 3)]
+    B = rnd(1, 5)
+    ctx = []
+    for _ in range(B):
+        pages = rnd(1, 300)
+        off = [0, rnd(1, BS - 2), BS - 1][rnd(0, 2)]
+        ctx.append(pages * BS + off)
+    inp = make_paged_inputs(B, H * G, H, D, ctx, block_size=BS, seed=seed, device=dev,
+                            spare_blocks=B + 4)
+    W = inp.block_tables.shape[1] + 1
+    bt = torch.zeros(B, W, dtype=torch.int32, device=dev)
+    bt[:, :W - 1] = inp.block_tables
+    alloc = torch.tensor([-(-c // BS) for c in ctx], dtype=torch.int32, device=dev)
+    width = rnd(1, 64)
+    pi = torch.zeros(B, H, width, dtype=torch.int32)
+    nph = torch.zeros(B, H, dtype=torch.int32)
+    for b in range(B):
+        n_valid = ctx[b] // BS + 1          # pages after the append
+        new_page = ctx[b] // BS
+        for h in range(H):
+            n = rnd(0, min(width, n_valid))
+            pages = torch.randperm(n_valid, generator=g)[:n]
+            if n and rnd(0, 1) and new_page not in pages.tolist():
+                pages[0] = new_page
+            pi[b, h, :n] = pages.sort().values.to(torch.int32)
+            nph[b, h] = n
+    kn = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(dev)
+    vn = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(dev)
+    return inp, bt, alloc, pi.to(dev), nph.to(dev), kn, vn, ctx
+
+
+def _slots(ctx, alloc, next_free, BS):
+    slots, r = [], 0
+    for c, a in zip(ctx, alloc.tolist()):
+        new = c % BS == 0 and c // BS >= a
+        slots += [c, next_free + r if new else -1]
+        r += int(new)
+    return slots
+
+
+@pytest.mark.parametrize("shape", [(128, 16, 4), (128, 16, 1), (128, 16, 16), (128, 16, 7),
+                                   (64, 16, 4), (256, 16, 4), (128, 32, 4), (128, 16, 20)],
+                         ids=lambda s: f"D{s[0]}_bs{s[1]}_G{s[2]}")
+@pytest.mark.parametrize("seed", range(3))
+def test_random_decode_append(gpu, seed, shape):
+    """cvsa_sparse_decode_append (one launch at D = 128, 16-token pages,
+    G <= 16; two launches otherwise) against cvsa_append_kv followed by
+    cvsa_sparse_decode on a copy of the same state: outputs bit-identical,
+    caches, tables, lengths, allocation counts and work counters equal; the
+    new token is on a selected page for about half of the heads."""
+    D, BS, G = shape
+    inp, bt, alloc, pi, nph, kn, vn, ctx = _append_case(seed, gpu, D, BS, G)
+    H = inp.k_cache.shape[2]
+    next_free = inp.used_blocks
+    state = [inp.k_cache.clone(), inp.v_cache.clone(), bt.clone(),
+             inp.context_lens.clone(), alloc.clone()]
+    ref = [t.clone() for t in state]
+    work_a = torch.zeros(2, dtype=torch.int64, device=gpu)
+    work_b = torch.zeros(2, dtype=torch.int64, device=gpu)
+    out = ops.sparse_decode_append(inp.q, state[0], state[1], state[2], state[3], pi, nph,
+                                   kn, vn, state[4], _slots(ctx, alloc, next_free, BS), H, G,
+                                   BS, work=work_a)
+    ops.append_kv(kn, vn, ref[0], ref[1], ref[2], ref[3], ref[4], 0, next_free, BS)
+    want = ops.sparse_decode(inp.q, ref[0], ref[1], ref[2], pi, nph, ref[3], H, G, BS)
+    pif, nphf = pi.reshape(-1, pi.shape[2]), nph.reshape(-1)
+    ops.sparse_decode_reuse(inp.q, ref[0], ref[1], ref[2], ref[3], pif, nphf, pi.shape[2], H,
+                            G, BS, work=work_b)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want), (seed, shape)
+    for a, b in zip(state, ref):
+        assert torch.equal(a, b), (seed, shape)
+    assert torch.equal(work_a, work_b), (work_a.tolist(), work_b.tolist())
+    # and against attention over the appended cache in fp32
+    for b in range(len(ctx)):
+        for h in range(H):
+            n = int(nph[b, h])
+            o, _ = _attention(inp.q, ref[0], ref[1], ref[2], b, ctx[b] + 1, h, G,
+                              pi[b, h, :n].long())
+            err = (out[b, h * G:(h + 1) * G].float() - o).abs().max().item()
+            assert err < 2e-2, (seed, shape, b, h, err)
