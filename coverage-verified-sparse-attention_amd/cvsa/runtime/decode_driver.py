@@ -126,12 +126,15 @@ class DecodeDriver:
         backend call, step_done -- the reference's order."""
         outs = []
         L = self.layers.num_layers
+        if k is not None and self.fuse_append:
+            call, done = self.backend.call_with_append, self.backend.step_done
+            managers = self.layers.managers
+            for l in (range(L) if layers is None else layers):
+                outs.append(call(q[l], k[l], v[l], managers[l], l))
+                done(l, L)
+            return outs
         for l in (range(L) if layers is None else layers):
             cache, mgr = self.layers.caches[l], self.layers.managers[l]
-            if k is not None and self.fuse_append:
-                outs.append(self.backend.call_with_append(q[l], k[l], v[l], mgr, l))
-                self.backend.step_done(l, L)
-                continue
             if k is not None:
                 mgr.append_tokens_kv(k[l], v[l])
             outs.append(self.backend(q[l], cache.k_cache, cache.v_cache, mgr.block_tables,

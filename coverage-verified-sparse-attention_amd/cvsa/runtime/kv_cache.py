@@ -104,6 +104,7 @@ class SequenceKVManager:
         self._pages_allocated_dev = torch.zeros(batch_size, dtype=torch.int32, device=dev)
         self._ctx_host = [0] * batch_size
         self._append_call = None
+        self._fuse_shape = None   # (row shape, cache, device) of fusable_rows
 
     def adopt(self, block_tables: torch.Tensor, context_lens: torch.Tensor,
               next_free_block: int) -> None:
@@ -187,10 +188,14 @@ class SequenceKVManager:
         (cvsa_sparse_decode_append): contiguous bf16 on the cache's device,
         one row per sequence."""
         c = self.cache.k_cache
-        return (k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16 and k.is_contiguous()
-                and v.is_contiguous() and k.device == c.device and v.device == c.device
-                and tuple(k.shape) == (self.batch_size, c.shape[2], c.shape[3])
-                and k.shape == v.shape and k.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0)
+        want = self._fuse_shape
+        if want is None or want[1] is not c:
+            want = self._fuse_shape = (torch.Size((self.batch_size, c.shape[2], c.shape[3])),
+                                       c, c.device)
+        return (k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16
+                and k.shape == want[0] and v.shape == want[0] and k.device == want[2]
+                and v.device == want[2] and k.is_contiguous() and v.is_contiguous()
+                and k.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0)
 
     def fused_append_slots(self):
         """The slots of one token appended to every sequence by a decode
