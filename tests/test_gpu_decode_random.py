@@ -228,3 +228,39 @@ def test_random_decode_append(gpu, seed, shape):
                               pi[b, h, :n].long())
             err = (out[b, h * G:(h + 1) * G].float() - o).abs().max().item()
             assert err < 2e-2, (seed, shape, b, h, err)
+
+
+def test_decode_append_large_batch(gpu):
+    """More sequences than the one-launch form takes (B = 260 > 256): the
+    entry point appends and decodes in two launches with the same results."""
+    B, H, G, D, BS = 260, 2, 4, 128, 16
+    g = torch.Generator().manual_seed(77)
+    ctx = [int(x) for x in torch.randint(1, 80, (B,), generator=g)]
+    inp = make_paged_inputs(B, H * G, H, D, ctx, block_size=BS, seed=77, device=gpu,
+                            spare_blocks=B + 4)
+    W = inp.block_tables.shape[1] + 1
+    bt = torch.zeros(B, W, dtype=torch.int32, device=gpu)
+    bt[:, :W - 1] = inp.block_tables
+    alloc = torch.tensor([-(-c // BS) for c in ctx], dtype=torch.int32, device=gpu)
+    width = 4
+    pi = torch.zeros(B, H, width, dtype=torch.int32)
+    nph = torch.zeros(B, H, dtype=torch.int32)
+    for b in range(B):
+        n_valid = ctx[b] // BS + 1
+        n = min(width, n_valid)
+        pi[b, :, :n] = torch.arange(n_valid - n, n_valid, dtype=torch.int32)
+        nph[b] = n
+    pi, nph = pi.to(gpu), nph.to(gpu)
+    kn = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(gpu)
+    vn = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(gpu)
+    state = [inp.k_cache.clone(), inp.v_cache.clone(), bt.clone(), inp.context_lens.clone(),
+             alloc.clone()]
+    ref = [t.clone() for t in state]
+    out = ops.sparse_decode_append(inp.q, *state[:4], pi, nph, kn, vn, state[4],
+                                   _slots(ctx, alloc, inp.used_blocks, BS), H, G, BS)
+    ops.append_kv(kn, vn, *ref, 0, inp.used_blocks, BS)
+    want = ops.sparse_decode(inp.q, ref[0], ref[1], ref[2], pi, nph, ref[3], H, G, BS)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    for a, b in zip(state, ref):
+        assert torch.equal(a, b)
