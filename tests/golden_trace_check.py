@@ -39,11 +39,15 @@ COV_ATOL = 1e-3      # coverage (BASELINE north-star tolerance)
 LSE_RTOL = 1e-3      # log-sum-exp of the merged result, relative
 
 
-def replay(name, make_backend, make_runtime, counters_of, state_of=None):
+def replay(name, make_backend, make_runtime, counters_of, state_of=None, fused_call=None):
     """make_backend(kwargs) -> backend; make_runtime(case) -> (call_args_fn,
     append_fn, state_fn); counters_of(backend) -> dict like the recorded one.
     state_of(backend, call_args) -> (coverage [B, H_kv], lse [B, H_q]) of the
-    backend's last scoring step, for scenarios that recorded them."""
+    backend's last scoring step, for scenarios that recorded them.
+    fused_call(backend, q, k_rows, v_rows) -> output: when given, the append of
+    step s's tokens (every sequence) and the call of step s + 1 are made by
+    this one call (the order the reference takes, append then call), and the
+    last step's append by append_fn."""
     sc = SCENARIOS[name]
     meta, arr = load(name)
     case = make_case(**sc["inputs"])
@@ -52,7 +56,10 @@ def replay(name, make_backend, make_runtime, counters_of, state_of=None):
     backend = make_backend(inp, sc["backend"])
     call_args, append, state = make_runtime(case)
     for s in range(inp["steps"]):
-        out = backend(*call_args(case.q[s]), 0)
+        if fused_call is not None and s > 0:
+            out = fused_call(backend, case.q[s], case.k_new[s - 1], case.v_new[s - 1])
+        else:
+            out = backend(*call_args(case.q[s]), 0)
         want = torch.from_numpy(arr[f"out_{s}"]).view(torch.bfloat16).float()
         err = (out.detach().cpu().float() - want).abs().max().item()
         assert err <= OUT_ATOL, (name, s, err)
@@ -80,8 +87,9 @@ def replay(name, make_backend, make_runtime, counters_of, state_of=None):
             rel = ((lse.cpu().float() - want_lse).abs() / want_lse.abs().clamp(min=1.0))
             assert rel.max().item() < LSE_RTOL, (name, s, "lse")
         backend.step_done(0, 1)
-        for b in range(inp["batch"]):
-            append(b, case.k_new[s][b], case.v_new[s][b])
+        if fused_call is None or s == inp["steps"] - 1:
+            for b in range(inp["batch"]):
+                append(b, case.k_new[s][b], case.v_new[s][b])
     bt, ctx = state()
     assert np.array_equal(bt, arr["block_tables"]) and np.array_equal(ctx, arr["context_lens"])
     stats = backend.get_stats()

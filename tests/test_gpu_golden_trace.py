@@ -38,7 +38,10 @@ def _runtime(dev):
         def state():
             return mgr.block_tables.cpu().numpy(), mgr.context_lens.cpu().numpy()
 
+        runtimes.append((dev, mgr))
         return call_args, append, state
+    runtimes = []
+    make.runtimes = runtimes
     return make
 
 
@@ -66,3 +69,32 @@ def test_hip_backend_matches_reference_trace(gpu, name):
     replay(name, lambda inp, kw: CVSABackend(inp["num_kv_heads"], inp["num_q_heads"],
                                              inp["head_dim"], 16, **kw),
            _runtime(gpu), _counters, _hip_state)
+
+
+@pytest.mark.parametrize("name", sorted(SCENARIOS))
+def test_hip_backend_matches_reference_trace_folded_appends(gpu, monkeypatch, name):
+    """The same traces with each step's appends folded into the next call
+    (CVSABackend.call_with_append, the decode loops' append-then-call order):
+    a reuse step through a step plan appends in its decode launch, every
+    other call appends first; all recorded quantities as above."""
+    from cvsa import ops
+    calls = []
+    orig = ops.StepPlan.run_reuse_append
+
+    def counted(self, *a, **k):
+        calls.append(1)
+        return orig(self, *a, **k)
+
+    monkeypatch.setattr(ops.StepPlan, "run_reuse_append", counted)
+    make = _runtime(gpu)
+
+    def fused(backend, q, k_rows, v_rows):
+        dev, mgr = make.runtimes[-1]
+        return backend.call_with_append(q.to(dev), k_rows.to(dev).contiguous(),
+                                        v_rows.to(dev).contiguous(), mgr, 0)
+
+    replay(name, lambda inp, kw: CVSABackend(inp["num_kv_heads"], inp["num_q_heads"],
+                                             inp["head_dim"], 16, **kw),
+           make, _counters, _hip_state, fused_call=fused)
+    if name in ("lazy_m3", "fixed_r3", "cfg1", "cfg1_mixed"):
+        assert calls, (name, "no reuse step took the folded path")
