@@ -214,15 +214,15 @@ def step_bytes(kind, accept, cfg, W, budget):
 def run_e2e(name, cfg, n_layers, args, dev, hot_shift, sink_shift):
     """Whole decode steps through the decode driver (the reference
     harness's per-layer protocol with appends): eager, with graph replay of
-    the reuse steps, and eager with each reuse step's append folded into its
-    decode launch; inputs of each step made before its timing."""
+    the reuse steps, and both again with each reuse step's append folded
+    into its decode launch; inputs of each step made before its timing."""
     import torch
     from cvsa.backend import CVSABackend
     from cvsa.runtime.decode_driver import DecodeDriver, SyntheticDecodeLayers
     out = {"layers": n_layers, "protocol": "per layer: append_tokens_kv, backend call, "
            "step_done; synchronised end-to-end step timing (latency_benchmark.py:478-520)"}
-    for key in ("eager", "graphs", "eager_fused_append"):
-        graphs = key == "graphs"
+    for key in ("eager", "graphs", "eager_fused_append", "graphs_fused_append"):
+        graphs = key.startswith("graphs")
         layers = SyntheticDecodeLayers(
             n_layers, cfg["B"], cfg["H_q"], cfg["H_kv"], D, cfg["ctx"],
             max_new_tokens=args.warmup + args.steps + 1, seed=2000 + int(name[3]), device=dev,
@@ -235,7 +235,7 @@ def run_e2e(name, cfg, n_layers, args, dev, hot_shift, sink_shift):
                               coverage_threshold=0.9, selector=cfg["selector"],
                               light_normalizer=cfg["light_normalizer"], **sched)
         res = DecodeDriver(backend, layers, graphs=graphs,
-                           fuse_append=key == "eager_fused_append").run(args.steps, args.warmup)
+                           fuse_append=key.endswith("fused_append")).run(args.steps, args.warmup)
         out[key] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()
                     if k != "per_step_ms"}
         out[key]["per_step_ms"] = [round(x, 3) for x in res["per_step_ms"]]

@@ -109,6 +109,14 @@ struct AppendArgs {
   const uint16_t *k_new, *v_new;  // [B, H_kv, D] rows, new_sb elements apart
   int64_t new_sb;
   int32_t *block_tables, *ctx_lens, *pages_allocated;  // updated by the append
+  int max_pages;  // block-table width W
+  // The slots in device memory (written before the launch, e.g. by a copy
+  // that a captured graph replays), or NULL: the slots are slot[].  The host
+  // checks slot[] before the launch; device slots are checked here: one out
+  // of range (context length outside [0, 16 W), a new block outside
+  // [-1, num_blocks), or a new block not at a page start) appends nothing
+  // and leaves that sequence's outputs undefined.
+  const int2 *slot_dev;
   int2 slot[kMaxAppendSeqs];  // (context length before the append, new block or -1)
 };
 
@@ -838,11 +846,13 @@ __global__ __launch_bounds__(NW * kWave) void listed_append_kernel(const DecodeA
   const int split = blockIdx.x, bh = blockIdx.y;
   const int b = bh / a.H_kv;
   const int h = bh - b * a.H_kv;
-  const int2 sl = app.slot[b];  // workgroup-uniform
+  const int2 sl = app.slot_dev != nullptr ? app.slot_dev[b] : app.slot[b];  // uniform
+  const bool ok = sl.x >= 0 && sl.x < app.max_pages * kPageTokens && sl.y >= -1 &&
+                  sl.y < a.num_blocks && (sl.y < 0 || (sl.x & 15) == 0);
   NewToken nt;
-  nt.page = sl.x >> 4;
-  nt.off = sl.x & 15;
-  nt.new_blk = sl.y;
+  nt.page = ok ? sl.x >> 4 : -1;
+  nt.off = ok ? sl.x & 15 : kPageTokens - 1;  // not ok: context length 0
+  nt.new_blk = ok ? sl.y : -1;
   const int64_t row = (int64_t)b * app.new_sb + (int64_t)h * Engine::kD;
   nt.k = app.k_new + row;
   nt.v = app.v_new + row;
@@ -852,7 +862,7 @@ __global__ __launch_bounds__(NW * kWave) void listed_append_kernel(const DecodeA
   // Split 0's wave 0 appends: lanes 0-15 copy the head's K row, lanes 16-31
   // its V row, 16 bytes each.  Their loads are requested with the walk's
   // first ones and the stores wait until the walk is done.
-  const bool writer = split == 0 && wave == 0;  // uniform
+  const bool writer = ok && split == 0 && wave == 0;  // uniform
   int blk = -1;
   uint4 x = make_uint4(0u, 0u, 0u, 0u);
   if (writer) {

@@ -363,8 +363,11 @@ extern "C" int cvsa_sparse_decode_append(
     const int32_t *n_per_head, int32_t max_selected, int32_t B, int32_t H_q, int32_t H_kv,
     int32_t D, int32_t block_size, int32_t W, void *out, int32_t out_dtype, int64_t *work,
     void *workspace, size_t workspace_bytes, const uint16_t *k_new, const uint16_t *v_new,
-    int64_t new_stride_b, int32_t *pages_allocated, const int32_t *slots, void *stream) {
+    int64_t new_stride_b, int32_t *pages_allocated, const int32_t *slots,
+    const int32_t *slots_dev, void *stream) {
   const char *name = "sparse_decode_append";
+  CVSA_REQUIRE((slots == nullptr) != (slots_dev == nullptr), CVSA_ERR_INVALID,
+               "%s: exactly one of slots (host) and slots_dev (device) is required", name);
   CVSA_REQUIRE(k_new && v_new && pages_allocated && page_indices, CVSA_ERR_INVALID,
                "%s: null pointer argument", name);
   CVSA_REQUIRE(((uintptr_t)k_new & 15) == 0 && ((uintptr_t)v_new & 15) == 0 &&
@@ -386,13 +389,19 @@ extern "C" int cvsa_sparse_decode_append(
   if (rc != CVSA_OK) return rc;
   if ((rc = check_workspace(name, workspace, workspace_bytes, need)) != CVSA_OK) return rc;
   int next_free = 0;
-  if ((rc = check_append_slots(name, slots, B, block_size, W, num_blocks, next_free)) !=
-      CVSA_OK)
+  if (slots != nullptr &&
+      (rc = check_append_slots(name, slots, B, block_size, W, num_blocks, next_free)) !=
+          CVSA_OK)
     return rc;
   const int G = H_q / H_kv;
   hipStream_t st = (hipStream_t)stream;
-  if (D != 128 || block_size != kPageTokens || G > kMaxGroup || B > kMaxAppendSeqs ||
-      p.streamk) {
+  const bool one_launch = D == 128 && block_size == kPageTokens && G <= kMaxGroup &&
+                          B <= kMaxAppendSeqs && !p.streamk;
+  CVSA_REQUIRE(one_launch || slots_dev == nullptr, CVSA_ERR_UNSUPPORTED,
+               "%s: device slots need the one-launch form (D = 128, block_size 16, "
+               "H_q / H_kv <= %d, B <= %d)",
+               name, kMaxGroup, kMaxAppendSeqs);
+  if (!one_launch) {
     if ((rc = cvsa_append_kv(k_new, v_new, new_stride_b, k_cache, v_cache, num_blocks,
                              block_tables, bt_stride_b, W, context_lens, pages_allocated, 0, B,
                              next_free, H_kv, D, block_size, stream)) != CVSA_OK)
@@ -406,7 +415,10 @@ extern "C" int cvsa_sparse_decode_append(
   app.block_tables = block_tables;
   app.ctx_lens = context_lens;
   app.pages_allocated = pages_allocated;
-  for (int b = 0; b < B; ++b) app.slot[b] = make_int2(slots[2 * b], slots[2 * b + 1]);
+  app.max_pages = W;
+  app.slot_dev = reinterpret_cast<const int2 *>(slots_dev);
+  if (slots != nullptr)
+    for (int b = 0; b < B; ++b) app.slot[b] = make_int2(slots[2 * b], slots[2 * b + 1]);
   bind_workspace(a, workspace, need);
   a.q_group = G;
   a.q_off = 0;

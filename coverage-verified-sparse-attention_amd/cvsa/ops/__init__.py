@@ -761,16 +761,21 @@ class StepPlan:
         return out
 
     def run_reuse_append(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
-                         pages_allocated: torch.Tensor, slots) -> torch.Tensor:
+                         pages_allocated: torch.Tensor, slots=None,
+                         slots_dev: Optional[torch.Tensor] = None) -> torch.Tensor:
         """A reuse step with the step's token append folded in
         (cvsa_step_plan_run_append): k_new / v_new [B, H_kv, D] contiguous
         bf16, pages_allocated the int32 [B] allocation counts on the device,
-        slots the host int32 array of SequenceKVManager.fused_append_slots.
-        Writes the plan's caches, block table and context lengths."""
+        slots the host int32 array of SequenceKVManager.fused_append_slots,
+        or slots_dev the same values in a contiguous int32 [B, 2] device
+        tensor (for a launch a captured graph replays).  Writes the plan's
+        caches, block table and context lengths."""
+        if (slots is None) == (slots_dev is None):
+            raise ValueError("run_reuse_append: give exactly one of slots and slots_dev")
         out = torch.empty(self.out_shape, device=self.dev, dtype=self.out_dtype)
         check(_lib.load().cvsa_step_plan_run_append(
             self._h, q.data_ptr(), out.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
-            k_new.stride(0), pages_allocated.data_ptr(), slots, self.stream),
+            k_new.stride(0), pages_allocated.data_ptr(), slots, _ptr(slots_dev), self.stream),
             "step_plan_run_append")
         return out
 
@@ -823,7 +828,11 @@ def sparse_decode_append(q, k_cache, v_cache, block_tables, context_lens, page_i
 
     ``slots``: a host sequence of 2 * B int32, (context length before the
     append, block the append allocates or -1) per sequence, as
-    SequenceKVManager.fused_append_slots builds them.  block_tables,
+    SequenceKVManager.fused_append_slots builds them, or the same values in a
+    contiguous int32 [B, 2] tensor on the device (the one-launch shapes
+    only: D = 128, 16-token pages, at most 16 query heads per KV head and
+    256 sequences; the launch checks them, and a sequence whose slot is out
+    of range appends nothing and gets an undefined output).  block_tables,
     context_lens and pages_allocated (contiguous int32) and the caches are
     updated in place.  Returns the normalised output [B, H_q, D] in q.dtype.
     """
@@ -846,9 +855,17 @@ def sparse_decode_append(q, k_cache, v_cache, block_tables, context_lens, page_i
             or not (k_new.is_contiguous() and v_new.is_contiguous())):
         raise ValueError(f"sparse_decode_append: k_new / v_new must be contiguous bfloat16 "
                          f"{shape}")
-    if len(slots) != 2 * B:
+    slot_arr = slot_dev = None
+    if isinstance(slots, torch.Tensor):
+        if (slots.dtype != torch.int32 or tuple(slots.shape) != (B, 2)
+                or not slots.is_contiguous() or slots.device != dev):
+            raise ValueError(f"sparse_decode_append: device slots must be a contiguous int32 "
+                             f"({B}, 2) tensor on {dev}")
+        slot_dev = slots
+    elif len(slots) != 2 * B:
         raise ValueError(f"sparse_decode_append: {2 * B} slot entries expected")
-    slot_arr = slots if isinstance(slots, ctypes.Array) else (ctypes.c_int32 * (2 * B))(*slots)
+    else:
+        slot_arr = slots if isinstance(slots, ctypes.Array) else (ctypes.c_int32 * (2 * B))(*slots)
     W = block_tables.shape[1]
     L = _lib.load()
     need = L.cvsa_decode_workspace_bytes(B, H_q, num_kv_heads, D, k, W, 0)
@@ -862,7 +879,7 @@ def sparse_decode_append(q, k_cache, v_cache, block_tables, context_lens, page_i
         context_lens.data_ptr(), pi.data_ptr(), pi.stride(0), nph.data_ptr(), k, B, H_q,
         num_kv_heads, D, block_size, W, out.data_ptr(), _DTYPE_CODE[q.dtype], _ptr(work),
         _ptr(ws), 0 if ws is None else ws.numel(), k_new.data_ptr(), v_new.data_ptr(),
-        k_new.stride(0), pages_allocated.data_ptr(), slot_arr, _stream(dev)),
+        k_new.stride(0), pages_allocated.data_ptr(), slot_arr, _ptr(slot_dev), _stream(dev)),
         "sparse_decode_append")
     return out
 

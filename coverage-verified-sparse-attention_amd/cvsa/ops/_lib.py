@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parents[1] / "libcvsa_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 CVSA_OK = 0
 CVSA_ERR_INVALID = -1
@@ -87,7 +87,7 @@ SIGNATURES = {
         _p, _i64, _i64, _p, _p, _i64, _p, _i64, _p,
         _p, _i64, _p, _i32,
         _i32, _i32, _i32, _i32, _i32, _i32,
-        _p, _i32, _p, _p, _sz, _p, _p, _i64, _p, _p, _p]),
+        _p, _i32, _p, _p, _sz, _p, _p, _i64, _p, _p, _p, _p]),
     "cvsa_dense_decode": (ctypes.c_int, [
         _p, _i64, _i64, _p, _p, _i64, _p, _i64, _p,
         _i32, _i32, _i32, _i32, _i32, _i32,
@@ -114,7 +114,7 @@ SIGNATURES = {
     "cvsa_step_workspace_bytes": (_sz, [ctypes.POINTER(StepDesc)]),
     "cvsa_step_plan_create": (ctypes.c_int, [ctypes.POINTER(StepDesc), ctypes.POINTER(_p)]),
     "cvsa_step_plan_run": (ctypes.c_int, [_p, _i32, _p, _p, _p]),
-    "cvsa_step_plan_run_append": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _p, _p, _p]),
+    "cvsa_step_plan_run_append": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _p, _p, _p, _p]),
     "cvsa_step_plan_destroy": (None, [_p]),
 }
 

@@ -24,6 +24,13 @@ every layer would leave the GPU idle while the host issues every append and
 checks every plan first).  Replays repeat the calls' host bookkeeping
 (``note_replayed_reuse``, ``step_done``), so schedule, counters and tracing
 state match an eager run; outputs are bit-identical to it.
+
+With ``fuse_append=True`` eager steps hand each layer's append to
+``CVSABackend.call_with_append``, which folds it into a reuse step's decode
+launch; with ``graphs=True`` as well, a chunk of such reuse steps is one
+replay of its fused launches, which read the step's new rows from static
+buffers and its append slots (block ids from the host allocator) from a
+device buffer written just before the replay.
 """
 from __future__ import annotations
 
@@ -31,6 +38,7 @@ import statistics
 import time
 from typing import List, Optional
 
+import numpy as np
 import torch
 
 from ..synthetic import jitter_query, make_paged_inputs
@@ -111,6 +119,19 @@ class DecodeDriver:
         self._graphs = {}   # chunk index -> (graph, plans, output buffers)
         self.replays = 0
         self.captures = 0
+        # Graphs with folded appends: the new rows in static buffers and each
+        # chunk's append slots copied to the device before its replay (the
+        # slots change every step; a captured launch's arguments do not).
+        # Only the one-launch shapes of cvsa_sparse_decode_append take device
+        # slots; other chunks run eagerly.
+        self._fold_graphs = (self.graphs and self.fuse_append and layers.head_dim == 128
+                             and layers.block_size == 16 and B <= 256
+                             and layers.num_q_heads // layers.num_kv_heads <= 16)
+        if self._fold_graphs:
+            shape = (L, B, layers.num_kv_heads, layers.head_dim)
+            self.k_static = torch.empty(shape, dtype=torch.bfloat16, device=layers.device)
+            self.v_static = torch.empty(shape, dtype=torch.bfloat16, device=layers.device)
+            self._slots = {}  # chunk index -> [device slots, pinned slots, event]
 
     # ------------------------------------------------------------ one step
     def _append(self, k, v, layers):
@@ -120,6 +141,18 @@ class DecodeDriver:
     def _chunks(self):
         L, c = self.layers.num_layers, self.graph_chunk
         return [range(i, min(L, i + c)) for i in range(0, L, c)]
+
+    def static_inputs(self):
+        """The graph-mode input buffers (q [L, B, H_q, D], and with folded
+        appends k / v [L, B, H_kv, D]; None where the mode has none).  A step
+        given these tensors themselves reads them in place: a caller that
+        makes its inputs there (as a captured model's projections would)
+        saves the per-step copies into them."""
+        if not self.graphs:
+            return None, None, None
+        if self._fold_graphs:
+            return self.q_static, self.k_static, self.v_static
+        return self.q_static, None, None
 
     def _eager(self, q, k=None, v=None, layers=None) -> List[torch.Tensor]:
         """Per layer: the append of the new token (when k / v are given), the
@@ -166,16 +199,90 @@ class DecodeDriver:
         caller.wait_stream(self.stream)
         return outs
 
+    def _stage_slots(self, ci, chunk):
+        """The append slots of every layer of a chunk (host mirrors) into the
+        chunk's pinned slot buffer, which the chunk's graph copies to the
+        device as its first node; the buffer is rewritten only once the
+        previous replay of the chunk is done with it.  Returns the slot
+        buffers and the mirrors' commit functions."""
+        B = self.layers.batch
+        st = self._slots.get(ci)
+        if st is None:
+            dev = torch.empty(len(chunk), B, 2, dtype=torch.int32, device=self.layers.device)
+            pin = torch.empty(len(chunk), B, 2, dtype=torch.int32, pin_memory=True)
+            st = self._slots[ci] = [dev, pin, torch.cuda.Event(), False]
+        dev, pin, done, used = st
+        if used:
+            done.synchronize()
+        host = pin.numpy()
+        commits = []
+        for j, l in enumerate(chunk):
+            slots, commit = self.layers.managers[l].fused_append_slots()
+            host[j] = np.frombuffer(slots, dtype=np.int32).reshape(B, 2)
+            commits.append(commit)
+        return dev, pin, done, commits
+
+    def _fold_graph_step(self, k, v) -> List[torch.Tensor]:
+        """Graph mode with folded appends: a chunk whose every layer is a
+        plan-driven reuse step with appendable rows replays (or captures) its
+        fused append-and-decode launches, which read the slots staged for
+        this step; other chunks run eagerly through call_with_append."""
+        if k is not self.k_static:
+            self.k_static.copy_(k)
+        if v is not self.v_static:
+            self.v_static.copy_(v)
+        L = self.layers.num_layers
+        managers = self.layers.managers
+        outs = []
+        for ci, chunk in enumerate(self._chunks()):
+            plans = self._plans_now(chunk)
+            if plans is not None and not all(
+                    managers[l].fusable_rows(self.k_static[l], self.v_static[l]) for l in chunk):
+                plans = None
+            if plans is None:
+                outs += self._eager(self.q_static, self.k_static, self.v_static, layers=chunk)
+                continue
+            slots_dev, slots_pin, done, commits = self._stage_slots(ci, chunk)
+            cached = self._graphs.get(ci)
+            if cached is None or any(a is not b for a, b in zip(plans, cached[1])):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=self.stream):
+                    slots_dev.copy_(slots_pin, non_blocking=True)
+                    chunk_outs = [
+                        p.run_reuse_append(self.q_static[l], self.k_static[l], self.v_static[l],
+                                           managers[l]._pages_allocated_dev,
+                                           slots_dev=slots_dev[j])
+                        for j, (p, l) in enumerate(zip(plans, chunk))]
+                graph.replay()
+                self._graphs[ci] = (graph, plans, chunk_outs)
+                self.captures += 1
+            else:
+                cached[0].replay()
+                self.replays += 1
+                chunk_outs = cached[2]
+            done.record(self.stream)
+            self._slots[ci][3] = True
+            for commit in commits:
+                commit()
+            for l in chunk:
+                self.backend.note_replayed_reuse(l)
+                self.backend.step_done(l, L)
+            outs += chunk_outs
+        return outs
+
     def _step(self, q, k, v) -> List[torch.Tensor]:
         with torch.cuda.stream(self.stream):
             if not self.graphs:
                 return self._eager(q, k, v)
+            if q is not self.q_static:
+                self.q_static.copy_(q)
+            if self._fold_graphs:
+                return self._fold_graph_step(k, v)
             # Graph mode, chunk by chunk: the chunk's appends, then its
             # calls -- replayed when every layer of the chunk maps to the
             # plans its graph was captured with, else captured (host
             # bookkeeping now, kernels at the replay) or, when a layer takes
             # another path, made eagerly.
-            self.q_static.copy_(q)
             L = self.layers.num_layers
             outs = []
             for ci, chunk in enumerate(self._chunks()):
@@ -209,9 +316,13 @@ class DecodeDriver:
         a synchronisation before each step.  Inputs of every step are made
         before its timing starts."""
         times, host = [], []
+        static = self.static_inputs()
         for i in range(warmup + steps):
             s = first_step + i
             q, k, v = self.layers.step_inputs(s)
+            # Graph modes read their inputs from fixed buffers: the inputs
+            # are made there, as a captured model's projections would.
+            q, k, v = [t if buf is None else buf.copy_(t) for t, buf in zip((q, k, v), static)]
             torch.cuda.synchronize()
             if i == warmup and hasattr(self.backend, "_accept_counts"):
                 self.backend._accept_counts = 0

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 10
+#define CVSA_ABI_VERSION 11
 
 enum {
   CVSA_OK = 0,
@@ -274,9 +274,14 @@ int cvsa_sparse_decode_noalloc(const uint16_t *q, int64_t q_stride_b,
  * slots[2b] / block_size is new: slots[2b] % block_size == 0 and not yet
  * allocated; the r-th such sequence in increasing b takes next_free + r), or
  * -1.  Inconsistent slots return CVSA_ERR_INVALID before anything is
- * enqueued.  block_tables, context_lens and pages_allocated are updated as
- * cvsa_append_kv does; the other arguments, outputs and errors are those of
- * cvsa_sparse_decode (normalised output only).
+ * enqueued.  slots_dev: the same 2 * B int32 in device memory instead, for a
+ * launch that a captured graph replays (the slots change every step, the
+ * kernel arguments of a captured launch do not); they are not checked, and
+ * only the one-launch shapes take them (CVSA_ERR_UNSUPPORTED otherwise).
+ * Exactly one of slots and slots_dev is given.  block_tables, context_lens
+ * and pages_allocated are updated as cvsa_append_kv does; the other
+ * arguments, outputs and errors are those of cvsa_sparse_decode (normalised
+ * output only).
  */
 int cvsa_sparse_decode_append(const uint16_t *q, int64_t q_stride_b,
                               int64_t q_stride_h, uint16_t *k_cache,
@@ -291,7 +296,7 @@ int cvsa_sparse_decode_append(const uint16_t *q, int64_t q_stride_b,
                               size_t workspace_bytes, const uint16_t *k_new,
                               const uint16_t *v_new, int64_t new_stride_b,
                               int32_t *pages_allocated, const int32_t *slots,
-                              void *stream);
+                              const int32_t *slots_dev, void *stream);
 
 /*
  * Dense paged decode over every valid page.  Replaces
@@ -533,7 +538,8 @@ int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint16_t *q, vo
 int cvsa_step_plan_run_append(cvsa_step_plan *plan, const uint16_t *q, void *out,
                               const uint16_t *k_new, const uint16_t *v_new,
                               int64_t new_stride_b, int32_t *pages_allocated,
-                              const int32_t *slots, void *stream);
+                              const int32_t *slots, const int32_t *slots_dev,
+                              void *stream);
 void cvsa_step_plan_destroy(cvsa_step_plan *plan);
 
 #ifdef __cplusplus

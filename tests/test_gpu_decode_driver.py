@@ -55,7 +55,7 @@ ORACLE_SHAPE = dict(num_layers=3, batch=2, num_q_heads=32, num_kv_heads=8, head_
                     hot_heads=[0, 2, 5, 7], n_hot=6, hot_shift=9.0)
 
 
-@pytest.mark.parametrize("mode", ["eager", "graphs", "fused"])
+@pytest.mark.parametrize("mode", ["eager", "graphs", "fused", "fused_graphs"])
 @pytest.mark.parametrize("kw", [dict(lazy=True, check_interval=3),
                                 dict(lazy=False, reuse_interval=2)])
 def test_driver_matches_oracle_backend(gpu, mode, kw):
@@ -70,8 +70,8 @@ def test_driver_matches_oracle_backend(gpu, mode, kw):
     backend = CVSABackend(**cfg)
     oracle = OracleCVSABackend(**cfg)
     state = _OracleLayers(layers)
-    graphs = mode == "graphs"
-    driver = DecodeDriver(backend, layers, graphs=graphs, fuse_append=mode == "fused")
+    graphs = mode in ("graphs", "fused_graphs")
+    driver = DecodeDriver(backend, layers, graphs=graphs, fuse_append=mode.startswith("fused"))
     kinds = set()
     for step in range(12):
         q, k, v = layers.step_inputs(step)
@@ -252,3 +252,53 @@ def test_fused_append_rejects_inconsistent_slots(gpu):
     torch.cuda.synchronize()
     assert torch.equal(mgr.context_lens, before[0]) and torch.equal(mgr.block_tables, before[1])
     assert torch.equal(cache.k_cache[:4], before[2])
+
+
+@pytest.mark.parametrize("kw,in_place", [(dict(lazy=True, check_interval=3), False),
+                                         (dict(lazy=False, reuse_interval=2), False),
+                                         (dict(lazy=True, check_interval=4), True)])
+def test_fused_graph_replay_equals_eager(gpu, kw, in_place):
+    """Graph replay of chunks of folded append-and-decode launches (device
+    slots staged before each replay) against the eager separate append and
+    call, step after step, with sequences crossing page boundaries: outputs,
+    masks, caches, tables, lengths, allocation counts and statistics equal.
+    With in_place the graph driver's inputs are made in its static buffers."""
+    shape = dict(SHAPE, context_len=[3000, 1792], max_new_tokens=30)
+    runs = []
+    for graphs, fuse in ((False, False), (True, True)):
+        layers = SyntheticDecodeLayers(device=gpu, **shape)
+        backend = CVSABackend(num_kv_heads=8, num_q_heads=32, head_dim=128, block_size=16,
+                              num_layers=SHAPE["num_layers"], budget_pct=0.2,
+                              coverage_threshold=0.9, **kw)
+        runs.append((layers, backend, DecodeDriver(backend, layers, graphs=graphs,
+                                                   graph_chunk=3 if in_place else 2,
+                                                   fuse_append=fuse)))
+    (la, ba, da), (lb, bb, db) = runs
+    for step in range(24):
+        q, k, v = la.step_inputs(step)
+        out_a = [o.clone() for o in da.step(q, k, v)]
+        if in_place:
+            qs, ks, vs = db.static_inputs()
+            qs.copy_(q), ks.copy_(k), vs.copy_(v)
+            out_b = [o.clone() for o in db.step(qs, ks, vs)]
+        else:
+            out_b = [o.clone() for o in db.step(q, k, v)]
+        for layer, (a, b) in enumerate(zip(out_a, out_b)):
+            assert torch.equal(a, b), (step, layer)
+        for layer in range(SHAPE["num_layers"]):
+            ma, mb = ba._last_accept_mask.get(layer), bb._last_accept_mask.get(layer)
+            assert (ma is None) == (mb is None), (step, layer)
+            if ma is not None:
+                assert torch.equal(ma, mb), (step, layer)
+        for ma, mb in zip(la.managers, lb.managers):
+            assert torch.equal(ma.context_lens, mb.context_lens), step
+            assert torch.equal(ma.block_tables, mb.block_tables), step
+            assert torch.equal(ma._pages_allocated_dev, mb._pages_allocated_dev), step
+            assert ma._ctx_host == mb._ctx_host and ma._pages_allocated == mb._pages_allocated
+    torch.cuda.synchronize()
+    for ca, cb in zip(la.caches, lb.caches):
+        assert torch.equal(ca.k_cache, cb.k_cache) and torch.equal(ca.v_cache, cb.v_cache)
+        assert ca._next_free == cb._next_free
+    assert db.captures >= 1 and db.replays >= 6, (db.captures, db.replays)
+    assert ba._step == bb._step
+    assert ba.get_stats() == bb.get_stats()

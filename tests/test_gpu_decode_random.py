@@ -230,6 +230,57 @@ def test_random_decode_append(gpu, seed, shape):
             assert err < 2e-2, (seed, shape, b, h, err)
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_decode_append_device_slots(gpu, seed):
+    """The slots of cvsa_sparse_decode_append read from device memory (the
+    form a captured graph replays) against the same slots from the host:
+    outputs, caches, tables, lengths and allocation counts identical."""
+    inp, bt, alloc, pi, nph, kn, vn, ctx = _append_case(seed, gpu, 128, 16, [4, 1, 16, 7][seed])
+    H, G = inp.k_cache.shape[2], inp.q.shape[1] // inp.k_cache.shape[2]
+    slots = _slots(ctx, alloc, inp.used_blocks, 16)
+    runs = []
+    for sl in (slots, torch.tensor(slots, dtype=torch.int32, device=gpu).view(-1, 2)):
+        st = [inp.k_cache.clone(), inp.v_cache.clone(), bt.clone(), inp.context_lens.clone(),
+              alloc.clone()]
+        out = ops.sparse_decode_append(inp.q, *st[:4], pi, nph, kn, vn, st[4], sl, H, G, 16)
+        runs.append([out] + st)
+    torch.cuda.synchronize()
+    for a, b in zip(*runs):
+        assert torch.equal(a, b), seed
+
+
+def test_decode_append_device_slots_out_of_range(gpu):
+    """Device slots the launch cannot take (context length past the table,
+    a new block past the cache or not at a page start, a negative length)
+    append nothing for their sequence; the other sequences are unaffected."""
+    inp, bt, alloc, pi, nph, kn, vn, ctx = _append_case(5, gpu, 128, 16, 4)
+    B, H, G = len(ctx), inp.k_cache.shape[2], 4
+    slots = _slots(ctx, alloc, inp.used_blocks, 16)
+    good = [inp.k_cache.clone(), inp.v_cache.clone(), bt.clone(), inp.context_lens.clone(),
+            alloc.clone()]
+    want = ops.sparse_decode_append(inp.q, *good[:4], pi, nph, kn, vn, good[4], slots, H, G, 16)
+    W, nb = bt.shape[1], inp.k_cache.shape[0]
+    bad_forms = [(W * 16, -1), (-1, -1), (ctx[0] // 16 * 16, nb), (ctx[0] // 16 * 16 + 1, 0)]
+    for bad in bad_forms:
+        sl = list(slots)
+        sl[0], sl[1] = bad
+        st = [inp.k_cache.clone(), inp.v_cache.clone(), bt.clone(), inp.context_lens.clone(),
+              alloc.clone()]
+        out = ops.sparse_decode_append(inp.q, *st[:4], pi, nph, kn, vn, st[4],
+                                       torch.tensor(sl, dtype=torch.int32,
+                                                    device=gpu).view(-1, 2), H, G, 16)
+        torch.cuda.synchronize()
+        assert torch.equal(st[3][0], inp.context_lens[0]), bad
+        assert torch.equal(st[4][0], alloc[0]) and torch.equal(st[2][0], bt[0]), bad
+        if B > 1:
+            assert torch.equal(out[1:], want[1:]), bad
+            assert torch.equal(st[3][1:], good[3][1:]) and torch.equal(st[2][1:], good[2][1:])
+        # sequence 0's rows of the cache are those before the append
+        blocks = bt[0, :-(-ctx[0] // 16)].long()
+        assert torch.equal(st[0][blocks], inp.k_cache[blocks]), bad
+        assert torch.equal(st[1][blocks], inp.v_cache[blocks]), bad
+
+
 def test_decode_append_large_batch(gpu):
     """More sequences than the one-launch form takes (B = 260 > 256): the
     entry point appends and decodes in two launches with the same results."""
