@@ -62,6 +62,23 @@ __device__ __forceinline__ uint4 stream_load16(const uint16_t *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// stream_load16 of byte voff + soff of the `bytes`-byte region at `base`
+// (base and soff the same in every lane of the wave).  A lane whose voff is
+// at or past `bytes` (kRegionSkip added to an in-region offset) gets 16 zero
+// bytes and makes no memory access: the buffer bounds check drops it.
+constexpr uint32_t kRegionSkip = 0x40000000u;
+__device__ __forceinline__ uint4 region_load16(const void *base, uint32_t bytes, uint32_t voff,
+                                               uint32_t soff) {
+  constexpr int kRsrcWord3 = 0x00020000;  // 32-bit data format, raw
+  constexpr int kCpolNontemporal = 2;     // nt
+  typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kRsrcWord3);
+  const v4u_t v = __builtin_bit_cast(
+      v4u_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kCpolNontemporal));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Sum of the 8 products of two 16-byte bf16 vectors, accumulated onto acc.
 __device__ __forceinline__ float dot8_bf16(const uint4 &a, const uint4 &b, float acc) {
   acc = dot2_bf16(a.x, b.x, acc);

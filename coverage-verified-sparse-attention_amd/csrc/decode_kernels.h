@@ -95,6 +95,11 @@ struct DecodeArgs {
   // [0] != 0 predicts that the check keeps its selection, [1] records
   // whether the speculative listed decode ran (and wrote the outputs).
   int32_t *spec_state;
+  // The speculative decode also writes the page scores of the pages it
+  // walks into spec_scores [B * H_kv, W] (or NULL), as the page scoring
+  // would (q_rep the group mean of q_group heads times inv_g).
+  float *spec_scores;
+  float inv_g;
 };
 
 // A reuse step's token append folded into its listed decode
@@ -451,6 +456,7 @@ struct MfmaEngine {
   static_assert(D == 64 || D == 128 || D == 256, "head dimension");
   static_assert(TS == 0 || TS == -1, "tile shift: 0 (16-token pages) or -1 (from the args)");
   static constexpr int kD = D;
+  static constexpr int kTileShift = TS;  // -1: from the args
   // Tiles per page = 1 << tshift(a): compiled in for 16-token pages.
   static __device__ __forceinline__ int tshift(const DecodeArgs &a) { return TS >= 0 ? TS : a.ts; }
   static constexpr int NK = D / 32;         // S = K Q^T MFMAs (32 dimensions each)
@@ -525,6 +531,39 @@ struct MfmaEngine {
       pg.v[i] = stream_load16(t == newrow ? v_row + 8 * (lane % LPR)
                                           : vp + voff + RPL * i * row_stride);
     }
+  }
+
+  // Page score of the walk's KV head from the page's keys, bit for bit the
+  // page scoring's (score_group_wave): lane (c16, grp) holds dimensions
+  // 32 kk + 8 grp .. +8 of token c16, the scorer's segment s = 4 kk + grp,
+  // so the scorer's pairwise sum over s (bit 0, 1, 2, 3 of s in turn) is
+  // the partner at lane ^ 16, at lane ^ 32, then the kk pairs; the maximum
+  // over the ntok valid tokens follows.  qrep: the 16 segments of q_rep.
+  __device__ __forceinline__ float page_score(const Page &pg, int ntok,
+                                              const uint4 *qrep) const {
+    static_assert(NK == 4, "segment mapping of the 128-dimension rows");
+    const int grp = lane >> 4;
+    float x[NK];
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) x[kk] = dot8_bf16(pg.k[kk], qrep[4 * kk + grp], 0.f);
+    float a, b;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
+      xchg16(x[kk], a, b);
+      x[kk] = a + b;
+    }
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
+      xchg32(x[kk], a, b);
+      x[kk] = a + b;
+    }
+    const float sc = ((x[0] + x[1]) + (x[2] + x[3])) * scale;
+    float m = (lane & 15) < ntok ? sc : -INFINITY;
+    m = fmaxf(m, dpp_f<kDppQuadXor1>(m));
+    m = fmaxf(m, dpp_f<kDppQuadXor2>(m));
+    m = fmaxf(m, dpp_f<kDppRowHalfMirror>(m));
+    m = fmaxf(m, dpp_f<kDppRowMirror>(m));
+    return m + 0.f;
   }
 
   __device__ __forceinline__ void consume(Page &pg, int ntok, Lds &lds) {
@@ -742,10 +781,14 @@ __device__ __forceinline__ void listed_first_pages(const DecodeArgs &a, int spli
 // context length is nt's page * 16 + row + 1 (16-token pages), and nt's page
 // reads that row from nt's rows (Engine::fetch_new) and, when the append
 // allocates the page, its block from nt.
-template <int G, class Engine, int NW, int PD, bool APP = false>
+// With SCORE and a.spec_scores, the walk also writes the page score of
+// every page it walks (Engine::page_score; qrep: this wave's LDS copy of the
+// 16 q_rep segments, 16-token pages).
+template <int G, class Engine, int NW, int PD, bool APP = false, bool SCORE = false>
 __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int bh, int spec_lp,
                                             int spec_phys, WalkLds<G, Engine, NW> &L,
-                                            const NewToken &nt = NewToken()) {
+                                            const NewToken &nt = NewToken(),
+                                            uint4 *qrep = nullptr) {
   using Page = typename Engine::Page;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -764,15 +807,27 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
 
   Engine eng;
   eng.init(a, b, h, lane, s_eng_of(L.tail.eng, wave));
+  // Wave-private q_rep: lane < 16 computes segment `lane` (its loads go out
+  // ahead of the first pages') and stores it to LDS just before the first
+  // page score, so no wait for q holds up the first page requests; the LDS
+  // store and the later reads are the same wave's, in order.
+  const bool scoring = SCORE && a.spec_scores != nullptr;  // uniform
+  uint4 qr_own = make_uint4(0u, 0u, 0u, 0u);
+  bool qr_stored = false;
+  if constexpr (SCORE) {
+    if (scoring)
+      qr_own = group_mean_q(a.q, a.q_sb, a.q_sh, b, h, a.q_group, min(lane, 15), a.inv_g);
+  }
   const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * Engine::kD;  // between blocks
   const int npw = max(0, (r1 - r0 - wave + NW - 1) / NW);
   for (int c0 = 0; c0 < npw; c0 += kWave) {
     const int cn = min(kWave, npw - c0);
-    int my_phys = 0, my_ntok = 0, my_new = -1;
+    int my_phys = 0, my_ntok = 0, my_new = -1, my_lt = -1;
     if (lane < cn) {
       const int lt =
           c0 == 0 ? spec_lp : listed_tile(a, idx_row, r0 + wave + NW * (c0 + lane), ts);
       if (lt >= 0 && lt < (a.W << ts)) {
+        my_lt = lt;
         int pt = c0 == 0 ? spec_phys : tile_block(a, b, lt, ts);
         if (APP && lt == nt.page && nt.new_blk >= 0) pt = nt.new_blk;
         if (pt >= 0 && pt < (a.num_blocks << ts)) {
@@ -805,7 +860,20 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
       for (int u = 0; u < PD; ++u) {
         const int slot = (u + PD - 1) % PD;  // slot of page j+u+PD-1
         nt[slot] = fetch(min(j + u + PD - 1, cn - 1), pbuf[slot]);
-        if (j + u >= 0 && j + u < cn) eng.consume(pbuf[u], nt[u], s_eng_of(L.tail.eng, wave));
+        if (j + u >= 0 && j + u < cn) {
+          if constexpr (SCORE) {
+            if (scoring) {
+              if (!qr_stored) {
+                if (lane < 16) qrep[lane] = qr_own;
+                qr_stored = true;
+              }
+              const float sc = eng.page_score(pbuf[u], nt[u], qrep);
+              const int lt = __builtin_amdgcn_readlane(my_lt, j + u);
+              if (lane == 0 && lt >= 0) a.spec_scores[(int64_t)bh * a.W + lt] = sc;
+            }
+          }
+          eng.consume(pbuf[u], nt[u], s_eng_of(L.tail.eng, wave));
+        }
       }
     }
   }
@@ -888,6 +956,9 @@ __global__ __launch_bounds__(NW * kWave) void listed_append_kernel(const DecodeA
 
 // 16-token tiles per scoring wave of the fused launch below.
 constexpr int kSpecScorePPW = 8;
+// Pages per scoring wave of the fused launch at 16-token pages (one head per
+// wave, score_head_wave).
+constexpr int kSpecHeadPPW = 16;
 
 // A lazy check's page scoring and the speculative listed decode of its
 // cached selection in one launch.  Workgroups [0, n_splits * heads) are the
@@ -895,16 +966,24 @@ constexpr int kSpecScorePPW = 8;
 // n_splits), bit for bit listed_decode_kernel; they run only if
 // spec_state[0] predicts that the check keeps its selection, and workgroup 0
 // records in spec_state[1] whether they ran.  The other workgroups score
-// pages as score_pages_group_kernel<128, ...> does (score_body.h; kSpecScorePPW
-// tiles per wave, workgroup x of sequence b at index n_dec + b * score_gx + x).
-// The parts share no memory: the decode reads the cached selection, which
-// only the check's select-or-keep, launched after this kernel, rewrites.
+// pages (workgroup x of sequence b at index n_dec + b * score_gx + x): at
+// 16-token pages one head and kSpecHeadPPW pages per wave (score_head_wave),
+// else as score_pages_group_kernel<128, ...> (kSpecScorePPW tiles of 4 heads
+// per wave).  With a selection map (s.skip_map) the decode part also writes
+// the page scores of the pages it walks, from the keys it reads anyway, and
+// the scoring part skips them when the decode runs: every page is scored
+// once, with the same bits (the per-token arithmetic is the same).
+// The parts share no memory otherwise: the decode reads the cached
+// selection, which only the check's select-or-keep, launched after this
+// kernel, rewrites.
 // One launch lets the decode's dependent metadata loads and split hand-off
 // overlap the scoring stream without a second stream and its events.
 // Three waves per SIMD (the register budget that allows, 168 VGPRs, holds
 // the decode without spills): 768 workgroups resident instead of 512, so the
 // decode and scoring workgroups of a cfg3 launch all run at once (check
-// step 68.4 -> 64.5 us at cfg3, 82.2 -> 75.5 us at cfg4).
+// step 68.4 -> 64.5 us at cfg3, 82.2 -> 75.5 us at cfg4).  Reading the kept
+// selection's keys once: kept check 64.0 -> 61.1 us at cfg3 (16 pages per
+// scoring wave; 8 and 32 measured 61.2 and 62.0).
 template <int G, class Engine, int NW, int PD>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(3)))
 void score_spec_kernel(const DecodeArgs a,
@@ -912,13 +991,23 @@ void score_spec_kernel(const DecodeArgs a,
                                                                 int score_gx) {
   static_assert(NW == 4, "the scoring part runs four waves per workgroup");
   __shared__ WalkLds<G, Engine, NW> L;
+  __shared__ uint4 s_qrep[NW][16];  // decode part: q_rep per wave
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n_dec = a.n_splits * a.heads;
   const int w = blockIdx.x;
   if (w >= n_dec) {  // uniform
     const int sw = w - n_dec;
-    score_group_wave<128, kSpecScorePPW>(s, a.H_kv, (sw % score_gx) * NW + wave, sw / score_gx);
+    const int gw = (sw % score_gx) * NW + wave, b = sw / score_gx;
+    if constexpr (Engine::kTileShift == 0) {
+      // With a skip map, the pages the speculative decode walks (when it
+      // runs) are scored there.
+      const bool go =
+          s.skip_map != nullptr && __builtin_amdgcn_readfirstlane(a.spec_state[0]) != 0;
+      score_head_wave<kSpecHeadPPW, 4>(s, a.H_kv, gw, b, go);
+    } else {
+      score_group_wave<128, kSpecScorePPW>(s, a.H_kv, gw, b);
+    }
     return;
   }
   const int split = w % a.n_splits;
@@ -928,7 +1017,8 @@ void score_spec_kernel(const DecodeArgs a,
   const int go = __builtin_amdgcn_readfirstlane(a.spec_state[0]);
   if (w == 0 && threadIdx.x == 0) a.spec_state[1] = go;
   if (go == 0) return;  // uniform
-  listed_walk<G, Engine, NW, PD>(a, split, bh, lp, phys, L);
+  listed_walk<G, Engine, NW, PD, false, Engine::kTileShift == 0>(a, split, bh, lp, phys, L,
+                                                                 NewToken(), s_qrep[wave]);
 }
 
 // Effective-budget counters of a verified launch whose heads were all

@@ -542,6 +542,10 @@ bool score_spec_fusable(int32_t H_kv, int32_t D, int32_t G) {
 // into out, run only if spec_state[0] predicts that the check keeps the
 // selection; spec_state[1] records whether it ran).  Effective-budget
 // counters are left to the verified decode.  H_kv must be 4, 8 or 16.
+// With sel_map (the selection's map, select_for_plan) and 16-token pages,
+// a speculative decode also scores the pages it walks, from the keys it
+// reads anyway, and the scoring part skips them: the selection's keys are
+// read once instead of twice, and the scores keep their bits.
 int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h,
                         const uint16_t *k_cache, const uint16_t *v_cache, int64_t num_blocks,
                         const int32_t *block_tables, int64_t bt_stride_b,
@@ -549,8 +553,8 @@ int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_
                         int64_t idx_stride, const int32_t *n_per_head, int32_t max_selected,
                         int32_t B, int32_t H_q, int32_t H_kv, int32_t D, int32_t block_size,
                         int32_t W, float *page_scores, void *out, int32_t out_dtype,
-                        int32_t *spec_state, void *workspace, size_t workspace_bytes,
-                        void *stream) {
+                        int32_t *spec_state, const uint8_t *sel_map, int64_t sel_map_stride,
+                        void *workspace, size_t workspace_bytes, void *stream) {
   const char *name = "score_pages + speculative decode";
   DecodeArgs a = base_args(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
                            block_tables, bt_stride_b, context_lens, nullptr, nullptr, nullptr,
@@ -572,12 +576,25 @@ int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_
   if ((rc = check_workspace(name, workspace, workspace_bytes, need)) != CVSA_OK) return rc;
   bind_workspace(a, workspace, need);
   const int G = H_q / H_kv;
-  const ScoreArgs sa{q, q_stride_b, q_stride_h, k_cache, num_blocks, block_tables,
-                     bt_stride_b, context_lens, page_scores, W, G, 1.0f / (float)G, a.scale,
-                     block_size, a.ts};
+  ScoreArgs sa{q, q_stride_b, q_stride_h, k_cache, num_blocks, block_tables,
+               bt_stride_b, context_lens, page_scores, W, G, 1.0f / (float)G, a.scale,
+               block_size, a.ts};
+  if (sel_map != nullptr && a.ts == 0) {
+    CVSA_REQUIRE(sel_map_stride >= W && sel_map_stride % 16 == 0 &&
+                     ((uintptr_t)sel_map & 15) == 0,
+                 CVSA_ERR_INVALID, "%s: selection map rows of %lld bytes", name,
+                 (long long)sel_map_stride);
+    sa.skip_map = sel_map;
+    sa.skip_stride = sel_map_stride;
+    a.spec_scores = page_scores;
+    a.inv_g = sa.inv_g;
+  }
   static_assert(kSpecScorePPW % 4 == 0, "a scoring wave holds whole pages of up to 4 tiles");
+  // 16-token pages: a wave per head and kSpecHeadPPW pages; else a wave per
+  // 4 heads and kSpecScorePPW tiles.
   const int64_t waves =
-      (int64_t)(((W << a.ts) + kSpecScorePPW - 1) / kSpecScorePPW) * (H_kv / 4);
+      a.ts == 0 ? (int64_t)((W + kSpecHeadPPW - 1) / kSpecHeadPPW) * H_kv
+                : (int64_t)(((W << a.ts) + kSpecScorePPW - 1) / kSpecScorePPW) * (H_kv / 4);
   const int score_gx = (int)((waves + kWavesPerWg - 1) / kWavesPerWg);
   const int64_t grid = (int64_t)p.grid_x * p.grid_y + (int64_t)score_gx * B;
   hipStream_t st = (hipStream_t)stream;

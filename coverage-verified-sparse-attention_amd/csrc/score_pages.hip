@@ -89,7 +89,8 @@ __global__ __launch_bounds__(256) void score_pages_kernel(
     }
     xchg32(mx, a, c);
     mx = fmaxf(a, c);
-    if (seg == 0 && rsub < HKV) dst[(int64_t)h * W] = mx;
+    // A zero score is written as +0, as by the group kernel.
+    if (seg == 0 && rsub < HKV) dst[(int64_t)h * W] = mx + 0.f;
   }
 }
 

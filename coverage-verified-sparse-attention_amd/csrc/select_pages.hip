@@ -263,7 +263,8 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
     uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
     const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
-    long long *__restrict__ stats, int count_gate, int32_t *__restrict__ keep_flag) {
+    long long *__restrict__ stats, int count_gate, int32_t *__restrict__ keep_flag,
+    uint8_t *__restrict__ sel_map, int64_t map_stride) {
   __shared__ uint32_t hist[256];
   __shared__ uint32_t hist_c[kHistCopies * kHistStride];
   __shared__ uint32_t hist_b[kBuckets];
@@ -711,6 +712,22 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     }
   }
   if (t == 0) n_per_head[bh] = n_sel;
+  if (sel_map != nullptr) {
+    // The row's selection map: this thread's pages i0 .. i0 + R - 1.
+    uint8_t *mrow = sel_map + (int64_t)bh * map_stride;
+    if constexpr (R % 4 == 0) {
+#pragma unroll
+      for (int r = 0; r < R; r += 4)
+        if (i0 + r < W)
+          *reinterpret_cast<uint32_t *>(mrow + i0 + r) =
+              (uint32_t)counted[r] | (uint32_t)counted[r + 1] << 8 |
+              (uint32_t)counted[r + 2] << 16 | (uint32_t)counted[r + 3] << 24;
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (i0 + r < W) mrow[i0 + r] = counted[r] ? 1 : 0;
+    }
+  }
 
   if (accept_out == nullptr) return;
   // ---- coverage of the new selection
@@ -977,7 +994,8 @@ static int launch_select(const char *name, const float *page_scores, const float
                          uint8_t *accept_out, float *coverage_out, const uint8_t *check_accept,
                          float *scores_cache, int64_t *stats, int count_gate,
                          void *stream, int mode = kUniform, float top_p = 0.f,
-                         const int32_t *row_budgets = nullptr, int32_t *keep_flag = nullptr) {
+                         const int32_t *row_budgets = nullptr, int32_t *keep_flag = nullptr,
+                         uint8_t *sel_map = nullptr, int64_t map_stride = 0) {
   CVSA_REQUIRE(page_scores && context_lens && page_indices && n_per_head, CVSA_ERR_INVALID,
                "%s: null pointer argument", name);
   CVSA_REQUIRE((accept_out == nullptr) == (coverage_out == nullptr), CVSA_ERR_INVALID,
@@ -992,6 +1010,11 @@ static int launch_select(const char *name, const float *page_scores, const float
                "%s: budget=%d must be in [1, W=%d]", name, budget, W);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
                kMaxPages);
+  CVSA_REQUIRE(sel_map == nullptr || (map_stride >= W && map_stride % 16 == 0 &&
+                                      ((uintptr_t)sel_map & 15) == 0),
+               CVSA_ERR_INVALID,
+               "%s: selection map rows of %lld bytes (16-byte aligned, >= W=%d) required",
+               name, (long long)map_stride, W);
   const int R = keys_per_thread(W);
   const dim3 grid(B * H_kv);
   hipStream_t st = (hipStream_t)stream;
@@ -1004,7 +1027,7 @@ static int launch_select(const char *name, const float *page_scores, const float
                      page_scores, sel_scores, W, H_kv, context_lens, block_size, budget,    \
                      width, top_p, row_budgets, page_indices, n_per_head, tau, accept_out,  \
                      coverage_out, check_accept, B * H_kv, scores_cache, st64, count_gate,    \
-                     keep_flag)
+                     keep_flag, sel_map, map_stride)
 #define CVSA_SEL_MODES(RR, SEP)                                    \
   if (mode == kTopP) CVSA_SEL_LAUNCH(RR, SEP, kTopP);              \
   else if (mode == kTable) CVSA_SEL_LAUNCH(RR, SEP, kTable);       \
@@ -1063,21 +1086,53 @@ extern "C" int cvsa_select_or_keep(const float *page_scores, const float *sel_sc
 
 namespace cvsa_internal {
 
-// cvsa_select_or_keep that also writes its keep decision to *keep_flag (1:
-// every head passed the check and the selection stayed, 0: reselected) --
-// the prediction a step plan's next lazy check speculates on.
-int select_or_keep_flag(const float *page_scores, const float *sel_scores,
-                        const uint8_t *check_accept, int32_t B, int32_t H_kv, int32_t W,
-                        const int32_t *context_lens, int32_t block_size, int32_t budget,
-                        int32_t *page_indices, int32_t *n_per_head, float tau,
-                        uint8_t *accept_out, float *coverage_out, float *scores_cache,
-                        int64_t *stats, int32_t *keep_flag, void *stream) {
-  CVSA_REQUIRE(accept_out && coverage_out && check_accept, CVSA_ERR_INVALID,
-               "select_or_keep: accept_out, coverage_out and check_accept are required");
+int select_for_plan(const float *page_scores, const float *sel_scores,
+                    const uint8_t *check_accept, int32_t B, int32_t H_kv, int32_t W,
+                    const int32_t *context_lens, int32_t block_size, int32_t budget,
+                    int32_t *page_indices, int32_t *n_per_head, float tau, uint8_t *accept_out,
+                    float *coverage_out, float *scores_cache, int64_t *stats,
+                    int32_t count_gate, int32_t *keep_flag, uint8_t *sel_map,
+                    int64_t sel_map_stride, void *stream) {
+  CVSA_REQUIRE(accept_out && coverage_out, CVSA_ERR_INVALID,
+               "select_or_keep: accept_out and coverage_out are required");
+  CVSA_REQUIRE(keep_flag == nullptr || check_accept != nullptr, CVSA_ERR_INVALID,
+               "select_or_keep: a keep flag needs check_accept");
   return launch_select("select_or_keep", page_scores, sel_scores, B, H_kv, W, context_lens,
                        block_size, budget, page_indices, n_per_head, tau, accept_out,
-                       coverage_out, check_accept, scores_cache, stats, 0, stream, kUniform,
-                       0.f, nullptr, keep_flag);
+                       coverage_out, check_accept, scores_cache, stats, count_gate, stream,
+                       kUniform, 0.f, nullptr, keep_flag, sel_map, sel_map_stride);
+}
+
+__global__ __launch_bounds__(kSelThreads) void selection_map_kernel(
+    const int32_t *__restrict__ page_indices, int64_t idx_stride,
+    const int32_t *__restrict__ n_per_head, int W, uint8_t *__restrict__ sel_map,
+    int64_t map_stride) {
+  const int row = blockIdx.x;
+  uint8_t *mrow = sel_map + (int64_t)row * map_stride;
+  for (int64_t i = threadIdx.x * 16; i < map_stride; i += kSelThreads * 16)
+    *reinterpret_cast<uint4 *>(mrow + i) = make_uint4(0u, 0u, 0u, 0u);
+  __syncthreads();  // the clearing stores before the marking ones
+  const int n = max(0, min(n_per_head[row], (int)idx_stride));
+  const int32_t *idx = page_indices + (int64_t)row * idx_stride;
+  for (int i = threadIdx.x; i < n; i += kSelThreads) {
+    const int p = idx[i];
+    if (p >= 0 && p < W) mrow[p] = 1;
+  }
+}
+
+int build_selection_map(const int32_t *page_indices, int64_t idx_stride,
+                        const int32_t *n_per_head, int32_t rows, int32_t W, uint8_t *sel_map,
+                        int64_t sel_map_stride, void *stream) {
+  CVSA_REQUIRE(page_indices && n_per_head && sel_map, CVSA_ERR_INVALID,
+               "selection map: null pointer argument");
+  CVSA_REQUIRE(rows > 0 && W > 0 && idx_stride > 0 && sel_map_stride >= W &&
+                   sel_map_stride % 16 == 0 && ((uintptr_t)sel_map & 15) == 0,
+               CVSA_ERR_INVALID, "selection map: bad sizes rows=%d W=%d stride=%lld", rows, W,
+               (long long)sel_map_stride);
+  hipLaunchKernelGGL(selection_map_kernel, dim3(rows), dim3(kSelThreads), 0,
+                     (hipStream_t)stream, page_indices, idx_stride, n_per_head, W, sel_map,
+                     sel_map_stride);
+  return cvsa_host::check_launch("selection map");
 }
 
 }  // namespace cvsa_internal

@@ -23,6 +23,10 @@ int fail(int code, const char *fmt, ...);
 
 struct cvsa_step_plan {
   cvsa_step_desc d;
+  // d.sel_map holds the map of the selection in d.page_indices: the plan's
+  // own selections write it; one made elsewhere (an adopted selection, or
+  // cvsa_step_plan_selection_changed) is mapped before the next lazy check.
+  bool map_valid;
 };
 
 namespace {
@@ -84,6 +88,12 @@ int check_desc(const cvsa_step_desc &d) {
   }
   STEP_REQUIRE(d.selector != CVSA_SELECT_QUEST || d.sel_scores != nullptr, CVSA_ERR_INVALID,
                "step_plan: CVSA_SELECT_QUEST needs a sel_scores buffer");
+  STEP_REQUIRE(d.sel_map == nullptr || (d.sel_map_stride >= d.W && d.sel_map_stride % 16 == 0 &&
+                                        aligned16(d.sel_map)),
+               CVSA_ERR_INVALID,
+               "step_plan: sel_map rows must be 16-byte aligned, a multiple of 16 bytes and "
+               "at least W=%d bytes apart (got %lld)",
+               d.W, (long long)d.sel_map_stride);
   const size_t need = workspace_need(d);
   STEP_REQUIRE(need < ((size_t)1 << 31), CVSA_ERR_UNSUPPORTED,
                "step_plan: a decode workspace of %zu bytes exceeds the 2 GiB buffer range",
@@ -144,7 +154,14 @@ extern "C" int cvsa_step_plan_create(const cvsa_step_desc *desc, cvsa_step_plan 
   cvsa_step_plan *p = new (std::nothrow) cvsa_step_plan;
   STEP_REQUIRE(p != nullptr, CVSA_ERR_INVALID, "step_plan_create: out of host memory");
   p->d = *desc;
+  p->map_valid = false;
   *plan = p;
+  return CVSA_OK;
+}
+
+extern "C" int cvsa_step_plan_selection_changed(cvsa_step_plan *plan) {
+  STEP_REQUIRE(plan, CVSA_ERR_INVALID, "step_plan_selection_changed: null plan");
+  plan->map_valid = false;
   return CVSA_OK;
 }
 
@@ -162,29 +179,52 @@ bool speculates(const cvsa_step_desc &d) {
          cvsa_internal::score_spec_fusable(d.H_kv, d.D, d.H_q / d.H_kv);
 }
 
+// The plan's selection map, when it has one (16-token pages).
+uint8_t *plan_map(const cvsa_step_desc &d) { return d.block_size == 16 ? d.sel_map : nullptr; }
+
+// The selection step of a plan: cvsa_select_or_keep writing the plan's
+// selection map with the selection.
+int plan_select(const cvsa_step_desc &d, const uint8_t *check, float *scores_cache,
+                int32_t count_gate, int32_t *keep_flag, void *stream) {
+  const float *sel = d.selector == CVSA_SELECT_QUEST ? d.sel_scores : nullptr;
+  return cvsa_internal::select_for_plan(
+      d.page_scores, sel, check, d.B, d.H_kv, d.W, d.context_lens, d.block_size, d.budget,
+      d.page_indices, d.n_per_head, d.tau, d.accept, d.coverage, scores_cache, d.stats,
+      count_gate, keep_flag, plan_map(d), d.sel_map_stride, stream);
+}
+
 // The lazy check with the speculative decode: one launch scores the pages
 // and decodes the cached selection (if spec_state[0] predicts a keep), then
 // the check, the select-or-keep that records its decision in spec_state[0],
 // and the verified decode, which only books counters when the selection was
-// kept and the speculative decode ran.
-int speculative_check(const cvsa_step_desc &d, const uint16_t *q, void *out, void *stream) {
+// kept and the speculative decode ran.  With a selection map the launch
+// scores the selection's pages from the decode's keys; a selection the plan
+// did not make is mapped first.
+int speculative_check(cvsa_step_plan &p, const uint16_t *q, void *out, void *stream) {
+  const cvsa_step_desc &d = p.d;
   int rc;
+  uint8_t *map = plan_map(d);
+  if (map != nullptr && !p.map_valid) {
+    if ((rc = cvsa_internal::build_selection_map(d.page_indices, d.budget, d.n_per_head,
+                                                 d.B * d.H_kv, d.W, map, d.sel_map_stride,
+                                                 stream)) != CVSA_OK)
+      return rc;
+    p.map_valid = true;
+  }
   if ((rc = cvsa_internal::score_and_speculate(
            q, d.q_stride_b, d.q_stride_h, d.k_cache, d.v_cache, d.num_blocks, d.block_tables,
            d.bt_stride_b, d.context_lens, d.page_indices, d.budget, d.n_per_head, d.budget, d.B,
            d.H_q, d.H_kv, d.D, d.block_size, d.W, d.page_scores, out, d.out_dtype,
-           d.spec_state, d.workspace, d.workspace_bytes, stream)) != CVSA_OK)
+           d.spec_state, map, d.sel_map_stride, d.workspace, d.workspace_bytes, stream)) !=
+      CVSA_OK)
     return rc;
   if ((rc = cvsa_check_coverage(d.page_scores, d.B, d.H_kv, d.W, d.page_indices, d.budget,
                                 d.n_per_head, d.tau, d.check_accept, d.coverage, stream)) !=
       CVSA_OK)
     return rc;
   if ((rc = rank(d, q, d.check_accept, stream)) != CVSA_OK) return rc;
-  const float *sel = d.selector == CVSA_SELECT_QUEST ? d.sel_scores : nullptr;
-  if ((rc = cvsa_internal::select_or_keep_flag(
-           d.page_scores, sel, d.check_accept, d.B, d.H_kv, d.W, d.context_lens, d.block_size,
-           d.budget, d.page_indices, d.n_per_head, d.tau, d.accept, d.coverage, d.scores_cache,
-           d.stats, d.spec_state, stream)) != CVSA_OK)
+  if ((rc = plan_select(d, d.check_accept, d.scores_cache, 0, d.spec_state, stream)) !=
+      CVSA_OK)
     return rc;
   return cvsa_internal::verified_decode_after_speculation(
       q, d.q_stride_b, d.q_stride_h, d.k_cache, d.v_cache, d.num_blocks, d.block_tables,
@@ -223,7 +263,6 @@ extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint
                    kind == CVSA_STEP_SCORE || kind == CVSA_STEP_FRESH,
                CVSA_ERR_INVALID, "step_plan_run: unknown step kind %d", kind);
   const cvsa_step_desc &d = plan->d;
-  const float *sel = d.selector == CVSA_SELECT_QUEST ? d.sel_scores : nullptr;
   int rc;
   switch (kind) {
     case CVSA_STEP_REUSE:
@@ -233,37 +272,28 @@ extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint
                                 d.H_kv, d.D, d.block_size, d.W, nullptr, nullptr, nullptr, out,
                                 d.out_dtype, d.work, d.workspace, d.workspace_bytes, stream);
     case CVSA_STEP_LAZY_CHECK:
-      if (speculates(d)) return speculative_check(d, q, out, stream);
+      if (speculates(d)) return speculative_check(*plan, q, out, stream);
       if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
       if ((rc = cvsa_check_coverage(d.page_scores, d.B, d.H_kv, d.W, d.page_indices, d.budget,
                                     d.n_per_head, d.tau, d.check_accept, d.coverage,
                                     stream)) != CVSA_OK)
         return rc;
       if ((rc = rank(d, q, d.check_accept, stream)) != CVSA_OK) return rc;
-      if ((rc = cvsa_select_or_keep(d.page_scores, sel, d.check_accept, d.B, d.H_kv, d.W,
-                                    d.context_lens, d.block_size, d.budget, d.page_indices,
-                                    d.n_per_head, d.tau, d.accept, d.coverage, d.scores_cache,
-                                    d.stats, 0, stream)) != CVSA_OK)
+      if ((rc = plan_select(d, d.check_accept, d.scores_cache, 0, nullptr, stream)) != CVSA_OK)
         return rc;
       return verified(d, q, out, stream);
     case CVSA_STEP_FRESH:
       if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
       if ((rc = rank(d, q, nullptr, stream)) != CVSA_OK) return rc;
-      if ((rc = cvsa_select_or_keep(d.page_scores, sel, nullptr, d.B, d.H_kv, d.W,
-                                    d.context_lens, d.block_size, d.budget, d.page_indices,
-                                    d.n_per_head, d.tau, d.accept, d.coverage, d.scores_cache,
-                                    d.stats, 0, stream)) != CVSA_OK)
+      if ((rc = plan_select(d, nullptr, d.scores_cache, 0, nullptr, stream)) != CVSA_OK)
         return rc;
+      plan->map_valid = true;  // every row selected anew
       return verified(d, q, out, stream);
     default:  // CVSA_STEP_SCORE
       if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
       if ((rc = rank(d, q, nullptr, stream)) != CVSA_OK) return rc;
-      if ((rc = cvsa_select_or_keep(d.page_scores, sel, nullptr, d.B, d.H_kv, d.W,
-                                    d.context_lens,
-                                    d.block_size, d.budget, d.page_indices, d.n_per_head,
-                                    d.tau, d.accept, d.coverage, nullptr, d.stats, 1,
-                                    stream)) != CVSA_OK)
-        return rc;
+      if ((rc = plan_select(d, nullptr, nullptr, 1, nullptr, stream)) != CVSA_OK) return rc;
+      plan->map_valid = true;
       return verified(d, q, out, stream);
   }
 }

@@ -705,6 +705,9 @@ class CVSABackend:
         counters of both branches accumulate on the device."""
         page_indices, n_per_head = self._cached_selection[layer_idx]
         budget = page_indices.shape[2]
+        plan = self._step_plans.get(layer_idx)
+        if plan is not None and plan.page_indices is page_indices:
+            plan.selection_changed()  # select_or_keep below may rewrite it in place
         self._per_head_total += check_accept.numel()
         sel_scores = self._sel_scores(q, k_cache, block_tables, context_lens, check_accept)
         if sel_scores is not None:

@@ -641,14 +641,16 @@ class StepPlan:
     in the same launch as the page scoring, and the verified decode skips
     its work when the check kept that selection (see
     cvsa_step_desc.spec_state; exact gate scores, H_kv in 4, 8, 16 and D = 128
-    only);
-    results are bit-identical either way.
+    only); with 16-token pages that decode also scores the selection's pages
+    from the keys it reads, which the page scoring then skips (``sel_map``,
+    the selection's page map).  Results are bit-identical either way.  A caller that writes
+    ``page_indices`` / ``n_per_head`` itself calls ``selection_changed()``.
     """
 
     __slots__ = ("dev", "stream", "q_meta", "out_shape", "out_dtype", "refs", "page_indices",
                  "n_per_head", "page_scores", "scores_cache", "check_accept", "accept",
                  "coverage", "budget", "owns_selection", "selector", "sel_scores", "spec_state",
-                 "_h", "_run", "_fin", "__weakref__")
+                 "sel_map", "_h", "_run", "_fin", "__weakref__")
 
     def __init__(self, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
                  num_q_per_kv, block_size, budget, tau, page_indices=None, n_per_head=None,
@@ -711,6 +713,11 @@ class StepPlan:
         # check), [1]: the speculative decode ran.
         self.spec_state = (torch.tensor([1, 0], dtype=torch.int32, device=dev)
                            if speculate else None)
+        # Byte p of row b * H_kv + h: page p is in the selection (rows of W
+        # rounded up to 16 bytes; zero past W).
+        map_stride = (W + 15) // 16 * 16
+        self.sel_map = (torch.zeros(B * H, map_stride, dtype=torch.uint8, device=dev)
+                        if speculate and block_size == 16 else None)
         d = _lib.StepDesc(
             B=B, H_q=H_q, H_kv=H, D=D, block_size=block_size, W=W, budget=budget,
             tau=float(tau), out_dtype=_DTYPE_CODE[q.dtype], q_stride_b=q.stride(0),
@@ -723,7 +730,8 @@ class StepPlan:
             coverage=self.coverage.data_ptr(), stats=_ptr(stats), work=_ptr(work),
             selector=selector, quest_meta=None if quest is None else quest.meta.data_ptr(),
             quest_ntok=None if quest is None else quest.ntok.data_ptr(),
-            sel_scores=_ptr(self.sel_scores), spec_state=_ptr(self.spec_state))
+            sel_scores=_ptr(self.sel_scores), spec_state=_ptr(self.spec_state),
+            sel_map=_ptr(self.sel_map), sel_map_stride=map_stride)
         L = _lib.load()
         ws = _workspace(dev, L.cvsa_step_workspace_bytes(ctypes.byref(d)))
         d.workspace = _ptr(ws)
@@ -753,6 +761,11 @@ class StepPlan:
                 and torch._C._cuda_getCurrentRawStream(self.dev.index) == self.stream
                 and q.device == self.dev and q.dtype == self.out_dtype
                 and (q.shape, q.stride()) == self.q_meta and q.data_ptr() % 16 == 0)
+
+    def selection_changed(self) -> None:
+        """page_indices / n_per_head were written outside the plan
+        (cvsa_step_plan_selection_changed)."""
+        check(_lib.load().cvsa_step_plan_selection_changed(self._h), "step_plan_selection_changed")
 
     def run(self, kind: int, q: torch.Tensor) -> torch.Tensor:
         out = torch.empty(self.out_shape, device=self.dev, dtype=self.out_dtype)

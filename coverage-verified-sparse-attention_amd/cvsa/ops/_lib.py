@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parents[1] / "libcvsa_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 CVSA_OK = 0
 CVSA_ERR_INVALID = -1
@@ -50,7 +50,7 @@ class StepDesc(ctypes.Structure):
         ("check_accept", _p), ("accept", _p), ("coverage", _p), ("stats", _p), ("work", _p),
         ("workspace", _p), ("workspace_bytes", _sz),
         ("selector", _i32), ("quest_meta", _p), ("quest_ntok", _p), ("sel_scores", _p),
-        ("spec_state", _p),
+        ("spec_state", _p), ("sel_map", _p), ("sel_map_stride", _i64),
     ]
 
 
@@ -116,6 +116,7 @@ SIGNATURES = {
     "cvsa_step_plan_run": (ctypes.c_int, [_p, _i32, _p, _p, _p]),
     "cvsa_step_plan_run_append": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _p, _p, _p, _p]),
     "cvsa_step_plan_destroy": (None, [_p]),
+    "cvsa_step_plan_selection_changed": (ctypes.c_int, [_p]),
 }
 
 _LIB = None

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 11
+#define CVSA_ABI_VERSION 12
 
 enum {
   CVSA_OK = 0,
@@ -489,6 +489,9 @@ typedef struct cvsa_step_desc {
   float *sel_scores;           /* CVSA_SELECT_QUEST: [B, H_kv, W] ranking scores (else NULL) */
   int32_t *spec_state;         /* int32[2] or NULL: speculative lazy checks (below); [0] is
                                   initialised to 1, [1] to 0 */
+  uint8_t *sel_map;            /* [B * H_kv, sel_map_stride] bytes, zeroed, or NULL: the map
+                                  of the selection (below) */
+  int64_t sel_map_stride;      /* >= W, a multiple of 16 (sel_map 16-byte aligned) */
 } cvsa_step_desc;
 
 /* Page scorers of a plan (CVSABackend selector / light_normalizer,
@@ -513,6 +516,14 @@ enum {
  * those of the sequential chain bit for bit.  Plans whose gate scores are
  * Quest scores (CVSA_SELECT_QUEST_LN), whose H_kv is 1 or 2 or whose D is
  * not 128 run the sequential chain and leave spec_state unchanged.
+ * With a selection map (sel_map; 16-token pages) the speculative decode
+ * also scores the pages it walks, from the keys it reads for the decode,
+ * and the page scoring skips them: the kept selection's keys are read once
+ * per check instead of twice, with the same score bits.  The plan writes
+ * the map with every selection it makes and maps a selection it adopted
+ * (page_indices given at creation) before its first speculative check; a
+ * caller that writes page_indices / n_per_head itself must then call
+ * cvsa_step_plan_selection_changed.
  */
 enum {
   CVSA_STEP_REUSE = 0,      /* sparse decode of the kept selection */
@@ -527,6 +538,11 @@ typedef struct cvsa_step_plan cvsa_step_plan;
 /* Workspace a plan needs: the larger of its listed and verified decodes. */
 size_t cvsa_step_workspace_bytes(const cvsa_step_desc *desc);
 int cvsa_step_plan_create(const cvsa_step_desc *desc, cvsa_step_plan **plan);
+/* The plan's page_indices / n_per_head were written by something other than
+ * the plan: its selection map is rebuilt before the next speculative check.
+ * No counterpart in the reference (its selection is a fresh tensor per
+ * scoring step). */
+int cvsa_step_plan_selection_changed(cvsa_step_plan *plan);
 /* q: [B, H_q, D] bf16 with the descriptor's strides; out: [B, H_q, D]. */
 int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint16_t *q, void *out,
                        void *stream);

@@ -137,6 +137,7 @@ def test_speculative_check_every_prediction(gpu, case, predict_keep, shape):
                                16, output_dtype=q1.dtype, work=work_r)
     for plan, b, out in ((plans[0], bufs[0], got), (plans[1], bufs[1], plain)):
         assert torch.equal(out, want)
+        assert torch.equal(plan.page_scores, ps)  # also where the decode part scored
         assert torch.equal(plan.accept.view(torch.bool), acc)
         assert torch.equal(plan.page_indices, sel_r) and torch.equal(plan.n_per_head, nph_r)
         assert torch.equal(b["cache"], cache_r)
@@ -444,3 +445,64 @@ def _plan_equals_separate_kernels(gpu, seed, D, BS=16, G_range=(1, 8)):
             assert torch.equal(got, ref_out), (seed, step, plan.spec_state is not None)
         assert torch.equal(plan.page_indices, sel) and torch.equal(plan.n_per_head, nph)
         assert torch.equal(p_stats, stats) and torch.equal(p_work, work), seed
+
+
+def _map_of(sel, nph, W, stride):
+    """The selection map a plan keeps: byte p of row r set for the row's
+    first n_per_head entries."""
+    rows = sel.reshape(-1, sel.shape[-1]).long().cpu()
+    n = nph.reshape(-1).cpu()
+    m = torch.zeros(rows.shape[0], stride, dtype=torch.uint8)
+    for r in range(rows.shape[0]):
+        m[r, rows[r, :int(n[r])]] = 1
+    return m
+
+
+@pytest.mark.parametrize("shape", [(8, 4), (4, 7), (16, 16), (8, 1)])
+def test_selection_map_and_scores_over_a_schedule(gpu, shape):
+    """A plan's selection map follows every selection it makes (fresh,
+    reselect, keep) and an adopted or externally written one
+    (selection_changed); the page scores of every lazy check, part of them
+    computed by the speculative decode from the keys it walks, equal
+    cvsa_score_pages bit for bit, whatever the prediction.  Two plans share
+    the selection buffers (tau 0: keeps; tau 0.999: reselects), each told
+    when the other may have rewritten the selection."""
+    H, G = shape
+    inp, W, budget = _inputs(gpu, h=H, g=G)
+    ctx, bt = inp.context_lens, inp.block_tables
+    stats = torch.zeros(6, dtype=torch.int64, device=gpu)
+    work = torch.zeros(2, dtype=torch.int64, device=gpu)
+    fresh = ops.StepPlan(inp.q, inp.k_cache, inp.v_cache, bt, ctx, H, G, 16, budget, 0.9,
+                         stats=stats, work=work, own_scores_cache=True)
+    stride = fresh.sel_map.shape[1]
+    assert stride % 16 == 0 and stride >= W
+    fresh.run(_lib.STEP_FRESH, jitter_query(inp.q, 0.5, 10))
+    torch.cuda.synchronize()
+    assert torch.equal(fresh.sel_map.cpu(),
+                       _map_of(fresh.page_indices, fresh.n_per_head, W, stride))
+    plans = {tau: ops.StepPlan(inp.q, inp.k_cache, inp.v_cache, bt, ctx, H, G, 16, budget, tau,
+                               fresh.page_indices, fresh.n_per_head, fresh.scores_cache, stats,
+                               work) for tau in (0.0, 0.999)}
+    schedule = [(11, 1, 0.0), (12, 0, 0.0), (13, 1, 0.999), (14, 1, 0.0), (15, 0, 0.999),
+                (16, 1, 0.0), (17, 1, 0.0), (18, 0, 0.999), (19, 0, 0.0)]
+    for step, (seed, predict, tau) in enumerate(schedule):
+        q = jitter_query(inp.q, 0.5, seed)
+        if step == 4:
+            # a selection written outside the plans: the worst pages
+            ps_prev = ops.score_pages(q, inp.k_cache, bt, ctx, H, G, 16)
+            nph = fresh.n_per_head
+            nph.copy_(torch.minimum(nph, torch.full_like(nph, budget // 2)))
+            fresh.page_indices.copy_(_worst_pages(ps_prev, budget, nph))
+            for p in plans.values():
+                p.selection_changed()
+        p = plans[tau]
+        p.spec_state[0] = predict
+        p.run(_lib.STEP_LAZY_CHECK, q)
+        for other in plans.values():
+            if other is not p:
+                other.selection_changed()
+        ps = ops.score_pages(q, inp.k_cache, bt, ctx, H, G, 16)
+        assert torch.equal(p.page_scores, ps), (step, predict, tau)
+        torch.cuda.synchronize()
+        assert torch.equal(p.sel_map.cpu(), _map_of(p.page_indices, p.n_per_head, W, stride)), \
+            (step, predict, tau)
