@@ -1021,42 +1021,6 @@ void score_spec_kernel(const DecodeArgs a,
                                                                  NewToken(), s_qrep[wave]);
 }
 
-// Effective-budget counters of a verified launch whose heads were all
-// accepted and whose outputs a speculative listed decode already wrote:
-// what the listed walks would have added, summed by one workgroup.  A
-// thread's first head (bh = threadIdx.x) comes in as n0 / nv0, requested
-// with the launch's first loads (listed_work_first).
-template <int NT>
-__device__ __forceinline__ void listed_work_first(const DecodeArgs &a, int ts,
-                                                  unsigned long long &n0,
-                                                  unsigned long long &nv0) {
-  const int bh = min((int)threadIdx.x, a.heads - 1);
-  const int np = a.n_pages[bh];
-  const int ctx = a.ctx_lens[bh / a.H_kv];
-  const bool live = (int)threadIdx.x < a.heads;
-  n0 = live ? (unsigned long long)min(max(np, 0), a.max_sel) : 0ull;
-  nv0 = live ? (unsigned long long)max(0, valid_pages_ts(ctx, ts)) : 0ull;
-}
-
-template <int NT>
-__device__ __forceinline__ void add_listed_work(const DecodeArgs &a, unsigned long long *red,
-                                                int ts, unsigned long long n,
-                                                unsigned long long nv) {
-  for (int bh = threadIdx.x + NT; bh < a.heads; bh += NT) {
-    n += (unsigned long long)min(max(a.n_pages[bh], 0), a.max_sel);
-    nv += (unsigned long long)max(0, valid_pages_ts(a.ctx_lens[bh / a.H_kv], ts));
-  }
-  if (threadIdx.x == 0) red[0] = red[1] = 0ull;
-  __syncthreads();
-  if (n) atomicAdd(&red[0], n);
-  if (nv) atomicAdd(&red[1], nv);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    atomicAdd(&a.work[0], red[0]);
-    atomicAdd(&a.work[1], red[1]);
-  }
-}
-
 // NW waves per workgroup, PD pages of K/V in flight per wave.
 //
 // Every workgroup first computes the pages each head walks and their prefix
@@ -1079,7 +1043,6 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   __shared__ int s_odd[NW];               // a head of the wave's pass walks != max_sel pages
   __shared__ int s_start[kMaxHeads + 1];  // exclusive prefix of pages per head
   __shared__ uint8_t s_listed[kMaxHeads];
-  __shared__ unsigned long long s_work[2];
   auto &s_o = L.o;
   auto &s_m = L.m;
   auto &s_l = L.l;
@@ -1104,10 +1067,10 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   // their block-table entries once the launch is known to walk.  When the
   // check kept its selection (spec_state[0], written by the check's
   // select-or-keep) and a speculative listed decode of that selection
-  // already wrote the outputs (spec_state[1]), only the effective-budget
-  // counters are booked.  Every head accepted does not imply a kept
-  // selection: a rejected head is reselected and accepted when the new
-  // selection passes its gate.
+  // already wrote the outputs (spec_state[1]), there is nothing left: the
+  // select-or-keep booked that decode's effective-budget counters.  Every
+  // head accepted does not imply a kept selection: a rejected head is
+  // reselected and accepted when the new selection passes its gate.
   if constexpr (MODE == kModeVerified) {
     const int n_listed = a.n_splits * heads;
     const int split = w % max(a.n_splits, 1);
@@ -1116,20 +1079,10 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     int spec_done = 0;
     if (a.spec_state != nullptr)
       spec_done = __builtin_amdgcn_readfirstlane(a.spec_state[0] & a.spec_state[1]);
-    // The counters of a kept speculation are booked by workgroup 0, whose
-    // threads request their first head's page count and context length
-    // here, in the same round trip as the flags.
-    unsigned long long n0 = 0, nv0 = 0;
-    if (a.spec_state != nullptr && w == 0 && a.work != nullptr)
-      listed_work_first<NT>(a, Engine::tshift(a), n0, nv0);
+    if (spec_done != 0) return;  // uniform; every head was accepted (kept)
     int rejected = 0;
     for (int i = threadIdx.x; i < heads; i += NT) rejected |= a.accept[i] == 0;
     if (__syncthreads_or(rejected) == 0) {  // uniform
-      if (spec_done != 0) {
-        if (w == 0 && a.work != nullptr)
-          add_listed_work<NT>(a, s_work, Engine::tshift(a), n0, nv0);
-        return;
-      }
       if (w < n_listed)
         listed_walk<G, Engine, NW, PD>(a, split, bh, lp,
                                        listed_first_block(a, bh, lp, Engine::tshift(a)), L);

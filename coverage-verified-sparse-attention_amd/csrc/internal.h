@@ -36,14 +36,17 @@ int verified_decode_after_speculation(
 // selection stayed, 0: reselected) -- the prediction the plan's next lazy
 // check speculates on; with sel_map, every row it (re)selects also gets its
 // selection map row (byte p = page p is among the row's first n_per_head
-// entries; rows sel_map_stride bytes apart, the bytes past W stay 0).
+// entries; rows sel_map_stride bytes apart, the bytes past W stay 0); with
+// keep_work, a kept selection whose speculative decode ran (keep_flag[1])
+// gets that decode's effective-budget counters booked here instead of by
+// the verified decode after it (verified_decode_after_speculation).
 int select_for_plan(const float *page_scores, const float *sel_scores,
                     const uint8_t *check_accept, int32_t B, int32_t H_kv, int32_t W,
                     const int32_t *context_lens, int32_t block_size, int32_t budget,
                     int32_t *page_indices, int32_t *n_per_head, float tau, uint8_t *accept_out,
                     float *coverage_out, float *scores_cache, int64_t *stats,
                     int32_t count_gate, int32_t *keep_flag, uint8_t *sel_map,
-                    int64_t sel_map_stride, void *stream);
+                    int64_t sel_map_stride, int64_t *keep_work, void *stream);
 
 // The selection map of a selection made elsewhere: row r (of `rows`) of
 // sel_map cleared over sel_map_stride bytes, then byte p set for each of the

@@ -264,7 +264,8 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
     const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
     long long *__restrict__ stats, int count_gate, int32_t *__restrict__ keep_flag,
-    uint8_t *__restrict__ sel_map, int64_t map_stride) {
+    uint8_t *__restrict__ sel_map, int64_t map_stride,
+    unsigned long long *__restrict__ keep_work) {
   __shared__ uint32_t hist[256];
   __shared__ uint32_t hist_c[kHistCopies * kHistStride];
   __shared__ uint32_t hist_b[kBuckets];
@@ -307,6 +308,14 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   // with LDS operations, so even a context-length load here would hold up
   // the check's barriers.)
   if (check_accept != nullptr) {
+    // A kept speculation's booking (below) needs these: requested with the
+    // flags, in the same round trip.
+    int spec_ran = 0, n_row = 0, ctx_row = 0;
+    if (keep_work != nullptr && t == 0) {
+      spec_ran = keep_flag[1];
+      n_row = n_per_head[bh];
+      ctx_row = context_lens[b];
+    }
     if (t == 0) {
       s_nok = 0;
       s_nbad = 0;
@@ -332,7 +341,17 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     // prediction that the check keeps its selection).
     if (keep_flag != nullptr && bh == 0 && t == 0) *keep_flag = all_ok ? 1 : 0;
     if (all_ok) {
-      if (t == 0) accept_out[bh] = 1;
+      if (t == 0) {
+        accept_out[bh] = 1;
+        // A kept selection whose speculative decode already ran (keep_flag[1]):
+        // the effective-budget counters of that decode's walk of this row
+        // (what the verified decode would book), so the verified decode after
+        // it has nothing left to do.
+        if (keep_work != nullptr && spec_ran != 0) {
+          atomicAdd(&keep_work[0], (unsigned long long)min(max(n_row, 0), width));
+          atomicAdd(&keep_work[1], (unsigned long long)max(0, n_valid_pages(ctx_row, block_size)));
+        }
+      }
       return;
     }
   } else if (stats != nullptr && !count_gate && bh == 0 && t == 0) {
@@ -995,7 +1014,8 @@ static int launch_select(const char *name, const float *page_scores, const float
                          float *scores_cache, int64_t *stats, int count_gate,
                          void *stream, int mode = kUniform, float top_p = 0.f,
                          const int32_t *row_budgets = nullptr, int32_t *keep_flag = nullptr,
-                         uint8_t *sel_map = nullptr, int64_t map_stride = 0) {
+                         uint8_t *sel_map = nullptr, int64_t map_stride = 0,
+                         int64_t *keep_work = nullptr) {
   CVSA_REQUIRE(page_scores && context_lens && page_indices && n_per_head, CVSA_ERR_INVALID,
                "%s: null pointer argument", name);
   CVSA_REQUIRE((accept_out == nullptr) == (coverage_out == nullptr), CVSA_ERR_INVALID,
@@ -1027,7 +1047,8 @@ static int launch_select(const char *name, const float *page_scores, const float
                      page_scores, sel_scores, W, H_kv, context_lens, block_size, budget,    \
                      width, top_p, row_budgets, page_indices, n_per_head, tau, accept_out,  \
                      coverage_out, check_accept, B * H_kv, scores_cache, st64, count_gate,    \
-                     keep_flag, sel_map, map_stride)
+                     keep_flag, sel_map, map_stride,                                         \
+                     reinterpret_cast<unsigned long long *>(keep_work))
 #define CVSA_SEL_MODES(RR, SEP)                                    \
   if (mode == kTopP) CVSA_SEL_LAUNCH(RR, SEP, kTopP);              \
   else if (mode == kTable) CVSA_SEL_LAUNCH(RR, SEP, kTable);       \
@@ -1092,15 +1113,17 @@ int select_for_plan(const float *page_scores, const float *sel_scores,
                     int32_t *page_indices, int32_t *n_per_head, float tau, uint8_t *accept_out,
                     float *coverage_out, float *scores_cache, int64_t *stats,
                     int32_t count_gate, int32_t *keep_flag, uint8_t *sel_map,
-                    int64_t sel_map_stride, void *stream) {
+                    int64_t sel_map_stride, int64_t *keep_work, void *stream) {
   CVSA_REQUIRE(accept_out && coverage_out, CVSA_ERR_INVALID,
                "select_or_keep: accept_out and coverage_out are required");
   CVSA_REQUIRE(keep_flag == nullptr || check_accept != nullptr, CVSA_ERR_INVALID,
                "select_or_keep: a keep flag needs check_accept");
+  CVSA_REQUIRE(keep_work == nullptr || keep_flag != nullptr, CVSA_ERR_INVALID,
+               "select_or_keep: booking a kept speculation needs the keep flag");
   return launch_select("select_or_keep", page_scores, sel_scores, B, H_kv, W, context_lens,
                        block_size, budget, page_indices, n_per_head, tau, accept_out,
                        coverage_out, check_accept, scores_cache, stats, count_gate, stream,
-                       kUniform, 0.f, nullptr, keep_flag, sel_map, sel_map_stride);
+                       kUniform, 0.f, nullptr, keep_flag, sel_map, sel_map_stride, keep_work);
 }
 
 __global__ __launch_bounds__(kSelThreads) void selection_map_kernel(

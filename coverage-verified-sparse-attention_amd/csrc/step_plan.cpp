@@ -187,10 +187,13 @@ uint8_t *plan_map(const cvsa_step_desc &d) { return d.block_size == 16 ? d.sel_m
 int plan_select(const cvsa_step_desc &d, const uint8_t *check, float *scores_cache,
                 int32_t count_gate, int32_t *keep_flag, void *stream) {
   const float *sel = d.selector == CVSA_SELECT_QUEST ? d.sel_scores : nullptr;
+  // With the keep flag (a speculative check), a kept speculation's counters
+  // are booked by the select.
   return cvsa_internal::select_for_plan(
       d.page_scores, sel, check, d.B, d.H_kv, d.W, d.context_lens, d.block_size, d.budget,
       d.page_indices, d.n_per_head, d.tau, d.accept, d.coverage, scores_cache, d.stats,
-      count_gate, keep_flag, plan_map(d), d.sel_map_stride, stream);
+      count_gate, keep_flag, plan_map(d), d.sel_map_stride,
+      keep_flag != nullptr ? d.work : nullptr, stream);
 }
 
 // The lazy check with the speculative decode: one launch scores the pages
