@@ -111,6 +111,12 @@ def test_step_plan_validates_on_the_host():
     assert lib.cvsa_step_plan_run(h, 7, 1 << 20, 1 << 20, None) == _lib.CVSA_ERR_INVALID
     assert b"kind" in lib.cvsa_last_error()
     assert lib.cvsa_step_plan_run(h, 0, (1 << 20) + 2, 1 << 20, None) == _lib.CVSA_ERR_INVALID
+    assert lib.cvsa_step_plan_selection_changed(h) == _lib.CVSA_OK  # host state only
+    assert lib.cvsa_step_plan_selection_changed(None) == _lib.CVSA_ERR_INVALID
+    lib.cvsa_step_plan_destroy(h)
+    # a valid selection map is accepted
+    ok = _step_desc(sel_map=1 << 26, sel_map_stride=512)
+    assert lib.cvsa_step_plan_create(ctypes.byref(ok), ctypes.byref(h)) == _lib.CVSA_OK
     lib.cvsa_step_plan_destroy(h)
     cases = [(dict(budget=513), _lib.CVSA_ERR_INVALID, b"budget"),
              (dict(H_kv=3, H_q=12), _lib.CVSA_ERR_UNSUPPORTED, b"H_kv"),
@@ -123,7 +129,12 @@ def test_step_plan_validates_on_the_host():
              (dict(selector=3), _lib.CVSA_ERR_INVALID, b"selector"),
              (dict(selector=_lib.SELECT_QUEST_LN), _lib.CVSA_ERR_INVALID, b"quest_meta"),
              (dict(selector=_lib.SELECT_QUEST, quest_meta=1 << 24, quest_ntok=1 << 25),
-              _lib.CVSA_ERR_INVALID, b"sel_scores")]
+              _lib.CVSA_ERR_INVALID, b"sel_scores"),
+             # selection map rows: at least W bytes, a multiple of 16, 16-byte aligned
+             (dict(sel_map=1 << 26, sel_map_stride=496), _lib.CVSA_ERR_INVALID, b"sel_map"),
+             (dict(sel_map=1 << 26, sel_map_stride=520), _lib.CVSA_ERR_INVALID, b"sel_map"),
+             (dict(sel_map=(1 << 26) + 8, sel_map_stride=512), _lib.CVSA_ERR_INVALID,
+              b"sel_map")]
     for over, code, word in cases:
         h = ctypes.c_void_p()
         rc = lib.cvsa_step_plan_create(ctypes.byref(_step_desc(**over)), ctypes.byref(h))
