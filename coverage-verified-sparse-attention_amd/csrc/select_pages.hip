@@ -316,26 +316,36 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
       n_row = n_per_head[bh];
       ctx_row = context_lens[b];
     }
-    if (t == 0) {
-      s_nok = 0;
-      s_nbad = 0;
+    int nok;
+    bool all_ok;
+    if (n_heads <= kWave) {  // uniform
+      // Every wave reads the flags itself (one per lane): no barrier.
+      const int lane = t & 63;
+      nok = __popcll(__ballot(lane < n_heads && check_accept[lane] != 0));
+      all_ok = nok == n_heads;
+    } else {
+      if (t == 0) {
+        s_nok = 0;
+        s_nbad = 0;
+      }
+      lds_barrier();
+      int cnt = 0, bad = 0;
+      for (int i = t; i < n_heads; i += kSelThreads) {
+        const int v = check_accept[i] != 0;
+        cnt += v;
+        bad |= !v;
+      }
+      if (cnt) atomicAdd(&s_nok, cnt);
+      if (bad) s_nbad = 1;
+      lds_barrier();
+      nok = s_nok;
+      all_ok = s_nbad == 0;
     }
-    lds_barrier();
-    int cnt = 0, bad = 0;
-    for (int i = t; i < n_heads; i += kSelThreads) {
-      const int v = check_accept[i] != 0;
-      cnt += v;
-      bad |= !v;
-    }
-    if (cnt) atomicAdd(&s_nok, cnt);
-    if (bad) s_nbad = 1;
-    lds_barrier();
-    const bool all_ok = s_nbad == 0;
     if (stats != nullptr && bh == 0 && t == 0) {
       stat_add(&stats[0], all_ok ? 1 : 0);
       stat_add(&stats[1], all_ok ? 0 : 1);
       stat_add(&stats[2], all_ok ? 0 : 1);
-      stat_add(&stats[3], s_nok);
+      stat_add(&stats[3], nok);
     }
     // The decision, for the next check's speculative decode (a step plan's
     // prediction that the check keeps its selection).
