@@ -650,7 +650,8 @@ class StepPlan:
     __slots__ = ("dev", "stream", "q_meta", "out_shape", "out_dtype", "refs", "page_indices",
                  "n_per_head", "page_scores", "scores_cache", "check_accept", "accept",
                  "coverage", "budget", "owns_selection", "selector", "sel_scores", "spec_state",
-                 "sel_map", "_h", "_run", "_fin", "__weakref__")
+                 "sel_map", "h_kv", "_h", "_run", "_run_append", "_pa_ok", "_slots_ok", "_fin",
+                 "__weakref__")
 
     def __init__(self, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
                  num_q_per_kv, block_size, budget, tau, page_indices=None, n_per_head=None,
@@ -740,6 +741,9 @@ class StepPlan:
         check(L.cvsa_step_plan_create(ctypes.byref(d), ctypes.byref(h)), "step_plan_create")
         self._h = h.value
         self._run = L.cvsa_step_plan_run
+        self._run_append = L.cvsa_step_plan_run_append
+        self._pa_ok = self._slots_ok = None     # append buffers already checked
+        self.h_kv = H
         self._fin = weakref.finalize(self, L.cvsa_step_plan_destroy, h.value)
         self.dev = dev
         self.stream = _stream(dev)
@@ -783,14 +787,65 @@ class StepPlan:
         or slots_dev the same values in a contiguous int32 [B, 2] device
         tensor (for a launch a captured graph replays).  Writes the plan's
         caches, block table and context lengths."""
+        who = "run_reuse_append"
         if (slots is None) == (slots_dev is None):
-            raise ValueError("run_reuse_append: give exactly one of slots and slots_dev")
+            raise ValueError(f"{who}: give exactly one of slots and slots_dev")
+        B, H_q, D = self.out_shape
+        if (q.device != self.dev or q.dtype != self.out_dtype
+                or (q.shape, q.stride()) != self.q_meta):
+            raise ValueError(f"{who}: q must have the plan's device, dtype, shape and strides")
+        _check_new_rows(who, k_new, v_new, (B, self.h_kv, D), self.dev)
+        if pages_allocated is not self._pa_ok:
+            _check_pages_allocated(who, pages_allocated, B, self.dev)
+            self._pa_ok = pages_allocated
+        if slots_dev is not None:
+            if slots_dev is not self._slots_ok:
+                _append_slots(who, slots_dev, B, self.dev)
+                self._slots_ok = slots_dev
+            slot_arr = None
+        else:
+            slot_arr, _ = _append_slots(who, slots, B, self.dev)
         out = torch.empty(self.out_shape, device=self.dev, dtype=self.out_dtype)
-        check(_lib.load().cvsa_step_plan_run_append(
+        check(self._run_append(
             self._h, q.data_ptr(), out.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
-            k_new.stride(0), pages_allocated.data_ptr(), slots, _ptr(slots_dev), self.stream),
-            "step_plan_run_append")
+            k_new.stride(0), pages_allocated.data_ptr(), slot_arr, _ptr(slots_dev),
+            self.stream), "step_plan_run_append")
         return out
+
+
+def _check_new_rows(who: str, k_new, v_new, shape, dev) -> None:
+    """k_new / v_new: the appended token's rows, contiguous bf16 ``shape`` on dev."""
+    for t in (k_new, v_new):
+        if (not isinstance(t, torch.Tensor) or t.dtype != torch.bfloat16
+                or t.shape != shape or t.device != dev or not t.is_contiguous()):
+            raise ValueError(f"{who}: k_new / v_new must be contiguous bfloat16 "
+                             f"{tuple(shape)} on {dev}")
+
+
+def _append_slots(who: str, slots, B: int, dev):
+    """(host ctypes array, device tensor) of an append's 2 * B slot entries:
+    a host sequence of (context length before the append, block to allocate
+    or -1) per sequence, or the same in a contiguous int32 [B, 2] tensor on
+    dev; exactly one of the two is returned non-None."""
+    if isinstance(slots, torch.Tensor):
+        if (slots.dtype != torch.int32 or slots.shape != (B, 2)
+                or not slots.is_contiguous() or slots.device != dev):
+            raise ValueError(f"{who}: device slots must be a contiguous int32 "
+                             f"({B}, 2) tensor on {dev}")
+        return None, slots
+    if slots is None or len(slots) != 2 * B:
+        raise ValueError(f"{who}: {2 * B} slot entries expected")
+    if isinstance(slots, ctypes.Array) and slots._type_ is ctypes.c_int32:
+        return slots, None
+    return (ctypes.c_int32 * (2 * B))(*slots), None
+
+
+def _check_pages_allocated(who: str, pages_allocated, B: int, dev) -> None:
+    if (not isinstance(pages_allocated, torch.Tensor) or pages_allocated.dtype != torch.int32
+            or pages_allocated.shape != (B,) or pages_allocated.device != dev
+            or not pages_allocated.is_contiguous()):
+        raise ValueError(f"{who}: pages_allocated must be a contiguous int32 ({B},) tensor "
+                         f"on {dev}")
 
 
 def _flat_selection(page_indices: torch.Tensor, n_per_head: torch.Tensor, num_kv_heads: int):
@@ -862,23 +917,8 @@ def sparse_decode_append(q, k_cache, v_cache, block_tables, context_lens, page_i
     B, H_q, D = q.shape
     if k_cache.shape[1] != block_size or k_cache.shape[3] != D:
         raise ValueError("sparse_decode_append: cache block_size / head_dim mismatch")
-    shape = (B, num_kv_heads, D)
-    if (k_new.dtype != torch.bfloat16 or v_new.dtype != torch.bfloat16
-            or tuple(k_new.shape) != shape or tuple(v_new.shape) != shape
-            or not (k_new.is_contiguous() and v_new.is_contiguous())):
-        raise ValueError(f"sparse_decode_append: k_new / v_new must be contiguous bfloat16 "
-                         f"{shape}")
-    slot_arr = slot_dev = None
-    if isinstance(slots, torch.Tensor):
-        if (slots.dtype != torch.int32 or tuple(slots.shape) != (B, 2)
-                or not slots.is_contiguous() or slots.device != dev):
-            raise ValueError(f"sparse_decode_append: device slots must be a contiguous int32 "
-                             f"({B}, 2) tensor on {dev}")
-        slot_dev = slots
-    elif len(slots) != 2 * B:
-        raise ValueError(f"sparse_decode_append: {2 * B} slot entries expected")
-    else:
-        slot_arr = slots if isinstance(slots, ctypes.Array) else (ctypes.c_int32 * (2 * B))(*slots)
+    _check_new_rows("sparse_decode_append", k_new, v_new, (B, num_kv_heads, D), dev)
+    slot_arr, slot_dev = _append_slots("sparse_decode_append", slots, B, dev)
     W = block_tables.shape[1]
     L = _lib.load()
     need = L.cvsa_decode_workspace_bytes(B, H_q, num_kv_heads, D, k, W, 0)

@@ -16,23 +16,35 @@ for the layers whose call ran a coverage gate.
 The reference collects the pages with one host read per KV head; here each
 layer call gathers them on the device and reads them once.
 
-``trace_result`` / ``save_traces_json`` / ``load_traces_json`` hold a run's
-traces in the reference's result layout (collect_page_traces.py:433-476:
-method, model, block_size, num_layers, num_kv_heads, task, max_steps and a
-list of samples with seq_len, n_pages, n_steps, traces and optional
-rich_traces) as JSON instead of a pickle; layer keys, which JSON stores as
-strings, are turned back into ints on loading.
+``trace_result`` builds one method's result in the reference's layout
+(collect_page_traces.py:433-476: method, model, block_size, num_layers,
+num_kv_heads, task, max_steps and a list of samples with sample_idx,
+seq_len, n_pages, n_steps, traces and optional rich_traces).
+``save_traces_pickle`` writes a run's results the way the reference's
+collector does (collect_page_traces.py:466-478): ``{method}.pkl`` per method
+and ``all_traces.pkl`` with every method, so the reference's readers
+(eval/plot_recovery_heatmap.py:97-114) open them unchanged.  The files hold
+only dicts, lists, ints, floats, strs, bools and None; ``save_traces_pickle``
+refuses anything else, and ``load_traces_pickle`` reads them back with an
+unpickler that refuses every global, so loading one executes nothing.
+``save_traces_json`` / ``load_traces_json`` keep the same layout as JSON;
+layer keys, which JSON stores as strings, are turned back into ints on
+loading.
 """
 from __future__ import annotations
 
+import io
 import json
+import os
+import pickle
 from typing import Dict, List, Optional
 
 import torch
 
 from .runtime.dense import DenseAttentionBackend
 
-__all__ = ["TracingWrapper", "trace_result", "save_traces_json", "load_traces_json"]
+__all__ = ["TracingWrapper", "trace_result", "save_traces_json", "load_traces_json",
+           "save_traces_pickle", "load_traces_pickle"]
 
 
 def _n_valid(context_lens: torch.Tensor, block_size: int) -> int:
@@ -157,3 +169,67 @@ def load_traces_json(path: str):
             if "rich_traces" in s:
                 s["rich_traces"] = _int_keys(s["rich_traces"])
     return data
+
+
+_PLAIN_SCALARS = (bool, int, float, str, type(None))
+
+
+def _check_plain(obj, where: str = "result") -> None:
+    """Raise TypeError unless obj is built from dicts, lists and scalars only
+    (tuples and torch/numpy values would pickle as globals)."""
+    if type(obj) in _PLAIN_SCALARS:
+        return
+    if type(obj) is list:
+        for i, v in enumerate(obj):
+            _check_plain(v, f"{where}[{i}]")
+        return
+    if type(obj) is dict:
+        for k, v in obj.items():
+            if type(k) not in _PLAIN_SCALARS:
+                raise TypeError(f"{where}: key {k!r} of type {type(k).__name__}")
+            _check_plain(v, f"{where}[{k!r}]")
+        return
+    raise TypeError(f"{where}: value of type {type(obj).__name__} is not a plain "
+                    "dict/list/int/float/str/bool/None")
+
+
+def save_traces_pickle(out_dir: str, results: Dict[str, dict]) -> List[str]:
+    """Write ``{method}.pkl`` for every ``{method: result}`` entry and
+    ``all_traces.pkl`` with all of them into out_dir (created if missing),
+    as collect_page_traces.py:466-478 does; returns the paths written."""
+    if not isinstance(results, dict) or not results:
+        raise ValueError("results must be a non-empty {method: result} dict")
+    for method, res in results.items():
+        if not isinstance(method, str) or not method or os.sep in method:
+            raise ValueError(f"method name {method!r} is not a file name")
+        if not isinstance(res, dict) or res.get("method") != method:
+            raise ValueError(f"result of {method!r} must be a trace_result dict "
+                             "whose 'method' is that name")
+        _check_plain(res, method)
+    os.makedirs(out_dir, exist_ok=True)
+    paths = []
+    for method, res in results.items():
+        path = os.path.join(out_dir, f"{method}.pkl")
+        with open(path, "wb") as f:
+            pickle.dump(res, f)
+        paths.append(path)
+    path = os.path.join(out_dir, "all_traces.pkl")
+    with open(path, "wb") as f:
+        pickle.dump(dict(results), f)
+    paths.append(path)
+    return paths
+
+
+class _PlainUnpickler(pickle.Unpickler):
+    """An unpickler that loads no class or function at all."""
+
+    def find_class(self, module, name):
+        raise pickle.UnpicklingError(f"trace files hold no globals ({module}.{name})")
+
+
+def load_traces_pickle(path: str):
+    """Read a ``{method}.pkl`` or ``all_traces.pkl``; refuses any file that
+    names a global (class, function), so nothing in it is executed."""
+    with open(path, "rb") as f:
+        data = f.read()
+    return _PlainUnpickler(io.BytesIO(data)).load()
