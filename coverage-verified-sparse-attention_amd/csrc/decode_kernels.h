@@ -37,7 +37,10 @@
 // all-pages head walks pages 0..n_valid-1 (dense decode).  In verified mode
 // accepted heads are listed and rejected heads walk every valid page: the
 // draft pages plus the complement pages in one pass, which equals the LSE
-// merge of the draft and complement partial softmaxes.
+// merge of the draft and complement partial softmaxes.  In approximate
+// mode rejected heads walk their expanded selection instead
+// (cvsa/backend.py:780-812: an expanded top-k at approx_recovery_pct of the
+// pages, decoded and normalised on its own).
 //
 // Tiles: the kernels walk 16-token tiles.  A page (block) of block_size =
 // 16 * 2^ts tokens is 2^ts consecutive tiles of its block, so tile sub of
@@ -100,6 +103,12 @@ struct DecodeArgs {
   // would (q_rep the group mean of q_group heads times inv_g).
   float *spec_scores;
   float inv_g;
+  // Approximate recovery (kModeApprox): a rejected head walks the first
+  // min(alt_budget, n_valid) pages of its expanded selection alt_idx[bh]
+  // instead of every valid page.
+  const int32_t *alt_idx;
+  int64_t alt_stride;
+  int alt_budget;
 };
 
 // A reuse step's token append folded into its listed decode
@@ -197,24 +206,40 @@ __device__ __forceinline__ int tile_block(const DecodeArgs &a, int b, int lt, in
 // n_per_head[bh] unconditionally and picks with selects: an earlier form
 // that branched on null pointers was miscompiled (a live scalar register was
 // reused across the branch).
-enum { kModeAll = 0, kModeListed = 1, kModeVerified = 2 };
+enum { kModeAll = 0, kModeListed = 1, kModeVerified = 2, kModeApprox = 3 };
+// Page lists of a head's walk: every valid page, page_indices, alt_idx.
+enum { kWalkAll = 0, kWalkListed = 1, kWalkAlt = 2 };
 
 template <int MODE>
-__device__ __forceinline__ int head_pages(const DecodeArgs &a, int bh, bool &listed, int ts) {
+__device__ __forceinline__ int head_pages(const DecodeArgs &a, int bh, int &walk, int ts) {
   int n_all = 0, n_list = 0;
   if constexpr (MODE != kModeListed)
     n_all = max(0, min(valid_pages_ts(a.ctx_lens[bh / a.H_kv], ts), a.W)) << ts;
   if constexpr (MODE != kModeAll) n_list = min(max(a.n_pages[bh], 0), a.max_sel) << ts;
   if constexpr (MODE == kModeAll) {
-    listed = false;
+    walk = kWalkAll;
     return n_all;
   } else if constexpr (MODE == kModeListed) {
-    listed = true;
+    walk = kWalkListed;
     return n_list;
+  } else if constexpr (MODE == kModeVerified) {
+    const bool acc = a.accept[bh] != 0;
+    walk = acc ? kWalkListed : kWalkAll;
+    return acc ? n_list : n_all;
   } else {
-    listed = a.accept[bh] != 0;
-    return listed ? n_list : n_all;
+    const bool acc = a.accept[bh] != 0;
+    const int n_alt = min(a.alt_budget << ts, n_all);
+    walk = acc ? kWalkListed : kWalkAlt;
+    return acc ? n_list : n_alt;
   }
+}
+
+// Pages booked in the effective-budget counters for head bh of an
+// approximate-recovery launch in which some head was rejected
+// (backend.py:812-850: the draft's n_per_head plus the expanded
+// selection's min(exp_budget, n_valid) on every head).
+__device__ __forceinline__ int approx_booked_pages(const DecodeArgs &a, int bh, int nv) {
+  return min(max(a.n_pages[bh], 0), a.max_sel) + min(a.alt_budget, max(0, nv));
 }
 
 // Stream-K partition.  The heads' page walks are concatenated (head-major)
@@ -1042,7 +1067,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   __shared__ int s_wsum[NW];
   __shared__ int s_odd[NW];               // a head of the wave's pass walks != max_sel pages
   __shared__ int s_start[kMaxHeads + 1];  // exclusive prefix of pages per head
-  __shared__ uint8_t s_listed[kMaxHeads];
+  __shared__ uint8_t s_listed[kMaxHeads];  // kWalk* of each head
   auto &s_o = L.o;
   auto &s_m = L.m;
   auto &s_l = L.l;
@@ -1071,7 +1096,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   // select-or-keep booked that decode's effective-budget counters.  Every
   // head accepted does not imply a kept selection: a rejected head is
   // reselected and accepted when the new selection passes its gate.
-  if constexpr (MODE == kModeVerified) {
+  if constexpr (MODE == kModeVerified || MODE == kModeApprox) {
     const int n_listed = a.n_splits * heads;
     const int split = w % max(a.n_splits, 1);
     const int bh = min(w / max(a.n_splits, 1), heads - 1);
@@ -1129,14 +1154,17 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   // without a branch, index clamped), scanned into their exclusive prefix
   // in s_start.
   auto wave_incl_scan = [&](int c) { return (int)wave_incl_scan_u32((uint32_t)c); };
-  bool l_first = false;
+  // A head walking its expanded selection never takes the speculated
+  // partition, whose first pages come from page_indices.
+  int l_first = kWalkAll;
   int c_first = head_pages<MODE>(a, min((int)threadIdx.x, heads - 1), l_first, ts);
   if constexpr (MODE != kModeAll)
     spec_phys = tile_block(a, b_spec, spec_lp, ts);
   if ((int)threadIdx.x >= heads) c_first = 0;
   const int incl_first = wave_incl_scan(c_first);
   if (lane == kWave - 1) s_wsum[wave] = incl_first;
-  const bool odd_first = __ballot((int)threadIdx.x < heads && c_first != max_sel_t) != 0;
+  const bool odd_first =
+      __ballot((int)threadIdx.x < heads && (c_first != max_sel_t || l_first == kWalkAlt)) != 0;
   if (lane == 0) s_odd[wave] = odd_first ? 1 : 0;
 
   // One wave's walk over its pages s0 + wave + NW*j of a segment, in chunks
@@ -1204,7 +1232,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   // Pass 0 (peeled: a loop header here makes the compiler wait for the
   // speculative loads), then the passes of launches with more than NT heads.
   int uneven = 0;  // some head walks a number of pages other than max_sel
-  auto finish_pass = [&](int hh, int c, int incl, bool lst, int &carry) {
+  auto finish_pass = [&](int hh, int c, int incl, int lst, int &carry) {
     lds_barrier();
     int excl = incl - c, total = 0;
 #pragma unroll
@@ -1215,7 +1243,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     }
     if (hh < heads) {
       s_start[hh] = carry + excl;
-      s_listed[hh] = lst;
+      s_listed[hh] = (uint8_t)lst;
     }
     carry += total;
     lds_barrier();  // s_wsum is rewritten by the next pass
@@ -1225,12 +1253,12 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   if (heads > NT) {  // uniform
     for (int base = NT; base < heads; base += NT) {
       const int hh = base + threadIdx.x;
-      bool lst = false;
+      int lst = kWalkAll;
       int c = head_pages<MODE>(a, min(hh, heads - 1), lst, ts);
       if (hh >= heads) c = 0;
       const int incl = wave_incl_scan(c);
       if (lane == kWave - 1) s_wsum[wave] = incl;
-      const bool odd = __ballot(hh < heads && c != max_sel_t) != 0;
+      const bool odd = __ballot(hh < heads && (c != max_sel_t || lst == kWalkAlt)) != 0;
       if (lane == 0) s_odd[wave] = odd ? 1 : 0;
       finish_pass(hh, c, incl, lst, carry);
     }
@@ -1253,8 +1281,10 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     const int64_t row0 = (int64_t)hh * a.q_group + a.q_off;
     for (int i = threadIdx.x; i < G * D; i += NT)
       write_outputs<D>(a, row0 + i / D, i % D, 0.f, -INFINITY, 0.f);
-    if (threadIdx.x == 0 && a.work != nullptr)
-      add_work(a, 0, valid_pages_ts(a.ctx_lens[hh / a.H_kv], ts));
+    if (threadIdx.x == 0 && a.work != nullptr) {
+      const int nv = valid_pages_ts(a.ctx_lens[hh / a.H_kv], ts);
+      add_work(a, MODE == kModeApprox ? approx_booked_pages(a, hh, nv) : 0, nv);
+    }
   }
   if (T == 0) return;
 
@@ -1282,11 +1312,14 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     const int s0 = max(g0, P) - P, s1 = min(g1, P + n) - P;
     const int b = h / a.H_kv;
     const int hk = h - b * a.H_kv;
-    const bool listed = s_listed[h] != 0;
+    const int walk = s_listed[h];
+    const bool listed = walk != kWalkAll;
     const bool on_spec = h == h_spec;  // eng, ctx_spec already belong to this head
     const int ctx = on_spec ? ctx_spec : __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
-    const int32_t *idx_row = a.page_idx + (int64_t)h * a.idx_stride;
-    const bool use_spec = spec_ok && on_spec && s0 == r_spec && listed;
+    const int32_t *idx_row = MODE == kModeApprox && walk == kWalkAlt
+                                 ? a.alt_idx + (int64_t)h * a.alt_stride
+                                 : a.page_idx + (int64_t)h * a.idx_stride;
+    const bool use_spec = spec_ok && on_spec && s0 == r_spec && walk == kWalkListed;
 
     if (!on_spec || h != lo) eng.init(a, b, hk, lane, s_eng[wave]);
     cur_ctx = ctx;
@@ -1303,7 +1336,9 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     __syncthreads();
 
     const int first = part.owner(P);
-    segment_epilogue<G, D, NW, kMergeBatchStreamK>(a, pb, h, n >> ts, valid_pages_ts(ctx, ts),
+    const int nv = valid_pages_ts(ctx, ts);
+    const int booked = MODE == kModeApprox ? approx_booked_pages(a, h, nv) : n >> ts;
+    segment_epilogue<G, D, NW, kMergeBatchStreamK>(a, pb, h, booked, nv,
                                part.owner(P + n - 1) - first + 1, (uint32_t)(w + h),
                                (uint32_t)(first + h), s_o, s_m, s_l, s_last, s_tail.merge);
     __syncthreads();  // LDS is reused by the next segment
@@ -1321,7 +1356,7 @@ constexpr int kWavesPerWg = 4;
 // four group sizes, so the library's objects compile in parallel).  Pages of
 // K/V in flight per wave: 2, or 1 at D = 256, whose pages hold twice the
 // registers.
-enum { kLaunchListed = 0, kLaunchVerified = 1, kLaunchAll = 2 };
+enum { kLaunchListed = 0, kLaunchVerified = 1, kLaunchAll = 2, kLaunchApprox = 3 };
 
 template <int G, int D, int TS>
 void launch_decode_gdt(const DecodeArgs &a, int kind, dim3 grid, dim3 block, hipStream_t st) {
@@ -1331,6 +1366,9 @@ void launch_decode_gdt(const DecodeArgs &a, int kind, dim3 grid, dim3 block, hip
     hipLaunchKernelGGL((listed_decode_kernel<G, E, kWavesPerWg, PD>), grid, block, 0, st, a);
   else if (kind == kLaunchVerified)
     hipLaunchKernelGGL((streamk_decode_kernel<G, E, kWavesPerWg, PD, kModeVerified>), grid,
+                       block, 0, st, a);
+  else if (kind == kLaunchApprox)
+    hipLaunchKernelGGL((streamk_decode_kernel<G, E, kWavesPerWg, PD, kModeApprox>), grid,
                        block, 0, st, a);
   else
     hipLaunchKernelGGL((streamk_decode_kernel<G, E, kWavesPerWg, PD, kModeAll>), grid, block, 0,

@@ -154,6 +154,14 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
                  CVSA_ERR_INVALID, "%s: bad selection width %d (row stride %lld)", name,
                  a.max_sel, (long long)a.idx_stride);
   }
+  if (a.alt_idx != nullptr) {
+    CVSA_REQUIRE(listed && a.accept != nullptr, CVSA_ERR_INVALID,
+                 "%s: an expanded selection needs accept flags", name);
+    CVSA_REQUIRE(a.alt_budget >= 1 && a.alt_budget <= W && a.alt_stride >= a.alt_budget,
+                 CVSA_ERR_INVALID,
+                 "%s: expanded budget %d must be in [1, W=%d] with a row stride >= it (%lld)",
+                 name, a.alt_budget, W, (long long)a.alt_stride);
+  }
   const bool want_unnorm = a.o_unnorm || a.m_out || a.l_out;
   CVSA_REQUIRE(!want_unnorm || (a.o_unnorm && a.m_out && a.l_out), CVSA_ERR_INVALID,
                "%s: o_unnorm, m_out and l_out must be given together", name);
@@ -200,7 +208,10 @@ static int enqueue_decode(const char *name, DecodeArgs a, int G, bool listed,
                           const DecodeLaunch &p, void *workspace, size_t need, hipStream_t st) {
   bind_workspace(a, workspace, need);
   const dim3 grid(p.grid_x, p.grid_y), block(kWavesPerWg * kWave);
-  const int kind = !p.streamk ? kLaunchListed : listed ? kLaunchVerified : kLaunchAll;
+  const int kind = !p.streamk ? kLaunchListed
+                   : !listed   ? kLaunchAll
+                   : a.alt_idx != nullptr ? kLaunchApprox
+                                          : kLaunchVerified;
   // Groups of more than kMaxGroup query heads: one launch per kMaxGroup of
   // them, in order on the stream (each leaves the workspace counters at
   // zero); the first books the effective-budget counters.
@@ -623,9 +634,10 @@ int verified_decode_after_speculation(
     const uint16_t *v_cache, int64_t num_blocks, const int32_t *block_tables,
     int64_t bt_stride_b, const int32_t *context_lens, const int32_t *page_indices,
     int64_t idx_stride, const int32_t *n_per_head, int32_t max_selected, const uint8_t *accept,
-    int32_t B, int32_t H_q, int32_t H_kv, int32_t D, int32_t block_size, int32_t W, void *out,
-    int32_t out_dtype, int64_t *work, int32_t *spec_state, void *workspace,
-    size_t workspace_bytes, void *stream) {
+    const int32_t *exp_indices, int64_t exp_stride, int32_t exp_budget, int32_t B, int32_t H_q,
+    int32_t H_kv, int32_t D, int32_t block_size, int32_t W, void *out, int32_t out_dtype,
+    int64_t *work, int32_t *spec_state, void *workspace, size_t workspace_bytes,
+    void *stream) {
   DecodeArgs a = base_args(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
                            block_tables, bt_stride_b, context_lens, nullptr, nullptr, nullptr,
                            out, out_dtype, work);
@@ -635,8 +647,11 @@ int verified_decode_after_speculation(
   a.n_pages = n_per_head;
   a.accept = accept;
   a.spec_state = spec_state;
-  CVSA_REQUIRE(page_indices && accept && spec_state, CVSA_ERR_INVALID,
-               "verified decode: page_indices, accept and spec_state are required");
+  a.alt_idx = exp_indices;
+  a.alt_stride = exp_stride;
+  a.alt_budget = exp_budget;
+  CVSA_REQUIRE(page_indices && accept, CVSA_ERR_INVALID,
+               "verified decode: page_indices and accept are required");
   return launch_decode("verified_decode", a, B, H_q, H_kv, D, block_size, W, true, true,
                        workspace, workspace_bytes, (hipStream_t)stream);
 }
@@ -682,5 +697,33 @@ extern "C" int cvsa_verified_decode(const uint16_t *q, int64_t q_stride_b,
     return cvsa_host::fail(CVSA_ERR_INVALID,
                            "verified_decode: page_indices and accept are required");
   return launch_decode("verified_decode", a, B, H_q, H_kv, D, block_size, W, true, true,
+                       workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int cvsa_verified_decode_approx(
+    const uint16_t *q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t *k_cache,
+    const uint16_t *v_cache, int64_t num_blocks, const int32_t *block_tables,
+    int64_t bt_stride_b, const int32_t *context_lens, const int32_t *page_indices,
+    int64_t idx_stride, const int32_t *n_per_head, int32_t max_selected, const uint8_t *accept,
+    const int32_t *exp_indices, int64_t exp_stride, int32_t exp_budget, int32_t B, int32_t H_q,
+    int32_t H_kv, int32_t D, int32_t block_size, int32_t W, float *o_unnorm, float *m_out,
+    float *l_out, void *out, int32_t out_dtype, int64_t *work, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  DecodeArgs a = base_args(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                           block_tables, bt_stride_b, context_lens, o_unnorm, m_out, l_out,
+                           out, out_dtype, work);
+  a.page_idx = page_indices;
+  a.idx_stride = idx_stride;
+  a.max_sel = max_selected;
+  a.n_pages = n_per_head;
+  a.accept = accept;
+  a.alt_idx = exp_indices;
+  a.alt_stride = exp_stride;
+  a.alt_budget = exp_budget;
+  if (page_indices == nullptr || accept == nullptr || exp_indices == nullptr)
+    return cvsa_host::fail(CVSA_ERR_INVALID,
+                           "verified_decode_approx: page_indices, accept and exp_indices are "
+                           "required");
+  return launch_decode("verified_decode_approx", a, B, H_q, H_kv, D, block_size, W, true, true,
                        workspace, workspace_bytes, (hipStream_t)stream);
 }

@@ -265,7 +265,8 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
     long long *__restrict__ stats, int count_gate, int32_t *__restrict__ keep_flag,
     uint8_t *__restrict__ sel_map, int64_t map_stride,
-    unsigned long long *__restrict__ keep_work) {
+    unsigned long long *__restrict__ keep_work, int exp_budget,
+    int32_t *__restrict__ exp_indices) {
   __shared__ uint32_t hist[256];
   __shared__ uint32_t hist_c[kHistCopies * kHistStride];
   __shared__ uint32_t hist_b[kBuckets];
@@ -274,7 +275,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   __shared__ uint32_t red_rng[kSelWaves][3];
   __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2];
   __shared__ uint32_t s_digit, s_krem, s_T, s_bucket, s_kb, s_nb, s_ncand;
-  __shared__ int s_nok, s_nbad;
+  __shared__ int s_nok, s_nbad, s_acc;
   // Top-p only: softmax mass per value bucket (64-bit fixed point, so the
   // sums do not depend on the order of the atomic adds).
   __shared__ unsigned long long mass_b[MODE == kTopP ? kBuckets : 1];
@@ -618,128 +619,143 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   if constexpr (MODE == kTable) k = min(max(row_budgets[bh], 1), W);
   if constexpr (MODE == kTopP) k = topp_budget(hist_ready);
   k = min(k, width);  // a row holds at most `width` pages: the best ones
-  // plan 0: T and krem found; 1: radix select over the row; 2: radix
-  // select of the k_radix-th largest inside bucket bstar.
-  uint32_t T = 0, krem = 0, k_radix = (uint32_t)k;
-  int plan = 1, bstar = -1;
-  if (n_odd == 0 && (uint32_t)k > n_fin) {
-    // Every finite page, then the lowest -inf pages.
-    T = order_key(-INFINITY);
-    krem = (uint32_t)k - n_fin;
-    plan = 0;
-  } else if (n_odd == 0 && kmin == kmax) {
-    T = kmax;
-    krem = (uint32_t)k;
-    plan = 0;
-  } else if (n_odd == 0) {
-    vmin = key_value(kmin);
-    inv = (float)kBuckets / (key_value(kmax) - vmin);
-    // Otherwise max - min overflows.
-    if (inv > 0.f && inv <= 3.402823466e38f) {
-      if (!hist_ready) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const int bk = bucket(r);
-          if (bk >= 0) atomicAdd(&hist_b[bk], 1u);
-        }
-      }
-      lds_barrier();
-      // Thread t holds buckets kBuckets-1-(4t+j), j = 0..3: the exclusive
-      // scan over threads counts the scores in higher buckets.
-      uint32_t c[kBucketsPerThread], local = 0;
-#pragma unroll
-      for (int j = 0; j < kBucketsPerThread; ++j) {
-        c[j] = hist_b[kBuckets - 1 - (kBucketsPerThread * t + j)];
-        local += c[j];
-      }
-      uint32_t total_b;
-      uint32_t above = block_exclusive_scan(local, wsum, total_b);
-#pragma unroll
-      for (int j = 0; j < kBucketsPerThread; ++j) {
-        if (above < (uint32_t)k && above + c[j] >= (uint32_t)k) {
-          s_bucket = (uint32_t)(kBuckets - 1 - (kBucketsPerThread * t + j));
-          s_kb = (uint32_t)k - above;
-          s_nb = c[j];
-        }
-        above += c[j];
-      }
-      lds_barrier();
-      bstar = (int)s_bucket;
-      const uint32_t kb = s_kb, nb = s_nb;
-      // The buckets are recomputed below rather than kept live across the
-      // scan (same operands, same bits).
-      asm volatile("" : "+v"(vmin), "+v"(inv));
-      if (nb <= (uint32_t)kRankCands) {
-        // Rank the bucket's scores: T is the key with gt < kb <= gt + eq.
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-          if (bucket(r) == bstar) s_cand[atomicAdd(&s_ncand, 1u)] = order_key(val[r]);
-        lds_barrier();
-        if (t < kWave) {
-          const uint32_t mine = t < (int)nb ? s_cand[t] : 0u;
-          uint32_t gt = 0, eq = 0;
-          for (uint32_t j = 0; j < nb; ++j) {
-            const uint32_t o = s_cand[j];
-            gt += o > mine;
-            eq += o == mine;
-          }
-          if (t < (int)nb && gt < kb && kb <= gt + eq) {
-            s_T = mine;
-            s_krem = kb - gt;
-          }
-        }
-        lds_barrier();
-        T = s_T;
-        krem = s_krem;
-        plan = 0;
-      } else {
-        plan = 2;
-        k_radix = kb;
-      }
-    }
-  }
-  if (plan != 0) {
-    const auto alive = [&](int r) { return i0 + r < W && (plan == 1 || bucket(r) == bstar); };
-    radix_select<R>(val, alive, k_radix, hist, hist_c, &s_digit, &s_krem, T, krem);
-  }
 
-  // ---- ascending-order compaction; ties at T go to the lowest pages
-  uint32_t gt = 0, eq = 0;
+  // The kk-th largest key T and krem = kk - #(keys > T).  Plan 0: T and
+  // krem found directly; 1: radix select over the row; 2: radix select of
+  // the k_radix-th largest inside bucket bstar.  Called a second time for
+  // the expanded selection of approximate recovery (its bucket counts are
+  // those of the first call).
+  const auto threshold = [&](int kk, uint32_t &T, uint32_t &krem) __attribute__((always_inline)) {
+    uint32_t k_radix = (uint32_t)kk;
+    int plan = 1, bstar = -1;
+    if (n_odd == 0 && (uint32_t)kk > n_fin) {
+      // Every finite page, then the lowest -inf pages.
+      T = order_key(-INFINITY);
+      krem = (uint32_t)kk - n_fin;
+      plan = 0;
+    } else if (n_odd == 0 && kmin == kmax) {
+      T = kmax;
+      krem = (uint32_t)kk;
+      plan = 0;
+    } else if (n_odd == 0) {
+      vmin = key_value(kmin);
+      inv = (float)kBuckets / (key_value(kmax) - vmin);
+      // Otherwise max - min overflows.
+      if (inv > 0.f && inv <= 3.402823466e38f) {
+        if (!hist_ready) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if (i0 + r < W) {
-      const uint32_t key = order_key(val[r]);
-      gt += key > T;
-      eq += key == T;
-    }
-  }
-  uint32_t total;
-  const uint32_t excl = block_exclusive_scan(gt | (eq << 16), wsum, total);
-  const uint32_t gt_before = excl & 0xFFFFu, eq_before = excl >> 16;
-  const int n_write = k;
-  const int n_sel = min(k, n_valid_pages(ctx, block_size));
-  uint32_t eq_seen = eq_before;
-  uint32_t pos = gt_before + min(eq_before, krem);
-  int32_t *out_row = page_indices + (int64_t)bh * width;
-  bool counted[R];
+          for (int r = 0; r < R; ++r) {
+            const int bk = bucket(r);
+            if (bk >= 0) atomicAdd(&hist_b[bk], 1u);
+          }
+          hist_ready = true;
+        }
+        lds_barrier();
+        // Thread t holds buckets kBuckets-1-(4t+j), j = 0..3: the exclusive
+        // scan over threads counts the scores in higher buckets.
+        uint32_t c[kBucketsPerThread], local = 0;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    bool sel = false;
-    const uint32_t key = order_key(val[r]);
-    if (i0 + r < W) {
-      if (key > T) {
-        sel = true;
-      } else if (key == T) {
-        sel = eq_seen < krem;
-        ++eq_seen;
+        for (int j = 0; j < kBucketsPerThread; ++j) {
+          c[j] = hist_b[kBuckets - 1 - (kBucketsPerThread * t + j)];
+          local += c[j];
+        }
+        uint32_t total_b;
+        uint32_t above = block_exclusive_scan(local, wsum, total_b);
+#pragma unroll
+        for (int j = 0; j < kBucketsPerThread; ++j) {
+          if (above < (uint32_t)kk && above + c[j] >= (uint32_t)kk) {
+            s_bucket = (uint32_t)(kBuckets - 1 - (kBucketsPerThread * t + j));
+            s_kb = (uint32_t)kk - above;
+            s_nb = c[j];
+          }
+          above += c[j];
+        }
+        lds_barrier();
+        bstar = (int)s_bucket;
+        const uint32_t kb = s_kb, nb = s_nb;
+        // The buckets are recomputed below rather than kept live across the
+        // scan (same operands, same bits).
+        asm volatile("" : "+v"(vmin), "+v"(inv));
+        if (nb <= (uint32_t)kRankCands) {
+          // Rank the bucket's scores: T is the key with gt < kb <= gt + eq.
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+            if (bucket(r) == bstar) s_cand[atomicAdd(&s_ncand, 1u)] = order_key(val[r]);
+          lds_barrier();
+          if (t < kWave) {
+            const uint32_t mine = t < (int)nb ? s_cand[t] : 0u;
+            uint32_t gt = 0, eq = 0;
+            for (uint32_t j = 0; j < nb; ++j) {
+              const uint32_t o = s_cand[j];
+              gt += o > mine;
+              eq += o == mine;
+            }
+            if (t < (int)nb && gt < kb && kb <= gt + eq) {
+              s_T = mine;
+              s_krem = kb - gt;
+            }
+            if (t == 0) s_ncand = 0;  // every lane has read nb candidates
+          }
+          lds_barrier();
+          T = s_T;
+          krem = s_krem;
+          plan = 0;
+        } else {
+          plan = 2;
+          k_radix = kb;
+        }
       }
     }
-    counted[r] = sel && (int)pos < n_sel;
-    if (sel) {
-      if ((int)pos < n_write) out_row[pos] = i0 + r;  // pos < k for a correct select
-      ++pos;
+    if (plan != 0) {
+      const auto alive = [&](int r) { return i0 + r < W && (plan == 1 || bucket(r) == bstar); };
+      radix_select<R>(val, alive, k_radix, hist, hist_c, &s_digit, &s_krem, T, krem);
     }
-  }
+  };
+
+  // Ascending-order compaction of the selection (T, krem): the first
+  // n_write entries into out_row; ties at T go to the lowest pages.  Sets
+  // in[r] for this thread's pages among the first n_sel entries.
+  const auto compact = [&](uint32_t T, uint32_t krem, int n_write, int n_sel, int32_t *out_row,
+                           bool (&in)[R]) __attribute__((always_inline)) {
+    uint32_t gt = 0, eq = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (i0 + r < W) {
+        const uint32_t key = order_key(val[r]);
+        gt += key > T;
+        eq += key == T;
+      }
+    }
+    uint32_t total;
+    const uint32_t excl = block_exclusive_scan(gt | (eq << 16), wsum, total);
+    const uint32_t gt_before = excl & 0xFFFFu, eq_before = excl >> 16;
+    uint32_t eq_seen = eq_before;
+    uint32_t pos = gt_before + min(eq_before, krem);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      bool sel = false;
+      const uint32_t key = order_key(val[r]);
+      if (i0 + r < W) {
+        if (key > T) {
+          sel = true;
+        } else if (key == T) {
+          sel = eq_seen < krem;
+          ++eq_seen;
+        }
+      }
+      in[r] = sel && (int)pos < n_sel;
+      if (sel) {
+        if ((int)pos < n_write) out_row[pos] = i0 + r;  // pos < kk for a correct select
+        ++pos;
+      }
+    }
+  };
+
+  uint32_t T = 0, krem = 0;
+  threshold(k, T, krem);
+  const int n_sel = min(k, n_valid_pages(ctx, block_size));
+  bool counted[R];
+  compact(T, krem, k, n_sel, page_indices + (int64_t)bh * width, counted);
   if (t == 0) n_per_head[bh] = n_sel;
   if (sel_map != nullptr) {
     // The row's selection map: this thread's pages i0 .. i0 + R - 1.
@@ -785,6 +801,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     const int acc = cov >= tau ? 1 : 0;
     coverage_out[bh] = cov;
     accept_out[bh] = (uint8_t)acc;
+    s_acc = acc;
     if (stats != nullptr && count_gate) {
       // Fixed-interval scoring step (backend.py:859-863): tally this head,
       // then the last head of the call books the step as all-accepted or
@@ -813,6 +830,21 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
         __hip_atomic_store(&stats[5], 0LL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
+  }
+
+  // Approximate recovery (cvsa/backend.py:780-799): a row whose new
+  // selection failed its gate also gets the exp_budget largest ranking
+  // scores, in ascending page order, as its expanded selection (the
+  // reference ranks every row; only rejected rows attend theirs).
+  if constexpr (MODE == kUniform) {
+    if (exp_indices == nullptr) return;  // uniform
+    lds_barrier();
+    if (s_acc != 0) return;  // uniform
+    const int k2 = min(exp_budget, W);
+    uint32_t T2 = 0, krem2 = 0;
+    threshold(k2, T2, krem2);
+    bool in2[R];
+    compact(T2, krem2, k2, k2, exp_indices + (int64_t)bh * exp_budget, in2);
   }
 }
 
@@ -1025,7 +1057,8 @@ static int launch_select(const char *name, const float *page_scores, const float
                          void *stream, int mode = kUniform, float top_p = 0.f,
                          const int32_t *row_budgets = nullptr, int32_t *keep_flag = nullptr,
                          uint8_t *sel_map = nullptr, int64_t map_stride = 0,
-                         int64_t *keep_work = nullptr) {
+                         int64_t *keep_work = nullptr, int32_t exp_budget = 0,
+                         int32_t *exp_indices = nullptr) {
   CVSA_REQUIRE(page_scores && context_lens && page_indices && n_per_head, CVSA_ERR_INVALID,
                "%s: null pointer argument", name);
   CVSA_REQUIRE((accept_out == nullptr) == (coverage_out == nullptr), CVSA_ERR_INVALID,
@@ -1045,6 +1078,12 @@ static int launch_select(const char *name, const float *page_scores, const float
                CVSA_ERR_INVALID,
                "%s: selection map rows of %lld bytes (16-byte aligned, >= W=%d) required",
                name, (long long)map_stride, W);
+  CVSA_REQUIRE(exp_indices == nullptr || (mode == kUniform && accept_out != nullptr &&
+                                          exp_budget >= 1 && exp_budget <= W),
+               CVSA_ERR_INVALID,
+               "%s: an expanded selection needs the uniform budget, the gate and an expanded "
+               "budget in [1, W=%d] (got %d)",
+               name, W, exp_budget);
   const int R = keys_per_thread(W);
   const dim3 grid(B * H_kv);
   hipStream_t st = (hipStream_t)stream;
@@ -1058,7 +1097,7 @@ static int launch_select(const char *name, const float *page_scores, const float
                      width, top_p, row_budgets, page_indices, n_per_head, tau, accept_out,  \
                      coverage_out, check_accept, B * H_kv, scores_cache, st64, count_gate,    \
                      keep_flag, sel_map, map_stride,                                         \
-                     reinterpret_cast<unsigned long long *>(keep_work))
+                     reinterpret_cast<unsigned long long *>(keep_work), exp_budget, exp_indices)
 #define CVSA_SEL_MODES(RR, SEP)                                    \
   if (mode == kTopP) CVSA_SEL_LAUNCH(RR, SEP, kTopP);              \
   else if (mode == kTable) CVSA_SEL_LAUNCH(RR, SEP, kTable);       \
@@ -1123,7 +1162,8 @@ int select_for_plan(const float *page_scores, const float *sel_scores,
                     int32_t *page_indices, int32_t *n_per_head, float tau, uint8_t *accept_out,
                     float *coverage_out, float *scores_cache, int64_t *stats,
                     int32_t count_gate, int32_t *keep_flag, uint8_t *sel_map,
-                    int64_t sel_map_stride, int64_t *keep_work, void *stream) {
+                    int64_t sel_map_stride, int64_t *keep_work, int32_t exp_budget,
+                    int32_t *exp_indices, void *stream) {
   CVSA_REQUIRE(accept_out && coverage_out, CVSA_ERR_INVALID,
                "select_or_keep: accept_out and coverage_out are required");
   CVSA_REQUIRE(keep_flag == nullptr || check_accept != nullptr, CVSA_ERR_INVALID,
@@ -1133,7 +1173,8 @@ int select_for_plan(const float *page_scores, const float *sel_scores,
   return launch_select("select_or_keep", page_scores, sel_scores, B, H_kv, W, context_lens,
                        block_size, budget, page_indices, n_per_head, tau, accept_out,
                        coverage_out, check_accept, scores_cache, stats, count_gate, stream,
-                       kUniform, 0.f, nullptr, keep_flag, sel_map, sel_map_stride, keep_work);
+                       kUniform, 0.f, nullptr, keep_flag, sel_map, sel_map_stride, keep_work,
+                       exp_budget, exp_indices);
 }
 
 __global__ __launch_bounds__(kSelThreads) void selection_map_kernel(

@@ -94,6 +94,13 @@ int check_desc(const cvsa_step_desc &d) {
                "step_plan: sel_map rows must be 16-byte aligned, a multiple of 16 bytes and "
                "at least W=%d bytes apart (got %lld)",
                d.W, (long long)d.sel_map_stride);
+  if (d.approx_budget != 0) {
+    STEP_REQUIRE(d.approx_budget >= 1 && d.approx_budget <= d.W && d.approx_indices != nullptr,
+                 CVSA_ERR_INVALID,
+                 "step_plan: approximate recovery needs approx_indices and an approx_budget in "
+                 "[1, W=%d] (got %d)",
+                 d.W, d.approx_budget);
+  }
   const size_t need = workspace_need(d);
   STEP_REQUIRE(need < ((size_t)1 << 31), CVSA_ERR_UNSUPPORTED,
                "step_plan: a decode workspace of %zu bytes exceeds the 2 GiB buffer range",
@@ -130,13 +137,17 @@ int rank(const cvsa_step_desc &d, const uint16_t *q, const uint8_t *check, void 
   return quest(d, q, check, d.sel_scores, stream);
 }
 
-int verified(const cvsa_step_desc &d, const uint16_t *q, void *out, void *stream) {
-  return cvsa_verified_decode(q, d.q_stride_b, d.q_stride_h, d.k_cache, d.v_cache,
-                              d.num_blocks, d.block_tables, d.bt_stride_b, d.context_lens,
-                              d.page_indices, d.budget, d.n_per_head, d.budget, d.accept, d.B,
-                              d.H_q, d.H_kv, d.D, d.block_size, d.W, nullptr, nullptr, nullptr,
-                              out, d.out_dtype, d.work, d.workspace, d.workspace_bytes,
-                              stream);
+// The step's verified decode (exact or approximate recovery); with
+// spec_state, after a speculative check.
+int verified(const cvsa_step_desc &d, const uint16_t *q, void *out, int32_t *spec_state,
+             void *stream) {
+  const bool ar = d.approx_budget > 0;
+  return cvsa_internal::verified_decode_after_speculation(
+      q, d.q_stride_b, d.q_stride_h, d.k_cache, d.v_cache, d.num_blocks, d.block_tables,
+      d.bt_stride_b, d.context_lens, d.page_indices, d.budget, d.n_per_head, d.budget, d.accept,
+      ar ? d.approx_indices : nullptr, d.approx_budget, d.approx_budget, d.B, d.H_q, d.H_kv,
+      d.D, d.block_size, d.W, out, d.out_dtype, d.work, spec_state, d.workspace,
+      d.workspace_bytes, stream);
 }
 
 }  // namespace
@@ -193,7 +204,8 @@ int plan_select(const cvsa_step_desc &d, const uint8_t *check, float *scores_cac
       d.page_scores, sel, check, d.B, d.H_kv, d.W, d.context_lens, d.block_size, d.budget,
       d.page_indices, d.n_per_head, d.tau, d.accept, d.coverage, scores_cache, d.stats,
       count_gate, keep_flag, plan_map(d), d.sel_map_stride,
-      keep_flag != nullptr ? d.work : nullptr, stream);
+      keep_flag != nullptr ? d.work : nullptr, d.approx_budget,
+      d.approx_budget > 0 ? d.approx_indices : nullptr, stream);
 }
 
 // The lazy check with the speculative decode: one launch scores the pages
@@ -229,11 +241,7 @@ int speculative_check(cvsa_step_plan &p, const uint16_t *q, void *out, void *str
   if ((rc = plan_select(d, d.check_accept, d.scores_cache, 0, d.spec_state, stream)) !=
       CVSA_OK)
     return rc;
-  return cvsa_internal::verified_decode_after_speculation(
-      q, d.q_stride_b, d.q_stride_h, d.k_cache, d.v_cache, d.num_blocks, d.block_tables,
-      d.bt_stride_b, d.context_lens, d.page_indices, d.budget, d.n_per_head, d.budget, d.accept,
-      d.B, d.H_q, d.H_kv, d.D, d.block_size, d.W, out, d.out_dtype, d.work, d.spec_state,
-      d.workspace, d.workspace_bytes, stream);
+  return verified(d, q, out, d.spec_state, stream);
 }
 
 }  // namespace
@@ -284,19 +292,19 @@ extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint
       if ((rc = rank(d, q, d.check_accept, stream)) != CVSA_OK) return rc;
       if ((rc = plan_select(d, d.check_accept, d.scores_cache, 0, nullptr, stream)) != CVSA_OK)
         return rc;
-      return verified(d, q, out, stream);
+      return verified(d, q, out, nullptr, stream);
     case CVSA_STEP_FRESH:
       if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
       if ((rc = rank(d, q, nullptr, stream)) != CVSA_OK) return rc;
       if ((rc = plan_select(d, nullptr, d.scores_cache, 0, nullptr, stream)) != CVSA_OK)
         return rc;
       plan->map_valid = true;  // every row selected anew
-      return verified(d, q, out, stream);
+      return verified(d, q, out, nullptr, stream);
     default:  // CVSA_STEP_SCORE
       if ((rc = score(d, q, stream)) != CVSA_OK) return rc;
       if ((rc = rank(d, q, nullptr, stream)) != CVSA_OK) return rc;
       if ((rc = plan_select(d, nullptr, nullptr, 1, nullptr, stream)) != CVSA_OK) return rc;
       plan->map_valid = true;
-      return verified(d, q, out, stream);
+      return verified(d, q, out, nullptr, stream);
   }
 }

@@ -24,9 +24,13 @@ merge of draft and complement.  The lazy accept-all decision is taken on
 the device (select_or_keep keeps the cached selection or refreshes it in
 place), and the statistics counters and effective-budget counters are
 accumulated there too, so a lazy decode step never waits for the host.
-Host reads remain where the reference's result needs one: approximate
-recovery, the random-rejection counterfactual, coverage-only steps and the
-counters of the fixed-interval schedule.
+Approximate recovery (approx_recovery_pct) runs through the step plans as
+well: the selection kernel writes each rejected row's expanded selection
+and the verified decode attends it (ops.verified_decode_approx), so the
+reference's deployed setting (budget 5%, tau 0.9, M=4, ar20, dense layer 0)
+takes no host read either.  Host reads remain where the reference's result
+needs one: the random-rejection counterfactual, coverage-only steps, the
+per-head budget selectors and the per-kernel path (timing enabled).
 
 The Quest selector (selector="quest", cvsa/backend.py:572-620) ranks pages
 by per-page key min/max metadata that is recomputed only for the pages
@@ -74,6 +78,28 @@ class _PendingComplement:
             return None
         return ops.compute_complement(self.page_indices, self.n_per_head, self.context_lens,
                                       self.block_size, self.accept)
+
+
+class _PendingExpanded:
+    """Expanded selection of an approximate-recovery step, computed only if
+    someone reads ``_last_expanded_selection`` (backend.py:780-815: the
+    top exp_budget pages of every row by the ranking scores, present when a
+    head was rejected)."""
+
+    __slots__ = ("accept", "scores", "exp_budget", "context_lens", "block_size")
+
+    def __init__(self, accept, scores, exp_budget, context_lens, block_size):
+        self.accept = accept
+        self.scores = scores
+        self.exp_budget = exp_budget
+        self.context_lens = context_lens
+        self.block_size = block_size
+
+    def resolve(self):
+        if bool(self.accept.all()):
+            return None
+        return ops.select_topk(self.scores, self.exp_budget, self.context_lens,
+                               self.block_size)
 
 
 def _device_counter(slot: int, host_name: str):
@@ -217,7 +243,7 @@ class CVSABackend:
         rejected (backend.py:815, :842).  Complements are built on first read."""
         for layer in list(self._expanded_store):
             v = self._expanded_store[layer]
-            if isinstance(v, _PendingComplement):
+            if isinstance(v, (_PendingComplement, _PendingExpanded)):
                 v = v.resolve()
                 if v is None:
                     del self._expanded_store[layer]
@@ -600,26 +626,45 @@ class CVSABackend:
         """Build the layer's step plan, or None where a step needs the
         per-kernel path (timing, host-side decisions, unsupported buffers)."""
         if (self._track_timing or self.random_reject_prob is not None
-                or self.approx_recovery_pct is not None or self.top_p is not None
-                or self.static_budget_table is not None or self.adaptive_selection):
+                or self.top_p is not None or self.static_budget_table is not None
+                or self.adaptive_selection):
             return None
         dev = q.device
         work = self._work(dev)
         stats = self._ensure_dev_stats(dev)
         if work is None or stats is None:
             return None
-        budget = max(3, int(block_tables.shape[1] * self.budget_pct))
+        W = block_tables.shape[1]
+        budget = max(3, int(W * self.budget_pct))
         selector, quest = self._plan_selector(k_cache)
         try:
             plan = ops.StepPlan(q, k_cache, v_cache, block_tables, context_lens,
                                 self.num_kv_heads, self.num_q_per_kv, self.block_size, budget,
                                 self.tau, page_indices, n_per_head, scores_cache, stats, work,
                                 own_scores_cache=own_scores_cache, selector=selector,
-                                quest=quest)
+                                quest=quest, approx_budget=self._approx_budget(budget, W))
         except (ValueError, NotImplementedError):
             return None
         self._step_plans[layer_idx] = plan
         return plan
+
+    def _approx_budget(self, budget: int, n_pages: int) -> int:
+        """Expanded budget of approximate recovery (backend.py:782-783), 0
+        under exact recovery."""
+        if self.approx_recovery_pct is None:
+            return 0
+        return min(max(budget + 1, int(n_pages * self.approx_recovery_pct)), n_pages)
+
+    def _plan_expanded(self, plan, accept_mask, context_lens):
+        """What a plan step leaves for ``_last_expanded_selection``: the
+        complement (exact recovery) or the expanded selection (approximate),
+        each built on first read."""
+        if plan.approx_budget > 0:
+            ranked = plan.sel_scores if plan.sel_scores is not None else plan.page_scores
+            return _PendingExpanded(accept_mask, ranked, plan.approx_budget, context_lens,
+                                    self.block_size)
+        return _PendingComplement(accept_mask, plan.page_indices, plan.n_per_head,
+                                  context_lens, self.block_size)
 
     def _fresh_plan(self, layer_idx, q, k_cache, v_cache, block_tables, context_lens,
                     own_scores_cache=False):
@@ -644,8 +689,7 @@ class CVSABackend:
         B = plan.page_indices.shape[0]
         accept_mask = plan.accept.view(torch.bool)
         self._last_accept_mask[layer_idx] = accept_mask
-        self._expanded_store[layer_idx] = _PendingComplement(
-            accept_mask, plan.page_indices, plan.n_per_head, context_lens, self.block_size)
+        self._expanded_store[layer_idx] = self._plan_expanded(plan, accept_mask, context_lens)
         self._cached_page_scores[layer_idx] = cached_scores
         self._reuse_state[layer_idx] = (plan.page_indices.view(B * self.num_kv_heads, -1),
                                         plan.n_per_head.view(B * self.num_kv_heads),
@@ -671,8 +715,7 @@ class CVSABackend:
         accept_mask = plan.accept.view(torch.bool)
         self._per_head_total += accept_mask.numel()
         self._last_accept_mask[layer_idx] = accept_mask
-        self._expanded_store[layer_idx] = _PendingComplement(
-            accept_mask, plan.page_indices, plan.n_per_head, context_lens, self.block_size)
+        self._expanded_store[layer_idx] = self._plan_expanded(plan, accept_mask, context_lens)
 
     def _device_decision_ok(self, layer_idx, page_scores, context_lens) -> bool:
         """Whether the lazy accept-all decision can stay on the device: exact
@@ -908,7 +951,7 @@ class CVSABackend:
             if not self.lazy:
                 self._h_accept_counts += 1
         else:
-            exp_budget = min(max(budget + 1, int(n_pages * self.approx_recovery_pct)), n_pages)
+            exp_budget = self._approx_budget(budget, n_pages)
             exp_indices, exp_nph = ops.select_topk(page_scores, exp_budget, context_lens,
                                                    self.block_size)
             expanded = self._time_kernel(

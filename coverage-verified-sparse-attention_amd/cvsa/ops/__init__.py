@@ -33,6 +33,7 @@ __all__ = [
     "sparse_decode_reuse",
     "dense_decode",
     "verified_decode",
+    "verified_decode_approx",
     "compute_complement",
     "lse_merge",
     "append_kv",
@@ -532,10 +533,10 @@ class DecodeCall:
 def prepare_decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
                    num_q_per_kv, block_size, pi_flat=None, nph_flat=None, max_sel=0,
                    accept=None, want_state=False, want_out=True, out_dtype=None,
-                   work=None) -> DecodeCall:
+                   work=None, exp_flat=None, exp_budget=0) -> DecodeCall:
     """Validate a decode launch and build its argument list (see DecodeCall)."""
     dev = _device_of(q, k_cache, v_cache, block_tables, context_lens, pi_flat, nph_flat,
-                     accept, work)
+                     accept, work, exp_flat)
     if work is not None and (work.dtype != torch.int64 or work.numel() < 2
                              or not work.is_contiguous()):
         raise ValueError(f"{kind}: work must be a contiguous int64 tensor of 2 counters")
@@ -554,7 +555,7 @@ def prepare_decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, n
     W = bt.shape[1]
     L = _lib.load()
     listed = pi_flat is not None
-    all_pages = kind in ("dense_decode", "verified_decode")
+    all_pages = kind in ("dense_decode", "verified_decode", "verified_decode_approx")
     need = L.cvsa_decode_workspace_bytes(B, H_q, num_kv_heads, D, max_sel if listed else 0,
                                          W, 1 if all_pages else 0)
     ws = _workspace(dev, need)
@@ -574,10 +575,14 @@ def prepare_decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, n
     elif kind == "dense_decode":
         fn = L.cvsa_dense_decode
         mid = []
-    else:
+    elif kind == "verified_decode":
         fn = L.cvsa_verified_decode
         mid = [pi_flat.data_ptr(), pi_flat.stride(0), nph_flat.data_ptr(), max_sel,
                accept.data_ptr()]
+    else:
+        fn = L.cvsa_verified_decode_approx
+        mid = [pi_flat.data_ptr(), pi_flat.stride(0), nph_flat.data_ptr(), max_sel,
+               accept.data_ptr(), exp_flat.data_ptr(), exp_flat.stride(0), exp_budget]
     sizes = [B, H_q, num_kv_heads, D, block_size, W]
     tail = [None, None, None, None, code, _ptr(work), _ptr(ws),
             0 if ws is None else ws.numel(), stream]
@@ -597,17 +602,18 @@ def prepare_decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, n
     # alive here but make the call non-reusable, since their content is a
     # snapshot of the caller's tensors.
     c.refs = (k_cache, v_cache, block_tables, context_lens, work, bt, ctx, pi_flat, nph_flat,
-              accept, ws)
+              accept, ws, exp_flat)
     c.reusable = bt is block_tables and ctx is context_lens
     return c
 
 
 def _decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
             num_q_per_kv, block_size, pi_flat=None, nph_flat=None, max_sel=0,
-            accept=None, want_state=False, want_out=True, out_dtype=None, work=None):
+            accept=None, want_state=False, want_out=True, out_dtype=None, work=None,
+            exp_flat=None, exp_budget=0):
     c = prepare_decode(kind, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
                        num_q_per_kv, block_size, pi_flat, nph_flat, max_sel, accept, want_state,
-                       want_out, out_dtype, work)
+                       want_out, out_dtype, work, exp_flat, exp_budget)
     return c.run(_check_q(q))
 
 
@@ -637,6 +643,11 @@ class StepPlan:
     SELECT_QUEST_LN ranks and gates by the Quest scores.
     ``matches`` tells whether a call's buffers, query layout and stream are
     the ones the plan was built for.
+    With ``approx_budget`` > 0 the plan's checks and scoring steps recover
+    rejected heads approximately (CVSABackend approx_recovery_pct,
+    cvsa/backend.py:780-817): the selection step writes each rejected
+    row's expanded selection into ``approx_indices`` [B, H_kv,
+    approx_budget] and the decode attends it (cvsa_verified_decode_approx).
     With ``speculate`` (default) a lazy check decodes the cached selection
     in the same launch as the page scoring, and the verified decode skips
     its work when the check kept that selection (see
@@ -650,13 +661,13 @@ class StepPlan:
     __slots__ = ("dev", "stream", "q_meta", "out_shape", "out_dtype", "refs", "page_indices",
                  "n_per_head", "page_scores", "scores_cache", "check_accept", "accept",
                  "coverage", "budget", "owns_selection", "selector", "sel_scores", "spec_state",
-                 "sel_map", "h_kv", "_h", "_run", "_run_append", "_pa_ok", "_slots_ok", "_fin",
-                 "__weakref__")
+                 "sel_map", "approx_budget", "approx_indices", "h_kv", "_h", "_run",
+                 "_run_append", "_pa_ok", "_slots_ok", "_fin", "__weakref__")
 
     def __init__(self, q, k_cache, v_cache, block_tables, context_lens, num_kv_heads,
                  num_q_per_kv, block_size, budget, tau, page_indices=None, n_per_head=None,
                  scores_cache=None, stats=None, work=None, own_scores_cache=False,
-                 selector=_lib.SELECT_EXACT, quest=None, speculate=True):
+                 selector=_lib.SELECT_EXACT, quest=None, speculate=True, approx_budget=0):
         dev = _device_of(q, k_cache, v_cache, block_tables, context_lens, page_indices,
                          n_per_head, scores_cache, stats, work)
         if selector not in (_lib.SELECT_EXACT, _lib.SELECT_QUEST, _lib.SELECT_QUEST_LN):
@@ -719,6 +730,13 @@ class StepPlan:
         map_stride = (W + 15) // 16 * 16
         self.sel_map = (torch.zeros(B * H, map_stride, dtype=torch.uint8, device=dev)
                         if speculate and block_size == 16 else None)
+        # Approximate recovery: the expanded selections of the rows that a
+        # selection step rejected (rows of accepted heads are stale).
+        if not 0 <= approx_budget <= W:
+            raise ValueError(f"step plan: approx_budget={approx_budget} not in [0, W={W}]")
+        self.approx_budget = approx_budget
+        self.approx_indices = (torch.zeros(B, H, approx_budget, dtype=torch.int32, device=dev)
+                               if approx_budget > 0 else None)
         d = _lib.StepDesc(
             B=B, H_q=H_q, H_kv=H, D=D, block_size=block_size, W=W, budget=budget,
             tau=float(tau), out_dtype=_DTYPE_CODE[q.dtype], q_stride_b=q.stride(0),
@@ -732,7 +750,8 @@ class StepPlan:
             selector=selector, quest_meta=None if quest is None else quest.meta.data_ptr(),
             quest_ntok=None if quest is None else quest.ntok.data_ptr(),
             sel_scores=_ptr(self.sel_scores), spec_state=_ptr(self.spec_state),
-            sel_map=_ptr(self.sel_map), sel_map_stride=map_stride)
+            sel_map=_ptr(self.sel_map), sel_map_stride=map_stride,
+            approx_budget=approx_budget, approx_indices=_ptr(self.approx_indices))
         L = _lib.load()
         ws = _workspace(dev, L.cvsa_step_workspace_bytes(ctypes.byref(d)))
         d.workspace = _ptr(ws)
@@ -1011,6 +1030,37 @@ def verified_decode(q, k_cache, v_cache, block_tables, context_lens, page_indice
     o, m, l, out = _decode("verified_decode", q, k_cache, v_cache, block_tables, context_lens,
                            num_kv_heads, num_q_per_kv, block_size, pi, nph, k, accept=acc,
                            want_state=return_state, out_dtype=output_dtype, work=work)
+    return (out, (o, m, l)) if return_state else out
+
+
+def verified_decode_approx(q, k_cache, v_cache, block_tables, context_lens, page_indices,
+                           n_per_head, accept_mask, exp_indices, num_kv_heads, num_q_per_kv,
+                           block_size, return_state: bool = False, output_dtype=None,
+                           work: Optional[torch.Tensor] = None):
+    """Draft for accepted heads, approximate recovery for rejected heads.
+
+    Equivalent to the approximate-recovery branch of
+    CVSABackend._scoring_step (cvsa/backend.py:775-817): accepted heads
+    return the normalised draft over their selected pages, rejected heads
+    the normalised sparse decode of the first min(exp_budget, n_valid)
+    pages of their row of ``exp_indices`` [B, H_kv, exp_budget] (the
+    expanded top-k, e.g. ``select_topk(scores, exp_budget, ...)``).  The
+    effective-budget counters book what the reference books: when a head
+    is rejected, n_per_head + min(exp_budget, n_valid) on every head.
+    """
+    pi, nph, k = _flat_selection(page_indices, n_per_head, num_kv_heads)
+    if exp_indices.dim() != 3 or exp_indices.shape[:2] != page_indices.shape[:2]:
+        raise ValueError("exp_indices must be [B, H_kv, exp_budget]")
+    exp_budget = exp_indices.shape[2]
+    ex = _i32(exp_indices).reshape(-1, exp_budget)
+    acc = accept_mask
+    if acc.dtype == torch.bool:
+        acc = acc.view(torch.uint8)
+    acc = acc.to(torch.uint8).contiguous().reshape(-1)
+    o, m, l, out = _decode("verified_decode_approx", q, k_cache, v_cache, block_tables,
+                           context_lens, num_kv_heads, num_q_per_kv, block_size, pi, nph, k,
+                           accept=acc, want_state=return_state, out_dtype=output_dtype,
+                           work=work, exp_flat=ex, exp_budget=exp_budget)
     return (out, (o, m, l)) if return_state else out
 
 

@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parents[1] / "libcvsa_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 CVSA_OK = 0
 CVSA_ERR_INVALID = -1
@@ -51,6 +51,7 @@ class StepDesc(ctypes.Structure):
         ("workspace", _p), ("workspace_bytes", _sz),
         ("selector", _i32), ("quest_meta", _p), ("quest_ntok", _p), ("sel_scores", _p),
         ("spec_state", _p), ("sel_map", _p), ("sel_map_stride", _i64),
+        ("approx_budget", _i32), ("approx_indices", _p),
     ]
 
 
@@ -95,6 +96,11 @@ SIGNATURES = {
     "cvsa_verified_decode": (ctypes.c_int, [
         _p, _i64, _i64, _p, _p, _i64, _p, _i64, _p,
         _p, _i64, _p, _i32, _p,
+        _i32, _i32, _i32, _i32, _i32, _i32,
+        _p, _p, _p, _p, _i32, _p, _p, _sz, _p]),
+    "cvsa_verified_decode_approx": (ctypes.c_int, [
+        _p, _i64, _i64, _p, _p, _i64, _p, _i64, _p,
+        _p, _i64, _p, _i32, _p, _p, _i64, _i32,
         _i32, _i32, _i32, _i32, _i32, _i32,
         _p, _p, _p, _p, _i32, _p, _p, _sz, _p]),
     "cvsa_compute_complement": (ctypes.c_int, [

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 12
+#define CVSA_ABI_VERSION 13
 
 enum {
   CVSA_OK = 0,
@@ -337,6 +337,35 @@ int cvsa_verified_decode(const uint16_t *q, int64_t q_stride_b,
                          size_t workspace_bytes, void *stream);
 
 /*
+ * Verified decode with approximate recovery: the draft/recovery branch of a
+ * scoring step when CVSABackend.approx_recovery_pct is set.  Replaces
+ * cvsa/backend.py:775-779 (accept-all: o_d / l_d) and :780-817 (expanded
+ * top-k, its sparse decode, and the per-head select between the normalised
+ * draft and the normalised expanded decode).  Accepted heads
+ * (accept[b*H_kv+h] != 0) attend their selected pages; rejected heads attend
+ * the first min(exp_budget, n_valid) pages of exp_indices[b,h,:] (the
+ * exp_budget largest ranking scores, e.g. cvsa_select_topk with budget
+ * exp_budget).  Effective-budget counters as the reference books them: when
+ * some head is rejected every head adds n_per_head + min(exp_budget,
+ * n_valid), else n_per_head.  exp_budget in [1, W], exp_stride >= exp_budget.
+ * Outputs as cvsa_sparse_decode.
+ */
+int cvsa_verified_decode_approx(const uint16_t *q, int64_t q_stride_b,
+                                int64_t q_stride_h, const uint16_t *k_cache,
+                                const uint16_t *v_cache, int64_t num_blocks,
+                                const int32_t *block_tables, int64_t bt_stride_b,
+                                const int32_t *context_lens,
+                                const int32_t *page_indices, int64_t idx_stride,
+                                const int32_t *n_per_head, int32_t max_selected,
+                                const uint8_t *accept, const int32_t *exp_indices,
+                                int64_t exp_stride, int32_t exp_budget, int32_t B,
+                                int32_t H_q, int32_t H_kv, int32_t D, int32_t block_size,
+                                int32_t W, float *o_unnorm, float *m_out,
+                                float *l_out, void *out, int32_t out_dtype,
+                                int64_t *work, void *workspace,
+                                size_t workspace_bytes, void *stream);
+
+/*
  * Complement page lists.  Replaces triton_compute_complement
  * (cvsa/kernels/coverage.py:99-150, kernel :30-96).
  *   comp_indices[b,h,:] = ascending valid pages p < n_valid(b) that are not
@@ -492,6 +521,8 @@ typedef struct cvsa_step_desc {
   uint8_t *sel_map;            /* [B * H_kv, sel_map_stride] bytes, zeroed, or NULL: the map
                                   of the selection (below) */
   int64_t sel_map_stride;      /* >= W, a multiple of 16 (sel_map 16-byte aligned) */
+  int32_t approx_budget;       /* > 0: approximate recovery (below); 0: exact recovery */
+  int32_t *approx_indices;     /* [B, H_kv, approx_budget] when approx_budget > 0 */
 } cvsa_step_desc;
 
 /* Page scorers of a plan (CVSABackend selector / light_normalizer,
@@ -524,6 +555,18 @@ enum {
  * (page_indices given at creation) before its first speculative check; a
  * caller that writes page_indices / n_per_head itself must then call
  * cvsa_step_plan_selection_changed.
+ */
+/*
+ * Approximate recovery (approx_budget > 0; CVSABackend approx_recovery_pct,
+ * cvsa/backend.py:780-817, with approx_budget = min(max(budget + 1,
+ * int(W * approx_recovery_pct)), W)): a selection step writes, for every
+ * row whose new selection fails its gate, that row's expanded selection
+ * (the approx_budget largest ranking scores, ascending) into
+ * approx_indices, and the step's decode is cvsa_verified_decode_approx:
+ * rejected heads attend their expanded selection instead of every valid
+ * page.  Rows whose gate passed keep stale approx_indices rows.  The
+ * expanded selection ranks the selection's scores (sel_scores under
+ * CVSA_SELECT_QUEST, else page_scores).
  */
 enum {
   CVSA_STEP_REUSE = 0,      /* sparse decode of the kept selection */

@@ -30,7 +30,7 @@ class OracleCVSABackend:
                  check_interval=None, coverage_interval=None, approx_recovery_pct=None,
                  selector="exact", light_normalizer=False, top_p=None,
                  static_budget_table=None, adaptive_selection=False, adaptive_floor_ratio=0.5,
-                 acc_dtype=torch.float64):
+                 random_reject_prob=None, acc_dtype=torch.float64):
         # :80-115
         self.num_kv_heads = num_kv_heads
         self.num_q_heads = num_q_heads
@@ -54,6 +54,7 @@ class OracleCVSABackend:
             for layer, f in static_budget_table.items()}
         self.adaptive_selection = adaptive_selection
         self.adaptive_floor_ratio = adaptive_floor_ratio
+        self.random_reject_prob = random_reject_prob
         self.acc_dtype = acc_dtype
         # Optional test hooks (None: the reference behaviour).  A parity test
         # that runs this oracle beside another implementation uses them to
@@ -64,8 +65,11 @@ class OracleCVSABackend:
         #   on_gate(layer, where, gate_scores, idx, nph, accept, cov) -> accept
         #     where: "check" (lazy check of the cached selection),
         #     "coverage_only", or "new" (gate of a new selection).
+        #   on_expand(layer, ranked, exp_idx, exp_budget) -> exp_idx
+        #     (the expanded selection of approximate recovery)
         self.on_select = None
         self.on_gate = None
+        self.on_expand = None
         self.reset()
 
     def reset(self):
@@ -157,6 +161,15 @@ class OracleCVSABackend:
         self._attn_work += torch.as_tensor(pages_attended).to(torch.long)
         self._attn_work_max += (nv.sum() * self.num_kv_heads).to(torch.long)
 
+    def _random_reject(self, accept):
+        """The counterfactual override of :433-441 / :762-767: one Bernoulli
+        draw per gate; every head of the layer is rejected or accepted."""
+        if self.random_reject_prob is None:
+            return accept
+        if torch.rand(1).item() < self.random_reject_prob:
+            return torch.zeros_like(accept)
+        return torch.ones_like(accept)
+
     def _reuse_decode(self, q, k_cache, v_cache, block_tables, context_lens, layer_idx):
         idx, nph = self._cached_selection[layer_idx]
         self._record_work(context_lens, nph.sum())
@@ -180,6 +193,7 @@ class OracleCVSABackend:
             accept, cov = ref.check_coverage(page_scores, idx, nph, self.tau, self.acc_dtype)
             if self.on_gate is not None:
                 accept = self.on_gate(layer_idx, "check", page_scores, idx, nph, accept, cov)
+            accept = self._random_reject(accept)
             self._per_head_accept_sum += int(accept.sum())
             self._per_head_total += accept.numel()
             if bool(accept.all()):
@@ -200,6 +214,7 @@ class OracleCVSABackend:
         accept, cov = ref.check_coverage(page_scores, idx, nph, self.tau, self.acc_dtype)
         if self.on_gate is not None:
             accept = self.on_gate(layer_idx, "coverage_only", page_scores, idx, nph, accept, cov)
+        accept = self._random_reject(accept)
         self._per_head_accept_sum += int(accept.sum())
         self._per_head_total += accept.numel()
         self._total_coverage_checks += 1
@@ -251,6 +266,7 @@ class OracleCVSABackend:
         accept, cov = ref.check_coverage(page_scores, idx, nph, self.tau, self.acc_dtype)
         if self.on_gate is not None:
             accept = self.on_gate(layer_idx, "new", page_scores, idx, nph, accept, cov)
+        accept = self._random_reject(accept)                                     # :762-767
         self._last_accept_mask[layer_idx] = accept
         recovery_pages = None
         if bool(accept.all()):                                                   # :775-779
@@ -262,6 +278,8 @@ class OracleCVSABackend:
             exp_budget = max(budget + 1, int(n_pages * self.approx_recovery_pct))
             exp_budget = min(exp_budget, n_pages)
             exp_idx, _ = ref.select_topk(sel_scores, exp_budget, context_lens, self.block_size)
+            if self.on_expand is not None:
+                exp_idx = self.on_expand(layer_idx, sel_scores, exp_idx, exp_budget)
             exp_nph = torch.clamp(nv, max=exp_budget).to(torch.int32).unsqueeze(1).expand(
                 B, self.num_kv_heads).contiguous()
             o_e, m_e, l_e = ref.sparse_decode_unnorm(q, k_cache, v_cache, block_tables, exp_idx,

@@ -114,8 +114,10 @@ class _Lockstep:
         self.margin_gate = 0                 # fp64 accept decided within the coverage error
         self.heads_checked = 0
         self.g = {}
+        self.expanded_checked = 0
         ora_b.on_select = self.on_select
         ora_b.on_gate = self.on_gate
+        ora_b.on_expand = self.on_expand
 
     # ------------------------------------------------------------ snapshots
     def before_gpu(self, layer=0):
@@ -136,6 +138,16 @@ class _Lockstep:
             g["gate"] = _cpu(b._cached_page_scores[layer])
             rank = b._last_rank_scores.get(layer)
             g["ranked"] = g["gate"] if rank is None else _cpu(rank)
+            # Approximate recovery: the expanded selection the tracing
+            # attribute reports, and the rows the step plan's selection
+            # kernel wrote for the rejected heads (when a plan ran the step).
+            exp = b._last_expanded_selection.get(layer) if b.approx_recovery_pct else None
+            g["exp"] = None if exp is None else (_cpu(exp[0]), _cpu(exp[1]))
+            plan = b._step_plans.get(layer)
+            g["plan_exp"] = None
+            if (plan is not None and plan.approx_budget > 0
+                    and b._cached_selection[layer][0] is plan.page_indices):
+                g["plan_exp"] = _cpu(plan.approx_indices)
         self.g = g
 
     # ------------------------------------------------------------ helpers
@@ -207,8 +219,52 @@ class _Lockstep:
                 assert float(rest.max()) <= kth + tol, ("near-tie set", b, h, tol)
         return gi, gn
 
+    def on_expand(self, layer, ranked_o, exp_o, exp_budget):
+        """The expanded selection of approximate recovery: the GPU's (the
+        tracing attribute's rows, and the step plan's rows for rejected
+        heads) exactly equals the oracle's selector on the GPU's own ranking
+        scores, and the oracle's fp64 choice outside the score-error margin."""
+        g = self.g
+        assert g.get("exp") is not None, "the oracle expanded where the GPU did not"
+        gi, gn = g["exp"]
+        R = g["ranked"]
+        err = self._score_error(R, ranked_o, "ranking scores (expansion)")
+        ri, rn = ref.select_topk(R, exp_budget, self.ctx, self.bs)
+        assert gi.shape[-1] == exp_budget and torch.equal(gn, rn), ("expanded counts", gn, rn)
+        B, H = gn.shape
+        rejected = ~g["accept"]
+        pe = g["plan_exp"]
+        for b in range(B):
+            for h in range(H):
+                n = int(gn[b, h])
+                assert torch.equal(gi[b, h, :n], ri[b, h, :n]), ("expanded", b, h)
+                if pe is not None and bool(rejected[b, h]):
+                    assert torch.equal(pe[b, h, :n], ri[b, h, :n]), ("plan expanded", b, h)
+                same = torch.equal(gi[b, h, :n], exp_o[b, h, :n])
+                if not same:
+                    self.margin_sel += 1
+                    tol = 2.0 * float(err[b, h]) + 1e-9
+                    S = ranked_o.double()
+                    kth = float(torch.sort(S[b, h], descending=True).values[n - 1])
+                    sel = gi[b, h, :n].long()
+                    assert float(S[b, h, sel].min()) >= kth - tol, ("near-tie set", b, h)
+        self.expanded_checked += int(rejected.sum())
+        return gi
+
     def on_gate(self, layer, where, scores_o, idx, nph, accept_o, cov_o):
         g = self.g
+        rr = self.kw.get("random_reject_prob")
+        if where == "new" and rr is not None:
+            # The new selection's gate is overridden on both sides (rr in
+            # {0, 1}: every head accepted or every head rejected); its
+            # coverage is still checked.
+            assert rr in (0.0, 1.0), rr
+            assert g.get("new")
+            assert bool((g["accept"] == (rr == 0.0)).all()), g["accept"]
+            acc_r, cov_r = ref.check_coverage(g["gate"], idx, nph, self.tau)
+            assert float((cov_r - cov_o).abs().max()) < COV_ATOL, (where, cov_r, cov_o)
+            self.heads_checked += acc_r.numel()
+            return g["accept"].clone()
         if where == "new":
             assert g.get("new"), "the oracle gated a new selection the GPU did not make"
             G, A = g["gate"], g["accept"]
@@ -241,10 +297,11 @@ class _Lockstep:
                 f"{self.own_margin}")
 
 
-def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, expect_margin=0):
-    """Run both backends for ``steps`` calls in lockstep and compare them.
-    ``expect_margin`` is the number of margin heads (of every kind) the seed
-    gives; the BASELINE bar is zero."""
+def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, expect_margin=0, layers=1):
+    """Run both backends for ``steps`` decode steps of ``layers`` layers (one
+    shared cache) in lockstep and compare them.  ``expect_margin`` is the
+    number of margin heads (of every kind) the seed gives; the BASELINE bar
+    is zero."""
     if gen_on_gpu:
         # Long contexts: draw the inputs on the GPU, then give the oracle host copies.
         inp = make_paged_inputs(**cfg, seed=seed, max_pages=None, spare_blocks=extra,
@@ -268,32 +325,37 @@ def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, expect_margin=0)
     lock = _Lockstep(gpu_b, ora_b, kw, rt.ctx)
     g = torch.Generator().manual_seed(seed + 1)
     for step in range(steps):
-        q = jitter_query(inp.q, 0.3, seed + 100 + step)
-        lock.before_gpu()
-        out = gpu_b(q.to(dev), rt.cache.k_cache, rt.cache.v_cache, rt.mgr.block_tables,
-                    rt.mgr.context_lens, 0).cpu()
-        lock.after_gpu()
-        n_tr = len(ora_b.trace)
-        want = ora_b(q, rt.K, rt.V, rt.bt, rt.ctx, 0)
-        kinds = [t["kind"] for t in ora_b.trace[n_tr:]]
-        new_sel = any(k.startswith("score") for k in kinds)
-        assert new_sel == lock.g["new"], (step, kinds)
-        err = (out.float() - want.float()).abs().max().item()
-        assert err < OUT_ATOL, (step, err, kinds)
-        ga, oa = gpu_b._last_accept_mask.get(0), ora_b._last_accept_mask.get(0)
-        assert (ga is None) == (oa is None), step
-        if ga is not None:
-            assert torch.equal(ga.cpu(), oa), step
-        gs, os_ = gpu_b._cached_selection.get(0), ora_b._cached_selection.get(0)
-        assert (gs is None) == (os_ is None), step      # none on a dense layer
-        if gs is not None:
-            assert torch.equal(gs[1].cpu(), os_[1]), step
-            for b in range(B):
-                for h in range(H):
-                    n = int(os_[1][b, h])
-                    assert torch.equal(gs[0][b, h, :n].cpu(), os_[0][b, h, :n]), (step, b, h)
-        gpu_b.step_done(0, 1)
-        ora_b.step_done(0, 1)
+        for layer in range(layers):
+            q = jitter_query(inp.q, 0.3, seed + 100 + step * layers + layer)
+            lock.before_gpu(layer)
+            out = gpu_b(q.to(dev), rt.cache.k_cache, rt.cache.v_cache, rt.mgr.block_tables,
+                        rt.mgr.context_lens, layer).cpu()
+            lock.after_gpu(layer)
+            n_tr = len(ora_b.trace)
+            want = ora_b(q, rt.K, rt.V, rt.bt, rt.ctx, layer)
+            kinds = [t["kind"] for t in ora_b.trace[n_tr:]]
+            new_sel = any(k.startswith("score") for k in kinds)
+            assert new_sel == lock.g["new"], (step, layer, kinds)
+            err = (out.float() - want.float()).abs().max().item()
+            assert err < OUT_ATOL, (step, layer, err, kinds)
+            ga, oa = gpu_b._last_accept_mask.get(layer), ora_b._last_accept_mask.get(layer)
+            assert (ga is None) == (oa is None), (step, layer)
+            if ga is not None:
+                assert torch.equal(ga.cpu(), oa), (step, layer)
+            ge = gpu_b._last_expanded_selection.get(layer)
+            oe = ora_b._last_expanded_selection.get(layer)
+            assert (ge is None) == (oe is None), (step, layer)
+            gs, os_ = gpu_b._cached_selection.get(layer), ora_b._cached_selection.get(layer)
+            assert (gs is None) == (os_ is None), (step, layer)   # none on a dense layer
+            if gs is not None:
+                assert torch.equal(gs[1].cpu(), os_[1]), (step, layer)
+                for b in range(B):
+                    for h in range(H):
+                        n = int(os_[1][b, h])
+                        assert torch.equal(gs[0][b, h, :n].cpu(), os_[0][b, h, :n]), (
+                            step, layer, b, h)
+            gpu_b.step_done(layer, layers)
+            ora_b.step_done(layer, layers)
         kn = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
         vn = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
         rt.append(kn, vn, dev)
@@ -499,3 +561,89 @@ def test_random_schedules_against_oracle(gpu, seed):
     cfg, kw = _random_schedule(seed)
     stats, trace, lock = _run(gpu, cfg, kw, steps=10, seed=600 + seed)
     print(f"seed {seed} {cfg} {kw}: {lock.summary()}")
+
+
+# The reference's deployed setting cvsa_5_90_c4_ar20_dL0 (the method-name
+# parser, eval/longbench_cvsa.py:190-236: budget 5%, tau 0.90, lazy checks
+# every 4 steps, approximate recovery at 20% of the pages, layer 0 dense;
+# every latency it publishes, eval/plot_pareto.py:141-150).
+DEPLOYED = dict(budget_pct=0.05, coverage_threshold=0.9, lazy=True, check_interval=4,
+                approx_recovery_pct=0.2, dense_layers=[0])
+
+
+_CFG2_ALL_HOT = dict(FULL_SIZE["cfg2"][0], random_hot_heads=0, hot_heads=list(range(8)),
+                     n_hot=8, hot_shift=16.0)
+
+
+@pytest.mark.parametrize("recipe", ["cfg2", "cfg2_all_hot"])
+def test_deployed_setting_cfg2_full_size(gpu, recipe):
+    """cvsa_5_90_c4_ar20_dL0 at cfg2's full size (B=32, 32/8/128, 8192
+    tokens, one token appended per sequence per step) over a dense layer 0
+    and a CVSA layer 1, nine decode steps, in lockstep with the oracle
+    backend: outputs, selections, accept masks, the expanded selections of
+    rejected heads (also the rows the step plan's selection kernel wrote)
+    and statistics; zero margin heads.  With cfg2's recipe (hot pages on
+    half of the heads) most heads are recovered and every check reselects;
+    with every head hot most heads pass and checks can keep."""
+    cfg = FULL_SIZE["cfg2"][0] if recipe == "cfg2" else _CFG2_ALL_HOT
+    stats, trace, lock = _run(gpu, cfg, DEPLOYED, steps=9, seed=7102, gen_on_gpu=True,
+                              layers=2)
+    kinds = [t["kind"] for t in trace]
+    assert "dense" in kinds and "reuse" in kinds, kinds
+    if recipe == "cfg2":
+        assert "score_approx" in kinds and lock.expanded_checked > 0, kinds
+    print(f"deployed {recipe}: {kinds}: {lock.summary()}, expanded rows checked "
+          f"{lock.expanded_checked}")
+
+
+@pytest.mark.parametrize("shift", [3.0, 12.0])
+def test_approx_recovery_cfg1(gpu, shift):
+    """Approximate recovery (20%) at cfg1's shape (B=1, 32/8/128, 8192
+    tokens, budget 1/4, tau 0.9, scoring every step): with the literal +3
+    sigma recipe every head is recovered through its expanded selection,
+    at +12 sigma the hot heads pass."""
+    cfg = dict(FULL_SIZE["cfg1_recipe"][0], hot_shift=shift)
+    kw = dict(budget_pct=0.25, coverage_threshold=0.9, lazy=False, reuse_interval=1,
+              approx_recovery_pct=0.2)
+    stats, trace, lock = _run(gpu, cfg, kw, steps=4, seed=1011, gen_on_gpu=True)
+    assert lock.expanded_checked > 0
+    if shift == 3.0:
+        assert all(not bool(t["accept"].any()) for t in trace if "accept" in t)
+    print(f"cfg1 approx {shift}: {lock.summary()}")
+
+
+def test_random_reject_every_gate(gpu):
+    """random_reject_prob=1.0 (backend.py:433-441, :762-767): every gate
+    rejects every head, so every lazy check rescores and recovers every
+    head; lockstep with the oracle backend."""
+    kw = dict(budget_pct=0.25, coverage_threshold=0.9, lazy=True, check_interval=3,
+              random_reject_prob=1.0)
+    stats, trace, lock = _run(gpu, CFG1, kw, steps=7, seed=1021)
+    assert all(not bool(t["accept"].any()) for t in trace if "accept" in t)
+    assert stats["all_accepted_pct"] == 0.0 and stats["rescore_rate"] == 100.0
+
+
+def test_random_reject_never(gpu):
+    """random_reject_prob=0.0: every gate accepts every head.  Lockstep
+    with the oracle, and bit for bit the backend that accepts every head by
+    its threshold (coverage_threshold=0): outputs, selections and
+    statistics."""
+    kw = dict(budget_pct=0.25, coverage_threshold=0.9, lazy=True, check_interval=3,
+              random_reject_prob=0.0)
+    _run(gpu, CFG1, kw, steps=7, seed=1031)
+    inp = make_paged_inputs(**CFG1, seed=1032)
+    q, K, V, bt, cl = (t.to(gpu) for t in (inp.q, inp.k_cache, inp.v_cache, inp.block_tables,
+                                            inp.context_lens))
+    never = CVSABackend(8, 32, 128, 16, **kw)
+    base = CVSABackend(8, 32, 128, 16, **dict(kw, coverage_threshold=0.0,
+                                              random_reject_prob=None))
+    for step in range(7):
+        qs = jitter_query(q, 0.3, 1040 + step)
+        a = never(qs, K, V, bt, cl, 0)
+        b = base(qs, K, V, bt, cl, 0)
+        assert torch.equal(a, b), step
+        assert torch.equal(never._cached_selection[0][0], base._cached_selection[0][0])
+        assert torch.equal(never._cached_selection[0][1], base._cached_selection[0][1])
+        never.step_done(0, 1)
+        base.step_done(0, 1)
+    assert never.get_stats() == base.get_stats()

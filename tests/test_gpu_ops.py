@@ -288,6 +288,54 @@ def test_verified_decode_matches_reference_recovery(gpu, geom):
     assert (out.cpu().float() - want.float()).abs().max().item() < OUT_ATOL
 
 
+@pytest.mark.parametrize("geom", GEOMS[:5] + [GEOMS[6]])
+@pytest.mark.parametrize("pattern", ["mixed", "all_rejected", "all_accepted"])
+def test_verified_decode_approx_matches_reference(gpu, geom, pattern):
+    """Approximate recovery in one launch (cvsa_verified_decode_approx) vs
+    the reference's branch (backend.py:775-817) restated with the oracle:
+    accepted heads = normalised draft over the selection, rejected heads =
+    normalised sparse decode of the expanded top-k's first min(exp_budget,
+    n_valid) pages; (o, m, l) of every head, and the effective-budget
+    counters as the reference books them (n_per_head, plus min(exp_budget,
+    n_valid) on every head when some head is rejected)."""
+    B, H_q, H_kv, ctx = geom
+    G = H_q // H_kv
+    inp = _inputs(410, B, H_q, H_kv, ctx, hot_heads=list(range(0, H_kv, 2)), n_hot=6,
+                  hot_shift=9.0)
+    q, K, V, bt, cl = _dev(inp, gpu)
+    ps = ref.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens, H_kv, G, 16)
+    W = inp.block_tables.shape[1]
+    budget = max(3, W // 8)
+    exp_budget = min(max(budget + 1, int(W * 0.3)), W)
+    idx, nph = ref.select_topk(ps, budget, inp.context_lens, 16)
+    exp, exp_n = ref.select_topk(ps, exp_budget, inp.context_lens, 16)
+    g = torch.Generator().manual_seed(2)
+    accept = {"mixed": torch.rand(B, H_kv, generator=g) > 0.5,
+              "all_rejected": torch.zeros(B, H_kv, dtype=torch.bool),
+              "all_accepted": torch.ones(B, H_kv, dtype=torch.bool)}[pattern]
+    work = torch.zeros(2, dtype=torch.int64, device=gpu)
+    out, (o, m, l) = ops.verified_decode_approx(
+        q, K, V, bt, cl, idx.to(gpu), nph.to(gpu), accept.to(gpu), exp.to(gpu), H_kv, G, 16,
+        return_state=True, work=work)
+    wd = ref.sparse_decode_unnorm(inp.q, inp.k_cache, inp.v_cache, inp.block_tables, idx, nph,
+                                  inp.context_lens, H_kv, G, 16)
+    we = ref.sparse_decode_unnorm(inp.q, inp.k_cache, inp.v_cache, inp.block_tables, exp,
+                                  exp_n, inp.context_lens, H_kv, G, 16)
+    acc_q = accept.repeat_interleave(G, dim=1)
+    wo = torch.where(acc_q.unsqueeze(-1), wd[0], we[0])
+    wm = torch.where(acc_q, wd[1], we[1])
+    wl = torch.where(acc_q, wd[2], we[2])
+    _check_state(o.cpu(), m.cpu(), l.cpu(), wo, wm, wl)
+    want = torch.where(acc_q.unsqueeze(-1), ref.normalise(wd[0], wd[2], torch.float64),
+                       ref.normalise(we[0], we[2], torch.float64)).to(torch.bfloat16)
+    assert (out.cpu().float() - want.float()).abs().max().item() < OUT_ATOL
+    nv = ref.n_valid_pages(inp.context_lens, 16)
+    booked = int(nph.sum())
+    if not bool(accept.all()):
+        booked += int(exp_n.sum())
+    assert work.tolist() == [booked, int(nv.sum()) * H_kv]
+
+
 def test_compute_complement_exact(gpu):
     g = torch.Generator().manual_seed(9)
     B, H, k = 3, 8, 20

@@ -77,6 +77,76 @@ def test_plan_kinds_equal_separate_kernels(gpu, tau):
     assert torch.equal(stats_p, stats_r) and torch.equal(work_p, work_r)
 
 
+@pytest.mark.parametrize("tau", [0.0, 0.6, 0.995])
+@pytest.mark.parametrize("predict_keep", [1, 0])
+@pytest.mark.parametrize("shape", [(8, 4), (2, 4)])
+def test_approx_plan_equals_separate_kernels(gpu, tau, predict_keep, shape):
+    """A plan with approximate recovery (approx_budget): the first selection,
+    a lazy check (kept at tau 0, reselected otherwise, with either
+    speculative prediction) and a fixed-interval scoring step equal the
+    separate kernels bit for bit -- select, the expanded top-k of the
+    rejected rows (select_topk at approx_budget), verified_decode_approx --
+    and the rows the plan's selection kernel expanded are those of the
+    separate top-k.  Shapes (H_kv, G): the fused check launch at H_kv 8,
+    the sequential chain at H_kv 2."""
+    H, G = shape
+    inp, W, budget = _inputs(gpu, h=H, g=G)
+    ctx, bt = inp.context_lens, inp.block_tables
+    exp_budget = min(max(budget + 1, int(W * 0.5)), W)
+    stats_p = torch.zeros(6, dtype=torch.int64, device=gpu)
+    stats_r = torch.zeros(6, dtype=torch.int64, device=gpu)
+    work_p = torch.zeros(2, dtype=torch.int64, device=gpu)
+    work_r = torch.zeros(2, dtype=torch.int64, device=gpu)
+    plan = ops.StepPlan(inp.q, inp.k_cache, inp.v_cache, bt, ctx, H, G, 16, budget, tau,
+                        stats=stats_p, work=work_p, own_scores_cache=True,
+                        approx_budget=exp_budget)
+    sel_r = torch.empty(2, H, budget, dtype=torch.int32, device=gpu)
+    nph_r = torch.empty(2, H, dtype=torch.int32, device=gpu)
+    cov_r = torch.empty(2, H, dtype=torch.float32, device=gpu)
+    cache_r = torch.empty(2, H, W, dtype=torch.float32, device=gpu)
+
+    def expanded_tail(q, ps, acc):
+        exp, _ = ops.select_topk(ps, exp_budget, ctx, 16)
+        out = ops.verified_decode_approx(q, inp.k_cache, inp.v_cache, bt, ctx, sel_r, nph_r,
+                                         acc, exp, H, G, 16, output_dtype=q.dtype, work=work_r)
+        rej = ~acc
+        assert torch.equal(plan.approx_indices[rej], exp[rej])
+        return out
+
+    # the first selection of a lazy layer
+    q0 = jitter_query(inp.q, 0.5, 3)
+    got = plan.run(_lib.STEP_FRESH, q0)
+    ps = ops.score_pages(q0, inp.k_cache, bt, ctx, H, G, 16)
+    acc = ops.select_or_keep(ps, None, budget, ctx, 16, tau, sel_r, nph_r, cov_r, cache_r,
+                             stats_r)
+    assert torch.equal(got, expanded_tail(q0, ps, acc))
+    assert torch.equal(plan.page_indices, sel_r) and torch.equal(plan.n_per_head, nph_r)
+
+    # a lazy check, with the prediction given
+    if plan.spec_state is not None:
+        plan.spec_state[0] = predict_keep
+    q1 = jitter_query(inp.q, 0.5, 4)
+    got = plan.run(_lib.STEP_LAZY_CHECK, q1)
+    ps = ops.score_pages(q1, inp.k_cache, bt, ctx, H, G, 16)
+    chk, cov = ops.check_coverage(ps, sel_r, nph_r, tau)
+    acc = ops.select_or_keep(ps, chk, budget, ctx, 16, tau, sel_r, nph_r, cov, cache_r, stats_r)
+    assert torch.equal(got, expanded_tail(q1, ps, acc))
+    assert torch.equal(plan.accept.view(torch.bool), acc)
+    assert torch.equal(plan.page_indices, sel_r) and torch.equal(plan.n_per_head, nph_r)
+    assert bool(chk.all()) == (tau == 0.0)
+
+    # a fixed-interval scoring step
+    q2 = jitter_query(inp.q, 0.5, 5)
+    got = plan.run(_lib.STEP_SCORE, q2)
+    ps = ops.score_pages(q2, inp.k_cache, bt, ctx, H, G, 16)
+    acc = ops.select_or_keep(ps, None, budget, ctx, 16, tau, sel_r, nph_r, cov, None, stats_r,
+                             count_gate=True)
+    assert torch.equal(got, expanded_tail(q2, ps, acc))
+    assert torch.equal(stats_p, stats_r) and torch.equal(work_p, work_r)
+    if tau == 0.995:
+        assert not bool(acc.all())
+
+
 def _worst_pages(ps, budget, nph):
     """The `budget` lowest-scoring valid pages of every row (ascending page
     order): a selection whose coverage any top-k selection exceeds."""
