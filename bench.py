@@ -81,6 +81,29 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def parse_method(method):
+    """Backend settings of a method name of the reference's evaluation
+    harness (eval/longbench_cvsa.py:190-236): cvsa_{budget%}_{tau%} with the
+    suffixes c{M} (lazy checks every M steps), ar{P} (approximate recovery
+    at P% of the pages) and dL{l.l...} (dense layers).  The reference's
+    deployed setting is cvsa_5_90_c4_ar20_dL0 (eval/plot_pareto.py:141-150)."""
+    parts = method.split("_")
+    if len(parts) < 3 or parts[0] != "cvsa":
+        raise ValueError(f"method {method!r}: expected cvsa_<budget>_<tau>[_suffixes]")
+    out = dict(budget=int(parts[1]) / 100.0, taus=[int(parts[2]) / 100.0], lazy=False,
+               M=16, approx=None, dense_layers=None)
+    for p in parts[3:]:
+        if p.startswith("c") and p[1:].isdigit():
+            out.update(lazy=True, M=int(p[1:]))
+        elif p.startswith("ar") and p[2:].isdigit():
+            out["approx"] = int(p[2:]) / 100.0
+        elif p.startswith("dL"):
+            out["dense_layers"] = [int(x) for x in p[2:].split(".")]
+        else:
+            raise ValueError(f"method {method!r}: suffix {p!r} is not supported by the bench")
+    return out
+
+
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -114,6 +137,11 @@ def parse_args():
     ap.add_argument("--light-normalizer", action="store_true",
                     help="with --selector quest: Quest scores also drive the coverage gate "
                          "(no full-key scan on any step)")
+    ap.add_argument("--method", default=None,
+                    help="backend settings by the reference harness's method name, e.g. "
+                         "cvsa_5_90_c4_ar20_dL0 (its deployed setting: budget 5%%, tau 0.9, "
+                         "lazy M=4, approximate recovery at 20%%, layer 0 dense); default: "
+                         "the configuration's own settings")
     args = ap.parse_args()
     if args.light_normalizer and args.selector != "quest":
         ap.error("--light-normalizer requires --selector quest")
@@ -159,6 +187,18 @@ class Layer:
                 self.mgr.context_lens)
 
 
+def backend_kwargs(cfg, tau):
+    """CVSABackend / OracleCVSABackend keywords of the workload."""
+    kw = dict(budget_pct=cfg["budget"], coverage_threshold=tau, lazy=cfg["lazy"],
+              selector=cfg["selector"], light_normalizer=cfg["light_normalizer"])
+    kw.update(dict(check_interval=cfg["M"]) if cfg["lazy"] else dict(reuse_interval=cfg["M"]))
+    if cfg.get("approx") is not None:
+        kw["approx_recovery_pct"] = cfg["approx"]
+    if cfg.get("dense_layers"):
+        kw["dense_layers"] = list(cfg["dense_layers"])
+    return kw
+
+
 def build_layers(name, cfg, dev, n_layers, hot_shift, sink_shift, steps):
     from cvsa.synthetic import make_paged_inputs
     append_steps = steps if cfg["append"] else 0
@@ -202,7 +242,16 @@ def step_bytes(kind, accept, cfg, W, budget):
         total += scores + 4 * n_sel * B * H                           # coverage of cached sel
     if kind in ("score", "rescore"):
         total += scores + 4 * n_sel * B * H                           # top-k select
-        pages = sum(n_sel if a else n_valid for a in accept)
+        if cfg.get("approx") is not None:
+            # Approximate recovery: a rejected head reads its expanded
+            # selection (which contains the draft's pages) instead of every
+            # valid page.
+            exp_n = min(min(max(budget + 1, int(W * cfg["approx"])), W), n_valid)
+            pages = sum(n_sel if a else exp_n for a in accept)
+        else:
+            pages = sum(n_sel if a else n_valid for a in accept)
+    elif kind == "dense":
+        pages = n_valid * B * H
     else:
         pages = n_sel * B * H
     total += pages * (2 * page_kv + 8) + q_bytes + out_bytes           # decode
@@ -228,12 +277,10 @@ def run_e2e(name, cfg, n_layers, args, dev, hot_shift, sink_shift):
             max_new_tokens=args.warmup + args.steps + 1, seed=2000 + int(name[3]), device=dev,
             hot_shift=hot_shift, sink_pages=cfg["sink_pages"], sink_shift=sink_shift,
             **cfg["gen"])
-        sched = (dict(lazy=True, check_interval=cfg["M"]) if cfg["lazy"]
-                 else dict(lazy=False, reuse_interval=cfg["M"]))
         backend = CVSABackend(num_kv_heads=cfg["H_kv"], num_q_heads=cfg["H_q"], head_dim=D,
-                              block_size=BS, num_layers=n_layers, budget_pct=cfg["budget"],
-                              coverage_threshold=0.9, selector=cfg["selector"],
-                              light_normalizer=cfg["light_normalizer"], **sched)
+                              block_size=BS, num_layers=n_layers,
+                              **backend_kwargs(cfg, cfg["taus"][0] if 0.9 not in cfg["taus"]
+                                               else 0.9))
         res = DecodeDriver(backend, layers, graphs=graphs,
                            fuse_append=key.endswith("fused_append")).run(args.steps, args.warmup)
         out[key] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()
@@ -294,7 +341,8 @@ def cpu_baseline(cfg, layer0, n_steps, tau):
     """The CPU oracle (fp32, all host cores) on layer 0's cache: decode steps
     from a fresh backend (the first is a scoring step), n_steps of them, or
     (n_steps None) whole schedule cycles of M steps until CPU_SAMPLE_S
-    seconds of step time have accumulated."""
+    seconds of step time have accumulated.  The calls use the first layer
+    index that is not a dense layer of the method."""
     import torch
     from oracle.backend_oracle import OracleCVSABackend
     from cvsa.synthetic import jitter_query
@@ -302,18 +350,18 @@ def cpu_baseline(cfg, layer0, n_steps, tau):
     inp = layer0.inp
     q0 = inp.q.cpu()
     args = [t.cpu() for t in (inp.k_cache, inp.v_cache, inp.block_tables, inp.context_lens)]
-    b = OracleCVSABackend(cfg["H_kv"], cfg["H_q"], D, BS, budget_pct=cfg["budget"],
-                          coverage_threshold=tau, lazy=cfg["lazy"], check_interval=cfg["M"],
-                          reuse_interval=cfg["M"], selector=cfg["selector"],
-                          light_normalizer=cfg["light_normalizer"], acc_dtype=torch.float32)
+    b = OracleCVSABackend(cfg["H_kv"], cfg["H_q"], D, BS, **backend_kwargs(cfg, tau),
+                          acc_dtype=torch.float32)
+    dense = set(cfg.get("dense_layers") or [])
+    lid = min(i for i in range(len(dense) + 1) if i not in dense)
     times = []
     s = 0
     while True:
         q = jitter_query(q0, Q_JITTER, 50_000 + s)
         t0 = time.perf_counter()
-        b(q, *args, 0)
+        b(q, *args, lid)
         times.append(time.perf_counter() - t0)
-        b.step_done(0, 1)
+        b.step_done(lid, lid + 1)
         s += 1
         if n_steps is not None:
             if s >= n_steps:
@@ -358,10 +406,7 @@ def run_schedule(cfg, layers, tau, args, dev):
         new_kv = [[(torch.randn(B, H_kv, D, generator=g, device=dev).to(torch.bfloat16),
                     torch.randn(B, H_kv, D, generator=g, device=dev).to(torch.bfloat16))
                    for _ in range(L)] for _ in range(total_steps)]
-    backend = CVSABackend(H_kv, H_q, D, BS, num_layers=L, budget_pct=cfg["budget"],
-                          coverage_threshold=tau, lazy=cfg["lazy"], check_interval=cfg["M"],
-                          reuse_interval=cfg["M"], selector=cfg["selector"],
-                          light_normalizer=cfg["light_normalizer"])
+    backend = CVSABackend(H_kv, H_q, D, BS, num_layers=L, **backend_kwargs(cfg, tau))
     kinds = []        # (step, layer, kind, accept tensor or None)
 
     def run_step(s, record):
@@ -374,7 +419,9 @@ def run_schedule(cfg, layers, tau, args, dev):
             if record:
                 checked = backend._total_coverage_checks > c0
                 scored = backend._total_scoring_steps > s0
-                if scored:
+                if l in backend._dense_layers:
+                    kind = "dense"
+                elif scored:
                     kind = "rescore" if (had and cfg["lazy"]) else "score"
                 else:
                     kind = "check" if checked else "reuse"
@@ -432,7 +479,7 @@ def run_schedule(cfg, layers, tau, args, dev):
             accepted_heads += sum(a)
             total_heads += len(a)
         total_bytes += step_bytes(kind, a, cfg, W, budget)
-        if kind == "rescore" or s not in step_kinds:
+        if kind == "rescore" or s not in step_kinds or step_kinds[s] == "dense":
             step_kinds[s] = kind
     by_kind = {}
     for i, us in enumerate(step_us):
@@ -458,6 +505,9 @@ def main():
 
     cfg = dict(CONFIGS[args.config], selector=args.selector,
                light_normalizer=args.light_normalizer)
+    if args.method is not None:
+        cfg.update(parse_method(args.method))
+        cfg["desc"] += f"; method {args.method}"
     if args.selector == "quest":
         cfg["desc"] += (", Quest selector + light normalizer" if args.light_normalizer
                         else ", Quest selector (exact gate)")
