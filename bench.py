@@ -21,6 +21,8 @@ the achieved HBM bandwidth of the average step (algorithmic bytes / time).
 from __future__ import annotations
 
 import argparse
+import contextlib
+import gc
 import json
 import os
 import platform
@@ -79,6 +81,21 @@ CONFIGS = {
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+@contextlib.contextmanager
+def no_gc():
+    """A timed region without Python's cyclic garbage collector: a
+    collection pause (tens of ms with the bench's many small objects) would
+    leave the GPU waiting for the host inside the timing."""
+    gc.collect()
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
 
 
 def parse_method(method):
@@ -281,8 +298,10 @@ def run_e2e(name, cfg, n_layers, args, dev, hot_shift, sink_shift):
                               block_size=BS, num_layers=n_layers,
                               **backend_kwargs(cfg, cfg["taus"][0] if 0.9 not in cfg["taus"]
                                                else 0.9))
-        res = DecodeDriver(backend, layers, graphs=graphs,
-                           fuse_append=key.endswith("fused_append")).run(args.steps, args.warmup)
+        with no_gc():
+            res = DecodeDriver(backend, layers, graphs=graphs,
+                               fuse_append=key.endswith("fused_append")).run(args.steps,
+                                                                             args.warmup)
         out[key] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in res.items()
                     if k != "per_step_ms"}
         out[key]["per_step_ms"] = [round(x, 3) for x in res["per_step_ms"]]
@@ -449,17 +468,18 @@ def run_schedule(cfg, layers, tau, args, dev):
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    host_each = []
-    for i in range(args.steps):
-        th = time.perf_counter()
-        evs[i][0].record()
-        run_step(args.warmup + i, False)
-        evs[i][1].record()
-        host_each.append((time.perf_counter() - th) * 1e6 / len(layers))
-    host = time.perf_counter() - t0
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with no_gc():
+        t0 = time.perf_counter()
+        host_each = []
+        for i in range(args.steps):
+            th = time.perf_counter()
+            evs[i][0].record()
+            run_step(args.warmup + i, False)
+            evs[i][1].record()
+            host_each.append((time.perf_counter() - th) * 1e6 / len(layers))
+        host = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     stats_pass2 = backend.get_stats()
     if stats_pass2 != stats_pass1:
         log(f"WARNING: timed pass diverged from the classification pass: "

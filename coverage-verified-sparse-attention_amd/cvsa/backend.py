@@ -52,6 +52,7 @@ from __future__ import annotations
 
 from typing import Dict, List, Optional, Set, Tuple
 
+import ctypes
 import weakref
 
 import torch
@@ -100,6 +101,74 @@ class _PendingExpanded:
             return None
         return ops.select_topk(self.scores, self.exp_budget, self.context_lens,
                                self.block_size)
+
+
+class _FusedReuse:
+    """A layer's reuse step with the token append folded in
+    (cvsa_step_plan_run_append), checked in full once by call_with_append.
+    A later call only compares identities (the layer's plan, selection,
+    scores, counters, the manager's buffers, the stream) and the layout of
+    q and the new rows with the ones checked; any difference sends the call
+    back to the checked path.  The slots go through one ctypes array."""
+
+    __slots__ = ("plan", "manager", "pages_dev", "kv_shape", "dev_index", "out_args",
+                 "slots", "fn", "handle", "stream", "new_stride")
+
+    def __init__(self, plan, manager, k_new):
+        self.plan = plan
+        self.manager = manager
+        self.pages_dev = manager._pages_allocated_dev
+        self.kv_shape = k_new.shape
+        self.dev_index = plan.dev.index
+        self.out_args = (plan.out_shape, plan.dev, plan.out_dtype)
+        self.slots = (ctypes.c_int32 * (2 * manager.batch_size))()
+        self.fn = plan._run_append
+        self.handle = plan._h
+        self.stream = plan.stream
+        self.new_stride = k_new.stride(0)
+
+    def fits(self, backend, q, k_new, v_new, layer_idx) -> bool:
+        plan = self.plan
+        m = self.manager
+        cache = m.cache
+        r = plan.refs
+        if (backend._step_plans.get(layer_idx) is not plan or backend._track_timing
+                or r[0] is not cache.k_cache or r[1] is not cache.v_cache
+                or r[2] is not m.block_tables or r[3] is not m.context_lens
+                or r[4] is not backend._work_buf or r[5] is not backend._dev_stats
+                or m._pages_allocated_dev is not self.pages_dev):
+            return False
+        sel = backend._cached_selection.get(layer_idx)
+        cached = backend._cached_page_scores.get(layer_idx)
+        if (sel is None or sel[0] is not plan.page_indices
+                or not (cached is plan.scores_cache or cached is plan.page_scores)):
+            return False
+        if r[7] is not None and backend._plan_selector(cache.k_cache)[1] is not r[7]:
+            return False
+        bf16 = torch.bfloat16
+        idx = self.dev_index
+        return (q.dtype is plan.out_dtype and (q.shape, q.stride()) == plan.q_meta
+                and q.get_device() == idx and k_new.dtype is bf16 and v_new.dtype is bf16
+                and k_new.shape == self.kv_shape and v_new.shape == self.kv_shape
+                and k_new.get_device() == idx and v_new.get_device() == idx
+                and k_new.is_contiguous() and v_new.is_contiguous()
+                and torch._C._cuda_getCurrentRawStream(idx) == self.stream)
+
+    def run(self, q, k_new, v_new):
+        """The launch, or None when a pointer is not 16-byte aligned."""
+        qp, kp, vp = q.data_ptr(), k_new.data_ptr(), v_new.data_ptr()
+        if (qp | kp | vp) & 15:
+            return None
+        m = self.manager
+        need = m.fill_fused_slots(self.slots)
+        shape, dev, dtype = self.out_args
+        out = torch.empty(shape, device=dev, dtype=dtype)
+        rc = self.fn(self.handle, qp, out.data_ptr(), kp, vp, self.new_stride,
+                     self.pages_dev.data_ptr(), self.slots, None, self.stream)
+        if rc != 0:
+            ops.check(rc, "step_plan_run_append")
+        m.commit_fused(need)
+        return out
 
 
 def _device_counter(slot: int, host_name: str):
@@ -216,6 +285,7 @@ class CVSABackend:
         self._reuse_state: Dict[int, Tuple[torch.Tensor, torch.Tensor, int]] = {}
         self._reuse_plans: Dict[int, ops.DecodeCall] = {}
         self._step_plans: Dict[int, ops.StepPlan] = {}
+        self._fused: Dict[int, _FusedReuse] = {}
         self._cached_selection: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
         self._cached_page_scores: Dict[int, torch.Tensor] = {}
 
@@ -282,6 +352,7 @@ class CVSABackend:
         self._step = 0
         self._reuse_state = {}
         self._reuse_plans = {}
+        self._fused = {}
         # Step plans that own their selection stay: the next first selection
         # of their layer is made in their buffers again.
         self._step_plans = {k: p for k, p in self._step_plans.items() if p.owns_selection}
@@ -415,13 +486,35 @@ class CVSABackend:
             return None
         return self._matching_plan(layer_idx, q, k_cache, v_cache, block_tables, context_lens)
 
+    def _plain_reuse_step(self, layer_idx) -> bool:
+        """Whether a call of this layer at the current step is a reuse step
+        (the schedule of __call__, backend.py:313-366)."""
+        if layer_idx in self._dense_layers or layer_idx not in self._reuse_state:
+            return False
+        step = self._step
+        if self.lazy:
+            return not (step % self.check_interval == 0
+                        or (step % self.coverage_interval == 0
+                            and layer_idx in self._cached_page_scores))
+        return step % self.reuse_interval != 0
+
     def call_with_append(self, q, k_new, v_new, manager, layer_idx):
         """The decode loops' append then call (``manager.append_tokens_kv(k_new,
         v_new)``, then this backend on the manager's cache, tables and context
         lengths), with the append folded into the decode launch when the call
         is a reuse step through a step plan (cvsa_step_plan_run_append);
         otherwise the two in turn.  Same outputs, cache, tables, context
-        lengths and statistics either way; no counterpart in the reference."""
+        lengths and statistics either way; no counterpart in the reference.
+        The first folded call of a layer is checked in full; later ones reuse
+        that check while the plan, buffers, stream and layouts stay the same
+        (a decode loop's per-layer host cost)."""
+        fc = self._fused.get(layer_idx)
+        if (fc is not None and fc.manager is manager and self._plain_reuse_step(layer_idx)
+                and fc.fits(self, q, k_new, v_new, layer_idx)):
+            out = fc.run(q, k_new, v_new)
+            if out is not None:
+                self.note_replayed_reuse(layer_idx)
+                return out
         cache = manager.cache
         args = (cache.k_cache, cache.v_cache, manager.block_tables, manager.context_lens)
         plan = None
@@ -433,6 +526,7 @@ class CVSABackend:
         slots, commit = manager.fused_append_slots()
         out = plan.run_reuse_append(q, k_new, v_new, manager._pages_allocated_dev, slots)
         commit()
+        self._fused[layer_idx] = _FusedReuse(plan, manager, k_new)
         self.note_replayed_reuse(layer_idx)
         return out
 

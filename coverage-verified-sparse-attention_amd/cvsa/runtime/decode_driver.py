@@ -127,10 +127,18 @@ class DecodeDriver:
         self._fold_graphs = (self.graphs and self.fuse_append and layers.head_dim == 128
                              and layers.block_size == 16 and B <= 256
                              and layers.num_q_heads // layers.num_kv_heads <= 16)
-        if self._fold_graphs:
+        # Eager steps with folded appends read their inputs from static
+        # buffers too, through per-layer views made once: a view made per
+        # layer and step (indexing or unbind) costs the host more than the
+        # folded call itself.
+        self._static_eager = self.fuse_append and not self.graphs
+        if self._fold_graphs or self._static_eager:
             shape = (L, B, layers.num_kv_heads, layers.head_dim)
             self.k_static = torch.empty(shape, dtype=torch.bfloat16, device=layers.device)
             self.v_static = torch.empty(shape, dtype=torch.bfloat16, device=layers.device)
+            self._views = tuple(t.unbind(0) for t in (self.q_static, self.k_static,
+                                                      self.v_static))
+        if self._fold_graphs:
             self._slots = {}  # chunk index -> [device slots, pinned slots, event]
 
     # ------------------------------------------------------------ one step
@@ -143,15 +151,16 @@ class DecodeDriver:
         return [range(i, min(L, i + c)) for i in range(0, L, c)]
 
     def static_inputs(self):
-        """The graph-mode input buffers (q [L, B, H_q, D], and with folded
-        appends k / v [L, B, H_kv, D]; None where the mode has none).  A step
-        given these tensors themselves reads them in place: a caller that
-        makes its inputs there (as a captured model's projections would)
-        saves the per-step copies into them."""
+        """The input buffers of the graph modes and of eager steps with
+        folded appends (q [L, B, H_q, D], and with folded appends k / v [L,
+        B, H_kv, D]; None where the mode has none).  A step given these
+        tensors themselves reads them in place: a caller that makes its
+        inputs there (as a captured model's projections would) saves the
+        per-step copies into them."""
+        if self._static_eager or self._fold_graphs:
+            return self.q_static, self.k_static, self.v_static
         if not self.graphs:
             return None, None, None
-        if self._fold_graphs:
-            return self.q_static, self.k_static, self.v_static
         return self.q_static, None, None
 
     def _eager(self, q, k=None, v=None, layers=None) -> List[torch.Tensor]:
@@ -162,8 +171,17 @@ class DecodeDriver:
         if k is not None and self.fuse_append:
             call, done = self.backend.call_with_append, self.backend.step_done
             managers = self.layers.managers
+            if self._static_eager or k is self.k_static:
+                # The static buffers' per-layer views (inputs copied in
+                # unless they were made there).
+                for t, buf in zip((q, k, v), (self.q_static, self.k_static, self.v_static)):
+                    if t is not buf:
+                        buf.copy_(t)
+                qs, ks, vs = self._views
+            else:
+                qs, ks, vs = q, k, v
             for l in (range(L) if layers is None else layers):
-                outs.append(call(q[l], k[l], v[l], managers[l], l))
+                outs.append(call(qs[l], ks[l], vs[l], managers[l], l))
                 done(l, L)
             return outs
         for l in (range(L) if layers is None else layers):

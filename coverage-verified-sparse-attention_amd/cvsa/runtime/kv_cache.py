@@ -204,29 +204,44 @@ class SequenceKVManager:
         of append_token_kv (kv_cache.py:133-150) applied to the host mirror.
         Returns (slots, commit); call commit() once the launch is enqueued
         (it reserves the blocks and advances the mirror)."""
-        seqs = range(self.batch_size)
-        need = self._plan_append(seqs)
-        first = self.cache._next_free
-        if first + need > self.cache._total_blocks:
-            raise AssertionError(f"Out of blocks: need {need}, have "
-                                 f"{self.cache._total_blocks - first}")
-        bs = self.block_size
         slots = (ctypes.c_int32 * (2 * self.batch_size))()
+        need = self.fill_fused_slots(slots)
+
+        def commit():
+            self.commit_fused(need)
+
+        return slots, commit
+
+    def fill_fused_slots(self, slots) -> int:
+        """fused_append_slots into an existing ctypes int32 array of 2 * B
+        entries; returns the number of blocks the append allocates, to be
+        reserved with commit_fused(n) once the launch is enqueued."""
+        bs = self.block_size
+        first = self.cache._next_free
+        pages = self._pages_allocated
+        ctxs = self._ctx_host
         r = 0
-        for s in seqs:
-            ctx = self._ctx_host[s]
+        for s in range(self.batch_size):
+            ctx = ctxs[s]
+            page = ctx // bs
+            if page >= self.max_pages:
+                raise IndexError(f"sequence {s}: context {ctx} + 1 exceeds the block table "
+                                 f"({self.max_pages} pages)")
             slots[2 * s] = ctx
-            if ctx % bs == 0 and ctx // bs >= self._pages_allocated[s]:
+            if ctx % bs == 0 and page >= pages[s]:
                 slots[2 * s + 1] = first + r
                 r += 1
             else:
                 slots[2 * s + 1] = -1
+        if first + r > self.cache._total_blocks:
+            raise AssertionError(f"Out of blocks: need {r}, have "
+                                 f"{self.cache._total_blocks - first}")
+        return r
 
-        def commit():
-            self.cache._reserve(need)
-            self._commit_append(seqs)
-
-        return slots, commit
+    def commit_fused(self, need: int) -> None:
+        """Reserve the blocks of a fused append and advance the host mirror."""
+        self.cache._reserve(need)
+        self._commit_append(range(self.batch_size))
 
     def _append(self, seq_begin: int, k: torch.Tensor, v: torch.Tensor):
         n = k.shape[0]

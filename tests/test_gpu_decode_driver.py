@@ -162,15 +162,26 @@ def test_driver_run_reports_latency(gpu):
 
 
 def _count_fused(monkeypatch):
+    """Counts folded reuse calls: the checked entry (StepPlan.run_reuse_append)
+    and the backend's prepared call (_FusedReuse.run)."""
     from cvsa import ops
+    from cvsa import backend as backend_mod
     calls = []
     orig = ops.StepPlan.run_reuse_append
+    orig_fast = backend_mod._FusedReuse.run
 
     def counted(self, *a, **k):
         calls.append(1)
         return orig(self, *a, **k)
 
+    def counted_fast(self, *a, **k):
+        out = orig_fast(self, *a, **k)
+        if out is not None:
+            calls.append(1)
+        return out
+
     monkeypatch.setattr(ops.StepPlan, "run_reuse_append", counted)
+    monkeypatch.setattr(backend_mod._FusedReuse, "run", counted_fast)
     return calls
 
 
@@ -224,6 +235,78 @@ def test_fused_append_equals_separate(gpu, monkeypatch, shape):
     assert ba.get_stats() == bb.get_stats()
     # every reuse call of the fused run (3 of every 4 steps per layer) was fused
     assert len(calls) == L * (steps - steps // 4), len(calls)
+
+
+def test_fused_fast_path_falls_back(gpu, monkeypatch):
+    """The prepared folded call (after a layer's first checked one) hands a
+    call back to the checked path when what it was checked for changes: a
+    non-contiguous row tensor, another stream, a reset backend, a cache
+    swapped under the manager.  Outputs, caches and statistics equal the
+    separate append and call throughout."""
+    from cvsa import backend as backend_mod
+    fast = []
+    orig_fast = backend_mod._FusedReuse.run
+
+    def counted_fast(self, *a, **k):
+        fast.append(1)
+        return orig_fast(self, *a, **k)
+
+    monkeypatch.setattr(backend_mod._FusedReuse, "run", counted_fast)
+    runs = []
+    for fuse in (False, True):
+        layers = SyntheticDecodeLayers(num_layers=1, batch=2, num_q_heads=32, num_kv_heads=8,
+                                       head_dim=128, context_len=[1500, 2100],
+                                       max_new_tokens=40, seed=31, device=gpu,
+                                       hot_heads=[0, 1], n_hot=6, hot_shift=9.0)
+        backend = CVSABackend(num_kv_heads=8, num_q_heads=32, head_dim=128, block_size=16,
+                              num_layers=1, budget_pct=0.25, coverage_threshold=0.9,
+                              lazy=True, check_interval=5)
+        runs.append((layers, backend))
+    (la, ba), (lb, bb) = runs
+    side = torch.cuda.Stream(gpu)
+
+    def step(i, variant):
+        q, k, v = la.step_inputs(i)
+        ma, mb = la.managers[0], lb.managers[0]
+        ma.append_tokens_kv(k[0], v[0])
+        ca = la.caches[0]
+        a = ba(q[0], ca.k_cache, ca.v_cache, ma.block_tables, ma.context_lens, 0)
+        kb, vb = k[0], v[0]
+        if variant == "strided":
+            kb = torch.empty(kb.shape[0], kb.shape[1], 2 * kb.shape[2], dtype=kb.dtype,
+                             device=gpu)[:, :, ::2].copy_(kb)
+            assert not kb.is_contiguous()
+        n0 = len(fast)
+        if variant == "stream":
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                b = bb.call_with_append(q[0], kb, vb, mb, 0)
+            torch.cuda.current_stream().wait_stream(side)
+        else:
+            b = bb.call_with_append(q[0], kb, vb, mb, 0)
+        ba.step_done(0, 1)
+        bb.step_done(0, 1)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), (i, variant)
+        return len(fast) > n0
+
+    took = [step(i, "plain") for i in range(8)]
+    assert any(took[2:5]) and any(took[6:8]), took  # reuse steps after the first
+    assert not step(8, "strided") and not step(9, "stream")
+    ba.reset()
+    bb.reset()
+    assert not step(10, "plain")          # a scoring step after reset
+    took = [step(i, "plain") for i in range(11, 16)]  # backend steps 1-5 (5: a check)
+    assert took[1] and took[2] and not took[4], took
+    for (layers, _b) in runs:             # the same blocks under a new tensor object
+        c = layers.caches[0]
+        c.k_cache = c.k_cache.clone()
+    assert not step(16, "plain")          # a reuse step over the new cache: checked path
+    torch.cuda.synchronize()
+    ca, cb = la.caches[0], lb.caches[0]
+    assert torch.equal(ca.k_cache, cb.k_cache) and torch.equal(ca.v_cache, cb.v_cache)
+    assert torch.equal(la.managers[0].context_lens, lb.managers[0].context_lens)
+    assert ba.get_stats() == bb.get_stats()
 
 
 def test_fused_append_rejects_inconsistent_slots(gpu):
