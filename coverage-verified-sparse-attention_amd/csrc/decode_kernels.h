@@ -128,9 +128,11 @@ struct AppendArgs {
   // that a captured graph replays), or NULL: the slots are slot[].  The host
   // checks slot[] before the launch; device slots are checked here: one out
   // of range (context length outside [0, 16 W), a new block outside
-  // [-1, num_blocks), or a new block not at a page start) appends nothing
-  // and leaves that sequence's outputs undefined.
+  // [-1, num_blocks), or a new block not at a page start) appends nothing,
+  // leaves that sequence's outputs undefined and adds 1 to *slot_errors
+  // (when given).
   const int2 *slot_dev;
+  int32_t *slot_errors;
   int2 slot[kMaxAppendSeqs];  // (context length before the append, new block or -1)
 };
 
@@ -962,6 +964,8 @@ __global__ __launch_bounds__(NW * kWave) void listed_append_kernel(const DecodeA
     blk = nt.new_blk >= 0 ? nt.new_blk : a.block_tables[(int64_t)b * a.bt_sb + nt.page];
     x = *reinterpret_cast<const uint4 *>((lane >= 16 ? nt.v : nt.k) + 8 * (lane & 15));
   }
+  if (!ok && split == 0 && h == 0 && threadIdx.x == 0 && app.slot_errors != nullptr)
+    atomicAdd(app.slot_errors, 1);  // a rejected device slot is reported, not dropped silently
   listed_walk<G, Engine, NW, PD, true>(a, split, bh, lp, phys, L, nt);
   if (!writer) return;
   if (lane < 32 && blk >= 0 && blk < a.num_blocks) {

@@ -375,7 +375,7 @@ extern "C" int cvsa_sparse_decode_append(
     int32_t D, int32_t block_size, int32_t W, void *out, int32_t out_dtype, int64_t *work,
     void *workspace, size_t workspace_bytes, const uint16_t *k_new, const uint16_t *v_new,
     int64_t new_stride_b, int32_t *pages_allocated, const int32_t *slots,
-    const int32_t *slots_dev, void *stream) {
+    const int32_t *slots_dev, int32_t *slot_errors, void *stream) {
   const char *name = "sparse_decode_append";
   CVSA_REQUIRE((slots == nullptr) != (slots_dev == nullptr), CVSA_ERR_INVALID,
                "%s: exactly one of slots (host) and slots_dev (device) is required", name);
@@ -428,6 +428,7 @@ extern "C" int cvsa_sparse_decode_append(
   app.pages_allocated = pages_allocated;
   app.max_pages = W;
   app.slot_dev = reinterpret_cast<const int2 *>(slots_dev);
+  app.slot_errors = slots_dev != nullptr ? slot_errors : nullptr;
   if (slots != nullptr)
     for (int b = 0; b < B; ++b) app.slot[b] = make_int2(slots[2 * b], slots[2 * b + 1]);
   bind_workspace(a, workspace, need);

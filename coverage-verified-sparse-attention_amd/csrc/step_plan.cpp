@@ -250,7 +250,7 @@ extern "C" int cvsa_step_plan_run_append(cvsa_step_plan *plan, const uint16_t *q
                                          const uint16_t *k_new, const uint16_t *v_new,
                                          int64_t new_stride_b, int32_t *pages_allocated,
                                          const int32_t *slots, const int32_t *slots_dev,
-                                         void *stream) {
+                                         int32_t *slot_errors, void *stream) {
   STEP_REQUIRE(plan && q && out, CVSA_ERR_INVALID, "step_plan_run_append: null argument");
   STEP_REQUIRE(aligned16(q), CVSA_ERR_INVALID,
                "step_plan_run_append: q must be 16-byte aligned");
@@ -263,7 +263,7 @@ extern "C" int cvsa_step_plan_run_append(cvsa_step_plan *plan, const uint16_t *q
       d.bt_stride_b, const_cast<int32_t *>(d.context_lens), d.page_indices, d.budget,
       d.n_per_head, d.budget, d.B, d.H_q, d.H_kv, d.D, d.block_size, d.W, out, d.out_dtype,
       d.work, d.workspace, d.workspace_bytes, k_new, v_new, new_stride_b, pages_allocated,
-      slots, slots_dev, stream);
+      slots, slots_dev, slot_errors, stream);
 }
 
 extern "C" int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint16_t *q,

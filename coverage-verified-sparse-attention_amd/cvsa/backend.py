@@ -164,7 +164,7 @@ class _FusedReuse:
         shape, dev, dtype = self.out_args
         out = torch.empty(shape, device=dev, dtype=dtype)
         rc = self.fn(self.handle, qp, out.data_ptr(), kp, vp, self.new_stride,
-                     self.pages_dev.data_ptr(), self.slots, None, self.stream)
+                     self.pages_dev.data_ptr(), self.slots, None, None, self.stream)
         if rc != 0:
             ops.check(rc, "step_plan_run_append")
         m.commit_fused(need)

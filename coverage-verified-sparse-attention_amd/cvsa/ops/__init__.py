@@ -798,14 +798,17 @@ class StepPlan:
 
     def run_reuse_append(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                          pages_allocated: torch.Tensor, slots=None,
-                         slots_dev: Optional[torch.Tensor] = None) -> torch.Tensor:
+                         slots_dev: Optional[torch.Tensor] = None,
+                         slot_errors: Optional[torch.Tensor] = None) -> torch.Tensor:
         """A reuse step with the step's token append folded in
         (cvsa_step_plan_run_append): k_new / v_new [B, H_kv, D] contiguous
         bf16, pages_allocated the int32 [B] allocation counts on the device,
         slots the host int32 array of SequenceKVManager.fused_append_slots,
         or slots_dev the same values in a contiguous int32 [B, 2] device
-        tensor (for a launch a captured graph replays).  Writes the plan's
-        caches, block table and context lengths."""
+        tensor (for a launch a captured graph replays; a sequence whose
+        device slot is out of range appends nothing and adds 1 to
+        ``slot_errors``, an optional int32 device counter).  Writes the
+        plan's caches, block table and context lengths."""
         who = "run_reuse_append"
         if (slots is None) == (slots_dev is None):
             raise ValueError(f"{who}: give exactly one of slots and slots_dev")
@@ -822,13 +825,14 @@ class StepPlan:
                 _append_slots(who, slots_dev, B, self.dev)
                 self._slots_ok = slots_dev
             slot_arr = None
+            _check_slot_errors(who, slot_errors, self.dev)
         else:
             slot_arr, _ = _append_slots(who, slots, B, self.dev)
         out = torch.empty(self.out_shape, device=self.dev, dtype=self.out_dtype)
         check(self._run_append(
             self._h, q.data_ptr(), out.data_ptr(), k_new.data_ptr(), v_new.data_ptr(),
             k_new.stride(0), pages_allocated.data_ptr(), slot_arr, _ptr(slots_dev),
-            self.stream), "step_plan_run_append")
+            _ptr(slot_errors), self.stream), "step_plan_run_append")
         return out
 
 
@@ -857,6 +861,13 @@ def _append_slots(who: str, slots, B: int, dev):
     if isinstance(slots, ctypes.Array) and slots._type_ is ctypes.c_int32:
         return slots, None
     return (ctypes.c_int32 * (2 * B))(*slots), None
+
+
+def _check_slot_errors(who: str, slot_errors, dev) -> None:
+    if slot_errors is not None and (
+            not isinstance(slot_errors, torch.Tensor) or slot_errors.dtype != torch.int32
+            or slot_errors.numel() < 1 or slot_errors.device != dev):
+        raise ValueError(f"{who}: slot_errors must be an int32 device tensor on {dev}")
 
 
 def _check_pages_allocated(who: str, pages_allocated, B: int, dev) -> None:
@@ -908,7 +919,8 @@ def sparse_decode(q, k_cache, v_cache, block_tables, page_indices, n_per_head,
 
 def sparse_decode_append(q, k_cache, v_cache, block_tables, context_lens, page_indices,
                          n_per_head, k_new, v_new, pages_allocated, slots, num_kv_heads,
-                         num_q_per_kv, block_size, work: Optional[torch.Tensor] = None):
+                         num_q_per_kv, block_size, work: Optional[torch.Tensor] = None,
+                         slot_errors: Optional[torch.Tensor] = None):
     """append_kv of one token per sequence, then sparse_decode over the
     appended cache, in one launch where the shapes allow
     (cvsa_sparse_decode_append; no reference counterpart).
@@ -919,7 +931,8 @@ def sparse_decode_append(q, k_cache, v_cache, block_tables, context_lens, page_i
     contiguous int32 [B, 2] tensor on the device (the one-launch shapes
     only: D = 128, 16-token pages, at most 16 query heads per KV head and
     256 sequences; the launch checks them, and a sequence whose slot is out
-    of range appends nothing and gets an undefined output).  block_tables,
+    of range appends nothing, gets an undefined output and adds 1 to
+    ``slot_errors``, an optional int32 [1] device counter).  block_tables,
     context_lens and pages_allocated (contiguous int32) and the caches are
     updated in place.  Returns the normalised output [B, H_q, D] in q.dtype.
     """
@@ -938,6 +951,7 @@ def sparse_decode_append(q, k_cache, v_cache, block_tables, context_lens, page_i
         raise ValueError("sparse_decode_append: cache block_size / head_dim mismatch")
     _check_new_rows("sparse_decode_append", k_new, v_new, (B, num_kv_heads, D), dev)
     slot_arr, slot_dev = _append_slots("sparse_decode_append", slots, B, dev)
+    _check_slot_errors("sparse_decode_append", slot_errors, dev)
     W = block_tables.shape[1]
     L = _lib.load()
     need = L.cvsa_decode_workspace_bytes(B, H_q, num_kv_heads, D, k, W, 0)
@@ -951,8 +965,8 @@ def sparse_decode_append(q, k_cache, v_cache, block_tables, context_lens, page_i
         context_lens.data_ptr(), pi.data_ptr(), pi.stride(0), nph.data_ptr(), k, B, H_q,
         num_kv_heads, D, block_size, W, out.data_ptr(), _DTYPE_CODE[q.dtype], _ptr(work),
         _ptr(ws), 0 if ws is None else ws.numel(), k_new.data_ptr(), v_new.data_ptr(),
-        k_new.stride(0), pages_allocated.data_ptr(), slot_arr, _ptr(slot_dev), _stream(dev)),
-        "sparse_decode_append")
+        k_new.stride(0), pages_allocated.data_ptr(), slot_arr, _ptr(slot_dev),
+        _ptr(slot_errors), _stream(dev)), "sparse_decode_append")
     return out
 
 

@@ -88,7 +88,7 @@ SIGNATURES = {
         _p, _i64, _i64, _p, _p, _i64, _p, _i64, _p,
         _p, _i64, _p, _i32,
         _i32, _i32, _i32, _i32, _i32, _i32,
-        _p, _i32, _p, _p, _sz, _p, _p, _i64, _p, _p, _p, _p]),
+        _p, _i32, _p, _p, _sz, _p, _p, _i64, _p, _p, _p, _p, _p]),
     "cvsa_dense_decode": (ctypes.c_int, [
         _p, _i64, _i64, _p, _p, _i64, _p, _i64, _p,
         _i32, _i32, _i32, _i32, _i32, _i32,
@@ -120,7 +120,8 @@ SIGNATURES = {
     "cvsa_step_workspace_bytes": (_sz, [ctypes.POINTER(StepDesc)]),
     "cvsa_step_plan_create": (ctypes.c_int, [ctypes.POINTER(StepDesc), ctypes.POINTER(_p)]),
     "cvsa_step_plan_run": (ctypes.c_int, [_p, _i32, _p, _p, _p]),
-    "cvsa_step_plan_run_append": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _p, _p, _p, _p]),
+    "cvsa_step_plan_run_append": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _p, _p, _p, _p,
+                                                  _p]),
     "cvsa_step_plan_destroy": (None, [_p]),
     "cvsa_step_plan_selection_changed": (ctypes.c_int, [_p]),
 }

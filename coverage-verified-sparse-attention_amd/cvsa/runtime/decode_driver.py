@@ -140,6 +140,9 @@ class DecodeDriver:
                                                       self.v_static))
         if self._fold_graphs:
             self._slots = {}  # chunk index -> [device slots, pinned slots, event]
+            # Sequences whose device slot a replayed launch refused (none
+            # while the slots follow the managers); checked by run().
+            self.slot_errors = torch.zeros(1, dtype=torch.int32, device=layers.device)
 
     # ------------------------------------------------------------ one step
     def _append(self, k, v, layers):
@@ -269,7 +272,8 @@ class DecodeDriver:
                     chunk_outs = [
                         p.run_reuse_append(self.q_static[l], self.k_static[l], self.v_static[l],
                                            managers[l]._pages_allocated_dev,
-                                           slots_dev=slots_dev[j])
+                                           slots_dev=slots_dev[j],
+                                           slot_errors=self.slot_errors)
                         for j, (p, l) in enumerate(zip(plans, chunk))]
                 graph.replay()
                 self._graphs[ci] = (graph, plans, chunk_outs)
@@ -359,6 +363,11 @@ class DecodeDriver:
             if i >= warmup:
                 times.append(start.elapsed_time(end))
                 host.append((t1 - t0) * 1e3)
+        if self._fold_graphs:
+            bad = int(self.slot_errors.item())
+            if bad:
+                raise RuntimeError(f"decode driver: {bad} device append slots were refused "
+                                   "(the slots no longer follow the managers)")
         ms = sorted(times)
         B = self.layers.batch
         return {

@@ -276,8 +276,12 @@ int cvsa_sparse_decode_noalloc(const uint16_t *q, int64_t q_stride_b,
  * -1.  Inconsistent slots return CVSA_ERR_INVALID before anything is
  * enqueued.  slots_dev: the same 2 * B int32 in device memory instead, for a
  * launch that a captured graph replays (the slots change every step, the
- * kernel arguments of a captured launch do not); they are not checked, and
- * only the one-launch shapes take them (CVSA_ERR_UNSUPPORTED otherwise).
+ * kernel arguments of a captured launch do not); only the one-launch shapes
+ * take them (CVSA_ERR_UNSUPPORTED otherwise).  The launch checks each device
+ * slot: a sequence whose slot is out of range (context length outside
+ * [0, 16 W), a new block outside [-1, num_blocks) or not at a page start)
+ * appends nothing, its output is undefined, and *slot_errors (an optional
+ * device int32, accumulated) is incremented once for it.
  * Exactly one of slots and slots_dev is given.  block_tables, context_lens
  * and pages_allocated are updated as cvsa_append_kv does; the other
  * arguments, outputs and errors are those of cvsa_sparse_decode (normalised
@@ -296,7 +300,8 @@ int cvsa_sparse_decode_append(const uint16_t *q, int64_t q_stride_b,
                               size_t workspace_bytes, const uint16_t *k_new,
                               const uint16_t *v_new, int64_t new_stride_b,
                               int32_t *pages_allocated, const int32_t *slots,
-                              const int32_t *slots_dev, void *stream);
+                              const int32_t *slots_dev, int32_t *slot_errors,
+                              void *stream);
 
 /*
  * Dense paged decode over every valid page.  Replaces
@@ -592,13 +597,13 @@ int cvsa_step_plan_run(cvsa_step_plan *plan, int32_t kind, const uint16_t *q, vo
 /* A reuse step (CVSA_STEP_REUSE) with the step's token append folded in:
  * cvsa_sparse_decode_append over the plan's buffers, whose k_cache,
  * v_cache, block_tables and context_lens it writes (see there for k_new,
- * v_new, new_stride_b, pages_allocated and slots).  No counterpart in the
+ * v_new, new_stride_b, pages_allocated, slots, slots_dev and slot_errors).  No counterpart in the
  * reference (its loops append, then call the backend). */
 int cvsa_step_plan_run_append(cvsa_step_plan *plan, const uint16_t *q, void *out,
                               const uint16_t *k_new, const uint16_t *v_new,
                               int64_t new_stride_b, int32_t *pages_allocated,
                               const int32_t *slots, const int32_t *slots_dev,
-                              void *stream);
+                              int32_t *slot_errors, void *stream);
 void cvsa_step_plan_destroy(cvsa_step_plan *plan);
 
 #ifdef __cplusplus

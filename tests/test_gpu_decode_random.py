@@ -239,12 +239,15 @@ def test_decode_append_device_slots(gpu, seed):
     H, G = inp.k_cache.shape[2], inp.q.shape[1] // inp.k_cache.shape[2]
     slots = _slots(ctx, alloc, inp.used_blocks, 16)
     runs = []
+    errors = torch.zeros(1, dtype=torch.int32, device=gpu)
     for sl in (slots, torch.tensor(slots, dtype=torch.int32, device=gpu).view(-1, 2)):
         st = [inp.k_cache.clone(), inp.v_cache.clone(), bt.clone(), inp.context_lens.clone(),
               alloc.clone()]
-        out = ops.sparse_decode_append(inp.q, *st[:4], pi, nph, kn, vn, st[4], sl, H, G, 16)
+        out = ops.sparse_decode_append(inp.q, *st[:4], pi, nph, kn, vn, st[4], sl, H, G, 16,
+                                       slot_errors=errors)
         runs.append([out] + st)
     torch.cuda.synchronize()
+    assert int(errors.item()) == 0
     for a, b in zip(*runs):
         assert torch.equal(a, b), seed
 
@@ -261,15 +264,18 @@ def test_decode_append_device_slots_out_of_range(gpu):
     want = ops.sparse_decode_append(inp.q, *good[:4], pi, nph, kn, vn, good[4], slots, H, G, 16)
     W, nb = bt.shape[1], inp.k_cache.shape[0]
     bad_forms = [(W * 16, -1), (-1, -1), (ctx[0] // 16 * 16, nb), (ctx[0] // 16 * 16 + 1, 0)]
-    for bad in bad_forms:
+    errors = torch.zeros(1, dtype=torch.int32, device=gpu)
+    for i, bad in enumerate(bad_forms):
         sl = list(slots)
         sl[0], sl[1] = bad
         st = [inp.k_cache.clone(), inp.v_cache.clone(), bt.clone(), inp.context_lens.clone(),
               alloc.clone()]
         out = ops.sparse_decode_append(inp.q, *st[:4], pi, nph, kn, vn, st[4],
                                        torch.tensor(sl, dtype=torch.int32,
-                                                    device=gpu).view(-1, 2), H, G, 16)
+                                                    device=gpu).view(-1, 2), H, G, 16,
+                                       slot_errors=errors)
         torch.cuda.synchronize()
+        assert int(errors.item()) == i + 1, bad   # the refused slot is reported
         assert torch.equal(st[3][0], inp.context_lens[0]), bad
         assert torch.equal(st[4][0], alloc[0]) and torch.equal(st[2][0], bt[0]), bad
         if B > 1:

@@ -118,3 +118,19 @@ def test_checked_append_buffers_are_rechecked_when_they_change():
     with pytest.raises(ValueError):
         p.run_reuse_append(q, slots=[0, -1] * B, **args)
     assert len(calls) == 1
+
+
+@pytest.mark.parametrize("errors", [torch.zeros(1, dtype=torch.int64), [0],
+                                    torch.zeros(0, dtype=torch.int32)])
+def test_run_reuse_append_refuses_bad_slot_errors(errors):
+    """The refused-slot counter of a device-slot append must be an int32
+    tensor on the plan's device."""
+    calls = []
+    p, q = _plan(calls)
+    with pytest.raises(ValueError):
+        p.run_reuse_append(q, slots_dev=torch.zeros(B, 2, dtype=torch.int32),
+                           slot_errors=errors, **_good())
+    assert not calls
+    out = p.run_reuse_append(q, slots_dev=torch.zeros(B, 2, dtype=torch.int32),
+                             slot_errors=torch.zeros(1, dtype=torch.int32), **_good())
+    assert out.shape == (B, H_KV * G, D) and len(calls) == 1 and calls[0][9] is not None
