@@ -340,6 +340,25 @@ def time_kernel(fn, samples):
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "listed_decode_cfg3_traffic.md")
 
 
+STEP_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "step_traffic_cfg3.md")
+
+
+def measured_step_bytes():
+    """HBM bytes actually read and written per step kind at cfg3 (exact
+    selector), from the committed FETCH_SIZE / WRITE_SIZE summary: {kind:
+    bytes} for reuse, check (kept) and rescore, or None if absent."""
+    out = {}
+    try:
+        with open(STEP_TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("bytes_read_"):
+                    k, v = line.split(":", 1)
+                    out[k[len("bytes_read_"):].strip()] = int(float(v.strip()))
+    except OSError:
+        return None
+    return out if {"reuse", "check", "rescore"} <= set(out) else None
+
+
 def measured_traffic():
     """HBM bytes per launch of the listed-page decode kernel at cfg3, from the
     committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None if absent)."""
@@ -408,8 +427,10 @@ def cpu_baseline(cfg, layer0, n_steps, tau):
     return times, torch.get_num_threads(), model, dense_s
 
 
-def run_schedule(cfg, layers, tau, args, dev):
-    """Classification pass, then the timed pass; returns the step results."""
+def run_schedule(cfg, layers, tau, args, dev, count_read=True):
+    """Classification pass, then the timed pass; returns the step results.
+    count_read: also count the bytes actually read per step kind (the
+    profiled cfg3 workload only)."""
     import torch
     from cvsa.backend import CVSABackend
     from cvsa.synthetic import jitter_query
@@ -492,6 +513,11 @@ def run_schedule(cfg, layers, tau, args, dev):
     step_us = [a.elapsed_time(b) * 1e3 / L for a, b in evs]       # per layer-step
     step_kinds = {}
     total_bytes = 0
+    read = measured_step_bytes() if (count_read and cfg.get("profile_name") == "cfg3"
+                                     and cfg["selector"] == "exact"
+                                     and cfg.get("approx") is None
+                                     and not cfg.get("dense_layers")) else None
+    read_bytes = 0 if read is not None else None
     accepted_heads = total_heads = 0
     for s, l, kind, acc in kinds:
         a = [True] * (B * H_kv) if acc is None else [bool(x) for x in acc.flatten().tolist()]
@@ -499,6 +525,8 @@ def run_schedule(cfg, layers, tau, args, dev):
             accepted_heads += sum(a)
             total_heads += len(a)
         total_bytes += step_bytes(kind, a, cfg, W, budget)
+        if read_bytes is not None:
+            read_bytes = read_bytes + read[kind] if kind in read else None
         if kind == "rescore" or s not in step_kinds or step_kinds[s] == "dense":
             step_kinds[s] = kind
     by_kind = {}
@@ -507,6 +535,9 @@ def run_schedule(cfg, layers, tau, args, dev):
     return dict(
         step_us=step_us, mean_us=statistics.mean(step_us), med_us=statistics.median(step_us),
         achieved=total_bytes / (sum(step_us) * L * 1e-6) / 1e9, by_kind=by_kind,
+        read_achieved=(None if read_bytes is None
+                       else read_bytes / (sum(step_us) * L * 1e-6) / 1e9),
+        read_bytes=read_bytes, algorithmic_bytes=total_bytes,
         stats=stats_pass2, same=stats_pass2 == stats_pass1, host=host, wall=wall,
         recovery=(1 - accepted_heads / total_heads) if total_heads else None, W=W,
         host_each=host_each,
@@ -524,7 +555,7 @@ def main():
     from cvsa.ops import _lib
 
     cfg = dict(CONFIGS[args.config], selector=args.selector,
-               light_normalizer=args.light_normalizer)
+               light_normalizer=args.light_normalizer, profile_name=args.config)
     if args.method is not None:
         cfg.update(parse_method(args.method))
         cfg["desc"] += f"; method {args.method}"
@@ -706,6 +737,14 @@ def main():
         "host_us_each": [round(x, 1) for x in res["host_each"]],
         "attention_layer_steps_per_s": round(1e6 / mean_us, 1),
         "roofline_frac_step": round(res["achieved"] * 1e9 / PEAK_HBM_BPS, 4),
+        # The same steps counted by the bytes actually read and written
+        # (rocprofv3 FETCH_SIZE + WRITE_SIZE per step kind, committed in
+        # profiles/step_traffic_cfg3.md; cfg3 only): value and
+        # roofline_frac_step count BASELINE's algorithmic bytes.
+        "bytes_read": res["read_bytes"],
+        "bytes_algorithmic": res["algorithmic_bytes"],
+        "roofline_frac_step_read": (None if res["read_achieved"] is None
+                                    else round(res["read_achieved"] * 1e9 / PEAK_HBM_BPS, 4)),
         "head_recovery_rate": res["recovery"],
         "schedule": {"rescore_rate_pct": res["stats"].get("rescore_rate"),
                      "per_head_accept_rate_pct": res["stats"].get("per_head_accept_rate"),
@@ -741,7 +780,7 @@ def main():
         del layers, prep
         torch.cuda.empty_cache()
         rlayers = build_layers(args.config, cfg, dev, L, 3.0, 2.0, args.warmup + args.steps)
-        r = run_schedule(cfg, rlayers, tau0, args, dev)
+        r = run_schedule(cfg, rlayers, tau0, args, dev, count_read=False)
         result["literal_recipe"] = {
             "hot_shift_sigma": 3.0, "sink_shift_sigma": 2.0, "value": round(r["achieved"], 2),
             "unit": "GB/s", "frac": round(r["achieved"] * 1e9 / PEAK_HBM_BPS, 4),
