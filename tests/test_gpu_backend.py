@@ -297,11 +297,7 @@ class _Lockstep:
                 f"{self.own_margin}")
 
 
-def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, expect_margin=0, layers=1):
-    """Run both backends for ``steps`` decode steps of ``layers`` layers (one
-    shared cache) in lockstep and compare them.  ``expect_margin`` is the
-    number of margin heads (of every kind) the seed gives; the BASELINE bar
-    is zero."""
+def _make_runtime(dev, cfg, seed, steps, extra, gen_on_gpu):
     if gen_on_gpu:
         # Long contexts: draw the inputs on the GPU, then give the oracle host copies.
         inp = make_paged_inputs(**cfg, seed=seed, max_pages=None, spare_blocks=extra,
@@ -310,8 +306,7 @@ def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, expect_margin=0,
             setattr(inp, name, getattr(inp, name).cpu())
     else:
         inp = make_paged_inputs(**cfg, seed=seed, max_pages=None, spare_blocks=extra)
-    B, H_q, D = inp.q.shape
-    H = inp.num_kv_heads
+    B = inp.q.shape[0]
     bs = inp.k_cache.shape[1]
     W = inp.block_tables.shape[1]
     # leave room in the block table for the appended tokens
@@ -319,13 +314,30 @@ def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, expect_margin=0,
     bt = torch.zeros(B, W2, dtype=torch.int32)
     bt[:, :W] = inp.block_tables
     inp.block_tables = bt
-    rt = _Runtime(inp, dev, extra)
+    return inp, _Runtime(inp, dev, extra)
+
+
+def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, expect_margin=0, layers=1,
+         own_caches=False):
+    """Run both backends for ``steps`` decode steps of ``layers`` layers in
+    lockstep and compare them.  The layers share one cache, or with
+    ``own_caches`` each has its own (independent inputs and hot pages per
+    layer, as a model's layers).  ``expect_margin`` is the number of margin
+    heads (of every kind) the seed gives; the BASELINE bar is zero."""
+    runs = [_make_runtime(dev, cfg, seed + 17 * l, steps, extra, gen_on_gpu)
+            for l in range(layers if own_caches else 1)]
+    inp, rt = runs[0]
+    B, H_q, D = inp.q.shape
+    H = inp.num_kv_heads
+    bs = inp.k_cache.shape[1]
     gpu_b = CVSABackend(num_kv_heads=H, num_q_heads=H_q, head_dim=D, block_size=bs, **kw)
     ora_b = OracleCVSABackend(num_kv_heads=H, num_q_heads=H_q, head_dim=D, block_size=bs, **kw)
     lock = _Lockstep(gpu_b, ora_b, kw, rt.ctx)
     g = torch.Generator().manual_seed(seed + 1)
     for step in range(steps):
         for layer in range(layers):
+            inp, rt = runs[layer if own_caches else 0]
+            lock.ctx = rt.ctx
             q = jitter_query(inp.q, 0.3, seed + 100 + step * layers + layer)
             lock.before_gpu(layer)
             out = gpu_b(q.to(dev), rt.cache.k_cache, rt.cache.v_cache, rt.mgr.block_tables,
@@ -356,9 +368,10 @@ def _run(dev, cfg, kw, steps, seed, extra=32, gen_on_gpu=False, expect_margin=0,
                             step, layer, b, h)
             gpu_b.step_done(layer, layers)
             ora_b.step_done(layer, layers)
-        kn = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
-        vn = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
-        rt.append(kn, vn, dev)
+        for inp_l, rt_l in runs:
+            kn = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+            vn = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+            rt_l.append(kn, vn, dev)
     sg, so = gpu_b.get_stats(), ora_b.get_stats()
     assert sg == so, (sg, so)
     total = lock.margin_sel + lock.margin_gate + lock.own_margin
@@ -647,3 +660,30 @@ def test_random_reject_never(gpu):
         never.step_done(0, 1)
         base.step_done(0, 1)
     assert never.get_stats() == base.get_stats()
+
+
+def test_cfg2_baseline_schedule_20_steps(gpu):
+    """cfg2 as BASELINE states it: B=32, 8B shapes, 8192-token contexts, 20
+    consecutive decode steps each appending one token per sequence, lazy
+    M=5, budget 1/4, tau 0.9 -- the whole schedule (4 checks, 16 reuse
+    steps) in lockstep with the oracle backend."""
+    cfg, budget, seed, kw = FULL_SIZE["cfg2"]
+    # 20 appended tokens from a page boundary: two new pages per sequence.
+    stats, trace, lock = _run(gpu, cfg, dict(kw, budget_pct=budget), steps=20, seed=seed,
+                              gen_on_gpu=True, extra=cfg["batch"] * 3)
+    kinds = [t["kind"] for t in trace]
+    assert kinds.count("reuse") == 16 and stats["total_decode_steps"] == 20, kinds
+    print(f"cfg2 x 20 steps: {kinds}: {lock.summary()}")
+
+
+def test_cfg5_layers_with_own_caches(gpu):
+    """cfg5's shapes (Llama-3.1-70B attention 64q/8kv/d128, B=4, 65536-token
+    contexts) over four layers, each with its own cache and hot-page
+    clusters (as BASELINE's per-layer independent caches), ten decode steps
+    with appends, lazy M=5, in lockstep with the oracle backend."""
+    cfg, budget, seed, kw = FULL_SIZE["cfg5"]
+    stats, trace, lock = _run(gpu, cfg, dict(kw, budget_pct=budget), steps=10, seed=seed,
+                              gen_on_gpu=True, layers=4, own_caches=True)
+    kinds = [t["kind"] for t in trace]
+    assert kinds.count("reuse") == 32, kinds
+    print(f"cfg5 x 4 layers x 10 steps: {lock.summary()}")
