@@ -251,6 +251,17 @@ __device__ __forceinline__ int approx_booked_pages(const DecodeArgs &a, int bh, 
 // pages.  T < 2^31 and n_wg <= kMaxSplits, so every quantity is computed in
 // 32 bits (64-bit division is a long instruction sequence on the GPU).
 constexpr int kMaxHeads = 4096;  // B * H_kv of one launch
+// Two-level merge of a stream-K head with more than kTwoLevelMin partials:
+// groups of kMergeGroup consecutive contributors, each merged by its last
+// arriver into the group's first partial row, then the groups by the last
+// group merger.  Group counters follow the kMaxHeads head counters: word
+// 2 w0 + (group > 0) for a group whose first contributor is workgroup w0 (a
+// workgroup starts at most one head's first group and one head's later
+// group, since a head with more than kTwoLevelMin partials covers every
+// workgroup between its first and last entirely).
+constexpr int kMergeGroup = 16;
+constexpr int kTwoLevelMin = 48;
+constexpr int kGroupCounters = 2 * 256;  // 2 x the largest stream-K grid
 constexpr int kMinPagesPerWg = kMinPagesPerWave * 4;
 
 struct Partition {
@@ -358,7 +369,10 @@ struct MergeLds {
 constexpr int kMergeBatchListed = 16;
 constexpr int kMergeBatchStreamK = 8;
 
-// Merge of a head's n_act split partials by the last of its workgroups.
+// Merge of a head's n_act split partials by the last of its workgroups
+// (partial sp at row offset head_off + sp * row_step rows).  TO_PART: the
+// merged (o, m, l) of the rows go to the partial row at part_off instead of
+// the outputs (the first level of a two-level merge; no counters booked).
 // Thread t owns float4 chunk c = t % NC of the head's G x D outputs and the
 // splits j, j + J, ... (j = t / NC); their o chunks are loaded KB at a time,
 // the first KB together with the (m, l) pairs.  When the
@@ -366,12 +380,14 @@ constexpr int kMergeBatchStreamK = 8;
 // thread takes chunks t, t + NT, ... in turn, every split of each.  The
 // (m, l) pairs go to LDS first; one wave per q-head turns them into the
 // weights exp(m_sp - M) and the totals (M, L).
-template <int G, int D, int NT, int KB>
+template <int G, int D, int NT, int KB, bool TO_PART = false>
 __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBuf &pb,
                                                uint32_t head_off, int n_act, int bh, int n,
-                                               int nv, MergeLds<G, NT> &s) {
+                                               int nv, MergeLds<G, NT> &s, int row_step = 1,
+                                               uint32_t part_off = 0) {
   constexpr int kChunksPerRow = D / 4;
   constexpr int kPartStride = part_stride(D);
+  const uint32_t row_elems = (uint32_t)row_step * (uint32_t)(G * kPartStride);
   constexpr int NC = G * kChunksPerRow;
   constexpr int J = NT / NC > 0 ? NT / NC : 1;
   constexpr int NPASS = (NC + NT - 1) / NT;
@@ -382,13 +398,14 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBu
   const int j = NPASS == 1 ? t / NC : 0;
   const bool active = t < NC * J;
 
-  for (int e = t; e < n_act * G; e += NT) s.ml[e] = pb.load2(head_off + e * kPartStride + D);
+  for (int e = t; e < n_act * G; e += NT)
+    s.ml[e] = pb.load2(head_off + (uint32_t)(e / G) * row_elems + (e % G) * kPartStride + D);
   const int per_lane = active ? (n_act - j + J - 1) / J : 0;  // splits of this thread
   auto load_batch = [&](int g, int d0, int b0, f32x4 (&v)[KB]) {
 #pragma unroll
     for (int k = 0; k < KB; ++k) {
       const int sp = min(j + (b0 + k) * J, n_act - 1);
-      v[k] = pb.load4(head_off + (sp * G + g) * kPartStride + d0);
+      v[k] = pb.load4(head_off + (uint32_t)sp * row_elems + g * kPartStride + d0);
     }
   };
   f32x4 cur[KB];
@@ -445,10 +462,16 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs &a, const PartBu
         for (int jj = 1; jj < J; ++jj) O += s.acc[t + jj * NC];
       }
     }
-    if (live && j == 0)
-      write_outputs4<D>(a, (int64_t)bh * a.q_group + a.q_off + g, d0, O, s.M[g], s.L[g]);
+    if (live && j == 0) {
+      if constexpr (TO_PART) {
+        pb.store4(part_off + g * kPartStride + d0, O);
+        if (d0 == 0) pb.store2(part_off + g * kPartStride + D, f32x2{s.M[g], s.L[g]});
+      } else {
+        write_outputs4<D>(a, (int64_t)bh * a.q_group + a.q_off + g, d0, O, s.M[g], s.L[g]);
+      }
+    }
   }
-  if (t == 0 && a.work != nullptr) add_work(a, n, nv);
+  if (!TO_PART && t == 0 && a.work != nullptr) add_work(a, n, nv);
 }
 
 // ---------------------------------------------------------------- engines
@@ -688,7 +711,15 @@ __device__ __forceinline__ L &s_eng_of(L (&eng)[NW], int wave) { return eng[wave
 // contributor (n_act == 1) it writes the outputs.  Otherwise it stores its
 // partial (o, m, l) in partial row my_row, bumps the head's counter, and the
 // last of the n_act contributors merges rows first_row .. first_row+n_act-1.
-template <int G, int D, int NW, int KB>
+// TWO (stream-K): a head with more than kTwoLevelMin contributors (rows
+// consecutive, contributor i = my_row - first_row) merges in two levels:
+// the last arriver of each group of kMergeGroup contributors merges the
+// group into the group's first row (after loading every row of the group)
+// and bumps the head's counter; the last of the groups merges the group
+// rows and writes the outputs.  One workgroup merging ~140 partials takes
+// ~9 dependent batches of loads; two levels take one batch each and one more
+// store-wait-counter.
+template <int G, int D, int NW, int KB, bool TWO = false>
 __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const PartBuf &pb, int h,
                                                  int n, int nv, int n_act, uint32_t my_row,
                                                  uint32_t first_row,
@@ -743,6 +774,43 @@ __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const Part
   // Every wave's partial stores have completed before the counter moves.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  constexpr uint32_t kRowElems = (uint32_t)(G * kPartStride);
+  if (TWO && n_act > kTwoLevelMin) {  // uniform
+    const int i = (int)(my_row - first_row);
+    const int gi = i / kMergeGroup;
+    const int g0 = gi * kMergeGroup;
+    const int gsize = min(kMergeGroup, n_act - g0);
+    const int ng = (n_act + kMergeGroup - 1) / kMergeGroup;
+    const uint32_t w0 = first_row - (uint32_t)h + (uint32_t)g0;  // the group's first workgroup
+    unsigned *gc = a.counters + kMaxHeads + 2 * w0 + (gi != 0 ? 1 : 0);
+    if (threadIdx.x == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      s_last = prev == (unsigned)(gsize - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;  // uniform
+    if (threadIdx.x == 0)
+      __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t grow = (first_row + (uint32_t)g0) * kRowElems;
+    merge_partials<G, D, NT, KB, true>(a, pb, grow, gsize, h, 0, 0, s_merge, 1, grow);
+    // The group row's stores have completed before the head's counter moves.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(&a.counters[h], 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      s_last = prev == (unsigned)(ng - 1);
+    }
+    __syncthreads();
+    if (s_last) {
+      if (threadIdx.x == 0)
+        __hip_atomic_store(&a.counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      merge_partials<G, D, NT, KB>(a, pb, first_row * kRowElems, ng, h, n, nv, s_merge,
+                                   kMergeGroup);
+    }
+    return;
+  }
   if (threadIdx.x == 0) {
     const unsigned prev = __hip_atomic_fetch_add(&a.counters[h], 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
@@ -753,8 +821,7 @@ __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const Part
     // Last contributor of the head: merge its partials, write the outputs.
     if (threadIdx.x == 0)
       __hip_atomic_store(&a.counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_partials<G, D, NT, KB>(a, pb, first_row * (uint32_t)(G * kPartStride), n_act, h, n,
-                             nv, s_merge);
+    merge_partials<G, D, NT, KB>(a, pb, first_row * kRowElems, n_act, h, n, nv, s_merge);
   }
 }
 
@@ -1342,7 +1409,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     const int first = part.owner(P);
     const int nv = valid_pages_ts(ctx, ts);
     const int booked = MODE == kModeApprox ? approx_booked_pages(a, h, nv) : n >> ts;
-    segment_epilogue<G, D, NW, kMergeBatchStreamK>(a, pb, h, booked, nv,
+    segment_epilogue<G, D, NW, kMergeBatchStreamK, true>(a, pb, h, booked, nv,
                                part.owner(P + n - 1) - first + 1, (uint32_t)(w + h),
                                (uint32_t)(first + h), s_o, s_m, s_l, s_last, s_tail.merge);
     __syncthreads();  // LDS is reused by the next segment

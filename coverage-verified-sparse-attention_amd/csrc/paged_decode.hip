@@ -93,14 +93,16 @@ static DecodeLaunch plan_launch(int B, int H_kv, int max_sel, int W, bool listed
   return p;
 }
 
-// Workspace: a fixed area of kMaxHeads completion counters (uint32), then
-// the partial rows.  The counter area has the same size and place for every
+// Workspace: a fixed area of kMaxHeads completion counters and
+// kGroupCounters group counters of the two-level merge (uint32), then the
+// partial rows.  The counter area has the same size and place for every
 // launch, so launches of different B * H_kv that share a workspace never
 // read one another's partial rows as counters: counter h of every launch is
 // word h, and every launch leaves the words it used at zero.  Launches with
 // split partials have at most kMaxHeads heads (stream-K: checked at launch;
 // listed: more than one split per head only below kMaxSplits heads).
-constexpr size_t kCounterAreaBytes = (size_t)kMaxHeads * sizeof(unsigned);
+constexpr size_t kCounterAreaBytes = (size_t)(kMaxHeads + kGroupCounters) * sizeof(unsigned);
+static_assert(kTargetWorkgroups * 2 <= kGroupCounters, "a group counter per group start");
 static_assert(kCounterAreaBytes % 256 == 0, "partial rows start 256-byte aligned");
 
 static size_t workspace_bytes_for(int B, int H_q, int H_kv, int D, int max_sel, int W,

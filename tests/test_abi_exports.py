@@ -58,8 +58,9 @@ def test_errors_are_reported_without_gpu_work():
 
 
 def test_decode_workspace_layout_is_fixed():
-    """Every decode workspace starts with the same 16 KiB counter area
-    (4096 heads x 4 bytes) followed by whole partial rows of G x (D + 4)
+    """Every decode workspace starts with the same 18 KiB counter area
+    (4096 head counters and 512 group counters of the two-level merge, 4
+    bytes each) followed by whole partial rows of G x (D + 4)
     fp32, so launches of any B * H_kv can share one workspace: the counters
     of one launch never overlap the partial rows of another.  Head dimensions
     outside {64, 128, 256} have no workspace (0)."""
@@ -75,7 +76,7 @@ def test_decode_workspace_layout_is_fixed():
                     if n == 0:
                         continue
                     seen += 1
-                    assert n > 16384 and (n - 16384) % (G * (D + 4) * 4) == 0, (B, H_kv, G, n)
+                    assert n > 18432 and (n - 18432) % (G * (D + 4) * 4) == 0, (B, H_kv, G, n)
     assert seen > 60
     assert lib.cvsa_decode_workspace_bytes(1, 32, 8, 96, 64, 8192, 1) == 0
 
