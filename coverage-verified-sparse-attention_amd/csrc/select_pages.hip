@@ -161,6 +161,40 @@ __device__ __forceinline__ void block_max2(float &a, float &b, float (*red)[2]) 
   }
 }
 
+// Sums of a and b and the max of c over the block in one barrier; `red`
+// holds 3 x kSelWaves floats and is not reused by another reduction.
+__device__ __forceinline__ void block_sum2_max1(float &a, float &b, float &c, float (*red)[3]) {
+  a = wave_sum_from_groups<1>(a);
+  b = wave_sum_from_groups<1>(b);
+  c = wave_max_from_groups<1>(c);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    red[wave][0] = a;
+    red[wave][1] = b;
+    red[wave][2] = c;
+  }
+  lds_barrier();
+  a = red[0][0];
+  b = red[0][1];
+  c = red[0][2];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) {
+    a += red[w][0];
+    b += red[w][1];
+    c = fmaxf(c, red[w][2]);
+  }
+}
+
+__device__ __forceinline__ void block_sum1(float &a, float *red) {
+  a = wave_sum_from_groups<1>(a);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = a;
+  lds_barrier();
+  a = red[0];
+#pragma unroll
+  for (int w = 1; w < kSelWaves; ++w) a += red[w];
+}
+
 __device__ __forceinline__ void block_sum2(float &a, float &b, float (*red)[2]) {
   a = wave_sum_from_groups<1>(a);
   b = wave_sum_from_groups<1>(b);
@@ -273,7 +307,8 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   __shared__ uint32_t s_cand[kRankCands];
   __shared__ uint32_t wsum[kSelWaves];
   __shared__ uint32_t red_rng[kSelWaves][3];
-  __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2];
+  __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2], red_s3[kSelWaves][3];
+  __shared__ float red_s1[kSelWaves];
   __shared__ uint32_t s_digit, s_krem, s_T, s_bucket, s_kb, s_nb, s_ncand;
   __shared__ int s_nok, s_nbad, s_acc;
   // Top-p only: softmax mass per value bucket (64-bit fixed point, so the
@@ -776,26 +811,53 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
 
   if (accept_out == nullptr) return;
   // ---- coverage of the new selection
+  // When the selection ranks the gate's scores and the row holds no +inf /
+  // NaN, the maximum over every page is the row's largest finite score
+  // (found with the value range above), and so, in all but odd cases (a
+  // finite score past the valid pages), is the maximum over the counted
+  // pages: that guess saves a block-wide max; the counted maximum is reduced
+  // with the sums, and a wrong guess recomputes the selection's sum.
+  const bool fast_max = !SEP && n_odd == 0;  // uniform
   float mx = -INFINITY, ms = -INFINITY;
+  if (fast_max) {
+    mx = n_fin > 0 ? key_value(kmax) : -INFINITY;
+    ms = mx;
+  } else {
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    mx = fmaxf(mx, gate(r));
-    if (counted[r]) ms = fmaxf(ms, gate(r));
+    for (int r = 0; r < R; ++r) {
+      mx = fmaxf(mx, gate(r));
+      if (counted[r]) ms = fmaxf(ms, gate(r));
+    }
+    block_max2(mx, ms, red_max);
   }
-  block_max2(mx, ms, red_max);
   const float m_all = fmaxf(mx, -1e20f);
   // Padding lanes of the reference's power-of-two selection block carry
   // -1e20 into the max whenever n_sel is below that block (coverage.py:205).
   int msel_block = 1;
   while (msel_block < width) msel_block <<= 1;
-  const float m_sel = n_sel < msel_block ? fmaxf(ms, -1e20f) : ms;
-  float se = 0.f, ss = 0.f;
+  float m_sel = n_sel < msel_block ? fmaxf(ms, -1e20f) : ms;
+  float se = 0.f, ss = 0.f, ms_true = -INFINITY;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     se += fast_exp(gate(r) - m_all);
-    if (counted[r]) ss += fast_exp(gate(r) - m_sel);
+    if (counted[r]) {
+      ss += fast_exp(gate(r) - m_sel);
+      ms_true = fmaxf(ms_true, gate(r));
+    }
   }
-  block_sum2(se, ss, red_sum);
+  if (fast_max) {
+    block_sum2_max1(se, ss, ms_true, red_s3);
+    if (ms_true != ms) {  // uniform; the counted pages miss the row's maximum
+      m_sel = n_sel < msel_block ? fmaxf(ms_true, -1e20f) : ms_true;
+      ss = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (counted[r]) ss += fast_exp(gate(r) - m_sel);
+      block_sum1(ss, red_s1);
+    }
+  } else {
+    block_sum2(se, ss, red_sum);
+  }
   if (t == 0) {
     const float cov = expf(lse_from(m_sel, ss) - lse_from(m_all, se));
     const int acc = cov >= tau ? 1 : 0;
