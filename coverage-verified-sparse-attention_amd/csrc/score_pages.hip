@@ -94,6 +94,91 @@ __global__ __launch_bounds__(256) void score_pages_kernel(
   }
 }
 
+// H_kv a multiple of R known only at run time (e.g. 12, 24, 32, 40 KV heads
+// at D = 128): the head-group layout with the head count as an argument.
+template <int D, int PPW>
+__global__ __launch_bounds__(256) void score_pages_group_any_kernel(const ScoreArgs s, int hkv) {
+  score_group_wave<D, PPW>(s, hkv, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+                           blockIdx.y);
+}
+
+// Any other H_kv (neither a multiple of R nor a divisor of it, e.g. 3, 5, 6
+// at D = 128): a wave scores one KV head, wave gw of sequence b head
+// gw % H_kv over pages [(gw / H_kv) * PPW, +PPW).  Lane l holds key row
+// l / LPR of each group of RPL = 64 / LPR rows of a 16-token tile and
+// d-segment (l % LPR) * 8 (LPR = D / 8), so a tile is NL = 16 / RPL loads of
+// RPL rows of 2D bytes (H_kv * 2D bytes apart).  A row's dot product is
+// finished by the LPR lanes that hold it with score_group_wave's DPP tree
+// (same bits); each lane keeps the maximum of its rows over the page's
+// tiles, and the RPL row groups are combined when the page ends.  The next
+// tile's keys are requested before the current one is reduced.
+template <int D, int PPW>
+__global__ __launch_bounds__(256) void score_pages_head_kernel(const ScoreArgs s, int hkv) {
+  constexpr int LPR = D / 8;
+  constexpr int RPL = kWave / LPR;
+  constexpr int NL = kPageTokens / RPL;
+  static_assert(PPW <= kWave, "a lane per page for the block ids");
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = blockIdx.y;
+  const int h = gw % hkv;
+  const int p_begin = (gw / hkv) * PPW;
+  if (p_begin >= s.W) return;
+  const int row = lane / LPR, seg = lane % LPR;
+  const int ctx = __builtin_amdgcn_readfirstlane(s.context_lens[b]);
+  const int n = min(PPW, s.W - p_begin);
+  // Page j of this wave: block id in lane j (-1 when the page holds no valid
+  // token or its id is outside the pool).
+  int my_phys = -1;
+  if (lane < n) {
+    const int p = p_begin + lane;
+    if (p * s.bs < ctx) {
+      const int id = s.block_tables[b * s.bt_sb + p];
+      if (id >= 0 && id < s.num_blocks) my_phys = id;
+    }
+  }
+  const uint4 qr = group_mean_q(s.q, s.q_sb, s.q_sh, b, h, s.G, seg, s.inv_g);
+  const int64_t row_stride = (int64_t)hkv * D;
+  const int64_t tile_elems = kPageTokens * row_stride;
+  const int64_t lane_off = row * row_stride + (int64_t)h * D + seg * 8;
+  const int tm = (1 << s.ts) - 1;
+  const int nt = n << s.ts;  // tiles of this wave
+  // Unconditional loads (block 0 for pages without valid tokens) keep the
+  // prefetch free of branches.
+  auto fetch = [&](int t, uint4 (&kv)[NL]) {
+    const int phys = max(__builtin_amdgcn_readlane(my_phys, t >> s.ts), 0);
+    const uint16_t *src = s.k_cache + (((int64_t)phys << s.ts) | (t & tm)) * tile_elems + lane_off;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) kv[i] = stream_load16(src + (int64_t)i * RPL * row_stride);
+  };
+  float pm = -INFINITY;  // this lane's rows, over the tiles of the current page
+  auto consume = [&](int t, const uint4 (&kv)[NL]) {
+    const int j = t >> s.ts, sub = t & tm;
+    const int p = p_begin + j;
+    const int tn = __builtin_amdgcn_readlane(my_phys, j) < 0
+                       ? 0
+                       : min(kPageTokens, ctx - p * s.bs - sub * kPageTokens);
+    float mx = sub == 0 ? -INFINITY : pm;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const float sc = group_sum<LPR>(dot8_bf16(kv[i], qr, 0.f)) * s.scale;
+      if (row + RPL * i < tn) mx = fmaxf(mx, sc);
+    }
+    pm = mx;
+    if (sub == tm) {
+      mx = wave_max_from_groups<LPR>(mx);
+      // A zero score is written as +0, as by the other layouts.
+      if (lane == 0) s.scores[((int64_t)b * hkv + h) * s.W + p] = mx + 0.f;
+    }
+  };
+  uint4 buf[2][NL];
+  fetch(0, buf[0]);
+  for (int t = 0; t < nt; ++t) {
+    if (t + 1 < nt) fetch(t + 1, buf[(t + 1) & 1]);
+    consume(t, buf[t & 1]);
+  }
+}
+
 }  // namespace cvsa
 
 using namespace cvsa;
@@ -120,8 +205,6 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
                D, block_size);
   CVSA_REQUIRE(num_blocks <= (INT32_MAX >> ts), CVSA_ERR_UNSUPPORTED,
                "score_pages: %lld blocks exceed the tile index range", (long long)num_blocks);
-  CVSA_REQUIRE(H_kv == 1 || H_kv == 2 || H_kv == 4 || H_kv == 8 || H_kv == 16,
-               CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d not in {1,2,4,8,16}", H_kv);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
                "score_pages: W=%d exceeds %d pages", W, kMaxPages);
   CVSA_REQUIRE(bt_stride_b >= W, CVSA_ERR_INVALID,
@@ -163,8 +246,41 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
     CVSA_GROUP_PPW(64, 8) CVSA_GROUP_PPW(64, 16)
     CVSA_GROUP_PPW(128, 4) CVSA_GROUP_PPW(128, 8) CVSA_GROUP_PPW(128, 16)
     CVSA_GROUP_PPW(256, 2) CVSA_GROUP_PPW(256, 4) CVSA_GROUP_PPW(256, 8) CVSA_GROUP_PPW(256, 16)
+#undef CVSA_GROUP_CASE
+#define CVSA_GROUP_CASE(DD, HK, PP)                                                      \
+  if (D == DD && ppw == PP) {                                                            \
+    hipLaunchKernelGGL((score_pages_group_any_kernel<DD, PP>), grid, dim3(256), 0, st, sa, \
+                       H_kv);                                                            \
+    return cvsa_host::check_launch("score_pages");                                       \
+  }
+    CVSA_GROUP_PPW(64, 0) CVSA_GROUP_PPW(128, 0) CVSA_GROUP_PPW(256, 0)
 #undef CVSA_GROUP_PPW
 #undef CVSA_GROUP_CASE
+    return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d, D=%d has no launch",
+                           H_kv, D);
+  }
+  if (R % H_kv != 0) {
+    // One KV head per wave: as many pages per wave (up to 16) as keep
+    // >= ~2048 waves in the launch.
+    const int64_t head_pages = (int64_t)B * W * H_kv;
+    int ppw = 1;
+    while (ppw < 16 && head_pages / (2 * ppw) >= 2048) ppw *= 2;
+    const int64_t waves = ((W + ppw - 1) / ppw) * (int64_t)H_kv;
+    dim3 grid((unsigned)((waves + 3) / 4), B);
+    const ScoreArgs sa{q, q_stride_b, q_stride_h, k_cache, (int64_t)num_blocks, block_tables,
+                       bt_stride_b, context_lens, page_scores, W, G, inv_g, scale,
+                       block_size, ts};
+#define CVSA_HEAD_CASE(DD, PP)                                                             \
+  if (D == DD && ppw == PP) {                                                              \
+    hipLaunchKernelGGL((score_pages_head_kernel<DD, PP>), grid, dim3(256), 0, st, sa, H_kv); \
+    return cvsa_host::check_launch("score_pages");                                         \
+  }
+#define CVSA_HEAD_PPW(DD) \
+  CVSA_HEAD_CASE(DD, 1) CVSA_HEAD_CASE(DD, 2) CVSA_HEAD_CASE(DD, 4) CVSA_HEAD_CASE(DD, 8) \
+  CVSA_HEAD_CASE(DD, 16)
+    CVSA_HEAD_PPW(64) CVSA_HEAD_PPW(128) CVSA_HEAD_PPW(256)
+#undef CVSA_HEAD_PPW
+#undef CVSA_HEAD_CASE
     return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d, D=%d has no launch",
                            H_kv, D);
   }

@@ -51,8 +51,6 @@ int check_desc(const cvsa_step_desc &d) {
   const int G = d.H_q / d.H_kv;
   STEP_REQUIRE(G <= 128, CVSA_ERR_UNSUPPORTED, "step_plan: GQA group size %d not in 1..128",
                G);
-  STEP_REQUIRE(d.H_kv == 1 || d.H_kv == 2 || d.H_kv == 4 || d.H_kv == 8 || d.H_kv == 16,
-               CVSA_ERR_UNSUPPORTED, "step_plan: H_kv=%d not in {1,2,4,8,16}", d.H_kv);
   STEP_REQUIRE((int64_t)d.B * d.H_kv <= kMaxDecodeHeads, CVSA_ERR_UNSUPPORTED,
                "step_plan: B * H_kv = %lld exceeds %lld heads", (long long)d.B * d.H_kv,
                (long long)kMaxDecodeHeads);

@@ -18,8 +18,8 @@
  *  - Supported geometry: D in {64, 128, 256}, block_size in {16, 32, 64},
  *    G = H_q / H_kv in 1..128 (decode launches serve 16 query heads per KV
  *    head; larger groups are enqueued as one launch per 16),
- *    H_kv in {1, 2, 4, 8, 16} (page scoring), W <= 32768 pages, and
- *    B * H_kv <= 4096 for dense and verified decode.  Anything else returns
+ *    any H_kv (B * H_kv <= 65535), W <= 32768 pages, and B * H_kv <= 4096
+ *    for dense and verified decode.  Anything else returns
  *    CVSA_ERR_UNSUPPORTED.
  *  - Entry points are re-entrant.  Calls that share a decode workspace must
  *    be ordered on one stream.

@@ -119,8 +119,12 @@ def test_step_plan_validates_on_the_host():
     ok = _step_desc(sel_map=1 << 26, sel_map_stride=512)
     assert lib.cvsa_step_plan_create(ctypes.byref(ok), ctypes.byref(h)) == _lib.CVSA_OK
     lib.cvsa_step_plan_destroy(h)
+    # any KV-head count is accepted (here one that is neither 1, 2, 4, 8 nor 16)
+    ok = _step_desc(H_kv=3, H_q=12)
+    assert lib.cvsa_step_plan_create(ctypes.byref(ok), ctypes.byref(h)) == _lib.CVSA_OK
+    lib.cvsa_step_plan_destroy(h)
     cases = [(dict(budget=513), _lib.CVSA_ERR_INVALID, b"budget"),
-             (dict(H_kv=3, H_q=12), _lib.CVSA_ERR_UNSUPPORTED, b"H_kv"),
+             (dict(H_kv=3, H_q=10), _lib.CVSA_ERR_INVALID, b"head counts"),
              (dict(D=96), _lib.CVSA_ERR_UNSUPPORTED, b"D=96"),
              (dict(block_size=8), _lib.CVSA_ERR_UNSUPPORTED, b"block_size=8"),
              (dict(bt_stride_b=100), _lib.CVSA_ERR_INVALID, b"stride"),

@@ -115,3 +115,56 @@ def test_random_schedules_wide_groups(gpu, G, H, bs):
                hot_heads=list(range(0, H, 2)))
     stats, trace, lock = _run(gpu, cfg, kw, steps=10, seed=800 + G)
     print(f"G {G} H {H} bs {bs} {cfg} {kw}: {lock.summary()}")
+
+
+# KV-head counts outside the compiled-in set: a multiple of the rows of one
+# wave load (64 / (D/8)) takes the head-group layout with the count as an
+# argument, any other count the one-head-per-wave layout.
+ANY_HKV = [  # (B, H_q, H_kv, ctx)
+    (1, 96, 32, 3000),          # MHA-sized head count (G = 3)
+    (2, 32, 32, [517, 2049]),   # G = 1, H_kv = 32
+    (1, 36, 12, 1500),          # a multiple of 4 not compiled in
+    (2, 18, 6, [800, 33]),      # neither a multiple nor a divisor of 4
+    (1, 15, 3, 4096 + 5),
+    (3, 35, 5, [17, 640, 2000]),
+    (1, 7, 7, 999),
+]
+
+
+@pytest.mark.parametrize("D,bs", GEOMETRIES + [(128, 16)])
+@pytest.mark.parametrize("geom", ANY_HKV)
+def test_score_pages_any_kv_heads(gpu, geom, D, bs):
+    B, H_q, H_kv, ctx = geom
+    inp = make_paged_inputs(B, H_q, H_kv, D, ctx, block_size=bs, seed=300 + H_kv, device=gpu,
+                            hot_heads=[0, H_kv - 1], n_hot=4, hot_shift=4.0)
+    got = ops.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens, H_kv,
+                          H_q // H_kv, bs).cpu()
+    want = ref.score_pages(inp.q.cpu(), inp.k_cache.cpu(), inp.block_tables.cpu(),
+                           inp.context_lens.cpu(), H_kv, H_q // H_kv, bs)
+    _close(got, want, SCORE_RTOL)
+
+
+@pytest.mark.parametrize("D,bs,H_kv,ctx", [(128, 16, 32, 65536), (128, 16, 6, 131072 - 3),
+                                           (64, 32, 5, 65536), (256, 16, 3, 40000)])
+def test_score_pages_any_kv_heads_long_context(gpu, D, bs, H_kv, ctx):
+    """Several pages per wave in the layouts for any head count."""
+    inp = make_paged_inputs(1, 2 * H_kv, H_kv, D, ctx, block_size=bs, seed=310 + H_kv,
+                            device=gpu)
+    got = ops.score_pages(inp.q, inp.k_cache, inp.block_tables, inp.context_lens, H_kv, 2,
+                          bs).cpu()
+    want = ref.score_pages(inp.q.cpu(), inp.k_cache.cpu(), inp.block_tables.cpu(),
+                           inp.context_lens.cpu(), H_kv, 2, bs)
+    _close(got, want, SCORE_RTOL)
+
+
+@pytest.mark.parametrize("G,H,bs", [(1, 32, 16), (4, 6, 16), (2, 12, 32), (7, 3, 16),
+                                    (1, 5, 64)])
+def test_random_schedules_any_kv_heads(gpu, G, H, bs):
+    """Backend schedules (step plans and the per-kernel path) at KV-head
+    counts outside {1, 2, 4, 8, 16}, ten steps with appends, in lockstep
+    with the oracle backend."""
+    cfg, kw = _random_schedule(G * 7 + H)
+    cfg.update(num_q_heads=H * G, num_kv_heads=H, block_size=bs,
+               hot_heads=list(range(0, H, 2)))
+    stats, trace, lock = _run(gpu, cfg, kw, steps=10, seed=900 + H)
+    print(f"G {G} H {H} bs {bs} {cfg} {kw}: {lock.summary()}")
