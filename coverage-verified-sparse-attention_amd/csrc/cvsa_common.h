@@ -17,7 +17,7 @@ constexpr int kPageTokens = 16; // tokens of a tile (a page is 1, 2 or 4 tiles)
 
 // Head dimensions the kernels are compiled for.
 __host__ __device__ constexpr bool head_dim_supported(int D) {
-  return D == 64 || D == 128 || D == 256;
+  return D == 32 || D == 64 || D == 128 || D == 256;
 }
 
 // The kernels walk pages as 16-token tiles: a page of block_size tokens is

@@ -503,7 +503,7 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 template <int G, int D, int TS>
 struct MfmaEngine {
   static_assert(G <= 16, "GQA group larger than the MFMA tile");
-  static_assert(D == 64 || D == 128 || D == 256, "head dimension");
+  static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head dimension");
   static_assert(TS == 0 || TS == -1, "tile shift: 0 (16-token pages) or -1 (from the args)");
   static constexpr int kD = D;
   static constexpr int kTileShift = TS;  // -1: from the args
@@ -1457,7 +1457,9 @@ void launch_decode_gd(const DecodeArgs &a, int kind, dim3 grid, dim3 block, hipS
 
 template <int G>
 void launch_decode_g(const DecodeArgs &a, int kind, dim3 grid, dim3 block, hipStream_t st) {
-  if (a.D == 64)
+  if (a.D == 32)
+    launch_decode_gd<G, 32>(a, kind, grid, block, st);
+  else if (a.D == 64)
     launch_decode_gd<G, 64>(a, kind, grid, block, st);
   else if (a.D == 256)
     launch_decode_gd<G, 256>(a, kind, grid, block, st);

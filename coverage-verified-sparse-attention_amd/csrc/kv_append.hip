@@ -132,7 +132,7 @@ extern "C" int cvsa_append_kv(const uint16_t *k_new, const uint16_t *v_new,
                CVSA_ERR_INVALID, "append_kv: bad sizes n_seqs=%d H_kv=%d W=%d", n_seqs,
                H_kv, W);
   CVSA_REQUIRE(head_dim_supported(D), CVSA_ERR_UNSUPPORTED,
-               "append_kv: D=%d not in {64, 128, 256}", D);
+               "append_kv: D=%d not in {32, 64, 128, 256}", D);
   CVSA_REQUIRE(((uintptr_t)k_new & 15) == 0 && ((uintptr_t)v_new & 15) == 0 &&
                    new_stride_b % 8 == 0 && ((uintptr_t)k_cache & 15) == 0 &&
                    ((uintptr_t)v_cache & 15) == 0,

@@ -116,7 +116,7 @@ static size_t workspace_bytes_for(int B, int H_q, int H_kv, int D, int max_sel, 
 }
 
 // Head dimensions with decode kernels.
-static bool decode_head_dim(int D) { return D == 64 || D == 128 || D == 256; }
+static bool decode_head_dim(int D) { return head_dim_supported(D); }
 
 // Argument checks of a decode launch (everything but the workspace) and its
 // launch plan; fills the launch-shape fields of `a`.  Returns a status.
@@ -134,7 +134,7 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
                "%s: GQA group size %d not in 1..%d", name, G, kMaxGroupTotal);
   const int ts = tile_shift(block_size);
   CVSA_REQUIRE(decode_head_dim(D) && ts >= 0, CVSA_ERR_UNSUPPORTED,
-               "%s: D=%d, block_size=%d not supported (D in {64, 128, 256}, block_size in "
+               "%s: D=%d, block_size=%d not supported (D in {32, 64, 128, 256}, block_size in "
                "{16, 32, 64})",
                name, D, block_size);
   CVSA_REQUIRE(a.num_blocks <= (INT32_MAX >> ts), CVSA_ERR_UNSUPPORTED,

@@ -198,7 +198,7 @@ int check_quest_sizes(const char *name, int32_t B, int32_t H_kv, int32_t D, int3
   CVSA_REQUIRE(B > 0 && H_kv > 0 && (int64_t)B * H_kv <= 65535 && W > 0 && num_blocks > 0,
                CVSA_ERR_INVALID, "%s: bad sizes B=%d H_kv=%d W=%d", name, B, H_kv, W);
   CVSA_REQUIRE(head_dim_supported(D) && tile_shift(block_size) >= 0, CVSA_ERR_UNSUPPORTED,
-               "%s: D=%d not in {64, 128, 256} or block_size=%d not in {16, 32, 64}", name, D,
+               "%s: D=%d not in {32, 64, 128, 256} or block_size=%d not in {16, 32, 64}", name, D,
                block_size);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
                kMaxPages);
@@ -241,7 +241,9 @@ extern "C" int cvsa_quest_meta_update(const uint16_t *k_cache, int64_t num_block
                      (hipStream_t)stream, nullptr, 0, 0, meta, meta_ntok, num_blocks,        \
                      block_tables, bt_stride_b, context_lens, k_cache, nullptr, 0, H_kv, 1,  \
                      1.0f, 1.0f, W, ppw, block_size, nullptr)
-  if (D == 64)
+  if (D == 32)
+    CVSA_QUEST_REFRESH(32);
+  else if (D == 64)
     CVSA_QUEST_REFRESH(64);
   else if (D == 256)
     CVSA_QUEST_REFRESH(256);
@@ -274,7 +276,9 @@ extern "C" int cvsa_quest_scores(const uint16_t *q, int64_t q_stride_b, int64_t 
                      const_cast<uint16_t *>(meta), nullptr, num_blocks, block_tables,        \
                      bt_stride_b, context_lens, nullptr, nullptr, 0, H_kv, G,                \
                      1.0f / (float)G, scale, W, ppw, block_size, page_scores)
-  if (D == 64)
+  if (D == 32)
+    CVSA_QUEST_SCORE(32);
+  else if (D == 64)
     CVSA_QUEST_SCORE(64);
   else if (D == 256)
     CVSA_QUEST_SCORE(256);
@@ -310,7 +314,9 @@ extern "C" int cvsa_quest_refresh_scores(const uint16_t *q, int64_t q_stride_b,
                      num_blocks, block_tables, bt_stride_b, context_lens, k_cache,            \
                      check_accept, B * H_kv, H_kv, G, 1.0f / (float)G, scale, W, ppw,         \
                      block_size, page_scores)
-  if (D == 64)
+  if (D == 32)
+    CVSA_QUEST_BOTH(32);
+  else if (D == 64)
     CVSA_QUEST_BOTH(64);
   else if (D == 256)
     CVSA_QUEST_BOTH(256);

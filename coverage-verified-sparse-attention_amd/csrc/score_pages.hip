@@ -201,7 +201,7 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
                "score_pages: H_q=%d is not a multiple of H_kv=%d", H_q, H_kv);
   const int ts = tile_shift(block_size);
   CVSA_REQUIRE(head_dim_supported(D) && ts >= 0, CVSA_ERR_UNSUPPORTED,
-               "score_pages: D=%d not in {64, 128, 256} or block_size=%d not in {16, 32, 64}",
+               "score_pages: D=%d not in {32, 64, 128, 256} or block_size=%d not in {16, 32, 64}",
                D, block_size);
   CVSA_REQUIRE(num_blocks <= (INT32_MAX >> ts), CVSA_ERR_UNSUPPORTED,
                "score_pages: %lld blocks exceed the tile index range", (long long)num_blocks);
@@ -253,15 +253,15 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
                        H_kv);                                                            \
     return cvsa_host::check_launch("score_pages");                                       \
   }
-    CVSA_GROUP_PPW(64, 0) CVSA_GROUP_PPW(128, 0) CVSA_GROUP_PPW(256, 0)
+    CVSA_GROUP_PPW(32, 0) CVSA_GROUP_PPW(64, 0) CVSA_GROUP_PPW(128, 0) CVSA_GROUP_PPW(256, 0)
 #undef CVSA_GROUP_PPW
 #undef CVSA_GROUP_CASE
     return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d, D=%d has no launch",
                            H_kv, D);
   }
-  if (R % H_kv != 0) {
-    // One KV head per wave: as many pages per wave (up to 16) as keep
-    // >= ~2048 waves in the launch.
+  if (R % H_kv != 0 || D == 32) {
+    // One KV head per wave (and every H_kv below 16 at D = 32): as many
+    // pages per wave (up to 16) as keep >= ~2048 waves in the launch.
     const int64_t head_pages = (int64_t)B * W * H_kv;
     int ppw = 1;
     while (ppw < 16 && head_pages / (2 * ppw) >= 2048) ppw *= 2;
@@ -278,7 +278,7 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
 #define CVSA_HEAD_PPW(DD) \
   CVSA_HEAD_CASE(DD, 1) CVSA_HEAD_CASE(DD, 2) CVSA_HEAD_CASE(DD, 4) CVSA_HEAD_CASE(DD, 8) \
   CVSA_HEAD_CASE(DD, 16)
-    CVSA_HEAD_PPW(64) CVSA_HEAD_PPW(128) CVSA_HEAD_PPW(256)
+    CVSA_HEAD_PPW(32) CVSA_HEAD_PPW(64) CVSA_HEAD_PPW(128) CVSA_HEAD_PPW(256)
 #undef CVSA_HEAD_PPW
 #undef CVSA_HEAD_CASE
     return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d, D=%d has no launch",

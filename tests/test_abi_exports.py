@@ -63,10 +63,10 @@ def test_decode_workspace_layout_is_fixed():
     bytes each) followed by whole partial rows of G x (D + 4)
     fp32, so launches of any B * H_kv can share one workspace: the counters
     of one launch never overlap the partial rows of another.  Head dimensions
-    outside {64, 128, 256} have no workspace (0)."""
+    outside {32, 64, 128, 256} have no workspace (0)."""
     lib = _lib_or_skip()
     seen = 0
-    for D in (64, 128, 256):
+    for D in (32, 64, 128, 256):
         for B in (1, 2, 3, 16, 32, 64):
             for H_kv, G in ((8, 4), (4, 7), (8, 8), (1, 1)):
                 for max_sel, W, all_pages in ((1024, 8192, 0), (128, 512, 1), (64, 2048, 0),

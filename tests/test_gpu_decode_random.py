@@ -117,7 +117,7 @@ def test_random_decode_launches(gpu, seed):
     _check(gpu, seed, 128)
 
 
-@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("D", [32, 64, 256])
 @pytest.mark.parametrize("seed", range(8))
 def test_random_decode_launches_head_dims(gpu, seed, D):
     _check(gpu, seed, D)

@@ -426,10 +426,10 @@ def test_random_shapes_plan_equals_separate_kernels(gpu, seed):
     _plan_equals_separate_kernels(gpu, seed, 128)
 
 
-@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("D", [32, 64, 256])
 @pytest.mark.parametrize("seed", range(3))
 def test_random_shapes_plan_head_dims(gpu, seed, D):
-    """The same at head dimensions 64 and 256 (no speculation there: the
+    """The same at head dimensions 32, 64 and 256 (no speculation there: the
     fused lazy-check launch is compiled for D = 128, so the plan runs the
     plain chain whether or not it was asked to speculate)."""
     _plan_equals_separate_kernels(gpu, seed, D)
