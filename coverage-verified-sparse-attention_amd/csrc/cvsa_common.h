@@ -26,6 +26,21 @@ __host__ __device__ constexpr bool head_dim_supported(int D) {
 __host__ __device__ constexpr int tile_shift(int block_size) {
   return block_size == 16 ? 0 : block_size == 32 ? 1 : block_size == 64 ? 2 : -1;
 }
+// 8-token pages: a page is one tile of which only rows 0..7 exist; the
+// kernels read row r & 7 in place of row r (in the page's own block, so no
+// load leaves the pool) and mask rows 8..15 out as tokens past the page.
+// Block sizes with kernels: 8, 16, 32, 64.
+__host__ __device__ constexpr bool block_size_supported(int block_size) {
+  return block_size == 8 || tile_shift(block_size) >= 0;
+}
+// Tiles per page as a shift (0 for 8-token pages) and log2 of the rows of
+// a tile (3 for 8-token pages, else 4).
+__host__ __device__ constexpr int page_tile_shift(int block_size) {
+  return block_size == 8 ? 0 : tile_shift(block_size);
+}
+__host__ __device__ constexpr int tile_rows_log2(int block_size) {
+  return block_size == 8 ? 3 : 4;
+}
 constexpr int kMaxPages = 32768;
 
 // ---------------------------------------------------------------- numerics

@@ -79,6 +79,7 @@ struct DecodeArgs {
   int H_kv, W;
   int D;      // head dimension (the launch's engine is compiled for it)
   int ts;     // tiles per page = 1 << ts
+  int tl;     // rows of a tile = 1 << tl: 4, or 3 for 8-token pages
   // Query heads: the launch serves heads q_off .. q_off + G - 1 (G the
   // kernel's group, at most 16) of each KV head's group of q_group; a larger
   // group runs as one launch per 16 of its heads.
@@ -174,9 +175,10 @@ __device__ __forceinline__ void add_work(const DecodeArgs &a, int n, int nv) {
   atomicAdd(&a.work[1], (unsigned long long)max(0, nv));
 }
 
-// n_valid_pages(ctx, 16 << ts), the division a shift where ctx > 0.
-__device__ __forceinline__ int valid_pages_ts(int ctx, int ts) {
-  return ctx > 0 ? ((ctx - 1) >> (4 + ts)) + 1 : n_valid_pages(ctx, kPageTokens << ts);
+// n_valid_pages(ctx, 1 << sh) for pages of 1 << sh tokens (sh = tl + ts),
+// the division a shift where ctx > 0.
+__device__ __forceinline__ int valid_pages_sh(int ctx, int sh) {
+  return ctx > 0 ? ((ctx - 1) >> sh) + 1 : n_valid_pages(ctx, 1 << sh);
 }
 
 // Logical tile of entry e of a head's listed walk: tile e & (2^ts - 1) of
@@ -213,10 +215,11 @@ enum { kModeAll = 0, kModeListed = 1, kModeVerified = 2, kModeApprox = 3 };
 enum { kWalkAll = 0, kWalkListed = 1, kWalkAlt = 2 };
 
 template <int MODE>
-__device__ __forceinline__ int head_pages(const DecodeArgs &a, int bh, int &walk, int ts) {
+__device__ __forceinline__ int head_pages(const DecodeArgs &a, int bh, int &walk, int ts,
+                                          int tl) {
   int n_all = 0, n_list = 0;
   if constexpr (MODE != kModeListed)
-    n_all = max(0, min(valid_pages_ts(a.ctx_lens[bh / a.H_kv], ts), a.W)) << ts;
+    n_all = max(0, min(valid_pages_sh(a.ctx_lens[bh / a.H_kv], tl + ts), a.W)) << ts;
   if constexpr (MODE != kModeAll) n_list = min(max(a.n_pages[bh], 0), a.max_sel) << ts;
   if constexpr (MODE == kModeAll) {
     walk = kWalkAll;
@@ -507,8 +510,10 @@ struct MfmaEngine {
   static_assert(TS == 0 || TS == -1, "tile shift: 0 (16-token pages) or -1 (from the args)");
   static constexpr int kD = D;
   static constexpr int kTileShift = TS;  // -1: from the args
-  // Tiles per page = 1 << tshift(a): compiled in for 16-token pages.
+  // Tiles per page = 1 << tshift(a), rows per tile = 1 << tlog(a): compiled
+  // in for 16-token pages.
   static __device__ __forceinline__ int tshift(const DecodeArgs &a) { return TS >= 0 ? TS : a.ts; }
+  static __device__ __forceinline__ int tlog(const DecodeArgs &a) { return TS >= 0 ? 4 : a.tl; }
   static constexpr int NK = D / 32;         // S = K Q^T MFMAs (32 dimensions each)
   static constexpr int NB = D / 16;         // O column blocks (16 dimensions each)
   static constexpr int LPR = D / 8;         // lanes per V row (16 bytes each)
@@ -527,16 +532,18 @@ struct MfmaEngine {
   bf16x8_t qb[NK];
   float m_g, l_g;
   int lane;
+  int rmask;  // rows of a tile - 1: a load of row r reads row r & rmask
   int64_t koff, voff, row_stride;
   float scale;
 
   __device__ __forceinline__ void init(const DecodeArgs &a, int b, int h, int lane_, Lds &) {
     lane = lane_;
     scale = a.scale;
+    rmask = (1 << tlog(a)) - 1;
     row_stride = (int64_t)a.H_kv * D;
     const int c16 = lane & 15, grp = lane >> 4;
-    koff = (int64_t)h * D + c16 * row_stride + 8 * grp;
-    voff = (int64_t)h * D + (lane / LPR) * row_stride + 8 * (lane % LPR);
+    koff = (int64_t)h * D + (c16 & rmask) * row_stride + 8 * grp;
+    voff = (int64_t)h * D + ((lane / LPR) & rmask) * row_stride + 8 * (lane % LPR);
     // Rows past the group repeat head G-1: MFMA output rows are independent
     // and those rows are never written out.  No select on the loaded value,
     // so nothing waits for q before the first page is consumed.
@@ -559,9 +566,11 @@ struct MfmaEngine {
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk)
       pg.k[kk] = *reinterpret_cast<const uint4 *>(kp + koff + 32 * kk);
+    // Load i reads rows RPL i + lane / LPR: with 8-row tiles those past row
+    // 7 fold onto rows 0..7 (RPL is a power of two, so the mask splits).
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-      pg.v[i] = stream_load16(vp + voff + RPL * i * row_stride);
+      pg.v[i] = stream_load16(vp + voff + ((RPL * i) & rmask) * row_stride);
   }
 
   // fetch() for a walk whose sequence appends a token in this launch: the
@@ -894,6 +903,7 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
   const int r0 = split * pps;
   const int32_t *idx_row = a.page_idx + (int64_t)bh * a.idx_stride;
   const int ts = Engine::tshift(a);
+  const int tl = Engine::tlog(a);
   const int n = min(max(__builtin_amdgcn_readfirstlane(a.n_pages[bh]), 0), a.max_sel) << ts;
   const int r1 = min(n, r0 + pps);
   const int n_act = (n + pps - 1) / pps;  // splits holding pages of this head
@@ -912,7 +922,7 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
     if (scoring)
       qr_own = group_mean_q(a.q, a.q_sb, a.q_sh, b, h, a.q_group, min(lane, 15), a.inv_g);
   }
-  const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * Engine::kD;  // between blocks
+  const int64_t page_elems = ((int64_t)a.H_kv * Engine::kD) << tl;  // between tiles
   const int npw = max(0, (r1 - r0 - wave + NW - 1) / NW);
   for (int c0 = 0; c0 < npw; c0 += kWave) {
     const int cn = min(kWave, npw - c0);
@@ -926,7 +936,7 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
         if (APP && lt == nt.page && nt.new_blk >= 0) pt = nt.new_blk;
         if (pt >= 0 && pt < (a.num_blocks << ts)) {
           my_phys = pt;
-          my_ntok = max(0, min(kPageTokens, ctx - lt * kPageTokens));
+          my_ntok = max(0, min(1 << tl, ctx - (lt << tl)));
           if (APP && lt == nt.page) my_new = nt.off;
         }
       }
@@ -975,7 +985,7 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
   __syncthreads();
   const PartBuf pb(a.part, a.part_bytes);
   segment_epilogue<G, Engine::kD, NW, kMergeBatchListed>(
-      a, pb, bh, n >> ts, valid_pages_ts(ctx, ts), n_act, (uint32_t)(bh * a.n_splits + split),
+      a, pb, bh, n >> ts, valid_pages_sh(ctx, tl + ts), n_act, (uint32_t)(bh * a.n_splits + split),
       (uint32_t)(bh * a.n_splits), L.o, L.m, L.l, L.last, L.tail.merge);
 }
 
@@ -1151,8 +1161,9 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   const int w = blockIdx.x;
   const int heads = a.heads;
   constexpr int D = Engine::kD;
-  const int64_t page_elems = (int64_t)kPageTokens * a.H_kv * D;  // between tiles
   const int ts = Engine::tshift(a);
+  const int tl = Engine::tlog(a);
+  const int64_t page_elems = ((int64_t)a.H_kv * D) << tl;  // between tiles
 
   // Verified launches whose heads are all accepted (a lazy check that keeps
   // its selection, or a scoring step whose gate passes everywhere) run the
@@ -1228,7 +1239,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
   // A head walking its expanded selection never takes the speculated
   // partition, whose first pages come from page_indices.
   int l_first = kWalkAll;
-  int c_first = head_pages<MODE>(a, min((int)threadIdx.x, heads - 1), l_first, ts);
+  int c_first = head_pages<MODE>(a, min((int)threadIdx.x, heads - 1), l_first, ts, tl);
   if constexpr (MODE != kModeAll)
     spec_phys = tile_block(a, b_spec, spec_lp, ts);
   if ((int)threadIdx.x >= heads) c_first = 0;
@@ -1274,7 +1285,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     eng.fetch(a.k_cache + base, a.v_cache + base, pg);
     return __builtin_amdgcn_readlane(my_lp, j);
   };
-  auto ntok = [&](int lp) { return min(kPageTokens, max(0, cur_ctx - lp * kPageTokens)); };
+  auto ntok = [&](int lp) { return min(1 << tl, max(0, cur_ctx - (lp << tl))); };
   auto prologue = [&](int cn) {
 #pragma unroll
     for (int u = 0; u < PD; ++u)
@@ -1325,7 +1336,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     for (int base = NT; base < heads; base += NT) {
       const int hh = base + threadIdx.x;
       int lst = kWalkAll;
-      int c = head_pages<MODE>(a, min(hh, heads - 1), lst, ts);
+      int c = head_pages<MODE>(a, min(hh, heads - 1), lst, ts, tl);
       if (hh >= heads) c = 0;
       const int incl = wave_incl_scan(c);
       if (lane == kWave - 1) s_wsum[wave] = incl;
@@ -1353,7 +1364,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     for (int i = threadIdx.x; i < G * D; i += NT)
       write_outputs<D>(a, row0 + i / D, i % D, 0.f, -INFINITY, 0.f);
     if (threadIdx.x == 0 && a.work != nullptr) {
-      const int nv = valid_pages_ts(a.ctx_lens[hh / a.H_kv], ts);
+      const int nv = valid_pages_sh(a.ctx_lens[hh / a.H_kv], tl + ts);
       add_work(a, MODE == kModeApprox ? approx_booked_pages(a, hh, nv) : 0, nv);
     }
   }
@@ -1407,7 +1418,7 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     __syncthreads();
 
     const int first = part.owner(P);
-    const int nv = valid_pages_ts(ctx, ts);
+    const int nv = valid_pages_sh(ctx, tl + ts);
     const int booked = MODE == kModeApprox ? approx_booked_pages(a, h, nv) : n >> ts;
     segment_epilogue<G, D, NW, kMergeBatchStreamK, true>(a, pb, h, booked, nv,
                                part.owner(P + n - 1) - first + 1, (uint32_t)(w + h),
@@ -1449,7 +1460,7 @@ void launch_decode_gdt(const DecodeArgs &a, int kind, dim3 grid, dim3 block, hip
 // 16-token pages run engines with the tile shift compiled in (0).
 template <int G, int D>
 void launch_decode_gd(const DecodeArgs &a, int kind, dim3 grid, dim3 block, hipStream_t st) {
-  if (a.ts == 0)
+  if (a.ts == 0 && a.tl == 4)
     launch_decode_gdt<G, D, 0>(a, kind, grid, block, st);
   else
     launch_decode_gdt<G, D, -1>(a, kind, grid, block, st);
@@ -1479,7 +1490,7 @@ void launch_append_g(const DecodeArgs &a, const AppendArgs &app, dim3 grid, hipS
 template <int G>
 void launch_spec_g(const DecodeArgs &a, const ScoreArgs &s, int score_gx, dim3 grid,
                    hipStream_t st) {
-  if (a.ts == 0)
+  if (a.ts == 0 && a.tl == 4)
     hipLaunchKernelGGL((score_spec_kernel<G, MfmaEngine<G, 128, 0>, kWavesPerWg, 2>), grid,
                        dim3(kWavesPerWg * kWave), 0, st, a, s, score_gx);
   else

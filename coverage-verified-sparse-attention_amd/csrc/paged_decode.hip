@@ -132,11 +132,11 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   const int G = H_q / H_kv;
   CVSA_REQUIRE(G >= 1 && G <= kMaxGroupTotal, CVSA_ERR_UNSUPPORTED,
                "%s: GQA group size %d not in 1..%d", name, G, kMaxGroupTotal);
-  const int ts = tile_shift(block_size);
-  CVSA_REQUIRE(decode_head_dim(D) && ts >= 0, CVSA_ERR_UNSUPPORTED,
+  CVSA_REQUIRE(decode_head_dim(D) && block_size_supported(block_size), CVSA_ERR_UNSUPPORTED,
                "%s: D=%d, block_size=%d not supported (D in {32, 64, 128, 256}, block_size in "
-               "{16, 32, 64})",
+               "{8, 16, 32, 64})",
                name, D, block_size);
+  const int ts = page_tile_shift(block_size);
   CVSA_REQUIRE(a.num_blocks <= (INT32_MAX >> ts), CVSA_ERR_UNSUPPORTED,
                "%s: %lld blocks exceed the tile index range", name, (long long)a.num_blocks);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
@@ -191,6 +191,7 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   a.sk_grid = p.sk_grid;
   a.D = D;
   a.ts = ts;
+  a.tl = tile_rows_log2(block_size);
   a.q_group = G;
   a.q_off = 0;
   a.scale = (float)pow((double)D, -0.5);
@@ -580,9 +581,11 @@ int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_
   a.spec_state = spec_state;
   CVSA_REQUIRE(page_indices && spec_state && page_scores, CVSA_ERR_INVALID,
                "%s: page_indices, spec_state and page_scores are required", name);
-  CVSA_REQUIRE(H_kv > 0 && H_q % H_kv == 0 && score_spec_fusable(H_kv, D, H_q / H_kv),
-               CVSA_ERR_UNSUPPORTED, "%s: H_kv=%d not in {4,8,16}, D=%d not 128 or G > %d",
-               name, H_kv, D, kMaxGroup);
+  CVSA_REQUIRE(H_kv > 0 && H_q % H_kv == 0 && score_spec_fusable(H_kv, D, H_q / H_kv) &&
+                   block_size != 8,
+               CVSA_ERR_UNSUPPORTED,
+               "%s: H_kv=%d not in {4,8,16}, D=%d not 128, G > %d or 8-token pages", name,
+               H_kv, D, kMaxGroup);
   DecodeLaunch p{};
   size_t need = 0;
   int rc = validate_decode(name, a, B, H_q, H_kv, D, block_size, W, true, false, p, need);

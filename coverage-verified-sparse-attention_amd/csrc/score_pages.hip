@@ -138,9 +138,13 @@ __global__ __launch_bounds__(256) void score_pages_head_kernel(const ScoreArgs s
     }
   }
   const uint4 qr = group_mean_q(s.q, s.q_sb, s.q_sh, b, h, s.G, seg, s.inv_g);
+  // Rows of a tile: 16, or 8 at 8-token pages, whose loads of rows 8..15
+  // read rows 0..7 of the same block again (masked out below).
+  const int tr = min(s.bs, kPageTokens);
+  const int rmask = tr - 1;
   const int64_t row_stride = (int64_t)hkv * D;
-  const int64_t tile_elems = kPageTokens * row_stride;
-  const int64_t lane_off = row * row_stride + (int64_t)h * D + seg * 8;
+  const int64_t tile_elems = tr * row_stride;
+  const int64_t lane_off = (row & rmask) * row_stride + (int64_t)h * D + seg * 8;
   const int tm = (1 << s.ts) - 1;
   const int nt = n << s.ts;  // tiles of this wave
   // Unconditional loads (block 0 for pages without valid tokens) keep the
@@ -149,7 +153,7 @@ __global__ __launch_bounds__(256) void score_pages_head_kernel(const ScoreArgs s
     const int phys = max(__builtin_amdgcn_readlane(my_phys, t >> s.ts), 0);
     const uint16_t *src = s.k_cache + (((int64_t)phys << s.ts) | (t & tm)) * tile_elems + lane_off;
 #pragma unroll
-    for (int i = 0; i < NL; ++i) kv[i] = stream_load16(src + (int64_t)i * RPL * row_stride);
+    for (int i = 0; i < NL; ++i) kv[i] = stream_load16(src + (int64_t)((i * RPL) & rmask) * row_stride);
   };
   float pm = -INFINITY;  // this lane's rows, over the tiles of the current page
   auto consume = [&](int t, const uint4 (&kv)[NL]) {
@@ -157,7 +161,7 @@ __global__ __launch_bounds__(256) void score_pages_head_kernel(const ScoreArgs s
     const int p = p_begin + j;
     const int tn = __builtin_amdgcn_readlane(my_phys, j) < 0
                        ? 0
-                       : min(kPageTokens, ctx - p * s.bs - sub * kPageTokens);
+                       : min(tr, ctx - p * s.bs - sub * tr);
     float mx = sub == 0 ? -INFINITY : pm;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -199,10 +203,11 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
                (long long)num_blocks);
   CVSA_REQUIRE(H_kv > 0 && H_q > 0 && H_q % H_kv == 0, CVSA_ERR_INVALID,
                "score_pages: H_q=%d is not a multiple of H_kv=%d", H_q, H_kv);
-  const int ts = tile_shift(block_size);
-  CVSA_REQUIRE(head_dim_supported(D) && ts >= 0, CVSA_ERR_UNSUPPORTED,
-               "score_pages: D=%d not in {32, 64, 128, 256} or block_size=%d not in {16, 32, 64}",
+  CVSA_REQUIRE(head_dim_supported(D) && block_size_supported(block_size), CVSA_ERR_UNSUPPORTED,
+               "score_pages: D=%d not in {32, 64, 128, 256} or block_size=%d not in {8, 16, 32, "
+               "64}",
                D, block_size);
+  const int ts = page_tile_shift(block_size);
   CVSA_REQUIRE(num_blocks <= (INT32_MAX >> ts), CVSA_ERR_UNSUPPORTED,
                "score_pages: %lld blocks exceed the tile index range", (long long)num_blocks);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
@@ -221,7 +226,7 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
 
   hipStream_t st = (hipStream_t)stream;
   const int R = kWave / (D / 8);
-  if (H_kv % R == 0) {
+  if (H_kv % R == 0 && block_size != 8) {
     // Head-group layout: waves = tiles / PPW x H_kv / R.  As many 16-token
     // tiles per wave (up to 8, at least one page) as keep >= ~2048 waves
     // (8 per CU) in the launch: the setup (q_rep, block-table fetch) is
@@ -259,9 +264,10 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
     return cvsa_host::fail(CVSA_ERR_UNSUPPORTED, "score_pages: H_kv=%d, D=%d has no launch",
                            H_kv, D);
   }
-  if (R % H_kv != 0 || D == 32) {
-    // One KV head per wave (and every H_kv below 16 at D = 32): as many
-    // pages per wave (up to 16) as keep >= ~2048 waves in the launch.
+  if (R % H_kv != 0 || D == 32 || block_size == 8) {
+    // One KV head per wave (also every H_kv below 16 at D = 32, and every
+    // H_kv at 8-token pages): as many pages per wave (up to 16) as keep
+    // >= ~2048 waves in the launch.
     const int64_t head_pages = (int64_t)B * W * H_kv;
     int ppw = 1;
     while (ppw < 16 && head_pages / (2 * ppw) >= 2048) ppw *= 2;

@@ -55,9 +55,10 @@ int check_desc(const cvsa_step_desc &d) {
                "step_plan: B * H_kv = %lld exceeds %lld heads", (long long)d.B * d.H_kv,
                (long long)kMaxDecodeHeads);
   STEP_REQUIRE((d.D == 32 || d.D == 64 || d.D == 128 || d.D == 256) &&
-                   (d.block_size == 16 || d.block_size == 32 || d.block_size == 64),
+                   (d.block_size == 8 || d.block_size == 16 || d.block_size == 32 ||
+                    d.block_size == 64),
                CVSA_ERR_UNSUPPORTED,
-               "step_plan: D=%d not in {32, 64, 128, 256} or block_size=%d not in {16, 32, 64}",
+               "step_plan: D=%d not in {32, 64, 128, 256} or block_size=%d not in {8, 16, 32, 64}",
                d.D, d.block_size);
   STEP_REQUIRE(d.W > 0 && d.W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
                "step_plan: W=%d not in 1..%d", d.W, kMaxPages);
@@ -184,7 +185,7 @@ namespace {
 // Whether a lazy check of this plan speculates: spec_state given, gate
 // scores from the exact scan, and a fused scoring + decode launch for H_kv.
 bool speculates(const cvsa_step_desc &d) {
-  return d.spec_state != nullptr && d.selector != CVSA_SELECT_QUEST_LN &&
+  return d.spec_state != nullptr && d.selector != CVSA_SELECT_QUEST_LN && d.block_size != 8 &&
          cvsa_internal::score_spec_fusable(d.H_kv, d.D, d.H_q / d.H_kv);
 }
 
