@@ -24,12 +24,13 @@ __host__ __device__ constexpr bool head_dim_supported(int D) {
 // 1 << tile_shift(block_size) consecutive tiles of its block.  -1: the block
 // size is not supported.
 __host__ __device__ constexpr int tile_shift(int block_size) {
-  return block_size == 16 ? 0 : block_size == 32 ? 1 : block_size == 64 ? 2 : -1;
+  return block_size == 16 ? 0 : block_size == 32 ? 1 : block_size == 64 ? 2
+         : block_size == 128 ? 3 : -1;
 }
 // 8-token pages: a page is one tile of which only rows 0..7 exist; the
 // kernels read row r & 7 in place of row r (in the page's own block, so no
 // load leaves the pool) and mask rows 8..15 out as tokens past the page.
-// Block sizes with kernels: 8, 16, 32, 64.
+// Block sizes with kernels: 8, 16, 32, 64, 128.
 __host__ __device__ constexpr bool block_size_supported(int block_size) {
   return block_size == 8 || tile_shift(block_size) >= 0;
 }

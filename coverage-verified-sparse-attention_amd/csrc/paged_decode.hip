@@ -134,7 +134,7 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
                "%s: GQA group size %d not in 1..%d", name, G, kMaxGroupTotal);
   CVSA_REQUIRE(decode_head_dim(D) && block_size_supported(block_size), CVSA_ERR_UNSUPPORTED,
                "%s: D=%d, block_size=%d not supported (D in {32, 64, 128, 256}, block_size in "
-               "{8, 16, 32, 64})",
+               "{8, 16, 32, 64, 128})",
                name, D, block_size);
   const int ts = page_tile_shift(block_size);
   CVSA_REQUIRE(a.num_blocks <= (INT32_MAX >> ts), CVSA_ERR_UNSUPPORTED,
@@ -606,7 +606,7 @@ int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_
     a.spec_scores = page_scores;
     a.inv_g = sa.inv_g;
   }
-  static_assert(kSpecScorePPW % 4 == 0, "a scoring wave holds whole pages of up to 4 tiles");
+  static_assert(kSpecScorePPW % 8 == 0, "a scoring wave holds whole pages of up to 8 tiles");
   // 16-token pages: a wave per head and kSpecHeadPPW pages; else a wave per
   // 4 heads and kSpecScorePPW tiles.
   const int64_t waves =

@@ -198,7 +198,7 @@ int check_quest_sizes(const char *name, int32_t B, int32_t H_kv, int32_t D, int3
   CVSA_REQUIRE(B > 0 && H_kv > 0 && (int64_t)B * H_kv <= 65535 && W > 0 && num_blocks > 0,
                CVSA_ERR_INVALID, "%s: bad sizes B=%d H_kv=%d W=%d", name, B, H_kv, W);
   CVSA_REQUIRE(head_dim_supported(D) && block_size_supported(block_size), CVSA_ERR_UNSUPPORTED,
-               "%s: D=%d not in {32, 64, 128, 256} or block_size=%d not in {8, 16, 32, 64}", name, D,
+               "%s: D=%d not in {32, 64, 128, 256} or block_size=%d not in {8, 16, 32, 64, 128}", name, D,
                block_size);
   CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
                kMaxPages);

@@ -205,7 +205,7 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
                "score_pages: H_q=%d is not a multiple of H_kv=%d", H_q, H_kv);
   CVSA_REQUIRE(head_dim_supported(D) && block_size_supported(block_size), CVSA_ERR_UNSUPPORTED,
                "score_pages: D=%d not in {32, 64, 128, 256} or block_size=%d not in {8, 16, 32, "
-               "64}",
+               "64, 128}",
                D, block_size);
   const int ts = page_tile_shift(block_size);
   CVSA_REQUIRE(num_blocks <= (INT32_MAX >> ts), CVSA_ERR_UNSUPPORTED,

@@ -56,9 +56,9 @@ int check_desc(const cvsa_step_desc &d) {
                (long long)kMaxDecodeHeads);
   STEP_REQUIRE((d.D == 32 || d.D == 64 || d.D == 128 || d.D == 256) &&
                    (d.block_size == 8 || d.block_size == 16 || d.block_size == 32 ||
-                    d.block_size == 64),
+                    d.block_size == 64 || d.block_size == 128),
                CVSA_ERR_UNSUPPORTED,
-               "step_plan: D=%d not in {32, 64, 128, 256} or block_size=%d not in {8, 16, 32, 64}",
+               "step_plan: D=%d not in {32, 64, 128, 256} or block_size=%d not in {8, 16, 32, 64, 128}",
                d.D, d.block_size);
   STEP_REQUIRE(d.W > 0 && d.W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
                "step_plan: W=%d not in 1..%d", d.W, kMaxPages);

@@ -15,7 +15,8 @@
  *    to the caller; a step plan (below) is a small host object.
  *  - Return value: CVSA_OK (0), or a negative CVSA_ERR_* code with nothing
  *    enqueued.  cvsa_last_error() then returns a thread-local message.
- *  - Supported geometry: D in {32, 64, 128, 256}, block_size in {8, 16, 32, 64},
+ *  - Supported geometry: D in {32, 64, 128, 256}, block_size in {8, 16, 32, 64,
+ *    128},
  *    G = H_q / H_kv in 1..128 (decode launches serve 16 query heads per KV
  *    head; larger groups are enqueued as one launch per 16),
  *    any H_kv (B * H_kv <= 65535), W <= 32768 pages, and B * H_kv <= 4096

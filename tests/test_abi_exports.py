@@ -127,6 +127,7 @@ def test_step_plan_validates_on_the_host():
              (dict(H_kv=3, H_q=10), _lib.CVSA_ERR_INVALID, b"head counts"),
              (dict(D=96), _lib.CVSA_ERR_UNSUPPORTED, b"D=96"),
              (dict(block_size=12), _lib.CVSA_ERR_UNSUPPORTED, b"block_size=12"),
+             (dict(block_size=256), _lib.CVSA_ERR_UNSUPPORTED, b"block_size=256"),
              (dict(bt_stride_b=100), _lib.CVSA_ERR_INVALID, b"stride"),
              (dict(coverage=None), _lib.CVSA_ERR_INVALID, b"null"),
              (dict(out_dtype=5), _lib.CVSA_ERR_INVALID, b"dtype"),

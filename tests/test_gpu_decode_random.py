@@ -123,7 +123,7 @@ def test_random_decode_launches_head_dims(gpu, seed, D):
     _check(gpu, seed, D)
 
 
-@pytest.mark.parametrize("BS", [8, 32, 64])
+@pytest.mark.parametrize("BS", [8, 32, 64, 128])
 @pytest.mark.parametrize("seed", range(8))
 def test_random_decode_launches_block_sizes(gpu, seed, BS):
     _check(gpu, seed, [128, 64, 256][seed % 3], BS)

@@ -1,4 +1,4 @@
-"""Head dimensions 32, 64 and 256, block sizes 8, 32 and 64 and GQA groups of 9 to
+"""Head dimensions 32, 64 and 256, block sizes 8, 32, 64 and 128 and GQA groups of 9 to
 40 query heads through the entry points that take them, against the
 oracle: page scoring in both of its layouts (a wave load holds 64 / (D/8)
 key rows, so the head-group layout needs H_kv a multiple of 8, 4, 2 at
@@ -41,7 +41,8 @@ def _close(got, want, rtol):
 
 
 GEOMETRIES = [(64, 16), (256, 16), (128, 32), (128, 64), (64, 32), (256, 64),
-              (32, 16), (32, 64), (128, 8), (64, 8), (256, 8), (32, 8)]  # (D, bs)
+              (32, 16), (32, 64), (128, 8), (64, 8), (256, 8), (32, 8), (128, 128),
+              (64, 128)]  # (D, bs)
 
 
 @pytest.mark.parametrize("D,bs", GEOMETRIES)

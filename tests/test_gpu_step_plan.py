@@ -435,10 +435,10 @@ def test_random_shapes_plan_head_dims(gpu, seed, D):
     _plan_equals_separate_kernels(gpu, seed, D)
 
 
-@pytest.mark.parametrize("BS", [8, 32, 64])
+@pytest.mark.parametrize("BS", [8, 32, 64, 128])
 @pytest.mark.parametrize("seed", range(3))
 def test_random_shapes_plan_block_sizes(gpu, seed, BS):
-    """The same at block sizes 8, 32 and 64 (speculation included at D = 128,
+    """The same at block sizes 8, 32, 64 and 128 (speculation included at D = 128,
     except at 8-token pages, where the plan runs the plain chain)."""
     _plan_equals_separate_kernels(gpu, seed, [128, 64, 128][seed], BS)
 
