@@ -86,6 +86,12 @@ struct DecodeArgs {
   int q_group, q_off;
   int heads;  // B * H_kv
   int pps, n_splits;  // listed partition: tiles per split, splits per head
+  // Identity partition (every valid page of every head, in page order, as
+  // a listed walk of the list 0, 1, 2, ...): tiles per split, splits per
+  // head.  Verified launches whose heads are all rejected use it, and so
+  // does the lazy check's speculative dense decode, so the two write the
+  // same bits.
+  int pps_all, n_splits_all;
   int sk_grid;        // stream-K partition: workgroups (<= kMaxSplits)
   float scale;
   float *o_unnorm, *m_out, *l_out;
@@ -95,9 +101,13 @@ struct DecodeArgs {
   uint32_t part_bytes;
   unsigned *counters;        // per head, zero between launches
   unsigned long long *work;  // optional effective-budget counters
-  // A lazy check's speculative decode of its kept selection (or NULL):
-  // [0] != 0 predicts that the check keeps its selection, [1] records
-  // whether the speculative listed decode ran (and wrote the outputs).
+  // A lazy check's speculation (or NULL).  [0]: the prediction, 1 = the
+  // check keeps its selection (speculative listed decode of the cached
+  // selection), 2 = every head is rejected (speculative dense decode, the
+  // identity partition), else none; the check's select-or-keep overwrites
+  // it with its keep flag (0 / 1), and a verified launch whose heads are
+  // all rejected sets it to 2.  [1]: which speculative decode ran and wrote
+  // the outputs (0 none, 1 listed, 2 dense).
   int32_t *spec_state;
   // The speculative decode also writes the page scores of the pages it
   // walks into spec_scores [B * H_kv, W] (or NULL), as the page scoring
@@ -875,6 +885,16 @@ __device__ __forceinline__ void listed_first_pages(const DecodeArgs &a, int spli
   phys = listed_first_block(a, bh, lp, ts);
 }
 
+// The first tiles of split `split` of a head's identity walk (lane j of wave
+// w: entry r0 + w + NW j, the tile of the same index) and their blocks.
+template <int NW>
+__device__ __forceinline__ void ident_first_pages(const DecodeArgs &a, int split, int bh,
+                                                  int wave, int lane, int ts, int &lp,
+                                                  int &phys) {
+  lp = split * a.pps_all + wave + NW * lane;
+  phys = tile_block(a, bh / a.H_kv, lp, ts);
+}
+
 // Listed pages of a head (the sparse decode of reuse steps, and verified
 // launches whose heads are all accepted): split s of head bh walks listed
 // pages [s * pps, (s + 1) * pps) of bh; splits past a head's pages only take
@@ -887,7 +907,8 @@ __device__ __forceinline__ void listed_first_pages(const DecodeArgs &a, int spli
 // With SCORE and a.spec_scores, the walk also writes the page score of
 // every page it walks (Engine::page_score; qrep: this wave's LDS copy of the
 // 16 q_rep segments, 16-token pages).
-template <int G, class Engine, int NW, int PD, bool APP = false, bool SCORE = false>
+template <int G, class Engine, int NW, int PD, bool APP = false, bool SCORE = false,
+          bool IDENT = false>
 __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int bh, int spec_lp,
                                             int spec_phys, WalkLds<G, Engine, NW> &L,
                                             const NewToken &nt = NewToken(),
@@ -899,12 +920,17 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
   const int h = bh - b * a.H_kv;
   const int ctx = APP ? nt.page * kPageTokens + nt.off + 1
                       : __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
-  const int pps = a.pps;
+  const int pps = IDENT ? a.pps_all : a.pps;
+  const int n_spl = IDENT ? a.n_splits_all : a.n_splits;
   const int r0 = split * pps;
   const int32_t *idx_row = a.page_idx + (int64_t)bh * a.idx_stride;
   const int ts = Engine::tshift(a);
   const int tl = Engine::tlog(a);
-  const int n = min(max(__builtin_amdgcn_readfirstlane(a.n_pages[bh]), 0), a.max_sel) << ts;
+  // IDENT: entry e is tile e of the head's valid pages (n_valid as the
+  // reference computes it, at most W).
+  const int n = IDENT ? max(0, min(valid_pages_sh(ctx, tl + ts), a.W)) << ts
+                      : min(max(__builtin_amdgcn_readfirstlane(a.n_pages[bh]), 0), a.max_sel)
+                            << ts;
   const int r1 = min(n, r0 + pps);
   const int n_act = (n + pps - 1) / pps;  // splits holding pages of this head
   if (r0 >= r1 && !(split == 0 && n_act == 0)) return;  // uniform
@@ -928,8 +954,9 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
     const int cn = min(kWave, npw - c0);
     int my_phys = 0, my_ntok = 0, my_new = -1, my_lt = -1;
     if (lane < cn) {
-      const int lt =
-          c0 == 0 ? spec_lp : listed_tile(a, idx_row, r0 + wave + NW * (c0 + lane), ts);
+      const int lt = c0 == 0 ? spec_lp
+                     : IDENT ? r0 + wave + NW * (c0 + lane)
+                             : listed_tile(a, idx_row, r0 + wave + NW * (c0 + lane), ts);
       if (lt >= 0 && lt < (a.W << ts)) {
         my_lt = lt;
         int pt = c0 == 0 ? spec_phys : tile_block(a, b, lt, ts);
@@ -985,8 +1012,8 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
   __syncthreads();
   const PartBuf pb(a.part, a.part_bytes);
   segment_epilogue<G, Engine::kD, NW, kMergeBatchListed>(
-      a, pb, bh, n >> ts, valid_pages_sh(ctx, tl + ts), n_act, (uint32_t)(bh * a.n_splits + split),
-      (uint32_t)(bh * a.n_splits), L.o, L.m, L.l, L.last, L.tail.merge);
+      a, pb, bh, n >> ts, valid_pages_sh(ctx, tl + ts), n_act, (uint32_t)(bh * n_spl + split),
+      (uint32_t)(bh * n_spl), L.o, L.m, L.l, L.last, L.tail.merge);
 }
 
 // The listed decode: a static grid of (split, head) workgroups.
@@ -1100,31 +1127,47 @@ void score_spec_kernel(const DecodeArgs a,
   __shared__ uint4 s_qrep[NW][16];  // decode part: q_rep per wave
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n_dec = a.n_splits * a.heads;
+  const int n_dec = max(a.n_splits, a.n_splits_all) * a.heads;
   const int w = blockIdx.x;
+  // The speculation that runs: 1 = listed decode of the cached selection
+  // (predicted keep), 2 = dense decode, which needs the scoring from its
+  // keys (16-token pages and a selection map), else 0.
+  const int pred = __builtin_amdgcn_readfirstlane(a.spec_state[0]);
+  const int go = pred == 1 ? 1
+                 : pred == 2 && Engine::kTileShift == 0 && a.spec_scores != nullptr ? 2
+                                                                                    : 0;
   if (w >= n_dec) {  // uniform
     const int sw = w - n_dec;
     const int gw = (sw % score_gx) * NW + wave, b = sw / score_gx;
     if constexpr (Engine::kTileShift == 0) {
       // With a skip map, the pages the speculative decode walks (when it
-      // runs) are scored there.
-      const bool go =
-          s.skip_map != nullptr && __builtin_amdgcn_readfirstlane(a.spec_state[0]) != 0;
-      score_head_wave<kSpecHeadPPW, 4>(s, a.H_kv, gw, b, go);
+      // runs) are scored there: the selection's, or every valid page.
+      const int ctx = __builtin_amdgcn_readfirstlane(s.context_lens[b]);
+      score_head_wave<kSpecHeadPPW, 4>(s, a.H_kv, gw, b, s.skip_map != nullptr && go == 1,
+                                       go == 2 ? n_valid_pages(ctx, kPageTokens) : 0);
     } else {
       score_group_wave<128, kSpecScorePPW>(s, a.H_kv, gw, b);
     }
     return;
   }
-  const int split = w % a.n_splits;
-  const int bh = w / a.n_splits;
-  int lp, phys;
-  listed_first_pages<NW>(a, split, bh, wave, lane, Engine::tshift(a), lp, phys);
-  const int go = __builtin_amdgcn_readfirstlane(a.spec_state[0]);
   if (w == 0 && threadIdx.x == 0) a.spec_state[1] = go;
-  if (go == 0) return;  // uniform
-  listed_walk<G, Engine, NW, PD, false, Engine::kTileShift == 0>(a, split, bh, lp, phys, L,
-                                                                 NewToken(), s_qrep[wave]);
+  if (go == 1) {  // uniform
+    if (w >= a.n_splits * a.heads) return;
+    const int split = w % a.n_splits;
+    const int bh = w / a.n_splits;
+    int lp, phys;
+    listed_first_pages<NW>(a, split, bh, wave, lane, Engine::tshift(a), lp, phys);
+    listed_walk<G, Engine, NW, PD, false, Engine::kTileShift == 0>(a, split, bh, lp, phys, L,
+                                                                   NewToken(), s_qrep[wave]);
+  } else if constexpr (Engine::kTileShift == 0) {
+    if (go != 2 || w >= a.n_splits_all * a.heads) return;  // uniform
+    const int split = w % a.n_splits_all;
+    const int bh = w / a.n_splits_all;
+    int lp, phys;
+    ident_first_pages<NW>(a, split, bh, wave, lane, 0, lp, phys);
+    listed_walk<G, Engine, NW, PD, false, true, true>(a, split, bh, lp, phys, L, NewToken(),
+                                                      s_qrep[wave]);
+  }
 }
 
 // NW waves per workgroup, PD pages of K/V in flight per wave.
@@ -1185,14 +1228,45 @@ __global__ __launch_bounds__(NW * kWave) void streamk_decode_kernel(const Decode
     const int lp = listed_first_entry<NW>(a, split, bh, wave, lane, Engine::tshift(a));
     int spec_done = 0;
     if (a.spec_state != nullptr)
-      spec_done = __builtin_amdgcn_readfirstlane(a.spec_state[0] & a.spec_state[1]);
+      spec_done = __builtin_amdgcn_readfirstlane(a.spec_state[0] == 1 && a.spec_state[1] == 1);
     if (spec_done != 0) return;  // uniform; every head was accepted (kept)
-    int rejected = 0;
-    for (int i = threadIdx.x; i < heads; i += NT) rejected |= a.accept[i] == 0;
-    if (__syncthreads_or(rejected) == 0) {  // uniform
+    int rejected = 0, accepted = 0;
+    for (int i = threadIdx.x; i < heads; i += NT) {
+      rejected |= a.accept[i] == 0;
+      accepted |= a.accept[i] != 0;
+    }
+    rejected = __syncthreads_or(rejected);
+    accepted = __syncthreads_or(accepted);
+    if (rejected == 0) {  // uniform
       if (w < n_listed)
         listed_walk<G, Engine, NW, PD>(a, split, bh, lp,
                                        listed_first_block(a, bh, lp, Engine::tshift(a)), L);
+      return;
+    }
+    // Every head rejected (exact recovery: each attends all its valid
+    // pages): the identity partition, whose outputs a speculative dense
+    // decode of the lazy check (spec_state[1] == 2) already wrote with the
+    // same bits; then only its effective-budget counters are booked.  The
+    // next check of the layer is told to speculate that way again.
+    if (MODE == kModeVerified && accepted == 0) {  // uniform
+      const bool dense_done =
+          a.spec_state != nullptr && __builtin_amdgcn_readfirstlane(a.spec_state[1]) == 2;
+      if (w == 0 && threadIdx.x == 0 && a.spec_state != nullptr) a.spec_state[0] = 2;
+      if (dense_done) {
+        if (w == 0 && a.work != nullptr) {
+          for (int i = threadIdx.x; i < heads; i += NT) {
+            const int nv = valid_pages_sh(a.ctx_lens[i / a.H_kv], tl + ts);
+            add_work(a, max(0, min(nv, a.W)), nv);
+          }
+        }
+        return;
+      }
+      if (w >= a.n_splits_all * heads) return;
+      const int isplit = w % a.n_splits_all;
+      const int ibh = w / a.n_splits_all;
+      int ilp, iphys;
+      ident_first_pages<NW>(a, isplit, ibh, wave, lane, ts, ilp, iphys);
+      listed_walk<G, Engine, NW, PD, false, false, true>(a, isplit, ibh, ilp, iphys, L);
       return;
     }
   }

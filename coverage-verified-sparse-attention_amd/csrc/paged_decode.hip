@@ -46,6 +46,7 @@ struct DecodeLaunch {
   bool streamk;
   int grid_x, grid_y;
   int pps, n_splits;    // listed partition
+  int pps_all, n_splits_all;  // identity partition (verified launches: every head rejected)
   int sk_grid;          // stream-K partition (<= kMaxSplits workgroups)
   size_t partial_rows;  // rows of G x part_stride(D) fp32 (0: no workspace)
 };
@@ -89,6 +90,14 @@ static DecodeLaunch plan_launch(int B, int H_kv, int max_sel, int W, bool listed
     const int64_t n_listed = (int64_t)lp.grid_x * lp.grid_y;
     if (n_listed > p.grid_x) p.grid_x = (int)n_listed;
     if (lp.partial_rows > p.partial_rows) p.partial_rows = lp.partial_rows;
+    // ... and the identity partition, which they run when every head is
+    // rejected: the listed partition of a W-page list.
+    const DecodeLaunch ip = plan_launch(B, H_kv, W, W, true, false);
+    p.pps_all = ip.pps;
+    p.n_splits_all = ip.n_splits;
+    const int64_t n_ident = (int64_t)ip.grid_x * ip.grid_y;
+    if (n_ident > p.grid_x) p.grid_x = (int)n_ident;
+    if (ip.partial_rows > p.partial_rows) p.partial_rows = ip.partial_rows;
   }
   return p;
 }
@@ -188,6 +197,8 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   a.heads = B * H_kv;
   a.pps = p.pps << ts;
   a.n_splits = p.n_splits;
+  a.pps_all = p.pps_all << ts;
+  a.n_splits_all = p.n_splits_all;
   a.sk_grid = p.sk_grid;
   a.D = D;
   a.ts = ts;
@@ -590,6 +601,14 @@ int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_
   size_t need = 0;
   int rc = validate_decode(name, a, B, H_q, H_kv, D, block_size, W, true, false, p, need);
   if (rc != CVSA_OK) return rc;
+  // The speculative dense decode walks the identity partition (a listed
+  // walk of a W-page list), as a verified launch whose heads are all
+  // rejected does.
+  const DecodeLaunch ip = plan_launch(B, H_kv, W, W, true, false);
+  a.pps_all = ip.pps << a.ts;
+  a.n_splits_all = ip.n_splits;
+  const size_t need_ident = workspace_bytes_for(B, H_q, H_kv, D, W, W, true, false);
+  if (need_ident > need) need = need_ident;
   if ((rc = check_workspace(name, workspace, workspace_bytes, need)) != CVSA_OK) return rc;
   bind_workspace(a, workspace, need);
   const int G = H_q / H_kv;
@@ -613,7 +632,8 @@ int score_and_speculate(const uint16_t *q, int64_t q_stride_b, int64_t q_stride_
       a.ts == 0 ? (int64_t)((W + kSpecHeadPPW - 1) / kSpecHeadPPW) * H_kv
                 : (int64_t)(((W << a.ts) + kSpecScorePPW - 1) / kSpecScorePPW) * (H_kv / 4);
   const int score_gx = (int)((waves + kWavesPerWg - 1) / kWavesPerWg);
-  const int64_t grid = (int64_t)p.grid_x * p.grid_y + (int64_t)score_gx * B;
+  const int64_t n_dec = (int64_t)max(p.grid_x * p.grid_y, ip.grid_x * ip.grid_y);
+  const int64_t grid = n_dec + (int64_t)score_gx * B;
   hipStream_t st = (hipStream_t)stream;
   switch (G) {
 #define CVSA_SPEC_CASE(GG)                                                \

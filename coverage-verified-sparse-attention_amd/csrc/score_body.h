@@ -120,12 +120,12 @@ __device__ __forceinline__ void score_group_wave(const ScoreArgs &s, int hkv, in
 // four loads read the page, and PD pages are in flight.  Each token's dot
 // product is score_group_wave's (segment s in lane s of a 16-lane row, the
 // same DPP tree), so the scores have the same bits.  With `skip` and
-// s.skip_map, the pages the map marks are neither read nor written: their
-// loads are moved past the page and dropped by the buffer bounds check, a
-// choice the whole wave shares.
+// s.skip_map, the pages the map marks are neither read nor written, and so
+// are pages below `skip_below`: their loads are moved past the page and
+// dropped by the buffer bounds check, a choice the whole wave shares.
 template <int PPW, int PD>
 __device__ __forceinline__ void score_head_wave(const ScoreArgs &s, int hkv, int gw, int b,
-                                                bool skip) {
+                                                bool skip, int skip_below = 0) {
   constexpr int D = 128, LPR = 16, NL = kPageTokens / (kWave / LPR);  // 4 loads per page
   static_assert(PPW <= kWave, "a lane per page for the block ids");
   const int lane = threadIdx.x & 63;
@@ -148,6 +148,7 @@ __device__ __forceinline__ void score_head_wave(const ScoreArgs &s, int hkv, int
       if (id >= 0 && id < s.num_blocks) my_phys = id;
     }
     if (skip && s.skip_map != nullptr) mark = s.skip_map[rowi * s.skip_stride + p] != 0;
+    mark = mark || p < skip_below;
   }
   const uint64_t skipped = __ballot(mark);
   const uint4 qr = group_mean_q(s.q, s.q_sb, s.q_sh, b, h, s.G, seg, s.inv_g);

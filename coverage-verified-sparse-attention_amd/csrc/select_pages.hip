@@ -389,11 +389,12 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
     if (all_ok) {
       if (t == 0) {
         accept_out[bh] = 1;
-        // A kept selection whose speculative decode already ran (keep_flag[1]):
-        // the effective-budget counters of that decode's walk of this row
-        // (what the verified decode would book), so the verified decode after
-        // it has nothing left to do.
-        if (keep_work != nullptr && spec_ran != 0) {
+        // A kept selection whose speculative listed decode already ran
+        // (keep_flag[1] == 1; 2 is the dense speculation, whose outputs the
+        // verified decode replaces): the effective-budget counters of that
+        // decode's walk of this row (what the verified decode would book),
+        // so the verified decode after it has nothing left to do.
+        if (keep_work != nullptr && spec_ran == 1) {
           atomicAdd(&keep_work[0], (unsigned long long)min(max(n_row, 0), width));
           atomicAdd(&keep_work[1], (unsigned long long)max(0, n_valid_pages(ctx_row, block_size)));
         }

@@ -156,27 +156,32 @@ def _worst_pages(ps, budget, nph):
     return torch.where(cols < nph.unsqueeze(2), worst, torch.zeros_like(worst))
 
 
-@pytest.mark.parametrize("case", ["keep", "reselect", "reselect_passes"])
-@pytest.mark.parametrize("predict_keep", [1, 0])
+@pytest.mark.parametrize("case", ["keep", "reselect", "reselect_passes", "reject_all"])
+@pytest.mark.parametrize("predict_keep", [1, 0, 2])
 @pytest.mark.parametrize("shape", [(8, 4), (4, 7), (16, 2), (2, 4)])
 def test_speculative_check_every_prediction(gpu, case, predict_keep, shape):
     """A lazy check whose speculative decode is predicted right or wrong
     equals the separate kernels and a plan without speculation bit for bit:
-    output, selection, gate, counters.  "keep": tau 0, the check keeps its
-    selection; "reselect": tau 0.995, it reselects and the new gate rejects;
+    output, selection, gate, counters, page scores.  Predictions: 1 = keep
+    (listed decode of the cached selection), 2 = every head rejected (dense
+    decode over the identity partition, which also scores every valid
+    page), 0 = none.  "keep": tau 0, the check keeps its selection;
+    "reselect": tau 0.995, it reselects and the new gate rejects;
     "reselect_passes": the cached selection is every row's worst page and
     tau lies between its coverage and the fresh selection's, so the check
-    rejects every head and the new gate accepts every head.  spec_state
-    records whether the speculative decode ran and, afterwards, the check's
-    own decision.  Shapes (H_kv, G): the fused launch for H_kv 8, 4 and 16;
-    H_kv 2 runs the sequential chain and leaves spec_state as it was."""
+    rejects every head and the new gate accepts every head; "reject_all":
+    tau above 1, every gate rejects every head.  spec_state records which
+    speculative decode ran and, afterwards, the check's own decision (2 when
+    the new gate rejected every head).  Shapes (H_kv, G): the fused launch
+    for H_kv 8, 4 and 16; H_kv 2 runs the sequential chain and leaves
+    spec_state as it was."""
     H, G = shape
     inp, W, budget = _inputs(gpu, h=H, g=G)
     ctx, bt = inp.context_lens, inp.block_tables
     ps0 = ops.score_pages(jitter_query(inp.q, 0.5, 3), inp.k_cache, bt, ctx, H, G, 16)
     sel0, nph0 = ops.select_topk(ps0, budget, ctx, 16)
     q1 = jitter_query(inp.q, 0.5, 4)
-    tau = {"keep": 0.0, "reselect": 0.995}.get(case)
+    tau = {"keep": 0.0, "reselect": 0.995, "reject_all": 1.5}.get(case)
     if case == "reselect_passes":
         ps1 = ops.score_pages(q1, inp.k_cache, bt, ctx, H, G, 16)
         nph0 = torch.ones_like(nph0)
@@ -214,10 +219,12 @@ def test_speculative_check_every_prediction(gpu, case, predict_keep, shape):
         assert torch.equal(b["stats"], stats_r) and torch.equal(b["work"], work_r)
     keep = bool(chk.all())
     assert keep == (case == "keep")
-    assert bool(acc.all()) == (case != "reselect")
-    assert case != "reselect_passes" or not bool(chk.any())
+    assert bool(acc.all()) == (case not in ("reselect", "reject_all"))
+    assert case not in ("reselect_passes", "reject_all") or not bool(chk.any())
+    assert case != "reject_all" or not bool(acc.any())
     fused = H in (4, 8, 16)
-    assert plans[0].spec_state.tolist() == ([int(keep), predict_keep] if fused
+    decision = 1 if keep else (2 if not bool(acc.any()) else 0)
+    assert plans[0].spec_state.tolist() == ([decision, predict_keep] if fused
                                             else [predict_keep, 0])
     # the next check speculates on this one's decision: a reuse step between
     # them reads the (possibly reselected) selection and still matches
