@@ -550,7 +550,16 @@ enum {
  * speculate is predicted from the previous check of the same plan
  * (spec_state[0], written by the selection kernel); a wrong prediction costs
  * time, never results: the outputs, selections, masks and counters equal
- * those of the sequential chain bit for bit.  Plans whose gate scores are
+ * those of the sequential chain bit for bit.  spec_state[0] = 1 predicts a
+ * keep; 2 predicts that every head will be rejected (exact recovery then
+ * attends every valid page of every head): with a selection map the launch
+ * then decodes every valid page of every head in the identity partition
+ * (the listed partition of the page list 0, 1, 2, ...), scoring every page
+ * it walks from its keys, so the keys are read once, and a verified decode
+ * whose heads are all rejected (which uses that partition itself) only
+ * books the counters; the verified decode writes 2 when every head of its
+ * launch was rejected.  spec_state[1] records which speculative decode ran
+ * (0 none, 1 listed, 2 dense).  Plans whose gate scores are
  * Quest scores (CVSA_SELECT_QUEST_LN), whose H_kv is 1 or 2 or whose D is
  * not 128 run the sequential chain and leave spec_state unchanged.
  * With a selection map (sel_map; 16-token pages) the speculative decode
