@@ -575,7 +575,9 @@ def main():
 
     per_tau = {}
     for tau in cfg["taus"]:
-        per_tau[tau] = run_schedule(cfg, layers, tau, args, dev)
+        # The per-kind traffic was profiled on the default data calibration.
+        per_tau[tau] = run_schedule(cfg, layers, tau, args, dev,
+                                    count_read=args.hot_shift is None and args.sink_shift is None)
     tau0 = 0.9 if 0.9 in per_tau else cfg["taus"][0]
     res = per_tau[tau0]
     W, budget = res["W"], res["budget"]

@@ -133,9 +133,10 @@ __device__ __forceinline__ void score_head_wave(const ScoreArgs &s, int hkv, int
   const int p_begin = (gw / hkv) * PPW;
   const int W = s.W;
   if (p_begin >= W) return;
+  const int n = min(PPW, W - p_begin);
+  if (p_begin + n <= skip_below) return;  // every page of the wave is scored elsewhere
   const int seg = lane % LPR, row = lane / LPR;
   const int ctx = __builtin_amdgcn_readfirstlane(s.context_lens[b]);
-  const int n = min(PPW, W - p_begin);
   const int64_t rowi = (int64_t)b * hkv + h;
   // Page j of this wave: block id in lane j (-1 when the page holds no valid
   // token or its id is outside the pool), skip flag in bit j of `skipped`.
