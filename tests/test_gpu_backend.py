@@ -487,6 +487,40 @@ def test_baseline_configuration_full_size(gpu, name):
     print(f"{name}: {lock.summary()}")
 
 
+def test_dense_speculation_literal_cfg3_full_size(gpu):
+    """The literal cfg3 recipe at full size (128K context) over 16 steps:
+    the first check rejects every head, so the checks after it speculate a
+    dense decode (spec_state [2, 2] after each) and their verified launches
+    only book counters.  Selections, masks, outputs and statistics in
+    lockstep with the oracle backend at every step."""
+    cfg, budget, seed, kw = FULL_SIZE["cfg3_recipe"]
+    stats, trace, lock = _run(gpu, cfg, dict(kw, budget_pct=budget), steps=16,
+                              seed=seed + 5, gen_on_gpu=True)
+    kinds = [t["kind"] for t in trace]
+    assert sum(k.startswith("score") for k in kinds) == 4, kinds  # fresh + three checks
+    assert all(not bool(t["accept"].any()) for t in trace if "accept" in t), kinds
+    plan = lock.gpu_b._step_plans[0]
+    assert plan.spec_state is not None and plan.spec_state.tolist() == [2, 2]
+    print(lock.summary())
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_dense_speculation_ragged_batch(gpu, seed):
+    """Ragged contexts (B = 3), tau 0.999 so every gate rejects every head,
+    lazy M = 3 over 14 steps with appends crossing pages: the checks after
+    the first speculate a dense decode over the identity partition of each
+    sequence's own context; in lockstep with the oracle backend."""
+    cfg = dict(batch=3, num_q_heads=32, num_kv_heads=8, head_dim=128,
+               context_len=[3001 + 97 * seed, 777, 5000 - 13 * seed], hot_heads=[0, 3],
+               n_hot=4, hot_shift=8.0)
+    kw = dict(budget_pct=0.125, coverage_threshold=0.999, lazy=True, check_interval=3)
+    stats, trace, lock = _run(gpu, cfg, kw, steps=14, seed=950 + seed)
+    assert all(not bool(t["accept"].any()) for t in trace if "accept" in t)
+    plan = lock.gpu_b._step_plans[0]
+    assert plan.spec_state is not None and plan.spec_state.tolist() == [2, 2]
+    print(lock.summary())
+
+
 @pytest.mark.parametrize("kw", [
     dict(selector="quest"),
     dict(selector="quest", light_normalizer=True),
