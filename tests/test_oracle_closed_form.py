@@ -3,7 +3,8 @@
 Brute force on tiny inputs, closed forms (all pages selected = textbook
 softmax attention), invariants (draft + complement = dense, coverage = 1 for
 a full selection) and the rounding rule of the bf16 group mean, at head
-dimensions 64, 128, 256 and block sizes 16, 32, 64 where they depend on them.  A few tests
+dimensions 32, 64, 128, 256 and block sizes 8, 16, 32, 64, 128 where they
+depend on them.  A few tests
 plant a plausible mistake in a copy of the oracle and show the checks fail.
 """
 import math
@@ -17,7 +18,7 @@ from cvsa.synthetic import make_paged_inputs
 
 # (head dimension, block size): the kernels' geometries.  Contexts scale with
 # the block size so that every geometry has full, partial and missing pages.
-GEOMETRIES = [(128, 16), (64, 32), (256, 64)]
+GEOMETRIES = [(128, 16), (64, 32), (256, 64), (32, 8), (128, 128)]
 
 
 def _tiny(seed=0, B=2, H_q=8, H_kv=2, ctx=(70, 33), W=6, D=128, bs=16):
@@ -211,7 +212,7 @@ def test_empty_selection_contract():
     assert bool(torch.isinf(m).all()) and bool((m < 0).all())
 
 
-@pytest.mark.parametrize("bs", [16, 32, 64])
+@pytest.mark.parametrize("bs", [8, 16, 32, 64, 128])
 def test_append_token_allocation_rule(bs):
     """kv_cache.py:133-150: a block is taken only at offset 0 of a new page."""
     K = torch.zeros(8, bs, 1, 4)
