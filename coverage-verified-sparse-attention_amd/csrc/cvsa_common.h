@@ -42,7 +42,11 @@ __host__ __device__ constexpr int page_tile_shift(int block_size) {
 __host__ __device__ constexpr int tile_rows_log2(int block_size) {
   return block_size == 8 ? 3 : 4;
 }
+// Pages per row: the register-resident select and coverage kernels hold
+// rows of up to kMaxPages; wider rows, up to kMaxPagesWide pages, stream
+// from memory (select_topk_wide_kernel, check_coverage_wide_kernel).
 constexpr int kMaxPages = 32768;
+constexpr int kMaxPagesWide = 1 << 18;
 
 // ---------------------------------------------------------------- numerics
 

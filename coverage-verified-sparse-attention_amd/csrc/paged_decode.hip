@@ -148,8 +148,8 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   const int ts = page_tile_shift(block_size);
   CVSA_REQUIRE(a.num_blocks <= (INT32_MAX >> ts), CVSA_ERR_UNSUPPORTED,
                "%s: %lld blocks exceed the tile index range", name, (long long)a.num_blocks);
-  CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
-               kMaxPages);
+  CVSA_REQUIRE(W <= kMaxPagesWide, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name,
+               W, kMaxPagesWide);
   CVSA_REQUIRE(a.bt_sb >= W, CVSA_ERR_INVALID, "%s: block-table row stride %lld < W=%d",
                name, (long long)a.bt_sb, W);
   CVSA_REQUIRE(((uintptr_t)a.q & 15) == 0 && a.q_sb % 8 == 0 && a.q_sh % 8 == 0 &&
@@ -161,7 +161,7 @@ static int validate_decode(const char *name, DecodeArgs &a, int B, int H_q, int 
   if (listed) {
     CVSA_REQUIRE(a.page_idx && a.n_pages, CVSA_ERR_INVALID,
                  "%s: page_indices / n_per_head missing", name);
-    CVSA_REQUIRE(a.max_sel >= 0 && a.max_sel <= kMaxPages && a.idx_stride >= a.max_sel,
+    CVSA_REQUIRE(a.max_sel >= 0 && a.max_sel <= kMaxPagesWide && a.idx_stride >= a.max_sel,
                  CVSA_ERR_INVALID, "%s: bad selection width %d (row stride %lld)", name,
                  a.max_sel, (long long)a.idx_stride);
   }

@@ -200,8 +200,8 @@ int check_quest_sizes(const char *name, int32_t B, int32_t H_kv, int32_t D, int3
   CVSA_REQUIRE(head_dim_supported(D) && block_size_supported(block_size), CVSA_ERR_UNSUPPORTED,
                "%s: D=%d not in {32, 64, 128, 256} or block_size=%d not in {8, 16, 32, 64, 128}", name, D,
                block_size);
-  CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
-               kMaxPages);
+  CVSA_REQUIRE(W <= kMaxPagesWide, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name,
+               W, kMaxPagesWide);
   CVSA_REQUIRE(bt_stride_b >= W, CVSA_ERR_INVALID, "%s: block-table row stride %lld < W=%d",
                name, (long long)bt_stride_b, W);
   CVSA_REQUIRE(((uintptr_t)meta & 15) == 0, CVSA_ERR_INVALID, "%s: meta must be 16-byte aligned",

@@ -22,7 +22,7 @@ __global__ __launch_bounds__(kCompThreads) void complement_kernel(
     const int32_t *__restrict__ n_per_head, const int32_t *__restrict__ context_lens,
     int block_size, const uint8_t *__restrict__ accept, int H_kv, int width,
     int32_t *__restrict__ comp, int32_t *__restrict__ n_comp) {
-  __shared__ uint32_t bitmap[kMaxPages / 32];
+  __shared__ uint32_t bitmap[kMaxPagesWide / 32];
   __shared__ uint32_t wsum[kCompThreads / kWave];
   const int bh = blockIdx.x;
   const int b = bh / H_kv;
@@ -120,10 +120,10 @@ extern "C" int cvsa_compute_complement(const int32_t *page_indices, int64_t idx_
   CVSA_REQUIRE(B > 0 && H_kv > 0 && block_size > 0 && width > 0 && idx_stride >= 0,
                CVSA_ERR_INVALID, "compute_complement: bad sizes B=%d H_kv=%d width=%d", B,
                H_kv, width);
-  CVSA_REQUIRE(width <= kMaxPages, CVSA_ERR_UNSUPPORTED,
-               "compute_complement: width=%d exceeds %d pages", width, kMaxPages);
+  CVSA_REQUIRE(width <= kMaxPagesWide, CVSA_ERR_UNSUPPORTED,
+               "compute_complement: width=%d exceeds %d pages", width, kMaxPagesWide);
   // Selection rows are idx_stride wide; all of a row is candidate selection.
-  const int sel_width = (int)(idx_stride > kMaxPages ? kMaxPages : idx_stride);
+  const int sel_width = (int)(idx_stride > kMaxPagesWide ? kMaxPagesWide : idx_stride);
   hipLaunchKernelGGL(complement_kernel, dim3(B * H_kv), dim3(kCompThreads), 0,
                      (hipStream_t)stream, page_indices, idx_stride, sel_width, n_per_head,
                      context_lens, block_size, accept, H_kv, width, comp_indices, n_comp);

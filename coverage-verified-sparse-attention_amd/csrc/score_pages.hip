@@ -210,8 +210,8 @@ extern "C" int cvsa_score_pages(const uint16_t *q, int64_t q_stride_b,
   const int ts = page_tile_shift(block_size);
   CVSA_REQUIRE(num_blocks <= (INT32_MAX >> ts), CVSA_ERR_UNSUPPORTED,
                "score_pages: %lld blocks exceed the tile index range", (long long)num_blocks);
-  CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED,
-               "score_pages: W=%d exceeds %d pages", W, kMaxPages);
+  CVSA_REQUIRE(W <= kMaxPagesWide, CVSA_ERR_UNSUPPORTED,
+               "score_pages: W=%d exceeds %d pages", W, kMaxPagesWide);
   CVSA_REQUIRE(bt_stride_b >= W, CVSA_ERR_INVALID,
                "score_pages: block-table row stride %lld < W=%d",
                (long long)bt_stride_b, W);

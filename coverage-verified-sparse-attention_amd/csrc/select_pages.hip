@@ -213,6 +213,50 @@ __device__ __forceinline__ void block_sum2(float &a, float &b, float (*red)[2]) 
   }
 }
 
+// One pass of the MSB radix select: hist_c holds kHistCopies copies of the
+// histogram of the pass's 8-bit digit over the keys still in the running
+// (behind an LDS barrier); returns the digit holding the krem-th largest of
+// them and krem minus the number of those keys with a higher digit.  Ends
+// with the histograms free for the next pass.
+__device__ __forceinline__ void radix_digit(const uint32_t *hist_c, uint32_t *hist,
+                                            uint32_t krem, uint32_t *s_digit, uint32_t *s_krem,
+                                            uint32_t &digit, uint32_t &krem_out) {
+  const int t = threadIdx.x, lane = t & 63;
+  if (t < 256) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int j = 0; j < kHistCopies; ++j) c += hist_c[j * kHistStride + t];
+    hist[t] = c;
+  }
+  lds_barrier();
+  if (t < 64) {
+    // Lane l holds digits 4l..4l+3; count the candidates above each digit.
+    const uint32_t c0 = hist[4 * lane], c1 = hist[4 * lane + 1];
+    const uint32_t c2 = hist[4 * lane + 2], c3 = hist[4 * lane + 3];
+    const uint32_t local = c0 + c1 + c2 + c3;
+    uint32_t suffix = local;  // inclusive sum over lanes >= l
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = __shfl_down(suffix, off, 64);
+      if (lane + off < 64) suffix += o;
+    }
+    uint32_t above = suffix - local;  // candidates with a higher digit
+    const uint32_t cs[4] = {c3, c2, c1, c0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (above < krem && above + cs[j] >= krem) {
+        *s_digit = (uint32_t)(4 * lane + 3 - j);
+        *s_krem = krem - above;
+      }
+      above += cs[j];
+    }
+  }
+  lds_barrier();
+  digit = *s_digit;
+  krem_out = *s_krem;
+  lds_barrier();
+}
+
 // 4-pass, 8-bit MSB radix select of the k-th largest key among the keys
 // with alive(r) set: returns that key T and k - #(alive keys > T), the
 // number of keys equal to T that the selection takes.  Every lane adds
@@ -239,110 +283,28 @@ __device__ __forceinline__ void radix_select(const float (&val)[R], Alive alive,
       if (alive(r) && (key & pmask) == prefix) atomicAdd(&my_hist[(key >> shift) & 255u], 1u);
     }
     lds_barrier();
-    if (t < 256) {
-      uint32_t c = 0;
-#pragma unroll
-      for (int j = 0; j < kHistCopies; ++j) c += hist_c[j * kHistStride + t];
-      hist[t] = c;
-    }
-    lds_barrier();
-    if (t < 64) {
-      // Lane l holds digits 4l..4l+3; count the candidates above each digit.
-      const uint32_t c0 = hist[4 * lane], c1 = hist[4 * lane + 1];
-      const uint32_t c2 = hist[4 * lane + 2], c3 = hist[4 * lane + 3];
-      const uint32_t local = c0 + c1 + c2 + c3;
-      uint32_t suffix = local;  // inclusive sum over lanes >= l
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t o = __shfl_down(suffix, off, 64);
-        if (lane + off < 64) suffix += o;
-      }
-      uint32_t above = suffix - local;  // candidates with a higher digit
-      const uint32_t cs[4] = {c3, c2, c1, c0};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (above < krem && above + cs[j] >= krem) {
-          *s_digit = (uint32_t)(4 * lane + 3 - j);
-          *s_krem = krem - above;
-        }
-        above += cs[j];
-      }
-    }
-    lds_barrier();
-    prefix |= *s_digit << shift;
+    uint32_t digit;
+    radix_digit(hist_c, hist, krem, s_digit, s_krem, digit, krem);
+    prefix |= digit << shift;
     pmask |= 0xFFu << shift;
-    krem = *s_krem;
-    lds_barrier();
   }
   T = prefix;
 }
 
-// Row budgets (MODE): kUniform, the same `budget` for every row;
-// kTopP, the smallest prefix of the row's pages by score whose softmax mass
-// reaches top_p (CVSABackend._topp_select, backend.py:652-681), at least 3;
-// kTable, row_budgets[b * H_kv + h] (_static_select, :622-650, and the
-// budgets of _adaptive_select, :522-570).  `width` is the row stride of
-// page_indices: k is clamped to it.
-enum { kUniform = 0, kTopP = 1, kTable = 2 };
-static_assert(kHistCopies * kHistStride >= kBuckets, "hist_c holds a second-level histogram");
-
-// SEP: the selection ranks sel_scores while the coverage gate (and
-// scores_cache) use scores (CVSABackend._scoring_step, backend.py:723-727:
-// the Quest selector proposes, the exact scan verifies).
-template <int R, bool SEP, int MODE>
-__global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
-    const float *__restrict__ scores, const float *__restrict__ sel_scores, int W, int H_kv,
-    const int32_t *__restrict__ context_lens, int block_size, int budget, int width,
-    float top_p, const int32_t *__restrict__ row_budgets,
-    int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
-    uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
-    const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
+// The lazy coverage check decided on the device (CVSABackend._lazy_step,
+// cvsa/backend.py:420-465), shared by the select kernels: when every head of
+// the layer kept its coverage on the cached selection (check_accept), that
+// selection stays and all heads are accepted (returns true: the workgroup
+// has nothing left to do); otherwise a fresh selection replaces it in place.
+// Counters: stats[0] accept-all checks, [1] rejections, [2] scoring steps,
+// [3] heads that passed the check.  All barriers here order LDS only.
+__device__ __forceinline__ bool lazy_decision(
+    const uint8_t *__restrict__ check_accept, int n_heads, int bh, int b, int width,
+    int block_size, const int32_t *__restrict__ n_per_head,
+    const int32_t *__restrict__ context_lens, uint8_t *__restrict__ accept_out,
     long long *__restrict__ stats, int count_gate, int32_t *__restrict__ keep_flag,
-    uint8_t *__restrict__ sel_map, int64_t map_stride,
-    unsigned long long *__restrict__ keep_work, int exp_budget,
-    int32_t *__restrict__ exp_indices) {
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t hist_c[kHistCopies * kHistStride];
-  __shared__ uint32_t hist_b[kBuckets];
-  __shared__ uint32_t s_cand[kRankCands];
-  __shared__ uint32_t wsum[kSelWaves];
-  __shared__ uint32_t red_rng[kSelWaves][3];
-  __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2], red_s3[kSelWaves][3];
-  __shared__ float red_s1[kSelWaves];
-  __shared__ uint32_t s_digit, s_krem, s_T, s_bucket, s_kb, s_nb, s_ncand;
-  __shared__ int s_nok, s_nbad, s_acc;
-  // Top-p only: softmax mass per value bucket (64-bit fixed point, so the
-  // sums do not depend on the order of the atomic adds).
-  __shared__ unsigned long long mass_b[MODE == kTopP ? kBuckets : 1];
-  __shared__ unsigned long long s_candm[MODE == kTopP ? kRankCands : 1];
-  __shared__ uint32_t s_candi[MODE == kTopP ? kRankCands : 1];
-  __shared__ unsigned long long wsum64[MODE == kTopP ? kSelWaves : 1];
-  __shared__ unsigned long long s_mass;
-
-  const int bh = blockIdx.x;
-  const int b = bh / H_kv;
+    unsigned long long *__restrict__ keep_work, int &s_nok, int &s_nbad) {
   const int t = threadIdx.x;
-  const float *row = (SEP ? sel_scores : scores) + (int64_t)bh * W;
-  const int i0 = t * R;
-  // 16-byte loads when W % 4 == 0 (row starts are then 16-byte aligned and
-  // each group of 4 lies wholly inside or outside the row).  The choice is
-  // uniform and the loads are unconditional (clamped into the row, values
-  // past it replaced by -inf): per-lane branches around loads would make the
-  // compiler wait for all of them at the first later use of any.
-  const bool vec = R >= 4 && (W & 3) == 0;
-
-  // Lazy coverage check decided on the device (CVSABackend._lazy_step,
-  // cvsa/backend.py:420-465): when every head of the layer kept its
-  // coverage on the cached selection, that selection stays and all heads
-  // are accepted; otherwise a fresh selection replaces it in place.
-  // Counters: stats[0] accept-all checks, [1] rejections, [2] scoring
-  // steps, [3] heads that passed the check.  The scores are requested only
-  // once a reselection is certain: a wave cannot retire before its loads
-  // return, so loads issued ahead would hold up the (common) keep path.
-  // All barriers below order LDS only: loads stay in flight across them and
-  // stores issued before them are not waited for.  (Scalar loads count
-  // with LDS operations, so even a context-length load here would hold up
-  // the check's barriers.)
   if (check_accept != nullptr) {
     // A kept speculation's booking (below) needs these: requested with the
     // flags, in the same round trip.
@@ -399,12 +361,80 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
           atomicAdd(&keep_work[1], (unsigned long long)max(0, n_valid_pages(ctx_row, block_size)));
         }
       }
-      return;
+      return true;
     }
   } else if (stats != nullptr && !count_gate && bh == 0 && t == 0) {
     stat_add(&stats[1], 1);  // a lazy scoring step without a cached selection
     stat_add(&stats[2], 1);
   }
+  return false;
+}
+
+// Row budgets (MODE): kUniform, the same `budget` for every row;
+// kTopP, the smallest prefix of the row's pages by score whose softmax mass
+// reaches top_p (CVSABackend._topp_select, backend.py:652-681), at least 3;
+// kTable, row_budgets[b * H_kv + h] (_static_select, :622-650, and the
+// budgets of _adaptive_select, :522-570).  `width` is the row stride of
+// page_indices: k is clamped to it.
+enum { kUniform = 0, kTopP = 1, kTable = 2 };
+static_assert(kHistCopies * kHistStride >= kBuckets, "hist_c holds a second-level histogram");
+
+// SEP: the selection ranks sel_scores while the coverage gate (and
+// scores_cache) use scores (CVSABackend._scoring_step, backend.py:723-727:
+// the Quest selector proposes, the exact scan verifies).
+template <int R, bool SEP, int MODE>
+__global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
+    const float *__restrict__ scores, const float *__restrict__ sel_scores, int W, int H_kv,
+    const int32_t *__restrict__ context_lens, int block_size, int budget, int width,
+    float top_p, const int32_t *__restrict__ row_budgets,
+    int32_t *__restrict__ page_indices, int32_t *__restrict__ n_per_head, float tau,
+    uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out,
+    const uint8_t *__restrict__ check_accept, int n_heads, float *__restrict__ scores_cache,
+    long long *__restrict__ stats, int count_gate, int32_t *__restrict__ keep_flag,
+    uint8_t *__restrict__ sel_map, int64_t map_stride,
+    unsigned long long *__restrict__ keep_work, int exp_budget,
+    int32_t *__restrict__ exp_indices) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist_c[kHistCopies * kHistStride];
+  __shared__ uint32_t hist_b[kBuckets];
+  __shared__ uint32_t s_cand[kRankCands];
+  __shared__ uint32_t wsum[kSelWaves];
+  __shared__ uint32_t red_rng[kSelWaves][3];
+  __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2], red_s3[kSelWaves][3];
+  __shared__ float red_s1[kSelWaves];
+  __shared__ uint32_t s_digit, s_krem, s_T, s_bucket, s_kb, s_nb, s_ncand;
+  __shared__ int s_nok, s_nbad, s_acc;
+  // Top-p only: softmax mass per value bucket (64-bit fixed point, so the
+  // sums do not depend on the order of the atomic adds).
+  __shared__ unsigned long long mass_b[MODE == kTopP ? kBuckets : 1];
+  __shared__ unsigned long long s_candm[MODE == kTopP ? kRankCands : 1];
+  __shared__ uint32_t s_candi[MODE == kTopP ? kRankCands : 1];
+  __shared__ unsigned long long wsum64[MODE == kTopP ? kSelWaves : 1];
+  __shared__ unsigned long long s_mass;
+
+  const int bh = blockIdx.x;
+  const int b = bh / H_kv;
+  const int t = threadIdx.x;
+  const float *row = (SEP ? sel_scores : scores) + (int64_t)bh * W;
+  const int i0 = t * R;
+  // 16-byte loads when W % 4 == 0 (row starts are then 16-byte aligned and
+  // each group of 4 lies wholly inside or outside the row).  The choice is
+  // uniform and the loads are unconditional (clamped into the row, values
+  // past it replaced by -inf): per-lane branches around loads would make the
+  // compiler wait for all of them at the first later use of any.
+  const bool vec = R >= 4 && (W & 3) == 0;
+
+  // The lazy check's keep decision (lazy_decision).  The scores are
+  // requested only once a reselection is certain: a wave cannot retire
+  // before its loads return, so loads issued ahead would hold up the
+  // (common) keep path.
+  // All barriers below order LDS only: loads stay in flight across them and
+  // stores issued before them are not waited for.  (Scalar loads count
+  // with LDS operations, so even a context-length load here would hold up
+  // the check's barriers.)
+  if (lazy_decision(check_accept, n_heads, bh, b, width, block_size, n_per_head, context_lens,
+                    accept_out, stats, count_gate, keep_flag, keep_work, s_nok, s_nbad))
+    return;
 
   const int ctx = context_lens[b];
   auto load_row = [&](const float *src, float (&dst)[R]) {
@@ -911,6 +941,226 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
   }
 }
 
+// Rows wider than the register-resident kernel holds (W > kMaxPages, up to
+// kMaxPagesWide pages): the same selection and gate (uniform or per-row
+// table budgets), streaming the row from memory.  The k-th largest key T
+// and krem come from the 4-pass 8-bit MSB radix select over the row's
+// order keys (the register kernel's bucket step finds the same T and krem
+// faster; here each pass reads the row), the ascending compaction walks
+// the row in tiles of kWideTile pages (a block scan per tile, running
+// counts between tiles), and the gate's two log-sum-exps take a pass of
+// their own once the counted pages are known (a bit per page in LDS).
+// Same outputs as select_topk_kernel: selection, n_per_head, selection
+// map, scores cache, coverage and accept, the lazy check's decision and
+// counters, and the expanded selection of approximate recovery.
+constexpr int kWidePerThread = 8;
+constexpr int kWideTile = kSelThreads * kWidePerThread;
+
+// The k-th largest key T of a row of W scores in memory and krem = k -
+// #(keys > T), as radix_select.
+__device__ __forceinline__ void wide_threshold(const float *__restrict__ row, int W, uint32_t k,
+                                               uint32_t *hist, uint32_t *hist_c,
+                                               uint32_t *s_digit, uint32_t *s_krem,
+                                               uint32_t &T, uint32_t &krem) {
+  const int t = threadIdx.x, lane = t & 63;
+  uint32_t prefix = 0, pmask = 0;
+  krem = k;
+#pragma unroll 1
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int i = t; i < kHistCopies * kHistStride; i += kSelThreads) hist_c[i] = 0;
+    lds_barrier();
+    uint32_t *my_hist = hist_c + (lane % kHistCopies) * kHistStride;
+    for (int i0 = t * 4; i0 < W; i0 += kSelThreads * 4) {
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = row[min(i0 + e, W - 1)];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t key = order_key(v[e]);
+        if (i0 + e < W && (key & pmask) == prefix)
+          atomicAdd(&my_hist[(key >> shift) & 255u], 1u);
+      }
+    }
+    lds_barrier();
+    uint32_t digit;
+    radix_digit(hist_c, hist, krem, s_digit, s_krem, digit, krem);
+    prefix |= digit << shift;
+    pmask |= 0xFFu << shift;
+  }
+  T = prefix;
+}
+
+template <bool SEP, int MODE>
+__global__ __launch_bounds__(kSelThreads) void select_topk_wide_kernel(
+    const float *__restrict__ scores, const float *__restrict__ sel_scores, int W, int H_kv,
+    const int32_t *__restrict__ context_lens, int block_size, int budget, int width,
+    const int32_t *__restrict__ row_budgets, int32_t *__restrict__ page_indices,
+    int32_t *__restrict__ n_per_head, float tau, uint8_t *__restrict__ accept_out,
+    float *__restrict__ coverage_out, const uint8_t *__restrict__ check_accept, int n_heads,
+    float *__restrict__ scores_cache, long long *__restrict__ stats, int count_gate,
+    int32_t *__restrict__ keep_flag, uint8_t *__restrict__ sel_map, int64_t map_stride,
+    unsigned long long *__restrict__ keep_work, int exp_budget,
+    int32_t *__restrict__ exp_indices) {
+  static_assert(MODE == kUniform || MODE == kTable, "wide rows: uniform or table budgets");
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist_c[kHistCopies * kHistStride];
+  __shared__ uint32_t wsum[kSelWaves];
+  __shared__ uint32_t s_digit, s_krem;
+  __shared__ uint32_t s_bits[kMaxPagesWide / 32];  // the counted pages
+  __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2];
+  __shared__ int s_nok, s_nbad, s_acc;
+
+  const int bh = blockIdx.x;
+  const int b = bh / H_kv;
+  const int t = threadIdx.x;
+  const float *row = (SEP ? sel_scores : scores) + (int64_t)bh * W;
+  const float *grow = scores + (int64_t)bh * W;
+  if (lazy_decision(check_accept, n_heads, bh, b, width, block_size, n_per_head, context_lens,
+                    accept_out, stats, count_gate, keep_flag, keep_work, s_nok, s_nbad))
+    return;
+  const int ctx = context_lens[b];
+  int k = budget;
+  if constexpr (MODE == kTable) k = min(max(row_budgets[bh], 1), W);
+  k = min(k, width);
+
+  // Ascending compaction of the selection (T, krem) into out_row (its first
+  // n_write entries; ties at T go to the lowest pages), tile by tile.  With
+  // `main`, also the counted bits, the selection map, the scores cache and
+  // the gate maxima (every page, counted pages).
+  float mx = -INFINITY, ms = -INFINITY;
+  const auto compact = [&](uint32_t T, uint32_t krem, int n_write, int n_sel, int32_t *out_row,
+                           bool main) __attribute__((always_inline)) {
+    uint32_t gt_run = 0, eq_run = 0;  // keys > T and == T in the tiles before
+    for (int base = 0; base < W; base += kWideTile) {
+      const int p0 = base + t * kWidePerThread;
+      float v[kWidePerThread], g[kWidePerThread];
+#pragma unroll
+      for (int e = 0; e < kWidePerThread; ++e) v[e] = row[min(p0 + e, W - 1)];
+      if (SEP && main) {
+#pragma unroll
+        for (int e = 0; e < kWidePerThread; ++e) g[e] = grow[min(p0 + e, W - 1)];
+      } else {
+#pragma unroll
+        for (int e = 0; e < kWidePerThread; ++e) g[e] = v[e];
+      }
+      uint32_t gt = 0, eq = 0;
+#pragma unroll
+      for (int e = 0; e < kWidePerThread; ++e) {
+        if (p0 + e < W) {
+          const uint32_t key = order_key(v[e]);
+          gt += key > T;
+          eq += key == T;
+        }
+      }
+      uint32_t total;
+      const uint32_t excl = block_exclusive_scan(gt | (eq << 16), wsum, total);
+      uint32_t eq_seen = eq_run + (excl >> 16);
+      uint32_t pos = gt_run + (excl & 0xFFFFu) + min(eq_seen, krem);
+      uint32_t bits = 0;
+#pragma unroll
+      for (int e = 0; e < kWidePerThread; ++e) {
+        bool sel = false;
+        if (p0 + e < W) {
+          const uint32_t key = order_key(v[e]);
+          if (key > T) {
+            sel = true;
+          } else if (key == T) {
+            sel = eq_seen < krem;
+            ++eq_seen;
+          }
+        }
+        const bool counted = sel && (int)pos < n_sel;
+        bits |= counted ? 1u << e : 0u;
+        if (sel) {
+          if ((int)pos < n_write) out_row[pos] = p0 + e;
+          ++pos;
+        }
+        if (main && p0 + e < W) {
+          mx = fmaxf(mx, g[e]);
+          if (counted) ms = fmaxf(ms, g[e]);
+        }
+      }
+      if (main && p0 < W) {
+        atomicOr(&s_bits[p0 >> 5], bits << (p0 & 31));
+        if (sel_map != nullptr) {
+          uint8_t *m = sel_map + (int64_t)bh * map_stride + p0;
+#pragma unroll
+          for (int e = 0; e < kWidePerThread; ++e)
+            if (p0 + e < W) m[e] = (bits >> e) & 1u;
+        }
+        if (scores_cache != nullptr) {
+          float *dst = scores_cache + (int64_t)bh * W + p0;
+#pragma unroll
+          for (int e = 0; e < kWidePerThread; ++e)
+            if (p0 + e < W) dst[e] = g[e];
+        }
+      }
+      gt_run += total & 0xFFFFu;
+      eq_run += total >> 16;
+    }
+  };
+
+  for (int i = t; i < (W + 31) / 32; i += kSelThreads) s_bits[i] = 0u;
+  uint32_t T = 0, krem = 0;
+  wide_threshold(row, W, (uint32_t)k, hist, hist_c, &s_digit, &s_krem, T, krem);
+  const int n_sel = min(k, n_valid_pages(ctx, block_size));
+  compact(T, krem, k, n_sel, page_indices + (int64_t)bh * width, true);
+  if (t == 0) n_per_head[bh] = n_sel;
+  if (accept_out == nullptr) return;
+
+  // ---- coverage of the new selection (the register kernel's rules)
+  block_max2(mx, ms, red_max);  // also orders the counted bits before their reads
+  const float m_all = fmaxf(mx, -1e20f);
+  int msel_block = 1;
+  while (msel_block < width) msel_block <<= 1;
+  const float m_sel = n_sel < msel_block ? fmaxf(ms, -1e20f) : ms;
+  float se = 0.f, ss = 0.f;
+  for (int p = t; p < W; p += kSelThreads) {
+    const float g = grow[p];
+    se += fast_exp(g - m_all);
+    if ((s_bits[p >> 5] >> (p & 31)) & 1u) ss += fast_exp(g - m_sel);
+  }
+  block_sum2(se, ss, red_sum);
+  if (t == 0) {
+    const float cov = expf(lse_from(m_sel, ss) - lse_from(m_all, se));
+    const int acc = cov >= tau ? 1 : 0;
+    coverage_out[bh] = cov;
+    accept_out[bh] = (uint8_t)acc;
+    s_acc = acc;
+    if (stats != nullptr && count_gate) {
+      // As in select_topk_kernel: the last head of a fixed-interval scoring
+      // step books it (the same gfx950 ordering of agent-scope atomics).
+      __hip_atomic_fetch_add(&stats[3], (long long)acc, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(&stats[4], (long long)(1 - acc), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      const long long done = __hip_atomic_fetch_add(&stats[5], 1LL, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+      if (done == (long long)n_heads - 1) {
+        const long long rej = __hip_atomic_fetch_add(&stats[4], 0LL, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        stats[0] += rej == 0 ? 1 : 0;
+        stats[1] += rej != 0 ? 1 : 0;
+        stats[2] += 1;
+        __hip_atomic_store(&stats[4], 0LL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&stats[5], 0LL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  // Approximate recovery: a rejected row's expanded selection.
+  if constexpr (MODE == kUniform) {
+    if (exp_indices == nullptr) return;  // uniform
+    lds_barrier();
+    if (s_acc != 0) return;  // uniform
+    const int k2 = min(exp_budget, W);
+    uint32_t T2 = 0, krem2 = 0;
+    wide_threshold(row, W, (uint32_t)k2, hist, hist_c, &s_digit, &s_krem, T2, krem2);
+    compact(T2, krem2, k2, k2, exp_indices + (int64_t)bh * exp_budget, false);
+  }
+}
+
 // Budgets of CVSABackend._adaptive_select (cvsa/backend.py:522-570): the
 // kv-heads of sequence b compete for K = H_kv * base slots.  raw[h] counts
 // head h's scores among the K largest of all H_kv * W scores of b (ties at
@@ -1104,6 +1354,41 @@ __global__ __launch_bounds__(kSelThreads) void check_coverage_kernel(
   }
 }
 
+// check_coverage_kernel for rows wider than it holds in registers (W or
+// the selection width above kMaxPages): the same two log-sum-exps and
+// rules, streaming the row and gathering the selected scores from memory.
+__global__ __launch_bounds__(kSelThreads) void check_coverage_wide_kernel(
+    const float *__restrict__ scores, int W, const int32_t *__restrict__ selected,
+    int sel_width, int sel_block, const int32_t *__restrict__ n_per_head,
+    float tau, uint8_t *__restrict__ accept_out, float *__restrict__ coverage_out) {
+  __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2];
+  const int bh = blockIdx.x;
+  const int t = threadIdx.x;
+  const float *row = scores + (int64_t)bh * W;
+  const int32_t *sel = selected + (int64_t)bh * sel_width;
+  const int n_sel = max(0, min(n_per_head[bh], sel_width));
+  // Selected score j < n_sel: -inf for an index outside [0, W).
+  const auto sel_score = [&](int j) {
+    const int p = sel[j];
+    return p >= 0 && p < W ? row[p] : -INFINITY;
+  };
+  float mx_all = -INFINITY, mx_sel = -INFINITY;
+  for (int i = t; i < W; i += kSelThreads) mx_all = fmaxf(mx_all, row[i]);
+  for (int j = t; j < n_sel; j += kSelThreads) mx_sel = fmaxf(mx_sel, sel_score(j));
+  block_max2(mx_all, mx_sel, red_max);
+  const float m_all = fmaxf(mx_all, -1e20f);
+  const float m_sel = n_sel < sel_block ? fmaxf(mx_sel, -1e20f) : mx_sel;
+  float se_all = 0.f, se_sel = 0.f;
+  for (int i = t; i < W; i += kSelThreads) se_all += fast_exp(row[i] - m_all);
+  for (int j = t; j < n_sel; j += kSelThreads) se_sel += fast_exp(sel_score(j) - m_sel);
+  block_sum2(se_all, se_sel, red_sum);
+  if (t == 0) {
+    const float cov = expf(lse_from(m_sel, se_sel) - lse_from(m_all, se_all));
+    coverage_out[bh] = cov;
+    accept_out[bh] = cov >= tau ? 1 : 0;
+  }
+}
+
 static int keys_per_thread(int n) {
   int r = 1;
   while (r * kSelThreads < n) r <<= 1;
@@ -1134,8 +1419,10 @@ static int launch_select(const char *name, const float *page_scores, const float
                "%s: bad sizes B=%d H_kv=%d W=%d bs=%d", name, B, H_kv, W, block_size);
   CVSA_REQUIRE(budget >= 1 && budget <= W, CVSA_ERR_INVALID,
                "%s: budget=%d must be in [1, W=%d]", name, budget, W);
-  CVSA_REQUIRE(W <= kMaxPages, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
-               kMaxPages);
+  CVSA_REQUIRE(W <= kMaxPagesWide, CVSA_ERR_UNSUPPORTED, "%s: W=%d exceeds %d pages", name, W,
+               kMaxPagesWide);
+  CVSA_REQUIRE(W <= kMaxPages || mode != kTopP, CVSA_ERR_UNSUPPORTED,
+               "%s: top-p budgets take rows of at most %d pages (W=%d)", name, kMaxPages, W);
   CVSA_REQUIRE(sel_map == nullptr || (map_stride >= W && map_stride % 16 == 0 &&
                                       ((uintptr_t)sel_map & 15) == 0),
                CVSA_ERR_INVALID,
@@ -1153,6 +1440,24 @@ static int launch_select(const char *name, const float *page_scores, const float
   long long *st64 = reinterpret_cast<long long *>(stats);
   // In the variable-budget modes `budget` is the row stride of page_indices.
   const int width = budget;
+  if (W > kMaxPages) {
+#define CVSA_WIDE_LAUNCH(SEP, MODE)                                                          \
+  hipLaunchKernelGGL((select_topk_wide_kernel<SEP, MODE>), grid, dim3(kSelThreads), 0, st,   \
+                     page_scores, sel_scores, W, H_kv, context_lens, block_size, budget,     \
+                     width, row_budgets, page_indices, n_per_head, tau, accept_out,          \
+                     coverage_out, check_accept, B * H_kv, scores_cache, st64, count_gate,   \
+                     keep_flag, sel_map, map_stride,                                          \
+                     reinterpret_cast<unsigned long long *>(keep_work), exp_budget, exp_indices)
+    if (sel_scores != nullptr) {
+      if (mode == kTable) CVSA_WIDE_LAUNCH(true, kTable);
+      else CVSA_WIDE_LAUNCH(true, kUniform);
+    } else {
+      if (mode == kTable) CVSA_WIDE_LAUNCH(false, kTable);
+      else CVSA_WIDE_LAUNCH(false, kUniform);
+    }
+#undef CVSA_WIDE_LAUNCH
+    return cvsa_host::check_launch(name);
+  }
   switch (R) {
 #define CVSA_SEL_LAUNCH(RR, SEP, MODE)                                                      \
   hipLaunchKernelGGL((select_topk_kernel<RR, SEP, MODE>), grid, dim3(kSelThreads), 0, st,   \
@@ -1324,16 +1629,22 @@ extern "C" int cvsa_check_coverage(const float *page_scores, int32_t B,
   CVSA_REQUIRE(B > 0 && H_kv > 0 && W > 0 && sel_stride > 0, CVSA_ERR_INVALID,
                "check_coverage: bad sizes B=%d H_kv=%d W=%d sel_stride=%lld", B, H_kv,
                W, (long long)sel_stride);
-  CVSA_REQUIRE(W <= kMaxPages && sel_stride <= kMaxPages, CVSA_ERR_UNSUPPORTED,
+  CVSA_REQUIRE(W <= kMaxPagesWide && sel_stride <= kMaxPagesWide, CVSA_ERR_UNSUPPORTED,
                "check_coverage: W=%d / selection width %lld exceed %d", W,
-               (long long)sel_stride, kMaxPages);
+               (long long)sel_stride, kMaxPagesWide);
   // The reference pads the selection to a power of two (coverage.py:234-237).
   int sel_block = 1;
   while (sel_block < sel_stride) sel_block <<= 1;
-  const int R = keys_per_thread(W > sel_block ? W : sel_block);
   const dim3 grid(B * H_kv);
   hipStream_t st = (hipStream_t)stream;
   const int width = (int)sel_stride;
+  if (W > kMaxPages || sel_block > kMaxPages) {
+    hipLaunchKernelGGL(check_coverage_wide_kernel, grid, dim3(kSelThreads), 0, st, page_scores,
+                       W, selected, width, sel_block, n_per_head, tau, accept_out,
+                       coverage_out);
+    return cvsa_host::check_launch("check_coverage");
+  }
+  const int R = keys_per_thread(W > sel_block ? W : sel_block);
   switch (R) {
 #define CVSA_COV_CASE(RR)                                                       \
   case RR:                                                                      \

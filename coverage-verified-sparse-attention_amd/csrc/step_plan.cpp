@@ -31,7 +31,7 @@ struct cvsa_step_plan {
 
 namespace {
 
-constexpr int kMaxPages = 32768;
+constexpr int kMaxPages = 1 << 18;  // pages per row (cvsa_common.h kMaxPagesWide)
 constexpr int64_t kMaxDecodeHeads = 4096;
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }

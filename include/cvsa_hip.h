@@ -19,9 +19,9 @@
  *    128},
  *    G = H_q / H_kv in 1..128 (decode launches serve 16 query heads per KV
  *    head; larger groups are enqueued as one launch per 16),
- *    any H_kv (B * H_kv <= 65535), W <= 32768 pages, and B * H_kv <= 4096
- *    for dense and verified decode.  Anything else returns
- *    CVSA_ERR_UNSUPPORTED.
+ *    any H_kv (B * H_kv <= 65535), W <= 262144 pages (top-p budgets:
+ *    W <= 32768), and B * H_kv <= 4096 for dense and verified decode.
+ *    Anything else returns CVSA_ERR_UNSUPPORTED.
  *  - Entry points are re-entrant.  Calls that share a decode workspace must
  *    be ordered on one stream.
  */
