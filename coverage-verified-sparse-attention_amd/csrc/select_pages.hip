@@ -952,9 +952,40 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
 // their own once the counted pages are known (a bit per page in LDS).
 // Same outputs as select_topk_kernel: selection, n_per_head, selection
 // map, scores cache, coverage and accept, the lazy check's decision and
-// counters, and the expanded selection of approximate recovery.
+// counters; the expanded selection of approximate recovery comes from
+// expand_wide_kernel, launched after it.
 constexpr int kWidePerThread = 8;
 constexpr int kWideTile = kSelThreads * kWidePerThread;
+// One workgroup streams its row, so the loads in flight bound the rate:
+// kStrip per thread (64 KiB per workgroup), the next strip requested
+// before the current one is used.
+constexpr int kStrip = 16;
+
+// f(i, row[i]) for every i in [0, n), in strips of kStrip coalesced loads
+// per thread (element e of thread t at strip base + e * kSelThreads + t).
+template <typename F>
+__device__ __forceinline__ void stream_row(const float *__restrict__ row, int n, F &&f) {
+  const int t = threadIdx.x;
+  constexpr int kLen = kStrip * kSelThreads;
+  float nxt[kStrip];
+#pragma unroll
+  for (int e = 0; e < kStrip; ++e) nxt[e] = row[min(e * kSelThreads + t, n - 1)];
+  for (int base = 0; base < n; base += kLen) {
+    float cur[kStrip];
+#pragma unroll
+    for (int e = 0; e < kStrip; ++e) cur[e] = nxt[e];
+    if (base + kLen < n) {  // uniform
+#pragma unroll
+      for (int e = 0; e < kStrip; ++e)
+        nxt[e] = row[min(base + kLen + e * kSelThreads + t, n - 1)];
+    }
+#pragma unroll
+    for (int e = 0; e < kStrip; ++e) {
+      const int i = base + e * kSelThreads + t;
+      if (i < n) f(i, cur[e]);
+    }
+  }
+}
 
 // The k-th largest key T of a row of W scores in memory and krem = k -
 // #(keys > T), as radix_select.
@@ -971,17 +1002,10 @@ __device__ __forceinline__ void wide_threshold(const float *__restrict__ row, in
     for (int i = t; i < kHistCopies * kHistStride; i += kSelThreads) hist_c[i] = 0;
     lds_barrier();
     uint32_t *my_hist = hist_c + (lane % kHistCopies) * kHistStride;
-    for (int i0 = t * 4; i0 < W; i0 += kSelThreads * 4) {
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = row[min(i0 + e, W - 1)];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t key = order_key(v[e]);
-        if (i0 + e < W && (key & pmask) == prefix)
-          atomicAdd(&my_hist[(key >> shift) & 255u], 1u);
-      }
-    }
+    stream_row(row, W, [&](int, float v) {
+      const uint32_t key = order_key(v);
+      if ((key & pmask) == prefix) atomicAdd(&my_hist[(key >> shift) & 255u], 1u);
+    });
     lds_barrier();
     uint32_t digit;
     radix_digit(hist_c, hist, krem, s_digit, s_krem, digit, krem);
@@ -989,6 +1013,96 @@ __device__ __forceinline__ void wide_threshold(const float *__restrict__ row, in
     pmask |= 0xFFu << shift;
   }
   T = prefix;
+}
+
+// Ascending compaction of a wide row's selection (T, krem) into out_row
+// (its first n_write entries; ties at T go to the lowest pages), in tiles of
+// kWideTile pages: a block scan per tile, running counts between tiles.
+// MAIN (the selection, not an expanded one) also writes the counted bits
+// (pages among the first n_sel selected) into s_bits, the selection map row
+// and the scores cache row (either may be null), and takes the gate maxima
+// of `grow` over every page (mx) and over the counted pages (ms).
+template <bool MAIN, bool SEP>
+__device__ __forceinline__ void wide_compact(const float *__restrict__ row,
+                                             const float *__restrict__ grow, int W, uint32_t T,
+                                             uint32_t krem, int n_write, int n_sel,
+                                             int32_t *__restrict__ out_row, uint32_t *wsum,
+                                             uint32_t *s_bits, uint8_t *__restrict__ map_row,
+                                             float *__restrict__ cache_row, float &mx,
+                                             float &ms) {
+  const int t = threadIdx.x;
+  uint32_t gt_run = 0, eq_run = 0;  // keys > T and == T in the tiles before
+  // The next tile's ranking scores are requested before the current tile is
+  // used (the gate scores of separate ranking, with the tile).
+  float nv[kWidePerThread];
+#pragma unroll
+  for (int e = 0; e < kWidePerThread; ++e) nv[e] = row[min(t * kWidePerThread + e, W - 1)];
+  for (int base = 0; base < W; base += kWideTile) {
+    const int p0 = base + t * kWidePerThread;
+    float v[kWidePerThread], g[kWidePerThread];
+#pragma unroll
+    for (int e = 0; e < kWidePerThread; ++e) v[e] = g[e] = nv[e];
+    if constexpr (SEP && MAIN) {
+#pragma unroll
+      for (int e = 0; e < kWidePerThread; ++e) g[e] = grow[min(p0 + e, W - 1)];
+    }
+    if (base + kWideTile < W) {  // uniform
+#pragma unroll
+      for (int e = 0; e < kWidePerThread; ++e) nv[e] = row[min(p0 + kWideTile + e, W - 1)];
+    }
+    uint32_t gt = 0, eq = 0;
+#pragma unroll
+    for (int e = 0; e < kWidePerThread; ++e) {
+      if (p0 + e < W) {
+        const uint32_t key = order_key(v[e]);
+        gt += key > T;
+        eq += key == T;
+      }
+    }
+    uint32_t total;
+    const uint32_t excl = block_exclusive_scan(gt | (eq << 16), wsum, total);
+    uint32_t eq_seen = eq_run + (excl >> 16);
+    uint32_t pos = gt_run + (excl & 0xFFFFu) + min(eq_seen, krem);
+    uint32_t bits = 0;
+#pragma unroll
+    for (int e = 0; e < kWidePerThread; ++e) {
+      bool sel = false;
+      if (p0 + e < W) {
+        const uint32_t key = order_key(v[e]);
+        if (key > T) {
+          sel = true;
+        } else if (key == T) {
+          sel = eq_seen < krem;
+          ++eq_seen;
+        }
+      }
+      const bool counted = sel && (int)pos < n_sel;
+      bits |= counted ? 1u << e : 0u;
+      if (sel) {
+        if ((int)pos < n_write) out_row[pos] = p0 + e;
+        ++pos;
+      }
+      if (MAIN && p0 + e < W) {
+        mx = fmaxf(mx, g[e]);
+        if (counted) ms = fmaxf(ms, g[e]);
+      }
+    }
+    if (MAIN && p0 < W) {
+      atomicOr(&s_bits[p0 >> 5], bits << (p0 & 31));
+      if (map_row != nullptr) {
+#pragma unroll
+        for (int e = 0; e < kWidePerThread; ++e)
+          if (p0 + e < W) map_row[p0 + e] = (bits >> e) & 1u;
+      }
+      if (cache_row != nullptr) {
+#pragma unroll
+        for (int e = 0; e < kWidePerThread; ++e)
+          if (p0 + e < W) cache_row[p0 + e] = g[e];
+      }
+    }
+    gt_run += total & 0xFFFFu;
+    eq_run += total >> 16;
+  }
 }
 
 template <bool SEP, int MODE>
@@ -1000,8 +1114,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_wide_kernel(
     float *__restrict__ coverage_out, const uint8_t *__restrict__ check_accept, int n_heads,
     float *__restrict__ scores_cache, long long *__restrict__ stats, int count_gate,
     int32_t *__restrict__ keep_flag, uint8_t *__restrict__ sel_map, int64_t map_stride,
-    unsigned long long *__restrict__ keep_work, int exp_budget,
-    int32_t *__restrict__ exp_indices) {
+    unsigned long long *__restrict__ keep_work) {
   static_assert(MODE == kUniform || MODE == kTable, "wide rows: uniform or table budgets");
   __shared__ uint32_t hist[256];
   __shared__ uint32_t hist_c[kHistCopies * kHistStride];
@@ -1009,7 +1122,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_wide_kernel(
   __shared__ uint32_t s_digit, s_krem;
   __shared__ uint32_t s_bits[kMaxPagesWide / 32];  // the counted pages
   __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2];
-  __shared__ int s_nok, s_nbad, s_acc;
+  __shared__ int s_nok, s_nbad;
 
   const int bh = blockIdx.x;
   const int b = bh / H_kv;
@@ -1024,88 +1137,16 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_wide_kernel(
   if constexpr (MODE == kTable) k = min(max(row_budgets[bh], 1), W);
   k = min(k, width);
 
-  // Ascending compaction of the selection (T, krem) into out_row (its first
-  // n_write entries; ties at T go to the lowest pages), tile by tile.  With
-  // `main`, also the counted bits, the selection map, the scores cache and
-  // the gate maxima (every page, counted pages).
-  float mx = -INFINITY, ms = -INFINITY;
-  const auto compact = [&](uint32_t T, uint32_t krem, int n_write, int n_sel, int32_t *out_row,
-                           bool main) __attribute__((always_inline)) {
-    uint32_t gt_run = 0, eq_run = 0;  // keys > T and == T in the tiles before
-    for (int base = 0; base < W; base += kWideTile) {
-      const int p0 = base + t * kWidePerThread;
-      float v[kWidePerThread], g[kWidePerThread];
-#pragma unroll
-      for (int e = 0; e < kWidePerThread; ++e) v[e] = row[min(p0 + e, W - 1)];
-      if (SEP && main) {
-#pragma unroll
-        for (int e = 0; e < kWidePerThread; ++e) g[e] = grow[min(p0 + e, W - 1)];
-      } else {
-#pragma unroll
-        for (int e = 0; e < kWidePerThread; ++e) g[e] = v[e];
-      }
-      uint32_t gt = 0, eq = 0;
-#pragma unroll
-      for (int e = 0; e < kWidePerThread; ++e) {
-        if (p0 + e < W) {
-          const uint32_t key = order_key(v[e]);
-          gt += key > T;
-          eq += key == T;
-        }
-      }
-      uint32_t total;
-      const uint32_t excl = block_exclusive_scan(gt | (eq << 16), wsum, total);
-      uint32_t eq_seen = eq_run + (excl >> 16);
-      uint32_t pos = gt_run + (excl & 0xFFFFu) + min(eq_seen, krem);
-      uint32_t bits = 0;
-#pragma unroll
-      for (int e = 0; e < kWidePerThread; ++e) {
-        bool sel = false;
-        if (p0 + e < W) {
-          const uint32_t key = order_key(v[e]);
-          if (key > T) {
-            sel = true;
-          } else if (key == T) {
-            sel = eq_seen < krem;
-            ++eq_seen;
-          }
-        }
-        const bool counted = sel && (int)pos < n_sel;
-        bits |= counted ? 1u << e : 0u;
-        if (sel) {
-          if ((int)pos < n_write) out_row[pos] = p0 + e;
-          ++pos;
-        }
-        if (main && p0 + e < W) {
-          mx = fmaxf(mx, g[e]);
-          if (counted) ms = fmaxf(ms, g[e]);
-        }
-      }
-      if (main && p0 < W) {
-        atomicOr(&s_bits[p0 >> 5], bits << (p0 & 31));
-        if (sel_map != nullptr) {
-          uint8_t *m = sel_map + (int64_t)bh * map_stride + p0;
-#pragma unroll
-          for (int e = 0; e < kWidePerThread; ++e)
-            if (p0 + e < W) m[e] = (bits >> e) & 1u;
-        }
-        if (scores_cache != nullptr) {
-          float *dst = scores_cache + (int64_t)bh * W + p0;
-#pragma unroll
-          for (int e = 0; e < kWidePerThread; ++e)
-            if (p0 + e < W) dst[e] = g[e];
-        }
-      }
-      gt_run += total & 0xFFFFu;
-      eq_run += total >> 16;
-    }
-  };
-
+  float mx = -INFINITY, ms = -INFINITY;  // gate maxima: every page, counted pages
   for (int i = t; i < (W + 31) / 32; i += kSelThreads) s_bits[i] = 0u;
+  const int n_sel = min(k, n_valid_pages(ctx, block_size));
   uint32_t T = 0, krem = 0;
   wide_threshold(row, W, (uint32_t)k, hist, hist_c, &s_digit, &s_krem, T, krem);
-  const int n_sel = min(k, n_valid_pages(ctx, block_size));
-  compact(T, krem, k, n_sel, page_indices + (int64_t)bh * width, true);
+  wide_compact<true, SEP>(row, grow, W, T, krem, k, n_sel, page_indices + (int64_t)bh * width,
+                          wsum, s_bits,
+                          sel_map != nullptr ? sel_map + (int64_t)bh * map_stride : nullptr,
+                          scores_cache != nullptr ? scores_cache + (int64_t)bh * W : nullptr,
+                          mx, ms);
   if (t == 0) n_per_head[bh] = n_sel;
   if (accept_out == nullptr) return;
 
@@ -1116,18 +1157,16 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_wide_kernel(
   while (msel_block < width) msel_block <<= 1;
   const float m_sel = n_sel < msel_block ? fmaxf(ms, -1e20f) : ms;
   float se = 0.f, ss = 0.f;
-  for (int p = t; p < W; p += kSelThreads) {
-    const float g = grow[p];
+  stream_row(grow, W, [&](int p, float g) {
     se += fast_exp(g - m_all);
     if ((s_bits[p >> 5] >> (p & 31)) & 1u) ss += fast_exp(g - m_sel);
-  }
+  });
   block_sum2(se, ss, red_sum);
   if (t == 0) {
     const float cov = expf(lse_from(m_sel, ss) - lse_from(m_all, se));
     const int acc = cov >= tau ? 1 : 0;
     coverage_out[bh] = cov;
     accept_out[bh] = (uint8_t)acc;
-    s_acc = acc;
     if (stats != nullptr && count_gate) {
       // As in select_topk_kernel: the last head of a fixed-interval scoring
       // step books it (the same gfx950 ordering of agent-scope atomics).
@@ -1149,16 +1188,29 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_wide_kernel(
       }
     }
   }
-  // Approximate recovery: a rejected row's expanded selection.
-  if constexpr (MODE == kUniform) {
-    if (exp_indices == nullptr) return;  // uniform
-    lds_barrier();
-    if (s_acc != 0) return;  // uniform
-    const int k2 = min(exp_budget, W);
-    uint32_t T2 = 0, krem2 = 0;
-    wide_threshold(row, W, (uint32_t)k2, hist, hist_c, &s_digit, &s_krem, T2, krem2);
-    compact(T2, krem2, k2, k2, exp_indices + (int64_t)bh * exp_budget, false);
-  }
+}
+
+// Approximate recovery of wide rows: a rejected row's expanded selection
+// (the exp_budget largest ranking scores in ascending page order), after
+// select_topk_wide_kernel on the same stream wrote the row's accept flag.
+// A launch of its own keeps both kernels within their registers.
+template <bool SEP>
+__global__ __launch_bounds__(kSelThreads) void expand_wide_kernel(
+    const float *__restrict__ scores, const float *__restrict__ sel_scores, int W,
+    const uint8_t *__restrict__ accept, int exp_budget, int32_t *__restrict__ exp_indices) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist_c[kHistCopies * kHistStride];
+  __shared__ uint32_t wsum[kSelWaves];
+  __shared__ uint32_t s_digit, s_krem;
+  const int bh = blockIdx.x;
+  if (accept[bh] != 0) return;  // uniform
+  const float *row = (SEP ? sel_scores : scores) + (int64_t)bh * W;
+  const int k2 = min(exp_budget, W);
+  uint32_t T = 0, krem = 0;
+  wide_threshold(row, W, (uint32_t)k2, hist, hist_c, &s_digit, &s_krem, T, krem);
+  float mx = -INFINITY, ms = -INFINITY;
+  wide_compact<false, SEP>(row, row, W, T, krem, k2, k2, exp_indices + (int64_t)bh * exp_budget,
+                           wsum, nullptr, nullptr, nullptr, mx, ms);
 }
 
 // Budgets of CVSABackend._adaptive_select (cvsa/backend.py:522-570): the
@@ -1372,15 +1424,29 @@ __global__ __launch_bounds__(kSelThreads) void check_coverage_wide_kernel(
     const int p = sel[j];
     return p >= 0 && p < W ? row[p] : -INFINITY;
   };
+  // f(score) for every selected j < n_sel, kStrip gathers in flight.
+  const auto for_selected = [&](auto &&f) {
+    for (int j0 = 0; j0 < n_sel; j0 += kStrip * kSelThreads) {
+      float v[kStrip];
+#pragma unroll
+      for (int e = 0; e < kStrip; ++e) {
+        const int j = j0 + e * kSelThreads + t;
+        v[e] = j < n_sel ? sel_score(j) : -INFINITY;
+      }
+#pragma unroll
+      for (int e = 0; e < kStrip; ++e)
+        if (j0 + e * kSelThreads + t < n_sel) f(v[e]);
+    }
+  };
   float mx_all = -INFINITY, mx_sel = -INFINITY;
-  for (int i = t; i < W; i += kSelThreads) mx_all = fmaxf(mx_all, row[i]);
-  for (int j = t; j < n_sel; j += kSelThreads) mx_sel = fmaxf(mx_sel, sel_score(j));
+  stream_row(row, W, [&](int, float v) { mx_all = fmaxf(mx_all, v); });
+  for_selected([&](float v) { mx_sel = fmaxf(mx_sel, v); });
   block_max2(mx_all, mx_sel, red_max);
   const float m_all = fmaxf(mx_all, -1e20f);
   const float m_sel = n_sel < sel_block ? fmaxf(mx_sel, -1e20f) : mx_sel;
   float se_all = 0.f, se_sel = 0.f;
-  for (int i = t; i < W; i += kSelThreads) se_all += fast_exp(row[i] - m_all);
-  for (int j = t; j < n_sel; j += kSelThreads) se_sel += fast_exp(sel_score(j) - m_sel);
+  stream_row(row, W, [&](int, float v) { se_all += fast_exp(v - m_all); });
+  for_selected([&](float v) { se_sel += fast_exp(v - m_sel); });
   block_sum2(se_all, se_sel, red_sum);
   if (t == 0) {
     const float cov = expf(lse_from(m_sel, se_sel) - lse_from(m_all, se_all));
@@ -1447,7 +1513,7 @@ static int launch_select(const char *name, const float *page_scores, const float
                      width, row_budgets, page_indices, n_per_head, tau, accept_out,          \
                      coverage_out, check_accept, B * H_kv, scores_cache, st64, count_gate,   \
                      keep_flag, sel_map, map_stride,                                          \
-                     reinterpret_cast<unsigned long long *>(keep_work), exp_budget, exp_indices)
+                     reinterpret_cast<unsigned long long *>(keep_work))
     if (sel_scores != nullptr) {
       if (mode == kTable) CVSA_WIDE_LAUNCH(true, kTable);
       else CVSA_WIDE_LAUNCH(true, kUniform);
@@ -1456,6 +1522,15 @@ static int launch_select(const char *name, const float *page_scores, const float
       else CVSA_WIDE_LAUNCH(false, kUniform);
     }
 #undef CVSA_WIDE_LAUNCH
+    // Approximate recovery: the expanded selection of every rejected row.
+    if (mode == kUniform && exp_indices != nullptr && accept_out != nullptr) {
+      if (sel_scores != nullptr)
+        hipLaunchKernelGGL(expand_wide_kernel<true>, grid, dim3(kSelThreads), 0, st,
+                           page_scores, sel_scores, W, accept_out, exp_budget, exp_indices);
+      else
+        hipLaunchKernelGGL(expand_wide_kernel<false>, grid, dim3(kSelThreads), 0, st,
+                           page_scores, sel_scores, W, accept_out, exp_budget, exp_indices);
+    }
     return cvsa_host::check_launch(name);
   }
   switch (R) {
