@@ -957,9 +957,12 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
 constexpr int kWidePerThread = 8;
 constexpr int kWideTile = kSelThreads * kWidePerThread;
 // One workgroup streams its row, so the loads in flight bound the rate:
-// kStrip per thread (64 KiB per workgroup), the next strip requested
-// before the current one is used.
-constexpr int kStrip = 16;
+// strips of kStrip coalesced loads per thread (32 KiB per workgroup) in two
+// buffers that alternate, so that one strip's loads are in flight while
+// the other is used.  The loads are unconditional (addresses clamped into
+// the row): loads under a branch make the compiler wait for every
+// outstanding load at the join.
+constexpr int kStrip = 8;
 
 // f(i, row[i]) for every i in [0, n), in strips of kStrip coalesced loads
 // per thread (element e of thread t at strip base + e * kSelThreads + t).
@@ -967,52 +970,183 @@ template <typename F>
 __device__ __forceinline__ void stream_row(const float *__restrict__ row, int n, F &&f) {
   const int t = threadIdx.x;
   constexpr int kLen = kStrip * kSelThreads;
-  float nxt[kStrip];
+  const auto load = [&](float (&x)[kStrip], int base) __attribute__((always_inline)) {
 #pragma unroll
-  for (int e = 0; e < kStrip; ++e) nxt[e] = row[min(e * kSelThreads + t, n - 1)];
-  for (int base = 0; base < n; base += kLen) {
-    float cur[kStrip];
-#pragma unroll
-    for (int e = 0; e < kStrip; ++e) cur[e] = nxt[e];
-    if (base + kLen < n) {  // uniform
-#pragma unroll
-      for (int e = 0; e < kStrip; ++e)
-        nxt[e] = row[min(base + kLen + e * kSelThreads + t, n - 1)];
-    }
+    for (int e = 0; e < kStrip; ++e) x[e] = row[min(base + e * kSelThreads + t, n - 1)];
+  };
+  const auto use = [&](const float (&x)[kStrip], int base) __attribute__((always_inline)) {
 #pragma unroll
     for (int e = 0; e < kStrip; ++e) {
       const int i = base + e * kSelThreads + t;
-      if (i < n) f(i, cur[e]);
+      if (i < n) f(i, x[e]);
     }
+  };
+  // The scheduling barriers keep the loads in program order (the compiler
+  // would otherwise move one buffer's use, or its first loads, past the
+  // other's loads and then wait for both).
+  float a[kStrip], b[kStrip];
+  load(a, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  load(b, kLen);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int base = 0; base < n; base += 2 * kLen) {
+    use(a, base);
+    load(a, base + 2 * kLen);
+    __builtin_amdgcn_sched_barrier(0);
+    use(b, base + kLen);
+    load(b, base + 3 * kLen);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-// The k-th largest key T of a row of W scores in memory and krem = k -
-// #(keys > T), as radix_select.
-__device__ __forceinline__ void wide_threshold(const float *__restrict__ row, int W, uint32_t k,
-                                               uint32_t *hist, uint32_t *hist_c,
-                                               uint32_t *s_digit, uint32_t *s_krem,
-                                               uint32_t &T, uint32_t &krem) {
+// LDS of the wide-row threshold: the radix histograms, the value-bucket
+// histogram (in hist_c), the block reductions and the candidates of the
+// k-th value bucket.
+constexpr int kWideCands = 4 * kSelThreads;
+struct WideLds {
+  uint32_t hist[256];
+  uint32_t hist_c[kHistCopies * kHistStride];
+  uint32_t wsum[kSelWaves];
+  uint32_t red_rng[kSelWaves][3];
+  float cand[kWideCands];
+  uint32_t digit, krem, bucket, kb, nb, ncand;
+  int odd;
+};
+
+// 8-bit MSB radix select over a row in memory (four passes over it) of the
+// k-th largest key among the pages with alive(v), as radix_select.
+template <typename Alive>
+__device__ __forceinline__ void wide_radix(const float *__restrict__ row, int W, uint32_t k,
+                                           Alive alive, WideLds &L, uint32_t &T,
+                                           uint32_t &krem) {
   const int t = threadIdx.x, lane = t & 63;
   uint32_t prefix = 0, pmask = 0;
   krem = k;
 #pragma unroll 1
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
-    for (int i = t; i < kHistCopies * kHistStride; i += kSelThreads) hist_c[i] = 0;
+    for (int i = t; i < kHistCopies * kHistStride; i += kSelThreads) L.hist_c[i] = 0;
     lds_barrier();
-    uint32_t *my_hist = hist_c + (lane % kHistCopies) * kHistStride;
+    uint32_t *my_hist = L.hist_c + (lane % kHistCopies) * kHistStride;
     stream_row(row, W, [&](int, float v) {
       const uint32_t key = order_key(v);
-      if ((key & pmask) == prefix) atomicAdd(&my_hist[(key >> shift) & 255u], 1u);
+      if ((key & pmask) == prefix && alive(v)) atomicAdd(&my_hist[(key >> shift) & 255u], 1u);
     });
     lds_barrier();
     uint32_t digit;
-    radix_digit(hist_c, hist, krem, s_digit, s_krem, digit, krem);
+    radix_digit(L.hist_c, L.hist, krem, &L.digit, &L.krem, digit, krem);
     prefix |= digit << shift;
     pmask |= 0xFFu << shift;
   }
   T = prefix;
+}
+
+// The k-th largest key T of a row of W scores in memory and krem = k -
+// #(keys > T), with the register kernel's plan: the range of the finite
+// scores (one pass), their counts in kBuckets value buckets (one pass),
+// then the bucket holding the k-th largest, whose scores (at most
+// kWideCands: one more pass gathers them) are ranked in LDS; a larger
+// bucket, or a row with +inf / NaN scores or too wide a range, takes the
+// radix select over the row (restricted to that bucket when there is one).
+__device__ __forceinline__ void wide_threshold(const float *__restrict__ row, int W, uint32_t k,
+                                               WideLds &L, uint32_t &T, uint32_t &krem) {
+  const int t = threadIdx.x, lane = t & 63;
+  if (t == 0) {
+    L.odd = 0;
+    L.ncand = 0;
+  }
+  lds_barrier();
+  // Range of the finite scores (as keys) and their count; any +inf / NaN
+  // sets L.odd.  -inf lies below every finite score.
+  uint32_t kmax = 0, kneg = 0, cnt = 0;
+  stream_row(row, W, [&](int, float v) {
+    if (fabsf(v) <= 3.402823466e38f) {
+      const uint32_t key = order_key(v);
+      kmax = max(kmax, key);
+      kneg = max(kneg, ~key);
+      cnt += 1;
+    } else if (v != -INFINITY) {
+      L.odd = 1;
+    }
+  });
+  block_range(kmax, kneg, cnt, L.red_rng);  // its barrier also orders L.odd
+  const uint32_t kmin = ~kneg, n_fin = cnt;
+  const auto everything = [](float) { return true; };
+  if (L.odd != 0) {  // uniform
+    wide_radix(row, W, k, everything, L, T, krem);
+    return;
+  }
+  if (k > n_fin) {  // every finite page, then the lowest -inf pages
+    T = order_key(-INFINITY);
+    krem = k - n_fin;
+    return;
+  }
+  if (kmin == kmax) {
+    T = kmax;
+    krem = k;
+    return;
+  }
+  const float vmin = key_value(kmin);
+  const float inv = (float)kBuckets / (key_value(kmax) - vmin);
+  if (!(inv > 0.f && inv <= 3.402823466e38f)) {  // max - min overflows
+    wide_radix(row, W, k, everything, L, T, krem);
+    return;
+  }
+  uint32_t *hist_b = L.hist_c;
+  for (int i = t; i < kBuckets; i += kSelThreads) hist_b[i] = 0;
+  lds_barrier();
+  stream_row(row, W, [&](int, float v) {
+    if (fabsf(v) <= 3.402823466e38f) atomicAdd(&hist_b[value_bucket(v, vmin, inv)], 1u);
+  });
+  lds_barrier();
+  // Thread t holds buckets kBuckets-1-(4t+j), j = 0..3: the exclusive scan
+  // over threads counts the scores in higher buckets.
+  uint32_t c[kBucketsPerThread], local = 0;
+#pragma unroll
+  for (int j = 0; j < kBucketsPerThread; ++j) {
+    c[j] = hist_b[kBuckets - 1 - (kBucketsPerThread * t + j)];
+    local += c[j];
+  }
+  uint32_t total_b;
+  uint32_t above = block_exclusive_scan(local, L.wsum, total_b);
+#pragma unroll
+  for (int j = 0; j < kBucketsPerThread; ++j) {
+    if (above < k && above + c[j] >= k) {
+      L.bucket = (uint32_t)(kBuckets - 1 - (kBucketsPerThread * t + j));
+      L.kb = k - above;
+      L.nb = c[j];
+    }
+    above += c[j];
+  }
+  lds_barrier();
+  const int bstar = (int)L.bucket;
+  const uint32_t kb = L.kb, nb = L.nb;
+  const auto in_bucket = [&](float v) {
+    return fabsf(v) <= 3.402823466e38f && value_bucket(v, vmin, inv) == bstar;
+  };
+  if (nb > (uint32_t)kWideCands) {  // uniform
+    wide_radix(row, W, kb, in_bucket, L, T, krem);
+    return;
+  }
+  // Gather the bucket's scores (a wave-aggregated append: exactly nb of
+  // them, the same bucket function as the counts), then rank them.
+  stream_row(row, W, [&](int, float v) {
+    const bool take = in_bucket(v);
+    const unsigned long long m = __ballot(take);
+    if (m == 0ull) return;
+    const int leader = __ffsll((long long)m) - 1;
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(&L.ncand, (uint32_t)__popcll(m));
+    base = __shfl(base, leader, 64);
+    if (take) L.cand[base + __popcll(m & ((1ull << lane) - 1ull))] = v;
+  });
+  lds_barrier();
+  constexpr int RC = kWideCands / kSelThreads;
+  float cv[RC];
+#pragma unroll
+  for (int r = 0; r < RC; ++r) cv[r] = L.cand[min(t + r * kSelThreads, kWideCands - 1)];
+  const auto alive = [&](int r) { return (uint32_t)(t + r * kSelThreads) < nb; };
+  radix_select<RC>(cv, alive, kb, L.hist, L.hist_c, &L.digit, &L.krem, T, krem);
 }
 
 // Ascending compaction of a wide row's selection (T, krem) into out_row
@@ -1032,24 +1166,27 @@ __device__ __forceinline__ void wide_compact(const float *__restrict__ row,
                                              float &ms) {
   const int t = threadIdx.x;
   uint32_t gt_run = 0, eq_run = 0;  // keys > T and == T in the tiles before
-  // The next tile's ranking scores are requested before the current tile is
-  // used (the gate scores of separate ranking, with the tile).
-  float nv[kWidePerThread];
-#pragma unroll
-  for (int e = 0; e < kWidePerThread; ++e) nv[e] = row[min(t * kWidePerThread + e, W - 1)];
-  for (int base = 0; base < W; base += kWideTile) {
+  // Two tiles in alternating buffers: one tile's loads are in flight while
+  // the other is compacted (unconditional loads at clamped addresses).
+  constexpr bool G = SEP && MAIN;  // separate gate scores
+  const auto fetch = [&](float (&v)[kWidePerThread], float (&g)[G ? kWidePerThread : 1],
+                         int base) __attribute__((always_inline)) {
     const int p0 = base + t * kWidePerThread;
-    float v[kWidePerThread], g[kWidePerThread];
 #pragma unroll
-    for (int e = 0; e < kWidePerThread; ++e) v[e] = g[e] = nv[e];
-    if constexpr (SEP && MAIN) {
+    for (int e = 0; e < kWidePerThread; ++e) v[e] = row[min(p0 + e, W - 1)];
+    if constexpr (G) {
 #pragma unroll
       for (int e = 0; e < kWidePerThread; ++e) g[e] = grow[min(p0 + e, W - 1)];
     }
-    if (base + kWideTile < W) {  // uniform
-#pragma unroll
-      for (int e = 0; e < kWidePerThread; ++e) nv[e] = row[min(p0 + kWideTile + e, W - 1)];
-    }
+  };
+  const auto tile = [&](const float (&v)[kWidePerThread],
+                        const float (&gs)[G ? kWidePerThread : 1], int base)
+                        __attribute__((always_inline)) {
+    const int p0 = base + t * kWidePerThread;
+    const auto g = [&](int e) {
+      if constexpr (G) return gs[e];
+      else return v[e];
+    };
     uint32_t gt = 0, eq = 0;
 #pragma unroll
     for (int e = 0; e < kWidePerThread; ++e) {
@@ -1083,8 +1220,8 @@ __device__ __forceinline__ void wide_compact(const float *__restrict__ row,
         ++pos;
       }
       if (MAIN && p0 + e < W) {
-        mx = fmaxf(mx, g[e]);
-        if (counted) ms = fmaxf(ms, g[e]);
+        mx = fmaxf(mx, g(e));
+        if (counted) ms = fmaxf(ms, g(e));
       }
     }
     if (MAIN && p0 < W) {
@@ -1097,11 +1234,25 @@ __device__ __forceinline__ void wide_compact(const float *__restrict__ row,
       if (cache_row != nullptr) {
 #pragma unroll
         for (int e = 0; e < kWidePerThread; ++e)
-          if (p0 + e < W) cache_row[p0 + e] = g[e];
+          if (p0 + e < W) cache_row[p0 + e] = g(e);
       }
     }
     gt_run += total & 0xFFFFu;
     eq_run += total >> 16;
+  };
+  float va[kWidePerThread], vb[kWidePerThread];
+  float ga[G ? kWidePerThread : 1], gb[G ? kWidePerThread : 1];
+  fetch(va, ga, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  fetch(vb, gb, kWideTile);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int base = 0; base < W; base += 2 * kWideTile) {
+    tile(va, ga, base);
+    fetch(va, ga, base + 2 * kWideTile);
+    __builtin_amdgcn_sched_barrier(0);
+    if (base + kWideTile < W) tile(vb, gb, base + kWideTile);  // uniform
+    fetch(vb, gb, base + 3 * kWideTile);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -1116,10 +1267,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_wide_kernel(
     int32_t *__restrict__ keep_flag, uint8_t *__restrict__ sel_map, int64_t map_stride,
     unsigned long long *__restrict__ keep_work) {
   static_assert(MODE == kUniform || MODE == kTable, "wide rows: uniform or table budgets");
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t hist_c[kHistCopies * kHistStride];
-  __shared__ uint32_t wsum[kSelWaves];
-  __shared__ uint32_t s_digit, s_krem;
+  __shared__ WideLds L;
   __shared__ uint32_t s_bits[kMaxPagesWide / 32];  // the counted pages
   __shared__ float red_max[kSelWaves][2], red_sum[kSelWaves][2];
   __shared__ int s_nok, s_nbad;
@@ -1141,9 +1289,9 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_wide_kernel(
   for (int i = t; i < (W + 31) / 32; i += kSelThreads) s_bits[i] = 0u;
   const int n_sel = min(k, n_valid_pages(ctx, block_size));
   uint32_t T = 0, krem = 0;
-  wide_threshold(row, W, (uint32_t)k, hist, hist_c, &s_digit, &s_krem, T, krem);
+  wide_threshold(row, W, (uint32_t)k, L, T, krem);
   wide_compact<true, SEP>(row, grow, W, T, krem, k, n_sel, page_indices + (int64_t)bh * width,
-                          wsum, s_bits,
+                          L.wsum, s_bits,
                           sel_map != nullptr ? sel_map + (int64_t)bh * map_stride : nullptr,
                           scores_cache != nullptr ? scores_cache + (int64_t)bh * W : nullptr,
                           mx, ms);
@@ -1198,19 +1346,16 @@ template <bool SEP>
 __global__ __launch_bounds__(kSelThreads) void expand_wide_kernel(
     const float *__restrict__ scores, const float *__restrict__ sel_scores, int W,
     const uint8_t *__restrict__ accept, int exp_budget, int32_t *__restrict__ exp_indices) {
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t hist_c[kHistCopies * kHistStride];
-  __shared__ uint32_t wsum[kSelWaves];
-  __shared__ uint32_t s_digit, s_krem;
+  __shared__ WideLds L;
   const int bh = blockIdx.x;
   if (accept[bh] != 0) return;  // uniform
   const float *row = (SEP ? sel_scores : scores) + (int64_t)bh * W;
   const int k2 = min(exp_budget, W);
   uint32_t T = 0, krem = 0;
-  wide_threshold(row, W, (uint32_t)k2, hist, hist_c, &s_digit, &s_krem, T, krem);
+  wide_threshold(row, W, (uint32_t)k2, L, T, krem);
   float mx = -INFINITY, ms = -INFINITY;
   wide_compact<false, SEP>(row, row, W, T, krem, k2, k2, exp_indices + (int64_t)bh * exp_budget,
-                           wsum, nullptr, nullptr, nullptr, mx, ms);
+                           L.wsum, nullptr, nullptr, nullptr, mx, ms);
 }
 
 // Budgets of CVSABackend._adaptive_select (cvsa/backend.py:522-570): the
@@ -1419,23 +1564,20 @@ __global__ __launch_bounds__(kSelThreads) void check_coverage_wide_kernel(
   const float *row = scores + (int64_t)bh * W;
   const int32_t *sel = selected + (int64_t)bh * sel_width;
   const int n_sel = max(0, min(n_per_head[bh], sel_width));
-  // Selected score j < n_sel: -inf for an index outside [0, W).
-  const auto sel_score = [&](int j) {
-    const int p = sel[j];
-    return p >= 0 && p < W ? row[p] : -INFINITY;
-  };
-  // f(score) for every selected j < n_sel, kStrip gathers in flight.
+  // f(score) for every selected j < n_sel (-inf for an id outside
+  // [0, W)): kStrip ids, then kStrip scores in flight (unconditional loads
+  // at clamped addresses).
   const auto for_selected = [&](auto &&f) {
     for (int j0 = 0; j0 < n_sel; j0 += kStrip * kSelThreads) {
+      int p[kStrip];
       float v[kStrip];
 #pragma unroll
-      for (int e = 0; e < kStrip; ++e) {
-        const int j = j0 + e * kSelThreads + t;
-        v[e] = j < n_sel ? sel_score(j) : -INFINITY;
-      }
+      for (int e = 0; e < kStrip; ++e) p[e] = sel[min(j0 + e * kSelThreads + t, n_sel - 1)];
+#pragma unroll
+      for (int e = 0; e < kStrip; ++e) v[e] = row[min(max(p[e], 0), W - 1)];
 #pragma unroll
       for (int e = 0; e < kStrip; ++e)
-        if (j0 + e * kSelThreads + t < n_sel) f(v[e]);
+        if (j0 + e * kSelThreads + t < n_sel) f(p[e] >= 0 && p[e] < W ? v[e] : -INFINITY);
     }
   };
   float mx_all = -INFINITY, mx_sel = -INFINITY;

@@ -61,7 +61,9 @@ def test_select_topk_wide_bit_exact(gpu, W, budget):
 def test_select_topk_wide_special_rows(gpu):
     """The register kernel's special rows at W = 40000: all equal, +0/-0,
     one huge outlier, an fp32-overflowing range, +inf and NaN entries,
-    near-ties in one bucket, fewer finite scores than the budget."""
+    near-ties in one bucket, fewer finite scores than the budget; and a
+    row whose k-th value bucket holds more scores than the kernel ranks in
+    LDS (an outlier stretches the range, so the bulk shares one bucket)."""
     W, budget = 40000, 5000
     g = torch.Generator().manual_seed(W)
     rows = [torch.full((W,), 1.25)]
@@ -82,6 +84,9 @@ def test_select_topk_wide_special_rows(gpu):
     r = torch.randn(W, generator=g)
     r[torch.randperm(W, generator=g)[: W - budget // 2]] = float("-inf")
     rows.append(r)
+    r = 1.0 + torch.randint(0, 3000, (W,), generator=g).float() * 2.0 ** -22
+    r[123] = 1000.0
+    rows.append(r)
     ps = torch.stack(rows).view(1, len(rows), W)
     ctx = torch.tensor([W * 16], dtype=torch.int32)
     idx, nph, acc, cov = ops.select_topk(ps.to(gpu), budget, ctx.to(gpu), 16, tau=0.9)
@@ -89,7 +94,7 @@ def test_select_topk_wide_special_rows(gpu):
     for h in range(len(rows)):
         assert torch.equal(idx.cpu()[0, h], widx[0, h]), h
     assert torch.equal(nph.cpu(), wnph)
-    finite_rows = [0, 1, 2, 5]
+    finite_rows = [0, 1, 2, 5, 7]
     wacc, wcov = ref.check_coverage(ps, widx, wnph, 0.9)
     assert (cov.cpu()[0, finite_rows] - wcov[0, finite_rows]).abs().max().item() < COV_ATOL
 
