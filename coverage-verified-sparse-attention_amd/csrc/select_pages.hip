@@ -954,7 +954,7 @@ __global__ __launch_bounds__(kSelThreads) void select_topk_kernel(
 // map, scores cache, coverage and accept, the lazy check's decision and
 // counters; the expanded selection of approximate recovery comes from
 // expand_wide_kernel, launched after it.
-constexpr int kWidePerThread = 8;
+constexpr int kWidePerThread = 4;  // pages per thread of a compaction tile
 constexpr int kWideTile = kSelThreads * kWidePerThread;
 // One workgroup streams its row, so the loads in flight bound the rate:
 // strips of kStrip coalesced loads per thread (32 KiB per workgroup) in two
