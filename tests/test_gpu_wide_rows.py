@@ -10,7 +10,9 @@ coverage within 1e-5, outputs within the north star's 2e-2.  The backend
 runs (lockstep with the oracle backend, every selection, mask, output and
 counter compared) cover the whole decode step at widths only these kernels
 serve: block size 16 and 8, a draft wider than 32768 pages, exact and
-approximate recovery, and the dense speculation of an all-rejected check.
+approximate recovery, a kept listed speculation and the dense speculation
+of an all-rejected check, and the Quest, adaptive and static-table
+selectors.
 """
 import pytest
 import torch
@@ -238,10 +240,35 @@ _SPEC = dict(batch=1, num_q_heads=16, num_kv_heads=4, head_dim=128, n_hot=24)
     dict(cfg=dict(_SPEC, context_len=33000 * 16 + 7, hot_heads=[0], hot_shift=4.0),
          kw=dict(budget_pct=0.125, coverage_threshold=0.999, lazy=True, check_interval=2),
          expect="dense"),
-], ids=["bs16_keep", "bs8", "wide_draft", "approx", "dense_spec"])
+    # the Quest selector: separate ranking scores with a uniform budget
+    dict(cfg=dict(_SPEC, context_len=34000 * 16 - 3, hot_heads=[1, 2], hot_shift=12.0),
+         kw=dict(budget_pct=0.125, coverage_threshold=0.9, lazy=True, check_interval=3,
+                 selector="quest"),
+         expect="recover"),
+    # ... with approximate recovery (the expansion ranks the Quest scores)
+    dict(cfg=dict(_SPEC, context_len=34000 * 16, hot_heads=[0], hot_shift=6.0),
+         kw=dict(budget_pct=0.1, coverage_threshold=0.95, lazy=True, check_interval=2,
+                 selector="quest", approx_recovery_pct=0.3),
+         expect="approx", seed=8811),
+    # adaptive per-head budgets (per-row budgets of the wide kernel)
+    dict(cfg=dict(_WIDE, num_kv_heads=2, num_q_heads=8, hot_heads=[1],
+                  context_len=36000 * 16, hot_shift=10.0),
+         kw=dict(budget_pct=0.125, coverage_threshold=0.9, lazy=True, check_interval=3,
+                 adaptive_selection=True),
+         expect="recover"),
+    # a static budget table (per-row budgets, fixed-interval schedule)
+    dict(cfg=dict(_WIDE, num_kv_heads=2, num_q_heads=8, hot_heads=[0],
+                  context_len=36000 * 16, hot_shift=10.0),
+         kw=dict(static_budget_table={0: [0.05, 0.2]}, coverage_threshold=0.9, lazy=False,
+                 reuse_interval=2),
+         expect="recover"),
+], ids=["bs16_keep", "bs8", "wide_draft", "approx", "dense_spec", "quest", "quest_approx",
+        "adaptive", "static_table"])
 def test_backend_wide_rows_lockstep(gpu, case):
-    stats, trace, lock = _run(gpu, case["cfg"], case["kw"], steps=6, seed=8800,
-                              gen_on_gpu=True)
+    # Seeds with no head within the fp64 margins (the lockstep harness
+    # counts them; the BASELINE bar is zero).
+    stats, trace, lock = _run(gpu, case["cfg"], case["kw"], steps=6,
+                              seed=case.get("seed", 8800), gen_on_gpu=True)
     kinds = [t["kind"] for t in trace]
     assert kinds[0].startswith("score"), kinds
     assert "reuse" in kinds, kinds
