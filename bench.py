@@ -151,6 +151,12 @@ def parse_args():
     ap.add_argument("--budget-samples", action="store_true",
                     help="also time the per-head budget selections (top-p 0.9, adaptive "
                          "budgets + selection, static table) on the workload's page scores")
+    ap.add_argument("--budget-mode", choices=("uniform", "topp", "adaptive", "static"),
+                    default="uniform",
+                    help="per-head budgets in the timed schedule: top-p 0.9 "
+                         "(CVSABackend(top_p=0.9)), adaptive budgets "
+                         "(adaptive_selection=True) or a static table (per-head fractions "
+                         "around the budget); value counts each head's own selection")
     ap.add_argument("--light-normalizer", action="store_true",
                     help="with --selector quest: Quest scores also drive the coverage gate "
                          "(no full-key scan on any step)")
@@ -204,10 +210,23 @@ class Layer:
                 self.mgr.context_lens)
 
 
+# Per-head budget fractions of --budget-mode static, relative to the
+# workload's budget (KV head h takes STATIC_SCALE[h % 8] * budget).
+STATIC_SCALE = (0.5, 1.5, 0.75, 1.25, 1.0, 2.0, 0.25, 0.75)
+
+
 def backend_kwargs(cfg, tau):
     """CVSABackend / OracleCVSABackend keywords of the workload."""
     kw = dict(budget_pct=cfg["budget"], coverage_threshold=tau, lazy=cfg["lazy"],
               selector=cfg["selector"], light_normalizer=cfg["light_normalizer"])
+    mode = cfg.get("budget_mode", "uniform")
+    if mode == "topp":
+        kw["top_p"] = 0.9
+    elif mode == "adaptive":
+        kw["adaptive_selection"] = True
+    elif mode == "static":
+        fr = [cfg["budget"] * STATIC_SCALE[h % len(STATIC_SCALE)] for h in range(cfg["H_kv"])]
+        kw["static_budget_table"] = {layer: fr for layer in range(128)}
     kw.update(dict(check_interval=cfg["M"]) if cfg["lazy"] else dict(reuse_interval=cfg["M"]))
     if cfg.get("approx") is not None:
         kw["approx_recovery_pct"] = cfg["approx"]
@@ -235,12 +254,15 @@ def build_layers(name, cfg, dev, n_layers, hot_shift, sink_shift, steps):
     return layers
 
 
-def step_bytes(kind, accept, cfg, W, budget):
+def step_bytes(kind, accept, cfg, W, budget, sel=None):
     """Algorithmic HBM bytes of one layer call (valid tokens only, each pass
-    reads its operands once; K+V counted once per KV head)."""
+    reads its operands once; K+V counted once per KV head).  sel: with
+    per-head budgets, (each head's selected pages before the call, after
+    it); else every head holds min(budget, n_valid)."""
     B, H, Hq, ctx = cfg["B"], cfg["H_kv"], cfg["H_q"], cfg["ctx"]
     n_valid = -(-ctx // BS)
     n_sel = min(budget, n_valid)
+    sel_prev, sel_new = ([n_sel] * (B * H),) * 2 if sel is None else sel
     page_kv = BS * D * 2            # one page of one head, K or V
     q_bytes = out_bytes = B * Hq * D * 2
     scores = B * H * W * 4
@@ -256,21 +278,21 @@ def step_bytes(kind, accept, cfg, W, budget):
         if (ln or ranks) and cfg["append"]:
             total += B * H * (page_kv + 2 * D * 2 + 4)                 # metadata refresh
     if kind in ("check", "rescore"):
-        total += scores + 4 * n_sel * B * H                           # coverage of cached sel
+        total += scores + 4 * sum(sel_prev)                           # coverage of cached sel
     if kind in ("score", "rescore"):
-        total += scores + 4 * n_sel * B * H                           # top-k select
+        total += scores + 4 * sum(sel_new)                            # top-k select
         if cfg.get("approx") is not None:
             # Approximate recovery: a rejected head reads its expanded
             # selection (which contains the draft's pages) instead of every
             # valid page.
             exp_n = min(min(max(budget + 1, int(W * cfg["approx"])), W), n_valid)
-            pages = sum(n_sel if a else exp_n for a in accept)
+            pages = sum(n if a else exp_n for n, a in zip(sel_new, accept))
         else:
-            pages = sum(n_sel if a else n_valid for a in accept)
+            pages = sum(n if a else n_valid for n, a in zip(sel_new, accept))
     elif kind == "dense":
         pages = n_valid * B * H
     else:
-        pages = n_sel * B * H
+        pages = sum(sel_new)
     total += pages * (2 * page_kv + 8) + q_bytes + out_bytes           # decode
     if cfg["append"]:
         total += B * H * D * 2 * 2 * 2                                 # token K/V read + write
@@ -448,6 +470,12 @@ def run_schedule(cfg, layers, tau, args, dev, count_read=True):
                    for _ in range(L)] for _ in range(total_steps)]
     backend = CVSABackend(H_kv, H_q, D, BS, num_layers=L, **backend_kwargs(cfg, tau))
     kinds = []        # (step, layer, kind, accept tensor or None)
+    per_head = cfg.get("budget_mode", "uniform") != "uniform"
+    sels = []         # per-head budgets: (selected pages per head before, after) per call
+
+    def selected(l):
+        cs = backend._cached_selection.get(l)
+        return None if cs is None else [int(x) for x in cs[1].flatten().tolist()]
 
     def run_step(s, record):
         for l, lay in enumerate(layers):
@@ -455,6 +483,7 @@ def run_schedule(cfg, layers, tau, args, dev, count_read=True):
             if record:  # reading the counters synchronises: classification pass only
                 had = l in backend._cached_selection
                 c0, s0 = backend._total_coverage_checks, backend._total_scoring_steps
+                before = selected(l) if per_head else None
             backend(queries[s][l], k, v, bt, cl, l)
             if record:
                 checked = backend._total_coverage_checks > c0
@@ -467,6 +496,9 @@ def run_schedule(cfg, layers, tau, args, dev, count_read=True):
                     kind = "check" if checked else "reuse"
                 kinds.append((s, l, kind, backend._last_accept_mask.get(l).clone()
                               if l in backend._last_accept_mask else None))
+                if per_head:
+                    after = selected(l)
+                    sels.append(None if after is None else (before or after, after))
             backend.step_done(l, L)
             if new_kv is not None:
                 lay.mgr.append_tokens_kv(*new_kv[s][l])
@@ -514,17 +546,17 @@ def run_schedule(cfg, layers, tau, args, dev, count_read=True):
     step_kinds = {}
     total_bytes = 0
     read = measured_step_bytes() if (count_read and cfg.get("profile_name") == "cfg3"
-                                     and cfg["selector"] == "exact"
+                                     and cfg["selector"] == "exact" and not per_head
                                      and cfg.get("approx") is None
                                      and not cfg.get("dense_layers")) else None
     read_bytes = 0 if read is not None else None
     accepted_heads = total_heads = 0
-    for s, l, kind, acc in kinds:
+    for i, (s, l, kind, acc) in enumerate(kinds):
         a = [True] * (B * H_kv) if acc is None else [bool(x) for x in acc.flatten().tolist()]
         if kind in ("score", "rescore"):
             accepted_heads += sum(a)
             total_heads += len(a)
-        total_bytes += step_bytes(kind, a, cfg, W, budget)
+        total_bytes += step_bytes(kind, a, cfg, W, budget, sels[i] if sels else None)
         if read_bytes is not None:
             read_bytes = read_bytes + read[kind] if kind in read else None
         if kind == "rescore" or s not in step_kinds or step_kinds[s] == "dense":
@@ -555,7 +587,13 @@ def main():
     from cvsa.ops import _lib
 
     cfg = dict(CONFIGS[args.config], selector=args.selector,
-               light_normalizer=args.light_normalizer, profile_name=args.config)
+               light_normalizer=args.light_normalizer, profile_name=args.config,
+               budget_mode=args.budget_mode)
+    if args.budget_mode != "uniform":
+        cfg["desc"] += {"topp": ", top-p 0.9 budgets", "adaptive": ", adaptive budgets",
+                        "static": ", static budget table (per-head fractions "
+                                  + "/".join(f"{x:g}" for x in STATIC_SCALE[:cfg["H_kv"]])
+                                  + " x budget)"}[args.budget_mode]
     if args.method is not None:
         cfg.update(parse_method(args.method))
         cfg["desc"] += f"; method {args.method}"

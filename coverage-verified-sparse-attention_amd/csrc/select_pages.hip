@@ -1739,6 +1739,21 @@ extern "C" int cvsa_select_or_keep(const float *page_scores, const float *sel_sc
                        coverage_out, check_accept, scores_cache, stats, count_gate, stream);
 }
 
+extern "C" int cvsa_select_or_keep_budgeted(
+    const float *page_scores, const float *sel_scores, const uint8_t *check_accept, int32_t B,
+    int32_t H_kv, int32_t W, const int32_t *context_lens, int32_t block_size,
+    const int32_t *row_budgets, int32_t width, int32_t *page_indices, int32_t *n_per_head,
+    float tau, uint8_t *accept_out, float *coverage_out, float *scores_cache, int64_t *stats,
+    int32_t count_gate, void *stream) {
+  CVSA_REQUIRE(accept_out && coverage_out && row_budgets, CVSA_ERR_INVALID,
+               "select_or_keep_budgeted: row_budgets, accept_out and coverage_out are "
+               "required");
+  return launch_select("select_or_keep_budgeted", page_scores, sel_scores, B, H_kv, W,
+                       context_lens, block_size, width, page_indices, n_per_head, tau,
+                       accept_out, coverage_out, check_accept, scores_cache, stats, count_gate,
+                       stream, kTable, 0.f, row_budgets);
+}
+
 namespace cvsa_internal {
 
 int select_for_plan(const float *page_scores, const float *sel_scores,

@@ -816,12 +816,15 @@ class CVSABackend:
         recovery, no counterfactual rejections, the cached selection and
         scores match this call's shape, counters live on this device."""
         if (self.random_reject_prob is not None or self.approx_recovery_pct is not None
-                or self.top_p is not None or self.static_budget_table is not None
-                or self.adaptive_selection):
+                or self.top_p is not None
+                or (self.adaptive_selection and self.static_budget_table is None)):
             return False
         page_indices, n_per_head = self._cached_selection[layer_idx]
         B, H_kv, W = page_scores.shape
-        budget = max(3, int(W * self.budget_pct))
+        if self._static_only():
+            budget = self._static_rows(layer_idx, B, W, page_scores.device)[1]
+        else:
+            budget = max(3, int(W * self.budget_pct))
         if (tuple(page_indices.shape) != (B, H_kv, budget) or not page_indices.is_contiguous()
                 or tuple(n_per_head.shape) != (B, H_kv) or not n_per_head.is_contiguous()):
             return False
@@ -849,10 +852,15 @@ class CVSABackend:
         sel_scores = self._sel_scores(q, k_cache, block_tables, context_lens, check_accept)
         if sel_scores is not None:
             self._last_rank_scores[layer_idx] = sel_scores
+        rows = None
+        if self._static_only():  # a new selection takes the table's budgets
+            rows = self._static_rows(layer_idx, page_scores.shape[0], page_scores.shape[2],
+                                     page_scores.device)[0]
         accept_mask = self._time_kernel(
             "coverage", ops.select_or_keep, page_scores, check_accept, budget, context_lens,
             self.block_size, self.tau, page_indices, n_per_head, coverage,
-            self._cached_page_scores.get(layer_idx), self._dev_stats, sel_scores=sel_scores)
+            self._cached_page_scores.get(layer_idx), self._dev_stats, sel_scores=sel_scores,
+            row_budgets=rows)
         self._last_accept_mask[layer_idx] = accept_mask
         output = self._time_kernel(
             "sparse_draft", ops.verified_decode, q, k_cache, v_cache, block_tables,
@@ -917,25 +925,31 @@ class CVSABackend:
         dev = page_scores.device
         budgeted = (self.top_p is not None or self.static_budget_table is not None
                     or self.adaptive_selection)
-        device_book = (not budgeted and not self.lazy and self.random_reject_prob is None
+        # A static table's budgets are known on the host, so its selection
+        # needs no host read either.
+        device_book = ((not budgeted or self._static_only()) and not self.lazy
+                       and self.random_reject_prob is None
                        and self.approx_recovery_pct is None
                        and self._ensure_dev_stats(dev) is not None)
-        if budgeted:
-            # Per-head budgets (:727-732), gate fused; budget becomes the
-            # largest one, as in the reference.
-            page_indices, n_per_head, accept_mask, budget = self._time_kernel(
-                "coverage", self._budgeted_select, page_scores, sel_scores, layer_idx,
-                context_lens, budget)
-        elif device_book:
+        if device_book:
             H = self.num_kv_heads
+            rows = None
+            if budgeted:
+                rows, budget = self._static_rows(layer_idx, B, n_pages, dev)
             page_indices = torch.empty(B, H, budget, dtype=torch.int32, device=dev)
             n_per_head = torch.empty(B, H, dtype=torch.int32, device=dev)
             coverage = torch.empty(B, H, dtype=torch.float32, device=dev)
             accept_mask = self._time_kernel(
                 "coverage", ops.select_or_keep, page_scores, None, budget, context_lens,
                 self.block_size, self.tau, page_indices, n_per_head, coverage, None,
-                self._dev_stats, count_gate=True, sel_scores=sel_scores)
+                self._dev_stats, count_gate=True, sel_scores=sel_scores, row_budgets=rows)
             self._per_head_total += B * H
+        elif budgeted:
+            # Per-head budgets (:727-732), gate fused; budget becomes the
+            # largest one, as in the reference.
+            page_indices, n_per_head, accept_mask, budget = self._time_kernel(
+                "coverage", self._budgeted_select, page_scores, sel_scores, layer_idx,
+                context_lens, budget)
         elif sel_scores is None:
             page_indices, n_per_head, accept_mask, _coverage = self._time_kernel(
                 "coverage", ops.select_topk, page_scores, budget, context_lens,
@@ -992,6 +1006,25 @@ class CVSABackend:
             self._h_total_scoring_steps += 1                                      # :859
         return output
 
+    def _static_only(self) -> bool:
+        """Per-head budgets from the static table alone (top-p takes
+        precedence over it, backend.py:727-736): budgets the host knows."""
+        return self.top_p is None and self.static_budget_table is not None
+
+    def _static_rows(self, layer_idx, B, W, device):
+        """The static table's budgets of this layer, [B, H_kv] int32 on the
+        device, and the largest (the selection's row width): clamp(round(
+        frac * P), 3, P) (backend.py:638), made once per shape."""
+        key = (layer_idx, B, W, device)
+        entry = self._table_budgets.get(key)
+        if entry is None:
+            fracs = self.static_budget_table[layer_idx]
+            per_head = torch.clamp((fracs * W).round().long(), min=3, max=W)      # :638
+            rows = per_head.to(torch.int32).view(1, -1).expand(B, -1).contiguous()
+            entry = (rows.to(device), int(per_head.max()))
+            self._table_budgets[key] = entry
+        return entry
+
     def _budgeted_select(self, page_scores, sel_scores, layer_idx, context_lens, base_budget):
         """_topp_select / _static_select / _adaptive_select (backend.py:
         522-681, in the reference's order of precedence, :727-736) with the
@@ -1013,16 +1046,8 @@ class CVSABackend:
                 sel_scores=sel_scores)
             max_budget = int(nph.max().item())   # :679, a host read as in the reference
             return idx[:, :, :max_budget].contiguous(), nph, acc, max_budget
-        B = page_scores.shape[0]
-        key = (layer_idx, B, W, page_scores.device)
-        entry = self._table_budgets.get(key)
-        if entry is None:
-            fracs = self.static_budget_table[layer_idx]
-            per_head = torch.clamp((fracs * W).round().long(), min=3, max=W)      # :638
-            rows = per_head.to(torch.int32).view(1, -1).expand(B, -1).contiguous()
-            entry = (rows.to(page_scores.device), int(per_head.max()))
-            self._table_budgets[key] = entry
-        budgets, max_budget = entry
+        budgets, max_budget = self._static_rows(layer_idx, page_scores.shape[0], W,
+                                                page_scores.device)
         idx, nph, acc, _cov = ops.select_budgeted(
             page_scores, context_lens, self.block_size, row_budgets=budgets, width=max_budget,
             tau=self.tau, sel_scores=sel_scores)

@@ -284,7 +284,8 @@ def select_or_keep(page_scores: torch.Tensor, check_accept: Optional[torch.Tenso
                    coverage: torch.Tensor, scores_cache: Optional[torch.Tensor] = None,
                    stats: Optional[torch.Tensor] = None,
                    count_gate: bool = False, *,
-                   sel_scores: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   sel_scores: Optional[torch.Tensor] = None,
+                   row_budgets: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The selection decisions of CVSABackend taken on the device.
 
     With ``check_accept`` (the coverage gate of the cached selection) this is
@@ -300,6 +301,10 @@ def select_or_keep(page_scores: torch.Tensor, check_accept: Optional[torch.Tenso
     With ``sel_scores`` a new selection ranks those scores while
     ``page_scores`` drive its gate and the cache (the Quest selector with the
     exact gate, backend.py:723-727).
+    With ``row_budgets`` ([B, H_kv] int32, e.g. a static table's,
+    backend.py:622-650) a new selection takes row (b, h)'s own budget, at
+    most ``budget``, the row width of ``page_indices``
+    (cvsa_select_or_keep_budgeted).
     Returns the accept mask [B, H_kv] bool of the heads for this step.
     """
     dev = _device_of(page_scores, check_accept, page_indices, n_per_head, coverage)
@@ -333,6 +338,18 @@ def select_or_keep(page_scores: torch.Tensor, check_accept: Optional[torch.Tenso
         sel_scores = sel_scores.contiguous()
     ctx = _i32(context_lens)
     acc = torch.empty(B, H_kv, device=dev, dtype=torch.uint8)
+    if row_budgets is not None:
+        if (row_budgets.dtype != torch.int32 or tuple(row_budgets.shape) != (B, H_kv)
+                or not row_budgets.is_contiguous() or row_budgets.device != dev):
+            raise ValueError(f"select_or_keep: row_budgets must be a contiguous int32 "
+                             f"[{B}, {H_kv}] on {dev}")
+        check(_lib.load().cvsa_select_or_keep_budgeted(
+            ps.data_ptr(), _ptr(sel_scores), _ptr(check_accept), B, H_kv, W, ctx.data_ptr(),
+            block_size, row_budgets.data_ptr(), budget, page_indices.data_ptr(),
+            n_per_head.data_ptr(), float(tau), acc.data_ptr(), coverage.data_ptr(),
+            _ptr(scores_cache), _ptr(stats), 1 if count_gate else 0, _stream(dev)),
+            "select_or_keep")
+        return acc.view(torch.bool)
     check(_lib.load().cvsa_select_or_keep(
         ps.data_ptr(), _ptr(sel_scores), _ptr(check_accept), B, H_kv, W, ctx.data_ptr(),
         block_size, budget,

@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parents[1] / "libcvsa_hip.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 CVSA_OK = 0
 CVSA_ERR_INVALID = -1
@@ -66,6 +66,9 @@ SIGNATURES = {
         _p, _i32, _i32, _i32, _p, _i32, _i32, _p, _p, _f32, _p, _p, _p]),
     "cvsa_select_or_keep": (ctypes.c_int, [
         _p, _p, _p, _i32, _i32, _i32, _p, _i32, _i32, _p, _p, _f32, _p, _p, _p, _p, _i32, _p]),
+    "cvsa_select_or_keep_budgeted": (ctypes.c_int, [
+        _p, _p, _p, _i32, _i32, _i32, _p, _i32, _p, _i32, _p, _p, _f32, _p, _p, _p, _p, _i32,
+        _p]),
     "cvsa_select_budgeted": (ctypes.c_int, [
         _p, _p, _i32, _i32, _i32, _p, _i32, _f32, _p, _i32, _p, _p, _f32, _p, _p, _p]),
     "cvsa_adaptive_budgets": (ctypes.c_int, [

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define CVSA_ABI_VERSION 13
+#define CVSA_ABI_VERSION 14
 
 enum {
   CVSA_OK = 0,
@@ -118,6 +118,28 @@ int cvsa_select_or_keep(const float *page_scores, const float *sel_scores,
                         int32_t *n_per_head, float tau, uint8_t *accept_out,
                         float *coverage_out, float *scores_cache,
                         int64_t *stats, int32_t count_gate, void *stream);
+
+/*
+ * cvsa_select_or_keep with a budget per (b, kv-head) row: the lazy check
+ * (and the fixed-interval scoring step's booking) of the static-table
+ * branch of CVSABackend (_static_select, cvsa/backend.py:622-650, whose
+ * budgets the host knows), or of any per-row budgets computed beforehand,
+ * taken on the device.  The keep decision, counters, scores_cache and
+ * sel_scores are those of cvsa_select_or_keep; a new selection is that of
+ * cvsa_select_budgeted with these row_budgets ([B*H_kv] int32, each
+ * clamped to [1, W]) and rows of `width` entries (the row stride of
+ * page_indices; a budget above it is clamped to it), with its coverage
+ * gate.  No counterpart of its own in the reference, whose lazy step reads
+ * the accept mask on the host (backend.py:440-446).
+ */
+int cvsa_select_or_keep_budgeted(const float *page_scores, const float *sel_scores,
+                                 const uint8_t *check_accept, int32_t B, int32_t H_kv,
+                                 int32_t W, const int32_t *context_lens, int32_t block_size,
+                                 const int32_t *row_budgets, int32_t width,
+                                 int32_t *page_indices, int32_t *n_per_head, float tau,
+                                 uint8_t *accept_out, float *coverage_out,
+                                 float *scores_cache, int64_t *stats, int32_t count_gate,
+                                 void *stream);
 
 /*
  * Selection with a budget per (b, kv-head) row.  Replaces the top-p branch

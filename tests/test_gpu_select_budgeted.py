@@ -199,6 +199,63 @@ def test_select_budgeted_rejects_bad_arguments(gpu):
                                                                 device=gpu))
 
 
+@pytest.mark.parametrize("sep", [False, True])
+def test_select_or_keep_row_budgets(gpu, sep):
+    """cvsa_select_or_keep_budgeted: keep the cached selection when every
+    head passed; else the selection of select_budgeted with the same row
+    budgets and width (budgets above the width clamped), with its gate,
+    the scores cache and the counters of select_or_keep; and a fresh
+    selection booked by its own gate."""
+    B, H, W, width = 2, 4, 3000, 800
+    valid = [W, 1100]
+    g = torch.Generator().manual_seed(31 + sep)
+    ps = _scores(B, H, W, valid, seed=41 + sep, temp=2.0)
+    rank = ps + 0.4 * torch.randn(B, H, W, generator=g) if sep else None
+    if rank is not None:
+        rank[ps == float("-inf")] = float("-inf")
+    ctx = _ctx_for(W, valid)
+    rows = torch.tensor([[3, 200, 700, 50], [1000, 3, 10, 3000]], dtype=torch.int32)
+    d = dict(sel_scores=None if rank is None else rank.to(gpu))
+    sel0 = torch.randint(0, W, (B, H, width), generator=g).to(torch.int32)
+    nph0 = torch.randint(0, width, (B, H), generator=g).to(torch.int32)
+    d_sel, d_nph = sel0.to(gpu), nph0.to(gpu)
+    old = torch.randn(B, H, W, generator=g)
+    d_cache = old.to(gpu)
+    cov = torch.full((B, H), -7.0, device=gpu)
+    stats = torch.zeros(6, dtype=torch.int64, device=gpu)
+    check = torch.ones(B, H, dtype=torch.bool, device=gpu)
+    acc = ops.select_or_keep(ps.to(gpu), check, width, ctx.to(gpu), 16, 0.9, d_sel, d_nph, cov,
+                             d_cache, stats, row_budgets=rows.to(gpu), **d)
+    assert bool(acc.all())
+    assert torch.equal(d_sel.cpu(), sel0) and torch.equal(d_nph.cpu(), nph0)
+    assert torch.equal(d_cache.cpu(), old) and stats.tolist() == [1, 0, 0, B * H, 0, 0]
+    check[1, 2] = False
+    acc = ops.select_or_keep(ps.to(gpu), check, width, ctx.to(gpu), 16, 0.9, d_sel, d_nph, cov,
+                             d_cache, stats, row_budgets=rows.to(gpu), **d)
+    widx, wnph, wacc, wcov = ops.select_budgeted(ps.to(gpu), ctx.to(gpu), 16,
+                                                 row_budgets=rows.to(gpu), width=width, tau=0.9,
+                                                 **d)
+    assert torch.equal(d_nph.cpu(), wnph.cpu())
+    for b in range(B):
+        for h in range(H):
+            n = int(wnph[b, h])
+            assert n == min(int(rows[b, h]), width, valid[b])
+            assert torch.equal(d_sel[b, h, :n].cpu(), widx[b, h, :n].cpu()), (b, h)
+    assert torch.equal(acc, wacc) and torch.equal(cov, wcov)
+    assert torch.equal(d_cache.cpu(), ps)
+    assert stats.tolist() == [1, 1, 1, 2 * B * H - 1, 0, 0]
+    sel3, nph3, cov3 = torch.empty_like(d_sel), torch.empty_like(d_nph), torch.empty_like(cov)
+    acc3 = ops.select_or_keep(ps.to(gpu), None, width, ctx.to(gpu), 16, 0.9, sel3, nph3, cov3,
+                              None, stats, count_gate=True, row_budgets=rows.to(gpu), **d)
+    assert torch.equal(nph3, wnph) and torch.equal(acc3, wacc)
+    n_acc = int(acc3.sum())
+    all_acc = int(n_acc == B * H)
+    assert stats.tolist() == [1 + all_acc, 2 - all_acc, 2, 2 * B * H - 1 + n_acc, 0, 0]
+    with pytest.raises(ValueError):
+        ops.select_or_keep(ps.to(gpu), check, width, ctx.to(gpu), 16, 0.9, d_sel, d_nph, cov,
+                           row_budgets=rows.to(gpu).to(torch.int64))
+
+
 CFG = dict(batch=2, num_q_heads=32, num_kv_heads=8, head_dim=128, context_len=[5000, 2600],
            hot_heads=[0, 3, 6], n_hot=8, hot_shift=10.0)
 
@@ -215,6 +272,8 @@ CFG = dict(batch=2, num_q_heads=32, num_kv_heads=8, head_dim=128, context_len=[5
          coverage_threshold=0.9, lazy=True, check_interval=3),
     dict(static_budget_table={0: [0.2] * 4 + [0.1] * 4}, coverage_threshold=0.9, lazy=False,
          reuse_interval=2),
+    dict(static_budget_table={0: [0.05, 0.3, 0.1, 0.2, 0.15, 0.1, 0.25, 0.05]},
+         coverage_threshold=0.9, lazy=True, check_interval=2, selector="quest"),
     dict(adaptive_selection=True, coverage_threshold=0.9, lazy=True, check_interval=3),
     dict(adaptive_selection=True, adaptive_floor_ratio=0.2, coverage_threshold=0.8,
          lazy=False, reuse_interval=2, selector="quest"),
