@@ -895,11 +895,25 @@ __device__ __forceinline__ void ident_first_pages(const DecodeArgs &a, int split
   phys = tile_block(a, bh / a.H_kv, lp, ts);
 }
 
+// Tiles per split of a listed walk over n tiles: the launch's a.pps (sized
+// on the host by its largest head, max_sel pages) for a head of max_sel
+// pages, whose first entries were requested at split * a.pps before its
+// count arrived; a shorter head (a per-head budget, a short context) sizes
+// its splits by its own count over the launch's n_splits (a multiple of NW,
+// at least kMinPagesPerWg pages), so its pages spread over every split
+// instead of the first n / a.pps.  ceil(n / pps) <= n_splits either way.
+template <int NW>
+__device__ __forceinline__ int listed_pps(const DecodeArgs &a, int n, int ts) {
+  if (n >= (a.max_sel << ts)) return a.pps;
+  const int per = (n + a.n_splits - 1) / a.n_splits;
+  return max((per + NW - 1) / NW * NW, kMinPagesPerWg << ts);
+}
+
 // Listed pages of a head (the sparse decode of reuse steps, and verified
 // launches whose heads are all accepted): split s of head bh walks listed
-// pages [s * pps, (s + 1) * pps) of bh; splits past a head's pages only take
-// part when the head is empty (split 0 writes its outputs).  Partial row of
-// (split, head) = head * n_splits + split.
+// pages [s * pps, (s + 1) * pps) of bh (pps: listed_pps); splits past a
+// head's pages only take part when the head is empty (split 0 writes its
+// outputs).  Partial row of (split, head) = head * n_splits + split.
 // With APP, the walk's sequence appends token nt in this launch: the
 // context length is nt's page * 16 + row + 1 (16-token pages), and nt's page
 // reads that row from nt's rows (Engine::fetch_new) and, when the append
@@ -920,9 +934,7 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
   const int h = bh - b * a.H_kv;
   const int ctx = APP ? nt.page * kPageTokens + nt.off + 1
                       : __builtin_amdgcn_readfirstlane(a.ctx_lens[b]);
-  const int pps = IDENT ? a.pps_all : a.pps;
   const int n_spl = IDENT ? a.n_splits_all : a.n_splits;
-  const int r0 = split * pps;
   const int32_t *idx_row = a.page_idx + (int64_t)bh * a.idx_stride;
   const int ts = Engine::tshift(a);
   const int tl = Engine::tlog(a);
@@ -931,6 +943,11 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
   const int n = IDENT ? max(0, min(valid_pages_sh(ctx, tl + ts), a.W)) << ts
                       : min(max(__builtin_amdgcn_readfirstlane(a.n_pages[bh]), 0), a.max_sel)
                             << ts;
+  const int pps = IDENT ? a.pps_all : listed_pps<NW>(a, n, ts);
+  // The first entries (spec_lp, spec_phys) were requested at split * a.pps:
+  // a head with splits of its own size requests them again.
+  const bool refetch = !IDENT && pps != a.pps;  // uniform
+  const int r0 = split * pps;
   const int r1 = min(n, r0 + pps);
   const int n_act = (n + pps - 1) / pps;  // splits holding pages of this head
   if (r0 >= r1 && !(split == 0 && n_act == 0)) return;  // uniform
@@ -954,12 +971,13 @@ __device__ __forceinline__ void listed_walk(const DecodeArgs &a, int split, int 
     const int cn = min(kWave, npw - c0);
     int my_phys = 0, my_ntok = 0, my_new = -1, my_lt = -1;
     if (lane < cn) {
-      const int lt = c0 == 0 ? spec_lp
+      const bool spec = c0 == 0 && !refetch;
+      const int lt = spec ? spec_lp
                      : IDENT ? r0 + wave + NW * (c0 + lane)
                              : listed_tile(a, idx_row, r0 + wave + NW * (c0 + lane), ts);
       if (lt >= 0 && lt < (a.W << ts)) {
         my_lt = lt;
-        int pt = c0 == 0 ? spec_phys : tile_block(a, b, lt, ts);
+        int pt = spec ? spec_phys : tile_block(a, b, lt, ts);
         if (APP && lt == nt.page && nt.new_blk >= 0) pt = nt.new_blk;
         if (pt >= 0 && pt < (a.num_blocks << ts)) {
           my_phys = pt;
