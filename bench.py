@@ -513,15 +513,22 @@ def run_schedule(cfg, layers, tau, args, dev, count_read=True):
     backend.reset()
     for lay in layers:
         lay.restore()
-    log("warmup")
-    for s in range(args.warmup):
-        run_step(s, False)
-    torch.cuda.synchronize()
-    log("timed steps")
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    torch.cuda.synchronize()
+    # The collector runs (and is then kept off) before the warmup, not
+    # between the warmup and the timed steps: a full collection walks the
+    # whole Python heap and leaves the host's caches cold, and the first
+    # launches after it take ~100 us each of host time (measured on the GPU
+    # box), which the idle GPU would wait out inside the timed region.
     with no_gc():
+        log("warmup")
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)]
+        for a, e in evs:  # a torch event makes its HIP event at its first record
+            a.record()
+            e.record()
+        for s in range(args.warmup):
+            run_step(s, False)
+        torch.cuda.synchronize()
+        log("timed steps")
         t0 = time.perf_counter()
         host_each = []
         for i in range(args.steps):

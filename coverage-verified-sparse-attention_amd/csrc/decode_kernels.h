@@ -31,7 +31,14 @@
 // before its relaxed agent-scope atomic increment of the head's counter; the
 // last arriver issues its partial loads only after that atomic has
 // returned.  This rests on the gfx950 cache policy described, not on the
-// HIP memory model's release / acquire pairing.
+// HIP memory model's release / acquire pairing.  Building with
+// -DCVSA_FORMAL_HANDOFF=1 replaces it with that pairing (an agent-scope
+// release fence in every thread before the counter, an acq_rel counter
+// increment, an agent-scope acquire fence in the last arriver): the same
+// bits, but the L2 writeback and invalidate those fences compile to cost
+// the cfg3 listed decode 31.5 us against 19.3 us (one rejected head 67 vs
+// 37 us, dense 135 vs 96 us), so the default build keeps the cache-policy
+// protocol.
 //
 // Head modes: a listed head walks page_indices[b,h,:n_per_head]; an
 // all-pages head walks pages 0..n_valid-1 (dense decode).  In verified mode
@@ -722,6 +729,34 @@ struct MfmaEngine {
   }
 };
 
+// The split hand-off's three steps.  publish_partials: every thread's
+// partial-row stores complete before the workgroup's counter moves;
+// handoff_count: thread 0 bumps the counter and returns its old value;
+// acquire_partials: the last arriver's partial loads come after it.
+#ifndef CVSA_FORMAL_HANDOFF
+#define CVSA_FORMAL_HANDOFF 0
+#endif
+__device__ __forceinline__ void publish_partials() {
+#if CVSA_FORMAL_HANDOFF
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+#else
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#endif
+  __syncthreads();
+}
+__device__ __forceinline__ unsigned handoff_count(unsigned *ctr) {
+#if CVSA_FORMAL_HANDOFF
+  return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#endif
+}
+__device__ __forceinline__ void acquire_partials() {
+#if CVSA_FORMAL_HANDOFF
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+#endif
+}
+
 template <class L, int NW>
 __device__ __forceinline__ L &s_eng_of(L (&eng)[NW], int wave) { return eng[wave]; }
 
@@ -790,9 +825,7 @@ __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const Part
     pb.store4(my_off + g * kPartStride + d0, O);
     if (d0 == 0) pb.store2(my_off + g * kPartStride + D, f32x2{M, L});
   }
-  // Every wave's partial stores have completed before the counter moves.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  publish_partials();
   constexpr uint32_t kRowElems = (uint32_t)(G * kPartStride);
   if (TWO && n_act > kTwoLevelMin) {  // uniform
     const int i = (int)(my_row - first_row);
@@ -802,27 +835,19 @@ __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const Part
     const int ng = (n_act + kMergeGroup - 1) / kMergeGroup;
     const uint32_t w0 = first_row - (uint32_t)h + (uint32_t)g0;  // the group's first workgroup
     unsigned *gc = a.counters + kMaxHeads + 2 * w0 + (gi != 0 ? 1 : 0);
-    if (threadIdx.x == 0) {
-      const unsigned prev = __hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-      s_last = prev == (unsigned)(gsize - 1);
-    }
+    if (threadIdx.x == 0) s_last = handoff_count(gc) == (unsigned)(gsize - 1);
     __syncthreads();
     if (!s_last) return;  // uniform
+    acquire_partials();
     if (threadIdx.x == 0)
       __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t grow = (first_row + (uint32_t)g0) * kRowElems;
     merge_partials<G, D, NT, KB, true>(a, pb, grow, gsize, h, 0, 0, s_merge, 1, grow);
-    // The group row's stores have completed before the head's counter moves.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const unsigned prev = __hip_atomic_fetch_add(&a.counters[h], 1u, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-      s_last = prev == (unsigned)(ng - 1);
-    }
+    publish_partials();
+    if (threadIdx.x == 0) s_last = handoff_count(&a.counters[h]) == (unsigned)(ng - 1);
     __syncthreads();
     if (s_last) {
+      acquire_partials();
       if (threadIdx.x == 0)
         __hip_atomic_store(&a.counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       merge_partials<G, D, NT, KB>(a, pb, first_row * kRowElems, ng, h, n, nv, s_merge,
@@ -830,13 +855,10 @@ __device__ __forceinline__ void segment_epilogue(const DecodeArgs &a, const Part
     }
     return;
   }
-  if (threadIdx.x == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(&a.counters[h], 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (unsigned)(n_act - 1);
-  }
+  if (threadIdx.x == 0) s_last = handoff_count(&a.counters[h]) == (unsigned)(n_act - 1);
   __syncthreads();
   if (s_last) {
+    acquire_partials();
     // Last contributor of the head: merge its partials, write the outputs.
     if (threadIdx.x == 0)
       __hip_atomic_store(&a.counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
