@@ -119,6 +119,30 @@ def _block_tables(bt: torch.Tensor) -> torch.Tensor:
     return bt
 
 
+def _check_seqs(who: str, B: int, block_tables=None, context_lens=None) -> None:
+    """The per-sequence inputs of a call over B sequences: block_tables
+    [B, W] and context_lens [B].  The kernels index them by sequence, so a
+    shorter tensor would be read past its end on the device."""
+    if block_tables is not None and (block_tables.dim() != 2 or block_tables.shape[0] != B):
+        raise ValueError(f"{who}: block_tables must be [{B}, W], got "
+                         f"{tuple(block_tables.shape)}")
+    if context_lens is not None and (context_lens.dim() != 1 or context_lens.shape[0] != B):
+        raise ValueError(f"{who}: context_lens must be [{B}], got {tuple(context_lens.shape)}")
+
+
+def _check_count(who: str, name: str, t, n: int) -> None:
+    """t (if given) holds exactly n entries: one per row the kernel reads."""
+    if t is not None and t.numel() != n:
+        raise ValueError(f"{who}: {name} must hold {n} entries, got {t.numel()}")
+
+
+def _check_rows(who: str, name: str, t, rows: int, min_cols: int) -> None:
+    """t (if given) is [rows, >= min_cols]: one row per (sequence, KV head)."""
+    if t is not None and (t.dim() != 2 or t.shape[0] != rows or t.shape[1] < min_cols):
+        raise ValueError(f"{who}: {name} must be [{rows}, >= {min_cols}], got "
+                         f"{tuple(t.shape)}")
+
+
 _WORKSPACES: dict = {}
 
 
@@ -154,6 +178,7 @@ def score_pages(q: torch.Tensor, k_cache: torch.Tensor, block_tables: torch.Tens
     bt = _block_tables(block_tables)
     ctx = _i32(context_lens)
     B, H_q, D = q.shape
+    _check_seqs("score_pages", B, bt, ctx)
     if num_kv_heads * num_q_per_kv != H_q or k_cache.shape[2] != num_kv_heads:
         raise ValueError("score_pages: head counts do not match q / k_cache")
     if k_cache.shape[1] != block_size or k_cache.shape[3] != D:
@@ -184,6 +209,7 @@ def select_topk(page_scores: torch.Tensor, budget: int, context_lens: torch.Tens
     ps = page_scores.contiguous()
     ctx = _i32(context_lens)
     B, H_kv, W = ps.shape
+    _check_seqs("select_topk", B, None, ctx)
     if not 1 <= budget <= W:
         raise ValueError(f"select_topk: budget {budget} must be in [1, {W}]")
     idx = torch.empty(B, H_kv, budget, device=dev, dtype=torch.int32)
@@ -240,6 +266,7 @@ def select_budgeted(page_scores: torch.Tensor, context_lens: torch.Tensor, block
     if not 1 <= width <= W:
         raise ValueError(f"select_budgeted: width {width} must be in [1, {W}]")
     ctx = _i32(context_lens)
+    _check_seqs("select_budgeted", B, None, ctx)
     idx = torch.empty(B, H_kv, width, device=dev, dtype=torch.int32)
     nph = torch.empty(B, H_kv, device=dev, dtype=torch.int32)
     acc = cov = None
@@ -271,6 +298,7 @@ def adaptive_budgets(sel_scores: torch.Tensor, base_budget: int, context_lens: t
     if base_budget < 1:
         raise ValueError("adaptive_budgets: base_budget must be >= 1")
     ctx = _i32(context_lens)
+    _check_seqs("adaptive_budgets", B, None, ctx)
     out = torch.empty(B, H_kv, device=dev, dtype=torch.int32)
     check(_lib.load().cvsa_adaptive_budgets(
         ss.data_ptr(), B, H_kv, W, ctx.data_ptr(), block_size, int(base_budget),
@@ -337,6 +365,7 @@ def select_or_keep(page_scores: torch.Tensor, check_accept: Optional[torch.Tenso
             raise ValueError("select_or_keep: sel_scores must be float32 like page_scores")
         sel_scores = sel_scores.contiguous()
     ctx = _i32(context_lens)
+    _check_seqs("select_or_keep", B, None, ctx)
     acc = torch.empty(B, H_kv, device=dev, dtype=torch.uint8)
     if row_budgets is not None:
         if (row_budgets.dtype != torch.int32 or tuple(row_budgets.shape) != (B, H_kv)
@@ -408,7 +437,10 @@ def quest_meta_update(k_cache: torch.Tensor, block_tables: torch.Tensor,
     nb, bs, H, D = k_cache.shape
     bt = _block_tables(block_tables)
     ctx = _i32(context_lens)
+    if bt.dim() != 2:
+        raise ValueError(f"quest_meta_update: block_tables must be [B, W], got {tuple(bt.shape)}")
     B, W = bt.shape
+    _check_seqs("quest_meta_update", B, bt, ctx)
     check(_lib.load().cvsa_quest_meta_update(
         k_cache.data_ptr(), nb, bt.data_ptr(), bt.stride(0), ctx.data_ptr(), B, H, D, bs, W,
         meta.data_ptr(), meta_ntok.data_ptr(), _stream(dev)), "quest_meta_update")
@@ -427,6 +459,7 @@ def quest_scores(q: torch.Tensor, meta: torch.Tensor, block_tables: torch.Tensor
     _check_meta(meta, num_kv_heads, D)
     bt = _block_tables(block_tables)
     ctx = _i32(context_lens)
+    _check_seqs("quest_scores", B, bt, ctx)
     W = bt.shape[1]
     out = torch.empty(B, num_kv_heads, W, device=dev, dtype=torch.float32)
     check(_lib.load().cvsa_quest_scores(
@@ -461,6 +494,7 @@ def quest_refresh_scores(q: torch.Tensor, k_cache: torch.Tensor, block_tables: t
         raise ValueError("quest_refresh_scores: head counts do not match q / k_cache")
     bt = _block_tables(block_tables)
     ctx = _i32(context_lens)
+    _check_seqs("quest_refresh_scores", B, bt, ctx)
     W = bt.shape[1]
     if check_accept is not None and (check_accept.shape != (B, num_kv_heads)
                                      or check_accept.dtype != torch.bool
@@ -565,6 +599,14 @@ def prepare_decode(kind: str, q, k_cache, v_cache, block_tables, context_lens, n
     bt = _block_tables(block_tables)
     ctx = _i32(context_lens)
     B, H_q, D = q.shape
+    _check_seqs(kind, B, bt, ctx)
+    rows = B * num_kv_heads
+    if pi_flat is not None:
+        _check_rows(kind, "page_indices", pi_flat, rows, max_sel)
+        _check_count(kind, "n_per_head", nph_flat, rows)
+    _check_count(kind, "accept_mask", accept, rows)
+    if exp_flat is not None:
+        _check_rows(kind, "exp_indices", exp_flat, rows, exp_budget)
     if num_kv_heads * num_q_per_kv != H_q or k_cache.shape[2] != num_kv_heads:
         raise ValueError(f"{kind}: head counts do not match q / caches")
     if k_cache.shape[1] != block_size or k_cache.shape[3] != D:
@@ -705,6 +747,7 @@ class StepPlan:
             raise ValueError("step plan: block_tables must be int32 [B, W] with unit page "
                              "stride and context_lens contiguous int32")
         B, H_q, D = q.shape
+        _check_seqs("step plan", B, block_tables, context_lens)
         H = num_kv_heads
         if H * num_q_per_kv != H_q or k_cache.shape[2] != H:
             raise ValueError("step plan: head counts do not match q / caches")
@@ -964,6 +1007,13 @@ def sparse_decode_append(q, k_cache, v_cache, block_tables, context_lens, page_i
         if t.dtype != torch.int32 or not t.is_contiguous():
             raise ValueError(f"sparse_decode_append: {name} must be contiguous int32")
     B, H_q, D = q.shape
+    who = "sparse_decode_append"
+    _check_seqs(who, B, block_tables, context_lens)
+    _check_pages_allocated(who, pages_allocated, B, dev)
+    _check_rows(who, "page_indices", pi, B * num_kv_heads, k)
+    _check_count(who, "n_per_head", nph, B * num_kv_heads)
+    if num_kv_heads * num_q_per_kv != H_q or k_cache.shape[2] != num_kv_heads:
+        raise ValueError(f"{who}: head counts do not match q / caches")
     if k_cache.shape[1] != block_size or k_cache.shape[3] != D:
         raise ValueError("sparse_decode_append: cache block_size / head_dim mismatch")
     _check_new_rows("sparse_decode_append", k_new, v_new, (B, num_kv_heads, D), dev)
@@ -1112,6 +1162,8 @@ def compute_complement(page_indices, n_per_head, context_lens, block_size, accep
     pi = _i32(page_indices).reshape(B * H, k)
     nph = _i32(n_per_head).reshape(B * H)
     ctx = _i32(context_lens)
+    _check_seqs("compute_complement", B, None, ctx)
+    _check_count("compute_complement", "accept_mask", accept_mask, B * H)
     if width is None:
         width = int(((ctx.max().item() - 1) // block_size) + 1)
         width = max(width, 1)
@@ -1137,6 +1189,11 @@ def lse_merge(o_draft, m_draft, l_draft, o_comp, m_comp, l_comp, accept_mask, nu
     B, H_q, D = o_draft.shape
     if num_kv_heads * num_q_per_kv != H_q:
         raise ValueError("lse_merge: head counts do not match")
+    _check_count("lse_merge", "o_comp", o_comp, B * H_q * D)
+    for name, t in (("m_draft", m_draft), ("l_draft", l_draft), ("m_comp", m_comp),
+                    ("l_comp", l_comp)):
+        _check_count("lse_merge", name, t, B * H_q)
+    _check_count("lse_merge", "accept_mask", accept_mask, B * num_kv_heads)
     f32 = lambda t: t.to(torch.float32).contiguous()
     od, md, ld, oc, mc, lc = map(f32, (o_draft, m_draft, l_draft, o_comp, m_comp, l_comp))
     acc = accept_mask.view(torch.uint8) if accept_mask.dtype == torch.bool else accept_mask
@@ -1173,6 +1230,12 @@ def append_kv(k_new, v_new, k_cache, v_cache, block_tables, context_lens, pages_
     n = k_new.shape[0]
     if not 1 <= n <= 1024:
         raise ValueError(f"append_kv: {n} sequences per call (1..1024 supported)")
+    batch = block_tables.shape[0] if block_tables.dim() == 2 else -1
+    _check_seqs("append_kv", batch, block_tables, context_lens)
+    _check_count("append_kv", "pages_allocated", pages_allocated, batch)
+    if not (0 <= seq_begin and seq_begin + n <= batch):
+        raise ValueError(f"append_kv: sequences [{seq_begin}, {seq_begin + n}) outside the "
+                         f"batch of {batch}")
     H_kv, D = k_cache.shape[2], k_cache.shape[3]
     kn = k_new.to(torch.bfloat16).reshape(n, H_kv * D).contiguous()
     vn = v_new.to(torch.bfloat16).reshape(n, H_kv * D).contiguous()
@@ -1207,7 +1270,9 @@ class AppendCall:
             if t.dtype != torch.int32 or not t.is_contiguous():
                 raise ValueError(f"append_kv: {name} must be contiguous int32")
         self.H_kv, self.D = k_cache.shape[2], k_cache.shape[3]
-        self.batch = block_tables.shape[0]
+        self.batch = block_tables.shape[0] if block_tables.dim() == 2 else -1
+        _check_seqs("append_kv", self.batch, block_tables, context_lens)
+        _check_count("append_kv", "pages_allocated", pages_allocated, self.batch)
         self.fn = _lib.load().cvsa_append_kv
         self.args = [0, 0, self.H_kv * self.D, k_cache.data_ptr(), v_cache.data_ptr(),
                      k_cache.shape[0], block_tables.data_ptr(), block_tables.stride(0),

@@ -134,3 +134,90 @@ def test_run_reuse_append_refuses_bad_slot_errors(errors):
     out = p.run_reuse_append(q, slots_dev=torch.zeros(B, 2, dtype=torch.int32),
                              slot_errors=torch.zeros(1, dtype=torch.int32), **_good())
     assert out.shape == (B, H_KV * G, D) and len(calls) == 1 and calls[0][9] is not None
+
+
+# ---------------------------------------------------------------- batch shapes
+#
+# Every op's kernel indexes block_tables, context_lens, selections and masks
+# by sequence and (sequence, KV head); a tensor shorter than the call's batch
+# would be read or written past its end on the device.  Each op refuses such
+# a call with ValueError before anything native runs: the fixture below
+# lets the ops see CPU tensors and turns any native call into a failure.
+
+NB, BS = 8, 16
+
+
+@pytest.fixture
+def host_only(monkeypatch):
+    def no_native(*a, **k):
+        raise AssertionError("reached the native library")
+    monkeypatch.setattr(ops, "_device_of", lambda *t: torch.device("cpu"))
+    monkeypatch.setattr(ops._lib, "load", no_native)
+    monkeypatch.setattr(ops, "_stream", lambda dev: 0)
+    monkeypatch.setattr(ops, "_workspace", lambda dev, n: None)
+
+
+def _inp(b=B, w=6):
+    q = torch.zeros(b, H_KV * G, D, dtype=torch.bfloat16)
+    kc = torch.zeros(NB, BS, H_KV, D, dtype=torch.bfloat16)
+    bt = torch.zeros(b, w, dtype=torch.int32)
+    ctx = torch.full((b,), 40, dtype=torch.int32)
+    sel = torch.zeros(b, H_KV, 3, dtype=torch.int32)
+    nph = torch.full((b, H_KV), 3, dtype=torch.int32)
+    acc = torch.ones(b, H_KV, dtype=torch.bool)
+    ps = torch.zeros(b, H_KV, w, dtype=torch.float32)
+    return q, kc, bt, ctx, sel, nph, acc, ps
+
+
+def _short(t):
+    return t[:-1]
+
+
+BATCH_CASES = {
+    "score_pages/block_tables": lambda q, kc, bt, ctx, sel, nph, acc, ps: ops.score_pages(
+        q, kc, _short(bt), ctx, H_KV, G, BS),
+    "score_pages/context_lens": lambda q, kc, bt, ctx, sel, nph, acc, ps: ops.score_pages(
+        q, kc, bt, _short(ctx), H_KV, G, BS),
+    "select_topk/context_lens": lambda q, kc, bt, ctx, sel, nph, acc, ps: ops.select_topk(
+        ps, 3, _short(ctx), BS),
+    "select_or_keep/context_lens": lambda q, kc, bt, ctx, sel, nph, acc, ps: ops.select_or_keep(
+        ps, acc, 3, _short(ctx), BS, 0.9, sel, nph, torch.zeros(B, H_KV)),
+    "select_budgeted/context_lens": lambda q, kc, bt, ctx, sel, nph, acc, ps:
+        ops.select_budgeted(ps, _short(ctx), BS, top_p=0.5),
+    "sparse_decode/page_indices": lambda q, kc, bt, ctx, sel, nph, acc, ps: ops.sparse_decode(
+        q, kc, kc, bt, _short(sel), _short(nph), ctx, H_KV, G, BS),
+    "dense_decode/context_lens": lambda q, kc, bt, ctx, sel, nph, acc, ps: ops.dense_decode(
+        q, kc, kc, bt, _short(ctx), H_KV, G, BS),
+    "verified_decode/accept_mask": lambda q, kc, bt, ctx, sel, nph, acc, ps:
+        ops.verified_decode(q, kc, kc, bt, ctx, sel, nph, _short(acc), H_KV, G, BS),
+    "verified_decode/block_tables": lambda q, kc, bt, ctx, sel, nph, acc, ps:
+        ops.verified_decode(q, kc, kc, _short(bt), ctx, sel, nph, acc, H_KV, G, BS),
+    "verified_decode_approx/exp_indices": lambda q, kc, bt, ctx, sel, nph, acc, ps:
+        ops.prepare_decode("verified_decode_approx", q, kc, kc, bt, ctx, H_KV, G, BS,
+                           sel.reshape(B * H_KV, 3), nph.reshape(-1), 3,
+                           accept=acc.view(torch.uint8).reshape(-1),
+                           exp_flat=torch.zeros(B * H_KV - 1, 4, dtype=torch.int32),
+                           exp_budget=4),
+    "sparse_decode_reuse/n_per_head": lambda q, kc, bt, ctx, sel, nph, acc, ps:
+        ops.sparse_decode_reuse(q, kc, kc, bt, ctx, sel.reshape(B * H_KV, 3),
+                                nph.reshape(-1)[:-1], 4, H_KV, G, BS),
+    "compute_complement/context_lens": lambda q, kc, bt, ctx, sel, nph, acc, ps:
+        ops.compute_complement(sel, nph, _short(ctx), BS, acc, width=6),
+    "lse_merge/m_comp": lambda q, kc, bt, ctx, sel, nph, acc, ps: ops.lse_merge(
+        torch.zeros(B, H_KV * G, D), torch.zeros(B, H_KV * G), torch.ones(B, H_KV * G),
+        torch.zeros(B, H_KV * G, D), torch.zeros(B - 1, H_KV * G), torch.ones(B, H_KV * G),
+        acc, H_KV, G),
+    "append_kv/batch": lambda q, kc, bt, ctx, sel, nph, acc, ps: ops.append_kv(
+        torch.zeros(2, H_KV, D, dtype=torch.bfloat16), torch.zeros(2, H_KV, D, dtype=torch.bfloat16),
+        kc, kc, bt, ctx, torch.zeros(B, dtype=torch.int32), B - 1, NB, BS),
+    "step_plan/block_tables": lambda q, kc, bt, ctx, sel, nph, acc, ps: ops.StepPlan(
+        q, kc, kc, _short(bt), ctx, H_KV, G, BS, 3, 0.9),
+}
+
+
+@pytest.mark.parametrize("case", sorted(BATCH_CASES))
+def test_ops_refuse_inputs_shorter_than_the_batch(host_only, case):
+    """The refusal names the short argument (and not some other check)."""
+    arg = case.split("/")[1]
+    with pytest.raises(ValueError, match=arg):
+        BATCH_CASES[case](*_inp())
