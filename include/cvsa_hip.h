@@ -8,7 +8,10 @@
  *  - The paged cache layout is the reference's: k_cache / v_cache are
  *    [num_blocks, block_size, H_kv, D] bf16, fully contiguous
  *    (cvsa/runtime/kv_cache.py:40-47).  block_tables are [B, >=W] int32 with
- *    unit stride along pages; context_lens are [B] int32.
+ *    unit stride along pages; context_lens are [B] int32.  Buffer lengths
+ *    are not passed: every per-sequence or per-(sequence, KV head) buffer
+ *    must cover the call's whole batch (B rows, or B * H_kv), or the kernels
+ *    read or write past its end; the caller checks this before the call.
  *  - `stream` is a hipStream_t (NULL = default stream).  Kernels are only
  *    enqueued; no entry point synchronises the host.
  *  - The library allocates no device memory.  Outputs and workspaces belong
